@@ -1,0 +1,161 @@
+/*
+ * gn_oracle.h - CPU restatement of gonano's RL-step arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (libgnhip.so, the
+ * gonano_amd package) may link, load or call this code; only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only
+ * as the checker.
+ *
+ * Every function states the reference file:line it restates
+ * (paths relative to the gonano source tree).  Floating-point formulas keep
+ * the reference's float32 data and its float64 accumulations.
+ */
+#ifndef GN_ORACLE_H
+#define GN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------- */
+/* kernels.Backend restated (kernels/scalar/ sources).                          */
+/* ---------------------------------------------------------------------- */
+void orc_add(float *dst, const float *l, const float *r, int64_t n);
+void orc_subtract(float *dst, const float *l, const float *r, int64_t n);
+void orc_multiply(float *dst, const float *l, const float *r, int64_t n);
+void orc_divide(float *dst, const float *l, const float *r, int64_t n);
+void orc_scale(float *dst, const float *s, float f, int64_t n);
+void orc_add_scaled(float *dst, const float *b, const float *s, float f, int64_t n);
+void orc_negate(float *dst, const float *s, int64_t n);
+void orc_abs(float *dst, const float *s, int64_t n);
+void orc_square(float *dst, const float *s, int64_t n);
+void orc_relu_squared(float *dst, const float *s, int64_t n);
+void orc_swiglu(float *dst, const float *gate, const float *up, float clamp, int64_t n);
+void orc_swiglu_backward(float *dgate, float *dup, const float *gate, const float *up,
+                         const float *dout, float clamp, int64_t n);
+void orc_exp(float *dst, const float *s, int64_t n);
+void orc_sigmoid(float *dst, const float *s, int64_t n);
+void orc_tanh(float *dst, const float *s, int64_t n);
+void orc_rsqrt(float *dst, const float *s, int64_t n);
+float orc_sum(const float *v, int64_t n);
+float orc_max(const float *v, int64_t n);
+int64_t orc_argmax(const float *v, int64_t n);
+void orc_matmul(float *dst, const float *l, const float *r, int64_t rows, int64_t cols, int64_t inner);
+void orc_matmul_transposed(float *dst, const float *l, const float *r, int64_t rows, int64_t cols,
+                           int64_t inner);
+float orc_dot(const float *l, const float *r, int64_t n);
+void orc_softmax_last_dim(float *dst, const float *s, int64_t rows, int64_t cols);
+void orc_rmsnorm_last_dim(float *dst, const float *s, int64_t rows, int64_t cols, float eps);
+void orc_indexer_scores(float *dst, const float *q, const float *k, const float *w, int64_t rows,
+                        int64_t blocks, int64_t heads, int64_t dim);
+void orc_indexer_block_max(float *dst, const float *scores, int64_t rows, int64_t blocks,
+                           int64_t group);
+void orc_topk_indices(int32_t *dst, const float *scores, int64_t rows, int64_t count, int64_t k);
+void orc_moe_gate_topk(const float *logits, const float *bias, float *probs, int32_t *selected,
+                       float *weights, int64_t rows, int64_t experts, int64_t k);
+void orc_grouped_matmul_transposed(float *dst, const float *in, const float *w,
+                                   const int32_t *counts, int64_t experts, int64_t cols,
+                                   int64_t inner);
+/* AttentionForward: lse may be NULL; segment may be NULL. */
+void orc_attention_forward(const float *q, const float *k, const float *v, float *out, float *lse,
+                           const int32_t *segment, int64_t nseg, int64_t qlen, int64_t klen,
+                           int64_t dim, int64_t offset, int64_t window);
+void orc_attention_backward(const float *q, const float *k, const float *v, const float *o,
+                            const float *dout, const float *lse, const float *row_correction,
+                            const int32_t *segment, int64_t nseg, float *dq, float *dk, float *dv,
+                            int64_t qlen, int64_t klen, int64_t dim, int64_t offset,
+                            int64_t window);
+void orc_attention_forward_split(const float *q, const float *k, const float *v, float *acc,
+                                 float *mx, float *sum, const int32_t *segment, int64_t nseg,
+                                 int64_t qlen, int64_t klen, int64_t dim, int64_t offset,
+                                 int64_t window, int64_t kstart, int64_t kend);
+/* partials: nparts accumulators [qlen*dim], maxima [qlen], sums [qlen] laid
+ * out contiguously (part-major). */
+void orc_attention_combine(const float *acc, const float *mx, const float *sum, int64_t nparts,
+                           float *out, float *lse, int64_t qlen, int64_t dim);
+
+/* ---------------------------------------------------------------------- */
+/* Go math/rand/v2 PCG + tensors.RNG + the top-k Gumbel sampler.           */
+/* ---------------------------------------------------------------------- */
+typedef struct {
+  uint64_t hi, lo;
+} orc_pcg;
+void orc_rng_new(orc_pcg *g, uint64_t seed);           /* tensors/random.go:16-18 */
+uint64_t orc_rng_uint64(orc_pcg *g);                    /* PCG.Uint64 (DXSM) */
+float orc_rng_float32(orc_pcg *g);                      /* Rand.Float32 */
+void orc_rng_advance(orc_pcg *g, uint64_t delta_hi, uint64_t delta_lo); /* jump ahead */
+float orc_kth_largest(const float *v, int64_t n, int64_t rank);
+int64_t orc_sample_multinomial(orc_pcg *g, const float *logits, int64_t n, float temperature);
+void orc_sample_next_token(const float *logits, int64_t rows, int64_t vocab, orc_pcg *g,
+                           float temperature, int64_t top_k, int32_t *out);
+float orc_gumbel_from_uniform(float u);
+
+/* ---------------------------------------------------------------------- */
+/* Calculator tool + byte-level tokenizer (inference/tooluse.go,           */
+/* tokenizer/tokenizer.go).                                               */
+/* ---------------------------------------------------------------------- */
+/* Returns 1 and writes a NUL-terminated result when the calculator
+ * understands expr; 0 otherwise. */
+int orc_calculator(const char *expr, char *out, size_t out_cap);
+
+/* ---------------------------------------------------------------------- */
+/* Dense transformer (model/ sources) in float32 and float64 builds.           */
+/* ---------------------------------------------------------------------- */
+typedef struct {
+  int32_t sequence_len, vocab_size, n_layer, n_head, n_kv_head, n_embd, rotary_dims;
+  char window_pattern[16];
+} orc_config;
+
+/* Sorted-name parameter table (model/params.go:14-85). */
+int orc_param_count(const orc_config *cfg);
+/* Writes name into name_out (cap 96) and returns numel; shape in rows/cols. */
+int64_t orc_param_info(const orc_config *cfg, int index, char *name_out, int64_t *rows,
+                       int64_t *cols);
+int64_t orc_param_total(const orc_config *cfg);
+
+#define ORC_MODEL_DECL(SFX, REAL)                                                                \
+  typedef struct orc_model##SFX orc_model##SFX;                                                  \
+  orc_model##SFX *orc_model_new##SFX(const orc_config *cfg, const REAL *params);                 \
+  void orc_model_free##SFX(orc_model##SFX *m);                                                   \
+  /* Inference forward without cache: logits [B,T,V]. */                                        \
+  void orc_forward##SFX(orc_model##SFX *m, const int32_t *ids, int B, int T, REAL *logits);     \
+  /* Token-by-token KV-cache decode of the same ids; logits [B,T,V]. */                          \
+  void orc_forward_decode##SFX(orc_model##SFX *m, const int32_t *ids, int B, int T, int chunk,   \
+                               REAL *logits);                                                    \
+  /* PolicyGradientStep (trainer/rl.go:14-60): returns loss; writes nll[B*T] and the           \
+   * parameter gradients grads[param_total] (overwritten). */                                   \
+  double orc_pg_step##SFX(orc_model##SFX *m, const int32_t *inputs, const int32_t *targets,     \
+                          int B, int T, const float *adv, float norm, REAL *nll, REAL *grads);   \
+  /* Mean cross-entropy with the gradcheck weighting (model/gradcheck_test.go:94-110). */         \
+  double orc_ce_loss##SFX(orc_model##SFX *m, const int32_t *inputs, const int32_t *targets,     \
+                          int B, int T, REAL *grads);                                            \
+  /* Engine.GenerateBatchWith (inference/engine.go:336-369) for one prompt.  rows_out is         \
+   * [S, P+max_tokens] (prompt + completion, terminal excluded); lens_out[S]. */                \
+  void orc_generate_batch##SFX(orc_model##SFX *m, const int32_t *prompt, int P, int S,          \
+                               int max_tokens, float temperature, int top_k, uint64_t seed,     \
+                               int32_t *rows_out, int32_t *lens_out);                           \
+  /* One chat_rl step (cmd/chat_rl/main.go:101-183) over G groups of S rollouts with           \
+   * precomputed rewards.  Outputs: rollouts/lengths as generate; adv[G*S]; maxLen;              \
+   * inputs/targets [G*S, maxLen-1]; nll; grads; returns loss. */                                \
+  double orc_rl_step##SFX(orc_model##SFX *m, const int32_t *prompts, int G, int P, int S,       \
+                          int max_tokens, float temperature, int top_k, const uint64_t *seeds,  \
+                          const float *rewards, int32_t *rows_out, int32_t *lens_out,           \
+                          float *adv_out, int32_t *max_len_out, int32_t *inputs_out,            \
+                          int32_t *targets_out, REAL *nll, REAL *grads);
+
+ORC_MODEL_DECL(_f32, float)
+ORC_MODEL_DECL(_f64, double)
+
+/* Window sizes (model/config.go:629-645): writes n_layer left widths. */
+void orc_window_sizes(const orc_config *cfg, int32_t *out);
+
+/* Number of OpenMP threads the oracle uses (for the CPU baseline report). */
+int orc_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,1203 @@
+/*
+ * model.c - the dense gonano transformer's inference forward, KV-cache
+ * decode, training forward/backward, policy-gradient step, batched
+ * generation and one chat_rl step, restated in C.
+ *
+ * TEST INFRASTRUCTURE ONLY (see gn_oracle.h).
+ *
+ * This file is compiled twice: with REAL=float (SFX=_f32), the parity
+ * oracle, which rounds to float32 where the reference does and accumulates
+ * matmuls/softmax sums in float64 like kernels/scalar; and with REAL=double
+ * (SFX=_f64), used by the finite-difference checks that pin the backward.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "gn_oracle.h"
+
+#ifndef REAL
+#define REAL float
+#define SFX _f32
+#endif
+
+#define CAT2(a, b) a##b
+#define CAT(a, b) CAT2(a, b)
+#define FN(name) CAT(name, SFX)
+#define MODEL CAT(orc_model, SFX)
+#define R(x) ((REAL)(x))
+
+/* model/attention.go:11-21, model/helpers.go:7, model/transformer.go:11,15 */
+#define NORM_EPS 1e-6f
+#define QK_SCALE 1.2f
+#define VE_GATE_CH 12
+#define VE_GATE_SCALE 3.0f
+#define SMEAR_CH 24
+#define SOFTCAP 15.0f
+#define ROT_OVER 10
+#define MASKED (-1e30f)
+#define MAXL 64
+
+/* ---------------------------------------------------------------------- */
+/* Parameter table shared by both builds (defined once, in the f32 build). */
+/* ---------------------------------------------------------------------- */
+typedef struct {
+  char name[96];
+  int64_t rows, cols, offset;
+} param_entry;
+
+static int has_value_embedding(int layer, int n_layer) { /* model/helpers.go:69-71 */
+  return layer % 2 == (n_layer - 1) % 2;
+}
+static int padded_vocab(const orc_config *c) { /* model/config.go:622-624 */
+  return ((c->vocab_size + 63) / 64) * 64;
+}
+static int rotary_dim(const orc_config *c) { /* model/config.go:430-444 */
+  int hd = c->n_embd / c->n_head;
+  return c->rotary_dims <= 0 ? hd : c->rotary_dims;
+}
+
+#if defined(ORC_DEFINE_SHARED)
+static int cmp_entry(const void *a, const void *b) {
+  return strcmp(((const param_entry *)a)->name, ((const param_entry *)b)->name);
+}
+/* model/params.go:14-85 (dense preset), sorted as ParameterNames does. */
+static int build_table(const orc_config *c, param_entry *t) {
+  int n = 0, C = c->n_embd, D = C / c->n_head, PV = padded_vocab(c);
+  int Hq = c->n_head, Hkv = c->n_kv_head, L = c->n_layer;
+#define ADD(nm, r, cc)                         \
+  do {                                         \
+    snprintf(t[n].name, 96, "%s", nm);         \
+    t[n].rows = (r);                           \
+    t[n].cols = (cc);                          \
+    n++;                                       \
+  } while (0)
+  char nm[96];
+  ADD("transformer.wte.weight", PV, C);
+  ADD("lm_head.weight", PV, C);
+  for (int l = 0; l < L; l++) {
+    snprintf(nm, 96, "transformer.h.%d.attn.c_q.weight", l); ADD(nm, Hq * D, C);
+    snprintf(nm, 96, "transformer.h.%d.attn.c_k.weight", l); ADD(nm, Hkv * D, C);
+    snprintf(nm, 96, "transformer.h.%d.attn.c_v.weight", l); ADD(nm, Hkv * D, C);
+    snprintf(nm, 96, "transformer.h.%d.attn.c_proj.weight", l); ADD(nm, C, C);
+    if (has_value_embedding(l, L)) {
+      snprintf(nm, 96, "transformer.h.%d.attn.ve_gate.weight", l); ADD(nm, Hkv, VE_GATE_CH);
+      snprintf(nm, 96, "value_embeds.%d.weight", l); ADD(nm, PV, Hkv * D);
+    }
+    snprintf(nm, 96, "transformer.h.%d.mlp.c_fc.weight", l); ADD(nm, 4 * C, C);
+    snprintf(nm, 96, "transformer.h.%d.mlp.c_proj.weight", l); ADD(nm, C, 4 * C);
+  }
+  ADD("resid_lambdas", L, 1);
+  ADD("x0_lambdas", L, 1);
+  ADD("smear_gate.weight", 1, SMEAR_CH);
+  ADD("smear_lambda", 1, 1);
+  ADD("backout_lambda", 1, 1);
+#undef ADD
+  qsort(t, n, sizeof(param_entry), cmp_entry);
+  int64_t off = 0;
+  for (int i = 0; i < n; i++) {
+    t[i].offset = off;
+    off += t[i].rows * t[i].cols;
+  }
+  return n;
+}
+int orc_param_count(const orc_config *c) {
+  param_entry t[16 * MAXL];
+  return build_table(c, t);
+}
+int64_t orc_param_info(const orc_config *c, int index, char *name_out, int64_t *rows,
+                       int64_t *cols) {
+  param_entry t[16 * MAXL];
+  int n = build_table(c, t);
+  if (index < 0 || index >= n) return -1;
+  snprintf(name_out, 96, "%s", t[index].name);
+  *rows = t[index].rows;
+  *cols = t[index].cols;
+  return t[index].rows * t[index].cols;
+}
+int64_t orc_param_total(const orc_config *c) {
+  param_entry t[16 * MAXL];
+  int n = build_table(c, t);
+  return t[n - 1].offset + t[n - 1].rows * t[n - 1].cols;
+}
+/* model/config.go:629-645: S = -((-T/4)/128)*128 in Go integer arithmetic
+ * (truncating division), L = T; the last layer is always long. */
+void orc_window_sizes(const orc_config *c, int32_t *out) {
+  int T = c->sequence_len;
+  int shortw = -((-T / 4) / 128) * 128;
+  size_t plen = strlen(c->window_pattern);
+  for (int l = 0; l < c->n_layer; l++) {
+    char p = c->window_pattern[l % plen];
+    out[l] = (p == 'L' || p == 'l') ? T : shortw;
+  }
+  out[c->n_layer - 1] = T;
+}
+int orc_num_threads(void) {
+#ifdef _OPENMP
+  extern int omp_get_max_threads(void);
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+#else
+int orc_param_count(const orc_config *c);
+#endif
+
+static int64_t param_offset(const orc_config *c, const char *name) {
+  char nm[96];
+  int64_t r, cc, off = 0;
+  int n = orc_param_count(c);
+  for (int i = 0; i < n; i++) {
+    int64_t numel = orc_param_info(c, i, nm, &r, &cc);
+    if (strcmp(nm, name) == 0) return off;
+    off += numel;
+  }
+  fprintf(stderr, "oracle: unknown parameter %s\n", name);
+  abort();
+}
+
+/* ---------------------------------------------------------------------- */
+/* Model                                                                   */
+/* ---------------------------------------------------------------------- */
+typedef struct {
+  int64_t wq, wk, wv, wo, wve, wfc, wproj, ve;
+  int has_ve, window;
+} layer_off;
+
+struct MODEL {
+  orc_config cfg;
+  int C, Hq, Hkv, D, R, F, L, V, PV, S, KVW;
+  int64_t total;
+  REAL *p;
+  int64_t wte, lm, rl, x0l, smg, sml, bkl;
+  layer_off lay[MAXL];
+  REAL *cosT, *sinT; /* [S*10][R/2] */
+};
+
+MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
+  MODEL *m = (MODEL *)calloc(1, sizeof(MODEL));
+  m->cfg = *cfg;
+  m->C = cfg->n_embd;
+  m->Hq = cfg->n_head;
+  m->Hkv = cfg->n_kv_head;
+  m->D = m->C / m->Hq;
+  m->R = rotary_dim(cfg);
+  m->F = 4 * m->C;
+  m->L = cfg->n_layer;
+  m->V = cfg->vocab_size;
+  m->PV = padded_vocab(cfg);
+  m->S = cfg->sequence_len;
+  m->KVW = m->Hkv * m->D;
+  m->total = orc_param_total(cfg);
+  m->p = (REAL *)malloc(sizeof(REAL) * m->total);
+  memcpy(m->p, params, sizeof(REAL) * m->total);
+  m->wte = param_offset(cfg, "transformer.wte.weight");
+  m->lm = param_offset(cfg, "lm_head.weight");
+  m->rl = param_offset(cfg, "resid_lambdas");
+  m->x0l = param_offset(cfg, "x0_lambdas");
+  m->smg = param_offset(cfg, "smear_gate.weight");
+  m->sml = param_offset(cfg, "smear_lambda");
+  m->bkl = param_offset(cfg, "backout_lambda");
+  int32_t win[MAXL];
+  orc_window_sizes(cfg, win);
+  char nm[96];
+  for (int l = 0; l < m->L; l++) {
+    layer_off *o = &m->lay[l];
+#define OFF(field, fmt)                      \
+  snprintf(nm, 96, fmt, l);                  \
+  o->field = param_offset(cfg, nm);
+    OFF(wq, "transformer.h.%d.attn.c_q.weight");
+    OFF(wk, "transformer.h.%d.attn.c_k.weight");
+    OFF(wv, "transformer.h.%d.attn.c_v.weight");
+    OFF(wo, "transformer.h.%d.attn.c_proj.weight");
+    OFF(wfc, "transformer.h.%d.mlp.c_fc.weight");
+    OFF(wproj, "transformer.h.%d.mlp.c_proj.weight");
+    o->has_ve = has_value_embedding(l, m->L);
+    if (o->has_ve) {
+      OFF(wve, "transformer.h.%d.attn.ve_gate.weight");
+      OFF(ve, "value_embeds.%d.weight");
+    }
+#undef OFF
+    o->window = win[l];
+  }
+  /* model/rotary.go:16-30 with SequenceLen*10 positions (transformer.go:54) */
+  int half = m->R / 2, npos = m->S * ROT_OVER;
+  m->cosT = (REAL *)malloc(sizeof(REAL) * npos * half);
+  m->sinT = (REAL *)malloc(sizeof(REAL) * npos * half);
+  for (int p = 0; p < npos; p++)
+    for (int j = 0; j < half; j++) {
+      double inv = pow(100000.0, -2.0 * (double)j / (double)m->R);
+      double f = (double)p * inv;
+      m->cosT[p * half + j] = R(cos(f));
+      m->sinT[p * half + j] = R(sin(f));
+    }
+  return m;
+}
+
+void FN(orc_model_free)(MODEL *m) {
+  if (!m) return;
+  free(m->p);
+  free(m->cosT);
+  free(m->sinT);
+  free(m);
+}
+
+/* ---- primitives ------------------------------------------------------- */
+
+/* kernels/scalar/norm.go:26-40 applied row-wise (model/attention.go:25-29) */
+static void rmsnorm_rows(REAL *dst, const REAL *src, int64_t rows, int cols) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++) {
+    const REAL *s = src + r * cols;
+    REAL *d = dst + r * cols;
+    double ss = 0;
+    for (int c = 0; c < cols; c++) ss += (double)s[c] * (double)s[c];
+    REAL ms = R(ss / (double)cols);
+    REAL inv = R(1.0 / sqrt((double)ms + (double)NORM_EPS));
+    for (int c = 0; c < cols; c++) d[c] = s[c] * inv;
+  }
+}
+/* tensors/backward.go:81-104 */
+static void rmsnorm_backward_rows(REAL *dst, const REAL *x, const REAL *g, int64_t rows, int cols) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++) {
+    const REAL *xr = x + r * cols, *gr = g + r * cols;
+    REAL *d = dst + r * cols;
+    double ss = 0, dot = 0;
+    for (int c = 0; c < cols; c++) {
+      ss += (double)xr[c] * (double)xr[c];
+      dot += (double)gr[c] * (double)xr[c];
+    }
+    double ms = ss / (double)cols;
+    double rms = sqrt(ms + (double)NORM_EPS);
+    double inv = 1.0 / rms;
+    double coef = dot / ((double)cols * rms * rms * rms);
+    for (int c = 0; c < cols; c++) d[c] = R((double)gr[c] * inv - coef * (double)xr[c]);
+  }
+}
+/* out[rows][outF] = in[rows][inF] . W[outF][inF]^T, float64 accumulation
+ * (model/layers/linear.go:32-40 -> kernels/scalar/matmul.go:22-33). */
+static void linear_fwd(REAL *out, const REAL *in, const REAL *W, int64_t rows, int inF, int outF) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++)
+    for (int o = 0; o < outF; o++) {
+      double a = 0;
+      const REAL *x = in + r * inF, *w = W + (int64_t)o * inF;
+      for (int i = 0; i < inF; i++) a += (double)x[i] * (double)w[i];
+      out[r * outF + o] = R(a);
+    }
+}
+/* model/layers/linear.go:45-53: dW += g^T x ; dx = g W (float64 accumulation). */
+static void linear_bwd(REAL *dx, REAL *dW, const REAL *x, const REAL *g, const REAL *W,
+                       int64_t rows, int inF, int outF) {
+#pragma omp parallel for schedule(static)
+  for (int o = 0; o < outF; o++)
+    for (int i = 0; i < inF; i++) {
+      double a = 0;
+      for (int64_t r = 0; r < rows; r++) a += (double)g[r * outF + o] * (double)x[r * inF + i];
+      dW[(int64_t)o * inF + i] += R(a);
+    }
+  if (!dx) return;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++)
+    for (int i = 0; i < inF; i++) {
+      double a = 0;
+      for (int o = 0; o < outF; o++) a += (double)g[r * outF + o] * (double)W[(int64_t)o * inF + i];
+      dx[r * inF + i] = R(a);
+    }
+}
+static REAL sigmoidR(REAL x) { return R(1.0 / (1.0 + exp(-(double)x))); }
+
+/* model/rotary.go:43-75 on rows of [heads][D] at the given position; sign
+ * -1 uses the negated sine table (model/train.go:14-20). */
+static void rope_row(MODEL *m, REAL *dst, const REAL *src, int heads, int pos, int sign) {
+  int D = m->D, half = m->R / 2, off = D - m->R;
+  const REAL *cw = m->cosT + (int64_t)pos * half, *sw = m->sinT + (int64_t)pos * half;
+  for (int h = 0; h < heads; h++) {
+    const REAL *s = src + h * D;
+    REAL *d = dst + h * D;
+    REAL tmp[1024];
+    memcpy(tmp, s, sizeof(REAL) * D);
+    for (int j = 0; j < half; j++) {
+      REAL x1 = tmp[off + j], x2 = tmp[off + half + j];
+      REAL c = cw[j], sn = sign > 0 ? sw[j] : -sw[j];
+      d[j + off] = x1 * c + x2 * sn;
+      d[off + half + j] = -x1 * sn + x2 * c;
+    }
+    for (int j = 0; j < off; j++) d[j] = tmp[j];
+  }
+}
+
+/* One (batch, head) attention with the reference mask; scores and
+ * probabilities materialized (kernels/scalar/attention.go:16-49). */
+static void attn_fwd(const REAL *q, const REAL *k, const REAL *v, REAL *out, REAL *lse, int qlen,
+                     int klen, int D, int offset, int window) {
+  REAL *sc = (REAL *)malloc(sizeof(REAL) * klen);
+  for (int qi = 0; qi < qlen; qi++) {
+    int qpos = offset + qi;
+    REAL mx = 0;
+    for (int kj = 0; kj < klen; kj++) {
+      double a = 0;
+      for (int d = 0; d < D; d++) a += (double)q[qi * D + d] * (double)k[(int64_t)kj * D + d];
+      REAL s = R(a);
+      if (kj > qpos || (window >= 0 && qpos - kj > window)) s = R(MASKED);
+      sc[kj] = s;
+      if (kj == 0 || s > mx) mx = s;
+    }
+    double tot = 0;
+    for (int kj = 0; kj < klen; kj++) {
+      double e = exp((double)(sc[kj] - mx));
+      sc[kj] = R(e);
+      tot += e;
+    }
+    if (lse) lse[qi] = mx + R(log(tot));
+    REAL inv = R(1.0 / tot);
+    for (int d = 0; d < D; d++) {
+      double a = 0;
+      for (int kj = 0; kj < klen; kj++) a += (double)sc[kj] * (double)v[(int64_t)kj * D + d];
+      out[qi * D + d] = R(a) * inv;
+    }
+  }
+  free(sc);
+}
+/* kernels/scalar/attention.go:145-205, gradients accumulated. */
+static void attn_bwd(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
+                     const REAL *lse, REAL *dq, REAL *dk, REAL *dv, int qlen, int klen, int D,
+                     int offset, int window) {
+  REAL *P = (REAL *)malloc(sizeof(REAL) * (int64_t)qlen * klen);
+  REAL *dS = (REAL *)malloc(sizeof(REAL) * (int64_t)qlen * klen);
+  for (int qi = 0; qi < qlen; qi++) {
+    int qpos = offset + qi;
+    for (int kj = 0; kj < klen; kj++) {
+      double a = 0;
+      for (int d = 0; d < D; d++) a += (double)q[qi * D + d] * (double)k[(int64_t)kj * D + d];
+      REAL s = R(a);
+      if (kj > qpos || (window >= 0 && qpos - kj > window)) s = R(MASKED);
+      P[(int64_t)qi * klen + kj] = s <= R(MASKED) ? R(0) : R(exp((double)(s - lse[qi])));
+    }
+  }
+  for (int kj = 0; kj < klen; kj++)
+    for (int d = 0; d < D; d++) {
+      double a = 0;
+      for (int qi = 0; qi < qlen; qi++) a += (double)P[(int64_t)qi * klen + kj] * (double)dout[qi * D + d];
+      dv[(int64_t)kj * D + d] += R(a);
+    }
+  for (int qi = 0; qi < qlen; qi++) {
+    double rd = 0;
+    REAL *dp = dS + (int64_t)qi * klen;
+    for (int kj = 0; kj < klen; kj++) {
+      double a = 0;
+      for (int d = 0; d < D; d++) a += (double)dout[qi * D + d] * (double)v[(int64_t)kj * D + d];
+      dp[kj] = R(a);
+      rd += (double)dp[kj] * (double)P[(int64_t)qi * klen + kj];
+    }
+    for (int kj = 0; kj < klen; kj++)
+      dp[kj] = R((double)P[(int64_t)qi * klen + kj] * ((double)dp[kj] - rd));
+  }
+  for (int qi = 0; qi < qlen; qi++)
+    for (int d = 0; d < D; d++) {
+      double a = 0;
+      for (int kj = 0; kj < klen; kj++) a += (double)dS[(int64_t)qi * klen + kj] * (double)k[(int64_t)kj * D + d];
+      dq[qi * D + d] += R(a);
+    }
+  for (int kj = 0; kj < klen; kj++)
+    for (int d = 0; d < D; d++) {
+      double a = 0;
+      for (int qi = 0; qi < qlen; qi++) a += (double)dS[(int64_t)qi * klen + kj] * (double)q[qi * D + d];
+      dk[(int64_t)kj * D + d] += R(a);
+    }
+  free(P);
+  free(dS);
+}
+
+/* tensors/math.go:38-45: z = 15*tanh(y*(1/15)) with the float32 reciprocal. */
+static REAL softcap(REAL y) {
+  REAL inv = R(1) / R(SOFTCAP);
+  REAL t = y * inv;
+  return R(tanh((double)t)) * R(SOFTCAP);
+}
+
+/* ---- KV cache (model/kvcache.go:10-140) -------------------------------- */
+typedef struct {
+  int B, maxSeq, pos, has_prev;
+  REAL *k, *v;  /* [L][B][Hkv][maxSeq][D] */
+  REAL *prev;   /* [B][C] */
+} kvcache;
+
+static kvcache *cache_new(MODEL *m, int B, int maxSeq) {
+  kvcache *c = (kvcache *)calloc(1, sizeof(kvcache));
+  c->B = B;
+  c->maxSeq = maxSeq;
+  size_t n = (size_t)m->L * B * m->Hkv * maxSeq * m->D;
+  c->k = (REAL *)calloc(n, sizeof(REAL));
+  c->v = (REAL *)calloc(n, sizeof(REAL));
+  c->prev = (REAL *)calloc((size_t)B * m->C, sizeof(REAL));
+  return c;
+}
+static void cache_free(kvcache *c) {
+  free(c->k);
+  free(c->v);
+  free(c->prev);
+  free(c);
+}
+static REAL *cache_k(MODEL *m, kvcache *c, int l, int b, int h) {
+  return c->k + ((((size_t)l * c->B + b) * m->Hkv + h) * c->maxSeq) * m->D;
+}
+static REAL *cache_v(MODEL *m, kvcache *c, int l, int b, int h) {
+  return c->v + ((((size_t)l * c->B + b) * m->Hkv + h) * c->maxSeq) * m->D;
+}
+/* model/kvcache.go:383-448 (PrefillFrom) for a batch-1 source. */
+static void prefill_from(MODEL *m, kvcache *dst, kvcache *src) {
+  int pos = src->pos;
+  for (int l = 0; l < m->L; l++)
+    for (int b = 0; b < dst->B; b++)
+      for (int h = 0; h < m->Hkv; h++) {
+        memcpy(cache_k(m, dst, l, b, h), cache_k(m, src, l, 0, h), sizeof(REAL) * pos * m->D);
+        memcpy(cache_v(m, dst, l, b, h), cache_v(m, src, l, 0, h), sizeof(REAL) * pos * m->D);
+      }
+  dst->pos = pos;
+  if (src->has_prev) {
+    for (int b = 0; b < dst->B; b++) memcpy(dst->prev + (size_t)b * m->C, src->prev, sizeof(REAL) * m->C);
+    dst->has_prev = 1;
+  }
+}
+
+/* ---- forward ---------------------------------------------------------- */
+typedef struct {
+  REAL *xin, *xb, *h, *qrot, *krot, *qn, *kn, *vh, *lse, *o, *vesig, *ve, *mid, *h2, *u, *act;
+} layer_ctx;
+
+typedef struct {
+  int B, T;
+  int32_t *ids;
+  REAL *raw, *embn, *smsig, *x0;
+  layer_ctx lc[MAXL];
+  REAL *backout, *final_pre, *final_norm, *logits;
+} train_ctx;
+
+static void ctx_free(train_ctx *c, int L) {
+  if (!c) return;
+  free(c->ids);
+  free(c->raw); free(c->embn); free(c->smsig); free(c->x0);
+  for (int l = 0; l < L; l++) {
+    layer_ctx *x = &c->lc[l];
+    free(x->xin); free(x->xb); free(x->h); free(x->qrot); free(x->krot); free(x->qn);
+    free(x->kn); free(x->vh); free(x->lse); free(x->o); free(x->vesig); free(x->ve);
+    free(x->mid); free(x->h2); free(x->u); free(x->act);
+  }
+  free(c->backout); free(c->final_pre); free(c->final_norm); free(c->logits);
+  free(c);
+}
+
+static REAL *dup_arr(const REAL *a, size_t n) {
+  REAL *b = (REAL *)malloc(sizeof(REAL) * n);
+  memcpy(b, a, sizeof(REAL) * n);
+  return b;
+}
+
+/*
+ * model/transformer.go:243-342 (forward) with model/block.go:38-47,
+ * model/attention.go:235-324 and model/mlp.go:62-77.  With cache == NULL it
+ * is also the training forward (model/train_transformer.go:63-142); ctx, when
+ * given, receives the saved activations.
+ */
+static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *cache, REAL *logits,
+                         train_ctx *ctx) {
+  int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, F = m->F, V = m->V, PV = m->PV;
+  int64_t N = (int64_t)B * T;
+  const REAL *P = m->p;
+  REAL *x = (REAL *)malloc(sizeof(REAL) * N * C);
+  REAL *raw = (REAL *)malloc(sizeof(REAL) * N * C);
+  for (int64_t n = 0; n < N; n++) memcpy(raw + n * C, P + m->wte + (int64_t)ids[n] * C, sizeof(REAL) * C);
+  rmsnorm_rows(x, raw, N, C);
+  REAL lam_s = P[m->sml];
+  const REAL *wsg = P + m->smg;
+  REAL *smsig = NULL;
+  if (ctx) {
+    ctx->raw = raw;
+    ctx->embn = dup_arr(x, (size_t)N * C);
+    smsig = (REAL *)calloc((size_t)B * (T > 1 ? T - 1 : 1), sizeof(REAL));
+    ctx->smsig = smsig;
+  }
+  /* smear (transformer.go:266-301, helpers.go:35-65) */
+  {
+    REAL *gate = (REAL *)calloc((size_t)B * (T > 1 ? T - 1 : 1), sizeof(REAL));
+    for (int b = 0; b < B; b++)
+      for (int t = 1; t < T; t++) {
+        double a = 0;
+        for (int c = 0; c < SMEAR_CH; c++) a += (double)x[((int64_t)b * T + t) * C + c] * (double)wsg[c];
+        REAL sg = sigmoidR(R(a));
+        if (smsig) smsig[b * (T - 1) + t - 1] = sg;
+        gate[b * (T - 1) + t - 1] = sg * lam_s;
+      }
+    REAL *seed = NULL;
+    int use_prev = cache && cache->has_prev;
+    REAL *newprev = NULL;
+    if (cache) {
+      newprev = (REAL *)malloc(sizeof(REAL) * B * C);
+      for (int b = 0; b < B; b++) memcpy(newprev + (int64_t)b * C, x + ((int64_t)b * T + T - 1) * C, sizeof(REAL) * C);
+    }
+    if (use_prev) {
+      seed = (REAL *)malloc(sizeof(REAL) * B);
+      for (int b = 0; b < B; b++) {
+        double a = 0;
+        for (int c = 0; c < SMEAR_CH; c++) a += (double)x[((int64_t)b * T) * C + c] * (double)wsg[c];
+        seed[b] = sigmoidR(R(a)) * lam_s;
+      }
+    }
+    if (!cache && T <= 1) { fprintf(stderr, "oracle: training forward requires T > 1\n"); abort(); }
+    for (int b = 0; b < B; b++)
+      for (int t = T - 1; t >= 1; t--) {
+        REAL gv = gate[b * (T - 1) + t - 1];
+        REAL *cur = x + ((int64_t)b * T + t) * C, *prv = x + ((int64_t)b * T + t - 1) * C;
+        for (int c = 0; c < C; c++) cur[c] += gv * prv[c];
+      }
+    if (seed)
+      for (int b = 0; b < B; b++) {
+        REAL *cur = x + ((int64_t)b * T) * C;
+        for (int c = 0; c < C; c++) cur[c] += seed[b] * cache->prev[(int64_t)b * C + c];
+      }
+    if (cache) {
+      memcpy(cache->prev, newprev, sizeof(REAL) * B * C);
+      cache->has_prev = 1;
+      free(newprev);
+    }
+    free(seed);
+    free(gate);
+  }
+  if (!ctx) free(raw);
+  REAL *x0 = dup_arr(x, (size_t)N * C);
+  if (ctx) ctx->x0 = x0;
+
+  int offset = cache ? cache->pos : 0;
+  int klen = cache ? cache->pos + T : T;
+  int ratio = Hq / Hkv;
+  int bkidx = m->L / 2;
+  REAL *backout = NULL;
+  REAL *h = (REAL *)malloc(sizeof(REAL) * N * C);
+  REAL *q = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  REAL *k = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+  REAL *v = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+  REAL *o = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  REAL *a = (REAL *)malloc(sizeof(REAL) * N * C);
+  REAL *u = (REAL *)malloc(sizeof(REAL) * N * F);
+  REAL *act = (REAL *)malloc(sizeof(REAL) * N * F);
+  REAL *qn = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  REAL *kn = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+  REAL *vesig = (REAL *)malloc(sizeof(REAL) * N * Hkv);
+  REAL *vev = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+  REAL *lseb = (REAL *)malloc(sizeof(REAL) * N * Hq);
+  for (int l = 0; l < m->L; l++) {
+    const layer_off *lo = &m->lay[l];
+    layer_ctx *lc = ctx ? &ctx->lc[l] : NULL;
+    if (lc) lc->xin = dup_arr(x, (size_t)N * C);
+    /* combineResidual (transformer.go:544-551) */
+    REAL lr = P[m->rl + l], l0 = P[m->x0l + l];
+    for (int64_t i = 0; i < N * C; i++) x[i] = lr * x[i] + l0 * x0[i];
+    if (lc) lc->xb = dup_arr(x, (size_t)N * C);
+    /* attention on norm(x) */
+    rmsnorm_rows(h, x, N, C);
+    if (lc) lc->h = dup_arr(h, (size_t)N * C);
+    linear_fwd(q, h, P + lo->wq, N, C, Hq * D);
+    linear_fwd(k, h, P + lo->wk, N, C, Hkv * D);
+    linear_fwd(v, h, P + lo->wv, N, C, Hkv * D);
+    if (lo->has_ve) { /* attention.go:245-250, 392-405 */
+      for (int64_t n = 0; n < N; n++) memcpy(vev + n * Hkv * D, P + lo->ve + (int64_t)ids[n] * Hkv * D, sizeof(REAL) * Hkv * D);
+      for (int64_t n = 0; n < N; n++)
+        for (int hh = 0; hh < Hkv; hh++) {
+          double acc = 0;
+          for (int c = 0; c < VE_GATE_CH; c++) acc += (double)h[n * C + c] * (double)P[lo->wve + hh * VE_GATE_CH + c];
+          REAL sg = sigmoidR(R(acc));
+          vesig[n * Hkv + hh] = sg;
+          REAL g = sg * R(VE_GATE_SCALE);
+          for (int d = 0; d < D; d++) v[(n * Hkv + hh) * D + d] += g * vev[(n * Hkv + hh) * D + d];
+        }
+      if (lc) { lc->vesig = dup_arr(vesig, (size_t)N * Hkv); lc->ve = dup_arr(vev, (size_t)N * Hkv * D); }
+    }
+    /* rotary then 1.2*RMSNorm per head (attention.go:252-256) */
+    for (int b = 0; b < B; b++)
+      for (int t = 0; t < T; t++) {
+        int64_t n = (int64_t)b * T + t;
+        rope_row(m, q + n * Hq * D, q + n * Hq * D, Hq, offset + t, 1);
+        rope_row(m, k + n * Hkv * D, k + n * Hkv * D, Hkv, offset + t, 1);
+      }
+    if (lc) { lc->qrot = dup_arr(q, (size_t)N * Hq * D); lc->krot = dup_arr(k, (size_t)N * Hkv * D); }
+    rmsnorm_rows(qn, q, N * Hq, D);
+    rmsnorm_rows(kn, k, N * Hkv, D);
+    for (int64_t i = 0; i < N * Hq * D; i++) qn[i] *= R(QK_SCALE);
+    for (int64_t i = 0; i < N * Hkv * D; i++) kn[i] *= R(QK_SCALE);
+    /* head-major copies and KV-cache write (attention.go:277-303) */
+    REAL *qh = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+    REAL *oh = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+    REAL *kh = (REAL *)malloc(sizeof(REAL) * (int64_t)B * Hkv * klen * D);
+    REAL *vh = (REAL *)malloc(sizeof(REAL) * (int64_t)B * Hkv * klen * D);
+    for (int b = 0; b < B; b++)
+      for (int t = 0; t < T; t++)
+        for (int hh = 0; hh < Hq; hh++)
+          memcpy(qh + (((int64_t)b * Hq + hh) * T + t) * D, qn + (((int64_t)b * T + t) * Hq + hh) * D, sizeof(REAL) * D);
+    for (int b = 0; b < B; b++)
+      for (int hh = 0; hh < Hkv; hh++) {
+        REAL *kd = kh + ((int64_t)b * Hkv + hh) * klen * D, *vd = vh + ((int64_t)b * Hkv + hh) * klen * D;
+        if (cache) {
+          REAL *ck = cache_k(m, cache, l, b, hh), *cv = cache_v(m, cache, l, b, hh);
+          for (int t = 0; t < T; t++) {
+            memcpy(ck + (int64_t)(offset + t) * D, kn + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+            memcpy(cv + (int64_t)(offset + t) * D, v + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+          }
+          memcpy(kd, ck, sizeof(REAL) * klen * D);
+          memcpy(vd, cv, sizeof(REAL) * klen * D);
+        } else {
+          for (int t = 0; t < T; t++) {
+            memcpy(kd + (int64_t)t * D, kn + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+            memcpy(vd + (int64_t)t * D, v + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+          }
+        }
+      }
+#pragma omp parallel for schedule(dynamic)
+    for (int bh = 0; bh < B * Hq; bh++) {
+      int b = bh / Hq, hq = bh % Hq, hk = hq / ratio;
+      attn_fwd(qh + (int64_t)bh * T * D, kh + ((int64_t)b * Hkv + hk) * klen * D,
+               vh + ((int64_t)b * Hkv + hk) * klen * D, oh + (int64_t)bh * T * D,
+               lseb + (int64_t)bh * T, T, klen, D, offset, lo->window);
+    }
+    if (lc) {
+      lc->qn = qh; lc->kn = kh; lc->vh = vh;
+      lc->o = dup_arr(oh, (size_t)N * Hq * D);
+      lc->lse = dup_arr(lseb, (size_t)N * Hq);
+    } else {
+      free(qh); free(kh); free(vh);
+    }
+    /* back to sequence layout, output projection, residual */
+    for (int b = 0; b < B; b++)
+      for (int t = 0; t < T; t++)
+        for (int hh = 0; hh < Hq; hh++)
+          memcpy(o + (((int64_t)b * T + t) * Hq + hh) * D, oh + (((int64_t)b * Hq + hh) * T + t) * D, sizeof(REAL) * D);
+    free(oh);
+    linear_fwd(a, o, P + lo->wo, N, Hq * D, C);
+    for (int64_t i = 0; i < N * C; i++) x[i] = x[i] + a[i];
+    if (lc) lc->mid = dup_arr(x, (size_t)N * C);
+    /* MLP (mlp.go:62-77) */
+    rmsnorm_rows(h, x, N, C);
+    if (lc) lc->h2 = dup_arr(h, (size_t)N * C);
+    linear_fwd(u, h, P + lo->wfc, N, C, F);
+    for (int64_t i = 0; i < N * F; i++) {
+      REAL t = u[i] < 0 ? R(0) : u[i];
+      act[i] = t * t;
+    }
+    if (lc) { lc->u = dup_arr(u, (size_t)N * F); lc->act = dup_arr(act, (size_t)N * F); }
+    linear_fwd(a, act, P + lo->wproj, N, F, C);
+    for (int64_t i = 0; i < N * C; i++) x[i] = x[i] + a[i];
+    if (l == bkidx) backout = dup_arr(x, (size_t)N * C);
+  }
+  if (cache) cache->pos += T;
+  /* backout, final norm, lm_head, trimVocab, softcap (transformer.go:333-341) */
+  if (backout) {
+    REAL nb = -P[m->bkl];
+    for (int64_t i = 0; i < N * C; i++) x[i] = x[i] + nb * backout[i];
+  }
+  if (ctx) { ctx->backout = backout; ctx->final_pre = dup_arr(x, (size_t)N * C); } else free(backout);
+  rmsnorm_rows(h, x, N, C);
+  if (ctx) ctx->final_norm = dup_arr(h, (size_t)N * C);
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; n++)
+    for (int j = 0; j < V; j++) {
+      double acc = 0;
+      const REAL *w = P + m->lm + (int64_t)j * C;
+      for (int c = 0; c < C; c++) acc += (double)h[n * C + c] * (double)w[c];
+      logits[n * V + j] = softcap(R(acc));
+    }
+  (void)PV;
+  if (!ctx) free(x0);
+  free(x); free(h); free(q); free(k); free(v); free(o); free(a); free(u); free(act);
+  free(qn); free(kn); free(vesig); free(vev); free(lseb);
+}
+
+void FN(orc_forward)(MODEL *m, const int32_t *ids, int B, int T, REAL *logits) {
+  forward_impl(m, ids, B, T, NULL, logits, NULL);
+}
+
+/* Token-by-token (or chunked) KV-cache decode, the invariant
+ * model/smear_test.go:30-82 checks against the full forward. */
+void FN(orc_forward_decode)(MODEL *m, const int32_t *ids, int B, int T, int chunk, REAL *logits) {
+  kvcache *c = cache_new(m, B, T);
+  if (chunk < 1) chunk = 1;
+  int32_t *col = (int32_t *)malloc(sizeof(int32_t) * B * chunk);
+  REAL *lg = (REAL *)malloc(sizeof(REAL) * (int64_t)B * chunk * m->V);
+  for (int t0 = 0; t0 < T; t0 += chunk) {
+    int n = T - t0 < chunk ? T - t0 : chunk;
+    for (int b = 0; b < B; b++)
+      for (int j = 0; j < n; j++) col[b * n + j] = ids[b * T + t0 + j];
+    forward_impl(m, col, B, n, c, lg, NULL);
+    for (int b = 0; b < B; b++)
+      for (int j = 0; j < n; j++)
+        memcpy(logits + ((int64_t)b * T + t0 + j) * m->V, lg + ((int64_t)b * n + j) * m->V, sizeof(REAL) * m->V);
+  }
+  free(col);
+  free(lg);
+  cache_free(c);
+}
+
+/* ---- backward (model/train_transformer.go:147-320, model/train.go) ---- */
+
+/* Block backward (model/train.go:554-572 with 198-427 and 505-514). Returns
+ * the gradient with respect to the block input in gx; parameter gradients
+ * accumulate into G. */
+static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, const int32_t *ids,
+                           int B, int T, const REAL *gout, REAL *gx, REAL *G) {
+  int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, F = m->F, ratio = Hq / Hkv;
+  int64_t N = (int64_t)B * T;
+  const REAL *P = m->p;
+  REAL *gmid = dup_arr(gout, (size_t)N * C);
+  /* MLP backward */
+  REAL *dact = (REAL *)malloc(sizeof(REAL) * N * F);
+  linear_bwd(dact, G + lo->wproj, lc->act, gout, P + lo->wproj, N, F, C);
+  for (int64_t i = 0; i < N * F; i++) dact[i] = lc->u[i] > 0 ? dact[i] * R(2) * lc->u[i] : R(0);
+  REAL *dh = (REAL *)malloc(sizeof(REAL) * N * C);
+  linear_bwd(dh, G + lo->wfc, lc->h2, dact, P + lo->wfc, N, C, F);
+  free(dact);
+  REAL *tmp = (REAL *)malloc(sizeof(REAL) * N * C);
+  rmsnorm_backward_rows(tmp, lc->mid, dh, N, C);
+  for (int64_t i = 0; i < N * C; i++) gmid[i] = gmid[i] + tmp[i];
+  /* attention backward */
+  REAL *oseq = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++)
+      for (int hh = 0; hh < Hq; hh++)
+        memcpy(oseq + (((int64_t)b * T + t) * Hq + hh) * D, lc->o + (((int64_t)b * Hq + hh) * T + t) * D, sizeof(REAL) * D);
+  REAL *dos = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  linear_bwd(dos, G + lo->wo, oseq, gmid, P + lo->wo, N, Hq * D, C);
+  free(oseq);
+  REAL *doh = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++)
+      for (int hh = 0; hh < Hq; hh++)
+        memcpy(doh + (((int64_t)b * Hq + hh) * T + t) * D, dos + (((int64_t)b * T + t) * Hq + hh) * D, sizeof(REAL) * D);
+  free(dos);
+  REAL *dqh = (REAL *)calloc((size_t)N * Hq * D, sizeof(REAL));
+  REAL *dkh = (REAL *)calloc((size_t)N * Hkv * D, sizeof(REAL));
+  REAL *dvh = (REAL *)calloc((size_t)N * Hkv * D, sizeof(REAL));
+  /* serial (b, qh) loop as train.go:305-326 so GQA accumulation is race-free */
+  for (int b = 0; b < B; b++)
+#pragma omp parallel for schedule(dynamic)
+    for (int hk = 0; hk < Hkv; hk++)
+      for (int r = 0; r < ratio; r++) {
+        int hq = hk * ratio + r;
+        int64_t bh = (int64_t)b * Hq + hq, bk = (int64_t)b * Hkv + hk;
+        attn_bwd(lc->qn + bh * T * D, lc->kn + bk * T * D, lc->vh + bk * T * D, doh + bh * T * D,
+                 lc->lse + bh * T, dqh + bh * T * D, dkh + bk * T * D, dvh + bk * T * D, T, T, D, 0,
+                 lo->window);
+      }
+  free(doh);
+  for (int64_t i = 0; i < N * Hq * D; i++) dqh[i] *= R(QK_SCALE);
+  for (int64_t i = 0; i < N * Hkv * D; i++) dkh[i] *= R(QK_SCALE);
+  REAL *dqs = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  REAL *dks = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+  REAL *dvs = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++) {
+      for (int hh = 0; hh < Hq; hh++)
+        memcpy(dqs + (((int64_t)b * T + t) * Hq + hh) * D, dqh + (((int64_t)b * Hq + hh) * T + t) * D, sizeof(REAL) * D);
+      for (int hh = 0; hh < Hkv; hh++) {
+        memcpy(dks + (((int64_t)b * T + t) * Hkv + hh) * D, dkh + (((int64_t)b * Hkv + hh) * T + t) * D, sizeof(REAL) * D);
+        memcpy(dvs + (((int64_t)b * T + t) * Hkv + hh) * D, dvh + (((int64_t)b * Hkv + hh) * T + t) * D, sizeof(REAL) * D);
+      }
+    }
+  free(dqh); free(dkh); free(dvh);
+  REAL *dq = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
+  REAL *dk = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+  rmsnorm_backward_rows(dq, lc->qrot, dqs, N * Hq, D);
+  rmsnorm_backward_rows(dk, lc->krot, dks, N * Hkv, D);
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++) {
+      int64_t n = (int64_t)b * T + t;
+      rope_row(m, dq + n * Hq * D, dq + n * Hq * D, Hq, t, -1);
+      rope_row(m, dk + n * Hkv * D, dk + n * Hkv * D, Hkv, t, -1);
+    }
+  REAL *dhin = (REAL *)malloc(sizeof(REAL) * N * C);
+  linear_bwd(dhin, G + lo->wq, lc->h, dq, P + lo->wq, N, C, Hq * D);
+  linear_bwd(tmp, G + lo->wk, lc->h, dk, P + lo->wk, N, C, Hkv * D);
+  for (int64_t i = 0; i < N * C; i++) dhin[i] = dhin[i] + tmp[i];
+  linear_bwd(tmp, G + lo->wv, lc->h, dvs, P + lo->wv, N, C, Hkv * D);
+  for (int64_t i = 0; i < N * C; i++) dhin[i] = dhin[i] + tmp[i];
+  free(dq); free(dk);
+  if (lo->has_ve) { /* model/train.go:369-397 */
+    REAL *dpre = (REAL *)malloc(sizeof(REAL) * N * Hkv);
+    for (int64_t n = 0; n < N; n++)
+      for (int hh = 0; hh < Hkv; hh++) {
+        int64_t row = n * Hkv + hh;
+        REAL sg = lc->vesig[row];
+        REAL scale = sg * R(VE_GATE_SCALE);
+        double dot = 0;
+        for (int d = 0; d < D; d++) {
+          REAL gvd = dvs[row * D + d];
+          /* value_embeds gradient scatter (Embedding.Backward, linear.go:90-104) */
+          G[lo->ve + (int64_t)ids[n] * Hkv * D + hh * D + d] += gvd * scale;
+          dot += (double)gvd * (double)lc->ve[row * D + d];
+        }
+        REAL gsig = R(dot) * R(VE_GATE_SCALE);
+        dpre[row] = gsig * sg * (R(1) - sg);
+      }
+    REAL *slice = (REAL *)malloc(sizeof(REAL) * N * VE_GATE_CH);
+    for (int64_t n = 0; n < N; n++) memcpy(slice + n * VE_GATE_CH, lc->h + n * C, sizeof(REAL) * VE_GATE_CH);
+    REAL *dslice = (REAL *)malloc(sizeof(REAL) * N * VE_GATE_CH);
+    linear_bwd(dslice, G + lo->wve, slice, dpre, P + lo->wve, N, VE_GATE_CH, Hkv);
+    for (int64_t n = 0; n < N; n++)
+      for (int c = 0; c < VE_GATE_CH; c++) dhin[n * C + c] += dslice[n * VE_GATE_CH + c];
+    free(dpre); free(slice); free(dslice);
+  }
+  free(dvs);
+  rmsnorm_backward_rows(gx, lc->xb, dhin, N, C);
+  for (int64_t i = 0; i < N * C; i++) gx[i] = gx[i] + gmid[i];
+  free(dhin); free(tmp); free(gmid); free(dh);
+}
+
+/* TrainBackward (train_transformer.go:147-156) from dL/d(softcapped logits). */
+static void train_backward(MODEL *m, train_ctx *ctx, const REAL *glogits, REAL *G) {
+  int B = ctx->B, T = ctx->T, C = m->C, V = m->V, PV = m->PV, L = m->L;
+  int64_t N = (int64_t)B * T;
+  const REAL *P = m->p;
+  /* SoftcapBackward (tensors/backward.go:108-116) and vocab padding */
+  REAL *gp = (REAL *)calloc((size_t)N * PV, sizeof(REAL));
+  REAL inv = R(1) / R(SOFTCAP);
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; n++)
+    for (int j = 0; j < V; j++) {
+      double s = (double)ctx->logits[n * V + j] * (double)inv;
+      gp[n * PV + j] = glogits[n * V + j] * R(1 - s * s);
+    }
+  REAL *g = (REAL *)malloc(sizeof(REAL) * N * C);
+  linear_bwd(g, G + m->lm, ctx->final_norm, gp, P + m->lm, N, C, PV);
+  free(gp);
+  /* trainBackwardFromHidden (train_transformer.go:176-265) */
+  REAL *ga = (REAL *)malloc(sizeof(REAL) * N * C);
+  rmsnorm_backward_rows(ga, ctx->final_pre, g, N, C);
+  REAL *gback = NULL;
+  if (ctx->backout) {
+    gback = (REAL *)malloc(sizeof(REAL) * N * C);
+    REAL nb = -P[m->bkl];
+    double dot = 0;
+    for (int64_t i = 0; i < N * C; i++) {
+      gback[i] = ga[i] * nb;
+      dot += (double)ga[i] * (double)(-ctx->backout[i]);
+    }
+    G[m->bkl] += R(dot);
+  }
+  int bkidx = L / 2;
+  REAL *gx0 = (REAL *)calloc((size_t)N * C, sizeof(REAL));
+  REAL *gb = (REAL *)malloc(sizeof(REAL) * N * C);
+  REAL *lg = (REAL *)malloc(sizeof(REAL) * N * C);
+  for (int l = L - 1; l >= 0; l--) {
+    memcpy(lg, ga, sizeof(REAL) * N * C);
+    if (l == bkidx && gback)
+      for (int64_t i = 0; i < N * C; i++) lg[i] = lg[i] + gback[i];
+    block_backward(m, &ctx->lc[l], &m->lay[l], ctx->ids, B, T, lg, gb, G);
+    REAL lr = P[m->rl + l], l0 = P[m->x0l + l];
+    double rdot = 0, idot = 0;
+    for (int64_t i = 0; i < N * C; i++) {
+      ga[i] = gb[i] * lr;
+      gx0[i] = gx0[i] + l0 * gb[i];
+      rdot += (double)gb[i] * (double)ctx->lc[l].xin[i];
+      idot += (double)gb[i] * (double)ctx->x0[i];
+    }
+    G[m->rl + l] += R(rdot);
+    G[m->x0l + l] += R(idot);
+  }
+  for (int64_t i = 0; i < N * C; i++) ga[i] = ga[i] + gx0[i];
+  /* smearBackward (train_transformer.go:269-305) */
+  REAL *ge = (REAL *)calloc((size_t)N * C, sizeof(REAL));
+  int Tm = T > 1 ? T - 1 : 1;
+  REAL *ggate = (REAL *)calloc((size_t)B * Tm, sizeof(REAL));
+  REAL lam = P[m->sml];
+  double dlam = 0;
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++) {
+      int64_t base = ((int64_t)b * T + t) * C;
+      if (t == 0) {
+        for (int c = 0; c < C; c++) ge[base + c] += ga[base + c];
+        continue;
+      }
+      int gi = b * (T - 1) + t - 1;
+      REAL sg = ctx->smsig[gi];
+      REAL gv = lam * sg;
+      int64_t pb = ((int64_t)b * T + t - 1) * C;
+      double gs = 0;
+      for (int c = 0; c < C; c++) {
+        ge[base + c] += ga[base + c];
+        ge[pb + c] += ga[base + c] * gv;
+        gs += (double)ga[base + c] * (double)ctx->embn[pb + c];
+      }
+      dlam += gs * (double)sg;
+      ggate[gi] = R(gs * (double)lam) * sg * (R(1) - sg);
+    }
+  G[m->sml] += R(dlam);
+  if (T > 1) {
+    int64_t NS = (int64_t)B * (T - 1);
+    REAL *slice = (REAL *)malloc(sizeof(REAL) * NS * SMEAR_CH);
+    REAL *gsl = (REAL *)malloc(sizeof(REAL) * NS * SMEAR_CH);
+    for (int b = 0; b < B; b++)
+      for (int t = 1; t < T; t++)
+        memcpy(slice + ((int64_t)b * (T - 1) + t - 1) * SMEAR_CH, ctx->embn + ((int64_t)b * T + t) * C, sizeof(REAL) * SMEAR_CH);
+    linear_bwd(gsl, G + m->smg, slice, ggate, P + m->smg, NS, SMEAR_CH, 1);
+    for (int b = 0; b < B; b++)
+      for (int t = 1; t < T; t++)
+        for (int c = 0; c < SMEAR_CH; c++)
+          ge[((int64_t)b * T + t) * C + c] += gsl[((int64_t)b * (T - 1) + t - 1) * SMEAR_CH + c];
+    free(slice); free(gsl);
+  }
+  /* embedding norm backward, then the wte scatter-add (linear.go:90-104) */
+  REAL *graw = (REAL *)malloc(sizeof(REAL) * N * C);
+  rmsnorm_backward_rows(graw, ctx->raw, ge, N, C);
+  for (int64_t n = 0; n < N; n++)
+    for (int c = 0; c < C; c++) G[m->wte + (int64_t)ctx->ids[n] * C + c] += graw[n * C + c];
+  free(graw); free(ge); free(ggate); free(gx0); free(gb); free(lg); free(ga); free(gback); free(g);
+}
+
+static train_ctx *train_forward(MODEL *m, const int32_t *ids, int B, int T) {
+  train_ctx *ctx = (train_ctx *)calloc(1, sizeof(train_ctx));
+  ctx->B = B;
+  ctx->T = T;
+  ctx->ids = (int32_t *)malloc(sizeof(int32_t) * B * T);
+  memcpy(ctx->ids, ids, sizeof(int32_t) * B * T);
+  ctx->logits = (REAL *)malloc(sizeof(REAL) * (int64_t)B * T * m->V);
+  forward_impl(m, ids, B, T, NULL, ctx->logits, ctx);
+  return ctx;
+}
+
+/* trainer/rl.go:14-60 with tensors/loss.go:16-46 and tensors/norm.go:5-10. */
+double FN(orc_pg_step)(MODEL *m, const int32_t *inputs, const int32_t *targets, int B, int T,
+                        const float *adv, float norm, REAL *nll, REAL *grads) {
+  int V = m->V;
+  int64_t N = (int64_t)B * T;
+  train_ctx *ctx = train_forward(m, inputs, B, T);
+  REAL *glog = (REAL *)calloc((size_t)N * V, sizeof(REAL));
+  double loss = 0;
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; n++) {
+    const REAL *row = ctx->logits + n * V;
+    REAL mx = row[0];
+    for (int j = 1; j < V; j++)
+      if (row[j] > mx) mx = row[j];
+    double s = 0;
+    for (int j = 0; j < V; j++) s += exp((double)(row[j] - mx));
+    int32_t tg = targets[n];
+    nll[n] = tg == -1 ? R(0) : mx + R(log(s)) - row[tg];
+    if (tg == -1) continue;
+    /* SoftmaxLastDim then (p - onehot) * adv/norm with a float32 scale */
+    REAL inv = R(1.0 / s);
+    REAL scale = R(adv[n / T]) / R(norm);
+    for (int j = 0; j < V; j++) {
+      REAL p = R(exp((double)(row[j] - mx))) * inv;
+      if (j == tg) p -= R(1);
+      glog[n * V + j] = p * scale;
+    }
+  }
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++) {
+      int64_t n = (int64_t)b * T + t;
+      if (targets[n] == -1) continue;
+      loss += (double)nll[n] * (double)adv[b] / (double)norm;
+    }
+  memset(grads, 0, sizeof(REAL) * m->total);
+  train_backward(m, ctx, glog, grads);
+  free(glog);
+  ctx_free(ctx, m->L);
+  return loss;
+}
+
+/* Mean cross-entropy and its gradient (model/gradcheck_test.go:94-110). */
+double FN(orc_ce_loss)(MODEL *m, const int32_t *inputs, const int32_t *targets, int B, int T,
+                        REAL *grads) {
+  int V = m->V;
+  int64_t N = (int64_t)B * T;
+  train_ctx *ctx = train_forward(m, inputs, B, T);
+  int valid = 0;
+  for (int64_t n = 0; n < N; n++) valid += targets[n] != -1;
+  double sum = 0;
+  REAL *glog = grads ? (REAL *)calloc((size_t)N * V, sizeof(REAL)) : NULL;
+  for (int64_t n = 0; n < N; n++) {
+    if (targets[n] == -1) continue;
+    const REAL *row = ctx->logits + n * V;
+    REAL mx = row[0];
+    for (int j = 1; j < V; j++)
+      if (row[j] > mx) mx = row[j];
+    double s = 0;
+    for (int j = 0; j < V; j++) s += exp((double)(row[j] - mx));
+    sum += (double)(mx + R(log(s)) - row[targets[n]]);
+    if (glog) { /* tensors/backward.go:11-38 */
+      double invs = 1.0 / s;
+      REAL scale = R(1) / R(valid);
+      for (int j = 0; j < V; j++) {
+        REAL p = R(exp((double)(row[j] - mx)) * invs);
+        if (j == targets[n]) p -= R(1);
+        glog[n * V + j] = p * scale;
+      }
+    }
+  }
+  if (grads) {
+    memset(grads, 0, sizeof(REAL) * m->total);
+    train_backward(m, ctx, glog, grads);
+    free(glog);
+  }
+  ctx_free(ctx, m->L);
+  return valid ? sum / valid : 0;
+}
+
+/* ---- generation (inference/engine.go:112-369) -------------------------- */
+enum { TOK_BOS = 256, TOK_ASSISTANT_END = 260, TOK_TOOL_START = 261, TOK_TOOL_END = 262,
+       TOK_TOOL_OUT_START = 263, TOK_TOOL_OUT_END = 264 };
+
+/* tokenizer.Decode for the byte-level tokenizer (tokenizer/tokenizer.go:110-118,
+ * tokenizer/special.go:19-31): bytes, then special names, unknown ids skipped. */
+static const char *SPECIAL_NAMES[11] = {
+    "<|bos|>", "<|user_start|>", "<|user_end|>", "<|assistant_start|>", "<|assistant_end|>",
+    "<|tool_start|>", "<|tool_end|>", "<|tool_output_start|>", "<|tool_output_end|>",
+    "<|think_start|>", "<|think_end|>"};
+
+typedef struct {
+  int *forced, nforced, cap_forced;
+  int in_tool, *tool, ntool, cap_tool;
+  int completed;
+} row_state;
+
+void FN(orc_generate_batch)(MODEL *m, const int32_t *prompt, int P, int S, int max_tokens,
+                            float temperature, int top_k, uint64_t seed, int32_t *rows_out,
+                            int32_t *lens_out) {
+  int V = m->V;
+  kvcache *pre = cache_new(m, 1, P);
+  REAL *lg = (REAL *)malloc(sizeof(REAL) * (int64_t)P * V);
+  forward_impl(m, prompt, 1, P, pre, lg, NULL);
+  float *logits = (float *)malloc(sizeof(float) * (int64_t)S * V);
+  for (int s = 0; s < S; s++)
+    for (int j = 0; j < V; j++) logits[(int64_t)s * V + j] = (float)lg[(int64_t)(P - 1) * V + j];
+  free(lg);
+  int cache_len = P + (max_tokens > 0 ? max_tokens : 0);
+  kvcache *dec = cache_new(m, S, cache_len);
+  prefill_from(m, dec, pre);
+  cache_free(pre);
+  row_state *st = (row_state *)calloc(S, sizeof(row_state));
+  int W = P + max_tokens;
+  int done_rows = 0;
+  int *completed_out = (int *)calloc(S, sizeof(int));
+  for (int s = 0; s < S; s++) {
+    memcpy(rows_out + (int64_t)s * W, prompt, sizeof(int32_t) * P);
+    lens_out[s] = P;
+  }
+  orc_pcg rng;
+  orc_rng_new(&rng, seed);
+  int32_t *next = (int32_t *)malloc(sizeof(int32_t) * S);
+  int32_t *col = (int32_t *)malloc(sizeof(int32_t) * S);
+  REAL *lg1 = (REAL *)malloc(sizeof(REAL) * (int64_t)S * V);
+  int generated = 0;
+  for (;;) {
+    if (max_tokens > 0 && generated >= max_tokens) break;
+    int all = 1;
+    for (int s = 0; s < S; s++)
+      if (!st[s].completed) { all = 0; break; }
+    if (all) break;
+    orc_sample_next_token(logits, S, V, &rng, temperature, top_k, next);
+    for (int s = 0; s < S; s++) {
+      row_state *r = &st[s];
+      int tok;
+      if (r->nforced > 0) {
+        tok = r->forced[0];
+        memmove(r->forced, r->forced + 1, sizeof(int) * (r->nforced - 1));
+        r->nforced--;
+      } else
+        tok = next[s];
+      col[s] = tok;
+      if (tok == TOK_ASSISTANT_END || tok == TOK_BOS) r->completed = 1;
+      if (tok == TOK_TOOL_START) {
+        r->in_tool = 1;
+        r->ntool = 0;
+      } else if (tok == TOK_TOOL_END && r->in_tool) {
+        r->in_tool = 0;
+        if (r->ntool > 0) {
+          char expr[8192];
+          size_t e = 0;
+          for (int i = 0; i < r->ntool; i++) {
+            int id = r->tool[i];
+            if (id >= 0 && id < 256) { if (e + 1 < sizeof expr) expr[e++] = (char)id; }
+            else if (id >= 256 && id < 267) {
+              const char *nm = SPECIAL_NAMES[id - 256];
+              for (size_t k = 0; nm[k] && e + 1 < sizeof expr; k++) expr[e++] = nm[k];
+            }
+          }
+          expr[e] = 0;
+          char res[512];
+          if (orc_calculator(expr, res, sizeof res)) {
+            size_t rl = strlen(res);
+            int need = r->nforced + (int)rl + 2;
+            if (need > r->cap_forced) {
+              r->cap_forced = need * 2;
+              r->forced = (int *)realloc(r->forced, sizeof(int) * r->cap_forced);
+            }
+            r->forced[r->nforced++] = TOK_TOOL_OUT_START;
+            for (size_t k = 0; k < rl; k++) r->forced[r->nforced++] = (unsigned char)res[k];
+            r->forced[r->nforced++] = TOK_TOOL_OUT_END;
+          }
+        }
+        r->ntool = 0;
+      } else if (r->in_tool) {
+        if (r->ntool + 1 > r->cap_tool) {
+          r->cap_tool = (r->ntool + 1) * 2;
+          r->tool = (int *)realloc(r->tool, sizeof(int) * r->cap_tool);
+        }
+        r->tool[r->ntool++] = tok;
+      }
+    }
+    /* GenerateBatchWith's yield (engine.go:349-366) */
+    for (int s = 0; s < S; s++) {
+      if (completed_out[s]) continue;
+      if (col[s] == TOK_ASSISTANT_END || col[s] == TOK_BOS) {
+        completed_out[s] = 1;
+        done_rows++;
+      } else
+        rows_out[(int64_t)s * W + lens_out[s]++] = col[s];
+    }
+    if (done_rows == S) break;
+    generated++;
+    forward_impl(m, col, S, 1, dec, lg1, NULL);
+    for (int64_t i = 0; i < (int64_t)S * V; i++) logits[i] = (float)lg1[i];
+  }
+  for (int s = 0; s < S; s++) { free(st[s].forced); free(st[s].tool); }
+  free(st); free(completed_out); free(next); free(col); free(lg1); free(logits);
+  cache_free(dec);
+}
+
+/* cmd/chat_rl/main.go:101-183 for G effort groups (seeds given), with the
+ * rewards supplied by the caller. */
+double FN(orc_rl_step)(MODEL *m, const int32_t *prompts, int G, int P, int S, int max_tokens,
+                        float temperature, int top_k, const uint64_t *seeds, const float *rewards,
+                        int32_t *rows_out, int32_t *lens_out, float *adv_out,
+                        int32_t *max_len_out, int32_t *inputs_out, int32_t *targets_out,
+                        REAL *nll, REAL *grads) {
+  int W = P + max_tokens, Bt = G * S;
+  for (int g = 0; g < G; g++)
+    FN(orc_generate_batch)(m, prompts + (int64_t)g * P, P, S, max_tokens, temperature, top_k,
+                           seeds[g], rows_out + (int64_t)g * S * W, lens_out + g * S);
+  /* group-mean advantages in float32 (main.go:139-155) */
+  for (int g = 0; g < G; g++) {
+    float mean = 0;
+    for (int i = 0; i < S; i++) mean += rewards[g * S + i];
+    mean /= (float)S;
+    for (int i = 0; i < S; i++) adv_out[g * S + i] = rewards[g * S + i] - mean;
+  }
+  int maxLen = 0;
+  for (int b = 0; b < Bt; b++)
+    if (lens_out[b] > maxLen) maxLen = lens_out[b];
+  *max_len_out = maxLen;
+  int T = maxLen - 1;
+  for (int b = 0; b < Bt; b++) {
+    for (int t = 0; t < T; t++) {
+      int32_t in = t < lens_out[b] ? rows_out[(int64_t)b * W + t] : TOK_ASSISTANT_END;
+      int32_t tg = t + 1 < lens_out[b] ? rows_out[(int64_t)b * W + t + 1] : TOK_ASSISTANT_END;
+      if (t < P) tg = -1;
+      inputs_out[(int64_t)b * T + t] = in;
+      targets_out[(int64_t)b * T + t] = tg;
+    }
+  }
+  if (T < 1) return 0;
+  return FN(orc_pg_step)(m, inputs_out, targets_out, Bt, T, adv_out, (float)maxLen, nll, grads);
+}

@@ -1,0 +1,301 @@
+"""ctypes wrapper over oracle/liboracle.so, the CPU restatement of gonano's
+RL-step arithmetic.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg as the checker.  The product never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+class OrcConfig(C.Structure):
+    _fields_ = [
+        ("sequence_len", C.c_int32),
+        ("vocab_size", C.c_int32),
+        ("n_layer", C.c_int32),
+        ("n_head", C.c_int32),
+        ("n_kv_head", C.c_int32),
+        ("n_embd", C.c_int32),
+        ("rotary_dims", C.c_int32),
+        ("window_pattern", C.c_char * 16),
+    ]
+
+
+class OrcPCG(C.Structure):
+    _fields_ = [("hi", C.c_uint64), ("lo", C.c_uint64)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        build()
+    L = C.CDLL(LIB_PATH)
+    v = None
+    sig = {
+        "orc_add": (v, [_f32p, _f32p, _f32p, _i64]),
+        "orc_subtract": (v, [_f32p, _f32p, _f32p, _i64]),
+        "orc_multiply": (v, [_f32p, _f32p, _f32p, _i64]),
+        "orc_divide": (v, [_f32p, _f32p, _f32p, _i64]),
+        "orc_scale": (v, [_f32p, _f32p, C.c_float, _i64]),
+        "orc_add_scaled": (v, [_f32p, _f32p, _f32p, C.c_float, _i64]),
+        "orc_negate": (v, [_f32p, _f32p, _i64]),
+        "orc_abs": (v, [_f32p, _f32p, _i64]),
+        "orc_square": (v, [_f32p, _f32p, _i64]),
+        "orc_relu_squared": (v, [_f32p, _f32p, _i64]),
+        "orc_swiglu": (v, [_f32p, _f32p, _f32p, C.c_float, _i64]),
+        "orc_swiglu_backward": (v, [_f32p, _f32p, _f32p, _f32p, _f32p, C.c_float, _i64]),
+        "orc_exp": (v, [_f32p, _f32p, _i64]),
+        "orc_sigmoid": (v, [_f32p, _f32p, _i64]),
+        "orc_tanh": (v, [_f32p, _f32p, _i64]),
+        "orc_rsqrt": (v, [_f32p, _f32p, _i64]),
+        "orc_sum": (C.c_float, [_f32p, _i64]),
+        "orc_max": (C.c_float, [_f32p, _i64]),
+        "orc_argmax": (C.c_int64, [_f32p, _i64]),
+        "orc_matmul": (v, [_f32p, _f32p, _f32p, _i64, _i64, _i64]),
+        "orc_matmul_transposed": (v, [_f32p, _f32p, _f32p, _i64, _i64, _i64]),
+        "orc_dot": (C.c_float, [_f32p, _f32p, _i64]),
+        "orc_softmax_last_dim": (v, [_f32p, _f32p, _i64, _i64]),
+        "orc_rmsnorm_last_dim": (v, [_f32p, _f32p, _i64, _i64, C.c_float]),
+        "orc_indexer_scores": (v, [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]),
+        "orc_indexer_block_max": (v, [_f32p, _f32p, _i64, _i64, _i64]),
+        "orc_topk_indices": (v, [_i32p, _f32p, _i64, _i64, _i64]),
+        "orc_moe_gate_topk": (v, [_f32p, _f32p, _f32p, _i32p, _f32p, _i64, _i64, _i64]),
+        "orc_grouped_matmul_transposed": (v, [_f32p, _f32p, _f32p, _i32p, _i64, _i64, _i64]),
+        "orc_attention_forward": (v, [_f32p, _f32p, _f32p, _f32p, C.c_void_p, C.c_void_p, _i64,
+                                      _i64, _i64, _i64, _i64, _i64]),
+        "orc_attention_backward": (v, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, C.c_void_p,
+                                       C.c_void_p, _i64, _f32p, _f32p, _f32p, _i64, _i64, _i64,
+                                       _i64, _i64]),
+        "orc_attention_forward_split": (v, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, C.c_void_p,
+                                            _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+        "orc_attention_combine": (v, [_f32p, _f32p, _f32p, _i64, _f32p, C.c_void_p, _i64, _i64]),
+        "orc_rng_new": (v, [C.POINTER(OrcPCG), C.c_uint64]),
+        "orc_rng_uint64": (C.c_uint64, [C.POINTER(OrcPCG)]),
+        "orc_rng_float32": (C.c_float, [C.POINTER(OrcPCG)]),
+        "orc_rng_advance": (v, [C.POINTER(OrcPCG), C.c_uint64, C.c_uint64]),
+        "orc_kth_largest": (C.c_float, [_f32p, _i64, _i64]),
+        "orc_sample_multinomial": (C.c_int64, [C.POINTER(OrcPCG), _f32p, _i64, C.c_float]),
+        "orc_sample_next_token": (v, [_f32p, _i64, _i64, C.POINTER(OrcPCG), C.c_float, _i64, _i32p]),
+        "orc_gumbel_from_uniform": (C.c_float, [C.c_float]),
+        "orc_calculator": (C.c_int, [C.c_char_p, C.c_char_p, C.c_size_t]),
+        "orc_param_count": (C.c_int, [C.POINTER(OrcConfig)]),
+        "orc_param_info": (C.c_int64, [C.POINTER(OrcConfig), C.c_int, C.c_char_p,
+                                       C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+        "orc_param_total": (C.c_int64, [C.POINTER(OrcConfig)]),
+        "orc_window_sizes": (v, [C.POINTER(OrcConfig), _i32p]),
+        "orc_num_threads": (C.c_int, []),
+    }
+    for sfx, fp in (("_f32", _f32p), ("_f64", _f64p)):
+        sig.update({
+            "orc_model_new" + sfx: (C.c_void_p, [C.POINTER(OrcConfig), fp]),
+            "orc_model_free" + sfx: (v, [C.c_void_p]),
+            "orc_forward" + sfx: (v, [C.c_void_p, _i32p, C.c_int, C.c_int, fp]),
+            "orc_forward_decode" + sfx: (v, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int, fp]),
+            "orc_pg_step" + sfx: (C.c_double, [C.c_void_p, _i32p, _i32p, C.c_int, C.c_int, _f32p,
+                                               C.c_float, fp, fp]),
+            "orc_ce_loss" + sfx: (C.c_double, [C.c_void_p, _i32p, _i32p, C.c_int, C.c_int,
+                                               C.c_void_p]),
+            "orc_generate_batch" + sfx: (v, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int,
+                                             C.c_float, C.c_int, C.c_uint64, _i32p, _i32p]),
+            "orc_rl_step" + sfx: (C.c_double, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int,
+                                               C.c_int, C.c_float, C.c_int, _u64p, _f32p, _i32p,
+                                               _i32p, _f32p, C.POINTER(C.c_int32), _i32p, _i32p,
+                                               fp, fp]),
+        })
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------------------
+# Config helpers (model/config.go restated for the test side)
+# ---------------------------------------------------------------------------
+@dataclass
+class ModelShape:
+    sequence_len: int
+    vocab_size: int
+    n_layer: int
+    n_head: int
+    n_kv_head: int
+    n_embd: int
+    rotary_dims: int
+    window_pattern: str
+
+    def orc(self) -> OrcConfig:
+        return OrcConfig(self.sequence_len, self.vocab_size, self.n_layer, self.n_head,
+                         self.n_kv_head, self.n_embd, self.rotary_dims,
+                         self.window_pattern.encode())
+
+
+def param_table(shape: ModelShape):
+    """[(name, rows, cols, offset)] in the sorted-name order."""
+    L = lib()
+    cfg = shape.orc()
+    out, off = [], 0
+    buf = C.create_string_buffer(96)
+    for i in range(L.orc_param_count(C.byref(cfg))):
+        r, c = C.c_int64(), C.c_int64()
+        n = L.orc_param_info(C.byref(cfg), i, buf, C.byref(r), C.byref(c))
+        out.append((buf.value.decode(), r.value, c.value, off))
+        off += n
+    return out
+
+
+def window_sizes(shape: ModelShape) -> np.ndarray:
+    out = np.zeros(shape.n_layer, np.int32)
+    lib().orc_window_sizes(C.byref(shape.orc()), out)
+    return out
+
+
+class OracleModel:
+    """Dense transformer oracle (float32 by default, float64 when dtype=np.float64)."""
+
+    def __init__(self, shape: ModelShape, params: np.ndarray, dtype=np.float32):
+        self.shape = shape
+        self.dtype = np.dtype(dtype)
+        self.sfx = "_f64" if self.dtype == np.float64 else "_f32"
+        self._cfg = shape.orc()
+        self.params = np.ascontiguousarray(params, dtype=self.dtype)
+        self.total = lib().orc_param_total(C.byref(self._cfg))
+        assert self.params.size == self.total, (self.params.size, self.total)
+        self._m = getattr(lib(), "orc_model_new" + self.sfx)(C.byref(self._cfg), self.params)
+
+    def __del__(self):
+        if getattr(self, "_m", None):
+            getattr(lib(), "orc_model_free" + self.sfx)(self._m)
+            self._m = None
+
+    def _fn(self, name):
+        return getattr(lib(), name + self.sfx)
+
+    def forward(self, ids: np.ndarray) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.int32)
+        B, T = ids.shape
+        out = np.zeros((B, T, self.shape.vocab_size), self.dtype)
+        self._fn("orc_forward")(self._m, ids, B, T, out)
+        return out
+
+    def forward_decode(self, ids: np.ndarray, chunk: int = 1) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.int32)
+        B, T = ids.shape
+        out = np.zeros((B, T, self.shape.vocab_size), self.dtype)
+        self._fn("orc_forward_decode")(self._m, ids, B, T, chunk, out)
+        return out
+
+    def pg_step(self, inputs, targets, adv, norm):
+        inputs = np.ascontiguousarray(inputs, np.int32)
+        targets = np.ascontiguousarray(targets, np.int32)
+        adv = np.ascontiguousarray(adv, np.float32)
+        B, T = inputs.shape
+        nll = np.zeros(B * T, self.dtype)
+        grads = np.zeros(self.total, self.dtype)
+        loss = self._fn("orc_pg_step")(self._m, inputs, targets, B, T, adv, float(norm), nll, grads)
+        return loss, nll.reshape(B, T), grads
+
+    def ce_loss(self, inputs, targets, want_grads=True):
+        inputs = np.ascontiguousarray(inputs, np.int32)
+        targets = np.ascontiguousarray(targets, np.int32)
+        B, T = inputs.shape
+        grads = np.zeros(self.total, self.dtype) if want_grads else None
+        loss = self._fn("orc_ce_loss")(self._m, inputs, targets, B, T, _ptr(grads))
+        return loss, grads
+
+    def generate_batch(self, prompt, samples, max_tokens, temperature, top_k, seed):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        P = prompt.size
+        rows = np.zeros((samples, P + max_tokens), np.int32)
+        lens = np.zeros(samples, np.int32)
+        self._fn("orc_generate_batch")(self._m, prompt, P, samples, max_tokens,
+                                       float(temperature), top_k, seed, rows, lens)
+        return [rows[s, :lens[s]].copy() for s in range(samples)]
+
+    def rl_step(self, prompts, samples, max_tokens, temperature, top_k, seeds, rewards):
+        prompts = np.ascontiguousarray(prompts, np.int32)
+        G, P = prompts.shape
+        Bt = G * samples
+        W = P + max_tokens
+        rows = np.zeros((Bt, W), np.int32)
+        lens = np.zeros(Bt, np.int32)
+        adv = np.zeros(Bt, np.float32)
+        max_len = C.c_int32()
+        inputs = np.zeros(Bt * W, np.int32)
+        targets = np.zeros(Bt * W, np.int32)
+        nll = np.zeros(Bt * W, self.dtype)
+        grads = np.zeros(self.total, self.dtype)
+        loss = self._fn("orc_rl_step")(
+            self._m, prompts, G, P, samples, max_tokens, float(temperature), top_k,
+            np.ascontiguousarray(seeds, np.uint64), np.ascontiguousarray(rewards, np.float32),
+            rows, lens, adv, C.byref(max_len), inputs, targets, nll, grads)
+        T = max_len.value - 1
+        return dict(loss=loss, rows=[rows[b, :lens[b]].copy() for b in range(Bt)], lens=lens,
+                    adv=adv, max_len=max_len.value, inputs=inputs[:Bt * T].reshape(Bt, T),
+                    targets=targets[:Bt * T].reshape(Bt, T), nll=nll[:Bt * T].reshape(Bt, T),
+                    grads=grads)
+
+
+class GoRNG:
+    """tensors.RNG: Go's math/rand/v2 PCG seeded as NewPCG(s, s^0x9e37...)."""
+
+    def __init__(self, seed: int):
+        self.state = OrcPCG()
+        lib().orc_rng_new(C.byref(self.state), C.c_uint64(seed))
+
+    def uint64(self) -> int:
+        return lib().orc_rng_uint64(C.byref(self.state))
+
+    def float32(self) -> float:
+        return lib().orc_rng_float32(C.byref(self.state))
+
+    def advance(self, n: int) -> None:
+        lib().orc_rng_advance(C.byref(self.state), C.c_uint64(n >> 64),
+                              C.c_uint64(n & ((1 << 64) - 1)))
+
+    @property
+    def hi_lo(self):
+        return self.state.hi, self.state.lo
+
+
+def sample_next_token(logits: np.ndarray, rng: GoRNG, temperature: float, top_k: int):
+    logits = np.ascontiguousarray(logits, np.float32)
+    rows, vocab = logits.shape
+    out = np.zeros(rows, np.int32)
+    lib().orc_sample_next_token(logits, rows, vocab, C.byref(rng.state), float(temperature),
+                                top_k, out)
+    return out
+
+
+def calculator(expr: str):
+    out = C.create_string_buffer(512)
+    ok = lib().orc_calculator(expr.encode(), out, 512)
+    return out.value.decode() if ok else None
