@@ -1,0 +1,174 @@
+"""RL-step benchmark on one MI355X (BASELINE.json metric: rollout tokens/sec
+and RL-step ms at the d12 dense config, plus the achieved fraction of the
+fp32-MFMA and HBM peaks).
+
+A step is one cmd/chat_rl step without the optimizer: 16 prompts x 16
+rollouts x 256 new tokens, the teacher-forced log-prob recompute over the
+padded [256, 511] batch, group-mean advantages of Bernoulli(0.3) rewards and
+the PG loss forward/backward over the full 65536 vocabulary.  Inputs are
+synthetic (uniform prompt ids, InitWeights-distributed random weights) and
+resident in HBM before the timed region.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config d12|d2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+METRIC = "rollout tokens/sec + RL-step ms at d12 on 1 MI355X; % of HBM/fp32-MFMA peak"
+
+WORKLOADS = {
+    # name: (config factory, groups, prompt len, samples, new tokens, temperature, reward p)
+    "d12": ("dense_d12", 16, 256, 16, 256, 1.0, 0.3),
+    "d2": ("dense_d2", 4, 32, 8, 24, 1.0, 0.3),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(cfg, w, prompts, seconds_hint: float) -> dict:
+    """The oracle (a scalar C port of the reference's arithmetic, float64
+    accumulation, OpenMP over rows) generating rollouts on the same d12
+    weights for a bounded sample."""
+    from oracle import oracle as O
+    shape = O.ModelShape(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head,
+                         cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern)
+    m = O.OracleModel(shape, w)
+    S, N, P = 8, 8, 16
+    t0 = time.perf_counter()
+    rows = m.generate_batch(prompts[0, :P], S, N, 1.0, 50, 0)
+    dt = time.perf_counter() - t0
+    toks = sum(len(r) - P for r in rows)
+    return {"value": toks / dt, "unit": "tokens/s", "cores": int(O.lib().orc_num_threads()),
+            "kind": "port",
+            "sample": f"oracle rollout of 1 prompt of {P} tokens x {S} samples x {N} new tokens "
+                      f"on the d12 weights ({toks} tokens in {dt:.1f} s)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="d12", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs the RL step on a single MI355X "
+              "(see DESIGN.md for how the step shards across GPUs); use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    from gonano_amd import config as G
+    from gonano_amd.session import Session
+
+    factory, groups, P, S, N, temp, reward_p = WORKLOADS[args.config]
+    cfg = getattr(G, factory)()
+    log(f"bench: config {args.config} {cfg}")
+    w = G.init_weights(cfg, seed=0)
+    prompts = np.random.default_rng(1).integers(0, cfg.vocab_size, (groups, P)).astype(np.int32)
+    reward_rng = np.random.default_rng(2)
+
+    sess = Session(cfg)
+    sess.set_params(w)
+    sess.set_timing(True)
+
+    def step(i: int):
+        seeds = np.array([i * 1000 + g for g in range(groups)], np.uint64)
+        rewards = (reward_rng.random(groups * S) < reward_p).astype(np.float32)
+        sess.zero_grad()
+        t0 = time.perf_counter()
+        out = sess.rl_step(prompts, S, N, temp, 50, seeds, rewards)
+        wall = time.perf_counter() - t0
+        return out, wall, sess.timing()
+
+    for i in range(args.warmup):
+        out, wall, t = step(i)
+        log(f"bench: warmup {i}: {wall * 1e3:.1f} ms (rollout {t['rollout_ms']:.1f} ms, "
+            f"train {t['train_ms']:.1f} ms), loss {out['loss']:.6f}")
+    walls, roll_ms, train_ms, toks = [], [], [], 0
+    gemm_ms = gemm_fl = attn_ms = attn_b = 0.0
+    gemm_n = attn_n = 0
+    for i in range(args.steps):
+        out, wall, t = step(args.warmup + i)
+        walls.append(wall)
+        roll_ms.append(t["rollout_ms"])
+        train_ms.append(t["train_ms"])
+        toks += int(np.sum(out["lens"] - P))
+        gemm_ms += t["gemm_ms"]; gemm_fl += t["gemm_flops"]; gemm_n += t["gemm_launches"]
+        attn_ms += t["decode_attn_ms"]; attn_b += t["decode_attn_bytes"]
+        attn_n += t["decode_attn_launches"]
+        log(f"bench: step {i}: {wall * 1e3:.1f} ms (rollout {t['rollout_ms']:.1f} ms, "
+            f"train {t['train_ms']:.1f} ms), loss {out['loss']:.6f}, max_len {out['max_len']}")
+    sess.close()
+
+    rollout_s = sum(roll_ms) / 1e3
+    value = toks / rollout_s
+    ms_step = 1e3 * sum(walls) / len(walls)
+    gemm_tflops = gemm_fl / (gemm_ms / 1e3) / 1e12 if gemm_ms else 0.0
+    attn_gbs = attn_b / (attn_ms / 1e3) / 1e9 if attn_ms else 0.0
+    res = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (uniform prompt ids, InitWeights-distributed random weights, "
+                "Bernoulli rewards)",
+        "config": {
+            "workload": f"{args.config} dense RL step: {groups} prompts x {S} samples, "
+                        f"{P} prompt + {N} new tokens, T={temp}, top-k 50, "
+                        f"Bernoulli({reward_p}) rewards, recompute + PG fwd/bwd, no optimizer",
+            "model": f"dense depth {cfg.n_layer} d_model {cfg.n_embd} heads {cfg.n_head}/"
+                     f"{cfg.n_kv_head} vocab {cfg.vocab_size}",
+            "rollouts": groups * S, "global_batch": groups * S, "seq_len": P + N,
+            "parallelism": "single GPU",
+            "rollout_ms": round(sum(roll_ms) / len(roll_ms), 2),
+            "rl_step_ms": round(ms_step, 2),
+            "train_ms": round(sum(train_ms) / len(train_ms), 2),
+        },
+        "roofline": {
+            "kernel": "gemm_kernel (fp32 MFMA, recompute + PG backward)",
+            "bound": "mfma",
+            "achieved": round(gemm_tflops, 2),
+            "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "launches": gemm_n,
+            "avg_launch_ms": round(gemm_ms / max(gemm_n, 1), 4),
+        },
+        "decode_attention": {
+            "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "launches": attn_n,
+            "avg_launch_ms": round(attn_ms / max(attn_n, 1), 5),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("bench: timing the CPU oracle on a bounded sample")
+        res["cpu_baseline"] = cpu_baseline(cfg, w, prompts, 20.0)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

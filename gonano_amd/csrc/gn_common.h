@@ -1,0 +1,110 @@
+// gn_common.h - shared host/device helpers for libgnhip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/gonano_hip.h"
+
+namespace gn {
+
+// A failed HIP call or a rejected argument throws; every extern "C" entry
+// point catches, records the message for gn_last_error() and returns a
+// gn_status code (the Go wrapper turns it into a panic, matching the
+// reference's panic-on-misuse convention).
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void set_last_error(const std::string& msg);
+
+#define GN_HIP(expr)                                                                   \
+  do {                                                                                 \
+    hipError_t _e = (expr);                                                            \
+    if (_e != hipSuccess)                                                              \
+      throw ::gn::Error(_e == hipErrorOutOfMemory ? GN_ERR_OOM : GN_ERR_HIP,           \
+                        std::string(#expr) + ": " + hipGetErrorString(_e));            \
+  } while (0)
+
+#define GN_CHECK(cond, msg)                                                            \
+  do {                                                                                 \
+    if (!(cond)) throw ::gn::Error(GN_ERR_INVALID, std::string(msg));                  \
+  } while (0)
+
+// Runs body, mapping exceptions to status codes.
+template <class F>
+int guard(F&& body) {
+  try {
+    body();
+    return GN_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host allocation failed");
+    return GN_ERR_OOM;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return GN_ERR_INTERNAL;
+  }
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ double warp_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Block-wide reductions for blockDim.x a multiple of 64 (<= 1024). `scratch`
+// must hold blockDim.x/64 values; the result is broadcast to every thread.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* scratch) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  T t = 0;
+  for (int i = 0; i < nw; i++) t += scratch[i];
+  return t;
+}
+__device__ __forceinline__ float block_max(float v, float* scratch) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = warp_max(v);
+  __syncthreads();
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  float t = scratch[0];
+  for (int i = 1; i < nw; i++) t = fmaxf(t, scratch[i]);
+  return t;
+}
+
+// Softcap (model/transformer.go:11, tensors/math.go:38-45):
+// 15 * tanh(y * float32(1/15)).
+__device__ __forceinline__ float softcap15(float y) {
+  const float inv = 1.0f / 15.0f;
+  return tanhf(y * inv) * 15.0f;
+}
+
+}  // namespace gn

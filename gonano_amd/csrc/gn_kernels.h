@@ -1,0 +1,123 @@
+// gn_kernels.h - launchers shared between the backend primitives and the
+// session.  All launchers enqueue on the given stream and never synchronize.
+#pragma once
+
+#include <algorithm>
+#include <map>
+#include <string>
+
+#include "gn_common.h"
+
+namespace gn {
+
+// ---------------------------------------------------------------------------
+// Grow-only named device buffers.  Growing synchronizes the owning stream
+// first so no in-flight kernel still reads the old allocation.
+// ---------------------------------------------------------------------------
+class DeviceArena {
+ public:
+  explicit DeviceArena(hipStream_t s = nullptr) : stream_(s) {}
+  ~DeviceArena() { release(); }
+  DeviceArena(const DeviceArena&) = delete;
+  DeviceArena& operator=(const DeviceArena&) = delete;
+  void set_stream(hipStream_t s) { stream_ = s; }
+
+  template <typename T>
+  T* get(const std::string& name, size_t count) {
+    size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    auto it = bufs_.find(name);
+    if (it != bufs_.end() && it->second.bytes >= bytes) return static_cast<T*>(it->second.ptr);
+    if (it != bufs_.end()) {
+      GN_HIP(hipStreamSynchronize(stream_));
+      GN_HIP(hipFree(it->second.ptr));
+      bufs_.erase(it);
+    }
+    void* p = nullptr;
+    GN_HIP(hipMalloc(&p, bytes));
+    bufs_[name] = Buf{p, bytes};
+    return static_cast<T*>(p);
+  }
+  void release() {
+    for (auto& kv : bufs_) (void)hipFree(kv.second.ptr);
+    bufs_.clear();
+  }
+  size_t bytes() const {
+    size_t t = 0;
+    for (auto& kv : bufs_) t += kv.second.bytes;
+    return t;
+  }
+
+ private:
+  struct Buf {
+    void* ptr;
+    size_t bytes;
+  };
+  hipStream_t stream_;
+  std::map<std::string, Buf> bufs_;
+};
+
+// ---------------------------------------------------------------------------
+// GEMM
+// ---------------------------------------------------------------------------
+enum GemmEpilogue {
+  EPI_STORE = 0,      // C = alpha * acc
+  EPI_ADD_SRC = 1,    // C = acc + aux            (residual add; aux may alias C)
+  EPI_ACCUM = 2,      // C += acc                 (gradient accumulation)
+  EPI_SOFTCAP = 3,    // C = 15 tanh(acc / 15)    (logits)
+  EPI_RELU2_SAVE = 4, // aux_out = acc, C = relu(acc)^2
+  EPI_DRELU2 = 5,     // C = acc * 2 * relu(aux)  (ReluSquared backward)
+  EPI_PARTIAL = 6     // internal: split-K partial
+};
+
+struct GemmDesc {
+  int M = 0, N = 0, K = 0;
+  const float* A = nullptr;
+  int64_t lda = 0;
+  bool a_kcontig = true;  // A(m,k) = a_kcontig ? A[m*lda+k] : A[k*lda+m]
+  const float* B = nullptr;
+  int64_t ldb = 0;
+  bool b_kcontig = true;  // B(n,k) = b_kcontig ? B[n*ldb+k] : B[k*ldb+n]
+  float* C = nullptr;
+  int64_t ldc = 0;
+  int epi = EPI_STORE;
+  const float* aux = nullptr;
+  float* aux_out = nullptr;
+  int64_t ldaux = 0;
+  float alpha = 1.f;
+  int force_splits = 0;
+};
+
+void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);
+
+// y[rows, out] = x[rows, in] . W[out, in]^T   (model/layers/linear.go:32-40)
+inline GemmDesc linear_fwd_desc(const float* x, const float* W, float* y, int rows, int in,
+                                int out, int epi = EPI_STORE) {
+  GemmDesc d;
+  d.M = rows; d.N = out; d.K = in;
+  d.A = x; d.lda = in; d.a_kcontig = true;
+  d.B = W; d.ldb = in; d.b_kcontig = true;
+  d.C = y; d.ldc = out; d.epi = epi;
+  return d;
+}
+// dx[rows, in] = g[rows, out] . W[out, in]    (linear.go:51)
+inline GemmDesc linear_dx_desc(const float* g, const float* W, float* dx, int rows, int in,
+                               int out, int epi = EPI_STORE) {
+  GemmDesc d;
+  d.M = rows; d.N = in; d.K = out;
+  d.A = g; d.lda = out; d.a_kcontig = true;
+  d.B = W; d.ldb = in; d.b_kcontig = false;
+  d.C = dx; d.ldc = in; d.epi = epi;
+  return d;
+}
+// dW[out, in] += g[rows, out]^T . x[rows, in]  (linear.go:49-50)
+inline GemmDesc linear_dw_desc(const float* g, const float* x, float* dW, int rows, int in,
+                               int out) {
+  GemmDesc d;
+  d.M = out; d.N = in; d.K = rows;
+  d.A = g; d.lda = out; d.a_kcontig = false;
+  d.B = x; d.ldb = in; d.b_kcontig = false;
+  d.C = dW; d.ldc = in; d.epi = EPI_ACCUM;
+  return d;
+}
+
+}  // namespace gn

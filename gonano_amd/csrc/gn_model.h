@@ -1,0 +1,139 @@
+// gn_model.h - launchers of the transformer kernels used by the session.
+#pragma once
+
+#include "gn_kernels.h"
+
+namespace gn {
+
+// ---- embedding / norms --------------------------------------------------
+void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, const float* lam,
+                        int B, int T, int C, float* raw, float* embn, float* smsig, float* x,
+                        hipStream_t st);
+void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg, const float* lam,
+                         int rows, int C, float* prev, float* x, float* x0, hipStream_t st);
+void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
+                       int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st);
+void launch_norm_rows(const float* x, const float* back, const float* lam, int64_t rows, int C,
+                      float* pre, float* y, hipStream_t st);
+
+// ---- q/k/v post-processing ----------------------------------------------
+struct QkvPostArgs {
+  const float* qkv;
+  const float* h;
+  const int32_t* ids;
+  const float* ve;
+  const float* wve;
+  const float* cosT;
+  const float* sinT;
+  int C, Hq, Hkv, R, T;
+  int pos0;
+  float* qn;
+  float* kn;
+  float* vout;
+  float* qrot;
+  float* krot;
+  float* vesig;
+  float* kcache;
+  float* vcache;
+  int maxSeq;
+  int rows_per_seq;
+};
+void launch_qkv_post(const QkvPostArgs& a, int64_t rows, hipStream_t st);
+void launch_replicate_kv(const float* src, float* dst, int G, int S, int Hkv, int P, int maxSrc,
+                         int maxDst, hipStream_t st);
+void launch_expand_last_rows(const float* src, float* dst, int G, int T, int S, int C,
+                             hipStream_t st);
+
+// ---- attention -----------------------------------------------------------
+struct DecodeAttnArgs {
+  const float* q;   // [rows, Hq, 128]
+  const float* kc;  // layer base of the K cache [rows][Hkv][maxSeq][128]
+  const float* vc;
+  float* part;      // [rows*Hkv][nsplit][Hq/Hkv][130]
+  float* o;         // [rows, Hq, 128]
+  int rows, Hq, Hkv, maxSeq;
+  int kstart, kend; // keys [kstart, kend)
+  int nsplit;       // set by the launcher
+};
+void launch_decode_attention(DecodeAttnArgs a, hipStream_t st);
+
+struct FlashArgs {
+  const float* q;  // [B*T, Hq, 128]
+  const float* k;  // [B*T, Hkv, 128]
+  const float* v;
+  float* o;        // [B*T, Hq, 128]
+  float* lse;      // [B*T, Hq] or null
+  int B, T, Hq, Hkv, window;
+};
+void launch_flash_fwd(const FlashArgs& a, hipStream_t st);
+
+struct FlashBwdArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* o;
+  const float* dout;
+  const float* lse;
+  float* delta;  // [B*T, Hq] scratch
+  float* dq;     // [B*T, Hq, 128] (overwritten)
+  float* dk;     // [B*T, Hkv, 128] (overwritten)
+  float* dv;
+  int B, T, Hq, Hkv, window;
+};
+void launch_flash_bwd(const FlashBwdArgs& a, hipStream_t st);
+
+// ---- loss ----------------------------------------------------------------
+void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t rows,
+                         const int32_t* targets, const float* adv, int T, float norm, float* nll,
+                         double* loss_rows, hipStream_t st);
+void launch_sum_f64(const double* v, int64_t n, double* out, bool accumulate, hipStream_t st);
+
+// ---- backward helpers -----------------------------------------------------
+void launch_rmsnorm_bwd(const float* x, const float* g, const float* extra, int64_t rows, int C,
+                        float* out, hipStream_t st);
+void launch_dot_into_grad(const float* a, const float* b0, const float* b1, float sign, int64_t n,
+                          float* dst0, float* dst1, double* part, hipStream_t st);
+void launch_resid_bwd(const float* gb, const float* lr, const float* l0, int layer, float* gnext,
+                      float* gx0, int64_t n, hipStream_t st);
+void launch_axpy(float* out, const float* a, const float* b, const float* neg_scale_ptr, float s,
+                 int64_t n, hipStream_t st);
+
+struct QkvPostBwdArgs {
+  const float* dqn;
+  const float* dkn;
+  const float* dv;
+  const float* qrot;
+  const float* krot;
+  const float* vesig;
+  const float* ve;
+  const int32_t* ids;
+  const float* cosT;
+  const float* sinT;
+  int Hq, Hkv, R, T;
+  float* dqkv;
+  float* dpre;
+  float* gve;
+};
+void launch_qkv_post_bwd(const QkvPostBwdArgs& a, int64_t rows, hipStream_t st);
+void launch_ve_gate_bwd(const float* dpre, const float* h, const float* W, int C, int Hkv,
+                        int64_t N, float* dW, float* dh, double* part, hipStream_t st);
+void launch_smear_bwd(const float* ga, const float* embn, const float* smsig, const float* lam,
+                      const float* wsg, int B, int T, int C, float* ge, float* ggate,
+                      double* lam_rows, double* part, float* dwsg, float* dlam, hipStream_t st);
+void launch_embed_scatter(const float* g, const int32_t* ids, int C, int64_t N, float* gw,
+                          hipStream_t st);
+
+// ---- sampler (inference/sampler.go + tensors/random.go) -------------------
+struct SamplerArgs {
+  const float* logits;          // [rows, V]
+  int64_t ldl;
+  int rows, V;
+  int samples_per_group;        // S: row r is index r % S of group r / S
+  const uint64_t* base_states;  // [groups][2] {hi, lo}: each group's stream before this call
+  float temperature;
+  int top_k;
+  int32_t* out;                 // [rows]
+};
+void launch_sampler(const SamplerArgs& a, hipStream_t st);
+
+}  // namespace gn

@@ -1,0 +1,755 @@
+// gn_model.hip - fused row kernels of the dense transformer's forward and
+// backward (model/transformer.go, model/attention.go, model/train.go,
+// model/train_transformer.go).  Rows are tokens; one block per row unless
+// noted.  Head dimension is 128 (every BASELINE config).
+#include "gn_model.h"
+
+namespace gn {
+
+static constexpr float NORM_EPS = 1e-6f;  // model/attention.go:11
+static constexpr float QK_SCALE = 1.2f;   // model/attention.go:14
+static constexpr int VE_CH = 12;          // model/attention.go:18
+static constexpr float VE_SCALE = 3.f;    // model/attention.go:21
+static constexpr int SMEAR_CH = 24;       // model/helpers.go:7
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
+// Sum of a per-thread value over a 256-thread block (float).
+__device__ __forceinline__ float bsum256(float v, float* sc) { return block_sum<float>(v, sc); }
+
+// ---------------------------------------------------------------------------
+// Embedding + RMSNorm + smear gate (model/transformer.go:255-301,
+// model/train_transformer.go:73-87).  Writes raw (optional), embn, and for
+// t >= 1 the smear sigmoid.  ids [B*T].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void embed_norm_kernel(const int32_t* __restrict__ ids,
+                                                         const float* __restrict__ wte, int C,
+                                                         int T, const float* __restrict__ wsg,
+                                                         float* __restrict__ raw,
+                                                         float* __restrict__ embn,
+                                                         float* __restrict__ smsig) {
+  __shared__ float sc[4];
+  const int64_t n = blockIdx.x;
+  const int t = (int)(n % T);
+  const float* src = wte + (int64_t)ids[n] * C;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < C; c += 256) {
+    float v = src[c];
+    if (raw) raw[n * C + c] = v;
+    ss += v * v;
+  }
+  ss = bsum256(ss, sc);
+  const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
+  for (int c = threadIdx.x; c < C; c += 256) embn[n * C + c] = src[c] * inv;
+  if (t >= 1 && smsig) {
+    // gate = sigmoid(embn[:24] . w) (smearGate Linear 24 -> 1)
+    float p = 0.f;
+    if (threadIdx.x < SMEAR_CH) p = src[threadIdx.x] * inv * wsg[threadIdx.x];
+    p = warp_sum(threadIdx.x < 64 ? p : 0.f);
+    if (threadIdx.x == 0) smsig[(n / T) * (T - 1) + t - 1] = sigmoidf_(p);
+  }
+}
+
+// x[t] = embn[t] + lambda * smsig[t-1] * embn[t-1] (helpers.go:35-48; reads the
+// pre-smear embedding of the previous row).
+__global__ void smear_apply_kernel(const float* __restrict__ embn, const float* __restrict__ smsig,
+                                   const float* __restrict__ lam, float* __restrict__ x, int C,
+                                   int T, int64_t total) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int64_t n = i / C;
+  int t = (int)(n % T);
+  float v = embn[i];
+  if (t >= 1) {
+    float g = smsig[(n / T) * (T - 1) + t - 1] * lam[0];
+    v += g * embn[i - C];
+  }
+  x[i] = v;
+}
+
+void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, const float* lam,
+                        int B, int T, int C, float* raw, float* embn, float* smsig, float* x,
+                        hipStream_t st) {
+  int64_t N = (int64_t)B * T;
+  hipLaunchKernelGGL(embed_norm_kernel, dim3((unsigned)N), dim3(256), 0, st, ids, wte, C, T, wsg,
+                     raw, embn, T > 1 ? smsig : nullptr);
+  GN_HIP(hipGetLastError());
+  int64_t tot = N * C;
+  hipLaunchKernelGGL(smear_apply_kernel, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st,
+                     embn, smsig, lam, x, C, T, tot);
+  GN_HIP(hipGetLastError());
+}
+
+// Decode step embedding (transformer.go:276-300 with T == 1): embn =
+// norm(wte[tok]); x = embn + lambda*sigmoid(embn[:24].w)*prev; prev = embn.
+__global__ __launch_bounds__(256) void embed_decode_kernel(const int32_t* __restrict__ tok,
+                                                           const float* __restrict__ wte, int C,
+                                                           const float* __restrict__ wsg,
+                                                           const float* __restrict__ lam,
+                                                           float* __restrict__ prev,
+                                                           float* __restrict__ x,
+                                                           float* __restrict__ x0) {
+  __shared__ float sc[4];
+  __shared__ float gate_s;
+  const int64_t r = blockIdx.x;
+  const float* src = wte + (int64_t)tok[r] * C;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < C; c += 256) ss += src[c] * src[c];
+  ss = bsum256(ss, sc);
+  const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
+  if (threadIdx.x < 64) {
+    float p = threadIdx.x < SMEAR_CH ? src[threadIdx.x] * inv * wsg[threadIdx.x] : 0.f;
+    p = warp_sum(p);
+    if (threadIdx.x == 0) gate_s = sigmoidf_(p) * lam[0];
+  }
+  __syncthreads();
+  const float g = gate_s;
+  for (int c = threadIdx.x; c < C; c += 256) {
+    float e = src[c] * inv;
+    float v = e + g * prev[r * C + c];
+    prev[r * C + c] = e;
+    x[r * C + c] = v;
+    x0[r * C + c] = v;
+  }
+}
+void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg, const float* lam,
+                         int rows, int C, float* prev, float* x, float* x0, hipStream_t st) {
+  hipLaunchKernelGGL(embed_decode_kernel, dim3(rows), dim3(256), 0, st, tok, wte, C, wsg, lam,
+                     prev, x, x0);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// combineResidual + RMSNorm (transformer.go:312,544-551; block.go:39):
+// xb = lr*xin + l0*x0 ; h = norm(xb).  xb may alias xin.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const float* __restrict__ x0,
+                                                         const float* __restrict__ lr,
+                                                         const float* __restrict__ l0, int layer,
+                                                         int C, float* xb, float* __restrict__ h) {
+  __shared__ float sc[4];
+  const int64_t r = blockIdx.x;
+  const float a = lr[layer], b = l0[layer];
+  float vals[4];
+  float ss = 0.f;
+  int k = 0;
+  for (int c = threadIdx.x; c < C; c += 256, k++) {
+    float v = a * xin[r * C + c] + b * x0[r * C + c];
+    vals[k] = v;
+    ss += v * v;
+  }
+  ss = bsum256(ss, sc);
+  const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
+  k = 0;
+  for (int c = threadIdx.x; c < C; c += 256, k++) {
+    xb[r * C + c] = vals[k];
+    h[r * C + c] = vals[k] * inv;
+  }
+}
+void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
+                       int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st) {
+  GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
+  hipLaunchKernelGGL(resid_norm_kernel, dim3((unsigned)rows), dim3(256), 0, st, xin, x0, lr, l0,
+                     layer, C, xb, h);
+  GN_HIP(hipGetLastError());
+}
+
+// y = norm(x - lam*back) (or norm(x) when back is null); pre receives x - lam*back.
+__global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ back,
+                                                        const float* __restrict__ lam, int C,
+                                                        float* __restrict__ pre,
+                                                        float* __restrict__ y) {
+  __shared__ float sc[4];
+  const int64_t r = blockIdx.x;
+  const float nl = back ? -lam[0] : 0.f;
+  float vals[4];
+  float ss = 0.f;
+  int k = 0;
+  for (int c = threadIdx.x; c < C; c += 256, k++) {
+    float v = x[r * C + c];
+    if (back) v = v + nl * back[r * C + c];
+    vals[k] = v;
+    ss += v * v;
+  }
+  ss = bsum256(ss, sc);
+  const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
+  k = 0;
+  for (int c = threadIdx.x; c < C; c += 256, k++) {
+    if (pre) pre[r * C + c] = vals[k];
+    y[r * C + c] = vals[k] * inv;
+  }
+}
+void launch_norm_rows(const float* x, const float* back, const float* lam, int64_t rows, int C,
+                      float* pre, float* y, hipStream_t st) {
+  GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
+  hipLaunchKernelGGL(norm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, back, lam, C,
+                     pre, y);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// Q/K/V post-processing (attention.go:240-256): VE gate on v, RoPE on the
+// trailing R dims of q and k, then 1.2 * RMSNorm per head.  One block of 256
+// threads per token; each wave handles whole heads (D = 128: two values per
+// lane).  Inputs: qkv [N, (Hq+2Hkv)*D] (GEMM output), h [N, C] (VE gate
+// reads h[:12]); token n sits at position pos0 + n % T.  The key and value
+// of token n land in cache row (n / T) at that position when a cache is
+// given (decode: T == 1, one row per token; prefill: one row per prompt).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
+  constexpr int D = 128;
+  __shared__ float row[16 * D];  // up to 16 heads of q/k/v
+  __shared__ float gate[8];
+  const int64_t n = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int H = a.Hq + 2 * a.Hkv;
+  const float* src = a.qkv + n * (int64_t)H * D;
+  for (int i = tid; i < H * D; i += 256) row[i] = src[i];
+  const int t = (int)(n % a.T);
+  const int pos = a.pos0 + t;
+  if (a.ve && wid == 0) {
+    // gate[hk] = 3 * sigmoid(h[:12] . wve[hk]) (attention.go:247-248)
+    for (int hk = 0; hk < a.Hkv; hk++) {
+      float p = lane < VE_CH ? a.h[n * a.C + lane] * a.wve[hk * VE_CH + lane] : 0.f;
+      p = warp_sum(p);
+      if (lane == 0) {
+        float s = sigmoidf_(p);
+        gate[hk] = s * VE_SCALE;
+        if (a.vesig) a.vesig[n * a.Hkv + hk] = s;
+      }
+    }
+  }
+  __syncthreads();
+  // v += gate * ve[id] (attention.go:392-405)
+  if (a.ve) {
+    const float* ver = a.ve + (int64_t)a.ids[n] * a.Hkv * D;
+    for (int i = tid; i < a.Hkv * D; i += 256) row[(a.Hq + a.Hkv) * D + i] += gate[i / D] * ver[i];
+  }
+  __syncthreads();
+  const int half = a.R / 2, off = D - a.R;
+  const float* cw = a.cosT + (int64_t)pos * half;
+  const float* sw = a.sinT + (int64_t)pos * half;
+  // q and k heads: rotate, then 1.2 * RMSNorm over the head
+  for (int hd = wid; hd < a.Hq + a.Hkv; hd += 4) {
+    const float* x = row + hd * D;
+    float y[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      int d = lane + 64 * e;
+      float v = x[d];
+      if (d >= off) {
+        int j = d - off;
+        if (j < half) v = x[d] * cw[j] + x[d + half] * sw[j];
+        else v = -x[d - half] * sw[j - half] + x[d] * cw[j - half];
+      }
+      y[e] = v;
+    }
+    float ss = warp_sum(y[0] * y[0] + y[1] * y[1]);
+    const float inv = 1.f / sqrtf(ss / (float)D + NORM_EPS);
+    const bool isq = hd < a.Hq;
+    const int hh = isq ? hd : hd - a.Hq;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      int d = lane + 64 * e;
+      float o = y[e] * inv * QK_SCALE;
+      if (isq) {
+        if (a.qrot) a.qrot[(n * a.Hq + hh) * D + d] = y[e];
+        a.qn[(n * a.Hq + hh) * D + d] = o;
+      } else {
+        if (a.krot) a.krot[(n * a.Hkv + hh) * D + d] = y[e];
+        if (a.kn) a.kn[(n * a.Hkv + hh) * D + d] = o;
+        if (a.kcache) {
+          int64_t crow = (n / a.T) * a.rows_per_seq;
+          a.kcache[((crow * a.Hkv + hh) * a.maxSeq + pos) * D + d] = o;
+        }
+      }
+    }
+  }
+  // v heads
+  for (int i = tid; i < a.Hkv * D; i += 256) {
+    float v = row[(a.Hq + a.Hkv) * D + i];
+    int hh = i / D, d = i % D;
+    if (a.vout) a.vout[n * a.Hkv * D + i] = v;
+    if (a.vcache) {
+      int64_t crow = (n / a.T) * a.rows_per_seq;
+      a.vcache[((crow * a.Hkv + hh) * a.maxSeq + pos) * D + d] = v;
+    }
+  }
+}
+void launch_qkv_post(const QkvPostArgs& a, int64_t rows, hipStream_t st) {
+  GN_CHECK(a.Hq + 2 * a.Hkv <= 16, "qkv_post: at most 16 heads");
+  GN_CHECK(a.Hkv <= 8, "qkv_post: at most 8 kv heads");
+  GN_CHECK(a.R % 2 == 0 && a.R <= 128, "qkv_post: rotary dims must be even and <= 128");
+  hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// Copies a prefill KV cache [G][Hkv][P][D] (per layer) into the decode cache
+// [G*S][Hkv][maxSeq][D] (model/kvcache.go:383-448, PrefillFrom), and the
+// prefill's last embedding into every row's previous-embedding slot.
+__global__ void replicate_kv_kernel(const float* __restrict__ src, float* __restrict__ dst, int G,
+                                    int S, int Hkv, int P, int maxSrc, int maxDst, int64_t total) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;  // total = G*S*Hkv*P*D
+  constexpr int D = 128;
+  int d = (int)(i % D);
+  int64_t r = i / D;
+  int p = (int)(r % P);
+  r /= P;
+  int hk = (int)(r % Hkv);
+  int64_t row = r / Hkv;
+  int g = (int)(row / S);
+  dst[((row * Hkv + hk) * maxDst + p) * D + d] = src[(((int64_t)g * Hkv + hk) * maxSrc + p) * D + d];
+}
+void launch_replicate_kv(const float* src, float* dst, int G, int S, int Hkv, int P, int maxSrc,
+                         int maxDst, hipStream_t st) {
+  int64_t total = (int64_t)G * S * Hkv * P * 128;
+  if (total == 0) return;
+  hipLaunchKernelGGL(replicate_kv_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                     src, dst, G, S, Hkv, P, maxSrc, maxDst, total);
+  GN_HIP(hipGetLastError());
+}
+
+// Gathers row (g*T + T-1) of src [G*T, C] into rows [g*S, (g+1)*S) of dst.
+__global__ void expand_last_rows_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                        int G, int T, int S, int C) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t total = (int64_t)G * S * C;
+  if (i >= total) return;
+  int c = (int)(i % C);
+  int64_t row = i / C;
+  int g = (int)(row / S);
+  dst[i] = src[((int64_t)g * T + T - 1) * C + c];
+}
+void launch_expand_last_rows(const float* src, float* dst, int G, int T, int S, int C,
+                             hipStream_t st) {
+  int64_t total = (int64_t)G * S * C;
+  if (total == 0) return;
+  hipLaunchKernelGGL(expand_last_rows_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
+                     st, src, dst, G, T, S, C);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// PG loss rows (trainer/rl.go:22-56, tensors/loss.go:16-46,
+// tensors/backward.go:108-116).  z [rows, V] softcapped logits (row stride
+// ldz) is overwritten by dL/d(pre-softcap logits):
+//   g = (softmax(z) - onehot(t)) * (adv/norm) * (1 - (z/15)^2),
+// zero for ignored rows.  nll (0 for ignored) and the per-row loss term
+// nll*adv/norm (float64) are written per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z, int64_t ldz,
+                                                           int V, int64_t row0,
+                                                           const int32_t* __restrict__ targets,
+                                                           const float* __restrict__ adv, int T,
+                                                           float norm, float* __restrict__ nll,
+                                                           double* __restrict__ loss_rows) {
+  __shared__ float sf[4];
+  __shared__ double sd[4];
+  const int64_t r = blockIdx.x;
+  const int64_t n = row0 + r;
+  float* zr = z + r * ldz;
+  const int32_t tg = targets[n];
+  if (tg < 0) {
+    for (int j = threadIdx.x; j < V; j += 256) zr[j] = 0.f;
+    if (threadIdx.x == 0) {
+      nll[n] = 0.f;
+      loss_rows[n] = 0.0;
+    }
+    return;
+  }
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, zr[j]);
+  m = block_max(m, sf);
+  double s = 0;
+  for (int j = threadIdx.x; j < V; j += 256) s += (double)expf(zr[j] - m);
+  s = block_sum<double>(s, sd);
+  const float a = adv[n / T];
+  const float nl = m + (float)log(s) - zr[tg];
+  if (threadIdx.x == 0) {
+    nll[n] = nl;
+    loss_rows[n] = (double)nl * (double)a / (double)norm;
+  }
+  const float inv = (float)(1.0 / s);
+  const float scale = a / norm;
+  const float ic = 1.0f / 15.0f;
+  __syncthreads();
+  for (int j = threadIdx.x; j < V; j += 256) {
+    float zj = zr[j];
+    float p = expf(zj - m) * inv;
+    if (j == tg) p -= 1.f;
+    float sc = zj * ic;
+    zr[j] = (p * scale) * (1.f - sc * sc);
+  }
+}
+void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t rows,
+                         const int32_t* targets, const float* adv, int T, float norm, float* nll,
+                         double* loss_rows, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(pg_loss_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, z, ldz, V, row0,
+                     targets, adv, T, norm, nll, loss_rows);
+  GN_HIP(hipGetLastError());
+}
+
+// Ordered float64 sum of n values into out[0] (one block).
+__global__ __launch_bounds__(1024) void sum_f64_kernel(const double* __restrict__ v, int64_t n,
+                                                       double* __restrict__ out, int accumulate) {
+  __shared__ double sd[16];
+  double acc = 0;
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) acc += v[i];
+  acc = block_sum<double>(acc, sd);
+  if (threadIdx.x == 0) out[0] = accumulate ? out[0] + acc : acc;
+}
+void launch_sum_f64(const double* v, int64_t n, double* out, bool accumulate, hipStream_t st) {
+  hipLaunchKernelGGL(sum_f64_kernel, dim3(1), dim3(1024), 0, st, v, n, out, accumulate ? 1 : 0);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// Backward row kernels
+// ---------------------------------------------------------------------------
+// RMSNorm backward (tensors/backward.go:81-104), float64 row statistics:
+// out = g/r - x*(g.x)/(C r^3) [+ extra].  out may alias g or extra.
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restrict__ x,
+                                                          const float* g, const float* extra,
+                                                          int C, float* out) {
+  __shared__ double sd[4];
+  const int64_t r = blockIdx.x;
+  double ss = 0, dot = 0;
+  for (int c = threadIdx.x; c < C; c += 256) {
+    double xv = x[r * C + c], gv = g[r * C + c];
+    ss += xv * xv;
+    dot += gv * xv;
+  }
+  ss = block_sum<double>(ss, sd);
+  dot = block_sum<double>(dot, sd);
+  const double rms = sqrt(ss / C + (double)NORM_EPS);
+  const double inv = 1.0 / rms;
+  const double coef = dot / ((double)C * rms * rms * rms);
+  float vals[4];
+  int k = 0;
+  for (int c = threadIdx.x; c < C; c += 256, k++) {
+    float v = (float)((double)g[r * C + c] * inv - coef * (double)x[r * C + c]);
+    if (extra) v += extra[r * C + c];
+    vals[k] = v;
+  }
+  __syncthreads();
+  k = 0;
+  for (int c = threadIdx.x; c < C; c += 256, k++) out[r * C + c] = vals[k];
+}
+void launch_rmsnorm_bwd(const float* x, const float* g, const float* extra, int64_t rows, int C,
+                        float* out, hipStream_t st) {
+  GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
+  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, g, extra, C,
+                     out);
+  GN_HIP(hipGetLastError());
+}
+
+// Per-block float64 partial dot products of a with up to two vectors; the
+// partials are reduced in a fixed order afterwards.
+__global__ __launch_bounds__(256) void dot_partials_kernel(const float* __restrict__ a,
+                                                           const float* __restrict__ b0,
+                                                           const float* __restrict__ b1,
+                                                           float sign, int64_t n,
+                                                           double* __restrict__ part) {
+  __shared__ double sd[4];
+  double s0 = 0, s1 = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    s0 += (double)a[i] * (double)(sign * b0[i]);
+    if (b1) s1 += (double)a[i] * (double)b1[i];
+  }
+  s0 = block_sum<double>(s0, sd);
+  s1 = block_sum<double>(s1, sd);
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = s0;
+    if (b1) part[gridDim.x + blockIdx.x] = s1;
+  }
+}
+// Reduces npart partials (ordered) and adds float32(sum) into dst[0].
+__global__ void partials_to_grad_kernel(const double* __restrict__ part, int npart,
+                                        float* __restrict__ dst) {
+  if (threadIdx.x != 0) return;
+  double s = 0;
+  for (int i = 0; i < npart; i++) s += part[i];
+  dst[0] += (float)s;
+}
+void launch_dot_into_grad(const float* a, const float* b0, const float* b1, float sign, int64_t n,
+                          float* dst0, float* dst1, double* part, hipStream_t st) {
+  const int nb = 1024;
+  hipLaunchKernelGGL(dot_partials_kernel, dim3(nb), dim3(256), 0, st, a, b0, b1, sign, n, part);
+  GN_HIP(hipGetLastError());
+  hipLaunchKernelGGL(partials_to_grad_kernel, dim3(1), dim3(64), 0, st, part, nb, dst0);
+  if (b1) hipLaunchKernelGGL(partials_to_grad_kernel, dim3(1), dim3(64), 0, st, part + nb, nb, dst1);
+  GN_HIP(hipGetLastError());
+}
+
+// Layer residual bookkeeping (train_transformer.go:218-230):
+// g_next = lr*gb ; gx0 += l0*gb.
+__global__ void resid_bwd_kernel(const float* __restrict__ gb, const float* __restrict__ lr,
+                                 const float* __restrict__ l0, int layer, float* __restrict__ gnext,
+                                 float* __restrict__ gx0, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float g = gb[i];
+  gnext[i] = g * lr[layer];
+  gx0[i] = gx0[i] + l0[layer] * g;
+}
+void launch_resid_bwd(const float* gb, const float* lr, const float* l0, int layer, float* gnext,
+                      float* gx0, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(resid_bwd_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st, gb, lr,
+                     l0, layer, gnext, gx0, n);
+  GN_HIP(hipGetLastError());
+}
+
+// out = a + s*b (element-wise); out may alias a.
+__global__ void axpy_kernel(float* out, const float* a, const float* __restrict__ b,
+                            const float* __restrict__ sptr, float s, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float sc = sptr ? -sptr[0] : s;
+  out[i] = a[i] + sc * b[i];
+}
+void launch_axpy(float* out, const float* a, const float* b, const float* neg_scale_ptr, float s,
+                 int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(axpy_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st, out, a, b,
+                     neg_scale_ptr, s, n);
+  GN_HIP(hipGetLastError());
+}
+
+// Backward of qkv_post (train.go:331-356 and 369-397) for one token per
+// block: dq = rope^T(rmsnorm_bwd(qrot, 1.2*dqn)), likewise k; dv passes
+// through; VE gate and value-embedding gradients.  Writes dqkv [N, (Hq+2Hkv)D];
+// dpre [N, Hkv] is the VE pre-gate gradient; the value-embedding table
+// gradient is scatter-added (repeated ids accumulate, linear.go:90-104).
+__global__ __launch_bounds__(256) void qkv_post_bwd_kernel(QkvPostBwdArgs a) {
+  constexpr int D = 128;
+  const int64_t n = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int H = a.Hq + 2 * a.Hkv;
+  const int t = (int)(n % a.T);
+  const int half = a.R / 2, off = D - a.R;
+  const float* cw = a.cosT + (int64_t)t * half;
+  const float* sw = a.sinT + (int64_t)t * half;
+  float* out = a.dqkv + n * (int64_t)H * D;
+  for (int hd = wid; hd < a.Hq + a.Hkv; hd += 4) {
+    const bool isq = hd < a.Hq;
+    const int hh = isq ? hd : hd - a.Hq;
+    const float* gsrc = isq ? a.dqn + (n * a.Hq + hh) * D : a.dkn + (n * a.Hkv + hh) * D;
+    const float* xsrc = isq ? a.qrot + (n * a.Hq + hh) * D : a.krot + (n * a.Hkv + hh) * D;
+    float x[2], g[2];
+    double ss = 0, dot = 0;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      int d = lane + 64 * e;
+      x[e] = xsrc[d];
+      g[e] = gsrc[d] * QK_SCALE;
+      ss += (double)x[e] * x[e];
+      dot += (double)g[e] * x[e];
+    }
+    ss = warp_sum_d(ss);
+    dot = warp_sum_d(dot);
+    const double rms = sqrt(ss / D + (double)NORM_EPS);
+    const double inv = 1.0 / rms, coef = dot / ((double)D * rms * rms * rms);
+    float gp[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) gp[e] = (float)((double)g[e] * inv - coef * (double)x[e]);
+    // rotary transpose: negated sine table (train.go:14-20, 334-336).  The
+    // partner of dim d is d +- R/2, held by lane (d +- R/2) % 64 in slot
+    // (d +- R/2) / 64.
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      int d = lane + 64 * e;
+      int j = d - off;
+      int pd = d >= off ? (j < half ? d + half : d - half) : d;
+      float p0 = __shfl(gp[0], pd & 63, 64);
+      float p1 = __shfl(gp[1], pd & 63, 64);
+      float partner = (pd >> 6) ? p1 : p0;
+      float v = gp[e];
+      if (d >= off) {
+        if (j < half) v = gp[e] * cw[j] - partner * sw[j];
+        else v = partner * sw[j - half] + gp[e] * cw[j - half];
+      }
+      out[hd * D + d] = v;
+    }
+  }
+  // v: gradient passes to the projection; VE pieces
+  for (int i = tid; i < a.Hkv * D; i += 256) out[(a.Hq + a.Hkv) * D + i] = a.dv[n * a.Hkv * D + i];
+  if (a.vesig) {
+    const float* ver = a.ve + (int64_t)a.ids[n] * a.Hkv * D;
+    float* gver = a.gve + (int64_t)a.ids[n] * a.Hkv * D;
+    for (int hk = wid; hk < a.Hkv; hk += 4) {
+      const float s = a.vesig[n * a.Hkv + hk];
+      const float scale = s * VE_SCALE;
+      double dot = 0;
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        int d = lane + 64 * e;
+        float gv = a.dv[(n * a.Hkv + hk) * D + d];
+        atomicAdd(&gver[hk * D + d], gv * scale);
+        dot += (double)gv * (double)ver[hk * D + d];
+      }
+      dot = warp_sum_d(dot);
+      if (lane == 0) {
+        float gs = (float)dot * VE_SCALE;
+        a.dpre[n * a.Hkv + hk] = gs * s * (1.f - s);
+      }
+    }
+  }
+}
+void launch_qkv_post_bwd(const QkvPostBwdArgs& a, int64_t rows, hipStream_t st) {
+  hipLaunchKernelGGL(qkv_post_bwd_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// VE gate backward: dW[hk][c] += sum_n dpre[n,hk] * h[n,c] (c < 12) and
+// dh[n, c] += sum_hk dpre[n,hk] * W[hk][c] (train.go:392-396).
+__global__ __launch_bounds__(256) void ve_gate_dw_kernel(const float* __restrict__ dpre,
+                                                         const float* __restrict__ h, int C,
+                                                         int Hkv, int64_t N,
+                                                         double* __restrict__ part) {
+  // part[block][Hkv*12]
+  __shared__ double sd[4];
+  for (int hk = 0; hk < Hkv; hk++)
+    for (int c = 0; c < VE_CH; c++) {
+      double s = 0;
+      for (int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x; n < N; n += (int64_t)gridDim.x * 256)
+        s += (double)dpre[n * Hkv + hk] * (double)h[n * C + c];
+      s = block_sum<double>(s, sd);
+      if (threadIdx.x == 0) part[(int64_t)blockIdx.x * Hkv * VE_CH + hk * VE_CH + c] = s;
+    }
+}
+__global__ void ve_gate_dw_reduce_kernel(const double* __restrict__ part, int nb, int count,
+                                         float* __restrict__ dW) {
+  int i = threadIdx.x;
+  if (i >= count) return;
+  double s = 0;
+  for (int b = 0; b < nb; b++) s += part[(int64_t)b * count + i];
+  dW[i] += (float)s;
+}
+__global__ void ve_gate_dh_kernel(const float* __restrict__ dpre, const float* __restrict__ W,
+                                  int C, int Hkv, int64_t N, float* __restrict__ dh) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N * VE_CH) return;
+  int64_t n = i / VE_CH;
+  int c = (int)(i % VE_CH);
+  float s = 0.f;
+  for (int hk = 0; hk < Hkv; hk++) s += dpre[n * Hkv + hk] * W[hk * VE_CH + c];
+  dh[n * C + c] += s;
+}
+void launch_ve_gate_bwd(const float* dpre, const float* h, const float* W, int C, int Hkv,
+                        int64_t N, float* dW, float* dh, double* part, hipStream_t st) {
+  const int nb = 256;
+  hipLaunchKernelGGL(ve_gate_dw_kernel, dim3(nb), dim3(256), 0, st, dpre, h, C, Hkv, N, part);
+  hipLaunchKernelGGL(ve_gate_dw_reduce_kernel, dim3(1), dim3(64), 0, st, part, nb, Hkv * VE_CH, dW);
+  hipLaunchKernelGGL(ve_gate_dh_kernel, dim3((unsigned)ceil_div(N * VE_CH, 256)), dim3(256), 0, st,
+                     dpre, W, C, Hkv, N, dh);
+  GN_HIP(hipGetLastError());
+}
+
+// Smear backward (train_transformer.go:269-305) for one token per block:
+// ge[t] += ga[t]; ge[t-1] += ga[t]*gate(t); the gate/lambda gradients use the
+// pre-smear embedding of t-1.  ge is written for row t only from ga[t] and
+// ga[t+1], so blocks do not race.
+__global__ __launch_bounds__(256) void smear_bwd_kernel(const float* __restrict__ ga,
+                                                        const float* __restrict__ embn,
+                                                        const float* __restrict__ smsig,
+                                                        const float* __restrict__ lam, int C,
+                                                        int T, float* __restrict__ ge,
+                                                        float* __restrict__ ggate,
+                                                        double* __restrict__ lam_rows) {
+  __shared__ double sd[4];
+  const int64_t n = blockIdx.x;
+  const int t = (int)(n % T);
+  const int64_t b = n / T;
+  const float l = lam[0];
+  // ge[t] = ga[t] + ga[t+1] * gate(t+1)
+  float gnext = 0.f;
+  if (t + 1 < T) gnext = l * smsig[b * (T - 1) + t];
+  for (int c = threadIdx.x; c < C; c += 256) {
+    float v = ga[n * C + c];
+    if (t + 1 < T) v += ga[(n + 1) * C + c] * gnext;
+    ge[n * C + c] = v;
+  }
+  if (t >= 1) {
+    double gs = 0;
+    for (int c = threadIdx.x; c < C; c += 256) gs += (double)ga[n * C + c] * (double)embn[(n - 1) * C + c];
+    gs = block_sum<double>(gs, sd);
+    if (threadIdx.x == 0) {
+      const int64_t gi = b * (T - 1) + t - 1;
+      const float s = smsig[gi];
+      lam_rows[gi] = gs * (double)s;
+      ggate[gi] = (float)(gs * (double)l) * s * (1.f - s);
+    }
+  }
+}
+// Smear-gate Linear backward (24 -> 1) and scatter of its input gradient into
+// the first 24 channels of ge for rows t >= 1.
+__global__ void smear_gate_bwd_kernel(const float* __restrict__ ggate,
+                                      const float* __restrict__ embn,
+                                      const float* __restrict__ wsg, int C, int T, int64_t NS,
+                                      float* __restrict__ ge) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= NS * SMEAR_CH) return;
+  int64_t gi = i / SMEAR_CH;
+  int c = (int)(i % SMEAR_CH);
+  int64_t b = gi / (T - 1);
+  int t = (int)(gi % (T - 1)) + 1;
+  int64_t n = b * T + t;
+  ge[n * C + c] += ggate[gi] * wsg[c];
+}
+__global__ __launch_bounds__(256) void smear_gate_dw_kernel(const float* __restrict__ ggate,
+                                                            const float* __restrict__ embn, int C,
+                                                            int T, int64_t NS,
+                                                            double* __restrict__ part) {
+  __shared__ double sd[4];
+  for (int c = 0; c < SMEAR_CH; c++) {
+    double s = 0;
+    for (int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x; gi < NS; gi += (int64_t)gridDim.x * 256) {
+      int64_t b = gi / (T - 1);
+      int t = (int)(gi % (T - 1)) + 1;
+      s += (double)ggate[gi] * (double)embn[(b * T + t) * C + c];
+    }
+    s = block_sum<double>(s, sd);
+    if (threadIdx.x == 0) part[(int64_t)blockIdx.x * SMEAR_CH + c] = s;
+  }
+}
+void launch_smear_bwd(const float* ga, const float* embn, const float* smsig, const float* lam,
+                      const float* wsg, int B, int T, int C, float* ge, float* ggate,
+                      double* lam_rows, double* part, float* dwsg, float* dlam, hipStream_t st) {
+  int64_t N = (int64_t)B * T;
+  hipLaunchKernelGGL(smear_bwd_kernel, dim3((unsigned)N), dim3(256), 0, st, ga, embn, smsig, lam,
+                     C, T, ge, ggate, lam_rows);
+  GN_HIP(hipGetLastError());
+  if (T <= 1) return;
+  int64_t NS = (int64_t)B * (T - 1);
+  launch_sum_f64(lam_rows, NS, part, false, st);
+  hipLaunchKernelGGL(partials_to_grad_kernel, dim3(1), dim3(64), 0, st, part, 1, dlam);
+  const int nb = 128;
+  hipLaunchKernelGGL(smear_gate_dw_kernel, dim3(nb), dim3(256), 0, st, ggate, embn, C, T, NS,
+                     part + 8);
+  hipLaunchKernelGGL(ve_gate_dw_reduce_kernel, dim3(1), dim3(64), 0, st, part + 8, nb, SMEAR_CH,
+                     dwsg);
+  hipLaunchKernelGGL(smear_gate_bwd_kernel, dim3((unsigned)ceil_div(NS * SMEAR_CH, 256)),
+                     dim3(256), 0, st, ggate, embn, wsg, C, T, NS, ge);
+  GN_HIP(hipGetLastError());
+}
+
+// Embedding backward: scatter-add rows of g into the table at ids
+// (linear.go:90-104).
+__global__ void embed_scatter_kernel(const float* __restrict__ g, const int32_t* __restrict__ ids,
+                                     int C, int64_t N, float* __restrict__ gw) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N * C) return;
+  int64_t n = i / C;
+  int c = (int)(i % C);
+  atomicAdd(&gw[(int64_t)ids[n] * C + c], g[i]);
+}
+void launch_embed_scatter(const float* g, const int32_t* ids, int C, int64_t N, float* gw,
+                          hipStream_t st) {
+  hipLaunchKernelGGL(embed_scatter_kernel, dim3((unsigned)ceil_div(N * C, 256)), dim3(256), 0, st,
+                     g, ids, C, N, gw);
+  GN_HIP(hipGetLastError());
+}
+
+}  // namespace gn

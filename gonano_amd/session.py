@@ -1,0 +1,125 @@
+"""Device-resident RL-step session over the HIP C ABI.
+
+Mirrors the reference entry points this path replaces:
+Transformer.Forward (model/transformer.go:211-214),
+Engine.GenerateBatchWith (inference/engine.go:336-369),
+trainer.PolicyGradientStep (trainer/rl.go:14-60), and the body of
+cmd/chat_rl's step loop (cmd/chat_rl/main.go:101-183).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import GnConfig, GnTiming, call, lib
+from .config import Config
+
+
+class Session:
+    def __init__(self, cfg: Config, device: int = 0):
+        cfg.validate()
+        self.cfg = cfg
+        self._c = GnConfig(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head,
+                           cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern.encode())
+        h = C.c_void_p()
+        call("gn_session_create", C.byref(self._c), device, C.byref(h))
+        self._h = h
+        t = C.c_int64()
+        call("gn_session_param_total", self._h, C.byref(t))
+        self.param_total = t.value
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().gn_session_destroy(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- parameters -----------------------------------------------------------
+    def param_table(self):
+        n = C.c_int32()
+        call("gn_session_param_count", self._h, C.byref(n))
+        out = []
+        buf = C.create_string_buffer(128)
+        r, c, o = C.c_int64(), C.c_int64(), C.c_int64()
+        for i in range(n.value):
+            call("gn_session_param_info", self._h, i, buf, 128, C.byref(r), C.byref(c), C.byref(o))
+            out.append((buf.value.decode(), r.value, c.value, o.value))
+        return out
+
+    def set_params(self, params: np.ndarray):
+        params = np.ascontiguousarray(params, np.float32)
+        call("gn_session_set_params", self._h, params, params.size)
+
+    def get_params(self) -> np.ndarray:
+        out = np.zeros(self.param_total, np.float32)
+        call("gn_session_get_params", self._h, out, out.size)
+        return out
+
+    def grads(self) -> np.ndarray:
+        out = np.zeros(self.param_total, np.float32)
+        call("gn_session_get_grads", self._h, out, out.size)
+        return out
+
+    def zero_grad(self):
+        call("gn_session_zero_grads", self._h)
+
+    # -- compute --------------------------------------------------------------
+    def forward(self, ids: np.ndarray) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.int32)
+        B, T = ids.shape
+        out = np.zeros((B, T, self.cfg.vocab_size), np.float32)
+        call("gn_forward", self._h, ids, B, T, out)
+        return out
+
+    def generate_batch(self, prompts: np.ndarray, samples: int, max_tokens: int,
+                       temperature: float, top_k: int, seeds) -> list[np.ndarray]:
+        prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
+        G, P = prompts.shape
+        rows = np.zeros((G * samples, P + max_tokens), np.int32)
+        lens = np.zeros(G * samples, np.int32)
+        call("gn_generate_batch", self._h, prompts, G, P, samples, max_tokens, float(temperature),
+             top_k, np.ascontiguousarray(seeds, np.uint64), rows, lens)
+        return [rows[i, :lens[i]].copy() for i in range(G * samples)]
+
+    def policy_gradient_step(self, inputs, targets, advantages, norm: float):
+        inputs = np.ascontiguousarray(inputs, np.int32)
+        targets = np.ascontiguousarray(targets, np.int32)
+        adv = np.ascontiguousarray(advantages, np.float32)
+        B, T = inputs.shape
+        nll = np.zeros(B * T, np.float32)
+        loss = C.c_float()
+        call("gn_policy_gradient_step", self._h, inputs, targets, B, T, adv, float(norm),
+             C.byref(loss), nll.ctypes.data_as(C.c_void_p))
+        return loss.value, nll.reshape(B, T)
+
+    def rl_step(self, prompts, samples, max_tokens, temperature, top_k, seeds, rewards):
+        prompts = np.ascontiguousarray(prompts, np.int32)
+        G, P = prompts.shape
+        Bt = G * samples
+        rows = np.zeros((Bt, P + max_tokens), np.int32)
+        lens = np.zeros(Bt, np.int32)
+        adv = np.zeros(Bt, np.float32)
+        max_len = C.c_int32()
+        loss = C.c_float()
+        call("gn_rl_step", self._h, prompts, G, P, samples, max_tokens, float(temperature), top_k,
+             np.ascontiguousarray(seeds, np.uint64), np.ascontiguousarray(rewards, np.float32),
+             rows, lens, adv, C.byref(max_len), C.byref(loss))
+        return dict(loss=loss.value, rows=[rows[b, :lens[b]].copy() for b in range(Bt)],
+                    lens=lens, adv=adv, max_len=max_len.value)
+
+    # -- timing ---------------------------------------------------------------
+    def set_timing(self, enabled: bool):
+        call("gn_session_set_timing", self._h, 1 if enabled else 0)
+
+    def timing(self) -> dict:
+        t = GnTiming()
+        call("gn_session_get_timing", self._h, C.byref(t))
+        return {f: getattr(t, f) for f, _ in GnTiming._fields_}

@@ -1,0 +1,232 @@
+/*
+ * gonano_hip.h - C ABI of libgnhip.so, the MI355X (gfx950) HIP backend for
+ * gonano's RL step.
+ *
+ * Two groups of entry points:
+ *
+ *  1. gn_<method>: the 33 methods of gonano's numeric plugin interface
+ *     kernels.Backend (kernels/backend.go:21-297), one C function each, on
+ *     host pointers with the same argument meaning.  They stage the operands
+ *     through device memory on a per-thread stream and are re-entrant, since
+ *     the reference calls its backend concurrently from goroutines
+ *     (model/attention.go:311-320, tensors/loss.go:30-37).  Lengths are the
+ *     Go slice lengths; destinations may alias sources.
+ *
+ *  2. gn_session_* / gn_generate_batch / gn_policy_gradient_step /
+ *     gn_rl_step: a device-resident session that runs the fused hot path the
+ *     interface cannot carry (SURVEY of the reference: the sampler, the PG
+ *     loss loops, softcap backward, smear and embedding scatter are Go loops
+ *     outside kernels.Backend).  They replace Engine.GenerateBatchWith
+ *     (inference/engine.go:336-369), trainer.PolicyGradientStep
+ *     (trainer/rl.go:14-60) and the body of cmd/chat_rl's step loop
+ *     (cmd/chat_rl/main.go:101-183).
+ *
+ * Every function returns a gn_status; on failure gn_last_error() gives the
+ * message for the calling thread.  Pointers are borrowed for the call only.
+ */
+#ifndef GONANO_HIP_H
+#define GONANO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  GN_OK = 0,
+  GN_ERR_INVALID = 1,     /* bad shape or argument (the reference panics) */
+  GN_ERR_HIP = 2,         /* a HIP runtime call failed */
+  GN_ERR_OOM = 3,         /* device or host allocation failed */
+  GN_ERR_UNSUPPORTED = 4, /* configuration not built for this device */
+  GN_ERR_INTERNAL = 5
+} gn_status;
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char *gn_last_error(void);
+/* Number of visible HIP devices (0 when none); never fails. */
+int gn_device_count(void);
+/* Selects the device the calling thread's backend calls run on (default 0). */
+int gn_set_device(int device);
+/* Waits for all work the calling thread queued. */
+int gn_synchronize(void);
+
+/* ---- kernels.Backend: Elementwise (kernels/backend.go:21-67) ------------- */
+int gn_add(float *destination, const float *left, const float *right, int64_t n);
+int gn_subtract(float *destination, const float *left, const float *right, int64_t n);
+int gn_multiply(float *destination, const float *left, const float *right, int64_t n);
+int gn_divide(float *destination, const float *left, const float *right, int64_t n);
+int gn_scale(float *destination, const float *source, float factor, int64_t n);
+int gn_add_scaled(float *destination, const float *base, const float *scaled, float factor,
+                  int64_t n);
+int gn_negate(float *destination, const float *source, int64_t n);
+int gn_abs(float *destination, const float *source, int64_t n);
+int gn_square(float *destination, const float *source, int64_t n);
+int gn_relu_squared(float *destination, const float *source, int64_t n);
+int gn_swiglu(float *destination, const float *gate, const float *up, float clamp, int64_t n);
+int gn_swiglu_backward(float *gate_gradient, float *up_gradient, const float *gate,
+                       const float *up, const float *output_gradient, float clamp, int64_t n);
+int gn_exp(float *destination, const float *source, int64_t n);
+int gn_sigmoid(float *destination, const float *source, int64_t n);
+int gn_tanh(float *destination, const float *source, int64_t n);
+int gn_rsqrt(float *destination, const float *source, int64_t n);
+
+/* ---- Reductions (kernels/backend.go:70-78) ------------------------------- */
+int gn_sum(const float *values, int64_t n, float *result);
+int gn_max(const float *values, int64_t n, float *result);
+int gn_argmax(const float *values, int64_t n, int64_t *result);
+
+/* ---- LinearAlgebra (kernels/backend.go:82-93) ---------------------------- */
+int gn_matmul(float *destination, const float *left, const float *right, int64_t row_count,
+              int64_t column_count, int64_t inner_count);
+int gn_matmul_transposed(float *destination, const float *left, const float *right,
+                         int64_t row_count, int64_t column_count, int64_t inner_count);
+int gn_dot_product(const float *left, int64_t left_len, const float *right, int64_t right_len,
+                   float *result);
+
+/* ---- Indexer (kernels/backend.go:103-116) -------------------------------- */
+int gn_indexer_scores(float *destination, const float *query, const float *key,
+                      const float *weight, int64_t row_count, int64_t block_count,
+                      int64_t head_count, int64_t dim);
+int gn_indexer_block_max(float *destination, const float *scores, int64_t row_count,
+                         int64_t block_count, int64_t group_size);
+
+/* ---- MoE (kernels/backend.go:119-141) ------------------------------------ */
+int gn_topk_indices(int32_t *destination, const float *scores, int64_t row_count,
+                    int64_t count, int64_t k);
+int gn_moe_gate_topk(const float *logits, const float *bias, float *probs, int32_t *selected,
+                     float *selected_weights, int64_t row_count, int64_t expert_count,
+                     int64_t k);
+int gn_grouped_matmul_transposed(float *destination, const float *input, const float *weight,
+                                 const int32_t *token_counts, int64_t expert_count,
+                                 int64_t column_count, int64_t inner_count);
+
+/* ---- Rows (kernels/backend.go:145-153) ----------------------------------- */
+int gn_softmax_last_dim(float *destination, const float *source, int64_t row_count,
+                        int64_t column_count);
+int gn_rmsnorm_last_dim(float *destination, const float *source, int64_t row_count,
+                        int64_t column_count, float epsilon);
+
+/* ---- Attention (kernels/backend.go:155-283) ------------------------------ */
+/* AttentionForward: query [query_length, head_dim], key/value
+ * [key_length, head_dim]; window < 0 is full causal context; segment_ids
+ * (nullable, segment_count entries) is the sample-level mask; log_sum_exp is
+ * nullable. */
+int gn_attention_forward(const float *query, const float *key, const float *value,
+                         const int32_t *segment_ids, int64_t segment_count, int64_t query_length,
+                         int64_t key_length, int64_t head_dim, int64_t position_offset,
+                         int64_t window, float *output, float *log_sum_exp);
+/* AttentionBackward: gradients ACCUMULATE into query/key/value_gradient;
+ * row_correction and segment_ids are nullable. */
+int gn_attention_backward(const float *query, const float *key, const float *value,
+                          const float *output, const float *output_gradient,
+                          const float *log_sum_exp, const float *row_correction,
+                          const int32_t *segment_ids, int64_t segment_count,
+                          int64_t query_length, int64_t key_length, int64_t head_dim,
+                          int64_t position_offset, int64_t window, float *query_gradient,
+                          float *key_gradient, float *value_gradient);
+/* AttentionForwardSplit over keys [key_start, key_end); overwrites
+ * accumulator [query_length, head_dim], maximum and sum [query_length]. */
+int gn_attention_forward_split(const float *query, const float *key, const float *value,
+                               const int32_t *segment_ids, int64_t segment_count,
+                               int64_t query_length, int64_t key_length, int64_t head_dim,
+                               int64_t position_offset, int64_t window, int64_t key_start,
+                               int64_t key_end, float *accumulator, float *maximum, float *sum);
+/* AttentionCombine of part_count shards given as pointer arrays. */
+int gn_attention_combine(const float *const *accumulators, const float *const *maxima,
+                         const float *const *sums, int64_t part_count, int64_t query_length,
+                         int64_t head_dim, float *output, float *log_sum_exp);
+
+/* ---- Session: device-resident model for the fused RL step --------------- */
+/* model.Config (model/config.go:9-124), dense preset fields. */
+typedef struct gn_config {
+  int32_t sequence_len;
+  int32_t vocab_size;
+  int32_t n_layer;
+  int32_t n_head;
+  int32_t n_kv_head;
+  int32_t n_embd;
+  int32_t rotary_dims;
+  char window_pattern[16];
+} gn_config;
+
+typedef struct gn_session gn_session;
+
+/* model.NewTransformer (model/transformer.go:50-80) on `device`. */
+int gn_session_create(const gn_config *config, int device, gn_session **out);
+int gn_session_destroy(gn_session *session);
+/* Total float count of the flat parameter vector: every tensor of
+ * Transformer.NamedParameters in ParameterNames (sorted) order
+ * (model/params.go:14-113). */
+int gn_session_param_total(const gn_session *session, int64_t *total);
+/* Name, shape and offset of the index-th parameter in that order. */
+int gn_session_param_info(const gn_session *session, int32_t index, char *name, size_t name_cap,
+                          int64_t *rows, int64_t *cols, int64_t *offset);
+int gn_session_param_count(const gn_session *session, int32_t *count);
+int gn_session_set_params(gn_session *session, const float *params, int64_t count);
+int gn_session_get_params(const gn_session *session, float *params, int64_t count);
+/* Parameter gradients (Tensor.Grad of every parameter) in the same layout. */
+int gn_session_get_grads(const gn_session *session, float *grads, int64_t count);
+/* Transformer.ZeroGrad (model/params.go:97-101). */
+int gn_session_zero_grads(gn_session *session);
+
+/* Transformer.Forward without a cache (model/transformer.go:211-214):
+ * logits [batch, seq_len, vocab] of ids [batch, seq_len]. */
+int gn_forward(gn_session *session, const int32_t *ids, int32_t batch, int32_t seq_len,
+               float *logits);
+
+/* Engine.GenerateBatchWith (inference/engine.go:336-369) for `groups`
+ * prompts at once, each expanded to `samples` rows and sampled from its own
+ * tensors.RNG stream seeds[g].  rows_out is [groups*samples,
+ * prompt_len+max_tokens] (prompt + completion, terminal token excluded),
+ * lengths_out [groups*samples]. */
+int gn_generate_batch(gn_session *session, const int32_t *prompts, int32_t groups,
+                      int32_t prompt_len, int32_t samples, int32_t max_tokens, float temperature,
+                      int32_t top_k, const uint64_t *seeds, int32_t *rows_out,
+                      int32_t *lengths_out);
+
+/* trainer.PolicyGradientStep (trainer/rl.go:14-60): teacher-forced
+ * recompute of inputs [batch, seq_len], per-token NLL (nll_out, nullable,
+ * [batch*seq_len]; logp = -nll), loss = sum_valid nll*adv/norm, and the
+ * backward of that loss ACCUMULATED into the session's parameter gradients. */
+int gn_policy_gradient_step(gn_session *session, const int32_t *inputs, const int32_t *targets,
+                            int32_t batch, int32_t seq_len, const float *advantages, float norm,
+                            float *loss_out, float *nll_out);
+
+/* One cmd/chat_rl step (cmd/chat_rl/main.go:101-183) without the optimizer:
+ * rollouts of every group, group-mean advantages of the supplied rewards,
+ * padding/masking, and PolicyGradientStep.  Outputs as gn_generate_batch plus
+ * advantages_out [groups*samples], max_len_out and loss_out. */
+int gn_rl_step(gn_session *session, const int32_t *prompts, int32_t groups, int32_t prompt_len,
+               int32_t samples, int32_t max_tokens, float temperature, int32_t top_k,
+               const uint64_t *seeds, const float *rewards, int32_t *rows_out,
+               int32_t *lengths_out, float *advantages_out, int32_t *max_len_out,
+               float *loss_out);
+
+/* inference.SampleNextToken (inference/sampler.go:16-60) on host logits
+ * [rows, vocab] with the tensors.RNG state rng_state = {hi, lo} of Go's PCG,
+ * which is advanced past the rows*vocab draws consumed. */
+int gn_sample_next_token(const float *logits, int64_t rows, int64_t vocab, uint64_t *rng_state,
+                         float temperature, int64_t top_k, int32_t *out);
+
+/* Device time (ms) the session spent in its most recent calls, by phase, and
+ * the average duration of the named kernel class measured with HIP events on
+ * the session stream.  Enabled by gn_session_set_timing(session, 1). */
+typedef struct gn_timing {
+  double rollout_ms;        /* gn_generate_batch wall time on device */
+  double decode_attn_ms;    /* sum over decode-attention launches */
+  int64_t decode_attn_launches;
+  double decode_attn_bytes; /* algorithmic K/V bytes those launches read */
+  double train_ms;          /* gn_policy_gradient_step on device */
+  double gemm_ms;           /* GEMM launches inside the train step */
+  double gemm_flops;        /* algorithmic flops of those launches */
+  int64_t gemm_launches;
+} gn_timing;
+int gn_session_set_timing(gn_session *session, int enabled);
+int gn_session_get_timing(const gn_session *session, gn_timing *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
