@@ -22,75 +22,154 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
-// Decode
+// Decode: one 256-thread block per (row, kv-head, split of up to 256 keys);
+// each wave streams a contiguous quarter of the split.  Lanes form 8 groups
+// of 8: group g takes key 8*step + g, lane part p of the group its dims
+// [16p, 16p+16), so one step of a wave reads 8 whole K rows and 8 whole V
+// rows (64 contiguous bytes per lane), and the next step's rows are loaded
+// before the current step is computed.  Scores reduce over the 8 lanes of a
+// group; an online softmax per head (running max / sum over the wave's keys)
+// rescales the per-lane P.V accumulators; at the end the 8 groups and then
+// the 4 waves are merged.  All r query heads of the GQA group share every
+// K/V load.  The split's unnormalized output, max and sum go to `part`.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
-  constexpr int MAXR = 8;
-  __shared__ __attribute__((aligned(16))) float qs[MAXR][HD];
-  __shared__ float ps[MAXR][64];
-  const int lane = threadIdx.x;
+static constexpr int DEC_KPS = 256;  // keys per split
+static constexpr int DEC_MAXR = 8;   // max GQA ratio
+
+__device__ __forceinline__ float xor_groups_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 8, 64));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float xor_groups_sum(float v) {
+  v += __shfl_xor(v, 8, 64);
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
+}
+
+template <int R>
+__device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
+  __shared__ __attribute__((aligned(16))) float qs[R][HD];
+  __shared__ __attribute__((aligned(16))) float red[4][R][HD];
+  __shared__ float wm[4][R], wl[4][R];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int g = lane >> 3, part = lane & 7;
   const int bh = blockIdx.x, s = blockIdx.y;
   const int row = bh / a.Hkv, hk = bh % a.Hkv;
-  const int r = a.Hq / a.Hkv;
-  const int ks = a.kstart + s * 64;
-  const int ke = min(a.kend, ks + 64);
-  const float* qrow = a.q + ((int64_t)row * a.Hq + hk * r) * HD;
-  for (int i = lane; i < r * HD; i += 64) qs[i / HD][i % HD] = qrow[i];
+  const int ks = a.kstart + s * DEC_KPS;
+  const int nk = min(a.kend, ks + DEC_KPS) - ks;
+  const float* qrow = a.q + ((int64_t)row * a.Hq + hk * R) * HD;
+  for (int i = tid; i < R * HD; i += 256) qs[i / HD][i % HD] = qrow[i];
   __syncthreads();
-  const int64_t cbase = ((int64_t)row * a.Hkv + hk) * a.maxSeq;
-  const int kj = ks + lane;
-  const bool valid = kj < ke;
-  float sc[MAXR];
+  float qv[R][16];
 #pragma unroll
-  for (int h = 0; h < MAXR; h++) sc[h] = 0.f;
-  if (valid) {
-    const v4f* kp = reinterpret_cast<const v4f*>(a.kc + (cbase + kj) * HD);
-#pragma unroll 8
-    for (int d4 = 0; d4 < HD / 4; d4++) {
-      v4f kv = kp[d4];
+  for (int h = 0; h < R; h++)
 #pragma unroll
-      for (int h = 0; h < MAXR; h++) {
-        if (h < r) {
-          v4f qv = *reinterpret_cast<const v4f*>(&qs[h][4 * d4]);
-          sc[h] += kv[0] * qv[0] + kv[1] * qv[1] + kv[2] * qv[2] + kv[3] * qv[3];
-        }
+    for (int i = 0; i < 16; i++) qv[h][i] = qs[h][16 * part + i];
+
+  const int q4 = (nk + 3) / 4;
+  const int j0 = wid * q4, j1 = min(nk, j0 + q4);
+  const int64_t cbase = ((int64_t)row * a.Hkv + hk) * a.maxSeq + ks;
+  const float* kb = a.kc + cbase * HD + 16 * part;
+  const float* vb = a.vc + cbase * HD + 16 * part;
+  float m[R], l[R], acc[R][16];
+#pragma unroll
+  for (int h = 0; h < R; h++) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[h][i] = 0.f;
+  }
+  v4f kc[4], vc[4];
+  auto load = [&](int j, v4f* kd, v4f* vd) {
+    const int jj = j < j1 ? j : j0;  // clamp (value unused when j >= j1)
+    const v4f* kp = reinterpret_cast<const v4f*>(kb + (int64_t)jj * HD);
+    const v4f* vp = reinterpret_cast<const v4f*>(vb + (int64_t)jj * HD);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      kd[i] = kp[i];
+      vd[i] = vp[i];
+    }
+  };
+  if (j0 < j1) load(j0 + g, kc, vc);
+  for (int jb = j0; jb < j1; jb += 8) {
+    const int j = jb + g;
+    const bool valid = j < j1;
+    v4f kn[4], vn[4];
+    if (jb + 8 < j1) load(jb + 8 + g, kn, vn);
+#pragma unroll
+    for (int h = 0; h < R; h++) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        d += kc[i][0] * qv[h][4 * i] + kc[i][1] * qv[h][4 * i + 1] + kc[i][2] * qv[h][4 * i + 2] +
+             kc[i][3] * qv[h][4 * i + 3];
+      d += __shfl_xor(d, 1, 64);
+      d += __shfl_xor(d, 2, 64);
+      d += __shfl_xor(d, 4, 64);
+      const float sc = valid ? d : -INFINITY;
+      const float mn = fmaxf(m[h], xor_groups_max(sc));
+      const float scale = expf(m[h] - mn);  // 0 while m is -inf
+      const float p = valid ? expf(sc - mn) : 0.f;
+      l[h] = l[h] * scale + xor_groups_sum(p);  // one p per key group
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        acc[h][4 * i] = acc[h][4 * i] * scale + p * vc[i][0];
+        acc[h][4 * i + 1] = acc[h][4 * i + 1] * scale + p * vc[i][1];
+        acc[h][4 * i + 2] = acc[h][4 * i + 2] * scale + p * vc[i][2];
+        acc[h][4 * i + 3] = acc[h][4 * i + 3] * scale + p * vc[i][3];
       }
+      m[h] = mn;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      kc[i] = kn[i];
+      vc[i] = vn[i];
     }
   }
-  float mh[MAXR], lh[MAXR];
+  // merge the 8 key groups of the wave, then the 4 waves
 #pragma unroll
-  for (int h = 0; h < MAXR; h++) {
-    if (h < r) {
-      float x = valid ? sc[h] : -INFINITY;
-      float m = warp_max(x);
-      float p = valid ? expf(x - m) : 0.f;
-      ps[h][lane] = p;
-      mh[h] = m;
-      lh[h] = warp_sum(p);
+  for (int h = 0; h < R; h++) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[h][i] = xor_groups_sum(acc[h][i]);
+    if (g == 0)
+#pragma unroll
+      for (int i = 0; i < 16; i++) red[wid][h][16 * part + i] = acc[h][i];
+    if (lane == 0) {
+      wm[wid][h] = m[h];
+      wl[wid][h] = l[h];
     }
   }
   __syncthreads();
-  v2f acc[MAXR];
+  float* out = a.part + ((int64_t)bh * a.nsplit + s) * R * (HD + 2);
+  for (int i = tid; i < R * HD; i += 256) {
+    const int h = i / HD, d = i % HD;
+    float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
+    float o = 0.f, L = 0.f;
 #pragma unroll
-  for (int h = 0; h < MAXR; h++) acc[h] = (v2f){0.f, 0.f};
-  const int nk = ke - ks;
-  const float* vbase = a.vc + (cbase + ks) * HD + 2 * lane;
-  for (int j = 0; j < nk; j++) {
-    v2f vv = *reinterpret_cast<const v2f*>(vbase + (int64_t)j * HD);
-#pragma unroll
-    for (int h = 0; h < MAXR; h++)
-      if (h < r) acc[h] += ps[h][j] * vv;
-  }
-  float* out = a.part + ((int64_t)bh * a.nsplit + s) * r * (HD + 2);
-#pragma unroll
-  for (int h = 0; h < MAXR; h++) {
-    if (h < r) {
-      *reinterpret_cast<v2f*>(out + h * (HD + 2) + 2 * lane) = acc[h];
-      if (lane == 0) {
-        out[h * (HD + 2) + HD] = mh[h];
-        out[h * (HD + 2) + HD + 1] = lh[h];
-      }
+    for (int w = 0; w < 4; w++) {
+      float sc = wm[w][h] > -INFINITY ? expf(wm[w][h] - M) : 0.f;
+      o += red[w][h][d] * sc;
+      L += wl[w][h] * sc;
     }
+    out[h * (HD + 2) + d] = o;
+    if (d == 0) {
+      out[h * (HD + 2) + HD] = M;
+      out[h * (HD + 2) + HD + 1] = L;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
+  switch (a.Hq / a.Hkv) {
+    case 1: decode_attn_body<1>(a); break;
+    case 2: decode_attn_body<2>(a); break;
+    case 3: decode_attn_body<3>(a); break;
+    case 4: decode_attn_body<4>(a); break;
+    case 5: decode_attn_body<5>(a); break;
+    case 6: decode_attn_body<6>(a); break;
+    case 8: decode_attn_body<8>(a); break;
+    default: break;
   }
 }
 
@@ -113,10 +192,10 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
 }
 
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
-  GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= 8, "decode attention: GQA ratio must be <= 8");
+  GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= DEC_MAXR, "decode attention: GQA ratio must be <= 8");
   GN_CHECK(a.kend > a.kstart, "decode attention: empty key range");
-  a.nsplit = (int)ceil_div(a.kend - a.kstart, 64);
-  hipLaunchKernelGGL(decode_attn_kernel, dim3(a.rows * a.Hkv, a.nsplit), dim3(64), 0, st, a);
+  a.nsplit = (int)ceil_div(a.kend - a.kstart, DEC_KPS);
+  hipLaunchKernelGGL(decode_attn_kernel, dim3(a.rows * a.Hkv, a.nsplit), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
   hipLaunchKernelGGL(decode_combine_kernel, dim3(a.rows * a.Hq), dim3(HD), 0, st, a);
   GN_HIP(hipGetLastError());

@@ -263,16 +263,19 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   // Tile choice: the 128x128 tile when it yields enough workgroups to cover
   // the 256 CUs, otherwise 64x64; split K when even that underfills the chip
   // and K is long enough to share.
+  // Long-K products (weight gradients, K = tokens) keep the 128x128 tile and
+  // split K instead, since each split still has thousands of K steps.
   const int64_t cus = 256;
   const int64_t big = ceil_div(d.M, 128) * ceil_div(d.N, 128);
-  const bool use_big = big >= cus;
+  const bool long_k = d.K >= 4096;
+  const bool use_big = big >= cus || long_k;
   const int bm = use_big ? 128 : 64, bn = use_big ? 128 : 64;
   const int64_t tiles = ceil_div(d.M, bm) * ceil_div(d.N, bn);
   int splits = 1;
   if (d.force_splits > 0) {
     splits = d.force_splits;
   } else if (tiles < 2 * cus && d.K >= 512) {
-    splits = (int)std::min<int64_t>(ceil_div(2 * cus, tiles), d.K / 256);
+    splits = (int)std::min<int64_t>(ceil_div(2 * cus, tiles), d.K / (long_k ? 1024 : 256));
     splits = std::max(1, std::min(splits, 64));
   }
   int kps = (int)ceil_div(ceil_div(d.K, splits), 16) * 16;

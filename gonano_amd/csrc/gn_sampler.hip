@@ -3,13 +3,19 @@
 //
 // The reference draws one tensors.RNG Float32 for EVERY vocabulary entry of
 // every row, masked or not (tensors/random.go:66-78), so draw v of row i of a
-// call starts at stream offset i*V + v.  Each thread owns a contiguous chunk
-// of the row, jumps Go's 128-bit PCG LCG to its chunk start in O(log n)
-// (affine-map squaring), and steps sequentially; the DXSM output, the
-// Float32 mapping and the float64 Gumbel transform are evaluated only for
-// entries that survive the top-k mask (value >= k-th largest, ties kept).
-// The k-th largest comes from a 4-pass 8-bit radix select over the
-// order-preserving integer image of the floats.
+// call is the (i*V + v + 1)-th step of the group's stream.  Go's PCG is a
+// 128-bit LCG, so any step is reachable in O(log n) by squaring the affine
+// map; the DXSM output, the Float32 mapping and the float64 Gumbel transform
+// are evaluated only for entries that survive the top-k mask.
+//
+// Top-k threshold (the k-th largest value of the row, ties kept):
+//  1. one pass over the row computes the maxima of ngroups contiguous groups;
+//  2. the k-th largest group maximum L is a lower bound of the k-th largest
+//     value (each of the k groups holds a value >= L);
+//  3. the values >= L (a few hundred at most for real logits) are compacted
+//     into LDS and bitonic-sorted; the k-th of them is the threshold.
+// If the candidates overflow the LDS buffer (e.g. massively tied logits) the
+// row falls back to an exact 4-pass 8-bit radix select over the whole row.
 #include "gn_model.h"
 
 namespace gn {
@@ -32,7 +38,6 @@ __device__ __forceinline__ u128 add128(u128 a, u128 b) {
 // Go math/rand/v2 PCG constants (multiplier and increment of the LCG).
 __device__ __forceinline__ u128 pcg_mul() { return {0x2360ED051FC65DA4ull, 0x4385DF649FCCF645ull}; }
 __device__ __forceinline__ u128 pcg_inc() { return {6364136223846793005ull, 1442695040888963407ull}; }
-
 __device__ __forceinline__ u128 pcg_step(u128 s) { return add128(mul128(s, pcg_mul()), pcg_inc()); }
 
 // state after n further LCG steps
@@ -44,8 +49,7 @@ __device__ u128 pcg_advance(u128 s, uint64_t n) {
       am = mul128(am, cm);
       ap = add128(mul128(ap, cm), cp);
     }
-    u128 cm1 = add128(cm, u128{0, 1});
-    cp = mul128(cm1, cp);
+    cp = mul128(add128(cm, u128{0, 1}), cp);
     cm = mul128(cm, cm);
     n >>= 1;
   }
@@ -63,6 +67,14 @@ __device__ __forceinline__ float pcg_float32(u128 s) {
   return (float)((u << 8) >> 8) / 16777216.0f;
 }
 
+// Gumbel score of entry v whose draw state is s (tensors/random.go:68-73).
+__device__ __forceinline__ float gumbel_score(float zv, float T, u128 s) {
+  float u = pcg_float32(s);
+  if (u <= 0.f) u = 1e-12f;
+  float gum = -(float)log(-log((double)u));
+  return __fadd_rn(__fdiv_rn(zv, T), gum);
+}
+
 __device__ __forceinline__ uint32_t order_key(float f) {
   uint32_t b = __float_as_uint(f);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -72,105 +84,181 @@ __device__ __forceinline__ float key_float(uint32_t u) {
   return __uint_as_float(b);
 }
 
-__global__ __launch_bounds__(256) void sampler_kernel(SamplerArgs a) {
+// Merges per-thread (score, index) winners: larger score, ties to the
+// smaller index; index -1 means "none".
+__device__ __forceinline__ void better(float& bv, int& bi, float ov, int oi) {
+  if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+// Descending bitonic sort of n (power of two) floats in LDS by all threads.
+__device__ void bitonic_desc(float* a, int n) {
+  for (int k = 2; k <= n; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        int ixj = i ^ j;
+        if (ixj > i) {
+          bool desc = (i & k) == 0;
+          float x = a[i], y = a[ixj];
+          if (desc ? (x < y) : (x > y)) {
+            a[i] = y;
+            a[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+static constexpr int NT = 256;
+static constexpr int MAXG = 4096;  // group maxima
+static constexpr int MAXC = 2048;  // candidates
+
+__global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
+  __shared__ float buf[MAXG];
+  __shared__ int cand_i[MAXC];
   __shared__ uint32_t hist[4][256];
   __shared__ uint32_t sel_prefix, sel_k;
-  __shared__ float best_v[4];
-  __shared__ int best_i[4];
+  __shared__ int ncand;
+  __shared__ float best_v[NT / 64];
+  __shared__ int best_i[NT / 64];
+  __shared__ uint64_t base_s[2];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int row = blockIdx.x;
   const float* z = a.logits + (int64_t)row * a.ldl;
   const int V = a.V;
+  float bv = -INFINITY;
+  int bi = -1;
 
   if (a.temperature <= 0.f) {
     // argMax: first index of the largest value (sampler.go:37-45)
-    float bv = -INFINITY;
-    int bi = -1;
-    for (int v = tid; v < V; v += 256)
-      if (bi < 0 || z[v] > bv) { bv = z[v]; bi = v; }
-    for (int o = 32; o > 0; o >>= 1) {
-      float ov = __shfl_xor(bv, o, 64);
-      int oi = __shfl_xor(bi, o, 64);
-      if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
-    }
-    if (lane == 0) { best_v[wid] = bv; best_i[wid] = bi; }
-    __syncthreads();
+    for (int v = tid; v < V; v += NT) better(bv, bi, z[v], v);
+  } else {
+    const int g = row / a.samples_per_group, ig = row % a.samples_per_group;
     if (tid == 0) {
-      for (int w = 1; w < 4; w++)
-        if (best_i[w] >= 0 && (bi < 0 || best_v[w] > bv || (best_v[w] == bv && best_i[w] < bi))) {
-          bv = best_v[w]; bi = best_i[w];
-        }
-      a.out[row] = bi < 0 ? 0 : bi;
+      u128 s = {a.base_states[2 * g], a.base_states[2 * g + 1]};
+      s = pcg_advance(s, (uint64_t)ig * (uint64_t)V);
+      base_s[0] = s.hi;
+      base_s[1] = s.lo;
     }
-    return;
-  }
-
-  // ---- threshold: k-th largest (multiset), or -inf when no top-k mask -----
-  float thr = -INFINITY;
-  const bool masking = a.top_k > 0 && a.top_k < V;
-  if (masking) {
-    uint32_t prefix = 0, pmask = 0, kk = (uint32_t)a.top_k;
-    for (int pass = 0; pass < 4; pass++) {
-      const int shift = 24 - 8 * pass;
-      for (int i = tid; i < 4 * 256; i += 256) (&hist[0][0])[i] = 0;
+    const int k = a.top_k;
+    const bool masking = k > 0 && k < V;
+    const float T = a.temperature;
+    __syncthreads();
+    const u128 rowbase = {base_s[0], base_s[1]};
+    if (!masking) {
+      // every entry is a candidate: walk the stream sequentially per chunk
+      const int chunk = (V + NT - 1) / NT;
+      const int v0 = tid * chunk, v1 = min(V, v0 + chunk);
+      u128 s = pcg_advance(rowbase, (uint64_t)v0);
+      for (int v = v0; v < v1; v++) {
+        s = pcg_step(s);
+        better(bv, bi, gumbel_score(z[v], T, s), v);
+      }
+    } else {
+      // 1) group maxima
+      int gs = max(1, min(256, V / (4 * k)));
+      int ngroups = (V + gs - 1) / gs;
+      if (ngroups > MAXG) {
+        gs = (V + MAXG - 1) / MAXG;
+        ngroups = (V + gs - 1) / gs;
+      }
+      for (int gi = tid; gi < ngroups; gi += NT) {
+        float m = -INFINITY;
+        const int e = min(V, (gi + 1) * gs);
+        for (int v = gi * gs; v < e; v++) m = fmaxf(m, z[v]);
+        buf[gi] = m;
+      }
+      int np2 = 1;
+      while (np2 < ngroups) np2 <<= 1;
+      for (int gi = ngroups + tid; gi < np2; gi += NT) buf[gi] = -INFINITY;
+      if (tid == 0) ncand = 0;
       __syncthreads();
-      for (int v = tid; v < V; v += 256) {
-        uint32_t u = order_key(z[v]);
-        if ((u & pmask) == prefix) atomicAdd(&hist[wid][(u >> shift) & 255u], 1u);
+      bitonic_desc(buf, np2);
+      const float lower = k <= ngroups ? buf[k - 1] : -INFINITY;
+      __syncthreads();
+      // 2) compact candidates >= lower
+      for (int v = tid; v < V; v += NT) {
+        if (z[v] >= lower) {
+          int slot = atomicAdd(&ncand, 1);
+          if (slot < MAXC) cand_i[slot] = v;
+        }
       }
       __syncthreads();
-      if (tid == 0) {
-        uint32_t cum = 0;
-        int bin = 0;
-        for (int bb = 255; bb >= 0; bb--) {
-          uint32_t c = hist[0][bb] + hist[1][bb] + hist[2][bb] + hist[3][bb];
-          if (cum + c >= kk) { bin = bb; break; }
-          cum += c;
+      const int nc = ncand;
+      float thr;
+      if (nc <= MAXC) {
+        int cp2 = 1;
+        while (cp2 < nc) cp2 <<= 1;
+        for (int i = tid; i < cp2; i += NT) buf[i] = i < nc ? z[cand_i[i]] : -INFINITY;
+        __syncthreads();
+        bitonic_desc(buf, cp2);
+        thr = buf[k - 1];
+        __syncthreads();
+        // 3) Gumbel-max over the survivors, in index order per thread
+        for (int i = tid; i < nc; i += NT) {
+          const int v = cand_i[i];
+          const float zv = z[v];
+          if (zv >= thr) {
+            float sc = gumbel_score(zv, T, pcg_advance(rowbase, (uint64_t)v + 1));
+            better(bv, bi, sc, v);
+          }
         }
-        sel_prefix = prefix | ((uint32_t)bin << shift);
-        sel_k = kk - cum;
+      } else {
+        // exact fallback: radix select of the k-th largest over the row
+        uint32_t prefix = 0, pmask = 0, kk = (uint32_t)k;
+        for (int pass = 0; pass < 4; pass++) {
+          const int shift = 24 - 8 * pass;
+          for (int i = tid; i < 4 * 256; i += NT) (&hist[0][0])[i] = 0;
+          __syncthreads();
+          for (int v = tid; v < V; v += NT) {
+            uint32_t u = order_key(z[v]);
+            if ((u & pmask) == prefix) atomicAdd(&hist[wid][(u >> shift) & 255u], 1u);
+          }
+          __syncthreads();
+          if (tid == 0) {
+            uint32_t cum = 0;
+            int bin = 0;
+            for (int bb = 255; bb >= 0; bb--) {
+              uint32_t c = hist[0][bb] + hist[1][bb] + hist[2][bb] + hist[3][bb];
+              if (cum + c >= kk) { bin = bb; break; }
+              cum += c;
+            }
+            sel_prefix = prefix | ((uint32_t)bin << shift);
+            sel_k = kk - cum;
+          }
+          __syncthreads();
+          prefix = sel_prefix;
+          kk = sel_k;
+          pmask |= 255u << shift;
+          __syncthreads();
+        }
+        thr = key_float(prefix);
+        for (int v = tid; v < V; v += NT) {
+          const float zv = z[v];
+          if (zv >= thr) {
+            float sc = gumbel_score(zv, T, pcg_advance(rowbase, (uint64_t)v + 1));
+            better(bv, bi, sc, v);
+          }
+        }
       }
-      __syncthreads();
-      prefix = sel_prefix;
-      kk = sel_k;
-      pmask |= 255u << shift;
-      __syncthreads();
-    }
-    thr = key_float(prefix);
-  }
-
-  // ---- Gumbel-max over the surviving entries ------------------------------
-  const int g = row / a.samples_per_group, i = row % a.samples_per_group;
-  const int chunk = (V + 255) / 256;
-  const int v0 = tid * chunk, v1 = min(V, v0 + chunk);
-  u128 s = {a.base_states[2 * g], a.base_states[2 * g + 1]};
-  s = pcg_advance(s, (uint64_t)i * (uint64_t)V + (uint64_t)v0);
-  float bv = -INFINITY;
-  int bi = -1;
-  const float T = a.temperature;
-  for (int v = v0; v < v1; v++) {
-    s = pcg_step(s);
-    const float zv = z[v];
-    if (zv >= thr) {
-      float u = pcg_float32(s);
-      if (u <= 0.f) u = 1e-12f;
-      float gum = -(float)log(-log((double)u));
-      float sc = __fadd_rn(__fdiv_rn(zv, T), gum);
-      if (sc > bv) { bv = sc; bi = v; }
     }
   }
   for (int o = 32; o > 0; o >>= 1) {
     float ov = __shfl_xor(bv, o, 64);
     int oi = __shfl_xor(bi, o, 64);
-    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+    better(bv, bi, ov, oi);
   }
-  if (lane == 0) { best_v[wid] = bv; best_i[wid] = bi; }
+  if (lane == 0) {
+    best_v[wid] = bv;
+    best_i[wid] = bi;
+  }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < 4; w++)
-      if (best_i[w] >= 0 && (bi < 0 || best_v[w] > bv || (best_v[w] == bv && best_i[w] < bi))) {
-        bv = best_v[w]; bi = best_i[w];
-      }
+    for (int w = 1; w < NT / 64; w++) better(bv, bi, best_v[w], best_i[w]);
     a.out[row] = bi < 0 ? 0 : bi;
   }
 }
@@ -178,7 +266,7 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerArgs a) {
 void launch_sampler(const SamplerArgs& a, hipStream_t st) {
   if (a.rows <= 0) return;
   GN_CHECK(a.V > 0, "sampler: empty vocabulary");
-  hipLaunchKernelGGL(sampler_kernel, dim3(a.rows), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(sampler_kernel, dim3(a.rows), dim3(NT), 0, st, a);
   GN_HIP(hipGetLastError());
 }
 
