@@ -6,11 +6,10 @@
 // serves Linear forward (x.W^T), its input gradient (g.W), its weight
 // gradient (g^T.x, split over K) and kernels.Backend MatMul/MatMulTransposed.
 //
-// Tiles are staged through LDS in K-major order ([k][m]) so that the 16 lanes
-// feeding one MFMA row block read 16 consecutive floats; rows are padded by
-// 16 floats so the four k-rows a wave touches land on disjoint banks.  Two
-// LDS buffers alternate so the global loads of tile k+1 overlap the MFMAs of
-// tile k with a single barrier per iteration.
+// Operand tiles go from global memory straight into a ring of LDS stages
+// (global_load_lds_dwordx4, no VGPR staging), laid out so that MFMA fragments
+// are read with conflict-free LDS accesses; see TileIO.  One barrier per K
+// tile; the loads of the next S-1 tiles stay in flight behind the MFMAs.
 #include "gn_kernels.h"
 
 namespace gn {
@@ -26,13 +25,13 @@ struct GemmParams {
   int64_t lda, ldb, ldc, ldaux;
   int M, N, K;
   int k_per_split;
-  int tiles_m;
+  int tiles_m, tiles_n, splits;
   int epi;
   float alpha;
+  float* part;  // split-K: [splits][M][N] partial sums
 };
 
-__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, int row, int col, float v,
-                                              int split) {
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, int row, int col, float v) {
   if (row >= p.M || col >= p.N) return;
   const int64_t ci = (int64_t)row * p.ldc + col;
   switch (p.epi) {
@@ -60,16 +59,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, int row, int 
       p.C[ci] = u > 0.f ? (v * 2.f) * u : 0.f;
       break;
     }
-    case EPI_PARTIAL:
-      p.C[(int64_t)split * p.M * p.N + (int64_t)row * p.N + col] = v;
-      break;
   }
 }
 
 template <bool VEC>
 __device__ __forceinline__ v4f load4(const float* __restrict__ ptr, int valid) {
   v4f r = {0.f, 0.f, 0.f, 0.f};
-  if (VEC && valid == 4) {
+  if (VEC && valid >= 4) {
     r = *reinterpret_cast<const v4f*>(ptr);
   } else {
     if (valid > 0) r[0] = ptr[0];
@@ -80,158 +76,283 @@ __device__ __forceinline__ v4f load4(const float* __restrict__ ptr, int valid) {
   return r;
 }
 
-// Loads the [BK=16] x [BD] tile of an operand whose logical index is
-// (d, k), d in [d0, d0+BD), k in [k0, k0+16), into registers.
-template <int BD, int NT, bool KCONTIG, bool VEC>
-struct TileLoader {
-  static constexpr int NV = (BD * 16 / 4) / NT;  // float4 per thread
-  v4f v[NV];
-  __device__ __forceinline__ void load(const float* __restrict__ X, int64_t ld, int d0, int dmax,
-                                       int k0, int kmax, int tid) {
+static constexpr int GK = 32;  // K depth of one LDS tile
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One operand tile of BD rows (the M or N extent) by GK k values, moved from
+// global memory into LDS by a workgroup of NT threads.
+//
+// Interior tiles use global_load_lds_dwordx4: each lane's 16 bytes land in
+// LDS at (wave-uniform base) + lane * 16 without passing through VGPRs, so
+// the LDS image is a sequence of 16-byte slots, slot s filled by thread
+// s mod NT of instruction s / NT.  Which global float4 a lane fetches is free,
+// so the layout is chosen by the addresses: a K-contiguous operand
+// (X[d*ld + k]) is stored as [d][k] rows of GK floats (8 slots), an operand
+// contiguous in d (X[k*ld + d]) as [k][d] rows of BD floats, and the slot
+// column is XOR-swizzled with the row (row & 7, resp. row & 4) so the MFMA
+// fragment reads below hit distinct banks.  Edge tiles (rows past the
+// operand end, a partial last K tile, unaligned operands) go through VGPRs
+// with zero fill and store to the same slots.
+//
+// MFMA k order: for the 16-deep k group g, lane (r = lane & 15, q = lane >> 4)
+// holds k = 16g + 4q + c in component c, and MFMA c of the group consumes
+// component c of both operands.  Every k is paired with itself in A and B,
+// so the products summed are the same as in natural order.
+template <int BD, int NT, bool KCONTIG>
+struct TileIO {
+  static constexpr int ROWSLOTS = KCONTIG ? GK / 4 : BD / 4;  // 16-byte slots per LDS row
+  static constexpr int SIZE = BD * GK;                         // floats
+  static constexpr int NV = SIZE / 4 / NT;                     // slots per thread
+  static constexpr int RSTEP = NT / ROWSLOTS;                  // LDS rows per instruction
+  static_assert(NV >= 1 && NT % ROWSLOTS == 0 && RSTEP % 8 == 0, "tile shape");
+  int row0, col;  // the thread's first LDS row and logical slot column
+
+  static __device__ __forceinline__ int swz(int row) { return KCONTIG ? (row & 7) : (row & 4); }
+
+  __device__ __forceinline__ void init(int tid) {
+    row0 = tid / ROWSLOTS;
+    col = (tid % ROWSLOTS) ^ swz(row0);  // swz(row0 + i * RSTEP) == swz(row0)
+  }
+  __device__ __forceinline__ const float* src(const float* X, int64_t ld, int d0, int k0,
+                                              int i) const {
+    const int row = row0 + i * RSTEP;
+    return KCONTIG ? X + (int64_t)(d0 + row) * ld + (k0 + 4 * col)
+                   : X + (int64_t)(k0 + row) * ld + (d0 + 4 * col);
+  }
+  // The whole tile lies inside the operand and is 16-byte aligned.
+  __device__ __forceinline__ void load_direct(const float* __restrict__ X, int64_t ld, int d0,
+                                              int k0, float* S, int wave) const {
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+      __builtin_amdgcn_global_load_lds((const void*)src(X, ld, d0, k0, i),
+                                       (lds_void*)(S + 4 * (i * NT + 64 * wave)), 16, 0, 0);
+  }
+  // Edge tiles: zero outside d < dmax, k < kmax.
+  template <bool VEC>
+  __device__ __forceinline__ void load_edge(const float* __restrict__ X, int64_t ld, int d0,
+                                            int dmax, int k0, int kmax, float* S, int tid) const {
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-      int idx = tid + i * NT;
-      if (KCONTIG) {
-        int d = idx % BD, kq = idx / BD;
-        int gd = d0 + d, gk = k0 + 4 * kq;
-        int valid = (gd < dmax) ? min(4, kmax - gk) : 0;
-        v[i] = load4<VEC>(X + (int64_t)gd * ld + gk, valid);
-      } else {
-        int k = idx / (BD / 4), dq = idx % (BD / 4);
-        int gd = d0 + 4 * dq, gk = k0 + k;
-        int valid = (gk < kmax) ? min(4, dmax - gd) : 0;
-        v[i] = load4<VEC>(X + (int64_t)gk * ld + gd, valid);
-      }
+      const int row = row0 + i * RSTEP;
+      int valid;
+      if (KCONTIG) valid = d0 + row < dmax ? kmax - (k0 + 4 * col) : 0;
+      else valid = k0 + row < kmax ? dmax - (d0 + 4 * col) : 0;
+      *reinterpret_cast<v4f*>(&S[4 * (i * NT + tid)]) = load4<VEC>(src(X, ld, d0, k0, i), valid);
     }
   }
-  template <int LD>
-  __device__ __forceinline__ void store(float* __restrict__ S, int tid) {
-#pragma unroll
-    for (int i = 0; i < NV; i++) {
-      int idx = tid + i * NT;
-      if (KCONTIG) {
-        int d = idx % BD, kq = idx / BD;
-#pragma unroll
-        for (int j = 0; j < 4; j++) S[(4 * kq + j) * LD + d] = v[i][j];
-      } else {
-        int k = idx / (BD / 4), dq = idx % (BD / 4);
-        *reinterpret_cast<v4f*>(&S[k * LD + 4 * dq]) = v[i];
-      }
+  // MFMA operand for the 16 rows starting at tile row d (a multiple of 16),
+  // k group g.
+  static __device__ __forceinline__ v4f frag(const float* __restrict__ S, int d, int g, int lane) {
+    const int r = lane & 15, q = lane >> 4;
+    if (KCONTIG) {
+      const int row = d + r;
+      return *reinterpret_cast<const v4f*>(&S[4 * (row * ROWSLOTS + ((4 * g + q) ^ swz(row)))]);
     }
+    v4f f;
+    const int dd = d + r;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int k = 16 * g + 4 * q + c;
+      f[c] = S[4 * (k * ROWSLOTS + ((dd >> 2) ^ swz(k))) + (dd & 3)];
+    }
+    return f;
   }
 };
 
-template <int BM, int BN, int WM, int WN, bool AK, bool BK, bool VEC>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmParams p) {
+// Workgroup -> (tile row, tile column, split).  Workgroups are dealt to the
+// 8 XCDs round-robin; renumbering gives each XCD a contiguous range of the
+// logical order, so the tiles that share operand rows share one L2.  The
+// logical order walks groups of 8 tile rows, column by column, so a group's
+// A rows and the B columns in flight stay cache-resident.
+__device__ __forceinline__ void tile_coords(const GemmParams& p, int& tm, int& tn, int& split) {
+  const int total = p.tiles_m * p.tiles_n * p.splits;
+  const int bid = blockIdx.x;
+  const int x = bid % 8, q = total / 8, rem = total % 8;
+  const int logical = x * q + min(x, rem) + bid / 8;
+  const int T = p.tiles_m * p.tiles_n;
+  split = logical / T;
+  const int t = logical - split * T;
+  constexpr int GM = 8;
+  const int per_group = GM * p.tiles_n;
+  const int first = (t / per_group) * GM;
+  const int gsz = min(p.tiles_m - first, GM);
+  const int r = t % per_group;
+  tm = first + r % gsz;
+  tn = r / gsz;
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] and [15:14],
+// expcnt[6:4], lgkmcnt[11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+}
+
+// Waits until at most `ahead` tiles of PT LDS-DMA instructions each are
+// still in flight (ahead <= MAXA), with every LDS access of this wave done.
+template <int PT, int MAXA>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+  if constexpr (MAXA > 0) {
+    if (ahead >= MAXA) {
+      wait_vm_lgkm0<PT * MAXA>();
+      return;
+    }
+    wait_tiles<PT, MAXA - 1>(ahead);
+  } else {
+    wait_vm_lgkm0<0>();
+  }
+}
+
+// Workgroup barrier for the tile pipeline.  No release fence: a fence would
+// make the compiler wait for every outstanding LDS-DMA load (vmcnt(0)) and
+// defeat the prefetch; the explicit wait before it covers this wave's own
+// accesses.  The acquire fence keeps LDS reads below the barrier.
+__device__ __forceinline__ void tile_barrier() {
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// C tile of BM x BN per workgroup of WM x WN waves, K in GK-deep tiles
+// through an S-stage LDS ring: tile kt + S - 1 is in flight while tile kt
+// is multiplied.  With p.splits > 1 each workgroup sums one K range into
+// p.part and gemm_reduce_kernel applies the epilogue.
+template <int BM, int BN, int WM, int WN, int S, bool AK, bool BK, bool VEC>
+__global__ __launch_bounds__(64 * WM * WN, 2) void gemm_kernel(GemmParams p) {
   constexpr int NT = 64 * WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int MI = TM / 16, NI = TN / 16;
-  constexpr int LDA = BM + 16, LDB = BN + 16;
-  __shared__ __attribute__((aligned(16))) float As[2][16 * LDA];
-  __shared__ __attribute__((aligned(16))) float Bs[2][16 * LDB];
+  using LA = TileIO<BM, NT, AK>;
+  using LB = TileIO<BN, NT, BK>;
+  constexpr int PT = LA::NV + LB::NV;  // LDS-DMA instructions per tile and thread
+  static_assert(S >= 2 && PT * (S - 2) < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(16))) float As[S][LA::SIZE];
+  __shared__ __attribute__((aligned(16))) float Bs[S][LB::SIZE];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid % WM, wn = wid / WM;
-  const int tile = blockIdx.x;
-  const int m0 = (tile % p.tiles_m) * BM, n0 = (tile / p.tiles_m) * BN;
-  const int split = blockIdx.z;
+  int tm, tn, split;
+  tile_coords(p, tm, tn, split);
+  const int m0 = tm * BM, n0 = tn * BN;
   const int kbeg = split * p.k_per_split;
   const int kend = min(p.K, kbeg + p.k_per_split);
+  const int nkt = kend > kbeg ? (kend - kbeg + GK - 1) / GK : 0;
+  const bool interior = VEC && m0 + BM <= p.M && n0 + BN <= p.N;
+  const int nfull = interior ? (kend - kbeg) / GK : 0;
 
-  // Two-level summation: MFMAs accumulate one 64-deep K block into `blk`,
-  // which is folded into `acc` between blocks.  Rounding error then grows
-  // with 64 + K/64 instead of K, which matters for the weight gradients (K =
-  // tokens) and the logits-gradient contraction (K = vocabulary).
-  constexpr int FOLD = 4;  // K tiles of 16 per block
-  v4f acc[MI][NI], blk[MI][NI];
+  LA la;
+  LB lb;
+  la.init(tid);
+  lb.init(tid);
+  // Fills LDS stage `buf` with K tile kt; readable after wait_tiles and
+  // tile_barrier.
+  auto load = [&](int kt, int buf) {
+    const int k0 = kbeg + kt * GK;
+    if (kt < nfull) {
+      la.load_direct(p.A, p.lda, m0, k0, As[buf], wid);
+      lb.load_direct(p.B, p.ldb, n0, k0, Bs[buf], wid);
+    } else {
+      la.template load_edge<VEC>(p.A, p.lda, m0, p.M, k0, kend, As[buf], tid);
+      lb.template load_edge<VEC>(p.B, p.ldb, n0, p.N, k0, kend, Bs[buf], tid);
+    }
+  };
+
+  // Two-level summation: the MFMAs of one GK-deep tile accumulate into
+  // `blk`, which is added to `acc` after the tile, so rounding error grows
+  // with GK + K/GK rather than K.  This matters for the weight gradients
+  // (K = tokens) and the logits-gradient contraction (K = vocabulary).
+  v4f acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; i++)
 #pragma unroll
-    for (int j = 0; j < NI; j++) {
-      acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
-      blk[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < NI; j++) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  TileLoader<BM, NT, AK, VEC> la;
-  TileLoader<BN, NT, BK, VEC> lb;
-  const int nkt = kend > kbeg ? (kend - kbeg + 15) / 16 : 0;
-  if (nkt > 0) {
-    la.load(p.A, p.lda, m0, p.M, kbeg, kend, tid);
-    lb.load(p.B, p.ldb, n0, p.N, kbeg, kend, tid);
-    la.template store<LDA>(As[0], tid);
-    lb.template store<LDB>(Bs[0], tid);
-  }
-  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < S - 1; s++)
+    if (s < nkt) load(s, s);
   for (int kt = 0; kt < nkt; kt++) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nkt;
-    if (more) {
-      la.load(p.A, p.lda, m0, p.M, kbeg + (kt + 1) * 16, kend, tid);
-      lb.load(p.B, p.ldb, n0, p.N, kbeg + (kt + 1) * 16, kend, tid);
+    const int cur = kt % S;
+    // Tiles kt+1 .. kt+S-2 may stay in flight.  (A tile loaded through
+    // VGPRs completes before its LDS stores, which waits for everything
+    // issued before it.)
+    wait_tiles<PT, S - 2>(min(S - 2, nkt - 1 - kt));
+    tile_barrier();
+    // Stage (kt - 1) % S was last read in iteration kt - 1, before the barrier.
+    if (kt + S - 1 < nkt) load(kt + S - 1, (kt + S - 1) % S);
+    v4f blk[MI][NI];
+#pragma unroll
+    for (int g = 0; g < GK / 16; g++) {
+      v4f fa[MI], fb[NI];
+#pragma unroll
+      for (int i = 0; i < MI; i++) fa[i] = LA::frag(As[cur], wm * TM + 16 * i, g, lane);
+#pragma unroll
+      for (int j = 0; j < NI; j++) fb[j] = LB::frag(Bs[cur], wn * TN + 16 * j, g, lane);
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+          for (int j = 0; j < NI; j++)
+            blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                fa[i][c], fb[j][c],
+                (g == 0 && c == 0) ? (v4f){0.f, 0.f, 0.f, 0.f} : blk[i][j], 0, 0, 0);
     }
-    const float* as = As[cur];
-    const float* bs = Bs[cur];
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-      const int k = 4 * kk + (lane >> 4);
-      float a[MI], b[NI];
+    for (int i = 0; i < MI; i++)
 #pragma unroll
-      for (int i = 0; i < MI; i++) a[i] = as[k * LDA + wm * TM + i * 16 + (lane & 15)];
-#pragma unroll
-      for (int j = 0; j < NI; j++) b[j] = bs[k * LDB + wn * TN + j * 16 + (lane & 15)];
-#pragma unroll
-      for (int i = 0; i < MI; i++)
-#pragma unroll
-        for (int j = 0; j < NI; j++)
-          blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], blk[i][j], 0, 0, 0);
-    }
-    if ((kt % FOLD) == FOLD - 1 || !more) {
-#pragma unroll
-      for (int i = 0; i < MI; i++)
-#pragma unroll
-        for (int j = 0; j < NI; j++) {
-          acc[i][j] += blk[i][j];
-          blk[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    if (more) {
-      la.template store<LDA>(As[cur ^ 1], tid);
-      lb.template store<LDB>(Bs[cur ^ 1], tid);
-    }
-    __syncthreads();
+      for (int j = 0; j < NI; j++) acc[i][j] += blk[i][j];
   }
-  // D[i][j] of a 16x16 block: lane holds column (lane & 15), rows 4*(lane>>4)+r.
+  // D of a 16x16 block: lane holds column (lane & 15), rows 4*(lane>>4)+r.
+  if (p.splits == 1) {
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int j = 0; j < NI; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int row = m0 + wm * TM + i * 16 + 4 * (lane >> 4) + r;
+          const int col = n0 + wn * TN + j * 16 + (lane & 15);
+          gemm_epilogue(p, row, col, acc[i][j][r]);
+        }
+    return;
+  }
+  // Split-K: this workgroup's partial sums; gemm_reduce_kernel adds them.
+  float* mine = p.part + (int64_t)split * p.M * p.N;
 #pragma unroll
   for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < NI; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        int row = m0 + wm * TM + i * 16 + 4 * (lane >> 4) + r;
-        int col = n0 + wn * TN + j * 16 + (lane & 15);
-        gemm_epilogue(p, row, col, acc[i][j][r], split);
+        const int row = m0 + wm * TM + i * 16 + 4 * (lane >> 4) + r;
+        const int col = n0 + wn * TN + j * 16 + (lane & 15);
+        if (row < p.M && col < p.N) mine[(int64_t)row * p.N + col] = acc[i][j][r];
       }
 }
 
 // Sums split-K partials in split order in float64 (deterministic) and applies
-// the real epilogue.
-__global__ void gemm_reduce_kernel(GemmParams p, const float* __restrict__ part, int splits) {
-  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t total = (int64_t)p.M * p.N;
+// the epilogue.
+__global__ void gemm_reduce_kernel(GemmParams p) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)p.M * p.N;
   if (idx >= total) return;
   double s = 0.0;
-  for (int z = 0; z < splits; z++) s += (double)part[(int64_t)z * total + idx];
-  int row = (int)(idx / p.N), col = (int)(idx % p.N);
-  gemm_epilogue(p, row, col, (float)s, 0);
+  for (int z = 0; z < p.splits; z++) s += (double)p.part[(int64_t)z * total + idx];
+  gemm_epilogue(p, (int)(idx / p.N), (int)(idx % p.N), (float)s);
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int S>
 static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int splits,
                        hipStream_t st) {
-  dim3 grid(p.tiles_m * (int)ceil_div(p.N, BN), 1, splits);
+  GemmParams q = p;
+  q.tiles_m = (int)ceil_div(p.M, BM);
+  q.tiles_n = (int)ceil_div(p.N, BN);
+  q.splits = splits;
+  dim3 grid(q.tiles_m * q.tiles_n * splits);
   dim3 block(64 * WM * WN);
 #define GN_GEMM_LAUNCH(AK, BK, V) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK, V>), grid, block, 0, st, p)
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, AK, BK, V>), grid, block, 0, st, q)
   if (vec) {
     if (ak && bk) GN_GEMM_LAUNCH(true, true, true);
     else if (ak && !bk) GN_GEMM_LAUNCH(true, false, true);
@@ -274,31 +395,43 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   int splits = 1;
   if (d.force_splits > 0) {
     splits = d.force_splits;
+  } else if (long_k && tiles < 8 * cus) {
+    // Aim for >= 9 workgroups per CU and prefer a total that is a multiple
+    // of the CU count, so the last round of workgroups is not a partial one.
+    const int smax = (int)std::max<int64_t>(1, std::min<int64_t>(64, d.K / 1024));
+    const int smin = (int)std::min<int64_t>(smax, ceil_div(9 * cus, tiles));
+    double best = -1.0;
+    for (int s = smin; s <= smax; s++) {
+      const int64_t wg = tiles * s;
+      const double eff = (double)wg / (double)(ceil_div(wg, cus) * cus);
+      if (eff > best + 1e-9) {
+        best = eff;
+        splits = s;
+      }
+      if (eff >= 0.999) break;
+    }
   } else if (tiles < 2 * cus && d.K >= 512) {
-    splits = (int)std::min<int64_t>(ceil_div(2 * cus, tiles), d.K / (long_k ? 1024 : 256));
+    splits = (int)std::min<int64_t>(ceil_div(2 * cus, tiles), d.K / 256);
     splits = std::max(1, std::min(splits, 64));
   }
-  int kps = (int)ceil_div(ceil_div(d.K, splits), 16) * 16;
+  // k_per_split is a whole number of LDS tiles so that every split but the
+  // last starts and ends on a tile boundary.
+  int kps = (int)ceil_div(ceil_div(d.K, splits), GK) * GK;
   splits = d.K > 0 ? (int)ceil_div(d.K, kps) : 1;
-  p.tiles_m = (int)ceil_div(d.M, bm);
 
+  p.k_per_split = d.K > 0 ? kps : 0;
+  p.splits = splits;
   if (splits > 1) {
     GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
-    float* part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
-    GemmParams q = p;
-    q.C = part;
-    q.epi = EPI_PARTIAL;
-    q.k_per_split = kps;
-    if (use_big) launch_cfg<128, 128, 2, 2>(q, d.a_kcontig, d.b_kcontig, vec, splits, st);
-    else launch_cfg<64, 64, 2, 2>(q, d.a_kcontig, d.b_kcontig, vec, splits, st);
-    int64_t total = (int64_t)d.M * d.N;
+    p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
+  }
+  if (use_big) launch_cfg<128, 128, 2, 2, 2>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  else launch_cfg<64, 64, 2, 2, 4>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  if (splits > 1) {
+    const int64_t total = (int64_t)d.M * d.N;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
-                       p, part, splits);
+                       p);
     GN_HIP(hipGetLastError());
-  } else {
-    p.k_per_split = d.K > 0 ? kps : 0;
-    if (use_big) launch_cfg<128, 128, 2, 2>(p, d.a_kcontig, d.b_kcontig, vec, 1, st);
-    else launch_cfg<64, 64, 2, 2>(p, d.a_kcontig, d.b_kcontig, vec, 1, st);
   }
 }
 

@@ -65,8 +65,7 @@ enum GemmEpilogue {
   EPI_ACCUM = 2,      // C += acc                 (gradient accumulation)
   EPI_SOFTCAP = 3,    // C = 15 tanh(acc / 15)    (logits)
   EPI_RELU2_SAVE = 4, // aux_out = acc, C = relu(acc)^2
-  EPI_DRELU2 = 5,     // C = acc * 2 * relu(aux)  (ReluSquared backward)
-  EPI_PARTIAL = 6     // internal: split-K partial
+  EPI_DRELU2 = 5      // C = acc * 2 * relu(aux)  (ReluSquared backward)
 };
 
 struct GemmDesc {
