@@ -39,23 +39,37 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg, w, prompts, seconds_hint: float) -> dict:
+def cpu_baseline(cfg, w, prompts, S: int, N: int, temp: float) -> dict:
     """The oracle (a scalar C port of the reference's arithmetic, float64
-    accumulation, OpenMP over rows) generating rollouts on the same d12
-    weights for a bounded sample."""
+    accumulation, OpenMP over rows) generating rollouts on the same weights.
+
+    Bounded sample: ONE prompt group of the workload (its full prompt, all
+    S samples), timed once with 1 new token (prefill) and once with
+    1 + STEPS new tokens; the difference gives the cost of one batched decode
+    step.  The reported rate is the workload's per-group token count over
+    the time one group would take, prefill + N decode steps, so it is in the
+    same unit and the same prefill/decode mix as the GPU's value."""
     from oracle import oracle as O
+    STEPS = 128  # about 15 s of CPU work on the GPU box's 16 host threads
     shape = O.ModelShape(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head,
                          cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern)
     m = O.OracleModel(shape, w)
-    S, N, P = 8, 8, 16
+    P = prompts.shape[1]
     t0 = time.perf_counter()
-    rows = m.generate_batch(prompts[0, :P], S, N, 1.0, 50, 0)
-    dt = time.perf_counter() - t0
-    toks = sum(len(r) - P for r in rows)
-    return {"value": toks / dt, "unit": "tokens/s", "cores": int(O.lib().orc_num_threads()),
-            "kind": "port",
-            "sample": f"oracle rollout of 1 prompt of {P} tokens x {S} samples x {N} new tokens "
-                      f"on the d12 weights ({toks} tokens in {dt:.1f} s)"}
+    m.generate_batch(prompts[0], S, 1, temp, 50, 0)
+    t_prefill = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    rows = m.generate_batch(prompts[0], S, 1 + STEPS, temp, 50, 0)
+    t_long = time.perf_counter() - t0
+    steps = max(1, max(len(r) for r in rows) - P - 1)
+    t_step = max(t_long - t_prefill, 1e-9) / steps
+    group_s = t_prefill + N * t_step
+    return {"value": round(S * N / group_s, 2), "unit": "tokens/s",
+            "cores": int(O.lib().orc_num_threads()), "kind": "port",
+            "sample": f"oracle rollout of 1 prompt group ({P} prompt tokens x {S} samples) on "
+                      f"the same weights: prefill {t_prefill:.2f} s, {steps} batched decode "
+                      f"steps {t_long - t_prefill:.2f} s; value = {S}x{N} tokens / "
+                      f"(prefill + {N} steps) = one group of the workload"}
 
 
 def main() -> int:
@@ -65,12 +79,22 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="d12", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phase", default="rl", choices=["rl", "train"],
+                    help="rl: the full RL step (the benchmark); train: only the recompute + "
+                         "PG fwd/bwd on a synthetic batch of the workload's shape (for "
+                         "counter profiles of the train-phase kernels)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a device copy of 1 GiB (5 times), the known-size "
+                         "reference for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the RL step on a single MI355X "
               "(see DESIGN.md for how the step shards across GPUs); use --gpus 1.",
               file=sys.stderr)
         return 2
+
+    if args.copy_calibration:
+        return copy_calibration()
 
     from gonano_amd import config as G
     from gonano_amd.session import Session
@@ -85,6 +109,9 @@ def main() -> int:
     sess = Session(cfg)
     sess.set_params(w)
     sess.set_timing(True)
+
+    if args.phase == "train":
+        return train_phase(args, sess, prompts, S, N, reward_rng, reward_p)
 
     def step(i: int):
         seeds = np.array([i * 1000 + g for g in range(groups)], np.uint64)
@@ -102,6 +129,8 @@ def main() -> int:
     walls, roll_ms, train_ms, toks = [], [], [], 0
     gemm_ms = gemm_fl = attn_ms = attn_b = 0.0
     gemm_n = attn_n = 0
+    sess.synchronize()
+    t_start = time.perf_counter()
     for i in range(args.steps):
         out, wall, t = step(args.warmup + i)
         walls.append(wall)
@@ -113,11 +142,12 @@ def main() -> int:
         attn_n += t["decode_attn_launches"]
         log(f"bench: step {i}: {wall * 1e3:.1f} ms (rollout {t['rollout_ms']:.1f} ms, "
             f"train {t['train_ms']:.1f} ms), loss {out['loss']:.6f}, max_len {out['max_len']}")
+    sess.synchronize()
+    ms_step = 1e3 * (time.perf_counter() - t_start) / args.steps
     sess.close()
 
     rollout_s = sum(roll_ms) / 1e3
     value = toks / rollout_s
-    ms_step = 1e3 * sum(walls) / len(walls)
     gemm_tflops = gemm_fl / (gemm_ms / 1e3) / 1e12 if gemm_ms else 0.0
     attn_gbs = attn_b / (attn_ms / 1e3) / 1e9 if attn_ms else 0.0
     res = {
@@ -153,7 +183,7 @@ def main() -> int:
             "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": gemm_traffic(args.config),
             "launches": gemm_n,
             "avg_launch_ms": round(gemm_ms / max(gemm_n, 1), 4),
         },
@@ -165,8 +195,75 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         log("bench: timing the CPU oracle on a bounded sample")
-        res["cpu_baseline"] = cpu_baseline(cfg, w, prompts, 20.0)
+        res["cpu_baseline"] = cpu_baseline(cfg, w, prompts, S, N, temp)
     print(json.dumps(res), flush=True)
+    return 0
+
+
+def gemm_traffic(config: str):
+    """HBM bytes per train-phase GEMM launch, from the committed rocprofv3
+    --pmc summary of `bench.py --phase train` (FETCH_SIZE + WRITE_SIZE,
+    each scaled by the copy-kernel calibration), or None if absent."""
+    path = os.path.join(ROOT, "profiles", f"gemm_kernel_{config}_train_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def train_phase(args, sess, prompts, S, N, reward_rng, reward_p) -> int:
+    """Recompute + PG forward/backward alone, on a synthetic batch shaped as
+    the RL step's: each prompt repeated S times followed by N uniform tokens,
+    inputs/targets shifted by one, targets before the prompt end masked
+    (gn_rl_step's layout), group-mean advantages of Bernoulli rewards."""
+    G_, P = prompts.shape
+    V = sess.cfg.vocab_size
+    rng = np.random.default_rng(3)
+    rows = np.concatenate([np.repeat(prompts, S, 0),
+                           rng.integers(0, V, (G_ * S, N)).astype(np.int32)], 1)
+    inputs, targets = rows[:, :-1].copy(), rows[:, 1:].copy()
+    targets[:, :P] = -1
+    rewards = (reward_rng.random(G_ * S) < reward_p).astype(np.float32)
+    adv = rewards - rewards.reshape(G_, S).mean(1).repeat(S)
+    norm = float(P + N)
+    for _ in range(args.warmup):
+        sess.zero_grad()
+        sess.policy_gradient_step(inputs, targets, adv, norm)
+    sess.synchronize()
+    t0 = time.perf_counter()
+    gemm_ms = gemm_fl = 0.0
+    gemm_n = 0
+    train = []
+    for _ in range(args.steps):
+        sess.zero_grad()
+        loss, _ = sess.policy_gradient_step(inputs, targets, adv, norm)
+        t = sess.timing()
+        train.append(t["train_ms"])
+        gemm_ms += t["gemm_ms"]; gemm_fl += t["gemm_flops"]; gemm_n += t["gemm_launches"]
+    sess.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / args.steps
+    sess.close()
+    tf = gemm_fl / (gemm_ms / 1e3) / 1e12 if gemm_ms else 0.0
+    print(json.dumps({
+        "metric": "train phase (recompute + PG fwd/bwd) ms", "value": round(ms, 2),
+        "unit": "ms", "higher_is_better": False, "steps": args.steps, "warmup": args.warmup,
+        "train_ms": round(sum(train) / len(train), 2), "loss": loss,
+        "gemm": {"achieved": round(tf, 2), "unit": "TFLOP/s", "launches": gemm_n,
+                 "avg_launch_ms": round(gemm_ms / max(gemm_n, 1), 4)}}), flush=True)
+    return 0
+
+
+def copy_calibration() -> int:
+    """A plain device copy of known size for scaling HBM byte counters:
+    torch's copy kernel run 5 times over 1 GiB (reads 1 GiB, writes 1 GiB)."""
+    import torch
+    n = 1 << 28  # floats = 1 GiB
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": 4 * n, "copies": 5}), flush=True)
     return 0
 
 

@@ -113,6 +113,7 @@ _SIGS = {
     "gn_sample_next_token": (C.c_int, [f32p, i64, i64, u64p, C.c_float, i64, i32p]),
     "gn_session_set_timing": (C.c_int, [vp, C.c_int]),
     "gn_session_get_timing": (C.c_int, [vp, C.POINTER(GnTiming)]),
+    "gn_session_synchronize": (C.c_int, [vp]),
 }
 
 _lib = None

@@ -1027,5 +1027,12 @@ int gn_session_get_timing(const gn_session* s, gn_timing* out) {
     *out = s->t;
   });
 }
+int gn_session_synchronize(gn_session* s) {
+  return guard([&] {
+    GN_CHECK(s, "null session");
+    GN_HIP(hipSetDevice(s->device));
+    GN_HIP(hipStreamSynchronize(s->stream));
+  });
+}
 
 }  // extern "C"

@@ -119,6 +119,10 @@ class Session:
     def set_timing(self, enabled: bool):
         call("gn_session_set_timing", self._h, 1 if enabled else 0)
 
+    def synchronize(self):
+        """Waits until the session stream is idle."""
+        call("gn_session_synchronize", self._h)
+
     def timing(self) -> dict:
         t = GnTiming()
         call("gn_session_get_timing", self._h, C.byref(t))

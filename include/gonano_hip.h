@@ -225,6 +225,9 @@ typedef struct gn_timing {
 } gn_timing;
 int gn_session_set_timing(gn_session *session, int enabled);
 int gn_session_get_timing(const gn_session *session, gn_timing *out);
+/* Waits until the session stream is idle (no reference counterpart: the Go
+ * backends are synchronous; used to bracket timed regions). */
+int gn_session_synchronize(gn_session *session);
 
 #ifdef __cplusplus
 }
