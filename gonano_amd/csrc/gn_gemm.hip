@@ -214,24 +214,30 @@ __device__ __forceinline__ void tile_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// C tile of BM x BN per workgroup of WM x WN waves, K in GK-deep tiles
+// C tile of BM x BN per workgroup of WM x WN x WK waves, K in GK-deep tiles
 // through an S-stage LDS ring: tile kt + S - 1 is in flight while tile kt
-// is multiplied.  With p.splits > 1 each workgroup sums one K range into
-// p.part and gemm_reduce_kernel applies the epilogue.
-template <int BM, int BN, int WM, int WN, int S, bool AK, bool BK, bool VEC>
-__global__ __launch_bounds__(64 * WM * WN, 2) void gemm_kernel(GemmParams p) {
-  constexpr int NT = 64 * WM * WN;
+// is multiplied.  The WK wave groups take alternate 16-deep k groups of
+// every tile (more waves per SIMD for small grids) and are added in LDS at
+// the end.  With p.splits > 1 each workgroup sums one K range into p.part
+// and gemm_reduce_kernel applies the epilogue.
+template <int BM, int BN, int WM, int WN, int WK, int S, bool AK, bool BK, bool VEC>
+__global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p) {
+  constexpr int NT = 64 * WM * WN * WK;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int MI = TM / 16, NI = TN / 16;
+  static_assert((GK / 16) % WK == 0, "k groups per wave group");
   using LA = TileIO<BM, NT, AK>;
   using LB = TileIO<BN, NT, BK>;
   constexpr int PT = LA::NV + LB::NV;  // LDS-DMA instructions per tile and thread
   static_assert(S >= 2 && PT * (S - 2) < 64, "pipeline depth");
+  static_assert((WK - 1) * WM * WN * MI * NI * 256 <= S * LA::SIZE,
+                "wave-group partials fit in the A stage buffers");
   __shared__ __attribute__((aligned(16))) float As[S][LA::SIZE];
   __shared__ __attribute__((aligned(16))) float Bs[S][LB::SIZE];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid % WM, wn = wid / WM;
+  const int wmn = wid % (WM * WN), wk = wid / (WM * WN);
+  const int wm = wmn % WM, wn = wmn / WM;
   int tm, tn, split;
   tile_coords(p, tm, tn, split);
   const int m0 = tm * BM, n0 = tn * BN;
@@ -282,7 +288,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm_kernel(GemmParams p) {
     if (kt + S - 1 < nkt) load(kt + S - 1, (kt + S - 1) % S);
     v4f blk[MI][NI];
 #pragma unroll
-    for (int g = 0; g < GK / 16; g++) {
+    for (int gi = 0; gi < GK / 16 / WK; gi++) {
+      const int g = gi * WK + wk;
       v4f fa[MI], fb[NI];
 #pragma unroll
       for (int i = 0; i < MI; i++) fa[i] = LA::frag(As[cur], wm * TM + 16 * i, g, lane);
@@ -296,12 +303,41 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm_kernel(GemmParams p) {
           for (int j = 0; j < NI; j++)
             blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                 fa[i][c], fb[j][c],
-                (g == 0 && c == 0) ? (v4f){0.f, 0.f, 0.f, 0.f} : blk[i][j], 0, 0, 0);
+                (gi == 0 && c == 0) ? (v4f){0.f, 0.f, 0.f, 0.f} : blk[i][j], 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
       for (int j = 0; j < NI; j++) acc[i][j] += blk[i][j];
+  }
+  if constexpr (WK > 1) {
+    // Wave groups 1..WK-1 park their sums in the (now idle) stage buffers;
+    // group 0 adds them in group order.  The last iteration waited for all
+    // loads (vmcnt(0)), so no LDS-DMA write is still in flight.
+    float* red = &As[0][0];
+    tile_barrier();
+    if (wk > 0) {
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NI; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            red[((((wk - 1) * WM * WN + wmn) * MI + i) * NI + j) * 256 + r * 64 + lane] =
+                acc[i][j][r];
+    }
+    wait_vm_lgkm0<0>();
+    tile_barrier();
+    if (wk > 0) return;
+#pragma unroll
+    for (int v = 1; v < WK; v++)
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NI; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            acc[i][j][r] += red[((((v - 1) * WM * WN + wmn) * MI + i) * NI + j) * 256 + r * 64 + lane];
   }
   // D of a 16x16 block: lane holds column (lane & 15), rows 4*(lane>>4)+r.
   if (p.splits == 1) {
@@ -342,7 +378,7 @@ __global__ void gemm_reduce_kernel(GemmParams p) {
   gemm_epilogue(p, (int)(idx / p.N), (int)(idx % p.N), (float)s);
 }
 
-template <int BM, int BN, int WM, int WN, int S>
+template <int BM, int BN, int WM, int WN, int WK, int S>
 static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int splits,
                        hipStream_t st) {
   GemmParams q = p;
@@ -350,9 +386,9 @@ static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int spli
   q.tiles_n = (int)ceil_div(p.N, BN);
   q.splits = splits;
   dim3 grid(q.tiles_m * q.tiles_n * splits);
-  dim3 block(64 * WM * WN);
+  dim3 block(64 * WM * WN * WK);
 #define GN_GEMM_LAUNCH(AK, BK, V) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, S, AK, BK, V>), grid, block, 0, st, q)
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, AK, BK, V>), grid, block, 0, st, q)
   if (vec) {
     if (ak && bk) GN_GEMM_LAUNCH(true, true, true);
     else if (ak && !bk) GN_GEMM_LAUNCH(true, false, true);
@@ -380,6 +416,7 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   p.epi = d.epi;
   p.alpha = d.alpha;
   const bool vec = aligned16(d.A) && aligned16(d.B) && d.lda % 4 == 0 && d.ldb % 4 == 0;
+
 
   // Tile choice: the 128x128 tile when it yields enough workgroups to cover
   // the 256 CUs, otherwise 64x64; split K when even that underfills the chip
@@ -410,8 +447,11 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
       }
       if (eff >= 0.999) break;
     }
-  } else if (tiles < 2 * cus && d.K >= 512) {
-    splits = (int)std::min<int64_t>(ceil_div(2 * cus, tiles), d.K / 256);
+  } else if (tiles < cus && d.K >= 512) {
+    // Small grids (the M = 256 decode projections): about 200 workgroups
+    // (25/32 of a workgroup per CU) measured fastest; more splits cost more
+    // in the reduction than they gain in parallelism.
+    splits = (int)std::min<int64_t>((25 * cus / 32 + tiles / 2) / tiles, d.K / 256);
     splits = std::max(1, std::min(splits, 64));
   }
   // k_per_split is a whole number of LDS tiles so that every split but the
@@ -425,8 +465,8 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
     p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
   }
-  if (use_big) launch_cfg<128, 128, 2, 2, 2>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
-  else launch_cfg<64, 64, 2, 2, 4>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  if (use_big) launch_cfg<128, 128, 2, 2, 1, 2>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  else launch_cfg<64, 64, 2, 2, 2, 4>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   if (splits > 1) {
     const int64_t total = (int64_t)d.M * d.N;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
