@@ -141,6 +141,10 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
     }
   }
   __syncthreads();
+  // One split covers every key of the row: write the normalized output
+  // directly (the combine pass is skipped).  Otherwise emit the split's
+  // (unnormalized output, max, sum) for decode_combine_kernel.
+  const bool whole = a.nsplit == 1;
   float* out = a.part + ((int64_t)bh * a.nsplit + s) * R * (HD + 2);
   for (int i = tid; i < R * HD; i += 256) {
     const int h = i / HD, d = i % HD;
@@ -152,25 +156,23 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
       o += red[w][h][d] * sc;
       L += wl[w][h] * sc;
     }
-    out[h * (HD + 2) + d] = o;
-    if (d == 0) {
-      out[h * (HD + 2) + HD] = M;
-      out[h * (HD + 2) + HD + 1] = L;
+    if (whole) {
+      a.o[((int64_t)row * a.Hq + hk * R + h) * HD + d] = o / L;
+    } else {
+      out[h * (HD + 2) + d] = o;
+      if (d == 0) {
+        out[h * (HD + 2) + HD] = M;
+        out[h * (HD + 2) + HD + 1] = L;
+      }
     }
   }
 }
 
+// One kernel per GQA ratio R, so each instance is sized (registers, LDS) for
+// its own R rather than for the largest.
+template <int R>
 __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
-  switch (a.Hq / a.Hkv) {
-    case 1: decode_attn_body<1>(a); break;
-    case 2: decode_attn_body<2>(a); break;
-    case 3: decode_attn_body<3>(a); break;
-    case 4: decode_attn_body<4>(a); break;
-    case 5: decode_attn_body<5>(a); break;
-    case 6: decode_attn_body<6>(a); break;
-    case 8: decode_attn_body<8>(a); break;
-    default: break;
-  }
+  decode_attn_body<R>(a);
 }
 
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
@@ -195,8 +197,19 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= DEC_MAXR, "decode attention: GQA ratio must be <= 8");
   GN_CHECK(a.kend > a.kstart, "decode attention: empty key range");
   a.nsplit = (int)ceil_div(a.kend - a.kstart, DEC_KPS);
-  hipLaunchKernelGGL(decode_attn_kernel, dim3(a.rows * a.Hkv, a.nsplit), dim3(256), 0, st, a);
+  const dim3 grid(a.rows * a.Hkv, a.nsplit);
+  switch (a.Hq / a.Hkv) {
+    case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(decode_attn_kernel<3>, grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, grid, dim3(256), 0, st, a); break;
+    case 5: hipLaunchKernelGGL(decode_attn_kernel<5>, grid, dim3(256), 0, st, a); break;
+    case 6: hipLaunchKernelGGL(decode_attn_kernel<6>, grid, dim3(256), 0, st, a); break;
+    case 7: hipLaunchKernelGGL(decode_attn_kernel<7>, grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, grid, dim3(256), 0, st, a); break;
+  }
   GN_HIP(hipGetLastError());
+  if (a.nsplit == 1) return;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(a.rows * a.Hq), dim3(HD), 0, st, a);
   GN_HIP(hipGetLastError());
 }
