@@ -1,11 +1,11 @@
 // gn_attention.hip - causal (sliding-window) attention for the RL step.
 //
 //  * decode: one new query per row against the KV cache.  Memory-bound: the
-//    grid is (row, kv-head) x key-chunks of 64 so K/V of a chunk are read once
-//    for all query heads of the GQA group, one key per lane; a combine kernel
-//    merges the chunks (model/attention.go:332-387 split-K, with the window
-//    applied by skipping keys the reference masks to -1e30, whose softmax
-//    weight is exactly zero).
+//    grid is (row, kv-head) x splits of up to 256 keys, so K/V are read once
+//    for all query heads of the GQA group; a combine kernel merges splits
+//    when a window needs more than one (model/attention.go:332-387 split-K,
+//    with the window applied by skipping keys the reference masks to -1e30,
+//    whose softmax weight is exactly zero).
 //  * training/prefill: flash-attention forward with the log-sum-exp, and the
 //    backward as two kernels (dQ per query block; dK/dV per key block over
 //    the whole GQA group), deterministic and atomic-free
@@ -22,147 +22,190 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
-// Decode: one 256-thread block per (row, kv-head, split of up to 256 keys);
-// each wave streams a contiguous quarter of the split.  Lanes form 8 groups
-// of 8: group g takes key 8*step + g, lane part p of the group its dims
-// [16p, 16p+16), so one step of a wave reads 8 whole K rows and 8 whole V
-// rows (64 contiguous bytes per lane), and the next step's rows are loaded
-// before the current step is computed.  Scores reduce over the 8 lanes of a
-// group; an online softmax per head (running max / sum over the wave's keys)
-// rescales the per-lane P.V accumulators; at the end the 8 groups and then
-// the 4 waves are merged.  All r query heads of the GQA group share every
-// K/V load.  The split's unnormalized output, max and sum go to `part`.
+// Decode: one 256-thread block per (row, kv-head, split of up to 256 keys),
+// in three phases; all r query heads of the GQA group share every K/V load.
+//  1. Scores.  Lanes form 8 groups of 8; in each step group g of a wave
+//     takes one key and lane part p of the group dims [16p, 16p+16) of it,
+//     so a step reads 8 whole K rows (64 contiguous bytes per lane).  An
+//     8-lane reduction gives the r scores, kept in LDS.  Each wave streams a
+//     contiguous quarter of the split, two steps of K rows in flight.
+//  2. Softmax over the split: block max and sum per head, p = exp(s - max)
+//     written back over the scores.
+//  3. P.V: thread t reads float4 (t mod 32) of V rows j = t/32 + 8i, i.e. two
+//     whole rows per wave instruction, and accumulates p[h][j] * V[j] for
+//     every head; the 8 row groups are added in LDS.  The first V rows are
+//     loaded before phase 1 so their latency hides behind the scores.
+// One split covering the whole window writes the normalized output; several
+// splits write (unnormalized output, max, sum) for decode_combine_kernel.
 // ---------------------------------------------------------------------------
-static constexpr int DEC_KPS = 256;  // keys per split
+// Keys per split: at most DEC_KPS, balanced (300 keys -> 2 x 150).  Smaller
+// splits were measured slower: the combine pass they need costs more than
+// the extra workgroups gain.
+static constexpr int DEC_KPS = 256;
 static constexpr int DEC_MAXR = 8;   // max GQA ratio
+static constexpr int DEC_VPRE = 8;   // V rows per thread loaded ahead of phase 1
 
-__device__ __forceinline__ float xor_groups_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 8, 64));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+__device__ __forceinline__ float red8_sum(float v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  return v + __shfl_xor(v, 4, 64);
 }
-__device__ __forceinline__ float xor_groups_sum(float v) {
-  v += __shfl_xor(v, 8, 64);
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
 }
 
 template <int R>
 __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
-  __shared__ __attribute__((aligned(16))) float qs[R][HD];
-  __shared__ __attribute__((aligned(16))) float red[4][R][HD];
-  __shared__ float wm[4][R], wl[4][R];
+  __shared__ float sc[R][DEC_KPS];
+  __shared__ __attribute__((aligned(16))) float pv[8][R][HD];
+  __shared__ float wred[4][R];
+  __shared__ float stat[2][R];  // max, sum per head
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int g = lane >> 3, part = lane & 7;
   const int bh = blockIdx.x, s = blockIdx.y;
   const int row = bh / a.Hkv, hk = bh % a.Hkv;
-  const int ks = a.kstart + s * DEC_KPS;
-  const int nk = min(a.kend, ks + DEC_KPS) - ks;
-  const float* qrow = a.q + ((int64_t)row * a.Hq + hk * R) * HD;
-  for (int i = tid; i < R * HD; i += 256) qs[i / HD][i % HD] = qrow[i];
+  const int ks = a.kstart + s * a.kps;
+  const int nk = min(a.kend, ks + a.kps) - ks;
+  const int64_t cbase = ((int64_t)row * a.Hkv + hk) * a.maxSeq + ks;
+
+  // V rows of phase 3, issued first
+  const int d4 = tid & 31, jr = tid >> 5;
+  const v4f* vrow = reinterpret_cast<const v4f*>(a.vc + cbase * HD) + d4;
+  v4f vpre[DEC_VPRE];
+#pragma unroll
+  for (int i = 0; i < DEC_VPRE; i++) {
+    const int j = jr + 8 * i;
+    vpre[i] = vrow[(int64_t)(j < nk ? j : 0) * (HD / 4)];
+  }
+
+  // ---- phase 1: scores
+  {
+    const int g = lane >> 3, part = lane & 7;
+    const float* qrow = a.q + ((int64_t)row * a.Hq + hk * R) * HD + 16 * part;
+    float qv[R][16];
+#pragma unroll
+    for (int h = 0; h < R; h++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const v4f t = *reinterpret_cast<const v4f*>(qrow + h * HD + 4 * i);
+        qv[h][4 * i] = t[0];
+        qv[h][4 * i + 1] = t[1];
+        qv[h][4 * i + 2] = t[2];
+        qv[h][4 * i + 3] = t[3];
+      }
+    const int q4 = (nk + 3) / 4;
+    const int j0 = wid * q4, j1 = min(nk, j0 + q4);
+    const v4f* kb = reinterpret_cast<const v4f*>(a.kc + cbase * HD + 16 * part);
+    auto load = [&](int j, v4f* kd) {
+      const int jj = j < j1 ? j : j0;  // clamp (value unused when j >= j1)
+#pragma unroll
+      for (int i = 0; i < 4; i++) kd[i] = kb[(int64_t)jj * (HD / 4) + i];
+    };
+    v4f k0[4], k1[4];
+    if (j0 < j1) load(j0 + g, k0);
+    if (j0 + 8 < j1) load(j0 + 8 + g, k1);
+    for (int jb = j0; jb < j1; jb += 8) {
+      float d[R];
+#pragma unroll
+      for (int h = 0; h < R; h++) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          t += k0[i][0] * qv[h][4 * i] + k0[i][1] * qv[h][4 * i + 1] +
+               k0[i][2] * qv[h][4 * i + 2] + k0[i][3] * qv[h][4 * i + 3];
+        d[h] = red8_sum(t);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) k0[i] = k1[i];
+      if (jb + 16 < j1) load(jb + 16 + g, k1);
+      const int j = jb + g;
+      if (part == 0 && j < j1)
+#pragma unroll
+        for (int h = 0; h < R; h++) sc[h][j] = d[h];
+    }
+  }
   __syncthreads();
-  float qv[R][16];
+
+  // ---- phase 2: softmax over the split (thread t owns key t)
+  {
+    float v[R], mx[R];
+#pragma unroll
+    for (int h = 0; h < R; h++) {
+      v[h] = tid < nk ? sc[h][tid] : -INFINITY;
+      const float m = wave_max(v[h]);
+      if (lane == 0) wred[wid][h] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < R; h++) {
+      mx[h] = fmaxf(fmaxf(wred[0][h], wred[1][h]), fmaxf(wred[2][h], wred[3][h]));
+      const float p = tid < nk ? expf(v[h] - mx[h]) : 0.f;
+      if (tid < nk) sc[h][tid] = p;
+      v[h] = wave_sum(p);
+    }
+    __syncthreads();  // everyone has read wred (max) and written p
+    if (lane == 0)
+#pragma unroll
+      for (int h = 0; h < R; h++) wred[wid][h] = v[h];
+    __syncthreads();
+    if (tid < R) {
+      stat[0][tid] = mx[tid];
+      stat[1][tid] = wred[0][tid] + wred[1][tid] + wred[2][tid] + wred[3][tid];
+    }
+  }
+
+  // ---- phase 3: P.V
+  float acc[R][4];
 #pragma unroll
   for (int h = 0; h < R; h++)
 #pragma unroll
-    for (int i = 0; i < 16; i++) qv[h][i] = qs[h][16 * part + i];
-
-  const int q4 = (nk + 3) / 4;
-  const int j0 = wid * q4, j1 = min(nk, j0 + q4);
-  const int64_t cbase = ((int64_t)row * a.Hkv + hk) * a.maxSeq + ks;
-  const float* kb = a.kc + cbase * HD + 16 * part;
-  const float* vb = a.vc + cbase * HD + 16 * part;
-  float m[R], l[R], acc[R][16];
-#pragma unroll
-  for (int h = 0; h < R; h++) {
-    m[h] = -INFINITY;
-    l[h] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) acc[h][i] = 0.f;
-  }
-  v4f kc[4], vc[4];
-  auto load = [&](int j, v4f* kd, v4f* vd) {
-    const int jj = j < j1 ? j : j0;  // clamp (value unused when j >= j1)
-    const v4f* kp = reinterpret_cast<const v4f*>(kb + (int64_t)jj * HD);
-    const v4f* vp = reinterpret_cast<const v4f*>(vb + (int64_t)jj * HD);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      kd[i] = kp[i];
-      vd[i] = vp[i];
-    }
-  };
-  if (j0 < j1) load(j0 + g, kc, vc);
-  for (int jb = j0; jb < j1; jb += 8) {
-    const int j = jb + g;
-    const bool valid = j < j1;
-    v4f kn[4], vn[4];
-    if (jb + 8 < j1) load(jb + 8 + g, kn, vn);
+    for (int c = 0; c < 4; c++) acc[h][c] = 0.f;
+  auto accumulate = [&](int j, const v4f& vv) {
 #pragma unroll
     for (int h = 0; h < R; h++) {
-      float d = 0.f;
+      const float p = sc[h][j];
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        d += kc[i][0] * qv[h][4 * i] + kc[i][1] * qv[h][4 * i + 1] + kc[i][2] * qv[h][4 * i + 2] +
-             kc[i][3] * qv[h][4 * i + 3];
-      d += __shfl_xor(d, 1, 64);
-      d += __shfl_xor(d, 2, 64);
-      d += __shfl_xor(d, 4, 64);
-      const float sc = valid ? d : -INFINITY;
-      const float mn = fmaxf(m[h], xor_groups_max(sc));
-      const float scale = expf(m[h] - mn);  // 0 while m is -inf
-      const float p = valid ? expf(sc - mn) : 0.f;
-      l[h] = l[h] * scale + xor_groups_sum(p);  // one p per key group
+      for (int c = 0; c < 4; c++) acc[h][c] += p * vv[c];
+    }
+  };
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        acc[h][4 * i] = acc[h][4 * i] * scale + p * vc[i][0];
-        acc[h][4 * i + 1] = acc[h][4 * i + 1] * scale + p * vc[i][1];
-        acc[h][4 * i + 2] = acc[h][4 * i + 2] * scale + p * vc[i][2];
-        acc[h][4 * i + 3] = acc[h][4 * i + 3] * scale + p * vc[i][3];
-      }
-      m[h] = mn;
+  for (int i = 0; i < DEC_VPRE; i++)
+    if (jr + 8 * i < nk) accumulate(jr + 8 * i, vpre[i]);
+  for (int jb = jr + 8 * DEC_VPRE; jb < nk; jb += 32) {
+    v4f vv[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int j = jb + 8 * u;
+      vv[u] = vrow[(int64_t)(j < nk ? j : 0) * (HD / 4)];
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      kc[i] = kn[i];
-      vc[i] = vn[i];
-    }
+    for (int u = 0; u < 4; u++)
+      if (jb + 8 * u < nk) accumulate(jb + 8 * u, vv[u]);
   }
-  // merge the 8 key groups of the wave, then the 4 waves
 #pragma unroll
-  for (int h = 0; h < R; h++) {
-#pragma unroll
-    for (int i = 0; i < 16; i++) acc[h][i] = xor_groups_sum(acc[h][i]);
-    if (g == 0)
-#pragma unroll
-      for (int i = 0; i < 16; i++) red[wid][h][16 * part + i] = acc[h][i];
-    if (lane == 0) {
-      wm[wid][h] = m[h];
-      wl[wid][h] = l[h];
-    }
-  }
+  for (int h = 0; h < R; h++)
+    *reinterpret_cast<v4f*>(&pv[jr][h][4 * d4]) = (v4f){acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
   __syncthreads();
-  // One split covers every key of the row: write the normalized output
-  // directly (the combine pass is skipped).  Otherwise emit the split's
-  // (unnormalized output, max, sum) for decode_combine_kernel.
   const bool whole = a.nsplit == 1;
   float* out = a.part + ((int64_t)bh * a.nsplit + s) * R * (HD + 2);
   for (int i = tid; i < R * HD; i += 256) {
-    const int h = i / HD, d = i % HD;
-    float M = fmaxf(fmaxf(wm[0][h], wm[1][h]), fmaxf(wm[2][h], wm[3][h]));
-    float o = 0.f, L = 0.f;
+    const int h = i / HD, dd = i % HD;
+    float o = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-      float sc = wm[w][h] > -INFINITY ? expf(wm[w][h] - M) : 0.f;
-      o += red[w][h][d] * sc;
-      L += wl[w][h] * sc;
-    }
+    for (int r = 0; r < 8; r++) o += pv[r][h][dd];
     if (whole) {
-      a.o[((int64_t)row * a.Hq + hk * R + h) * HD + d] = o / L;
+      a.o[((int64_t)row * a.Hq + hk * R + h) * HD + dd] = o / stat[1][h];
     } else {
-      out[h * (HD + 2) + d] = o;
-      if (d == 0) {
-        out[h * (HD + 2) + HD] = M;
-        out[h * (HD + 2) + HD + 1] = L;
+      out[h * (HD + 2) + dd] = o;
+      if (dd == 0) {
+        out[h * (HD + 2) + HD] = stat[0][h];
+        out[h * (HD + 2) + HD + 1] = stat[1][h];
       }
     }
   }
@@ -196,7 +239,9 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= DEC_MAXR, "decode attention: GQA ratio must be <= 8");
   GN_CHECK(a.kend > a.kstart, "decode attention: empty key range");
-  a.nsplit = (int)ceil_div(a.kend - a.kstart, DEC_KPS);
+  const int nkeys = a.kend - a.kstart;
+  a.kps = (int)ceil_div(nkeys, ceil_div(nkeys, DEC_KPS));
+  a.nsplit = (int)ceil_div(nkeys, a.kps);  // every split non-empty
   const dim3 grid(a.rows * a.Hkv, a.nsplit);
   switch (a.Hq / a.Hkv) {
     case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), 0, st, a); break;

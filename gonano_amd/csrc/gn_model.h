@@ -53,7 +53,7 @@ struct DecodeAttnArgs {
   float* o;         // [rows, Hq, 128]
   int rows, Hq, Hkv, maxSeq;
   int kstart, kend; // keys [kstart, kend)
-  int nsplit;       // set by the launcher
+  int nsplit, kps;  // set by the launcher: splits and keys per split
 };
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st);
 
