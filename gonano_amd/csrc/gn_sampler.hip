@@ -9,7 +9,9 @@
 // are evaluated only for entries that survive the top-k mask.
 //
 // Top-k threshold (the k-th largest value of the row, ties kept):
-//  1. one pass over the row computes the maxima of ngroups contiguous groups;
+//  1. one coalesced pass over the row computes the maxima of ngroups strided
+//     groups (float4 c, or entry c when the row is not float4-aligned, in
+//     group c mod ngroups);
 //  2. the k-th largest group maximum L is a lower bound of the k-th largest
 //     value (each of the k groups holds a value >= L);
 //  3. the values >= L (a few hundred at most for real logits) are compacted
@@ -19,6 +21,8 @@
 #include "gn_model.h"
 
 namespace gn {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct u128 {
   uint64_t hi, lo;
@@ -113,7 +117,7 @@ __device__ void bitonic_desc(float* a, int n) {
   }
 }
 
-static constexpr int NT = 256;
+static constexpr int NT = 1024;  // 16 waves per row: loads of a pass in flight together
 static constexpr int MAXG = 4096;  // group maxima
 static constexpr int MAXC = 2048;  // candidates
 
@@ -159,33 +163,60 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
         better(bv, bi, gumbel_score(z[v], T, s), v);
       }
     } else {
-      // 1) group maxima
-      int gs = max(1, min(256, V / (4 * k)));
-      int ngroups = (V + gs - 1) / gs;
-      if (ngroups > MAXG) {
-        gs = (V + MAXG - 1) / MAXG;
-        ngroups = (V + gs - 1) / gs;
+      // 1) group maxima.  The bound holds for any partition of the row, so
+      //    the groups are strided (entry v belongs to group v mod ngroups)
+      //    and the pass reads the row with coalesced loads.
+      int ngroups = NT;  // a power of two >= 4k (at most MAXG)
+      while (ngroups < MAXG && ngroups < 4 * k) ngroups <<= 1;
+      const bool vec = V % 4 == 0 && a.ldl % 4 == 0 && ((uintptr_t)a.logits & 15) == 0;
+      const v4f* z4 = reinterpret_cast<const v4f*>(z);
+      const int V4 = V / 4;
+      if (vec) {
+        // float4 c belongs to group c mod ngroups
+        for (int gi = tid; gi < ngroups; gi += NT) {
+          float m = -INFINITY;
+#pragma unroll 16
+          for (int c = gi; c < V4; c += ngroups) {
+            const v4f t = z4[c];
+            m = fmaxf(m, fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])));
+          }
+          buf[gi] = m;
+        }
+      } else {
+        for (int gi = tid; gi < ngroups; gi += NT) {
+          float m = -INFINITY;
+          for (int v = gi; v < V; v += ngroups) m = fmaxf(m, z[v]);
+          buf[gi] = m;
+        }
       }
-      for (int gi = tid; gi < ngroups; gi += NT) {
-        float m = -INFINITY;
-        const int e = min(V, (gi + 1) * gs);
-        for (int v = gi * gs; v < e; v++) m = fmaxf(m, z[v]);
-        buf[gi] = m;
-      }
-      int np2 = 1;
-      while (np2 < ngroups) np2 <<= 1;
-      for (int gi = ngroups + tid; gi < np2; gi += NT) buf[gi] = -INFINITY;
       if (tid == 0) ncand = 0;
       __syncthreads();
-      bitonic_desc(buf, np2);
+      bitonic_desc(buf, ngroups);
       const float lower = k <= ngroups ? buf[k - 1] : -INFINITY;
       __syncthreads();
-      // 2) compact candidates >= lower
-      for (int v = tid; v < V; v += NT) {
-        if (z[v] >= lower) {
-          int slot = atomicAdd(&ncand, 1);
+      // 2) compact candidates >= lower (the row is read 8 float4 per thread
+      //    at a time so the loads overlap)
+      auto keep = [&](int v, float zv) {
+        if (zv >= lower) {
+          const int slot = atomicAdd(&ncand, 1);
           if (slot < MAXC) cand_i[slot] = v;
         }
+      };
+      if (vec) {
+        for (int c0 = tid; c0 < V4; c0 += 8 * NT) {
+          v4f t[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            const int c = c0 + u * NT;
+            t[u] = c < V4 ? z4[c] : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          }
+#pragma unroll
+          for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) keep(4 * (c0 + u * NT) + j, t[u][j]);
+        }
+      } else {
+        for (int v = tid; v < V; v += NT) keep(v, z[v]);
       }
       __syncthreads();
       const int nc = ncand;
@@ -216,7 +247,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
           __syncthreads();
           for (int v = tid; v < V; v += NT) {
             uint32_t u = order_key(z[v]);
-            if ((u & pmask) == prefix) atomicAdd(&hist[wid][(u >> shift) & 255u], 1u);
+            if ((u & pmask) == prefix) atomicAdd(&hist[wid & 3][(u >> shift) & 255u], 1u);
           }
           __syncthreads();
           if (tid == 0) {
