@@ -114,6 +114,7 @@ _SIGS = {
     "gn_session_set_timing": (C.c_int, [vp, C.c_int]),
     "gn_session_get_timing": (C.c_int, [vp, C.POINTER(GnTiming)]),
     "gn_session_synchronize": (C.c_int, [vp]),
+    "gn_session_set_decode_graph": (C.c_int, [vp, C.c_int]),
 }
 
 _lib = None

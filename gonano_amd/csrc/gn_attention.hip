@@ -45,6 +45,27 @@ static constexpr int DEC_KPS = 256;
 static constexpr int DEC_MAXR = 8;   // max GQA ratio
 static constexpr int DEC_VPRE = 8;   // V rows per thread loaded ahead of phase 1
 
+// The key range of the call and its balanced splits (same arithmetic on the
+// host for eager launches).
+struct DecSplit {
+  int kstart, kend, kps, nsplit;
+};
+__host__ __device__ inline DecSplit dec_split(int kstart, int kend) {
+  DecSplit d;
+  d.kstart = kstart;
+  d.kend = kend;
+  const int n = kend - kstart;
+  const int ns = (n + DEC_KPS - 1) / DEC_KPS;
+  d.kps = (n + ns - 1) / ns;
+  d.nsplit = (n + d.kps - 1) / d.kps;  // every split non-empty
+  return d;
+}
+__device__ __forceinline__ DecSplit dec_split(const DecodeAttnArgs& a) {
+  if (!a.pos_dev) return dec_split(a.kstart, a.kend);
+  const int pos = *a.pos_dev;
+  return dec_split(max(0, pos - a.window), pos + 1);
+}
+
 __device__ __forceinline__ float red8_sum(float v) {
   v += __shfl_xor(v, 1, 64);
   v += __shfl_xor(v, 2, 64);
@@ -69,9 +90,11 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   __shared__ float stat[2][R];  // max, sum per head
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int bh = blockIdx.x, s = blockIdx.y;
+  const DecSplit sp = dec_split(a);
+  if (s >= sp.nsplit) return;  // graph launches size the grid for the longest window
   const int row = bh / a.Hkv, hk = bh % a.Hkv;
-  const int ks = a.kstart + s * a.kps;
-  const int nk = min(a.kend, ks + a.kps) - ks;
+  const int ks = sp.kstart + s * sp.kps;
+  const int nk = min(sp.kend, ks + sp.kps) - ks;
   const int64_t cbase = ((int64_t)row * a.Hkv + hk) * a.maxSeq + ks;
 
   // V rows of phase 3, issued first
@@ -192,8 +215,8 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   for (int h = 0; h < R; h++)
     *reinterpret_cast<v4f*>(&pv[jr][h][4 * d4]) = (v4f){acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
   __syncthreads();
-  const bool whole = a.nsplit == 1;
-  float* out = a.part + ((int64_t)bh * a.nsplit + s) * R * (HD + 2);
+  const bool whole = sp.nsplit == 1;
+  float* out = a.part + ((int64_t)bh * a.nsplit_max + s) * R * (HD + 2);
   for (int i = tid; i < R * HD; i += 256) {
     const int h = i / HD, dd = i % HD;
     float o = 0.f;
@@ -219,16 +242,19 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
 }
 
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
+  const DecSplit sp = dec_split(a);
+  if (sp.nsplit == 1) return;  // the attention kernel wrote the output
   const int rq = blockIdx.x;  // row * Hq + qh
   const int row = rq / a.Hq, qh = rq % a.Hq;
   const int r = a.Hq / a.Hkv;
   const int hk = qh / r, h = qh % r;
-  const float* base = a.part + ((int64_t)(row * a.Hkv + hk) * a.nsplit) * r * (HD + 2) + h * (HD + 2);
+  const float* base =
+      a.part + ((int64_t)(row * a.Hkv + hk) * a.nsplit_max) * r * (HD + 2) + h * (HD + 2);
   const int64_t stride = (int64_t)r * (HD + 2);
   float gm = -INFINITY;
-  for (int s = 0; s < a.nsplit; s++) gm = fmaxf(gm, base[s * stride + HD]);
+  for (int s = 0; s < sp.nsplit; s++) gm = fmaxf(gm, base[s * stride + HD]);
   float total = 0.f, o = 0.f;
-  for (int s = 0; s < a.nsplit; s++) {
+  for (int s = 0; s < sp.nsplit; s++) {
     float sc = expf(base[s * stride + HD] - gm);
     total += base[s * stride + HD + 1] * sc;
     o += base[s * stride + threadIdx.x] * sc;
@@ -236,13 +262,24 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
   a.o[(int64_t)rq * HD + threadIdx.x] = o / total;
 }
 
+static int decode_attention_max_splits(int window, int maxSeq) {
+  return dec_split(0, std::min(window + 1, maxSeq)).nsplit;
+}
+
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= DEC_MAXR, "decode attention: GQA ratio must be <= 8");
-  GN_CHECK(a.kend > a.kstart, "decode attention: empty key range");
-  const int nkeys = a.kend - a.kstart;
-  a.kps = (int)ceil_div(nkeys, ceil_div(nkeys, DEC_KPS));
-  a.nsplit = (int)ceil_div(nkeys, a.kps);  // every split non-empty
-  const dim3 grid(a.rows * a.Hkv, a.nsplit);
+  bool combine;
+  if (a.pos_dev) {
+    // position read on the device: size for the longest key range
+    GN_CHECK(a.window >= 0, "decode attention: bad window");
+    a.nsplit_max = decode_attention_max_splits(a.window, a.maxSeq);
+    combine = a.nsplit_max > 1;
+  } else {
+    GN_CHECK(a.kend > a.kstart, "decode attention: empty key range");
+    a.nsplit_max = dec_split(a.kstart, a.kend).nsplit;
+    combine = a.nsplit_max > 1;
+  }
+  const dim3 grid(a.rows * a.Hkv, a.nsplit_max);
   switch (a.Hq / a.Hkv) {
     case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), 0, st, a); break;
     case 2: hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), 0, st, a); break;
@@ -254,7 +291,7 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
     case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, grid, dim3(256), 0, st, a); break;
   }
   GN_HIP(hipGetLastError());
-  if (a.nsplit == 1) return;
+  if (!combine) return;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(a.rows * a.Hq), dim3(HD), 0, st, a);
   GN_HIP(hipGetLastError());
 }

@@ -27,6 +27,7 @@ struct QkvPostArgs {
   const float* sinT;
   int C, Hq, Hkv, R, T;
   int pos0;
+  const int* pos_dev;  // when set, pos0 is read from the device instead
   float* qn;
   float* kn;
   float* vout;
@@ -52,8 +53,11 @@ struct DecodeAttnArgs {
   float* part;      // [rows*Hkv][nsplit][Hq/Hkv][130]
   float* o;         // [rows, Hq, 128]
   int rows, Hq, Hkv, maxSeq;
-  int kstart, kend; // keys [kstart, kend)
-  int nsplit, kps;  // set by the launcher: splits and keys per split
+  int kstart, kend;    // keys [kstart, kend) when pos_dev is null; else
+  const int* pos_dev;  // the query position is *pos_dev (read on the device,
+  int window;          // so a captured graph serves every step) and the keys
+                       // are [max(0, pos - window), pos]
+  int nsplit_max;      // set by the launcher: grid.y and the split stride of part
 };
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st);
 

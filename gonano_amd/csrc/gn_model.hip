@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   const float* src = a.qkv + n * (int64_t)H * D;
   for (int i = tid; i < H * D; i += 256) row[i] = src[i];
   const int t = (int)(n % a.T);
-  const int pos = a.pos0 + t;
+  const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
   if (a.ve && wid == 0) {
     // gate[hk] = 3 * sigmoid(h[:12] . wve[hk]) (attention.go:247-248)
     for (int hk = 0; hk < a.Hkv; hk++) {

@@ -90,6 +90,11 @@ struct gn_session {
   std::vector<double> gemm_ev_flops, attn_ev_bytes;
   std::vector<hipEvent_t> event_pool;
   size_t event_next = 0;
+  // decode steps replayed from one captured HIP graph per rollout
+  bool decode_graph = true;
+  bool capturing = false;
+  void* pinned = nullptr;  // host staging for the per-step copies
+  size_t pinned_bytes = 0;
 };
 
 namespace gn {
@@ -103,9 +108,23 @@ static hipEvent_t next_event(gn_session* s) {
   return s->event_pool[s->event_next++];
 }
 
-// GEMM launch with optional event timing.
+// Grow-only pinned host buffer (hipHostMalloc; the stream must be idle when
+// it grows).
+static void* pinned(gn_session* s, size_t bytes) {
+  if (bytes > s->pinned_bytes) {
+    GN_HIP(hipStreamSynchronize(s->stream));
+    if (s->pinned) GN_HIP(hipHostFree(s->pinned));
+    s->pinned = nullptr;
+    s->pinned_bytes = 0;
+    GN_HIP(hipHostMalloc(&s->pinned, bytes, hipHostMallocDefault));
+    s->pinned_bytes = bytes;
+  }
+  return s->pinned;
+}
+
+// GEMM launch with optional event timing (not while a graph is captured).
 static void sgemm(gn_session* s, const GemmDesc& d) {
-  if (s->timing) {
+  if (s->timing && !s->capturing) {
     hipEvent_t a = next_event(s), b = next_event(s);
     GN_HIP(hipEventRecord(a, s->stream));
     gemm(d, s->stream, s->arena.get());
@@ -607,8 +626,11 @@ struct RowState {  // inference/engine.go:11-22
   bool completed = false;
 };
 
+// One decode forward: tokens dtok at position pos -> logits.  With dpos set
+// the position is read on the device (the step is captured once and
+// replayed).
 static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* dtok, float* kc,
-                        float* vc, float* logits) {
+                        float* vc, float* logits, const int* dpos = nullptr) {
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, F = s->F, L = s->L;
   hipStream_t st = s->stream;
   float* x = A<float>(s, "dec_x", (size_t)rows * C);
@@ -632,6 +654,7 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     qa.ve = ly.has_ve ? ly.ve : nullptr; qa.wve = ly.wve;
     qa.cosT = s->cosT; qa.sinT = s->sinT;
     qa.C = C; qa.Hq = Hq; qa.Hkv = Hkv; qa.R = s->R; qa.T = 1; qa.pos0 = pos;
+    qa.pos_dev = dpos;
     qa.qn = q;
     qa.kcache = kc + (int64_t)l * rows * Hkv * maxSeq * HD;
     qa.vcache = vc + (int64_t)l * rows * Hkv * maxSeq * HD;
@@ -643,7 +666,9 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     da.rows = rows; da.Hq = Hq; da.Hkv = Hkv; da.maxSeq = maxSeq;
     da.kstart = std::max(0, pos - ly.window);
     da.kend = pos + 1;
-    if (s->timing) {
+    da.pos_dev = dpos;
+    da.window = ly.window;
+    if (s->timing && !s->capturing) {
       hipEvent_t e0 = next_event(s), e1 = next_event(s);
       GN_HIP(hipEventRecord(e0, st));
       launch_decode_attention(da, st);
@@ -715,28 +740,81 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   float* prev = A<float>(s, "dec_prev", (size_t)rows * C);
   launch_expand_last_rows(sb.embn, prev, G, P, S, C, st);
 
-  // 3) decode loop (engine.go:238-325)
+  // 3) decode loop (engine.go:238-325).  Iteration `step` runs the forward
+  //    that feeds the previous column (none at step 0: the prefill logits)
+  //    and samples column `step`.  After two eager iterations (which size
+  //    every buffer) forward + sampler are captured once as a HIP graph and
+  //    replayed; the step position, the column and the group streams'
+  //    base states reach the device through small copies before each launch.
   std::vector<RowState> states(rows);
   std::vector<u128h> stream(G);
   for (int g = 0; g < G; g++) stream[g] = new_rng_state(seeds[g]);
-  std::vector<uint64_t> base(2 * G);
   uint64_t* dbase = A<uint64_t>(s, "rng_base", 2 * G);
   int32_t* dtok = A<int32_t>(s, "dec_tok", rows);
-  std::vector<int32_t> sampled(rows), column(rows);
+  int* dpos = A<int>(s, "dec_pos", 1);
+  // pinned staging: base states | column | sampled | position
+  char* hp = static_cast<char*>(pinned(s, sizeof(uint64_t) * 2 * G + sizeof(int32_t) * (2 * rows + 1)));
+  uint64_t* base = reinterpret_cast<uint64_t*>(hp);
+  int32_t* column = reinterpret_cast<int32_t*>(base + 2 * G);
+  int32_t* sampled = column + rows;
+  int32_t* hpos = sampled + rows;
   std::vector<char> done(rows, 0);
   int ndone = 0;
+  SamplerArgs sa{};
+  sa.logits = logits; sa.ldl = V; sa.rows = rows; sa.V = V; sa.samples_per_group = S;
+  sa.base_states = dbase; sa.temperature = temperature; sa.top_k = top_k; sa.out = dtok;
+
+  struct Graph {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t e = nullptr;
+    ~Graph() {
+      if (e) (void)hipGraphExecDestroy(e);
+      if (g) (void)hipGraphDestroy(g);
+    }
+  } graph;
+  // (Per-launch attention timing needs events between launches, which a
+  // replayed graph does not give: timed rollouts report attention only
+  // for their eager steps.)
+  const bool use_graph = s->decode_graph && N >= 4;
+
   for (int step = 0; step < N; step++) {
     for (int g = 0; g < G; g++) {
       base[2 * g] = (uint64_t)(stream[g] >> 64);
       base[2 * g + 1] = (uint64_t)stream[g];
       stream[g] = pcg_advance_host(stream[g], (u128h)S * (u128h)V);
     }
-    GN_HIP(hipMemcpyAsync(dbase, base.data(), sizeof(uint64_t) * 2 * G, hipMemcpyHostToDevice, st));
-    SamplerArgs sa{};
-    sa.logits = logits; sa.ldl = V; sa.rows = rows; sa.V = V; sa.samples_per_group = S;
-    sa.base_states = dbase; sa.temperature = temperature; sa.top_k = top_k; sa.out = dtok;
-    launch_sampler(sa, st);
-    GN_HIP(hipMemcpyAsync(sampled.data(), dtok, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
+    const int pos = P + step - 1;  // position of the previous column
+    if (step > 0) {
+      *hpos = pos;
+      GN_HIP(hipMemcpyAsync(dtok, column, sizeof(int32_t) * rows, hipMemcpyHostToDevice, st));
+    }
+    GN_HIP(hipMemcpyAsync(dbase, base, sizeof(uint64_t) * 2 * G, hipMemcpyHostToDevice, st));
+    const bool replay = use_graph && step >= 2;
+    if (replay) {
+      GN_HIP(hipMemcpyAsync(dpos, hpos, sizeof(int), hipMemcpyHostToDevice, st));
+      if (!graph.e) {
+        GN_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        s->capturing = true;
+        try {
+          decode_step(s, rows, pos, maxSeq, dtok, kc, vc, logits, dpos);
+          launch_sampler(sa, st);
+        } catch (...) {
+          s->capturing = false;
+          hipGraph_t g = nullptr;
+          (void)hipStreamEndCapture(st, &g);
+          if (g) (void)hipGraphDestroy(g);
+          throw;
+        }
+        s->capturing = false;
+        GN_HIP(hipStreamEndCapture(st, &graph.g));
+        GN_HIP(hipGraphInstantiate(&graph.e, graph.g, nullptr, nullptr, 0));
+      }
+      GN_HIP(hipGraphLaunch(graph.e, st));
+    } else {
+      if (step > 0) decode_step(s, rows, pos, maxSeq, dtok, kc, vc, logits);
+      launch_sampler(sa, st);
+    }
+    GN_HIP(hipMemcpyAsync(sampled, dtok, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
     GN_HIP(hipStreamSynchronize(st));
     for (int r = 0; r < rows; r++) {
       RowState& rs = states[r];
@@ -776,8 +854,6 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
     if (step + 1 == N) break;  // the reference's final forward feeds no sample
     for (int r = 0; r < rows; r++)
       GN_CHECK(column[r] >= 0 && column[r] < s->PV, "forced token outside the embedding table");
-    GN_HIP(hipMemcpyAsync(dtok, column.data(), sizeof(int32_t) * rows, hipMemcpyHostToDevice, st));
-    decode_step(s, rows, P + step, maxSeq, dtok, kc, vc, logits);
   }
   if (s->timing) {
     GN_HIP(hipEventRecord(ev1, st));
@@ -823,6 +899,7 @@ int gn_session_destroy(gn_session* s) {
     (void)hipStreamSynchronize(s->stream);
     s->arena.reset();
     for (auto e : s->event_pool) (void)hipEventDestroy(e);
+    if (s->pinned) (void)hipHostFree(s->pinned);
     (void)hipFree(s->params);
     (void)hipFree(s->grads);
     (void)hipFree(s->cosT);
@@ -1025,6 +1102,12 @@ int gn_session_get_timing(const gn_session* s, gn_timing* out) {
   return guard([&] {
     GN_CHECK(s && out, "null argument");
     *out = s->t;
+  });
+}
+int gn_session_set_decode_graph(gn_session* s, int enabled) {
+  return guard([&] {
+    GN_CHECK(s, "null session");
+    s->decode_graph = enabled != 0;
   });
 }
 int gn_session_synchronize(gn_session* s) {

@@ -123,6 +123,11 @@ class Session:
         """Waits until the session stream is idle."""
         call("gn_session_synchronize", self._h)
 
+    def set_decode_graph(self, enabled: bool):
+        """Replay rollout decode steps from one captured HIP graph (default)
+        or launch every kernel of every step."""
+        call("gn_session_set_decode_graph", self._h, 1 if enabled else 0)
+
     def timing(self) -> dict:
         t = GnTiming()
         call("gn_session_get_timing", self._h, C.byref(t))

@@ -225,6 +225,11 @@ typedef struct gn_timing {
 } gn_timing;
 int gn_session_set_timing(gn_session *session, int enabled);
 int gn_session_get_timing(const gn_session *session, gn_timing *out);
+/* Rollout decode steps are captured once per gn_generate_batch / gn_rl_step
+ * call as a HIP graph and replayed (default 1); 0 launches every kernel of
+ * every step.  Results are identical either way.  No reference counterpart
+ * (an execution knob of this backend). */
+int gn_session_set_decode_graph(gn_session *session, int enabled);
 /* Waits until the session stream is idle (no reference counterpart: the Go
  * backends are synchronous; used to bracket timed regions). */
 int gn_session_synchronize(gn_session *session);
