@@ -83,6 +83,10 @@ def main() -> int:
                     help="rl: the full RL step (the benchmark); train: only the recompute + "
                          "PG fwd/bwd on a synthetic batch of the workload's shape (for "
                          "counter profiles of the train-phase kernels)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch every decode kernel instead of replaying the captured decode "
+                         "graph (for kernel-trace profiles: rocprofv3 --kernel-trace has "
+                         "crashed on the graph replays)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a device copy of 1 GiB (5 times), the known-size "
                          "reference for HBM byte counters")
@@ -109,6 +113,8 @@ def main() -> int:
     sess = Session(cfg)
     sess.set_params(w)
     sess.set_timing(True)
+    if args.no_graph:
+        sess.set_decode_graph(False)
 
     if args.phase == "train":
         return train_phase(args, sess, prompts, S, N, reward_rng, reward_p)
