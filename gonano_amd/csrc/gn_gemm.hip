@@ -10,6 +10,8 @@
 // (global_load_lds_dwordx4, no VGPR staging), laid out so that MFMA fragments
 // are read with conflict-free LDS accesses; see TileIO.  One barrier per K
 // tile; the loads of the next S-1 tiles stay in flight behind the MFMAs.
+#include <type_traits>
+
 #include "gn_kernels.h"
 
 namespace gn {
@@ -220,7 +222,7 @@ __device__ __forceinline__ void tile_barrier() {
 // every tile (more waves per SIMD for small grids) and are added in LDS at
 // the end.  With p.splits > 1 each workgroup sums one K range into p.part
 // and gemm_reduce_kernel applies the epilogue.
-template <int BM, int BN, int WM, int WN, int WK, int S, bool AK, bool BK, bool VEC>
+template <int BM, int BN, int WM, int WN, int WK, int S, bool FOLD, bool AK, bool BK, bool VEC>
 __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p) {
   constexpr int NT = 64 * WM * WN * WK;
   constexpr int TM = BM / WM, TN = BN / WN;
@@ -264,10 +266,12 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
     }
   };
 
-  // Two-level summation: the MFMAs of one GK-deep tile accumulate into
-  // `blk`, which is added to `acc` after the tile, so rounding error grows
-  // with GK + K/GK rather than K.  This matters for the weight gradients
-  // (K = tokens) and the logits-gradient contraction (K = vocabulary).
+  // FOLD (two-level summation): the MFMAs of one GK-deep tile accumulate
+  // into `blk`, which is added to `acc` after the tile, so rounding error
+  // grows with GK + K/GK rather than K.  It is used for long K ranges (the
+  // weight gradients, K = tokens, and the logits-gradient contraction, K =
+  // vocabulary); it costs 5-9 % of throughput, so short-K products
+  // accumulate in `acc` directly.
   v4f acc[MI][NI];
 #pragma unroll
   for (int i = 0; i < MI; i++)
@@ -286,29 +290,39 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
     tile_barrier();
     // Stage (kt - 1) % S was last read in iteration kt - 1, before the barrier.
     if (kt + S - 1 < nkt) load(kt + S - 1, (kt + S - 1) % S);
-    v4f blk[MI][NI];
+    // one tile's MFMAs into t; `fresh`: the first MFMA starts from zero
+    auto tile_mma = [&](v4f(&t)[MI][NI], auto fresh) {
 #pragma unroll
-    for (int gi = 0; gi < GK / 16 / WK; gi++) {
-      const int g = gi * WK + wk;
-      v4f fa[MI], fb[NI];
+      for (int gi = 0; gi < GK / 16 / WK; gi++) {
+        const int g = gi * WK + wk;
+        v4f fa[MI], fb[NI];
 #pragma unroll
-      for (int i = 0; i < MI; i++) fa[i] = LA::frag(As[cur], wm * TM + 16 * i, g, lane);
+        for (int i = 0; i < MI; i++) fa[i] = LA::frag(As[cur], wm * TM + 16 * i, g, lane);
 #pragma unroll
-      for (int j = 0; j < NI; j++) fb[j] = LB::frag(Bs[cur], wn * TN + 16 * j, g, lane);
+        for (int j = 0; j < NI; j++) fb[j] = LB::frag(Bs[cur], wn * TN + 16 * j, g, lane);
 #pragma unroll
-      for (int c = 0; c < 4; c++)
+        for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int i = 0; i < MI; i++)
+          for (int i = 0; i < MI; i++)
 #pragma unroll
-          for (int j = 0; j < NI; j++)
-            blk[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                fa[i][c], fb[j][c],
-                (gi == 0 && c == 0) ? (v4f){0.f, 0.f, 0.f, 0.f} : blk[i][j], 0, 0, 0);
+            for (int j = 0; j < NI; j++)
+              t[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                  fa[i][c], fb[j][c],
+                  (decltype(fresh)::value && gi == 0 && c == 0) ? (v4f){0.f, 0.f, 0.f, 0.f}
+                                                                : t[i][j],
+                  0, 0, 0);
+      }
+    };
+    if constexpr (FOLD) {
+      v4f blk[MI][NI];
+      tile_mma(blk, std::true_type{});
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < NI; j++) acc[i][j] += blk[i][j];
+    } else {
+      tile_mma(acc, std::false_type{});
     }
-#pragma unroll
-    for (int i = 0; i < MI; i++)
-#pragma unroll
-      for (int j = 0; j < NI; j++) acc[i][j] += blk[i][j];
   }
   if constexpr (WK > 1) {
     // Wave groups 1..WK-1 park their sums in the (now idle) stage buffers;
@@ -378,7 +392,7 @@ __global__ void gemm_reduce_kernel(GemmParams p) {
   gemm_epilogue(p, (int)(idx / p.N), (int)(idx % p.N), (float)s);
 }
 
-template <int BM, int BN, int WM, int WN, int WK, int S>
+template <int BM, int BN, int WM, int WN, int WK, int S, bool FOLD>
 static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int splits,
                        hipStream_t st) {
   GemmParams q = p;
@@ -388,7 +402,7 @@ static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int spli
   dim3 grid(q.tiles_m * q.tiles_n * splits);
   dim3 block(64 * WM * WN * WK);
 #define GN_GEMM_LAUNCH(AK, BK, V) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, AK, BK, V>), grid, block, 0, st, q)
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, FOLD, AK, BK, V>), grid, block, 0, st, q)
   if (vec) {
     if (ak && bk) GN_GEMM_LAUNCH(true, true, true);
     else if (ak && !bk) GN_GEMM_LAUNCH(true, false, true);
@@ -465,8 +479,16 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
     p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
   }
-  if (use_big) launch_cfg<128, 128, 2, 2, 1, 2>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
-  else launch_cfg<64, 64, 2, 2, 2, 4>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  // two-level summation for long K ranges per workgroup (see gemm_kernel)
+  const bool fold = kps >= 4096;
+  if (use_big && fold)
+    launch_cfg<128, 128, 2, 2, 1, 2, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  else if (use_big)
+    launch_cfg<128, 128, 2, 2, 1, 2, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  else if (fold)
+    launch_cfg<64, 64, 2, 2, 2, 4, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  else
+    launch_cfg<64, 64, 2, 2, 2, 4, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   if (splits > 1) {
     const int64_t total = (int64_t)d.M * d.N;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
