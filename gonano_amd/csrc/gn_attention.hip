@@ -296,114 +296,150 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   GN_HIP(hipGetLastError());
 }
 
-// ---------------------------------------------------------------------------
-// Flash forward (training / prefill).  Block: 32 queries x 8 threads, each
-// thread owning 16 of the 128 dims; keys streamed through LDS 32 at a time.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float red8(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  return v;
-}
+// Key kj is visible from query t: causal, inside the sliding window (a
+// window w admits w + 1 keys, kernels/scalar/attention.go:210-228).
 __device__ __forceinline__ bool key_valid(int kj, int t, int T, int window) {
   return kj < T && kj <= t && (window < 0 || t - kj <= window);
 }
 
-__global__ __launch_bounds__(256) void flash_fwd_kernel(FlashArgs a) {
-  constexpr int LD = HD + 4;
-  __shared__ __attribute__((aligned(16))) float Ks[32 * LD];
-  __shared__ __attribute__((aligned(16))) float Vs[32 * LD];
-  const int tid = threadIdx.x, qi = tid >> 3, part = tid & 7;
-  const int qb = blockIdx.x * 32;
+// ---------------------------------------------------------------------------
+// Flash forward on the matrix cores.  Block: 4 waves x 16 queries of one
+// (sequence, query head); keys in tiles of 64 through LDS (K row-major, V
+// transposed).  Each wave computes S^T = K.Q^T and O^T += V^T.P^T with
+// v_mfma_f32_16x16x4f32, so in both products a lane's column is one query
+// (lane & 15): the running max, the sum and the O rescale stay in the lane,
+// and the P values of a lane are directly the B operand of the second
+// product.  k order inside a 16-key block: MFMA c of the PV product takes
+// key 4*(lane >> 4) + c, which is where the S^T accumulator left it.
+// ---------------------------------------------------------------------------
+static constexpr int FQ = 64;   // queries per block
+static constexpr int FK = 64;   // keys per LDS tile
+static constexpr int FLK = HD + 4;   // K tile row stride (floats)
+static constexpr int FLV = FK + 4;   // V^T tile row stride
+
+__global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
+  __shared__ __attribute__((aligned(16))) float Ks[FK * FLK];
+  __shared__ __attribute__((aligned(16))) float Vt[HD * FLV];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int q0 = blockIdx.x * FQ;
   const int bh = blockIdx.y, b = bh / a.Hq, qh = bh % a.Hq;
   const int hk = qh / (a.Hq / a.Hkv);
-  const int t = qb + qi;
+  const int t = q0 + 16 * w + l16;  // this lane's query
   const bool active = t < a.T;
-  float q[16];
+
+  // Q^T fragments: lane holds Q[t][16s + 4g .. +3], s = 0..7
+  v4f qf[8];
   {
-    const float* qp = a.q + (((int64_t)b * a.T + min(t, a.T - 1)) * a.Hq + qh) * HD + 16 * part;
+    const float* qp = a.q + (((int64_t)b * a.T + min(t, a.T - 1)) * a.Hq + qh) * HD + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 16; i += 4) {
-      v4f v = *reinterpret_cast<const v4f*>(qp + i);
-      q[i] = v[0]; q[i + 1] = v[1]; q[i + 2] = v[2]; q[i + 3] = v[3];
-    }
+    for (int s = 0; s < 8; s++) qf[s] = *reinterpret_cast<const v4f*>(qp + 16 * s);
   }
-  const int kmin = a.window >= 0 ? max(0, qb - a.window) : 0;
-  const int kmax = min(a.T, qb + 32);
+  v4f acc[8];  // O^T[16i + 4g + r][t]
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
-  float acc[16];
+
+  const int qlast = min(a.T, q0 + FQ) - 1;
+  const int kmin = a.window >= 0 ? max(0, q0 - a.window) : 0;
+  const int kmax = qlast + 1;
+  for (int kt = (kmin / FK) * FK; kt < kmax; kt += FK) {
+    __syncthreads();  // previous tile fully consumed
+    // K tile rows (coalesced float4), V tile transposed into Vt[d][key]
 #pragma unroll
-  for (int i = 0; i < 16; i++) acc[i] = 0.f;
-  for (int kb = (kmin / 32) * 32; kb < kmax; kb += 32) {
+    for (int i = 0; i < FK * HD / 4 / 256; i++) {
+      const int idx = tid + 256 * i;
+      const int kr = idx >> 5, c4 = idx & 31;
+      const int kj = kt + kr;
+      v4f kv = {0.f, 0.f, 0.f, 0.f};
+      if (kj < a.T) kv = *reinterpret_cast<const v4f*>(
+          a.k + (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4);
+      *reinterpret_cast<v4f*>(&Ks[kr * FLK + 4 * c4]) = kv;
+    }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      int idx = tid + 256 * i;  // 32 rows x 32 float4
-      int rr = idx >> 5, c4 = idx & 31;
-      int kj = kb + rr;
-      v4f kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-      if (kj < a.T) {
-        int64_t off = (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4;
-        kv = *reinterpret_cast<const v4f*>(a.k + off);
-        vv = *reinterpret_cast<const v4f*>(a.v + off);
-      }
-      *reinterpret_cast<v4f*>(&Ks[rr * LD + 4 * c4]) = kv;
-      *reinterpret_cast<v4f*>(&Vs[rr * LD + 4 * c4]) = vv;
+    for (int i = 0; i < FK * HD / 4 / 256; i++) {
+      const int idx = tid + 256 * i;
+      const int kr = idx & 63, c4 = idx >> 6;  // lanes walk keys: conflict-free stores
+      const int kj = kt + kr;
+      v4f vv = {0.f, 0.f, 0.f, 0.f};
+      if (kj < a.T) vv = *reinterpret_cast<const v4f*>(
+          a.v + (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4);
+#pragma unroll
+      for (int j = 0; j < 4; j++) Vt[(4 * c4 + j) * FLV + kr] = vv[j];
     }
     __syncthreads();
-    float s[32];
-    float bm = -INFINITY;
+
+    // S^T for the tile: st[kb] = S^T[kt + 16kb + 4g + r][t]
+    v4f st[4];
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-      const float* kr = &Ks[j * LD + 16 * part];
-      float p = 0.f;
+    for (int kb = 0; kb < 4; kb++) {
+      st[kb] = (v4f){0.f, 0.f, 0.f, 0.f};
+      const float* kp = &Ks[(16 * kb + l16) * FLK + 4 * g];
 #pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        v4f kv = *reinterpret_cast<const v4f*>(kr + i);
-        p += q[i] * kv[0] + q[i + 1] * kv[1] + q[i + 2] * kv[2] + q[i + 3] * kv[3];
+      for (int s = 0; s < 8; s++) {
+        const v4f kf = *reinterpret_cast<const v4f*>(kp + 16 * s);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          st[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[c], qf[s][c], st[kb], 0, 0, 0);
       }
-      p = red8(p);
-      s[j] = key_valid(kb + j, t, a.T, a.window) ? p : -INFINITY;
-      bm = fmaxf(bm, s[j]);
     }
-    if (bm > -INFINITY) {
-      const float mn = fmaxf(m, bm);
-      const float sc = expf(m - mn);
-      l *= sc;
+    // mask, online softmax (the lane's column is query t)
+    float tmax = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 16; i++) acc[i] *= sc;
+    for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-      for (int j = 0; j < 32; j++) {
-        float p = expf(s[j] - mn);
-        l += p;
-        const float* vr = &Vs[j * LD + 16 * part];
+      for (int r = 0; r < 4; r++) {
+        const int kj = kt + 16 * kb + 4 * g + r;
+        if (!key_valid(kj, t, a.T, a.window)) st[kb][r] = -INFINITY;
+        tmax = fmaxf(tmax, st[kb][r]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    if (tmax > -INFINITY) {  // uniform over the 4 lanes of a query
+      const float mn = fmaxf(m, tmax);
+      const float sc = expf(m - mn);  // 0 while m is -inf
+      float ps = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-          v4f vv = *reinterpret_cast<const v4f*>(vr + i);
-          acc[i] += p * vv[0];
-          acc[i + 1] += p * vv[1];
-          acc[i + 2] += p * vv[2];
-          acc[i + 3] += p * vv[3];
+      for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float p = expf(st[kb][r] - mn);  // masked: exp(-inf) = 0
+          st[kb][r] = p;
+          ps += p;
         }
-      }
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      l = l * sc + ps;
       m = mn;
+#pragma unroll
+      for (int i = 0; i < 8; i++) acc[i] *= sc;
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) st[kb] = (v4f){0.f, 0.f, 0.f, 0.f};
     }
-    __syncthreads();
+    // O^T += V^T P^T
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const v4f vf = *reinterpret_cast<const v4f*>(&Vt[(16 * i + l16) * FLV + 16 * kb + 4 * g]);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[c], st[kb][c], acc[i], 0, 0, 0);
+      }
   }
   if (active) {
     const float inv = 1.f / l;
-    float* op = a.o + (((int64_t)b * a.T + t) * a.Hq + qh) * HD + 16 * part;
+    float* op = a.o + (((int64_t)b * a.T + t) * a.Hq + qh) * HD + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 16; i += 4)
-      *reinterpret_cast<v4f*>(op + i) = (v4f){acc[i] * inv, acc[i + 1] * inv, acc[i + 2] * inv,
-                                               acc[i + 3] * inv};
-    if (a.lse && part == 0) a.lse[((int64_t)b * a.T + t) * a.Hq + qh] = m + logf(l);
+    for (int i = 0; i < 8; i++) *reinterpret_cast<v4f*>(op + 16 * i) = acc[i] * inv;
+    if (a.lse && g == 0) a.lse[((int64_t)b * a.T + t) * a.Hq + qh] = m + logf(l);
   }
 }
 
 void launch_flash_fwd(const FlashArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(flash_fwd_kernel, dim3((unsigned)ceil_div(a.T, 32), a.B * a.Hq), dim3(256), 0,
-                     st, a);
+  hipLaunchKernelGGL(flash_fwd_mfma_kernel, dim3((unsigned)ceil_div(a.T, FQ), a.B * a.Hq),
+                     dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }
 
@@ -420,146 +456,193 @@ __global__ __launch_bounds__(256) void flash_delta_kernel(const float* __restric
   if (lane == 0) delta[r] = s;
 }
 
-// dQ for 32 queries per block.
-__global__ __launch_bounds__(256) void flash_bwd_dq_kernel(FlashBwdArgs a) {
-  constexpr int LD = HD + 4;
-  __shared__ __attribute__((aligned(16))) float Ks[32 * LD];
-  __shared__ __attribute__((aligned(16))) float Vs[32 * LD];
-  const int tid = threadIdx.x, qi = tid >> 3, part = tid & 7;
-  const int qb = blockIdx.x * 32;
+// ---------------------------------------------------------------------------
+// Flash backward on the matrix cores, deterministic and atomic-free as two
+// kernels (kernels/scalar/attention.go:145-205 semantics, from the forward's
+// log-sum-exp and delta = rowsum(dO * O)):
+//  * dQ: 4 waves x 16 queries per block, keys in tiles of 64.  Per 16-key
+//    block a wave forms S^T and dP^T (lane column = its query), dS^T =
+//    P^T (dP^T - delta) in the lane, and dQ^T += K^T dS^T.
+//  * dK/dV: 4 waves x 16 keys per block, over every query head of the GQA
+//    group and query tiles of 64.  Per 16-query block S and dP come out with
+//    the lane column = its key, so P and dS feed dV^T += dO^T P and
+//    dK^T += Q^T dS as B operands straight from the lane.
+// Both use the k order of the forward (k-slot g of MFMA c is element 4g + c
+// of a 16 block), so no accumulator is transposed through LDS.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs a) {
+  __shared__ __attribute__((aligned(16))) float Ks[FK * FLK];
+  __shared__ __attribute__((aligned(16))) float Vs[FK * FLK];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int q0 = blockIdx.x * FQ;
   const int bh = blockIdx.y, b = bh / a.Hq, qh = bh % a.Hq;
   const int hk = qh / (a.Hq / a.Hkv);
-  const int t = qb + qi;
+  const int t = q0 + 16 * w + l16;
   const bool active = t < a.T;
   const int64_t qrow = ((int64_t)b * a.T + min(t, a.T - 1)) * a.Hq + qh;
-  float q[16], g[16], dq[16];
+  v4f qf[8], gf[8];
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    q[i] = a.q[qrow * HD + 16 * part + i];
-    g[i] = a.dout[qrow * HD + 16 * part + i];
-    dq[i] = 0.f;
+  for (int s = 0; s < 8; s++) {
+    qf[s] = *reinterpret_cast<const v4f*>(a.q + qrow * HD + 16 * s + 4 * g);
+    gf[s] = *reinterpret_cast<const v4f*>(a.dout + qrow * HD + 16 * s + 4 * g);
   }
   const float lse = a.lse[qrow], dl = a.delta[qrow];
-  const int kmin = a.window >= 0 ? max(0, qb - a.window) : 0;
-  const int kmax = min(a.T, qb + 32);
-  for (int kb = (kmin / 32) * 32; kb < kmax; kb += 32) {
+  v4f dq[8];  // dQ^T[16i + 4g + r][t]
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      int idx = tid + 256 * i;
-      int rr = idx >> 5, c4 = idx & 31;
-      int kj = kb + rr;
+  for (int i = 0; i < 8; i++) dq[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  const int qlast = min(a.T, q0 + FQ) - 1;
+  const int kmin = a.window >= 0 ? max(0, q0 - a.window) : 0;
+  for (int kt = (kmin / FK) * FK; kt <= qlast; kt += FK) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FK * HD / 4 / 256; i++) {
+      const int idx = tid + 256 * i;
+      const int kr = idx >> 5, c4 = idx & 31;
+      const int kj = kt + kr;
       v4f kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
       if (kj < a.T) {
-        int64_t off = (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4;
+        const int64_t off = (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4;
         kv = *reinterpret_cast<const v4f*>(a.k + off);
         vv = *reinterpret_cast<const v4f*>(a.v + off);
       }
-      *reinterpret_cast<v4f*>(&Ks[rr * LD + 4 * c4]) = kv;
-      *reinterpret_cast<v4f*>(&Vs[rr * LD + 4 * c4]) = vv;
+      *reinterpret_cast<v4f*>(&Ks[kr * FLK + 4 * c4]) = kv;
+      *reinterpret_cast<v4f*>(&Vs[kr * FLK + 4 * c4]) = vv;
     }
     __syncthreads();
-    for (int j = 0; j < 32; j++) {
-      const float* kr = &Ks[j * LD + 16 * part];
-      const float* vr = &Vs[j * LD + 16 * part];
-      float s = 0.f, dp = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; i++) {
-        s += q[i] * kr[i];
-        dp += g[i] * vr[i];
-      }
-      s = red8(s);
-      dp = red8(dp);
-      if (key_valid(kb + j, t, a.T, a.window)) {
-        float p = expf(s - lse);
-        float ds = p * (dp - dl);
+    for (int kb = 0; kb < FK / 16; kb++) {
+      v4f st = {0.f, 0.f, 0.f, 0.f}, dpt = {0.f, 0.f, 0.f, 0.f};
+      const float* kp = &Ks[(16 * kb + l16) * FLK + 4 * g];
+      const float* vp = &Vs[(16 * kb + l16) * FLK + 4 * g];
 #pragma unroll
-        for (int i = 0; i < 16; i++) dq[i] += ds * kr[i];
+      for (int s = 0; s < 8; s++) {
+        const v4f kf = *reinterpret_cast<const v4f*>(kp + 16 * s);
+        const v4f vf = *reinterpret_cast<const v4f*>(vp + 16 * s);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          st = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[c], qf[s][c], st, 0, 0, 0);
+          dpt = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[c], gf[s][c], dpt, 0, 0, 0);
+        }
       }
+      v4f ds;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int kj = kt + 16 * kb + 4 * g + r;
+        const float p = (active && key_valid(kj, t, a.T, a.window)) ? expf(st[r] - lse) : 0.f;
+        ds[r] = p * (dpt[r] - dl);
+      }
+      // dQ^T += K^T dS^T: A = K[16kb + 4g + c][16i + l16]
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          dq[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              Ks[(16 * kb + 4 * g + c) * FLK + 16 * i + l16], ds[c], dq[i], 0, 0, 0);
     }
-    __syncthreads();
   }
   if (active) {
+    float* op = a.dq + qrow * HD + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 16; i++) a.dq[qrow * HD + 16 * part + i] = dq[i];
+    for (int i = 0; i < 8; i++) *reinterpret_cast<v4f*>(op + 16 * i) = dq[i];
   }
 }
 
-// dK, dV for 32 keys per block, summed over the query heads of the group.
-__global__ __launch_bounds__(256) void flash_bwd_dkdv_kernel(FlashBwdArgs a) {
-  constexpr int LD = HD + 4;
-  __shared__ __attribute__((aligned(16))) float Qs[32 * LD];
-  __shared__ __attribute__((aligned(16))) float Gs[32 * LD];
-  __shared__ float Ls[32], Ds[32];
-  const int tid = threadIdx.x, ki = tid >> 3, part = tid & 7;
-  const int kb = blockIdx.x * 32;
+__global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArgs a) {
+  __shared__ __attribute__((aligned(16))) float Qs[FQ * FLK];
+  __shared__ __attribute__((aligned(16))) float Gs[FQ * FLK];
+  __shared__ float Ls[FQ], Ds[FQ];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int k0 = blockIdx.x * FK;
   const int bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
   const int r = a.Hq / a.Hkv;
-  const int kj = kb + ki;
-  const bool active = kj < a.T;
-  const int64_t krow = ((int64_t)b * a.T + min(kj, a.T - 1)) * a.Hkv + hk;
-  float k[16], v[16], dk[16], dv[16];
+  const int j = k0 + 16 * w + l16;  // this lane's key
+  const bool active = j < a.T;
+  const int64_t krow = ((int64_t)b * a.T + min(j, a.T - 1)) * a.Hkv + hk;
+  v4f kf[8], vf[8];
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    k[i] = a.k[krow * HD + 16 * part + i];
-    v[i] = a.v[krow * HD + 16 * part + i];
-    dk[i] = 0.f;
-    dv[i] = 0.f;
+  for (int s = 0; s < 8; s++) {
+    kf[s] = *reinterpret_cast<const v4f*>(a.k + krow * HD + 16 * s + 4 * g);
+    vf[s] = *reinterpret_cast<const v4f*>(a.v + krow * HD + 16 * s + 4 * g);
   }
-  const int qend = a.window >= 0 ? min(a.T, kb + 32 + a.window) : a.T;
+  v4f dk[8], dv[8];  // dK^T, dV^T [16i + 4g + r][j]
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    dk[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+    dv[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+  const int klast = min(a.T, k0 + FK) - 1;
+  const int qend = a.window >= 0 ? min(a.T, klast + a.window + 1) : a.T;
   for (int h = 0; h < r; h++) {
     const int qh = hk * r + h;
-    for (int qb = kb; qb < qend; qb += 32) {
+    for (int qt = (k0 / FQ) * FQ; qt < qend; qt += FQ) {
+      __syncthreads();
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        int idx = tid + 256 * i;
-        int rr = idx >> 5, c4 = idx & 31;
-        int t = qb + rr;
+      for (int i = 0; i < FQ * HD / 4 / 256; i++) {
+        const int idx = tid + 256 * i;
+        const int qr = idx >> 5, c4 = idx & 31;
+        const int tq = qt + qr;
         v4f qv = {0.f, 0.f, 0.f, 0.f}, gv = {0.f, 0.f, 0.f, 0.f};
-        if (t < a.T) {
-          int64_t off = (((int64_t)b * a.T + t) * a.Hq + qh) * HD + 4 * c4;
+        if (tq < a.T) {
+          const int64_t off = (((int64_t)b * a.T + tq) * a.Hq + qh) * HD + 4 * c4;
           qv = *reinterpret_cast<const v4f*>(a.q + off);
           gv = *reinterpret_cast<const v4f*>(a.dout + off);
         }
-        *reinterpret_cast<v4f*>(&Qs[rr * LD + 4 * c4]) = qv;
-        *reinterpret_cast<v4f*>(&Gs[rr * LD + 4 * c4]) = gv;
+        *reinterpret_cast<v4f*>(&Qs[qr * FLK + 4 * c4]) = qv;
+        *reinterpret_cast<v4f*>(&Gs[qr * FLK + 4 * c4]) = gv;
       }
-      if (tid < 32) {
-        int t = qb + tid;
-        int64_t qrow = ((int64_t)b * a.T + min(t, a.T - 1)) * a.Hq + qh;
-        Ls[tid] = a.lse[qrow];
-        Ds[tid] = a.delta[qrow];
+      if (tid < FQ) {
+        const int tq = qt + tid;
+        const int64_t row = ((int64_t)b * a.T + min(tq, a.T - 1)) * a.Hq + qh;
+        Ls[tid] = a.lse[row];
+        Ds[tid] = a.delta[row];
       }
       __syncthreads();
-      for (int i2 = 0; i2 < 32; i2++) {
-        const float* qr = &Qs[i2 * LD + 16 * part];
-        const float* gr = &Gs[i2 * LD + 16 * part];
-        float s = 0.f, dp = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-          s += qr[i] * k[i];
-          dp += gr[i] * v[i];
-        }
-        s = red8(s);
-        dp = red8(dp);
-        const int t = qb + i2;
-        if (active && t < a.T && key_valid(kj, t, a.T, a.window)) {
-          float p = expf(s - Ls[i2]);
-          float ds = p * (dp - Ds[i2]);
+      for (int qb = 0; qb < FQ / 16; qb++) {
+        v4f sv = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+        const float* qp = &Qs[(16 * qb + l16) * FLK + 4 * g];
+        const float* gp = &Gs[(16 * qb + l16) * FLK + 4 * g];
 #pragma unroll
-          for (int i = 0; i < 16; i++) {
-            dv[i] += p * gr[i];
-            dk[i] += ds * qr[i];
+        for (int s = 0; s < 8; s++) {
+          const v4f qv = *reinterpret_cast<const v4f*>(qp + 16 * s);
+          const v4f gv = *reinterpret_cast<const v4f*>(gp + 16 * s);
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[c], kf[s][c], sv, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_16x16x4f32(gv[c], vf[s][c], dp, 0, 0, 0);
           }
         }
+        // S[q][j], dP[q][j] for q = qt + 16qb + 4g + rr
+        v4f p, ds;
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+          const int ql = 16 * qb + 4 * g + rr, tq = qt + ql;
+          const bool ok = active && tq < a.T && key_valid(j, tq, a.T, a.window);
+          p[rr] = ok ? expf(sv[rr] - Ls[ql]) : 0.f;
+          ds[rr] = p[rr] * (dp[rr] - Ds[ql]);
+        }
+        // dV^T += dO^T P, dK^T += Q^T dS: A = X[16qb + 4g + c][16i + l16]
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            const int row = (16 * qb + 4 * g + c) * FLK + 16 * i + l16;
+            dv[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(Gs[row], p[c], dv[i], 0, 0, 0);
+            dk[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[row], ds[c], dk[i], 0, 0, 0);
+          }
       }
-      __syncthreads();
     }
   }
   if (active) {
+    float* kp = a.dk + krow * HD + 4 * g;
+    float* vp = a.dv + krow * HD + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      a.dk[krow * HD + 16 * part + i] = dk[i];
-      a.dv[krow * HD + 16 * part + i] = dv[i];
+    for (int i = 0; i < 8; i++) {
+      *reinterpret_cast<v4f*>(kp + 16 * i) = dk[i];
+      *reinterpret_cast<v4f*>(vp + 16 * i) = dv[i];
     }
   }
 }
@@ -569,10 +652,10 @@ void launch_flash_bwd(const FlashBwdArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(flash_delta_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st, a.o,
                      a.dout, a.delta, rows);
   GN_HIP(hipGetLastError());
-  hipLaunchKernelGGL(flash_bwd_dq_kernel, dim3((unsigned)ceil_div(a.T, 32), a.B * a.Hq), dim3(256),
-                     0, st, a);
+  hipLaunchKernelGGL(flash_bwd_dq_mfma_kernel, dim3((unsigned)ceil_div(a.T, FQ), a.B * a.Hq),
+                     dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
-  hipLaunchKernelGGL(flash_bwd_dkdv_kernel, dim3((unsigned)ceil_div(a.T, 32), a.B * a.Hkv),
+  hipLaunchKernelGGL(flash_bwd_dkdv_mfma_kernel, dim3((unsigned)ceil_div(a.T, FK), a.B * a.Hkv),
                      dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }
