@@ -16,9 +16,17 @@ VE_GATE_CHANNELS = 12  # model/attention.go:18
 VOCAB_PADDING = 64  # model/config.go:620
 
 
+DEFAULT_ROTARY_DIMS = 64  # model/config.go:425
+DEFAULT_MOE_CLAMP = 10.0  # model/config.go:125
+DEFAULT_MOE_BALANCE_WEIGHT = 1e-4  # model/config.go:134
+
+
 @dataclass
 class Config:
-    """model.Config (model/config.go:9-124), dense fields."""
+    """model.Config (model/config.go:9-124): the dense fields plus the latent
+    preset's MLA and DeepSeekMoE fields.  MoE fields hold resolved values
+    (ApplyMoEDefaults, MoEEffectiveClamp/Scale, MoEBalanceLossWeight); zeros
+    keep the dense model."""
 
     sequence_len: int
     vocab_size: int
@@ -28,6 +36,15 @@ class Config:
     n_embd: int
     window_pattern: str = "SSSL"
     rotary_dims: int = 0
+    mla_latent: int = 0          # Config.MLALatent
+    mla_rope_dims: int = 0       # Config.MLARotaryDims (0: default)
+    n_experts: int = 0           # Config.NumExperts
+    experts_per_token: int = 0   # MoEActiveExperts()
+    expert_hidden: int = 0       # MoEExpertHidden()
+    shared_hidden: int = 0       # MoESharedHidden()
+    moe_clamp: float = 0.0       # MoEEffectiveClamp()
+    moe_scale: float = 0.0       # MoEEffectiveScale()
+    balance_weight: float = 0.0  # MoEBalanceLossWeight()
 
     # -- derived quantities -------------------------------------------------
     @property
@@ -35,7 +52,28 @@ class Config:
         return self.n_embd // self.n_head
 
     @property
+    def mla_rope_dimension(self) -> int:  # model/config.go:262-280
+        if self.mla_rope_dims <= 0:
+            width = min(self.head_dim // 2, DEFAULT_ROTARY_DIMS)
+            return width - (width % 2)
+        if self.mla_rope_dims > self.head_dim:
+            raise ValueError(f"MLARotaryDims {self.mla_rope_dims} exceeds head dim {self.head_dim}")
+        if self.mla_rope_dims % 2:
+            raise ValueError(f"MLARotaryDims {self.mla_rope_dims} must be even")
+        return self.mla_rope_dims
+
+    @property
+    def mla(self) -> bool:  # model/config.go:250
+        return self.mla_latent > 0
+
+    @property
+    def moe(self) -> bool:  # model/config.go:138
+        return self.n_experts > 0
+
+    @property
     def rotary_dimension(self) -> int:  # model/config.go:430-444
+        if self.mla:
+            return self.mla_rope_dimension
         if self.rotary_dims <= 0:
             return self.head_dim
         if self.rotary_dims > self.head_dim:
@@ -49,11 +87,12 @@ class Config:
         return ((self.vocab_size + VOCAB_PADDING - 1) // VOCAB_PADDING) * VOCAB_PADDING
 
     @property
-    def mlp_hidden(self) -> int:  # model/mlp.go:35-37
-        return 4 * self.n_embd
+    def mlp_hidden(self) -> int:  # model/mlp.go:35-37, model/block.go:23-28
+        return self.shared_hidden if self.moe else 4 * self.n_embd
 
-    def has_value_embedding(self, layer: int) -> bool:  # model/helpers.go:69-71
-        return layer % 2 == (self.n_layer - 1) % 2
+    def has_value_embedding(self, layer: int) -> bool:
+        """model/helpers.go:69-71; never under MLA (model/transformer.go:72-78)."""
+        return not self.mla and layer % 2 == (self.n_layer - 1) % 2
 
     def window_sizes(self) -> list[int]:
         """model/config.go:629-645; Go's integer division truncates toward zero."""
@@ -76,22 +115,46 @@ class Config:
             if ch not in "LSls":
                 raise ValueError(f"invalid window pattern {self.window_pattern!r}")
         _ = self.rotary_dimension
+        if self.mla and self.head_dim - self.mla_rope_dimension <= 0:  # config.go:502-504
+            raise ValueError("MLA content dimension must be positive")
+        if self.moe and not 0 < self.experts_per_token <= self.n_experts:  # config.go:535-541
+            raise ValueError(f"NumExpertsPerToken {self.experts_per_token} must be in "
+                             f"[1, NumExperts={self.n_experts}]")
 
     # -- parameter table (model/params.go:14-85, sorted as ParameterNames) ---
     def param_table(self) -> list[tuple[str, int, int, int]]:
         C_, D, PV = self.n_embd, self.head_dim, self.padded_vocab
         ents = [("transformer.wte.weight", PV, C_), ("lm_head.weight", PV, C_)]
+        Hq, Hkv, F = self.n_head, self.n_kv_head, self.mlp_hidden
         for l in range(self.n_layer):
             p = f"transformer.h.{l}."
-            ents += [(p + "attn.c_q.weight", self.n_head * D, C_),
-                     (p + "attn.c_k.weight", self.n_kv_head * D, C_),
-                     (p + "attn.c_v.weight", self.n_kv_head * D, C_),
-                     (p + "attn.c_proj.weight", C_, C_)]
+            if self.mla:  # model/params.go:19-27, model/mla.go:41-58
+                lat, rd = self.mla_latent, self.mla_rope_dimension
+                cd = D - rd
+                ents += [(p + "attn.mla_q_down.weight", lat, C_),
+                         (p + "attn.mla_q_up.weight", Hq * cd, lat),
+                         (p + "attn.mla_q_rope.weight", Hq * rd, C_),
+                         (p + "attn.mla_kv_down.weight", lat, C_),
+                         (p + "attn.mla_k_up.weight", Hkv * cd, lat),
+                         (p + "attn.mla_v_up.weight", Hkv * D, lat),
+                         (p + "attn.mla_k_rope.weight", Hkv * rd, C_)]
+            else:
+                ents += [(p + "attn.c_q.weight", Hq * D, C_),
+                         (p + "attn.c_k.weight", Hkv * D, C_),
+                         (p + "attn.c_v.weight", Hkv * D, C_)]
+            ents += [(p + "attn.c_proj.weight", C_, C_)]
             if self.has_value_embedding(l):
-                ents += [(p + "attn.ve_gate.weight", self.n_kv_head, VE_GATE_CHANNELS),
-                         (f"value_embeds.{l}.weight", PV, self.n_kv_head * D)]
-            ents += [(p + "mlp.c_fc.weight", self.mlp_hidden, C_),
-                     (p + "mlp.c_proj.weight", C_, self.mlp_hidden)]
+                ents += [(p + "attn.ve_gate.weight", Hkv, VE_GATE_CHANNELS),
+                         (f"value_embeds.{l}.weight", PV, Hkv * D)]
+            ents += [(p + "mlp.c_fc.weight", F, C_), (p + "mlp.c_proj.weight", C_, F)]
+            if self.moe:  # model/params.go:53-63; packed [E, H, C] / [E, C, H]
+                E, EH = self.n_experts, self.expert_hidden
+                ents += [(p + "mlp.c_gate.weight", F, C_),
+                         (p + "moe.router.weight", E, C_),
+                         (p + "moe.router_bias", E, 1),
+                         (p + "moe.experts.gate.weight", E * EH, C_),
+                         (p + "moe.experts.up.weight", E * EH, C_),
+                         (p + "moe.experts.down.weight", E * C_, EH)]
         ents += [("resid_lambdas", self.n_layer, 1), ("x0_lambdas", self.n_layer, 1),
                  ("smear_gate.weight", 1, SMEAR_GATE_CHANNELS), ("smear_lambda", 1, 1),
                  ("backout_lambda", 1, 1)]
@@ -144,6 +207,48 @@ def dense_d20() -> Config:
     return config_for_depth_ratio(20, 65536, 64, 128, 2048, "SSSL", 5)
 
 
+def moe_experts_for_depth(depth: int) -> int:
+    """model/config.go:609-615: max(2*depth, 8) routed experts."""
+    return max(2 * depth, 8)
+
+
+def apply_latent_preset(cfg: Config, mla_latent: int = 0, n_experts: int = 0,
+                        experts_per_token: int = 0, expert_hidden: int = 0,
+                        shared_hidden: int = 0, moe_scale: float = 0.0,
+                        balance_weight: float = 0.0) -> Config:
+    """Config.ApplyPreset(PresetLatent) (model/preset.go:120-152) followed by
+    ApplyMoEDefaults (model/config.go:210-227), with the effective clamp,
+    scale and balance weight resolved (config.go:152-188).  Fields already
+    set by the caller are respected, as the preset does."""
+    if cfg.n_kv_head == cfg.n_head and cfg.n_head % 2 == 0:  # applyDefaultGroupedQuery
+        cfg.n_kv_head = cfg.n_head // 2
+    cfg.mla_latent = mla_latent if mla_latent > 0 else cfg.n_embd // 2
+    cfg.n_experts = n_experts if n_experts > 0 else moe_experts_for_depth(cfg.n_layer)
+    k = experts_per_token if experts_per_token > 0 else 2
+    cfg.experts_per_token = min(k, cfg.n_experts)
+    cfg.expert_hidden = expert_hidden if expert_hidden > 0 else cfg.n_embd
+    cfg.shared_hidden = shared_hidden if shared_hidden > 0 else cfg.expert_hidden
+    cfg.moe_clamp = DEFAULT_MOE_CLAMP
+    cfg.moe_scale = moe_scale if moe_scale > 0 else 1.0
+    if balance_weight < 0:
+        cfg.balance_weight = 0.0
+    else:
+        cfg.balance_weight = balance_weight if balance_weight > 0 else DEFAULT_MOE_BALANCE_WEIGHT
+    cfg.validate()
+    return cfg
+
+
+def latent_d12() -> Config:
+    """latent preset depth 12 (d_model 768, 6 query heads,
+    3 KV heads by the preset's grouped-query default), absorbed MLA with
+    latent 256 (one MLALatent serves both the query and the KV latent, so
+    BASELINE's separate q latent of 384 cannot be expressed), rope 64,
+    DeepSeekMoE 1 shared + 16 routed experts of hidden 512, top-2."""
+    cfg = config_for_depth_ratio(12, 65536, 64, 128, 512, "SSSL", 1)
+    return apply_latent_preset(cfg, mla_latent=256, n_experts=16, experts_per_token=2,
+                               expert_hidden=512)
+
+
 # ---------------------------------------------------------------------------
 # Weights with InitWeights' distributions (model/transformer.go:139-205).
 # Go's NormFloat64 stream and its map-ordered value-embedding init are not
@@ -170,10 +275,23 @@ def init_weights(cfg: Config, seed: int = 0, perturb: float = 0.0,
     put("lm_head.weight", rng.standard_normal(n("lm_head.weight")) * 0.001)
     for l in range(cfg.n_layer):
         p = f"transformer.h.{l}."
-        for k in ("attn.c_q.weight", "attn.c_k.weight", "attn.c_v.weight"):
+        if cfg.mla:
+            keys = ("attn.mla_q_down.weight", "attn.mla_q_up.weight", "attn.mla_q_rope.weight",
+                    "attn.mla_kv_down.weight", "attn.mla_k_up.weight", "attn.mla_v_up.weight",
+                    "attn.mla_k_rope.weight")
+        else:
+            keys = ("attn.c_q.weight", "attn.c_k.weight", "attn.c_v.weight")
+        for k in keys:
             put(p + k, rng.uniform(-bound, bound, n(p + k)))
         put(p + "mlp.c_fc.weight", rng.uniform(-0.4 * bound, 0.4 * bound, n(p + "mlp.c_fc.weight")))
-        # c_proj weights stay zero (transformer.go:162,167)
+        if cfg.moe:  # transformer.go:163-174
+            put(p + "mlp.c_gate.weight",
+                rng.uniform(-0.4 * bound, 0.4 * bound, n(p + "mlp.c_gate.weight")))
+            for k in ("moe.experts.gate.weight", "moe.experts.up.weight"):
+                put(p + k, rng.uniform(-0.4 * bound, 0.4 * bound, n(p + k)))
+            put(p + "moe.router.weight", rng.standard_normal(n(p + "moe.router.weight")) * 0.02)
+        # c_proj, expert down weights and the router bias stay zero
+        # (transformer.go:162,167,172-173)
     L1 = max(cfg.n_layer - 1, 1)
     put("resid_lambdas", [1.15 - 0.10 * l / L1 for l in range(cfg.n_layer)])
     put("x0_lambdas", [0.20 - 0.15 * l / L1 for l in range(cfg.n_layer)])

@@ -107,6 +107,16 @@ int orc_calculator(const char *expr, char *out, size_t out_cap);
 typedef struct {
   int32_t sequence_len, vocab_size, n_layer, n_head, n_kv_head, n_embd, rotary_dims;
   char window_pattern[16];
+  /* Latent preset (model/preset.go:122-129), resolved by the caller; zeros
+   * select the dense model.  mla_latent > 0 enables absorbed MLA
+   * (Config.MLALatent) with mla_rope_dims decoupled rotary dims
+   * (Config.MLARotaryDimension); n_experts > 0 enables the DeepSeekMoE
+   * feed-forward: a shared SwiGLU expert of shared_hidden plus n_experts
+   * routed experts of expert_hidden, experts_per_token selected
+   * (model/config.go:138-227). */
+  int32_t mla_latent, mla_rope_dims;
+  int32_t n_experts, experts_per_token, expert_hidden, shared_hidden;
+  float moe_clamp, moe_scale, balance_weight;
 } orc_config;
 
 /* Sorted-name parameter table (model/params.go:14-85). */
@@ -148,6 +158,10 @@ int64_t orc_param_total(const orc_config *cfg);
 
 ORC_MODEL_DECL(_f32, float)
 ORC_MODEL_DECL(_f64, double)
+/* Sequence-level MoE balance loss of the last training forward
+ * (model/train_transformer.go:121-123; 0 without MoE). */
+double orc_aux_loss_f32(const orc_model_f32 *m);
+double orc_aux_loss_f64(const orc_model_f64 *m);
 
 /* Window sizes (model/config.go:629-645): writes n_layer left widths. */
 void orc_window_sizes(const orc_config *cfg, int32_t *out);

@@ -55,14 +55,21 @@ static int padded_vocab(const orc_config *c) { /* model/config.go:622-624 */
 }
 static int rotary_dim(const orc_config *c) { /* model/config.go:430-444 */
   int hd = c->n_embd / c->n_head;
+  if (c->mla_latent > 0) return c->mla_rope_dims; /* MLARotaryDimension */
   return c->rotary_dims <= 0 ? hd : c->rotary_dims;
 }
+static int mlp_hidden(const orc_config *c) { /* model/block.go:23-28 */
+  return c->n_experts > 0 ? c->shared_hidden : 4 * c->n_embd;
+}
+#define TABLE_MAX (24 * MAXL)
 
 #if defined(ORC_DEFINE_SHARED)
 static int cmp_entry(const void *a, const void *b) {
   return strcmp(((const param_entry *)a)->name, ((const param_entry *)b)->name);
 }
-/* model/params.go:14-85 (dense preset), sorted as ParameterNames does. */
+/* model/params.go:14-85 (dense and latent presets), sorted as ParameterNames
+ * does.  Packed expert tensors [E, H, C] / [E, C, H] are listed as rows E*H
+ * (resp. E*C) by cols C (resp. H). */
 static int build_table(const orc_config *c, param_entry *t) {
   int n = 0, C = c->n_embd, D = C / c->n_head, PV = padded_vocab(c);
   int Hq = c->n_head, Hkv = c->n_kv_head, L = c->n_layer;
@@ -76,17 +83,38 @@ static int build_table(const orc_config *c, param_entry *t) {
   char nm[96];
   ADD("transformer.wte.weight", PV, C);
   ADD("lm_head.weight", PV, C);
+  const int mla = c->mla_latent > 0, F = mlp_hidden(c);
+  const int lat = c->mla_latent, rd = c->mla_rope_dims, cd = D - rd;
+  const int E = c->n_experts, EH = c->expert_hidden;
   for (int l = 0; l < L; l++) {
-    snprintf(nm, 96, "transformer.h.%d.attn.c_q.weight", l); ADD(nm, Hq * D, C);
-    snprintf(nm, 96, "transformer.h.%d.attn.c_k.weight", l); ADD(nm, Hkv * D, C);
-    snprintf(nm, 96, "transformer.h.%d.attn.c_v.weight", l); ADD(nm, Hkv * D, C);
+    if (mla) { /* params.go:19-27, mla.go:41-58 */
+      snprintf(nm, 96, "transformer.h.%d.attn.mla_q_down.weight", l); ADD(nm, lat, C);
+      snprintf(nm, 96, "transformer.h.%d.attn.mla_q_up.weight", l); ADD(nm, Hq * cd, lat);
+      snprintf(nm, 96, "transformer.h.%d.attn.mla_q_rope.weight", l); ADD(nm, Hq * rd, C);
+      snprintf(nm, 96, "transformer.h.%d.attn.mla_kv_down.weight", l); ADD(nm, lat, C);
+      snprintf(nm, 96, "transformer.h.%d.attn.mla_k_up.weight", l); ADD(nm, Hkv * cd, lat);
+      snprintf(nm, 96, "transformer.h.%d.attn.mla_v_up.weight", l); ADD(nm, Hkv * D, lat);
+      snprintf(nm, 96, "transformer.h.%d.attn.mla_k_rope.weight", l); ADD(nm, Hkv * rd, C);
+    } else {
+      snprintf(nm, 96, "transformer.h.%d.attn.c_q.weight", l); ADD(nm, Hq * D, C);
+      snprintf(nm, 96, "transformer.h.%d.attn.c_k.weight", l); ADD(nm, Hkv * D, C);
+      snprintf(nm, 96, "transformer.h.%d.attn.c_v.weight", l); ADD(nm, Hkv * D, C);
+    }
     snprintf(nm, 96, "transformer.h.%d.attn.c_proj.weight", l); ADD(nm, C, C);
-    if (has_value_embedding(l, L)) {
+    if (!mla && has_value_embedding(l, L)) { /* transformer.go:72-78: no VE under MLA */
       snprintf(nm, 96, "transformer.h.%d.attn.ve_gate.weight", l); ADD(nm, Hkv, VE_GATE_CH);
       snprintf(nm, 96, "value_embeds.%d.weight", l); ADD(nm, PV, Hkv * D);
     }
-    snprintf(nm, 96, "transformer.h.%d.mlp.c_fc.weight", l); ADD(nm, 4 * C, C);
-    snprintf(nm, 96, "transformer.h.%d.mlp.c_proj.weight", l); ADD(nm, C, 4 * C);
+    snprintf(nm, 96, "transformer.h.%d.mlp.c_fc.weight", l); ADD(nm, F, C);
+    if (E > 0) { snprintf(nm, 96, "transformer.h.%d.mlp.c_gate.weight", l); ADD(nm, F, C); }
+    snprintf(nm, 96, "transformer.h.%d.mlp.c_proj.weight", l); ADD(nm, C, F);
+    if (E > 0) { /* params.go:57-63, moe.go:49-69 */
+      snprintf(nm, 96, "transformer.h.%d.moe.router.weight", l); ADD(nm, E, C);
+      snprintf(nm, 96, "transformer.h.%d.moe.router_bias", l); ADD(nm, E, 1);
+      snprintf(nm, 96, "transformer.h.%d.moe.experts.gate.weight", l); ADD(nm, E * EH, C);
+      snprintf(nm, 96, "transformer.h.%d.moe.experts.up.weight", l); ADD(nm, E * EH, C);
+      snprintf(nm, 96, "transformer.h.%d.moe.experts.down.weight", l); ADD(nm, E * C, EH);
+    }
   }
   ADD("resid_lambdas", L, 1);
   ADD("x0_lambdas", L, 1);
@@ -103,12 +131,12 @@ static int build_table(const orc_config *c, param_entry *t) {
   return n;
 }
 int orc_param_count(const orc_config *c) {
-  param_entry t[16 * MAXL];
+  param_entry t[TABLE_MAX];
   return build_table(c, t);
 }
 int64_t orc_param_info(const orc_config *c, int index, char *name_out, int64_t *rows,
                        int64_t *cols) {
-  param_entry t[16 * MAXL];
+  param_entry t[TABLE_MAX];
   int n = build_table(c, t);
   if (index < 0 || index >= n) return -1;
   snprintf(name_out, 96, "%s", t[index].name);
@@ -117,7 +145,7 @@ int64_t orc_param_info(const orc_config *c, int index, char *name_out, int64_t *
   return t[index].rows * t[index].cols;
 }
 int64_t orc_param_total(const orc_config *c) {
-  param_entry t[16 * MAXL];
+  param_entry t[TABLE_MAX];
   int n = build_table(c, t);
   return t[n - 1].offset + t[n - 1].rows * t[n - 1].cols;
 }
@@ -163,12 +191,18 @@ static int64_t param_offset(const orc_config *c, const char *name) {
 /* ---------------------------------------------------------------------- */
 typedef struct {
   int64_t wq, wk, wv, wo, wve, wfc, wproj, ve;
+  /* latent preset: MLA projections, shared-expert gate, router, experts */
+  int64_t wqd, wqu, wqr, wkvd, wku, wvu, wkr, wgate, wr, rbias, eg, eu, ed;
   int has_ve, window;
 } layer_off;
 
 struct MODEL {
   orc_config cfg;
   int C, Hq, Hkv, D, R, F, L, V, PV, S, KVW;
+  /* latent preset: MLA latent width, rope/content widths, experts */
+  int mla, lat, rd, cd, E, K, EH;
+  REAL clamp, mscale, bw;
+  double aux_loss;
   int64_t total;
   REAL *p;
   int64_t wte, lm, rl, x0l, smg, sml, bkl;
@@ -184,7 +218,17 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
   m->Hkv = cfg->n_kv_head;
   m->D = m->C / m->Hq;
   m->R = rotary_dim(cfg);
-  m->F = 4 * m->C;
+  m->F = mlp_hidden(cfg);
+  m->mla = cfg->mla_latent > 0;
+  m->lat = cfg->mla_latent;
+  m->rd = cfg->mla_rope_dims;
+  m->cd = m->D - m->rd;
+  m->E = cfg->n_experts;
+  m->K = cfg->experts_per_token;
+  m->EH = cfg->expert_hidden;
+  m->clamp = R(cfg->moe_clamp);
+  m->mscale = R(cfg->moe_scale);
+  m->bw = R(cfg->balance_weight);
   m->L = cfg->n_layer;
   m->V = cfg->vocab_size;
   m->PV = padded_vocab(cfg);
@@ -208,13 +252,31 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
 #define OFF(field, fmt)                      \
   snprintf(nm, 96, fmt, l);                  \
   o->field = param_offset(cfg, nm);
-    OFF(wq, "transformer.h.%d.attn.c_q.weight");
-    OFF(wk, "transformer.h.%d.attn.c_k.weight");
-    OFF(wv, "transformer.h.%d.attn.c_v.weight");
+    if (m->mla) {
+      OFF(wqd, "transformer.h.%d.attn.mla_q_down.weight");
+      OFF(wqu, "transformer.h.%d.attn.mla_q_up.weight");
+      OFF(wqr, "transformer.h.%d.attn.mla_q_rope.weight");
+      OFF(wkvd, "transformer.h.%d.attn.mla_kv_down.weight");
+      OFF(wku, "transformer.h.%d.attn.mla_k_up.weight");
+      OFF(wvu, "transformer.h.%d.attn.mla_v_up.weight");
+      OFF(wkr, "transformer.h.%d.attn.mla_k_rope.weight");
+    } else {
+      OFF(wq, "transformer.h.%d.attn.c_q.weight");
+      OFF(wk, "transformer.h.%d.attn.c_k.weight");
+      OFF(wv, "transformer.h.%d.attn.c_v.weight");
+    }
     OFF(wo, "transformer.h.%d.attn.c_proj.weight");
     OFF(wfc, "transformer.h.%d.mlp.c_fc.weight");
     OFF(wproj, "transformer.h.%d.mlp.c_proj.weight");
-    o->has_ve = has_value_embedding(l, m->L);
+    if (m->E > 0) {
+      OFF(wgate, "transformer.h.%d.mlp.c_gate.weight");
+      OFF(wr, "transformer.h.%d.moe.router.weight");
+      OFF(rbias, "transformer.h.%d.moe.router_bias");
+      OFF(eg, "transformer.h.%d.moe.experts.gate.weight");
+      OFF(eu, "transformer.h.%d.moe.experts.up.weight");
+      OFF(ed, "transformer.h.%d.moe.experts.down.weight");
+    }
+    o->has_ve = !m->mla && has_value_embedding(l, m->L);
     if (o->has_ve) {
       OFF(wve, "transformer.h.%d.attn.ve_gate.weight");
       OFF(ve, "value_embeds.%d.weight");
@@ -312,8 +374,9 @@ static REAL sigmoidR(REAL x) { return R(1.0 / (1.0 + exp(-(double)x))); }
 
 /* model/rotary.go:43-75 on rows of [heads][D] at the given position; sign
  * -1 uses the negated sine table (model/train.go:14-20). */
-static void rope_row(MODEL *m, REAL *dst, const REAL *src, int heads, int pos, int sign) {
-  int D = m->D, half = m->R / 2, off = D - m->R;
+static void rope_rows_w(MODEL *m, REAL *dst, const REAL *src, int heads, int D, int pos,
+                        int sign) {
+  int half = m->R / 2, off = D - m->R;
   const REAL *cw = m->cosT + (int64_t)pos * half, *sw = m->sinT + (int64_t)pos * half;
   for (int h = 0; h < heads; h++) {
     const REAL *s = src + h * D;
@@ -328,6 +391,9 @@ static void rope_row(MODEL *m, REAL *dst, const REAL *src, int heads, int pos, i
     }
     for (int j = 0; j < off; j++) d[j] = tmp[j];
   }
+}
+static void rope_row(MODEL *m, REAL *dst, const REAL *src, int heads, int pos, int sign) {
+  rope_rows_w(m, dst, src, heads, m->D, pos, sign);
 }
 
 /* One (batch, head) attention with the reference mask; scores and
@@ -422,7 +488,9 @@ static REAL softcap(REAL y) {
 /* ---- KV cache (model/kvcache.go:10-140) -------------------------------- */
 typedef struct {
   int B, maxSeq, pos, has_prev;
-  REAL *k, *v;  /* [L][B][Hkv][maxSeq][D] */
+  REAL *k, *v;  /* [L][B][Hkv][maxSeq][D] (dense) */
+  REAL *lat;    /* [L][B][maxSeq][lat]      (MLA latent, kvcache.go:224-274) */
+  REAL *rk;     /* [L][B][maxSeq][Hkv*rd]   (MLA rotary key) */
   REAL *prev;   /* [B][C] */
 } kvcache;
 
@@ -430,15 +498,22 @@ static kvcache *cache_new(MODEL *m, int B, int maxSeq) {
   kvcache *c = (kvcache *)calloc(1, sizeof(kvcache));
   c->B = B;
   c->maxSeq = maxSeq;
-  size_t n = (size_t)m->L * B * m->Hkv * maxSeq * m->D;
-  c->k = (REAL *)calloc(n, sizeof(REAL));
-  c->v = (REAL *)calloc(n, sizeof(REAL));
+  if (m->mla) {
+    c->lat = (REAL *)calloc((size_t)m->L * B * maxSeq * m->lat, sizeof(REAL));
+    c->rk = (REAL *)calloc((size_t)m->L * B * maxSeq * m->Hkv * m->rd, sizeof(REAL));
+  } else {
+    size_t n = (size_t)m->L * B * m->Hkv * maxSeq * m->D;
+    c->k = (REAL *)calloc(n, sizeof(REAL));
+    c->v = (REAL *)calloc(n, sizeof(REAL));
+  }
   c->prev = (REAL *)calloc((size_t)B * m->C, sizeof(REAL));
   return c;
 }
 static void cache_free(kvcache *c) {
   free(c->k);
   free(c->v);
+  free(c->lat);
+  free(c->rk);
   free(c->prev);
   free(c);
 }
@@ -448,10 +523,21 @@ static REAL *cache_k(MODEL *m, kvcache *c, int l, int b, int h) {
 static REAL *cache_v(MODEL *m, kvcache *c, int l, int b, int h) {
   return c->v + ((((size_t)l * c->B + b) * m->Hkv + h) * c->maxSeq) * m->D;
 }
+static REAL *cache_lat(MODEL *m, kvcache *c, int l, int b) {
+  return c->lat + (((size_t)l * c->B + b) * c->maxSeq) * m->lat;
+}
+static REAL *cache_rk(MODEL *m, kvcache *c, int l, int b) {
+  return c->rk + (((size_t)l * c->B + b) * c->maxSeq) * m->Hkv * m->rd;
+}
 /* model/kvcache.go:383-448 (PrefillFrom) for a batch-1 source. */
 static void prefill_from(MODEL *m, kvcache *dst, kvcache *src) {
   int pos = src->pos;
-  for (int l = 0; l < m->L; l++)
+  for (int l = 0; l < m->L && m->mla; l++)
+    for (int b = 0; b < dst->B; b++) {
+      memcpy(cache_lat(m, dst, l, b), cache_lat(m, src, l, 0), sizeof(REAL) * pos * m->lat);
+      memcpy(cache_rk(m, dst, l, b), cache_rk(m, src, l, 0), sizeof(REAL) * pos * m->Hkv * m->rd);
+    }
+  for (int l = 0; l < m->L && !m->mla; l++)
     for (int b = 0; b < dst->B; b++)
       for (int h = 0; h < m->Hkv; h++) {
         memcpy(cache_k(m, dst, l, b, h), cache_k(m, src, l, 0, h), sizeof(REAL) * pos * m->D);
@@ -464,9 +550,376 @@ static void prefill_from(MODEL *m, kvcache *dst, kvcache *src) {
   }
 }
 
+/* ---- DeepSeekMoE routed experts (model/moe.go) ----------------------- */
+typedef struct moe_ctx {
+  int64_t rows, NK;
+  REAL *probs;       /* [rows][E] router softmax */
+  int64_t *counts;   /* [E] tokens per expert */
+  int64_t *offsets;  /* [E] first gathered row of each expert */
+  int64_t *grow;     /* [NK] gathered pair -> token row */
+  REAL *gw;          /* [NK] router probability of the pair */
+  REAL *xg, *gg, *ug, *hg, *yg; /* gathered input, gate, up, hidden, output */
+  double *bal_gp;    /* [rows][E] balance-loss gradient wrt probs, or NULL */
+  double bal_loss;
+} moe_ctx;
+
+static void moe_ctx_free(moe_ctx *c) {
+  if (!c) return;
+  free(c->probs); free(c->counts); free(c->offsets); free(c->grow); free(c->gw);
+  free(c->xg); free(c->gg); free(c->ug); free(c->hg); free(c->yg); free(c->bal_gp);
+  free(c);
+}
+
+/* kernels/scalar/elementwise.go:85-134 (clamped SwiGLU and its backward) */
+static REAL swiglu_value(REAL g, REAL u, REAL clamp, REAL *gm, REAL *um, REAL *sg_out) {
+  *gm = R(1);
+  *um = R(1);
+  if (clamp > 0 && g >= clamp) { g = clamp; *gm = R(0); }
+  if (clamp > 0) {
+    if (u > clamp) { u = clamp; *um = R(0); }
+    else if (u < -clamp) { u = -clamp; *um = R(0); }
+  }
+  REAL sg = R(1.0 / (1.0 + exp(-(double)g)));
+  if (sg_out) *sg_out = sg;
+  return g * sg * u;
+}
+static void swiglu_fwd(REAL *dst, const REAL *g, const REAL *u, REAL clamp, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    REAL gm, um;
+    dst[i] = swiglu_value(g[i], u[i], clamp, &gm, &um, NULL);
+  }
+}
+static void swiglu_bwd(REAL *dg, REAL *du, const REAL *g, const REAL *u, const REAL *dout,
+                       REAL clamp, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    REAL gm, um, sg;
+    REAL gv = g[i], uv = u[i];
+    swiglu_value(gv, uv, clamp, &gm, &um, &sg);
+    if (clamp > 0 && gv >= clamp) gv = clamp;
+    if (clamp > 0) uv = uv > clamp ? clamp : (uv < -clamp ? -clamp : uv);
+    REAL silu = gv * sg;
+    REAL sgrad = sg * (R(1) + gv * (R(1) - sg));
+    dg[i] = dout[i] * uv * sgrad * gm;
+    du[i] = dout[i] * silu * um;
+  }
+}
+
+/* GroupedMatMulTransposed for one expert's rows (kernels/scalar/moe.go:54-73,
+ * a running REAL sum in inner order). */
+static void expert_matmul(REAL *dst, const REAL *in, const REAL *W, int64_t rows, int cols,
+                          int inner) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; r++)
+    for (int c = 0; c < cols; c++) {
+      REAL t = 0;
+      const REAL *x = in + r * inner, *w = W + (int64_t)c * inner;
+      for (int i = 0; i < inner; i++) t += x[i] * w[i];
+      dst[r * cols + c] = t;
+    }
+}
+
+/* MoE.forward (model/moe.go:118-198) with MoEGateTopK (kernels/scalar/moe.go:
+ * 8-52) and sequenceBalance (moe.go:276-326).  out[rows][C] is overwritten
+ * with the routed contribution; seqlen > 0 (training) also computes the
+ * balance loss; ctx_out, when given, keeps the activations. */
+static void moe_forward(MODEL *m, const layer_off *lo, const REAL *x, int64_t rows, int seqlen,
+                        REAL *out, moe_ctx **ctx_out) {
+  const int C = m->C, E = m->E, K = m->K, EH = m->EH;
+  const REAL *P = m->p;
+  moe_ctx *c = (moe_ctx *)calloc(1, sizeof(moe_ctx));
+  c->rows = rows;
+  c->NK = rows * K;
+  REAL *logits = (REAL *)malloc(sizeof(REAL) * rows * E);
+  linear_fwd(logits, x, P + lo->wr, rows, C, E);
+  c->probs = (REAL *)malloc(sizeof(REAL) * rows * E);
+  int32_t *sel = (int32_t *)malloc(sizeof(int32_t) * rows * K);
+  for (int64_t r = 0; r < rows; r++) {
+    const REAL *lg = logits + r * E;
+    REAL *pr = c->probs + r * E;
+    REAL mx = lg[0]; /* SoftmaxLastDim (scalar/norm.go:7-23) */
+    for (int e = 1; e < E; e++)
+      if (lg[e] > mx) mx = lg[e];
+    double tot = 0;
+    for (int e = 0; e < E; e++) {
+      double ex = exp((double)(lg[e] - mx));
+      pr[e] = R(ex);
+      tot += ex;
+    }
+    REAL inv = R(1.0 / tot);
+    for (int e = 0; e < E; e++) pr[e] = pr[e] * inv;
+    REAL work[256]; /* TopKIndices on logits + bias, ties to the smaller index */
+    for (int e = 0; e < E; e++) work[e] = lg[e] + P[lo->rbias + e];
+    for (int k = 0; k < K; k++) {
+      int best = 0;
+      for (int e = 1; e < E; e++)
+        if (work[e] > work[best]) best = e;
+      sel[r * K + k] = best;
+      work[best] = R(-INFINITY);
+    }
+  }
+  free(logits);
+  c->counts = (int64_t *)calloc(E, sizeof(int64_t));
+  c->offsets = (int64_t *)calloc(E, sizeof(int64_t));
+  for (int64_t i = 0; i < rows * K; i++) c->counts[sel[i]]++;
+  for (int e = 1; e < E; e++) c->offsets[e] = c->offsets[e - 1] + c->counts[e - 1];
+  int64_t NK = c->NK, *fill = (int64_t *)calloc(E, sizeof(int64_t));
+  c->grow = (int64_t *)malloc(sizeof(int64_t) * NK);
+  c->gw = (REAL *)malloc(sizeof(REAL) * NK);
+  c->xg = (REAL *)malloc(sizeof(REAL) * NK * C);
+  for (int64_t r = 0; r < rows; r++)
+    for (int k = 0; k < K; k++) {
+      int e = sel[r * K + k];
+      int64_t pos = c->offsets[e] + fill[e]++;
+      memcpy(c->xg + pos * C, x + r * C, sizeof(REAL) * C);
+      c->grow[pos] = r;
+      c->gw[pos] = c->probs[r * E + e];
+    }
+  free(fill);
+  c->gg = (REAL *)malloc(sizeof(REAL) * NK * EH);
+  c->ug = (REAL *)malloc(sizeof(REAL) * NK * EH);
+  c->hg = (REAL *)malloc(sizeof(REAL) * NK * EH);
+  c->yg = (REAL *)malloc(sizeof(REAL) * NK * C);
+  for (int e = 0; e < E; e++) {
+    int64_t o = c->offsets[e], n = c->counts[e];
+    if (!n) continue;
+    expert_matmul(c->gg + o * EH, c->xg + o * C, P + lo->eg + (int64_t)e * EH * C, n, EH, C);
+    expert_matmul(c->ug + o * EH, c->xg + o * C, P + lo->eu + (int64_t)e * EH * C, n, EH, C);
+  }
+  swiglu_fwd(c->hg, c->gg, c->ug, m->clamp, NK * EH);
+  for (int e = 0; e < E; e++) {
+    int64_t o = c->offsets[e], n = c->counts[e];
+    if (!n) continue;
+    expert_matmul(c->yg + o * C, c->hg + o * EH, P + lo->ed + (int64_t)e * C * EH, n, C, EH);
+  }
+  memset(out, 0, sizeof(REAL) * rows * C);
+  for (int64_t i = 0; i < NK; i++) {
+    REAL w = c->gw[i] * m->mscale;
+    REAL *dst = out + c->grow[i] * C;
+    const REAL *y = c->yg + i * C;
+    for (int j = 0; j < C; j++) dst[j] += w * y[j];
+  }
+  /* sequenceBalance (moe.go:276-326) */
+  if (m->bw > 0 && seqlen > 0 && rows > 0 && rows % seqlen == 0) {
+    int64_t S = rows / seqlen;
+    double tc = (double)seqlen;
+    double *cnt = (double *)calloc((size_t)S * E, sizeof(double));
+    double *sum = (double *)calloc((size_t)S * E, sizeof(double));
+    for (int64_t i = 0; i < rows * K; i++) cnt[((i / K) / seqlen) * E + sel[i]] += 1.0;
+    for (int64_t r = 0; r < rows; r++)
+      for (int e = 0; e < E; e++) sum[(r / seqlen) * E + e] += (double)c->probs[r * E + e];
+    double ss = (double)E / ((double)K * tc), loss = 0;
+    for (int64_t sq = 0; sq < S; sq++)
+      for (int e = 0; e < E; e++) loss += ss * cnt[sq * E + e] * (sum[sq * E + e] / tc);
+    c->bal_loss = (double)m->bw * loss / (double)S;
+    double coef = (double)m->bw / ((double)S * tc);
+    c->bal_gp = (double *)malloc(sizeof(double) * rows * E);
+    for (int64_t r = 0; r < rows; r++)
+      for (int e = 0; e < E; e++) c->bal_gp[r * E + e] = coef * ss * cnt[(r / seqlen) * E + e];
+    free(cnt);
+    free(sum);
+  }
+  free(sel);
+  if (ctx_out) *ctx_out = c;
+  else moe_ctx_free(c);
+}
+
+/* MoE.backwardTraining (model/moe.go:203-267): gx[rows][C] is overwritten with
+ * the gradient wrt the MoE input; expert and router gradients accumulate. */
+static void moe_backward(MODEL *m, const layer_off *lo, const moe_ctx *c, const REAL *x,
+                         const REAL *gout, REAL *gx, REAL *G) {
+  const int C = m->C, E = m->E, EH = m->EH;
+  const int64_t rows = c->rows;
+  const REAL *P = m->p;
+  memset(gx, 0, sizeof(REAL) * rows * C);
+  double *gp = (double *)calloc((size_t)rows * E, sizeof(double));
+  for (int e = 0; e < E; e++) {
+    int64_t o = c->offsets[e], n = c->counts[e];
+    if (!n) continue;
+    REAL *gy = (REAL *)malloc(sizeof(REAL) * n * C);
+    for (int64_t i = 0; i < n; i++) {
+      int64_t row = c->grow[o + i];
+      REAL w = c->gw[o + i] * m->mscale;
+      double dot = 0;
+      for (int j = 0; j < C; j++) {
+        REAL g = gout[row * C + j];
+        gy[i * C + j] = g * w;
+        dot += (double)g * (double)c->yg[(o + i) * C + j];
+      }
+      gp[row * E + e] += dot * (double)m->mscale;
+    }
+    REAL *gh = (REAL *)malloc(sizeof(REAL) * n * EH);
+    linear_bwd(gh, G + lo->ed + (int64_t)e * C * EH, c->hg + o * EH, gy, P + lo->ed + (int64_t)e * C * EH,
+               n, EH, C);
+    REAL *dg = (REAL *)malloc(sizeof(REAL) * n * EH), *du = (REAL *)malloc(sizeof(REAL) * n * EH);
+    swiglu_bwd(dg, du, c->gg + o * EH, c->ug + o * EH, gh, m->clamp, n * EH);
+    REAL *fg = (REAL *)malloc(sizeof(REAL) * n * C), *fu = (REAL *)malloc(sizeof(REAL) * n * C);
+    linear_bwd(fg, G + lo->eg + (int64_t)e * EH * C, c->xg + o * C, dg, P + lo->eg + (int64_t)e * EH * C,
+               n, C, EH);
+    linear_bwd(fu, G + lo->eu + (int64_t)e * EH * C, c->xg + o * C, du, P + lo->eu + (int64_t)e * EH * C,
+               n, C, EH);
+    for (int64_t i = 0; i < n; i++) {
+      REAL *dst = gx + c->grow[o + i] * C;
+      for (int j = 0; j < C; j++) dst[j] += fg[i * C + j] + fu[i * C + j];
+    }
+    free(gy); free(gh); free(dg); free(du); free(fg); free(fu);
+  }
+  if (c->bal_gp)
+    for (int64_t i = 0; i < rows * E; i++) gp[i] += c->bal_gp[i];
+  REAL *gl = (REAL *)malloc(sizeof(REAL) * rows * E);
+  for (int64_t r = 0; r < rows; r++) {
+    double dot = 0;
+    for (int e = 0; e < E; e++) dot += (double)c->probs[r * E + e] * gp[r * E + e];
+    for (int e = 0; e < E; e++) {
+      double p = (double)c->probs[r * E + e];
+      gl[r * E + e] = R(p * (gp[r * E + e] - dot));
+    }
+  }
+  REAL *gr = (REAL *)malloc(sizeof(REAL) * rows * C);
+  linear_bwd(gr, G + lo->wr, x, gl, P + lo->wr, rows, C, E);
+  for (int64_t i = 0; i < rows * C; i++) gx[i] = gx[i] + gr[i];
+  free(gr); free(gl); free(gp);
+}
+
+/* ---- Multi-head latent attention (model/mla.go) ------------------------ */
+
+/* mlaProjectHeads (mla.go:106-122): q [N][Hq][D] = [QueryUp.QueryDown.h |
+ * QueryRope.h], k [N][Hkv][D] = [KeyUp.KVDown.h | KeyRope.h], v = ValueUp.
+ * KVDown.h; the query and key latents are returned for the backward. */
+static void mla_project(MODEL *m, const layer_off *lo, const REAL *h, int64_t N, REAL *q, REAL *k,
+                        REAL *v, REAL **ql_out, REAL **kvl_out) {
+  const int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, lat = m->lat, rd = m->rd, cd = m->cd;
+  const REAL *P = m->p;
+  REAL *ql = (REAL *)malloc(sizeof(REAL) * N * lat), *kvl = (REAL *)malloc(sizeof(REAL) * N * lat);
+  REAL *qc = (REAL *)malloc(sizeof(REAL) * N * Hq * cd), *qr = (REAL *)malloc(sizeof(REAL) * N * Hq * rd);
+  REAL *kc = (REAL *)malloc(sizeof(REAL) * N * Hkv * cd), *kr = (REAL *)malloc(sizeof(REAL) * N * Hkv * rd);
+  linear_fwd(ql, h, P + lo->wqd, N, C, lat);
+  linear_fwd(qc, ql, P + lo->wqu, N, lat, Hq * cd);
+  linear_fwd(qr, h, P + lo->wqr, N, C, Hq * rd);
+  linear_fwd(kvl, h, P + lo->wkvd, N, C, lat);
+  linear_fwd(kc, kvl, P + lo->wku, N, lat, Hkv * cd);
+  linear_fwd(kr, h, P + lo->wkr, N, C, Hkv * rd);
+  linear_fwd(v, kvl, P + lo->wvu, N, lat, Hkv * D);
+  for (int64_t n = 0; n < N; n++) { /* concatHeads (mla.go:150-160) */
+    for (int hh = 0; hh < Hq; hh++) {
+      memcpy(q + (n * Hq + hh) * D, qc + (n * Hq + hh) * cd, sizeof(REAL) * cd);
+      memcpy(q + (n * Hq + hh) * D + cd, qr + (n * Hq + hh) * rd, sizeof(REAL) * rd);
+    }
+    for (int hh = 0; hh < Hkv; hh++) {
+      memcpy(k + (n * Hkv + hh) * D, kc + (n * Hkv + hh) * cd, sizeof(REAL) * cd);
+      memcpy(k + (n * Hkv + hh) * D + cd, kr + (n * Hkv + hh) * rd, sizeof(REAL) * rd);
+    }
+  }
+  free(qc); free(qr); free(kc); free(kr);
+  *ql_out = ql;
+  *kvl_out = kvl;
+}
+
+/* mlaProjectBackward (mla.go:126-146) from the post-rotary-backward q/k
+ * gradients dq [N][Hq][D], dk [N][Hkv][D] and dv [N][Hkv][D]; dh is
+ * overwritten with the gradient wrt the attention input. */
+static void mla_project_backward(MODEL *m, const layer_off *lo, const REAL *h, const REAL *ql,
+                                 const REAL *kvl, const REAL *dq, const REAL *dk, const REAL *dv,
+                                 int64_t N, REAL *dh, REAL *G) {
+  const int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, lat = m->lat, rd = m->rd, cd = m->cd;
+  const REAL *P = m->p;
+  REAL *qc = (REAL *)malloc(sizeof(REAL) * N * Hq * cd), *qr = (REAL *)malloc(sizeof(REAL) * N * Hq * rd);
+  REAL *kc = (REAL *)malloc(sizeof(REAL) * N * Hkv * cd), *kr = (REAL *)malloc(sizeof(REAL) * N * Hkv * rd);
+  for (int64_t n = 0; n < N; n++) { /* splitHeads (mla.go:163-170) */
+    for (int hh = 0; hh < Hq; hh++) {
+      memcpy(qc + (n * Hq + hh) * cd, dq + (n * Hq + hh) * D, sizeof(REAL) * cd);
+      memcpy(qr + (n * Hq + hh) * rd, dq + (n * Hq + hh) * D + cd, sizeof(REAL) * rd);
+    }
+    for (int hh = 0; hh < Hkv; hh++) {
+      memcpy(kc + (n * Hkv + hh) * cd, dk + (n * Hkv + hh) * D, sizeof(REAL) * cd);
+      memcpy(kr + (n * Hkv + hh) * rd, dk + (n * Hkv + hh) * D + cd, sizeof(REAL) * rd);
+    }
+  }
+  REAL *dql = (REAL *)malloc(sizeof(REAL) * N * lat), *dkvl = (REAL *)malloc(sizeof(REAL) * N * lat);
+  REAL *t = (REAL *)malloc(sizeof(REAL) * N * (lat > C ? lat : C));
+  linear_bwd(dql, G + lo->wqu, ql, qc, P + lo->wqu, N, lat, Hq * cd);
+  linear_bwd(dh, G + lo->wqd, h, dql, P + lo->wqd, N, C, lat);
+  linear_bwd(t, G + lo->wqr, h, qr, P + lo->wqr, N, C, Hq * rd);
+  for (int64_t i = 0; i < N * C; i++) dh[i] = dh[i] + t[i];
+  linear_bwd(dkvl, G + lo->wku, kvl, kc, P + lo->wku, N, lat, Hkv * cd);
+  linear_bwd(t, G + lo->wvu, kvl, dv, P + lo->wvu, N, lat, Hkv * D);
+  for (int64_t i = 0; i < N * lat; i++) dkvl[i] = dkvl[i] + t[i];
+  linear_bwd(t, G + lo->wkvd, h, dkvl, P + lo->wkvd, N, C, lat);
+  for (int64_t i = 0; i < N * C; i++) dh[i] = dh[i] + t[i];
+  linear_bwd(t, G + lo->wkr, h, kr, P + lo->wkr, N, C, Hkv * rd);
+  for (int64_t i = 0; i < N * C; i++) dh[i] = dh[i] + t[i];
+  free(qc); free(qr); free(kc); free(kr); free(dql); free(dkvl); free(t);
+}
+
+/* mlaForwardInference (mla.go:185-279): absorbed attention against the
+ * latent cache for T new tokens at cache->pos; o [N][Hq][D] receives the
+ * per-head outputs before the output projection. */
+static void mla_decode_attention(MODEL *m, const layer_off *lo, int l, const REAL *h, int B, int T,
+                                 kvcache *cache, REAL *o) {
+  const int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, lat = m->lat, rd = m->rd, cd = m->cd;
+  const int64_t N = (int64_t)B * T;
+  const int hd = lat + rd, ratio = Hq / Hkv, offset = cache->pos, count = cache->pos + T;
+  const REAL *P = m->p;
+  REAL *ql = (REAL *)malloc(sizeof(REAL) * N * lat), *kvl = (REAL *)malloc(sizeof(REAL) * N * lat);
+  REAL *qc = (REAL *)malloc(sizeof(REAL) * N * Hq * cd), *qr = (REAL *)malloc(sizeof(REAL) * N * Hq * rd);
+  REAL *kr = (REAL *)malloc(sizeof(REAL) * N * Hkv * rd);
+  linear_fwd(ql, h, P + lo->wqd, N, C, lat);
+  linear_fwd(qc, ql, P + lo->wqu, N, lat, Hq * cd);
+  linear_fwd(qr, h, P + lo->wqr, N, C, Hq * rd);
+  linear_fwd(kvl, h, P + lo->wkvd, N, C, lat);
+  linear_fwd(kr, h, P + lo->wkr, N, C, Hkv * rd);
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++) {
+      int64_t n = (int64_t)b * T + t;
+      rope_rows_w(m, qr + n * Hq * rd, qr + n * Hq * rd, Hq, rd, offset + t, 1);
+      rope_rows_w(m, kr + n * Hkv * rd, kr + n * Hkv * rd, Hkv, rd, offset + t, 1);
+      memcpy(cache_lat(m, cache, l, b) + (int64_t)(offset + t) * lat, kvl + n * lat, sizeof(REAL) * lat);
+      memcpy(cache_rk(m, cache, l, b) + (int64_t)(offset + t) * Hkv * rd, kr + n * Hkv * rd,
+             sizeof(REAL) * Hkv * rd);
+    }
+  const REAL *ku = P + lo->wku, *vu = P + lo->wvu;
+#pragma omp parallel for schedule(dynamic)
+  for (int bh = 0; bh < B * Hq; bh++) {
+    int b = bh / Hq, hq = bh % Hq, hk = hq / ratio;
+    REAL *query = (REAL *)malloc(sizeof(REAL) * T * hd);
+    REAL *key = (REAL *)malloc(sizeof(REAL) * (int64_t)count * hd);
+    REAL *val = (REAL *)malloc(sizeof(REAL) * (int64_t)count * hd);
+    REAL *ao = (REAL *)malloc(sizeof(REAL) * T * hd);
+    REAL *lse = (REAL *)malloc(sizeof(REAL) * T);
+    for (int t = 0; t < T; t++) {
+      const REAL *qcr = qc + (((int64_t)b * T + t) * Hq + hq) * cd;
+      for (int rk = 0; rk < lat; rk++) {
+        REAL sum = 0; /* a running float32 sum, as mla.go:239-242 */
+        for (int ch = 0; ch < cd; ch++) sum += qcr[ch] * ku[(int64_t)(hk * cd + ch) * lat + rk];
+        query[t * hd + rk] = sum;
+      }
+      memcpy(query + t * hd + lat, qr + (((int64_t)b * T + t) * Hq + hq) * rd, sizeof(REAL) * rd);
+    }
+    const REAL *lc = cache_lat(m, cache, l, b), *rc = cache_rk(m, cache, l, b);
+    for (int j = 0; j < count; j++) {
+      memcpy(key + (int64_t)j * hd, lc + (int64_t)j * lat, sizeof(REAL) * lat);
+      memcpy(key + (int64_t)j * hd + lat, rc + (int64_t)j * Hkv * rd + hk * rd, sizeof(REAL) * rd);
+      memcpy(val + (int64_t)j * hd, lc + (int64_t)j * lat, sizeof(REAL) * lat);
+      memset(val + (int64_t)j * hd + lat, 0, sizeof(REAL) * rd);
+    }
+    attn_fwd(query, key, val, ao, lse, T, count, hd, offset, lo->window);
+    for (int t = 0; t < T; t++)
+      for (int d = 0; d < D; d++) {
+        REAL sum = 0; /* mla.go:266-273 */
+        for (int rk = 0; rk < lat; rk++) sum += ao[t * hd + rk] * vu[(int64_t)(hk * D + d) * lat + rk];
+        o[(((int64_t)b * T + t) * Hq + hq) * D + d] = sum;
+      }
+    free(query); free(key); free(val); free(ao); free(lse);
+  }
+  free(ql); free(kvl); free(qc); free(qr); free(kr);
+  (void)C;
+}
+
 /* ---- forward ---------------------------------------------------------- */
 typedef struct {
   REAL *xin, *xb, *h, *qrot, *krot, *qn, *kn, *vh, *lse, *o, *vesig, *ve, *mid, *h2, *u, *act;
+  /* latent preset: MLA latents, shared-expert gate, MoE routing and experts */
+  REAL *ql, *kvl, *g2;
+  struct moe_ctx *moe;
 } layer_ctx;
 
 typedef struct {
@@ -486,6 +939,8 @@ static void ctx_free(train_ctx *c, int L) {
     free(x->xin); free(x->xb); free(x->h); free(x->qrot); free(x->krot); free(x->qn);
     free(x->kn); free(x->vh); free(x->lse); free(x->o); free(x->vesig); free(x->ve);
     free(x->mid); free(x->h2); free(x->u); free(x->act);
+    free(x->ql); free(x->kvl); free(x->g2);
+    moe_ctx_free(x->moe);
   }
   free(c->backout); free(c->final_pre); free(c->final_norm); free(c->logits);
   free(c);
@@ -600,9 +1055,19 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
     /* attention on norm(x) */
     rmsnorm_rows(h, x, N, C);
     if (lc) lc->h = dup_arr(h, (size_t)N * C);
-    linear_fwd(q, h, P + lo->wq, N, C, Hq * D);
-    linear_fwd(k, h, P + lo->wk, N, C, Hkv * D);
-    linear_fwd(v, h, P + lo->wv, N, C, Hkv * D);
+    if (m->mla && cache) { /* absorbed MLA against the latent cache */
+      mla_decode_attention(m, lo, l, h, B, T, cache, o);
+      goto attn_out;
+    }
+    if (m->mla) {
+      REAL *ql, *kvl;
+      mla_project(m, lo, h, N, q, k, v, &ql, &kvl);
+      if (lc) { lc->ql = ql; lc->kvl = kvl; } else { free(ql); free(kvl); }
+    } else {
+      linear_fwd(q, h, P + lo->wq, N, C, Hq * D);
+      linear_fwd(k, h, P + lo->wk, N, C, Hkv * D);
+      linear_fwd(v, h, P + lo->wv, N, C, Hkv * D);
+    }
     if (lo->has_ve) { /* attention.go:245-250, 392-405 */
       for (int64_t n = 0; n < N; n++) memcpy(vev + n * Hkv * D, P + lo->ve + (int64_t)ids[n] * Hkv * D, sizeof(REAL) * Hkv * D);
       for (int64_t n = 0; n < N; n++)
@@ -623,11 +1088,16 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
         rope_row(m, q + n * Hq * D, q + n * Hq * D, Hq, offset + t, 1);
         rope_row(m, k + n * Hkv * D, k + n * Hkv * D, Hkv, offset + t, 1);
       }
-    if (lc) { lc->qrot = dup_arr(q, (size_t)N * Hq * D); lc->krot = dup_arr(k, (size_t)N * Hkv * D); }
-    rmsnorm_rows(qn, q, N * Hq, D);
-    rmsnorm_rows(kn, k, N * Hkv, D);
-    for (int64_t i = 0; i < N * Hq * D; i++) qn[i] *= R(QK_SCALE);
-    for (int64_t i = 0; i < N * Hkv * D; i++) kn[i] *= R(QK_SCALE);
+    if (m->mla) { /* no QK-norm under MLA (train.go:82-85) */
+      memcpy(qn, q, sizeof(REAL) * N * Hq * D);
+      memcpy(kn, k, sizeof(REAL) * N * Hkv * D);
+    } else {
+      if (lc) { lc->qrot = dup_arr(q, (size_t)N * Hq * D); lc->krot = dup_arr(k, (size_t)N * Hkv * D); }
+      rmsnorm_rows(qn, q, N * Hq, D);
+      rmsnorm_rows(kn, k, N * Hkv, D);
+      for (int64_t i = 0; i < N * Hq * D; i++) qn[i] *= R(QK_SCALE);
+      for (int64_t i = 0; i < N * Hkv * D; i++) kn[i] *= R(QK_SCALE);
+    }
     /* head-major copies and KV-cache write (attention.go:277-303) */
     REAL *qh = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
     REAL *oh = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
@@ -675,6 +1145,7 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
         for (int hh = 0; hh < Hq; hh++)
           memcpy(o + (((int64_t)b * T + t) * Hq + hh) * D, oh + (((int64_t)b * Hq + hh) * T + t) * D, sizeof(REAL) * D);
     free(oh);
+  attn_out:
     linear_fwd(a, o, P + lo->wo, N, Hq * D, C);
     for (int64_t i = 0; i < N * C; i++) x[i] = x[i] + a[i];
     if (lc) lc->mid = dup_arr(x, (size_t)N * C);
@@ -682,12 +1153,26 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
     rmsnorm_rows(h, x, N, C);
     if (lc) lc->h2 = dup_arr(h, (size_t)N * C);
     linear_fwd(u, h, P + lo->wfc, N, C, F);
-    for (int64_t i = 0; i < N * F; i++) {
-      REAL t = u[i] < 0 ? R(0) : u[i];
-      act[i] = t * t;
+    if (m->E > 0) { /* shared SwiGLU expert (mlp.go:62-76) + routed experts (block.go:40-45) */
+      REAL *g2 = (REAL *)malloc(sizeof(REAL) * N * F);
+      linear_fwd(g2, h, P + lo->wgate, N, C, F);
+      swiglu_fwd(act, g2, u, m->clamp, N * F);
+      if (lc) lc->g2 = g2; else free(g2);
+    } else {
+      for (int64_t i = 0; i < N * F; i++) {
+        REAL t = u[i] < 0 ? R(0) : u[i];
+        act[i] = t * t;
+      }
     }
     if (lc) { lc->u = dup_arr(u, (size_t)N * F); lc->act = dup_arr(act, (size_t)N * F); }
     linear_fwd(a, act, P + lo->wproj, N, F, C);
+    if (m->E > 0) {
+      REAL *mo = (REAL *)malloc(sizeof(REAL) * N * C);
+      moe_forward(m, lo, h, N, lc ? T : 0, mo, lc ? &lc->moe : NULL);
+      if (lc) m->aux_loss += lc->moe->bal_loss;
+      for (int64_t i = 0; i < N * C; i++) a[i] = a[i] + mo[i];
+      free(mo);
+    }
     for (int64_t i = 0; i < N * C; i++) x[i] = x[i] + a[i];
     if (l == bkidx) backout = dup_arr(x, (size_t)N * C);
   }
@@ -753,11 +1238,22 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
   /* MLP backward */
   REAL *dact = (REAL *)malloc(sizeof(REAL) * N * F);
   linear_bwd(dact, G + lo->wproj, lc->act, gout, P + lo->wproj, N, F, C);
-  for (int64_t i = 0; i < N * F; i++) dact[i] = lc->u[i] > 0 ? dact[i] * R(2) * lc->u[i] : R(0);
   REAL *dh = (REAL *)malloc(sizeof(REAL) * N * C);
-  linear_bwd(dh, G + lo->wfc, lc->h2, dact, P + lo->wfc, N, C, F);
-  free(dact);
   REAL *tmp = (REAL *)malloc(sizeof(REAL) * N * C);
+  if (m->E > 0) { /* train.go:505-511 (SwiGLU shared expert), then moe.go:203-267 */
+    REAL *dg = (REAL *)malloc(sizeof(REAL) * N * F), *du = (REAL *)malloc(sizeof(REAL) * N * F);
+    swiglu_bwd(dg, du, lc->g2, lc->u, dact, m->clamp, N * F);
+    linear_bwd(dh, G + lo->wgate, lc->h2, dg, P + lo->wgate, N, C, F);
+    linear_bwd(tmp, G + lo->wfc, lc->h2, du, P + lo->wfc, N, C, F);
+    for (int64_t i = 0; i < N * C; i++) dh[i] = dh[i] + tmp[i];
+    moe_backward(m, lo, lc->moe, lc->h2, gout, tmp, G);
+    for (int64_t i = 0; i < N * C; i++) dh[i] = dh[i] + tmp[i];
+    free(dg); free(du);
+  } else {
+    for (int64_t i = 0; i < N * F; i++) dact[i] = lc->u[i] > 0 ? dact[i] * R(2) * lc->u[i] : R(0);
+    linear_bwd(dh, G + lo->wfc, lc->h2, dact, P + lo->wfc, N, C, F);
+  }
+  free(dact);
   rmsnorm_backward_rows(tmp, lc->mid, dh, N, C);
   for (int64_t i = 0; i < N * C; i++) gmid[i] = gmid[i] + tmp[i];
   /* attention backward */
@@ -790,8 +1286,10 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
                  lo->window);
       }
   free(doh);
-  for (int64_t i = 0; i < N * Hq * D; i++) dqh[i] *= R(QK_SCALE);
-  for (int64_t i = 0; i < N * Hkv * D; i++) dkh[i] *= R(QK_SCALE);
+  if (!m->mla) { /* unscale QK (train.go:331-333); MLA has no QK norm */
+    for (int64_t i = 0; i < N * Hq * D; i++) dqh[i] *= R(QK_SCALE);
+    for (int64_t i = 0; i < N * Hkv * D; i++) dkh[i] *= R(QK_SCALE);
+  }
   REAL *dqs = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
   REAL *dks = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
   REAL *dvs = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
@@ -807,8 +1305,13 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
   free(dqh); free(dkh); free(dvh);
   REAL *dq = (REAL *)malloc(sizeof(REAL) * N * Hq * D);
   REAL *dk = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
-  rmsnorm_backward_rows(dq, lc->qrot, dqs, N * Hq, D);
-  rmsnorm_backward_rows(dk, lc->krot, dks, N * Hkv, D);
+  if (m->mla) {
+    memcpy(dq, dqs, sizeof(REAL) * N * Hq * D);
+    memcpy(dk, dks, sizeof(REAL) * N * Hkv * D);
+  } else {
+    rmsnorm_backward_rows(dq, lc->qrot, dqs, N * Hq, D);
+    rmsnorm_backward_rows(dk, lc->krot, dks, N * Hkv, D);
+  }
   for (int b = 0; b < B; b++)
     for (int t = 0; t < T; t++) {
       int64_t n = (int64_t)b * T + t;
@@ -816,11 +1319,16 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
       rope_row(m, dk + n * Hkv * D, dk + n * Hkv * D, Hkv, t, -1);
     }
   REAL *dhin = (REAL *)malloc(sizeof(REAL) * N * C);
-  linear_bwd(dhin, G + lo->wq, lc->h, dq, P + lo->wq, N, C, Hq * D);
-  linear_bwd(tmp, G + lo->wk, lc->h, dk, P + lo->wk, N, C, Hkv * D);
-  for (int64_t i = 0; i < N * C; i++) dhin[i] = dhin[i] + tmp[i];
-  linear_bwd(tmp, G + lo->wv, lc->h, dvs, P + lo->wv, N, C, Hkv * D);
-  for (int64_t i = 0; i < N * C; i++) dhin[i] = dhin[i] + tmp[i];
+  if (m->mla) { /* train.go:371-419: zero, then the MLA projection backward */
+    mla_project_backward(m, lo, lc->h, lc->ql, lc->kvl, dq, dk, dvs, N, tmp, G);
+    for (int64_t i = 0; i < N * C; i++) dhin[i] = R(0) + tmp[i];
+  } else {
+    linear_bwd(dhin, G + lo->wq, lc->h, dq, P + lo->wq, N, C, Hq * D);
+    linear_bwd(tmp, G + lo->wk, lc->h, dk, P + lo->wk, N, C, Hkv * D);
+    for (int64_t i = 0; i < N * C; i++) dhin[i] = dhin[i] + tmp[i];
+    linear_bwd(tmp, G + lo->wv, lc->h, dvs, P + lo->wv, N, C, Hkv * D);
+    for (int64_t i = 0; i < N * C; i++) dhin[i] = dhin[i] + tmp[i];
+  }
   free(dq); free(dk);
   if (lo->has_ve) { /* model/train.go:369-397 */
     REAL *dpre = (REAL *)malloc(sizeof(REAL) * N * Hkv);
@@ -961,6 +1469,7 @@ static train_ctx *train_forward(MODEL *m, const int32_t *ids, int B, int T) {
   ctx->ids = (int32_t *)malloc(sizeof(int32_t) * B * T);
   memcpy(ctx->ids, ids, sizeof(int32_t) * B * T);
   ctx->logits = (REAL *)malloc(sizeof(REAL) * (int64_t)B * T * m->V);
+  m->aux_loss = 0;
   forward_impl(m, ids, B, T, NULL, ctx->logits, ctx);
   return ctx;
 }
@@ -1201,3 +1710,5 @@ double FN(orc_rl_step)(MODEL *m, const int32_t *prompts, int G, int P, int S, in
   if (T < 1) return 0;
   return FN(orc_pg_step)(m, inputs_out, targets_out, Bt, T, adv_out, (float)maxLen, nll, grads);
 }
+
+double FN(orc_aux_loss)(const MODEL *m) { return m->aux_loss; }

@@ -37,6 +37,15 @@ class OrcConfig(C.Structure):
         ("n_embd", C.c_int32),
         ("rotary_dims", C.c_int32),
         ("window_pattern", C.c_char * 16),
+        ("mla_latent", C.c_int32),
+        ("mla_rope_dims", C.c_int32),
+        ("n_experts", C.c_int32),
+        ("experts_per_token", C.c_int32),
+        ("expert_hidden", C.c_int32),
+        ("shared_hidden", C.c_int32),
+        ("moe_clamp", C.c_float),
+        ("moe_scale", C.c_float),
+        ("balance_weight", C.c_float),
     ]
 
 
@@ -108,6 +117,8 @@ def lib():
         "orc_param_total": (C.c_int64, [C.POINTER(OrcConfig)]),
         "orc_window_sizes": (v, [C.POINTER(OrcConfig), _i32p]),
         "orc_num_threads": (C.c_int, []),
+        "orc_aux_loss_f32": (C.c_double, [C.c_void_p]),
+        "orc_aux_loss_f64": (C.c_double, [C.c_void_p]),
     }
     for sfx, fp in (("_f32", _f32p), ("_f64", _f64p)):
         sig.update({
@@ -151,11 +162,33 @@ class ModelShape:
     n_embd: int
     rotary_dims: int
     window_pattern: str
+    # latent preset, resolved (0 = dense): see gonano_amd.config.Config
+    mla_latent: int = 0
+    mla_rope_dims: int = 0
+    n_experts: int = 0
+    experts_per_token: int = 0
+    expert_hidden: int = 0
+    shared_hidden: int = 0
+    moe_clamp: float = 0.0
+    moe_scale: float = 0.0
+    balance_weight: float = 0.0
+
+    @classmethod
+    def from_config(cls, cfg) -> "ModelShape":
+        """The oracle's shape of a gonano_amd.config.Config."""
+        return cls(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head, cfg.n_kv_head,
+                   cfg.n_embd, cfg.rotary_dims, cfg.window_pattern, cfg.mla_latent,
+                   cfg.mla_rope_dimension if cfg.mla_latent > 0 else 0, cfg.n_experts,
+                   cfg.experts_per_token, cfg.expert_hidden, cfg.shared_hidden, cfg.moe_clamp,
+                   cfg.moe_scale, cfg.balance_weight)
 
     def orc(self) -> OrcConfig:
         return OrcConfig(self.sequence_len, self.vocab_size, self.n_layer, self.n_head,
                          self.n_kv_head, self.n_embd, self.rotary_dims,
-                         self.window_pattern.encode())
+                         self.window_pattern.encode(), self.mla_latent, self.mla_rope_dims,
+                         self.n_experts, self.experts_per_token, self.expert_hidden,
+                         self.shared_hidden, self.moe_clamp, self.moe_scale,
+                         self.balance_weight)
 
 
 def param_table(shape: ModelShape):
@@ -222,6 +255,10 @@ class OracleModel:
         grads = np.zeros(self.total, self.dtype)
         loss = self._fn("orc_pg_step")(self._m, inputs, targets, B, T, adv, float(norm), nll, grads)
         return loss, nll.reshape(B, T), grads
+
+    def aux_loss(self) -> float:
+        """MoE balance loss of the last training forward (pg_step / ce_loss)."""
+        return self._fn("orc_aux_loss")(self._m)
 
     def ce_loss(self, inputs, targets, want_grads=True):
         inputs = np.ascontiguousarray(inputs, np.int32)
