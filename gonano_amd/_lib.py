@@ -27,6 +27,15 @@ class GnConfig(C.Structure):
         ("n_embd", C.c_int32),
         ("rotary_dims", C.c_int32),
         ("window_pattern", C.c_char * 16),
+        ("mla_latent", C.c_int32),
+        ("mla_rope_dims", C.c_int32),
+        ("n_experts", C.c_int32),
+        ("experts_per_token", C.c_int32),
+        ("expert_hidden", C.c_int32),
+        ("shared_hidden", C.c_int32),
+        ("moe_clamp", C.c_float),
+        ("moe_scale", C.c_float),
+        ("balance_weight", C.c_float),
     ]
 
 
@@ -114,6 +123,7 @@ _SIGS = {
     "gn_session_set_timing": (C.c_int, [vp, C.c_int]),
     "gn_session_get_timing": (C.c_int, [vp, C.POINTER(GnTiming)]),
     "gn_session_synchronize": (C.c_int, [vp]),
+    "gn_session_aux_loss": (C.c_int, [vp, C.POINTER(C.c_double)]),
     "gn_session_set_decode_graph": (C.c_int, [vp, C.c_int]),
 }
 

@@ -24,6 +24,7 @@ SOURCES = [
     "gn_gemm.hip",
     "gn_model.hip",
     "gn_attention.hip",
+    "gn_latent.hip",
     "gn_sampler.hip",
     "gn_session.cpp",
     "gn_tools.cpp",

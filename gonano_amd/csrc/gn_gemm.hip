@@ -31,6 +31,12 @@ struct GemmParams {
   int epi;
   float alpha;
   float* part;  // split-K: [splits][M][N] partial sums
+  // Expert-grouped products (GEMM_GROUP_ROWS / GEMM_GROUP_K): goff[0..groups]
+  // are row offsets on the device; gstride is the per-group element offset
+  // of B (rows mode) or of C (K mode).
+  const int* goff;
+  int groups;
+  int64_t gstride;
 };
 
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, int row, int col, float v) {
@@ -222,8 +228,9 @@ __device__ __forceinline__ void tile_barrier() {
 // every tile (more waves per SIMD for small grids) and are added in LDS at
 // the end.  With p.splits > 1 each workgroup sums one K range into p.part
 // and gemm_reduce_kernel applies the epilogue.
-template <int BM, int BN, int WM, int WN, int WK, int S, bool FOLD, bool AK, bool BK, bool VEC>
-__global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p) {
+template <int BM, int BN, int WM, int WN, int WK, int S, bool FOLD, bool AK, bool BK, bool VEC,
+          int GRP>
+__global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p0) {
   constexpr int NT = 64 * WM * WN * WK;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int MI = TM / 16, NI = TN / 16;
@@ -241,10 +248,38 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
   const int wmn = wid % (WM * WN), wk = wid / (WM * WN);
   const int wm = wmn % WM, wn = wmn / WM;
   int tm, tn, split;
-  tile_coords(p, tm, tn, split);
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int kbeg = split * p.k_per_split;
-  const int kend = min(p.K, kbeg + p.k_per_split);
+  tile_coords(p0, tm, tn, split);
+  GemmParams p = p0;
+  int m0 = tm * BM, kbeg, kend;
+  const int n0 = tn * BN;
+  if constexpr (GRP == GEMM_GROUP_ROWS) {
+    // Rows grouped by expert: logical tile row tm walks each group's tiles
+    // in turn (the grid is sized for the worst case; spare tiles exit).
+    int base = 0, g = -1, mt = 0;
+    for (int e = 0; e < p.groups; e++) {
+      const int nt = (p.goff[e + 1] - p.goff[e] + BM - 1) / BM;
+      if (tm < base + nt) {
+        g = e;
+        mt = tm - base;
+        break;
+      }
+      base += nt;
+    }
+    if (g < 0) return;
+    m0 = p.goff[g] + mt * BM;
+    p.M = p.goff[g + 1];
+    p.B += g * p.gstride;
+    kbeg = 0;
+    kend = p.K;
+  } else if constexpr (GRP == GEMM_GROUP_K) {
+    // The reduction runs over one group's rows; group g owns C + g*gstride.
+    kbeg = p.goff[split];
+    kend = p.goff[split + 1];
+    p.C += split * p.gstride;
+  } else {
+    kbeg = split * p.k_per_split;
+    kend = min(p.K, kbeg + p.k_per_split);
+  }
   const int nkt = kend > kbeg ? (kend - kbeg + GK - 1) / GK : 0;
   const bool interior = VEC && m0 + BM <= p.M && n0 + BN <= p.N;
   const int nfull = interior ? (kend - kbeg) / GK : 0;
@@ -354,7 +389,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
             acc[i][j][r] += red[((((v - 1) * WM * WN + wmn) * MI + i) * NI + j) * 256 + r * 64 + lane];
   }
   // D of a 16x16 block: lane holds column (lane & 15), rows 4*(lane>>4)+r.
-  if (p.splits == 1) {
+  if (GRP != GEMM_GROUP_NONE || p.splits == 1) {
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
@@ -401,8 +436,9 @@ static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int spli
   q.splits = splits;
   dim3 grid(q.tiles_m * q.tiles_n * splits);
   dim3 block(64 * WM * WN * WK);
-#define GN_GEMM_LAUNCH(AK, BK, V) \
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, FOLD, AK, BK, V>), grid, block, 0, st, q)
+#define GN_GEMM_LAUNCH(AK, BK, V)                                                             \
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, FOLD, AK, BK, V, GEMM_GROUP_NONE>), \
+                     grid, block, 0, st, q)
   if (vec) {
     if (ak && bk) GN_GEMM_LAUNCH(true, true, true);
     else if (ak && !bk) GN_GEMM_LAUNCH(true, false, true);
@@ -412,6 +448,38 @@ static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int spli
     if (ak && bk) GN_GEMM_LAUNCH(true, true, false);
     else if (ak && !bk) GN_GEMM_LAUNCH(true, false, false);
     else if (!ak && bk) GN_GEMM_LAUNCH(false, true, false);
+    else GN_GEMM_LAUNCH(false, false, false);
+  }
+#undef GN_GEMM_LAUNCH
+  GN_HIP(hipGetLastError());
+}
+
+// Expert-grouped launches.  Rows mode: p.M is the total row count (the sum
+// over groups); the grid has one tile row per BM rows plus one per group
+// (each group's last tile may be partial).  K mode: one "split" per group.
+template <int BM, int BN, int WM, int WN, int WK, int S, bool FOLD, int GRP>
+static void launch_grouped(const GemmParams& p, bool ak, bool bk, bool vec, hipStream_t st) {
+  GemmParams q = p;
+  q.tiles_m = GRP == GEMM_GROUP_ROWS ? (int)ceil_div(p.M, BM) + p.groups : (int)ceil_div(p.M, BM);
+  q.tiles_n = (int)ceil_div(p.N, BN);
+  q.splits = GRP == GEMM_GROUP_K ? p.groups : 1;
+  q.k_per_split = p.K;
+  dim3 grid(q.tiles_m * q.tiles_n * q.splits);
+  dim3 block(64 * WM * WN * WK);
+#define GN_GEMM_LAUNCH(AK, BK, V) \
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, FOLD, AK, BK, V, GRP>), grid, block, 0, st, q)
+  if constexpr (GRP == GEMM_GROUP_ROWS) {
+    GN_CHECK(ak, "grouped gemm: rows mode needs a K-contiguous A");
+    if (vec) {
+      if (bk) GN_GEMM_LAUNCH(true, true, true);
+      else GN_GEMM_LAUNCH(true, false, true);
+    } else {
+      if (bk) GN_GEMM_LAUNCH(true, true, false);
+      else GN_GEMM_LAUNCH(true, false, false);
+    }
+  } else {
+    GN_CHECK(!ak && !bk, "grouped gemm: K mode needs M- and N-contiguous operands");
+    if (vec) GN_GEMM_LAUNCH(false, false, true);
     else GN_GEMM_LAUNCH(false, false, false);
   }
 #undef GN_GEMM_LAUNCH
@@ -429,7 +497,29 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   p.M = d.M; p.N = d.N; p.K = d.K;
   p.epi = d.epi;
   p.alpha = d.alpha;
-  const bool vec = aligned16(d.A) && aligned16(d.B) && d.lda % 4 == 0 && d.ldb % 4 == 0;
+  const bool vec = aligned16(d.A) && aligned16(d.B) && d.lda % 4 == 0 && d.ldb % 4 == 0 &&
+                   d.group_stride % 4 == 0;
+  if (d.group != GEMM_GROUP_NONE) {
+    GN_CHECK(d.group_off != nullptr && d.groups > 0, "grouped gemm: missing group offsets");
+    p.goff = d.group_off;
+    p.groups = d.groups;
+    p.gstride = d.group_stride;
+    p.splits = 1;
+    if (d.group == GEMM_GROUP_ROWS) {
+      // per-group tiles: large tiles once the average group fills them
+      if (d.M / d.groups >= 1024)
+        launch_grouped<128, 128, 2, 2, 1, 2, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig,
+                                                                     vec, st);
+      else
+        launch_grouped<64, 64, 2, 2, 2, 4, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig,
+                                                                   vec, st);
+    } else {
+      // K mode: a group's whole row range per workgroup, two-level summation
+      launch_grouped<128, 128, 2, 2, 1, 2, true, GEMM_GROUP_K>(p, d.a_kcontig, d.b_kcontig, vec,
+                                                               st);
+    }
+    return;
+  }
 
 
   // Tile choice: the 128x128 tile when it yields enough workgroups to cover

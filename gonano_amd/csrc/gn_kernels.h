@@ -68,6 +68,15 @@ enum GemmEpilogue {
   EPI_DRELU2 = 5      // C = acc * 2 * relu(aux)  (ReluSquared backward)
 };
 
+// Expert-grouped GEMM modes (the MoE feed-forward): rows of A and C, or the
+// reduction rows, are concatenated groups whose offsets live on the device,
+// so the launch shape does not depend on how tokens were routed.
+enum GemmGroup {
+  GEMM_GROUP_NONE = 0,
+  GEMM_GROUP_ROWS = 1,  // C[goff[g]:goff[g+1]] = A[same rows] . B_g^T, B_g = B + g*group_stride
+  GEMM_GROUP_K = 2      // C_g (= C + g*group_stride) op= sum over k in [goff[g], goff[g+1])
+};
+
 struct GemmDesc {
   int M = 0, N = 0, K = 0;
   const float* A = nullptr;
@@ -84,6 +93,10 @@ struct GemmDesc {
   int64_t ldaux = 0;
   float alpha = 1.f;
   int force_splits = 0;
+  int group = GEMM_GROUP_NONE;
+  const int* group_off = nullptr;  // device [groups + 1]
+  int groups = 0;
+  int64_t group_stride = 0;
 };
 
 void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);

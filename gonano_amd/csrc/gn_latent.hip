@@ -1,0 +1,740 @@
+// gn_latent.hip - kernels of the latent preset (model/preset.go:120-129):
+// multi-head latent attention (model/mla.go) and the DeepSeekMoE
+// feed-forward (model/moe.go, model/mlp.go's clamped SwiGLU shared expert).
+//
+// MLA.  Training and prefill run the non-absorbed form (mlaProjectHeads,
+// mla.go:106-122): q = [QueryUp.q_lat | rope(QueryRope.h)] and k = [KeyUp.
+// kv_lat | rope(KeyRope.h)] per head, v = ValueUp.kv_lat, then the flash
+// kernels with head dim 128 and no QK-norm.  Decode runs the absorbed form
+// (mlaForwardInference, mla.go:185-279) against a cache of one latent row
+// per token plus the rotary keys; the content key and value up-projections
+// are folded into the query and output projections once per weight upload
+// (W_qabs = KeyUp^T.QueryUp per head, W_comb = Wo.ValueUp per head), so a
+// decode step needs no per-head projection kernels.
+//
+// MoE.  Routing (softmax, top-k on logits + bias, expert-major placement in
+// (token, slot) order) is computed on the device; the expert products are
+// the GEMM's expert-grouped modes, so the launch shape never depends on the
+// routing and the decode step can be captured in a graph.
+#include "gn_model.h"
+
+namespace gn {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+static constexpr int HDIM = 128;
+
+// Rotation of one rotary pair (model/rotary.go:43-75): the first half gets
+// x1*cos + x2*sin, the second -x1*sin + x2*cos; sign -1 transposes it (the
+// negated sine table of model/train.go:14-20).
+__device__ __forceinline__ float rope_elem(const float* x, int j, int rd, const float* cosr,
+                                           const float* sinr, float sign) {
+  const int half = rd >> 1;
+  if (j < half) {
+    const float c = cosr[j], s = sign * sinr[j];
+    return x[j] * c + x[j + half] * s;
+  }
+  const int i = j - half;
+  const float c = cosr[i], s = sign * sinr[i];
+  return -x[i] * s + x[i + half] * c;
+}
+
+// ---------------------------------------------------------------------------
+// MLA, training / prefill: assemble q, k, v per token (one block per token).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mla_assemble_kernel(MlaAssembleArgs a) {
+  const int64_t n = blockIdx.x;
+  const int t = (int)(n % a.T), b = (int)(n / a.T);
+  const int pos = a.pos0 + t;
+  const int cd = HDIM - a.rd, half = a.rd >> 1;
+  const float* cosr = a.cosT + (int64_t)pos * half;
+  const float* sinr = a.sinT + (int64_t)pos * half;
+  const float* xa = a.xa + n * a.xw;
+  const float* qr = xa + 2 * a.lat;
+  const float* kr = qr + a.Hq * a.rd;
+  const int kvuw = a.Hkv * (cd + HDIM);
+  const float* kvu = a.kvu + n * kvuw;
+  for (int i = threadIdx.x; i < a.Hq * HDIM; i += blockDim.x) {
+    const int h = i / HDIM, d = i % HDIM;
+    a.q[n * a.Hq * HDIM + i] = d < cd ? a.qc[(n * a.Hq + h) * cd + d]
+                                      : rope_elem(qr + h * a.rd, d - cd, a.rd, cosr, sinr, 1.f);
+  }
+  for (int i = threadIdx.x; i < a.Hkv * HDIM; i += blockDim.x) {
+    const int h = i / HDIM, d = i % HDIM;
+    float kv;
+    if (d < cd) {
+      kv = kvu[h * cd + d];
+    } else {
+      kv = rope_elem(kr + h * a.rd, d - cd, a.rd, cosr, sinr, 1.f);
+      if (a.rk_cache)
+        a.rk_cache[((int64_t)b * a.maxSeq + pos) * a.Hkv * a.rd + h * a.rd + (d - cd)] = kv;
+    }
+    a.k[n * a.Hkv * HDIM + i] = kv;
+    a.v[n * a.Hkv * HDIM + i] = kvu[a.Hkv * cd + i];
+  }
+  if (a.lat_cache)
+    for (int i = threadIdx.x; i < a.lat; i += blockDim.x)
+      a.lat_cache[((int64_t)b * a.maxSeq + pos) * a.lat + i] = xa[a.lat + i];
+}
+
+void launch_mla_assemble(const MlaAssembleArgs& a, int64_t rows, hipStream_t st) {
+  GN_CHECK(a.rd > 0 && a.rd < HDIM && a.rd % 2 == 0, "mla: bad rotary width");
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(mla_assemble_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// MLA backward glue (model/train.go:414-419, mla.go:126-146): the flash
+// gradients dq, dk, dv -> the QueryUp input gradient dqc, the rotary parts of
+// dxa (transposed rotation) and dkvu = [dk content | dv].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mla_post_bwd_kernel(MlaPostBwdArgs a) {
+  const int64_t n = blockIdx.x;
+  const int pos = (int)(n % a.T);
+  const int cd = HDIM - a.rd, half = a.rd >> 1;
+  const float* cosr = a.cosT + (int64_t)pos * half;
+  const float* sinr = a.sinT + (int64_t)pos * half;
+  float* dxa = a.dxa + n * a.xw;
+  float* dqr = dxa + 2 * a.lat;
+  float* dkr = dqr + a.Hq * a.rd;
+  const int kvuw = a.Hkv * (cd + HDIM);
+  float* dkvu = a.dkvu + n * kvuw;
+  const float* dq = a.dq + n * a.Hq * HDIM;
+  const float* dk = a.dk + n * a.Hkv * HDIM;
+  for (int i = threadIdx.x; i < a.Hq * HDIM; i += blockDim.x) {
+    const int h = i / HDIM, d = i % HDIM;
+    if (d < cd) a.dqc[(n * a.Hq + h) * cd + d] = dq[i];
+    else dqr[h * a.rd + d - cd] = rope_elem(dq + h * HDIM + cd, d - cd, a.rd, cosr, sinr, -1.f);
+  }
+  for (int i = threadIdx.x; i < a.Hkv * HDIM; i += blockDim.x) {
+    const int h = i / HDIM, d = i % HDIM;
+    if (d < cd) dkvu[h * cd + d] = dk[i];
+    else dkr[h * a.rd + d - cd] = rope_elem(dk + h * HDIM + cd, d - cd, a.rd, cosr, sinr, -1.f);
+    dkvu[a.Hkv * cd + i] = a.dv[n * a.Hkv * HDIM + i];
+  }
+}
+
+void launch_mla_post_bwd(const MlaPostBwdArgs& a, int64_t rows, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(mla_post_bwd_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// MLA decode.  mla_decode_prep: rotate the new token's query/key rotary
+// parts and append (latent, rotary key) to the cache at the step position
+// (kvcache.go:224-274 AppendMLA*).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int decode_pos(const MlaDecodeArgs& a) {
+  return a.pos_dev ? *a.pos_dev : a.pos;
+}
+
+__global__ __launch_bounds__(256) void mla_decode_prep_kernel(MlaDecodeArgs a) {
+  const int row = blockIdx.x;
+  const int pos = decode_pos(a), half = a.rd >> 1;
+  const float* cosr = a.cosT + (int64_t)pos * half;
+  const float* sinr = a.sinT + (int64_t)pos * half;
+  const float* xa = a.xa + (int64_t)row * a.xw;
+  const float* qr = xa + 2 * a.lat;
+  const float* kr = qr + a.Hq * a.rd;
+  for (int i = threadIdx.x; i < a.Hq * a.rd; i += blockDim.x) {
+    const int h = i / a.rd, j = i % a.rd;
+    a.qrope[(int64_t)row * a.Hq * a.rd + i] = rope_elem(qr + h * a.rd, j, a.rd, cosr, sinr, 1.f);
+  }
+  float* rk = a.rk_cache + ((int64_t)row * a.maxSeq + pos) * a.Hkv * a.rd;
+  for (int i = threadIdx.x; i < a.Hkv * a.rd; i += blockDim.x) {
+    const int h = i / a.rd, j = i % a.rd;
+    rk[i] = rope_elem(kr + h * a.rd, j, a.rd, cosr, sinr, 1.f);
+  }
+  float* lc = a.lat_cache + ((int64_t)row * a.maxSeq + pos) * a.lat;
+  for (int i = threadIdx.x; i < a.lat; i += blockDim.x) lc[i] = xa[a.lat + i];
+}
+
+// Absorbed attention for one row and one split of its key range, all NH
+// query heads at once: score(h, j) = q_abs[h] . lat[j] + q_rope[h] .
+// rk[j][kv(h)], softmax over the keys, out[h] = sum_j p(h, j) lat[j] (the
+// value is [latent | 0], mla.go:249-259).  Each wave streams a contiguous
+// quarter of the split once, with an online softmax over chunks of 4 keys:
+// lane l holds latent float4 l and rotary-key float4 l of a key, partial
+// dot products are wave-reduced per head.  Waves are merged in LDS; a
+// split covering the whole range writes the normalized latent output,
+// otherwise (sum, max, total) for mla_decode_combine_kernel.
+static constexpr int MLA_KPS = 256;  // keys per split
+static constexpr int MLA_MAXLAT = 256;
+
+__host__ __device__ inline void mla_split(int kstart, int kend, int* kps, int* nsplit) {
+  const int n = kend - kstart;
+  const int ns = (n + MLA_KPS - 1) / MLA_KPS;
+  *kps = (n + ns - 1) / ns;
+  *nsplit = (n + *kps - 1) / *kps;
+}
+
+template <int NH>
+__global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) float wacc[4][NH][MLA_MAXLAT];
+  __shared__ float wm[4][NH], ws[4][NH];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int row = blockIdx.x, split = blockIdx.y;
+  const int pos = decode_pos(a);
+  const int kstart = max(0, pos - a.window), kend = pos + 1;
+  int kps, nsplit;
+  mla_split(kstart, kend, &kps, &nsplit);
+  if (split >= nsplit) return;  // graph launches size the grid for the longest range
+  const int ks = kstart + split * kps, ke = min(kend, ks + kps);
+  const int nk = ke - ks;
+  const int q4 = (nk + 3) / 4;
+  const int j0 = ks + wid * q4, j1 = min(ke, j0 + q4);
+  const int ratio = NH / a.Hkv;
+  const bool has_lat = lane * 4 < a.lat;
+  const bool has_rk = lane * 4 < a.Hkv * a.rd;
+  const int my_kv = (lane * 4) / a.rd;  // kv head of this lane's rotary float4
+
+  v4f ql[NH], qr[NH], acc[NH];
+  float m[NH], s[NH];
+  const float* qa = a.qabs + (int64_t)row * NH * a.lat;
+  const float* qp = a.qrope + (int64_t)row * NH * a.rd;
+#pragma unroll
+  for (int h = 0; h < NH; h++) {
+    ql[h] = has_lat ? *reinterpret_cast<const v4f*>(qa + h * a.lat + 4 * lane) : (v4f){0, 0, 0, 0};
+    qr[h] = (has_rk && h / ratio == my_kv)
+                ? *reinterpret_cast<const v4f*>(qp + h * a.rd + 4 * lane - my_kv * a.rd)
+                : (v4f){0, 0, 0, 0};
+    acc[h] = (v4f){0, 0, 0, 0};
+    m[h] = -INFINITY;
+    s[h] = 0.f;
+  }
+  const float* lbase = a.lat_cache + (int64_t)row * a.maxSeq * a.lat + 4 * lane;
+  const float* rbase = a.rk_cache + (int64_t)row * a.maxSeq * a.Hkv * a.rd + 4 * lane;
+  const int64_t lstride = a.lat, rstride = (int64_t)a.Hkv * a.rd;
+  constexpr int CH = 4;
+  for (int jb = j0; jb < j1; jb += CH) {
+    v4f L[CH], K[CH];
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      const int j = min(jb + u, j1 - 1);  // clamp: duplicates are not accumulated
+      L[u] = has_lat ? *reinterpret_cast<const v4f*>(lbase + j * lstride) : (v4f){0, 0, 0, 0};
+      K[u] = has_rk ? *reinterpret_cast<const v4f*>(rbase + j * rstride) : (v4f){0, 0, 0, 0};
+    }
+    float sc[CH][NH];
+#pragma unroll
+    for (int u = 0; u < CH; u++)
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        float t = ql[h][0] * L[u][0] + ql[h][1] * L[u][1] + ql[h][2] * L[u][2] + ql[h][3] * L[u][3];
+        t += qr[h][0] * K[u][0] + qr[h][1] * K[u][1] + qr[h][2] * K[u][2] + qr[h][3] * K[u][3];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+        sc[u][h] = jb + u < j1 ? t : -INFINITY;
+      }
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      float mn = m[h];
+#pragma unroll
+      for (int u = 0; u < CH; u++) mn = fmaxf(mn, sc[u][h]);
+      const float f = expf(m[h] - mn);  // m = -inf on the first chunk: f = 0
+      s[h] *= f;
+      acc[h] *= f;
+#pragma unroll
+      for (int u = 0; u < CH; u++) {
+        const float p = expf(sc[u][h] - mn);
+        s[h] += p;
+        acc[h] += p * L[u];
+      }
+      m[h] = mn;
+    }
+  }
+  // merge the waves
+#pragma unroll
+  for (int h = 0; h < NH; h++) {
+    if (has_lat) *reinterpret_cast<v4f*>(&wacc[wid][h][4 * lane]) = acc[h];
+    if (lane == 0) {
+      wm[wid][h] = m[h];
+      ws[wid][h] = s[h];
+    }
+  }
+  __syncthreads();
+  const bool whole = nsplit == 1;
+  for (int i = tid; i < NH * a.lat; i += 256) {
+    const int h = i / a.lat, d = i % a.lat;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][h]);
+    float o = 0.f, tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      if (wm[w][h] == -INFINITY) continue;  // a wave without keys
+      const float f = expf(wm[w][h] - M);
+      o += wacc[w][h][d] * f;
+      tot += ws[w][h] * f;
+    }
+    if (whole) {
+      a.out[((int64_t)row * NH + h) * a.lat + d] = o / tot;
+    } else {
+      float* part = a.part + (((int64_t)row * a.nsplit_max + split) * NH + h) * (a.lat + 2);
+      part[d] = o;
+      if (d == 0) {
+        part[a.lat] = M;
+        part[a.lat + 1] = tot;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaDecodeArgs a) {
+  const int pos = decode_pos(a);
+  int kps, nsplit;
+  mla_split(max(0, pos - a.window), pos + 1, &kps, &nsplit);
+  if (nsplit == 1) return;  // the attention kernel wrote the output
+  const int rh = blockIdx.x;  // row * Hq + h
+  const int row = rh / a.Hq, h = rh % a.Hq;
+  const int64_t stride = (int64_t)a.Hq * (a.lat + 2);
+  const float* base = a.part + ((int64_t)row * a.nsplit_max * a.Hq + h) * (a.lat + 2);
+  float M = -INFINITY;
+  for (int sp = 0; sp < nsplit; sp++) M = fmaxf(M, base[sp * stride + a.lat]);
+  for (int d = threadIdx.x; d < a.lat; d += blockDim.x) {
+    float tot = 0.f, o = 0.f;
+    for (int sp = 0; sp < nsplit; sp++) {
+      const float f = expf(base[sp * stride + a.lat] - M);
+      tot += base[sp * stride + a.lat + 1] * f;
+      o += base[sp * stride + d] * f;
+    }
+    a.out[(int64_t)rh * a.lat + d] = o / tot;
+  }
+}
+
+void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
+  GN_CHECK(a.lat % 4 == 0 && a.lat <= MLA_MAXLAT, "mla decode: latent width must be a multiple "
+                                                  "of 4 and at most 256");
+  GN_CHECK(a.rd % 4 == 0 && a.Hkv * a.rd <= 256, "mla decode: rotary keys too wide");
+  GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq <= 8, "mla decode: at most 8 query heads");
+  GN_CHECK(a.window >= 0, "mla decode: bad window");
+  const int pos_max = a.pos_dev ? a.maxSeq - 1 : a.pos;
+  int kps, ns_max;
+  // the longest key range a step of this launch can have
+  mla_split(0, std::min(a.window, pos_max) + 1, &kps, &ns_max);
+  a.nsplit_max = ns_max;
+  hipLaunchKernelGGL(mla_decode_prep_kernel, dim3(a.rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+  const dim3 grid(a.rows, ns_max);
+  switch (a.Hq) {
+    case 1: hipLaunchKernelGGL(mla_decode_attn_kernel<1>, grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(mla_decode_attn_kernel<2>, grid, dim3(256), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(mla_decode_attn_kernel<3>, grid, dim3(256), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(mla_decode_attn_kernel<4>, grid, dim3(256), 0, st, a); break;
+    case 5: hipLaunchKernelGGL(mla_decode_attn_kernel<5>, grid, dim3(256), 0, st, a); break;
+    case 6: hipLaunchKernelGGL(mla_decode_attn_kernel<6>, grid, dim3(256), 0, st, a); break;
+    case 7: hipLaunchKernelGGL(mla_decode_attn_kernel<7>, grid, dim3(256), 0, st, a); break;
+    case 8: hipLaunchKernelGGL(mla_decode_attn_kernel<8>, grid, dim3(256), 0, st, a); break;
+  }
+  GN_HIP(hipGetLastError());
+  if (ns_max > 1) {
+    hipLaunchKernelGGL(mla_decode_combine_kernel, dim3(a.rows * a.Hq), dim3(256), 0, st, a);
+    GN_HIP(hipGetLastError());
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Clamped SwiGLU over [gate | up] rows (kernels/scalar/elementwise.go:85-134):
+// act[r][j] = silu(min(g, c)) * clamp(u, -c, c), sigmoid in float64.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void swiglu_eval(float g, float u, float c, float* out, float* dg,
+                                            float* du, float dout) {
+  float gm = 1.f, um = 1.f;
+  if (c > 0.f && g >= c) { g = c; gm = 0.f; }
+  if (c > 0.f) {
+    if (u > c) { u = c; um = 0.f; }
+    else if (u < -c) { u = -c; um = 0.f; }
+  }
+  const float sg = (float)(1.0 / (1.0 + exp(-(double)g)));
+  const float silu = g * sg;
+  if (out) *out = silu * u;
+  if (dg) {
+    const float sgrad = sg * (1.f + g * (1.f - sg));
+    *dg = dout * u * sgrad * gm;
+    *du = dout * silu * um;
+  }
+}
+
+__global__ void swiglu_rows_kernel(const float* __restrict__ gu, int F, int64_t rows, float clamp,
+                                   float* __restrict__ act) {
+  const int64_t n = rows * F;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / F, j = i % F;
+    float o;
+    swiglu_eval(gu[r * 2 * F + j], gu[r * 2 * F + F + j], clamp, &o, nullptr, nullptr, 0.f);
+    act[i] = o;
+  }
+}
+
+__global__ void swiglu_rows_bwd_kernel(const float* __restrict__ gu, const float* __restrict__ dact,
+                                       int F, int64_t rows, float clamp, float* __restrict__ dgu) {
+  const int64_t n = rows * F;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / F, j = i % F;
+    float dg, du;
+    swiglu_eval(gu[r * 2 * F + j], gu[r * 2 * F + F + j], clamp, nullptr, &dg, &du, dact[i]);
+    dgu[r * 2 * F + j] = dg;
+    dgu[r * 2 * F + F + j] = du;
+  }
+}
+
+static unsigned grid_for(int64_t n) {
+  return (unsigned)std::min<int64_t>(std::max<int64_t>(ceil_div(n, 256), 1), 16384);
+}
+
+void launch_swiglu_rows(const float* gu, int F, int64_t rows, float clamp, float* act,
+                        hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(swiglu_rows_kernel, dim3(grid_for(rows * F)), dim3(256), 0, st, gu, F, rows,
+                     clamp, act);
+  GN_HIP(hipGetLastError());
+}
+void launch_swiglu_rows_bwd(const float* gu, const float* dact, int F, int64_t rows, float clamp,
+                            float* dgu, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(swiglu_rows_bwd_kernel, dim3(grid_for(rows * F)), dim3(256), 0, st, gu, dact,
+                     F, rows, clamp, dgu);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// MoE routing (moe.go:123-153, kernels/scalar/moe.go:8-52).
+// ---------------------------------------------------------------------------
+static constexpr int MOE_MAXE = 64;
+static constexpr int MOE_MAXK = 8;
+static constexpr int MOE_PB = 256;  // (token, slot) pairs per placement block
+
+// One thread per token: SoftmaxLastDim of the router logits (float64 total,
+// p = float32(exp) * float32(1/total)), top-k of logits + bias (largest first,
+// ties to the smaller index), weights = probs of the chosen experts.
+__global__ void moe_gate_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
+                                int64_t rows, int E, int K, float* __restrict__ probs,
+                                int32_t* __restrict__ sel, float* __restrict__ w) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* lg = logits + r * E;
+  float mx = lg[0];
+  for (int e = 1; e < E; e++) mx = lg[e] > mx ? lg[e] : mx;
+  double tot = 0.0;
+  float pr[MOE_MAXE], work[MOE_MAXE];
+  for (int e = 0; e < E; e++) {
+    const double x = exp((double)(lg[e] - mx));
+    pr[e] = (float)x;
+    tot += x;
+    work[e] = lg[e] + bias[e];
+  }
+  const float inv = (float)(1.0 / tot);
+  for (int e = 0; e < E; e++) {
+    pr[e] = pr[e] * inv;
+    probs[r * E + e] = pr[e];
+  }
+  for (int k = 0; k < K; k++) {
+    int best = 0;
+    for (int e = 1; e < E; e++)
+      if (work[e] > work[best]) best = e;
+    sel[r * K + k] = best;
+    w[r * K + k] = pr[best];
+    work[best] = -INFINITY;
+  }
+}
+
+// Rank of each pair among the pairs of its block that chose the same expert,
+// in pair order, and the block's per-expert counts (wave ballots).
+__device__ __forceinline__ int block_rank(int e_mine, bool valid, int E, int* cnt_lds,
+                                          int (*wcnt)[MOE_MAXE]) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;
+  int rank = 0;
+  for (int e = 0; e < E; e++) {
+    const uint64_t mask = __ballot(valid && e_mine == e);
+    if (e == e_mine) rank = __popcll(mask & lt);
+    if (lane == 0) wcnt[wid][e] = __popcll(mask);
+  }
+  __syncthreads();
+  if (valid)
+    for (int w = 0; w < wid; w++) rank += wcnt[w][e_mine];
+  if (tid < E) cnt_lds[tid] = wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+  __syncthreads();
+  return rank;
+}
+
+__global__ __launch_bounds__(MOE_PB) void moe_count_kernel(const int32_t* __restrict__ sel,
+                                                           int64_t npairs, int E,
+                                                           int* __restrict__ blockcnt) {
+  __shared__ int wcnt[4][MOE_MAXE];
+  __shared__ int cnt[MOE_MAXE];
+  const int64_t p = (int64_t)blockIdx.x * MOE_PB + threadIdx.x;
+  const bool valid = p < npairs;
+  block_rank(valid ? sel[p] : -1, valid, E, cnt, wcnt);
+  if (threadIdx.x < E) blockcnt[(int64_t)blockIdx.x * E + threadIdx.x] = cnt[threadIdx.x];
+}
+
+// One block: per-expert exclusive scans over the blocks, expert totals and
+// offsets (off[E] = the pair count).
+__global__ void moe_scan_kernel(int* __restrict__ blockcnt, int nblk, int E,
+                                int* __restrict__ off) {
+  __shared__ int tot[MOE_MAXE];
+  const int e = threadIdx.x;
+  if (e < E) {
+    int run = 0;
+    for (int b = 0; b < nblk; b++) {
+      const int c = blockcnt[(int64_t)b * E + e];
+      blockcnt[(int64_t)b * E + e] = run;
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  if (e == 0) {
+    int run = 0;
+    for (int x = 0; x < E; x++) {
+      off[x] = run;
+      run += tot[x];
+    }
+    off[E] = run;
+  }
+}
+
+// Expert-major placement in (token, slot) order (moe.go:139-153): the pair
+// row, weight and position, then the gathered input rows.
+__global__ __launch_bounds__(MOE_PB) void moe_place_kernel(MoePlaceArgs a) {
+  __shared__ int wcnt[4][MOE_MAXE];
+  __shared__ int cnt[MOE_MAXE];
+  __shared__ int spos[MOE_PB];
+  __shared__ int srow[MOE_PB];
+  const int64_t p = (int64_t)blockIdx.x * MOE_PB + threadIdx.x;
+  const bool valid = p < a.npairs;
+  const int e = valid ? a.sel[p] : -1;
+  const int rank = block_rank(e, valid, a.E, cnt, wcnt);
+  int pos = -1;
+  if (valid) {
+    pos = a.off[e] + a.blockoff[(int64_t)blockIdx.x * a.E + e] + rank;
+    a.perm_row[pos] = (int)(p / a.K);
+    a.perm_w[pos] = a.w[p];
+    a.inv[p] = pos;
+  }
+  spos[threadIdx.x] = pos;
+  srow[threadIdx.x] = valid ? (int)(p / a.K) : -1;
+  __syncthreads();
+  // gather: each wave copies 64 pairs' rows, float4 per lane
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int c4 = a.C / 4;
+  for (int i = wid * 64; i < wid * 64 + 64; i++) {
+    if (srow[i] < 0) break;
+    const v4f* src = reinterpret_cast<const v4f*>(a.x + (int64_t)srow[i] * a.C);
+    v4f* dst = reinterpret_cast<v4f*>(a.xg + (int64_t)spos[i] * a.C);
+    for (int c = lane; c < c4; c += 64) dst[c] = src[c];
+  }
+}
+
+void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
+  GN_CHECK(a.E <= MOE_MAXE && a.K <= MOE_MAXK && a.K <= a.E, "moe: at most 64 experts, top-8");
+  GN_CHECK(a.C % 4 == 0, "moe: model width must be a multiple of 4");
+  const int64_t npairs = a.rows * a.K;
+  if (a.rows <= 0) return;
+  hipLaunchKernelGGL(moe_gate_kernel, dim3((unsigned)ceil_div(a.rows, 256)), dim3(256), 0, st,
+                     a.logits, a.bias, a.rows, a.E, a.K, a.probs, a.sel, a.w);
+  GN_HIP(hipGetLastError());
+  const int nblk = (int)ceil_div(npairs, MOE_PB);
+  hipLaunchKernelGGL(moe_count_kernel, dim3(nblk), dim3(MOE_PB), 0, st, a.sel, npairs, a.E,
+                     a.blockcnt);
+  GN_HIP(hipGetLastError());
+  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(64), 0, st, a.blockcnt, nblk, a.E, a.off);
+  GN_HIP(hipGetLastError());
+  MoePlaceArgs pa{};
+  pa.sel = a.sel; pa.w = a.w; pa.x = a.x; pa.off = a.off; pa.blockoff = a.blockcnt;
+  pa.npairs = npairs; pa.K = a.K; pa.E = a.E; pa.C = a.C;
+  pa.perm_row = a.perm_row; pa.perm_w = a.perm_w; pa.inv = a.inv; pa.xg = a.xg;
+  hipLaunchKernelGGL(moe_place_kernel, dim3(nblk), dim3(MOE_PB), 0, st, pa);
+  GN_HIP(hipGetLastError());
+}
+
+// The K pairs of a token ordered by expert id: the reference scatters in
+// expert-major order (moe.go:161-169, 233-239).
+__device__ __forceinline__ int sorted_pairs(const int32_t* sel, const int* inv, int64_t r, int K,
+                                            int* pos) {
+  int es[MOE_MAXK];
+  for (int k = 0; k < K; k++) {
+    es[k] = sel[r * K + k];
+    pos[k] = inv[r * K + k];
+  }
+  for (int i = 1; i < K; i++)
+    for (int j = i; j > 0 && es[j] < es[j - 1]; j--) {
+      int t = es[j]; es[j] = es[j - 1]; es[j - 1] = t;
+      t = pos[j]; pos[j] = pos[j - 1]; pos[j - 1] = t;
+    }
+  return K;
+}
+
+// x_next = mid + (shared + routed), routed = sum over the token's pairs in
+// expert order of (w * scale) * y (block.go:40-45, moe.go:161-169).
+__global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
+  const int64_t r = blockIdx.x;
+  int pos[MOE_MAXK];
+  sorted_pairs(a.sel, a.inv, r, a.K, pos);
+  float wk[MOE_MAXK];
+  for (int k = 0; k < a.K; k++) wk[k] = a.perm_w[pos[k]] * a.scale;
+  for (int c = threadIdx.x; c < a.C; c += blockDim.x) {
+    float moe = 0.f;
+    for (int k = 0; k < a.K; k++) moe += wk[k] * a.yg[(int64_t)pos[k] * a.C + c];
+    a.out[r * a.C + c] = a.mid[r * a.C + c] + (a.shared[r * a.C + c] + moe);
+  }
+}
+
+void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// MoE backward (moe.go:203-267).
+// ---------------------------------------------------------------------------
+// Per pair (one wave): gy = g[row] * (w * scale) and the probability
+// gradient term <g[row], y> * scale in float64.
+__global__ __launch_bounds__(256) void moe_bwd_prep_kernel(const float* __restrict__ g,
+                                                           const float* __restrict__ yg,
+                                                           const int* __restrict__ perm_row,
+                                                           const float* __restrict__ perm_w,
+                                                           float scale, int64_t npairs, int C,
+                                                           float* __restrict__ gy,
+                                                           double* __restrict__ dotp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t pidx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pidx >= npairs) return;
+  const int64_t row = perm_row[pidx];
+  const float w = perm_w[pidx] * scale;
+  double d = 0.0;
+  for (int c = lane; c < C; c += 64) {
+    const float gv = g[row * C + c];
+    gy[pidx * C + c] = gv * w;
+    d += (double)gv * (double)yg[pidx * C + c];
+  }
+  d = warp_sum_d(d);
+  if (lane == 0) dotp[pidx] = d * (double)scale;
+}
+
+void launch_moe_bwd_prep(const float* g, const float* yg, const int* perm_row, const float* perm_w,
+                         float scale, int64_t npairs, int C, float* gy, double* dotp,
+                         hipStream_t st) {
+  if (npairs <= 0) return;
+  hipLaunchKernelGGL(moe_bwd_prep_kernel, dim3((unsigned)ceil_div(npairs, 4)), dim3(256), 0, st, g,
+                     yg, perm_row, perm_w, scale, npairs, C, gy, dotp);
+  GN_HIP(hipGetLastError());
+}
+
+// Sequence-level balance loss (moe.go:276-326): per sequence, the selection
+// counts and probability sums per expert; loss_seq = sum_e ss * count *
+// sum / T with ss = E / (K T).  One block per sequence.
+__global__ __launch_bounds__(256) void moe_balance_kernel(const float* __restrict__ probs,
+                                                          const int32_t* __restrict__ sel, int T,
+                                                          int E, int K, float* __restrict__ cnt,
+                                                          double* __restrict__ loss_seq) {
+  __shared__ int c[MOE_MAXE];
+  __shared__ double term[MOE_MAXE];
+  const int64_t s = blockIdx.x;
+  if (threadIdx.x < E) c[threadIdx.x] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * K; i += blockDim.x) atomicAdd(&c[sel[s * T * K + i]], 1);
+  __syncthreads();
+  if (threadIdx.x < E) {
+    const int e = threadIdx.x;
+    double sum = 0.0;
+    for (int t = 0; t < T; t++) sum += (double)probs[(s * T + t) * E + e];
+    const double ss = (double)E / ((double)K * (double)T);
+    term[e] = ss * (double)c[e] * (sum / (double)T);
+    cnt[s * E + e] = (float)c[e];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double l = 0.0;
+    for (int e = 0; e < E; e++) l += term[e];
+    loss_seq[s] = l;
+  }
+}
+
+void launch_moe_balance(const float* probs, const int32_t* sel, int S, int T, int E, int K,
+                        float* cnt, double* loss_seq, hipStream_t st) {
+  if (S <= 0) return;
+  hipLaunchKernelGGL(moe_balance_kernel, dim3(S), dim3(256), 0, st, probs, sel, T, E, K, cnt,
+                     loss_seq);
+  GN_HIP(hipGetLastError());
+}
+
+// Router softmax backward per token: dProbs[e] = (sum of its pair terms) +
+// balance gradient coef * count[seq][e]; dLogits = p * (dProbs - <p, dProbs>)
+// in float64 (moe.go:245-263).
+__global__ void moe_router_bwd_kernel(MoeRouterBwdArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= a.rows) return;
+  double gp[MOE_MAXE];
+  for (int e = 0; e < a.E; e++) gp[e] = 0.0;
+  for (int k = 0; k < a.K; k++) {
+    const int e = a.sel[r * a.K + k];
+    gp[e] += a.dotp[a.inv[r * a.K + k]];
+  }
+  if (a.bal_cnt) {
+    const float* c = a.bal_cnt + (r / a.T) * a.E;
+    for (int e = 0; e < a.E; e++) gp[e] += a.bal_coef * (double)c[e];
+  }
+  double dot = 0.0;
+  for (int e = 0; e < a.E; e++) dot += (double)a.probs[r * a.E + e] * gp[e];
+  for (int e = 0; e < a.E; e++) {
+    const double p = (double)a.probs[r * a.E + e];
+    a.glog[r * a.E + e] = (float)(p * (gp[e] - dot));
+  }
+}
+
+void launch_moe_router_bwd(const MoeRouterBwdArgs& a, hipStream_t st) {
+  if (a.rows <= 0) return;
+  hipLaunchKernelGGL(moe_router_bwd_kernel, dim3((unsigned)ceil_div(a.rows, 256)), dim3(256), 0, st,
+                     a);
+  GN_HIP(hipGetLastError());
+}
+
+// dh2 = dshared + ((sum over the token's pairs, expert order, of dxg) +
+// drouter) (moe.go:233-266, train.go:561-564).
+__global__ __launch_bounds__(256) void moe_bwd_combine_kernel(MoeBwdCombineArgs a) {
+  const int64_t r = blockIdx.x;
+  int pos[MOE_MAXK];
+  sorted_pairs(a.sel, a.inv, r, a.K, pos);
+  for (int c = threadIdx.x; c < a.C; c += blockDim.x) {
+    float s = 0.f;
+    for (int k = 0; k < a.K; k++) s += a.dxg[(int64_t)pos[k] * a.C + c];
+    a.out[r * a.C + c] = a.dshared[r * a.C + c] + (s + a.drouter[r * a.C + c]);
+  }
+}
+
+void launch_moe_bwd_combine(const MoeBwdCombineArgs& a, int64_t rows, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(moe_bwd_combine_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// PrefillFrom for position-major caches (kvcache.go:383-448): rows
+// [0, P) of src [G][maxSrc][W] are copied to each of the S rows of their
+// group in dst [G*S][maxDst][W].
+__global__ void replicate_rows_kernel(const float* __restrict__ src, float* __restrict__ dst, int G,
+                                      int S, int P, int W, int maxSrc, int maxDst, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;  // total = G*S*P*W
+  const int w = (int)(i % W);
+  int64_t r = i / W;
+  const int p = (int)(r % P);
+  const int64_t row = r / P;
+  const int64_t g = row / S;
+  dst[(row * maxDst + p) * W + w] = src[(g * maxSrc + p) * W + w];
+}
+
+void launch_replicate_rows(const float* src, float* dst, int G, int S, int P, int W, int maxSrc,
+                           int maxDst, hipStream_t st) {
+  const int64_t total = (int64_t)G * S * P * W;
+  if (total <= 0) return;
+  hipLaunchKernelGGL(replicate_rows_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                     src, dst, G, S, P, W, maxSrc, maxDst, total);
+  GN_HIP(hipGetLastError());
+}
+
+}  // namespace gn

@@ -127,6 +127,139 @@ void launch_smear_bwd(const float* ga, const float* embn, const float* smsig, co
 void launch_embed_scatter(const float* g, const int32_t* ids, int C, int64_t N, float* gw,
                           hipStream_t st);
 
+// ---- latent preset: MLA (model/mla.go) ------------------------------------
+// xa rows are [q_lat (lat) | kv_lat (lat) | q_rope (Hq*rd) | k_rope (Hkv*rd)]
+// (one GEMM of h against the stacked QueryDown, KVDown, QueryRope, KeyRope);
+// kvu rows are [k_content (Hkv*cd) | v (Hkv*128)] (KeyUp and ValueUp on
+// kv_lat); cd = 128 - rd.
+struct MlaAssembleArgs {
+  const float* xa;
+  int xw;
+  const float* qc;  // [N, Hq*cd] = QueryUp . q_lat
+  const float* kvu;
+  const float* cosT;
+  const float* sinT;
+  int Hq, Hkv, lat, rd, T, pos0;
+  float* q;  // [N, Hq, 128]
+  float* k;  // [N, Hkv, 128]
+  float* v;
+  float* lat_cache;  // prefill: [B][maxSeq][lat] (or null)
+  float* rk_cache;   // prefill: [B][maxSeq][Hkv*rd]
+  int maxSeq;
+};
+void launch_mla_assemble(const MlaAssembleArgs& a, int64_t rows, hipStream_t st);
+
+struct MlaPostBwdArgs {
+  const float* dq;  // [N, Hq, 128]
+  const float* dk;  // [N, Hkv, 128]
+  const float* dv;
+  const float* cosT;
+  const float* sinT;
+  int Hq, Hkv, lat, rd, T, xw;
+  float* dqc;   // [N, Hq*cd]
+  float* dxa;   // rotary parts written: [N, xw] columns 2*lat ..
+  float* dkvu;  // [N, Hkv*(cd+128)]
+};
+void launch_mla_post_bwd(const MlaPostBwdArgs& a, int64_t rows, hipStream_t st);
+
+struct MlaDecodeArgs {
+  const float* xa;    // [rows, xw]
+  int xw;
+  const float* qabs;  // [rows, Hq, lat] absorbed content queries
+  float* qrope;       // [rows, Hq, rd] (written by the prep kernel)
+  float* lat_cache;   // layer base [rows][maxSeq][lat]
+  float* rk_cache;    // layer base [rows][maxSeq][Hkv*rd]
+  const float* cosT;
+  const float* sinT;
+  float* out;         // [rows, Hq, lat] attention-weighted latents
+  float* part;        // [rows][nsplit_max][Hq][lat + 2] split partials
+  int rows, Hq, Hkv, lat, rd, maxSeq, window;
+  int pos;            // query position (eager launches)
+  const int* pos_dev; // when set, the position is read on the device
+  int nsplit_max;     // set by the launcher
+};
+void launch_mla_decode(MlaDecodeArgs a, hipStream_t st);
+void launch_replicate_rows(const float* src, float* dst, int G, int S, int P, int W, int maxSrc,
+                           int maxDst, hipStream_t st);
+
+// ---- latent preset: DeepSeekMoE (model/moe.go) ---------------------------
+void launch_swiglu_rows(const float* gu, int F, int64_t rows, float clamp, float* act,
+                        hipStream_t st);
+void launch_swiglu_rows_bwd(const float* gu, const float* dact, int F, int64_t rows, float clamp,
+                            float* dgu, hipStream_t st);
+
+struct MoeRouteArgs {
+  const float* logits;  // [rows, E] router logits
+  const float* bias;    // [E] router correction bias
+  const float* x;       // [rows, C] MoE input (gathered into xg)
+  int64_t rows;
+  int E, K, C;
+  float* probs;     // [rows, E]
+  int32_t* sel;     // [rows*K]
+  float* w;         // [rows*K]
+  int* blockcnt;    // [ceil(rows*K/256)][E] scratch
+  int* off;         // [E+1] expert offsets into the gathered rows
+  int* perm_row;    // [rows*K] gathered pair -> token
+  float* perm_w;    // [rows*K] gathered pair -> router weight
+  int* inv;         // [rows*K] (token, slot) -> gathered pair
+  float* xg;        // [rows*K, C]
+};
+void launch_moe_route(const MoeRouteArgs& a, hipStream_t st);
+struct MoePlaceArgs {
+  const int32_t* sel;
+  const float* w;
+  const float* x;
+  const int* off;
+  const int* blockoff;
+  int64_t npairs;
+  int K, E, C;
+  int* perm_row;
+  float* perm_w;
+  int* inv;
+  float* xg;
+};
+
+struct MoeCombineArgs {
+  const float* mid;     // residual stream after attention
+  const float* shared;  // shared-expert output
+  const float* yg;      // [rows*K, C] expert outputs (gathered order)
+  const float* perm_w;
+  const int32_t* sel;
+  const int* inv;
+  float scale;
+  int K, C;
+  float* out;
+};
+void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st);
+
+void launch_moe_bwd_prep(const float* g, const float* yg, const int* perm_row, const float* perm_w,
+                         float scale, int64_t npairs, int C, float* gy, double* dotp,
+                         hipStream_t st);
+void launch_moe_balance(const float* probs, const int32_t* sel, int S, int T, int E, int K,
+                        float* cnt, double* loss_seq, hipStream_t st);
+struct MoeRouterBwdArgs {
+  const float* probs;
+  const int32_t* sel;
+  const int* inv;
+  const double* dotp;
+  const float* bal_cnt;  // [S][E] or null
+  double bal_coef;       // weight / (S T) * E / (K T)
+  int64_t rows;
+  int E, K, T;
+  float* glog;           // [rows, E]
+};
+void launch_moe_router_bwd(const MoeRouterBwdArgs& a, hipStream_t st);
+struct MoeBwdCombineArgs {
+  const float* dshared;
+  const float* dxg;
+  const float* drouter;
+  const int32_t* sel;
+  const int* inv;
+  int K, C;
+  float* out;
+};
+void launch_moe_bwd_combine(const MoeBwdCombineArgs& a, int64_t rows, hipStream_t st);
+
 // ---- sampler (inference/sampler.go + tensors/random.go) -------------------
 struct SamplerArgs {
   const float* logits;          // [rows, V]

@@ -62,6 +62,14 @@ struct Layer {
   float *gqkv, *go, *gfc, *gproj, *gwve, *gve;
   int window;
   bool has_ve;
+  // latent preset.  MLA: wxa = [QueryDown; KVDown; QueryRope; KeyRope] (all
+  // read h), wqu = QueryUp, wkvu = [KeyUp; ValueUp] (read the KV latent);
+  // wqabs / wcomb are the absorbed decode weights derived from them.
+  float *wxa, *wqu, *wkvu, *gxa, *gqu, *gkvu;
+  float *wqabs, *wcomb;
+  // MoE: wgu = [c_gate; c_fc] of the shared expert, router, packed experts
+  float *wgu, *ggu, *wr, *rbias, *gwr;
+  float *eg, *eu, *ed, *geg, *geu, *ged;
 };
 
 }  // namespace gn
@@ -71,6 +79,15 @@ struct gn_session {
   int device = 0;
   int C = 0, Hq = 0, Hkv = 0, D = 0, R = 0, F = 0, L = 0, V = 0, PV = 0, S = 0;
   int QKVW = 0, KVW = 0;
+  // latent preset: MLA widths (xa row = 2*lat + (Hq+Hkv)*rd, kvu row =
+  // Hkv*(cd+D)) and MoE shape; derived decode weights are refreshed lazily
+  bool mla = false, moe = false;
+  int lat = 0, rd = 0, cd = 0, XW = 0, KVUW = 0;
+  int E = 0, K = 0, EH = 0;
+  float clamp = 0.f, mscale = 1.f, bw = 0.f;
+  bool derived_dirty = true;
+  float* derived = nullptr;
+  double aux_loss = 0.0;
   int64_t total = 0;
   hipStream_t stream = nullptr;
   std::unique_ptr<gn::DeviceArena> arena;
@@ -196,12 +213,43 @@ static void build_session(gn_session* s, const gn_config& cfg) {
   s->Hkv = cfg.n_kv_head;
   s->D = s->C / s->Hq;
   GN_CHECK(s->D == HD, "session: head dimension must be 128");
-  s->R = cfg.rotary_dims <= 0 ? s->D : cfg.rotary_dims;
+  s->mla = cfg.mla_latent > 0;
+  s->moe = cfg.n_experts > 0;
+  if (s->mla) {  // model/config.go:262-280, 476-505
+    s->lat = cfg.mla_latent;
+    s->rd = cfg.mla_rope_dims;
+    GN_CHECK(s->rd > 0 && s->rd < s->D && s->rd % 4 == 0,
+             "config: MLA rotary dims must be a positive multiple of 4 below the head dim");
+    GN_CHECK(s->lat % 4 == 0 && s->lat <= 256, "session: MLA latent must be a multiple of 4, <= 256");
+    GN_CHECK(s->Hkv * s->rd <= 256, "session: MLA rotary keys wider than 256");
+    GN_CHECK(s->Hq <= 8, "session: MLA decode supports at most 8 query heads");
+    s->cd = s->D - s->rd;
+    s->R = s->rd;
+    s->XW = 2 * s->lat + (s->Hq + s->Hkv) * s->rd;
+    s->KVUW = s->Hkv * (s->cd + s->D);
+  } else {
+    s->R = cfg.rotary_dims <= 0 ? s->D : cfg.rotary_dims;
+  }
   GN_CHECK(s->R <= s->D && s->R % 2 == 0, "config: RotaryDims must be even and <= head dim");
   GN_CHECK(s->C <= 1024, "session: EmbedDim above 1024 is not supported");
   GN_CHECK(s->Hq / s->Hkv <= 8, "session: GQA ratio above 8 is not supported");
   GN_CHECK(s->Hq + 2 * s->Hkv <= 16, "session: at most 16 q+k+v heads");
-  s->F = 4 * s->C;
+  if (s->moe) {  // model/config.go:138-227
+    s->E = cfg.n_experts;
+    s->K = cfg.experts_per_token;
+    s->EH = cfg.expert_hidden;
+    GN_CHECK(s->E <= 64 && s->K >= 1 && s->K <= 8 && s->K <= s->E,
+             "session: MoE needs 1 <= top-k <= min(8, experts) and at most 64 experts");
+    GN_CHECK(s->EH > 0 && s->EH % 4 == 0 && cfg.shared_hidden > 0 && cfg.shared_hidden % 4 == 0,
+             "session: expert widths must be positive multiples of 4");
+    GN_CHECK(s->C % 4 == 0, "session: MoE needs EmbedDim % 4 == 0");
+    s->F = cfg.shared_hidden;
+    s->clamp = cfg.moe_clamp;
+    s->mscale = cfg.moe_scale;
+    s->bw = cfg.balance_weight;
+  } else {
+    s->F = 4 * s->C;
+  }
   s->L = cfg.n_layer;
   s->V = cfg.vocab_size;
   GN_CHECK(s->V > 0, "config: vocab_size must be positive");
@@ -211,47 +259,10 @@ static void build_session(gn_session* s, const gn_config& cfg) {
   s->KVW = s->Hkv * s->D;
   s->QKVW = s->Hq * s->D + 2 * s->KVW;
 
-  // sorted-name table with packed placement
-  struct Ent {
-    std::string name;
-    int64_t rows, cols;
-    int kind;  // 0 global, 1 q, 2 k, 3 v, 4 proj, 5 vegate, 6 ve, 7 fc, 8 mproj
-    int layer;
-  };
-  std::vector<Ent> ents;
-  auto add = [&](const std::string& n, int64_t r, int64_t c, int kind, int layer) {
-    ents.push_back({n, r, c, kind, layer});
-  };
-  add("transformer.wte.weight", s->PV, s->C, 0, -1);
-  add("lm_head.weight", s->PV, s->C, 0, -1);
-  for (int l = 0; l < s->L; l++) {
-    std::string p = "transformer.h." + std::to_string(l) + ".";
-    add(p + "attn.c_q.weight", s->Hq * s->D, s->C, 1, l);
-    add(p + "attn.c_k.weight", s->KVW, s->C, 2, l);
-    add(p + "attn.c_v.weight", s->KVW, s->C, 3, l);
-    add(p + "attn.c_proj.weight", s->C, s->C, 4, l);
-    if (has_value_embedding(l, s->L)) {
-      add(p + "attn.ve_gate.weight", s->Hkv, VE_CH, 5, l);
-      add("value_embeds." + std::to_string(l) + ".weight", s->PV, s->KVW, 6, l);
-    }
-    add(p + "mlp.c_fc.weight", s->F, s->C, 7, l);
-    add(p + "mlp.c_proj.weight", s->C, s->F, 8, l);
-  }
-  add("resid_lambdas", s->L, 1, 0, -1);
-  add("x0_lambdas", s->L, 1, 0, -1);
-  add("smear_gate.weight", 1, SMEAR_CH, 0, -1);
-  add("smear_lambda", 1, 1, 0, -1);
-  add("backout_lambda", 1, 1, 0, -1);
-  std::sort(ents.begin(), ents.end(), [](const Ent& a, const Ent& b) { return a.name < b.name; });
-  int64_t total = 0;
-  for (auto& e : ents) total += e.rows * e.cols;
-  s->total = total;
-  GN_HIP(hipMalloc(&s->params, sizeof(float) * total));
-  GN_HIP(hipMalloc(&s->grads, sizeof(float) * total));
-  GN_HIP(hipMemsetAsync(s->params, 0, sizeof(float) * total, s->stream));
-  GN_HIP(hipMemsetAsync(s->grads, 0, sizeof(float) * total, s->stream));
-
-  // packed placement: per layer [wqkv | wo | wfc | wproj | wve | ve], then globals
+  // Packed device placement: per layer the attention block(s), c_proj, the
+  // value embedding, then the feed-forward; globals last.  Tensors that feed
+  // one GEMM together are adjacent (q/k/v; the four MLA projections of h;
+  // KeyUp/ValueUp; c_gate/c_fc).
   s->layers.assign(s->L, Layer{});
   int64_t cur = 0;
   auto place = [&](int64_t n) {
@@ -259,38 +270,120 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     cur += (n + 63) / 64 * 64;
     return o;
   };
-  std::vector<int64_t> lay_qkv(s->L), lay_o(s->L), lay_fc(s->L), lay_pj(s->L), lay_vg(s->L),
-      lay_ve(s->L);
+  struct Ent {
+    std::string name;
+    int64_t rows, cols, loc;
+  };
+  std::vector<Ent> ents;
+  auto add = [&](const std::string& n, int64_t r, int64_t c, int64_t loc) {
+    ents.push_back({n, r, c, loc});
+  };
+  struct Off {
+    int64_t qkv = -1, o = -1, fc = -1, pj = -1, vg = -1, ve = -1;
+    int64_t xa = -1, qu = -1, kvu = -1, gu = -1, r = -1, rb = -1, eg = -1, eu = -1, ed = -1;
+  };
+  std::vector<Off> off(s->L);
+  const int C = s->C, D = s->D, Hq = s->Hq, Hkv = s->Hkv, F = s->F;
   for (int l = 0; l < s->L; l++) {
-    lay_qkv[l] = place((int64_t)s->QKVW * s->C);
-    lay_o[l] = place((int64_t)s->C * s->C);
-    lay_fc[l] = place((int64_t)s->F * s->C);
-    lay_pj[l] = place((int64_t)s->C * s->F);
-    bool hv = has_value_embedding(l, s->L);
-    lay_vg[l] = hv ? place((int64_t)s->Hkv * VE_CH) : -1;
-    lay_ve[l] = hv ? place((int64_t)s->PV * s->KVW) : -1;
+    Off& o = off[l];
+    const std::string p = "transformer.h." + std::to_string(l) + ".";
+    if (s->mla) {  // model/params.go:19-27
+      const int lat = s->lat, rd = s->rd, cd = s->cd;
+      o.xa = place((int64_t)s->XW * C);
+      add(p + "attn.mla_q_down.weight", lat, C, o.xa);
+      add(p + "attn.mla_kv_down.weight", lat, C, o.xa + (int64_t)lat * C);
+      add(p + "attn.mla_q_rope.weight", Hq * rd, C, o.xa + (int64_t)2 * lat * C);
+      add(p + "attn.mla_k_rope.weight", Hkv * rd, C, o.xa + (int64_t)(2 * lat + Hq * rd) * C);
+      o.qu = place((int64_t)Hq * cd * lat);
+      add(p + "attn.mla_q_up.weight", Hq * cd, lat, o.qu);
+      o.kvu = place((int64_t)s->KVUW * lat);
+      add(p + "attn.mla_k_up.weight", Hkv * cd, lat, o.kvu);
+      add(p + "attn.mla_v_up.weight", Hkv * D, lat, o.kvu + (int64_t)Hkv * cd * lat);
+    } else {
+      o.qkv = place((int64_t)s->QKVW * C);
+      add(p + "attn.c_q.weight", Hq * D, C, o.qkv);
+      add(p + "attn.c_k.weight", s->KVW, C, o.qkv + (int64_t)Hq * D * C);
+      add(p + "attn.c_v.weight", s->KVW, C, o.qkv + ((int64_t)Hq * D + s->KVW) * C);
+    }
+    o.o = place((int64_t)C * C);
+    add(p + "attn.c_proj.weight", C, C, o.o);
+    if (!s->mla && has_value_embedding(l, s->L)) {  // no VE under MLA (transformer.go:72-78)
+      o.vg = place((int64_t)Hkv * VE_CH);
+      add(p + "attn.ve_gate.weight", Hkv, VE_CH, o.vg);
+      o.ve = place((int64_t)s->PV * s->KVW);
+      add("value_embeds." + std::to_string(l) + ".weight", s->PV, s->KVW, o.ve);
+    }
+    if (s->moe) {  // model/params.go:52-63
+      o.gu = place((int64_t)2 * F * C);
+      add(p + "mlp.c_gate.weight", F, C, o.gu);
+      o.fc = o.gu + (int64_t)F * C;
+      add(p + "mlp.c_fc.weight", F, C, o.fc);
+      o.pj = place((int64_t)C * F);
+      add(p + "mlp.c_proj.weight", C, F, o.pj);
+      const int E = s->E, EH = s->EH;
+      o.r = place((int64_t)E * C);
+      add(p + "moe.router.weight", E, C, o.r);
+      o.rb = place(E);
+      add(p + "moe.router_bias", E, 1, o.rb);
+      o.eg = place((int64_t)E * EH * C);
+      add(p + "moe.experts.gate.weight", (int64_t)E * EH, C, o.eg);
+      o.eu = place((int64_t)E * EH * C);
+      add(p + "moe.experts.up.weight", (int64_t)E * EH, C, o.eu);
+      o.ed = place((int64_t)E * C * EH);
+      add(p + "moe.experts.down.weight", (int64_t)E * C, EH, o.ed);
+    } else {
+      o.fc = place((int64_t)F * C);
+      add(p + "mlp.c_fc.weight", F, C, o.fc);
+      o.pj = place((int64_t)C * F);
+      add(p + "mlp.c_proj.weight", C, F, o.pj);
+    }
   }
-  int64_t off_wte = place((int64_t)s->PV * s->C), off_lm = place((int64_t)s->PV * s->C);
-  int64_t off_rl = place(s->L), off_x0 = place(s->L), off_smg = place(SMEAR_CH),
-          off_sml = place(1), off_bkl = place(1);
-  // re-allocate with padding room
-  GN_HIP(hipFree(s->params));
-  GN_HIP(hipFree(s->grads));
+  const int64_t off_wte = place((int64_t)s->PV * C), off_lm = place((int64_t)s->PV * C);
+  const int64_t off_rl = place(s->L), off_x0 = place(s->L), off_smg = place(SMEAR_CH),
+                off_sml = place(1), off_bkl = place(1);
+  add("transformer.wte.weight", s->PV, C, off_wte);
+  add("lm_head.weight", s->PV, C, off_lm);
+  add("resid_lambdas", s->L, 1, off_rl);
+  add("x0_lambdas", s->L, 1, off_x0);
+  add("smear_gate.weight", 1, SMEAR_CH, off_smg);
+  add("smear_lambda", 1, 1, off_sml);
+  add("backout_lambda", 1, 1, off_bkl);
+  std::sort(ents.begin(), ents.end(), [](const Ent& a, const Ent& b) { return a.name < b.name; });
+  int64_t total = 0;
+  for (auto& e : ents) total += e.rows * e.cols;
+  s->total = total;
   GN_HIP(hipMalloc(&s->params, sizeof(float) * cur));
   GN_HIP(hipMalloc(&s->grads, sizeof(float) * cur));
   GN_HIP(hipMemsetAsync(s->params, 0, sizeof(float) * cur, s->stream));
   GN_HIP(hipMemsetAsync(s->grads, 0, sizeof(float) * cur, s->stream));
-  auto P = [&](int64_t o) { return s->params + o; };
-  auto G = [&](int64_t o) { return s->grads + o; };
+  auto P = [&](int64_t o) { return o >= 0 ? s->params + o : nullptr; };
+  auto G = [&](int64_t o) { return o >= 0 ? s->grads + o : nullptr; };
   for (int l = 0; l < s->L; l++) {
     Layer& ly = s->layers[l];
-    ly.wqkv = P(lay_qkv[l]); ly.gqkv = G(lay_qkv[l]);
-    ly.wo = P(lay_o[l]); ly.go = G(lay_o[l]);
-    ly.wfc = P(lay_fc[l]); ly.gfc = G(lay_fc[l]);
-    ly.wproj = P(lay_pj[l]); ly.gproj = G(lay_pj[l]);
-    ly.has_ve = lay_vg[l] >= 0;
-    ly.wve = ly.has_ve ? P(lay_vg[l]) : nullptr; ly.gwve = ly.has_ve ? G(lay_vg[l]) : nullptr;
-    ly.ve = ly.has_ve ? P(lay_ve[l]) : nullptr; ly.gve = ly.has_ve ? G(lay_ve[l]) : nullptr;
+    const Off& o = off[l];
+    ly.wqkv = P(o.qkv); ly.gqkv = G(o.qkv);
+    ly.wo = P(o.o); ly.go = G(o.o);
+    ly.wfc = P(o.fc); ly.gfc = G(o.fc);
+    ly.wproj = P(o.pj); ly.gproj = G(o.pj);
+    ly.has_ve = o.vg >= 0;
+    ly.wve = P(o.vg); ly.gwve = G(o.vg);
+    ly.ve = P(o.ve); ly.gve = G(o.ve);
+    ly.wxa = P(o.xa); ly.gxa = G(o.xa);
+    ly.wqu = P(o.qu); ly.gqu = G(o.qu);
+    ly.wkvu = P(o.kvu); ly.gkvu = G(o.kvu);
+    ly.wgu = P(o.gu); ly.ggu = G(o.gu);
+    ly.wr = P(o.r); ly.gwr = G(o.r); ly.rbias = P(o.rb);
+    ly.eg = P(o.eg); ly.geg = G(o.eg);
+    ly.eu = P(o.eu); ly.geu = G(o.eu);
+    ly.ed = P(o.ed); ly.ged = G(o.ed);
+  }
+  if (s->mla) {  // absorbed decode weights, per layer [Hq*lat, lat] and [C, Hq*lat]
+    const int64_t per = (int64_t)Hq * s->lat * s->lat + (int64_t)C * Hq * s->lat;
+    GN_HIP(hipMalloc(&s->derived, sizeof(float) * per * s->L));
+    for (int l = 0; l < s->L; l++) {
+      s->layers[l].wqabs = s->derived + per * l;
+      s->layers[l].wcomb = s->derived + per * l + (int64_t)Hq * s->lat * s->lat;
+    }
   }
   s->wte = P(off_wte); s->gwte = G(off_wte);
   s->lm = P(off_lm); s->glm = G(off_lm);
@@ -301,36 +394,10 @@ static void build_session(gn_session* s, const gn_config& cfg) {
   s->bkl = P(off_bkl); s->gbkl = G(off_bkl);
   auto w = window_sizes(cfg);
   for (int l = 0; l < s->L; l++) s->layers[l].window = w[l];
-
-  int64_t off = 0;
+  int64_t offset = 0;
   for (auto& e : ents) {
-    ParamEntry pe{e.name, e.rows, e.cols, off, nullptr, nullptr};
-    int64_t loc = -1;
-    const int l = e.layer;
-    switch (e.kind) {
-      case 0:
-        if (e.name == "transformer.wte.weight") loc = off_wte;
-        else if (e.name == "lm_head.weight") loc = off_lm;
-        else if (e.name == "resid_lambdas") loc = off_rl;
-        else if (e.name == "x0_lambdas") loc = off_x0;
-        else if (e.name == "smear_gate.weight") loc = off_smg;
-        else if (e.name == "smear_lambda") loc = off_sml;
-        else if (e.name == "backout_lambda") loc = off_bkl;
-        break;
-      case 1: loc = lay_qkv[l]; break;
-      case 2: loc = lay_qkv[l] + (int64_t)s->Hq * s->D * s->C; break;
-      case 3: loc = lay_qkv[l] + ((int64_t)s->Hq * s->D + s->KVW) * s->C; break;
-      case 4: loc = lay_o[l]; break;
-      case 5: loc = lay_vg[l]; break;
-      case 6: loc = lay_ve[l]; break;
-      case 7: loc = lay_fc[l]; break;
-      case 8: loc = lay_pj[l]; break;
-    }
-    GN_CHECK(loc >= 0, "internal: unplaced parameter " + e.name);
-    pe.dev = P(loc);
-    pe.grad = G(loc);
-    s->table.push_back(pe);
-    off += e.rows * e.cols;
+    s->table.push_back(ParamEntry{e.name, e.rows, e.cols, offset, P(e.loc), G(e.loc)});
+    offset += e.rows * e.cols;
   }
 
   // rotary tables (model/rotary.go:16-30), SequenceLen*10 positions, computed
@@ -357,12 +424,23 @@ static void build_session(gn_session* s, const gn_config& cfg) {
 // ---------------------------------------------------------------------------
 enum SeqMode { SEQ_TRAIN, SEQ_PREFILL, SEQ_FORWARD };
 
+// Routing and expert activations of one MoE layer (saved for the backward
+// when training).
+struct MoeBuffers {
+  float *probs = nullptr, *w = nullptr, *perm_w = nullptr;
+  int32_t* sel = nullptr;
+  int *off = nullptr, *perm_row = nullptr, *inv = nullptr, *blockcnt = nullptr;
+  float *xg = nullptr, *gug = nullptr, *hg = nullptr, *yg = nullptr;
+};
+
 struct SeqBuffers {
   int B = 0, T = 0;
   int64_t N = 0;
   int32_t* ids = nullptr;
   float *raw, *embn, *smsig, *x0;
   std::vector<float*> xin, xb, h, qrot, krot, qn, kn, v, vesig, o, lse, mid, h2, u, act;
+  std::vector<float*> xa, gu;  // latent preset: MLA xa rows, shared-expert [gate | up]
+  std::vector<MoeBuffers> moe;
   float *xfinal, *fpre, *fn;
   float* backout;
 };
@@ -372,6 +450,66 @@ struct SeqBuffers {
 static float* layer_buf(gn_session* s, const char* nm, int l, bool per_layer, size_t count) {
   std::string key = std::string(nm) + (per_layer ? std::to_string(l) : std::string("*"));
   return A<float>(s, key, count);
+}
+
+// MoE buffers of `rows` tokens under name prefix `pre` (per layer when
+// training saves them).
+static MoeBuffers moe_buffers(gn_session* s, const std::string& pre, int64_t rows) {
+  const int64_t NK = rows * s->K;
+  MoeBuffers m;
+  m.probs = A<float>(s, pre + "probs", rows * s->E);
+  m.sel = A<int32_t>(s, pre + "sel", NK);
+  m.w = A<float>(s, pre + "w", NK);
+  m.off = A<int>(s, pre + "off", s->E + 1);
+  m.perm_row = A<int>(s, pre + "prow", NK);
+  m.perm_w = A<float>(s, pre + "pw", NK);
+  m.inv = A<int>(s, pre + "inv", NK);
+  m.blockcnt = A<int>(s, "moe_blockcnt", ceil_div(NK, 256) * s->E);
+  m.xg = A<float>(s, pre + "xg", NK * s->C);
+  m.gug = A<float>(s, pre + "gug", NK * 2 * s->EH);
+  m.hg = A<float>(s, pre + "hg", NK * s->EH);
+  m.yg = A<float>(s, pre + "yg", NK * s->C);
+  return m;
+}
+
+// The feed-forward of a MoE block (model/block.go:40-45, mlp.go:62-76,
+// moe.go:118-198): xout = mid + (shared(h2) + routed(h2)).  gu and act
+// receive the shared expert's [gate | up] pre-activations and its SwiGLU.
+static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, const float* h2,
+                            int64_t rows, float* gu, float* act, const MoeBuffers& m,
+                            float* xout) {
+  const int C = s->C, F = s->F, E = s->E, EH = s->EH;
+  const int64_t NK = rows * s->K;
+  hipStream_t st = s->stream;
+  sgemm(s, linear_fwd_desc(h2, ly.wgu, gu, (int)rows, C, 2 * F));
+  launch_swiglu_rows(gu, F, rows, s->clamp, act, st);
+  float* shared = A<float>(s, "moe_shared", rows * C);
+  sgemm(s, linear_fwd_desc(act, ly.wproj, shared, (int)rows, F, C));
+  float* logits = A<float>(s, "moe_logits", rows * E);
+  sgemm(s, linear_fwd_desc(h2, ly.wr, logits, (int)rows, C, E));
+  MoeRouteArgs ra{};
+  ra.logits = logits; ra.bias = ly.rbias; ra.x = h2; ra.rows = rows;
+  ra.E = E; ra.K = s->K; ra.C = C;
+  ra.probs = m.probs; ra.sel = m.sel; ra.w = m.w; ra.blockcnt = m.blockcnt; ra.off = m.off;
+  ra.perm_row = m.perm_row; ra.perm_w = m.perm_w; ra.inv = m.inv; ra.xg = m.xg;
+  launch_moe_route(ra, st);
+  // expert gate and up projections into [gate | up] rows, SwiGLU, down
+  for (int half = 0; half < 2; half++) {
+    GemmDesc d = linear_fwd_desc(m.xg, half ? ly.eu : ly.eg, m.gug + half * EH, (int)NK, C, EH);
+    d.ldc = 2 * EH;
+    d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
+    d.group_stride = (int64_t)EH * C;
+    sgemm(s, d);
+  }
+  launch_swiglu_rows(m.gug, EH, NK, s->clamp, m.hg, st);
+  GemmDesc dd = linear_fwd_desc(m.hg, ly.ed, m.yg, (int)NK, EH, C);
+  dd.group = GEMM_GROUP_ROWS; dd.group_off = m.off; dd.groups = E;
+  dd.group_stride = (int64_t)C * EH;
+  sgemm(s, dd);
+  MoeCombineArgs ca{};
+  ca.mid = mid; ca.shared = shared; ca.yg = m.yg; ca.perm_w = m.perm_w; ca.sel = m.sel;
+  ca.inv = m.inv; ca.scale = s->mscale; ca.K = s->K; ca.C = C; ca.out = xout;
+  launch_moe_combine(ca, rows, st);
 }
 
 static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcache_pf,
@@ -387,9 +525,10 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   sb.x0 = A<float>(s, "x0", N * C);
   launch_embed_smear(sb.ids, s->wte, s->smg, s->sml, B, T, C, sb.raw, sb.embn, sb.smsig, sb.x0, st);
   for (auto* vec : {&sb.xin, &sb.xb, &sb.h, &sb.qrot, &sb.krot, &sb.qn, &sb.kn, &sb.v, &sb.vesig,
-                    &sb.o, &sb.lse, &sb.mid, &sb.h2, &sb.u, &sb.act})
+                    &sb.o, &sb.lse, &sb.mid, &sb.h2, &sb.u, &sb.act, &sb.xa, &sb.gu})
     vec->assign(L, nullptr);
-  float* qkv = A<float>(s, "qkv", N * s->QKVW);
+  sb.moe.assign(L, MoeBuffers{});
+  float* qkv = s->mla ? nullptr : A<float>(s, "qkv", N * s->QKVW);
   float* xcur = sb.x0;
   const int bk = L / 2;
   sb.backout = nullptr;
@@ -401,6 +540,34 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     launch_resid_norm(xcur, sb.x0, s->rl, s->x0l, l, N, C, xb, h, st);
     sb.xb[l] = xb;
     sb.h[l] = h;
+    if (s->mla) {
+      // mlaProjectHeads (mla.go:106-122): one GEMM for the four projections
+      // of h, then QueryUp and [KeyUp; ValueUp] on the latents
+      float* xa = layer_buf(s, "xa", l, save, N * s->XW);
+      sgemm(s, linear_fwd_desc(h, ly.wxa, xa, (int)N, C, s->XW));
+      float* qc = A<float>(s, "mla_qc", N * Hq * s->cd);
+      GemmDesc dq = linear_fwd_desc(xa, ly.wqu, qc, (int)N, s->lat, Hq * s->cd);
+      dq.lda = s->XW;
+      sgemm(s, dq);
+      float* kvu = A<float>(s, "mla_kvu", N * s->KVUW);
+      GemmDesc dk = linear_fwd_desc(xa + s->lat, ly.wkvu, kvu, (int)N, s->lat, s->KVUW);
+      dk.lda = s->XW;
+      sgemm(s, dk);
+      MlaAssembleArgs ma{};
+      ma.xa = xa; ma.xw = s->XW; ma.qc = qc; ma.kvu = kvu; ma.cosT = s->cosT; ma.sinT = s->sinT;
+      ma.Hq = Hq; ma.Hkv = Hkv; ma.lat = s->lat; ma.rd = s->rd; ma.T = T; ma.pos0 = 0;
+      ma.q = layer_buf(s, "qn", l, save, N * Hq * HD);
+      ma.k = layer_buf(s, "kn", l, save, N * s->KVW);
+      ma.v = layer_buf(s, "v", l, save, N * s->KVW);
+      if (mode == SEQ_PREFILL) {  // latent + rotary-key cache of the prompt
+        ma.lat_cache = kcache_pf + (int64_t)l * B * T * s->lat;
+        ma.rk_cache = vcache_pf + (int64_t)l * B * T * Hkv * s->rd;
+        ma.maxSeq = T;
+      }
+      launch_mla_assemble(ma, N, st);
+      sb.xa[l] = xa;
+      sb.qn[l] = ma.q; sb.kn[l] = ma.k; sb.v[l] = ma.v;
+    } else {
     sgemm(s, linear_fwd_desc(h, ly.wqkv, qkv, (int)N, C, s->QKVW));
     QkvPostArgs qa{};
     qa.qkv = qkv; qa.h = h; qa.ids = sb.ids;
@@ -422,8 +589,9 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     launch_qkv_post(qa, N, st);
     sb.qn[l] = qa.qn; sb.kn[l] = qa.kn; sb.v[l] = qa.vout;
     sb.qrot[l] = qa.qrot; sb.krot[l] = qa.krot; sb.vesig[l] = qa.vesig;
+    }
     FlashArgs fa{};
-    fa.q = qa.qn; fa.k = qa.kn; fa.v = qa.vout;
+    fa.q = sb.qn[l]; fa.k = sb.kn[l]; fa.v = sb.v[l];
     fa.o = layer_buf(s, "o", l, save, N * Hq * HD);
     fa.lse = save ? layer_buf(s, "lse", l, true, N * Hq) : nullptr;
     fa.B = B; fa.T = T; fa.Hq = Hq; fa.Hkv = Hkv; fa.window = ly.window;
@@ -437,6 +605,21 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     float* h2 = layer_buf(s, "h2", l, save, N * C);
     launch_norm_rows(mid, nullptr, nullptr, N, C, nullptr, h2, st);
     sb.h2[l] = h2;
+    if (s->moe) {
+      float* xout = save ? A<float>(s, "xout" + std::to_string(l), N * C)
+                         : A<float>(s, (l % 2) ? "xpong" : "xping", N * C);
+      float* gu = layer_buf(s, "gu", l, save, N * 2 * F);
+      float* act = layer_buf(s, "act", l, save, N * F);
+      MoeBuffers mb = moe_buffers(s, save ? "moe" + std::to_string(l) + "_" : "moe*_", N);
+      moe_ffn_forward(s, ly, mid, h2, N, gu, act, mb, xout);
+      sb.gu[l] = gu; sb.act[l] = act; sb.moe[l] = mb;
+      if (l == bk) {
+        sb.backout = A<float>(s, "backout", N * C);
+        GN_HIP(hipMemcpyAsync(sb.backout, xout, sizeof(float) * N * C, hipMemcpyDeviceToDevice, st));
+      }
+      xcur = xout;
+      continue;
+    }
     float* act = layer_buf(s, "act", l, save, N * F);
     float* u = save ? layer_buf(s, "u", l, true, N * F) : nullptr;
     GemmDesc gf = linear_fwd_desc(h2, ly.wfc, act, (int)N, C, F, EPI_RELU2_SAVE);
@@ -477,6 +660,113 @@ static int64_t logits_chunk(gn_session* s, int64_t N) {
   int64_t rows = std::max<int64_t>(1, budget / ((int64_t)s->V * 4));
   rows = std::min<int64_t>(rows, N);
   return rows;
+}
+
+// MoE block feed-forward backward (train.go:505-514 with the SwiGLU shared
+// expert, moe.go:203-267): dh2 (overwritten) is the gradient wrt the FFN
+// input; parameter gradients accumulate.  dauxl, when set, accumulates the
+// per-sequence balance-loss terms (moe.go:276-326).
+static void moe_ffn_backward(gn_session* s, const Layer& ly, const MoeBuffers& m, const float* g,
+                             const float* h2, const float* gu, const float* act, int B, int T,
+                             float* dh2, double* dauxl) {
+  const int C = s->C, F = s->F, E = s->E, EH = s->EH, K = s->K;
+  const int64_t N = (int64_t)B * T, NK = N * K;
+  hipStream_t st = s->stream;
+  // shared expert
+  float* dact = A<float>(s, "moe_dact", N * F);
+  sgemm(s, linear_dx_desc(g, ly.wproj, dact, (int)N, F, C));
+  sgemm(s, linear_dw_desc(g, act, ly.gproj, (int)N, F, C));
+  float* dgu = A<float>(s, "moe_dgu", N * 2 * F);
+  launch_swiglu_rows_bwd(gu, dact, F, N, s->clamp, dgu, st);
+  float* dsh = A<float>(s, "moe_dsh", N * C);
+  sgemm(s, linear_dx_desc(dgu, ly.wgu, dsh, (int)N, C, 2 * F));
+  sgemm(s, linear_dw_desc(dgu, h2, ly.ggu, (int)N, C, 2 * F));
+  // routed experts
+  float* gy = A<float>(s, "moe_gy", NK * C);
+  double* dotp = A<double>(s, "moe_dotp", NK);
+  launch_moe_bwd_prep(g, m.yg, m.perm_row, m.perm_w, s->mscale, NK, C, gy, dotp, st);
+  float* dhg = A<float>(s, "moe_dhg", NK * EH);
+  {  // dhg = gy . Wd_e; dWd_e += gy_e^T . hg_e
+    GemmDesc d = linear_dx_desc(gy, ly.ed, dhg, (int)NK, EH, C);
+    d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
+    d.group_stride = (int64_t)C * EH;
+    sgemm(s, d);
+    GemmDesc w = linear_dw_desc(gy, m.hg, ly.ged, (int)NK, EH, C);
+    w.group = GEMM_GROUP_K; w.group_off = m.off; w.groups = E;
+    w.group_stride = (int64_t)C * EH;
+    sgemm(s, w);
+  }
+  float* dgug = A<float>(s, "moe_dgug", NK * 2 * EH);
+  launch_swiglu_rows_bwd(m.gug, dhg, EH, NK, s->clamp, dgug, st);
+  float* dxg = A<float>(s, "moe_dxg", NK * C);
+  for (int half = 0; half < 2; half++) {  // dxg = dgate . Wg_e + dup . Wu_e
+    GemmDesc d = linear_dx_desc(dgug + half * EH, half ? ly.eu : ly.eg, dxg, (int)NK, C, EH,
+                                half ? EPI_ACCUM : EPI_STORE);
+    d.lda = 2 * EH;
+    d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
+    d.group_stride = (int64_t)EH * C;
+    sgemm(s, d);
+    GemmDesc w = linear_dw_desc(dgug + half * EH, m.xg, half ? ly.geu : ly.geg, (int)NK, C, EH);
+    w.lda = 2 * EH;
+    w.group = GEMM_GROUP_K; w.group_off = m.off; w.groups = E;
+    w.group_stride = (int64_t)EH * C;
+    sgemm(s, w);
+  }
+  // router softmax backward with the balance-loss gradient
+  MoeRouterBwdArgs rb{};
+  if (s->bw > 0.f) {
+    float* cnt = A<float>(s, "moe_balcnt", (int64_t)B * E);
+    double* lseq = A<double>(s, "moe_balloss", B);
+    launch_moe_balance(m.probs, m.sel, B, T, E, K, cnt, lseq, st);
+    if (dauxl) launch_sum_f64(lseq, B, dauxl, true, st);
+    rb.bal_cnt = cnt;
+    rb.bal_coef = (double)s->bw / ((double)B * T) * ((double)E / ((double)K * T));
+  }
+  float* glog = A<float>(s, "moe_glog", N * E);
+  rb.probs = m.probs; rb.sel = m.sel; rb.inv = m.inv; rb.dotp = dotp; rb.rows = N;
+  rb.E = E; rb.K = K; rb.T = T; rb.glog = glog;
+  launch_moe_router_bwd(rb, st);
+  float* drt = A<float>(s, "moe_drt", N * C);
+  sgemm(s, linear_dx_desc(glog, ly.wr, drt, (int)N, C, E));
+  sgemm(s, linear_dw_desc(glog, h2, ly.gwr, (int)N, C, E));
+  MoeBwdCombineArgs cb{};
+  cb.dshared = dsh; cb.dxg = dxg; cb.drouter = drt; cb.sel = m.sel; cb.inv = m.inv;
+  cb.K = K; cb.C = C; cb.out = dh2;
+  launch_moe_bwd_combine(cb, N, st);
+}
+
+// MLA attention backward after the flash kernels (train.go:414-419,
+// mla.go:126-146): dh (overwritten) is the gradient wrt the attention input.
+static void mla_backward(gn_session* s, const Layer& ly, const float* xa, const float* h,
+                         const float* dq, const float* dk, const float* dv, int64_t N, int T,
+                         float* dh) {
+  const int C = s->C, lat = s->lat, XW = s->XW;
+  hipStream_t st = s->stream;
+  float* dxa = A<float>(s, "mla_dxa", N * XW);
+  float* dqc = A<float>(s, "mla_dqc", N * s->Hq * s->cd);
+  float* dkvu = A<float>(s, "mla_dkvu", N * s->KVUW);
+  MlaPostBwdArgs pb{};
+  pb.dq = dq; pb.dk = dk; pb.dv = dv; pb.cosT = s->cosT; pb.sinT = s->sinT;
+  pb.Hq = s->Hq; pb.Hkv = s->Hkv; pb.lat = lat; pb.rd = s->rd; pb.T = T; pb.xw = XW;
+  pb.dqc = dqc; pb.dxa = dxa; pb.dkvu = dkvu;
+  launch_mla_post_bwd(pb, N, st);
+  // query latent: dq_lat = dqc . QueryUp -> dxa[:, :lat]
+  GemmDesc a1 = linear_dx_desc(dqc, ly.wqu, dxa, (int)N, lat, s->Hq * s->cd);
+  a1.ldc = XW;
+  sgemm(s, a1);
+  GemmDesc a2 = linear_dw_desc(dqc, xa, ly.gqu, (int)N, lat, s->Hq * s->cd);
+  a2.ldb = XW;
+  sgemm(s, a2);
+  // KV latent: dkv_lat = [dk content | dv] . [KeyUp; ValueUp] -> dxa[:, lat:2lat]
+  GemmDesc a3 = linear_dx_desc(dkvu, ly.wkvu, dxa + lat, (int)N, lat, s->KVUW);
+  a3.ldc = XW;
+  sgemm(s, a3);
+  GemmDesc a4 = linear_dw_desc(dkvu, xa + lat, ly.gkvu, (int)N, lat, s->KVUW);
+  a4.ldb = XW;
+  sgemm(s, a4);
+  // the four projections of h
+  sgemm(s, linear_dx_desc(dxa, ly.wxa, dh, (int)N, C, XW));
+  sgemm(s, linear_dw_desc(dxa, h, ly.gxa, (int)N, C, XW));
 }
 
 // ---------------------------------------------------------------------------
@@ -545,8 +835,13 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
   float* dkn = A<float>(s, "dkn", N * s->KVW);
   float* dvv = A<float>(s, "dv", N * s->KVW);
   float* delta = A<float>(s, "delta", N * Hq);
-  float* dqkv = A<float>(s, "dqkv", N * s->QKVW);
-  float* dpre = A<float>(s, "dpre", N * Hkv);
+  float* dqkv = s->mla ? nullptr : A<float>(s, "dqkv", N * s->QKVW);
+  float* dpre = s->mla ? nullptr : A<float>(s, "dpre", N * Hkv);
+  double* dauxl = nullptr;
+  if (s->moe && s->bw > 0.f) {
+    dauxl = A<double>(s, "aux_loss", 1);
+    GN_HIP(hipMemsetAsync(dauxl, 0, sizeof(double), st));
+  }
   const int bk = L / 2;
   for (int l = L - 1; l >= 0; l--) {
     Layer& ly = s->layers[l];
@@ -555,13 +850,17 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
       launch_axpy(lg, g, gback, nullptr, 1.f, N * C, st);
       lgp = lg;
     }
-    // MLP (train.go:505-514): du = (lg . Wproj) * 2 relu(u); dh2 = du . Wfc
-    GemmDesc d1 = linear_dx_desc(lgp, ly.wproj, du, (int)N, F, C, EPI_DRELU2);
-    d1.aux = sb.u[l]; d1.ldaux = F;
-    sgemm(s, d1);
-    sgemm(s, linear_dw_desc(lgp, sb.act[l], ly.gproj, (int)N, F, C));
-    sgemm(s, linear_dx_desc(du, ly.wfc, dtmp, (int)N, C, F));
-    sgemm(s, linear_dw_desc(du, sb.h2[l], ly.gfc, (int)N, C, F));
+    if (s->moe) {
+      moe_ffn_backward(s, ly, sb.moe[l], lgp, sb.h2[l], sb.gu[l], sb.act[l], B, T, dtmp, dauxl);
+    } else {
+      // MLP (train.go:505-514): du = (lg . Wproj) * 2 relu(u); dh2 = du . Wfc
+      GemmDesc d1 = linear_dx_desc(lgp, ly.wproj, du, (int)N, F, C, EPI_DRELU2);
+      d1.aux = sb.u[l]; d1.ldaux = F;
+      sgemm(s, d1);
+      sgemm(s, linear_dw_desc(lgp, sb.act[l], ly.gproj, (int)N, F, C));
+      sgemm(s, linear_dx_desc(du, ly.wfc, dtmp, (int)N, C, F));
+      sgemm(s, linear_dw_desc(du, sb.h2[l], ly.gfc, (int)N, C, F));
+    }
     launch_rmsnorm_bwd(sb.mid[l], dtmp, lgp, N, C, gmid, st);
     // attention (train.go:198-427)
     float* dout = dtmp;  // [N, Hq*D] (Hq*D == C)
@@ -572,6 +871,10 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     fb.lse = sb.lse[l]; fb.delta = delta; fb.dq = dqn; fb.dk = dkn; fb.dv = dvv;
     fb.B = B; fb.T = T; fb.Hq = Hq; fb.Hkv = Hkv; fb.window = ly.window;
     launch_flash_bwd(fb, st);
+    float* dh = dout;  // reuse: dout no longer needed
+    if (s->mla) {
+      mla_backward(s, ly, sb.xa[l], sb.h[l], dqn, dkn, dvv, N, T, dh);
+    } else {
     QkvPostBwdArgs qb{};
     qb.dqn = dqn; qb.dkn = dkn; qb.dv = dvv; qb.qrot = sb.qrot[l]; qb.krot = sb.krot[l];
     qb.vesig = ly.has_ve ? sb.vesig[l] : nullptr;
@@ -579,10 +882,10 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     qb.Hq = Hq; qb.Hkv = Hkv; qb.R = s->R; qb.T = T;
     qb.dqkv = dqkv; qb.dpre = dpre; qb.gve = ly.gve;
     launch_qkv_post_bwd(qb, N, st);
-    float* dh = dout;  // reuse: dout no longer needed
     sgemm(s, linear_dx_desc(dqkv, ly.wqkv, dh, (int)N, C, s->QKVW));
     sgemm(s, linear_dw_desc(dqkv, sb.h[l], ly.gqkv, (int)N, C, s->QKVW));
     if (ly.has_ve) launch_ve_gate_bwd(dpre, sb.h[l], ly.wve, C, Hkv, N, ly.gwve, dh, part, st);
+    }
     launch_rmsnorm_bwd(sb.xb[l], dh, gmid, N, C, gb, st);
     // residual mixing (train_transformer.go:218-240)
     launch_dot_into_grad(gb, sb.xin[l], sb.x0, 1.f, N * C, s->grl + l, s->gx0l + l, part, st);
@@ -598,12 +901,15 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
   launch_rmsnorm_bwd(sb.raw, ge, nullptr, N, C, gb, st);
   launch_embed_scatter(gb, sb.ids, C, N, s->gwte, st);
 
-  double loss = 0;
+  double loss = 0, aux = 0;
   GN_HIP(hipMemcpyAsync(&loss, dloss, sizeof(double), hipMemcpyDeviceToHost, st));
+  if (dauxl) GN_HIP(hipMemcpyAsync(&aux, dauxl, sizeof(double), hipMemcpyDeviceToHost, st));
   if (nll_out) GN_HIP(hipMemcpyAsync(nll_out, nll, sizeof(float) * N, hipMemcpyDeviceToHost, st));
   if (s->timing) GN_HIP(hipEventRecord(ev1, st));
   GN_HIP(hipStreamSynchronize(st));
   if (loss_out) *loss_out = (float)loss;
+  // moe.go:313: weight * sum over sequences / sequences, summed over layers
+  s->aux_loss = dauxl ? (double)s->bw * aux / (double)B : 0.0;
   if (s->timing) {
     float ms = 0;
     GN_HIP(hipEventElapsedTime(&ms, ev0, ev1));
@@ -626,6 +932,75 @@ struct RowState {  // inference/engine.go:11-22
   bool completed = false;
 };
 
+// Absorbed decode weights (mla.go:233-273 folded): per query head h with KV
+// head kv, W_qabs[h] = KeyUp_kv^T . QueryUp_h ([lat, lat]: the content query
+// times the key up-projection, as a map of the query latent) and
+// W_comb[:, h] = Wo[:, h] . ValueUp_kv ([C, lat]: the value up-projection
+// followed by the output projection).
+static void prepare_decode_weights(gn_session* s) {
+  if (!s->mla || !s->derived_dirty) return;
+  const int lat = s->lat, cd = s->cd, Hq = s->Hq, ratio = s->Hq / s->Hkv, C = s->C;
+  for (int l = 0; l < s->L; l++) {
+    Layer& ly = s->layers[l];
+    const float* wku = ly.wkvu;
+    const float* wvu = ly.wkvu + (int64_t)s->Hkv * cd * lat;
+    for (int h = 0; h < Hq; h++) {
+      const int kv = h / ratio;
+      GemmDesc a;  // [rank][j] = sum_c KeyUp[kv*cd + c][rank] * QueryUp[h*cd + c][j]
+      a.M = lat; a.N = lat; a.K = cd;
+      a.A = wku + (int64_t)kv * cd * lat; a.lda = lat; a.a_kcontig = false;
+      a.B = ly.wqu + (int64_t)h * cd * lat; a.ldb = lat; a.b_kcontig = false;
+      a.C = ly.wqabs + (int64_t)h * lat * lat; a.ldc = lat;
+      gemm(a, s->stream, s->arena.get());
+      GemmDesc b;  // [c][h*lat + rank] = sum_d Wo[c][h*D + d] * ValueUp[kv*D + d][rank]
+      b.M = C; b.N = lat; b.K = HD;
+      b.A = ly.wo + (int64_t)h * HD; b.lda = C; b.a_kcontig = true;
+      b.B = wvu + (int64_t)kv * HD * lat; b.ldb = lat; b.b_kcontig = false;
+      b.C = ly.wcomb + (int64_t)h * lat; b.ldc = (int64_t)Hq * lat;
+      gemm(b, s->stream, s->arena.get());
+    }
+  }
+  s->derived_dirty = false;
+}
+
+// One absorbed-MLA decode layer (mlaForwardInference, mla.go:185-279) on
+// h; the attention output projection is added into x.
+static void mla_decode_layer(gn_session* s, const Layer& ly, int l, int rows, int pos, int maxSeq,
+                             const float* h, float* latc, float* rkc, float* x, const int* dpos) {
+  const int C = s->C, Hq = s->Hq, lat = s->lat;
+  hipStream_t st = s->stream;
+  float* xa = A<float>(s, "dec_xa", (size_t)rows * s->XW);
+  sgemm(s, linear_fwd_desc(h, ly.wxa, xa, rows, C, s->XW));
+  float* qabs = A<float>(s, "dec_qabs", (size_t)rows * Hq * lat);
+  GemmDesc gq = linear_fwd_desc(xa, ly.wqabs, qabs, rows, lat, Hq * lat);
+  gq.lda = s->XW;
+  sgemm(s, gq);
+  MlaDecodeArgs md{};
+  md.xa = xa; md.xw = s->XW; md.qabs = qabs;
+  md.qrope = A<float>(s, "dec_qrope", (size_t)rows * Hq * s->rd);
+  md.lat_cache = latc + (int64_t)l * rows * maxSeq * lat;
+  md.rk_cache = rkc + (int64_t)l * rows * maxSeq * s->Hkv * s->rd;
+  md.cosT = s->cosT; md.sinT = s->sinT;
+  md.out = A<float>(s, "dec_ol", (size_t)rows * Hq * lat);
+  md.part = A<float>(s, "dec_mlapart", (size_t)rows * ((maxSeq + 255) / 256) * Hq * (lat + 2));
+  md.rows = rows; md.Hq = Hq; md.Hkv = s->Hkv; md.lat = lat; md.rd = s->rd;
+  md.maxSeq = maxSeq; md.window = ly.window; md.pos = pos; md.pos_dev = dpos;
+  if (s->timing && !s->capturing) {
+    hipEvent_t e0 = next_event(s), e1 = next_event(s);
+    GN_HIP(hipEventRecord(e0, st));
+    launch_mla_decode(md, st);
+    GN_HIP(hipEventRecord(e1, st));
+    s->attn_events.push_back({e0, e1});
+    const int keys = pos + 1 - std::max(0, pos - ly.window);
+    s->attn_ev_bytes.push_back((double)rows * keys * (lat + s->Hkv * s->rd) * 4.0);
+  } else {
+    launch_mla_decode(md, st);
+  }
+  GemmDesc go = linear_fwd_desc(md.out, ly.wcomb, x, rows, Hq * lat, C, EPI_ADD_SRC);
+  go.aux = x; go.ldaux = C;
+  sgemm(s, go);
+}
+
 // One decode forward: tokens dtok at position pos -> logits.  With dpos set
 // the position is read on the device (the step is captured once and
 // replayed).
@@ -637,17 +1012,22 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   float* x0 = A<float>(s, "dec_x0", (size_t)rows * C);
   float* h = A<float>(s, "dec_h", (size_t)rows * C);
   float* prev = A<float>(s, "dec_prev", (size_t)rows * C);
-  float* qkv = A<float>(s, "dec_qkv", (size_t)rows * s->QKVW);
-  float* q = A<float>(s, "dec_q", (size_t)rows * Hq * HD);
-  float* o = A<float>(s, "dec_o", (size_t)rows * Hq * HD);
+  float* qkv = s->mla ? nullptr : A<float>(s, "dec_qkv", (size_t)rows * s->QKVW);
+  float* q = s->mla ? nullptr : A<float>(s, "dec_q", (size_t)rows * Hq * HD);
+  float* o = s->mla ? nullptr : A<float>(s, "dec_o", (size_t)rows * Hq * HD);
   float* act = A<float>(s, "dec_act", (size_t)rows * F);
   float* back = A<float>(s, "dec_back", (size_t)rows * C);
-  float* part = A<float>(s, "dec_part", (size_t)rows * Hkv * ((maxSeq + 63) / 64) * (Hq / Hkv) * (HD + 2));
+  float* part = s->mla ? nullptr
+                       : A<float>(s, "dec_part", (size_t)rows * Hkv * ((maxSeq + 63) / 64) *
+                                                     (Hq / Hkv) * (HD + 2));
   launch_embed_decode(dtok, s->wte, s->smg, s->sml, rows, C, prev, x, x0, st);
   const int bk = L / 2;
   for (int l = 0; l < L; l++) {
     Layer& ly = s->layers[l];
     launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st);
+    if (s->mla) {
+      mla_decode_layer(s, ly, l, rows, pos, maxSeq, h, kc, vc, x, dpos);
+    } else {
     sgemm(s, linear_fwd_desc(h, ly.wqkv, qkv, rows, C, s->QKVW));
     QkvPostArgs qa{};
     qa.qkv = qkv; qa.h = h; qa.ids = dtok;
@@ -681,7 +1061,15 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     GemmDesc go = linear_fwd_desc(o, ly.wo, x, rows, Hq * HD, C, EPI_ADD_SRC);
     go.aux = x; go.ldaux = C;
     sgemm(s, go);
+    }
     launch_norm_rows(x, nullptr, nullptr, rows, C, nullptr, h, st);
+    if (s->moe) {
+      float* gu = A<float>(s, "dec_gu", (size_t)rows * 2 * F);
+      MoeBuffers mb = moe_buffers(s, "dec_moe_", rows);
+      moe_ffn_forward(s, ly, x, h, rows, gu, act, mb, x);
+      if (l == bk) GN_HIP(hipMemcpyAsync(back, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
+      continue;
+    }
     GemmDesc gf = linear_fwd_desc(h, ly.wfc, act, rows, C, F, EPI_RELU2_SAVE);
     sgemm(s, gf);
     GemmDesc gp = linear_fwd_desc(act, ly.wproj, x, rows, F, C, EPI_ADD_SRC);
@@ -719,8 +1107,13 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   SeqBuffers sb;
   sb.B = G; sb.T = P; sb.N = (int64_t)G * P;
   sb.ids = upload_ids(s, "pf_ids", prompts, sb.N, V);
-  float* kpf = A<float>(s, "pf_k", (size_t)L * G * Hkv * P * HD);
-  float* vpf = A<float>(s, "pf_v", (size_t)L * G * Hkv * P * HD);
+  prepare_decode_weights(s);
+  // dense: K and V [L][G][Hkv][P][D]; MLA: latent [L][G][P][lat] and rotary
+  // keys [L][G][P][Hkv*rd]
+  const size_t kw = s->mla ? (size_t)s->lat : (size_t)Hkv * HD;
+  const size_t vw = s->mla ? (size_t)Hkv * s->rd : (size_t)Hkv * HD;
+  float* kpf = A<float>(s, "pf_k", (size_t)L * G * P * kw);
+  float* vpf = A<float>(s, "pf_v", (size_t)L * G * P * vw);
   seq_forward(s, sb, SEQ_PREFILL, kpf, vpf);
   // last-position logits of each prompt, expanded to its S rows (engine.go:182-191)
   float* lastfn = A<float>(s, "pf_lastfn", (size_t)rows * C);
@@ -729,9 +1122,16 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   sgemm(s, linear_fwd_desc(lastfn, s->lm, logits, rows, C, V, EPI_SOFTCAP));
   // 2) PrefillFrom (kvcache.go:383-448): replicate KV and the smear state
   const int maxSeq = W;
-  float* kc = A<float>(s, "kv_k", (size_t)L * rows * Hkv * maxSeq * HD);
-  float* vc = A<float>(s, "kv_v", (size_t)L * rows * Hkv * maxSeq * HD);
+  float* kc = A<float>(s, "kv_k", (size_t)L * rows * maxSeq * kw);
+  float* vc = A<float>(s, "kv_v", (size_t)L * rows * maxSeq * vw);
   for (int l = 0; l < L; l++) {
+    if (s->mla) {
+      launch_replicate_rows(kpf + (int64_t)l * G * P * kw, kc + (int64_t)l * rows * maxSeq * kw, G,
+                            S, P, (int)kw, P, maxSeq, st);
+      launch_replicate_rows(vpf + (int64_t)l * G * P * vw, vc + (int64_t)l * rows * maxSeq * vw, G,
+                            S, P, (int)vw, P, maxSeq, st);
+      continue;
+    }
     launch_replicate_kv(kpf + (int64_t)l * G * Hkv * P * HD, kc + (int64_t)l * rows * Hkv * maxSeq * HD,
                         G, S, Hkv, P, P, maxSeq, st);
     launch_replicate_kv(vpf + (int64_t)l * G * Hkv * P * HD, vc + (int64_t)l * rows * Hkv * maxSeq * HD,
@@ -904,6 +1304,7 @@ int gn_session_destroy(gn_session* s) {
     (void)hipFree(s->grads);
     (void)hipFree(s->cosT);
     (void)hipFree(s->sinT);
+    if (s->derived) (void)hipFree(s->derived);
     (void)hipStreamDestroy(s->stream);
     delete s;
   });
@@ -951,6 +1352,7 @@ int gn_session_set_params(gn_session* s, const float* params, int64_t count) {
   return guard([&] {
     GN_CHECK(s && params, "null argument");
     copy_params(s, const_cast<float*>(params), count, true, false);
+    s->derived_dirty = true;
   });
 }
 int gn_session_get_params(const gn_session* s, float* params, int64_t count) {
@@ -1108,6 +1510,12 @@ int gn_session_set_decode_graph(gn_session* s, int enabled) {
   return guard([&] {
     GN_CHECK(s, "null session");
     s->decode_graph = enabled != 0;
+  });
+}
+int gn_session_aux_loss(const gn_session* s, double* out) {
+  return guard([&] {
+    GN_CHECK(s && out, "null argument");
+    *out = s->aux_loss;
   });
 }
 int gn_session_synchronize(gn_session* s) {

@@ -21,7 +21,10 @@ class Session:
         cfg.validate()
         self.cfg = cfg
         self._c = GnConfig(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head,
-                           cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern.encode())
+                           cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern.encode(),
+                           cfg.mla_latent, cfg.mla_rope_dimension if cfg.mla else 0,
+                           cfg.n_experts, cfg.experts_per_token, cfg.expert_hidden,
+                           cfg.shared_hidden, cfg.moe_clamp, cfg.moe_scale, cfg.balance_weight)
         h = C.c_void_p()
         call("gn_session_create", C.byref(self._c), device, C.byref(h))
         self._h = h
@@ -118,6 +121,13 @@ class Session:
     # -- timing ---------------------------------------------------------------
     def set_timing(self, enabled: bool):
         call("gn_session_set_timing", self._h, 1 if enabled else 0)
+
+    def aux_loss(self) -> float:
+        """Transformer.AuxiliaryLoss: the MoE balance loss of the last
+        policy-gradient step (model/transformer.go:108-116)."""
+        v = C.c_double()
+        call("gn_session_aux_loss", self._h, C.byref(v))
+        return v.value
 
     def synchronize(self):
         """Waits until the session stream is idle."""

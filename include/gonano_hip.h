@@ -139,7 +139,17 @@ int gn_attention_combine(const float *const *accumulators, const float *const *m
                          int64_t head_dim, float *output, float *log_sum_exp);
 
 /* ---- Session: device-resident model for the fused RL step --------------- */
-/* model.Config (model/config.go:9-124), dense preset fields. */
+/* model.Config (model/config.go:9-124): the dense fields, then the latent
+ * preset's (model/preset.go:120-129) with resolved values; zeros keep the
+ * dense model.  mla_latent > 0 selects absorbed multi-head latent attention
+ * (Config.MLALatent) with mla_rope_dims decoupled rotary dims
+ * (Config.MLARotaryDimension()); n_experts > 0 selects the DeepSeekMoE
+ * feed-forward: a clamped-SwiGLU shared expert of shared_hidden plus
+ * n_experts routed experts of expert_hidden, experts_per_token chosen per
+ * token, outputs scaled by moe_scale, SwiGLU clamp moe_clamp and the
+ * sequence-level balance loss weight balance_weight
+ * (Config.MoEActiveExperts / MoEExpertHidden / MoESharedHidden /
+ * MoEEffectiveScale / MoEEffectiveClamp / MoEBalanceLossWeight). */
 typedef struct gn_config {
   int32_t sequence_len;
   int32_t vocab_size;
@@ -149,6 +159,15 @@ typedef struct gn_config {
   int32_t n_embd;
   int32_t rotary_dims;
   char window_pattern[16];
+  int32_t mla_latent;
+  int32_t mla_rope_dims;
+  int32_t n_experts;
+  int32_t experts_per_token;
+  int32_t expert_hidden;
+  int32_t shared_hidden;
+  float moe_clamp;
+  float moe_scale;
+  float balance_weight;
 } gn_config;
 
 typedef struct gn_session gn_session;
@@ -230,6 +249,11 @@ int gn_session_get_timing(const gn_session *session, gn_timing *out);
  * every step.  Results are identical either way.  No reference counterpart
  * (an execution knob of this backend). */
 int gn_session_set_decode_graph(gn_session *session, int enabled);
+/* Transformer.AuxiliaryLoss (model/transformer.go:108-116): the MoE
+ * sequence-level balance loss of the most recent gn_policy_gradient_step /
+ * gn_rl_step (0 without MoE); its gradient is already in the session's
+ * parameter gradients. */
+int gn_session_aux_loss(const gn_session *session, double *out);
 /* Waits until the session stream is idle (no reference counterpart: the Go
  * backends are synchronous; used to bracket timed regions). */
 int gn_session_synchronize(gn_session *session);
