@@ -32,6 +32,8 @@ WORKLOADS = {
     # name: (config factory, groups, prompt len, samples, new tokens, temperature, reward p)
     "d12": ("dense_d12", 16, 256, 16, 256, 1.0, 0.3),
     "d2": ("dense_d2", 4, 32, 8, 24, 1.0, 0.3),
+    # BASELINE configs[3] (the group split is unspecified there: 16 x 16 as d12)
+    "latent_d12": ("latent_d12", 16, 256, 16, 256, 1.0, 0.3),
 }
 
 
@@ -51,9 +53,7 @@ def cpu_baseline(cfg, w, prompts, S: int, N: int, temp: float) -> dict:
     same unit and the same prefill/decode mix as the GPU's value."""
     from oracle import oracle as O
     STEPS = 128  # about 15 s of CPU work on the GPU box's 16 host threads
-    shape = O.ModelShape(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head,
-                         cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern)
-    m = O.OracleModel(shape, w)
+    m = O.OracleModel(O.ModelShape.from_config(cfg), w)
     P = prompts.shape[1]
     t0 = time.perf_counter()
     m.generate_batch(prompts[0], S, 1, temp, 50, 0)
@@ -178,11 +178,15 @@ def main() -> int:
         "data": "synthetic (uniform prompt ids, InitWeights-distributed random weights, "
                 "Bernoulli rewards)",
         "config": {
-            "workload": f"{args.config} dense RL step: {groups} prompts x {S} samples, "
+            "workload": f"{args.config} RL step: {groups} prompts x {S} samples, "
                         f"{P} prompt + {N} new tokens, T={temp}, top-k 50, "
                         f"Bernoulli({reward_p}) rewards, recompute + PG fwd/bwd, no optimizer",
-            "model": f"dense depth {cfg.n_layer} d_model {cfg.n_embd} heads {cfg.n_head}/"
-                     f"{cfg.n_kv_head} vocab {cfg.vocab_size}",
+            "model": (f"{'latent' if cfg.mla else 'dense'} depth {cfg.n_layer} d_model "
+                      f"{cfg.n_embd} heads {cfg.n_head}/{cfg.n_kv_head} vocab {cfg.vocab_size}"
+                      + (f" MLA latent {cfg.mla_latent} rope {cfg.mla_rope_dimension}"
+                         if cfg.mla else "")
+                      + (f" MoE 1 shared + {cfg.n_experts} routed x {cfg.expert_hidden}, "
+                         f"top-{cfg.experts_per_token}" if cfg.moe else "")),
             "rollouts": groups * S, "global_batch": groups * S, "seq_len": P + N,
             "parallelism": "single GPU",
             "rollout_ms": round(sum(roll_ms) / len(roll_ms), 2),

@@ -269,8 +269,8 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
     m0 = p.goff[g] + mt * BM;
     p.M = p.goff[g + 1];
     p.B += g * p.gstride;
-    kbeg = 0;
-    kend = p.K;
+    kbeg = split * p.k_per_split;  // optional split-K (small decode groups)
+    kend = min(p.K, kbeg + p.k_per_split);
   } else if constexpr (GRP == GEMM_GROUP_K) {
     // The reduction runs over one group's rows; group g owns C + g*gstride.
     kbeg = p.goff[split];
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
             acc[i][j][r] += red[((((v - 1) * WM * WN + wmn) * MI + i) * NI + j) * 256 + r * 64 + lane];
   }
   // D of a 16x16 block: lane holds column (lane & 15), rows 4*(lane>>4)+r.
-  if (GRP != GEMM_GROUP_NONE || p.splits == 1) {
+  if (GRP == GEMM_GROUP_K || p.splits == 1) {
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
@@ -403,7 +403,8 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
     return;
   }
   // Split-K: this workgroup's partial sums; gemm_reduce_kernel adds them.
-  float* mine = p.part + (int64_t)split * p.M * p.N;
+  // (rows mode: p.M is this group's end row; the partial buffer spans all rows)
+  float* mine = p.part + (int64_t)split * p0.M * p.N;
 #pragma unroll
   for (int i = 0; i < MI; i++)
 #pragma unroll
@@ -462,8 +463,10 @@ static void launch_grouped(const GemmParams& p, bool ak, bool bk, bool vec, hipS
   GemmParams q = p;
   q.tiles_m = GRP == GEMM_GROUP_ROWS ? (int)ceil_div(p.M, BM) + p.groups : (int)ceil_div(p.M, BM);
   q.tiles_n = (int)ceil_div(p.N, BN);
-  q.splits = GRP == GEMM_GROUP_K ? p.groups : 1;
-  q.k_per_split = p.K;
+  if (GRP == GEMM_GROUP_K) {
+    q.splits = p.groups;
+    q.k_per_split = p.K;
+  }
   dim3 grid(q.tiles_m * q.tiles_n * q.splits);
   dim3 block(64 * WM * WN * WK);
 #define GN_GEMM_LAUNCH(AK, BK, V) \
@@ -505,14 +508,37 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     p.groups = d.groups;
     p.gstride = d.group_stride;
     p.splits = 1;
+    p.k_per_split = d.K;
     if (d.group == GEMM_GROUP_ROWS) {
       // per-group tiles: large tiles once the average group fills them
-      if (d.M / d.groups >= 1024)
+      if (d.M / d.groups >= 1024) {
         launch_grouped<128, 128, 2, 2, 1, 2, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig,
                                                                      vec, st);
-      else
-        launch_grouped<64, 64, 2, 2, 2, 4, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig,
-                                                                   vec, st);
+        return;
+      }
+      // Small groups (decode: tens of rows per expert) stream each expert's
+      // weights once; split K so that enough workgroups keep loads in flight
+      // (about 2 per CU), summed by gemm_reduce_kernel.
+      const int64_t tiles = (ceil_div(d.M, 64) + d.groups) * ceil_div(d.N, 64);
+      int splits = 1;
+      if (tiles < 2 * 256 && d.K >= 256)
+        splits = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(2 * 256, tiles), d.K / 128));
+      const int kps = (int)ceil_div(ceil_div(d.K, splits), GK) * GK;
+      splits = (int)ceil_div(d.K, kps);
+      p.k_per_split = kps;
+      p.splits = splits;
+      if (splits > 1) {
+        GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
+        p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
+      }
+      launch_grouped<64, 64, 2, 2, 2, 4, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig, vec,
+                                                                 st);
+      if (splits > 1) {
+        const int64_t total = (int64_t)d.M * d.N;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
+                           st, p);
+        GN_HIP(hipGetLastError());
+      }
     } else {
       // K mode: a group's whole row range per workgroup, two-level summation
       launch_grouped<128, 128, 2, 2, 1, 2, true, GEMM_GROUP_K>(p, d.a_kcontig, d.b_kcontig, vec,

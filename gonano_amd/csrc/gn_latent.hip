@@ -156,10 +156,13 @@ __global__ __launch_bounds__(256) void mla_decode_prep_kernel(MlaDecodeArgs a) {
 // value is [latent | 0], mla.go:249-259).  Each wave streams a contiguous
 // quarter of the split once, with an online softmax over chunks of 4 keys:
 // lane l holds latent float4 l and rotary-key float4 l of a key, partial
-// dot products are wave-reduced per head.  Waves are merged in LDS; a
-// split covering the whole range writes the normalized latent output,
-// otherwise (sum, max, total) for mla_decode_combine_kernel.
-static constexpr int MLA_KPS = 256;  // keys per split
+// dot products are wave-reduced per head; the next chunk's rows are loaded
+// before the current chunk is reduced.  Waves are merged in LDS; a split
+// covering the whole range writes the normalized latent output, otherwise
+// (sum, max, total) for mla_decode_combine_kernel.  Splits are short (64
+// keys) so a decode step has several workgroups per CU in flight: the
+// kernel is bound by how many cache rows are being fetched at once.
+static constexpr int MLA_KPS = 64;  // keys per split
 static constexpr int MLA_MAXLAT = 256;
 
 __host__ __device__ inline void mla_split(int kstart, int kend, int* kps, int* nsplit) {
@@ -172,6 +175,7 @@ __host__ __device__ inline void mla_split(int kstart, int kend, int* kps, int* n
 template <int NH>
 __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
   __shared__ __attribute__((aligned(16))) float wacc[4][NH][MLA_MAXLAT];
+  static_assert(MLA_KPS % 4 == 0, "split length");
   __shared__ float wm[4][NH], ws[4][NH];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int row = blockIdx.x, split = blockIdx.y;
@@ -207,14 +211,24 @@ __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
   const float* rbase = a.rk_cache + (int64_t)row * a.maxSeq * a.Hkv * a.rd + 4 * lane;
   const int64_t lstride = a.lat, rstride = (int64_t)a.Hkv * a.rd;
   constexpr int CH = 4;
+  v4f Ln[CH], Kn[CH];
+  auto fetch = [&](int jb) {
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      const int j = min(jb + u, j1 - 1);  // clamp: duplicates are not accumulated
+      Ln[u] = has_lat ? *reinterpret_cast<const v4f*>(lbase + j * lstride) : (v4f){0, 0, 0, 0};
+      Kn[u] = has_rk ? *reinterpret_cast<const v4f*>(rbase + j * rstride) : (v4f){0, 0, 0, 0};
+    }
+  };
+  if (j0 < j1) fetch(j0);
   for (int jb = j0; jb < j1; jb += CH) {
     v4f L[CH], K[CH];
 #pragma unroll
     for (int u = 0; u < CH; u++) {
-      const int j = min(jb + u, j1 - 1);  // clamp: duplicates are not accumulated
-      L[u] = has_lat ? *reinterpret_cast<const v4f*>(lbase + j * lstride) : (v4f){0, 0, 0, 0};
-      K[u] = has_rk ? *reinterpret_cast<const v4f*>(rbase + j * rstride) : (v4f){0, 0, 0, 0};
+      L[u] = Ln[u];
+      K[u] = Kn[u];
     }
+    if (jb + CH < j1) fetch(jb + CH);
     float sc[CH][NH];
 #pragma unroll
     for (int u = 0; u < CH; u++)
@@ -302,6 +316,12 @@ __global__ __launch_bounds__(256) void mla_decode_combine_kernel(MlaDecodeArgs a
   }
 }
 
+int mla_decode_max_splits(int window, int maxSeq) {
+  int kps, ns;
+  mla_split(0, std::min(window, maxSeq - 1) + 1, &kps, &ns);
+  return ns;
+}
+
 void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
   GN_CHECK(a.lat % 4 == 0 && a.lat <= MLA_MAXLAT, "mla decode: latent width must be a multiple "
                                                   "of 4 and at most 256");
@@ -313,6 +333,8 @@ void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
   // the longest key range a step of this launch can have
   mla_split(0, std::min(a.window, pos_max) + 1, &kps, &ns_max);
   a.nsplit_max = ns_max;
+  GN_CHECK(a.part_splits >= ns_max, "mla decode: split buffer too small");
+  GN_CHECK(a.pos_dev || a.pos < a.maxSeq, "mla decode: position outside the cache");
   hipLaunchKernelGGL(mla_decode_prep_kernel, dim3(a.rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
   const dim3 grid(a.rows, ns_max);
@@ -406,37 +428,50 @@ static constexpr int MOE_MAXE = 64;
 static constexpr int MOE_MAXK = 8;
 static constexpr int MOE_PB = 256;  // (token, slot) pairs per placement block
 
-// One thread per token: SoftmaxLastDim of the router logits (float64 total,
-// p = float32(exp) * float32(1/total)), top-k of logits + bias (largest first,
-// ties to the smaller index), weights = probs of the chosen experts.
-__global__ void moe_gate_kernel(const float* __restrict__ logits, const float* __restrict__ bias,
-                                int64_t rows, int E, int K, float* __restrict__ probs,
-                                int32_t* __restrict__ sel, float* __restrict__ w) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// One wave per token, lane e = expert e: SoftmaxLastDim of the router
+// logits (float64 total, p = float32(exp) * float32(1/total)), top-k of
+// logits + bias (largest first, ties to the smaller index), weights = the
+// chosen experts' probabilities.
+__global__ __launch_bounds__(256) void moe_gate_kernel(const float* __restrict__ logits,
+                                                       const float* __restrict__ bias,
+                                                       int64_t rows, int E, int K,
+                                                       float* __restrict__ probs,
+                                                       int32_t* __restrict__ sel,
+                                                       float* __restrict__ w) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
-  const float* lg = logits + r * E;
-  float mx = lg[0];
-  for (int e = 1; e < E; e++) mx = lg[e] > mx ? lg[e] : mx;
-  double tot = 0.0;
-  float pr[MOE_MAXE], work[MOE_MAXE];
-  for (int e = 0; e < E; e++) {
-    const double x = exp((double)(lg[e] - mx));
-    pr[e] = (float)x;
-    tot += x;
-    work[e] = lg[e] + bias[e];
-  }
+  const bool on = lane < E;
+  const float lg = on ? logits[r * E + lane] : -INFINITY;
+  float mx = lg;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  const double x = on ? exp((double)(lg - mx)) : 0.0;
+  double tot = x;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
   const float inv = (float)(1.0 / tot);
-  for (int e = 0; e < E; e++) {
-    pr[e] = pr[e] * inv;
-    probs[r * E + e] = pr[e];
-  }
+  const float pr = (float)x * inv;
+  if (on) probs[r * E + lane] = pr;
+  float work = on ? lg + bias[lane] : -INFINITY;
   for (int k = 0; k < K; k++) {
-    int best = 0;
-    for (int e = 1; e < E; e++)
-      if (work[e] > work[best]) best = e;
-    sel[r * K + k] = best;
-    w[r * K + k] = pr[best];
-    work[best] = -INFINITY;
+    // largest value, smallest index among equals
+    float bv = work;
+    int bi = on ? lane : 64;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (lane == bi) {
+      sel[r * K + k] = bi;
+      w[r * K + k] = pr;
+      work = -INFINITY;
+    }
   }
 }
 
@@ -502,31 +537,29 @@ __global__ void moe_scan_kernel(int* __restrict__ blockcnt, int nblk, int E,
 __global__ __launch_bounds__(MOE_PB) void moe_place_kernel(MoePlaceArgs a) {
   __shared__ int wcnt[4][MOE_MAXE];
   __shared__ int cnt[MOE_MAXE];
-  __shared__ int spos[MOE_PB];
-  __shared__ int srow[MOE_PB];
   const int64_t p = (int64_t)blockIdx.x * MOE_PB + threadIdx.x;
   const bool valid = p < a.npairs;
   const int e = valid ? a.sel[p] : -1;
   const int rank = block_rank(e, valid, a.E, cnt, wcnt);
-  int pos = -1;
   if (valid) {
-    pos = a.off[e] + a.blockoff[(int64_t)blockIdx.x * a.E + e] + rank;
+    const int pos = a.off[e] + a.blockoff[(int64_t)blockIdx.x * a.E + e] + rank;
     a.perm_row[pos] = (int)(p / a.K);
     a.perm_w[pos] = a.w[p];
     a.inv[p] = pos;
   }
-  spos[threadIdx.x] = pos;
-  srow[threadIdx.x] = valid ? (int)(p / a.K) : -1;
-  __syncthreads();
-  // gather: each wave copies 64 pairs' rows, float4 per lane
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int c4 = a.C / 4;
-  for (int i = wid * 64; i < wid * 64 + 64; i++) {
-    if (srow[i] < 0) break;
-    const v4f* src = reinterpret_cast<const v4f*>(a.x + (int64_t)srow[i] * a.C);
-    v4f* dst = reinterpret_cast<v4f*>(a.xg + (int64_t)spos[i] * a.C);
-    for (int c = lane; c < c4; c += 64) dst[c] = src[c];
-  }
+}
+
+// xg[pos] = x[perm_row[pos]], one wave per gathered row.
+__global__ __launch_bounds__(256) void moe_gather_kernel(const float* __restrict__ x,
+                                                         const int* __restrict__ perm_row,
+                                                         int64_t npairs, int C,
+                                                         float* __restrict__ xg) {
+  const int lane = threadIdx.x & 63;
+  const int64_t pos = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pos >= npairs) return;
+  const v4f* src = reinterpret_cast<const v4f*>(x + (int64_t)perm_row[pos] * C);
+  v4f* dst = reinterpret_cast<v4f*>(xg + pos * C);
+  for (int c = lane; c < C / 4; c += 64) dst[c] = src[c];
 }
 
 void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
@@ -534,7 +567,7 @@ void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
   GN_CHECK(a.C % 4 == 0, "moe: model width must be a multiple of 4");
   const int64_t npairs = a.rows * a.K;
   if (a.rows <= 0) return;
-  hipLaunchKernelGGL(moe_gate_kernel, dim3((unsigned)ceil_div(a.rows, 256)), dim3(256), 0, st,
+  hipLaunchKernelGGL(moe_gate_kernel, dim3((unsigned)ceil_div(a.rows, 4)), dim3(256), 0, st,
                      a.logits, a.bias, a.rows, a.E, a.K, a.probs, a.sel, a.w);
   GN_HIP(hipGetLastError());
   const int nblk = (int)ceil_div(npairs, MOE_PB);
@@ -548,6 +581,9 @@ void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
   pa.npairs = npairs; pa.K = a.K; pa.E = a.E; pa.C = a.C;
   pa.perm_row = a.perm_row; pa.perm_w = a.perm_w; pa.inv = a.inv; pa.xg = a.xg;
   hipLaunchKernelGGL(moe_place_kernel, dim3(nblk), dim3(MOE_PB), 0, st, pa);
+  GN_HIP(hipGetLastError());
+  hipLaunchKernelGGL(moe_gather_kernel, dim3((unsigned)ceil_div(npairs, 4)), dim3(256), 0, st, a.x,
+                     a.perm_row, npairs, a.C, a.xg);
   GN_HIP(hipGetLastError());
 }
 

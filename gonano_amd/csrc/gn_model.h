@@ -176,8 +176,12 @@ struct MlaDecodeArgs {
   int rows, Hq, Hkv, lat, rd, maxSeq, window;
   int pos;            // query position (eager launches)
   const int* pos_dev; // when set, the position is read on the device
+  int part_splits;    // splits the part buffer holds per row
   int nsplit_max;     // set by the launcher
 };
+// Largest number of key splits a decode step with this window and cache
+// length can use (sizes MlaDecodeArgs::part).
+int mla_decode_max_splits(int window, int maxSeq);
 void launch_mla_decode(MlaDecodeArgs a, hipStream_t st);
 void launch_replicate_rows(const float* src, float* dst, int G, int S, int P, int W, int maxSrc,
                            int maxDst, hipStream_t st);

@@ -982,7 +982,8 @@ static void mla_decode_layer(gn_session* s, const Layer& ly, int l, int rows, in
   md.rk_cache = rkc + (int64_t)l * rows * maxSeq * s->Hkv * s->rd;
   md.cosT = s->cosT; md.sinT = s->sinT;
   md.out = A<float>(s, "dec_ol", (size_t)rows * Hq * lat);
-  md.part = A<float>(s, "dec_mlapart", (size_t)rows * ((maxSeq + 255) / 256) * Hq * (lat + 2));
+  md.part_splits = mla_decode_max_splits(maxSeq, maxSeq);
+  md.part = A<float>(s, "dec_mlapart", (size_t)rows * md.part_splits * Hq * (lat + 2));
   md.rows = rows; md.Hq = Hq; md.Hkv = s->Hkv; md.lat = lat; md.rd = s->rd;
   md.maxSeq = maxSeq; md.window = ly.window; md.pos = pos; md.pos_dev = dpos;
   if (s->timing && !s->capturing) {
