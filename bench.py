@@ -208,7 +208,9 @@ def main() -> int:
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "launches": attn_n,
             "avg_launch_ms": round(attn_ms / max(attn_n, 1), 5),
-            "measured_on": "an extra untimed rollout of the workload with per-launch events",
+            "measured_on": "an extra untimed rollout of the workload: HIP events around a "
+                           "burst of 4 back-to-back launches of every step's attention call "
+                           "(the kernels' own duration, as rocprof reports it)",
         },
     }
     if not args.no_cpu_baseline:

@@ -66,11 +66,7 @@ __device__ __forceinline__ DecSplit dec_split(const DecodeAttnArgs& a) {
   return dec_split(max(0, pos - a.window), pos + 1);
 }
 
-__device__ __forceinline__ float red8_sum(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  return v + __shfl_xor(v, 4, 64);
-}
+__device__ __forceinline__ float red8_sum(float v) { return sum8_dpp(v); }
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

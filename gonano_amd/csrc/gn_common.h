@@ -100,6 +100,33 @@ __device__ __forceinline__ float block_max(float v, float* scratch) {
   return t;
 }
 
+// Cross-lane sums inside groups of 8 / 16 lanes with DPP (no LDS traffic,
+// unlike __shfl_xor, which lowers to ds_bpermute): quad_perm [1,0,3,2] and
+// [2,3,0,1] give each quad its sum, row_half_mirror adds the other quad of
+// the 8-lane half-row, row_mirror the other half of the 16-lane row.  Every
+// lane ends with the same value (each step adds two equal partial sums in
+// either order).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float sum8_dpp(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  return v + dpp_f32<0x141>(v);  // row_half_mirror
+}
+__device__ __forceinline__ float sum16_dpp(float v) {
+  v = sum8_dpp(v);
+  return v + dpp_f32<0x140>(v);  // row_mirror
+}
+__device__ __forceinline__ float max16_dpp(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  return fmaxf(v, dpp_f32<0x140>(v));
+}
+
 // Softcap (model/transformer.go:11, tensors/math.go:38-45):
 // 15 * tanh(y * float32(1/15)).
 __device__ __forceinline__ float softcap15(float y) {

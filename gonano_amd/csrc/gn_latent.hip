@@ -153,17 +153,23 @@ __global__ __launch_bounds__(256) void mla_decode_prep_kernel(MlaDecodeArgs a) {
 // Absorbed attention for one row and one split of its key range, all NH
 // query heads at once: score(h, j) = q_abs[h] . lat[j] + q_rope[h] .
 // rk[j][kv(h)], softmax over the keys, out[h] = sum_j p(h, j) lat[j] (the
-// value is [latent | 0], mla.go:249-259).  Each wave streams a contiguous
-// quarter of the split once, with an online softmax over chunks of 4 keys:
-// lane l holds latent float4 l and rotary-key float4 l of a key, partial
-// dot products are wave-reduced per head; the next chunk's rows are loaded
-// before the current chunk is reduced.  Waves are merged in LDS; a split
-// covering the whole range writes the normalized latent output, otherwise
-// (sum, max, total) for mla_decode_combine_kernel.  Splits are short (64
-// keys) so a decode step has several workgroups per CU in flight: the
-// kernel is bound by how many cache rows are being fetched at once.
+// value is [latent | 0], mla.go:249-259).  Three phases, as the dense decode
+// kernel:
+//  1. scores: each 16-lane quarter-wave takes one key at a time (keys qw,
+//     qw + 16, ... of the split), lane l holds latent float4s l + 16c and
+//     rotary-key float4 l of kv head c (rotary width 64: 16 float4 per kv
+//     head), the next key is fetched while the current one is reduced
+//     (16-lane DPP sums); scores go to LDS;
+//  2. softmax per head over the split;
+//  3. P.V: wave w takes keys w, w + 4, ...; lane l accumulates latent float4
+//     l for every head (the rows were just read, so they come from L2);
+//     waves are added in LDS.
+// A split covering the whole range writes the normalized latent output,
+// otherwise (sum, max, total) for mla_decode_combine_kernel.  Splits are
+// short (64 keys) so a decode step has several workgroups per CU in flight.
 static constexpr int MLA_KPS = 64;  // keys per split
 static constexpr int MLA_MAXLAT = 256;
+static constexpr int MLA_RD = 64;   // rotary width the kernel is laid out for
 
 __host__ __device__ inline void mla_split(int kstart, int kend, int* kps, int* nsplit) {
   const int n = kend - kstart;
@@ -174,121 +180,152 @@ __host__ __device__ inline void mla_split(int kstart, int kend, int* kps, int* n
 
 template <int NH>
 __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
+  __shared__ float sc[NH][MLA_KPS];
   __shared__ __attribute__((aligned(16))) float wacc[4][NH][MLA_MAXLAT];
-  static_assert(MLA_KPS % 4 == 0, "split length");
-  __shared__ float wm[4][NH], ws[4][NH];
+  __shared__ float wred[4][NH];
+  __shared__ float stat[2][NH];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int qw = tid >> 4, l16 = tid & 15;
   const int row = blockIdx.x, split = blockIdx.y;
   const int pos = decode_pos(a);
   const int kstart = max(0, pos - a.window), kend = pos + 1;
   int kps, nsplit;
   mla_split(kstart, kend, &kps, &nsplit);
   if (split >= nsplit) return;  // graph launches size the grid for the longest range
-  const int ks = kstart + split * kps, ke = min(kend, ks + kps);
-  const int nk = ke - ks;
-  const int q4 = (nk + 3) / 4;
-  const int j0 = ks + wid * q4, j1 = min(ke, j0 + q4);
+  const int ks = kstart + split * kps;
+  const int nk = min(kend, ks + kps) - ks;
   const int ratio = NH / a.Hkv;
-  const bool has_lat = lane * 4 < a.lat;
-  const bool has_rk = lane * 4 < a.Hkv * a.rd;
-  const int my_kv = (lane * 4) / a.rd;  // kv head of this lane's rotary float4
+  const int nl4 = a.lat / 4, nr4 = a.Hkv * (MLA_RD / 4);
+  const float* lbase = a.lat_cache + ((int64_t)row * a.maxSeq + ks) * a.lat;
+  const float* rbase = a.rk_cache + ((int64_t)row * a.maxSeq + ks) * a.Hkv * MLA_RD;
 
-  v4f ql[NH], qr[NH], acc[NH];
-  float m[NH], s[NH];
-  const float* qa = a.qabs + (int64_t)row * NH * a.lat;
-  const float* qp = a.qrope + (int64_t)row * NH * a.rd;
-#pragma unroll
-  for (int h = 0; h < NH; h++) {
-    ql[h] = has_lat ? *reinterpret_cast<const v4f*>(qa + h * a.lat + 4 * lane) : (v4f){0, 0, 0, 0};
-    qr[h] = (has_rk && h / ratio == my_kv)
-                ? *reinterpret_cast<const v4f*>(qp + h * a.rd + 4 * lane - my_kv * a.rd)
-                : (v4f){0, 0, 0, 0};
-    acc[h] = (v4f){0, 0, 0, 0};
-    m[h] = -INFINITY;
-    s[h] = 0.f;
-  }
-  const float* lbase = a.lat_cache + (int64_t)row * a.maxSeq * a.lat + 4 * lane;
-  const float* rbase = a.rk_cache + (int64_t)row * a.maxSeq * a.Hkv * a.rd + 4 * lane;
-  const int64_t lstride = a.lat, rstride = (int64_t)a.Hkv * a.rd;
-  constexpr int CH = 4;
-  v4f Ln[CH], Kn[CH];
-  auto fetch = [&](int jb) {
-#pragma unroll
-    for (int u = 0; u < CH; u++) {
-      const int j = min(jb + u, j1 - 1);  // clamp: duplicates are not accumulated
-      Ln[u] = has_lat ? *reinterpret_cast<const v4f*>(lbase + j * lstride) : (v4f){0, 0, 0, 0};
-      Kn[u] = has_rk ? *reinterpret_cast<const v4f*>(rbase + j * rstride) : (v4f){0, 0, 0, 0};
-    }
-  };
-  if (j0 < j1) fetch(j0);
-  for (int jb = j0; jb < j1; jb += CH) {
-    v4f L[CH], K[CH];
-#pragma unroll
-    for (int u = 0; u < CH; u++) {
-      L[u] = Ln[u];
-      K[u] = Kn[u];
-    }
-    if (jb + CH < j1) fetch(jb + CH);
-    float sc[CH][NH];
-#pragma unroll
-    for (int u = 0; u < CH; u++)
-#pragma unroll
-      for (int h = 0; h < NH; h++) {
-        float t = ql[h][0] * L[u][0] + ql[h][1] * L[u][1] + ql[h][2] * L[u][2] + ql[h][3] * L[u][3];
-        t += qr[h][0] * K[u][0] + qr[h][1] * K[u][1] + qr[h][2] * K[u][2] + qr[h][3] * K[u][3];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
-        sc[u][h] = jb + u < j1 ? t : -INFINITY;
-      }
+  // ---- phase 1: scores
+  {
+    v4f ql[NH][4], qr[NH];
+    const float* qa = a.qabs + (int64_t)row * NH * a.lat;
+    const float* qp = a.qrope + (int64_t)row * NH * MLA_RD;
 #pragma unroll
     for (int h = 0; h < NH; h++) {
-      float mn = m[h];
 #pragma unroll
-      for (int u = 0; u < CH; u++) mn = fmaxf(mn, sc[u][h]);
-      const float f = expf(m[h] - mn);  // m = -inf on the first chunk: f = 0
-      s[h] *= f;
-      acc[h] *= f;
-#pragma unroll
-      for (int u = 0; u < CH; u++) {
-        const float p = expf(sc[u][h] - mn);
-        s[h] += p;
-        acc[h] += p * L[u];
+      for (int c = 0; c < 4; c++) {
+        const int f = l16 + 16 * c;
+        ql[h][c] = f < nl4 ? *reinterpret_cast<const v4f*>(qa + h * a.lat + 4 * f)
+                           : (v4f){0.f, 0.f, 0.f, 0.f};
       }
-      m[h] = mn;
+      qr[h] = *reinterpret_cast<const v4f*>(qp + h * MLA_RD + 4 * l16);
+    }
+    v4f L[4], K[4];
+    auto fetch = [&](int j) {
+      const int jj = j < nk ? j : 0;  // clamp (value unused)
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int f = l16 + 16 * c;
+        L[c] = f < nl4 ? *reinterpret_cast<const v4f*>(lbase + (int64_t)jj * a.lat + 4 * f)
+                       : (v4f){0.f, 0.f, 0.f, 0.f};
+        K[c] = f < nr4 ? *reinterpret_cast<const v4f*>(rbase + (int64_t)jj * a.Hkv * MLA_RD + 4 * f)
+                       : (v4f){0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    if (qw < nk) fetch(qw);
+    for (int j = qw; j < nk; j += 16) {
+      v4f Lc[4], Kc[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        Lc[c] = L[c];
+        Kc[c] = K[c];
+      }
+      if (j + 16 < nk) fetch(j + 16);
+#pragma unroll
+      for (int h = 0; h < NH; h++) {
+        float t = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          t += ql[h][c][0] * Lc[c][0] + ql[h][c][1] * Lc[c][1] + ql[h][c][2] * Lc[c][2] +
+               ql[h][c][3] * Lc[c][3];
+        const int c = h / ratio;  // this head's kv rotary float4 sits in slot c
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++)
+          if (cc == c)
+            t += qr[h][0] * Kc[cc][0] + qr[h][1] * Kc[cc][1] + qr[h][2] * Kc[cc][2] +
+                 qr[h][3] * Kc[cc][3];
+        t = sum16_dpp(t);
+        if (l16 == 0) sc[h][j] = t;
+      }
     }
   }
-  // merge the waves
+  __syncthreads();
+
+  // ---- phase 2: softmax over the split (thread t < nk owns key t)
+  {
+    float v[NH], mx[NH];
 #pragma unroll
-  for (int h = 0; h < NH; h++) {
-    if (has_lat) *reinterpret_cast<v4f*>(&wacc[wid][h][4 * lane]) = acc[h];
-    if (lane == 0) {
-      wm[wid][h] = m[h];
-      ws[wid][h] = s[h];
+    for (int h = 0; h < NH; h++) {
+      v[h] = tid < nk ? sc[h][tid] : -INFINITY;
+      float m = v[h];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      if (lane == 0) wred[wid][h] = m;
     }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+      mx[h] = fmaxf(fmaxf(wred[0][h], wred[1][h]), fmaxf(wred[2][h], wred[3][h]));
+      const float p = tid < nk ? expf(v[h] - mx[h]) : 0.f;
+      if (tid < nk) sc[h][tid] = p;
+      float t = p;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+      v[h] = t;
+    }
+    __syncthreads();  // everyone has read wred (max) and written p
+    if (lane == 0)
+#pragma unroll
+      for (int h = 0; h < NH; h++) wred[wid][h] = v[h];
+    __syncthreads();
+    if (tid < NH) {
+      stat[0][tid] = mx[tid];
+      stat[1][tid] = wred[0][tid] + wred[1][tid] + wred[2][tid] + wred[3][tid];
+    }
+  }
+
+  // ---- phase 3: P.V over the latent rows
+  {
+    const bool has = lane < nl4;
+    v4f acc[NH];
+#pragma unroll
+    for (int h = 0; h < NH; h++) acc[h] = (v4f){0.f, 0.f, 0.f, 0.f};
+    constexpr int PV = MLA_KPS / 4;  // keys per wave at most
+    v4f Lr[PV];
+#pragma unroll
+    for (int i = 0; i < PV; i++) {
+      const int j = wid + 4 * i;
+      Lr[i] = (has && j < nk) ? *reinterpret_cast<const v4f*>(lbase + (int64_t)j * a.lat + 4 * lane)
+                              : (v4f){0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < PV; i++) {
+      const int j = wid + 4 * i;
+      if (j < nk)
+#pragma unroll
+        for (int h = 0; h < NH; h++) acc[h] += sc[h][j] * Lr[i];
+    }
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+      if (has) *reinterpret_cast<v4f*>(&wacc[wid][h][4 * lane]) = acc[h];
   }
   __syncthreads();
   const bool whole = nsplit == 1;
   for (int i = tid; i < NH * a.lat; i += 256) {
     const int h = i / a.lat, d = i % a.lat;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][h]);
-    float o = 0.f, tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-      if (wm[w][h] == -INFINITY) continue;  // a wave without keys
-      const float f = expf(wm[w][h] - M);
-      o += wacc[w][h][d] * f;
-      tot += ws[w][h] * f;
-    }
+    const float o = wacc[0][h][d] + wacc[1][h][d] + wacc[2][h][d] + wacc[3][h][d];
     if (whole) {
-      a.out[((int64_t)row * NH + h) * a.lat + d] = o / tot;
+      a.out[((int64_t)row * NH + h) * a.lat + d] = o / stat[1][h];
     } else {
       float* part = a.part + (((int64_t)row * a.nsplit_max + split) * NH + h) * (a.lat + 2);
       part[d] = o;
       if (d == 0) {
-        part[a.lat] = M;
-        part[a.lat + 1] = tot;
+        part[a.lat] = stat[0][h];
+        part[a.lat + 1] = stat[1][h];
       }
     }
   }
@@ -325,7 +362,8 @@ int mla_decode_max_splits(int window, int maxSeq) {
 void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
   GN_CHECK(a.lat % 4 == 0 && a.lat <= MLA_MAXLAT, "mla decode: latent width must be a multiple "
                                                   "of 4 and at most 256");
-  GN_CHECK(a.rd % 4 == 0 && a.Hkv * a.rd <= 256, "mla decode: rotary keys too wide");
+  GN_CHECK(a.rd == MLA_RD && a.Hkv * a.rd <= 256,
+           "mla decode: rotary width must be 64 and rotary keys at most 256 wide");
   GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq <= 8, "mla decode: at most 8 query heads");
   GN_CHECK(a.window >= 0, "mla decode: bad window");
   const int pos_max = a.pos_dev ? a.maxSeq - 1 : a.pos;
