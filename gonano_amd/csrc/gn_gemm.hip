@@ -37,6 +37,7 @@ struct GemmParams {
   const int* goff;
   int groups;
   int64_t gstride;
+  int a_pad;  // rows mode: A is readable for at least 128 rows past its last row
 };
 
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, int row, int col, float v) {
@@ -281,7 +282,12 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
     kend = min(p.K, kbeg + p.k_per_split);
   }
   const int nkt = kend > kbeg ? (kend - kbeg + GK - 1) / GK : 0;
-  const bool interior = VEC && m0 + BM <= p.M && n0 + BN <= p.N;
+  // Rows mode with a padded A (a_pad): a tile may read up to BM rows past
+  // its group's end (the next group's rows or the padding); those rows only
+  // feed output rows >= p.M, which the epilogue discards, so partial groups
+  // still take the direct path.
+  const bool interior = VEC && (m0 + BM <= p.M || (GRP == GEMM_GROUP_ROWS && p.a_pad)) &&
+                        n0 + BN <= p.N;
   const int nfull = interior ? (kend - kbeg) / GK : 0;
 
   LA la;
@@ -507,6 +513,7 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     p.goff = d.group_off;
     p.groups = d.groups;
     p.gstride = d.group_stride;
+    p.a_pad = d.a_pad_rows >= 128;
     p.splits = 1;
     p.k_per_split = d.K;
     if (d.group == GEMM_GROUP_ROWS) {

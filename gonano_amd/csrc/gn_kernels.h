@@ -97,6 +97,7 @@ struct GemmDesc {
   const int* group_off = nullptr;  // device [groups + 1]
   int groups = 0;
   int64_t group_stride = 0;
+  int a_pad_rows = 0;  // rows mode: readable rows of A past row M (>= 128 enables full tiles)
 };
 
 void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);

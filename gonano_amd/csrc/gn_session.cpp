@@ -471,6 +471,8 @@ static float* layer_buf(gn_session* s, const char* nm, int l, bool per_layer, si
   return A<float>(s, key, count);
 }
 
+static constexpr int MOE_PAD = 128;
+
 // MoE buffers of `rows` tokens under name prefix `pre` (per layer when
 // training saves them).
 static MoeBuffers moe_buffers(gn_session* s, const std::string& pre, int64_t rows) {
@@ -484,9 +486,11 @@ static MoeBuffers moe_buffers(gn_session* s, const std::string& pre, int64_t row
   m.perm_w = A<float>(s, pre + "pw", NK);
   m.inv = A<int>(s, pre + "inv", NK);
   m.blockcnt = A<int>(s, "moe_blockcnt", ceil_div(NK, 256) * s->E);
-  m.xg = A<float>(s, pre + "xg", NK * s->C);
+  // rows read as the A operand of expert-grouped GEMMs carry MOE_PAD rows of
+  // padding (full tiles may read past a group's end)
+  m.xg = A<float>(s, pre + "xg", (NK + MOE_PAD) * s->C);
   m.gug = A<float>(s, pre + "gug", NK * 2 * s->EH);
-  m.hg = A<float>(s, pre + "hg", NK * s->EH);
+  m.hg = A<float>(s, pre + "hg", (NK + MOE_PAD) * s->EH);
   m.yg = A<float>(s, pre + "yg", NK * s->C);
   return m;
 }
@@ -518,12 +522,14 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
     d.ldc = 2 * EH;
     d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
     d.group_stride = (int64_t)EH * C;
+    d.a_pad_rows = MOE_PAD;
     sgemm(s, d);
   }
   launch_swiglu_rows(m.gug, EH, NK, s->clamp, m.hg, st);
   GemmDesc dd = linear_fwd_desc(m.hg, ly.ed, m.yg, (int)NK, EH, C);
   dd.group = GEMM_GROUP_ROWS; dd.group_off = m.off; dd.groups = E;
   dd.group_stride = (int64_t)C * EH;
+  dd.a_pad_rows = MOE_PAD;
   sgemm(s, dd);
   MoeCombineArgs ca{};
   ca.mid = mid; ca.shared = shared; ca.yg = m.yg; ca.perm_w = m.perm_w; ca.sel = m.sel;
@@ -701,7 +707,7 @@ static void moe_ffn_backward(gn_session* s, const Layer& ly, const MoeBuffers& m
   sgemm(s, linear_dx_desc(dgu, ly.wgu, dsh, (int)N, C, 2 * F));
   sgemm(s, linear_dw_desc(dgu, h2, ly.ggu, (int)N, C, 2 * F));
   // routed experts
-  float* gy = A<float>(s, "moe_gy", NK * C);
+  float* gy = A<float>(s, "moe_gy", (NK + MOE_PAD) * C);
   double* dotp = A<double>(s, "moe_dotp", NK);
   launch_moe_bwd_prep(g, m.yg, m.perm_row, m.perm_w, s->mscale, NK, C, gy, dotp, st);
   float* dhg = A<float>(s, "moe_dhg", NK * EH);
@@ -709,13 +715,14 @@ static void moe_ffn_backward(gn_session* s, const Layer& ly, const MoeBuffers& m
     GemmDesc d = linear_dx_desc(gy, ly.ed, dhg, (int)NK, EH, C);
     d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
     d.group_stride = (int64_t)C * EH;
+    d.a_pad_rows = MOE_PAD;
     sgemm(s, d);
     GemmDesc w = linear_dw_desc(gy, m.hg, ly.ged, (int)NK, EH, C);
     w.group = GEMM_GROUP_K; w.group_off = m.off; w.groups = E;
     w.group_stride = (int64_t)C * EH;
     sgemm(s, w);
   }
-  float* dgug = A<float>(s, "moe_dgug", NK * 2 * EH);
+  float* dgug = A<float>(s, "moe_dgug", (NK + MOE_PAD) * 2 * EH);
   launch_swiglu_rows_bwd(m.gug, dhg, EH, NK, s->clamp, dgug, st);
   float* dxg = A<float>(s, "moe_dxg", NK * C);
   for (int half = 0; half < 2; half++) {  // dxg = dgate . Wg_e + dup . Wu_e
@@ -724,6 +731,7 @@ static void moe_ffn_backward(gn_session* s, const Layer& ly, const MoeBuffers& m
     d.lda = 2 * EH;
     d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
     d.group_stride = (int64_t)EH * C;
+    d.a_pad_rows = MOE_PAD;
     sgemm(s, d);
     GemmDesc w = linear_dw_desc(dgug + half * EH, m.xg, half ? ly.geu : ly.geg, (int)NK, C, EH);
     w.lda = 2 * EH;
