@@ -45,6 +45,8 @@ class Config:
     moe_clamp: float = 0.0       # MoEEffectiveClamp()
     moe_scale: float = 0.0       # MoEEffectiveScale()
     balance_weight: float = 0.0  # MoEBalanceLossWeight()
+    compression_ratio: int = 0   # Config.CompressionRatio (> 1: HCA compressed layers)
+    swa_window: int = 0          # Config.SWAWindowSize(): local branch of compressed layers
 
     # -- derived quantities -------------------------------------------------
     @property
@@ -69,6 +71,10 @@ class Config:
     @property
     def moe(self) -> bool:  # model/config.go:138
         return self.n_experts > 0
+
+    @property
+    def compression(self) -> int:  # model/config.go:407-414
+        return self.compression_ratio if self.compression_ratio > 1 else 1
 
     @property
     def rotary_dimension(self) -> int:  # model/config.go:430-444
@@ -117,6 +123,8 @@ class Config:
         _ = self.rotary_dimension
         if self.mla and self.head_dim - self.mla_rope_dimension <= 0:  # config.go:502-504
             raise ValueError("MLA content dimension must be positive")
+        if self.mla and self.compression > 1:  # config.go:483-486
+            raise ValueError("MLA is not supported with compression")
         if self.moe and not 0 < self.experts_per_token <= self.n_experts:  # config.go:535-541
             raise ValueError(f"NumExpertsPerToken {self.experts_per_token} must be in "
                              f"[1, NumExperts={self.n_experts}]")
@@ -143,6 +151,9 @@ class Config:
                          (p + "attn.c_k.weight", Hkv * D, C_),
                          (p + "attn.c_v.weight", Hkv * D, C_)]
             ents += [(p + "attn.c_proj.weight", C_, C_)]
+            if self.compression > 1:  # model/params.go:43-46 (every layer owns a compressor)
+                ents += [(p + "attn.compress_logits.weight", D, C_),
+                         (p + "attn.compress_bias", self.compression, D)]
             if self.has_value_embedding(l):
                 ents += [(p + "attn.ve_gate.weight", Hkv, VE_GATE_CHANNELS),
                          (f"value_embeds.{l}.weight", PV, Hkv * D)]
@@ -284,6 +295,9 @@ def init_weights(cfg: Config, seed: int = 0, perturb: float = 0.0,
         for k in keys:
             put(p + k, rng.uniform(-bound, bound, n(p + k)))
         put(p + "mlp.c_fc.weight", rng.uniform(-0.4 * bound, 0.4 * bound, n(p + "mlp.c_fc.weight")))
+        if cfg.compression > 1:  # transformer.go:196-199
+            k = p + "attn.compress_logits.weight"
+            put(k, rng.uniform(-bound, bound, n(k)))
         if cfg.moe:  # transformer.go:163-174
             put(p + "mlp.c_gate.weight",
                 rng.uniform(-0.4 * bound, 0.4 * bound, n(p + "mlp.c_gate.weight")))

@@ -117,6 +117,16 @@ typedef struct {
   int32_t mla_latent, mla_rope_dims;
   int32_t n_experts, experts_per_token, expert_hidden, shared_hidden;
   float moe_clamp, moe_scale, balance_weight;
+  /* Flash preset (model/preset.go:93-118): KV compression ratio > 1 makes
+   * every layer an HCA compressed-attention layer (model/compress.go,
+   * model/compress_attention.go) with a local sliding window of swa_window
+   * keys merged in (0: none).  The sparse indexer, cross-layer reuse and
+   * CED fields are reserved: this restatement requires them to be zero. */
+  int32_t compression_ratio, swa_window;
+  int32_t sparse_topk, indexer_dim, indexer_heads, indexer_pool, indexer_candidates;
+  float indexer_weight;
+  char reuse_pattern[16];
+  int32_t ced;
 } orc_config;
 
 /* Sorted-name parameter table (model/params.go:14-85). */
@@ -162,6 +172,15 @@ ORC_MODEL_DECL(_f64, double)
  * (model/train_transformer.go:121-123; 0 without MoE). */
 double orc_aux_loss_f32(const orc_model_f32 *m);
 double orc_aux_loss_f64(const orc_model_f64 *m);
+
+/* ChannelCompressor.Forward of one sequence (model/compress.go:110-164):
+ * logits [T][D] (bias added), value [T][D] -> comp [ceil(T/ratio)][D],
+ * probs [blocks][ratio][D]. */
+void orc_channel_compress(int T, int D, int ratio, const float *logits, const float *value,
+                          float *comp, float *probs);
+/* mergeAttentionBranches (model/compress_attention.go:440-466). */
+void orc_merge_attention_rows(float *out, float *lse, const float *oa, const float *la,
+                              const float *ob, const float *lb, int rows, int D);
 
 /* Window sizes (model/config.go:629-645): writes n_layer left widths. */
 void orc_window_sizes(const orc_config *cfg, int32_t *out);

@@ -1,7 +1,10 @@
 /*
- * model.c - the dense gonano transformer's inference forward, KV-cache
- * decode, training forward/backward, policy-gradient step, batched
- * generation and one chat_rl step, restated in C.
+ * model.c - the gonano transformer's inference forward, KV-cache decode,
+ * training forward/backward, policy-gradient step, batched generation and
+ * one chat_rl step, restated in C: the dense preset, the latent preset
+ * (MLA attention, DeepSeekMoE feed-forward) and compressed attention (HCA:
+ * channel compressor, block-causal attention over compressed keys, sliding-
+ * window local branch merged by log-sum-exp).
  *
  * TEST INFRASTRUCTURE ONLY (see gn_oracle.h).
  *
@@ -101,6 +104,10 @@ static int build_table(const orc_config *c, param_entry *t) {
       snprintf(nm, 96, "transformer.h.%d.attn.c_v.weight", l); ADD(nm, Hkv * D, C);
     }
     snprintf(nm, 96, "transformer.h.%d.attn.c_proj.weight", l); ADD(nm, C, C);
+    if (c->compression_ratio > 1) { /* params.go:43-46, compress.go:33-43 (every layer Full) */
+      snprintf(nm, 96, "transformer.h.%d.attn.compress_logits.weight", l); ADD(nm, D, C);
+      snprintf(nm, 96, "transformer.h.%d.attn.compress_bias", l); ADD(nm, c->compression_ratio, D);
+    }
     if (!mla && has_value_embedding(l, L)) { /* transformer.go:72-78: no VE under MLA */
       snprintf(nm, 96, "transformer.h.%d.attn.ve_gate.weight", l); ADD(nm, Hkv, VE_GATE_CH);
       snprintf(nm, 96, "value_embeds.%d.weight", l); ADD(nm, PV, Hkv * D);
@@ -193,6 +200,7 @@ typedef struct {
   int64_t wq, wk, wv, wo, wve, wfc, wproj, ve;
   /* latent preset: MLA projections, shared-expert gate, router, experts */
   int64_t wqd, wqu, wqr, wkvd, wku, wvu, wkr, wgate, wr, rbias, eg, eu, ed;
+  int64_t wcl, cbias; /* HCA compressor logit weight [D, C] and bias [ratio, D] */
   int has_ve, window;
 } layer_off;
 
@@ -201,6 +209,7 @@ struct MODEL {
   int C, Hq, Hkv, D, R, F, L, V, PV, S, KVW;
   /* latent preset: MLA latent width, rope/content widths, experts */
   int mla, lat, rd, cd, E, K, EH;
+  int ratio, swa; /* HCA compression ratio (> 1 = compressed layers) and SWA width */
   REAL clamp, mscale, bw;
   double aux_loss;
   int64_t total;
@@ -229,6 +238,12 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
   m->clamp = R(cfg->moe_clamp);
   m->mscale = R(cfg->moe_scale);
   m->bw = R(cfg->balance_weight);
+  m->ratio = cfg->compression_ratio > 1 ? cfg->compression_ratio : 1;
+  m->swa = cfg->swa_window > 0 ? cfg->swa_window : 0;
+  if (cfg->sparse_topk > 0 || cfg->reuse_pattern[0] || cfg->ced) {
+    fprintf(stderr, "oracle: sparse indexer, cross-layer reuse and CED are not restated\n");
+    abort();
+  }
   m->L = cfg->n_layer;
   m->V = cfg->vocab_size;
   m->PV = padded_vocab(cfg);
@@ -275,6 +290,10 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
       OFF(eg, "transformer.h.%d.moe.experts.gate.weight");
       OFF(eu, "transformer.h.%d.moe.experts.up.weight");
       OFF(ed, "transformer.h.%d.moe.experts.down.weight");
+    }
+    if (m->ratio > 1) {
+      OFF(wcl, "transformer.h.%d.attn.compress_logits.weight");
+      OFF(cbias, "transformer.h.%d.attn.compress_bias");
     }
     o->has_ve = !m->mla && has_value_embedding(l, m->L);
     if (o->has_ve) {
@@ -429,9 +448,19 @@ static void attn_fwd(const REAL *q, const REAL *k, const REAL *v, REAL *out, REA
   free(sc);
 }
 /* kernels/scalar/attention.go:145-205, gradients accumulated. */
+static void attn_bwd_corr(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
+                          const REAL *lse, const REAL *corr, REAL *dq, REAL *dk, REAL *dv,
+                          int qlen, int klen, int D, int offset, int window);
 static void attn_bwd(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
                      const REAL *lse, REAL *dq, REAL *dk, REAL *dv, int qlen, int klen, int D,
                      int offset, int window) {
+  attn_bwd_corr(q, k, v, dout, lse, NULL, dq, dk, dv, qlen, klen, D, offset, window);
+}
+/* corr, when given, replaces the row sum of dP*P (the merged-branch row
+ * correction dO.O, model/train.go:211-226). */
+static void attn_bwd_corr(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
+                          const REAL *lse, const REAL *corr, REAL *dq, REAL *dk, REAL *dv,
+                          int qlen, int klen, int D, int offset, int window) {
   REAL *P = (REAL *)malloc(sizeof(REAL) * (int64_t)qlen * klen);
   REAL *dS = (REAL *)malloc(sizeof(REAL) * (int64_t)qlen * klen);
   for (int qi = 0; qi < qlen; qi++) {
@@ -459,6 +488,7 @@ static void attn_bwd(const REAL *q, const REAL *k, const REAL *v, const REAL *do
       dp[kj] = R(a);
       rd += (double)dp[kj] * (double)P[(int64_t)qi * klen + kj];
     }
+    if (corr) rd = (double)corr[qi];
     for (int kj = 0; kj < klen; kj++)
       dp[kj] = R((double)P[(int64_t)qi * klen + kj] * ((double)dp[kj] - rd));
   }
@@ -492,12 +522,27 @@ typedef struct {
   REAL *lat;    /* [L][B][maxSeq][lat]      (MLA latent, kvcache.go:224-274) */
   REAL *rk;     /* [L][B][maxSeq][Hkv*rd]   (MLA rotary key) */
   REAL *prev;   /* [B][C] */
+  /* HCA (kvcache.go:142-220): tail buffer of the current block (hidden rows;
+   * its keys/values are the raw cache rows), compressed blocks and counts */
+  int maxBlocks;
+  REAL *tailh;  /* [L][B][ratio][C] */
+  int *taillen; /* [L] (all rows advance together) */
+  REAL *ck, *cv;  /* [L][B][Hkv][maxBlocks][D] */
+  int *ccount;  /* [L][B] */
 } kvcache;
 
 static kvcache *cache_new(MODEL *m, int B, int maxSeq) {
   kvcache *c = (kvcache *)calloc(1, sizeof(kvcache));
   c->B = B;
   c->maxSeq = maxSeq;
+  if (m->ratio > 1) {
+    c->maxBlocks = maxSeq / m->ratio + 1;
+    c->tailh = (REAL *)calloc((size_t)m->L * B * m->ratio * m->C, sizeof(REAL));
+    c->taillen = (int *)calloc(m->L, sizeof(int));
+    c->ck = (REAL *)calloc((size_t)m->L * B * m->Hkv * c->maxBlocks * m->D, sizeof(REAL));
+    c->cv = (REAL *)calloc((size_t)m->L * B * m->Hkv * c->maxBlocks * m->D, sizeof(REAL));
+    c->ccount = (int *)calloc((size_t)m->L * B, sizeof(int));
+  }
   if (m->mla) {
     c->lat = (REAL *)calloc((size_t)m->L * B * maxSeq * m->lat, sizeof(REAL));
     c->rk = (REAL *)calloc((size_t)m->L * B * maxSeq * m->Hkv * m->rd, sizeof(REAL));
@@ -514,6 +559,7 @@ static void cache_free(kvcache *c) {
   free(c->v);
   free(c->lat);
   free(c->rk);
+  free(c->tailh); free(c->taillen); free(c->ck); free(c->cv); free(c->ccount);
   free(c->prev);
   free(c);
 }
@@ -543,6 +589,22 @@ static void prefill_from(MODEL *m, kvcache *dst, kvcache *src) {
         memcpy(cache_k(m, dst, l, b, h), cache_k(m, src, l, 0, h), sizeof(REAL) * pos * m->D);
         memcpy(cache_v(m, dst, l, b, h), cache_v(m, src, l, 0, h), sizeof(REAL) * pos * m->D);
       }
+  if (m->ratio > 1) { /* PrefillFrom copies the compression state too */
+    for (int l = 0; l < m->L; l++) {
+      dst->taillen[l] = src->taillen[l];
+      for (int b = 0; b < dst->B; b++) {
+        memcpy(dst->tailh + ((size_t)l * dst->B + b) * m->ratio * m->C,
+               src->tailh + (size_t)l * m->ratio * m->C, sizeof(REAL) * m->ratio * m->C);
+        dst->ccount[l * dst->B + b] = src->ccount[l];
+        for (int h = 0; h < m->Hkv; h++) {
+          size_t so = (((size_t)l * src->B) * m->Hkv + h) * src->maxBlocks * m->D;
+          size_t dd = (((size_t)l * dst->B + b) * m->Hkv + h) * dst->maxBlocks * m->D;
+          memcpy(dst->ck + dd, src->ck + so, sizeof(REAL) * src->ccount[l] * m->D);
+          memcpy(dst->cv + dd, src->cv + so, sizeof(REAL) * src->ccount[l] * m->D);
+        }
+      }
+    }
+  }
   dst->pos = pos;
   if (src->has_prev) {
     for (int b = 0; b < dst->B; b++) memcpy(dst->prev + (size_t)b * m->C, src->prev, sizeof(REAL) * m->C);
@@ -914,12 +976,310 @@ static void mla_decode_attention(MODEL *m, const layer_off *lo, int l, const REA
   (void)C;
 }
 
+/* ---- HCA compressed attention (model/compress.go, compress_attention.go) ---- */
+
+/* Compression logits of rows [T][C]: logitWeight.Forward then + bias[row %
+ * ratio] (compress.go:98-109). */
+static void compress_logits(MODEL *m, const layer_off *lo, const REAL *h, int T, REAL *out) {
+  const int D = m->D, ratio = m->ratio;
+  linear_fwd(out, h, m->p + lo->wcl, T, m->C, D);
+  for (int t = 0; t < T; t++)
+    for (int d = 0; d < D; d++) out[(int64_t)t * D + d] += m->p[lo->cbias + (t % ratio) * D + d];
+}
+
+/* ChannelCompressor.Forward (compress.go:110-164) of one sequence: per block
+ * and channel, softmax over the block's rows of the logits, weighted sum of
+ * value [T][D]; compressed [blocks][D], probabilities [blocks][ratio][D]. */
+static void compress_seq(int T, int D, int ratio, const REAL *logits, const REAL *value,
+                         REAL *comp, REAL *probs) {
+  const int blocks = (T + ratio - 1) / ratio;
+  for (int bl = 0; bl < blocks; bl++)
+    for (int d = 0; d < D; d++) {
+      REAL mx = R(-INFINITY);
+      for (int r = 0; r < ratio; r++) {
+        int t = bl * ratio + r;
+        if (t < T && logits[(int64_t)t * D + d] > mx) mx = logits[(int64_t)t * D + d];
+      }
+      double tot = 0;
+      REAL *pr = probs + (int64_t)bl * ratio * D;
+      for (int r = 0; r < ratio; r++) {
+        int t = bl * ratio + r;
+        REAL p = R(0);
+        if (t < T && mx > R(-INFINITY)) p = R(exp((double)(logits[(int64_t)t * D + d] - mx)));
+        pr[r * D + d] = p;
+        tot += (double)p;
+      }
+      REAL acc = 0;
+      if (tot > 0) {
+        REAL inv = R(1.0 / tot);
+        for (int r = 0; r < ratio; r++) {
+          pr[r * D + d] *= inv;
+          int t = bl * ratio + r;
+          if (t < T) acc += pr[r * D + d] * value[(int64_t)t * D + d];
+        }
+      }
+      comp[(int64_t)bl * D + d] = acc;
+    }
+}
+
+/* ChannelCompressor.Backward's softmax part (compress.go:199-222): gradients
+ * of the logits and of value, accumulated. */
+static void compress_seq_bwd(int T, int D, int ratio, const REAL *probs, const REAL *value,
+                             const REAL *comp, const REAL *g, REAL *glog, REAL *gval) {
+  const int blocks = (T + ratio - 1) / ratio;
+  for (int bl = 0; bl < blocks; bl++)
+    for (int d = 0; d < D; d++) {
+      REAL gr = g[(int64_t)bl * D + d], cv = comp[(int64_t)bl * D + d];
+      for (int r = 0; r < ratio; r++) {
+        int t = bl * ratio + r;
+        if (t >= T) continue;
+        REAL p = probs[((int64_t)bl * ratio + r) * D + d], v = value[(int64_t)t * D + d];
+        glog[(int64_t)t * D + d] += p * gr * (v - cv);
+        gval[(int64_t)t * D + d] += p * gr;
+      }
+    }
+}
+
+/* mergeAttentionBranches / mergeAttentionRow (compress_attention.go:440-486). */
+static void merge_rows(REAL *out, REAL *lse, const REAL *oa, const REAL *la, const REAL *ob,
+                       const REAL *lb, int rows, int D) {
+  for (int i = 0; i < rows; i++) {
+    REAL mx = la[i] > lb[i] ? la[i] : lb[i];
+    if (mx == R(-INFINITY)) {
+      for (int d = 0; d < D; d++) out[(int64_t)i * D + d] = 0;
+      if (lse) lse[i] = mx;
+      continue;
+    }
+    REAL wa = R(exp((double)(la[i] - mx))), wb = R(exp((double)(lb[i] - mx)));
+    REAL tot = wa + wb;
+    REAL inv = R(1.0 / (double)tot);
+    for (int d = 0; d < D; d++)
+      out[(int64_t)i * D + d] = (wa * oa[(int64_t)i * D + d] + wb * ob[(int64_t)i * D + d]) * inv;
+    if (lse) lse[i] = mx + R(log((double)tot));
+  }
+}
+
+/* Training-side HCA attention (model/train.go:99-169 with compressForward and
+ * compressedAttentionForward, compress_attention.go:562-677): qh [B][Hq][T][D],
+ * kh/vh [B][Hkv][T][D] (post-norm keys, gated values), h [B*T][C]; writes oh,
+ * lse and, in hc, the compressed keys/values and probabilities. */
+typedef struct {
+  int blocks;
+  REAL *kc, *vc;   /* [B][Hkv][blocks][D] */
+  REAL *probs;     /* [B][blocks][ratio][D] (one per sequence: K and V share the logits) */
+} hca_ctx;
+
+static void hca_train_forward(MODEL *m, const layer_off *lo, const REAL *qh, const REAL *kh,
+                              const REAL *vh, const REAL *h, int B, int T, REAL *oh, REAL *lse,
+                              hca_ctx *hc) {
+  const int D = m->D, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
+  const int blocks = (T + ratio - 1) / ratio;
+  hc->blocks = blocks;
+  hc->kc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+  hc->vc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+  hc->probs = (REAL *)calloc((size_t)B * blocks * ratio * D, sizeof(REAL));
+  REAL *logits = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
+  for (int b = 0; b < B; b++) {
+    compress_logits(m, lo, h + (int64_t)b * T * m->C, T, logits);
+    REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
+    for (int hh = 0; hh < Hkv; hh++) {
+      int64_t bk = (int64_t)b * Hkv + hh;
+      compress_seq(T, D, ratio, logits, kh + bk * T * D, hc->kc + bk * blocks * D, pb);
+      compress_seq(T, D, ratio, logits, vh + bk * T * D, hc->vc + bk * blocks * D, pb);
+    }
+  }
+  free(logits);
+#pragma omp parallel for schedule(dynamic)
+  for (int bh = 0; bh < B * Hq; bh++) {
+    int b = bh / Hq, hq = bh % Hq;
+    int64_t bk = (int64_t)b * Hkv + hq / rr;
+    const REAL *q = qh + (int64_t)bh * T * D;
+    REAL *go = (REAL *)calloc((size_t)T * D, sizeof(REAL));
+    REAL *gl = (REAL *)malloc(sizeof(REAL) * T);
+    for (int bl = 0; bl < blocks; bl++) { /* queries of block bl see blocks < bl */
+      int t0 = bl * ratio, t1 = t0 + ratio < T ? t0 + ratio : T;
+      if (bl == 0) {
+        for (int t = t0; t < t1; t++) gl[t] = R(-INFINITY);
+        continue;
+      }
+      attn_fwd(q + (int64_t)t0 * D, hc->kc + bk * blocks * D, hc->vc + bk * blocks * D,
+               go + (int64_t)t0 * D, gl + t0, t1 - t0, bl, D, bl, -1);
+    }
+    if (m->swa > 0) {
+      REAL *loc = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
+      REAL *ll = (REAL *)malloc(sizeof(REAL) * T);
+      attn_fwd(q, kh + bk * T * D, vh + bk * T * D, loc, ll, T, T, D, 0, m->swa);
+      merge_rows(oh + (int64_t)bh * T * D, lse + (int64_t)bh * T, go, gl, loc, ll, T, D);
+      free(loc); free(ll);
+    } else {
+      memcpy(oh + (int64_t)bh * T * D, go, sizeof(REAL) * T * D);
+      memcpy(lse + (int64_t)bh * T, gl, sizeof(REAL) * T);
+    }
+    free(go); free(gl);
+  }
+}
+
+/* Training-side HCA backward (model/train.go:211-303 with
+ * compressedAttentionBackward, attentionBackwardWindowed and
+ * compressBackward): dqh/dkh/dvh (head-major, zeroed by the caller) receive
+ * the query and raw key/value gradients, dhin_c [B*T][C] the compressor's
+ * gradient wrt the attention input; parameter gradients accumulate in G. */
+static void hca_train_backward(MODEL *m, const layer_off *lo, const hca_ctx *hc, const REAL *qh,
+                               const REAL *kh, const REAL *vh, const REAL *oh, const REAL *doh,
+                               const REAL *lse, const REAL *h, int B, int T, REAL *dqh,
+                               REAL *dkh, REAL *dvh, REAL *dhin_c, REAL *G) {
+  const int D = m->D, C = m->C, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
+  const int blocks = hc->blocks;
+  REAL *corr = NULL;
+  if (m->swa > 0) { /* merged row correction dO.O (train.go:211-226) */
+    corr = (REAL *)malloc(sizeof(REAL) * (int64_t)B * Hq * T);
+    for (int64_t row = 0; row < (int64_t)B * Hq * T; row++) {
+      double dot = 0;
+      for (int d = 0; d < D; d++) dot += (double)doh[row * D + d] * (double)oh[row * D + d];
+      corr[row] = R(dot);
+    }
+  }
+  REAL *dkc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+  REAL *dvc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+  REAL *dkl = (REAL *)calloc((size_t)B * Hkv * T * D, sizeof(REAL));
+  REAL *dvl = (REAL *)calloc((size_t)B * Hkv * T * D, sizeof(REAL));
+  /* serial over query heads so GQA accumulation into the shared K/V is race-free */
+  for (int b = 0; b < B; b++)
+#pragma omp parallel for schedule(dynamic)
+    for (int hh = 0; hh < Hkv; hh++)
+      for (int r = 0; r < rr; r++) {
+        int hq = hh * rr + r;
+        int64_t bh = (int64_t)b * Hq + hq, bk = (int64_t)b * Hkv + hh;
+        for (int bl = 1; bl < blocks; bl++) {
+          int t0 = bl * ratio, t1 = t0 + ratio < T ? t0 + ratio : T;
+          attn_bwd_corr(qh + (bh * T + t0) * D, hc->kc + bk * blocks * D, hc->vc + bk * blocks * D,
+                        doh + (bh * T + t0) * D, lse + bh * T + t0, corr ? corr + bh * T + t0 : NULL,
+                        dqh + (bh * T + t0) * D, dkc + bk * blocks * D, dvc + bk * blocks * D,
+                        t1 - t0, bl, D, bl, -1);
+        }
+        if (m->swa > 0)
+          attn_bwd_corr(qh + bh * T * D, kh + bk * T * D, vh + bk * T * D, doh + bh * T * D,
+                        lse + bh * T, corr + bh * T, dqh + bh * T * D, dkl + bk * T * D,
+                        dvl + bk * T * D, T, T, D, 0, m->swa);
+      }
+  /* compressBackward (compress_attention.go:1182-1209) */
+  memset(dhin_c, 0, sizeof(REAL) * (int64_t)B * T * C);
+  REAL *glk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
+  REAL *glv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
+  REAL *dhk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
+  REAL *dhv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
+  for (int b = 0; b < B; b++) {
+    const REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
+    const REAL *hb = h + (int64_t)b * T * C;
+    for (int hh = 0; hh < Hkv; hh++) {
+      int64_t bk = (int64_t)b * Hkv + hh;
+      memset(glk, 0, sizeof(REAL) * (int64_t)T * D);
+      memset(glv, 0, sizeof(REAL) * (int64_t)T * D);
+      compress_seq_bwd(T, D, ratio, pb, kh + bk * T * D, hc->kc + bk * blocks * D,
+                       dkc + bk * blocks * D, glk, dkh + bk * T * D);
+      linear_bwd(dhk, G + lo->wcl, hb, glk, m->p + lo->wcl, T, C, D);
+      for (int t = 0; t < T; t++)
+        for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glk[(int64_t)t * D + d];
+      compress_seq_bwd(T, D, ratio, pb, vh + bk * T * D, hc->vc + bk * blocks * D,
+                       dvc + bk * blocks * D, glv, dvh + bk * T * D);
+      linear_bwd(dhv, G + lo->wcl, hb, glv, m->p + lo->wcl, T, C, D);
+      for (int t = 0; t < T; t++)
+        for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glv[(int64_t)t * D + d];
+      for (int64_t i = 0; i < (int64_t)T * C; i++) dhin_c[(int64_t)b * T * C + i] += dhk[i] + dhv[i];
+    }
+  }
+  /* raw key/value gradients: compressor part + local branch */
+  for (int64_t i = 0; i < (int64_t)B * Hkv * T * D; i++) {
+    dkh[i] = dkh[i] + dkl[i];
+    dvh[i] = dvh[i] + dvl[i];
+  }
+  free(glk); free(glv); free(dhk); free(dhv);
+  free(dkc); free(dvc); free(dkl); free(dvl); free(corr);
+}
+
+/* Inference HCA (forwardCompressed, compress_attention.go:895-1006 with
+ * appendGlobalTail / compressTail, :848-890): buffer the T new rows of h,
+ * compress each completed block from its hidden rows and the raw cached
+ * keys/values, then attend every query to the compressed blocks strictly
+ * before its own and merge the local window branch. */
+static void hca_decode(MODEL *m, const layer_off *lo, int l, kvcache *cache, const REAL *h,
+                       const REAL *qh, int B, int T, REAL *oh) {
+  const int D = m->D, C = m->C, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
+  const int offset = cache->pos, klen = cache->pos + T;
+  REAL *logits = (REAL *)malloc(sizeof(REAL) * (int64_t)ratio * D);
+  REAL *probs = (REAL *)malloc(sizeof(REAL) * (int64_t)ratio * D);
+  for (int t = 0; t < T; t++) {
+    for (int b = 0; b < B; b++)
+      memcpy(cache->tailh + (((size_t)l * B + b) * ratio + cache->taillen[l]) * C,
+             h + ((int64_t)b * T + t) * C, sizeof(REAL) * C);
+    cache->taillen[l]++;
+    if (cache->taillen[l] < ratio) continue;
+    const int start = offset + t - ratio + 1; /* first position of the block */
+    for (int b = 0; b < B; b++) {
+      compress_logits(m, lo, cache->tailh + ((size_t)l * B + b) * ratio * C, ratio, logits);
+      int slot = cache->ccount[l * B + b];
+      for (int hh = 0; hh < Hkv; hh++) {
+        size_t cb = ((((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks + slot) * D;
+        compress_seq(ratio, D, ratio, logits, cache_k(m, cache, l, b, hh) + (int64_t)start * D,
+                     cache->ck + cb, probs);
+        compress_seq(ratio, D, ratio, logits, cache_v(m, cache, l, b, hh) + (int64_t)start * D,
+                     cache->cv + cb, probs);
+      }
+      cache->ccount[l * B + b]++;
+    }
+    cache->taillen[l] = 0;
+  }
+  free(logits); free(probs);
+#pragma omp parallel for schedule(dynamic)
+  for (int bh = 0; bh < B * Hq; bh++) {
+    int b = bh / Hq, hq = bh % Hq, hh = hq / rr;
+    REAL go[1024], lo_[1024], gl, ll;
+    for (int t = 0; t < T; t++) {
+      int pos = offset + t;
+      int count = pos / ratio;
+      if (count > cache->ccount[l * B + b]) count = cache->ccount[l * B + b];
+      const REAL *q = qh + ((int64_t)bh * T + t) * D;
+      REAL *out = oh + ((int64_t)bh * T + t) * D;
+      size_t cb = (((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks * D;
+      if (count == 0) {
+        gl = R(-INFINITY);
+        memset(go, 0, sizeof(REAL) * D);
+      } else {
+        attn_fwd(q, cache->ck + cb, cache->cv + cb, go, &gl, 1, count, D, count, -1);
+      }
+      if (m->swa > 0) { /* localAttentionRow (compress_attention.go:543-560) */
+        int ls = pos - m->swa < 0 ? 0 : pos - m->swa;
+        int n = pos - ls + 1;
+        attn_fwd(q, cache_k(m, cache, l, b, hh) + (int64_t)ls * D,
+                 cache_v(m, cache, l, b, hh) + (int64_t)ls * D, lo_, &ll, 1, n, D, n - 1, -1);
+        merge_rows(out, NULL, go, &gl, lo_, &ll, 1, D);
+      } else {
+        memcpy(out, go, sizeof(REAL) * D);
+      }
+    }
+  }
+  (void)klen;
+}
+
+#if defined(ORC_DEFINE_SHARED)
+/* Test entry points for the HCA pieces (float32 build). */
+void orc_channel_compress(int T, int D, int ratio, const float *logits, const float *value,
+                          float *comp, float *probs) {
+  compress_seq(T, D, ratio, logits, value, comp, probs);
+}
+void orc_merge_attention_rows(float *out, float *lse, const float *oa, const float *la,
+                              const float *ob, const float *lb, int rows, int D) {
+  merge_rows(out, lse, oa, la, ob, lb, rows, D);
+}
+#endif
+
 /* ---- forward ---------------------------------------------------------- */
 typedef struct {
   REAL *xin, *xb, *h, *qrot, *krot, *qn, *kn, *vh, *lse, *o, *vesig, *ve, *mid, *h2, *u, *act;
   /* latent preset: MLA latents, shared-expert gate, MoE routing and experts */
   REAL *ql, *kvl, *g2;
   struct moe_ctx *moe;
+  hca_ctx *hca;
 } layer_ctx;
 
 typedef struct {
@@ -941,6 +1301,7 @@ static void ctx_free(train_ctx *c, int L) {
     free(x->mid); free(x->h2); free(x->u); free(x->act);
     free(x->ql); free(x->kvl); free(x->g2);
     moe_ctx_free(x->moe);
+    if (x->hca) { free(x->hca->kc); free(x->hca->vc); free(x->hca->probs); free(x->hca); }
   }
   free(c->backout); free(c->final_pre); free(c->final_norm); free(c->logits);
   free(c);
@@ -1125,12 +1486,21 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
           }
         }
       }
+    if (m->ratio > 1 && cache) {
+      hca_decode(m, lo, l, cache, h, qh, B, T, oh);
+    } else if (m->ratio > 1) {
+      hca_ctx *hc = (hca_ctx *)calloc(1, sizeof(hca_ctx));
+      hca_train_forward(m, lo, qh, kh, vh, h, B, T, oh, lseb, hc);
+      if (lc) lc->hca = hc;
+      else { free(hc->kc); free(hc->vc); free(hc->probs); free(hc); }
+    } else {
 #pragma omp parallel for schedule(dynamic)
     for (int bh = 0; bh < B * Hq; bh++) {
       int b = bh / Hq, hq = bh % Hq, hk = hq / ratio;
       attn_fwd(qh + (int64_t)bh * T * D, kh + ((int64_t)b * Hkv + hk) * klen * D,
                vh + ((int64_t)b * Hkv + hk) * klen * D, oh + (int64_t)bh * T * D,
                lseb + (int64_t)bh * T, T, klen, D, offset, lo->window);
+    }
     }
     if (lc) {
       lc->qn = qh; lc->kn = kh; lc->vh = vh;
@@ -1274,6 +1644,12 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
   REAL *dqh = (REAL *)calloc((size_t)N * Hq * D, sizeof(REAL));
   REAL *dkh = (REAL *)calloc((size_t)N * Hkv * D, sizeof(REAL));
   REAL *dvh = (REAL *)calloc((size_t)N * Hkv * D, sizeof(REAL));
+  REAL *dhin_c = NULL;
+  if (m->ratio > 1) {
+    dhin_c = (REAL *)malloc(sizeof(REAL) * N * C);
+    hca_train_backward(m, lo, lc->hca, lc->qn, lc->kn, lc->vh, lc->o, doh, lc->lse, lc->h, B, T,
+                       dqh, dkh, dvh, dhin_c, G);
+  } else {
   /* serial (b, qh) loop as train.go:305-326 so GQA accumulation is race-free */
   for (int b = 0; b < B; b++)
 #pragma omp parallel for schedule(dynamic)
@@ -1285,6 +1661,7 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
                  lc->lse + bh * T, dqh + bh * T * D, dkh + bk * T * D, dvh + bk * T * D, T, T, D, 0,
                  lo->window);
       }
+  }
   free(doh);
   if (!m->mla) { /* unscale QK (train.go:331-333); MLA has no QK norm */
     for (int64_t i = 0; i < N * Hq * D; i++) dqh[i] *= R(QK_SCALE);
@@ -1356,6 +1733,10 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
     free(dpre); free(slice); free(dslice);
   }
   free(dvs);
+  if (dhin_c) { /* the compressor's logit projection reads the attention input (train.go:421-424) */
+    for (int64_t i = 0; i < N * C; i++) dhin[i] = dhin[i] + dhin_c[i];
+    free(dhin_c);
+  }
   rmsnorm_backward_rows(gx, lc->xb, dhin, N, C);
   for (int64_t i = 0; i < N * C; i++) gx[i] = gx[i] + gmid[i];
   free(dhin); free(tmp); free(gmid); free(dh);

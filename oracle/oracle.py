@@ -46,6 +46,16 @@ class OrcConfig(C.Structure):
         ("moe_clamp", C.c_float),
         ("moe_scale", C.c_float),
         ("balance_weight", C.c_float),
+        ("compression_ratio", C.c_int32),
+        ("swa_window", C.c_int32),
+        ("sparse_topk", C.c_int32),
+        ("indexer_dim", C.c_int32),
+        ("indexer_heads", C.c_int32),
+        ("indexer_pool", C.c_int32),
+        ("indexer_candidates", C.c_int32),
+        ("indexer_weight", C.c_float),
+        ("reuse_pattern", C.c_char * 16),
+        ("ced", C.c_int32),
     ]
 
 
@@ -118,6 +128,9 @@ def lib():
         "orc_window_sizes": (v, [C.POINTER(OrcConfig), _i32p]),
         "orc_num_threads": (C.c_int, []),
         "orc_aux_loss_f32": (C.c_double, [C.c_void_p]),
+        "orc_channel_compress": (v, [C.c_int, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]),
+        "orc_merge_attention_rows": (v, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, C.c_int,
+                                         C.c_int]),
         "orc_aux_loss_f64": (C.c_double, [C.c_void_p]),
     }
     for sfx, fp in (("_f32", _f32p), ("_f64", _f64p)):
@@ -172,6 +185,8 @@ class ModelShape:
     moe_clamp: float = 0.0
     moe_scale: float = 0.0
     balance_weight: float = 0.0
+    compression_ratio: int = 0
+    swa_window: int = 0
 
     @classmethod
     def from_config(cls, cfg) -> "ModelShape":
@@ -180,7 +195,7 @@ class ModelShape:
                    cfg.n_embd, cfg.rotary_dims, cfg.window_pattern, cfg.mla_latent,
                    cfg.mla_rope_dimension if cfg.mla_latent > 0 else 0, cfg.n_experts,
                    cfg.experts_per_token, cfg.expert_hidden, cfg.shared_hidden, cfg.moe_clamp,
-                   cfg.moe_scale, cfg.balance_weight)
+                   cfg.moe_scale, cfg.balance_weight, cfg.compression_ratio, cfg.swa_window)
 
     def orc(self) -> OrcConfig:
         return OrcConfig(self.sequence_len, self.vocab_size, self.n_layer, self.n_head,
@@ -188,7 +203,7 @@ class ModelShape:
                          self.window_pattern.encode(), self.mla_latent, self.mla_rope_dims,
                          self.n_experts, self.experts_per_token, self.expert_hidden,
                          self.shared_hidden, self.moe_clamp, self.moe_scale,
-                         self.balance_weight)
+                         self.balance_weight, self.compression_ratio, self.swa_window)
 
 
 def param_table(shape: ModelShape):
