@@ -36,6 +36,16 @@ class GnConfig(C.Structure):
         ("moe_clamp", C.c_float),
         ("moe_scale", C.c_float),
         ("balance_weight", C.c_float),
+        ("compression_ratio", C.c_int32),
+        ("swa_window", C.c_int32),
+        ("sparse_topk", C.c_int32),
+        ("indexer_dim", C.c_int32),
+        ("indexer_heads", C.c_int32),
+        ("indexer_pool", C.c_int32),
+        ("indexer_candidates", C.c_int32),
+        ("indexer_weight", C.c_float),
+        ("reuse_pattern", C.c_char * 16),
+        ("ced", C.c_int32),
     ]
 
 

@@ -25,6 +25,7 @@ SOURCES = [
     "gn_model.hip",
     "gn_attention.hip",
     "gn_latent.hip",
+    "gn_compress.hip",
     "gn_sampler.hip",
     "gn_session.cpp",
     "gn_tools.cpp",

@@ -234,6 +234,17 @@ def apply_latent_preset(cfg: Config, mla_latent: int = 0, n_experts: int = 0,
     if cfg.n_kv_head == cfg.n_head and cfg.n_head % 2 == 0:  # applyDefaultGroupedQuery
         cfg.n_kv_head = cfg.n_head // 2
     cfg.mla_latent = mla_latent if mla_latent > 0 else cfg.n_embd // 2
+    return enable_moe(cfg, n_experts, experts_per_token, expert_hidden, shared_hidden, moe_scale,
+                      balance_weight)
+
+
+def enable_moe(cfg: Config, n_experts: int = 0, experts_per_token: int = 0,
+               expert_hidden: int = 0, shared_hidden: int = 0, moe_scale: float = 0.0,
+               balance_weight: float = 0.0) -> Config:
+    """Config.enableMoE (model/preset.go:142-152) and ApplyMoEDefaults
+    (model/config.go:210-227) with the effective clamp, scale and balance
+    weight resolved (config.go:152-188): the DeepSeekMoE feed-forward of the
+    latent and flash presets."""
     cfg.n_experts = n_experts if n_experts > 0 else moe_experts_for_depth(cfg.n_layer)
     k = experts_per_token if experts_per_token > 0 else 2
     cfg.experts_per_token = min(k, cfg.n_experts)

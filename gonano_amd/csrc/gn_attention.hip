@@ -60,10 +60,34 @@ __host__ __device__ inline DecSplit dec_split(int kstart, int kend) {
   d.nsplit = (n + d.kps - 1) / d.kps;  // every split non-empty
   return d;
 }
-__device__ __forceinline__ DecSplit dec_split(const DecodeAttnArgs& a) {
-  if (!a.pos_dev) return dec_split(a.kstart, a.kend);
-  const int pos = *a.pos_dev;
-  return dec_split(max(0, pos - a.window), pos + 1);
+__host__ __device__ inline DecSplit dec_empty() {
+  DecSplit d;
+  d.kstart = d.kend = 0;
+  d.kps = 1;
+  d.nsplit = 0;
+  return d;
+}
+// The splits of one step: first those of the compressed blocks (ratio > 1),
+// then those of the raw keys.
+struct DecPlan {
+  DecSplit g, l;
+  int nsplit;
+};
+__host__ __device__ inline DecPlan dec_plan_at(const DecodeAttnArgs& a, int pos) {
+  DecPlan p;
+  if (a.ratio > 1) {
+    const int count = pos / a.ratio;
+    p.g = count > 0 ? dec_split(0, count) : dec_empty();
+    p.l = a.window > 0 ? dec_split(max(0, pos - a.window), pos + 1) : dec_empty();
+  } else {
+    p.g = dec_empty();
+    p.l = a.pos_dev ? dec_split(max(0, pos - a.window), pos + 1) : dec_split(a.kstart, a.kend);
+  }
+  p.nsplit = p.g.nsplit + p.l.nsplit;
+  return p;
+}
+__device__ __forceinline__ DecPlan dec_plan(const DecodeAttnArgs& a) {
+  return dec_plan_at(a, a.pos_dev ? *a.pos_dev : a.kend - 1);
 }
 
 __device__ __forceinline__ float red8_sum(float v) { return sum8_dpp(v); }
@@ -86,16 +110,20 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   __shared__ float stat[2][R];  // max, sum per head
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int bh = blockIdx.x, s = blockIdx.y;
-  const DecSplit sp = dec_split(a);
-  if (s >= sp.nsplit) return;  // graph launches size the grid for the longest window
+  const DecPlan pl = dec_plan(a);
+  if (s >= pl.nsplit) return;  // graph launches size the grid for the longest window
   const int row = bh / a.Hkv, hk = bh % a.Hkv;
-  const int ks = sp.kstart + s * sp.kps;
+  const bool glob = s < pl.g.nsplit;  // a split of compressed blocks
+  const DecSplit& sp = glob ? pl.g : pl.l;
+  const int ks = sp.kstart + (glob ? s : s - pl.g.nsplit) * sp.kps;
   const int nk = min(sp.kend, ks + sp.kps) - ks;
-  const int64_t cbase = ((int64_t)row * a.Hkv + hk) * a.maxSeq + ks;
+  const float* kbase = glob ? a.ck : a.kc;
+  const float* vbase = glob ? a.cv : a.vc;
+  const int64_t cbase = ((int64_t)row * a.Hkv + hk) * (glob ? a.maxBlocks : a.maxSeq) + ks;
 
   // V rows of phase 3, issued first
   const int d4 = tid & 31, jr = tid >> 5;
-  const v4f* vrow = reinterpret_cast<const v4f*>(a.vc + cbase * HD) + d4;
+  const v4f* vrow = reinterpret_cast<const v4f*>(vbase + cbase * HD) + d4;
   v4f vpre[DEC_VPRE];
 #pragma unroll
   for (int i = 0; i < DEC_VPRE; i++) {
@@ -120,7 +148,7 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
       }
     const int q4 = (nk + 3) / 4;
     const int j0 = wid * q4, j1 = min(nk, j0 + q4);
-    const v4f* kb = reinterpret_cast<const v4f*>(a.kc + cbase * HD + 16 * part);
+    const v4f* kb = reinterpret_cast<const v4f*>(kbase + cbase * HD + 16 * part);
     auto load = [&](int j, v4f* kd) {
       const int jj = j < j1 ? j : j0;  // clamp (value unused when j >= j1)
 #pragma unroll
@@ -211,7 +239,7 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   for (int h = 0; h < R; h++)
     *reinterpret_cast<v4f*>(&pv[jr][h][4 * d4]) = (v4f){acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
   __syncthreads();
-  const bool whole = sp.nsplit == 1;
+  const bool whole = pl.nsplit == 1;
   float* out = a.part + ((int64_t)bh * a.nsplit_max + s) * R * (HD + 2);
   for (int i = tid; i < R * HD; i += 256) {
     const int h = i / HD, dd = i % HD;
@@ -238,9 +266,13 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
 }
 
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
-  const DecSplit sp = dec_split(a);
-  if (sp.nsplit == 1) return;  // the attention kernel wrote the output
+  const DecPlan pl = dec_plan(a);
+  if (pl.nsplit == 1) return;  // the attention kernel wrote the output
   const int rq = blockIdx.x;  // row * Hq + qh
+  if (pl.nsplit == 0) {  // compressed attention with nothing visible yet
+    a.o[(int64_t)rq * HD + threadIdx.x] = 0.f;
+    return;
+  }
   const int row = rq / a.Hq, qh = rq % a.Hq;
   const int r = a.Hq / a.Hkv;
   const int hk = qh / r, h = qh % r;
@@ -248,9 +280,9 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
       a.part + ((int64_t)(row * a.Hkv + hk) * a.nsplit_max) * r * (HD + 2) + h * (HD + 2);
   const int64_t stride = (int64_t)r * (HD + 2);
   float gm = -INFINITY;
-  for (int s = 0; s < sp.nsplit; s++) gm = fmaxf(gm, base[s * stride + HD]);
+  for (int s = 0; s < pl.nsplit; s++) gm = fmaxf(gm, base[s * stride + HD]);
   float total = 0.f, o = 0.f;
-  for (int s = 0; s < sp.nsplit; s++) {
+  for (int s = 0; s < pl.nsplit; s++) {
     float sc = expf(base[s * stride + HD] - gm);
     total += base[s * stride + HD + 1] * sc;
     o += base[s * stride + threadIdx.x] * sc;
@@ -262,10 +294,29 @@ static int decode_attention_max_splits(int window, int maxSeq) {
   return dec_split(0, std::min(window + 1, maxSeq)).nsplit;
 }
 
+int decode_attention_split_cap(const DecodeAttnArgs& a) {
+  if (a.ratio > 1) {
+    int n = a.maxBlocks > 0 ? dec_split(0, a.maxBlocks).nsplit : 0;
+    if (a.window > 0) n += decode_attention_max_splits(a.window, a.maxSeq);
+    return std::max(n, 1);
+  }
+  return decode_attention_max_splits(std::max(a.window, 0), a.maxSeq);
+}
+
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= DEC_MAXR, "decode attention: GQA ratio must be <= 8");
   bool combine;
-  if (a.pos_dev) {
+  if (a.ratio > 1) {
+    GN_CHECK(a.ck && a.cv && a.maxBlocks > 0 && a.window >= 0, "decode attention: bad compressed cache");
+    if (a.pos_dev) {
+      a.nsplit_max = decode_attention_split_cap(a);
+    } else {
+      GN_CHECK(a.kend >= 1 && a.kend <= a.maxSeq && (a.kend - 1) / a.ratio <= a.maxBlocks,
+               "decode attention: position outside the caches");
+      a.nsplit_max = std::max(dec_plan_at(a, a.kend - 1).nsplit, 1);
+    }
+    combine = true;  // also writes the zero output of a step with no visible key
+  } else if (a.pos_dev) {
     // position read on the device: size for the longest key range
     GN_CHECK(a.window >= 0, "decode attention: bad window");
     a.nsplit_max = decode_attention_max_splits(a.window, a.maxSeq);
@@ -296,6 +347,23 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
 // window w admits w + 1 keys, kernels/scalar/attention.go:210-228).
 __device__ __forceinline__ bool key_valid(int kj, int t, int T, int window) {
   return kj < T && kj <= t && (window < 0 || t - kj <= window);
+}
+// The flash kernels' mask: causal/windowed keys, or compressed blocks that
+// ended before the query's block (ratio > 1).
+__device__ __forceinline__ bool key_ok(int kj, int t, int Tk, int ratio, int window) {
+  if (ratio > 1) return kj < Tk && (kj + 1) * ratio <= t;
+  return key_valid(kj, t, Tk, window);
+}
+// Key tiles a query block [q0, qlast] needs: [kbeg, kend).
+__device__ __forceinline__ void key_range(int q0, int qlast, int Tk, int ratio, int window,
+                                          int* kbeg, int* kend) {
+  if (ratio > 1) {
+    *kbeg = 0;
+    *kend = min(Tk, qlast / ratio);
+  } else {
+    *kbeg = window >= 0 ? max(0, q0 - window) : 0;
+    *kend = qlast + 1;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -337,8 +405,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
   float m = -INFINITY, l = 0.f;
 
   const int qlast = min(a.T, q0 + FQ) - 1;
-  const int kmin = a.window >= 0 ? max(0, q0 - a.window) : 0;
-  const int kmax = qlast + 1;
+  int kmin, kmax;
+  key_range(q0, qlast, a.Tk, a.ratio, a.window, &kmin, &kmax);
   for (int kt = (kmin / FK) * FK; kt < kmax; kt += FK) {
     __syncthreads();  // previous tile fully consumed
     // K tile rows (coalesced float4), V tile transposed into Vt[d][key]
@@ -348,8 +416,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
       const int kr = idx >> 5, c4 = idx & 31;
       const int kj = kt + kr;
       v4f kv = {0.f, 0.f, 0.f, 0.f};
-      if (kj < a.T) kv = *reinterpret_cast<const v4f*>(
-          a.k + (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4);
+      if (kj < a.Tk) kv = *reinterpret_cast<const v4f*>(
+          a.k + (((int64_t)b * a.Tk + kj) * a.Hkv + hk) * HD + 4 * c4);
       *reinterpret_cast<v4f*>(&Ks[kr * FLK + 4 * c4]) = kv;
     }
 #pragma unroll
@@ -358,8 +426,8 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
       const int kr = idx & 63, c4 = idx >> 6;  // lanes walk keys: conflict-free stores
       const int kj = kt + kr;
       v4f vv = {0.f, 0.f, 0.f, 0.f};
-      if (kj < a.T) vv = *reinterpret_cast<const v4f*>(
-          a.v + (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4);
+      if (kj < a.Tk) vv = *reinterpret_cast<const v4f*>(
+          a.v + (((int64_t)b * a.Tk + kj) * a.Hkv + hk) * HD + 4 * c4);
 #pragma unroll
       for (int j = 0; j < 4; j++) Vt[(4 * c4 + j) * FLV + kr] = vv[j];
     }
@@ -386,7 +454,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int kj = kt + 16 * kb + 4 * g + r;
-        if (!key_valid(kj, t, a.T, a.window)) st[kb][r] = -INFINITY;
+        if (!key_ok(kj, t, a.Tk, a.ratio, a.window)) st[kb][r] = -INFINITY;
         tmax = fmaxf(tmax, st[kb][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -425,15 +493,19 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
       }
   }
   if (active) {
-    const float inv = 1.f / l;
+    // l == 0: no visible key (compressed attention before the first block)
+    const float inv = l > 0.f ? 1.f / l : 0.f;
     float* op = a.o + (((int64_t)b * a.T + t) * a.Hq + qh) * HD + 4 * g;
 #pragma unroll
     for (int i = 0; i < 8; i++) *reinterpret_cast<v4f*>(op + 16 * i) = acc[i] * inv;
-    if (a.lse && g == 0) a.lse[((int64_t)b * a.T + t) * a.Hq + qh] = m + logf(l);
+    if (a.lse && g == 0)
+      a.lse[((int64_t)b * a.T + t) * a.Hq + qh] = l > 0.f ? m + logf(l) : -INFINITY;
   }
 }
 
-void launch_flash_fwd(const FlashArgs& a, hipStream_t st) {
+void launch_flash_fwd(FlashArgs a, hipStream_t st) {
+  if (a.Tk <= 0) a.Tk = a.T;
+  GN_CHECK(a.ratio <= 1 || a.window < 0, "flash: compressed keys take no window");
   hipLaunchKernelGGL(flash_fwd_mfma_kernel, dim3((unsigned)ceil_div(a.T, FQ), a.B * a.Hq),
                      dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
@@ -489,8 +561,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
   for (int i = 0; i < 8; i++) dq[i] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   const int qlast = min(a.T, q0 + FQ) - 1;
-  const int kmin = a.window >= 0 ? max(0, q0 - a.window) : 0;
-  for (int kt = (kmin / FK) * FK; kt <= qlast; kt += FK) {
+  int kmin, kmax;
+  key_range(q0, qlast, a.Tk, a.ratio, a.window, &kmin, &kmax);
+  for (int kt = (kmin / FK) * FK; kt < kmax; kt += FK) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < FK * HD / 4 / 256; i++) {
@@ -498,8 +571,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
       const int kr = idx >> 5, c4 = idx & 31;
       const int kj = kt + kr;
       v4f kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-      if (kj < a.T) {
-        const int64_t off = (((int64_t)b * a.T + kj) * a.Hkv + hk) * HD + 4 * c4;
+      if (kj < a.Tk) {
+        const int64_t off = (((int64_t)b * a.Tk + kj) * a.Hkv + hk) * HD + 4 * c4;
         kv = *reinterpret_cast<const v4f*>(a.k + off);
         vv = *reinterpret_cast<const v4f*>(a.v + off);
       }
@@ -526,7 +599,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int kj = kt + 16 * kb + 4 * g + r;
-        const float p = (active && key_valid(kj, t, a.T, a.window)) ? expf(st[r] - lse) : 0.f;
+        const float p = (active && key_ok(kj, t, a.Tk, a.ratio, a.window)) ? expf(st[r] - lse) : 0.f;
         ds[r] = p * (dpt[r] - dl);
       }
       // dQ^T += K^T dS^T: A = K[16kb + 4g + c][16i + l16]
@@ -540,8 +613,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
   }
   if (active) {
     float* op = a.dq + qrow * HD + 4 * g;
+    if (a.dq_accum) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) *reinterpret_cast<v4f*>(op + 16 * i) = dq[i];
+      for (int i = 0; i < 8; i++)
+        *reinterpret_cast<v4f*>(op + 16 * i) = *reinterpret_cast<const v4f*>(op + 16 * i) + dq[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) *reinterpret_cast<v4f*>(op + 16 * i) = dq[i];
+    }
   }
 }
 
@@ -555,8 +634,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
   const int bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
   const int r = a.Hq / a.Hkv;
   const int j = k0 + 16 * w + l16;  // this lane's key
-  const bool active = j < a.T;
-  const int64_t krow = ((int64_t)b * a.T + min(j, a.T - 1)) * a.Hkv + hk;
+  const bool active = j < a.Tk;
+  const int64_t krow = ((int64_t)b * a.Tk + min(j, a.Tk - 1)) * a.Hkv + hk;
   v4f kf[8], vf[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) {
@@ -569,11 +648,19 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
     dk[i] = (v4f){0.f, 0.f, 0.f, 0.f};
     dv[i] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
-  const int klast = min(a.T, k0 + FK) - 1;
-  const int qend = a.window >= 0 ? min(a.T, klast + a.window + 1) : a.T;
+  const int klast = min(a.Tk, k0 + FK) - 1;
+  // queries that can see a key of the block: [qbeg, qend)
+  int qbeg, qend;
+  if (a.ratio > 1) {
+    qbeg = min(a.T, (k0 + 1) * a.ratio);
+    qend = a.T;
+  } else {
+    qbeg = k0;
+    qend = a.window >= 0 ? min(a.T, klast + a.window + 1) : a.T;
+  }
   for (int h = 0; h < r; h++) {
     const int qh = hk * r + h;
-    for (int qt = (k0 / FQ) * FQ; qt < qend; qt += FQ) {
+    for (int qt = (qbeg / FQ) * FQ; qt < qend; qt += FQ) {
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < FQ * HD / 4 / 256; i++) {
@@ -616,7 +703,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
 #pragma unroll
         for (int rr = 0; rr < 4; rr++) {
           const int ql = 16 * qb + 4 * g + rr, tq = qt + ql;
-          const bool ok = active && tq < a.T && key_valid(j, tq, a.T, a.window);
+          const bool ok = active && tq < a.T && key_ok(j, tq, a.Tk, a.ratio, a.window);
           p[rr] = ok ? expf(sv[rr] - Ls[ql]) : 0.f;
           ds[rr] = p[rr] * (dp[rr] - Ds[ql]);
         }
@@ -643,15 +730,20 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
   }
 }
 
-void launch_flash_bwd(const FlashBwdArgs& a, hipStream_t st) {
-  int64_t rows = (int64_t)a.B * a.T * a.Hq;
-  hipLaunchKernelGGL(flash_delta_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st, a.o,
-                     a.dout, a.delta, rows);
+void launch_row_dot(const float* o, const float* dout, float* delta, int64_t rows, hipStream_t st) {
+  hipLaunchKernelGGL(flash_delta_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st, o,
+                     dout, delta, rows);
   GN_HIP(hipGetLastError());
+}
+
+void launch_flash_bwd(FlashBwdArgs a, hipStream_t st) {
+  if (a.Tk <= 0) a.Tk = a.T;
+  GN_CHECK(a.ratio <= 1 || a.window < 0, "flash: compressed keys take no window");
+  if (!a.delta_ready) launch_row_dot(a.o, a.dout, a.delta, (int64_t)a.B * a.T * a.Hq, st);
   hipLaunchKernelGGL(flash_bwd_dq_mfma_kernel, dim3((unsigned)ceil_div(a.T, FQ), a.B * a.Hq),
                      dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
-  hipLaunchKernelGGL(flash_bwd_dkdv_mfma_kernel, dim3((unsigned)ceil_div(a.T, FK), a.B * a.Hkv),
+  hipLaunchKernelGGL(flash_bwd_dkdv_mfma_kernel, dim3((unsigned)ceil_div(a.Tk, FK), a.B * a.Hkv),
                      dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }

@@ -57,19 +57,41 @@ struct DecodeAttnArgs {
   const int* pos_dev;  // the query position is *pos_dev (read on the device,
   int window;          // so a captured graph serves every step) and the keys
                        // are [max(0, pos - window), pos]
+  // Compressed attention (ratio > 1): the keys are the compressed blocks
+  // [0, pos / ratio) of ck/cv ([rows][Hkv][maxBlocks][128]) followed, when
+  // window > 0, by the raw keys [max(0, pos - window), pos] of kc/vc: one
+  // softmax over both, which is the log-sum-exp merge of the global and
+  // local branches (model/compress_attention.go:440-484, 543-560).  With
+  // neither (pos < ratio, no window) the output is zero.  kend - 1 is the
+  // query position of eager launches.
+  const float* ck = nullptr;
+  const float* cv = nullptr;
+  int maxBlocks = 0;
+  int ratio = 0;
   int nsplit_max;      // set by the launcher: grid.y and the split stride of part
 };
+// Split capacity a part buffer needs for launches with these arguments
+// (window, maxSeq, ratio, maxBlocks).
+int decode_attention_split_cap(const DecodeAttnArgs& a);
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st);
 
+// Key masks of the flash kernels.  ratio <= 1: causal with a sliding window
+// (key j visible from query t when j <= t and t - j <= window, window < 0:
+// none).  ratio > 1: the keys are compressed blocks of `ratio` positions and
+// query t sees the blocks that ended before its own, j < t / ratio
+// (model/compress_attention.go:562-677); a query with no visible key gets a
+// zero output and log-sum-exp -inf.
 struct FlashArgs {
   const float* q;  // [B*T, Hq, 128]
-  const float* k;  // [B*T, Hkv, 128]
+  const float* k;  // [B*Tk, Hkv, 128]
   const float* v;
   float* o;        // [B*T, Hq, 128]
   float* lse;      // [B*T, Hq] or null
   int B, T, Hq, Hkv, window;
+  int Tk = 0;      // keys per sequence (0: T)
+  int ratio = 0;
 };
-void launch_flash_fwd(const FlashArgs& a, hipStream_t st);
+void launch_flash_fwd(FlashArgs a, hipStream_t st);
 
 struct FlashBwdArgs {
   const float* q;
@@ -78,13 +100,19 @@ struct FlashBwdArgs {
   const float* o;
   const float* dout;
   const float* lse;
-  float* delta;  // [B*T, Hq] scratch
-  float* dq;     // [B*T, Hq, 128] (overwritten)
-  float* dk;     // [B*T, Hkv, 128] (overwritten)
+  float* delta;  // [B*T, Hq]: rowsum(dO * O), computed here unless delta_ready
+  float* dq;     // [B*T, Hq, 128] (overwritten, or accumulated with dq_accum)
+  float* dk;     // [B*Tk, Hkv, 128] (overwritten)
   float* dv;
   int B, T, Hq, Hkv, window;
+  int Tk = 0;
+  int ratio = 0;
+  bool delta_ready = false;  // branches of a merged softmax share the merged
+  bool dq_accum = false;     // log-sum-exp and row correction dO . O_merged
 };
-void launch_flash_bwd(const FlashBwdArgs& a, hipStream_t st);
+void launch_flash_bwd(FlashBwdArgs a, hipStream_t st);
+// delta[r] = dO[r, :] . O[r, :] over rows of 128
+void launch_row_dot(const float* o, const float* dout, float* delta, int64_t rows, hipStream_t st);
 
 // ---- loss ----------------------------------------------------------------
 void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t rows,
@@ -263,6 +291,58 @@ struct MoeBwdCombineArgs {
   float* out;
 };
 void launch_moe_bwd_combine(const MoeBwdCombineArgs& a, int64_t rows, hipStream_t st);
+
+// ---- flash preset: compressed attention (model/compress*.go) --------------
+bool hca_ratio_supported(int ratio);
+struct HcaCompressArgs {
+  const float* clog;  // [B*T, 128] h . Wl^T (the bias is added here)
+  const float* bias;  // [ratio, 128]
+  const float* k;     // [B*T, Hkv, 128] keys after norm and rotary
+  const float* v;     // [B*T, Hkv, 128]
+  int B, T, Hkv, ratio;
+  float* probs;       // [B*blocks][ratio][128] softmax weights (saved for the backward)
+  float* kc;          // [B*blocks, Hkv, 128] compressed keys
+  float* vc;
+  // prefill (optional): compressed keys/values of the complete blocks as a
+  // cache [B][Hkv][T / ratio][128], and the logits of an incomplete last
+  // block into its ring [B][ratio][128] (slot = position % ratio)
+  float* ck_pf = nullptr;
+  float* cv_pf = nullptr;
+  float* ring_pf = nullptr;
+};
+void launch_hca_compress(const HcaCompressArgs& a, hipStream_t st);
+void launch_merge_branches(const float* oa, const float* la, const float* ob, const float* lb,
+                           float* out, float* lse, int64_t rows, hipStream_t st);
+struct HcaCompressBwdArgs {
+  const float* probs;
+  const float* k;
+  const float* v;
+  const float* kc;
+  const float* vc;
+  const float* dkc;  // [B*blocks, Hkv, 128] gradients of the compressed keys/values
+  const float* dvc;
+  int B, T, Hkv, ratio;
+  float* glog;       // [B*T, 128] logit gradient (overwritten)
+  float* dk;         // [B*T, Hkv, 128] accumulated
+  float* dv;
+  float* gbias;      // [ratio, 128] accumulated
+  float* bias_part;  // hca_bias_part_floats(ratio) scratch
+};
+size_t hca_bias_part_floats(int ratio);
+void launch_hca_compress_bwd(const HcaCompressBwdArgs& a, hipStream_t st);
+struct HcaDecodeArgs {
+  const float* clog;  // [rows, 128] this token's h . Wl^T
+  const float* bias;
+  float* ring;        // [rows][ratio][128] logits of the current block
+  const float* kc;    // layer base of the raw caches [rows][Hkv][maxSeq][128]
+  const float* vc;
+  float* ck;          // layer base of the compressed caches [rows][Hkv][maxBlocks][128]
+  float* cv;
+  int rows, Hkv, ratio, maxSeq, maxBlocks;
+  int pos;             // position of this token (eager launches)
+  const int* pos_dev;  // when set, read on the device
+};
+void launch_hca_decode_compress(const HcaDecodeArgs& a, hipStream_t st);
 
 // ---- sampler (inference/sampler.go + tensors/random.go) -------------------
 struct SamplerArgs {

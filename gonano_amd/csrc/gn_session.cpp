@@ -70,6 +70,9 @@ struct Layer {
   // MoE: wgu = [c_gate; c_fc] of the shared expert, router, packed experts
   float *wgu, *ggu, *wr, *rbias, *gwr;
   float *eg, *eu, *ed, *geg, *geu, *ged;
+  // flash preset: the layer's channel compressor (logit weight [128, C] and
+  // per-slot bias [ratio, 128])
+  float *wcl, *gcl, *cbias, *gcbias;
 };
 
 }  // namespace gn
@@ -87,6 +90,13 @@ struct gn_session {
   float clamp = 0.f, mscale = 1.f, bw = 0.f;
   bool derived_dirty = true;
   float* derived = nullptr;
+  // flash preset: compressed attention (ratio > 1) with a local window
+  bool hca = false;
+  int ratio = 1, swa = 0;
+  // decode-time compressed caches of the current rollout: [L][rows][Hkv]
+  // [maxBlocks][128] keys and values, [L][rows][ratio][128] logit rings
+  float *hck = nullptr, *hcv = nullptr, *hring = nullptr;
+  int maxBlocks = 0;
   double aux_loss = 0.0;
   int64_t total = 0;
   hipStream_t stream = nullptr;
@@ -250,6 +260,18 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     s->R = cfg.rotary_dims <= 0 ? s->D : cfg.rotary_dims;
   }
   GN_CHECK(s->R <= s->D && s->R % 2 == 0, "config: RotaryDims must be even and <= head dim");
+  if (cfg.sparse_topk > 0 || strnlen(cfg.reuse_pattern, sizeof(cfg.reuse_pattern)) > 0 || cfg.ced)
+    throw Error(GN_ERR_UNSUPPORTED,
+                "session: sparse attention, cross-layer reuse and CED prefill are not built yet");
+  s->hca = cfg.compression_ratio > 1;  // Config.Compression() (config.go:407-414)
+  if (s->hca) {
+    GN_CHECK(!s->mla, "config: MLA is not supported with compression");  // config.go:483-486
+    GN_CHECK(hca_ratio_supported(cfg.compression_ratio),
+             "session: compression ratio must be 2..8 or 16");
+    GN_CHECK(cfg.swa_window >= 0, "config: negative SWA window");
+    s->ratio = cfg.compression_ratio;
+    s->swa = cfg.swa_window;
+  }
   GN_CHECK(s->C <= 1024, "session: EmbedDim above 1024 is not supported");
   GN_CHECK(s->Hq / s->Hkv <= 8, "session: GQA ratio above 8 is not supported");
   GN_CHECK(s->Hq + 2 * s->Hkv <= 16, "session: at most 16 q+k+v heads");
@@ -300,6 +322,7 @@ static void build_session(gn_session* s, const gn_config& cfg) {
   struct Off {
     int64_t qkv = -1, o = -1, fc = -1, pj = -1, vg = -1, ve = -1;
     int64_t xa = -1, qu = -1, kvu = -1, gu = -1, r = -1, rb = -1, eg = -1, eu = -1, ed = -1;
+    int64_t cl = -1, cb = -1;
   };
   std::vector<Off> off(s->L);
   const int C = s->C, D = s->D, Hq = s->Hq, Hkv = s->Hkv, F = s->F;
@@ -326,6 +349,12 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     }
     o.o = place((int64_t)C * C);
     add(p + "attn.c_proj.weight", C, C, o.o);
+    if (s->hca) {  // model/params.go:43-46
+      o.cl = place((int64_t)D * C);
+      add(p + "attn.compress_logits.weight", D, C, o.cl);
+      o.cb = place((int64_t)s->ratio * D);
+      add(p + "attn.compress_bias", s->ratio, D, o.cb);
+    }
     if (!s->mla && has_value_embedding(l, s->L)) {  // no VE under MLA (transformer.go:72-78)
       o.vg = place((int64_t)Hkv * VE_CH);
       add(p + "attn.ve_gate.weight", Hkv, VE_CH, o.vg);
@@ -395,6 +424,8 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     ly.eg = P(o.eg); ly.geg = G(o.eg);
     ly.eu = P(o.eu); ly.geu = G(o.eu);
     ly.ed = P(o.ed); ly.ged = G(o.ed);
+    ly.wcl = P(o.cl); ly.gcl = G(o.cl);
+    ly.cbias = P(o.cb); ly.gcbias = G(o.cb);
   }
   if (s->mla) {  // absorbed decode weights, per layer [Hq*lat, lat] and [C, Hq*lat]
     const int64_t per = (int64_t)Hq * s->lat * s->lat + (int64_t)C * Hq * s->lat;
@@ -460,6 +491,11 @@ struct SeqBuffers {
   std::vector<float*> xin, xb, h, qrot, krot, qn, kn, v, vesig, o, lse, mid, h2, u, act;
   std::vector<float*> xa, gu;  // latent preset: MLA xa rows, shared-expert [gate | up]
   std::vector<MoeBuffers> moe;
+  // flash preset: per layer the compressed keys/values and the compressor's
+  // softmax weights; prefill outputs (layer-major) of the compressed caches
+  // [L][B][Hkv][T / ratio][128] and of the logit rings [L][B][ratio][128]
+  std::vector<float*> hkc, hvc, hprobs;
+  float *pf_ck = nullptr, *pf_cv = nullptr, *pf_ring = nullptr;
   float *xfinal, *fpre, *fn;
   float* backout;
 };
@@ -537,6 +573,61 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
   launch_moe_combine(ca, rows, st);
 }
 
+// Compressed attention of one layer over full sequences (model/train.go:
+// 99-169 with compressForward / compressedAttentionForward,
+// compress_attention.go:562-677): compressor logits on the matrix cores, the
+// compressor, the global branch over compressed blocks and, with a window,
+// the local branch, merged by log-sum-exp.  Writes sb.o[l] (and sb.lse[l],
+// the merged log-sum-exp, when training).
+static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, SeqMode mode) {
+  const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, B = sb.B, T = sb.T, ratio = s->ratio;
+  const int64_t N = sb.N;
+  const bool save = mode == SEQ_TRAIN;
+  hipStream_t st = s->stream;
+  const int blocks = (int)ceil_div(T, ratio);
+  float* clog = A<float>(s, "hca_clog", N * HD);
+  sgemm(s, linear_fwd_desc(sb.h[l], ly.wcl, clog, (int)N, C, HD));
+  HcaCompressArgs ca{};
+  ca.clog = clog; ca.bias = ly.cbias; ca.k = sb.kn[l]; ca.v = sb.v[l];
+  ca.B = B; ca.T = T; ca.Hkv = Hkv; ca.ratio = ratio;
+  ca.probs = layer_buf(s, "hca_probs", l, save, (size_t)B * blocks * ratio * HD);
+  ca.kc = layer_buf(s, "hca_kc", l, save, (size_t)B * blocks * s->KVW);
+  ca.vc = layer_buf(s, "hca_vc", l, save, (size_t)B * blocks * s->KVW);
+  if (mode == SEQ_PREFILL) {
+    const int64_t full = T / ratio;
+    if (full > 0) {
+      ca.ck_pf = sb.pf_ck + (int64_t)l * B * Hkv * full * HD;
+      ca.cv_pf = sb.pf_cv + (int64_t)l * B * Hkv * full * HD;
+    }
+    ca.ring_pf = sb.pf_ring + (int64_t)l * B * ratio * HD;
+  }
+  launch_hca_compress(ca, st);
+  sb.hkc[l] = ca.kc; sb.hvc[l] = ca.vc; sb.hprobs[l] = ca.probs;
+  float* o = layer_buf(s, "o", l, save, N * Hq * HD);
+  float* lse = save ? layer_buf(s, "lse", l, true, N * Hq) : A<float>(s, "hca_lse", N * Hq);
+  FlashArgs fg{};
+  fg.q = sb.qn[l]; fg.k = ca.kc; fg.v = ca.vc;
+  fg.B = B; fg.T = T; fg.Tk = blocks; fg.ratio = ratio; fg.Hq = Hq; fg.Hkv = Hkv; fg.window = -1;
+  if (s->swa > 0) {
+    fg.o = A<float>(s, "hca_og", N * Hq * HD);
+    fg.lse = A<float>(s, "hca_lg", N * Hq);
+    launch_flash_fwd(fg, st);
+    FlashArgs fl{};  // localAttentionRow over the sliding window (compress_attention.go:543-560)
+    fl.q = sb.qn[l]; fl.k = sb.kn[l]; fl.v = sb.v[l];
+    fl.o = A<float>(s, "hca_ol", N * Hq * HD);
+    fl.lse = A<float>(s, "hca_ll", N * Hq);
+    fl.B = B; fl.T = T; fl.Hq = Hq; fl.Hkv = Hkv; fl.window = s->swa;
+    launch_flash_fwd(fl, st);
+    launch_merge_branches(fg.o, fg.lse, fl.o, fl.lse, o, lse, N * Hq, st);
+  } else {
+    fg.o = o;
+    fg.lse = lse;
+    launch_flash_fwd(fg, st);
+  }
+  sb.o[l] = o;
+  sb.lse[l] = save ? lse : nullptr;
+}
+
 static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcache_pf,
                         float* vcache_pf) {
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, F = s->F, L = s->L;
@@ -550,7 +641,8 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   sb.x0 = A<float>(s, "x0", N * C);
   launch_embed_smear(sb.ids, s->wte, s->smg, s->sml, B, T, C, sb.raw, sb.embn, sb.smsig, sb.x0, st);
   for (auto* vec : {&sb.xin, &sb.xb, &sb.h, &sb.qrot, &sb.krot, &sb.qn, &sb.kn, &sb.v, &sb.vesig,
-                    &sb.o, &sb.lse, &sb.mid, &sb.h2, &sb.u, &sb.act, &sb.xa, &sb.gu})
+                    &sb.o, &sb.lse, &sb.mid, &sb.h2, &sb.u, &sb.act, &sb.xa, &sb.gu, &sb.hkc,
+                    &sb.hvc, &sb.hprobs})
     vec->assign(L, nullptr);
   sb.moe.assign(L, MoeBuffers{});
   float* qkv = s->mla ? nullptr : A<float>(s, "qkv", N * s->QKVW);
@@ -615,15 +707,19 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     sb.qn[l] = qa.qn; sb.kn[l] = qa.kn; sb.v[l] = qa.vout;
     sb.qrot[l] = qa.qrot; sb.krot[l] = qa.krot; sb.vesig[l] = qa.vesig;
     }
-    FlashArgs fa{};
-    fa.q = sb.qn[l]; fa.k = sb.kn[l]; fa.v = sb.v[l];
-    fa.o = layer_buf(s, "o", l, save, N * Hq * HD);
-    fa.lse = save ? layer_buf(s, "lse", l, true, N * Hq) : nullptr;
-    fa.B = B; fa.T = T; fa.Hq = Hq; fa.Hkv = Hkv; fa.window = ly.window;
-    launch_flash_fwd(fa, st);
-    sb.o[l] = fa.o; sb.lse[l] = fa.lse;
+    if (s->hca) {
+      hca_forward(s, sb, ly, l, mode);
+    } else {
+      FlashArgs fa{};
+      fa.q = sb.qn[l]; fa.k = sb.kn[l]; fa.v = sb.v[l];
+      fa.o = layer_buf(s, "o", l, save, N * Hq * HD);
+      fa.lse = save ? layer_buf(s, "lse", l, true, N * Hq) : nullptr;
+      fa.B = B; fa.T = T; fa.Hq = Hq; fa.Hkv = Hkv; fa.window = ly.window;
+      launch_flash_fwd(fa, st);
+      sb.o[l] = fa.o; sb.lse[l] = fa.lse;
+    }
     float* mid = layer_buf(s, "mid", l, save, N * C);
-    GemmDesc go = linear_fwd_desc(fa.o, ly.wo, mid, (int)N, Hq * HD, C, EPI_ADD_SRC);
+    GemmDesc go = linear_fwd_desc(sb.o[l], ly.wo, mid, (int)N, Hq * HD, C, EPI_ADD_SRC);
     go.aux = xb; go.ldaux = C;
     sgemm(s, go);
     sb.mid[l] = mid;
@@ -799,6 +895,52 @@ static void mla_backward(gn_session* s, const Layer& ly, const float* xa, const 
 // ---------------------------------------------------------------------------
 // PolicyGradientStep
 // ---------------------------------------------------------------------------
+// Backward of hca_forward (model/train.go:211-303 with compressedAttention-
+// Backward, attentionBackwardWindowed and compressBackward,
+// compress_attention.go:376-433, 737-845, 1182-1209): both branches from the
+// merged log-sum-exp and the merged row correction dO . O, the compressor's
+// softmax backward into the raw key/value gradients, its weight and bias
+// gradients.  Returns the compressor's logit gradient [N, 128], whose product
+// with the logit weight the caller adds to the attention input's gradient.
+static float* hca_backward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l,
+                           const float* dout, float* delta, float* dqn, float* dkn, float* dvv) {
+  const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, B = sb.B, T = sb.T, ratio = s->ratio;
+  const int64_t N = sb.N;
+  hipStream_t st = s->stream;
+  const int blocks = (int)ceil_div(T, ratio);
+  launch_row_dot(sb.o[l], dout, delta, N * Hq, st);
+  float* dkc = A<float>(s, "hca_dkc", (size_t)B * blocks * s->KVW);
+  float* dvc = A<float>(s, "hca_dvc", (size_t)B * blocks * s->KVW);
+  FlashBwdArgs bg{};
+  bg.q = sb.qn[l]; bg.k = sb.hkc[l]; bg.v = sb.hvc[l]; bg.o = sb.o[l]; bg.dout = dout;
+  bg.lse = sb.lse[l]; bg.delta = delta; bg.delta_ready = true;
+  bg.dq = dqn; bg.dk = dkc; bg.dv = dvc;
+  bg.B = B; bg.T = T; bg.Tk = blocks; bg.ratio = ratio; bg.Hq = Hq; bg.Hkv = Hkv; bg.window = -1;
+  launch_flash_bwd(bg, st);
+  if (s->swa > 0) {
+    FlashBwdArgs bl{};
+    bl.q = sb.qn[l]; bl.k = sb.kn[l]; bl.v = sb.v[l]; bl.o = sb.o[l]; bl.dout = dout;
+    bl.lse = sb.lse[l]; bl.delta = delta; bl.delta_ready = true;
+    bl.dq = dqn; bl.dq_accum = true; bl.dk = dkn; bl.dv = dvv;
+    bl.B = B; bl.T = T; bl.Hq = Hq; bl.Hkv = Hkv; bl.window = s->swa;
+    launch_flash_bwd(bl, st);
+  } else {
+    GN_HIP(hipMemsetAsync(dkn, 0, sizeof(float) * N * s->KVW, st));
+    GN_HIP(hipMemsetAsync(dvv, 0, sizeof(float) * N * s->KVW, st));
+  }
+  HcaCompressBwdArgs cb{};
+  cb.probs = sb.hprobs[l]; cb.k = sb.kn[l]; cb.v = sb.v[l]; cb.kc = sb.hkc[l]; cb.vc = sb.hvc[l];
+  cb.dkc = dkc; cb.dvc = dvc;
+  cb.B = B; cb.T = T; cb.Hkv = Hkv; cb.ratio = ratio;
+  cb.glog = A<float>(s, "hca_glog", N * HD);
+  cb.dk = dkn; cb.dv = dvv;
+  cb.gbias = ly.gcbias;
+  cb.bias_part = A<float>(s, "hca_bpart", hca_bias_part_floats(ratio));
+  launch_hca_compress_bwd(cb, st);
+  sgemm(s, linear_dw_desc(cb.glog, sb.h[l], ly.gcl, (int)N, C, HD));
+  return cb.glog;
+}
+
 static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets, int B, int T,
                     const float* adv, float norm, float* loss_out, float* nll_out) {
   GN_CHECK(B > 0 && T > 1, "policy gradient step: need batch > 0 and seq_len > 1");
@@ -893,11 +1035,16 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     float* dout = dtmp;  // [N, Hq*D] (Hq*D == C)
     sgemm(s, linear_dx_desc(gmid, ly.wo, dout, (int)N, Hq * HD, C));
     sgemm(s, linear_dw_desc(gmid, sb.o[l], ly.go, (int)N, Hq * HD, C));
-    FlashBwdArgs fb{};
-    fb.q = sb.qn[l]; fb.k = sb.kn[l]; fb.v = sb.v[l]; fb.o = sb.o[l]; fb.dout = dout;
-    fb.lse = sb.lse[l]; fb.delta = delta; fb.dq = dqn; fb.dk = dkn; fb.dv = dvv;
-    fb.B = B; fb.T = T; fb.Hq = Hq; fb.Hkv = Hkv; fb.window = ly.window;
-    launch_flash_bwd(fb, st);
+    float* glog = nullptr;
+    if (s->hca) {
+      glog = hca_backward(s, sb, ly, l, dout, delta, dqn, dkn, dvv);
+    } else {
+      FlashBwdArgs fb{};
+      fb.q = sb.qn[l]; fb.k = sb.kn[l]; fb.v = sb.v[l]; fb.o = sb.o[l]; fb.dout = dout;
+      fb.lse = sb.lse[l]; fb.delta = delta; fb.dq = dqn; fb.dk = dkn; fb.dv = dvv;
+      fb.B = B; fb.T = T; fb.Hq = Hq; fb.Hkv = Hkv; fb.window = ly.window;
+      launch_flash_bwd(fb, st);
+    }
     float* dh = dout;  // reuse: dout no longer needed
     if (s->mla) {
       mla_backward(s, ly, sb.xa[l], sb.h[l], dqn, dkn, dvv, N, T, dh);
@@ -912,6 +1059,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     sgemm(s, linear_dx_desc(dqkv, ly.wqkv, dh, (int)N, C, s->QKVW));
     sgemm(s, linear_dw_desc(dqkv, sb.h[l], ly.gqkv, (int)N, C, s->QKVW));
     if (ly.has_ve) launch_ve_gate_bwd(dpre, sb.h[l], ly.wve, C, Hkv, N, ly.gwve, dh, part, st);
+    if (glog) sgemm(s, linear_dx_desc(glog, ly.wcl, dh, (int)N, C, HD, EPI_ACCUM));
     }
     launch_rmsnorm_bwd(sb.xb[l], dh, gmid, N, C, gb, st);
     // residual mixing (train_transformer.go:218-240)
@@ -1041,8 +1189,14 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   float* o = s->mla ? nullptr : A<float>(s, "dec_o", (size_t)rows * Hq * HD);
   float* act = A<float>(s, "dec_act", (size_t)rows * F);
   float* back = A<float>(s, "dec_back", (size_t)rows * C);
+  int part_splits = (maxSeq + 63) / 64;
+  if (s->hca) {
+    DecodeAttnArgs cap{};
+    cap.maxSeq = maxSeq; cap.window = s->swa; cap.ratio = s->ratio; cap.maxBlocks = s->maxBlocks;
+    part_splits = decode_attention_split_cap(cap);
+  }
   float* part = s->mla ? nullptr
-                       : A<float>(s, "dec_part", (size_t)rows * Hkv * ((maxSeq + 63) / 64) *
+                       : A<float>(s, "dec_part", (size_t)rows * Hkv * part_splits *
                                                      (Hq / Hkv) * (HD + 2));
   launch_embed_decode(dtok, s->wte, s->smg, s->sml, rows, C, prev, x, x0, st);
   const int bk = L / 2;
@@ -1072,8 +1226,29 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     da.kend = pos + 1;
     da.pos_dev = dpos;
     da.window = ly.window;
+    int64_t nkeys = da.kend - da.kstart;
+    if (s->hca) {
+      // forwardCompressed (compress_attention.go:895-1006): compress a
+      // completed block, then attend to the compressed blocks before this
+      // token's block and to the local window
+      float* clog = A<float>(s, "dec_clog", (size_t)rows * HD);
+      sgemm(s, linear_fwd_desc(h, ly.wcl, clog, rows, C, HD));
+      HcaDecodeArgs hd{};
+      hd.clog = clog; hd.bias = ly.cbias;
+      hd.ring = s->hring + (int64_t)l * rows * s->ratio * HD;
+      hd.kc = qa.kcache; hd.vc = qa.vcache;
+      hd.ck = s->hck + (int64_t)l * rows * Hkv * s->maxBlocks * HD;
+      hd.cv = s->hcv + (int64_t)l * rows * Hkv * s->maxBlocks * HD;
+      hd.rows = rows; hd.Hkv = Hkv; hd.ratio = s->ratio; hd.maxSeq = maxSeq;
+      hd.maxBlocks = s->maxBlocks; hd.pos = pos; hd.pos_dev = dpos;
+      launch_hca_decode_compress(hd, st);
+      da.ck = hd.ck; da.cv = hd.cv; da.maxBlocks = s->maxBlocks; da.ratio = s->ratio;
+      da.window = s->swa;
+      da.kstart = 0;
+      nkeys = pos / s->ratio + (s->swa > 0 ? pos - std::max(0, pos - s->swa) + 1 : 0);
+    }
     if (s->timing && !s->capturing) {
-      timed_attention(s, 2.0 * rows * Hkv * HD * 4.0 * (da.kend - da.kstart),
+      timed_attention(s, 2.0 * rows * Hkv * HD * 4.0 * nkeys,
                       [&] { launch_decode_attention(da, st); });
     } else {
       launch_decode_attention(da, st);
@@ -1134,6 +1309,13 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   const size_t vw = s->mla ? (size_t)Hkv * s->rd : (size_t)Hkv * HD;
   float* kpf = A<float>(s, "pf_k", (size_t)L * G * P * kw);
   float* vpf = A<float>(s, "pf_v", (size_t)L * G * P * vw);
+  const int maxSeq = W;
+  const int pfull = s->hca ? P / s->ratio : 0;  // complete blocks of the prompt
+  if (s->hca) {
+    sb.pf_ck = A<float>(s, "pf_hck", (size_t)L * G * Hkv * std::max(pfull, 1) * HD);
+    sb.pf_cv = A<float>(s, "pf_hcv", (size_t)L * G * Hkv * std::max(pfull, 1) * HD);
+    sb.pf_ring = A<float>(s, "pf_ring", (size_t)L * G * s->ratio * HD);
+  }
   seq_forward(s, sb, SEQ_PREFILL, kpf, vpf);
   // last-position logits of each prompt, expanded to its S rows (engine.go:182-191)
   float* lastfn = A<float>(s, "pf_lastfn", (size_t)rows * C);
@@ -1141,9 +1323,24 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   float* logits = A<float>(s, "dec_logits", (size_t)rows * V);
   sgemm(s, linear_fwd_desc(lastfn, s->lm, logits, rows, C, V, EPI_SOFTCAP));
   // 2) PrefillFrom (kvcache.go:383-448): replicate KV and the smear state
-  const int maxSeq = W;
   float* kc = A<float>(s, "kv_k", (size_t)L * rows * maxSeq * kw);
   float* vc = A<float>(s, "kv_v", (size_t)L * rows * maxSeq * vw);
+  if (s->hca) {  // compressed caches and logit rings (kvcache.go:142-220, 276-378)
+    s->maxBlocks = maxSeq / s->ratio + 1;
+    const size_t cbytes = (size_t)L * rows * Hkv * s->maxBlocks * HD;
+    s->hck = A<float>(s, "kv_hck", cbytes);
+    s->hcv = A<float>(s, "kv_hcv", cbytes);
+    s->hring = A<float>(s, "kv_ring", (size_t)L * rows * s->ratio * HD);
+    for (int l = 0; l < L; l++) {
+      const int64_t dst = (int64_t)l * rows * Hkv * s->maxBlocks * HD;
+      const int64_t src = (int64_t)l * G * Hkv * pfull * HD;
+      launch_replicate_kv(sb.pf_ck + src, s->hck + dst, G, S, Hkv, pfull, pfull, s->maxBlocks, st);
+      launch_replicate_kv(sb.pf_cv + src, s->hcv + dst, G, S, Hkv, pfull, pfull, s->maxBlocks, st);
+      launch_replicate_rows(sb.pf_ring + (int64_t)l * G * s->ratio * HD,
+                            s->hring + (int64_t)l * rows * s->ratio * HD, G, S, s->ratio, HD,
+                            s->ratio, s->ratio, st);
+    }
+  }
   for (int l = 0; l < L; l++) {
     if (s->mla) {
       launch_replicate_rows(kpf + (int64_t)l * G * P * kw, kc + (int64_t)l * rows * maxSeq * kw, G,

@@ -16,15 +16,22 @@ from ._lib import GnConfig, GnTiming, call, lib
 from .config import Config
 
 
+def gn_config_of(cfg: Config) -> GnConfig:
+    """The C-ABI gn_config of a host Config (resolved preset values)."""
+    return GnConfig(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head,
+                    cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern.encode(),
+                    cfg.mla_latent, cfg.mla_rope_dimension if cfg.mla else 0,
+                    cfg.n_experts, cfg.experts_per_token, cfg.expert_hidden,
+                    cfg.shared_hidden, cfg.moe_clamp, cfg.moe_scale, cfg.balance_weight,
+                    cfg.compression_ratio if cfg.compression > 1 else 0,
+                    cfg.swa_window if cfg.compression > 1 else 0)
+
+
 class Session:
     def __init__(self, cfg: Config, device: int = 0):
         cfg.validate()
         self.cfg = cfg
-        self._c = GnConfig(cfg.sequence_len, cfg.vocab_size, cfg.n_layer, cfg.n_head,
-                           cfg.n_kv_head, cfg.n_embd, cfg.rotary_dims, cfg.window_pattern.encode(),
-                           cfg.mla_latent, cfg.mla_rope_dimension if cfg.mla else 0,
-                           cfg.n_experts, cfg.experts_per_token, cfg.expert_hidden,
-                           cfg.shared_hidden, cfg.moe_clamp, cfg.moe_scale, cfg.balance_weight)
+        self._c = gn_config_of(cfg)
         h = C.c_void_p()
         call("gn_session_create", C.byref(self._c), device, C.byref(h))
         self._h = h

@@ -149,7 +149,19 @@ int gn_attention_combine(const float *const *accumulators, const float *const *m
  * token, outputs scaled by moe_scale, SwiGLU clamp moe_clamp and the
  * sequence-level balance loss weight balance_weight
  * (Config.MoEActiveExperts / MoEExpertHidden / MoESharedHidden /
- * MoEEffectiveScale / MoEEffectiveClamp / MoEBalanceLossWeight). */
+ * MoEEffectiveScale / MoEEffectiveClamp / MoEBalanceLossWeight).
+ *
+ * The flash preset's fields (model/preset.go:93-118, model/config.go:9-124):
+ * compression_ratio > 1 makes every layer's attention compressed (HCA,
+ * Config.Compression(): a channel compressor per layer reduces each block of
+ * compression_ratio positions to one key/value row; queries attend to the
+ * blocks before their own) merged with a sliding-window local branch of
+ * swa_window keys (Config.SWAWindowSize(); 0: none).  sparse_topk,
+ * indexer_dim, indexer_heads, indexer_pool, indexer_candidates,
+ * indexer_weight (the CSA lightning indexer), reuse_pattern (FRU cross-layer
+ * reuse, e.g. "FRU") and ced (encoder/decoder prefill) are carried with the
+ * reference's meaning; gn_session_create rejects non-zero values of them
+ * with GN_ERR_UNSUPPORTED until the session implements them. */
 typedef struct gn_config {
   int32_t sequence_len;
   int32_t vocab_size;
@@ -168,6 +180,16 @@ typedef struct gn_config {
   float moe_clamp;
   float moe_scale;
   float balance_weight;
+  int32_t compression_ratio;
+  int32_t swa_window;
+  int32_t sparse_topk;
+  int32_t indexer_dim;
+  int32_t indexer_heads;
+  int32_t indexer_pool;
+  int32_t indexer_candidates;
+  float indexer_weight;
+  char reuse_pattern[16];
+  int32_t ced;
 } gn_config;
 
 typedef struct gn_session gn_session;
