@@ -47,6 +47,14 @@ class Config:
     balance_weight: float = 0.0  # MoEBalanceLossWeight()
     compression_ratio: int = 0   # Config.CompressionRatio (> 1: HCA compressed layers)
     swa_window: int = 0          # Config.SWAWindowSize(): local branch of compressed layers
+    sparse_topk: int = 0         # Config.SparseTopK (> 0: CSA lightning-indexer selection)
+    indexer_dim: int = 0         # Config.IndexerDim (0: 64)
+    indexer_heads: int = 0       # Config.IndexerHeads (0: 1)
+    indexer_pool: int = 0        # Config.IndexerPool (> 1: hierarchical indexer)
+    indexer_candidates: int = 0  # Config.IndexerCandidates (0: max(8*SparseTopK, 64))
+    indexer_weight: float = 0.0  # Config.IndexerLossWeight (0: 1)
+    reuse_pattern: str = ""      # Config.ReusePattern ("FRU": Full / Reindex / Reuse layers)
+    ced: bool = False            # Config.CED (causal encoder-decoder split)
 
     # -- derived quantities -------------------------------------------------
     @property
@@ -96,6 +104,42 @@ class Config:
     def mlp_hidden(self) -> int:  # model/mlp.go:35-37, model/block.go:23-28
         return self.shared_hidden if self.moe else 4 * self.n_embd
 
+    # -- flash preset layer roles (model/config.go:282-402) ------------------
+    @property
+    def ced_split(self) -> int:
+        return self.n_layer // 2 if self.ced else 0
+
+    def _reuse_start(self, layer: int) -> int:
+        split = self.ced_split
+        return split if (self.ced and split > 0 and layer >= split) else 0
+
+    def reuse_mode_at(self, layer: int) -> str:
+        """'F' (owns compressor and indexer), 'R' (own indexer on the group's
+        compressed KV) or 'U' (reuses both), config.go:326-344."""
+        if not self.reuse_pattern:
+            return "F"
+        ch = self.reuse_pattern[(layer - self._reuse_start(layer)) % len(self.reuse_pattern)]
+        return {"R": "R", "r": "R", "U": "U", "u": "U"}.get(ch, "F")
+
+    def reuse_producer(self, layer: int) -> int:  # config.go:357-370
+        if self.reuse_mode_at(layer) == "F":
+            return layer
+        for i in range(layer - 1, self._reuse_start(layer) - 1, -1):
+            if self.reuse_mode_at(i) == "F":
+                return i
+        return layer
+
+    @property
+    def indexer_shape(self) -> tuple[int, int]:  # (dim, heads), config.go:391-402
+        return (self.indexer_dim if self.indexer_dim > 0 else 64,
+                self.indexer_heads if self.indexer_heads > 0 else 1)
+
+    @property
+    def indexer_budget(self) -> int:  # config.go:372-381
+        if self.indexer_candidates > 0:
+            return self.indexer_candidates
+        return max(8 * self.sparse_topk, 64)
+
     def has_value_embedding(self, layer: int) -> bool:
         """model/helpers.go:69-71; never under MLA (model/transformer.go:72-78)."""
         return not self.mla and layer % 2 == (self.n_layer - 1) % 2
@@ -125,6 +169,20 @@ class Config:
             raise ValueError("MLA content dimension must be positive")
         if self.mla and self.compression > 1:  # config.go:483-486
             raise ValueError("MLA is not supported with compression")
+        if self.sparse_topk > 0 and self.compression <= 1:  # config.go:465-467
+            raise ValueError("SparseTopK requires CompressionRatio > 1")
+        if self.reuse_pattern:  # config.go:506-520
+            if self.compression <= 1:
+                raise ValueError("ReusePattern requires CompressionRatio > 1")
+            if any(ch not in "FRUfru" for ch in self.reuse_pattern):
+                raise ValueError(f"invalid reuse pattern {self.reuse_pattern!r}")
+            if self.reuse_pattern[0] not in "Ff":
+                raise ValueError(f"reuse pattern {self.reuse_pattern!r} must start with F")
+        if self.ced:  # config.go:521-533
+            if self.compression <= 1 or self.swa_window <= 0 or self.n_layer < 2:
+                raise ValueError("CED requires compression, a local window and >= 2 layers")
+            if self.reuse_pattern and self.reuse_mode_at(self.ced_split) != "F":
+                raise ValueError("CED reuse pattern must start each half with F")
         if self.moe and not 0 < self.experts_per_token <= self.n_experts:  # config.go:535-541
             raise ValueError(f"NumExpertsPerToken {self.experts_per_token} must be in "
                              f"[1, NumExperts={self.n_experts}]")
@@ -151,9 +209,16 @@ class Config:
                          (p + "attn.c_k.weight", Hkv * D, C_),
                          (p + "attn.c_v.weight", Hkv * D, C_)]
             ents += [(p + "attn.c_proj.weight", C_, C_)]
-            if self.compression > 1:  # model/params.go:43-46 (every layer owns a compressor)
-                ents += [(p + "attn.compress_logits.weight", D, C_),
-                         (p + "attn.compress_bias", self.compression, D)]
+            if self.compression > 1:  # model/params.go:43-51, attention.go:210-226
+                mode = self.reuse_mode_at(l)
+                if mode == "F":
+                    ents += [(p + "attn.compress_logits.weight", D, C_),
+                             (p + "attn.compress_bias", self.compression, D)]
+                if self.sparse_topk > 0 and mode != "U":
+                    idim, ih = self.indexer_shape
+                    ents += [(p + "attn.indexer_query.weight", ih * idim, C_),
+                             (p + "attn.indexer_key.weight", ih * idim, D),
+                             (p + "attn.indexer_heads", ih, 1)]
             if self.has_value_embedding(l):
                 ents += [(p + "attn.ve_gate.weight", Hkv, VE_GATE_CHANNELS),
                          (f"value_embeds.{l}.weight", PV, Hkv * D)]
@@ -306,9 +371,13 @@ def init_weights(cfg: Config, seed: int = 0, perturb: float = 0.0,
         for k in keys:
             put(p + k, rng.uniform(-bound, bound, n(p + k)))
         put(p + "mlp.c_fc.weight", rng.uniform(-0.4 * bound, 0.4 * bound, n(p + "mlp.c_fc.weight")))
-        if cfg.compression > 1:  # transformer.go:196-199
+        if cfg.compression > 1 and cfg.reuse_mode_at(l) == "F":  # transformer.go:196-199
             k = p + "attn.compress_logits.weight"
             put(k, rng.uniform(-bound, bound, n(k)))
+        if cfg.compression > 1 and cfg.sparse_topk > 0 and cfg.reuse_mode_at(l) != "U":
+            for k in ("attn.indexer_query.weight", "attn.indexer_key.weight"):  # :200-204
+                put(p + k, rng.uniform(-bound, bound, n(p + k)))
+            put(p + "attn.indexer_heads", np.ones(n(p + "attn.indexer_heads")))
         if cfg.moe:  # transformer.go:163-174
             put(p + "mlp.c_gate.weight",
                 rng.uniform(-0.4 * bound, 0.4 * bound, n(p + "mlp.c_gate.weight")))

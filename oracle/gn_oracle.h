@@ -172,6 +172,18 @@ ORC_MODEL_DECL(_f64, double)
  * (model/train_transformer.go:121-123; 0 without MoE). */
 double orc_aux_loss_f32(const orc_model_f32 *m);
 double orc_aux_loss_f64(const orc_model_f64 *m);
+/* The CSA indexer's distillation (compress_attention.go:133-147): its
+ * gradient holds the targets constant, so finite-difference checks freeze
+ * them -- mode 1 records every layer's targets at the next training
+ * forward, 2 reuses them, 0 computes them -- and differentiate CE plus
+ * orc_distill_loss (weight * sum of -target . log softmax(I) of the last
+ * forward). */
+void orc_set_freeze_targets_f32(orc_model_f32 *m, int mode);
+void orc_set_freeze_targets_f64(orc_model_f64 *m, int mode);
+double orc_distill_loss_f32(const orc_model_f32 *m);
+void orc_model_set_params_f32(orc_model_f32 *m, const float *params);
+void orc_model_set_params_f64(orc_model_f64 *m, const double *params);
+double orc_distill_loss_f64(const orc_model_f64 *m);
 
 /* ChannelCompressor.Forward of one sequence (model/compress.go:110-164):
  * logits [T][D] (bias added), value [T][D] -> comp [ceil(T/ratio)][D],
@@ -181,6 +193,25 @@ void orc_channel_compress(int T, int D, int ratio, const float *logits, const fl
 /* mergeAttentionBranches (model/compress_attention.go:440-466). */
 void orc_merge_attention_rows(float *out, float *lse, const float *oa, const float *la,
                               const float *ob, const float *lb, int rows, int D);
+
+/* CSA lightning-indexer pieces (model/indexer.go), float32 build:
+ * topKIndices (:226-268, returns the count); IndexerScores
+ * (kernels/scalar/indexer.go:11-34); the hierarchical selection of T rows at
+ * positions offset.. (selectFromScoreMatrix / selectRows /
+ * selectRowBlockMax, indexer.go:378-530; sel rows of kcap, candidate rows of
+ * ccap, may be NULL); fineSelect (:560-606); restrictIndexerToPool
+ * (compress_attention.go:199-230). */
+int orc_indexer_topk(const float *values, int n, int k, int32_t *out);
+void orc_indexer_scores_rows(const float *iq, const float *ik, const float *w, int rows, int blocks,
+                             int heads, int dim, float *out);
+void orc_select_rows(const float *scores, int T, int blocks, int offset, int ratio, int topk,
+                     int pool, int budget, int kcap, int ccap, int32_t *sel, int32_t *nsel,
+                     int32_t *cand, int32_t *ncand);
+void orc_fine_select(const float *iq_row, const float *ik, const float *w, int heads, int dim,
+                     const int32_t *cand, int nc, int topk, int max_block, int32_t *sel,
+                     int32_t *nsel);
+void orc_restrict_to_pool(float *scores, float *target, int T, int blocks, const int32_t *pool,
+                          const int32_t *npool, int ccap);
 
 /* Window sizes (model/config.go:629-645): writes n_layer left widths. */
 void orc_window_sizes(const orc_config *cfg, int32_t *out);

@@ -66,6 +66,37 @@ static int mlp_hidden(const orc_config *c) { /* model/block.go:23-28 */
 }
 #define TABLE_MAX (24 * MAXL)
 
+/* Flash preset layer roles (model/config.go:282-381). */
+enum { REUSE_FULL = 0, REUSE_REINDEX = 1, REUSE_REUSE = 2 };
+static int ced_split(const orc_config *c) { return c->ced ? c->n_layer / 2 : 0; }
+static int reuse_half_start(const orc_config *c, int layer) {
+  int split = ced_split(c);
+  return (c->ced && split > 0 && layer >= split) ? split : 0;
+}
+static int reuse_mode_at(const orc_config *c, int layer) { /* config.go:326-344 */
+  size_t n = strnlen(c->reuse_pattern, sizeof c->reuse_pattern);
+  if (n == 0) return REUSE_FULL;
+  char ch = c->reuse_pattern[(layer - reuse_half_start(c, layer)) % n];
+  if (ch == 'R' || ch == 'r') return REUSE_REINDEX;
+  if (ch == 'U' || ch == 'u') return REUSE_REUSE;
+  return REUSE_FULL;
+}
+static int reuse_producer(const orc_config *c, int layer) { /* config.go:357-370 */
+  if (reuse_mode_at(c, layer) == REUSE_FULL) return layer;
+  for (int i = layer - 1; i >= reuse_half_start(c, layer); i--)
+    if (reuse_mode_at(c, i) == REUSE_FULL) return i;
+  return layer;
+}
+static void indexer_dims(const orc_config *c, int *dim, int *heads) { /* config.go:391-402 */
+  *dim = c->indexer_dim > 0 ? c->indexer_dim : 64;
+  *heads = c->indexer_heads > 0 ? c->indexer_heads : 1;
+}
+static int indexer_budget(const orc_config *c) { /* config.go:372-381 */
+  if (c->indexer_candidates > 0) return c->indexer_candidates;
+  int b = 8 * c->sparse_topk;
+  return b < 64 ? 64 : b;
+}
+
 #if defined(ORC_DEFINE_SHARED)
 static int cmp_entry(const void *a, const void *b) {
   return strcmp(((const param_entry *)a)->name, ((const param_entry *)b)->name);
@@ -104,9 +135,22 @@ static int build_table(const orc_config *c, param_entry *t) {
       snprintf(nm, 96, "transformer.h.%d.attn.c_v.weight", l); ADD(nm, Hkv * D, C);
     }
     snprintf(nm, 96, "transformer.h.%d.attn.c_proj.weight", l); ADD(nm, C, C);
-    if (c->compression_ratio > 1) { /* params.go:43-46, compress.go:33-43 (every layer Full) */
-      snprintf(nm, 96, "transformer.h.%d.attn.compress_logits.weight", l); ADD(nm, D, C);
-      snprintf(nm, 96, "transformer.h.%d.attn.compress_bias", l); ADD(nm, c->compression_ratio, D);
+    if (c->compression_ratio > 1) {
+      /* params.go:43-51: Full layers own a compressor (compress.go:33-43),
+       * Full and Reindex layers an indexer when sparse (indexer.go:33-43,
+       * attention.go:210-226) */
+      int mode = reuse_mode_at(c, l);
+      if (mode == REUSE_FULL) {
+        snprintf(nm, 96, "transformer.h.%d.attn.compress_logits.weight", l); ADD(nm, D, C);
+        snprintf(nm, 96, "transformer.h.%d.attn.compress_bias", l); ADD(nm, c->compression_ratio, D);
+      }
+      if (c->sparse_topk > 0 && mode != REUSE_REUSE) {
+        int idim, ih;
+        indexer_dims(c, &idim, &ih);
+        snprintf(nm, 96, "transformer.h.%d.attn.indexer_query.weight", l); ADD(nm, ih * idim, C);
+        snprintf(nm, 96, "transformer.h.%d.attn.indexer_key.weight", l); ADD(nm, ih * idim, D);
+        snprintf(nm, 96, "transformer.h.%d.attn.indexer_heads", l); ADD(nm, ih, 1);
+      }
     }
     if (!mla && has_value_embedding(l, L)) { /* transformer.go:72-78: no VE under MLA */
       snprintf(nm, 96, "transformer.h.%d.attn.ve_gate.weight", l); ADD(nm, Hkv, VE_GATE_CH);
@@ -201,7 +245,9 @@ typedef struct {
   /* latent preset: MLA projections, shared-expert gate, router, experts */
   int64_t wqd, wqu, wqr, wkvd, wku, wvu, wkr, wgate, wr, rbias, eg, eu, ed;
   int64_t wcl, cbias; /* HCA compressor logit weight [D, C] and bias [ratio, D] */
+  int64_t wiq, wik, wih; /* CSA indexer query [HI, C], key [HI, D], head weights [ih] */
   int has_ve, window;
+  int mode, producer, has_idx; /* reuse role, producing Full layer, owns an indexer */
 } layer_off;
 
 struct MODEL {
@@ -210,6 +256,19 @@ struct MODEL {
   /* latent preset: MLA latent width, rope/content widths, experts */
   int mla, lat, rd, cd, E, K, EH;
   int ratio, swa; /* HCA compression ratio (> 1 = compressed layers) and SWA width */
+  /* CSA: top-k, indexer head dim / heads / width, hierarchical pool, candidate
+   * budget, distillation weight; CED encoder/decoder split (0: off) */
+  int topk, idim, ih, HI, ipool, ibudget, split;
+  REAL iw;
+  /* Test hook for finite differences of the indexer's distillation: the
+   * reference's gradient treats the targets as constants, so a check freezes
+   * them (1: record each layer's final targets, 2: use the recorded ones)
+   * and differentiates CE + weight * sum over rows of -target . log softmax(I),
+   * accumulated here by every training forward. */
+  int freeze;
+  REAL *ftarget[MAXL];
+  int64_t ftarget_n[MAXL];
+  double distill_loss;
   REAL clamp, mscale, bw;
   double aux_loss;
   int64_t total;
@@ -240,8 +299,15 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
   m->bw = R(cfg->balance_weight);
   m->ratio = cfg->compression_ratio > 1 ? cfg->compression_ratio : 1;
   m->swa = cfg->swa_window > 0 ? cfg->swa_window : 0;
-  if (cfg->sparse_topk > 0 || cfg->reuse_pattern[0] || cfg->ced) {
-    fprintf(stderr, "oracle: sparse indexer, cross-layer reuse and CED are not restated\n");
+  m->topk = m->ratio > 1 && cfg->sparse_topk > 0 ? cfg->sparse_topk : 0;
+  indexer_dims(cfg, &m->idim, &m->ih);
+  m->HI = m->idim * m->ih;
+  m->ipool = cfg->indexer_pool;
+  m->ibudget = indexer_budget(cfg);
+  m->iw = R(cfg->indexer_weight > 0 ? cfg->indexer_weight : 1.0f); /* config.go:383-389 */
+  m->split = ced_split(cfg);
+  if (m->split > 0) {
+    fprintf(stderr, "oracle: CED is not restated yet\n");
     abort();
   }
   m->L = cfg->n_layer;
@@ -291,9 +357,17 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
       OFF(eu, "transformer.h.%d.moe.experts.up.weight");
       OFF(ed, "transformer.h.%d.moe.experts.down.weight");
     }
-    if (m->ratio > 1) {
+    o->mode = m->ratio > 1 ? reuse_mode_at(cfg, l) : REUSE_FULL;
+    o->producer = m->ratio > 1 ? reuse_producer(cfg, l) : l;
+    if (m->ratio > 1 && o->mode == REUSE_FULL) {
       OFF(wcl, "transformer.h.%d.attn.compress_logits.weight");
       OFF(cbias, "transformer.h.%d.attn.compress_bias");
+    }
+    o->has_idx = m->topk > 0 && o->mode != REUSE_REUSE;
+    if (o->has_idx) {
+      OFF(wiq, "transformer.h.%d.attn.indexer_query.weight");
+      OFF(wik, "transformer.h.%d.attn.indexer_key.weight");
+      OFF(wih, "transformer.h.%d.attn.indexer_heads");
     }
     o->has_ve = !m->mla && has_value_embedding(l, m->L);
     if (o->has_ve) {
@@ -319,6 +393,7 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
 
 void FN(orc_model_free)(MODEL *m) {
   if (!m) return;
+  for (int l = 0; l < MAXL; l++) free(m->ftarget[l]);
   free(m->p);
   free(m->cosT);
   free(m->sinT);
@@ -522,13 +597,16 @@ typedef struct {
   REAL *lat;    /* [L][B][maxSeq][lat]      (MLA latent, kvcache.go:224-274) */
   REAL *rk;     /* [L][B][maxSeq][Hkv*rd]   (MLA rotary key) */
   REAL *prev;   /* [B][C] */
-  /* HCA (kvcache.go:142-220): tail buffer of the current block (hidden rows;
-   * its keys/values are the raw cache rows), compressed blocks and counts */
+  /* HCA (kvcache.go:142-220): tail buffer of the current block (hidden,
+   * key and value rows), compressed blocks and counts; CSA indexer key
+   * projections of the compressed blocks (kvcache.go:197-220) */
   int maxBlocks;
   REAL *tailh;  /* [L][B][ratio][C] */
+  REAL *tailk, *tailv; /* [L][B][Hkv][ratio][D] */
   int *taillen; /* [L] (all rows advance together) */
   REAL *ck, *cv;  /* [L][B][Hkv][maxBlocks][D] */
-  int *ccount;  /* [L][B] */
+  int *ccount;  /* [L][B] (a Reindex layer counts its cached indexer keys) */
+  REAL *ikc;    /* [L][B][Hkv][maxBlocks][HI] */
 } kvcache;
 
 static kvcache *cache_new(MODEL *m, int B, int maxSeq) {
@@ -538,7 +616,11 @@ static kvcache *cache_new(MODEL *m, int B, int maxSeq) {
   if (m->ratio > 1) {
     c->maxBlocks = maxSeq / m->ratio + 1;
     c->tailh = (REAL *)calloc((size_t)m->L * B * m->ratio * m->C, sizeof(REAL));
+    c->tailk = (REAL *)calloc((size_t)m->L * B * m->Hkv * m->ratio * m->D, sizeof(REAL));
+    c->tailv = (REAL *)calloc((size_t)m->L * B * m->Hkv * m->ratio * m->D, sizeof(REAL));
     c->taillen = (int *)calloc(m->L, sizeof(int));
+    if (m->topk > 0)
+      c->ikc = (REAL *)calloc((size_t)m->L * B * m->Hkv * c->maxBlocks * m->HI, sizeof(REAL));
     c->ck = (REAL *)calloc((size_t)m->L * B * m->Hkv * c->maxBlocks * m->D, sizeof(REAL));
     c->cv = (REAL *)calloc((size_t)m->L * B * m->Hkv * c->maxBlocks * m->D, sizeof(REAL));
     c->ccount = (int *)calloc((size_t)m->L * B, sizeof(int));
@@ -559,7 +641,8 @@ static void cache_free(kvcache *c) {
   free(c->v);
   free(c->lat);
   free(c->rk);
-  free(c->tailh); free(c->taillen); free(c->ck); free(c->cv); free(c->ccount);
+  free(c->tailh); free(c->tailk); free(c->tailv); free(c->taillen); free(c->ck); free(c->cv);
+  free(c->ccount); free(c->ikc);
   free(c->prev);
   free(c);
 }
@@ -590,6 +673,7 @@ static void prefill_from(MODEL *m, kvcache *dst, kvcache *src) {
         memcpy(cache_v(m, dst, l, b, h), cache_v(m, src, l, 0, h), sizeof(REAL) * pos * m->D);
       }
   if (m->ratio > 1) { /* PrefillFrom copies the compression state too */
+    const int RD = m->ratio * m->D;
     for (int l = 0; l < m->L; l++) {
       dst->taillen[l] = src->taillen[l];
       for (int b = 0; b < dst->B; b++) {
@@ -597,10 +681,16 @@ static void prefill_from(MODEL *m, kvcache *dst, kvcache *src) {
                src->tailh + (size_t)l * m->ratio * m->C, sizeof(REAL) * m->ratio * m->C);
         dst->ccount[l * dst->B + b] = src->ccount[l];
         for (int h = 0; h < m->Hkv; h++) {
-          size_t so = (((size_t)l * src->B) * m->Hkv + h) * src->maxBlocks * m->D;
-          size_t dd = (((size_t)l * dst->B + b) * m->Hkv + h) * dst->maxBlocks * m->D;
-          memcpy(dst->ck + dd, src->ck + so, sizeof(REAL) * src->ccount[l] * m->D);
-          memcpy(dst->cv + dd, src->cv + so, sizeof(REAL) * src->ccount[l] * m->D);
+          size_t so = (((size_t)l * src->B) * m->Hkv + h) * src->maxBlocks;
+          size_t dd = (((size_t)l * dst->B + b) * m->Hkv + h) * dst->maxBlocks;
+          size_t to = ((size_t)l * src->B * m->Hkv + h) * RD;
+          size_t td = (((size_t)l * dst->B + b) * m->Hkv + h) * RD;
+          memcpy(dst->tailk + td, src->tailk + to, sizeof(REAL) * RD);
+          memcpy(dst->tailv + td, src->tailv + to, sizeof(REAL) * RD);
+          memcpy(dst->ck + dd * m->D, src->ck + so * m->D, sizeof(REAL) * src->ccount[l] * m->D);
+          memcpy(dst->cv + dd * m->D, src->cv + so * m->D, sizeof(REAL) * src->ccount[l] * m->D);
+          if (m->topk > 0)
+            memcpy(dst->ikc + dd * m->HI, src->ikc + so * m->HI, sizeof(REAL) * src->ccount[l] * m->HI);
         }
       }
     }
@@ -1059,51 +1149,422 @@ static void merge_rows(REAL *out, REAL *lse, const REAL *oa, const REAL *la, con
   }
 }
 
-/* Training-side HCA attention (model/train.go:99-169 with compressForward and
- * compressedAttentionForward, compress_attention.go:562-677): qh [B][Hq][T][D],
- * kh/vh [B][Hkv][T][D] (post-norm keys, gated values), h [B*T][C]; writes oh,
- * lse and, in hc, the compressed keys/values and probabilities. */
+/* ---- CSA lightning indexer (model/indexer.go) --------------------------- */
+
+/* IndexerScores (kernels/scalar/indexer.go:11-34): out[r][s] = sum over heads
+ * of w_h * ReLU(q[r,h] . k[s,h]), float32 dot products summed in order. */
+static void indexer_scores(const REAL *iq, const REAL *ik, const REAL *w, int rows, int blocks,
+                           int H, int dim, REAL *out) {
+  const int HI = H * dim;
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; r++)
+    for (int s = 0; s < blocks; s++) {
+      REAL total = 0;
+      for (int h = 0; h < H; h++) {
+        REAL dot = 0;
+        const REAL *a = iq + (int64_t)r * HI + h * dim, *b = ik + (int64_t)s * HI + h * dim;
+        for (int e = 0; e < dim; e++) dot += a[e] * b[e];
+        if (dot > 0) total += w[h] * dot;
+      }
+      out[(int64_t)r * blocks + s] = total;
+    }
+}
+
+/* topKIndices (indexer.go:226-268): the k largest values in descending
+ * order, ties toward the smaller index; returns the count. */
+static int topk_indices(const REAL *v, int n, int k, int *out) {
+  if (k > n) k = n;
+  if (k <= 0) return 0;
+  int cnt = 0;
+  for (int i = 0; i < n; i++) {
+    int pos = cnt;
+    while (pos > 0 && v[i] > v[out[pos - 1]]) pos--; /* equal values keep index order */
+    if (pos >= k) continue;
+    int last = cnt < k ? cnt : k - 1;
+    for (int j = last; j > pos; j--) out[j] = out[j - 1];
+    out[pos] = i;
+    if (cnt < k) cnt++;
+  }
+  return cnt;
+}
+
+/* selectRowBlockMax + topKFromScoreRow (indexer.go:476-530): groups of
+ * `pool` entries scored by their maximum (the trailing partially allowed
+ * group over its allowed entries only), the best ceil(budget/pool) groups
+ * give the candidates, and the final top-k is taken over the candidates'
+ * scores in candidate order.  gmax is the row's group maxima (modified). */
+static void select_row_block_max(const REAL *score, REAL *gmax, int allowed, int topk, int pool,
+                                 int budget, int *sel, int *nsel, int *cand, int *ncand) {
+  *nsel = 0;
+  if (ncand) *ncand = 0;
+  if (allowed <= 0 || topk <= 0) return;
+  if (pool < 1) pool = 1;
+  int gpt = (budget + pool - 1) / pool;
+  if (gpt < 1) gpt = 1;
+  int ag = (allowed + pool - 1) / pool;
+  if (allowed % pool != 0 && ag > 0) {
+    REAL mx = R(-INFINITY);
+    for (int e = (ag - 1) * pool; e < allowed; e++)
+      if (score[e] > mx) mx = score[e];
+    gmax[ag - 1] = mx;
+  }
+  int *chosen = (int *)malloc(sizeof(int) * (gpt < ag ? gpt : ag) + sizeof(int));
+  int nch = topk_indices(gmax, ag, gpt, chosen);
+  int *c = (int *)malloc(sizeof(int) * (nch * pool + 1));
+  int nc = 0;
+  for (int i = 0; i < nch; i++) {
+    int st = chosen[i] * pool, en = st + pool < allowed ? st + pool : allowed;
+    for (int e = st; e < en; e++) c[nc++] = e;
+  }
+  REAL *fine = (REAL *)malloc(sizeof(REAL) * (nc + 1));
+  for (int i = 0; i < nc; i++) fine[i] = score[c[i]];
+  int *order = (int *)malloc(sizeof(int) * (nc + 1));
+  int n = topk_indices(fine, nc, topk, order);
+  for (int i = 0; i < n; i++) sel[i] = c[order[i]];
+  *nsel = n;
+  if (cand) {
+    memcpy(cand, c, sizeof(int) * nc);
+    *ncand = nc;
+  }
+  free(chosen); free(c); free(fine); free(order);
+}
+
+/* selectFromScoreMatrix / selectRows (indexer.go:378-474) for T rows at
+ * positions offset.. of one (sequence, kv-head): IndexerBlockMax over all
+ * `blocks` entries, then the per-row selection with allowed = pos / ratio. */
+static void select_rows(const REAL *scores, int T, int blocks, int offset, int ratio, int topk,
+                        int pool, int budget, int kcap, int ccap, int *sel, int *nsel, int *cand,
+                        int *ncand) {
+  if (pool < 1) pool = 1;
+  const int groups = (blocks + pool - 1) / pool;
+#pragma omp parallel for schedule(dynamic)
+  for (int t = 0; t < T; t++) {
+    const REAL *row = scores + (int64_t)t * blocks;
+    REAL *gmax = (REAL *)malloc(sizeof(REAL) * (groups + 1));
+    for (int g = 0; g < groups; g++) { /* IndexerBlockMax (scalar/indexer.go:44-61) */
+      REAL mx = R(-INFINITY);
+      int en = (g + 1) * pool < blocks ? (g + 1) * pool : blocks;
+      for (int e = g * pool; e < en; e++)
+        if (row[e] > mx) mx = row[e];
+      gmax[g] = mx;
+    }
+    int allowed = (offset + t) / ratio;
+    if (allowed > blocks) allowed = blocks;
+    select_row_block_max(row, gmax, allowed, topk, pool, budget, sel + (int64_t)t * kcap,
+                         nsel + t, cand ? cand + (int64_t)t * ccap : NULL, cand ? ncand + t : NULL);
+    free(gmax);
+  }
+}
+
+/* fineSelect (indexer.go:560-606): score the candidate entries below
+ * maxBlock and take their top-k in candidate order. */
+static void fine_select(const REAL *iq_row, const REAL *ik, const REAL *w, int H, int dim,
+                        const int *cand, int nc, int topk, int maxBlock, int *sel, int *nsel) {
+  *nsel = 0;
+  if (nc <= 0 || topk <= 0) return;
+  int *kept = (int *)malloc(sizeof(int) * nc);
+  REAL *fine = (REAL *)malloc(sizeof(REAL) * nc);
+  int nk = 0;
+  for (int i = 0; i < nc; i++) {
+    int e = cand[i];
+    if (e < 0 || e >= maxBlock) continue;
+    indexer_scores(iq_row, ik + (int64_t)e * H * dim, w, 1, 1, H, dim, fine + nk);
+    kept[nk++] = e;
+  }
+  int *order = (int *)malloc(sizeof(int) * (nk + 1));
+  int n = topk_indices(fine, nk, topk, order);
+  for (int i = 0; i < n; i++) sel[i] = kept[order[i]];
+  *nsel = n;
+  free(kept); free(fine); free(order);
+}
+
+/* distillationTarget (compress_attention.go:149-196): per query the softmax
+ * over its allowed blocks of the mean main attention logit of the query heads
+ * sharing kv-head hh.  qh [B][Hq][T][D], kc of (b, hh) [blocks][D]. */
+static void distill_target(const REAL *qh, const REAL *kcb, int b, int hh, int Hq, int rr,
+                           int ratio, int T, int blocks, int D, REAL *target) {
+#pragma omp parallel for schedule(dynamic)
+  for (int t = 0; t < T; t++) {
+    REAL *trow = target + (int64_t)t * blocks;
+    memset(trow, 0, sizeof(REAL) * blocks);
+    int allowed = t / ratio;
+    if (allowed > blocks) allowed = blocks;
+    if (allowed == 0) continue;
+    REAL *lg = (REAL *)malloc(sizeof(REAL) * allowed);
+    REAL mx = R(-INFINITY);
+    for (int s = 0; s < allowed; s++) {
+      REAL sum = 0;
+      for (int r = 0; r < rr; r++) {
+        const REAL *q = qh + (((int64_t)b * Hq + hh * rr + r) * T + t) * D, *k = kcb + (int64_t)s * D;
+        REAL dot = 0;
+        for (int e = 0; e < D; e++) dot += q[e] * k[e];
+        sum += dot;
+      }
+      lg[s] = sum / R(rr);
+      if (lg[s] > mx) mx = lg[s];
+    }
+    double total = 0;
+    for (int s = 0; s < allowed; s++) {
+      double v = exp((double)(lg[s] - mx));
+      trow[s] = R(v);
+      total += v;
+    }
+    for (int s = 0; s < allowed; s++) trow[s] /= R(total);
+    free(lg);
+  }
+}
+
+/* restrictIndexerToPool (compress_attention.go:199-230). */
+static void restrict_to_pool(REAL *scores, REAL *target, int T, int blocks, const int *pool,
+                             const int *npool, int ccap) {
+  char *in = (char *)malloc(blocks + 1);
+  for (int t = 0; t < T; t++) {
+    memset(in, 0, blocks + 1);
+    for (int i = 0; i < npool[t]; i++) in[pool[(int64_t)t * ccap + i]] = 1;
+    REAL *sr = scores + (int64_t)t * blocks, *tr = target + (int64_t)t * blocks;
+    double total = 0;
+    for (int e = 0; e < blocks; e++) {
+      if (!in[e]) {
+        sr[e] = R(-INFINITY);
+        tr[e] = 0;
+        continue;
+      }
+      total += (double)tr[e];
+    }
+    if (total > 0)
+      for (int e = 0; e < blocks; e++)
+        if (in[e]) tr[e] = R((double)tr[e] / total);
+  }
+  free(in);
+}
+
+/* maskedIndexerSoftmax (compress_attention.go:262-298). */
+static void masked_softmax(const REAL *scores, int T, int blocks, int ratio, REAL *probs) {
+  for (int t = 0; t < T; t++) {
+    const REAL *sr = scores + (int64_t)t * blocks;
+    REAL *pr = probs + (int64_t)t * blocks;
+    memset(pr, 0, sizeof(REAL) * blocks);
+    int allowed = t / ratio;
+    if (allowed > blocks) allowed = blocks;
+    if (allowed == 0) continue;
+    REAL mx = sr[0];
+    for (int s = 1; s < allowed; s++)
+      if (sr[s] > mx) mx = sr[s];
+    if (isinf((double)mx) && mx < 0) continue;
+    double total = 0;
+    for (int s = 0; s < allowed; s++) {
+      double v = exp((double)(sr[s] - mx));
+      pr[s] = R(v);
+      total += v;
+    }
+    for (int s = 0; s < allowed; s++) pr[s] /= R(total);
+  }
+}
+
+/* ---- compressed attention (model/compress_attention.go) ----------------- */
+
+/* Group state shared by a Full layer and the Reindex/Reuse layers after it
+ * (model/share.go:16-42). */
+typedef struct hca_share {
+  int producer, blocks;
+  REAL *kc, *vc;        /* the producer's compressed keys/values (borrowed) */
+  REAL *gkc, *gvc;      /* training: the group's compressed-KV gradients (owned) */
+  int *sel, *nsel;      /* most recently published selection (borrowed) */
+  int *pool, *npool;    /* the producer's candidate pool (borrowed), or NULL */
+} hca_share;
+
+/* One layer's training context.  kc/vc/probs are owned by Full layers (the
+ * others point at the producer's); the indexer arrays belong to layers with
+ * an indexer. */
 typedef struct {
-  int blocks;
-  REAL *kc, *vc;   /* [B][Hkv][blocks][D] */
-  REAL *probs;     /* [B][blocks][ratio][D] (one per sequence: K and V share the logits) */
+  int blocks, owns, own_sel, kcap, ccap;
+  REAL *kc, *vc, *probs;  /* [B][Hkv][blocks][D], probs [B][blocks][ratio][D] */
+  int *sel, *nsel;        /* [B*Hkv][T][kcap], [B*Hkv][T] */
+  int *pool, *npool;      /* [B*Hkv][T][ccap] (Full layer, pool > 1) */
+  REAL *iq, *ik;          /* [B*T][HI], [B*Hkv][blocks][HI] */
+  REAL *scores, *target;  /* [B*Hkv][T][blocks] */
+  hca_share *share;
 } hca_ctx;
 
+static void hca_ctx_free(hca_ctx *hc) {
+  if (!hc) return;
+  if (hc->owns) { free(hc->kc); free(hc->vc); free(hc->probs); }
+  if (hc->own_sel) { free(hc->sel); free(hc->nsel); }
+  free(hc->pool); free(hc->npool);
+  free(hc->iq); free(hc->ik); free(hc->scores); free(hc->target);
+  free(hc);
+}
+static void hca_share_free(hca_share *sh) {
+  if (!sh) return;
+  free(sh->gkc); free(sh->gvc);
+  free(sh);
+}
+static int candidate_cap(const MODEL *m) {
+  int pool = m->ipool < 1 ? 1 : m->ipool;
+  int gpt = (m->ibudget + pool - 1) / pool;
+  return (gpt < 1 ? 1 : gpt) * pool;
+}
+
+/* sparseTrainingPlan (compress_attention.go:45-131) of a layer with an
+ * indexer: indexer projections, scores, distillation targets and the top-k
+ * selection (within the producer's candidate pool on a Reindex layer). */
+static void sparse_training_plan(MODEL *m, const layer_off *lo, const REAL *h, const REAL *qh,
+                                 int B, int T, hca_ctx *hc, hca_share *sh) {
+  const int Hkv = m->Hkv, D = m->D, HI = m->HI, blocks = hc->blocks, rr = m->Hq / Hkv;
+  const REAL *P = m->p;
+  hc->kcap = m->topk;
+  hc->ccap = candidate_cap(m);
+  hc->sel = (int *)calloc((size_t)B * Hkv * T * hc->kcap, sizeof(int));
+  hc->nsel = (int *)calloc((size_t)B * Hkv * T, sizeof(int));
+  hc->own_sel = 1;
+  const int produce_pool = lo->mode == REUSE_FULL && m->ipool > 1;
+  const int use_pool = lo->mode == REUSE_REINDEX && m->ipool > 1 && sh->pool;
+  if (produce_pool) {
+    hc->pool = (int *)calloc((size_t)B * Hkv * T * hc->ccap, sizeof(int));
+    hc->npool = (int *)calloc((size_t)B * Hkv * T, sizeof(int));
+  }
+  hc->iq = (REAL *)malloc(sizeof(REAL) * (int64_t)B * T * HI);
+  linear_fwd(hc->iq, h, P + lo->wiq, (int64_t)B * T, m->C, HI);
+  hc->ik = (REAL *)malloc(sizeof(REAL) * (int64_t)B * Hkv * blocks * HI);
+  linear_fwd(hc->ik, hc->kc, P + lo->wik, (int64_t)B * Hkv * blocks, D, HI);
+  hc->scores = (REAL *)malloc(sizeof(REAL) * (int64_t)B * Hkv * T * blocks);
+  hc->target = (REAL *)malloc(sizeof(REAL) * (int64_t)B * Hkv * T * blocks);
+  for (int b = 0; b < B; b++)
+    for (int hh = 0; hh < Hkv; hh++) {
+      const int64_t bk = (int64_t)b * Hkv + hh;
+      REAL *sc = hc->scores + bk * T * blocks, *tg = hc->target + bk * T * blocks;
+      const REAL *iqb = hc->iq + (int64_t)b * T * HI, *ikb = hc->ik + bk * blocks * HI;
+      indexer_scores(iqb, ikb, P + lo->wih, T, blocks, m->ih, m->idim, sc);
+      distill_target(qh, hc->kc + bk * blocks * D, b, hh, m->Hq, rr, m->ratio, T, blocks, D, tg);
+      int *sel = hc->sel + bk * T * hc->kcap, *nsel = hc->nsel + bk * T;
+      if (use_pool) {
+        const int *pl = sh->pool + bk * T * hc->ccap, *npl = sh->npool + bk * T;
+        for (int t = 0; t < T; t++) {
+          int allowed = t / m->ratio;
+          if (allowed > blocks) allowed = blocks;
+          fine_select(iqb + (int64_t)t * HI, ikb, P + lo->wih, m->ih, m->idim,
+                      pl + (int64_t)t * hc->ccap, npl[t], m->topk, allowed,
+                      sel + (int64_t)t * hc->kcap, nsel + t);
+        }
+        restrict_to_pool(sc, tg, T, blocks, pl, npl, hc->ccap);
+      } else {
+        select_rows(sc, T, blocks, 0, m->ratio, m->topk, m->ipool < 1 ? 1 : m->ipool, m->ibudget,
+                    hc->kcap, hc->ccap, sel, nsel, produce_pool ? hc->pool + bk * T * hc->ccap : NULL,
+                    produce_pool ? hc->npool + bk * T : NULL);
+      }
+    }
+  const int l = (int)(lo - m->lay);
+  const int64_t nt = (int64_t)B * Hkv * T * blocks;
+  if (m->freeze == 1) {
+    free(m->ftarget[l]);
+    m->ftarget[l] = (REAL *)malloc(sizeof(REAL) * nt);
+    memcpy(m->ftarget[l], hc->target, sizeof(REAL) * nt);
+    m->ftarget_n[l] = nt;
+  } else if (m->freeze == 2 && m->ftarget[l] && m->ftarget_n[l] == nt) {
+    memcpy(hc->target, m->ftarget[l], sizeof(REAL) * nt);
+  }
+  /* the distillation objective whose gradient the backward takes */
+  REAL *pr = (REAL *)malloc(sizeof(REAL) * (int64_t)T * blocks);
+  double dl = 0;
+  for (int64_t bk = 0; bk < (int64_t)B * Hkv; bk++) {
+    const REAL *sc = hc->scores + bk * T * blocks, *tg = hc->target + bk * T * blocks;
+    masked_softmax(sc, T, blocks, m->ratio, pr);
+    for (int64_t i = 0; i < (int64_t)T * blocks; i++)
+      if (tg[i] > 0) dl -= (double)tg[i] * log((double)pr[i]);
+  }
+  m->distill_loss += (double)m->iw * dl;
+  free(pr);
+}
+
+/* Training-side compressed attention (model/train.go:99-169 with
+ * compressForward, sparseTrainingPlan, compressedAttentionForward[Sparse],
+ * attentionForwardWindowed and mergeAttentionBranches): qh [B][Hq][T][D],
+ * kh/vh [B][Hkv][T][D] (post-norm keys, gated values), h [B*T][C]; writes oh
+ * and lse.  A Full layer starts a new group share (*shp); the others use the
+ * group's compressed keys/values and, for Reuse, its selection. */
 static void hca_train_forward(MODEL *m, const layer_off *lo, const REAL *qh, const REAL *kh,
                               const REAL *vh, const REAL *h, int B, int T, REAL *oh, REAL *lse,
-                              hca_ctx *hc) {
+                              hca_ctx *hc, hca_share **shp) {
   const int D = m->D, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
   const int blocks = (T + ratio - 1) / ratio;
   hc->blocks = blocks;
-  hc->kc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
-  hc->vc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
-  hc->probs = (REAL *)calloc((size_t)B * blocks * ratio * D, sizeof(REAL));
-  REAL *logits = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
-  for (int b = 0; b < B; b++) {
-    compress_logits(m, lo, h + (int64_t)b * T * m->C, T, logits);
-    REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
-    for (int hh = 0; hh < Hkv; hh++) {
-      int64_t bk = (int64_t)b * Hkv + hh;
-      compress_seq(T, D, ratio, logits, kh + bk * T * D, hc->kc + bk * blocks * D, pb);
-      compress_seq(T, D, ratio, logits, vh + bk * T * D, hc->vc + bk * blocks * D, pb);
+  if (lo->mode == REUSE_FULL) {
+    hc->owns = 1;
+    hc->kc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+    hc->vc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+    hc->probs = (REAL *)calloc((size_t)B * blocks * ratio * D, sizeof(REAL));
+    REAL *logits = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
+    for (int b = 0; b < B; b++) {
+      compress_logits(m, lo, h + (int64_t)b * T * m->C, T, logits);
+      REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
+      for (int hh = 0; hh < Hkv; hh++) {
+        int64_t bk = (int64_t)b * Hkv + hh;
+        compress_seq(T, D, ratio, logits, kh + bk * T * D, hc->kc + bk * blocks * D, pb);
+        compress_seq(T, D, ratio, logits, vh + bk * T * D, hc->vc + bk * blocks * D, pb);
+      }
+    }
+    free(logits);
+    hca_share *sh = (hca_share *)calloc(1, sizeof(hca_share));
+    sh->blocks = blocks;
+    sh->kc = hc->kc;
+    sh->vc = hc->vc;
+    sh->gkc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+    sh->gvc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+    *shp = sh;
+  } else {
+    hc->kc = (*shp)->kc;
+    hc->vc = (*shp)->vc;
+  }
+  hca_share *sh = *shp;
+  hc->share = sh;
+  if (m->topk > 0) {
+    if (lo->mode == REUSE_REUSE) {
+      hc->sel = sh->sel;
+      hc->nsel = sh->nsel;
+      hc->kcap = m->topk;
+    } else {
+      sparse_training_plan(m, lo, h, qh, B, T, hc, sh);
+      sh->sel = hc->sel;
+      sh->nsel = hc->nsel;
+      if (lo->mode == REUSE_FULL) {
+        sh->pool = hc->pool;
+        sh->npool = hc->npool;
+      }
     }
   }
-  free(logits);
 #pragma omp parallel for schedule(dynamic)
   for (int bh = 0; bh < B * Hq; bh++) {
     int b = bh / Hq, hq = bh % Hq;
     int64_t bk = (int64_t)b * Hkv + hq / rr;
     const REAL *q = qh + (int64_t)bh * T * D;
+    const REAL *kcb = hc->kc + bk * blocks * D, *vcb = hc->vc + bk * blocks * D;
     REAL *go = (REAL *)calloc((size_t)T * D, sizeof(REAL));
     REAL *gl = (REAL *)malloc(sizeof(REAL) * T);
-    for (int bl = 0; bl < blocks; bl++) { /* queries of block bl see blocks < bl */
-      int t0 = bl * ratio, t1 = t0 + ratio < T ? t0 + ratio : T;
-      if (bl == 0) {
-        for (int t = t0; t < t1; t++) gl[t] = R(-INFINITY);
-        continue;
+    if (m->topk > 0) { /* compressedAttentionForwardSparse (:326-373) */
+      REAL *kg = (REAL *)malloc(sizeof(REAL) * hc->kcap * D), *vg = (REAL *)malloc(sizeof(REAL) * hc->kcap * D);
+      for (int t = 0; t < T; t++) {
+        const int *sel = hc->sel + (bk * T + t) * hc->kcap;
+        int n = hc->nsel[bk * T + t];
+        if (n == 0) {
+          gl[t] = R(-INFINITY);
+          continue;
+        }
+        for (int i = 0; i < n; i++) {
+          memcpy(kg + (int64_t)i * D, kcb + (int64_t)sel[i] * D, sizeof(REAL) * D);
+          memcpy(vg + (int64_t)i * D, vcb + (int64_t)sel[i] * D, sizeof(REAL) * D);
+        }
+        attn_fwd(q + (int64_t)t * D, kg, vg, go + (int64_t)t * D, gl + t, 1, n, D, n, -1);
       }
-      attn_fwd(q + (int64_t)t0 * D, hc->kc + bk * blocks * D, hc->vc + bk * blocks * D,
-               go + (int64_t)t0 * D, gl + t0, t1 - t0, bl, D, bl, -1);
+      free(kg); free(vg);
+    } else { /* compressedAttentionForward (:603-650): queries of block bl see blocks < bl */
+      for (int bl = 0; bl < blocks; bl++) {
+        int t0 = bl * ratio, t1 = t0 + ratio < T ? t0 + ratio : T;
+        if (bl == 0) {
+          for (int t = t0; t < t1; t++) gl[t] = R(-INFINITY);
+          continue;
+        }
+        attn_fwd(q + (int64_t)t0 * D, kcb, vcb, go + (int64_t)t0 * D, gl + t0, t1 - t0, bl, D, bl, -1);
+      }
     }
     if (m->swa > 0) {
       REAL *loc = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
@@ -1119,17 +1580,68 @@ static void hca_train_forward(MODEL *m, const layer_off *lo, const REAL *qh, con
   }
 }
 
-/* Training-side HCA backward (model/train.go:211-303 with
- * compressedAttentionBackward, attentionBackwardWindowed and
- * compressBackward): dqh/dkh/dvh (head-major, zeroed by the caller) receive
- * the query and raw key/value gradients, dhin_c [B*T][C] the compressor's
- * gradient wrt the attention input; parameter gradients accumulate in G. */
+/* indexerDistillationGradient (compress_attention.go:133-147) with
+ * SparseIndexer.Backward (indexer.go:107-151): gradient (softmax(I) - target)
+ * * weight of the index scores into the indexer weights, the attention input
+ * (dh, [B*T][C], accumulated) and the compressed keys (dkc, accumulated). */
+static void indexer_distill_backward(MODEL *m, const layer_off *lo, const hca_ctx *hc,
+                                     const REAL *h, int B, int T, REAL *dh, REAL *dkc, REAL *G) {
+  const int Hkv = m->Hkv, D = m->D, C = m->C, HI = m->HI, H = m->ih, dim = m->idim;
+  const int blocks = hc->blocks;
+  const REAL *P = m->p, *w = P + lo->wih;
+  REAL *probs = (REAL *)malloc(sizeof(REAL) * (int64_t)T * blocks);
+  REAL *gq = (REAL *)malloc(sizeof(REAL) * (int64_t)T * HI);
+  REAL *gk = (REAL *)malloc(sizeof(REAL) * (int64_t)blocks * HI);
+  REAL *dhb = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
+  REAL *dkb = (REAL *)malloc(sizeof(REAL) * (int64_t)blocks * D);
+  for (int b = 0; b < B; b++)
+    for (int hh = 0; hh < Hkv; hh++) {
+      const int64_t bk = (int64_t)b * Hkv + hh;
+      const REAL *sc = hc->scores + bk * T * blocks, *tg = hc->target + bk * T * blocks;
+      const REAL *q = hc->iq + (int64_t)b * T * HI, *k = hc->ik + bk * blocks * HI;
+      masked_softmax(sc, T, blocks, m->ratio, probs);
+      memset(gq, 0, sizeof(REAL) * (int64_t)T * HI);
+      memset(gk, 0, sizeof(REAL) * (int64_t)blocks * HI);
+      for (int t = 0; t < T; t++)
+        for (int s = 0; s < blocks; s++) {
+          const REAL gs = (probs[(int64_t)t * blocks + s] - tg[(int64_t)t * blocks + s]) * m->iw;
+          for (int hd = 0; hd < H; hd++) {
+            const REAL *qa = q + (int64_t)t * HI + hd * dim, *ka = k + (int64_t)s * HI + hd * dim;
+            REAL dot = 0;
+            for (int e = 0; e < dim; e++) dot += qa[e] * ka[e];
+            if (dot <= 0) continue;
+            G[lo->wih + hd] += gs * dot;
+            const REAL wt = gs * w[hd];
+            REAL *gqa = gq + (int64_t)t * HI + hd * dim, *gka = gk + (int64_t)s * HI + hd * dim;
+            for (int e = 0; e < dim; e++) {
+              gqa[e] += wt * ka[e];
+              gka[e] += wt * qa[e];
+            }
+          }
+        }
+      linear_bwd(dhb, G + lo->wiq, h + (int64_t)b * T * C, gq, P + lo->wiq, T, C, HI);
+      linear_bwd(dkb, G + lo->wik, hc->kc + bk * blocks * D, gk, P + lo->wik, blocks, D, HI);
+      for (int64_t i = 0; i < (int64_t)T * C; i++) dh[(int64_t)b * T * C + i] += dhb[i];
+      for (int64_t i = 0; i < (int64_t)blocks * D; i++) dkc[bk * blocks * D + i] += dkb[i];
+    }
+  free(probs); free(gq); free(gk); free(dhb); free(dkb);
+}
+
+/* Training-side compressed attention backward (model/train.go:211-303 with
+ * compressedAttentionBackward[Sparse], indexerDistillationGradient,
+ * attentionBackwardWindowed and compressBackward): dqh/dkh/dvh (head-major,
+ * zeroed by the caller) receive the query and raw key/value gradients,
+ * dhin_c [B*T][C] the gradient wrt the attention input from the compressor
+ * and the indexer (zero on Reuse layers); parameter gradients accumulate in
+ * G.  Compressed-KV gradients accumulate in the group share; the Full layer,
+ * visited last in the backward, runs the compressor backward on the sum. */
 static void hca_train_backward(MODEL *m, const layer_off *lo, const hca_ctx *hc, const REAL *qh,
                                const REAL *kh, const REAL *vh, const REAL *oh, const REAL *doh,
                                const REAL *lse, const REAL *h, int B, int T, REAL *dqh,
                                REAL *dkh, REAL *dvh, REAL *dhin_c, REAL *G) {
   const int D = m->D, C = m->C, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
   const int blocks = hc->blocks;
+  hca_share *sh = hc->share;
   REAL *corr = NULL;
   if (m->swa > 0) { /* merged row correction dO.O (train.go:211-226) */
     corr = (REAL *)malloc(sizeof(REAL) * (int64_t)B * Hq * T);
@@ -1139,113 +1651,246 @@ static void hca_train_backward(MODEL *m, const layer_off *lo, const hca_ctx *hc,
       corr[row] = R(dot);
     }
   }
-  REAL *dkc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
-  REAL *dvc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
+  REAL *dkc = sh->gkc, *dvc = sh->gvc;
   REAL *dkl = (REAL *)calloc((size_t)B * Hkv * T * D, sizeof(REAL));
   REAL *dvl = (REAL *)calloc((size_t)B * Hkv * T * D, sizeof(REAL));
   /* serial over query heads so GQA accumulation into the shared K/V is race-free */
   for (int b = 0; b < B; b++)
 #pragma omp parallel for schedule(dynamic)
-    for (int hh = 0; hh < Hkv; hh++)
+    for (int hh = 0; hh < Hkv; hh++) {
+      REAL *kg = NULL, *vg = NULL, *dkg = NULL, *dvg = NULL;
+      if (m->topk > 0) {
+        kg = (REAL *)malloc(sizeof(REAL) * hc->kcap * D); vg = (REAL *)malloc(sizeof(REAL) * hc->kcap * D);
+        dkg = (REAL *)malloc(sizeof(REAL) * hc->kcap * D); dvg = (REAL *)malloc(sizeof(REAL) * hc->kcap * D);
+      }
+      int64_t bk = (int64_t)b * Hkv + hh;
+      REAL *kcb = hc->kc + bk * blocks * D, *vcb = hc->vc + bk * blocks * D;
       for (int r = 0; r < rr; r++) {
         int hq = hh * rr + r;
-        int64_t bh = (int64_t)b * Hq + hq, bk = (int64_t)b * Hkv + hh;
-        for (int bl = 1; bl < blocks; bl++) {
-          int t0 = bl * ratio, t1 = t0 + ratio < T ? t0 + ratio : T;
-          attn_bwd_corr(qh + (bh * T + t0) * D, hc->kc + bk * blocks * D, hc->vc + bk * blocks * D,
-                        doh + (bh * T + t0) * D, lse + bh * T + t0, corr ? corr + bh * T + t0 : NULL,
-                        dqh + (bh * T + t0) * D, dkc + bk * blocks * D, dvc + bk * blocks * D,
-                        t1 - t0, bl, D, bl, -1);
+        int64_t bh = (int64_t)b * Hq + hq;
+        if (m->topk > 0) { /* compressedAttentionBackwardSparse (:376-433) */
+          for (int t = 0; t < T; t++) {
+            const int *sel = hc->sel + (bk * T + t) * hc->kcap;
+            int n = hc->nsel[bk * T + t];
+            if (n == 0) continue;
+            for (int i = 0; i < n; i++) {
+              memcpy(kg + (int64_t)i * D, kcb + (int64_t)sel[i] * D, sizeof(REAL) * D);
+              memcpy(vg + (int64_t)i * D, vcb + (int64_t)sel[i] * D, sizeof(REAL) * D);
+            }
+            memset(dkg, 0, sizeof(REAL) * n * D);
+            memset(dvg, 0, sizeof(REAL) * n * D);
+            attn_bwd_corr(qh + (bh * T + t) * D, kg, vg, doh + (bh * T + t) * D, lse + bh * T + t,
+                          corr ? corr + bh * T + t : NULL, dqh + (bh * T + t) * D, dkg, dvg, 1, n,
+                          D, n, -1);
+            for (int i = 0; i < n; i++)
+              for (int d = 0; d < D; d++) {
+                dkc[(bk * blocks + sel[i]) * D + d] += dkg[(int64_t)i * D + d];
+                dvc[(bk * blocks + sel[i]) * D + d] += dvg[(int64_t)i * D + d];
+              }
+          }
+        } else {
+          for (int bl = 1; bl < blocks; bl++) {
+            int t0 = bl * ratio, t1 = t0 + ratio < T ? t0 + ratio : T;
+            attn_bwd_corr(qh + (bh * T + t0) * D, kcb, vcb, doh + (bh * T + t0) * D,
+                          lse + bh * T + t0, corr ? corr + bh * T + t0 : NULL,
+                          dqh + (bh * T + t0) * D, dkc + bk * blocks * D, dvc + bk * blocks * D,
+                          t1 - t0, bl, D, bl, -1);
+          }
         }
         if (m->swa > 0)
           attn_bwd_corr(qh + bh * T * D, kh + bk * T * D, vh + bk * T * D, doh + bh * T * D,
                         lse + bh * T, corr + bh * T, dqh + bh * T * D, dkl + bk * T * D,
                         dvl + bk * T * D, T, T, D, 0, m->swa);
       }
-  /* compressBackward (compress_attention.go:1182-1209) */
-  memset(dhin_c, 0, sizeof(REAL) * (int64_t)B * T * C);
-  REAL *glk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
-  REAL *glv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
-  REAL *dhk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
-  REAL *dhv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
-  for (int b = 0; b < B; b++) {
-    const REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
-    const REAL *hb = h + (int64_t)b * T * C;
-    for (int hh = 0; hh < Hkv; hh++) {
-      int64_t bk = (int64_t)b * Hkv + hh;
-      memset(glk, 0, sizeof(REAL) * (int64_t)T * D);
-      memset(glv, 0, sizeof(REAL) * (int64_t)T * D);
-      compress_seq_bwd(T, D, ratio, pb, kh + bk * T * D, hc->kc + bk * blocks * D,
-                       dkc + bk * blocks * D, glk, dkh + bk * T * D);
-      linear_bwd(dhk, G + lo->wcl, hb, glk, m->p + lo->wcl, T, C, D);
-      for (int t = 0; t < T; t++)
-        for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glk[(int64_t)t * D + d];
-      compress_seq_bwd(T, D, ratio, pb, vh + bk * T * D, hc->vc + bk * blocks * D,
-                       dvc + bk * blocks * D, glv, dvh + bk * T * D);
-      linear_bwd(dhv, G + lo->wcl, hb, glv, m->p + lo->wcl, T, C, D);
-      for (int t = 0; t < T; t++)
-        for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glv[(int64_t)t * D + d];
-      for (int64_t i = 0; i < (int64_t)T * C; i++) dhin_c[(int64_t)b * T * C + i] += dhk[i] + dhv[i];
+      free(kg); free(vg); free(dkg); free(dvg);
     }
+  memset(dhin_c, 0, sizeof(REAL) * (int64_t)B * T * C);
+  REAL *dh_idx = NULL;
+  if (lo->has_idx) { /* the indexer's distillation into the group's key gradient */
+    dh_idx = (REAL *)calloc((size_t)B * T * C, sizeof(REAL));
+    indexer_distill_backward(m, lo, hc, h, B, T, dh_idx, dkc, G);
+  }
+  if (lo->mode == REUSE_FULL) { /* compressBackward (compress_attention.go:1182-1209) */
+    REAL *glk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
+    REAL *glv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
+    REAL *dhk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
+    REAL *dhv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
+    for (int b = 0; b < B; b++) {
+      const REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
+      const REAL *hb = h + (int64_t)b * T * C;
+      for (int hh = 0; hh < Hkv; hh++) {
+        int64_t bk = (int64_t)b * Hkv + hh;
+        memset(glk, 0, sizeof(REAL) * (int64_t)T * D);
+        memset(glv, 0, sizeof(REAL) * (int64_t)T * D);
+        compress_seq_bwd(T, D, ratio, pb, kh + bk * T * D, hc->kc + bk * blocks * D,
+                         dkc + bk * blocks * D, glk, dkh + bk * T * D);
+        linear_bwd(dhk, G + lo->wcl, hb, glk, m->p + lo->wcl, T, C, D);
+        for (int t = 0; t < T; t++)
+          for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glk[(int64_t)t * D + d];
+        compress_seq_bwd(T, D, ratio, pb, vh + bk * T * D, hc->vc + bk * blocks * D,
+                         dvc + bk * blocks * D, glv, dvh + bk * T * D);
+        linear_bwd(dhv, G + lo->wcl, hb, glv, m->p + lo->wcl, T, C, D);
+        for (int t = 0; t < T; t++)
+          for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glv[(int64_t)t * D + d];
+        for (int64_t i = 0; i < (int64_t)T * C; i++) dhin_c[(int64_t)b * T * C + i] += dhk[i] + dhv[i];
+      }
+    }
+    free(glk); free(glv); free(dhk); free(dhv);
+  }
+  if (dh_idx) {
+    for (int64_t i = 0; i < (int64_t)B * T * C; i++) dhin_c[i] = dhin_c[i] + dh_idx[i];
+    free(dh_idx);
   }
   /* raw key/value gradients: compressor part + local branch */
   for (int64_t i = 0; i < (int64_t)B * Hkv * T * D; i++) {
     dkh[i] = dkh[i] + dkl[i];
     dvh[i] = dvh[i] + dvl[i];
   }
-  free(glk); free(glv); free(dhk); free(dhv);
-  free(dkc); free(dvc); free(dkl); free(dvl); free(corr);
+  free(dkl); free(dvl); free(corr);
 }
 
-/* Inference HCA (forwardCompressed, compress_attention.go:895-1006 with
- * appendGlobalTail / compressTail, :848-890): buffer the T new rows of h,
- * compress each completed block from its hidden rows and the raw cached
- * keys/values, then attend every query to the compressed blocks strictly
- * before its own and merge the local window branch. */
-static void hca_decode(MODEL *m, const layer_off *lo, int l, kvcache *cache, const REAL *h,
-                       const REAL *qh, int B, int T, REAL *oh) {
-  const int D = m->D, C = m->C, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
-  const int offset = cache->pos, klen = cache->pos + T;
+/* Per-forward-call group state of inference: the most recent selection and
+ * the producer's candidate pool for the call's T rows. */
+typedef struct {
+  int *sel, *nsel, *pool, *npool;
+} dec_share;
+
+/* compressTail (compress_attention.go:848-866) of layer l for every row:
+ * compress the buffered block, cache its indexer key projections. */
+static void compress_tail(MODEL *m, const layer_off *lo, int l, kvcache *cache, int B) {
+  const int D = m->D, C = m->C, ratio = m->ratio, Hkv = m->Hkv;
   REAL *logits = (REAL *)malloc(sizeof(REAL) * (int64_t)ratio * D);
   REAL *probs = (REAL *)malloc(sizeof(REAL) * (int64_t)ratio * D);
-  for (int t = 0; t < T; t++) {
-    for (int b = 0; b < B; b++)
-      memcpy(cache->tailh + (((size_t)l * B + b) * ratio + cache->taillen[l]) * C,
-             h + ((int64_t)b * T + t) * C, sizeof(REAL) * C);
-    cache->taillen[l]++;
-    if (cache->taillen[l] < ratio) continue;
-    const int start = offset + t - ratio + 1; /* first position of the block */
-    for (int b = 0; b < B; b++) {
-      compress_logits(m, lo, cache->tailh + ((size_t)l * B + b) * ratio * C, ratio, logits);
-      int slot = cache->ccount[l * B + b];
-      for (int hh = 0; hh < Hkv; hh++) {
-        size_t cb = ((((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks + slot) * D;
-        compress_seq(ratio, D, ratio, logits, cache_k(m, cache, l, b, hh) + (int64_t)start * D,
-                     cache->ck + cb, probs);
-        compress_seq(ratio, D, ratio, logits, cache_v(m, cache, l, b, hh) + (int64_t)start * D,
-                     cache->cv + cb, probs);
-      }
-      cache->ccount[l * B + b]++;
+  for (int b = 0; b < B; b++) {
+    compress_logits(m, lo, cache->tailh + ((size_t)l * B + b) * ratio * C, ratio, logits);
+    int slot = cache->ccount[l * B + b];
+    for (int hh = 0; hh < Hkv; hh++) {
+      size_t cb = ((((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks + slot);
+      size_t tb = (((size_t)l * B + b) * Hkv + hh) * ratio * D;
+      compress_seq(ratio, D, ratio, logits, cache->tailk + tb, cache->ck + cb * D, probs);
+      compress_seq(ratio, D, ratio, logits, cache->tailv + tb, cache->cv + cb * D, probs);
+      if (lo->has_idx)
+        linear_fwd(cache->ikc + cb * m->HI, cache->ck + cb * D, m->p + lo->wik, 1, D, m->HI);
     }
-    cache->taillen[l] = 0;
+    cache->ccount[l * B + b]++;
   }
+  cache->taillen[l] = 0;
   free(logits); free(probs);
+}
+
+/* Inference compressed attention (forwardCompressed / forwardCompressedSparse,
+ * compress_attention.go:895-1146): a Full layer buffers the T new rows and
+ * compresses each completed block (appendGlobalTail); a Reindex layer caches
+ * its own indexer keys of the producer's new blocks (cacheReusedIndexerKeys,
+ * :1160-1176); every query attends to the compressed blocks before its own
+ * block of the producer's cache -- all of them, or the indexer's top-k --
+ * merged with the local window branch. */
+static void hca_decode(MODEL *m, const layer_off *lo, int l, kvcache *cache, const REAL *h,
+                       const REAL *qh, const REAL *kn, const REAL *vn, int B, int T, REAL *oh,
+                       dec_share *ds) {
+  const int D = m->D, C = m->C, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
+  const int offset = cache->pos, cl = lo->producer, HI = m->HI;
+  if (lo->mode == REUSE_FULL) { /* appendGlobalTail (:868-890) */
+    for (int t = 0; t < T; t++) {
+      for (int b = 0; b < B; b++) {
+        int slot = cache->taillen[l];
+        memcpy(cache->tailh + (((size_t)l * B + b) * ratio + slot) * C, h + ((int64_t)b * T + t) * C,
+               sizeof(REAL) * C);
+        for (int hh = 0; hh < Hkv; hh++) {
+          size_t tb = ((((size_t)l * B + b) * Hkv + hh) * ratio + slot) * D;
+          memcpy(cache->tailk + tb, kn + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+          memcpy(cache->tailv + tb, vn + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+        }
+      }
+      cache->taillen[l]++;
+      if (cache->taillen[l] == ratio) compress_tail(m, lo, l, cache, B);
+    }
+  } else if (lo->mode == REUSE_REINDEX && m->topk > 0) { /* cacheReusedIndexerKeys */
+    int own = cache->ccount[l * B], prod = cache->ccount[cl * B];
+    for (int blk = own; blk < prod; blk++) {
+      for (int b = 0; b < B; b++)
+        for (int hh = 0; hh < Hkv; hh++) {
+          size_t pc = (((size_t)cl * B + b) * Hkv + hh) * cache->maxBlocks + blk;
+          size_t oc = (((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks + blk;
+          linear_fwd(cache->ikc + oc * HI, cache->ck + pc * D, m->p + lo->wik, 1, D, HI);
+        }
+      for (int b = 0; b < B; b++) cache->ccount[l * B + b]++;
+    }
+  }
+  const int kcap = m->topk, ccap = candidate_cap(m);
+  int *lsel = NULL, *lnsel = NULL;
+  if (m->topk > 0 && lo->mode != REUSE_REUSE) { /* this layer's selection */
+    lsel = (int *)calloc((size_t)B * Hkv * T * kcap + 1, sizeof(int));
+    lnsel = (int *)calloc((size_t)B * Hkv * T, sizeof(int));
+    const int produce_pool = lo->mode == REUSE_FULL && m->ipool > 1;
+    const int use_pool = lo->mode == REUSE_REINDEX && m->ipool > 1 && ds->pool;
+    if (produce_pool) {
+      free(ds->pool); free(ds->npool);
+      ds->pool = (int *)calloc((size_t)B * Hkv * T * ccap, sizeof(int));
+      ds->npool = (int *)calloc((size_t)B * Hkv * T, sizeof(int));
+    }
+    REAL *iq = (REAL *)malloc(sizeof(REAL) * (int64_t)B * T * HI);
+    linear_fwd(iq, h, m->p + lo->wiq, (int64_t)B * T, C, HI);
+    for (int b = 0; b < B; b++) {
+      const int avail = cache->ccount[cl * B + b];
+      if (avail == 0) continue;
+      for (int hh = 0; hh < Hkv; hh++) {
+        const int64_t bk = (int64_t)b * Hkv + hh;
+        const REAL *keys = cache->ikc + (((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks * HI;
+        int *sel = lsel + bk * T * kcap, *nsel = lnsel + bk * T;
+        if (use_pool) { /* SelectWithinPool (indexer.go:532-558) */
+          for (int t = 0; t < T; t++) {
+            int allowed = (offset + t) / ratio;
+            if (allowed > avail) allowed = avail;
+            fine_select(iq + ((int64_t)b * T + t) * HI, keys, m->p + lo->wih, m->ih, m->idim,
+                        ds->pool + (bk * T + t) * ccap, ds->npool[bk * T + t], m->topk, allowed,
+                        sel + (int64_t)t * kcap, nsel + t);
+          }
+        } else { /* SelectProjectedWithCandidates (indexer.go:337-376) */
+          const int pool = m->ipool < 1 ? 1 : m->ipool;
+          const int budget = pool == 1 ? avail : m->ibudget;
+          REAL *sc = (REAL *)malloc(sizeof(REAL) * (int64_t)T * avail);
+          indexer_scores(iq + (int64_t)b * T * HI, keys, m->p + lo->wih, T, avail, m->ih, m->idim, sc);
+          select_rows(sc, T, avail, offset, ratio, m->topk, pool, budget, kcap, ccap, sel, nsel,
+                      produce_pool ? ds->pool + bk * T * ccap : NULL,
+                      produce_pool ? ds->npool + bk * T : NULL);
+          free(sc);
+        }
+      }
+    }
+    free(iq);
+    free(ds->sel); free(ds->nsel);
+    ds->sel = lsel;
+    ds->nsel = lnsel;
+  }
 #pragma omp parallel for schedule(dynamic)
   for (int bh = 0; bh < B * Hq; bh++) {
     int b = bh / Hq, hq = bh % Hq, hh = hq / rr;
+    const int64_t bk = (int64_t)b * Hkv + hh;
     REAL go[1024], lo_[1024], gl, ll;
+    REAL *kg = (REAL *)malloc(sizeof(REAL) * (kcap + 1) * D), *vg = (REAL *)malloc(sizeof(REAL) * (kcap + 1) * D);
+    const int avail = cache->ccount[cl * B + b];
+    size_t cb = (((size_t)cl * B + b) * Hkv + hh) * cache->maxBlocks * D;
     for (int t = 0; t < T; t++) {
       int pos = offset + t;
-      int count = pos / ratio;
-      if (count > cache->ccount[l * B + b]) count = cache->ccount[l * B + b];
       const REAL *q = qh + ((int64_t)bh * T + t) * D;
       REAL *out = oh + ((int64_t)bh * T + t) * D;
-      size_t cb = (((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks * D;
-      if (count == 0) {
-        gl = R(-INFINITY);
-        memset(go, 0, sizeof(REAL) * D);
+      gl = R(-INFINITY);
+      memset(go, 0, sizeof(REAL) * D);
+      if (m->topk > 0) {
+        int n = avail > 0 ? ds->nsel[bk * T + t] : 0;
+        const int *sel = ds->sel + (bk * T + t) * kcap;
+        if (n > 0) {
+          for (int i = 0; i < n; i++) {
+            memcpy(kg + (int64_t)i * D, cache->ck + cb + (int64_t)sel[i] * D, sizeof(REAL) * D);
+            memcpy(vg + (int64_t)i * D, cache->cv + cb + (int64_t)sel[i] * D, sizeof(REAL) * D);
+          }
+          attn_fwd(q, kg, vg, go, &gl, 1, n, D, n, -1);
+        }
       } else {
-        attn_fwd(q, cache->ck + cb, cache->cv + cb, go, &gl, 1, count, D, count, -1);
+        int count = pos / ratio;
+        if (count > avail) count = avail;
+        if (count > 0) attn_fwd(q, cache->ck + cb, cache->cv + cb, go, &gl, 1, count, D, count, -1);
       }
       if (m->swa > 0) { /* localAttentionRow (compress_attention.go:543-560) */
         int ls = pos - m->swa < 0 ? 0 : pos - m->swa;
@@ -1257,9 +1902,15 @@ static void hca_decode(MODEL *m, const layer_off *lo, int l, kvcache *cache, con
         memcpy(out, go, sizeof(REAL) * D);
       }
     }
+    free(kg); free(vg);
   }
-  (void)klen;
 }
+
+void FN(orc_set_freeze_targets)(MODEL *m, int mode) { m->freeze = mode; }
+void FN(orc_model_set_params)(MODEL *m, const REAL *params) {
+  memcpy(m->p, params, sizeof(REAL) * m->total);
+}
+double FN(orc_distill_loss)(const MODEL *m) { return m->distill_loss; }
 
 #if defined(ORC_DEFINE_SHARED)
 /* Test entry points for the HCA pieces (float32 build). */
@@ -1270,6 +1921,28 @@ void orc_channel_compress(int T, int D, int ratio, const float *logits, const fl
 void orc_merge_attention_rows(float *out, float *lse, const float *oa, const float *la,
                               const float *ob, const float *lb, int rows, int D) {
   merge_rows(out, lse, oa, la, ob, lb, rows, D);
+}
+int orc_indexer_topk(const float *values, int n, int k, int32_t *out) {
+  return topk_indices(values, n, k, out);
+}
+void orc_indexer_scores_rows(const float *iq, const float *ik, const float *w, int rows, int blocks,
+                             int heads, int dim, float *out) {
+  indexer_scores(iq, ik, w, rows, blocks, heads, dim, out);
+}
+void orc_select_rows(const float *scores, int T, int blocks, int offset, int ratio, int topk,
+                     int pool, int budget, int kcap, int ccap, int32_t *sel, int32_t *nsel,
+                     int32_t *cand, int32_t *ncand) {
+  select_rows(scores, T, blocks, offset, ratio, topk, pool, budget, kcap, ccap, sel, nsel, cand,
+              ncand);
+}
+void orc_fine_select(const float *iq_row, const float *ik, const float *w, int heads, int dim,
+                     const int32_t *cand, int nc, int topk, int max_block, int32_t *sel,
+                     int32_t *nsel) {
+  fine_select(iq_row, ik, w, heads, dim, cand, nc, topk, max_block, sel, nsel);
+}
+void orc_restrict_to_pool(float *scores, float *target, int T, int blocks, const int32_t *pool,
+                          const int32_t *npool, int ccap) {
+  restrict_to_pool(scores, target, T, blocks, pool, npool, ccap);
 }
 #endif
 
@@ -1287,6 +1960,7 @@ typedef struct {
   int32_t *ids;
   REAL *raw, *embn, *smsig, *x0;
   layer_ctx lc[MAXL];
+  hca_share *shares[MAXL]; /* compressed-attention groups, by producing layer */
   REAL *backout, *final_pre, *final_norm, *logits;
 } train_ctx;
 
@@ -1301,7 +1975,8 @@ static void ctx_free(train_ctx *c, int L) {
     free(x->mid); free(x->h2); free(x->u); free(x->act);
     free(x->ql); free(x->kvl); free(x->g2);
     moe_ctx_free(x->moe);
-    if (x->hca) { free(x->hca->kc); free(x->hca->vc); free(x->hca->probs); free(x->hca); }
+    hca_ctx_free(x->hca);
+    hca_share_free(c->shares[l]);
   }
   free(c->backout); free(c->final_pre); free(c->final_norm); free(c->logits);
   free(c);
@@ -1324,6 +1999,13 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
   int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, F = m->F, V = m->V, PV = m->PV;
   int64_t N = (int64_t)B * T;
   const REAL *P = m->p;
+  /* compressed attention: the current group's share (training) or its
+   * per-call selection state (inference); contexts not kept by ctx */
+  hca_share *cur_share = NULL, *shares[MAXL] = {0};
+  hca_ctx *hcs[MAXL] = {0};
+  dec_share ds;
+  memset(&ds, 0, sizeof ds);
+  m->distill_loss = 0;
   REAL *x = (REAL *)malloc(sizeof(REAL) * N * C);
   REAL *raw = (REAL *)malloc(sizeof(REAL) * N * C);
   for (int64_t n = 0; n < N; n++) memcpy(raw + n * C, P + m->wte + (int64_t)ids[n] * C, sizeof(REAL) * C);
@@ -1487,12 +2169,17 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
         }
       }
     if (m->ratio > 1 && cache) {
-      hca_decode(m, lo, l, cache, h, qh, B, T, oh);
+      if (lo->mode == REUSE_FULL) { /* a new group: fresh share (transformer.go:320-325) */
+        free(ds.sel); free(ds.nsel); free(ds.pool); free(ds.npool);
+        memset(&ds, 0, sizeof ds);
+      }
+      hca_decode(m, lo, l, cache, h, qh, kn, v, B, T, oh, &ds);
     } else if (m->ratio > 1) {
       hca_ctx *hc = (hca_ctx *)calloc(1, sizeof(hca_ctx));
-      hca_train_forward(m, lo, qh, kh, vh, h, B, T, oh, lseb, hc);
+      hca_train_forward(m, lo, qh, kh, vh, h, B, T, oh, lseb, hc, &cur_share);
+      if (lo->mode == REUSE_FULL) shares[l] = cur_share;
       if (lc) lc->hca = hc;
-      else { free(hc->kc); free(hc->vc); free(hc->probs); free(hc); }
+      else hcs[l] = hc;
     } else {
 #pragma omp parallel for schedule(dynamic)
     for (int bh = 0; bh < B * Hq; bh++) {
@@ -1547,6 +2234,12 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
     if (l == bkidx) backout = dup_arr(x, (size_t)N * C);
   }
   if (cache) cache->pos += T;
+  for (int l = 0; l < m->L; l++) {
+    hca_ctx_free(hcs[l]);
+    if (ctx) ctx->shares[l] = shares[l];
+    else hca_share_free(shares[l]);
+  }
+  free(ds.sel); free(ds.nsel); free(ds.pool); free(ds.npool);
   /* backout, final norm, lm_head, trimVocab, softcap (transformer.go:333-341) */
   if (backout) {
     REAL nb = -P[m->bkl];

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i32pn = C.c_void_p  # optional int32 array: pass _ptr(array) or None
 _u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
 _i64 = C.c_int64
 
@@ -128,6 +129,19 @@ def lib():
         "orc_window_sizes": (v, [C.POINTER(OrcConfig), _i32p]),
         "orc_num_threads": (C.c_int, []),
         "orc_aux_loss_f32": (C.c_double, [C.c_void_p]),
+        "orc_indexer_topk": (C.c_int, [_f32p, C.c_int, C.c_int, _i32p]),
+        "orc_indexer_scores_rows": (v, [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        _f32p]),
+        "orc_select_rows": (v, [_f32p] + [C.c_int] * 9 + [_i32p, _i32p, _i32pn, _i32pn]),
+        "orc_fine_select": (v, [_f32p, _f32p, _f32p, C.c_int, C.c_int, _i32p, C.c_int, C.c_int,
+                                C.c_int, _i32p, _i32p]),
+        "orc_restrict_to_pool": (v, [_f32p, _f32p, C.c_int, C.c_int, _i32p, _i32p, C.c_int]),
+        "orc_set_freeze_targets_f32": (v, [C.c_void_p, C.c_int]),
+        "orc_set_freeze_targets_f64": (v, [C.c_void_p, C.c_int]),
+        "orc_distill_loss_f32": (C.c_double, [C.c_void_p]),
+        "orc_model_set_params_f32": (v, [C.c_void_p, _f32p]),
+        "orc_model_set_params_f64": (v, [C.c_void_p, _f64p]),
+        "orc_distill_loss_f64": (C.c_double, [C.c_void_p]),
         "orc_channel_compress": (v, [C.c_int, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]),
         "orc_merge_attention_rows": (v, [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, C.c_int,
                                          C.c_int]),
@@ -187,6 +201,15 @@ class ModelShape:
     balance_weight: float = 0.0
     compression_ratio: int = 0
     swa_window: int = 0
+    # flash preset: CSA indexer, cross-layer reuse, CED
+    sparse_topk: int = 0
+    indexer_dim: int = 0
+    indexer_heads: int = 0
+    indexer_pool: int = 0
+    indexer_candidates: int = 0
+    indexer_weight: float = 0.0
+    reuse_pattern: str = ""
+    ced: int = 0
 
     @classmethod
     def from_config(cls, cfg) -> "ModelShape":
@@ -195,7 +218,9 @@ class ModelShape:
                    cfg.n_embd, cfg.rotary_dims, cfg.window_pattern, cfg.mla_latent,
                    cfg.mla_rope_dimension if cfg.mla_latent > 0 else 0, cfg.n_experts,
                    cfg.experts_per_token, cfg.expert_hidden, cfg.shared_hidden, cfg.moe_clamp,
-                   cfg.moe_scale, cfg.balance_weight, cfg.compression_ratio, cfg.swa_window)
+                   cfg.moe_scale, cfg.balance_weight, cfg.compression_ratio, cfg.swa_window,
+                   cfg.sparse_topk, cfg.indexer_dim, cfg.indexer_heads, cfg.indexer_pool,
+                   cfg.indexer_candidates, cfg.indexer_weight, cfg.reuse_pattern, int(cfg.ced))
 
     def orc(self) -> OrcConfig:
         return OrcConfig(self.sequence_len, self.vocab_size, self.n_layer, self.n_head,
@@ -203,7 +228,10 @@ class ModelShape:
                          self.window_pattern.encode(), self.mla_latent, self.mla_rope_dims,
                          self.n_experts, self.experts_per_token, self.expert_hidden,
                          self.shared_hidden, self.moe_clamp, self.moe_scale,
-                         self.balance_weight, self.compression_ratio, self.swa_window)
+                         self.balance_weight, self.compression_ratio, self.swa_window,
+                         self.sparse_topk, self.indexer_dim, self.indexer_heads,
+                         self.indexer_pool, self.indexer_candidates, self.indexer_weight,
+                         self.reuse_pattern.encode(), self.ced)
 
 
 def param_table(shape: ModelShape):
@@ -274,6 +302,22 @@ class OracleModel:
     def aux_loss(self) -> float:
         """MoE balance loss of the last training forward (pg_step / ce_loss)."""
         return self._fn("orc_aux_loss")(self._m)
+
+    def set_params(self, params: np.ndarray):
+        self.params = np.ascontiguousarray(params, self.dtype)
+        assert self.params.size == self.total
+        self._fn("orc_model_set_params")(self._m, self.params)
+
+    def freeze_targets(self, mode: int):
+        """Indexer distillation targets: 0 computed, 1 computed and recorded,
+        2 the recorded ones (finite-difference checks)."""
+        self._fn("orc_set_freeze_targets")(self._m, mode)
+
+    def distill_loss(self) -> float:
+        """weight * sum over rows of -target . log softmax(I) of the last
+        forward (the objective whose gradient the backward takes, targets
+        held constant)."""
+        return self._fn("orc_distill_loss")(self._m)
 
     def ce_loss(self, inputs, targets, want_grads=True):
         inputs = np.ascontiguousarray(inputs, np.int32)
