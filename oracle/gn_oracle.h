@@ -182,6 +182,10 @@ void orc_set_freeze_targets_f32(orc_model_f32 *m, int mode);
 void orc_set_freeze_targets_f64(orc_model_f64 *m, int mode);
 double orc_distill_loss_f32(const orc_model_f32 *m);
 void orc_model_set_params_f32(orc_model_f32 *m, const float *params);
+/* PrefillCED (model/transformer.go:363-449) of a batch-1 prompt into a fresh
+ * cache: the last replayed row's logits [vocab]. */
+void orc_prefill_ced_f32(orc_model_f32 *m, const int32_t *ids, int T, float *last_logits);
+void orc_prefill_ced_f64(orc_model_f64 *m, const int32_t *ids, int T, double *last_logits);
 void orc_model_set_params_f64(orc_model_f64 *m, const double *params);
 double orc_distill_loss_f64(const orc_model_f64 *m);
 

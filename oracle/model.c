@@ -2,9 +2,13 @@
  * model.c - the gonano transformer's inference forward, KV-cache decode,
  * training forward/backward, policy-gradient step, batched generation and
  * one chat_rl step, restated in C: the dense preset, the latent preset
- * (MLA attention, DeepSeekMoE feed-forward) and compressed attention (HCA:
- * channel compressor, block-causal attention over compressed keys, sliding-
- * window local branch merged by log-sum-exp).
+ * (MLA attention, DeepSeekMoE feed-forward) and the flash preset's
+ * attention: compressed attention (HCA: channel compressor, block-causal
+ * attention over compressed keys, sliding-window local branch merged by
+ * log-sum-exp), sparse selection of compressed blocks (CSA: lightning
+ * indexer, hierarchical top-k, distillation gradient), cross-layer reuse
+ * (Full / Reindex / Reuse layers) and the causal encoder-decoder split (CED,
+ * with its bounded-replay prefill).
  *
  * TEST INFRASTRUCTURE ONLY (see gn_oracle.h).
  *
@@ -305,11 +309,7 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
   m->ipool = cfg->indexer_pool;
   m->ibudget = indexer_budget(cfg);
   m->iw = R(cfg->indexer_weight > 0 ? cfg->indexer_weight : 1.0f); /* config.go:383-389 */
-  m->split = ced_split(cfg);
-  if (m->split > 0) {
-    fprintf(stderr, "oracle: CED is not restated yet\n");
-    abort();
-  }
+  m->split = m->ratio > 1 ? ced_split(cfg) : 0;
   m->L = cfg->n_layer;
   m->V = cfg->vocab_size;
   m->PV = padded_vocab(cfg);
@@ -1384,6 +1384,12 @@ typedef struct {
   REAL *iq, *ik;          /* [B*T][HI], [B*Hkv][blocks][HI] */
   REAL *scores, *target;  /* [B*Hkv][T][blocks] */
   hca_share *share;
+  /* CED decoder Full layer: the compressor reads the encoder hidden state
+   * (borrowed) and compresses its own projections of it, kg/vg [B][Hkv][T][D]
+   * (keys after RoPE and QK norm), ced_krot the post-RoPE pre-norm keys
+   * [B*T][Hkv][D] */
+  const REAL *enc;
+  REAL *kg, *vg, *ced_krot;
 } hca_ctx;
 
 static void hca_ctx_free(hca_ctx *hc) {
@@ -1392,7 +1398,29 @@ static void hca_ctx_free(hca_ctx *hc) {
   if (hc->own_sel) { free(hc->sel); free(hc->nsel); }
   free(hc->pool); free(hc->npool);
   free(hc->iq); free(hc->ik); free(hc->scores); free(hc->target);
+  free(hc->kg); free(hc->vg); free(hc->ced_krot);
   free(hc);
+}
+
+/* cedGlobalKeyValue (attention.go:156-171): a CED decoder layer's global keys
+ * and values, its own key and value projections of the encoder hidden state
+ * (no value embedding); RoPE at positions offset.. and the 1.2 QK norm on
+ * the keys.  Sequence layout [B*T][Hkv][D]; krot (optional) receives the
+ * post-RoPE pre-norm keys. */
+static void ced_kv(MODEL *m, const layer_off *lo, const REAL *enc, int B, int T, int offset,
+                   REAL *kseq, REAL *vseq, REAL *krot) {
+  const int Hkv = m->Hkv, D = m->D, C = m->C;
+  const int64_t N = (int64_t)B * T;
+  linear_fwd(kseq, enc, m->p + lo->wk, N, C, Hkv * D);
+  linear_fwd(vseq, enc, m->p + lo->wv, N, C, Hkv * D);
+  for (int b = 0; b < B; b++)
+    for (int t = 0; t < T; t++) {
+      int64_t n = (int64_t)b * T + t;
+      rope_row(m, kseq + n * Hkv * D, kseq + n * Hkv * D, Hkv, offset + t, 1);
+    }
+  if (krot) memcpy(krot, kseq, sizeof(REAL) * N * Hkv * D);
+  rmsnorm_rows(kseq, kseq, N * Hkv, D);
+  for (int64_t i = 0; i < N * Hkv * D; i++) kseq[i] *= R(QK_SCALE);
 }
 static void hca_share_free(hca_share *sh) {
   if (!sh) return;
@@ -1483,24 +1511,45 @@ static void sparse_training_plan(MODEL *m, const layer_off *lo, const REAL *h, c
  * and lse.  A Full layer starts a new group share (*shp); the others use the
  * group's compressed keys/values and, for Reuse, its selection. */
 static void hca_train_forward(MODEL *m, const layer_off *lo, const REAL *qh, const REAL *kh,
-                              const REAL *vh, const REAL *h, int B, int T, REAL *oh, REAL *lse,
-                              hca_ctx *hc, hca_share **shp) {
+                              const REAL *vh, const REAL *h, const REAL *enc, int B, int T,
+                              REAL *oh, REAL *lse, hca_ctx *hc, hca_share **shp) {
   const int D = m->D, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
   const int blocks = (T + ratio - 1) / ratio;
   hc->blocks = blocks;
   if (lo->mode == REUSE_FULL) {
     hc->owns = 1;
+    const REAL *hin = h, *kin = kh, *vin = vh;
+    if (enc) { /* CED decoder (train.go:104-111): global KV from the encoder */
+      const int64_t N = (int64_t)B * T;
+      REAL *ks = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+      REAL *vs = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+      hc->ced_krot = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+      ced_kv(m, lo, enc, B, T, 0, ks, vs, hc->ced_krot);
+      hc->kg = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+      hc->vg = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+      for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++)
+          for (int hh = 0; hh < Hkv; hh++) {
+            memcpy(hc->kg + (((int64_t)b * Hkv + hh) * T + t) * D, ks + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+            memcpy(hc->vg + (((int64_t)b * Hkv + hh) * T + t) * D, vs + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+          }
+      free(ks); free(vs);
+      hc->enc = enc;
+      hin = enc;
+      kin = hc->kg;
+      vin = hc->vg;
+    }
     hc->kc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
     hc->vc = (REAL *)calloc((size_t)B * Hkv * blocks * D, sizeof(REAL));
     hc->probs = (REAL *)calloc((size_t)B * blocks * ratio * D, sizeof(REAL));
     REAL *logits = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
     for (int b = 0; b < B; b++) {
-      compress_logits(m, lo, h + (int64_t)b * T * m->C, T, logits);
+      compress_logits(m, lo, hin + (int64_t)b * T * m->C, T, logits);
       REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
       for (int hh = 0; hh < Hkv; hh++) {
         int64_t bk = (int64_t)b * Hkv + hh;
-        compress_seq(T, D, ratio, logits, kh + bk * T * D, hc->kc + bk * blocks * D, pb);
-        compress_seq(T, D, ratio, logits, vh + bk * T * D, hc->vc + bk * blocks * D, pb);
+        compress_seq(T, D, ratio, logits, kin + bk * T * D, hc->kc + bk * blocks * D, pb);
+        compress_seq(T, D, ratio, logits, vin + bk * T * D, hc->vc + bk * blocks * D, pb);
       }
     }
     free(logits);
@@ -1638,7 +1687,7 @@ static void indexer_distill_backward(MODEL *m, const layer_off *lo, const hca_ct
 static void hca_train_backward(MODEL *m, const layer_off *lo, const hca_ctx *hc, const REAL *qh,
                                const REAL *kh, const REAL *vh, const REAL *oh, const REAL *doh,
                                const REAL *lse, const REAL *h, int B, int T, REAL *dqh,
-                               REAL *dkh, REAL *dvh, REAL *dhin_c, REAL *G) {
+                               REAL *dkh, REAL *dvh, REAL *dhin_c, REAL *genc, REAL *G) {
   const int D = m->D, C = m->C, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
   const int blocks = hc->blocks;
   hca_share *sh = hc->share;
@@ -1711,31 +1760,68 @@ static void hca_train_backward(MODEL *m, const layer_off *lo, const hca_ctx *hc,
     indexer_distill_backward(m, lo, hc, h, B, T, dh_idx, dkc, G);
   }
   if (lo->mode == REUSE_FULL) { /* compressBackward (compress_attention.go:1182-1209) */
+    /* a CED decoder layer compresses its projections of the encoder hidden
+     * state: those gradients flow to the encoder (train.go:249-262) */
+    const int ced = hc->enc != NULL;
+    const REAL *hin = ced ? hc->enc : h, *kin = ced ? hc->kg : kh, *vin = ced ? hc->vg : vh;
+    REAL *dkin = dkh, *dvin = dvh, *dhc = dhin_c;
+    if (ced) {
+      dkin = (REAL *)calloc((size_t)B * Hkv * T * D, sizeof(REAL));
+      dvin = (REAL *)calloc((size_t)B * Hkv * T * D, sizeof(REAL));
+      dhc = (REAL *)calloc((size_t)B * T * C, sizeof(REAL));
+    }
     REAL *glk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
     REAL *glv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * D);
     REAL *dhk = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
     REAL *dhv = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
     for (int b = 0; b < B; b++) {
       const REAL *pb = hc->probs + (int64_t)b * blocks * ratio * D;
-      const REAL *hb = h + (int64_t)b * T * C;
+      const REAL *hb = hin + (int64_t)b * T * C;
       for (int hh = 0; hh < Hkv; hh++) {
         int64_t bk = (int64_t)b * Hkv + hh;
         memset(glk, 0, sizeof(REAL) * (int64_t)T * D);
         memset(glv, 0, sizeof(REAL) * (int64_t)T * D);
-        compress_seq_bwd(T, D, ratio, pb, kh + bk * T * D, hc->kc + bk * blocks * D,
-                         dkc + bk * blocks * D, glk, dkh + bk * T * D);
+        compress_seq_bwd(T, D, ratio, pb, kin + bk * T * D, hc->kc + bk * blocks * D,
+                         dkc + bk * blocks * D, glk, dkin + bk * T * D);
         linear_bwd(dhk, G + lo->wcl, hb, glk, m->p + lo->wcl, T, C, D);
         for (int t = 0; t < T; t++)
           for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glk[(int64_t)t * D + d];
-        compress_seq_bwd(T, D, ratio, pb, vh + bk * T * D, hc->vc + bk * blocks * D,
-                         dvc + bk * blocks * D, glv, dvh + bk * T * D);
+        compress_seq_bwd(T, D, ratio, pb, vin + bk * T * D, hc->vc + bk * blocks * D,
+                         dvc + bk * blocks * D, glv, dvin + bk * T * D);
         linear_bwd(dhv, G + lo->wcl, hb, glv, m->p + lo->wcl, T, C, D);
         for (int t = 0; t < T; t++)
           for (int d = 0; d < D; d++) G[lo->cbias + (t % ratio) * D + d] += glv[(int64_t)t * D + d];
-        for (int64_t i = 0; i < (int64_t)T * C; i++) dhin_c[(int64_t)b * T * C + i] += dhk[i] + dhv[i];
+        for (int64_t i = 0; i < (int64_t)T * C; i++) dhc[(int64_t)b * T * C + i] += dhk[i] + dhv[i];
       }
     }
     free(glk); free(glv); free(dhk); free(dhv);
+    if (ced) { /* cedKey/ValueProjectionBackward (train.go:454-479) */
+      const int64_t N = (int64_t)B * T;
+      REAL *gs = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+      REAL *gpre = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
+      REAL *tmp = (REAL *)malloc(sizeof(REAL) * N * C);
+      for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++)
+          for (int hh = 0; hh < Hkv; hh++)
+            for (int d = 0; d < D; d++)
+              gs[(((int64_t)b * T + t) * Hkv + hh) * D + d] = dkin[(((int64_t)b * Hkv + hh) * T + t) * D + d] * R(QK_SCALE);
+      rmsnorm_backward_rows(gpre, hc->ced_krot, gs, N * Hkv, D);
+      for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++) {
+          int64_t n = (int64_t)b * T + t;
+          rope_row(m, gpre + n * Hkv * D, gpre + n * Hkv * D, Hkv, t, -1);
+        }
+      linear_bwd(tmp, G + lo->wk, hc->enc, gpre, m->p + lo->wk, N, C, Hkv * D);
+      for (int64_t i = 0; i < N * C; i++) dhc[i] = dhc[i] + tmp[i];
+      for (int b = 0; b < B; b++)
+        for (int t = 0; t < T; t++)
+          for (int hh = 0; hh < Hkv; hh++)
+            memcpy(gs + (((int64_t)b * T + t) * Hkv + hh) * D, dvin + (((int64_t)b * Hkv + hh) * T + t) * D, sizeof(REAL) * D);
+      linear_bwd(tmp, G + lo->wv, hc->enc, gs, m->p + lo->wv, N, C, Hkv * D);
+      for (int64_t i = 0; i < N * C; i++) dhc[i] = dhc[i] + tmp[i];
+      for (int64_t i = 0; i < N * C; i++) genc[i] += dhc[i];
+      free(gs); free(gpre); free(tmp); free(dkin); free(dvin); free(dhc);
+    }
   }
   if (dh_idx) {
     for (int64_t i = 0; i < (int64_t)B * T * C; i++) dhin_c[i] = dhin_c[i] + dh_idx[i];
@@ -1785,37 +1871,66 @@ static void compress_tail(MODEL *m, const layer_off *lo, int l, kvcache *cache, 
  * :1160-1176); every query attends to the compressed blocks before its own
  * block of the producer's cache -- all of them, or the indexer's top-k --
  * merged with the local window branch. */
+/* appendGlobalTail (compress_attention.go:868-890): rows of hid [B*T][C]
+ * and their keys/values [B*T][Hkv][D] enter layer l's tail, each completed
+ * block is compressed. */
+static void append_global_tail(MODEL *m, const layer_off *lo, int l, kvcache *cache,
+                               const REAL *hid, const REAL *kseq, const REAL *vseq, int B, int T) {
+  const int D = m->D, C = m->C, Hkv = m->Hkv, ratio = m->ratio;
+  for (int t = 0; t < T; t++) {
+    for (int b = 0; b < B; b++) {
+      int slot = cache->taillen[l];
+      memcpy(cache->tailh + (((size_t)l * B + b) * ratio + slot) * C, hid + ((int64_t)b * T + t) * C,
+             sizeof(REAL) * C);
+      for (int hh = 0; hh < Hkv; hh++) {
+        size_t tb = ((((size_t)l * B + b) * Hkv + hh) * ratio + slot) * D;
+        memcpy(cache->tailk + tb, kseq + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+        memcpy(cache->tailv + tb, vseq + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
+      }
+    }
+    cache->taillen[l]++;
+    if (cache->taillen[l] == ratio) compress_tail(m, lo, l, cache, B);
+  }
+}
+
+/* cacheReusedIndexerKeys (compress_attention.go:1160-1176): a Reindex layer
+ * projects the producer's new compressed blocks with its own indexer key. */
+static void cache_reused_indexer_keys(MODEL *m, const layer_off *lo, int l, kvcache *cache, int B) {
+  const int D = m->D, Hkv = m->Hkv, HI = m->HI, cl = lo->producer;
+  int own = cache->ccount[l * B], prod = cache->ccount[cl * B];
+  for (int blk = own; blk < prod; blk++) {
+    for (int b = 0; b < B; b++)
+      for (int hh = 0; hh < Hkv; hh++) {
+        size_t pc = (((size_t)cl * B + b) * Hkv + hh) * cache->maxBlocks + blk;
+        size_t oc = (((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks + blk;
+        linear_fwd(cache->ikc + oc * HI, cache->ck + pc * D, m->p + lo->wik, 1, D, HI);
+      }
+    for (int b = 0; b < B; b++) cache->ccount[l * B + b]++;
+  }
+}
+
+/* enc: the encoder hidden state of the T rows for a CED decoder layer (its
+ * global tail buffers enc and its own projections of it), else NULL.
+ * replay: CED bounded replay (the global caches are already filled; the
+ * local window does not reach before the replay start). */
 static void hca_decode(MODEL *m, const layer_off *lo, int l, kvcache *cache, const REAL *h,
-                       const REAL *qh, const REAL *kn, const REAL *vn, int B, int T, REAL *oh,
-                       dec_share *ds) {
+                       const REAL *qh, const REAL *kn, const REAL *vn, const REAL *enc, int replay,
+                       int B, int T, REAL *oh, dec_share *ds) {
   const int D = m->D, C = m->C, Hq = m->Hq, Hkv = m->Hkv, ratio = m->ratio, rr = Hq / Hkv;
   const int offset = cache->pos, cl = lo->producer, HI = m->HI;
-  if (lo->mode == REUSE_FULL) { /* appendGlobalTail (:868-890) */
-    for (int t = 0; t < T; t++) {
-      for (int b = 0; b < B; b++) {
-        int slot = cache->taillen[l];
-        memcpy(cache->tailh + (((size_t)l * B + b) * ratio + slot) * C, h + ((int64_t)b * T + t) * C,
-               sizeof(REAL) * C);
-        for (int hh = 0; hh < Hkv; hh++) {
-          size_t tb = ((((size_t)l * B + b) * Hkv + hh) * ratio + slot) * D;
-          memcpy(cache->tailk + tb, kn + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
-          memcpy(cache->tailv + tb, vn + (((int64_t)b * T + t) * Hkv + hh) * D, sizeof(REAL) * D);
-        }
-      }
-      cache->taillen[l]++;
-      if (cache->taillen[l] == ratio) compress_tail(m, lo, l, cache, B);
+  const int floor_pos = replay ? offset : 0;
+  if (lo->mode == REUSE_FULL && !replay) {
+    if (enc) {
+      REAL *ks = (REAL *)malloc(sizeof(REAL) * (int64_t)B * T * Hkv * D);
+      REAL *vs = (REAL *)malloc(sizeof(REAL) * (int64_t)B * T * Hkv * D);
+      ced_kv(m, lo, enc, B, T, offset, ks, vs, NULL);
+      append_global_tail(m, lo, l, cache, enc, ks, vs, B, T);
+      free(ks); free(vs);
+    } else {
+      append_global_tail(m, lo, l, cache, h, kn, vn, B, T);
     }
-  } else if (lo->mode == REUSE_REINDEX && m->topk > 0) { /* cacheReusedIndexerKeys */
-    int own = cache->ccount[l * B], prod = cache->ccount[cl * B];
-    for (int blk = own; blk < prod; blk++) {
-      for (int b = 0; b < B; b++)
-        for (int hh = 0; hh < Hkv; hh++) {
-          size_t pc = (((size_t)cl * B + b) * Hkv + hh) * cache->maxBlocks + blk;
-          size_t oc = (((size_t)l * B + b) * Hkv + hh) * cache->maxBlocks + blk;
-          linear_fwd(cache->ikc + oc * HI, cache->ck + pc * D, m->p + lo->wik, 1, D, HI);
-        }
-      for (int b = 0; b < B; b++) cache->ccount[l * B + b]++;
-    }
+  } else if (lo->mode == REUSE_REINDEX && m->topk > 0 && !replay) {
+    cache_reused_indexer_keys(m, lo, l, cache, B);
   }
   const int kcap = m->topk, ccap = candidate_cap(m);
   int *lsel = NULL, *lnsel = NULL;
@@ -1893,7 +2008,8 @@ static void hca_decode(MODEL *m, const layer_off *lo, int l, kvcache *cache, con
         if (count > 0) attn_fwd(q, cache->ck + cb, cache->cv + cb, go, &gl, 1, count, D, count, -1);
       }
       if (m->swa > 0) { /* localAttentionRow (compress_attention.go:543-560) */
-        int ls = pos - m->swa < 0 ? 0 : pos - m->swa;
+        int ls = pos - m->swa < floor_pos ? floor_pos : pos - m->swa;
+        if (ls < 0) ls = 0;
         int n = pos - ls + 1;
         attn_fwd(q, cache_k(m, cache, l, b, hh) + (int64_t)ls * D,
                  cache_v(m, cache, l, b, hh) + (int64_t)ls * D, lo_, &ll, 1, n, D, n - 1, -1);
@@ -1961,6 +2077,7 @@ typedef struct {
   REAL *raw, *embn, *smsig, *x0;
   layer_ctx lc[MAXL];
   hca_share *shares[MAXL]; /* compressed-attention groups, by producing layer */
+  REAL *enc, *ced_genc;    /* CED: encoder hidden state and its decoder gradient */
   REAL *backout, *final_pre, *final_norm, *logits;
 } train_ctx;
 
@@ -1978,6 +2095,7 @@ static void ctx_free(train_ctx *c, int L) {
     hca_ctx_free(x->hca);
     hca_share_free(c->shares[l]);
   }
+  free(c->enc); free(c->ced_genc);
   free(c->backout); free(c->final_pre); free(c->final_norm); free(c->logits);
   free(c);
 }
@@ -1994,8 +2112,24 @@ static REAL *dup_arr(const REAL *a, size_t n) {
  * is also the training forward (model/train_transformer.go:63-142); ctx, when
  * given, receives the saved activations.
  */
+/* Options of a partial forward (PrefillCED's phases): a layer range, given
+ * activations and initial residual instead of the embedding, bounded replay,
+ * the final activations out, and no cache advance. */
+typedef struct {
+  int l0, l1, replay, no_advance;
+  const REAL *x_in, *x0_in;
+  REAL *x_out;
+} fwd_opts;
+
+static void forward_run(MODEL *m, const int32_t *ids, int B, int T, kvcache *cache, REAL *logits,
+                        train_ctx *ctx, const fwd_opts *op);
 static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *cache, REAL *logits,
                          train_ctx *ctx) {
+  forward_run(m, ids, B, T, cache, logits, ctx, NULL);
+}
+
+static void forward_run(MODEL *m, const int32_t *ids, int B, int T, kvcache *cache, REAL *logits,
+                        train_ctx *ctx, const fwd_opts *op) {
   int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, F = m->F, V = m->V, PV = m->PV;
   int64_t N = (int64_t)B * T;
   const REAL *P = m->p;
@@ -2006,7 +2140,16 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
   dec_share ds;
   memset(&ds, 0, sizeof ds);
   m->distill_loss = 0;
+  const int l_begin = op ? op->l0 : 0, l_end = op ? op->l1 : m->L;
+  const int replay = op ? op->replay : 0;
+  REAL *enc = NULL; /* CED: the input of the first decoder layer */
   REAL *x = (REAL *)malloc(sizeof(REAL) * N * C);
+  REAL *x0 = NULL;
+  if (op && op->x_in) {
+    memcpy(x, op->x_in, sizeof(REAL) * N * C);
+    x0 = dup_arr(op->x0_in, (size_t)N * C);
+    goto layers;
+  }
   REAL *raw = (REAL *)malloc(sizeof(REAL) * N * C);
   for (int64_t n = 0; n < N; n++) memcpy(raw + n * C, P + m->wte + (int64_t)ids[n] * C, sizeof(REAL) * C);
   rmsnorm_rows(x, raw, N, C);
@@ -2066,8 +2209,9 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
     free(gate);
   }
   if (!ctx) free(raw);
-  REAL *x0 = dup_arr(x, (size_t)N * C);
+  x0 = dup_arr(x, (size_t)N * C);
   if (ctx) ctx->x0 = x0;
+layers:;
 
   int offset = cache ? cache->pos : 0;
   int klen = cache ? cache->pos + T : T;
@@ -2087,9 +2231,14 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
   REAL *vesig = (REAL *)malloc(sizeof(REAL) * N * Hkv);
   REAL *vev = (REAL *)malloc(sizeof(REAL) * N * Hkv * D);
   REAL *lseb = (REAL *)malloc(sizeof(REAL) * N * Hq);
-  for (int l = 0; l < m->L; l++) {
+  for (int l = l_begin; l < l_end; l++) {
     const layer_off *lo = &m->lay[l];
     layer_ctx *lc = ctx ? &ctx->lc[l] : NULL;
+    if (m->split > 0 && l == m->split) { /* encoderHidden (transformer.go:310-312) */
+      enc = dup_arr(x, (size_t)N * C);
+      if (ctx) ctx->enc = enc;
+    }
+    const REAL *enc_l = (m->split > 0 && l >= m->split) ? enc : NULL;
     if (lc) lc->xin = dup_arr(x, (size_t)N * C);
     /* combineResidual (transformer.go:544-551) */
     REAL lr = P[m->rl + l], l0 = P[m->x0l + l];
@@ -2173,10 +2322,10 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
         free(ds.sel); free(ds.nsel); free(ds.pool); free(ds.npool);
         memset(&ds, 0, sizeof ds);
       }
-      hca_decode(m, lo, l, cache, h, qh, kn, v, B, T, oh, &ds);
+      hca_decode(m, lo, l, cache, h, qh, kn, v, enc_l, replay, B, T, oh, &ds);
     } else if (m->ratio > 1) {
       hca_ctx *hc = (hca_ctx *)calloc(1, sizeof(hca_ctx));
-      hca_train_forward(m, lo, qh, kh, vh, h, B, T, oh, lseb, hc, &cur_share);
+      hca_train_forward(m, lo, qh, kh, vh, h, enc_l, B, T, oh, lseb, hc, &cur_share);
       if (lo->mode == REUSE_FULL) shares[l] = cur_share;
       if (lc) lc->hca = hc;
       else hcs[l] = hc;
@@ -2233,13 +2382,19 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
     for (int64_t i = 0; i < N * C; i++) x[i] = x[i] + a[i];
     if (l == bkidx) backout = dup_arr(x, (size_t)N * C);
   }
-  if (cache) cache->pos += T;
+  if (cache && !(op && op->no_advance)) cache->pos += T;
   for (int l = 0; l < m->L; l++) {
     hca_ctx_free(hcs[l]);
     if (ctx) ctx->shares[l] = shares[l];
     else hca_share_free(shares[l]);
   }
   free(ds.sel); free(ds.nsel); free(ds.pool); free(ds.npool);
+  if (!ctx) free(enc);
+  if (op && op->x_out) memcpy(op->x_out, x, sizeof(REAL) * N * C);
+  if (!logits) {
+    free(backout);
+    goto done;
+  }
   /* backout, final norm, lm_head, trimVocab, softcap (transformer.go:333-341) */
   if (backout) {
     REAL nb = -P[m->bkl];
@@ -2257,13 +2412,90 @@ static void forward_impl(MODEL *m, const int32_t *ids, int B, int T, kvcache *ca
       logits[n * V + j] = softcap(R(acc));
     }
   (void)PV;
+done:
   if (!ctx) free(x0);
   free(x); free(h); free(q); free(k); free(v); free(o); free(a); free(u); free(act);
   free(qn); free(kn); free(vesig); free(vev); free(lseb);
 }
 
+/* PrefillCED (transformer.go:363-449) of a batch-1 prompt: the encoder over
+ * the full prompt; every decoder Full layer's global compressed cache filled
+ * from its projections of the encoder's final hidden state (Reindex layers
+ * cache their indexer keys); the decoder replayed over the last SWA-window
+ * tokens from the encoder rows, with embedAndSmear's smear (the first
+ * replayed row is not mixed with the previous token; a single replayed row
+ * is mixed with the cached previous embedding, which is its own).  Writes
+ * the last replayed row's logits; the cache ends at the prompt length. */
+static void prefill_ced(MODEL *m, const int32_t *ids, int T, kvcache *cache, REAL *last_logits) {
+  const int C = m->C, split = m->split, V = m->V, D = m->D, Hkv = m->Hkv;
+  int replay_len = m->swa < T ? m->swa : T;
+  const int rstart = T - replay_len;
+  /* phase 1: the encoder (embedAndSmear with a fresh cache: smearAdd) */
+  REAL *enc = (REAL *)malloc(sizeof(REAL) * (int64_t)T * C);
+  fwd_opts op1 = {0, split, 0, 1, NULL, NULL, enc};
+  forward_run(m, ids, 1, T, cache, NULL, NULL, &op1);
+  /* phase 2: decoder global caches from the encoder hidden state */
+  REAL *ks = (REAL *)malloc(sizeof(REAL) * (int64_t)T * Hkv * D);
+  REAL *vs = (REAL *)malloc(sizeof(REAL) * (int64_t)T * Hkv * D);
+  for (int l = split; l < m->L; l++) {
+    const layer_off *lo = &m->lay[l];
+    if (lo->mode == REUSE_FULL) {
+      ced_kv(m, lo, enc, 1, T, 0, ks, vs, NULL);
+      append_global_tail(m, lo, l, cache, enc, ks, vs, 1, T);
+    } else if (lo->mode == REUSE_REINDEX && m->topk > 0) {
+      cache_reused_indexer_keys(m, lo, l, cache, 1);
+    }
+  }
+  free(ks); free(vs);
+  /* phase 3: bounded replay (embedAndSmear, transformer.go:452-477) */
+  const int32_t *rids = ids + rstart;
+  REAL *xr = (REAL *)malloc(sizeof(REAL) * (int64_t)replay_len * C);
+  const REAL *P = m->p, *wsg = P + m->smg;
+  const REAL lam = P[m->sml];
+  for (int t = 0; t < replay_len; t++) {
+    REAL *row = xr + (int64_t)t * C;
+    memcpy(row, P + m->wte + (int64_t)rids[t] * C, sizeof(REAL) * C);
+    rmsnorm_rows(row, row, 1, C);
+  }
+  REAL *prev = cache->has_prev ? dup_arr(cache->prev, (size_t)C) : NULL;
+  memcpy(cache->prev, xr + (int64_t)(replay_len - 1) * C, sizeof(REAL) * C);
+  cache->has_prev = 1;
+  if (replay_len > 1) {
+    REAL *gate = (REAL *)malloc(sizeof(REAL) * replay_len);
+    for (int t = 1; t < replay_len; t++) {
+      double a = 0;
+      for (int c = 0; c < SMEAR_CH; c++) a += (double)xr[(int64_t)t * C + c] * (double)wsg[c];
+      gate[t] = sigmoidR(R(a)) * lam;
+    }
+    for (int t = replay_len - 1; t >= 1; t--)
+      for (int c = 0; c < C; c++) xr[(int64_t)t * C + c] += gate[t] * xr[(int64_t)(t - 1) * C + c];
+    free(gate);
+  } else if (prev) {
+    double a = 0;
+    for (int c = 0; c < SMEAR_CH; c++) a += (double)xr[c] * (double)wsg[c];
+    REAL g = sigmoidR(R(a)) * lam;
+    for (int c = 0; c < C; c++) xr[c] += g * prev[c];
+  }
+  free(prev);
+  cache->pos = rstart;
+  REAL *lg = (REAL *)malloc(sizeof(REAL) * (int64_t)replay_len * V);
+  fwd_opts op3 = {split, m->L, 1, 1, enc + (int64_t)rstart * C, xr, NULL};
+  forward_run(m, rids, 1, replay_len, cache, lg, NULL, &op3);
+  memcpy(last_logits, lg + (int64_t)(replay_len - 1) * V, sizeof(REAL) * V);
+  cache->pos = T;
+  free(lg); free(xr); free(enc);
+}
+
 void FN(orc_forward)(MODEL *m, const int32_t *ids, int B, int T, REAL *logits) {
   forward_impl(m, ids, B, T, NULL, logits, NULL);
+}
+
+/* PrefillCED of a batch-1 prompt into a fresh cache; the last replayed row's
+ * logits [V] (the row Engine.GenerateWith samples from). */
+void FN(orc_prefill_ced)(MODEL *m, const int32_t *ids, int T, REAL *last_logits) {
+  kvcache *c = cache_new(m, 1, T);
+  prefill_ced(m, ids, T, c, last_logits);
+  cache_free(c);
 }
 
 /* Token-by-token (or chunked) KV-cache decode, the invariant
@@ -2293,7 +2525,7 @@ void FN(orc_forward_decode)(MODEL *m, const int32_t *ids, int B, int T, int chun
  * the gradient with respect to the block input in gx; parameter gradients
  * accumulate into G. */
 static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, const int32_t *ids,
-                           int B, int T, const REAL *gout, REAL *gx, REAL *G) {
+                           int B, int T, const REAL *gout, REAL *gx, REAL *genc, REAL *G) {
   int C = m->C, Hq = m->Hq, Hkv = m->Hkv, D = m->D, F = m->F, ratio = Hq / Hkv;
   int64_t N = (int64_t)B * T;
   const REAL *P = m->p;
@@ -2341,7 +2573,7 @@ static void block_backward(MODEL *m, const layer_ctx *lc, const layer_off *lo, c
   if (m->ratio > 1) {
     dhin_c = (REAL *)malloc(sizeof(REAL) * N * C);
     hca_train_backward(m, lo, lc->hca, lc->qn, lc->kn, lc->vh, lc->o, doh, lc->lse, lc->h, B, T,
-                       dqh, dkh, dvh, dhin_c, G);
+                       dqh, dkh, dvh, dhin_c, genc, G);
   } else {
   /* serial (b, qh) loop as train.go:305-326 so GQA accumulation is race-free */
   for (int b = 0; b < B; b++)
@@ -2467,6 +2699,7 @@ static void train_backward(MODEL *m, train_ctx *ctx, const REAL *glogits, REAL *
     G[m->bkl] += R(dot);
   }
   int bkidx = L / 2;
+  if (m->split > 0) ctx->ced_genc = (REAL *)calloc((size_t)N * C, sizeof(REAL));
   REAL *gx0 = (REAL *)calloc((size_t)N * C, sizeof(REAL));
   REAL *gb = (REAL *)malloc(sizeof(REAL) * N * C);
   REAL *lg = (REAL *)malloc(sizeof(REAL) * N * C);
@@ -2474,7 +2707,7 @@ static void train_backward(MODEL *m, train_ctx *ctx, const REAL *glogits, REAL *
     memcpy(lg, ga, sizeof(REAL) * N * C);
     if (l == bkidx && gback)
       for (int64_t i = 0; i < N * C; i++) lg[i] = lg[i] + gback[i];
-    block_backward(m, &ctx->lc[l], &m->lay[l], ctx->ids, B, T, lg, gb, G);
+    block_backward(m, &ctx->lc[l], &m->lay[l], ctx->ids, B, T, lg, gb, ctx->ced_genc, G);
     REAL lr = P[m->rl + l], l0 = P[m->x0l + l];
     double rdot = 0, idot = 0;
     for (int64_t i = 0; i < N * C; i++) {
@@ -2483,6 +2716,8 @@ static void train_backward(MODEL *m, train_ctx *ctx, const REAL *glogits, REAL *
       rdot += (double)gb[i] * (double)ctx->lc[l].xin[i];
       idot += (double)gb[i] * (double)ctx->x0[i];
     }
+    if (m->split > 0 && l == m->split) /* the decoder's global-KV gradient (:221-229) */
+      for (int64_t i = 0; i < N * C; i++) ga[i] = ga[i] + ctx->ced_genc[i];
     G[m->rl + l] += R(rdot);
     G[m->x0l + l] += R(idot);
   }
@@ -2650,7 +2885,10 @@ void FN(orc_generate_batch)(MODEL *m, const int32_t *prompt, int P, int S, int m
   int V = m->V;
   kvcache *pre = cache_new(m, 1, P);
   REAL *lg = (REAL *)malloc(sizeof(REAL) * (int64_t)P * V);
-  forward_impl(m, prompt, 1, P, pre, lg, NULL);
+  if (m->split > 0) /* engine.go:164-173 */
+    prefill_ced(m, prompt, P, pre, lg + (int64_t)(P - 1) * V);
+  else
+    forward_impl(m, prompt, 1, P, pre, lg, NULL);
   float *logits = (float *)malloc(sizeof(float) * (int64_t)S * V);
   for (int s = 0; s < S; s++)
     for (int j = 0; j < V; j++) logits[(int64_t)s * V + j] = (float)lg[(int64_t)(P - 1) * V + j];

@@ -140,6 +140,8 @@ def lib():
         "orc_set_freeze_targets_f64": (v, [C.c_void_p, C.c_int]),
         "orc_distill_loss_f32": (C.c_double, [C.c_void_p]),
         "orc_model_set_params_f32": (v, [C.c_void_p, _f32p]),
+        "orc_prefill_ced_f32": (v, [C.c_void_p, _i32p, C.c_int, _f32p]),
+        "orc_prefill_ced_f64": (v, [C.c_void_p, _i32p, C.c_int, _f64p]),
         "orc_model_set_params_f64": (v, [C.c_void_p, _f64p]),
         "orc_distill_loss_f64": (C.c_double, [C.c_void_p]),
         "orc_channel_compress": (v, [C.c_int, C.c_int, C.c_int, _f32p, _f32p, _f32p, _f32p]),
@@ -302,6 +304,13 @@ class OracleModel:
     def aux_loss(self) -> float:
         """MoE balance loss of the last training forward (pg_step / ce_loss)."""
         return self._fn("orc_aux_loss")(self._m)
+
+    def prefill_ced(self, prompt: np.ndarray) -> np.ndarray:
+        """Model.PrefillCED of one prompt: the last replayed row's logits."""
+        prompt = np.ascontiguousarray(prompt, np.int32).reshape(-1)
+        out = np.zeros(self.shape.vocab_size, self.dtype)
+        self._fn("orc_prefill_ced")(self._m, prompt, prompt.size, out)
+        return out
 
     def set_params(self, params: np.ndarray):
         self.params = np.ascontiguousarray(params, self.dtype)

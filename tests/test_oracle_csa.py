@@ -245,3 +245,99 @@ def test_csa_decode_matches_training_forward(orc, case, chunk):
     full = m.forward(ids)
     dec = m.forward_decode(ids, chunk)
     assert np.abs(full - dec).max() <= 2e-6 * np.abs(full).max()
+
+
+# ---- CED: causal encoder-decoder split (model/transformer.go:363-449) -------
+def ced_cfg(**kw):
+    # cedBaseConfig (model/ced_test.go:12-17): four layers split 2 + 2
+    base = dict(topk=0, ratio=2, swa=3, n_layer=4, kv=2, head=2, seq=16, vocab=16, embd=32, dim=4)
+    base.update(kw)
+    cfg = csa_cfg(**base)
+    cfg.ced = True
+    cfg.validate()
+    return cfg
+
+
+def test_ced_roles(orc):
+    cfg = ced_cfg(reuse="FR", topk=2)
+    assert cfg.ced_split == 2
+    # the reuse pattern restarts at the split: each half starts with a Full layer
+    assert [cfg.reuse_mode_at(l) for l in range(4)] == ["F", "R", "F", "R"]
+    assert [cfg.reuse_producer(l) for l in range(4)] == [0, 0, 2, 2]
+    tab = orc.param_table(orc.ModelShape.from_config(cfg))
+    assert [tuple(t) for t in tab] == [tuple(t) for t in cfg.param_table()]
+
+
+CED_FD = {
+    "dense": dict(),
+    "reindex": dict(reuse="FR", topk=2, pool=2, budget=4),
+    "fru_sparse": dict(reuse="FRU", topk=2, n_layer=6, swa=4),
+}
+
+
+@pytest.mark.parametrize("case", list(CED_FD))
+def test_ced_gradients_match_finite_differences(orc, case):
+    """ced_test.go:117-125: the backward through the split, including the
+    decoder's global-KV gradient injected into the encoder output."""
+    cfg = ced_cfg(**CED_FD[case])
+    w = G.init_weights(cfg, seed=11, perturb=0.1).astype(np.float64)
+    sh = orc.ModelShape.from_config(cfg)
+    rng = np.random.default_rng(4)
+    ids = rng.integers(0, cfg.vocab_size, (2, 11)).astype(np.int32)
+    tg = rng.integers(0, cfg.vocab_size, (2, 11)).astype(np.int32)
+    tg[:, :2] = -1
+    m = orc.OracleModel(sh, w, np.float64)
+    m.freeze_targets(1)
+    _, g = m.ce_loss(ids, tg)
+    m.freeze_targets(2)
+
+    def total(wv):
+        m.set_params(wv)
+        loss, _ = m.ce_loss(ids, tg, want_grads=False)
+        return loss + m.distill_loss()
+
+    eps = 1e-6
+    d = rng.standard_normal(w.size)
+    fd = (total(w + eps * d) - total(w - eps * d)) / (2 * eps)
+    an = float(g @ d)
+    assert abs(fd - an) <= 1e-6 * abs(an), (fd, an)
+    tab = orc.param_table(sh)
+    for name, r, c, off in tab:
+        for i in off + rng.integers(0, r * c, 2):
+            e = np.zeros_like(w)
+            e[i] = 1
+            fdv = (total(w + eps * e) - total(w - eps * e)) / (2 * eps)
+            assert abs(fdv - g[i]) <= 1e-7 + 1e-5 * abs(g[i]), (name, int(i - off), fdv, g[i])
+    # ced_test.go:284-300: the last encoder layer receives the decoder's gradient
+    split = cfg.ced_split
+    off, r, c = cfg.param_slices()[f"transformer.h.{split - 1}.mlp.c_proj.weight"]
+    assert np.any(g[off:off + r * c])
+
+
+@pytest.mark.parametrize("chunk", [1, 3])
+@pytest.mark.parametrize("case", ["dense", "fru_sparse"])
+def test_ced_decode_matches_training_forward(orc, case, chunk):
+    cfg = ced_cfg(seq=64, vocab=40, embd=64, head=4, **CED_FD[case])
+    w = G.init_weights(cfg, seed=3, perturb=0.1)
+    m = orc.OracleModel(orc.ModelShape.from_config(cfg), w)
+    ids = np.random.default_rng(0).integers(0, cfg.vocab_size, (2, 29)).astype(np.int32)
+    full = m.forward(ids)
+    dec = m.forward_decode(ids, chunk)
+    assert np.abs(full - dec).max() <= 2e-6 * np.abs(full).max()
+
+
+@pytest.mark.parametrize("topk", [0, 2])
+def test_ced_prefill_matches_full_when_window_covers_prompt(orc, topk):
+    """ced_test.go:193-235: with the window covering the prompt the replay
+    starts at position 0, so PrefillCED's last logits equal the full
+    forward's; a shorter window truncates the replay and changes them."""
+    cfg = ced_cfg(swa=16, topk=topk)
+    w = G.init_weights(cfg, seed=42, perturb=0.1).astype(np.float64)
+    prompt = np.array([1, 5, 2, 8, 3, 7], np.int32)
+    m = orc.OracleModel(orc.ModelShape.from_config(cfg), w, np.float64)
+    full = m.forward(prompt[None])[0, -1]
+    ced = m.prefill_ced(prompt)
+    assert np.abs(full - ced).max() <= 1e-12 * max(1, np.abs(full).max())
+    short = ced_cfg(swa=3, topk=topk)
+    m2 = orc.OracleModel(orc.ModelShape.from_config(short), w, np.float64)
+    assert np.abs(m2.prefill_ced(prompt) - m2.forward(prompt[None])[0, -1]).max() > 1e-6
