@@ -26,6 +26,7 @@ SOURCES = [
     "gn_attention.hip",
     "gn_latent.hip",
     "gn_compress.hip",
+    "gn_sparse.hip",
     "gn_sampler.hip",
     "gn_session.cpp",
     "gn_tools.cpp",

@@ -350,16 +350,16 @@ __device__ __forceinline__ bool key_valid(int kj, int t, int T, int window) {
 }
 // The flash kernels' mask: causal/windowed keys, or compressed blocks that
 // ended before the query's block (ratio > 1).
-__device__ __forceinline__ bool key_ok(int kj, int t, int Tk, int ratio, int window) {
-  if (ratio > 1) return kj < Tk && (kj + 1) * ratio <= t;
+__device__ __forceinline__ bool key_ok(int kj, int t, int Tk, int ratio, int window, int qoff) {
+  if (ratio > 1) return kj < Tk && (kj + 1) * ratio <= t + qoff;
   return key_valid(kj, t, Tk, window);
 }
 // Key tiles a query block [q0, qlast] needs: [kbeg, kend).
 __device__ __forceinline__ void key_range(int q0, int qlast, int Tk, int ratio, int window,
-                                          int* kbeg, int* kend) {
+                                          int qoff, int* kbeg, int* kend) {
   if (ratio > 1) {
     *kbeg = 0;
-    *kend = min(Tk, qlast / ratio);
+    *kend = min(Tk, (qlast + qoff) / ratio);
   } else {
     *kbeg = window >= 0 ? max(0, q0 - window) : 0;
     *kend = qlast + 1;
@@ -406,7 +406,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
 
   const int qlast = min(a.T, q0 + FQ) - 1;
   int kmin, kmax;
-  key_range(q0, qlast, a.Tk, a.ratio, a.window, &kmin, &kmax);
+  key_range(q0, qlast, a.Tk, a.ratio, a.window, a.qoff, &kmin, &kmax);
   for (int kt = (kmin / FK) * FK; kt < kmax; kt += FK) {
     __syncthreads();  // previous tile fully consumed
     // K tile rows (coalesced float4), V tile transposed into Vt[d][key]
@@ -454,7 +454,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int kj = kt + 16 * kb + 4 * g + r;
-        if (!key_ok(kj, t, a.Tk, a.ratio, a.window)) st[kb][r] = -INFINITY;
+        if (!key_ok(kj, t, a.Tk, a.ratio, a.window, a.qoff)) st[kb][r] = -INFINITY;
         tmax = fmaxf(tmax, st[kb][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -562,7 +562,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
 
   const int qlast = min(a.T, q0 + FQ) - 1;
   int kmin, kmax;
-  key_range(q0, qlast, a.Tk, a.ratio, a.window, &kmin, &kmax);
+  key_range(q0, qlast, a.Tk, a.ratio, a.window, a.qoff, &kmin, &kmax);
   for (int kt = (kmin / FK) * FK; kt < kmax; kt += FK) {
     __syncthreads();
 #pragma unroll
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int kj = kt + 16 * kb + 4 * g + r;
-        const float p = (active && key_ok(kj, t, a.Tk, a.ratio, a.window)) ? expf(st[r] - lse) : 0.f;
+        const float p = (active && key_ok(kj, t, a.Tk, a.ratio, a.window, a.qoff)) ? expf(st[r] - lse) : 0.f;
         ds[r] = p * (dpt[r] - dl);
       }
       // dQ^T += K^T dS^T: A = K[16kb + 4g + c][16i + l16]
@@ -652,7 +652,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
   // queries that can see a key of the block: [qbeg, qend)
   int qbeg, qend;
   if (a.ratio > 1) {
-    qbeg = min(a.T, (k0 + 1) * a.ratio);
+    qbeg = min(a.T, max(0, (k0 + 1) * a.ratio - a.qoff));
     qend = a.T;
   } else {
     qbeg = k0;
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
 #pragma unroll
         for (int rr = 0; rr < 4; rr++) {
           const int ql = 16 * qb + 4 * g + rr, tq = qt + ql;
-          const bool ok = active && tq < a.T && key_ok(j, tq, a.Tk, a.ratio, a.window);
+          const bool ok = active && tq < a.T && key_ok(j, tq, a.Tk, a.ratio, a.window, a.qoff);
           p[rr] = ok ? expf(sv[rr] - Ls[ql]) : 0.f;
           ds[rr] = p[rr] * (dp[rr] - Ds[ql]);
         }

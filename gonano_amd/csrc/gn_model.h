@@ -78,9 +78,9 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st);
 // Key masks of the flash kernels.  ratio <= 1: causal with a sliding window
 // (key j visible from query t when j <= t and t - j <= window, window < 0:
 // none).  ratio > 1: the keys are compressed blocks of `ratio` positions and
-// query t sees the blocks that ended before its own, j < t / ratio
-// (model/compress_attention.go:562-677); a query with no visible key gets a
-// zero output and log-sum-exp -inf.
+// query t (at position qoff + t) sees the blocks that ended before its own,
+// j < (qoff + t) / ratio (model/compress_attention.go:562-677); a query with
+// no visible key gets a zero output and log-sum-exp -inf.
 struct FlashArgs {
   const float* q;  // [B*T, Hq, 128]
   const float* k;  // [B*Tk, Hkv, 128]
@@ -90,6 +90,7 @@ struct FlashArgs {
   int B, T, Hq, Hkv, window;
   int Tk = 0;      // keys per sequence (0: T)
   int ratio = 0;
+  int qoff = 0;    // compressed keys: position of the first query
 };
 void launch_flash_fwd(FlashArgs a, hipStream_t st);
 
@@ -107,6 +108,7 @@ struct FlashBwdArgs {
   int B, T, Hq, Hkv, window;
   int Tk = 0;
   int ratio = 0;
+  int qoff = 0;
   bool delta_ready = false;  // branches of a merged softmax share the merged
   bool dq_accum = false;     // log-sum-exp and row correction dO . O_merged
 };
@@ -343,6 +345,79 @@ struct HcaDecodeArgs {
   const int* pos_dev;  // when set, read on the device
 };
 void launch_hca_decode_compress(const HcaDecodeArgs& a, hipStream_t st);
+
+// ---- flash preset: sparse compressed attention (model/indexer.go) ---------
+// A chunk of sequences [b0, b0 + chunk) of one layer: rows (z, t) with
+// z = (b - b0) * Hkv + hk; row t may select compressed blocks
+// s < min(blocks, (qoff + t) / ratio).
+struct CsaShape {
+  int T, blocks, Hkv, ratio, qoff, b0;
+  int ldo;      // row stride of the chunk's score-like matrices (>= blocks)
+  int H, dim;   // indexer heads and head dim
+};
+struct IndexerScoreArgs {
+  CsaShape shape;
+  const float* iq;  // [B*T][H*dim] indexer queries
+  const float* ik;  // [B*blocks][Hkv][H*dim] indexer keys of the compressed blocks
+  const float* w;   // [H] head weights
+  float* out;       // forward: chunk scores [chunk*Hkv][T][ldo]
+  // backward (mask_out set): per-head masks [H][chunk*Hkv][T][ldo] (stride
+  // mask_stride between heads) from the row gradient gs, and per-block
+  // partials of the head-weight gradient [H][indexer_mask_blocks()]
+  const float* gs;
+  float* mask_out;
+  int64_t mask_stride;
+  float* gw_blocks;
+};
+void launch_indexer_scores(const IndexerScoreArgs& a, int chunk_seqs, hipStream_t st);
+int64_t indexer_mask_blocks(const CsaShape& s, int chunk_seqs);
+
+struct CsaSelectArgs {
+  CsaShape shape;
+  int chunk_seqs;
+  const float* scores;    // chunk scores
+  int K, pool, gpt, ccap; // top-k, group size, groups kept, candidate capacity
+  const int* pool_in;     // Reindex: the producer's candidates [B*Hkv][T][ccap] (or null)
+  const int* npool_in;
+  int* sel;               // [B*Hkv][T][K]
+  int* nsel;              // [B*Hkv][T]
+  int* pool_out;          // Full with pool > 1: candidates published, or null
+  int* npool_out;
+  int groups_cap, wave_floats;  // set by the launcher
+};
+void launch_csa_select(CsaSelectArgs a, hipStream_t st);
+
+struct CsaAttnArgs {
+  const float* q;   // [B*T, Hq, 128]
+  const float* kc;  // [B*blocks, Hkv, 128]
+  const float* vc;
+  const int* sel;   // [B*Hkv][T][K]
+  const int* nsel;
+  int B, T, blocks, Hq, Hkv, K;
+  float* o;         // forward: [B*T, Hq, 128] and lse [B*T, Hq]
+  float* lse;
+  const float* dout;   // backward: with the merged lse and delta (dO . O)
+  const float* delta;
+  float* dq;           // overwritten
+  float* dkc;          // accumulated (atomics)
+  float* dvc;
+};
+void launch_csa_attn_fwd(const CsaAttnArgs& a, hipStream_t st);
+void launch_csa_attn_bwd(const CsaAttnArgs& a, hipStream_t st);
+void launch_query_group_sum(const float* q, int Hq, int Hkv, int64_t N, float* out,
+                            hipStream_t st);
+struct CsaDistillArgs {
+  CsaShape shape;
+  const float* scores;  // chunk indexer scores
+  const float* tlog;    // chunk mean main-attention logits
+  const int* pool_in;   // Reindex restriction (or null)
+  const int* npool_in;
+  int ccap;
+  float weight;
+  float* gs;            // chunk (softmax(I) - target) * weight
+};
+void launch_csa_distill(const CsaDistillArgs& a, int chunk_seqs, hipStream_t st);
+void launch_sum_partials(const float* part, int64_t n, float* out, hipStream_t st);
 
 // ---- sampler (inference/sampler.go + tensors/random.go) -------------------
 struct SamplerArgs {

@@ -71,8 +71,14 @@ struct Layer {
   float *wgu, *ggu, *wr, *rbias, *gwr;
   float *eg, *eu, *ed, *geg, *geu, *ged;
   // flash preset: the layer's channel compressor (logit weight [128, C] and
-  // per-slot bias [ratio, 128])
+  // per-slot bias [ratio, 128]), lightning indexer (query [HI, C], key
+  // [HI, 128], head weights [H]); its reuse role ('F', 'R', 'U') and the
+  // group's producing layer
   float *wcl, *gcl, *cbias, *gcbias;
+  float *wiq, *giq, *wik, *gik, *wih, *gih;
+  char mode;
+  int producer;
+  bool has_idx;
 };
 
 }  // namespace gn
@@ -93,6 +99,10 @@ struct gn_session {
   // flash preset: compressed attention (ratio > 1) with a local window
   bool hca = false;
   int ratio = 1, swa = 0;
+  // CSA: top-k, indexer heads/dim/width, hierarchical pool, groups kept per
+  // row, candidate capacity, distillation weight; CED split (0: off)
+  int topk = 0, ih = 1, idim = 64, HI = 64, ipool = 1, gpt = 1, ccap = 1, split = 0;
+  float iweight = 1.f;
   // decode-time compressed caches of the current rollout: [L][rows][Hkv]
   // [maxBlocks][128] keys and values, [L][rows][ratio][128] logit rings
   float *hck = nullptr, *hcv = nullptr, *hring = nullptr;
@@ -260,10 +270,18 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     s->R = cfg.rotary_dims <= 0 ? s->D : cfg.rotary_dims;
   }
   GN_CHECK(s->R <= s->D && s->R % 2 == 0, "config: RotaryDims must be even and <= head dim");
-  if (cfg.sparse_topk > 0 || strnlen(cfg.reuse_pattern, sizeof(cfg.reuse_pattern)) > 0 || cfg.ced)
-    throw Error(GN_ERR_UNSUPPORTED,
-                "session: sparse attention, cross-layer reuse and CED prefill are not built yet");
   s->hca = cfg.compression_ratio > 1;  // Config.Compression() (config.go:407-414)
+  const size_t plen_r = strnlen(cfg.reuse_pattern, sizeof(cfg.reuse_pattern));
+  GN_CHECK(plen_r < sizeof(cfg.reuse_pattern), "config: reuse pattern not terminated");
+  // config.go:465-533
+  GN_CHECK(cfg.sparse_topk <= 0 || s->hca, "config: SparseTopK requires CompressionRatio > 1");
+  GN_CHECK(plen_r == 0 || s->hca, "config: ReusePattern requires CompressionRatio > 1");
+  for (size_t i = 0; i < plen_r; i++)
+    GN_CHECK(strchr("FRUfru", cfg.reuse_pattern[i]) != nullptr, "config: invalid reuse pattern");
+  GN_CHECK(plen_r == 0 || cfg.reuse_pattern[0] == 'F' || cfg.reuse_pattern[0] == 'f',
+           "config: reuse pattern must start with F");
+  GN_CHECK(!cfg.ced || (s->hca && cfg.swa_window > 0 && cfg.n_layer >= 2),
+           "config: CED requires compression, a local window and >= 2 layers");
   if (s->hca) {
     GN_CHECK(!s->mla, "config: MLA is not supported with compression");  // config.go:483-486
     GN_CHECK(hca_ratio_supported(cfg.compression_ratio),
@@ -271,6 +289,21 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     GN_CHECK(cfg.swa_window >= 0, "config: negative SWA window");
     s->ratio = cfg.compression_ratio;
     s->swa = cfg.swa_window;
+    s->split = cfg.ced ? cfg.n_layer / 2 : 0;
+    if (cfg.sparse_topk > 0) {  // config.go:372-402
+      s->topk = cfg.sparse_topk;
+      GN_CHECK(s->topk <= 64, "session: sparse top-k above 64 is not supported");
+      s->idim = cfg.indexer_dim > 0 ? cfg.indexer_dim : 64;
+      s->ih = cfg.indexer_heads > 0 ? cfg.indexer_heads : 1;
+      s->HI = s->idim * s->ih;
+      GN_CHECK(s->HI <= 256 && s->ih <= 8, "session: indexer heads * dim must be <= 256");
+      s->ipool = cfg.indexer_pool > 1 ? cfg.indexer_pool : 1;
+      const int budget = cfg.indexer_candidates > 0 ? cfg.indexer_candidates
+                                                    : std::max(8 * s->topk, 64);
+      s->gpt = std::max(1, (budget + s->ipool - 1) / s->ipool);
+      s->ccap = std::max(s->gpt * s->ipool, s->topk);
+      s->iweight = cfg.indexer_weight > 0 ? cfg.indexer_weight : 1.f;
+    }
   }
   GN_CHECK(s->C <= 1024, "session: EmbedDim above 1024 is not supported");
   GN_CHECK(s->Hq / s->Hkv <= 8, "session: GQA ratio above 8 is not supported");
@@ -304,7 +337,6 @@ static void build_session(gn_session* s, const gn_config& cfg) {
   // value embedding, then the feed-forward; globals last.  Tensors that feed
   // one GEMM together are adjacent (q/k/v; the four MLA projections of h;
   // KeyUp/ValueUp; c_gate/c_fc).
-  s->layers.assign(s->L, Layer{});
   int64_t cur = 0;
   auto place = [&](int64_t n) {
     int64_t o = cur;
@@ -322,9 +354,30 @@ static void build_session(gn_session* s, const gn_config& cfg) {
   struct Off {
     int64_t qkv = -1, o = -1, fc = -1, pj = -1, vg = -1, ve = -1;
     int64_t xa = -1, qu = -1, kvu = -1, gu = -1, r = -1, rb = -1, eg = -1, eu = -1, ed = -1;
-    int64_t cl = -1, cb = -1;
+    int64_t cl = -1, cb = -1, iq = -1, ik = -1, ih = -1;
   };
   std::vector<Off> off(s->L);
+  // reuse roles (config.go:303-370): the pattern restarts at the CED split
+  auto half_start = [&](int l) { return (s->split > 0 && l >= s->split) ? s->split : 0; };
+  auto mode_at = [&](int l) -> char {
+    if (!s->hca || plen_r == 0) return 'F';
+    const char ch = cfg.reuse_pattern[(l - half_start(l)) % plen_r];
+    return (ch == 'R' || ch == 'r') ? 'R' : (ch == 'U' || ch == 'u') ? 'U' : 'F';
+  };
+  s->layers.assign(s->L, Layer{});
+  for (int l = 0; l < s->L; l++) {
+    Layer& ly = s->layers[l];
+    ly.mode = mode_at(l);
+    ly.producer = l;
+    if (ly.mode != 'F')
+      for (int i = l - 1; i >= half_start(l); i--)
+        if (mode_at(i) == 'F') {
+          ly.producer = i;
+          break;
+        }
+    ly.has_idx = s->topk > 0 && ly.mode != 'U';
+  }
+  GN_CHECK(!s->split || mode_at(s->split) == 'F', "config: CED reuse pattern must start each half with F");
   const int C = s->C, D = s->D, Hq = s->Hq, Hkv = s->Hkv, F = s->F;
   for (int l = 0; l < s->L; l++) {
     Off& o = off[l];
@@ -349,11 +402,19 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     }
     o.o = place((int64_t)C * C);
     add(p + "attn.c_proj.weight", C, C, o.o);
-    if (s->hca) {  // model/params.go:43-46
+    if (s->hca && s->layers[l].mode == 'F') {  // model/params.go:43-51
       o.cl = place((int64_t)D * C);
       add(p + "attn.compress_logits.weight", D, C, o.cl);
       o.cb = place((int64_t)s->ratio * D);
       add(p + "attn.compress_bias", s->ratio, D, o.cb);
+    }
+    if (s->layers[l].has_idx) {
+      o.iq = place((int64_t)s->HI * C);
+      add(p + "attn.indexer_query.weight", s->HI, C, o.iq);
+      o.ik = place((int64_t)s->HI * D);
+      add(p + "attn.indexer_key.weight", s->HI, D, o.ik);
+      o.ih = place(s->ih);
+      add(p + "attn.indexer_heads", s->ih, 1, o.ih);
     }
     if (!s->mla && has_value_embedding(l, s->L)) {  // no VE under MLA (transformer.go:72-78)
       o.vg = place((int64_t)Hkv * VE_CH);
@@ -426,6 +487,9 @@ static void build_session(gn_session* s, const gn_config& cfg) {
     ly.ed = P(o.ed); ly.ged = G(o.ed);
     ly.wcl = P(o.cl); ly.gcl = G(o.cl);
     ly.cbias = P(o.cb); ly.gcbias = G(o.cb);
+    ly.wiq = P(o.iq); ly.giq = G(o.iq);
+    ly.wik = P(o.ik); ly.gik = G(o.ik);
+    ly.wih = P(o.ih); ly.gih = G(o.ih);
   }
   if (s->mla) {  // absorbed decode weights, per layer [Hq*lat, lat] and [C, Hq*lat]
     const int64_t per = (int64_t)Hq * s->lat * s->lat + (int64_t)C * Hq * s->lat;
@@ -496,6 +560,13 @@ struct SeqBuffers {
   // [L][B][Hkv][T / ratio][128] and of the logit rings [L][B][ratio][128]
   std::vector<float*> hkc, hvc, hprobs;
   float *pf_ck = nullptr, *pf_cv = nullptr, *pf_ring = nullptr;
+  // sparse selection per layer (a Reuse layer points at the published one),
+  // a Full layer's candidate pool, indexer query/key projections; CED: the
+  // encoder hidden state and, per decoder Full layer, its projections of it
+  std::vector<int*> sel, nsel, pool, npool;
+  std::vector<float*> iq, ik, ced_k, ced_v, ced_krot;
+  float* enc = nullptr;
+  int qoff = 0;  // position of the first row (CED bounded replay)
   float *xfinal, *fpre, *fn;
   float* backout;
 };
@@ -579,50 +650,151 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
 // compressor, the global branch over compressed blocks and, with a window,
 // the local branch, merged by log-sum-exp.  Writes sb.o[l] (and sb.lse[l],
 // the merged log-sum-exp, when training).
+// Sequences per chunk of the indexer's [T][blocks] score-like matrices: about
+// 2^27 floats (512 MB) per matrix.
+static int csa_chunk(gn_session* s, int B, int T, int blocks) {
+  const int64_t per = (int64_t)s->Hkv * T * std::max(blocks, 1);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(B, ((int64_t)1 << 27) / per));
+}
+static CsaShape csa_shape(gn_session* s, int T, int blocks, int qoff, int b0) {
+  CsaShape c{};
+  c.T = T; c.blocks = blocks; c.Hkv = s->Hkv; c.ratio = s->ratio; c.qoff = qoff; c.b0 = b0;
+  c.ldo = std::max(blocks, 1); c.H = s->ih; c.dim = s->idim;
+  return c;
+}
+
+// sparseTrainingPlan's projections and selection (compress_attention.go:
+// 45-131, indexer.go:378-558) of a layer with an indexer: indexer queries of
+// h, keys of the group's compressed keys, chunked scores and the per-row
+// selection (within the Full layer's candidate pool on a Reindex layer).
+static void csa_select_layer(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, bool save,
+                             const float* kc, int blocks) {
+  const int B = sb.B, T = sb.T, Hkv = s->Hkv, HI = s->HI;
+  const int64_t N = sb.N;
+  hipStream_t st = s->stream;
+  float* iq = layer_buf(s, "csa_iq", l, save, N * HI);
+  sgemm(s, linear_fwd_desc(sb.h[l], ly.wiq, iq, (int)N, s->C, HI));
+  float* ik = layer_buf(s, "csa_ik", l, save, (size_t)B * blocks * Hkv * HI);
+  sgemm(s, linear_fwd_desc(kc, ly.wik, ik, B * blocks * Hkv, HD, HI));
+  int* sel = reinterpret_cast<int*>(layer_buf(s, "csa_sel", l, save, (size_t)B * Hkv * T * s->topk));
+  int* nsel = reinterpret_cast<int*>(layer_buf(s, "csa_nsel", l, save, (size_t)B * Hkv * T));
+  const bool produce = ly.mode == 'F' && s->ipool > 1;
+  const int p = ly.producer;
+  const bool within = ly.mode == 'R' && s->ipool > 1 && sb.pool[p];
+  int *pool = nullptr, *npool = nullptr;
+  if (produce) {
+    pool = reinterpret_cast<int*>(layer_buf(s, "csa_pool", l, true, (size_t)B * Hkv * T * s->ccap));
+    npool = reinterpret_cast<int*>(layer_buf(s, "csa_npool", l, true, (size_t)B * Hkv * T));
+  }
+  const int chunk = csa_chunk(s, B, T, blocks);
+  float* scores = A<float>(s, "csa_scores", (size_t)chunk * Hkv * T * std::max(blocks, 1));
+  for (int b0 = 0; b0 < B; b0 += chunk) {
+    const int nb = std::min(chunk, B - b0);
+    IndexerScoreArgs ia{};
+    ia.shape = csa_shape(s, T, blocks, sb.qoff, b0);
+    ia.iq = iq; ia.ik = ik; ia.w = ly.wih; ia.out = scores;
+    launch_indexer_scores(ia, nb, st);
+    CsaSelectArgs ca{};
+    ca.shape = ia.shape; ca.chunk_seqs = nb; ca.scores = scores;
+    ca.K = s->topk; ca.pool = s->ipool; ca.gpt = s->gpt; ca.ccap = s->ccap;
+    ca.pool_in = within ? sb.pool[p] : nullptr;
+    ca.npool_in = within ? sb.npool[p] : nullptr;
+    ca.sel = sel; ca.nsel = nsel; ca.pool_out = pool; ca.npool_out = npool;
+    launch_csa_select(ca, st);
+  }
+  sb.iq[l] = iq; sb.ik[l] = ik;
+  sb.sel[l] = sel; sb.nsel[l] = nsel;
+  sb.pool[l] = pool; sb.npool[l] = npool;
+}
+
+// Compressed attention of one layer over full sequences (model/train.go:
+// 99-169 with compressForward, sparseTrainingPlan, compressedAttentionForward
+// [Sparse], attentionForwardWindowed and mergeAttentionBranches): a Full
+// layer compresses (on a CED decoder layer, its own projections of the
+// encoder hidden state); every layer attends to its group's compressed
+// blocks -- all blocks before its own, or the indexer's selection (a Reuse
+// layer takes the latest published one) -- merged with the local window by
+// log-sum-exp.  Writes sb.o[l] (and sb.lse[l], the merged log-sum-exp, when
+// training).
 static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, SeqMode mode) {
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, B = sb.B, T = sb.T, ratio = s->ratio;
   const int64_t N = sb.N;
   const bool save = mode == SEQ_TRAIN;
   hipStream_t st = s->stream;
   const int blocks = (int)ceil_div(T, ratio);
-  float* clog = A<float>(s, "hca_clog", N * HD);
-  sgemm(s, linear_fwd_desc(sb.h[l], ly.wcl, clog, (int)N, C, HD));
-  HcaCompressArgs ca{};
-  ca.clog = clog; ca.bias = ly.cbias; ca.k = sb.kn[l]; ca.v = sb.v[l];
-  ca.B = B; ca.T = T; ca.Hkv = Hkv; ca.ratio = ratio;
-  ca.probs = layer_buf(s, "hca_probs", l, save, (size_t)B * blocks * ratio * HD);
-  ca.kc = layer_buf(s, "hca_kc", l, save, (size_t)B * blocks * s->KVW);
-  ca.vc = layer_buf(s, "hca_vc", l, save, (size_t)B * blocks * s->KVW);
-  if (mode == SEQ_PREFILL) {
-    const int64_t full = T / ratio;
-    if (full > 0) {
-      ca.ck_pf = sb.pf_ck + (int64_t)l * B * Hkv * full * HD;
-      ca.cv_pf = sb.pf_cv + (int64_t)l * B * Hkv * full * HD;
+  const bool ced = s->split > 0 && l >= s->split;
+  if (ly.mode == 'F') {
+    const float *hin = sb.h[l], *kin = sb.kn[l], *vin = sb.v[l];
+    if (ced) {  // cedGlobalKeyValue (attention.go:156-171) of the encoder hidden state
+      float* kv = A<float>(s, "ced_kv", N * 2 * s->KVW);
+      GemmDesc d = linear_fwd_desc(sb.enc, ly.wqkv + (int64_t)Hq * HD * C, kv, (int)N, C, 2 * s->KVW);
+      sgemm(s, d);
+      QkvPostArgs qa{};
+      qa.qkv = kv; qa.cosT = s->cosT; qa.sinT = s->sinT;
+      qa.C = C; qa.Hq = 0; qa.Hkv = Hkv; qa.R = s->R; qa.T = T; qa.pos0 = sb.qoff;
+      qa.kn = layer_buf(s, "ced_k", l, save, N * s->KVW);
+      qa.vout = layer_buf(s, "ced_v", l, save, N * s->KVW);
+      qa.krot = save ? layer_buf(s, "ced_krot", l, true, N * s->KVW) : nullptr;
+      launch_qkv_post(qa, N, st);
+      sb.ced_k[l] = qa.kn; sb.ced_v[l] = qa.vout; sb.ced_krot[l] = qa.krot;
+      hin = sb.enc; kin = qa.kn; vin = qa.vout;
     }
-    ca.ring_pf = sb.pf_ring + (int64_t)l * B * ratio * HD;
+    float* clog = A<float>(s, "hca_clog", N * HD);
+    sgemm(s, linear_fwd_desc(hin, ly.wcl, clog, (int)N, C, HD));
+    HcaCompressArgs ca{};
+    ca.clog = clog; ca.bias = ly.cbias; ca.k = kin; ca.v = vin;
+    ca.B = B; ca.T = T; ca.Hkv = Hkv; ca.ratio = ratio;
+    ca.probs = layer_buf(s, "hca_probs", l, save, (size_t)B * blocks * ratio * HD);
+    ca.kc = layer_buf(s, "hca_kc", l, true, (size_t)B * blocks * s->KVW);
+    ca.vc = layer_buf(s, "hca_vc", l, true, (size_t)B * blocks * s->KVW);
+    if (mode == SEQ_PREFILL) {
+      const int64_t full = T / ratio;
+      if (full > 0) {
+        ca.ck_pf = sb.pf_ck + (int64_t)l * B * Hkv * full * HD;
+        ca.cv_pf = sb.pf_cv + (int64_t)l * B * Hkv * full * HD;
+      }
+      ca.ring_pf = sb.pf_ring + (int64_t)l * B * ratio * HD;
+    }
+    launch_hca_compress(ca, st);
+    sb.hkc[l] = ca.kc; sb.hvc[l] = ca.vc; sb.hprobs[l] = ca.probs;
   }
-  launch_hca_compress(ca, st);
-  sb.hkc[l] = ca.kc; sb.hvc[l] = ca.vc; sb.hprobs[l] = ca.probs;
+  const int p = ly.producer;
+  const float *kc = sb.hkc[p], *vc = sb.hvc[p];
+  if (s->topk > 0) {
+    if (ly.mode == 'U') {  // the group's latest published selection
+      int q = l - 1;
+      while (q > p && s->layers[q].mode == 'U') q--;
+      sb.sel[l] = sb.sel[q];
+      sb.nsel[l] = sb.nsel[q];
+    } else {
+      csa_select_layer(s, sb, ly, l, save, kc, blocks);
+    }
+  }
   float* o = layer_buf(s, "o", l, save, N * Hq * HD);
   float* lse = save ? layer_buf(s, "lse", l, true, N * Hq) : A<float>(s, "hca_lse", N * Hq);
-  FlashArgs fg{};
-  fg.q = sb.qn[l]; fg.k = ca.kc; fg.v = ca.vc;
-  fg.B = B; fg.T = T; fg.Tk = blocks; fg.ratio = ratio; fg.Hq = Hq; fg.Hkv = Hkv; fg.window = -1;
-  if (s->swa > 0) {
-    fg.o = A<float>(s, "hca_og", N * Hq * HD);
-    fg.lse = A<float>(s, "hca_lg", N * Hq);
+  float* og = s->swa > 0 ? A<float>(s, "hca_og", N * Hq * HD) : o;
+  float* lg = s->swa > 0 ? A<float>(s, "hca_lg", N * Hq) : lse;
+  if (s->topk > 0) {
+    CsaAttnArgs aa{};
+    aa.q = sb.qn[l]; aa.kc = kc; aa.vc = vc; aa.sel = sb.sel[l]; aa.nsel = sb.nsel[l];
+    aa.B = B; aa.T = T; aa.blocks = blocks; aa.Hq = Hq; aa.Hkv = Hkv; aa.K = s->topk;
+    aa.o = og; aa.lse = lg;
+    launch_csa_attn_fwd(aa, st);
+  } else {
+    FlashArgs fg{};
+    fg.q = sb.qn[l]; fg.k = kc; fg.v = vc; fg.o = og; fg.lse = lg;
+    fg.B = B; fg.T = T; fg.Tk = blocks; fg.ratio = ratio; fg.qoff = sb.qoff;
+    fg.Hq = Hq; fg.Hkv = Hkv; fg.window = -1;
     launch_flash_fwd(fg, st);
+  }
+  if (s->swa > 0) {
     FlashArgs fl{};  // localAttentionRow over the sliding window (compress_attention.go:543-560)
     fl.q = sb.qn[l]; fl.k = sb.kn[l]; fl.v = sb.v[l];
     fl.o = A<float>(s, "hca_ol", N * Hq * HD);
     fl.lse = A<float>(s, "hca_ll", N * Hq);
     fl.B = B; fl.T = T; fl.Hq = Hq; fl.Hkv = Hkv; fl.window = s->swa;
     launch_flash_fwd(fl, st);
-    launch_merge_branches(fg.o, fg.lse, fl.o, fl.lse, o, lse, N * Hq, st);
-  } else {
-    fg.o = o;
-    fg.lse = lse;
-    launch_flash_fwd(fg, st);
+    launch_merge_branches(og, lg, fl.o, fl.lse, o, lse, N * Hq, st);
   }
   sb.o[l] = o;
   sb.lse[l] = save ? lse : nullptr;
@@ -642,8 +814,9 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   launch_embed_smear(sb.ids, s->wte, s->smg, s->sml, B, T, C, sb.raw, sb.embn, sb.smsig, sb.x0, st);
   for (auto* vec : {&sb.xin, &sb.xb, &sb.h, &sb.qrot, &sb.krot, &sb.qn, &sb.kn, &sb.v, &sb.vesig,
                     &sb.o, &sb.lse, &sb.mid, &sb.h2, &sb.u, &sb.act, &sb.xa, &sb.gu, &sb.hkc,
-                    &sb.hvc, &sb.hprobs})
+                    &sb.hvc, &sb.hprobs, &sb.iq, &sb.ik, &sb.ced_k, &sb.ced_v, &sb.ced_krot})
     vec->assign(L, nullptr);
+  for (auto* vec : {&sb.sel, &sb.nsel, &sb.pool, &sb.npool}) vec->assign(L, nullptr);
   sb.moe.assign(L, MoeBuffers{});
   float* qkv = s->mla ? nullptr : A<float>(s, "qkv", N * s->QKVW);
   float* xcur = sb.x0;
@@ -652,6 +825,10 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   for (int l = 0; l < L; l++) {
     Layer& ly = s->layers[l];
     sb.xin[l] = xcur;
+    if (s->split > 0 && l == s->split) {  // encoderHidden (transformer.go:310-312)
+      sb.enc = A<float>(s, "ced_enc", N * C);
+      GN_HIP(hipMemcpyAsync(sb.enc, xcur, sizeof(float) * N * C, hipMemcpyDeviceToDevice, st));
+    }
     float* xb = layer_buf(s, "xb", l, save, N * C);
     float* h = layer_buf(s, "h", l, save, N * C);
     launch_resid_norm(xcur, sb.x0, s->rl, s->x0l, l, N, C, xb, h, st);
@@ -895,28 +1072,139 @@ static void mla_backward(gn_session* s, const Layer& ly, const float* xa, const 
 // ---------------------------------------------------------------------------
 // PolicyGradientStep
 // ---------------------------------------------------------------------------
-// Backward of hca_forward (model/train.go:211-303 with compressedAttention-
-// Backward, attentionBackwardWindowed and compressBackward,
-// compress_attention.go:376-433, 737-845, 1182-1209): both branches from the
-// merged log-sum-exp and the merged row correction dO . O, the compressor's
-// softmax backward into the raw key/value gradients, its weight and bias
-// gradients.  Returns the compressor's logit gradient [N, 128], whose product
-// with the logit weight the caller adds to the attention input's gradient.
-static float* hca_backward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l,
-                           const float* dout, float* delta, float* dqn, float* dkn, float* dvv) {
+// A GEMM whose product with the attention input's gradient (dh += g . W)
+// the caller adds after the q/k/v projection backward.
+struct DhExtra {
+  const float* g;
+  const float* W;
+  int K;
+};
+
+// The indexer's distillation backward of one layer (compress_attention.go:
+// 133-196 with SparseIndexer.Backward, indexer.go:107-151): per chunk of
+// sequences the scores are recomputed, the target is the softmax of the
+// mean main-attention logit, gs = (softmax(I) - target) * weight, the
+// per-head ReLU masks give the query/key gradients by GEMMs; the head
+// weights' gradient is reduced in a fixed order.  Adds the key gradient's
+// image into the group's compressed-key gradient gkc and returns the query
+// gradient [N, HI] for the attention input.
+static float* csa_distill_backward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l,
+                                   int blocks, const float* kc, float* gkc) {
+  const int B = sb.B, T = sb.T, Hkv = s->Hkv, HI = s->HI, H = s->ih, dim = s->idim;
+  const int64_t N = sb.N;
+  const int rr = s->Hq / Hkv, p = ly.producer;
+  const bool within = ly.mode == 'R' && s->ipool > 1 && sb.pool[p];
+  hipStream_t st = s->stream;
+  float* qsum = A<float>(s, "csa_qsum", N * Hkv * HD);
+  launch_query_group_sum(sb.qn[l], s->Hq, Hkv, N, qsum, st);
+  float* gq = A<float>(s, "csa_gq", N * HI);
+  GN_HIP(hipMemsetAsync(gq, 0, sizeof(float) * N * HI, st));
+  float* gk = A<float>(s, "csa_gk", (size_t)B * blocks * Hkv * HI);
+  const int chunk = csa_chunk(s, B, T, blocks);
+  const CsaShape s0 = csa_shape(s, T, blocks, sb.qoff, 0);
+  const int64_t per = (int64_t)chunk * Hkv * T * s0.ldo;
+  float* scores = A<float>(s, "csa_scores", per);
+  float* tlog = A<float>(s, "csa_tlog", per);
+  float* gs = A<float>(s, "csa_gs", per);
+  float* masks = A<float>(s, "csa_mask", per * H);
+  const int64_t nblk = indexer_mask_blocks(s0, chunk);
+  float* gwb = A<float>(s, "csa_gwb", nblk * H);
+  for (int b0 = 0; b0 < B; b0 += chunk) {
+    const int nb = std::min(chunk, B - b0);
+    const CsaShape sh = csa_shape(s, T, blocks, sb.qoff, b0);
+    IndexerScoreArgs ia{};
+    ia.shape = sh; ia.iq = sb.iq[l]; ia.ik = sb.ik[l]; ia.w = ly.wih; ia.out = scores;
+    launch_indexer_scores(ia, nb, st);
+    for (int bl = 0; bl < nb; bl++)
+      for (int hh = 0; hh < Hkv; hh++) {  // mean main-attention logits
+        const int b = b0 + bl, z = bl * Hkv + hh;
+        GemmDesc d;
+        d.M = T; d.N = blocks; d.K = HD;
+        d.A = qsum + ((int64_t)b * T * Hkv + hh) * HD; d.lda = (int64_t)Hkv * HD;
+        d.B = kc + ((int64_t)b * blocks * Hkv + hh) * HD; d.ldb = (int64_t)Hkv * HD;
+        d.C = tlog + (int64_t)z * T * sh.ldo; d.ldc = sh.ldo;
+        d.alpha = 1.f / (float)rr;
+        sgemm(s, d);
+      }
+    CsaDistillArgs da{};
+    da.shape = sh; da.scores = scores; da.tlog = tlog;
+    da.pool_in = within ? sb.pool[p] : nullptr;
+    da.npool_in = within ? sb.npool[p] : nullptr;
+    da.ccap = s->ccap; da.weight = s->iweight; da.gs = gs;
+    launch_csa_distill(da, nb, st);
+    IndexerScoreArgs ma = ia;
+    ma.out = nullptr; ma.gs = gs; ma.mask_out = masks; ma.mask_stride = per;
+    ma.gw_blocks = gwb;
+    launch_indexer_scores(ma, nb, st);
+    const int64_t nbk = indexer_mask_blocks(sh, nb);
+    for (int h = 0; h < H; h++) launch_sum_partials(gwb + (int64_t)h * nbk, nbk, ly.gih + h, st);
+    for (int bl = 0; bl < nb; bl++)
+      for (int hh = 0; hh < Hkv; hh++)
+        for (int h = 0; h < H; h++) {
+          const int b = b0 + bl, z = bl * Hkv + hh;
+          const float* mh = masks + (int64_t)h * per + (int64_t)z * T * sh.ldo;
+          GemmDesc dq;  // gq[b, t, h] += mask . ik
+          dq.M = T; dq.N = dim; dq.K = blocks;
+          dq.A = mh; dq.lda = sh.ldo;
+          dq.B = sb.ik[l] + ((int64_t)b * blocks * Hkv + hh) * HI + h * dim;
+          dq.ldb = (int64_t)Hkv * HI; dq.b_kcontig = false;
+          dq.C = gq + (int64_t)b * T * HI + h * dim; dq.ldc = HI; dq.epi = EPI_ACCUM;
+          sgemm(s, dq);
+          GemmDesc dk;  // gk[b, s, hh, h] = mask^T . iq
+          dk.M = blocks; dk.N = dim; dk.K = T;
+          dk.A = mh; dk.lda = sh.ldo; dk.a_kcontig = false;
+          dk.B = sb.iq[l] + (int64_t)b * T * HI + h * dim; dk.ldb = HI; dk.b_kcontig = false;
+          dk.C = gk + ((int64_t)b * blocks * Hkv + hh) * HI + h * dim; dk.ldc = (int64_t)Hkv * HI;
+          sgemm(s, dk);
+        }
+  }
+  sgemm(s, linear_dw_desc(gq, sb.h[l], ly.giq, (int)N, s->C, HI));
+  sgemm(s, linear_dw_desc(gk, kc, ly.gik, B * blocks * Hkv, HD, HI));
+  sgemm(s, linear_dx_desc(gk, ly.wik, gkc, B * blocks * Hkv, HD, HI, EPI_ACCUM));
+  return gq;
+}
+
+// Backward of hca_forward (model/train.go:198-303 with compressedAttention-
+// Backward[Sparse], indexerDistillationGradient, attentionBackwardWindowed
+// and compressBackward, compress_attention.go:376-433, 737-845, 1182-1209):
+// both branches from the merged log-sum-exp and the merged row correction
+// dO . O; compressed-key/value gradients accumulate in the group's buffers,
+// which the Full layer -- the last of its group in the backward -- runs
+// through the compressor (a CED decoder layer's into the encoder gradient
+// genc).  Appends the attention input's extra gradient GEMMs to `extra`.
+static void hca_backward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, const float* dout,
+                         float* delta, float* dqn, float* dkn, float* dvv,
+                         std::vector<DhExtra>& extra, float* genc) {
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, B = sb.B, T = sb.T, ratio = s->ratio;
   const int64_t N = sb.N;
   hipStream_t st = s->stream;
   const int blocks = (int)ceil_div(T, ratio);
+  const int p = ly.producer;
+  const bool ced = s->split > 0 && l >= s->split;
+  const float *kc = sb.hkc[p], *vc = sb.hvc[p];
+  const size_t cw = (size_t)B * blocks * s->KVW;
+  float* gkc = A<float>(s, "hca_gkc" + std::to_string(p), cw);
+  float* gvc = A<float>(s, "hca_gvc" + std::to_string(p), cw);
   launch_row_dot(sb.o[l], dout, delta, N * Hq, st);
-  float* dkc = A<float>(s, "hca_dkc", (size_t)B * blocks * s->KVW);
-  float* dvc = A<float>(s, "hca_dvc", (size_t)B * blocks * s->KVW);
-  FlashBwdArgs bg{};
-  bg.q = sb.qn[l]; bg.k = sb.hkc[l]; bg.v = sb.hvc[l]; bg.o = sb.o[l]; bg.dout = dout;
-  bg.lse = sb.lse[l]; bg.delta = delta; bg.delta_ready = true;
-  bg.dq = dqn; bg.dk = dkc; bg.dv = dvc;
-  bg.B = B; bg.T = T; bg.Tk = blocks; bg.ratio = ratio; bg.Hq = Hq; bg.Hkv = Hkv; bg.window = -1;
-  launch_flash_bwd(bg, st);
+  if (s->topk > 0) {
+    CsaAttnArgs aa{};
+    aa.q = sb.qn[l]; aa.kc = kc; aa.vc = vc; aa.sel = sb.sel[l]; aa.nsel = sb.nsel[l];
+    aa.B = B; aa.T = T; aa.blocks = blocks; aa.Hq = Hq; aa.Hkv = Hkv; aa.K = s->topk;
+    aa.lse = sb.lse[l]; aa.dout = dout; aa.delta = delta; aa.dq = dqn; aa.dkc = gkc; aa.dvc = gvc;
+    launch_csa_attn_bwd(aa, st);
+  } else {
+    float* tk = A<float>(s, "hca_dkc", cw);
+    float* tv = A<float>(s, "hca_dvc", cw);
+    FlashBwdArgs bg{};
+    bg.q = sb.qn[l]; bg.k = kc; bg.v = vc; bg.o = sb.o[l]; bg.dout = dout;
+    bg.lse = sb.lse[l]; bg.delta = delta; bg.delta_ready = true;
+    bg.dq = dqn; bg.dk = tk; bg.dv = tv;
+    bg.B = B; bg.T = T; bg.Tk = blocks; bg.ratio = ratio; bg.qoff = sb.qoff;
+    bg.Hq = Hq; bg.Hkv = Hkv; bg.window = -1;
+    launch_flash_bwd(bg, st);
+    launch_axpy(gkc, gkc, tk, nullptr, 1.f, (int64_t)cw, st);
+    launch_axpy(gvc, gvc, tv, nullptr, 1.f, (int64_t)cw, st);
+  }
   if (s->swa > 0) {
     FlashBwdArgs bl{};
     bl.q = sb.qn[l]; bl.k = sb.kn[l]; bl.v = sb.v[l]; bl.o = sb.o[l]; bl.dout = dout;
@@ -928,17 +1216,42 @@ static float* hca_backward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l
     GN_HIP(hipMemsetAsync(dkn, 0, sizeof(float) * N * s->KVW, st));
     GN_HIP(hipMemsetAsync(dvv, 0, sizeof(float) * N * s->KVW, st));
   }
+  if (ly.has_idx) {
+    float* gq = csa_distill_backward(s, sb, ly, l, blocks, kc, gkc);
+    extra.push_back({gq, ly.wiq, s->HI});
+  }
+  if (ly.mode != 'F') return;
   HcaCompressBwdArgs cb{};
-  cb.probs = sb.hprobs[l]; cb.k = sb.kn[l]; cb.v = sb.v[l]; cb.kc = sb.hkc[l]; cb.vc = sb.hvc[l];
-  cb.dkc = dkc; cb.dvc = dvc;
+  cb.probs = sb.hprobs[l]; cb.kc = kc; cb.vc = vc; cb.dkc = gkc; cb.dvc = gvc;
   cb.B = B; cb.T = T; cb.Hkv = Hkv; cb.ratio = ratio;
-  cb.glog = A<float>(s, "hca_glog", N * HD);
-  cb.dk = dkn; cb.dv = dvv;
+  cb.glog = A<float>(s, "hca_glog" + std::to_string(l % 2), N * HD);
   cb.gbias = ly.gcbias;
   cb.bias_part = A<float>(s, "hca_bpart", hca_bias_part_floats(ratio));
+  if (!ced) {
+    cb.k = sb.kn[l]; cb.v = sb.v[l]; cb.dk = dkn; cb.dv = dvv;
+    launch_hca_compress_bwd(cb, st);
+    sgemm(s, linear_dw_desc(cb.glog, sb.h[l], ly.gcl, (int)N, C, HD));
+    extra.push_back({cb.glog, ly.wcl, HD});
+    return;
+  }
+  // CED decoder: the compressor read the encoder hidden state and its own
+  // projections of it (cedKey/ValueProjectionBackward, train.go:454-479)
+  float* dkg = A<float>(s, "ced_dk", N * s->KVW);
+  float* dvg = A<float>(s, "ced_dv", N * s->KVW);
+  GN_HIP(hipMemsetAsync(dkg, 0, sizeof(float) * N * s->KVW, st));
+  GN_HIP(hipMemsetAsync(dvg, 0, sizeof(float) * N * s->KVW, st));
+  cb.k = sb.ced_k[l]; cb.v = sb.ced_v[l]; cb.dk = dkg; cb.dv = dvg;
   launch_hca_compress_bwd(cb, st);
-  sgemm(s, linear_dw_desc(cb.glog, sb.h[l], ly.gcl, (int)N, C, HD));
-  return cb.glog;
+  sgemm(s, linear_dw_desc(cb.glog, sb.enc, ly.gcl, (int)N, C, HD));
+  sgemm(s, linear_dx_desc(cb.glog, ly.wcl, genc, (int)N, C, HD, EPI_ACCUM));
+  float* dkv = A<float>(s, "ced_dkv", N * 2 * s->KVW);
+  QkvPostBwdArgs qb{};
+  qb.dkn = dkg; qb.dv = dvg; qb.krot = sb.ced_krot[l]; qb.cosT = s->cosT; qb.sinT = s->sinT;
+  qb.Hq = 0; qb.Hkv = Hkv; qb.R = s->R; qb.T = T; qb.dqkv = dkv;
+  launch_qkv_post_bwd(qb, N, st);
+  const int64_t kvoff = (int64_t)Hq * HD * C;
+  sgemm(s, linear_dw_desc(dkv, sb.enc, ly.gqkv + kvoff, (int)N, C, 2 * s->KVW));
+  sgemm(s, linear_dx_desc(dkv, ly.wqkv + kvoff, genc, (int)N, C, 2 * s->KVW, EPI_ACCUM));
 }
 
 static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets, int B, int T,
@@ -1012,6 +1325,19 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     GN_HIP(hipMemsetAsync(dauxl, 0, sizeof(double), st));
   }
   const int bk = L / 2;
+  float* genc = nullptr;
+  if (s->hca) {  // the groups' compressed-KV gradient accumulators
+    const size_t cw = (size_t)B * ceil_div(T, s->ratio) * s->KVW;
+    for (int l = 0; l < L; l++)
+      if (s->layers[l].mode == 'F') {
+        GN_HIP(hipMemsetAsync(A<float>(s, "hca_gkc" + std::to_string(l), cw), 0, sizeof(float) * cw, st));
+        GN_HIP(hipMemsetAsync(A<float>(s, "hca_gvc" + std::to_string(l), cw), 0, sizeof(float) * cw, st));
+      }
+    if (s->split > 0) {
+      genc = A<float>(s, "ced_genc", N * C);
+      GN_HIP(hipMemsetAsync(genc, 0, sizeof(float) * N * C, st));
+    }
+  }
   for (int l = L - 1; l >= 0; l--) {
     Layer& ly = s->layers[l];
     const float* lgp = g;
@@ -1035,9 +1361,9 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     float* dout = dtmp;  // [N, Hq*D] (Hq*D == C)
     sgemm(s, linear_dx_desc(gmid, ly.wo, dout, (int)N, Hq * HD, C));
     sgemm(s, linear_dw_desc(gmid, sb.o[l], ly.go, (int)N, Hq * HD, C));
-    float* glog = nullptr;
+    std::vector<DhExtra> extra;
     if (s->hca) {
-      glog = hca_backward(s, sb, ly, l, dout, delta, dqn, dkn, dvv);
+      hca_backward(s, sb, ly, l, dout, delta, dqn, dkn, dvv, extra, genc);
     } else {
       FlashBwdArgs fb{};
       fb.q = sb.qn[l]; fb.k = sb.kn[l]; fb.v = sb.v[l]; fb.o = sb.o[l]; fb.dout = dout;
@@ -1059,12 +1385,15 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     sgemm(s, linear_dx_desc(dqkv, ly.wqkv, dh, (int)N, C, s->QKVW));
     sgemm(s, linear_dw_desc(dqkv, sb.h[l], ly.gqkv, (int)N, C, s->QKVW));
     if (ly.has_ve) launch_ve_gate_bwd(dpre, sb.h[l], ly.wve, C, Hkv, N, ly.gwve, dh, part, st);
-    if (glog) sgemm(s, linear_dx_desc(glog, ly.wcl, dh, (int)N, C, HD, EPI_ACCUM));
+    for (const DhExtra& e : extra) sgemm(s, linear_dx_desc(e.g, e.W, dh, (int)N, C, e.K, EPI_ACCUM));
     }
     launch_rmsnorm_bwd(sb.xb[l], dh, gmid, N, C, gb, st);
     // residual mixing (train_transformer.go:218-240)
     launch_dot_into_grad(gb, sb.xin[l], sb.x0, 1.f, N * C, s->grl + l, s->gx0l + l, part, st);
     launch_resid_bwd(gb, s->rl, s->x0l, l, g, gx0, N * C, st);
+    // CED: the decoder's global-KV gradient enters at the encoder output
+    // (train_transformer.go:221-229)
+    if (genc && l == s->split) launch_axpy(g, g, genc, nullptr, 1.f, N * C, st);
   }
   launch_axpy(g, g, gx0, nullptr, 1.f, N * C, st);
   // smear, embedding norm, embedding scatter (train_transformer.go:244-264)
@@ -1280,6 +1609,11 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
                      float temperature, int top_k, const uint64_t* seeds, int32_t* rows_out,
                      int32_t* lens_out) {
   GN_CHECK(G > 0 && S > 0 && P > 0 && N >= 0, "generate: bad sizes");
+  if (s->topk > 0 || s->split > 0)
+    throw Error(GN_ERR_UNSUPPORTED, "generate: sparse selection and CED decode are not built yet");
+  for (const Layer& ly : s->layers)
+    if (ly.mode != 'F')
+      throw Error(GN_ERR_UNSUPPORTED, "generate: cross-layer reuse decode is not built yet");
   GN_CHECK(P + N <= s->S * 10, "generate: context exceeds the rotary table");
   GN_CHECK(P <= s->S, "model: sequence longer than rotary cache");
   const int C = s->C, Hkv = s->Hkv, L = s->L, V = s->V;

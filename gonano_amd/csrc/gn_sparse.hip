@@ -1,0 +1,481 @@
+// gn_sparse.hip - the flash preset's sparse compressed attention (CSA:
+// model/indexer.go, model/compress_attention.go).
+//
+// Every query row (sequence, kv-head, position t) selects at most K of the
+// compressed blocks before its own block, allowed(t) = (qoff + t) / ratio,
+// by the lightning indexer's score I[t,s] = sum_h w_h ReLU(q_h . k_h[s]):
+// blocks are grouped by `pool`, the best groups by their maximum score give
+// the candidates, and the top-K candidates by score are attended (ties go to
+// the smaller group index, then to the earlier candidate, as topKIndices
+// orders them).  The selection is integer work and is exact given the
+// scores.
+//
+// Kernels:
+//  * indexer_scores: one 16x16 (t, s) tile per block from LDS copies of the
+//    query and key projections; tiles past every row's causal limit are
+//    skipped (their entries are never read).
+//  * csa_select: one wave per row.  Group maxima live in LDS; the chosen
+//    groups and the final top-K come from repeated wave-wide argmax
+//    reductions over (value desc, index asc).
+//  * csa_attn_fwd / _bwd: one block per (token, kv-head) for all query heads
+//    of the GQA group, over the <= K gathered compressed rows held in LDS.
+//    The backward adds its compressed-key/value gradients with atomics.
+//  * distillation: the indexer's softmax against the softmax of the mean
+//    main-attention logit (compress_attention.go:133-196), per row, then the
+//    per-head ReLU masks that feed the indexer's backward GEMMs.
+#include "gn_model.h"
+
+namespace gn {
+
+static constexpr int SD = 128;   // head dim
+static constexpr int ST = 16;    // score tile
+static constexpr int HIMAX = 256;
+
+// ---------------------------------------------------------------------------
+// Indexer scores
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int allowed_blocks(int t, const CsaShape& s) {
+  return min(s.blocks, (s.qoff + t) / s.ratio);
+}
+
+static constexpr int IHMAX = 8;  // indexer heads
+
+// Forward (mask_out null): out[z][t][s] = sum_h w_h ReLU(q_h . k_h) for
+// s < allowed(t).  Backward (mask_out set): for every s < ldo the per-head
+// gradient masks mask_out[h][z][t][s] = gs * w_h * [q_h . k_h > 0] (zero past
+// allowed(t)), and this block's partial of each head weight's gradient
+// sum gs * dot * [dot > 0] into gw_blocks[h * nblocks + block].
+__global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerScoreArgs a) {
+  __shared__ float qs[ST][HIMAX + 1];
+  __shared__ float ks[ST][HIMAX + 1];
+  __shared__ float red[4];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const CsaShape& sh = a.shape;
+  const int HI = sh.H * sh.dim;
+  const int s0 = blockIdx.x * ST, t0 = blockIdx.y * ST, z = blockIdx.z;
+  const int b = sh.b0 + z / sh.Hkv, hh = z % sh.Hkv;
+  const int tl = min(sh.T, t0 + ST) - 1;
+  const bool live = s0 < allowed_blocks(tl, sh);
+  const bool bwd = a.mask_out != nullptr;
+  const int64_t blk = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  const int64_t nblk = (int64_t)gridDim.x * gridDim.y * gridDim.z;
+  const int t = t0 + ty, s = s0 + tx;
+  const bool in = t < sh.T && s < sh.ldo;
+  if (!live) {  // past every row's causal limit: scores unread, masks zero
+    if (bwd) {
+      if (in)
+        for (int h = 0; h < sh.H; h++)
+          a.mask_out[(int64_t)h * a.mask_stride + ((int64_t)z * sh.T + t) * sh.ldo + s] = 0.f;
+      if (tid < sh.H) a.gw_blocks[(int64_t)tid * nblk + blk] = 0.f;
+    }
+    return;
+  }
+  for (int i = tid; i < ST * HI; i += 256) {
+    const int r = i / HI, c = i % HI;
+    const int tt = t0 + r, ss = s0 + r;
+    qs[r][c] = tt < sh.T ? a.iq[((int64_t)b * sh.T + tt) * HI + c] : 0.f;
+    ks[r][c] = ss < sh.blocks ? a.ik[(((int64_t)b * sh.blocks + ss) * sh.Hkv + hh) * HI + c] : 0.f;
+  }
+  __syncthreads();
+  const bool ok = in && s < allowed_blocks(t, sh);
+  const float g = (bwd && ok) ? a.gs[((int64_t)z * sh.T + t) * sh.ldo + s] : 0.f;
+  float total = 0.f;
+  float wpart[IHMAX];
+  for (int h = 0; h < sh.H; h++) {
+    float dot = 0.f;
+    for (int e = 0; e < sh.dim; e++) dot += qs[ty][h * sh.dim + e] * ks[tx][h * sh.dim + e];
+    const bool pos = ok && dot > 0.f;
+    if (bwd) {
+      if (in) a.mask_out[(int64_t)h * a.mask_stride + ((int64_t)z * sh.T + t) * sh.ldo + s] =
+          pos ? g * a.w[h] : 0.f;
+      wpart[h] = pos ? g * dot : 0.f;
+    } else if (pos) {
+      total += a.w[h] * dot;
+    }
+  }
+  if (bwd) {
+    for (int h = 0; h < sh.H; h++) {
+      const float v = block_sum(wpart[h], red);
+      if (tid == 0) a.gw_blocks[(int64_t)h * nblk + blk] = v;
+    }
+    return;
+  }
+  if (ok) a.out[((int64_t)z * sh.T + t) * sh.ldo + s] = total;
+}
+
+void launch_indexer_scores(const IndexerScoreArgs& a, int chunk_seqs, hipStream_t st) {
+  const CsaShape& s = a.shape;
+  GN_CHECK(s.H * s.dim <= HIMAX && s.H <= IHMAX, "indexer: heads * dim must be <= 256, heads <= 8");
+  GN_CHECK(s.ldo >= s.blocks, "indexer: score row stride below the block count");
+  dim3 grid((unsigned)ceil_div(s.ldo, ST), (unsigned)ceil_div(s.T, ST), (unsigned)(chunk_seqs * s.Hkv));
+  hipLaunchKernelGGL(indexer_scores_kernel, grid, dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+int64_t indexer_mask_blocks(const CsaShape& s, int chunk_seqs) {
+  return ceil_div(s.ldo, ST) * ceil_div(s.T, ST) * (int64_t)chunk_seqs * s.Hkv;
+}
+
+// ---------------------------------------------------------------------------
+// Selection: one wave per row
+// ---------------------------------------------------------------------------
+// LDS writes of one lane visible to the rest of its wave
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+// (value desc, index asc): a outranks b
+__device__ __forceinline__ bool outranks(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+__device__ __forceinline__ void wave_best(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (outranks(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+// n values in LDS (NaN marks taken entries, which never outrank): take the
+// best `count` in rank order into out[].  All lanes return the same count.
+__device__ int wave_topk(float* vals, int n, int count, int* out) {
+  const int lane = threadIdx.x & 63;
+  int got = 0;
+  for (int r = 0; r < count && r < n; r++) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = lane; j < n; j += 64) {
+      const float v = vals[j];
+      if (outranks(v, j, bv, bi)) {
+        bv = v;
+        bi = j;
+      }
+    }
+    wave_best(bv, bi);
+    if (bi == 0x7fffffff) break;  // every remaining entry taken
+    if (lane == 0) {
+      out[r] = bi;
+      vals[bi] = __builtin_nanf("");
+    }
+    got++;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    wave_sync();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+  return got;
+}
+
+__global__ __launch_bounds__(256) void csa_select_kernel(CsaSelectArgs a) {
+  extern __shared__ float sm[];
+  const CsaShape& sh = a.shape;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wid;  // chunk row (z, t)
+  if (row >= (int64_t)a.chunk_seqs * sh.Hkv * sh.T) return;
+  const int z = (int)(row / sh.T), t = (int)(row % sh.T);
+  const int64_t grow = ((int64_t)(sh.b0 * sh.Hkv) + z) * sh.T + t;  // global row
+  float* vals = sm + (int64_t)wid * a.wave_floats;  // groups or candidate scores
+  int* cand = reinterpret_cast<int*>(vals + a.groups_cap);  // ccap entries
+  int* rank = cand + a.ccap;                                // ranks (<= max(gpt, K))
+  const float* score = a.scores + ((int64_t)z * sh.T + t) * sh.ldo;
+  const int allowed = allowed_blocks(t, sh);
+  int* sel = a.sel + grow * a.K;
+  if (allowed <= 0 || a.K <= 0) {
+    if (lane == 0) {
+      a.nsel[grow] = 0;
+      if (a.npool_out) a.npool_out[grow] = 0;
+    }
+    return;
+  }
+  int nc = 0;  // candidates (in candidate order) in cand[]
+  if (a.pool_in) {  // Reindex: the fine stage within the producer's pool
+    const int np = a.npool_in[grow];
+    const int* pl = a.pool_in + grow * a.ccap;
+    if (lane == 0) {
+      for (int i = 0; i < np; i++) {
+        const int e = pl[i];
+        if (e >= 0 && e < allowed) cand[nc++] = e;
+      }
+    }
+    nc = __shfl(nc, 0, 64);
+  } else if (a.pool == 1 && a.gpt >= a.K) {
+    // flat: the top-K of the top-budget entries are the top-K entries
+    for (int j = lane; j < allowed; j += 64) vals[j] = score[j];
+    wave_sync();
+    const int n = wave_topk(vals, allowed, a.K, rank);
+    if (lane == 0) {
+      for (int i = 0; i < n; i++) sel[i] = rank[i];
+      a.nsel[grow] = n;
+    }
+    return;
+  } else {
+    const int ag = (allowed + a.pool - 1) / a.pool;
+    for (int g = lane; g < ag; g += 64) {  // IndexerBlockMax over the allowed entries
+      const int st = g * a.pool, en = min(st + a.pool, allowed);
+      float mx = -INFINITY;
+      for (int e = st; e < en; e++) mx = fmaxf(mx, score[e]);
+      vals[g] = mx;
+    }
+    wave_sync();
+    const int ng = wave_topk(vals, ag, a.gpt, rank);
+    if (lane == 0) {
+      for (int r = 0; r < ng; r++) {
+        const int st = rank[r] * a.pool, en = min(st + a.pool, allowed);
+        for (int e = st; e < en; e++) cand[nc++] = e;
+      }
+    }
+    nc = __shfl(nc, 0, 64);
+  }
+  wave_sync();
+  if (a.pool_out) {
+    int* po = a.pool_out + grow * a.ccap;
+    for (int i = lane; i < nc; i += 64) po[i] = cand[i];
+    if (lane == 0) a.npool_out[grow] = nc;
+  }
+  for (int i = lane; i < nc; i += 64) vals[i] = score[cand[i]];
+  wave_sync();
+  const int n = wave_topk(vals, nc, a.K, rank);
+  if (lane == 0) {
+    for (int i = 0; i < n; i++) sel[i] = cand[rank[i]];
+    a.nsel[grow] = n;
+  }
+}
+
+void launch_csa_select(CsaSelectArgs a, hipStream_t st) {
+  const CsaShape& s = a.shape;
+  GN_CHECK(a.pool >= 1 && a.gpt >= 1 && a.K >= 1, "csa select: bad pool / budget / top-k");
+  GN_CHECK(a.gpt * a.pool <= a.ccap && a.K <= a.ccap, "csa select: candidate capacity too small");
+  a.groups_cap = std::max<int>((s.blocks + a.pool - 1) / a.pool, a.ccap);
+  a.wave_floats = a.groups_cap + a.ccap + std::max(a.gpt, a.K) + 1;
+  const size_t lds = sizeof(float) * 4 * (size_t)a.wave_floats;
+  GN_CHECK(lds <= 160 * 1024, "csa select: too many compressed blocks for one row in LDS");
+  const int64_t rows = (int64_t)a.chunk_seqs * s.Hkv * s.T;
+  hipLaunchKernelGGL(csa_select_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), lds, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// Attention over the selected compressed rows
+// ---------------------------------------------------------------------------
+template <bool BWD>
+__global__ __launch_bounds__(128) void csa_attn_kernel(CsaAttnArgs a) {
+  extern __shared__ float sm[];
+  const int tid = threadIdx.x;
+  const int64_t n = blockIdx.x;  // token b*T + t
+  const int hk = blockIdx.y;
+  const int rr = a.Hq / a.Hkv;
+  const int b = (int)(n / a.T), t = (int)(n % a.T);
+  const int64_t grow = ((int64_t)b * a.Hkv + hk) * a.T + t;
+  const int ns = a.nsel[grow];
+  const int* sel = a.sel + grow * a.K;
+  const int K = a.K;
+  float* Ks = sm;                          // [K][SD + 1]
+  float* Vs = Ks + K * (SD + 1);           // [K][SD + 1]
+  float* Ss = Vs + K * (SD + 1);           // [rr][K] scores -> probabilities
+  float* Dp = Ss + rr * K;                 // [rr][K] dP -> dS (backward)
+  float* stat = Dp + rr * K;               // [rr][2] max / sum
+  const int64_t qbase = (n * a.Hq + (int64_t)hk * rr) * SD;
+  if (ns == 0) {
+    if (!BWD) {
+      for (int i = tid; i < rr * SD; i += 128) a.o[qbase + i] = 0.f;
+      if (tid < rr) a.lse[n * a.Hq + hk * rr + tid] = -INFINITY;
+    } else {
+      for (int i = tid; i < rr * SD; i += 128) a.dq[qbase + i] = 0.f;
+    }
+    return;
+  }
+  for (int i = tid; i < ns * SD; i += 128) {
+    const int j = i / SD, d = i % SD;
+    const int64_t off = (((int64_t)b * a.blocks + sel[j]) * a.Hkv + hk) * SD + d;
+    Ks[j * (SD + 1) + d] = a.kc[off];
+    Vs[j * (SD + 1) + d] = a.vc[off];
+  }
+  __syncthreads();
+  // scores (and dP): thread per (head, key)
+  for (int p = tid; p < rr * ns; p += 128) {
+    const int h = p / ns, j = p % ns;
+    const float* q = a.q + qbase + (int64_t)h * SD;
+    float s = 0.f, dp = 0.f;
+    for (int d = 0; d < SD; d++) s += q[d] * Ks[j * (SD + 1) + d];
+    if (BWD) {
+      const float* g = a.dout + qbase + (int64_t)h * SD;
+      for (int d = 0; d < SD; d++) dp += g[d] * Vs[j * (SD + 1) + d];
+      const float lse = a.lse[n * a.Hq + hk * rr + h];
+      const float pr = expf(s - lse);
+      Ss[h * K + j] = pr;
+      Dp[h * K + j] = pr * (dp - a.delta[n * a.Hq + hk * rr + h]);
+    } else {
+      Ss[h * K + j] = s;
+    }
+  }
+  __syncthreads();
+  if (!BWD) {
+    if (tid < rr) {
+      float mx = -INFINITY;
+      for (int j = 0; j < ns; j++) mx = fmaxf(mx, Ss[tid * K + j]);
+      float sum = 0.f;
+      for (int j = 0; j < ns; j++) {
+        const float e = expf(Ss[tid * K + j] - mx);
+        Ss[tid * K + j] = e;
+        sum += e;
+      }
+      stat[2 * tid] = mx;
+      stat[2 * tid + 1] = sum;
+      a.lse[n * a.Hq + hk * rr + tid] = mx + logf(sum);
+    }
+    __syncthreads();
+    for (int i = tid; i < rr * SD; i += 128) {
+      const int h = i / SD, d = i % SD;
+      float acc = 0.f;
+      for (int j = 0; j < ns; j++) acc += Ss[h * K + j] * Vs[j * (SD + 1) + d];
+      a.o[qbase + i] = acc / stat[2 * h + 1];
+    }
+    return;
+  }
+  // backward: dq (overwritten; the local branch adds after), dk/dv scattered
+  for (int i = tid; i < rr * SD; i += 128) {
+    const int h = i / SD, d = i % SD;
+    float acc = 0.f;
+    for (int j = 0; j < ns; j++) acc += Dp[h * K + j] * Ks[j * (SD + 1) + d];
+    a.dq[qbase + i] = acc;
+  }
+  for (int i = tid; i < ns * SD; i += 128) {
+    const int j = i / SD, d = i % SD;
+    float gk = 0.f, gv = 0.f;
+    for (int h = 0; h < rr; h++) {
+      gk += Dp[h * K + j] * a.q[qbase + (int64_t)h * SD + d];
+      gv += Ss[h * K + j] * a.dout[qbase + (int64_t)h * SD + d];
+    }
+    const int64_t off = (((int64_t)b * a.blocks + sel[j]) * a.Hkv + hk) * SD + d;
+    atomicAdd(a.dkc + off, gk);
+    atomicAdd(a.dvc + off, gv);
+  }
+}
+
+static size_t csa_attn_lds(const CsaAttnArgs& a) {
+  const int rr = a.Hq / a.Hkv;
+  return sizeof(float) * ((size_t)2 * a.K * (SD + 1) + 2 * (size_t)rr * a.K + 2 * rr);
+}
+
+void launch_csa_attn_fwd(const CsaAttnArgs& a, hipStream_t st) {
+  GN_CHECK(a.K >= 1 && a.K <= 64, "sparse attention: top-k must be in [1, 64]");
+  hipLaunchKernelGGL(csa_attn_kernel<false>, dim3((unsigned)((int64_t)a.B * a.T), a.Hkv), dim3(128),
+                     csa_attn_lds(a), st, a);
+  GN_HIP(hipGetLastError());
+}
+void launch_csa_attn_bwd(const CsaAttnArgs& a, hipStream_t st) {
+  GN_CHECK(a.K >= 1 && a.K <= 64, "sparse attention: top-k must be in [1, 64]");
+  hipLaunchKernelGGL(csa_attn_kernel<true>, dim3((unsigned)((int64_t)a.B * a.T), a.Hkv), dim3(128),
+                     csa_attn_lds(a), st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// Distillation (compress_attention.go:133-196, 199-230, 262-298)
+// ---------------------------------------------------------------------------
+// qsum[n][hk][:] = sum of the query heads of kv-head hk
+__global__ void query_group_sum_kernel(const float* __restrict__ q, int Hq, int Hkv, int64_t N,
+                                       float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N * Hkv * SD) return;
+  const int d = (int)(i % SD);
+  const int64_t r = i / SD;
+  const int hk = (int)(r % Hkv);
+  const int64_t n = r / Hkv;
+  const int rr = Hq / Hkv;
+  float s = 0.f;
+  for (int h = 0; h < rr; h++) s += q[(n * Hq + hk * rr + h) * SD + d];
+  out[i] = s;
+}
+void launch_query_group_sum(const float* q, int Hq, int Hkv, int64_t N, float* out,
+                            hipStream_t st) {
+  const int64_t total = N * Hkv * SD;
+  hipLaunchKernelGGL(query_group_sum_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                     q, Hq, Hkv, N, out);
+  GN_HIP(hipGetLastError());
+}
+
+// One block per chunk row: gs = (softmax(I) - target) * weight over the
+// allowed blocks (zero elsewhere in the row); the target is the softmax of
+// the mean main-attention logits tl (already divided by the group size),
+// restricted and renormalized to the pool on Reindex layers, whose indexer
+// scores outside the pool count as -inf.
+__global__ __launch_bounds__(256) void csa_distill_kernel(CsaDistillArgs a) {
+  extern __shared__ float sm[];
+  __shared__ float red[8];
+  const CsaShape& sh = a.shape;
+  const int64_t row = blockIdx.x;
+  const int z = (int)(row / sh.T), t = (int)(row % sh.T);
+  const int64_t grow = ((int64_t)(sh.b0 * sh.Hkv) + z) * sh.T + t;
+  const int tid = threadIdx.x;
+  const int allowed = allowed_blocks(t, sh);
+  const float* sc = a.scores + row * sh.ldo;
+  const float* tl = a.tlog + row * sh.ldo;
+  float* gs = a.gs + row * sh.ldo;
+  unsigned char* inpool = reinterpret_cast<unsigned char*>(sm);
+  if (a.pool_in) {
+    for (int e = tid; e < allowed; e += 256) inpool[e] = 0;
+    __syncthreads();
+    const int np = a.npool_in[grow];
+    for (int i = tid; i < np; i += 256) {
+      const int e = a.pool_in[grow * a.ccap + i];
+      if (e >= 0 && e < allowed) inpool[e] = 1;
+    }
+    __syncthreads();
+  }
+  auto member = [&](int e) { return !a.pool_in || inpool[e]; };
+  float ms = -INFINITY, mt = -INFINITY;
+  for (int e = tid; e < allowed; e += 256) {
+    if (member(e)) ms = fmaxf(ms, sc[e]);
+    mt = fmaxf(mt, tl[e]);
+  }
+  ms = block_max(ms, red);
+  mt = block_max(mt, red);
+  float ss = 0.f, st_ = 0.f, sp = 0.f;
+  for (int e = tid; e < allowed; e += 256) {
+    if (member(e) && ms > -INFINITY) ss += expf(sc[e] - ms);
+    const float v = expf(tl[e] - mt);
+    st_ += v;
+    if (member(e)) sp += v;
+  }
+  ss = block_sum(ss, red);
+  st_ = block_sum(st_, red);
+  sp = block_sum(sp, red);
+  for (int e = tid; e < sh.ldo; e += 256) {
+    float g = 0.f;
+    if (e < allowed) {
+      const float p = (member(e) && ms > -INFINITY) ? expf(sc[e] - ms) / ss : 0.f;
+      float tg = expf(tl[e] - mt) / st_;
+      if (a.pool_in) tg = member(e) && sp > 0.f ? expf(tl[e] - mt) / sp : 0.f;
+      g = (p - tg) * a.weight;
+    }
+    gs[e] = g;
+  }
+}
+
+void launch_csa_distill(const CsaDistillArgs& a, int chunk_seqs, hipStream_t st) {
+  const CsaShape& s = a.shape;
+  const size_t lds = a.pool_in ? (size_t)s.blocks + 16 : 16;
+  GN_CHECK(lds <= 64 * 1024, "distillation: too many compressed blocks");
+  hipLaunchKernelGGL(csa_distill_kernel, dim3((unsigned)((int64_t)chunk_seqs * s.Hkv * s.T)),
+                     dim3(256), lds, st, a);
+  GN_HIP(hipGetLastError());
+}
+
+// gw[h] += sum of the per-block partials (fixed order)
+__global__ void sum_partials_kernel(const float* __restrict__ part, int64_t n, float* __restrict__ out) {
+  __shared__ float red[4];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 256) s += part[i];
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) *out += s;
+}
+void launch_sum_partials(const float* part, int64_t n, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(sum_partials_kernel, dim3(1), dim3(256), 0, st, part, n, out);
+  GN_HIP(hipGetLastError());
+}
+
+}  // namespace gn

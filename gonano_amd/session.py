@@ -24,7 +24,10 @@ def gn_config_of(cfg: Config) -> GnConfig:
                     cfg.n_experts, cfg.experts_per_token, cfg.expert_hidden,
                     cfg.shared_hidden, cfg.moe_clamp, cfg.moe_scale, cfg.balance_weight,
                     cfg.compression_ratio if cfg.compression > 1 else 0,
-                    cfg.swa_window if cfg.compression > 1 else 0)
+                    cfg.swa_window if cfg.compression > 1 else 0,
+                    cfg.sparse_topk, cfg.indexer_dim, cfg.indexer_heads, cfg.indexer_pool,
+                    cfg.indexer_candidates, cfg.indexer_weight, cfg.reuse_pattern.encode(),
+                    int(cfg.ced))
 
 
 class Session:

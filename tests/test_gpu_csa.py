@@ -1,0 +1,101 @@
+"""Parity of the flash preset's sparse compressed attention on the GPU with the
+oracle on identical inputs: Transformer.Forward logits and
+PolicyGradientStep's loss, NLL and every parameter gradient -- the
+indexer's (trained by its distillation alone), the compressor's, and the
+shared projections' -- for the lightning-indexer selection (flat and
+hierarchical), Full / Reindex / Reuse cross-layer reuse (dense and sparse)
+and the causal encoder-decoder split (model/indexer.go,
+model/compress_attention.go, model/share.go, model/transformer.go:363-449).
+
+Floating-point bars as the dense tests: 1e-4 normwise relative per tensor
+plus kerneltest.Close(1e-3, 1e-4) element-wise.  The selection is integer
+work decided by float scores; on these seeded inputs the GPU's selection
+agrees with the oracle's (a near-tie flip would show as an outlier far
+beyond the float tolerance).
+
+The CED case perturbs InitWeights by N(0, 0.05) (the others by 0.1): the
+decoder's compressor reads the unnormalized encoder hidden state, and at 0.1
+the oracle's own float32 build is already 1.4e-4 normwise from its float64
+build on this step's gradient (fwd 1.2e-5); at 0.05 that is 3.2e-5."""
+import numpy as np
+import pytest
+
+from conftest import assert_close, rel_err
+from gonano_amd import config as G
+from test_gpu_session import _compare_grads
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    # flat top-4 with a two-head indexer
+    "flat": dict(sparse_topk=4, indexer_dim=32, indexer_heads=2),
+    # hierarchical (groups of 2, 8 candidates) with Full / Reindex / Reuse
+    "hier_fru": dict(sparse_topk=3, indexer_pool=2, indexer_candidates=8, indexer_dim=16,
+                     reuse_pattern="FRU"),
+    # dense compressed attention with reuse
+    "dense_fu": dict(reuse_pattern="FU"),
+    # CED (layers 0-1 encoder, 2-3 decoder) with per-half reuse and selection
+    "ced": dict(sparse_topk=3, indexer_pool=2, indexer_candidates=6, indexer_dim=16,
+                reuse_pattern="FR", ced=True, n_layer=4),
+}
+
+
+def csa_cfg(case):
+    kw = dict(CASES[case])
+    n_layer = kw.pop("n_layer", 3)
+    cfg = G.Config(sequence_len=512, vocab_size=4096, n_layer=n_layer, n_head=2, n_kv_head=1,
+                   n_embd=256, window_pattern="SSSL", rotary_dims=64, compression_ratio=4,
+                   swa_window=64, **kw)
+    cfg.validate()
+    return cfg
+
+
+def oracle(orc, cfg, w):
+    return orc.OracleModel(orc.ModelShape.from_config(cfg), w)
+
+
+@pytest.fixture(scope="module", params=list(CASES))
+def csa(request):
+    from gonano_amd.session import Session
+    cfg = csa_cfg(request.param)
+    w = G.init_weights(cfg, seed=41, perturb=0.05 if cfg.ced else 0.1)
+    s = Session(cfg)
+    s.set_params(w)
+    yield request.param, cfg, w, s
+    s.close()
+
+
+def test_csa_param_roundtrip(csa):
+    _, cfg, w, s = csa
+    assert s.param_total == cfg.param_total()
+    assert [(n, r, c, o) for n, r, c, o in s.param_table()] == cfg.param_table()
+    assert np.array_equal(s.get_params(), w)
+
+
+def test_csa_forward_matches_oracle(csa, orc):
+    _, cfg, w, s = csa
+    ids = np.random.default_rng(1).integers(0, cfg.vocab_size, (2, 203)).astype(np.int32)
+    got = s.forward(ids)
+    want = oracle(orc, cfg, w).forward(ids)
+    assert rel_err(got, want) < 1e-4
+    assert_close(got, want, 1e-3, 1e-4, "logits")
+
+
+def test_csa_policy_gradient_step_matches_oracle(csa, orc):
+    case, cfg, w, s = csa
+    rng = np.random.default_rng(2)
+    B, T = 3, 162
+    inputs = rng.integers(0, cfg.vocab_size, (B, T)).astype(np.int32)
+    targets = rng.integers(0, cfg.vocab_size, (B, T)).astype(np.int32)
+    targets[:, :40] = -1
+    adv = np.array([0.5, -0.25, -0.25], np.float32)
+    s.zero_grad()
+    loss, nll = s.policy_gradient_step(inputs, targets, adv, float(T + 1))
+    grads = s.grads()
+    wl, wnll, wg = oracle(orc, cfg, w).pg_step(inputs, targets, adv, float(T + 1))
+    assert abs(loss - wl) <= 1e-4 * max(abs(wl), 1e-3)
+    assert rel_err(nll, wnll) < 1e-4
+    _compare_grads(cfg, grads, wg)
+    for name, r, c, off in cfg.param_table():
+        if "indexer" in name or "compress" in name:
+            assert np.any(grads[off:off + r * c]), name

@@ -195,13 +195,16 @@ def test_flash_rl_step_with_moe_matches_oracle(orc):
     _compare_grads(cfg, grads, wg)
 
 
-def test_unbuilt_flash_features_are_rejected():
-    import ctypes
-    from gonano_amd._lib import lib
-    from gonano_amd.session import gn_config_of
-    for field, value in (("sparse_topk", 16), ("reuse_pattern", b"FRU"), ("ced", 1)):
-        c = gn_config_of(flash_small_cfg())
-        setattr(c, field, value)
-        h = ctypes.c_void_p()
-        assert lib().gn_session_create(ctypes.byref(c), 0, ctypes.byref(h)) == 4  # GN_ERR_UNSUPPORTED
-        assert b"not built yet" in lib().gn_last_error()
+def test_unbuilt_flash_decode_is_rejected():
+    """Sparse selection, cross-layer reuse and CED train and run Forward;
+    their rollouts are refused with a clear error until the decode path
+    supports them."""
+    from gonano_amd._lib import HipError
+    from gonano_amd.session import Session
+    for kw in (dict(sparse_topk=4), dict(reuse_pattern="FU"), dict(ced=True, n_layer=2)):
+        cfg = flash_small_cfg()
+        for k, v in kw.items():
+            setattr(cfg, k, v)
+        with Session(cfg) as s:
+            with pytest.raises(HipError, match="not built yet"):
+                s.generate_batch(np.zeros((1, 8), np.int32), 2, 4, 1.0, 50, np.array([1], np.uint64))
