@@ -73,10 +73,10 @@ struct DecPlan {
   DecSplit g, l;
   int nsplit;
 };
-__host__ __device__ inline DecPlan dec_plan_at(const DecodeAttnArgs& a, int pos) {
+__host__ __device__ inline DecPlan dec_plan_at(const DecodeAttnArgs& a, int pos, int nsel) {
   DecPlan p;
   if (a.ratio > 1) {
-    const int count = pos / a.ratio;
+    const int count = a.sel ? nsel : pos / a.ratio;
     p.g = count > 0 ? dec_split(0, count) : dec_empty();
     p.l = a.window > 0 ? dec_split(max(0, pos - a.window), pos + 1) : dec_empty();
   } else {
@@ -86,8 +86,9 @@ __host__ __device__ inline DecPlan dec_plan_at(const DecodeAttnArgs& a, int pos)
   p.nsplit = p.g.nsplit + p.l.nsplit;
   return p;
 }
-__device__ __forceinline__ DecPlan dec_plan(const DecodeAttnArgs& a) {
-  return dec_plan_at(a, a.pos_dev ? *a.pos_dev : a.kend - 1);
+// bk = row * Hkv + kv-head (sparse selection counts are per row and head)
+__device__ __forceinline__ DecPlan dec_plan(const DecodeAttnArgs& a, int bk) {
+  return dec_plan_at(a, a.pos_dev ? *a.pos_dev : a.kend - 1, a.sel ? a.nsel[bk] : 0);
 }
 
 __device__ __forceinline__ float red8_sum(float v) { return sum8_dpp(v); }
@@ -110,7 +111,7 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   __shared__ float stat[2][R];  // max, sum per head
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int bh = blockIdx.x, s = blockIdx.y;
-  const DecPlan pl = dec_plan(a);
+  const DecPlan pl = dec_plan(a, bh);
   if (s >= pl.nsplit) return;  // graph launches size the grid for the longest window
   const int row = bh / a.Hkv, hk = bh % a.Hkv;
   const bool glob = s < pl.g.nsplit;  // a split of compressed blocks
@@ -120,15 +121,19 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   const float* kbase = glob ? a.ck : a.kc;
   const float* vbase = glob ? a.cv : a.vc;
   const int64_t cbase = ((int64_t)row * a.Hkv + hk) * (glob ? a.maxBlocks : a.maxSeq) + ks;
+  // key j of the split is row (cbase + j), or a gathered block of the selection
+  const int* gsel = (glob && a.sel) ? a.sel + (int64_t)bh * a.kcap + ks : nullptr;
+  const int64_t gbase = cbase - ks;
+  auto krow = [&](int j) -> int64_t { return gsel ? gbase + gsel[j] : cbase + j; };
 
   // V rows of phase 3, issued first
   const int d4 = tid & 31, jr = tid >> 5;
-  const v4f* vrow = reinterpret_cast<const v4f*>(vbase + cbase * HD) + d4;
+  const v4f* vrow = reinterpret_cast<const v4f*>(vbase) + d4;
   v4f vpre[DEC_VPRE];
 #pragma unroll
   for (int i = 0; i < DEC_VPRE; i++) {
     const int j = jr + 8 * i;
-    vpre[i] = vrow[(int64_t)(j < nk ? j : 0) * (HD / 4)];
+    vpre[i] = vrow[krow(j < nk ? j : 0) * (HD / 4)];
   }
 
   // ---- phase 1: scores
@@ -148,11 +153,12 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
       }
     const int q4 = (nk + 3) / 4;
     const int j0 = wid * q4, j1 = min(nk, j0 + q4);
-    const v4f* kb = reinterpret_cast<const v4f*>(kbase + cbase * HD + 16 * part);
+    const v4f* kb = reinterpret_cast<const v4f*>(kbase + 16 * part);
     auto load = [&](int j, v4f* kd) {
       const int jj = j < j1 ? j : j0;  // clamp (value unused when j >= j1)
+      const int64_t r = krow(jj) * (HD / 4);
 #pragma unroll
-      for (int i = 0; i < 4; i++) kd[i] = kb[(int64_t)jj * (HD / 4) + i];
+      for (int i = 0; i < 4; i++) kd[i] = kb[r + i];
     };
     v4f k0[4], k1[4];
     if (j0 < j1) load(j0 + g, k0);
@@ -229,7 +235,7 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
       const int j = jb + 8 * u;
-      vv[u] = vrow[(int64_t)(j < nk ? j : 0) * (HD / 4)];
+      vv[u] = vrow[krow(j < nk ? j : 0) * (HD / 4)];
     }
 #pragma unroll
     for (int u = 0; u < 4; u++)
@@ -266,9 +272,9 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
 }
 
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
-  const DecPlan pl = dec_plan(a);
-  if (pl.nsplit == 1) return;  // the attention kernel wrote the output
   const int rq = blockIdx.x;  // row * Hq + qh
+  const DecPlan pl = dec_plan(a, (rq / a.Hq) * a.Hkv + (rq % a.Hq) / (a.Hq / a.Hkv));
+  if (pl.nsplit == 1) return;  // the attention kernel wrote the output
   if (pl.nsplit == 0) {  // compressed attention with nothing visible yet
     a.o[(int64_t)rq * HD + threadIdx.x] = 0.f;
     return;
@@ -296,7 +302,7 @@ static int decode_attention_max_splits(int window, int maxSeq) {
 
 int decode_attention_split_cap(const DecodeAttnArgs& a) {
   if (a.ratio > 1) {
-    int n = a.maxBlocks > 0 ? dec_split(0, a.maxBlocks).nsplit : 0;
+    int n = a.sel ? 1 : a.maxBlocks > 0 ? dec_split(0, a.maxBlocks).nsplit : 0;
     if (a.window > 0) n += decode_attention_max_splits(a.window, a.maxSeq);
     return std::max(n, 1);
   }
@@ -308,12 +314,13 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   bool combine;
   if (a.ratio > 1) {
     GN_CHECK(a.ck && a.cv && a.maxBlocks > 0 && a.window >= 0, "decode attention: bad compressed cache");
-    if (a.pos_dev) {
+    GN_CHECK(!a.sel || (a.nsel && a.kcap >= 1 && a.kcap <= DEC_KPS), "decode attention: bad selection");
+    if (a.pos_dev || a.sel) {
       a.nsplit_max = decode_attention_split_cap(a);
     } else {
       GN_CHECK(a.kend >= 1 && a.kend <= a.maxSeq && (a.kend - 1) / a.ratio <= a.maxBlocks,
                "decode attention: position outside the caches");
-      a.nsplit_max = std::max(dec_plan_at(a, a.kend - 1).nsplit, 1);
+      a.nsplit_max = std::max(dec_plan_at(a, a.kend - 1, 0).nsplit, 1);
     }
     combine = true;  // also writes the zero output of a step with no visible key
   } else if (a.pos_dev) {

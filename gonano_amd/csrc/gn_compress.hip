@@ -71,11 +71,20 @@ __global__ __launch_bounds__(256) void hca_compress_kernel(HcaCompressArgs a) {
       a.cv_pf[po] = av;
     }
   }
-  // the logits of an incomplete last block wait in the decode ring
+  // the logits (and, in tail mode, keys/values) of an incomplete last block
+  // wait in the decode ring
   if (a.ring_pf && n < RT)
 #pragma unroll
     for (int r = 0; r < RT; r++)
       if (r < n) a.ring_pf[((int64_t)b * RT + r) * CD + d] = lg[r];
+  if (a.tailk_pf && n < RT)
+    for (int hk = 0; hk < a.Hkv; hk++)
+      for (int r = 0; r < n; r++) {
+        const int64_t off = ((row0 + r) * a.Hkv + hk) * CD + d;
+        const int64_t to = (((int64_t)b * a.Hkv + hk) * RT + r) * CD + d;
+        a.tailk_pf[to] = a.k[off];
+        a.tailv_pf[to] = a.v[off];
+      }
 }
 
 #define GN_RATIO_SWITCH(ratio, KERNEL, ...)                                 \
@@ -250,6 +259,12 @@ __global__ __launch_bounds__(128) void hca_decode_compress_kernel(HcaDecodeArgs 
   float* ring = a.ring + (int64_t)row * RT * CD + d;
   const float cur = a.clog[(int64_t)row * CD + d] + a.bias[slot * CD + d];
   ring[slot * CD] = cur;
+  if (a.tailk)  // this token's keys/values into its tail slot
+    for (int hk = 0; hk < a.Hkv; hk++) {
+      const int64_t tb = (((int64_t)row * a.Hkv + hk) * RT + slot) * CD + d;
+      a.tailk[tb] = a.knew[((int64_t)row * a.Hkv + hk) * CD + d];
+      a.tailv[tb] = a.vnew[((int64_t)row * a.Hkv + hk) * CD + d];
+    }
   if (slot != RT - 1) return;
   const int blk = pos / RT;
   if (blk >= a.maxBlocks) return;  // the host sizes maxBlocks past every position
@@ -271,12 +286,15 @@ __global__ __launch_bounds__(128) void hca_decode_compress_kernel(HcaDecodeArgs 
   for (int r = 0; r < RT; r++) p[r] *= inv;
   const int start = pos - RT + 1;
   for (int hk = 0; hk < a.Hkv; hk++) {
-    const int64_t kb = (((int64_t)row * a.Hkv + hk) * a.maxSeq + start) * CD + d;
+    const float* ksrc = a.tailk ? a.tailk + ((int64_t)row * a.Hkv + hk) * RT * CD + d
+                                : a.kc + (((int64_t)row * a.Hkv + hk) * a.maxSeq + start) * CD + d;
+    const float* vsrc = a.tailk ? a.tailv + ((int64_t)row * a.Hkv + hk) * RT * CD + d
+                                : a.vc + (((int64_t)row * a.Hkv + hk) * a.maxSeq + start) * CD + d;
     float ak = 0.f, av = 0.f;
 #pragma unroll
     for (int r = 0; r < RT; r++) {
-      ak += p[r] * a.kc[kb + (int64_t)r * CD];
-      av += p[r] * a.vc[kb + (int64_t)r * CD];
+      ak += p[r] * ksrc[(int64_t)r * CD];
+      av += p[r] * vsrc[(int64_t)r * CD];
     }
     const int64_t co = (((int64_t)row * a.Hkv + hk) * a.maxBlocks + blk) * CD + d;
     a.ck[co] = ak;
@@ -287,6 +305,37 @@ __global__ __launch_bounds__(128) void hca_decode_compress_kernel(HcaDecodeArgs 
 template <int RT>
 static void run_decode_compress(const HcaDecodeArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(hca_decode_compress_kernel<RT>, dim3(a.rows), dim3(CD), 0, st, a);
+}
+
+// The indexer key of the block completed at this step (one block per
+// (row, kv-head), one thread per output, 128-term dot in order).
+__global__ __launch_bounds__(256) void indexer_key_step_kernel(const float* __restrict__ ck,
+                                                               const float* __restrict__ wik,
+                                                               float* __restrict__ ik, int Hkv,
+                                                               int maxBlocks, int HI, int ratio,
+                                                               int pos0, const int* pos_dev) {
+  const int pos = pos_dev ? *pos_dev : pos0;
+  if (pos % ratio != ratio - 1) return;
+  const int blk = pos / ratio;
+  if (blk >= maxBlocks) return;
+  const int row = blockIdx.x / Hkv, hk = blockIdx.x % Hkv;
+  __shared__ float crow[CD];
+  const float* src = ck + (((int64_t)row * Hkv + hk) * maxBlocks + blk) * CD;
+  for (int i = threadIdx.x; i < CD; i += blockDim.x) crow[i] = src[i];
+  __syncthreads();
+  for (int o = threadIdx.x; o < HI; o += blockDim.x) {
+    const float* w = wik + (int64_t)o * CD;
+    float acc = 0.f;
+    for (int i = 0; i < CD; i++) acc += crow[i] * w[i];
+    ik[(((int64_t)row * maxBlocks + blk) * Hkv + hk) * HI + o] = acc;
+  }
+}
+void launch_indexer_key_step(const float* ck, const float* wik, float* ik, int rows, int Hkv,
+                             int maxBlocks, int HI, int ratio, int pos, const int* pos_dev,
+                             hipStream_t st) {
+  hipLaunchKernelGGL(indexer_key_step_kernel, dim3(rows * Hkv), dim3(256), 0, st, ck, wik, ik, Hkv,
+                     maxBlocks, HI, ratio, pos, pos_dev);
+  GN_HIP(hipGetLastError());
 }
 
 void launch_hca_decode_compress(const HcaDecodeArgs& a, hipStream_t st) {

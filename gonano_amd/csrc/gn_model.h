@@ -68,6 +68,11 @@ struct DecodeAttnArgs {
   const float* cv = nullptr;
   int maxBlocks = 0;
   int ratio = 0;
+  // sparse selection (ratio > 1): the compressed keys are only the selected
+  // blocks sel[(row*Hkv + hk)*kcap + j], j < nsel[row*Hkv + hk] (<= 256)
+  const int* sel = nullptr;
+  const int* nsel = nullptr;
+  int kcap = 0;
   int nsplit_max;      // set by the launcher: grid.y and the split stride of part
 };
 // Split capacity a part buffer needs for launches with these arguments
@@ -311,6 +316,8 @@ struct HcaCompressArgs {
   float* ck_pf = nullptr;
   float* cv_pf = nullptr;
   float* ring_pf = nullptr;
+  float* tailk_pf = nullptr;  // [B][Hkv][ratio][128] keys/values of that block
+  float* tailv_pf = nullptr;
 };
 void launch_hca_compress(const HcaCompressArgs& a, hipStream_t st);
 void launch_merge_branches(const float* oa, const float* la, const float* ob, const float* lb,
@@ -338,6 +345,13 @@ struct HcaDecodeArgs {
   float* ring;        // [rows][ratio][128] logits of the current block
   const float* kc;    // layer base of the raw caches [rows][Hkv][maxSeq][128]
   const float* vc;
+  // tail mode (CED decoder layers, whose compressed keys/values are not the
+  // raw cache rows): knew/vnew [rows][Hkv][128] enter tail slots
+  // [rows][Hkv][ratio][128] and complete blocks compress from there
+  const float* knew = nullptr;
+  const float* vnew = nullptr;
+  float* tailk = nullptr;
+  float* tailv = nullptr;
   float* ck;          // layer base of the compressed caches [rows][Hkv][maxBlocks][128]
   float* cv;
   int rows, Hkv, ratio, maxSeq, maxBlocks;
@@ -345,6 +359,12 @@ struct HcaDecodeArgs {
   const int* pos_dev;  // when set, read on the device
 };
 void launch_hca_decode_compress(const HcaDecodeArgs& a, hipStream_t st);
+// The indexer key of a block completed at this step (pos % ratio == ratio - 1):
+// ik[row][blk][hk][:] = ck[row][hk][blk][:] . Wik^T, blk = pos / ratio;
+// ck layer base [rows][Hkv][maxBlocks][128], ik [rows][maxBlocks][Hkv][HI].
+void launch_indexer_key_step(const float* ck, const float* wik, float* ik, int rows, int Hkv,
+                             int maxBlocks, int HI, int ratio, int pos, const int* pos_dev,
+                             hipStream_t st);
 
 // ---- flash preset: sparse compressed attention (model/indexer.go) ---------
 // A chunk of sequences [b0, b0 + chunk) of one layer: rows (z, t) with
@@ -354,6 +374,7 @@ struct CsaShape {
   int T, blocks, Hkv, ratio, qoff, b0;
   int ldo;      // row stride of the chunk's score-like matrices (>= blocks)
   int H, dim;   // indexer heads and head dim
+  const int* qoff_dev = nullptr;  // decode: qoff read on the device
 };
 struct IndexerScoreArgs {
   CsaShape shape;

@@ -107,6 +107,12 @@ struct gn_session {
   // [maxBlocks][128] keys and values, [L][rows][ratio][128] logit rings
   float *hck = nullptr, *hcv = nullptr, *hring = nullptr;
   int maxBlocks = 0;
+  // CSA decode: indexer keys [L][rows][maxBlocks][Hkv][HI], per-layer step
+  // selections [L][rows*Hkv][K] (+ counts) and Full layers' candidate pools;
+  // CED decoder layers' tail keys/values [L][rows][Hkv][ratio][128]
+  float* hikc = nullptr;
+  int *dsel = nullptr, *dnsel = nullptr, *dpool = nullptr, *dnpool = nullptr;
+  float *htailk = nullptr, *htailv = nullptr;
   double aux_loss = 0.0;
   int64_t total = 0;
   hipStream_t stream = nullptr;
@@ -567,6 +573,21 @@ struct SeqBuffers {
   std::vector<float*> iq, ik, ced_k, ced_v, ced_krot;
   float* enc = nullptr;
   int qoff = 0;  // position of the first row (CED bounded replay)
+  // partial forwards (CED prefill): layer range [l0, l1) (l1 < 0: all),
+  // given activations and initial residual instead of the embedding, the
+  // final activations out; replay: Full layers use the precomputed group
+  // compressed blocks pre_kc/pre_vc (gblocks of them) instead of compressing
+  int l0 = 0, l1 = -1;
+  const float *x_in = nullptr, *x0_in = nullptr;
+  float* x_out = nullptr;
+  bool replay = false;
+  std::vector<float*> pre_kc, pre_vc;
+  int gblocks = 0;
+  int pf_maxseq = 0;  // prefill raw caches' length (0: T)
+  // prefill: the decode caches to fill (indexer keys [L][G*S][maxBlocks]
+  // [Hkv][HI] of the complete blocks, replicated over S rows per prompt)
+  float* dec_ikc = nullptr;
+  int dec_S = 0, dec_maxBlocks = 0;
   float *xfinal, *fpre, *fn;
   float* backout;
 };
@@ -721,9 +742,12 @@ static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, S
   const int64_t N = sb.N;
   const bool save = mode == SEQ_TRAIN;
   hipStream_t st = s->stream;
-  const int blocks = (int)ceil_div(T, ratio);
+  const int blocks = sb.replay ? sb.gblocks : (int)ceil_div(T, ratio);
   const bool ced = s->split > 0 && l >= s->split;
-  if (ly.mode == 'F') {
+  if (ly.mode == 'F' && sb.replay) {  // the global blocks were filled from the encoder
+    sb.hkc[l] = sb.pre_kc[l];
+    sb.hvc[l] = sb.pre_vc[l];
+  } else if (ly.mode == 'F') {
     const float *hin = sb.h[l], *kin = sb.kn[l], *vin = sb.v[l];
     if (ced) {  // cedGlobalKeyValue (attention.go:156-171) of the encoder hidden state
       float* kv = A<float>(s, "ced_kv", N * 2 * s->KVW);
@@ -768,6 +792,12 @@ static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, S
       sb.nsel[l] = sb.nsel[q];
     } else {
       csa_select_layer(s, sb, ly, l, save, kc, blocks);
+      if (mode == SEQ_PREFILL && sb.dec_ikc && !sb.replay) {  // the decode indexer-key cache
+        const int full = T / ratio;
+        launch_replicate_rows(sb.iq[l] ? sb.ik[l] : nullptr,
+                              sb.dec_ikc + (int64_t)l * B * sb.dec_S * sb.dec_maxBlocks * Hkv * s->HI,
+                              B, sb.dec_S, full, Hkv * s->HI, blocks, sb.dec_maxBlocks, st);
+      }
     }
   }
   float* o = layer_buf(s, "o", l, save, N * Hq * HD);
@@ -807,11 +837,22 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   const int64_t N = sb.N;
   const bool save = mode == SEQ_TRAIN;
   hipStream_t st = s->stream;
-  sb.raw = save ? A<float>(s, "raw", N * C) : nullptr;
-  sb.embn = A<float>(s, "embn", N * C);
-  sb.smsig = A<float>(s, "smsig", std::max<int64_t>((int64_t)B * (T - 1), 1));
-  sb.x0 = A<float>(s, "x0", N * C);
-  launch_embed_smear(sb.ids, s->wte, s->smg, s->sml, B, T, C, sb.raw, sb.embn, sb.smsig, sb.x0, st);
+  float* xcur;
+  if (sb.x_in) {
+    sb.x0 = A<float>(s, "x0", N * C);
+    GN_HIP(hipMemcpyAsync(sb.x0, sb.x0_in, sizeof(float) * N * C, hipMemcpyDeviceToDevice, st));
+    xcur = A<float>(s, "replay_x", N * C);
+    GN_HIP(hipMemcpyAsync(xcur, sb.x_in, sizeof(float) * N * C, hipMemcpyDeviceToDevice, st));
+  } else {
+    sb.raw = save ? A<float>(s, "raw", N * C) : nullptr;
+    sb.embn = A<float>(s, "embn", N * C);
+    sb.smsig = A<float>(s, "smsig", std::max<int64_t>((int64_t)B * (T - 1), 1));
+    sb.x0 = A<float>(s, "x0", N * C);
+    launch_embed_smear(sb.ids, s->wte, s->smg, s->sml, B, T, C, sb.raw, sb.embn, sb.smsig, sb.x0,
+                       st);
+    xcur = sb.x0;
+  }
+  const int l_end = sb.l1 < 0 ? L : sb.l1;
   for (auto* vec : {&sb.xin, &sb.xb, &sb.h, &sb.qrot, &sb.krot, &sb.qn, &sb.kn, &sb.v, &sb.vesig,
                     &sb.o, &sb.lse, &sb.mid, &sb.h2, &sb.u, &sb.act, &sb.xa, &sb.gu, &sb.hkc,
                     &sb.hvc, &sb.hprobs, &sb.iq, &sb.ik, &sb.ced_k, &sb.ced_v, &sb.ced_krot})
@@ -819,10 +860,9 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   for (auto* vec : {&sb.sel, &sb.nsel, &sb.pool, &sb.npool}) vec->assign(L, nullptr);
   sb.moe.assign(L, MoeBuffers{});
   float* qkv = s->mla ? nullptr : A<float>(s, "qkv", N * s->QKVW);
-  float* xcur = sb.x0;
   const int bk = L / 2;
   sb.backout = nullptr;
-  for (int l = 0; l < L; l++) {
+  for (int l = sb.l0; l < l_end; l++) {
     Layer& ly = s->layers[l];
     sb.xin[l] = xcur;
     if (s->split > 0 && l == s->split) {  // encoderHidden (transformer.go:310-312)
@@ -867,7 +907,7 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     qa.qkv = qkv; qa.h = h; qa.ids = sb.ids;
     qa.ve = ly.has_ve ? ly.ve : nullptr; qa.wve = ly.wve;
     qa.cosT = s->cosT; qa.sinT = s->sinT;
-    qa.C = C; qa.Hq = Hq; qa.Hkv = Hkv; qa.R = s->R; qa.T = T; qa.pos0 = 0;
+    qa.C = C; qa.Hq = Hq; qa.Hkv = Hkv; qa.R = s->R; qa.T = T; qa.pos0 = sb.qoff;
     qa.qn = layer_buf(s, "qn", l, save, N * Hq * HD);
     qa.kn = layer_buf(s, "kn", l, save, N * s->KVW);
     qa.vout = layer_buf(s, "v", l, save, N * s->KVW);
@@ -875,9 +915,10 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     qa.krot = save ? layer_buf(s, "krot", l, true, N * s->KVW) : nullptr;
     qa.vesig = (save && ly.has_ve) ? layer_buf(s, "vesig", l, true, N * Hkv) : nullptr;
     if (mode == SEQ_PREFILL) {
-      qa.kcache = kcache_pf + (int64_t)l * B * Hkv * T * HD;
-      qa.vcache = vcache_pf + (int64_t)l * B * Hkv * T * HD;
-      qa.maxSeq = T;
+      const int pm = sb.pf_maxseq > 0 ? sb.pf_maxseq : T;
+      qa.kcache = kcache_pf + (int64_t)l * B * Hkv * pm * HD;
+      qa.vcache = vcache_pf + (int64_t)l * B * Hkv * pm * HD;
+      qa.maxSeq = pm;
       qa.rows_per_seq = 1;
     }
     launch_qkv_post(qa, N, st);
@@ -938,6 +979,8 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     xcur = xout;
   }
   sb.xfinal = xcur;
+  if (sb.x_out) GN_HIP(hipMemcpyAsync(sb.x_out, xcur, sizeof(float) * N * C, hipMemcpyDeviceToDevice, st));
+  if (l_end < L) return;  // a partial forward (CED prefill encoder)
   sb.fpre = A<float>(s, "fpre", N * C);
   sb.fn = A<float>(s, "fn", N * C);
   launch_norm_rows(xcur, sb.backout, s->bkl, N, C, sb.fpre, sb.fn, st);
@@ -1505,6 +1548,93 @@ static void mla_decode_layer(gn_session* s, const Layer& ly, int l, int rows, in
 // One decode forward: tokens dtok at position pos -> logits.  With dpos set
 // the position is read on the device (the step is captured once and
 // replayed).
+// forwardCompressed / forwardCompressedSparse (compress_attention.go:895-1146)
+// for one decode step of layer l: a Full layer buffers the token (on a CED
+// decoder layer its projections of the encoder hidden state) and compresses
+// a completed block (with its indexer key); a Reindex layer caches its own
+// indexer key of the producer's new block; then the selection -- the
+// indexer's top-k (within the Full layer's pool on a Reindex layer, the
+// published one on a Reuse layer) -- and the attention arguments over the
+// group's compressed cache merged with the local window.
+static void hca_decode_layer(gn_session* s, const Layer& ly, int l, int rows, int pos, int maxSeq,
+                             const float* h, const float* enc, const float* kcl, const float* vcl,
+                             const int* dpos, DecodeAttnArgs& da) {
+  const int C = s->C, Hkv = s->Hkv, HI = s->HI, mb = s->maxBlocks;
+  hipStream_t st = s->stream;
+  const int64_t cstride = (int64_t)rows * Hkv * mb * HD;
+  const bool ced = s->split > 0 && l >= s->split;
+  if (ly.mode == 'F') {
+    const float* hin = ced ? enc : h;
+    float* clog = A<float>(s, "dec_clog", (size_t)rows * HD);
+    sgemm(s, linear_fwd_desc(hin, ly.wcl, clog, rows, C, HD));
+    HcaDecodeArgs hd{};
+    hd.clog = clog; hd.bias = ly.cbias;
+    hd.ring = s->hring + (int64_t)l * rows * s->ratio * HD;
+    hd.kc = kcl; hd.vc = vcl;
+    if (ced) {  // the token's global key/value from the encoder hidden state
+      float* kv = A<float>(s, "dec_cedkv", (size_t)rows * 2 * s->KVW);
+      sgemm(s, linear_fwd_desc(enc, ly.wqkv + (int64_t)s->Hq * HD * C, kv, rows, C, 2 * s->KVW));
+      QkvPostArgs qa{};
+      qa.qkv = kv; qa.cosT = s->cosT; qa.sinT = s->sinT;
+      qa.C = C; qa.Hq = 0; qa.Hkv = Hkv; qa.R = s->R; qa.T = 1; qa.pos0 = pos; qa.pos_dev = dpos;
+      qa.kn = A<float>(s, "dec_cedk", (size_t)rows * s->KVW);
+      qa.vout = A<float>(s, "dec_cedv", (size_t)rows * s->KVW);
+      launch_qkv_post(qa, rows, st);
+      const int64_t tw = (int64_t)rows * Hkv * s->ratio * HD;
+      hd.knew = qa.kn; hd.vnew = qa.vout;
+      hd.tailk = s->htailk + (int64_t)l * tw;
+      hd.tailv = s->htailv + (int64_t)l * tw;
+    }
+    hd.ck = s->hck + (int64_t)l * cstride;
+    hd.cv = s->hcv + (int64_t)l * cstride;
+    hd.rows = rows; hd.Hkv = Hkv; hd.ratio = s->ratio; hd.maxSeq = maxSeq;
+    hd.maxBlocks = mb; hd.pos = pos; hd.pos_dev = dpos;
+    launch_hca_decode_compress(hd, st);
+  }
+  const int p = ly.producer;
+  const int64_t ikstride = (int64_t)rows * mb * Hkv * HI;
+  if (ly.has_idx)  // this layer's indexer key of the block completed now
+    launch_indexer_key_step(s->hck + (int64_t)p * cstride, ly.wik, s->hikc + (int64_t)l * ikstride,
+                            rows, Hkv, mb, HI, s->ratio, pos, dpos, st);
+  da.ck = s->hck + (int64_t)p * cstride;
+  da.cv = s->hcv + (int64_t)p * cstride;
+  da.maxBlocks = mb; da.ratio = s->ratio; da.window = s->swa; da.kstart = 0;
+  if (s->topk == 0) return;
+  const int64_t sstride = (int64_t)rows * Hkv;
+  int q = l;  // the layer whose selection this one attends
+  if (ly.mode == 'U')
+    for (q = l - 1; q > p && s->layers[q].mode == 'U'; q--) {
+    }
+  if (ly.mode != 'U') {
+    float* iq = A<float>(s, "dec_iq", (size_t)rows * HI);
+    sgemm(s, linear_fwd_desc(h, ly.wiq, iq, rows, C, HI));
+    CsaShape sh{};
+    sh.T = 1; sh.blocks = mb; sh.Hkv = Hkv; sh.ratio = s->ratio; sh.qoff = pos; sh.b0 = 0;
+    sh.ldo = mb; sh.H = s->ih; sh.dim = s->idim; sh.qoff_dev = dpos;
+    float* scores = A<float>(s, "dec_scores", (size_t)sstride * mb);
+    IndexerScoreArgs ia{};
+    ia.shape = sh; ia.iq = iq; ia.ik = s->hikc + (int64_t)l * ikstride; ia.w = ly.wih; ia.out = scores;
+    launch_indexer_scores(ia, rows, st);
+    CsaSelectArgs ca{};
+    ca.shape = sh; ca.chunk_seqs = rows; ca.scores = scores;
+    ca.K = s->topk; ca.pool = s->ipool; ca.gpt = s->gpt; ca.ccap = s->ccap;
+    if (ly.mode == 'R' && s->ipool > 1) {
+      ca.pool_in = s->dpool + (int64_t)p * sstride * s->ccap;
+      ca.npool_in = s->dnpool + (int64_t)p * sstride;
+    }
+    if (ly.mode == 'F' && s->ipool > 1) {
+      ca.pool_out = s->dpool + (int64_t)l * sstride * s->ccap;
+      ca.npool_out = s->dnpool + (int64_t)l * sstride;
+    }
+    ca.sel = s->dsel + (int64_t)l * sstride * s->topk;
+    ca.nsel = s->dnsel + (int64_t)l * sstride;
+    launch_csa_select(ca, st);
+  }
+  da.sel = s->dsel + (int64_t)q * sstride * s->topk;
+  da.nsel = s->dnsel + (int64_t)q * sstride;
+  da.kcap = s->topk;
+}
+
 static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* dtok, float* kc,
                         float* vc, float* logits, const int* dpos = nullptr) {
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, F = s->F, L = s->L;
@@ -1522,8 +1652,9 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   if (s->hca) {
     DecodeAttnArgs cap{};
     cap.maxSeq = maxSeq; cap.window = s->swa; cap.ratio = s->ratio; cap.maxBlocks = s->maxBlocks;
-    part_splits = decode_attention_split_cap(cap);
+    part_splits = decode_attention_split_cap(cap);  // >= the sparse layout's
   }
+  float* dec_enc = s->split > 0 ? A<float>(s, "dec_enc", (size_t)rows * C) : nullptr;
   float* part = s->mla ? nullptr
                        : A<float>(s, "dec_part", (size_t)rows * Hkv * part_splits *
                                                      (Hq / Hkv) * (HD + 2));
@@ -1531,6 +1662,8 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   const int bk = L / 2;
   for (int l = 0; l < L; l++) {
     Layer& ly = s->layers[l];
+    if (dec_enc && l == s->split)  // encoderHidden (transformer.go:310-312)
+      GN_HIP(hipMemcpyAsync(dec_enc, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
     launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st);
     if (s->mla) {
       mla_decode_layer(s, ly, l, rows, pos, maxSeq, h, kc, vc, x, dpos);
@@ -1557,24 +1690,9 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     da.window = ly.window;
     int64_t nkeys = da.kend - da.kstart;
     if (s->hca) {
-      // forwardCompressed (compress_attention.go:895-1006): compress a
-      // completed block, then attend to the compressed blocks before this
-      // token's block and to the local window
-      float* clog = A<float>(s, "dec_clog", (size_t)rows * HD);
-      sgemm(s, linear_fwd_desc(h, ly.wcl, clog, rows, C, HD));
-      HcaDecodeArgs hd{};
-      hd.clog = clog; hd.bias = ly.cbias;
-      hd.ring = s->hring + (int64_t)l * rows * s->ratio * HD;
-      hd.kc = qa.kcache; hd.vc = qa.vcache;
-      hd.ck = s->hck + (int64_t)l * rows * Hkv * s->maxBlocks * HD;
-      hd.cv = s->hcv + (int64_t)l * rows * Hkv * s->maxBlocks * HD;
-      hd.rows = rows; hd.Hkv = Hkv; hd.ratio = s->ratio; hd.maxSeq = maxSeq;
-      hd.maxBlocks = s->maxBlocks; hd.pos = pos; hd.pos_dev = dpos;
-      launch_hca_decode_compress(hd, st);
-      da.ck = hd.ck; da.cv = hd.cv; da.maxBlocks = s->maxBlocks; da.ratio = s->ratio;
-      da.window = s->swa;
-      da.kstart = 0;
-      nkeys = pos / s->ratio + (s->swa > 0 ? pos - std::max(0, pos - s->swa) + 1 : 0);
+      hca_decode_layer(s, ly, l, rows, pos, maxSeq, h, dec_enc, qa.kcache, qa.vcache, dpos, da);
+      nkeys = (s->topk > 0 ? std::min(s->topk, pos / s->ratio) : pos / s->ratio) +
+              (s->swa > 0 ? pos - std::max(0, pos - s->swa) + 1 : 0);
     }
     if (s->timing && !s->capturing) {
       timed_attention(s, 2.0 * rows * Hkv * HD * 4.0 * nkeys,
@@ -1605,15 +1723,98 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   sgemm(s, linear_fwd_desc(h, s->lm, logits, rows, C, s->V, EPI_SOFTCAP));
 }
 
+// PrefillCED (model/transformer.go:363-449) of G prompts: the encoder over
+// the full prompts (its caches filled as in a plain prefill); every decoder
+// Full layer's compressed blocks, logit ring and tail from its projections of
+// the encoder's final hidden state (Reindex layers' indexer keys of them);
+// then the decoder replayed over the last min(SWA window, P) tokens from the
+// encoder rows with embedAndSmear's smear (the first replayed row is not
+// mixed with the previous token; a lone replayed row is mixed with its own
+// embedding, the cached previous one).  Leaves the replay's final norm in
+// sb.fn and its embeddings in sb.embn; returns the replay length.
+static int prefill_ced(gn_session* s, SeqBuffers& sb, const int32_t* prompts, int G, int P,
+                       float* kpf, float* vpf, float* pf_tailk, float* pf_tailv) {
+  const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, L = s->L, split = s->split, ratio = s->ratio;
+  hipStream_t st = s->stream;
+  const int R = std::min(s->swa, P), rstart = P - R;
+  const int64_t NP = (int64_t)G * P, NR = (int64_t)G * R;
+  // 1) the encoder
+  float* enc = A<float>(s, "cedpf_enc", NP * C);
+  sb.l0 = 0; sb.l1 = split; sb.x_out = enc;
+  seq_forward(s, sb, SEQ_PREFILL, kpf, vpf);
+  // 2) the decoder's global caches
+  const int blocks = (int)ceil_div(P, ratio), full = P / ratio;
+  std::vector<float*> pre_kc(L, nullptr), pre_vc(L, nullptr);
+  float* kv = A<float>(s, "cedpf_kv", NP * 2 * s->KVW);
+  float* kg = A<float>(s, "cedpf_k", NP * s->KVW);
+  float* vg = A<float>(s, "cedpf_v", NP * s->KVW);
+  float* clog = A<float>(s, "cedpf_clog", NP * HD);
+  float* probs = A<float>(s, "cedpf_probs", (size_t)G * blocks * ratio * HD);
+  float* ik = s->topk > 0 ? A<float>(s, "cedpf_ik", (size_t)G * blocks * Hkv * s->HI) : nullptr;
+  for (int l = split; l < L; l++) {
+    const Layer& ly = s->layers[l];
+    if (ly.mode == 'F') {
+      sgemm(s, linear_fwd_desc(enc, ly.wqkv + (int64_t)Hq * HD * C, kv, (int)NP, C, 2 * s->KVW));
+      QkvPostArgs qa{};
+      qa.qkv = kv; qa.cosT = s->cosT; qa.sinT = s->sinT;
+      qa.C = C; qa.Hq = 0; qa.Hkv = Hkv; qa.R = s->R; qa.T = P; qa.pos0 = 0;
+      qa.kn = kg; qa.vout = vg;
+      launch_qkv_post(qa, NP, st);
+      sgemm(s, linear_fwd_desc(enc, ly.wcl, clog, (int)NP, C, HD));
+      HcaCompressArgs ca{};
+      ca.clog = clog; ca.bias = ly.cbias; ca.k = kg; ca.v = vg;
+      ca.B = G; ca.T = P; ca.Hkv = Hkv; ca.ratio = ratio; ca.probs = probs;
+      pre_kc[l] = ca.kc = A<float>(s, "cedpf_kc" + std::to_string(l), (size_t)G * blocks * s->KVW);
+      pre_vc[l] = ca.vc = A<float>(s, "cedpf_vc" + std::to_string(l), (size_t)G * blocks * s->KVW);
+      if (full > 0) {
+        ca.ck_pf = sb.pf_ck + (int64_t)l * G * Hkv * full * HD;
+        ca.cv_pf = sb.pf_cv + (int64_t)l * G * Hkv * full * HD;
+      }
+      ca.ring_pf = sb.pf_ring + (int64_t)l * G * ratio * HD;
+      ca.tailk_pf = pf_tailk + (int64_t)l * G * Hkv * ratio * HD;
+      ca.tailv_pf = pf_tailv + (int64_t)l * G * Hkv * ratio * HD;
+      launch_hca_compress(ca, st);
+    }
+    if (ly.has_idx) {  // compressTail's / cacheReusedIndexerKeys' indexer keys
+      sgemm(s, linear_fwd_desc(pre_kc[ly.producer], ly.wik, ik, G * blocks * Hkv, HD, s->HI));
+      launch_replicate_rows(ik, sb.dec_ikc + (int64_t)l * G * sb.dec_S * sb.dec_maxBlocks * Hkv * s->HI,
+                            G, sb.dec_S, full, Hkv * s->HI, blocks, sb.dec_maxBlocks, st);
+    }
+  }
+  // 3) bounded replay of the decoder
+  SeqBuffers rb;
+  rb.B = G; rb.T = R; rb.N = NR;
+  std::vector<int32_t> rids((size_t)NR);
+  for (int g = 0; g < G; g++)
+    memcpy(rids.data() + (size_t)g * R, prompts + (size_t)g * P + rstart, sizeof(int32_t) * R);
+  rb.ids = upload_ids(s, "cedpf_rids", rids.data(), NR, s->V);
+  float* xr = A<float>(s, "cedpf_xr", NR * C);
+  GN_HIP(hipMemcpy2DAsync(xr, sizeof(float) * R * C, enc + (int64_t)rstart * C, sizeof(float) * P * C,
+                          sizeof(float) * R * C, G, hipMemcpyDeviceToDevice, st));
+  // embedAndSmear of the replayed tokens (transformer.go:452-477)
+  float* embn = A<float>(s, "cedpf_embn", NR * C);
+  float* smsig = A<float>(s, "cedpf_smsig", std::max<int64_t>((int64_t)G * (R - 1), 1));
+  float* x0 = A<float>(s, "cedpf_x0", NR * C);
+  launch_embed_smear(rb.ids, s->wte, s->smg, s->sml, G, R, C, nullptr, embn, smsig, x0, st);
+  if (R == 1) {  // smearDecode with the cached previous embedding: its own
+    float* prev = A<float>(s, "cedpf_prev", NR * C);
+    float* xd = A<float>(s, "cedpf_xd", NR * C);
+    GN_HIP(hipMemcpyAsync(prev, embn, sizeof(float) * NR * C, hipMemcpyDeviceToDevice, st));
+    launch_embed_decode(rb.ids, s->wte, s->smg, s->sml, G, C, prev, xd, x0, st);
+  }
+  rb.qoff = rstart; rb.l0 = split; rb.x_in = xr; rb.x0_in = x0;
+  rb.replay = true; rb.pre_kc = pre_kc; rb.pre_vc = pre_vc; rb.gblocks = blocks;
+  rb.pf_maxseq = P;
+  seq_forward(s, rb, SEQ_PREFILL, kpf, vpf);
+  sb.fn = rb.fn;
+  sb.embn = embn;
+  return R;
+}
+
 static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S, int N,
                      float temperature, int top_k, const uint64_t* seeds, int32_t* rows_out,
                      int32_t* lens_out) {
   GN_CHECK(G > 0 && S > 0 && P > 0 && N >= 0, "generate: bad sizes");
-  if (s->topk > 0 || s->split > 0)
-    throw Error(GN_ERR_UNSUPPORTED, "generate: sparse selection and CED decode are not built yet");
-  for (const Layer& ly : s->layers)
-    if (ly.mode != 'F')
-      throw Error(GN_ERR_UNSUPPORTED, "generate: cross-layer reuse decode is not built yet");
   GN_CHECK(P + N <= s->S * 10, "generate: context exceeds the rotary table");
   GN_CHECK(P <= s->S, "model: sequence longer than rotary cache");
   const int C = s->C, Hkv = s->Hkv, L = s->L, V = s->V;
@@ -1645,27 +1846,54 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   float* vpf = A<float>(s, "pf_v", (size_t)L * G * P * vw);
   const int maxSeq = W;
   const int pfull = s->hca ? P / s->ratio : 0;  // complete blocks of the prompt
-  if (s->hca) {
-    sb.pf_ck = A<float>(s, "pf_hck", (size_t)L * G * Hkv * std::max(pfull, 1) * HD);
-    sb.pf_cv = A<float>(s, "pf_hcv", (size_t)L * G * Hkv * std::max(pfull, 1) * HD);
-    sb.pf_ring = A<float>(s, "pf_ring", (size_t)L * G * s->ratio * HD);
-  }
-  seq_forward(s, sb, SEQ_PREFILL, kpf, vpf);
-  // last-position logits of each prompt, expanded to its S rows (engine.go:182-191)
-  float* lastfn = A<float>(s, "pf_lastfn", (size_t)rows * C);
-  launch_expand_last_rows(sb.fn, lastfn, G, P, S, C, st);
-  float* logits = A<float>(s, "dec_logits", (size_t)rows * V);
-  sgemm(s, linear_fwd_desc(lastfn, s->lm, logits, rows, C, V, EPI_SOFTCAP));
-  // 2) PrefillFrom (kvcache.go:383-448): replicate KV and the smear state
-  float* kc = A<float>(s, "kv_k", (size_t)L * rows * maxSeq * kw);
-  float* vc = A<float>(s, "kv_v", (size_t)L * rows * maxSeq * vw);
-  if (s->hca) {  // compressed caches and logit rings (kvcache.go:142-220, 276-378)
+  float *pf_tailk = nullptr, *pf_tailv = nullptr;
+  if (s->hca) {  // decode caches (kvcache.go:142-220, 276-378)
     s->maxBlocks = maxSeq / s->ratio + 1;
     const size_t cbytes = (size_t)L * rows * Hkv * s->maxBlocks * HD;
     s->hck = A<float>(s, "kv_hck", cbytes);
     s->hcv = A<float>(s, "kv_hcv", cbytes);
     s->hring = A<float>(s, "kv_ring", (size_t)L * rows * s->ratio * HD);
+    if (s->topk > 0) {
+      s->hikc = A<float>(s, "kv_ikc", (size_t)L * rows * s->maxBlocks * Hkv * s->HI);
+      s->dsel = A<int>(s, "dec_sel", (size_t)L * rows * Hkv * s->topk);
+      s->dnsel = A<int>(s, "dec_nsel", (size_t)L * rows * Hkv);
+      s->dpool = A<int>(s, "dec_pool", (size_t)L * rows * Hkv * s->ccap);
+      s->dnpool = A<int>(s, "dec_npool", (size_t)L * rows * Hkv);
+      sb.dec_ikc = s->hikc;
+      sb.dec_S = S;
+      sb.dec_maxBlocks = s->maxBlocks;
+    }
+    if (s->split > 0) {
+      const size_t tw = (size_t)L * rows * Hkv * s->ratio * HD;
+      s->htailk = A<float>(s, "kv_tailk", tw);
+      s->htailv = A<float>(s, "kv_tailv", tw);
+      pf_tailk = A<float>(s, "pf_tailk", (size_t)L * G * Hkv * s->ratio * HD);
+      pf_tailv = A<float>(s, "pf_tailv", (size_t)L * G * Hkv * s->ratio * HD);
+    }
+    sb.pf_ck = A<float>(s, "pf_hck", (size_t)L * G * Hkv * std::max(pfull, 1) * HD);
+    sb.pf_cv = A<float>(s, "pf_hcv", (size_t)L * G * Hkv * std::max(pfull, 1) * HD);
+    sb.pf_ring = A<float>(s, "pf_ring", (size_t)L * G * s->ratio * HD);
+  }
+  int Tlast = P;
+  if (s->split > 0) Tlast = prefill_ced(s, sb, prompts, G, P, kpf, vpf, pf_tailk, pf_tailv);
+  else seq_forward(s, sb, SEQ_PREFILL, kpf, vpf);
+  // last-position logits of each prompt, expanded to its S rows (engine.go:182-191)
+  float* lastfn = A<float>(s, "pf_lastfn", (size_t)rows * C);
+  launch_expand_last_rows(sb.fn, lastfn, G, Tlast, S, C, st);
+  float* logits = A<float>(s, "dec_logits", (size_t)rows * V);
+  sgemm(s, linear_fwd_desc(lastfn, s->lm, logits, rows, C, V, EPI_SOFTCAP));
+  // 2) PrefillFrom (kvcache.go:383-448): replicate KV and the smear state
+  float* kc = A<float>(s, "kv_k", (size_t)L * rows * maxSeq * kw);
+  float* vc = A<float>(s, "kv_v", (size_t)L * rows * maxSeq * vw);
+  if (s->hca) {
     for (int l = 0; l < L; l++) {
+      if (pf_tailk) {
+        const int64_t tw = (int64_t)Hkv * s->ratio * HD;
+        launch_replicate_rows(pf_tailk + (int64_t)l * G * tw, s->htailk + (int64_t)l * rows * tw, G,
+                              S, 1, (int)tw, 1, 1, st);
+        launch_replicate_rows(pf_tailv + (int64_t)l * G * tw, s->htailv + (int64_t)l * rows * tw, G,
+                              S, 1, (int)tw, 1, 1, st);
+      }
       const int64_t dst = (int64_t)l * rows * Hkv * s->maxBlocks * HD;
       const int64_t src = (int64_t)l * G * Hkv * pfull * HD;
       launch_replicate_kv(sb.pf_ck + src, s->hck + dst, G, S, Hkv, pfull, pfull, s->maxBlocks, st);
@@ -1689,7 +1917,7 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
                         G, S, Hkv, P, P, maxSeq, st);
   }
   float* prev = A<float>(s, "dec_prev", (size_t)rows * C);
-  launch_expand_last_rows(sb.embn, prev, G, P, S, C, st);
+  launch_expand_last_rows(sb.embn, prev, G, Tlast, S, C, st);
 
   // 3) decode loop (engine.go:238-325).  Iteration `step` runs the forward
   //    that feeds the previous column (none at step 0: the prefill logits)

@@ -35,7 +35,7 @@ static constexpr int HIMAX = 256;
 // Indexer scores
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int allowed_blocks(int t, const CsaShape& s) {
-  return min(s.blocks, (s.qoff + t) / s.ratio);
+  return min(s.blocks, ((s.qoff_dev ? *s.qoff_dev : s.qoff) + t) / s.ratio);
 }
 
 static constexpr int IHMAX = 8;  // indexer heads

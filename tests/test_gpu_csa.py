@@ -99,3 +99,78 @@ def test_csa_policy_gradient_step_matches_oracle(csa, orc):
     for name, r, c, off in cfg.param_table():
         if "indexer" in name or "compress" in name:
             assert np.any(grads[off:off + r * c]), name
+
+
+def _oracle_rows(orc, cfg, w, prompts, S, N, seeds):
+    m = oracle(orc, cfg, w)
+    out = []
+    for g in range(prompts.shape[0]):
+        out += m.generate_batch(prompts[g], S, N, 1.0, 50, int(seeds[g]))
+    return out
+
+
+def test_csa_rollouts_match_oracle(csa, orc):
+    """Engine.GenerateBatchWith end to end (engine.go:112-369): the prefill
+    (PrefillCED's bounded replay under CED), PrefillFrom, and every decode
+    step's compression, indexer keys, selection and attention; the sampled
+    rows equal the oracle's token for token."""
+    _, cfg, w, s = csa
+    G_, P, S, N = 2, 37, 3, 20
+    prompts = np.random.default_rng(4).integers(0, cfg.vocab_size, (G_, P)).astype(np.int32)
+    seeds = np.array([7, 1000], np.uint64)
+    got = s.generate_batch(prompts, S, N, 1.0, 50, seeds)
+    want = _oracle_rows(orc, cfg, w, prompts, S, N, seeds)
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert np.array_equal(a, b), (i, a[P:].tolist(), b[P:].tolist())
+
+
+def test_csa_decode_graph_matches_eager(csa):
+    _, cfg, w, s = csa
+    prompts = np.random.default_rng(5).integers(0, cfg.vocab_size, (3, 17)).astype(np.int32)
+    seeds = np.array([3, 77, 901], np.uint64)
+    try:
+        s.set_decode_graph(False)
+        eager = s.generate_batch(prompts, 2, 26, 1.0, 50, seeds)
+        s.set_decode_graph(True)
+        for _ in range(2):
+            got = s.generate_batch(prompts, 2, 26, 1.0, 50, seeds)
+            for a, b in zip(got, eager):
+                assert np.array_equal(a, b)
+            s.forward(prompts[:, :5])  # eager work between replays
+    finally:
+        s.set_decode_graph(True)
+
+
+def test_csa_long_rollout_matches_oracle(orc):
+    """A 300-token prompt and 180 decode steps of the hierarchical Full /
+    Reindex / Reuse model: up to 119 compressed blocks per row, pools of 2,
+    selections published and reused across layers while the local window
+    slides."""
+    from gonano_amd.session import Session
+    cfg = csa_cfg("hier_fru")
+    w = G.init_weights(cfg, seed=8, perturb=0.1)
+    prompts = np.random.default_rng(9).integers(0, cfg.vocab_size, (1, 300)).astype(np.int32)
+    seeds = np.array([5], np.uint64)
+    with Session(cfg) as s:
+        s.set_params(w)
+        got = s.generate_batch(prompts, 2, 180, 1.0, 50, seeds)
+    want = _oracle_rows(orc, cfg, w, prompts, 2, 180, seeds)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)
+
+
+def test_ced_bounded_replay_rollout_matches_oracle(orc):
+    """A 150-token prompt under a 64-token window: PrefillCED replays only
+    the last 64 tokens through the decoder (its first replayed row unmixed
+    by the smear), then decodes 40 steps."""
+    from gonano_amd.session import Session
+    cfg = csa_cfg("ced")
+    w = G.init_weights(cfg, seed=12, perturb=0.05)
+    prompts = np.random.default_rng(13).integers(0, cfg.vocab_size, (2, 150)).astype(np.int32)
+    seeds = np.array([21, 22], np.uint64)
+    with Session(cfg) as s:
+        s.set_params(w)
+        got = s.generate_batch(prompts, 2, 40, 1.0, 50, seeds)
+    want = _oracle_rows(orc, cfg, w, prompts, 2, 40, seeds)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)

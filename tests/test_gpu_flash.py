@@ -193,18 +193,3 @@ def test_flash_rl_step_with_moe_matches_oracle(orc):
     assert abs(out["loss"] - wl) <= 1e-4 * max(abs(wl), 1e-3)
     assert abs(aux - m.aux_loss()) <= 1e-6 * abs(m.aux_loss())
     _compare_grads(cfg, grads, wg)
-
-
-def test_unbuilt_flash_decode_is_rejected():
-    """Sparse selection, cross-layer reuse and CED train and run Forward;
-    their rollouts are refused with a clear error until the decode path
-    supports them."""
-    from gonano_amd._lib import HipError
-    from gonano_amd.session import Session
-    for kw in (dict(sparse_topk=4), dict(reuse_pattern="FU"), dict(ced=True, n_layer=2)):
-        cfg = flash_small_cfg()
-        for k, v in kw.items():
-            setattr(cfg, k, v)
-        with Session(cfg) as s:
-            with pytest.raises(HipError, match="not built yet"):
-                s.generate_batch(np.zeros((1, 8), np.int32), 2, 4, 1.0, 50, np.array([1], np.uint64))
