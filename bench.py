@@ -34,6 +34,8 @@ WORKLOADS = {
     "d2": ("dense_d2", 4, 32, 8, 24, 1.0, 0.3),
     # BASELINE configs[3] (the group split is unspecified there: 16 x 16 as d12)
     "latent_d12": ("latent_d12", 16, 256, 16, 256, 1.0, 0.3),
+    # 64 rollouts (4 groups x 16) of 8192-token prompts + 512 new tokens
+    "flash_d12": ("flash_d12", 4, 8192, 16, 512, 1.0, 0.3),
 }
 
 

@@ -325,6 +325,43 @@ def enable_moe(cfg: Config, n_experts: int = 0, experts_per_token: int = 0,
     return cfg
 
 
+def apply_flash_preset(cfg: Config, sparse_topk: int = 0, swa_window: int = 0,
+                       n_experts: int = 0, experts_per_token: int = 0, expert_hidden: int = 0,
+                       shared_hidden: int = 0, balance_weight: float = 0.0) -> Config:
+    """Config.ApplyPreset(PresetFlash) (model/preset.go:93-118) with the
+    MoE defaults resolved: compression ratio 4, SparseTopK 8, IndexerPool 8,
+    ReusePattern "FRU", SWAWindow 128 and CED (with >= 2 layers) unless the
+    caller set them, then the DeepSeekMoE feed-forward."""
+    if cfg.n_kv_head == cfg.n_head and cfg.n_head % 2 == 0:  # applyDefaultGroupedQuery
+        cfg.n_kv_head = cfg.n_head // 2
+    if cfg.compression <= 1:
+        cfg.compression_ratio = 4
+    cfg.sparse_topk = sparse_topk if sparse_topk > 0 else (cfg.sparse_topk or 8)
+    if cfg.indexer_pool <= 1:
+        cfg.indexer_pool = 8
+    if not cfg.reuse_pattern:
+        cfg.reuse_pattern = "FRU"
+    if swa_window > 0:
+        cfg.swa_window = swa_window
+    elif cfg.swa_window <= 0:
+        cfg.swa_window = 128
+    if cfg.n_layer >= 2:
+        cfg.ced = True
+    return enable_moe(cfg, n_experts, experts_per_token, expert_hidden, shared_hidden, 0.0,
+                      balance_weight)
+
+
+def flash_d12() -> Config:
+    """flash preset depth 12 (d_model 768, 6 query heads,
+    one KV head), compression 4, top-16 sparse selection (pool 8, 128
+    candidates, indexer 64 x 1 head), SWA window 512, FRU reuse, CED split at
+    layer 6, DeepSeekMoE 1 shared + 16 routed experts of hidden 768, top-2;
+    SequenceLen 16384 so 8192-token prompts + 512 new tokens fit."""
+    cfg = config_for_depth_ratio(12, 65536, 64, 128, 16384, "SSSL", 1)
+    cfg.n_kv_head = 1
+    return apply_flash_preset(cfg, sparse_topk=16, swa_window=512, n_experts=16)
+
+
 def latent_d12() -> Config:
     """latent preset depth 12 (d_model 768, 6 query heads,
     3 KV heads by the preset's grouped-query default), absorbed MLA with

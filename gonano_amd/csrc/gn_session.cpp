@@ -12,6 +12,7 @@
 #include <array>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -113,6 +114,9 @@ struct gn_session {
   float* hikc = nullptr;
   int *dsel = nullptr, *dnsel = nullptr, *dpool = nullptr, *dnpool = nullptr;
   float *htailk = nullptr, *htailv = nullptr;
+  // sequences of the whole policy-gradient batch when it runs in micro-batches
+  // (the balance loss averages over every sequence); 0: the batch itself
+  int bal_batch = 0;
   double aux_loss = 0.0;
   int64_t total = 0;
   hipStream_t stream = nullptr;
@@ -1063,7 +1067,8 @@ static void moe_ffn_backward(gn_session* s, const Layer& ly, const MoeBuffers& m
     launch_moe_balance(m.probs, m.sel, B, T, E, K, cnt, lseq, st);
     if (dauxl) launch_sum_f64(lseq, B, dauxl, true, st);
     rb.bal_cnt = cnt;
-    rb.bal_coef = (double)s->bw / ((double)B * T) * ((double)E / ((double)K * T));
+    const int Bs = s->bal_batch > 0 ? s->bal_batch : B;
+    rb.bal_coef = (double)s->bw / ((double)Bs * T) * ((double)E / ((double)K * T));
   }
   float* glog = A<float>(s, "moe_glog", N * E);
   rb.probs = m.probs; rb.sel = m.sel; rb.inv = m.inv; rb.dotp = dotp; rb.rows = N;
@@ -1297,8 +1302,8 @@ static void hca_backward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, 
   sgemm(s, linear_dx_desc(dkv, ly.wqkv + kvoff, genc, (int)N, C, 2 * s->KVW, EPI_ACCUM));
 }
 
-static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets, int B, int T,
-                    const float* adv, float norm, float* loss_out, float* nll_out) {
+static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* targets, int B,
+                          int T, const float* adv, float norm, double* loss_out, float* nll_out) {
   GN_CHECK(B > 0 && T > 1, "policy gradient step: need batch > 0 and seq_len > 1");
   GN_CHECK(T <= s->S, "model: sequence longer than rotary cache");
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, F = s->F, L = s->L, V = s->V;
@@ -1454,7 +1459,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
   if (nll_out) GN_HIP(hipMemcpyAsync(nll_out, nll, sizeof(float) * N, hipMemcpyDeviceToHost, st));
   if (s->timing) GN_HIP(hipEventRecord(ev1, st));
   GN_HIP(hipStreamSynchronize(st));
-  if (loss_out) *loss_out = (float)loss;
+  if (loss_out) *loss_out = loss;
   // moe.go:313: weight * sum over sequences / sequences, summed over layers
   s->aux_loss = dauxl ? (double)s->bw * aux / (double)B : 0.0;
   if (s->timing) {
@@ -1465,6 +1470,55 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
     double am = 0, ab = 0;
     int64_t an = 0;
     collect_timing(s, &s->t.gemm_ms, &s->t.gemm_flops, &s->t.gemm_launches, &am, &ab, &an);
+  }
+}
+
+// Sequences per micro-batch of the policy-gradient step: the saved
+// activations of one micro-batch stay within 160 GB (an estimate per token
+// of every layer's saved tensors).  The loss, the NLL and the gradients are
+// sums over sequences, so micro-batching changes only the float summation
+// order (the balance loss keeps the whole batch's sequence count).
+static int pg_micro_batch(gn_session* s, int B, int T) {
+  const int64_t C = s->C;
+  const int64_t per_layer = 10 * C + 3 * (int64_t)s->Hq * HD + 6 * (int64_t)s->KVW +
+                            3 * (int64_t)s->F +
+                            (s->moe ? (int64_t)s->K * (2 * C + 3 * (int64_t)s->EH) + 2 * s->E : 0) +
+                            (s->hca ? 4 * HD : 0);
+  const int64_t per_tok = s->L * per_layer + 16 * C;
+  const int64_t budget = (int64_t)160 << 30;
+  int64_t mb = std::max<int64_t>(1, std::min<int64_t>(B, budget / (4 * per_tok * T)));
+  if (const char* e = getenv("GN_PG_MICRO_BATCH"))  // a smaller cap (tests)
+    mb = std::min<int64_t>(mb, std::max(1, atoi(e)));
+  return (int)mb;
+}
+
+// trainer.PolicyGradientStep (trainer/rl.go:14-60) over the batch, in
+// micro-batches of sequences when it is too large for one pass.
+static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets, int B, int T,
+                    const float* adv, float norm, float* loss_out, float* nll_out) {
+  const int mb = pg_micro_batch(s, B, T);
+  double loss = 0, aux = 0, tms = 0, gms = 0, gfl = 0;
+  int64_t gn = 0;
+  s->bal_batch = B;
+  try {
+    for (int b0 = 0; b0 < B; b0 += mb) {
+      const int nb = std::min(mb, B - b0);
+      double l = 0;
+      pg_step_chunk(s, inputs + (int64_t)b0 * T, targets + (int64_t)b0 * T, nb, T, adv + b0, norm,
+                    &l, nll_out ? nll_out + (int64_t)b0 * T : nullptr);
+      loss += l;
+      aux += s->aux_loss * nb;
+      tms += s->t.train_ms; gms += s->t.gemm_ms; gfl += s->t.gemm_flops; gn += s->t.gemm_launches;
+    }
+  } catch (...) {
+    s->bal_batch = 0;
+    throw;
+  }
+  s->bal_batch = 0;
+  if (loss_out) *loss_out = (float)loss;
+  s->aux_loss = aux / B;
+  if (s->timing) {
+    s->t.train_ms = tms; s->t.gemm_ms = gms; s->t.gemm_flops = gfl; s->t.gemm_launches = gn;
   }
 }
 

@@ -5,6 +5,11 @@ import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+# Under pytest-xdist every worker loads the OpenMP oracle: one thread each,
+# or the workers' spinning thread teams oversubscribe the cores and the
+# oracle's many short parallel regions slow down a hundredfold.
+if os.environ.get("PYTEST_XDIST_WORKER"):
+    os.environ.setdefault("OMP_NUM_THREADS", "1")
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
