@@ -47,31 +47,55 @@ def cpu_baseline(cfg, w, prompts, S: int, N: int, temp: float) -> dict:
     """The oracle (a scalar C port of the reference's arithmetic, float64
     accumulation, OpenMP over rows) generating rollouts on the same weights.
 
-    Bounded sample: ONE prompt group of the workload (its full prompt, all
-    S samples), timed once with 1 new token (prefill) and once with
-    1 + STEPS new tokens; the difference gives the cost of one batched decode
-    step.  The reported rate is the workload's per-group token count over
-    the time one group would take, prefill + N decode steps, so it is in the
-    same unit and the same prefill/decode mix as the GPU's value."""
+    Bounded sample: ONE prompt group of the workload (all S samples), timed
+    once with 1 new token (prefill) and once with 1 + STEPS new tokens; the
+    difference gives the cost of one batched decode step.  The reported rate
+    is the workload's per-group token count over the time one group would
+    take, prefill + N decode steps, so it is in the same unit and the same
+    prefill/decode mix as the GPU's value.
+
+    Prompts longer than PREFIX (the flash workload's 8192 tokens, ~100 s of
+    oracle prefill) are sampled on their first PREFIX tokens and the
+    prefill time is scaled by layer-tokens: every layer reads every prompt
+    token, except a CED decoder layer, which replays only the last
+    min(window, P) tokens (PrefillCED, model/transformer.go:363-449).  The
+    per-token cost is taken as constant (the indexer's quadratic score term
+    is ~8 % of a layer-token at P = 8192), so the scaled prefill is a slight
+    underestimate and the CPU rate a slight overestimate."""
     from oracle import oracle as O
-    STEPS = 128  # about 15 s of CPU work on the GPU box's 16 host threads
-    m = O.OracleModel(O.ModelShape.from_config(cfg), w)
     P = prompts.shape[1]
+    PREFIX = 1024
+    Ps = min(P, PREFIX)
+    STEPS = 128 if Ps == P else 8  # about 15 s of CPU work on 16 host threads
+    m = O.OracleModel(O.ModelShape.from_config(cfg), w)
+
+    def layer_tokens(p):
+        split = cfg.ced_split
+        if split <= 0:
+            return cfg.n_layer * p
+        return split * p + (cfg.n_layer - split) * min(cfg.swa_window or p, p)
+
+    prompt = prompts[0, :Ps]
     t0 = time.perf_counter()
-    m.generate_batch(prompts[0], S, 1, temp, 50, 0)
+    m.generate_batch(prompt, S, 1, temp, 50, 0)
     t_prefill = time.perf_counter() - t0
     t0 = time.perf_counter()
-    rows = m.generate_batch(prompts[0], S, 1 + STEPS, temp, 50, 0)
+    rows = m.generate_batch(prompt, S, 1 + STEPS, temp, 50, 0)
     t_long = time.perf_counter() - t0
-    steps = max(1, max(len(r) for r in rows) - P - 1)
+    steps = max(1, max(len(r) for r in rows) - Ps - 1)
     t_step = max(t_long - t_prefill, 1e-9) / steps
-    group_s = t_prefill + N * t_step
+    scale = layer_tokens(P) / layer_tokens(Ps)
+    group_s = t_prefill * scale + N * t_step
+    sample = (f"oracle rollout of 1 prompt group ({Ps} prompt tokens x {S} samples) on the "
+              f"same weights: prefill {t_prefill:.2f} s, {steps} batched decode steps "
+              f"{t_long - t_prefill:.2f} s")
+    if Ps < P:
+        sample += (f"; prefill scaled to the {P}-token prompt by layer-tokens "
+                   f"(x{scale:.3f} = {t_prefill * scale:.1f} s)")
     return {"value": round(S * N / group_s, 2), "unit": "tokens/s",
             "cores": int(O.lib().orc_num_threads()), "kind": "port",
-            "sample": f"oracle rollout of 1 prompt group ({P} prompt tokens x {S} samples) on "
-                      f"the same weights: prefill {t_prefill:.2f} s, {steps} batched decode "
-                      f"steps {t_long - t_prefill:.2f} s; value = {S}x{N} tokens / "
-                      f"(prefill + {N} steps) = one group of the workload"}
+            "sample": sample + f"; value = {S}x{N} tokens / (prefill + {N} steps) = one "
+                               f"group of the workload"}
 
 
 def main() -> int:
@@ -183,10 +207,15 @@ def main() -> int:
             "workload": f"{args.config} RL step: {groups} prompts x {S} samples, "
                         f"{P} prompt + {N} new tokens, T={temp}, top-k 50, "
                         f"Bernoulli({reward_p}) rewards, recompute + PG fwd/bwd, no optimizer",
-            "model": (f"{'latent' if cfg.mla else 'dense'} depth {cfg.n_layer} d_model "
+            "model": (f"{'flash' if cfg.compression_ratio else 'latent' if cfg.mla else 'dense'}"
+                      f" depth {cfg.n_layer} d_model "
                       f"{cfg.n_embd} heads {cfg.n_head}/{cfg.n_kv_head} vocab {cfg.vocab_size}"
                       + (f" MLA latent {cfg.mla_latent} rope {cfg.mla_rope_dimension}"
                          if cfg.mla else "")
+                      + (f" HCA ratio {cfg.compression_ratio} SWA {cfg.swa_window}"
+                         f" CSA top-{cfg.sparse_topk} pool {cfg.indexer_pool}"
+                         f" FRU {cfg.reuse_pattern}{' CED' if cfg.ced else ''}"
+                         if cfg.compression_ratio else "")
                       + (f" MoE 1 shared + {cfg.n_experts} routed x {cfg.expert_hidden}, "
                          f"top-{cfg.experts_per_token}" if cfg.moe else "")),
             "rollouts": groups * S, "global_batch": groups * S, "seq_len": P + N,
