@@ -158,10 +158,20 @@ int gn_attention_combine(const float *const *accumulators, const float *const *m
  * blocks before their own) merged with a sliding-window local branch of
  * swa_window keys (Config.SWAWindowSize(); 0: none).  sparse_topk,
  * indexer_dim, indexer_heads, indexer_pool, indexer_candidates,
- * indexer_weight (the CSA lightning indexer), reuse_pattern (FRU cross-layer
- * reuse, e.g. "FRU") and ced (encoder/decoder prefill) are carried with the
- * reference's meaning; gn_session_create rejects non-zero values of them
- * with GN_ERR_UNSUPPORTED until the session implements them. */
+ * indexer_weight (the CSA lightning indexer: top-k compressed blocks per
+ * query, hierarchical over groups of indexer_pool blocks within a budget of
+ * indexer_candidates, trained by its distillation loss of weight
+ * indexer_weight), reuse_pattern (FRU cross-layer reuse, e.g. "FRU") and
+ * ced (the causal encoder-decoder split at n_layer / 2) take the
+ * reference's resolved values (Config.Compression, SWAWindowSize,
+ * SparseTopK, indexerDefaults, IndexerPool, IndexerCandidateBudget,
+ * IndexerWeight, ReusePattern, CEDEnabled; model/config.go:282-420).
+ * compression_ratio 0 turns the preset off; zero indexer_dim,
+ * indexer_heads, indexer_candidates and indexer_weight take the reference's
+ * defaults (64, 1, max(8 * sparse_topk, 64), 1).  gn_session_create returns
+ * a non-zero status for the combinations Config.Validate rejects and for
+ * shapes the kernels do not cover (ratio 2..8 or 16, top-k <= 64, indexer
+ * heads * dim <= 256). */
 typedef struct gn_config {
   int32_t sequence_len;
   int32_t vocab_size;
