@@ -523,13 +523,19 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
                                                                      vec, st);
         return;
       }
-      // Small groups (decode: tens of rows per expert) stream each expert's
-      // weights once; split K so that enough workgroups keep loads in flight
-      // (about 2 per CU), summed by gemm_reduce_kernel.
-      const int64_t tiles = (ceil_div(d.M, 64) + d.groups) * ceil_div(d.N, 64);
+      // Small groups (decode: a few to tens of rows per expert) stream each
+      // expert's weights once; split K so that enough workgroups keep loads
+      // in flight, summed by gemm_reduce_kernel.  Tile rows follow the
+      // average group: 16 or 32 rows with 2-wave workgroups (about 4 per
+      // CU) when groups are that small, else 64 rows with 8 waves (about 2
+      // per CU) -- taller tiles would multiply mostly padding rows.
+      const int64_t avg = ceil_div(d.M, d.groups);
+      const int bm = avg <= 16 ? 16 : avg <= 32 ? 32 : 64;
+      const int64_t want = bm < 64 ? 4 * 256 : 2 * 256;
+      const int64_t tiles = (ceil_div(d.M, bm) + d.groups) * ceil_div(d.N, 64);
       int splits = 1;
-      if (tiles < 2 * 256 && d.K >= 256)
-        splits = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(2 * 256, tiles), d.K / 128));
+      if (tiles < want && d.K >= 256)
+        splits = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(want, tiles), d.K / 128));
       const int kps = (int)ceil_div(ceil_div(d.K, splits), GK) * GK;
       splits = (int)ceil_div(d.K, kps);
       p.k_per_split = kps;
@@ -538,8 +544,15 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
         GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
         p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
       }
-      launch_grouped<64, 64, 2, 2, 2, 4, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig, vec,
-                                                                 st);
+      if (bm == 16)
+        launch_grouped<16, 64, 1, 2, 1, 4, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig, vec,
+                                                                   st);
+      else if (bm == 32)
+        launch_grouped<32, 64, 1, 2, 1, 4, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig, vec,
+                                                                   st);
+      else
+        launch_grouped<64, 64, 2, 2, 2, 4, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig, vec,
+                                                                   st);
       if (splits > 1) {
         const int64_t total = (int64_t)d.M * d.N;
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,

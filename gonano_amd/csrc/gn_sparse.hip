@@ -27,6 +27,7 @@
 
 namespace gn {
 
+typedef float v4f __attribute__((ext_vector_type(4)));
 static constexpr int SD = 128;   // head dim
 static constexpr int ST = 16;    // score tile
 static constexpr int HIMAX = 256;
@@ -103,10 +104,71 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerScoreArgs a)
   if (ok) a.out[((int64_t)z * sh.T + t) * sh.ldo + s] = total;
 }
 
+// Decode scores (one query per row, T == 1): the row's keys are streamed
+// once, coalesced.  LK = H * dim / 4 lanes share a key, each holding 4
+// channels of one head (dim % 4 == 0): the per-head dot is summed over the
+// head's dim / 4 lanes, ReLU-weighted by its lane 0, and the heads are
+// summed over the key's lanes.  A block covers DEC_IT * 256 / LK keys, every
+// thread's DEC_IT loads in flight at once.
+static constexpr int DEC_IT = 8;
+template <int LK>
+__global__ __launch_bounds__(256) void indexer_scores_decode_kernel(IndexerScoreArgs a) {
+  constexpr int KPI = 256 / LK;  // keys per block iteration
+  const CsaShape& sh = a.shape;
+  const int tid = threadIdx.x, kl = tid % LK, ks = tid / LK;
+  const int z = blockIdx.y, b = sh.b0 + z / sh.Hkv, hh = z % sh.Hkv;
+  const int allowed = allowed_blocks(0, sh);
+  const int s0 = blockIdx.x * (DEC_IT * KPI);
+  if (s0 >= allowed) return;  // past the causal limit: never read
+  const int seg = sh.dim / 4;  // lanes per head
+  const v4f q = *reinterpret_cast<const v4f*>(a.iq + (int64_t)b * (LK * 4) + 4 * kl);
+  const float wh = a.w[(4 * kl) / sh.dim];
+  const v4f* kb = reinterpret_cast<const v4f*>(a.ik + ((int64_t)b * sh.blocks * sh.Hkv + hh) * (LK * 4)) + kl;
+  const int64_t kstride = (int64_t)sh.Hkv * LK;  // float4 per block key
+  v4f kv[DEC_IT];
+#pragma unroll
+  for (int i = 0; i < DEC_IT; i++) {
+    const int s = s0 + ks + i * KPI;
+    kv[i] = s < allowed ? kb[s * kstride] : (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int i = 0; i < DEC_IT; i++) {
+    const int s = s0 + ks + i * KPI;
+    float d = q[0] * kv[i][0] + q[1] * kv[i][1] + q[2] * kv[i][2] + q[3] * kv[i][3];
+    for (int o = 1; o < seg; o <<= 1) d += __shfl_xor(d, o, 64);
+    float v = (kl % seg == 0 && d > 0.f) ? wh * d : 0.f;
+    for (int o = seg; o < LK; o <<= 1) v += __shfl_xor(v, o, 64);
+    if (kl == 0 && s < allowed) a.out[(int64_t)z * sh.ldo + s] = v;
+  }
+}
+
+template <int LK>
+static void run_scores_decode(const IndexerScoreArgs& a, int chunk_seqs, hipStream_t st) {
+  const int per = DEC_IT * (256 / LK);
+  hipLaunchKernelGGL(indexer_scores_decode_kernel<LK>,
+                     dim3((unsigned)ceil_div(a.shape.ldo, per), (unsigned)(chunk_seqs * a.shape.Hkv)),
+                     dim3(256), 0, st, a);
+}
+
 void launch_indexer_scores(const IndexerScoreArgs& a, int chunk_seqs, hipStream_t st) {
   const CsaShape& s = a.shape;
   GN_CHECK(s.H * s.dim <= HIMAX && s.H <= IHMAX, "indexer: heads * dim must be <= 256, heads <= 8");
   GN_CHECK(s.ldo >= s.blocks, "indexer: score row stride below the block count");
+  const int seg = s.dim / 4, LK = s.H * s.dim / 4;
+  if (s.T == 1 && !a.mask_out && s.dim % 4 == 0 && seg > 0 && (seg & (seg - 1)) == 0 &&
+      (LK & (LK - 1)) == 0) {
+    switch (LK) {  // LK = H * dim / 4 <= 64, a power of two
+      case 1: run_scores_decode<1>(a, chunk_seqs, st); break;
+      case 2: run_scores_decode<2>(a, chunk_seqs, st); break;
+      case 4: run_scores_decode<4>(a, chunk_seqs, st); break;
+      case 8: run_scores_decode<8>(a, chunk_seqs, st); break;
+      case 16: run_scores_decode<16>(a, chunk_seqs, st); break;
+      case 32: run_scores_decode<32>(a, chunk_seqs, st); break;
+      case 64: run_scores_decode<64>(a, chunk_seqs, st); break;
+    }
+    GN_HIP(hipGetLastError());
+    return;
+  }
   dim3 grid((unsigned)ceil_div(s.ldo, ST), (unsigned)ceil_div(s.T, ST), (unsigned)(chunk_seqs * s.Hkv));
   hipLaunchKernelGGL(indexer_scores_kernel, grid, dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
@@ -142,7 +204,41 @@ __device__ __forceinline__ void wave_best(float& v, int& i) {
 }
 // n values in LDS (NaN marks taken entries, which never outrank): take the
 // best `count` in rank order into out[].  All lanes return the same count.
+// Up to 64 * TOPK_M values: every lane ranks its values against all n at
+// once -- rank(i) = #{j : (v_j, j) outranks (v_i, i)}, a strict total order,
+// so the ranks are distinct and rank r goes to out[r] -- one pass over the
+// LDS (broadcast reads) instead of `count` rounds of wave-wide argmax.
+static constexpr int TOPK_M = 8;
+__device__ int wave_topk_iter(float* vals, int n, int count, int* out);
 __device__ int wave_topk(float* vals, int n, int count, int* out) {
+  if (n > 64 * TOPK_M) return wave_topk_iter(vals, n, count, out);
+  const int lane = threadIdx.x & 63;
+  float v[TOPK_M];
+  int r[TOPK_M];
+  int mine = 0;
+#pragma unroll
+  for (int m = 0; m < TOPK_M; m++) {
+    const int i = lane + 64 * m;
+    v[m] = i < n ? vals[i] : __builtin_nanf("");
+    r[m] = 0;
+    mine += i < n && v[m] == v[m];
+  }
+#pragma unroll 8
+  for (int j = 0; j < n; j++) {
+    const float vj = vals[j];
+#pragma unroll
+    for (int m = 0; m < TOPK_M; m++) r[m] += outranks(vj, j, v[m], lane + 64 * m);
+  }
+#pragma unroll
+  for (int m = 0; m < TOPK_M; m++)
+    if (v[m] == v[m] && r[m] < count) out[r[m]] = lane + 64 * m;
+  wave_sync();
+  int valid = mine;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) valid += __shfl_xor(valid, o, 64);
+  return min(count, valid);
+}
+__device__ int wave_topk_iter(float* vals, int n, int count, int* out) {
   const int lane = threadIdx.x & 63;
   int got = 0;
   for (int r = 0; r < count && r < n; r++) {
@@ -194,13 +290,14 @@ __global__ __launch_bounds__(256) void csa_select_kernel(CsaSelectArgs a) {
   if (a.pool_in) {  // Reindex: the fine stage within the producer's pool
     const int np = a.npool_in[grow];
     const int* pl = a.pool_in + grow * a.ccap;
-    if (lane == 0) {
-      for (int i = 0; i < np; i++) {
-        const int e = pl[i];
-        if (e >= 0 && e < allowed) cand[nc++] = e;
-      }
+    for (int i0 = 0; i0 < np; i0 += 64) {  // the pool's allowed entries, in order
+      const int i = i0 + lane;
+      const int e = i < np ? pl[i] : -1;
+      const bool ok = e >= 0 && e < allowed;
+      const uint64_t m = __ballot(ok);
+      if (ok) cand[nc + __popcll(m & ((1ull << lane) - 1))] = e;
+      nc += __popcll(m);
     }
-    nc = __shfl(nc, 0, 64);
   } else if (a.pool == 1 && a.gpt >= a.K) {
     // flat: the top-K of the top-budget entries are the top-K entries
     for (int j = lane; j < allowed; j += 64) vals[j] = score[j];
@@ -213,21 +310,41 @@ __global__ __launch_bounds__(256) void csa_select_kernel(CsaSelectArgs a) {
     return;
   } else {
     const int ag = (allowed + a.pool - 1) / a.pool;
-    for (int g = lane; g < ag; g += 64) {  // IndexerBlockMax over the allowed entries
-      const int st = g * a.pool, en = min(st + a.pool, allowed);
-      float mx = -INFINITY;
-      for (int e = st; e < en; e++) mx = fmaxf(mx, score[e]);
-      vals[g] = mx;
+    if (a.pool <= 64 && (a.pool & (a.pool - 1)) == 0) {
+      // IndexerBlockMax over the allowed entries, coalesced: lane j of a
+      // 256-entry stretch reads entry j, a group is `pool` adjacent lanes
+      for (int j0 = 0; j0 < allowed; j0 += 256) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int j = j0 + 64 * u + lane;
+          v[u] = j < allowed ? score[j] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int j = j0 + 64 * u + lane;
+          for (int o = 1; o < a.pool; o <<= 1) v[u] = fmaxf(v[u], __shfl_xor(v[u], o, 64));
+          if ((lane & (a.pool - 1)) == 0 && j < allowed) vals[j / a.pool] = v[u];
+        }
+      }
+    } else {
+      for (int g = lane; g < ag; g += 64) {  // IndexerBlockMax over the allowed entries
+        const int st = g * a.pool, en = min(st + a.pool, allowed);
+        float mx = -INFINITY;
+        for (int e = st; e < en; e++) mx = fmaxf(mx, score[e]);
+        vals[g] = mx;
+      }
     }
     wave_sync();
     const int ng = wave_topk(vals, ag, a.gpt, rank);
-    if (lane == 0) {
-      for (int r = 0; r < ng; r++) {
-        const int st = rank[r] * a.pool, en = min(st + a.pool, allowed);
-        for (int e = st; e < en; e++) cand[nc++] = e;
-      }
+    for (int i0 = 0; i0 < ng * a.pool; i0 += 64) {  // the chosen groups' allowed entries
+      const int i = i0 + lane;
+      const int e = i < ng * a.pool ? rank[i / a.pool] * a.pool + i % a.pool : allowed;
+      const bool ok = e < allowed;
+      const uint64_t m = __ballot(ok);
+      if (ok) cand[nc + __popcll(m & ((1ull << lane) - 1))] = e;
+      nc += __popcll(m);
     }
-    nc = __shfl(nc, 0, 64);
   }
   wave_sync();
   if (a.pool_out) {
