@@ -204,39 +204,62 @@ __device__ __forceinline__ void wave_best(float& v, int& i) {
 }
 // n values in LDS (NaN marks taken entries, which never outrank): take the
 // best `count` in rank order into out[].  All lanes return the same count.
-// Up to 64 * TOPK_M values: every lane ranks its values against all n at
-// once -- rank(i) = #{j : (v_j, j) outranks (v_i, i)}, a strict total order,
-// so the ranks are distinct and rank r goes to out[r] -- one pass over the
-// LDS (broadcast reads) instead of `count` rounds of wave-wide argmax.
-static constexpr int TOPK_M = 8;
-__device__ int wave_topk_iter(float* vals, int n, int count, int* out);
-__device__ int wave_topk(float* vals, int n, int count, int* out) {
-  if (n > 64 * TOPK_M) return wave_topk_iter(vals, n, count, out);
+// Up to 64 * 8 values: every lane ranks its M = ceil(n / 64) values against
+// all n at once -- rank(i) = #{j : (v_j, j) outranks (v_i, i)}, a strict
+// total order, so the ranks are distinct and rank r goes to out[r] -- one
+// pass over the LDS (broadcast reads) instead of `count` rounds of
+// wave-wide argmax.  The order is compared as one 64-bit key: the float
+// mapped to an order-preserving unsigned (-0 as +0, so the zeros tie as in
+// a float compare) above the complemented index; NaN maps to key 0, which
+// outranks nothing.
+__device__ __forceinline__ uint64_t rank_key(float v, int i) {
+  if (v != v) return 0;
+  uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+template <int M>
+__device__ int wave_topk_rank(const float* vals, int n, int count, int* out) {
   const int lane = threadIdx.x & 63;
-  float v[TOPK_M];
-  int r[TOPK_M];
+  uint64_t key[M];
+  int r[M];
   int mine = 0;
 #pragma unroll
-  for (int m = 0; m < TOPK_M; m++) {
+  for (int m = 0; m < M; m++) {
     const int i = lane + 64 * m;
-    v[m] = i < n ? vals[i] : __builtin_nanf("");
+    key[m] = i < n ? rank_key(vals[i], i) : 0;
     r[m] = 0;
-    mine += i < n && v[m] == v[m];
+    mine += key[m] != 0;
   }
-#pragma unroll 8
+#pragma unroll 4
   for (int j = 0; j < n; j++) {
-    const float vj = vals[j];
+    const uint64_t kj = rank_key(vals[j], j);
 #pragma unroll
-    for (int m = 0; m < TOPK_M; m++) r[m] += outranks(vj, j, v[m], lane + 64 * m);
+    for (int m = 0; m < M; m++) r[m] += kj > key[m];
   }
 #pragma unroll
-  for (int m = 0; m < TOPK_M; m++)
-    if (v[m] == v[m] && r[m] < count) out[r[m]] = lane + 64 * m;
+  for (int m = 0; m < M; m++)
+    if (key[m] != 0 && r[m] < count) out[r[m]] = lane + 64 * m;
   wave_sync();
   int valid = mine;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) valid += __shfl_xor(valid, o, 64);
   return min(count, valid);
+}
+__device__ int wave_topk_iter(float* vals, int n, int count, int* out);
+__device__ int wave_topk(float* vals, int n, int count, int* out) {
+  switch ((n + 63) / 64) {
+    case 0:
+    case 1: return wave_topk_rank<1>(vals, n, count, out);
+    case 2: return wave_topk_rank<2>(vals, n, count, out);
+    case 3: return wave_topk_rank<3>(vals, n, count, out);
+    case 4: return wave_topk_rank<4>(vals, n, count, out);
+    case 5: return wave_topk_rank<5>(vals, n, count, out);
+    case 6: return wave_topk_rank<6>(vals, n, count, out);
+    case 7: return wave_topk_rank<7>(vals, n, count, out);
+    case 8: return wave_topk_rank<8>(vals, n, count, out);
+    default: return wave_topk_iter(vals, n, count, out);
+  }
 }
 __device__ int wave_topk_iter(float* vals, int n, int count, int* out) {
   const int lane = threadIdx.x & 63;
