@@ -22,19 +22,32 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
-// Decode: one 256-thread block per (row, kv-head, split of up to 256 keys),
+// Decode: one block of NW waves per (row, kv-head, split of up to 256 keys),
 // in three phases; all r query heads of the GQA group share every K/V load.
 //  1. Scores.  Lanes form 8 groups of 8; in each step group g of a wave
-//     takes one key and lane part p of the group dims [16p, 16p+16) of it,
-//     so a step reads 8 whole K rows (64 contiguous bytes per lane).  An
-//     8-lane reduction gives the r scores, kept in LDS.  Each wave streams a
-//     contiguous quarter of the split, two steps of K rows in flight.
+//     takes one key, and load i of lane part p of the group reads dims
+//     [4(p + 8i), 4(p + 8i) + 4) of it: each of the 4 load instructions of a
+//     step covers 128 contiguous bytes of each of 8 whole K rows (one cache
+//     line per row, as the P.V loads do), and a step reads the 8 rows whole.
+//     An 8-lane reduction gives the r scores, kept in LDS.  Each wave
+//     streams a contiguous 1/NW of the split with two steps of K rows in
+//     flight.
 //  2. Softmax over the split: block max and sum per head, p = exp(s - max)
 //     written back over the scores.
-//  3. P.V: thread t reads float4 (t mod 32) of V rows j = t/32 + 8i, i.e. two
-//     whole rows per wave instruction, and accumulates p[h][j] * V[j] for
-//     every head; the 8 row groups are added in LDS.  The first V rows are
-//     loaded before phase 1 so their latency hides behind the scores.
+//  3. P.V: thread t reads float4 (t mod 32) of V rows j = t/32 + 2*NW*i,
+//     i.e. two whole rows per wave instruction, and accumulates p[h][j] *
+//     V[j] for every head; the 2*NW row groups are added in LDS.  The first
+//     VP rows per thread are requested right after the first K steps, the
+//     rest double-buffered.
+// A short split (the 129-key sliding windows) gives one block per (row,
+// kv-head) and only 2 blocks per CU, so the waves per block set how many
+// loads a CU keeps in flight: r <= 3 runs 8 waves (<= 128 VGPRs, two blocks
+// per CU); larger r keep 4 waves to bound registers.  Measured on d12
+// shapes: 8 waves beat 4 on long windows (512 keys: 5.6 vs 5.4 TB/s) and
+// tie on short ones; deeper per-wave queues at 4 waves (every K and V byte
+// of a 129-key split requested before the first wait, 219 VGPRs) were 8 %
+// slower; spreading a step's K loads over whole 128-byte lines (instead of
+// 64 bytes per lane) gained 3 %.
 // One split covering the whole window writes the normalized output; several
 // splits write (unnormalized output, max, sum) for decode_combine_kernel.
 // ---------------------------------------------------------------------------
@@ -43,7 +56,18 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 // the extra workgroups gain.
 static constexpr int DEC_KPS = 256;
 static constexpr int DEC_MAXR = 8;   // max GQA ratio
-static constexpr int DEC_VPRE = 8;   // V rows per thread loaded ahead of phase 1
+// NW waves per block; the V rows of phase 3 are dealt to 2*NW row groups.
+template <int R, int NW>
+struct DecDepth {
+  static constexpr int KD = 2;                // K steps in flight per wave
+  static constexpr int VP = NW == 4 ? 8 : 4;  // V rows per thread requested before phase 1
+  static constexpr int RS = 2 * NW;           // V row stride between a thread's rows
+};
+// waves per block for GQA ratio R
+template <int R>
+struct DecWaves {
+  static constexpr int NW = R <= 3 ? 8 : 4;
+};
 
 // The key range of the call and its balanced splits (same arithmetic on the
 // host for eager launches).
@@ -103,11 +127,13 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <int R>
+template <int R, int NW>
 __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
+  constexpr int NT = 64 * NW;
+  constexpr int KD = DecDepth<R, NW>::KD, VP = DecDepth<R, NW>::VP, RS = DecDepth<R, NW>::RS;
   __shared__ float sc[R][DEC_KPS];
-  __shared__ __attribute__((aligned(16))) float pv[8][R][HD];
-  __shared__ float wred[4][R];
+  __shared__ __attribute__((aligned(16))) float pv[RS][R][HD];
+  __shared__ float wred[NW][R];
   __shared__ float stat[2][R];  // max, sum per head
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int bh = blockIdx.x, s = blockIdx.y;
@@ -126,61 +152,67 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   const int64_t gbase = cbase - ks;
   auto krow = [&](int j) -> int64_t { return gsel ? gbase + gsel[j] : cbase + j; };
 
-  // V rows of phase 3, issued first
   const int d4 = tid & 31, jr = tid >> 5;
   const v4f* vrow = reinterpret_cast<const v4f*>(vbase) + d4;
-  v4f vpre[DEC_VPRE];
-#pragma unroll
-  for (int i = 0; i < DEC_VPRE; i++) {
-    const int j = jr + 8 * i;
-    vpre[i] = vrow[krow(j < nk ? j : 0) * (HD / 4)];
-  }
+  v4f vpre[VP];
 
   // ---- phase 1: scores
   {
     const int g = lane >> 3, part = lane & 7;
-    const float* qrow = a.q + ((int64_t)row * a.Hq + hk * R) * HD + 16 * part;
+    const float* qrow = a.q + ((int64_t)row * a.Hq + hk * R) * HD + 4 * part;
     float qv[R][16];
 #pragma unroll
     for (int h = 0; h < R; h++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const v4f t = *reinterpret_cast<const v4f*>(qrow + h * HD + 4 * i);
+        const v4f t = *reinterpret_cast<const v4f*>(qrow + h * HD + 32 * i);
         qv[h][4 * i] = t[0];
         qv[h][4 * i + 1] = t[1];
         qv[h][4 * i + 2] = t[2];
         qv[h][4 * i + 3] = t[3];
       }
-    const int q4 = (nk + 3) / 4;
-    const int j0 = wid * q4, j1 = min(nk, j0 + q4);
-    const v4f* kb = reinterpret_cast<const v4f*>(kbase + 16 * part);
+    const int qw = (nk + NW - 1) / NW;
+    const int j0 = wid * qw, j1 = min(nk, j0 + qw);
+    const v4f* kb = reinterpret_cast<const v4f*>(kbase + 4 * part);
     auto load = [&](int j, v4f* kd) {
       const int jj = j < j1 ? j : j0;  // clamp (value unused when j >= j1)
       const int64_t r = krow(jj) * (HD / 4);
 #pragma unroll
-      for (int i = 0; i < 4; i++) kd[i] = kb[r + i];
+      for (int i = 0; i < 4; i++) kd[i] = kb[r + 8 * i];
     };
-    v4f k0[4], k1[4];
-    if (j0 < j1) load(j0 + g, k0);
-    if (j0 + 8 < j1) load(j0 + 8 + g, k1);
-    for (int jb = j0; jb < j1; jb += 8) {
-      float d[R];
+    // the first KD steps of K, then the V rows of phase 3 (loads complete in
+    // issue order, so the K rows the loop needs first are queued first)
+    v4f kr[KD][4];
 #pragma unroll
-      for (int h = 0; h < R; h++) {
-        float t = 0.f;
+    for (int t = 0; t < KD; t++)
+      if (j0 + 8 * t < j1) load(j0 + 8 * t + g, kr[t]);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-          t += k0[i][0] * qv[h][4 * i] + k0[i][1] * qv[h][4 * i + 1] +
-               k0[i][2] * qv[h][4 * i + 2] + k0[i][3] * qv[h][4 * i + 3];
-        d[h] = red8_sum(t);
+    for (int i = 0; i < VP; i++) {
+      const int j = jr + RS * i;
+      vpre[i] = vrow[krow(j < nk ? j : 0) * (HD / 4)];
+    }
+    for (int jb = j0; jb < j1; jb += 8 * KD) {
+#pragma unroll
+      for (int t = 0; t < KD; t++) {
+        const int jc = jb + 8 * t;  // wave-uniform
+        if (jc < j1) {
+          float d[R];
+#pragma unroll
+          for (int h = 0; h < R; h++) {
+            float x = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              x += kr[t][i][0] * qv[h][4 * i] + kr[t][i][1] * qv[h][4 * i + 1] +
+                   kr[t][i][2] * qv[h][4 * i + 2] + kr[t][i][3] * qv[h][4 * i + 3];
+            d[h] = red8_sum(x);
+          }
+          if (jc + 8 * KD < j1) load(jc + 8 * KD + g, kr[t]);
+          const int j = jc + g;
+          if (part == 0 && j < j1)
+#pragma unroll
+            for (int h = 0; h < R; h++) sc[h][j] = d[h];
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) k0[i] = k1[i];
-      if (jb + 16 < j1) load(jb + 16 + g, k1);
-      const int j = jb + g;
-      if (part == 0 && j < j1)
-#pragma unroll
-        for (int h = 0; h < R; h++) sc[h][j] = d[h];
     }
   }
   __syncthreads();
@@ -197,7 +229,9 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < R; h++) {
-      mx[h] = fmaxf(fmaxf(wred[0][h], wred[1][h]), fmaxf(wred[2][h], wred[3][h]));
+      mx[h] = wred[0][h];
+#pragma unroll
+      for (int w = 1; w < NW; w++) mx[h] = fmaxf(mx[h], wred[w][h]);
       const float p = tid < nk ? expf(v[h] - mx[h]) : 0.f;
       if (tid < nk) sc[h][tid] = p;
       v[h] = wave_sum(p);
@@ -209,7 +243,10 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
     __syncthreads();
     if (tid < R) {
       stat[0][tid] = mx[tid];
-      stat[1][tid] = wred[0][tid] + wred[1][tid] + wred[2][tid] + wred[3][tid];
+      float l = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) l += wred[w][tid];
+      stat[1][tid] = l;
     }
   }
 
@@ -228,18 +265,31 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
     }
   };
 #pragma unroll
-  for (int i = 0; i < DEC_VPRE; i++)
-    if (jr + 8 * i < nk) accumulate(jr + 8 * i, vpre[i]);
-  for (int jb = jr + 8 * DEC_VPRE; jb < nk; jb += 32) {
-    v4f vv[4];
+  for (int i = 0; i < VP; i++)
+    if (jr + RS * i < nk) accumulate(jr + RS * i, vpre[i]);
+  if (RS * VP < nk) {  // block-uniform: the rest of a long split, two sets of 4 rows in flight
+    auto load4 = [&](int j, v4f* vv) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int j = jb + 8 * u;
-      vv[u] = vrow[krow(j < nk ? j : 0) * (HD / 4)];
+      for (int u = 0; u < 4; u++) {
+        const int jj = j + RS * u;
+        vv[u] = vrow[krow(jj < nk ? jj : 0) * (HD / 4)];
+      }
+    };
+    auto acc4 = [&](int j, const v4f* vv) {
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        if (j + RS * u < nk) accumulate(j + RS * u, vv[u]);
+    };
+    v4f va[4], vb[4];
+    int jb = jr + RS * VP;
+    load4(jb, va);
+    for (; jb < nk; jb += 8 * RS) {
+      if (jb + 4 * RS < nk) load4(jb + 4 * RS, vb);
+      acc4(jb, va);
+      if (jb + 4 * RS >= nk) break;
+      if (jb + 8 * RS < nk) load4(jb + 8 * RS, va);
+      acc4(jb + 4 * RS, vb);
     }
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      if (jb + 8 * u < nk) accumulate(jb + 8 * u, vv[u]);
   }
 #pragma unroll
   for (int h = 0; h < R; h++)
@@ -247,11 +297,11 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   __syncthreads();
   const bool whole = pl.nsplit == 1;
   float* out = a.part + ((int64_t)bh * a.nsplit_max + s) * R * (HD + 2);
-  for (int i = tid; i < R * HD; i += 256) {
+  for (int i = tid; i < R * HD; i += NT) {
     const int h = i / HD, dd = i % HD;
     float o = 0.f;
 #pragma unroll
-    for (int r = 0; r < 8; r++) o += pv[r][h][dd];
+    for (int r = 0; r < RS; r++) o += pv[r][h][dd];
     if (whole) {
       a.o[((int64_t)row * a.Hq + hk * R + h) * HD + dd] = o / stat[1][h];
     } else {
@@ -266,9 +316,14 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
 
 // One kernel per GQA ratio R, so each instance is sized (registers, LDS) for
 // its own R rather than for the largest.
+template <int R, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_attn_kernel(DecodeAttnArgs a) {
+  decode_attn_body<R, NW>(a);
+}
 template <int R>
-__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
-  decode_attn_body<R>(a);
+static void launch_decode_attn(dim3 grid, hipStream_t st, const DecodeAttnArgs& a) {
+  constexpr int NW = DecWaves<R>::NW;
+  hipLaunchKernelGGL((decode_attn_kernel<R, NW>), grid, dim3(64 * NW), 0, st, a);
 }
 
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
@@ -335,14 +390,14 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   }
   const dim3 grid(a.rows * a.Hkv, a.nsplit_max);
   switch (a.Hq / a.Hkv) {
-    case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(decode_attn_kernel<2>, grid, dim3(256), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(decode_attn_kernel<3>, grid, dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, grid, dim3(256), 0, st, a); break;
-    case 5: hipLaunchKernelGGL(decode_attn_kernel<5>, grid, dim3(256), 0, st, a); break;
-    case 6: hipLaunchKernelGGL(decode_attn_kernel<6>, grid, dim3(256), 0, st, a); break;
-    case 7: hipLaunchKernelGGL(decode_attn_kernel<7>, grid, dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL(decode_attn_kernel<8>, grid, dim3(256), 0, st, a); break;
+    case 1: launch_decode_attn<1>(grid, st, a); break;
+    case 2: launch_decode_attn<2>(grid, st, a); break;
+    case 3: launch_decode_attn<3>(grid, st, a); break;
+    case 4: launch_decode_attn<4>(grid, st, a); break;
+    case 5: launch_decode_attn<5>(grid, st, a); break;
+    case 6: launch_decode_attn<6>(grid, st, a); break;
+    case 7: launch_decode_attn<7>(grid, st, a); break;
+    case 8: launch_decode_attn<8>(grid, st, a); break;
   }
   GN_HIP(hipGetLastError());
   if (!combine) return;
