@@ -611,9 +611,18 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
 
   p.k_per_split = d.K > 0 ? kps : 0;
   p.splits = splits;
+  const bool defer = d.defer && splits > 1;
+  if (d.defer) {
+    GN_CHECK(d.ldc == d.N && ((d.epi == EPI_STORE && d.alpha == 1.f) ||
+                              (d.epi == EPI_ADD_SRC && d.aux == d.C && d.ldaux == d.N)),
+             "gemm: a deferred split-K sum needs a plain or in-place residual product");
+    *d.defer = PendingSum{};
+  }
   if (splits > 1) {
     GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
-    p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
+    // deferred partials live until their consumer runs, past later GEMMs'
+    p.part = ws->get<float>(defer ? "gemm_splitk_defer" : "gemm_splitk",
+                            (size_t)splits * d.M * d.N);
   }
   // two-level summation for long K ranges per workgroup (see gemm_kernel)
   const bool fold = kps >= 4096;
@@ -625,7 +634,11 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     launch_cfg<64, 64, 2, 2, 2, 4, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   else
     launch_cfg<64, 64, 2, 2, 2, 4, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
-  if (splits > 1) {
+  if (defer) {
+    d.defer->part = p.part;
+    d.defer->splits = splits;
+    d.defer->stride = (int64_t)d.M * d.N;
+  } else if (splits > 1) {
     const int64_t total = (int64_t)d.M * d.N;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
                        p);

@@ -77,6 +77,16 @@ enum GemmGroup {
   GEMM_GROUP_K = 2      // C_g (= C + g*group_stride) op= sum over k in [goff[g], goff[g+1])
 };
 
+// Split-K partial sums left for the kernel that reads the product next:
+// value (m, n) = (float) sum over z < splits, in z order, of (double)
+// part[z * stride + m * N + n] -- what gemm_reduce_kernel computes.
+// splits == 0: the GEMM wrote its output itself.
+struct PendingSum {
+  const float* part = nullptr;
+  int splits = 0;
+  int64_t stride = 0;
+};
+
 struct GemmDesc {
   int M = 0, N = 0, K = 0;
   const float* A = nullptr;
@@ -98,6 +108,11 @@ struct GemmDesc {
   int groups = 0;
   int64_t group_stride = 0;
   int a_pad_rows = 0;  // rows mode: readable rows of A past row M (>= 128 enables full tiles)
+  // Plain products only (EPI_STORE with alpha 1, or EPI_ADD_SRC with aux ==
+  // C, ldc == ldaux == N): when the product splits K, leave the partials in
+  // *defer instead of launching the reduction; the consumer applies the sum
+  // (and the residual add) as gemm_reduce_kernel would.
+  PendingSum* defer = nullptr;
 };
 
 void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);

@@ -11,10 +11,14 @@ void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, 
                         hipStream_t st);
 void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg, const float* lam,
                          int rows, int C, float* prev, float* x, float* x0, hipStream_t st);
+// xin (resp. x) may be the target of a residual-add GEMM whose split-K sum
+// was deferred (pend): the kernels then read xin + sum, and norm_rows
+// writes that value back to x.
 void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
-                       int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st);
-void launch_norm_rows(const float* x, const float* back, const float* lam, int64_t rows, int C,
-                      float* pre, float* y, hipStream_t st);
+                       int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st,
+                       const PendingSum& pend = PendingSum{});
+void launch_norm_rows(float* x, const float* back, const float* lam, int64_t rows, int C,
+                      float* pre, float* y, hipStream_t st, const PendingSum& pend = PendingSum{});
 
 // ---- q/k/v post-processing ----------------------------------------------
 struct QkvPostArgs {
@@ -38,6 +42,7 @@ struct QkvPostArgs {
   float* vcache;
   int maxSeq;
   int rows_per_seq;
+  PendingSum qkv_sum;  // qkv is a deferred split-K product (its partials)
 };
 void launch_qkv_post(const QkvPostArgs& a, int64_t rows, hipStream_t st);
 void launch_replicate_kv(const float* src, float* dst, int G, int S, int Hkv, int P, int maxSrc,

@@ -119,14 +119,24 @@ void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg,
   GN_HIP(hipGetLastError());
 }
 
+// The value of element i of a deferred split-K product: the float64 sum of
+// its partials in split order, rounded once (gemm_reduce_kernel's result).
+__device__ __forceinline__ float pending_value(const PendingSum& ps, int64_t i) {
+  double s = 0.0;
+  for (int z = 0; z < ps.splits; z++) s += (double)ps.part[z * ps.stride + i];
+  return (float)s;
+}
+
 // ---------------------------------------------------------------------------
 // combineResidual + RMSNorm (transformer.go:312,544-551; block.go:39):
-// xb = lr*xin + l0*x0 ; h = norm(xb).  xb may alias xin.
+// xb = lr*xin + l0*x0 ; h = norm(xb).  xb may alias xin.  With a deferred
+// residual-add product pending on xin, xin stands for xin + sum.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const float* __restrict__ x0,
                                                          const float* __restrict__ lr,
                                                          const float* __restrict__ l0, int layer,
-                                                         int C, float* xb, float* __restrict__ h) {
+                                                         int C, float* xb, float* __restrict__ h,
+                                                         PendingSum pend) {
   __shared__ float sc[4];
   const int64_t r = blockIdx.x;
   const float a = lr[layer], b = l0[layer];
@@ -134,7 +144,9 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
   float ss = 0.f;
   int k = 0;
   for (int c = threadIdx.x; c < C; c += 256, k++) {
-    float v = a * xin[r * C + c] + b * x0[r * C + c];
+    float xi = xin[r * C + c];
+    if (pend.splits > 0) xi = pending_value(pend, r * C + c) + xi;
+    float v = a * xi + b * x0[r * C + c];
     vals[k] = v;
     ss += v * v;
   }
@@ -147,19 +159,22 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
   }
 }
 void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
-                       int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st) {
+                       int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st,
+                       const PendingSum& pend) {
   GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
+  GN_CHECK(pend.splits == 0 || pend.stride == rows * (int64_t)C, "resid_norm: pending sum shape");
   hipLaunchKernelGGL(resid_norm_kernel, dim3((unsigned)rows), dim3(256), 0, st, xin, x0, lr, l0,
-                     layer, C, xb, h);
+                     layer, C, xb, h, pend);
   GN_HIP(hipGetLastError());
 }
 
 // y = norm(x - lam*back) (or norm(x) when back is null); pre receives x - lam*back.
-__global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict__ x,
-                                                        const float* __restrict__ back,
+// With a deferred residual-add product pending on x, x first becomes
+// x + sum (written back).
+__global__ __launch_bounds__(256) void norm_rows_kernel(float* x, const float* __restrict__ back,
                                                         const float* __restrict__ lam, int C,
                                                         float* __restrict__ pre,
-                                                        float* __restrict__ y) {
+                                                        float* __restrict__ y, PendingSum pend) {
   __shared__ float sc[4];
   const int64_t r = blockIdx.x;
   const float nl = back ? -lam[0] : 0.f;
@@ -168,6 +183,10 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
   int k = 0;
   for (int c = threadIdx.x; c < C; c += 256, k++) {
     float v = x[r * C + c];
+    if (pend.splits > 0) {
+      v = pending_value(pend, r * C + c) + v;
+      x[r * C + c] = v;
+    }
     if (back) v = v + nl * back[r * C + c];
     vals[k] = v;
     ss += v * v;
@@ -180,11 +199,12 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
     y[r * C + c] = vals[k] * inv;
   }
 }
-void launch_norm_rows(const float* x, const float* back, const float* lam, int64_t rows, int C,
-                      float* pre, float* y, hipStream_t st) {
+void launch_norm_rows(float* x, const float* back, const float* lam, int64_t rows, int C,
+                      float* pre, float* y, hipStream_t st, const PendingSum& pend) {
   GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
+  GN_CHECK(pend.splits == 0 || pend.stride == rows * (int64_t)C, "norm_rows: pending sum shape");
   hipLaunchKernelGGL(norm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, back, lam, C,
-                     pre, y);
+                     pre, y, pend);
   GN_HIP(hipGetLastError());
 }
 
@@ -205,7 +225,10 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int H = a.Hq + 2 * a.Hkv;
   const float* src = a.qkv + n * (int64_t)H * D;
-  for (int i = tid; i < H * D; i += 256) row[i] = src[i];
+  if (a.qkv_sum.splits > 0)
+    for (int i = tid; i < H * D; i += 256) row[i] = pending_value(a.qkv_sum, n * (int64_t)H * D + i);
+  else
+    for (int i = tid; i < H * D; i += 256) row[i] = src[i];
   const int t = (int)(n % a.T);
   const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
   if (a.ve && wid == 0) {
@@ -281,6 +304,8 @@ void launch_qkv_post(const QkvPostArgs& a, int64_t rows, hipStream_t st) {
   GN_CHECK(a.Hq + 2 * a.Hkv <= 16, "qkv_post: at most 16 heads");
   GN_CHECK(a.Hkv <= 8, "qkv_post: at most 8 kv heads");
   GN_CHECK(a.R % 2 == 0 && a.R <= 128, "qkv_post: rotary dims must be even and <= 128");
+  GN_CHECK(a.qkv_sum.splits == 0 || a.qkv_sum.stride == rows * (int64_t)(a.Hq + 2 * a.Hkv) * 128,
+           "qkv_post: pending sum shape");
   hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }

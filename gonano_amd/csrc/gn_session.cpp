@@ -1714,15 +1714,24 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
                                                      (Hq / Hkv) * (HD + 2));
   launch_embed_decode(dtok, s->wte, s->smg, s->sml, rows, C, prev, x, x0, st);
   const int bk = L / 2;
+  // The decode projections split K (M = rows is small); their partial sums
+  // are added by the next row kernel instead of a reduction launch: qkv by
+  // qkv_post, the attention output projection by the MLP norm, the MLP
+  // output projection by the next layer's residual mix (or the final norm).
+  PendingSum pend;  // a residual-add product pending on x
   for (int l = 0; l < L; l++) {
     Layer& ly = s->layers[l];
     if (dec_enc && l == s->split)  // encoderHidden (transformer.go:310-312)
       GN_HIP(hipMemcpyAsync(dec_enc, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
-    launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st);
+    launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st, pend);
+    pend = PendingSum{};
     if (s->mla) {
       mla_decode_layer(s, ly, l, rows, pos, maxSeq, h, kc, vc, x, dpos);
     } else {
-    sgemm(s, linear_fwd_desc(h, ly.wqkv, qkv, rows, C, s->QKVW));
+    PendingSum qsum;
+    GemmDesc gq = linear_fwd_desc(h, ly.wqkv, qkv, rows, C, s->QKVW);
+    gq.defer = &qsum;
+    sgemm(s, gq);
     QkvPostArgs qa{};
     qa.qkv = qkv; qa.h = h; qa.ids = dtok;
     qa.ve = ly.has_ve ? ly.ve : nullptr; qa.wve = ly.wve;
@@ -1734,6 +1743,7 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     qa.vcache = vc + (int64_t)l * rows * Hkv * maxSeq * HD;
     qa.maxSeq = maxSeq;
     qa.rows_per_seq = 1;
+    qa.qkv_sum = qsum;
     launch_qkv_post(qa, rows, st);
     DecodeAttnArgs da{};
     da.q = q; da.kc = qa.kcache; da.vc = qa.vcache; da.part = part; da.o = o;
@@ -1756,9 +1766,11 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     }
     GemmDesc go = linear_fwd_desc(o, ly.wo, x, rows, Hq * HD, C, EPI_ADD_SRC);
     go.aux = x; go.ldaux = C;
+    go.defer = &pend;
     sgemm(s, go);
     }
-    launch_norm_rows(x, nullptr, nullptr, rows, C, nullptr, h, st);
+    launch_norm_rows(x, nullptr, nullptr, rows, C, nullptr, h, st, pend);
+    pend = PendingSum{};
     if (s->moe) {
       float* gu = A<float>(s, "dec_gu", (size_t)rows * 2 * F);
       MoeBuffers mb = moe_buffers(s, "dec_moe_", rows);
@@ -1770,10 +1782,13 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     sgemm(s, gf);
     GemmDesc gp = linear_fwd_desc(act, ly.wproj, x, rows, F, C, EPI_ADD_SRC);
     gp.aux = x; gp.ldaux = C;
+    // x is copied right after this layer (backout) or the next one's start
+    // (CED encoder state): those layers sum their own product
+    if (l != bk && !(dec_enc && l + 1 == s->split)) gp.defer = &pend;
     sgemm(s, gp);
     if (l == bk) GN_HIP(hipMemcpyAsync(back, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
   }
-  launch_norm_rows(x, back, s->bkl, rows, C, nullptr, h, st);
+  launch_norm_rows(x, back, s->bkl, rows, C, nullptr, h, st, pend);
   sgemm(s, linear_fwd_desc(h, s->lm, logits, rows, C, s->V, EPI_SOFTCAP));
 }
 
