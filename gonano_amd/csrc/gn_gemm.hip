@@ -611,7 +611,7 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
 
   p.k_per_split = d.K > 0 ? kps : 0;
   p.splits = splits;
-  const bool defer = d.defer && splits > 1;
+  const bool defer = d.defer && splits > 1 && splits <= PENDING_MAX_SPLITS;
   if (d.defer) {
     GN_CHECK(d.ldc == d.N && ((d.epi == EPI_STORE && d.alpha == 1.f) ||
                               (d.epi == EPI_ADD_SRC && d.aux == d.C && d.ldaux == d.N)),

@@ -86,6 +86,9 @@ struct PendingSum {
   int splits = 0;
   int64_t stride = 0;
 };
+// Consumers hold every partial of their elements in registers (all loads in
+// flight at once), so a GEMM defers its sum only up to this many splits.
+constexpr int PENDING_MAX_SPLITS = 8;
 
 struct GemmDesc {
   int M = 0, N = 0, K = 0;

@@ -6,6 +6,8 @@
 
 namespace gn {
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 static constexpr float NORM_EPS = 1e-6f;  // model/attention.go:11
 static constexpr float QK_SCALE = 1.2f;   // model/attention.go:14
 static constexpr int VE_CH = 12;          // model/attention.go:18
@@ -119,13 +121,30 @@ void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg,
   GN_HIP(hipGetLastError());
 }
 
-// The value of element i of a deferred split-K product: the float64 sum of
-// its partials in split order, rounded once (gemm_reduce_kernel's result).
-__device__ __forceinline__ float pending_value(const PendingSum& ps, int64_t i) {
-  double s = 0.0;
-  for (int z = 0; z < ps.splits; z++) s += (double)ps.part[z * ps.stride + i];
-  return (float)s;
-}
+// Deferred split-K products: element i is the float64 sum of its partials
+// in split order, rounded once (gemm_reduce_kernel's result).  The row
+// kernels are latency-bound (one block per row, a few elements per
+// thread), so a thread first issues the loads of all its elements'
+// partials (a fixed, unrolled count) and sums them afterwards.
+template <int NE>
+struct PendingLoad {
+  float v[NE][PENDING_MAX_SPLITS];
+  // element e (index idx[e], valid[e]) of thread-local slot e
+  __device__ __forceinline__ void load(const PendingSum& ps, const int64_t* idx, const bool* valid) {
+#pragma unroll
+    for (int e = 0; e < NE; e++)
+#pragma unroll
+      for (int z = 0; z < PENDING_MAX_SPLITS; z++)
+        if (valid[e] && z < ps.splits) v[e][z] = ps.part[z * ps.stride + idx[e]];
+  }
+  __device__ __forceinline__ float sum(const PendingSum& ps, int e) const {
+    double s = 0.0;
+#pragma unroll
+    for (int z = 0; z < PENDING_MAX_SPLITS; z++)
+      if (z < ps.splits) s += (double)v[e][z];
+    return (float)s;
+  }
+};
 
 // ---------------------------------------------------------------------------
 // combineResidual + RMSNorm (transformer.go:312,544-551; block.go:39):
@@ -140,29 +159,47 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
   __shared__ float sc[4];
   const int64_t r = blockIdx.x;
   const float a = lr[layer], b = l0[layer];
+  // element k of this thread: column threadIdx.x + 256k (C <= 1024)
+  int64_t idx[4];
+  bool ok[4];
+  float xi[4], xz[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int c = threadIdx.x + 256 * k;
+    ok[k] = c < C;
+    idx[k] = r * C + c;
+    if (ok[k]) {
+      xi[k] = xin[idx[k]];
+      xz[k] = x0[idx[k]];
+    }
+  }
+  PendingLoad<4> pl;
+  if (pend.splits > 0) pl.load(pend, idx, ok);
   float vals[4];
   float ss = 0.f;
-  int k = 0;
-  for (int c = threadIdx.x; c < C; c += 256, k++) {
-    float xi = xin[r * C + c];
-    if (pend.splits > 0) xi = pending_value(pend, r * C + c) + xi;
-    float v = a * xi + b * x0[r * C + c];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if (!ok[k]) continue;
+    const float x = pend.splits > 0 ? pl.sum(pend, k) + xi[k] : xi[k];
+    const float v = __fmaf_rn(a, x, b * xz[k]);  // one rounding order on every build
     vals[k] = v;
     ss += v * v;
   }
   ss = bsum256(ss, sc);
   const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
-  k = 0;
-  for (int c = threadIdx.x; c < C; c += 256, k++) {
-    xb[r * C + c] = vals[k];
-    h[r * C + c] = vals[k] * inv;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if (!ok[k]) continue;
+    xb[idx[k]] = vals[k];
+    h[idx[k]] = vals[k] * inv;
   }
 }
 void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
                        int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st,
                        const PendingSum& pend) {
   GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
-  GN_CHECK(pend.splits == 0 || pend.stride == rows * (int64_t)C, "resid_norm: pending sum shape");
+  GN_CHECK(pend.splits == 0 || (pend.stride == rows * (int64_t)C && pend.splits <= PENDING_MAX_SPLITS),
+           "resid_norm: pending sum shape");
   hipLaunchKernelGGL(resid_norm_kernel, dim3((unsigned)rows), dim3(256), 0, st, xin, x0, lr, l0,
                      layer, C, xb, h, pend);
   GN_HIP(hipGetLastError());
@@ -178,31 +215,49 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(float* x, const float* _
   __shared__ float sc[4];
   const int64_t r = blockIdx.x;
   const float nl = back ? -lam[0] : 0.f;
+  int64_t idx[4];
+  bool ok[4];
+  float xv[4], bv[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int c = threadIdx.x + 256 * k;
+    ok[k] = c < C;
+    idx[k] = r * C + c;
+    if (ok[k]) {
+      xv[k] = x[idx[k]];
+      bv[k] = back ? back[idx[k]] : 0.f;
+    }
+  }
+  PendingLoad<4> pl;
+  if (pend.splits > 0) pl.load(pend, idx, ok);
   float vals[4];
   float ss = 0.f;
-  int k = 0;
-  for (int c = threadIdx.x; c < C; c += 256, k++) {
-    float v = x[r * C + c];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if (!ok[k]) continue;
+    float v = xv[k];
     if (pend.splits > 0) {
-      v = pending_value(pend, r * C + c) + v;
-      x[r * C + c] = v;
+      v = pl.sum(pend, k) + v;
+      x[idx[k]] = v;
     }
-    if (back) v = v + nl * back[r * C + c];
+    if (back) v = v + nl * bv[k];
     vals[k] = v;
     ss += v * v;
   }
   ss = bsum256(ss, sc);
   const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
-  k = 0;
-  for (int c = threadIdx.x; c < C; c += 256, k++) {
-    if (pre) pre[r * C + c] = vals[k];
-    y[r * C + c] = vals[k] * inv;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if (!ok[k]) continue;
+    if (pre) pre[idx[k]] = vals[k];
+    y[idx[k]] = vals[k] * inv;
   }
 }
 void launch_norm_rows(float* x, const float* back, const float* lam, int64_t rows, int C,
                       float* pre, float* y, hipStream_t st, const PendingSum& pend) {
   GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
-  GN_CHECK(pend.splits == 0 || pend.stride == rows * (int64_t)C, "norm_rows: pending sum shape");
+  GN_CHECK(pend.splits == 0 || (pend.stride == rows * (int64_t)C && pend.splits <= PENDING_MAX_SPLITS),
+           "norm_rows: pending sum shape");
   hipLaunchKernelGGL(norm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, back, lam, C,
                      pre, y, pend);
   GN_HIP(hipGetLastError());
@@ -217,24 +272,87 @@ void launch_norm_rows(float* x, const float* back, const float* lam, int64_t row
 // of token n land in cache row (n / T) at that position when a cache is
 // given (decode: T == 1, one row per token; prefill: one row per prompt).
 // ---------------------------------------------------------------------------
+// The kernel is latency-bound (one block per token, ~1-2 K floats each), so
+// every load that does not depend on another -- the q/k/v row (or its
+// split-K partials), the VE gate inputs, the token's VE row and the RoPE
+// table entries of this lane's dims -- is issued before the first wait.
 __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   constexpr int D = 128;
-  __shared__ float row[16 * D];  // up to 16 heads of q/k/v
+  __shared__ __attribute__((aligned(16))) float row[16 * D];  // up to 16 heads of q/k/v
   __shared__ float gate[8];
   const int64_t n = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int H = a.Hq + 2 * a.Hkv;
-  const float* src = a.qkv + n * (int64_t)H * D;
-  if (a.qkv_sum.splits > 0)
-    for (int i = tid; i < H * D; i += 256) row[i] = pending_value(a.qkv_sum, n * (int64_t)H * D + i);
-  else
-    for (int i = tid; i < H * D; i += 256) row[i] = src[i];
+  const int n4 = H * D / 4;  // <= 512 float4 per token: at most 2 per thread
   const int t = (int)(n % a.T);
   const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
+  // q/k/v row: float4 e of this thread is element (tid + 256e) of the row
+  const bool pend = a.qkv_sum.splits > 0;
+  v4f rv[2];
+  v4f pv[2][PENDING_MAX_SPLITS];
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const int i = tid + 256 * e;
+    if (i >= n4) continue;
+    if (pend) {
+      const v4f* P = reinterpret_cast<const v4f*>(a.qkv_sum.part) + n * n4 + i;
+      const int64_t zs = a.qkv_sum.stride / 4;
+#pragma unroll
+      for (int z = 0; z < PENDING_MAX_SPLITS; z++)
+        if (z < a.qkv_sum.splits) pv[e][z] = P[z * zs];
+    } else {
+      rv[e] = reinterpret_cast<const v4f*>(a.qkv)[n * n4 + i];
+    }
+  }
+  // VE inputs: h[:12] and the gate weights (wave 0), the token's VE row
+  float hv = 0.f, wv[8];
+  if (a.ve && wid == 0 && lane < VE_CH) {
+    hv = a.h[n * a.C + lane];
+#pragma unroll
+    for (int hk = 0; hk < 8; hk++)
+      if (hk < a.Hkv) wv[hk] = a.wve[hk * VE_CH + lane];
+  }
+  float vev[4];
+  if (a.ve) {
+    const float* ver = a.ve + (int64_t)a.ids[n] * a.Hkv * D;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (tid + 256 * e < a.Hkv * D) vev[e] = ver[tid + 256 * e];
+  }
+  // RoPE table entries of this lane's two dims (the same for every head)
+  const int half = a.R / 2, off = D - a.R;
+  float cv[2] = {0.f, 0.f}, sv[2] = {0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const int d = lane + 64 * e;
+    if (d >= off) {
+      const int j = d - off, jj = j < half ? j : j - half;
+      cv[e] = a.cosT[(int64_t)pos * half + jj];
+      sv[e] = a.sinT[(int64_t)pos * half + jj];
+    }
+  }
+  // the row into LDS
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const int i = tid + 256 * e;
+    if (i >= n4) continue;
+    v4f v = rv[e];
+    if (pend) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        double sum = 0.0;
+#pragma unroll
+        for (int z = 0; z < PENDING_MAX_SPLITS; z++)
+          if (z < a.qkv_sum.splits) sum += (double)pv[e][z][c];
+        v[c] = (float)sum;
+      }
+    }
+    *reinterpret_cast<v4f*>(&row[4 * i]) = v;
+  }
   if (a.ve && wid == 0) {
     // gate[hk] = 3 * sigmoid(h[:12] . wve[hk]) (attention.go:247-248)
     for (int hk = 0; hk < a.Hkv; hk++) {
-      float p = lane < VE_CH ? a.h[n * a.C + lane] * a.wve[hk * VE_CH + lane] : 0.f;
+      float p = lane < VE_CH ? hv * wv[hk] : 0.f;
       p = warp_sum(p);
       if (lane == 0) {
         float s = sigmoidf_(p);
@@ -246,13 +364,13 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   __syncthreads();
   // v += gate * ve[id] (attention.go:392-405)
   if (a.ve) {
-    const float* ver = a.ve + (int64_t)a.ids[n] * a.Hkv * D;
-    for (int i = tid; i < a.Hkv * D; i += 256) row[(a.Hq + a.Hkv) * D + i] += gate[i / D] * ver[i];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int i = tid + 256 * e;
+      if (i < a.Hkv * D) row[(a.Hq + a.Hkv) * D + i] += gate[i / D] * vev[e];
+    }
   }
   __syncthreads();
-  const int half = a.R / 2, off = D - a.R;
-  const float* cw = a.cosT + (int64_t)pos * half;
-  const float* sw = a.sinT + (int64_t)pos * half;
   // q and k heads: rotate, then 1.2 * RMSNorm over the head
   for (int hd = wid; hd < a.Hq + a.Hkv; hd += 4) {
     const float* x = row + hd * D;
@@ -263,8 +381,8 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
       float v = x[d];
       if (d >= off) {
         int j = d - off;
-        if (j < half) v = x[d] * cw[j] + x[d + half] * sw[j];
-        else v = -x[d - half] * sw[j - half] + x[d] * cw[j - half];
+        if (j < half) v = x[d] * cv[e] + x[d + half] * sv[e];
+        else v = -x[d - half] * sv[e] + x[d] * cv[e];
       }
       y[e] = v;
     }
@@ -302,9 +420,13 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
 }
 void launch_qkv_post(const QkvPostArgs& a, int64_t rows, hipStream_t st) {
   GN_CHECK(a.Hq + 2 * a.Hkv <= 16, "qkv_post: at most 16 heads");
+  GN_CHECK(((uintptr_t)a.qkv & 15) == 0 && ((uintptr_t)a.qkv_sum.part & 15) == 0,
+           "qkv_post: q/k/v rows must be 16-byte aligned");
   GN_CHECK(a.Hkv <= 8, "qkv_post: at most 8 kv heads");
   GN_CHECK(a.R % 2 == 0 && a.R <= 128, "qkv_post: rotary dims must be even and <= 128");
-  GN_CHECK(a.qkv_sum.splits == 0 || a.qkv_sum.stride == rows * (int64_t)(a.Hq + 2 * a.Hkv) * 128,
+  GN_CHECK(a.qkv_sum.splits == 0 ||
+               (a.qkv_sum.stride == rows * (int64_t)(a.Hq + 2 * a.Hkv) * 128 &&
+                a.qkv_sum.splits <= PENDING_MAX_SPLITS),
            "qkv_post: pending sum shape");
   hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
