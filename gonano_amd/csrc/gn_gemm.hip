@@ -461,6 +461,25 @@ static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int spli
   GN_HIP(hipGetLastError());
 }
 
+// Both operands K-contiguous only (x.W^T): tile shapes whose M/N-contiguous
+// LDS layout would not divide into the workgroup's slots.
+template <int BM, int BN, int WM, int WN, int WK, int S>
+static void launch_cfg_kk(const GemmParams& p, bool vec, int splits, hipStream_t st) {
+  GemmParams q = p;
+  q.tiles_m = (int)ceil_div(p.M, BM);
+  q.tiles_n = (int)ceil_div(p.N, BN);
+  q.splits = splits;
+  dim3 grid(q.tiles_m * q.tiles_n * splits);
+  dim3 block(64 * WM * WN * WK);
+  if (vec)
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, false, true, true, true, GEMM_GROUP_NONE>),
+                       grid, block, 0, st, q);
+  else
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, false, true, true, false, GEMM_GROUP_NONE>),
+                       grid, block, 0, st, q);
+  GN_HIP(hipGetLastError());
+}
+
 // Expert-grouped launches.  Rows mode: p.M is the total row count (the sum
 // over groups); the grid has one tile row per BM rows plus one per group
 // (each group's last tile may be partial).  K mode: one "split" per group.
@@ -604,6 +623,29 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     splits = (int)std::min<int64_t>((25 * cus / 32 + tiles / 2) / tiles, d.K / 256);
     splits = std::max(1, std::min(splits, 64));
   }
+  // Narrow tiles for small grids whose N is a multiple of 96 (the d12 decode
+  // projections, N = 768 or 3072 at M = 256): 32x96 tiles with a split
+  // count that makes the workgroups fill whole rounds of the CUs (the MLP
+  // input projection: exactly 256 tiles; the output projections: 64 tiles
+  // x 4 splits), where 64x64 tiles leave a quarter of the CUs idle.
+  bool narrow = false;
+  if (!use_big && !long_k && d.force_splits == 0 && d.N % 96 == 0 && d.a_kcontig && d.b_kcontig) {
+    const int64_t nt = ceil_div(d.M, 32) * (d.N / 96);
+    double best = 0.0;
+    int bs = 1;
+    for (int s = 1; s <= PENDING_MAX_SPLITS && (s == 1 || d.K / s >= 128); s++) {
+      const int64_t wg = nt * s;
+      const double eff = (double)wg / (double)(ceil_div(wg, cus) * cus);
+      if (eff > best + 1e-9) {
+        best = eff;
+        bs = s;
+      }
+    }
+    if (best >= 0.9) {
+      narrow = true;
+      splits = bs;
+    }
+  }
   // k_per_split is a whole number of LDS tiles so that every split but the
   // last starts and ends on a tile boundary.
   int kps = (int)ceil_div(ceil_div(d.K, splits), GK) * GK;
@@ -632,6 +674,8 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     launch_cfg<128, 128, 2, 2, 1, 2, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   else if (fold)
     launch_cfg<64, 64, 2, 2, 2, 4, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
+  else if (narrow)
+    launch_cfg_kk<32, 96, 1, 2, 2, 4>(p, vec, splits, st);
   else
     launch_cfg<64, 64, 2, 2, 2, 4, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   if (defer) {
