@@ -55,6 +55,7 @@ class Config:
     indexer_weight: float = 0.0  # Config.IndexerLossWeight (0: 1)
     reuse_pattern: str = ""      # Config.ReusePattern ("FRU": Full / Reindex / Reuse layers)
     ced: bool = False            # Config.CED (causal encoder-decoder split)
+    head_wise_muon: bool = False  # Config.HeadWiseMuon (optimizer: per-head q/k views)
 
     # -- derived quantities -------------------------------------------------
     @property
@@ -299,6 +300,7 @@ def apply_latent_preset(cfg: Config, mla_latent: int = 0, n_experts: int = 0,
     if cfg.n_kv_head == cfg.n_head and cfg.n_head % 2 == 0:  # applyDefaultGroupedQuery
         cfg.n_kv_head = cfg.n_head // 2
     cfg.mla_latent = mla_latent if mla_latent > 0 else cfg.n_embd // 2
+    cfg.head_wise_muon = False
     return enable_moe(cfg, n_experts, experts_per_token, expert_hidden, shared_hidden, moe_scale,
                       balance_weight)
 
@@ -347,6 +349,7 @@ def apply_flash_preset(cfg: Config, sparse_topk: int = 0, swa_window: int = 0,
         cfg.swa_window = 128
     if cfg.n_layer >= 2:
         cfg.ced = True
+    cfg.head_wise_muon = True
     return enable_moe(cfg, n_experts, experts_per_token, expert_hidden, shared_hidden, 0.0,
                       balance_weight)
 

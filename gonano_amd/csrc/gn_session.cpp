@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "gn_model.h"
+#include "gn_optimizer.h"
 #include "gn_tools.h"
 
 namespace gn {
@@ -2371,6 +2372,94 @@ int gn_session_synchronize(gn_session* s) {
     GN_CHECK(s, "null session");
     GN_HIP(hipSetDevice(s->device));
     GN_HIP(hipStreamSynchronize(s->stream));
+  });
+}
+
+// ---- optimizer ---------------------------------------------------------------
+struct gn_optimizer {
+  gn_session* s = nullptr;
+  std::vector<OptTensor> ts;
+  float* state = nullptr;  // device, every entry's region in table order
+  int64_t state_floats = 0;
+};
+
+int gn_optimizer_create(gn_session* s, const gn_opt_param* table, int32_t count,
+                        gn_optimizer** out) {
+  return guard([&] {
+    GN_CHECK(s && table && out && count > 0, "optimizer: null argument or empty table");
+    *out = nullptr;
+    GN_HIP(hipSetDevice(s->device));
+    auto o = std::make_unique<gn_optimizer>();
+    o->s = s;
+    for (int32_t i = 0; i < count; i++) {
+      const gn_opt_param& h = table[i];
+      GN_CHECK(h.kind == GN_OPT_ADAMW || h.kind == GN_OPT_MUON || h.kind == GN_OPT_SINKHORN,
+               "optimizer: unknown parameter kind");
+      GN_CHECK(h.rows > 0 && h.cols > 0 && h.offset >= 0, "optimizer: bad tensor shape");
+      GN_CHECK(h.kind != GN_OPT_MUON || (h.ns_steps >= 0 && h.ns_steps <= 5),
+               "optimizer: Muon takes at most 5 Polar Express steps");
+      GN_CHECK(h.kind != GN_OPT_SINKHORN || h.sinkhorn_steps >= 1,
+               "optimizer: Sinkhorn needs at least one normalization step");
+      const int64_t n = (int64_t)h.rows * h.cols;
+      const ParamEntry* owner = nullptr;
+      for (const ParamEntry& e : s->table)
+        if (h.offset >= e.offset && h.offset + n <= e.offset + e.rows * e.cols) owner = &e;
+      GN_CHECK(owner != nullptr, "optimizer: entry is not inside one parameter tensor");
+      OptTensor t;
+      t.p = owner->dev + (h.offset - owner->offset);
+      t.g = owner->grad + (h.offset - owner->offset);
+      t.rows = h.rows;
+      t.cols = h.cols;
+      t.h = h;
+      o->ts.push_back(t);
+      o->state_floats += opt_state_floats(h);
+    }
+    GN_HIP(hipMalloc(&o->state, sizeof(float) * o->state_floats));
+    GN_HIP(hipMemsetAsync(o->state, 0, sizeof(float) * o->state_floats, s->stream));
+    float* st = o->state;
+    for (OptTensor& t : o->ts) {
+      t.st = st;
+      st += opt_state_floats(t.h);
+    }
+    GN_HIP(hipStreamSynchronize(s->stream));
+    *out = o.release();
+  });
+}
+int gn_optimizer_step(gn_optimizer* o) {
+  return guard([&] {
+    GN_CHECK(o && o->s, "null optimizer");
+    gn_session* s = o->s;
+    GN_HIP(hipSetDevice(s->device));
+    optimizer_step(o->ts, s->stream, s->arena.get());
+    GN_HIP(hipStreamSynchronize(s->stream));
+    s->derived_dirty = true;  // absorbed decode weights follow the parameters
+  });
+}
+int gn_optimizer_state_size(const gn_optimizer* o, int64_t* count) {
+  return guard([&] {
+    GN_CHECK(o && count, "null argument");
+    *count = o->state_floats;
+  });
+}
+int gn_optimizer_get_state(const gn_optimizer* o, float* state, int64_t count) {
+  return guard([&] {
+    GN_CHECK(o && state, "null argument");
+    GN_CHECK(count == o->state_floats, "optimizer state length mismatch");
+    GN_HIP(hipSetDevice(o->s->device));
+    GN_HIP(hipMemcpyAsync(state, o->state, sizeof(float) * count, hipMemcpyDeviceToHost,
+                          o->s->stream));
+    GN_HIP(hipStreamSynchronize(o->s->stream));
+  });
+}
+int gn_optimizer_destroy(gn_optimizer* o) {
+  return guard([&] {
+    if (!o) return;
+    if (o->state) {
+      GN_HIP(hipSetDevice(o->s->device));
+      GN_HIP(hipStreamSynchronize(o->s->stream));
+      GN_HIP(hipFree(o->state));
+    }
+    delete o;
   });
 }
 

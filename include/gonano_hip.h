@@ -222,6 +222,42 @@ int gn_session_get_grads(const gn_session *session, float *grads, int64_t count)
 /* Transformer.ZeroGrad (model/params.go:97-101). */
 int gn_session_zero_grads(gn_session *session);
 
+/* ---- optimizer step (optimizer/optimizer.go, muon.go, sinkhorn.go) -------
+ * MuonAdamW (optimizer/optimizer.go:72-137) over the session's parameters
+ * and gradients.  The host builds the parameter groups exactly as
+ * Transformer.SetupOptimizer (model/optimizer.go:16-181) and passes one
+ * entry per optimized tensor or tensor view (a head of c_q/c_k under
+ * head-wise Muon, one expert of a packed expert weight), in the order
+ * MuonAdamW.Step visits them; `offset` indexes the flat parameter vector
+ * (gn_session_param_info) and the view is rows x cols floats from there.
+ * Fields a kind does not use are ignored. */
+enum { GN_OPT_ADAMW = 0, GN_OPT_MUON = 1, GN_OPT_SINKHORN = 2 };
+typedef struct {
+  int64_t offset;
+  int32_t rows, cols;
+  int32_t kind;
+  float lr, beta1, beta2, eps, weight_decay; /* ParamGroup.LR .. WeightDecay */
+  float momentum;                            /* ParamGroup.Momentum */
+  int32_t ns_steps;                          /* ParamGroup.NSSteps (<= 5) */
+  float muon_beta2;                          /* ParamGroup.MuonBeta2 */
+  float gamma;                               /* ParamGroup.Gamma */
+  int32_t sinkhorn_steps;                    /* ParamGroup.SinkhornSteps */
+  float tau, sinkhorn_eps;                   /* ParamGroup.SinkhornTau, SinkhornEps */
+} gn_opt_param;
+typedef struct gn_optimizer gn_optimizer;
+/* optimizer.NewMuonAdamW (optimizer/optimizer.go:81-110): zeroed state. */
+int gn_optimizer_create(gn_session *session, const gn_opt_param *table, int32_t count,
+                        gn_optimizer **out);
+/* MuonAdamW.Step (optimizer/optimizer.go:118-137) on the device parameters,
+ * consuming the accumulated gradients (which stay as they are; ZeroGrad is
+ * gn_session_zero_grads). */
+int gn_optimizer_step(gn_optimizer *optimizer);
+/* The optimizer state, entry by entry: AdamW expAvg[n] expAvgSq[n]; Muon
+ * momentum[n] secondMom[max(rows, cols)]; Sinkhorn momentum[n]. */
+int gn_optimizer_state_size(const gn_optimizer *optimizer, int64_t *count);
+int gn_optimizer_get_state(const gn_optimizer *optimizer, float *state, int64_t count);
+int gn_optimizer_destroy(gn_optimizer *optimizer);
+
 /* Transformer.Forward without a cache (model/transformer.go:211-214):
  * logits [batch, seq_len, vocab] of ids [batch, seq_len]. */
 int gn_forward(gn_session *session, const int32_t *ids, int32_t batch, int32_t seq_len,

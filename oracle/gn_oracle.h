@@ -223,6 +223,27 @@ void orc_window_sizes(const orc_config *cfg, int32_t *out);
 /* Number of OpenMP threads the oracle uses (for the CPU baseline report). */
 int orc_num_threads(void);
 
+/* ---- MuonAdamW optimizer step (optimizer.c) ------------------------------
+ * One table entry per optimized tensor or tensor view, in MuonAdamW's
+ * iteration order; same layout as gn_opt_param in include/gonano_hip.h. */
+enum { ORC_OPT_ADAMW = 0, ORC_OPT_MUON = 1, ORC_OPT_SINKHORN = 2 };
+typedef struct {
+  int64_t offset; /* into the flat parameter / gradient vectors */
+  int32_t rows, cols;
+  int32_t kind;
+  float lr, beta1, beta2, eps, weight_decay; /* AdamW (lr, weight_decay: all kinds) */
+  float momentum;                            /* Muon, Sinkhorn */
+  int32_t ns_steps;                          /* Muon */
+  float muon_beta2;                          /* Muon */
+  float gamma;                               /* Sinkhorn */
+  int32_t sinkhorn_steps;
+  float tau, sinkhorn_eps;
+} orc_opt_param;
+int64_t orc_opt_state_floats(const orc_opt_param *t, int n);
+void orc_opt_step(float *params, const float *grads, const orc_opt_param *t, int n, float *state,
+                  int32_t *steps);
+void orc_polar_express(float *u, int64_t rows, int64_t cols, int steps);
+
 #ifdef __cplusplus
 }
 #endif

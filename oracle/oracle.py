@@ -76,6 +76,9 @@ def lib():
     L = C.CDLL(LIB_PATH)
     v = None
     sig = {
+        "orc_opt_state_floats": (C.c_int64, [C.c_void_p, C.c_int]),
+        "orc_opt_step": (v, [_f32p, _f32p, C.c_void_p, C.c_int, _f32p, _i32p]),
+        "orc_polar_express": (v, [_f32p, _i64, _i64, C.c_int]),
         "orc_add": (v, [_f32p, _f32p, _f32p, _i64]),
         "orc_subtract": (v, [_f32p, _f32p, _f32p, _i64]),
         "orc_multiply": (v, [_f32p, _f32p, _f32p, _i64]),
@@ -404,3 +407,27 @@ def calculator(expr: str):
     out = C.create_string_buffer(512)
     ok = lib().orc_calculator(expr.encode(), out, 512)
     return out.value.decode() if ok else None
+
+
+class OracleOptimizer:
+    """MuonAdamW.Step restated in C (oracle/optimizer.c) over a gn_opt_param
+    table (gonano_amd.optimizer.OPT_PARAM_DTYPE layout); test infrastructure."""
+
+    def __init__(self, table: np.ndarray):
+        self.table = np.ascontiguousarray(table)
+        n = len(self.table)
+        self.state = np.zeros(lib().orc_opt_state_floats(self.table.ctypes.data, n), np.float32)
+        self.steps = np.zeros(n, np.int32)
+
+    def step(self, params: np.ndarray, grads: np.ndarray) -> None:
+        """One step in place on the flat parameter vector."""
+        assert params.dtype == np.float32 and grads.dtype == np.float32
+        lib().orc_opt_step(params, np.ascontiguousarray(grads), self.table.ctypes.data,
+                           len(self.table), self.state, self.steps)
+
+
+def polar_express(u: np.ndarray, steps: int = 5) -> np.ndarray:
+    """The Muon orthogonalization of a float32 matrix (optimizer/muon.go:50-74)."""
+    x = np.ascontiguousarray(u, np.float32).copy()
+    lib().orc_polar_express(x, x.shape[0], x.shape[1], steps)
+    return x
