@@ -105,10 +105,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="d12", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--phase", default="rl", choices=["rl", "train"],
+    ap.add_argument("--phase", default="rl", choices=["rl", "train", "optimizer"],
                     help="rl: the full RL step (the benchmark); train: only the recompute + "
                          "PG fwd/bwd on a synthetic batch of the workload's shape (for "
-                         "counter profiles of the train-phase kernels)")
+                         "counter profiles of the train-phase kernels); optimizer: only "
+                         "MuonAdamW steps with cmd/chat_rl's parameter groups")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every decode kernel instead of replaying the captured decode "
                          "graph (for kernel-trace profiles: rocprofv3 --kernel-trace has "
@@ -144,6 +145,8 @@ def main() -> int:
 
     if args.phase == "train":
         return train_phase(args, sess, prompts, S, N, reward_rng, reward_p)
+    if args.phase == "optimizer":
+        return optimizer_phase(args, cfg, sess, prompts)
 
     def step(i: int):
         seeds = np.array([i * 1000 + g for g in range(groups)], np.uint64)
@@ -183,6 +186,9 @@ def main() -> int:
                                  np.uint64))
     t = sess.timing()
     attn_ms, attn_b, attn_n = t["decode_attn_ms"], t["decode_attn_bytes"], t["decode_attn_launches"]
+    # RLStep's optimizer.Step (trainer/rl.go:65), outside the metric: timed
+    # on the last step's gradients
+    opt = optimizer_timing(cfg, sess, steps=2)
     sess.close()
 
     rollout_s = sum(roll_ms) / 1e3
@@ -243,6 +249,7 @@ def main() -> int:
                            "burst of 4 back-to-back launches of every step's attention call "
                            "(the kernels' own duration, as rocprof reports it)",
         },
+        "optimizer": opt,
     }
     if not args.no_cpu_baseline:
         log("bench: timing the CPU oracle on a bounded sample")
@@ -301,6 +308,51 @@ def train_phase(args, sess, prompts, S, N, reward_rng, reward_p) -> int:
         "train_ms": round(sum(train) / len(train), 2), "loss": loss,
         "gemm": {"achieved": round(tf, 2), "unit": "TFLOP/s", "launches": gemm_n,
                  "avg_launch_ms": round(gemm_ms / max(gemm_n, 1), 4)}}), flush=True)
+    return 0
+
+
+def optimizer_timing(cfg, sess, steps: int) -> dict:
+    """MuonAdamW.Step with cmd/chat_rl's groups (cmd/chat_rl/main.go:68-71)
+    on the session's current gradients: wall time per step (one untimed
+    step first) and the Polar Express matrix-product work it contains
+    (per Muon tensor and quintic step: Gram matrix, its square and the
+    polynomial product, 4*r*c*min(r,c) + 2*min(r,c)^3 flops)."""
+    from gonano_amd import optimizer as OPT
+    table = OPT.chat_rl_table(cfg)
+    mu = table[table["kind"] == OPT.KIND_MUON]
+    r, c = mu["rows"].astype(np.float64), mu["cols"].astype(np.float64)
+    g = np.minimum(r, c)
+    flop = float((mu["ns_steps"] * (4 * r * c * g + 2 * g ** 3)).sum())
+    with OPT.Optimizer(sess, table) as opt:
+        opt.step()
+        sess.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            opt.step()
+        sess.synchronize()
+        ms = 1e3 * (time.perf_counter() - t0) / steps
+    kinds = {n: int((table["kind"] == k).sum()) for n, k in
+             (("adamw", OPT.KIND_ADAMW), ("muon", OPT.KIND_MUON), ("sinkhorn", OPT.KIND_SINKHORN))}
+    return {"ms_per_step": round(ms, 2), "tensors": kinds,
+            "polar_express_tflop": round(flop / 1e12, 4),
+            "note": "optimizer.Step of RLStep (trainer/rl.go:65), excluded from ms_per_step "
+                    "as the metric defines the RL step without it; its kernels' times are in "
+                    "profiles/optimizer_step_d12_kernel_stats.md"}
+
+
+def optimizer_phase(args, cfg, sess, prompts) -> int:
+    """Optimizer steps alone (for kernel-trace profiles): gradients from one
+    policy-gradient step on the first prompts, then warmup + timed steps."""
+    rng = np.random.default_rng(3)
+    B, T = 4, prompts.shape[1]
+    inputs = prompts[:B]
+    targets = rng.integers(0, cfg.vocab_size, (B, T)).astype(np.int32)
+    sess.zero_grad()
+    sess.policy_gradient_step(inputs, targets, np.array([1, -1, 0.5, -0.5], np.float32),
+                              float(T + 1))
+    res = optimizer_timing(cfg, sess, steps=args.steps)
+    sess.close()
+    print(json.dumps({"config": args.config, "optimizer": res}), flush=True)
     return 0
 
 
