@@ -135,6 +135,8 @@ _SIGS = {
     "gn_session_synchronize": (C.c_int, [vp]),
     "gn_session_aux_loss": (C.c_int, [vp, C.POINTER(C.c_double)]),
     "gn_session_set_decode_graph": (C.c_int, [vp, C.c_int]),
+    "gn_distill_step": (C.c_int, [vp, vp, i32p, vp, C.c_int32, C.c_int32, C.c_float, C.c_int32,
+                                  C.POINTER(C.c_float)]),
     "gn_optimizer_create": (C.c_int, [vp, vp, C.c_int32, C.POINTER(C.c_void_p)]),
     "gn_optimizer_step": (C.c_int, [vp]),
     "gn_optimizer_state_size": (C.c_int, [vp, C.POINTER(C.c_int64)]),

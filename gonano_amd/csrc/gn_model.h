@@ -127,6 +127,9 @@ void launch_flash_bwd(FlashBwdArgs a, hipStream_t st);
 void launch_row_dot(const float* o, const float* dout, float* delta, int64_t rows, hipStream_t st);
 
 // ---- loss ----------------------------------------------------------------
+void launch_distill_rows(float* z, const float* zt, int64_t ldz, int V, int64_t row0, int64_t rows,
+                         const int32_t* targets, double tau, float scale, double* loss_rows,
+                         hipStream_t st);
 void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t rows,
                          const int32_t* targets, const float* adv, int T, float norm, float* nll,
                          double* loss_rows, hipStream_t st);

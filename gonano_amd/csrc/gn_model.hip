@@ -539,6 +539,87 @@ void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t row
   GN_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------
+// Distillation rows (tensors/loss.go:84-214, trainer/distill.go:13-46).
+// z [rows, V] the student's softcapped logits (row stride ldz) is
+// overwritten by dL/d(pre-softcap logits):
+//   g = (float)((softmax(z/tau) - softmax(zt/tau)) * scale/tau) * (1 - (z/15)^2)
+// with zt the teacher's softcapped logits; the forward-KL loss of the row,
+// rounded to float32, is written to loss_rows (float64).  Rows whose target
+// slot is negative are masked: zero gradient, zero loss.  The maxima, sums
+// and exponentials are float64, as the reference computes them.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void distill_rows_kernel(float* __restrict__ z,
+                                                           const float* __restrict__ zt,
+                                                           int64_t ldz, int V, int64_t row0,
+                                                           const int32_t* __restrict__ targets,
+                                                           double tau, float scale,
+                                                           double* __restrict__ loss_rows) {
+  __shared__ double sd[4];
+  const int64_t r = blockIdx.x;
+  const int64_t n = row0 + r;
+  float* zr = z + r * ldz;
+  const float* tr = zt + r * ldz;
+  if (targets[n] < 0) {
+    for (int j = threadIdx.x; j < V; j += 256) zr[j] = 0.f;
+    if (threadIdx.x == 0) loss_rows[n] = 0.0;
+    return;
+  }
+  double smax = -INFINITY, tmax = -INFINITY;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    smax = fmax(smax, (double)zr[j] / tau);
+    tmax = fmax(tmax, (double)tr[j] / tau);
+  }
+  // block maxima in float64 (max is exact in any order)
+  {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      smax = fmax(smax, __shfl_xor(smax, o, 64));
+      tmax = fmax(tmax, __shfl_xor(tmax, o, 64));
+    }
+    __shared__ double mx[2][4];
+    if (lane == 0) {
+      mx[0][wid] = smax;
+      mx[1][wid] = tmax;
+    }
+    __syncthreads();
+    smax = fmax(fmax(mx[0][0], mx[0][1]), fmax(mx[0][2], mx[0][3]));
+    tmax = fmax(fmax(mx[1][0], mx[1][1]), fmax(mx[1][2], mx[1][3]));
+  }
+  double ss = 0.0, ts = 0.0, ws = 0.0;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const double a = (double)zr[j] / tau, b = (double)tr[j] / tau;
+    const double tw = exp(b - tmax);
+    ss += exp(a - smax);
+    ts += tw;
+    ws += tw * a;
+  }
+  ss = block_sum<double>(ss, sd);
+  ts = block_sum<double>(ts, sd);
+  ws = block_sum<double>(ws, sd);
+  if (threadIdx.x == 0) loss_rows[n] = (double)(float)(smax + log(ss) - ws / ts);
+  const double is = 1.0 / ss, it = 1.0 / ts, gs = (double)scale / tau;
+  const float ic = 1.0f / 15.0f;
+  __syncthreads();
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const float zj = zr[j];
+    const double ps = exp((double)zj / tau - smax) * is;
+    const double pt = exp((double)tr[j] / tau - tmax) * it;
+    const float g = (float)((ps - pt) * gs);
+    const float sc = zj * ic;
+    zr[j] = g * (1.f - sc * sc);
+  }
+}
+void launch_distill_rows(float* z, const float* zt, int64_t ldz, int V, int64_t row0, int64_t rows,
+                         const int32_t* targets, double tau, float scale, double* loss_rows,
+                         hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(distill_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, z, zt, ldz, V,
+                     row0, targets, tau, scale, loss_rows);
+  GN_HIP(hipGetLastError());
+}
+
 // Ordered float64 sum of n values into out[0] (one block).
 __global__ __launch_bounds__(1024) void sum_f64_kernel(const double* __restrict__ v, int64_t n,
                                                        double* __restrict__ out, int accumulate) {

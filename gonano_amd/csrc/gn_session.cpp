@@ -1303,8 +1303,20 @@ static void hca_backward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, 
   sgemm(s, linear_dx_desc(dkv, ly.wqkv + kvoff, genc, (int)N, C, 2 * s->KVW, EPI_ACCUM));
 }
 
+// On-policy distillation (trainer/distill.go:13-46) runs the policy-gradient
+// step's training forward and backward with the distillation loss in place
+// of the PG loss: the frozen teacher's final hidden states of the same rows
+// (teacher.Forward up to its final norm) give its logits chunk by chunk.
+struct DistillCtx {
+  const gn_session* teacher;
+  const float* tfn;  // teacher's final normalized hidden states [N, teacher C]
+  double tau;
+  float scale;  // 1 / (valid tokens * gradient-accumulation steps)
+};
+
 static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* targets, int B,
-                          int T, const float* adv, float norm, double* loss_out, float* nll_out) {
+                          int T, const float* adv, float norm, double* loss_out, float* nll_out,
+                          const DistillCtx* dc = nullptr) {
   GN_CHECK(B > 0 && T > 1, "policy gradient step: need batch > 0 and seq_len > 1");
   GN_CHECK(T <= s->S, "model: sequence longer than rotary cache");
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, F = s->F, L = s->L, V = s->V;
@@ -1333,10 +1345,18 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
   float* dfn = A<float>(s, "dfn", N * C);
   const int64_t chunk = logits_chunk(s, N);
   float* Z = A<float>(s, "logits", chunk * V);
+  float* Zt = dc ? A<float>(s, "teacher_logits", chunk * V) : nullptr;
   for (int64_t r0 = 0; r0 < N; r0 += chunk) {
     const int64_t rows = std::min(chunk, N - r0);
     sgemm(s, linear_fwd_desc(sb.fn + r0 * C, s->lm, Z, (int)rows, C, V, EPI_SOFTCAP));
-    launch_pg_loss_rows(Z, V, V, r0, rows, dtg, dadv, T, norm, nll, loss_rows, st);
+    if (dc) {
+      const int Ct = dc->teacher->C;
+      sgemm(s, linear_fwd_desc(dc->tfn + r0 * Ct, dc->teacher->lm, Zt, (int)rows, Ct, V,
+                               EPI_SOFTCAP));
+      launch_distill_rows(Z, Zt, V, V, r0, rows, dtg, dc->tau, dc->scale, loss_rows, st);
+    } else {
+      launch_pg_loss_rows(Z, V, V, r0, rows, dtg, dadv, T, norm, nll, loss_rows, st);
+    }
     sgemm(s, linear_dx_desc(Z, s->lm, dfn + r0 * C, (int)rows, C, V));
     sgemm(s, linear_dw_desc(Z, sb.fn + r0 * C, s->glm, (int)rows, C, V));
   }
@@ -2267,6 +2287,65 @@ int gn_policy_gradient_step(gn_session* s, const int32_t* inputs, const int32_t*
     GN_CHECK(s && inputs && targets && advantages, "null argument");
     GN_HIP(hipSetDevice(s->device));
     pg_step(s, inputs, targets, batch, seq_len, advantages, norm, loss_out, nll_out);
+  });
+}
+
+int gn_distill_step(gn_session* s, gn_session* teacher, const int32_t* inputs,
+                    const int32_t* mask, int32_t batch, int32_t seq_len, float temperature,
+                    int32_t grad_accum_steps, float* loss_out) {
+  return guard([&] {
+    GN_CHECK(s && teacher && inputs && loss_out, "null argument");
+    GN_CHECK(s != teacher, "distillation: the teacher must be another session");
+    GN_CHECK(s->device == teacher->device, "distillation: teacher and student on one device");
+    GN_CHECK(s->V == teacher->V, "distillation: teacher and student vocabularies differ");
+    GN_CHECK(batch > 0 && seq_len > 1, "distillation: need batch > 0 and seq_len > 1");
+    GN_CHECK(seq_len <= teacher->S, "model: sequence longer than the teacher's rotary cache");
+    GN_HIP(hipSetDevice(s->device));
+    const int B = batch, T = seq_len;
+    const int64_t NT = (int64_t)B * T;
+    // the valid positions fix the scale of every row (distill.go:33-36)
+    int64_t valid = 0;
+    std::vector<int32_t> slot((size_t)NT);
+    for (int64_t i = 0; i < NT; i++) {
+      const bool on = !mask || mask[i] != 0;
+      slot[i] = on ? 0 : -1;
+      valid += on;
+    }
+    const int64_t vt = valid == 0 ? 1 : valid;
+    GN_CHECK(grad_accum_steps >= 1, "distillation: gradient-accumulation steps must be >= 1");
+    // the balance loss's gradient would need the 1/steps scale of
+    // SetAuxiliaryGradientScale (distill.go:21), which this step does not apply
+    GN_CHECK(grad_accum_steps == 1 || !(s->moe && s->bw > 0.f),
+             "distillation: a MoE student with a balance loss takes one accumulation step");
+    DistillCtx dc;
+    dc.teacher = teacher;
+    dc.tau = temperature <= 0.f ? 1.0 : (double)temperature;  // distillationTemperature
+    dc.scale = 1.0f / ((float)vt * (float)grad_accum_steps);
+    const std::vector<float> zero_adv((size_t)B, 0.f);
+    const int mb = pg_micro_batch(s, B, T);
+    double sum = 0;
+    s->bal_batch = B;
+    try {
+      for (int b0 = 0; b0 < B; b0 += mb) {
+        const int nb = std::min(mb, B - b0);
+        // teacher.Forward of these sequences up to its final norm, on its stream
+        SeqBuffers tb;
+        tb.B = nb; tb.T = T; tb.N = (int64_t)nb * T;
+        tb.ids = upload_ids(teacher, "ids", inputs + (int64_t)b0 * T, tb.N, teacher->V);
+        seq_forward(teacher, tb, SEQ_FORWARD, nullptr, nullptr);
+        GN_HIP(hipStreamSynchronize(teacher->stream));
+        dc.tfn = tb.fn;
+        double l = 0;
+        pg_step_chunk(s, inputs + (int64_t)b0 * T, slot.data() + (int64_t)b0 * T, nb, T,
+                      zero_adv.data() + b0, 1.f, &l, nullptr, &dc);
+        sum += l;
+      }
+    } catch (...) {
+      s->bal_batch = 0;
+      throw;
+    }
+    s->bal_batch = 0;
+    *loss_out = (float)(sum / (double)vt);
   });
 }
 

@@ -113,6 +113,20 @@ class Session:
              C.byref(loss), nll.ctypes.data_as(C.c_void_p))
         return loss.value, nll.reshape(B, T)
 
+    def distill_step(self, teacher: "Session", inputs, mask=None, temperature: float = 1.0,
+                     grad_accum_steps: int = 1) -> float:
+        """trainer.DistillStep (trainer/distill.go:13-46): the teacher session
+        scores inputs, this session's gradients accumulate the forward-KL
+        distillation loss; returns the mean per-position loss."""
+        inputs = np.ascontiguousarray(inputs, np.int32)
+        B, T = inputs.shape
+        mk = None if mask is None else np.ascontiguousarray(mask, np.int32)
+        loss = C.c_float()
+        call("gn_distill_step", self._h, teacher._h, inputs,
+             None if mk is None else mk.ctypes.data_as(C.c_void_p), B, T, float(temperature),
+             int(grad_accum_steps), C.byref(loss))
+        return loss.value
+
     def rl_step(self, prompts, samples, max_tokens, temperature, top_k, seeds, rewards):
         prompts = np.ascontiguousarray(prompts, np.int32)
         G, P = prompts.shape

@@ -222,6 +222,17 @@ int gn_session_get_grads(const gn_session *session, float *grads, int64_t count)
 /* Transformer.ZeroGrad (model/params.go:97-101). */
 int gn_session_zero_grads(gn_session *session);
 
+/* trainer.DistillStep (trainer/distill.go:13-46) for one micro-batch:
+ * the frozen `teacher` session (same device and vocabulary, any
+ * architecture) scores inputs [batch, seq_len]; the student `session`'s
+ * gradients accumulate (d/dθ of) the forward-KL loss
+ * (tensors/loss.go:84-214) of every position whose mask entry is non-zero
+ * (mask NULL: every position), scaled by 1 / (valid positions *
+ * grad_accum_steps).  loss_out: the mean per-position loss. */
+int gn_distill_step(gn_session *session, gn_session *teacher, const int32_t *inputs,
+                    const int32_t *mask, int32_t batch, int32_t seq_len, float temperature,
+                    int32_t grad_accum_steps, float *loss_out);
+
 /* ---- optimizer step (optimizer/optimizer.go, muon.go, sinkhorn.go) -------
  * MuonAdamW (optimizer/optimizer.go:72-137) over the session's parameters
  * and gradients.  The host builds the parameter groups exactly as

@@ -149,6 +149,10 @@ int64_t orc_param_total(const orc_config *cfg);
    * parameter gradients grads[param_total] (overwritten). */                                   \
   double orc_pg_step##SFX(orc_model##SFX *m, const int32_t *inputs, const int32_t *targets,     \
                           int B, int T, const float *adv, float norm, REAL *nll, REAL *grads);   \
+  /* trainer.DistillStep given the teacher's logits (trainer/distill.go:13-46). */                \
+  double orc_distill_step##SFX(orc_model##SFX *m, const float *teacher, const int32_t *inputs,   \
+                               const int32_t *mask, int B, int T, float temperature, int accum,  \
+                               REAL *grads);                                                      \
   /* Mean cross-entropy with the gradcheck weighting (model/gradcheck_test.go:94-110). */         \
   double orc_ce_loss##SFX(orc_model##SFX *m, const int32_t *inputs, const int32_t *targets,     \
                           int B, int T, REAL *grads);                                            \

@@ -2824,6 +2824,63 @@ double FN(orc_pg_step)(MODEL *m, const int32_t *inputs, const int32_t *targets, 
   return loss;
 }
 
+/* trainer.DistillStep (trainer/distill.go:13-46) for one micro-batch with
+ * GradAccumSteps = accum, given the frozen teacher's logits [N, V]
+ * (teacher.Forward): the forward-KL loss of every position whose mask is
+ * non-zero (mask NULL: every position) and its gradient
+ * (softmax(s/tau) - softmax(t/tau)) * scale / tau into the student's
+ * parameters (tensors/loss.go:84-214, float64 exp and sums; losses float32
+ * per row).  Returns the mean loss over the valid positions. */
+double FN(orc_distill_step)(MODEL *m, const float *teacher, const int32_t *inputs,
+                            const int32_t *mask, int B, int T, float temperature, int accum,
+                            REAL *grads) {
+  int V = m->V;
+  int64_t N = (int64_t)B * T;
+  train_ctx *ctx = train_forward(m, inputs, B, T);
+  const double tau = temperature <= 0 ? 1.0 : (double)temperature;
+  int valid = 0;
+  for (int64_t n = 0; n < N; n++) valid += !mask || mask[n] != 0;
+  const int vt = valid == 0 ? 1 : valid;
+  const float scale = 1.0f / ((float)vt * (float)accum);
+  REAL *losses = (REAL *)calloc((size_t)N, sizeof(REAL));
+  REAL *glog = (REAL *)calloc((size_t)N * V, sizeof(REAL));
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; n++) {
+    if (mask && mask[n] == 0) continue;
+    const REAL *sr = ctx->logits + n * V;
+    const float *tr = teacher + n * V;
+    double smax = -INFINITY, tmax = -INFINITY;
+    for (int j = 0; j < V; j++) {
+      const double a = (double)sr[j] / tau, b = (double)tr[j] / tau;
+      if (a > smax) smax = a;
+      if (b > tmax) tmax = b;
+    }
+    double ssum = 0, tsum = 0, wsum = 0;
+    for (int j = 0; j < V; j++) {
+      const double a = (double)sr[j] / tau, b = (double)tr[j] / tau;
+      const double sw = exp(a - smax), tw = exp(b - tmax);
+      ssum += sw;
+      tsum += tw;
+      wsum += tw * a;
+    }
+    losses[n] = (REAL)(smax + log(ssum) - wsum / tsum);
+    const double is = 1.0 / ssum, it = 1.0 / tsum, gs = (double)scale / tau;
+    for (int j = 0; j < V; j++) {
+      const double ps = exp((double)sr[j] / tau - smax) * is;
+      const double pt = exp((double)tr[j] / tau - tmax) * it;
+      glog[n * V + j] = (REAL)((ps - pt) * gs);
+    }
+  }
+  double sum = 0;
+  for (int64_t n = 0; n < N; n++) sum += (double)losses[n];
+  memset(grads, 0, sizeof(REAL) * m->total);
+  train_backward(m, ctx, glog, grads);
+  free(glog);
+  free(losses);
+  ctx_free(ctx, m->L);
+  return (double)(REAL)(sum / (double)vt);
+}
+
 /* Mean cross-entropy and its gradient (model/gradcheck_test.go:94-110). */
 double FN(orc_ce_loss)(MODEL *m, const int32_t *inputs, const int32_t *targets, int B, int T,
                         REAL *grads) {

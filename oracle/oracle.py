@@ -162,6 +162,8 @@ def lib():
                                                C.c_float, fp, fp]),
             "orc_ce_loss" + sfx: (C.c_double, [C.c_void_p, _i32p, _i32p, C.c_int, C.c_int,
                                                C.c_void_p]),
+            "orc_distill_step" + sfx: (C.c_double, [C.c_void_p, _f32p, _i32p, C.c_void_p, C.c_int,
+                                                    C.c_int, C.c_float, C.c_int, fp]),
             "orc_generate_batch" + sfx: (v, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int,
                                              C.c_float, C.c_int, C.c_uint64, _i32p, _i32p]),
             "orc_rl_step" + sfx: (C.c_double, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int,
@@ -303,6 +305,18 @@ class OracleModel:
         grads = np.zeros(self.total, self.dtype)
         loss = self._fn("orc_pg_step")(self._m, inputs, targets, B, T, adv, float(norm), nll, grads)
         return loss, nll.reshape(B, T), grads
+
+    def distill_step(self, teacher_logits, inputs, mask=None, temperature=1.0, accum=1):
+        """trainer.DistillStep given the teacher's logits [B, T, V]."""
+        inputs = np.ascontiguousarray(inputs, np.int32)
+        B, T = inputs.shape
+        tl = np.ascontiguousarray(teacher_logits, np.float32)
+        mk = None if mask is None else np.ascontiguousarray(mask, np.int32)
+        grads = np.zeros(self.total, self.dtype)
+        loss = self._fn("orc_distill_step")(self._m, tl, inputs,
+                                            None if mk is None else mk.ctypes.data, B, T,
+                                            float(temperature), int(accum), grads)
+        return loss, grads
 
     def aux_loss(self) -> float:
         """MoE balance loss of the last training forward (pg_step / ce_loss)."""
