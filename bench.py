@@ -114,6 +114,9 @@ def main() -> int:
                     help="launch every decode kernel instead of replaying the captured decode "
                          "graph (for kernel-trace profiles: rocprofv3 --kernel-trace has "
                          "crashed on the graph replays)")
+    ap.add_argument("--no-optimizer", action="store_true",
+                    help="skip the (untimed by the metric) optimizer-step timing, e.g. in "
+                         "kernel-trace profiles of the RL step")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a device copy of 1 GiB (5 times), the known-size "
                          "reference for HBM byte counters")
@@ -188,7 +191,7 @@ def main() -> int:
     attn_ms, attn_b, attn_n = t["decode_attn_ms"], t["decode_attn_bytes"], t["decode_attn_launches"]
     # RLStep's optimizer.Step (trainer/rl.go:65), outside the metric: timed
     # on the last step's gradients
-    opt = optimizer_timing(cfg, sess, steps=2)
+    opt = None if args.no_optimizer else optimizer_timing(cfg, sess, steps=2)
     sess.close()
 
     rollout_s = sum(roll_ms) / 1e3
@@ -249,8 +252,9 @@ def main() -> int:
                            "burst of 4 back-to-back launches of every step's attention call "
                            "(the kernels' own duration, as rocprof reports it)",
         },
-        "optimizer": opt,
     }
+    if opt is not None:
+        res["optimizer"] = opt
     if not args.no_cpu_baseline:
         log("bench: timing the CPU oracle on a bounded sample")
         res["cpu_baseline"] = cpu_baseline(cfg, w, prompts, S, N, temp)
