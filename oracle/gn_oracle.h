@@ -161,6 +161,10 @@ int64_t orc_param_total(const orc_config *cfg);
   void orc_generate_batch##SFX(orc_model##SFX *m, const int32_t *prompt, int P, int S,          \
                                int max_tokens, float temperature, int top_k, uint64_t seed,     \
                                int32_t *rows_out, int32_t *lens_out);                           \
+  /* GenerateWith's logits for one group with the fed columns given: out [ncols+1][S][V]      \
+   * (the prefill's last logits, then those after each column cols[t][S]). */                    \
+  void orc_decode_forced##SFX(orc_model##SFX *m, const int32_t *prompt, int P, int S,           \
+                              const int32_t *cols, int ncols, REAL *out);                       \
   /* One chat_rl step (cmd/chat_rl/main.go:101-183) over G groups of S rollouts with           \
    * precomputed rewards.  Outputs: rollouts/lengths as generate; adv[G*S]; maxLen;              \
    * inputs/targets [G*S, maxLen-1]; nll; grads; returns loss. */                                \

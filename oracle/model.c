@@ -433,36 +433,94 @@ static void rmsnorm_backward_rows(REAL *dst, const REAL *x, const REAL *g, int64
     for (int c = 0; c < cols; c++) d[c] = R((double)gr[c] * inv - coef * (double)xr[c]);
   }
 }
-/* out[rows][outF] = in[rows][inF] . W[outF][inF]^T, float64 accumulation
- * (model/layers/linear.go:32-40 -> kernels/scalar/matmul.go:22-33). */
-static void linear_fwd(REAL *out, const REAL *in, const REAL *W, int64_t rows, int inF, int outF) {
-#pragma omp parallel for schedule(static)
-  for (int64_t r = 0; r < rows; r++)
-    for (int o = 0; o < outF; o++) {
-      double a = 0;
-      const REAL *x = in + r * inF, *w = W + (int64_t)o * inF;
-      for (int i = 0; i < inF; i++) a += (double)x[i] * (double)w[i];
-      out[r * outF + o] = R(a);
+/* dst[r][o] (= or +=) sum over k ascending of a[r][k] * b[o][k] in float64,
+ * for r < rows, o < cols, k < inner (a, b row-major with row lengths lda,
+ * ldb; dst row length ldd).  Every entry is one in-order float64 sum; tiles
+ * of 64 x 64 entries keep their operand rows in cache, and 2 x 4 entries
+ * are summed side by side so that independent adds overlap. */
+static void dot_rows(REAL *dst, int64_t ldd, int accumulate, const REAL *a, int64_t lda,
+                     const REAL *b, int64_t ldb, int64_t rows, int64_t cols, int64_t inner) {
+  const int64_t TR = 64, TC = 64;
+  const int64_t nrt = (rows + TR - 1) / TR, nct = (cols + TC - 1) / TC;
+#pragma omp parallel for schedule(dynamic)
+  for (int64_t t = 0; t < nrt * nct; t++) {
+    const int64_t rb = (t / nct) * TR, cb = (t % nct) * TC;
+    const int64_t re = rb + TR < rows ? rb + TR : rows, ce = cb + TC < cols ? cb + TC : cols;
+    for (int64_t r0 = rb; r0 < re; r0 += 2) {
+      const int64_t r1 = r0 + 1 < re ? r0 + 1 : r0;
+      const REAL *x0 = a + r0 * lda, *x1 = a + r1 * lda;
+      int64_t o = cb;
+      for (; o + 4 <= ce; o += 4) {
+        const REAL *w0 = b + o * ldb, *w1 = w0 + ldb, *w2 = w1 + ldb, *w3 = w2 + ldb;
+        double a00 = 0, a01 = 0, a02 = 0, a03 = 0, a10 = 0, a11 = 0, a12 = 0, a13 = 0;
+        for (int64_t k = 0; k < inner; k++) {
+          const double u = (double)x0[k], v = (double)x1[k];
+          const double b0 = (double)w0[k], b1 = (double)w1[k], b2 = (double)w2[k], b3 = (double)w3[k];
+          a00 += u * b0; a01 += u * b1; a02 += u * b2; a03 += u * b3;
+          a10 += v * b0; a11 += v * b1; a12 += v * b2; a13 += v * b3;
+        }
+        REAL *d0 = dst + r0 * ldd + o, *d1 = dst + r1 * ldd + o;
+        if (accumulate) {
+          d0[0] += R(a00); d0[1] += R(a01); d0[2] += R(a02); d0[3] += R(a03);
+          if (r1 != r0) { d1[0] += R(a10); d1[1] += R(a11); d1[2] += R(a12); d1[3] += R(a13); }
+        } else {
+          d0[0] = R(a00); d0[1] = R(a01); d0[2] = R(a02); d0[3] = R(a03);
+          if (r1 != r0) { d1[0] = R(a10); d1[1] = R(a11); d1[2] = R(a12); d1[3] = R(a13); }
+        }
+      }
+      for (; o < ce; o++) {
+        const REAL *w = b + o * ldb;
+        double a0 = 0, a1 = 0;
+        for (int64_t k = 0; k < inner; k++) {
+          a0 += (double)x0[k] * (double)w[k];
+          a1 += (double)x1[k] * (double)w[k];
+        }
+        if (accumulate) {
+          dst[r0 * ldd + o] += R(a0);
+          if (r1 != r0) dst[r1 * ldd + o] += R(a1);
+        } else {
+          dst[r0 * ldd + o] = R(a0);
+          if (r1 != r0) dst[r1 * ldd + o] = R(a1);
+        }
+      }
     }
+  }
 }
-/* model/layers/linear.go:45-53: dW += g^T x ; dx = g W (float64 accumulation). */
+/* out[rows][outF] = in[rows][inF] . W[outF][inF]^T, float64 accumulation
+ * (model/layers/linear.go:32-40 -> kernels/scalar/matmul.go:22-33): each
+ * output is one float64 sum over i ascending. */
+static void linear_fwd(REAL *out, const REAL *in, const REAL *W, int64_t rows, int inF, int outF) {
+  dot_rows(out, outF, 0, in, inF, W, inF, rows, outF, inF);
+}
+/* dst[cols][rows] = src[rows][cols] */
+static void transpose_rows(REAL *dst, const REAL *src, int64_t rows, int64_t cols) {
+#pragma omp parallel for schedule(static)
+  for (int64_t c0 = 0; c0 < cols; c0 += 32)
+    for (int64_t r0 = 0; r0 < rows; r0 += 32)
+      for (int64_t c = c0; c < c0 + 32 && c < cols; c++)
+        for (int64_t r = r0; r < r0 + 32 && r < rows; r++) dst[c * rows + r] = src[r * cols + c];
+}
+/* model/layers/linear.go:45-53: dW += g^T x ; dx = g W (float64 accumulation).
+ * Each dW entry is one float64 sum over r ascending and each dx entry one
+ * over o ascending, as in the reference's loops; transposed copies of g, x
+ * and W let those sums run over contiguous memory. */
 static void linear_bwd(REAL *dx, REAL *dW, const REAL *x, const REAL *g, const REAL *W,
                        int64_t rows, int inF, int outF) {
-#pragma omp parallel for schedule(static)
-  for (int o = 0; o < outF; o++)
-    for (int i = 0; i < inF; i++) {
-      double a = 0;
-      for (int64_t r = 0; r < rows; r++) a += (double)g[r * outF + o] * (double)x[r * inF + i];
-      dW[(int64_t)o * inF + i] += R(a);
-    }
-  if (!dx) return;
-#pragma omp parallel for schedule(static)
-  for (int64_t r = 0; r < rows; r++)
-    for (int i = 0; i < inF; i++) {
-      double a = 0;
-      for (int o = 0; o < outF; o++) a += (double)g[r * outF + o] * (double)W[(int64_t)o * inF + i];
-      dx[r * inF + i] = R(a);
-    }
+  REAL *gT = (REAL *)malloc(sizeof(REAL) * (size_t)rows * outF);
+  REAL *xT = (REAL *)malloc(sizeof(REAL) * (size_t)rows * inF);
+  if (!gT || !xT) abort();
+  transpose_rows(gT, g, rows, outF);
+  transpose_rows(xT, x, rows, inF);
+  dot_rows(dW, inF, 1, gT, rows, xT, rows, outF, inF, rows);
+  free(xT);
+  free(gT);
+  if (dx) {
+    REAL *WT = (REAL *)malloc(sizeof(REAL) * (size_t)outF * inF);
+    if (!WT) abort();
+    transpose_rows(WT, W, outF, inF);
+    dot_rows(dx, inF, 0, g, outF, WT, outF, rows, inF, outF);
+    free(WT);
+  }
 }
 static REAL sigmoidR(REAL x) { return R(1.0 / (1.0 + exp(-(double)x))); }
 
@@ -3041,6 +3099,32 @@ void FN(orc_generate_batch)(MODEL *m, const int32_t *prompt, int P, int S, int m
   }
   for (int s = 0; s < S; s++) { free(st[s].forced); free(st[s].tool); }
   free(st); free(completed_out); free(next); free(col); free(lg1); free(logits);
+  cache_free(dec);
+}
+
+/* The logits Engine.GenerateWith samples from (inference/engine.go:131-325)
+ * for one group of S rows when the token columns it feeds are given instead
+ * of sampled: out[0] is the prefill's last-position logits (PrefillCED for
+ * the causal encoder-decoder split, Forward otherwise) expanded to the S
+ * rows, out[t] the logits after feeding column t-1, cols [ncols][S], for t =
+ * 1..ncols; out is [ncols + 1][S][V].  Test infrastructure: rollouts of
+ * another engine are checked by sampling each step from these logits. */
+void FN(orc_decode_forced)(MODEL *m, const int32_t *prompt, int P, int S, const int32_t *cols,
+                           int ncols, REAL *out) {
+  const int64_t V = m->V;
+  kvcache *pre = cache_new(m, 1, P);
+  REAL *lg = (REAL *)malloc(sizeof(REAL) * (int64_t)P * V);
+  if (m->split > 0) /* engine.go:164-173 */
+    prefill_ced(m, prompt, P, pre, lg + (int64_t)(P - 1) * V);
+  else
+    forward_impl(m, prompt, 1, P, pre, lg, NULL);
+  for (int s = 0; s < S; s++) memcpy(out + s * V, lg + (int64_t)(P - 1) * V, sizeof(REAL) * V);
+  free(lg);
+  kvcache *dec = cache_new(m, S, P + ncols + 1);
+  prefill_from(m, dec, pre);
+  cache_free(pre);
+  for (int t = 0; t < ncols; t++)
+    forward_impl(m, cols + (int64_t)t * S, S, 1, dec, out + (int64_t)(t + 1) * S * V, NULL);
   cache_free(dec);
 }
 

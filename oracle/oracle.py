@@ -166,6 +166,8 @@ def lib():
                                                     C.c_int, C.c_float, C.c_int, fp]),
             "orc_generate_batch" + sfx: (v, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int,
                                              C.c_float, C.c_int, C.c_uint64, _i32p, _i32p]),
+            "orc_decode_forced" + sfx: (v, [C.c_void_p, _i32p, C.c_int, C.c_int, _i32p, C.c_int,
+                                            fp]),
             "orc_rl_step" + sfx: (C.c_double, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int,
                                                C.c_int, C.c_float, C.c_int, _u64p, _f32p, _i32p,
                                                _i32p, _f32p, C.POINTER(C.c_int32), _i32p, _i32p,
@@ -361,6 +363,17 @@ class OracleModel:
         self._fn("orc_generate_batch")(self._m, prompt, P, samples, max_tokens,
                                        float(temperature), top_k, seed, rows, lens)
         return [rows[s, :lens[s]].copy() for s in range(samples)]
+
+    def decode_forced(self, prompt, cols):
+        """The logits Engine.GenerateWith samples from for one group when the
+        fed columns cols [ncols, S] are given: [ncols + 1, S, V] (the
+        prefill's last logits, then those after each fed column)."""
+        prompt = np.ascontiguousarray(prompt, np.int32).reshape(-1)
+        cols = np.ascontiguousarray(cols, np.int32)
+        ncols, S = cols.shape
+        out = np.zeros((ncols + 1, S, self.shape.vocab_size), self.dtype)
+        self._fn("orc_decode_forced")(self._m, prompt, prompt.size, S, cols, ncols, out)
+        return out
 
     def rl_step(self, prompts, samples, max_tokens, temperature, top_k, seeds, rewards):
         prompts = np.ascontiguousarray(prompts, np.int32)

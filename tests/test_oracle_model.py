@@ -296,3 +296,30 @@ def test_advantages_and_padding(orc):
         tg = padded[1:].copy()
         tg[:3] = -1
         assert (out["targets"][b] == tg).all()
+
+
+@pytest.mark.parametrize("temperature,top_k", [(1.0, 50), (0.7, 5)])
+def test_decode_forced_reproduces_generate(orc, temperature, top_k):
+    """The teacher-forced checker is itself pinned: sampling every step of a
+    group from orc_decode_forced's logits (the rows' own columns fed) with
+    the group stream reproduces the oracle's own generate_batch rows, and its
+    step logits equal the full forward's at the same positions (decode ==
+    prefill)."""
+    from tf_check import teacher_forced_group
+    cfg = G.Config(sequence_len=512, vocab_size=300, n_layer=2, n_head=2, n_kv_head=1,
+                   n_embd=64, window_pattern="SSSL", rotary_dims=32)
+    w = G.init_weights(cfg, seed=3, perturb=0.1)
+    m = orc.OracleModel(shape_of(cfg), w)
+    prompt = np.random.default_rng(4).integers(0, 256, 20).astype(np.int32)
+    rows = m.generate_batch(prompt, 6, 12, temperature, top_k, 99)
+    assert teacher_forced_group(orc, m, prompt, rows, 99, 12, temperature, top_k) > 30
+    # a wrong stream position is caught
+    with pytest.raises(AssertionError):
+        teacher_forced_group(orc, m, prompt, rows, 98, 12, temperature, top_k)
+    full = [r for r in rows if len(r) == 32]
+    if full:
+        cols = np.stack([r[20:31] for r in full], 1)
+        z = m.decode_forced(prompt, cols)
+        ref = m.forward(np.stack(full)[:, :31])
+        for i in range(len(full)):
+            assert rel_err(z[:, i, :], ref[i, 19:31, :]) < 1e-5
