@@ -388,6 +388,12 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
     a.nsplit_max = dec_split(a.kstart, a.kend).nsplit;
     combine = a.nsplit_max > 1;
   }
+  // every block that does not cover its whole key range writes its split's
+  // partial at (row * Hkv + kv-head, split) with stride nsplit_max
+  GN_CHECK(a.nsplit_max <= 1 ||
+               (a.part && (int64_t)a.rows * a.Hkv * a.nsplit_max * (a.Hq / a.Hkv) * (HD + 2) <=
+                              a.part_floats),
+           "decode attention: the split partial buffer is too small for this key range");
   const dim3 grid(a.rows * a.Hkv, a.nsplit_max);
   switch (a.Hq / a.Hkv) {
     case 1: launch_decode_attn<1>(grid, st, a); break;

@@ -79,6 +79,8 @@ struct DecodeAttnArgs {
   const int* nsel = nullptr;
   int kcap = 0;
   int nsplit_max;      // set by the launcher: grid.y and the split stride of part
+  int64_t part_floats = 0;  // capacity of part in floats; the launcher rejects a
+                            // grid whose split layout would not fit
 };
 // Split capacity a part buffer needs for launches with these arguments
 // (window, maxSeq, ratio, maxBlocks).
@@ -127,12 +129,19 @@ void launch_flash_bwd(FlashBwdArgs a, hipStream_t st);
 void launch_row_dot(const float* o, const float* dout, float* delta, int64_t rows, hipStream_t st);
 
 // ---- loss ----------------------------------------------------------------
+// Loss rows of one logits chunk: chunk row r is batch row rowmap[row0 + r]
+// (rowmap null: row0 + r); loss_rows is indexed by row0 + r.
 void launch_distill_rows(float* z, const float* zt, int64_t ldz, int V, int64_t row0, int64_t rows,
-                         const int32_t* targets, double tau, float scale, double* loss_rows,
-                         hipStream_t st);
-void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t rows,
-                         const int32_t* targets, const float* adv, int T, float norm, float* nll,
+                         const int32_t* rowmap, const int32_t* targets, double tau, float scale,
                          double* loss_rows, hipStream_t st);
+void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t rows,
+                         const int32_t* rowmap, const int32_t* targets, const float* adv, int T,
+                         float norm, float* nll, double* loss_rows, hipStream_t st);
+// dst[i] = src[idx[i]] / dst[idx[i]] = src[i] for rows of C floats, i < n
+void launch_gather_rows(const float* src, const int32_t* idx, float* dst, int64_t n, int C,
+                        hipStream_t st);
+void launch_scatter_rows(const float* src, const int32_t* idx, float* dst, int64_t n, int C,
+                         hipStream_t st);
 void launch_sum_f64(const double* v, int64_t n, double* out, bool accumulate, hipStream_t st);
 
 // ---- backward helpers -----------------------------------------------------
@@ -460,5 +469,8 @@ struct SamplerArgs {
   int32_t* out;                 // [rows]
 };
 void launch_sampler(const SamplerArgs& a, hipStream_t st);
+// Advances the Go PCG state {hi, lo} by n draws (tensors.RNG after n Float32
+// calls, tensors/random.go:66-78).
+void advance_rng_state(uint64_t* state, uint64_t n);
 
 }  // namespace gn

@@ -151,6 +151,7 @@ struct PendingLoad {
 // xb = lr*xin + l0*x0 ; h = norm(xb).  xb may alias xin.  With a deferred
 // residual-add product pending on xin, xin stands for xin + sum.
 // ---------------------------------------------------------------------------
+template <int NE>
 __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const float* __restrict__ x0,
                                                          const float* __restrict__ lr,
                                                          const float* __restrict__ l0, int layer,
@@ -159,12 +160,12 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
   __shared__ float sc[4];
   const int64_t r = blockIdx.x;
   const float a = lr[layer], b = l0[layer];
-  // element k of this thread: column threadIdx.x + 256k (C <= 1024)
-  int64_t idx[4];
-  bool ok[4];
-  float xi[4], xz[4];
+  // element k of this thread: column threadIdx.x + 256k (C <= 256 * NE)
+  int64_t idx[NE];
+  bool ok[NE];
+  float xi[NE], xz[NE];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < NE; k++) {
     const int c = threadIdx.x + 256 * k;
     ok[k] = c < C;
     idx[k] = r * C + c;
@@ -173,12 +174,12 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
       xz[k] = x0[idx[k]];
     }
   }
-  PendingLoad<4> pl;
+  PendingLoad<NE> pl;
   if (pend.splits > 0) pl.load(pend, idx, ok);
-  float vals[4];
+  float vals[NE];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < NE; k++) {
     if (!ok[k]) continue;
     const float x = pend.splits > 0 ? pl.sum(pend, k) + xi[k] : xi[k];
     const float v = __fmaf_rn(a, x, b * xz[k]);  // one rounding order on every build
@@ -188,26 +189,36 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
   ss = bsum256(ss, sc);
   const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < NE; k++) {
     if (!ok[k]) continue;
     xb[idx[k]] = vals[k];
     h[idx[k]] = vals[k] * inv;
   }
 }
+// Elements per thread of a 256-thread row kernel over C columns.
+#define GN_ROW_NE_DISPATCH(C, KERNEL_LAUNCH)                                        \
+  do {                                                                              \
+    GN_CHECK((C) >= 1 && (C) <= 2048, "embedding width above 2048 is not supported"); \
+    if ((C) <= 768) { constexpr int NE = 3; KERNEL_LAUNCH; }                        \
+    else if ((C) <= 1024) { constexpr int NE = 4; KERNEL_LAUNCH; }                  \
+    else if ((C) <= 1280) { constexpr int NE = 5; KERNEL_LAUNCH; }                  \
+    else if ((C) <= 1536) { constexpr int NE = 6; KERNEL_LAUNCH; }                  \
+    else { constexpr int NE = 8; KERNEL_LAUNCH; }                                   \
+  } while (0)
 void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
                        int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st,
                        const PendingSum& pend) {
-  GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
   GN_CHECK(pend.splits == 0 || (pend.stride == rows * (int64_t)C && pend.splits <= PENDING_MAX_SPLITS),
            "resid_norm: pending sum shape");
-  hipLaunchKernelGGL(resid_norm_kernel, dim3((unsigned)rows), dim3(256), 0, st, xin, x0, lr, l0,
-                     layer, C, xb, h, pend);
+  GN_ROW_NE_DISPATCH(C, hipLaunchKernelGGL(resid_norm_kernel<NE>, dim3((unsigned)rows), dim3(256),
+                                           0, st, xin, x0, lr, l0, layer, C, xb, h, pend));
   GN_HIP(hipGetLastError());
 }
 
 // y = norm(x - lam*back) (or norm(x) when back is null); pre receives x - lam*back.
 // With a deferred residual-add product pending on x, x first becomes
 // x + sum (written back).
+template <int NE>
 __global__ __launch_bounds__(256) void norm_rows_kernel(float* x, const float* __restrict__ back,
                                                         const float* __restrict__ lam, int C,
                                                         float* __restrict__ pre,
@@ -215,11 +226,11 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(float* x, const float* _
   __shared__ float sc[4];
   const int64_t r = blockIdx.x;
   const float nl = back ? -lam[0] : 0.f;
-  int64_t idx[4];
-  bool ok[4];
-  float xv[4], bv[4];
+  int64_t idx[NE];
+  bool ok[NE];
+  float xv[NE], bv[NE];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < NE; k++) {
     const int c = threadIdx.x + 256 * k;
     ok[k] = c < C;
     idx[k] = r * C + c;
@@ -228,12 +239,12 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(float* x, const float* _
       bv[k] = back ? back[idx[k]] : 0.f;
     }
   }
-  PendingLoad<4> pl;
+  PendingLoad<NE> pl;
   if (pend.splits > 0) pl.load(pend, idx, ok);
-  float vals[4];
+  float vals[NE];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < NE; k++) {
     if (!ok[k]) continue;
     float v = xv[k];
     if (pend.splits > 0) {
@@ -247,7 +258,7 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(float* x, const float* _
   ss = bsum256(ss, sc);
   const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
+  for (int k = 0; k < NE; k++) {
     if (!ok[k]) continue;
     if (pre) pre[idx[k]] = vals[k];
     y[idx[k]] = vals[k] * inv;
@@ -255,11 +266,10 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(float* x, const float* _
 }
 void launch_norm_rows(float* x, const float* back, const float* lam, int64_t rows, int C,
                       float* pre, float* y, hipStream_t st, const PendingSum& pend) {
-  GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
   GN_CHECK(pend.splits == 0 || (pend.stride == rows * (int64_t)C && pend.splits <= PENDING_MAX_SPLITS),
            "norm_rows: pending sum shape");
-  hipLaunchKernelGGL(norm_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, back, lam, C,
-                     pre, y, pend);
+  GN_ROW_NE_DISPATCH(C, hipLaunchKernelGGL(norm_rows_kernel<NE>, dim3((unsigned)rows), dim3(256),
+                                           0, st, x, back, lam, C, pre, y, pend));
   GN_HIP(hipGetLastError());
 }
 
@@ -484,10 +494,103 @@ void launch_expand_last_rows(const float* src, float* dst, int G, int T, int S, 
 // ldz) is overwritten by dL/d(pre-softcap logits):
 //   g = (softmax(z) - onehot(t)) * (adv/norm) * (1 - (z/15)^2),
 // zero for ignored rows.  nll (0 for ignored) and the per-row loss term
-// nll*adv/norm (float64) are written per row.
+// nll*adv/norm (float64) are written per row.  Chunk row r is batch row
+// n = rowmap[row0 + r] (rowmap: the rows that have a target, in order) or
+// n = row0 + r (rowmap null); targets, the advantage of sequence n / T and
+// nll are indexed by n, loss_rows by row0 + r.
+//
+// When the row fits in registers (V a multiple of 4, at most 1024 * 4 * Q
+// floats) one 1024-thread block holds it as Q float4 per thread: the logits
+// are read once and the gradient written once (the maximum, the float64
+// sum of exponentials and the gradient come from the registers).  Otherwise
+// the row is streamed three times (maximum, sum, gradient).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t loss_row_index(const int32_t* rowmap, int64_t row0, int64_t r) {
+  return rowmap ? (int64_t)rowmap[row0 + r] : row0 + r;
+}
+// Buffer resource over `bytes` bytes from p (gfx9 word 3): loads beyond the
+// range return 0 and stores beyond it are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+template <int Q, bool FULL>
+__global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
+    float* __restrict__ z, int64_t ldz, int V, int64_t row0, const int32_t* __restrict__ rowmap,
+    const int32_t* __restrict__ targets, const float* __restrict__ adv, int T, float norm,
+    float* __restrict__ nll, double* __restrict__ loss_rows) {
+  __shared__ float sf[16];
+  __shared__ double sd[16];
+  const int64_t r = blockIdx.x;
+  const int64_t n = loss_row_index(rowmap, row0, r);
+  float* zr = z + r * ldz;
+  // float4 group k of this thread is row bytes [16 * (tid + 1024 k), +16):
+  // one VGPR offset and the group's byte offset as a scalar
+  const __amdgpu_buffer_rsrc_t rs = row_rsrc(zr, V * 4);
+  const int V4 = V >> 2, tid = threadIdx.x, voff = tid * 16;
+  const int32_t tg = targets[n];
+  if (tg < 0) {
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < Q; k++) __builtin_amdgcn_raw_buffer_store_b128(zero, rs, voff, k * 16384, 0);
+    if (tid == 0) {
+      nll[n] = 0.f;
+      loss_rows[row0 + r] = 0.0;
+    }
+    return;
+  }
+  const float zt = zr[tg];
+  v4f v[Q];
+#pragma unroll
+  for (int k = 0; k < Q; k++) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * 16384, 0);
+  if (!FULL) {
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (tid + k * 1024 >= V4) v[k] = (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < Q; k++) m = fmaxf(fmaxf(m, fmaxf(v[k][0], v[k][1])), fmaxf(v[k][2], v[k][3]));
+  m = block_max(m, sf);
+  double s = 0;
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+    if (FULL || tid + k * 1024 < V4)
+      s += ((double)expf(v[k][0] - m) + (double)expf(v[k][1] - m)) +
+           ((double)expf(v[k][2] - m) + (double)expf(v[k][3] - m));
+  }
+  s = block_sum<double>(s, sd);
+  const float a = adv[n / T];
+  const float nl = m + (float)log(s) - zt;
+  if (tid == 0) {
+    nll[n] = nl;
+    loss_rows[row0 + r] = (double)nl * (double)a / (double)norm;
+  }
+  const float inv = (float)(1.0 / s);
+  const float scale = a / norm;
+  const float ic = 1.0f / 15.0f;
+  // the same maximum, hidden from common-subexpression elimination: the
+  // exponentials are recomputed here rather than kept live from the sum
+  // (64 more registers per thread than the budget holds)
+  float mg = m;
+  asm volatile("" : "+v"(mg));
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+    const int j = tid + k * 1024;
+    v4f g;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float zj = v[k][c];
+      float p = expf(zj - mg) * inv;
+      if (4 * j + c == tg) p -= 1.f;
+      const float sc = zj * ic;
+      g[c] = (p * scale) * (1.f - sc * sc);
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(g, rs, voff, k * 16384, 0);
+  }
+}
 __global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z, int64_t ldz,
                                                            int V, int64_t row0,
+                                                           const int32_t* __restrict__ rowmap,
                                                            const int32_t* __restrict__ targets,
                                                            const float* __restrict__ adv, int T,
                                                            float norm, float* __restrict__ nll,
@@ -495,14 +598,14 @@ __global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z
   __shared__ float sf[4];
   __shared__ double sd[4];
   const int64_t r = blockIdx.x;
-  const int64_t n = row0 + r;
+  const int64_t n = loss_row_index(rowmap, row0, r);
   float* zr = z + r * ldz;
   const int32_t tg = targets[n];
   if (tg < 0) {
     for (int j = threadIdx.x; j < V; j += 256) zr[j] = 0.f;
     if (threadIdx.x == 0) {
       nll[n] = 0.f;
-      loss_rows[n] = 0.0;
+      loss_rows[row0 + r] = 0.0;
     }
     return;
   }
@@ -516,7 +619,7 @@ __global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z
   const float nl = m + (float)log(s) - zr[tg];
   if (threadIdx.x == 0) {
     nll[n] = nl;
-    loss_rows[n] = (double)nl * (double)a / (double)norm;
+    loss_rows[row0 + r] = (double)nl * (double)a / (double)norm;
   }
   const float inv = (float)(1.0 / s);
   const float scale = a / norm;
@@ -531,11 +634,67 @@ __global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z
   }
 }
 void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t rows,
-                         const int32_t* targets, const float* adv, int T, float norm, float* nll,
-                         double* loss_rows, hipStream_t st) {
+                         const int32_t* rowmap, const int32_t* targets, const float* adv, int T,
+                         float norm, float* nll, double* loss_rows, hipStream_t st) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(pg_loss_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, z, ldz, V, row0,
-                     targets, adv, T, norm, nll, loss_rows);
+  const bool vec = V % 4 == 0 && ldz % 4 == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0;
+  const int q = ceil_div(V, 4096);
+  const dim3 grid((unsigned)rows);
+#define GN_PG_REG(Q)                                                                           \
+  do {                                                                                         \
+    if (V == 4096 * Q)                                                                         \
+      hipLaunchKernelGGL((pg_loss_rows_reg_kernel<Q, true>), grid, dim3(1024), 0, st, z, ldz, V, \
+                         row0, rowmap, targets, adv, T, norm, nll, loss_rows);                 \
+    else                                                                                       \
+      hipLaunchKernelGGL((pg_loss_rows_reg_kernel<Q, false>), grid, dim3(1024), 0, st, z, ldz, \
+                         V, row0, rowmap, targets, adv, T, norm, nll, loss_rows);              \
+  } while (0)
+  if (vec && q <= 1) GN_PG_REG(1);
+  else if (vec && q <= 2) GN_PG_REG(2);
+  else if (vec && q <= 4) GN_PG_REG(4);
+  else if (vec && q <= 8) GN_PG_REG(8);
+  else if (vec && q <= 16) GN_PG_REG(16);
+  else
+    hipLaunchKernelGGL(pg_loss_rows_kernel, grid, dim3(256), 0, st, z, ldz, V, row0, rowmap,
+                       targets, adv, T, norm, nll, loss_rows);
+#undef GN_PG_REG
+  GN_HIP(hipGetLastError());
+}
+
+// dst[i, :] = src[idx[i], :] for i < n (rows of C floats)
+__global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restrict__ src,
+                                                          const int32_t* __restrict__ idx,
+                                                          float* __restrict__ dst, int64_t n,
+                                                          int C) {
+  const int64_t total = n * C;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t i = e / C;
+    dst[e] = src[(int64_t)idx[i] * C + (e - i * C)];
+  }
+}
+// dst[idx[i], :] = src[i, :] for i < n (rows of C floats; other rows untouched)
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const float* __restrict__ src,
+                                                           const int32_t* __restrict__ idx,
+                                                           float* __restrict__ dst, int64_t n,
+                                                           int C) {
+  const int64_t total = n * C;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t i = e / C;
+    dst[(int64_t)idx[i] * C + (e - i * C)] = src[e];
+  }
+}
+void launch_gather_rows(const float* src, const int32_t* idx, float* dst, int64_t n, int C,
+                        hipStream_t st) {
+  if (n <= 0) return;
+  const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(n * C, 256), 65536);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks), dim3(256), 0, st, src, idx, dst, n, C);
+  GN_HIP(hipGetLastError());
+}
+void launch_scatter_rows(const float* src, const int32_t* idx, float* dst, int64_t n, int C,
+                         hipStream_t st) {
+  if (n <= 0) return;
+  const unsigned blocks = (unsigned)std::min<int64_t>(ceil_div(n * C, 256), 65536);
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3(blocks), dim3(256), 0, st, src, idx, dst, n, C);
   GN_HIP(hipGetLastError());
 }
 
@@ -552,17 +711,18 @@ void launch_pg_loss_rows(float* z, int64_t ldz, int V, int64_t row0, int64_t row
 __global__ __launch_bounds__(256) void distill_rows_kernel(float* __restrict__ z,
                                                            const float* __restrict__ zt,
                                                            int64_t ldz, int V, int64_t row0,
+                                                           const int32_t* __restrict__ rowmap,
                                                            const int32_t* __restrict__ targets,
                                                            double tau, float scale,
                                                            double* __restrict__ loss_rows) {
   __shared__ double sd[4];
   const int64_t r = blockIdx.x;
-  const int64_t n = row0 + r;
+  const int64_t n = loss_row_index(rowmap, row0, r);
   float* zr = z + r * ldz;
   const float* tr = zt + r * ldz;
   if (targets[n] < 0) {
     for (int j = threadIdx.x; j < V; j += 256) zr[j] = 0.f;
-    if (threadIdx.x == 0) loss_rows[n] = 0.0;
+    if (threadIdx.x == 0) loss_rows[row0 + r] = 0.0;
     return;
   }
   double smax = -INFINITY, tmax = -INFINITY;
@@ -598,7 +758,7 @@ __global__ __launch_bounds__(256) void distill_rows_kernel(float* __restrict__ z
   ss = block_sum<double>(ss, sd);
   ts = block_sum<double>(ts, sd);
   ws = block_sum<double>(ws, sd);
-  if (threadIdx.x == 0) loss_rows[n] = (double)(float)(smax + log(ss) - ws / ts);
+  if (threadIdx.x == 0) loss_rows[row0 + r] = (double)(float)(smax + log(ss) - ws / ts);
   const double is = 1.0 / ss, it = 1.0 / ts, gs = (double)scale / tau;
   const float ic = 1.0f / 15.0f;
   __syncthreads();
@@ -612,11 +772,11 @@ __global__ __launch_bounds__(256) void distill_rows_kernel(float* __restrict__ z
   }
 }
 void launch_distill_rows(float* z, const float* zt, int64_t ldz, int V, int64_t row0, int64_t rows,
-                         const int32_t* targets, double tau, float scale, double* loss_rows,
-                         hipStream_t st) {
+                         const int32_t* rowmap, const int32_t* targets, double tau, float scale,
+                         double* loss_rows, hipStream_t st) {
   if (rows <= 0) return;
   hipLaunchKernelGGL(distill_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, z, zt, ldz, V,
-                     row0, targets, tau, scale, loss_rows);
+                     row0, rowmap, targets, tau, scale, loss_rows);
   GN_HIP(hipGetLastError());
 }
 
@@ -639,6 +799,7 @@ void launch_sum_f64(const double* v, int64_t n, double* out, bool accumulate, hi
 // ---------------------------------------------------------------------------
 // RMSNorm backward (tensors/backward.go:81-104), float64 row statistics:
 // out = g/r - x*(g.x)/(C r^3) [+ extra].  out may alias g or extra.
+template <int NE>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restrict__ x,
                                                           const float* g, const float* extra,
                                                           int C, float* out) {
@@ -655,7 +816,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
   const double rms = sqrt(ss / C + (double)NORM_EPS);
   const double inv = 1.0 / rms;
   const double coef = dot / ((double)C * rms * rms * rms);
-  float vals[4];
+  float vals[NE];
   int k = 0;
   for (int c = threadIdx.x; c < C; c += 256, k++) {
     float v = (float)((double)g[r * C + c] * inv - coef * (double)x[r * C + c]);
@@ -668,9 +829,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
 }
 void launch_rmsnorm_bwd(const float* x, const float* g, const float* extra, int64_t rows, int C,
                         float* out, hipStream_t st) {
-  GN_CHECK(C <= 1024, "embedding width above 1024 is not supported");
-  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, g, extra, C,
-                     out);
+  GN_ROW_NE_DISPATCH(C, hipLaunchKernelGGL(rmsnorm_bwd_kernel<NE>, dim3((unsigned)rows), dim3(256),
+                                           0, st, x, g, extra, C, out));
   GN_HIP(hipGetLastError());
 }
 

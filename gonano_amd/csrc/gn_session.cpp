@@ -50,6 +50,12 @@ static u128h pcg_advance_host(u128h s, u128h n) {
 static u128h new_rng_state(uint64_t seed) {
   return ((u128h)seed << 64) | (seed ^ 0x9e3779b97f4a7c15ull);
 }
+void advance_rng_state(uint64_t* state, uint64_t n) {
+  u128h sv = ((u128h)state[0] << 64) | state[1];
+  sv = pcg_advance_host(sv, (u128h)n);
+  state[0] = (uint64_t)(sv >> 64);
+  state[1] = (uint64_t)sv;
+}
 
 // -------------------------------------------------------------------------
 struct ParamEntry {
@@ -316,7 +322,7 @@ static void build_session(gn_session* s, const gn_config& cfg) {
       s->iweight = cfg.indexer_weight > 0 ? cfg.indexer_weight : 1.f;
     }
   }
-  GN_CHECK(s->C <= 1024, "session: EmbedDim above 1024 is not supported");
+  GN_CHECK(s->C <= 2048, "session: EmbedDim above 2048 is not supported");
   GN_CHECK(s->Hq / s->Hkv <= 8, "session: GQA ratio above 8 is not supported");
   GN_CHECK(s->Hq + 2 * s->Hkv <= 16, "session: at most 16 q+k+v heads");
   if (s->moe) {  // model/config.go:138-227
@@ -1004,6 +1010,8 @@ static int32_t* upload_ids(gn_session* s, const char* name, const int32_t* ids, 
 static int64_t logits_chunk(gn_session* s, int64_t N) {
   const int64_t budget = (int64_t)4 << 30;  // 4 GiB of logits per chunk
   int64_t rows = std::max<int64_t>(1, budget / ((int64_t)s->V * 4));
+  if (const char* e = getenv("GN_LOGITS_CHUNK"))  // a smaller chunk (tests: several chunks at small V)
+    rows = std::min<int64_t>(rows, std::max(1, atoi(e)));
   rows = std::min<int64_t>(rows, N);
   return rows;
 }
@@ -1340,28 +1348,64 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
   seq_forward(s, sb, SEQ_TRAIN, nullptr, nullptr);
 
   // ---- fused lm_head + softcap + PG loss + softcap backward, row chunks --
+  // Only rows with a target have a loss and a logits gradient: an ignored
+  // row's NLL, loss term and gradient row are exactly zero (rl.go:25-56,
+  // loss.go:16-46), so the lm_head forward and both of its backward
+  // products run over the rows with targets alone (gathered in order), and
+  // their hidden-state gradients are scattered back into a zeroed dfn.
+  std::vector<int32_t> vrows;
+  vrows.reserve(N);
+  for (int64_t i = 0; i < N; i++)
+    if (targets[i] >= 0) vrows.push_back((int32_t)i);
+  const int64_t Nv = (int64_t)vrows.size();
+  const bool compact = Nv < N;
   float* nll = A<float>(s, "nll", N);
-  double* loss_rows = A<double>(s, "loss_rows", N);
+  double* loss_rows = A<double>(s, "loss_rows", std::max<int64_t>(Nv, 1));
   float* dfn = A<float>(s, "dfn", N * C);
-  const int64_t chunk = logits_chunk(s, N);
+  const int32_t* rowmap = nullptr;
+  const float* fnv = sb.fn;  // [Nv, C] final-norm rows with targets
+  const float* tfnv = dc ? dc->tfn : nullptr;
+  float* dfnv = dfn;
+  if (compact) {
+    GN_HIP(hipMemsetAsync(nll, 0, sizeof(float) * N, st));
+    GN_HIP(hipMemsetAsync(dfn, 0, sizeof(float) * N * C, st));
+    if (Nv > 0) {
+      int32_t* drm = A<int32_t>(s, "loss_rowmap", Nv);
+      GN_HIP(hipMemcpyAsync(drm, vrows.data(), sizeof(int32_t) * Nv, hipMemcpyHostToDevice, st));
+      rowmap = drm;
+      float* g1 = A<float>(s, "loss_fn_rows", Nv * C);
+      launch_gather_rows(sb.fn, drm, g1, Nv, C, st);
+      fnv = g1;
+      if (dc) {
+        const int Ct = dc->teacher->C;
+        float* g2 = A<float>(s, "loss_tfn_rows", Nv * Ct);
+        launch_gather_rows(dc->tfn, drm, g2, Nv, Ct, st);
+        tfnv = g2;
+      }
+      dfnv = A<float>(s, "loss_dfn_rows", Nv * C);
+    }
+  }
+  const int64_t chunk = logits_chunk(s, std::max<int64_t>(Nv, 1));
   float* Z = A<float>(s, "logits", chunk * V);
   float* Zt = dc ? A<float>(s, "teacher_logits", chunk * V) : nullptr;
-  for (int64_t r0 = 0; r0 < N; r0 += chunk) {
-    const int64_t rows = std::min(chunk, N - r0);
-    sgemm(s, linear_fwd_desc(sb.fn + r0 * C, s->lm, Z, (int)rows, C, V, EPI_SOFTCAP));
+  for (int64_t r0 = 0; r0 < Nv; r0 += chunk) {
+    const int64_t rows = std::min(chunk, Nv - r0);
+    sgemm(s, linear_fwd_desc(fnv + r0 * C, s->lm, Z, (int)rows, C, V, EPI_SOFTCAP));
     if (dc) {
       const int Ct = dc->teacher->C;
-      sgemm(s, linear_fwd_desc(dc->tfn + r0 * Ct, dc->teacher->lm, Zt, (int)rows, Ct, V,
+      sgemm(s, linear_fwd_desc(tfnv + r0 * Ct, dc->teacher->lm, Zt, (int)rows, Ct, V,
                                EPI_SOFTCAP));
-      launch_distill_rows(Z, Zt, V, V, r0, rows, dtg, dc->tau, dc->scale, loss_rows, st);
+      launch_distill_rows(Z, Zt, V, V, r0, rows, rowmap, dtg, dc->tau, dc->scale, loss_rows, st);
     } else {
-      launch_pg_loss_rows(Z, V, V, r0, rows, dtg, dadv, T, norm, nll, loss_rows, st);
+      launch_pg_loss_rows(Z, V, V, r0, rows, rowmap, dtg, dadv, T, norm, nll, loss_rows, st);
     }
-    sgemm(s, linear_dx_desc(Z, s->lm, dfn + r0 * C, (int)rows, C, V));
-    sgemm(s, linear_dw_desc(Z, sb.fn + r0 * C, s->glm, (int)rows, C, V));
+    sgemm(s, linear_dx_desc(Z, s->lm, dfnv + r0 * C, (int)rows, C, V));
+    sgemm(s, linear_dw_desc(Z, fnv + r0 * C, s->glm, (int)rows, C, V));
   }
+  if (compact && Nv > 0) launch_scatter_rows(dfnv, rowmap, dfn, Nv, C, st);
   double* dloss = A<double>(s, "loss", 1);
-  launch_sum_f64(loss_rows, N, dloss, false, st);
+  if (Nv > 0) launch_sum_f64(loss_rows, Nv, dloss, false, st);
+  else GN_HIP(hipMemsetAsync(dloss, 0, sizeof(double), st));
 
   // ---- trunk backward (train_transformer.go:176-265) ---------------------
   double* part = A<double>(s, "partials", 65536);
@@ -1723,11 +1767,17 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   float* o = s->mla ? nullptr : A<float>(s, "dec_o", (size_t)rows * Hq * HD);
   float* act = A<float>(s, "dec_act", (size_t)rows * F);
   float* back = A<float>(s, "dec_back", (size_t)rows * C);
-  int part_splits = (maxSeq + 63) / 64;
-  if (s->hca) {
+  // split capacity of the attention partials: the largest split count of
+  // any layer's key range (dense: the full-context layer's; compressed: the
+  // blocks plus the local window)
+  int part_splits = 1;
+  for (const Layer& ly : s->layers) {
     DecodeAttnArgs cap{};
-    cap.maxSeq = maxSeq; cap.window = s->swa; cap.ratio = s->ratio; cap.maxBlocks = s->maxBlocks;
-    part_splits = decode_attention_split_cap(cap);  // >= the sparse layout's
+    cap.maxSeq = maxSeq; cap.window = std::min(ly.window, maxSeq);
+    if (s->hca) {
+      cap.window = s->swa; cap.ratio = s->ratio; cap.maxBlocks = s->maxBlocks;
+    }
+    part_splits = std::max(part_splits, decode_attention_split_cap(cap));
   }
   float* dec_enc = s->split > 0 ? A<float>(s, "dec_enc", (size_t)rows * C) : nullptr;
   float* part = s->mla ? nullptr
@@ -1768,6 +1818,7 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     launch_qkv_post(qa, rows, st);
     DecodeAttnArgs da{};
     da.q = q; da.kc = qa.kcache; da.vc = qa.vcache; da.part = part; da.o = o;
+    da.part_floats = (int64_t)rows * Hkv * part_splits * (Hq / Hkv) * (HD + 2);
     da.rows = rows; da.Hq = Hq; da.Hkv = Hkv; da.maxSeq = maxSeq;
     da.kstart = std::max(0, pos - ly.window);
     da.kend = pos + 1;
@@ -2410,12 +2461,7 @@ int gn_sample_next_token(const float* logits, int64_t rows, int64_t vocab, uint6
     GN_HIP(hipStreamSynchronize(st));
     ar.release();
     GN_HIP(hipStreamDestroy(st));
-    if (temperature > 0) {
-      u128h sv = ((u128h)rng_state[0] << 64) | rng_state[1];
-      sv = pcg_advance_host(sv, (u128h)rows * (u128h)vocab);
-      rng_state[0] = (uint64_t)(sv >> 64);
-      rng_state[1] = (uint64_t)sv;
-    }
+    if (temperature > 0) advance_rng_state(rng_state, (uint64_t)rows * (uint64_t)vocab);
   });
 }
 

@@ -1,0 +1,293 @@
+"""Parity at the benchmark's shapes.
+
+The other GPU tests use narrow models (C = 256, two query heads) that the
+oracle finishes quickly; the kernel paths the BASELINE workloads select
+depend on width, head counts, row counts and context lengths, so these
+tests run those exact widths -- d12 (C 768, 6:2 heads, F 3072), d20 (C 1280,
+10:2 heads), latent d12 (MLA latent 256 over 6:3 heads, 16 experts of 512)
+and flash d12 (6:1 heads, ratio 4, top-16 of 128 candidates, SWA 512, FRU,
+CED, 16 experts of 768) -- with the row counts of their rollouts (256, 512,
+256, 64) and prompts long enough to reach the multi-split decode attention
+and the hierarchical selection, at a depth and vocabulary the oracle handles
+in seconds; plus the full d12 model (12 layers, V = 65536).  The paths
+checked include decode attention at GQA ratios 3, 5 and 6 with two and
+three key splits and the combine, the 32 x 96 decode GEMM tiles with
+deferred split-K sums (M = 256, N a multiple of 96), MLA decode at 6:3
+heads, the sparse decode at 6:1, and the policy-gradient loss over several
+logits chunks (GN_LOGITS_CHUNK) with the rows without a target left out of
+the lm_head products.
+
+Rollouts are checked by teacher forcing (tests/tf_check.py: every sampled
+token of every checked group equals the oracle's draw from the group stream
+given the same prefix, bit-exact); logits at the 1e-4 normwise bar of the
+other GPU tests.  The policy-gradient step is compared with the oracle's
+float32 build, which takes the same discrete decisions (expert routing,
+block selection) as the GPU, at 1e-4 or at twice the oracle's own float32
+error (float32 build against float64 build) where that is larger.
+
+MLA has no QK-norm, so its attention logits grow with the width and the
+weight perturbation: the latent and flash tests perturb InitWeights by
+N(0, 0.02) at C = 768 (the narrow tests' 0.05 at C = 256).  At 0.05 and
+C = 768 the problem is ill-conditioned: the oracle's float32 build is 3.7e-5
+from its float64 build on the latent gradient and a float32-accumulating
+implementation (the GPU, like the reference's SIMD backend) 2e-4; at 0.02
+both are below 1e-5."""
+import dataclasses
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rel_err
+from gonano_amd import config as G
+from tf_check import teacher_forced_group
+
+pytestmark = pytest.mark.gpu
+
+
+def with_depth(cfg, layers, vocab):
+    return dataclasses.replace(cfg, n_layer=layers, vocab_size=vocab)
+
+
+def d12_width():
+    return with_depth(G.dense_d12(), 2, 4096)
+
+
+def d20_width():
+    return with_depth(G.dense_d20(), 2, 4096)
+
+
+def latent_width():
+    cfg = G.config_for_depth_ratio(12, 4096, 64, 128, 512, "SSSL", 1)
+    cfg.n_layer = 2
+    return G.apply_latent_preset(cfg, mla_latent=256, n_experts=16, experts_per_token=2,
+                                 expert_hidden=512)
+
+
+def flash_width():
+    cfg = G.config_for_depth_ratio(12, 4096, 64, 128, 2048, "SSSL", 1)
+    cfg.n_kv_head = 1
+    cfg.n_layer = 6
+    return G.apply_flash_preset(cfg, sparse_topk=16, swa_window=512, n_experts=16)
+
+
+def _model(orc, cfg, w):
+    return orc.OracleModel(orc.ModelShape.from_config(cfg), w)
+
+
+def _rollout_check(orc, cfg, w, G_, S, P, N, temperature, groups, seed0=1000):
+    from gonano_amd.session import Session
+    prompts = np.random.default_rng(cfg.n_embd + P).integers(0, cfg.vocab_size, (G_, P)).astype(np.int32)
+    seeds = (seed0 + np.arange(G_)).astype(np.uint64)
+    with Session(cfg) as s:
+        s.set_params(w)
+        rows = s.generate_batch(prompts, S, N, temperature, 50, seeds)
+    assert len(rows) == G_ * S
+    m = _model(orc, cfg, w)
+    checked = 0
+    for g in groups:
+        checked += teacher_forced_group(orc, m, prompts[g], rows[g * S:(g + 1) * S], seeds[g], N,
+                                        temperature, 50)
+    assert checked >= len(groups) * S * min(N, 4)
+    return checked
+
+
+def _bar(e32, tol):
+    """The accuracy bar of one quantity: tol (the north-star 1e-4), or twice
+    the oracle's own float32 error (its float32 build against its float64
+    build) where the float32 arithmetic itself is further than that from the
+    exact result -- an ill-conditioned tensor, which no float32
+    implementation can be held closer to than its own rounding."""
+    return max(tol, 2.0 * e32)
+
+
+def _compare_grads(cfg, got, w32, w64, tol=1e-4, scalar_tol=5e-4):
+    """Every parameter's gradient against the oracle's float32 build (which
+    takes the same discrete decisions -- expert routing, block selection --
+    as the GPU): normwise within _bar(float32-vs-float64 error, tol) --
+    scalar_tol for the per-layer lambdas and smear scalars (single dot
+    products over every token and channel) -- and element-wise within 1e-3 of
+    the tensor's largest entry.  Tensors whose gradient is roundoff on both
+    sides pass below 1e-5 of the largest entry of the model."""
+    floor = 1e-5 * float(np.abs(w32).max())
+    rows, bad = [], []
+    for name, r, c, off in cfg.param_table():
+        g, a, b = got[off:off + r * c], w32[off:off + r * c], w64[off:off + r * c]
+        d = float(np.abs(g - a).max())
+        e, e32 = rel_err(g, a), rel_err(a, b)
+        bar = _bar(e32, tol if r * c >= 64 else scalar_tol)
+        rows.append((e, e32, name))
+        if d <= floor:
+            continue
+        if e >= bar or d > 1e-3 * np.abs(a).max() + floor:
+            bad.append((name, e, e32, d))
+    worst = "\n".join(f"  {n:45s} gpu-f32 {e:.2e}  f32-f64 {e32:.2e}" for e, e32, n in
+                      sorted(rows, reverse=True)[:8])
+    assert rel_err(got, w32) < _bar(rel_err(w32, w64), tol), worst
+    assert not bad, f"{bad}\n{worst}"
+
+
+def _pg_check(orc, cfg, w, B, T, prompt_len, chunk, monkeypatch, seed=7):
+    """PolicyGradientStep on random sequences whose first prompt_len targets
+    are ignored (the chat_rl masking); the logits run in chunks of `chunk`
+    rows, so several chunks and a partial last one are exercised.  Loss, NLL
+    and gradients are compared with the oracle's float32 build within the
+    1e-4 bar, or twice the oracle's own float32 error (its float64 build
+    runs too) where that is larger."""
+    from gonano_amd.session import Session
+    rng = np.random.default_rng(seed)
+    inputs = rng.integers(0, cfg.vocab_size, (B, T)).astype(np.int32)
+    targets = rng.integers(0, cfg.vocab_size, (B, T)).astype(np.int32)
+    targets[:, :prompt_len] = -1
+    adv = np.linspace(-0.5, 0.5, B).astype(np.float32) + 0.1
+    monkeypatch.setenv("GN_LOGITS_CHUNK", str(chunk))
+    with Session(cfg) as s:
+        s.set_params(w)
+        s.zero_grad()
+        loss, nll = s.policy_gradient_step(inputs, targets, adv, float(T + 1))
+        grads = s.grads()
+        aux = s.aux_loss()
+    monkeypatch.delenv("GN_LOGITS_CHUNK")
+    m32 = _model(orc, cfg, w)
+    l32, n32, g32 = m32.pg_step(inputs, targets, adv, float(T + 1))
+    m64 = orc.OracleModel(orc.ModelShape.from_config(cfg), w.astype(np.float64), dtype=np.float64)
+    l64, n64, g64 = m64.pg_step(inputs, targets, adv, float(T + 1))
+    assert abs(loss - l32) <= max(1e-4 * max(abs(l32), 1e-3), 2 * abs(l32 - l64)), (loss, l32, l64)
+    assert np.all(nll[:, :prompt_len] == 0)
+    assert rel_err(nll, n32) < _bar(rel_err(n32, n64), 1e-4), (rel_err(nll, n32), rel_err(n32, n64))
+    assert_close(nll, n32, 1e-3, 1e-4, "nll")
+    if cfg.moe:
+        assert abs(aux - m32.aux_loss()) <= 1e-6 * max(abs(m32.aux_loss()), 1e-9)
+    _compare_grads(cfg, grads, g32, g64)
+
+
+# ---- dense d12 width (BASELINE configs[1] at 2 layers, V 4096) -------------
+@pytest.fixture(scope="module")
+def d12w():
+    cfg = d12_width()
+    assert (cfg.n_embd, cfg.n_head, cfg.n_kv_head, cfg.mlp_hidden) == (768, 6, 2, 3072)
+    assert cfg.window_sizes() == [128, 512]
+    return cfg, G.init_weights(cfg, seed=12, perturb=0.1)
+
+
+def test_d12_width_rollout_teacher_forced(orc, d12w):
+    """256 rows (16 groups x 16), 260-token prompts: the full-context layer
+    attends 260..267 keys in two splits with the combine, the windowed layer
+    129 keys in one; the decode MLP and output projections take the 32 x 96
+    tiles at M = 256."""
+    cfg, w = d12w
+    _rollout_check(orc, cfg, w, 16, 16, 260, 8, 1.0, groups=(0, 7, 15))
+
+
+def test_d12_width_pg_step_chunked(orc, d12w, monkeypatch):
+    cfg, w = d12w
+    _pg_check(orc, cfg, w, B=3, T=300, prompt_len=150, chunk=128, monkeypatch=monkeypatch)
+
+
+def test_d12_width_graph_equals_eager(d12w):
+    """The captured decode graph at the d12 width replays the eager steps
+    token for token (two replays, eager work between them)."""
+    from gonano_amd.session import Session
+    cfg, w = d12w
+    prompts = np.random.default_rng(9).integers(0, cfg.vocab_size, (16, 260)).astype(np.int32)
+    seeds = np.arange(16, dtype=np.uint64)
+    with Session(cfg) as s:
+        s.set_params(w)
+        s.set_decode_graph(False)
+        eager = s.generate_batch(prompts, 16, 10, 1.0, 50, seeds)
+        s.set_decode_graph(True)
+        for _ in range(2):
+            got = s.generate_batch(prompts, 16, 10, 1.0, 50, seeds)
+            assert all(np.array_equal(a, b) for a, b in zip(got, eager))
+            s.forward(prompts[:2, :8])
+
+
+# ---- the full d12 model -------------------------------
+@pytest.fixture(scope="module")
+def d12full():
+    cfg = G.dense_d12()
+    return cfg, G.init_weights(cfg, seed=0, perturb=0.1)
+
+
+def test_d12_forward_logits(orc, d12full):
+    """12 layers, V = 65536: Transformer.Forward logits of a short batch."""
+    from gonano_amd.session import Session
+    cfg, w = d12full
+    ids = np.random.default_rng(1).integers(0, cfg.vocab_size, (2, 96)).astype(np.int32)
+    with Session(cfg) as s:
+        s.set_params(w)
+        got = s.forward(ids)
+    want = _model(orc, cfg, w).forward(ids)
+    assert rel_err(got, want) < 1e-4
+    assert_close(got, want, 1e-3, 1e-4, "logits")
+
+
+def test_d12_rollout_teacher_forced(orc, d12full):
+    """The benchmark's rollout shape (16 x 16 rows, 256-token prompts, the
+    12-layer model, V = 65536 through the lm_head and the sampler) for its
+    first columns."""
+    cfg, w = d12full
+    _rollout_check(orc, cfg, w, 16, 16, 256, 4, 1.0, groups=(5,))
+
+
+# ---- dense d20 width (BASELINE configs[2] at 2 layers, V 4096) --------------
+@pytest.fixture(scope="module")
+def d20w():
+    cfg = d20_width()
+    assert (cfg.n_embd, cfg.n_head, cfg.n_kv_head) == (1280, 10, 2)
+    assert cfg.window_sizes() == [512, 2048]
+    return cfg, G.init_weights(cfg, seed=20, perturb=0.1)
+
+
+def test_d20_width_rollout_teacher_forced(orc, d20w):
+    """512 rows (32 x 16), 520-token prompts, T = 0.8: GQA ratio 5 with three
+    key splits on both layers (the 512-token window admits 513 keys)."""
+    cfg, w = d20w
+    _rollout_check(orc, cfg, w, 32, 16, 520, 6, 0.8, groups=(0, 31))
+
+
+def test_d20_width_pg_step_chunked(orc, d20w, monkeypatch):
+    cfg, w = d20w
+    _pg_check(orc, cfg, w, B=1, T=540, prompt_len=520, chunk=8, monkeypatch=monkeypatch)
+
+
+# ---- latent d12 width (BASELINE configs[3] at 2 layers, V 4096) -------------
+@pytest.fixture(scope="module")
+def latw():
+    cfg = latent_width()
+    assert (cfg.n_embd, cfg.n_head, cfg.n_kv_head, cfg.mla_latent) == (768, 6, 3, 256)
+    assert (cfg.n_experts, cfg.experts_per_token, cfg.expert_hidden) == (16, 2, 512)
+    return cfg, G.init_weights(cfg, seed=31, perturb=0.02)
+
+
+def test_latent_width_rollout_teacher_forced(orc, latw):
+    cfg, w = latw
+    _rollout_check(orc, cfg, w, 16, 16, 260, 8, 1.0, groups=(0, 15))
+
+
+def test_latent_width_pg_step_chunked(orc, latw, monkeypatch):
+    cfg, w = latw
+    _pg_check(orc, cfg, w, B=2, T=300, prompt_len=150, chunk=100, monkeypatch=monkeypatch)
+
+
+# ---- flash d12 width (BASELINE configs[4] at 6 layers, V 4096) --------------
+@pytest.fixture(scope="module")
+def flashw():
+    cfg = flash_width()
+    assert (cfg.n_embd, cfg.n_head, cfg.n_kv_head, cfg.compression_ratio) == (768, 6, 1, 4)
+    assert (cfg.sparse_topk, cfg.swa_window, cfg.indexer_pool, cfg.indexer_budget) == (16, 512, 8, 128)
+    assert cfg.ced and cfg.reuse_pattern == "FRU" and cfg.expert_hidden == 768
+    return cfg, G.init_weights(cfg, seed=41, perturb=0.02)
+
+
+def test_flash_width_rollout_teacher_forced(orc, flashw):
+    """64 rows (4 x 16), 600-token prompts: 150 compressed blocks exceed the
+    128-candidate budget (hierarchical selection over pools of 8), the
+    512-key window is shorter than the prompt (CED's bounded replay), and
+    decode attention runs the 6:1 group over the selection and the window."""
+    cfg, w = flashw
+    _rollout_check(orc, cfg, w, 4, 16, 600, 8, 1.0, groups=(0, 3))
+
+
+def test_flash_width_pg_step_chunked(orc, flashw, monkeypatch):
+    cfg, w = flashw
+    _pg_check(orc, cfg, w, B=1, T=560, prompt_len=300, chunk=96, monkeypatch=monkeypatch)
