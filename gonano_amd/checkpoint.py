@@ -70,11 +70,34 @@ def load(path: str) -> tuple[dict, dict[str, np.ndarray]]:
     return meta, params
 
 
+# model.Config's JSON names (model/config.go:10-123)
+MODEL_CONFIG_KEYS = frozenset((
+    "sequence_len", "vocab_size", "n_layer", "n_head", "n_kv_head", "n_embd", "window_pattern",
+    "rotary_dims", "compression_ratio", "sparse_top_k", "indexer_dim", "indexer_heads",
+    "indexer_loss_weight", "indexer_pool", "indexer_candidates", "reuse_pattern", "swa_window",
+    "ced", "head_wise_muon", "query_compression_dim", "kv_latent_dim", "mla_latent",
+    "mla_rotary_dims", "num_experts", "num_experts_per_token", "expert_hidden_dim",
+    "shared_expert_hidden_dim", "moe_clamp", "moe_scale", "router_bias_update",
+    "moe_balance_weight"))
+# fields of model.Config this backend does not build (the low-rank query
+# and KV-latent projections of config.go:68-79): a checkpoint that sets them
+# is refused rather than loaded as a different model
+UNSUPPORTED_KEYS = ("query_compression_dim", "kv_latent_dim")
+
+
 def config_from_meta(meta: dict) -> Config:
     """The resolved host Config of meta["model_config"] (model.Config JSON
     names, model/config.go:10-123), with the preset defaults that
-    NewTransformer resolves (MoE, indexer) filled in."""
+    NewTransformer resolves (MoE, indexer) filled in.  Keys model.Config
+    does not have, and the fields this backend does not build, raise
+    CheckpointError."""
     mc = meta["model_config"]
+    unknown = sorted(set(mc) - MODEL_CONFIG_KEYS)
+    if unknown:
+        raise CheckpointError(f"checkpoint: unknown model_config keys {unknown}")
+    for k in UNSUPPORTED_KEYS:
+        if mc.get(k, 0):
+            raise CheckpointError(f"checkpoint: model_config {k} is not supported by this backend")
     cfg = Config(sequence_len=mc["sequence_len"], vocab_size=mc["vocab_size"],
                  n_layer=mc["n_layer"], n_head=mc["n_head"], n_kv_head=mc["n_kv_head"],
                  n_embd=mc["n_embd"], window_pattern=mc.get("window_pattern", "L"),
@@ -87,20 +110,23 @@ def config_from_meta(meta: dict) -> Config:
                  indexer_candidates=mc.get("indexer_candidates", 0),
                  indexer_weight=mc.get("indexer_loss_weight", 0.0),
                  reuse_pattern=mc.get("reuse_pattern", ""), ced=bool(mc.get("ced", False)),
-                 head_wise_muon=bool(mc.get("head_wise_muon", False)))
+                 head_wise_muon=bool(mc.get("head_wise_muon", False)),
+                 router_bias_update=float(mc.get("router_bias_update", 0.0)))
     if mc.get("num_experts", 0) > 0:
         G.enable_moe(cfg, mc["num_experts"], mc.get("num_experts_per_token", 0),
                      mc.get("expert_hidden_dim", 0), mc.get("shared_expert_hidden_dim", 0),
-                     mc.get("moe_scale", 0.0), mc.get("moe_balance_weight", 0.0))
-        if mc.get("moe_clamp", 0.0) > 0:
-            cfg.moe_clamp = float(mc["moe_clamp"])
+                     mc.get("moe_scale", 0.0), mc.get("moe_balance_weight", 0.0),
+                     mc.get("moe_clamp", 0.0))
     cfg.validate()
     return cfg
 
 
 def meta_for(cfg: Config, step: int = 0, **extra) -> dict:
-    """Metadata whose model_config reproduces cfg (resolved values written
-    explicitly; model.Config keeps explicit values as they are)."""
+    """Metadata whose model_config reproduces cfg as model.Config JSON
+    (omitempty): resolved values are written explicitly, which model.Config
+    keeps as they are, except where zero would read back as a default -- a
+    disabled balance loss is written as -1 (MoEBalanceLossWeight: negative
+    disables it)."""
     mc = {"sequence_len": cfg.sequence_len, "vocab_size": cfg.vocab_size,
           "n_layer": cfg.n_layer, "n_head": cfg.n_head, "n_kv_head": cfg.n_kv_head,
           "n_embd": cfg.n_embd, "window_pattern": cfg.window_pattern}
@@ -110,30 +136,46 @@ def meta_for(cfg: Config, step: int = 0, **extra) -> dict:
            "indexer_dim": cfg.indexer_dim, "indexer_heads": cfg.indexer_heads,
            "indexer_pool": cfg.indexer_pool, "indexer_candidates": cfg.indexer_candidates,
            "indexer_loss_weight": cfg.indexer_weight, "reuse_pattern": cfg.reuse_pattern,
-           "ced": cfg.ced, "head_wise_muon": cfg.head_wise_muon}
+           "ced": cfg.ced, "head_wise_muon": cfg.head_wise_muon,
+           "router_bias_update": cfg.router_bias_update}
     if cfg.moe:
         opt.update({"num_experts": cfg.n_experts, "num_experts_per_token": cfg.experts_per_token,
                     "expert_hidden_dim": cfg.expert_hidden,
                     "shared_expert_hidden_dim": cfg.shared_hidden, "moe_clamp": cfg.moe_clamp,
-                    "moe_scale": cfg.moe_scale, "moe_balance_weight": cfg.balance_weight})
+                    "moe_scale": cfg.moe_scale,
+                    "moe_balance_weight": cfg.balance_weight if cfg.balance_weight > 0 else -1.0})
     mc.update({k: v for k, v in opt.items() if v})  # omitempty
     meta = {"step": step, "model_config": mc}
     meta.update(extra)
     return meta
 
 
-def flat_from_params(cfg: Config, params: dict[str, np.ndarray]) -> np.ndarray:
-    """LoadModel (checkpoint.go:130-141) into the session's flat vector:
-    every parameter of cfg must be present with its shape (a file from a
-    different architecture is rejected rather than partly copied)."""
-    out = np.empty(cfg.param_total(), np.float32)
-    for name, rows, cols, off in cfg.param_table():
-        if name not in params:
-            raise CheckpointError(f"checkpoint: missing parameter {name}")
-        a = np.asarray(params[name], np.float32)
-        if a.size != rows * cols:
-            raise CheckpointError(f"checkpoint: {name} has {a.size} values, want {rows}x{cols}")
-        out[off:off + rows * cols] = a.ravel()
+def flat_from_params(cfg: Config, params: dict[str, np.ndarray], base: np.ndarray | None = None,
+                     strict: bool = False) -> np.ndarray:
+    """LoadModel (checkpoint.go:146-155) into the session's flat vector: the
+    model's own initial weights (`base`, default init_weights(cfg)), then
+    every tensor of the file whose name the model has copied over it with Go's
+    copy (the shorter length wins); names the model lacks are ignored and
+    parameters the file lacks keep their initial values.  strict=True
+    instead requires every parameter with its exact size (CheckpointError
+    otherwise), for callers that want a file of another architecture
+    refused rather than partly loaded."""
+    table = cfg.param_table()
+    if strict:
+        for name, rows, cols, _ in table:
+            if name not in params:
+                raise CheckpointError(f"checkpoint: missing parameter {name}")
+            n = np.asarray(params[name]).size
+            if n != rows * cols:
+                raise CheckpointError(f"checkpoint: {name} has {n} values, want {rows}x{cols}")
+    out = np.array(G.init_weights(cfg) if base is None else base, np.float32, copy=True)
+    if out.size != cfg.param_total():
+        raise CheckpointError("checkpoint: base weights do not match the config")
+    for name, rows, cols, off in table:
+        if name in params:
+            a = np.asarray(params[name], np.float32).ravel()
+            n = min(a.size, rows * cols)
+            out[off:off + n] = a[:n]
     return out
 
 

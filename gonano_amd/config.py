@@ -42,7 +42,7 @@ class Config:
     experts_per_token: int = 0   # MoEActiveExperts()
     expert_hidden: int = 0       # MoEExpertHidden()
     shared_hidden: int = 0       # MoESharedHidden()
-    moe_clamp: float = 0.0       # MoEEffectiveClamp()
+    moe_clamp: float = 0.0       # MoEEffectiveClamp() (negative: no clamping)
     moe_scale: float = 0.0       # MoEEffectiveScale()
     balance_weight: float = 0.0  # MoEBalanceLossWeight()
     compression_ratio: int = 0   # Config.CompressionRatio (> 1: HCA compressed layers)
@@ -56,6 +56,8 @@ class Config:
     reuse_pattern: str = ""      # Config.ReusePattern ("FRU": Full / Reindex / Reuse layers)
     ced: bool = False            # Config.CED (causal encoder-decoder split)
     head_wise_muon: bool = False  # Config.HeadWiseMuon (optimizer: per-head q/k views)
+    router_bias_update: float = 0.0  # Config.RouterBiasUpdate as given (0: 0.001); only the
+                                     # router-bias update reads it, which the RL step skips
 
     # -- derived quantities -------------------------------------------------
     @property
@@ -307,18 +309,22 @@ def apply_latent_preset(cfg: Config, mla_latent: int = 0, n_experts: int = 0,
 
 def enable_moe(cfg: Config, n_experts: int = 0, experts_per_token: int = 0,
                expert_hidden: int = 0, shared_hidden: int = 0, moe_scale: float = 0.0,
-               balance_weight: float = 0.0) -> Config:
+               balance_weight: float = 0.0, moe_clamp: float = 0.0) -> Config:
     """Config.enableMoE (model/preset.go:142-152) and ApplyMoEDefaults
     (model/config.go:210-227) with the effective clamp, scale and balance
     weight resolved (config.go:152-188): the DeepSeekMoE feed-forward of the
-    latent and flash presets."""
+    latent and flash presets.  As the reference: a zero clamp is the default
+    10 and a negative one disables clamping (MoEEffectiveClamp and the
+    clamp > 0 tests of kernels/scalar/elementwise.go:105-126); a zero scale
+    is 1; a zero balance weight is 1e-4 and a negative one disables the
+    loss."""
     cfg.n_experts = n_experts if n_experts > 0 else moe_experts_for_depth(cfg.n_layer)
     k = experts_per_token if experts_per_token > 0 else 2
     cfg.experts_per_token = min(k, cfg.n_experts)
     cfg.expert_hidden = expert_hidden if expert_hidden > 0 else cfg.n_embd
     cfg.shared_hidden = shared_hidden if shared_hidden > 0 else cfg.expert_hidden
-    cfg.moe_clamp = DEFAULT_MOE_CLAMP
-    cfg.moe_scale = moe_scale if moe_scale > 0 else 1.0
+    cfg.moe_clamp = float(moe_clamp) if moe_clamp != 0 else DEFAULT_MOE_CLAMP
+    cfg.moe_scale = float(moe_scale) if moe_scale != 0 else 1.0
     if balance_weight < 0:
         cfg.balance_weight = 0.0
     else:

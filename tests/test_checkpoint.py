@@ -57,8 +57,45 @@ def test_roundtrip_model(tmp_path, factory):  # checkpoint_test.go:12-57, 90-130
     meta, params = CK.load(path)
     assert meta["step"] == 12 and meta["val_bpb"] == 1.25
     cfg2 = CK.config_from_meta(meta)
-    assert cfg2.param_table() == cfg.param_table()
+    assert cfg2 == cfg  # the whole resolved Config, not only its parameter table
     np.testing.assert_array_equal(CK.flat_from_params(cfg2, params), w)
+
+
+@pytest.mark.parametrize("clamp,balance,scale,bias", [(-1.0, -1.0, 0.5, 0.002), (0.0, 0.0, 0.0, 0.0),
+                                                      (7.5, 3e-4, -2.0, 0.0)])
+def test_moe_config_semantics_roundtrip(tmp_path, clamp, balance, scale, bias):
+    """model.Config's MoE fields keep their meaning through a file
+    (model/config.go:104-123, 152-188): a negative clamp disables clamping, a
+    negative balance weight disables the loss (written back as -1, not left
+    out, which would read as the 1e-4 default), zeros take the defaults, a
+    negative scale is kept, and router_bias_update survives."""
+    meta = {"step": 0, "model_config": {
+        "sequence_len": 64, "vocab_size": 256, "n_layer": 2, "n_head": 2, "n_kv_head": 1,
+        "n_embd": 128, "window_pattern": "L", "num_experts": 4, "num_experts_per_token": 2,
+        "moe_clamp": clamp, "moe_balance_weight": balance, "moe_scale": scale,
+        "router_bias_update": bias}}
+    cfg = CK.config_from_meta(meta)
+    assert cfg.moe_clamp == (clamp if clamp != 0 else 10.0)
+    assert cfg.balance_weight == (0.0 if balance < 0 else balance if balance > 0 else 1e-4)
+    assert cfg.moe_scale == (scale if scale != 0 else 1.0)
+    assert cfg.router_bias_update == bias
+    path = str(tmp_path / "moe.gn")
+    CK.save(path, CK.meta_for(cfg), CK.params_from_flat(cfg, G.init_weights(cfg, seed=2)))
+    meta2, _ = CK.load(path)
+    assert CK.config_from_meta(meta2) == cfg
+    if balance < 0:
+        assert meta2["model_config"]["moe_balance_weight"] < 0
+
+
+def test_model_config_rejections():
+    base = {"sequence_len": 64, "vocab_size": 256, "n_layer": 1, "n_head": 1, "n_kv_head": 1,
+            "n_embd": 128}
+    with pytest.raises(CK.CheckpointError, match="unknown model_config keys"):
+        CK.config_from_meta({"model_config": dict(base, n_embdd=3)})
+    for key in ("query_compression_dim", "kv_latent_dim"):
+        with pytest.raises(CK.CheckpointError, match="not supported"):
+            CK.config_from_meta({"model_config": dict(base, **{key: 32})})
+    assert CK.config_from_meta({"model_config": dict(base, kv_latent_dim=0)}).n_embd == 128
 
 
 def test_load_rejects_non_checkpoint(tmp_path):  # checkpoint_test.go:185-195
@@ -76,12 +113,35 @@ def test_load_rejects_non_checkpoint(tmp_path):  # checkpoint_test.go:185-195
         CK.load(str(tmp_path / "p.gn"))
 
 
-def test_flat_rejects_other_architecture():
+def test_flat_follows_load_model():
+    """LoadModel (checkpoint.go:146-155): the model's initial weights, then
+    each tensor the file has copied over with Go's copy (the shorter length
+    wins); names the model lacks are ignored, missing parameters keep their
+    initial values.  strict=True refuses such a file instead."""
     cfg = G.dense_d2()
-    params = CK.params_from_flat(cfg, G.init_weights(cfg, seed=0))
+    w = G.init_weights(cfg, seed=0, perturb=0.1)
+    base = G.init_weights(cfg, seed=9)
+    params = CK.params_from_flat(cfg, w)
     del params["lm_head.weight"]
+    params["not.a.parameter"] = np.ones(3, np.float32)
+    params["resid_lambdas"] = np.array([5.0], np.float32)  # shorter than the model's
+    got = CK.flat_from_params(cfg, params, base=base)
+    sl = cfg.param_slices()
+    for name, r, c, off in cfg.param_table():
+        seg = got[off:off + r * c]
+        if name == "lm_head.weight":
+            np.testing.assert_array_equal(seg, base[off:off + r * c])
+        elif name == "resid_lambdas":
+            assert seg[0] == 5.0
+            np.testing.assert_array_equal(seg[1:], base[off + 1:off + r * c])
+        else:
+            np.testing.assert_array_equal(seg, w[off:off + r * c])
+    assert sl["lm_head.weight"][0] >= 0
     with pytest.raises(CK.CheckpointError, match="missing parameter"):
-        CK.flat_from_params(cfg, params)
+        CK.flat_from_params(cfg, params, strict=True)
+    params["lm_head.weight"] = w[:10]
+    with pytest.raises(CK.CheckpointError, match="values, want"):
+        CK.flat_from_params(cfg, params, strict=True)
 
 
 def test_find_last_step(tmp_path):  # checkpoint_test.go:169-183
