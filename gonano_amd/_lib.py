@@ -130,6 +130,7 @@ _SIGS = {
                              C.c_int32, u64p, f32p, i32p, i32p, f32p, C.POINTER(C.c_int32),
                              C.POINTER(C.c_float)]),
     "gn_sample_next_token": (C.c_int, [f32p, i64, i64, u64p, C.c_float, i64, i32p]),
+    "gn_sample_next_token_static": (C.c_int, [f32p, i64, i64, u64p, C.c_float, i64, i32p]),
     "gn_session_set_timing": (C.c_int, [vp, C.c_int]),
     "gn_session_get_timing": (C.c_int, [vp, C.POINTER(GnTiming)]),
     "gn_session_synchronize": (C.c_int, [vp]),

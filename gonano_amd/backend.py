@@ -225,3 +225,16 @@ def sample_next_token(logits: np.ndarray, rng_state: np.ndarray, temperature: fl
     out = np.zeros(rows, np.int32)
     call("gn_sample_next_token", logits, rows, vocab, rng_state, float(temperature), top_k, out)
     return out
+
+
+def sample_next_token_static(logits: np.ndarray, rng_state: np.ndarray, temperature: float,
+                             top_k: int) -> np.ndarray:
+    """sample_next_token through the allocation-free entry point (the
+    library's fixed device staging array: rows <= 65536, rows * vocab <=
+    16 Mi floats; concurrent calls on one device must be serialized)."""
+    logits = _f(np.ascontiguousarray(logits, np.float32))
+    rows, vocab = logits.shape
+    out = np.zeros(rows, np.int32)
+    call("gn_sample_next_token_static", logits, rows, vocab, rng_state, float(temperature), top_k,
+         out)
+    return out

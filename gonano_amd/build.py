@@ -28,6 +28,7 @@ SOURCES = [
     "gn_compress.hip",
     "gn_sparse.hip",
     "gn_sampler.hip",
+    "gn_static.hip",
     "gn_optimizer.hip",
     "gn_session.cpp",
     "gn_tools.cpp",
