@@ -1,6 +1,7 @@
 // gn_tools.cpp - calculator tool and byte-level token codec used by the
 // rollout state machine (inference/engine.go:279-297).
 #include "gn_tools.h"
+#include "gn_common.h"
 
 #include <cctype>
 #include <cmath>
@@ -232,3 +233,20 @@ std::optional<std::string> calculator(const std::string& expr_in) {
 }
 
 }  // namespace gn
+
+extern "C" int gn_use_calculator(const char* expression, char* out, size_t cap, int32_t* ok) {
+  if (!expression || !out || !ok || cap == 0) {
+    gn::set_last_error("gn_use_calculator: null argument");
+    return GN_ERR_INVALID;
+  }
+  auto res = gn::calculator(expression);
+  *ok = res ? 1 : 0;
+  out[0] = 0;
+  if (!res) return GN_OK;
+  if (res->size() + 1 > cap) {
+    gn::set_last_error("gn_use_calculator: result longer than the output buffer");
+    return GN_ERR_INVALID;
+  }
+  memcpy(out, res->c_str(), res->size() + 1);
+  return GN_OK;
+}

@@ -161,6 +161,11 @@ int64_t orc_param_total(const orc_config *cfg);
   void orc_generate_batch##SFX(orc_model##SFX *m, const int32_t *prompt, int P, int S,          \
                                int max_tokens, float temperature, int top_k, uint64_t seed,     \
                                int32_t *rows_out, int32_t *lens_out);                           \
+  /* precomputeRotary (model/rotary.go:16-30) and ApplyRotary for one token's heads           \
+   * (model/rotary.go:43-75), the functions the model uses. */                                   \
+  void orc_rotary_table##SFX(int npos, int R, REAL *cosT, REAL *sinT);                          \
+  void orc_apply_rotary##SFX(REAL *dst, const REAL *src, int heads, int D, int R,               \
+                             const REAL *cw, const REAL *sw);                                    \
   /* GenerateWith's logits for one group with the fed columns given: out [ncols+1][S][V]      \
    * (the prefill's last logits, then those after each column cols[t][S]). */                    \
   void orc_decode_forced##SFX(orc_model##SFX *m, const int32_t *prompt, int P, int S,           \

@@ -60,6 +60,19 @@ static int has_value_embedding(int layer, int n_layer) { /* model/helpers.go:69-
 static int padded_vocab(const orc_config *c) { /* model/config.go:622-624 */
   return ((c->vocab_size + 63) / 64) * 64;
 }
+/* precomputeRotary (model/rotary.go:16-30): cos/sin [npos][R/2] of
+ * position * base^(-2j/R), base 100000, in float64 rounded once. */
+void FN(orc_rotary_table)(int npos, int R, REAL *cosT, REAL *sinT) {
+  int half = R / 2;
+  for (int p = 0; p < npos; p++)
+    for (int j = 0; j < half; j++) {
+      double inv = pow(100000.0, -2.0 * (double)j / (double)R);
+      double f = (double)p * inv;
+      cosT[(int64_t)p * half + j] = R(cos(f));
+      sinT[(int64_t)p * half + j] = R(sin(f));
+    }
+}
+
 static int rotary_dim(const orc_config *c) { /* model/config.go:430-444 */
   int hd = c->n_embd / c->n_head;
   if (c->mla_latent > 0) return c->mla_rope_dims; /* MLARotaryDimension */
@@ -381,13 +394,7 @@ MODEL *FN(orc_model_new)(const orc_config *cfg, const REAL *params) {
   int half = m->R / 2, npos = m->S * ROT_OVER;
   m->cosT = (REAL *)malloc(sizeof(REAL) * npos * half);
   m->sinT = (REAL *)malloc(sizeof(REAL) * npos * half);
-  for (int p = 0; p < npos; p++)
-    for (int j = 0; j < half; j++) {
-      double inv = pow(100000.0, -2.0 * (double)j / (double)m->R);
-      double f = (double)p * inv;
-      m->cosT[p * half + j] = R(cos(f));
-      m->sinT[p * half + j] = R(sin(f));
-    }
+  FN(orc_rotary_table)(npos, m->R, m->cosT, m->sinT);
   return m;
 }
 
@@ -524,12 +531,14 @@ static void linear_bwd(REAL *dx, REAL *dW, const REAL *x, const REAL *g, const R
 }
 static REAL sigmoidR(REAL x) { return R(1.0 / (1.0 + exp(-(double)x))); }
 
-/* model/rotary.go:43-75 on rows of [heads][D] at the given position; sign
- * -1 uses the negated sine table (model/train.go:14-20). */
-static void rope_rows_w(MODEL *m, REAL *dst, const REAL *src, int heads, int D, int pos,
-                        int sign) {
-  int half = m->R / 2, off = D - m->R;
-  const REAL *cw = m->cosT + (int64_t)pos * half, *sw = m->sinT + (int64_t)pos * half;
+/* model/rotary.go:43-75 (ApplyRotary) for the heads of one token: the
+ * trailing R of each head's D channels rotate pairwise with the table row
+ * cw/sw (R/2 entries), y1 = x1 cos + x2 sin, y2 = -x1 sin + x2 cos; the
+ * leading D-R channels are copied.  sign -1 uses the negated sine table
+ * (model/train.go:14-20).  dst may alias src. */
+static void rotary_apply(REAL *dst, const REAL *src, int heads, int D, int R, const REAL *cw,
+                         const REAL *sw, int sign) {
+  int half = R / 2, off = D - R;
   for (int h = 0; h < heads; h++) {
     const REAL *s = src + h * D;
     REAL *d = dst + h * D;
@@ -543,6 +552,19 @@ static void rope_rows_w(MODEL *m, REAL *dst, const REAL *src, int heads, int D, 
     }
     for (int j = 0; j < off; j++) d[j] = tmp[j];
   }
+}
+/* The same, exported: the function the model rotates with (pinned by the
+ * reference's known answers, model/model_test.go:196-211,283-311). */
+void FN(orc_apply_rotary)(REAL *dst, const REAL *src, int heads, int D, int R, const REAL *cw,
+                          const REAL *sw) {
+  rotary_apply(dst, src, heads, D, R, cw, sw, 1);
+}
+/* rows of [heads][D] at the given position of the model's table */
+static void rope_rows_w(MODEL *m, REAL *dst, const REAL *src, int heads, int D, int pos,
+                        int sign) {
+  int half = m->R / 2;
+  rotary_apply(dst, src, heads, D, m->R, m->cosT + (int64_t)pos * half,
+               m->sinT + (int64_t)pos * half, sign);
 }
 static void rope_row(MODEL *m, REAL *dst, const REAL *src, int heads, int pos, int sign) {
   rope_rows_w(m, dst, src, heads, m->D, pos, sign);

@@ -168,6 +168,8 @@ def lib():
                                              C.c_float, C.c_int, C.c_uint64, _i32p, _i32p]),
             "orc_decode_forced" + sfx: (v, [C.c_void_p, _i32p, C.c_int, C.c_int, _i32p, C.c_int,
                                             fp]),
+            "orc_rotary_table" + sfx: (v, [C.c_int, C.c_int, fp, fp]),
+            "orc_apply_rotary" + sfx: (v, [fp, fp, C.c_int, C.c_int, C.c_int, fp, fp]),
             "orc_rl_step" + sfx: (C.c_double, [C.c_void_p, _i32p, C.c_int, C.c_int, C.c_int,
                                                C.c_int, C.c_float, C.c_int, _u64p, _f32p, _i32p,
                                                _i32p, _f32p, C.POINTER(C.c_int32), _i32p, _i32p,
@@ -427,6 +429,26 @@ def sample_next_token(logits: np.ndarray, rng: GoRNG, temperature: float, top_k:
     out = np.zeros(rows, np.int32)
     lib().orc_sample_next_token(logits, rows, vocab, C.byref(rng.state), float(temperature),
                                 top_k, out)
+    return out
+
+
+def rotary_table(positions: int, rotary_dim: int):
+    """precomputeRotary (model/rotary.go:16-30): cos, sin [positions, R/2]."""
+    c = np.zeros((positions, rotary_dim // 2), np.float32)
+    s = np.zeros_like(c)
+    lib().orc_rotary_table_f32(positions, rotary_dim, c, s)
+    return c, s
+
+
+def apply_rotary(x: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.ndarray:
+    """ApplyRotary (model/rotary.go:43-75) of one token's heads x [heads, D]
+    with one table row (R/2 entries each): the model's own rotation."""
+    x = np.ascontiguousarray(x, np.float32)
+    heads, D = x.shape
+    out = np.zeros_like(x)
+    c = np.ascontiguousarray(cos_row, np.float32)
+    s = np.ascontiguousarray(sin_row, np.float32)
+    lib().orc_apply_rotary_f32(out, x, heads, D, 2 * c.size, c, s)
     return out
 
 

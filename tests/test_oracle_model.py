@@ -8,7 +8,8 @@
   jump-ahead) and PCG64DXSM (output permutation);
 * the top-k threshold against a sort, and sampler properties
   (inference/inference_test.go:11-30);
-* the RoPE known answers (model/model_test.go:196-311).
+* the RoPE known answers (model/model_test.go:196-311) on the oracle's own
+  rotation and its table's frequencies.
 """
 import math
 
@@ -140,10 +141,46 @@ def test_sampler_stream_positions(orc):
 
 
 # ------------------------------------------------------------------- model --
-def test_rope_known_answers():
-    """model/model_test.go:196-311 restated on the GPU's host mirror is not
-    needed; the oracle's rope is exercised through the model checks below, and
-    the quarter-turn / partial-rotation answers through a 1-layer probe."""
+def test_rope_known_answers(orc):
+    """The oracle's RoPE (the function its model rotates with) against the
+    reference's known answers: a quarter turn of [3, 4] at position 1 gives
+    [4, -3] (model/model_test.go:196-211); with D = 4 and R = 2 the leading
+    channels stay and the trailing pair turns, [10, 20, 3, 4] -> [10, 20, 4,
+    -3] (:283-300).  Then its table: rotation preserves each head's norm
+    (:302-311); the angle of column j at position p is p * 100000^(-2j/R)
+    (rotary.go:10,16-30: base 100000, frequencies over the rotary width, not
+    the head width), read back through atan2, which a wrong base, a
+    transposed table or a half-split at the wrong offset fails."""
+    cos_row, sin_row = np.array([0.0], np.float32), np.array([1.0], np.float32)
+    got = orc.apply_rotary(np.array([[3.0, 4.0]], np.float32), cos_row, sin_row)
+    assert got.tolist() == [[4.0, -3.0]]
+    got = orc.apply_rotary(np.array([[10.0, 20.0, 3.0, 4.0]], np.float32), cos_row, sin_row)
+    assert got.tolist() == [[10.0, 20.0, 4.0, -3.0]]
+    # two heads: each rotates on its own trailing pair
+    got = orc.apply_rotary(np.array([[1, 2, 3, 4], [5, 6, 7, 8]], np.float32), cos_row, sin_row)
+    assert got.tolist() == [[1, 2, 4, -3], [5, 6, 8, -7]]
+    # norm preservation with the real table (R = D = 8, 32 positions)
+    c, sn = orc.rotary_table(32, 8)
+    x = np.random.default_rng(3).standard_normal((2, 8)).astype(np.float32)
+    for p in range(32):
+        y = orc.apply_rotary(x, c[p], sn[p])
+        assert np.allclose(np.linalg.norm(y, axis=1), np.linalg.norm(x, axis=1), rtol=1e-6)
+    # the frequencies: partial RoPE over R = 64 of a 128-wide head
+    c, sn = orc.rotary_table(8, 64)
+    assert c.shape == (8, 32)
+    assert np.all(c[0] == 1) and np.all(sn[0] == 0)
+    ang = np.arctan2(sn[1].astype(np.float64), c[1].astype(np.float64))
+    want = 100000.0 ** (-2.0 * np.arange(32) / 64.0)
+    assert np.allclose(ang, want, rtol=1e-6, atol=1e-7)
+    assert abs(ang[0] - 1.0) < 1e-7 and abs(ang[16] - 100000.0 ** -0.5) < 1e-9
+    # a position's angles are that multiple of position 1's (mod 2 pi)
+    ang5 = np.arctan2(sn[5].astype(np.float64), c[5].astype(np.float64))
+    assert np.allclose(np.cos(ang5), np.cos(5 * want), atol=1e-6)
+    # rotation by p then by q equals rotation by p + q (rotations compose)
+    big_c, big_s = orc.rotary_table(16, 8)
+    y = orc.apply_rotary(orc.apply_rotary(x, big_c[3], big_s[3]), big_c[4], big_s[4])
+    assert np.allclose(y, orc.apply_rotary(x, big_c[7], big_s[7]), atol=1e-5)
+    # the config side: R defaults to the head width and must be even and <= D
     cfg = tiny_cfg()
     assert cfg.rotary_dimension == 16
     assert G.Config(16, 16, 1, 4, 4, 32, "L", 4).rotary_dimension == 4
