@@ -62,6 +62,28 @@ class GnTiming(C.Structure):
     ]
 
 
+# int32_t (*)(void *user, const int32_t *call, int32_t n, int32_t *out, int32_t cap)
+GnToolFn = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.POINTER(C.c_int32), C.c_int32,
+                       C.POINTER(C.c_int32), C.c_int32)
+
+
+class GnGenerateOptions(C.Structure):
+    _fields_ = [
+        ("thinking", C.c_int32),
+        ("thinking_budget", C.c_int32),
+        ("bos", C.c_int32),
+        ("assistant_end", C.c_int32),
+        ("tool_start", C.c_int32),
+        ("tool_end", C.c_int32),
+        ("tool_output_start", C.c_int32),
+        ("tool_output_end", C.c_int32),
+        ("think_start", C.c_int32),
+        ("think_end", C.c_int32),
+        ("tool", GnToolFn),
+        ("tool_user", C.c_void_p),
+    ]
+
+
 class HipError(RuntimeError):
     """A gn_* call returned a non-zero gn_status (the reference panics)."""
 
@@ -129,6 +151,14 @@ _SIGS = {
     "gn_rl_step": (C.c_int, [vp, i32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
                              C.c_int32, u64p, f32p, i32p, i32p, f32p, C.POINTER(C.c_int32),
                              C.POINTER(C.c_float)]),
+    "gn_generate_options_default": (C.c_int, [C.POINTER(GnGenerateOptions)]),
+    "gn_generate_batch_with": (C.c_int, [vp, i32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                         C.c_float, C.c_int32, u64p, C.POINTER(GnGenerateOptions),
+                                         i32p, i32p, vp]),
+    "gn_rl_step_with": (C.c_int, [vp, i32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
+                                  C.c_int32, u64p, C.POINTER(GnGenerateOptions), f32p, i32p, i32p,
+                                  f32p, C.POINTER(C.c_int32), C.POINTER(C.c_float)]),
+    "gn_use_calculator": (C.c_int, [C.c_char_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_int32)]),
     "gn_sample_next_token": (C.c_int, [f32p, i64, i64, u64p, C.c_float, i64, i32p]),
     "gn_sample_next_token_static": (C.c_int, [f32p, i64, i64, u64p, C.c_float, i64, i32p]),
     "gn_session_set_timing": (C.c_int, [vp, C.c_int]),

@@ -13,6 +13,8 @@
 //
 // Scores carry no 1/sqrt(D) factor: q and k arrive already multiplied by 1.2
 // after their RMSNorm (model/attention.go:252-256).
+#include <hip/hip_ext.h>
+
 #include "gn_model.h"
 
 namespace gn {
@@ -321,9 +323,14 @@ __global__ __launch_bounds__(64 * NW) void decode_attn_kernel(DecodeAttnArgs a) 
   decode_attn_body<R, NW>(a);
 }
 template <int R>
-static void launch_decode_attn(dim3 grid, hipStream_t st, const DecodeAttnArgs& a) {
+static void launch_decode_attn(dim3 grid, hipStream_t st, const DecodeAttnArgs& a,
+                               hipEvent_t stop) {
   constexpr int NW = DecWaves<R>::NW;
-  hipLaunchKernelGGL((decode_attn_kernel<R, NW>), grid, dim3(64 * NW), 0, st, a);
+  if (a.t_start || stop)
+    hipExtLaunchKernelGGL((decode_attn_kernel<R, NW>), grid, dim3(64 * NW), 0, st, a.t_start,
+                          stop, 0, a);
+  else
+    hipLaunchKernelGGL((decode_attn_kernel<R, NW>), grid, dim3(64 * NW), 0, st, a);
 }
 
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
@@ -395,19 +402,24 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
                               a.part_floats),
            "decode attention: the split partial buffer is too small for this key range");
   const dim3 grid(a.rows * a.Hkv, a.nsplit_max);
+  hipEvent_t stop = combine ? nullptr : a.t_stop;
   switch (a.Hq / a.Hkv) {
-    case 1: launch_decode_attn<1>(grid, st, a); break;
-    case 2: launch_decode_attn<2>(grid, st, a); break;
-    case 3: launch_decode_attn<3>(grid, st, a); break;
-    case 4: launch_decode_attn<4>(grid, st, a); break;
-    case 5: launch_decode_attn<5>(grid, st, a); break;
-    case 6: launch_decode_attn<6>(grid, st, a); break;
-    case 7: launch_decode_attn<7>(grid, st, a); break;
-    case 8: launch_decode_attn<8>(grid, st, a); break;
+    case 1: launch_decode_attn<1>(grid, st, a, stop); break;
+    case 2: launch_decode_attn<2>(grid, st, a, stop); break;
+    case 3: launch_decode_attn<3>(grid, st, a, stop); break;
+    case 4: launch_decode_attn<4>(grid, st, a, stop); break;
+    case 5: launch_decode_attn<5>(grid, st, a, stop); break;
+    case 6: launch_decode_attn<6>(grid, st, a, stop); break;
+    case 7: launch_decode_attn<7>(grid, st, a, stop); break;
+    case 8: launch_decode_attn<8>(grid, st, a, stop); break;
   }
   GN_HIP(hipGetLastError());
   if (!combine) return;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(a.rows * a.Hq), dim3(HD), 0, st, a);
+  if (a.t_stop)
+    hipExtLaunchKernelGGL(decode_combine_kernel, dim3(a.rows * a.Hq), dim3(HD), 0, st, nullptr,
+                          a.t_stop, 0, a);
+  else
+    hipLaunchKernelGGL(decode_combine_kernel, dim3(a.rows * a.Hq), dim3(HD), 0, st, a);
   GN_HIP(hipGetLastError());
 }
 

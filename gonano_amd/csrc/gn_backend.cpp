@@ -246,7 +246,10 @@ int gn_indexer_block_max(float* d, const float* s, int64_t rows, int64_t blocks,
 // kernels/backend.go:125-140 -----------------------------------------------
 int gn_topk_indices(int32_t* d, const float* scores, int64_t rows, int64_t count, int64_t k) {
   return guard([&] {
-    if (count == 0 || k <= 0 || rows <= 0) return;
+    GN_CHECK(rows >= 0 && count >= 0 && k >= 0, "negative extent");
+    if (count == 0 || k == 0 || rows == 0) return;
+    check_ptrs(rows * count, {scores});
+    check_ptrs(rows * k, {d});
     ThreadCtx& c = ctx();
     float* ds = up(c, "a", scores, rows * count);
     int32_t* dd = dev<int32_t>(c, "i", rows * k);
@@ -261,7 +264,11 @@ int gn_topk_indices(int32_t* d, const float* scores, int64_t rows, int64_t count
 int gn_moe_gate_topk(const float* logits, const float* bias, float* probs, int32_t* selected,
                      float* weights, int64_t rows, int64_t experts, int64_t k) {
   return guard([&] {
-    if (rows <= 0 || experts <= 0) return;
+    GN_CHECK(rows >= 0 && experts >= 0 && k >= 0, "negative extent");
+    if (rows == 0 || experts == 0) return;
+    check_ptrs(rows * experts, {logits, probs});
+    check_ptrs(experts, {bias});
+    check_ptrs(rows * k, {selected, weights});
     ThreadCtx& c = ctx();
     float* dl = up(c, "a", logits, rows * experts);
     float* db = up(c, "b", bias, experts);
@@ -313,7 +320,9 @@ int gn_grouped_matmul_transposed(float* d, const float* in, const float* w, cons
 // kernels/backend.go:146-152 -----------------------------------------------
 int gn_softmax_last_dim(float* d, const float* s, int64_t rows, int64_t cols) {
   return guard([&] {
-    if (rows <= 0 || cols <= 0) return;
+    GN_CHECK(rows >= 0 && cols >= 0, "negative extent");
+    if (rows == 0 || cols == 0) return;
+    check_ptrs(rows * cols, {d, s});
     ThreadCtx& c = ctx();
     float* ds = up(c, "a", s, rows * cols);
     float* dd = dev<float>(c, "d", rows * cols);
@@ -324,7 +333,9 @@ int gn_softmax_last_dim(float* d, const float* s, int64_t rows, int64_t cols) {
 }
 int gn_rmsnorm_last_dim(float* d, const float* s, int64_t rows, int64_t cols, float eps) {
   return guard([&] {
-    if (rows <= 0 || cols <= 0) return;
+    GN_CHECK(rows >= 0 && cols >= 0, "negative extent");
+    if (rows == 0 || cols == 0) return;
+    check_ptrs(rows * cols, {d, s});
     ThreadCtx& c = ctx();
     float* ds = up(c, "a", s, rows * cols);
     float* dd = dev<float>(c, "d", rows * cols);

@@ -36,7 +36,10 @@ void set_last_error(const std::string& msg);
     if (!(cond)) throw ::gn::Error(GN_ERR_INVALID, std::string(msg));                  \
   } while (0)
 
-// Runs body, mapping exceptions to status codes.
+// Runs body, mapping exceptions to status codes.  A failed runtime call
+// (an allocation beyond the device memory, say) stays recorded as the
+// thread's last HIP error; it is cleared here, so the next call's launch
+// checks do not report it again.
 template <class F>
 int guard(F&& body) {
   try {
@@ -44,6 +47,7 @@ int guard(F&& body) {
     return GN_OK;
   } catch (const Error& e) {
     set_last_error(e.what());
+    if (e.code == GN_ERR_HIP || e.code == GN_ERR_OOM) (void)hipGetLastError();
     return e.code;
   } catch (const std::bad_alloc&) {
     set_last_error("host allocation failed");

@@ -16,6 +16,8 @@
 // (token, slot) order) is computed on the device; the expert products are
 // the GEMM's expert-grouped modes, so the launch shape never depends on the
 // routing and the decode step can be captured in a graph.
+#include <hip/hip_ext.h>
+
 #include "gn_model.h"
 
 namespace gn {
@@ -376,19 +378,33 @@ void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
   hipLaunchKernelGGL(mla_decode_prep_kernel, dim3(a.rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
   const dim3 grid(a.rows, ns_max);
+  hipEvent_t stop = ns_max > 1 ? nullptr : a.t_stop;
+#define GN_MLA_ATTN(H)                                                                        \
+  do {                                                                                        \
+    if (a.t_start || stop)                                                                    \
+      hipExtLaunchKernelGGL(mla_decode_attn_kernel<H>, grid, dim3(256), 0, st, a.t_start,    \
+                            stop, 0, a);                                                      \
+    else                                                                                      \
+      hipLaunchKernelGGL(mla_decode_attn_kernel<H>, grid, dim3(256), 0, st, a);               \
+  } while (0)
   switch (a.Hq) {
-    case 1: hipLaunchKernelGGL(mla_decode_attn_kernel<1>, grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(mla_decode_attn_kernel<2>, grid, dim3(256), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(mla_decode_attn_kernel<3>, grid, dim3(256), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(mla_decode_attn_kernel<4>, grid, dim3(256), 0, st, a); break;
-    case 5: hipLaunchKernelGGL(mla_decode_attn_kernel<5>, grid, dim3(256), 0, st, a); break;
-    case 6: hipLaunchKernelGGL(mla_decode_attn_kernel<6>, grid, dim3(256), 0, st, a); break;
-    case 7: hipLaunchKernelGGL(mla_decode_attn_kernel<7>, grid, dim3(256), 0, st, a); break;
-    case 8: hipLaunchKernelGGL(mla_decode_attn_kernel<8>, grid, dim3(256), 0, st, a); break;
+    case 1: GN_MLA_ATTN(1); break;
+    case 2: GN_MLA_ATTN(2); break;
+    case 3: GN_MLA_ATTN(3); break;
+    case 4: GN_MLA_ATTN(4); break;
+    case 5: GN_MLA_ATTN(5); break;
+    case 6: GN_MLA_ATTN(6); break;
+    case 7: GN_MLA_ATTN(7); break;
+    case 8: GN_MLA_ATTN(8); break;
   }
+#undef GN_MLA_ATTN
   GN_HIP(hipGetLastError());
   if (ns_max > 1) {
-    hipLaunchKernelGGL(mla_decode_combine_kernel, dim3(a.rows * a.Hq), dim3(256), 0, st, a);
+    if (a.t_stop)
+      hipExtLaunchKernelGGL(mla_decode_combine_kernel, dim3(a.rows * a.Hq), dim3(256), 0, st,
+                            nullptr, a.t_stop, 0, a);
+    else
+      hipLaunchKernelGGL(mla_decode_combine_kernel, dim3(a.rows * a.Hq), dim3(256), 0, st, a);
     GN_HIP(hipGetLastError());
   }
 }

@@ -81,6 +81,10 @@ struct DecodeAttnArgs {
   int nsplit_max;      // set by the launcher: grid.y and the split stride of part
   int64_t part_floats = 0;  // capacity of part in floats; the launcher rejects a
                             // grid whose split layout would not fit
+  // optional events recorded by the dispatch itself (hipExtLaunchKernelGGL):
+  // t_start when the attention kernel starts, t_stop when the last kernel of
+  // the call (the combine, when launched) ends -- the calls' own duration
+  hipEvent_t t_start = nullptr, t_stop = nullptr;
 };
 // Split capacity a part buffer needs for launches with these arguments
 // (window, maxSeq, ratio, maxBlocks).
@@ -230,6 +234,9 @@ struct MlaDecodeArgs {
   const int* pos_dev; // when set, the position is read on the device
   int part_splits;    // splits the part buffer holds per row
   int nsplit_max;     // set by the launcher
+  // optional events recorded by the dispatch (hipExtLaunchKernelGGL): at the
+  // start of the attention kernel and the end of the call's last kernel
+  hipEvent_t t_start = nullptr, t_stop = nullptr;
 };
 // Largest number of key splits a decode step with this window and cache
 // length can use (sizes MlaDecodeArgs::part).

@@ -215,21 +215,20 @@ static void collect_timing(gn_session* s, double* gemm_ms, double* gemm_flops, i
   s->event_next = 0;
 }
 
-// Decode attention is timed over a burst of back-to-back launches of the
-// same call (the kernels only read the cache and overwrite their outputs,
-// so repeating them leaves the step's result unchanged): the event pair then
-// measures the kernels' own duration rather than one launch plus the gaps
-// around it.
-static constexpr int ATTN_BURST = 4;
-template <class F>
-static void timed_attention(gn_session* s, double bytes, F&& launch) {
-  hipEvent_t e0 = next_event(s), e1 = next_event(s);
-  GN_HIP(hipEventRecord(e0, s->stream));
-  for (int i = 0; i < ATTN_BURST; i++) launch();
-  GN_HIP(hipEventRecord(e1, s->stream));
-  s->attn_events.push_back({e0, e1});
-  s->attn_ev_bytes.push_back(bytes * ATTN_BURST);
-  s->attn_ev_launches.push_back(ATTN_BURST);
+// Decode attention is timed per call, in place in the step: the launcher
+// records the event pair through the dispatch itself (hipExtLaunchKernelGGL:
+// the start of the attention kernel, the end of the call's last kernel), so
+// the pair measures the kernels' own duration, as a kernel trace does, and
+// not the launch gaps around them.
+template <class Args, class F>
+static void timed_attention(gn_session* s, double bytes, Args& args, F&& launch) {
+  args.t_start = next_event(s);
+  args.t_stop = next_event(s);
+  launch();
+  s->attn_events.push_back({args.t_start, args.t_stop});
+  s->attn_ev_bytes.push_back(bytes);
+  s->attn_ev_launches.push_back(1);
+  args.t_start = args.t_stop = nullptr;
 }
 
 template <typename T>
@@ -1595,8 +1594,55 @@ struct RowState {  // inference/engine.go:11-22
   size_t forced_pos = 0;
   bool in_tool = false;
   std::vector<int> tool;
+  bool in_thinking = false;
+  int thinking_tokens = 0;
   bool completed = false;
 };
+
+// GenerateOptions with the engine's tokenizer ids and tool registry
+// (inference/engine.go:25-34, 215-224): the byte-level tokenizer
+// (tokenizer/special.go:19-31), thinking off and the built-in calculator.
+static gn_generate_options default_generate_options() {
+  gn_generate_options o{};
+  o.thinking = 0;
+  o.thinking_budget = 0;
+  o.bos = TOK_BOS;
+  o.assistant_end = TOK_ASSISTANT_END;
+  o.tool_start = TOK_TOOL_START;
+  o.tool_end = TOK_TOOL_END;
+  o.tool_output_start = TOK_TOOL_OUTPUT_START;
+  o.tool_output_end = TOK_TOOL_OUTPUT_END;
+  o.think_start = TOK_THINK_START;
+  o.think_end = TOK_THINK_END;
+  o.tool = nullptr;
+  o.tool_user = nullptr;
+  return o;
+}
+
+// Registry.Execute(Tokenizer.Decode(call)) then Tokenizer.Encode of the
+// result (engine.go:282-296): the caller's tool, or the built-in calculator
+// over the byte-level tokenizer.  Appends <|tool_output_start|>, the result
+// ids and <|tool_output_end|> to the row's forced tokens when a tool
+// understands the call.
+static void run_tool(const gn_generate_options& o, RowState& rs) {
+  std::vector<int> result;
+  if (o.tool) {
+    std::vector<int32_t> call(rs.tool.begin(), rs.tool.end());
+    std::vector<int32_t> out(4096);
+    int32_t n = o.tool(o.tool_user, call.data(), (int32_t)call.size(), out.data(),
+                       (int32_t)out.size());
+    if (n < 0) return;
+    GN_CHECK(n <= (int32_t)out.size(), "tool: result longer than 4096 tokens");
+    result.assign(out.begin(), out.begin() + n);
+  } else {
+    auto res = calculator(decode_tokens(rs.tool));
+    if (!res) return;
+    result = encode_bytes(*res);
+  }
+  rs.forced.push_back(o.tool_output_start);
+  rs.forced.insert(rs.forced.end(), result.begin(), result.end());
+  rs.forced.push_back(o.tool_output_end);
+}
 
 // Absorbed decode weights (mla.go:233-273 folded): per query head h with KV
 // head kv, W_qabs[h] = KeyUp_kv^T . QueryUp_h ([lat, lat]: the content query
@@ -1654,7 +1700,7 @@ static void mla_decode_layer(gn_session* s, const Layer& ly, int l, int rows, in
   md.maxSeq = maxSeq; md.window = ly.window; md.pos = pos; md.pos_dev = dpos;
   if (s->timing && !s->capturing) {
     const int keys = pos + 1 - std::max(0, pos - ly.window);
-    timed_attention(s, (double)rows * keys * (lat + s->Hkv * s->rd) * 4.0,
+    timed_attention(s, (double)rows * keys * (lat + s->Hkv * s->rd) * 4.0, md,
                     [&] { launch_mla_decode(md, st); });
   } else {
     launch_mla_decode(md, st);
@@ -1831,7 +1877,7 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
               (s->swa > 0 ? pos - std::max(0, pos - s->swa) + 1 : 0);
     }
     if (s->timing && !s->capturing) {
-      timed_attention(s, 2.0 * rows * Hkv * HD * 4.0 * nkeys,
+      timed_attention(s, 2.0 * rows * Hkv * HD * 4.0 * nkeys, da,
                       [&] { launch_decode_attention(da, st); });
     } else {
       launch_decode_attention(da, st);
@@ -1954,7 +2000,7 @@ static int prefill_ced(gn_session* s, SeqBuffers& sb, const int32_t* prompts, in
 
 static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S, int N,
                      float temperature, int top_k, const uint64_t* seeds, int32_t* rows_out,
-                     int32_t* lens_out) {
+                     int32_t* lens_out, const gn_generate_options& opt, int32_t* masks_out) {
   GN_CHECK(G > 0 && S > 0 && P > 0 && N >= 0, "generate: bad sizes");
   GN_CHECK(P + N <= s->S * 10, "generate: context exceeds the rotary table");
   GN_CHECK(P <= s->S, "model: sequence longer than rotary cache");
@@ -1972,6 +2018,7 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   for (int r = 0; r < rows; r++) {
     memcpy(rows_out + (int64_t)r * W, prompts + (int64_t)(r / S) * P, sizeof(int32_t) * P);
     lens_out[r] = P;
+    if (masks_out) memset(masks_out + (int64_t)r * W, 0, sizeof(int32_t) * W);
   }
   if (N == 0) return;
   // 1) batch prefill of every prompt (engine.go:141-173)
@@ -2067,6 +2114,12 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   //    replayed; the step position, the column and the group streams'
   //    base states reach the device through small copies before each launch.
   std::vector<RowState> states(rows);
+  // a prompt that ends inside a reasoning trace starts every row of its group
+  // there, so the budget counts from the first generated token (engine.go:226-236)
+  const bool think = opt.thinking != 0 || opt.thinking_budget > 0;
+  if (think)
+    for (int r = 0; r < rows; r++)
+      states[r].in_thinking = prompts[(int64_t)(r / S) * P + P - 1] == opt.think_start;
   std::vector<u128h> stream(G);
   for (int g = 0; g < G; g++) stream[g] = new_rng_state(seeds[g]);
   uint64_t* dbase = A<uint64_t>(s, "rng_base", 2 * G);
@@ -2136,36 +2189,45 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
     }
     GN_HIP(hipMemcpyAsync(sampled, dtok, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
     GN_HIP(hipStreamSynchronize(st));
+    // the row state machine (engine.go:258-314)
     for (int r = 0; r < rows; r++) {
       RowState& rs = states[r];
       int tok;
-      if (rs.forced_pos < rs.forced.size()) tok = rs.forced[rs.forced_pos++];
+      const bool forced = rs.forced_pos < rs.forced.size();
+      if (forced) tok = rs.forced[rs.forced_pos++];
       else tok = sampled[r];
       column[r] = tok;
-      if (tok == TOK_ASSISTANT_END || tok == TOK_BOS) rs.completed = true;
-      if (tok == TOK_TOOL_START) {
+      if (tok == opt.assistant_end || tok == opt.bos) rs.completed = true;
+      if (tok == opt.tool_start) {
         rs.in_tool = true;
         rs.tool.clear();
-      } else if (tok == TOK_TOOL_END && rs.in_tool) {
+      } else if (tok == opt.tool_end && rs.in_tool) {
         rs.in_tool = false;
-        if (!rs.tool.empty()) {
-          auto res = calculator(decode_tokens(rs.tool));
-          if (res) {
-            rs.forced.push_back(TOK_TOOL_OUTPUT_START);
-            for (int id : encode_bytes(*res)) rs.forced.push_back(id);
-            rs.forced.push_back(TOK_TOOL_OUTPUT_END);
-          }
-        }
+        if (!rs.tool.empty()) run_tool(opt, rs);
         rs.tool.clear();
       } else if (rs.in_tool) {
         rs.tool.push_back(tok);
       }
-      // GenerateBatchWith's collection (engine.go:349-366)
+      if (think) {  // thinking-trace tracking and the budget (engine.go:298-313)
+        if (tok == opt.think_start) {
+          rs.in_thinking = true;
+          rs.thinking_tokens = 0;
+        } else if (tok == opt.think_end && rs.in_thinking) {
+          rs.in_thinking = false;
+        } else if (rs.in_thinking) {
+          rs.thinking_tokens++;
+          if (opt.thinking_budget > 0 && rs.thinking_tokens >= opt.thinking_budget)
+            rs.forced.push_back(opt.think_end);
+        }
+      }
+      // GenerateBatchWith's collection (engine.go:349-366): 1 for sampled,
+      // 0 for forced tokens
       if (!done[r]) {
-        if (tok == TOK_ASSISTANT_END || tok == TOK_BOS) {
+        if (tok == opt.assistant_end || tok == opt.bos) {
           done[r] = 1;
           ndone++;
         } else {
+          if (masks_out) masks_out[(int64_t)r * W + lens_out[r]] = forced ? 0 : 1;
           rows_out[(int64_t)r * W + lens_out[r]++] = tok;
         }
       }
@@ -2203,12 +2265,18 @@ int gn_session_create(const gn_config* config, int device, gn_session** out) {
     GN_HIP(hipGetDeviceCount(&n));
     GN_CHECK(device >= 0 && device < n, "device index out of range");
     GN_HIP(hipSetDevice(device));
-    auto s = std::make_unique<gn_session>();
+    gn_session* s = new gn_session();
     s->device = device;
-    GN_HIP(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
-    s->arena = std::make_unique<DeviceArena>(s->stream);
-    build_session(s.get(), *config);
-    *out = s.release();
+    try {
+      GN_HIP(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+      s->arena = std::make_unique<DeviceArena>(s->stream);
+      build_session(s, *config);
+    } catch (...) {  // a rejected config or a failed allocation frees what was made
+      if (s->stream) (void)gn_session_destroy(s);
+      else delete s;
+      throw;
+    }
+    *out = s;
   });
 }
 
@@ -2320,14 +2388,31 @@ int gn_forward(gn_session* s, const int32_t* ids, int32_t B, int32_t T, float* l
   });
 }
 
+int gn_generate_options_default(gn_generate_options* out) {
+  return guard([&] {
+    GN_CHECK(out, "null argument");
+    *out = default_generate_options();
+  });
+}
+
 int gn_generate_batch(gn_session* s, const int32_t* prompts, int32_t groups, int32_t prompt_len,
                       int32_t samples, int32_t max_tokens, float temperature, int32_t top_k,
                       const uint64_t* seeds, int32_t* rows_out, int32_t* lengths_out) {
+  return gn_generate_batch_with(s, prompts, groups, prompt_len, samples, max_tokens, temperature,
+                                top_k, seeds, nullptr, rows_out, lengths_out, nullptr);
+}
+
+int gn_generate_batch_with(gn_session* s, const int32_t* prompts, int32_t groups,
+                           int32_t prompt_len, int32_t samples, int32_t max_tokens,
+                           float temperature, int32_t top_k, const uint64_t* seeds,
+                           const gn_generate_options* options, int32_t* rows_out,
+                           int32_t* lengths_out, int32_t* masks_out) {
   return guard([&] {
     GN_CHECK(s && prompts && seeds && rows_out && lengths_out, "null argument");
     GN_HIP(hipSetDevice(s->device));
+    const gn_generate_options o = options ? *options : default_generate_options();
     generate(s, prompts, groups, prompt_len, samples, max_tokens, temperature, top_k, seeds,
-             rows_out, lengths_out);
+             rows_out, lengths_out, o, masks_out);
   });
 }
 
@@ -2404,11 +2489,21 @@ int gn_rl_step(gn_session* s, const int32_t* prompts, int32_t G, int32_t P, int3
                float temperature, int32_t top_k, const uint64_t* seeds, const float* rewards,
                int32_t* rows_out, int32_t* lens_out, float* adv_out, int32_t* max_len_out,
                float* loss_out) {
+  return gn_rl_step_with(s, prompts, G, P, S, N, temperature, top_k, seeds, nullptr, rewards,
+                         rows_out, lens_out, adv_out, max_len_out, loss_out);
+}
+
+int gn_rl_step_with(gn_session* s, const int32_t* prompts, int32_t G, int32_t P, int32_t S,
+                    int32_t N, float temperature, int32_t top_k, const uint64_t* seeds,
+                    const gn_generate_options* options, const float* rewards, int32_t* rows_out,
+                    int32_t* lens_out, float* adv_out, int32_t* max_len_out, float* loss_out) {
   return guard([&] {
     GN_CHECK(s && prompts && seeds && rewards && rows_out && lens_out && adv_out && max_len_out,
              "null argument");
     GN_HIP(hipSetDevice(s->device));
-    generate(s, prompts, G, P, S, N, temperature, top_k, seeds, rows_out, lens_out);
+    const gn_generate_options o = options ? *options : default_generate_options();
+    generate(s, prompts, G, P, S, N, temperature, top_k, seeds, rows_out, lens_out, o, nullptr);
+    const int32_t pad = o.assistant_end;
     const int Bt = G * S, W = P + N;
     // group-relative advantages in float32 (main.go:139-155)
     for (int g = 0; g < G; g++) {
@@ -2426,8 +2521,8 @@ int gn_rl_step(gn_session* s, const int32_t* prompts, int32_t G, int32_t P, int3
     std::vector<int32_t> inputs((size_t)Bt * T), targets((size_t)Bt * T);
     for (int b = 0; b < Bt; b++)
       for (int t = 0; t < T; t++) {
-        int32_t in = t < lens_out[b] ? rows_out[(int64_t)b * W + t] : TOK_ASSISTANT_END;
-        int32_t tg = t + 1 < lens_out[b] ? rows_out[(int64_t)b * W + t + 1] : TOK_ASSISTANT_END;
+        int32_t in = t < lens_out[b] ? rows_out[(int64_t)b * W + t] : pad;
+        int32_t tg = t + 1 < lens_out[b] ? rows_out[(int64_t)b * W + t + 1] : pad;
         if (t < P) tg = -1;
         inputs[(size_t)b * T + t] = in;
         targets[(size_t)b * T + t] = tg;

@@ -12,8 +12,56 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import GnConfig, GnTiming, call, lib
+from ._lib import GnConfig, GnGenerateOptions, GnTiming, GnToolFn, call, lib
 from .config import Config
+
+
+class GenerateOptions:
+    """inference.GenerateOptions (inference/engine.go:25-34) plus the ids the
+    host's tokenizer gives the engine (Tokenizer.EncodeSpecial / BOSTokenID)
+    and its tool registry: tool(call_ids) -> result ids, or None when no
+    tool understands the call (Registry.Execute over Tokenizer.Decode /
+    Encode).  Defaults: the byte-level tokenizer, thinking off, the built-in
+    calculator."""
+
+    def __init__(self, thinking: bool = False, thinking_budget: int = 0, tool=None, **ids):
+        o = GnGenerateOptions()
+        call("gn_generate_options_default", C.byref(o))
+        o.thinking = 1 if thinking else 0
+        o.thinking_budget = int(thinking_budget)
+        for k, v in ids.items():
+            if k not in ("bos", "assistant_end", "tool_start", "tool_end", "tool_output_start",
+                         "tool_output_end", "think_start", "think_end"):
+                raise TypeError(f"unknown special id {k}")
+            setattr(o, k, int(v))
+        self._tool = tool
+        self._cb = None
+        if tool is not None:
+            def cb(user, ids_p, n, out_p, cap):
+                res = tool([ids_p[i] for i in range(n)])
+                if res is None:
+                    return -1
+                res = list(res)
+                if len(res) > cap:
+                    return cap + 1
+                for i, v in enumerate(res):
+                    out_p[i] = int(v)
+                return len(res)
+            self._cb = GnToolFn(cb)
+            o.tool = self._cb
+        self.c = o
+
+    def __getattr__(self, name):
+        return getattr(self.__dict__["c"], name)
+
+
+def use_calculator(expression: str):
+    """inference.UseCalculator (inference/tooluse.go:83-90) through the C ABI:
+    the result string, or None when the calculator rejects the expression."""
+    out = C.create_string_buffer(512)
+    ok = C.c_int32()
+    call("gn_use_calculator", expression.encode(), out, 512, C.byref(ok))
+    return out.value.decode() if ok.value else None
 
 
 def gn_config_of(cfg: Config) -> GnConfig:
@@ -93,14 +141,28 @@ class Session:
         return out
 
     def generate_batch(self, prompts: np.ndarray, samples: int, max_tokens: int,
-                       temperature: float, top_k: int, seeds) -> list[np.ndarray]:
+                       temperature: float, top_k: int, seeds, options: GenerateOptions = None,
+                       masks: bool = False):
+        """Engine.GenerateBatchWith for every group (one prompt row each):
+        the rows (prompt + completion, terminal token excluded) and, with
+        masks=True, GenerateBatchWith's masks (1 sampled, 0 prompt/forced)."""
         prompts = np.ascontiguousarray(np.atleast_2d(prompts), np.int32)
         G, P = prompts.shape
         rows = np.zeros((G * samples, P + max_tokens), np.int32)
         lens = np.zeros(G * samples, np.int32)
-        call("gn_generate_batch", self._h, prompts, G, P, samples, max_tokens, float(temperature),
-             top_k, np.ascontiguousarray(seeds, np.uint64), rows, lens)
-        return [rows[i, :lens[i]].copy() for i in range(G * samples)]
+        mk = np.zeros((G * samples, P + max_tokens), np.int32) if masks else None
+        if options is None and not masks:
+            call("gn_generate_batch", self._h, prompts, G, P, samples, max_tokens,
+                 float(temperature), top_k, np.ascontiguousarray(seeds, np.uint64), rows, lens)
+        else:
+            call("gn_generate_batch_with", self._h, prompts, G, P, samples, max_tokens,
+                 float(temperature), top_k, np.ascontiguousarray(seeds, np.uint64),
+                 None if options is None else C.byref(options.c), rows, lens,
+                 None if mk is None else mk.ctypes.data_as(C.c_void_p))
+        out = [rows[i, :lens[i]].copy() for i in range(G * samples)]
+        if masks:
+            return out, [mk[i, :lens[i]].copy() for i in range(G * samples)]
+        return out
 
     def policy_gradient_step(self, inputs, targets, advantages, norm: float):
         inputs = np.ascontiguousarray(inputs, np.int32)
@@ -127,7 +189,8 @@ class Session:
              int(grad_accum_steps), C.byref(loss))
         return loss.value
 
-    def rl_step(self, prompts, samples, max_tokens, temperature, top_k, seeds, rewards):
+    def rl_step(self, prompts, samples, max_tokens, temperature, top_k, seeds, rewards,
+                options: GenerateOptions = None):
         prompts = np.ascontiguousarray(prompts, np.int32)
         G, P = prompts.shape
         Bt = G * samples
@@ -136,9 +199,15 @@ class Session:
         adv = np.zeros(Bt, np.float32)
         max_len = C.c_int32()
         loss = C.c_float()
-        call("gn_rl_step", self._h, prompts, G, P, samples, max_tokens, float(temperature), top_k,
-             np.ascontiguousarray(seeds, np.uint64), np.ascontiguousarray(rewards, np.float32),
-             rows, lens, adv, C.byref(max_len), C.byref(loss))
+        seeds = np.ascontiguousarray(seeds, np.uint64)
+        rewards = np.ascontiguousarray(rewards, np.float32)
+        if options is None:
+            call("gn_rl_step", self._h, prompts, G, P, samples, max_tokens, float(temperature),
+                 top_k, seeds, rewards, rows, lens, adv, C.byref(max_len), C.byref(loss))
+        else:
+            call("gn_rl_step_with", self._h, prompts, G, P, samples, max_tokens,
+                 float(temperature), top_k, seeds, C.byref(options.c), rewards, rows, lens, adv,
+                 C.byref(max_len), C.byref(loss))
         return dict(loss=loss.value, rows=[rows[b, :lens[b]].copy() for b in range(Bt)],
                     lens=lens, adv=adv, max_len=max_len.value)
 

@@ -284,6 +284,42 @@ int gn_generate_batch(gn_session *session, const int32_t *prompts, int32_t group
                       int32_t top_k, const uint64_t *seeds, int32_t *rows_out,
                       int32_t *lengths_out);
 
+/* inference.GenerateOptions (inference/engine.go:25-34) together with what
+ * GenerateWith takes from the engine's tokenizer and tool registry
+ * (engine.go:215-224, 282-296): the ids Tokenizer.EncodeSpecial /
+ * BOSTokenID return for the host's tokenizer, and the tool call.
+ *
+ * tool, when set, is Registry.Execute(Tokenizer.Decode(call)) followed by
+ * Tokenizer.Encode of the result, run on the host: it receives the n ids
+ * between <|tool_start|> and <|tool_end|>, writes at most cap result ids
+ * into out and returns their count, or -1 when no tool understands the
+ * call (no output is forced then).  It is called from the calling thread
+ * during gn_generate_batch_with / gn_rl_step_with.  tool NULL uses the
+ * built-in calculator (inference/tooluse.go:27-90) over the byte-level
+ * tokenizer's Decode/Encode (tokenizer/special.go:19-31). */
+typedef struct gn_generate_options {
+  int32_t thinking;        /* GenerateOptions.Thinking */
+  int32_t thinking_budget; /* GenerateOptions.ThinkingBudget (<= 0: no budget) */
+  int32_t bos;             /* Tokenizer.BOSTokenID() */
+  int32_t assistant_end;   /* EncodeSpecial("<|assistant_end|>") (also chat_rl's padding) */
+  int32_t tool_start, tool_end, tool_output_start, tool_output_end;
+  int32_t think_start, think_end;
+  int32_t (*tool)(void *user, const int32_t *call, int32_t n, int32_t *out, int32_t cap);
+  void *tool_user;
+} gn_generate_options;
+/* The byte-level tokenizer's ids, thinking off, the built-in calculator:
+ * what gn_generate_batch and gn_rl_step use. */
+int gn_generate_options_default(gn_generate_options *out);
+/* Engine.GenerateBatchWith (inference/engine.go:336-369) with options
+ * (NULL: the defaults); masks_out (nullable, [groups*samples,
+ * prompt_len+max_tokens]) is GenerateBatchWith's masks: 0 for prompt and
+ * forced tokens, 1 for sampled ones. */
+int gn_generate_batch_with(gn_session *session, const int32_t *prompts, int32_t groups,
+                           int32_t prompt_len, int32_t samples, int32_t max_tokens,
+                           float temperature, int32_t top_k, const uint64_t *seeds,
+                           const gn_generate_options *options, int32_t *rows_out,
+                           int32_t *lengths_out, int32_t *masks_out);
+
 /* trainer.PolicyGradientStep (trainer/rl.go:14-60): teacher-forced
  * recompute of inputs [batch, seq_len], per-token NLL (nll_out, nullable,
  * [batch*seq_len]; logp = -nll), loss = sum_valid nll*adv/norm, and the
@@ -301,6 +337,17 @@ int gn_rl_step(gn_session *session, const int32_t *prompts, int32_t groups, int3
                const uint64_t *seeds, const float *rewards, int32_t *rows_out,
                int32_t *lengths_out, float *advantages_out, int32_t *max_len_out,
                float *loss_out);
+/* gn_rl_step with generation options (NULL: the defaults); rows are padded
+ * with options->assistant_end (cmd/chat_rl/main.go:157-180). */
+int gn_rl_step_with(gn_session *session, const int32_t *prompts, int32_t groups,
+                    int32_t prompt_len, int32_t samples, int32_t max_tokens, float temperature,
+                    int32_t top_k, const uint64_t *seeds, const gn_generate_options *options,
+                    const float *rewards, int32_t *rows_out, int32_t *lengths_out,
+                    float *advantages_out, int32_t *max_len_out, float *loss_out);
+/* inference.UseCalculator (inference/tooluse.go:83-90), the built-in tool:
+ * *ok = 1 and the NUL-terminated result in out (cap bytes), or *ok = 0 when
+ * the expression is rejected.  Host code; needs no device. */
+int gn_use_calculator(const char *expression, char *out, size_t cap, int32_t *ok);
 
 /* inference.SampleNextToken (inference/sampler.go:16-60) on host logits
  * [rows, vocab] with the tensors.RNG state rng_state = {hi, lo} of Go's PCG,
