@@ -9,7 +9,8 @@ the PG loss forward/backward over the full 65536 vocabulary.  Inputs are
 synthetic (uniform prompt ids, InitWeights-distributed random weights) and
 resident in HBM before the timed region.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config d12|d2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config d12|d2|d20|latent_d12|flash_d12]
+                    [--phase rl|train|rollout|optimizer] [--no-graph]
 """
 from __future__ import annotations
 
@@ -32,6 +33,9 @@ WORKLOADS = {
     # name: (config factory, groups, prompt len, samples, new tokens, temperature, reward p)
     "d12": ("dense_d12", 16, 256, 16, 256, 1.0, 0.3),
     "d2": ("dense_d2", 4, 32, 8, 24, 1.0, 0.3),
+    # 32 prompts of 512 tokens x 16 samples, 1024 new tokens, T=0.8,
+    # rewards uniform on {0, 1} (Bernoulli(0.5))
+    "d20": ("dense_d20", 32, 512, 16, 1024, 0.8, 0.5),
     # BASELINE configs[3] (the group split is unspecified there: 16 x 16 as d12)
     "latent_d12": ("latent_d12", 16, 256, 16, 256, 1.0, 0.3),
     # 64 rollouts (4 groups x 16) of 8192-token prompts + 512 new tokens
@@ -66,7 +70,9 @@ def cpu_baseline(cfg, w, prompts, S: int, N: int, temp: float) -> dict:
     P = prompts.shape[1]
     PREFIX = 1024
     Ps = min(P, PREFIX)
-    STEPS = 128 if Ps == P else 8  # about 15 s of CPU work on 16 host threads
+    # about 15 s of CPU work on 16 host threads: 128 decode steps of a d12
+    # group, fewer for larger models and for long sampled prompts
+    STEPS = 8 if Ps < P else max(8, min(128, int(128 * 1.3e8 / cfg.param_total())))
     m = O.OracleModel(O.ModelShape.from_config(cfg), w)
 
     def layer_tokens(p):
@@ -105,11 +111,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="d12", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--phase", default="rl", choices=["rl", "train", "optimizer"],
+    ap.add_argument("--phase", default="rl", choices=["rl", "train", "rollout", "optimizer"],
                     help="rl: the full RL step (the benchmark); train: only the recompute + "
                          "PG fwd/bwd on a synthetic batch of the workload's shape (for "
-                         "counter profiles of the train-phase kernels); optimizer: only "
-                         "MuonAdamW steps with cmd/chat_rl's parameter groups")
+                         "counter profiles of the train-phase kernels); rollout: only the "
+                         "rollouts (for kernel-trace and counter profiles of the decode "
+                         "kernels in place); optimizer: only MuonAdamW steps with "
+                         "cmd/chat_rl's parameter groups")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every decode kernel instead of replaying the captured decode "
                          "graph (for kernel-trace profiles: rocprofv3 --kernel-trace has "
@@ -148,6 +156,8 @@ def main() -> int:
 
     if args.phase == "train":
         return train_phase(args, sess, prompts, S, N, reward_rng, reward_p)
+    if args.phase == "rollout":
+        return rollout_phase(args, sess, prompts, S, N, temp)
     if args.phase == "optimizer":
         return optimizer_phase(args, cfg, sess, prompts)
 
@@ -180,9 +190,10 @@ def main() -> int:
             f"train {t['train_ms']:.1f} ms), loss {out['loss']:.6f}, max_len {out['max_len']}")
     sess.synchronize()
     ms_step = 1e3 * (time.perf_counter() - t_start) / args.steps
-    # Decode attention is timed per launch with HIP events, which the timed
-    # rollouts (decode steps replayed from a captured graph) cannot carry:
-    # one more rollout of the same workload, untimed, launches every kernel.
+    # Decode attention is timed per call with events the dispatch records
+    # (kernel start, last kernel's end), which the timed rollouts (decode
+    # steps replayed from a captured graph) cannot carry: one more rollout of
+    # the same workload, untimed, launches every kernel.
     sess.set_decode_graph(False)
     sess.generate_batch(prompts, S, N, temp, 50,
                         np.array([(args.warmup + args.steps) * 1000 + g for g in range(groups)],
@@ -248,9 +259,10 @@ def main() -> int:
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "launches": attn_n,
             "avg_launch_ms": round(attn_ms / max(attn_n, 1), 5),
-            "measured_on": "an extra untimed rollout of the workload: HIP events around a "
-                           "burst of 4 back-to-back launches of every step's attention call "
-                           "(the kernels' own duration, as rocprof reports it)",
+            "measured_on": "an extra untimed rollout of the workload with every kernel "
+                           "launched: each step's attention call (attention kernel + split "
+                           "combine) timed once, in place, by events the dispatch records "
+                           "(hipExtLaunchKernelGGL: first kernel's start, last kernel's end)",
         },
     }
     if opt is not None:
@@ -271,6 +283,38 @@ def gemm_traffic(config: str):
         return None
     with open(path) as f:
         return json.load(f).get("bytes_per_launch")
+
+
+def rollout_phase(args, sess, prompts, S, N, temp) -> int:
+    """Rollouts alone (Engine.GenerateBatchWith for every group), for kernel
+    traces and counters of the decode kernels in their place in the step:
+    warmup + timed rollouts, then the decode-attention figure of the last."""
+    G_, P = prompts.shape
+    for i in range(args.warmup):
+        sess.generate_batch(prompts, S, N, temp, 50, np.arange(G_, dtype=np.uint64) + 1000 * i)
+    sess.synchronize()
+    t0 = time.perf_counter()
+    toks, roll = 0, []
+    for i in range(args.steps):
+        rows = sess.generate_batch(prompts, S, N, temp, 50,
+                                   np.arange(G_, dtype=np.uint64) + 1000 * (args.warmup + i))
+        toks += sum(len(r) - P for r in rows)
+        roll.append(sess.timing()["rollout_ms"])
+    sess.synchronize()
+    wall = time.perf_counter() - t0
+    t = sess.timing()
+    sess.close()
+    attn = t["decode_attn_bytes"] / (t["decode_attn_ms"] / 1e3) / 1e9 if t["decode_attn_ms"] else 0
+    print(json.dumps({
+        "metric": "rollout tokens/s", "value": round(toks / wall, 1), "unit": "tokens/s",
+        "steps": args.steps, "warmup": args.warmup, "graph": not args.no_graph,
+        "rollout_ms": round(sum(roll) / len(roll), 2),
+        "decode_attention_last_rollout": {
+            "achieved_gbs": round(attn, 1), "frac": round(attn / HBM_PEAK_GBS, 4),
+            "calls": t["decode_attn_launches"],
+            "avg_call_ms": round(t["decode_attn_ms"] / max(t["decode_attn_launches"], 1), 5)}}),
+        flush=True)
+    return 0
 
 
 def train_phase(args, sess, prompts, S, N, reward_rng, reward_p) -> int:
