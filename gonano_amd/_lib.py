@@ -84,6 +84,15 @@ class GnGenerateOptions(C.Structure):
     ]
 
 
+class GnPrefixCacheOptions(C.Structure):
+    _fields_ = [
+        ("max_entries", C.c_int32),
+        ("max_prefix", C.c_int32),
+        ("max_bytes", C.c_int64),
+        ("ttl_seconds", C.c_double),
+    ]
+
+
 class HipError(RuntimeError):
     """A gn_* call returned a non-zero gn_status (the reference panics)."""
 
@@ -166,6 +175,10 @@ _SIGS = {
     "gn_session_synchronize": (C.c_int, [vp]),
     "gn_session_aux_loss": (C.c_int, [vp, C.POINTER(C.c_double)]),
     "gn_session_set_decode_graph": (C.c_int, [vp, C.c_int]),
+    "gn_session_set_prefix_cache": (C.c_int, [vp, C.POINTER(GnPrefixCacheOptions)]),
+    "gn_session_prefix_cache_invalidate": (C.c_int, [vp]),
+    "gn_session_prefix_cache_len": (C.c_int, [vp, C.POINTER(C.c_int32), C.POINTER(C.c_int64)]),
+    "gn_session_prefix_cache_hits": (C.c_int, [vp, i32p, C.c_int32]),
     "gn_distill_step": (C.c_int, [vp, vp, i32p, vp, C.c_int32, C.c_int32, C.c_float, C.c_int32,
                                   C.POINTER(C.c_float)]),
     "gn_optimizer_create": (C.c_int, [vp, vp, C.c_int32, C.POINTER(C.c_void_p)]),

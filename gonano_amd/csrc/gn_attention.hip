@@ -429,10 +429,12 @@ __device__ __forceinline__ bool key_valid(int kj, int t, int T, int window) {
   return kj < T && kj <= t && (window < 0 || t - kj <= window);
 }
 // The flash kernels' mask: causal/windowed keys, or compressed blocks that
-// ended before the query's block (ratio > 1).
+// ended before the query's block (ratio > 1).  Query t sits at position
+// t + qoff: a forward that continues a cached prefix of qoff tokens attends
+// keys [0, qoff + T) with its queries at the end.
 __device__ __forceinline__ bool key_ok(int kj, int t, int Tk, int ratio, int window, int qoff) {
   if (ratio > 1) return kj < Tk && (kj + 1) * ratio <= t + qoff;
-  return key_valid(kj, t, Tk, window);
+  return key_valid(kj, t + qoff, Tk, window);
 }
 // Key tiles a query block [q0, qlast] needs: [kbeg, kend).
 __device__ __forceinline__ void key_range(int q0, int qlast, int Tk, int ratio, int window,
@@ -441,8 +443,8 @@ __device__ __forceinline__ void key_range(int q0, int qlast, int Tk, int ratio, 
     *kbeg = 0;
     *kend = min(Tk, (qlast + qoff) / ratio);
   } else {
-    *kbeg = window >= 0 ? max(0, q0 - window) : 0;
-    *kend = qlast + 1;
+    *kbeg = window >= 0 ? max(0, q0 + qoff - window) : 0;
+    *kend = min(Tk, qlast + qoff + 1);
   }
 }
 
@@ -586,6 +588,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
 void launch_flash_fwd(FlashArgs a, hipStream_t st) {
   if (a.Tk <= 0) a.Tk = a.T;
   GN_CHECK(a.ratio <= 1 || a.window < 0, "flash: compressed keys take no window");
+  GN_CHECK(a.ratio > 1 || a.qoff + a.T <= a.Tk, "flash: queries past the last key");
   hipLaunchKernelGGL(flash_fwd_mfma_kernel, dim3((unsigned)ceil_div(a.T, FQ), a.B * a.Hq),
                      dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());

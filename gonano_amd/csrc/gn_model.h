@@ -8,7 +8,8 @@ namespace gn {
 // ---- embedding / norms --------------------------------------------------
 void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, const float* lam,
                         int B, int T, int C, float* raw, float* embn, float* smsig, float* x,
-                        hipStream_t st);
+                        hipStream_t st, const float* seed_prev = nullptr,
+                        float* seedsig = nullptr);
 void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg, const float* lam,
                          int rows, int C, float* prev, float* x, float* x0, hipStream_t st);
 // xin (resp. x) may be the target of a residual-add GEMM whose split-K sum

@@ -29,7 +29,8 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(const int32_t* __restri
                                                          int T, const float* __restrict__ wsg,
                                                          float* __restrict__ raw,
                                                          float* __restrict__ embn,
-                                                         float* __restrict__ smsig) {
+                                                         float* __restrict__ smsig,
+                                                         float* __restrict__ seedsig) {
   __shared__ float sc[4];
   const int64_t n = blockIdx.x;
   const int t = (int)(n % T);
@@ -43,20 +44,27 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(const int32_t* __restri
   ss = bsum256(ss, sc);
   const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
   for (int c = threadIdx.x; c < C; c += 256) embn[n * C + c] = src[c] * inv;
-  if (t >= 1 && smsig) {
-    // gate = sigmoid(embn[:24] . w) (smearGate Linear 24 -> 1)
+  if ((t >= 1 && smsig) || (t == 0 && seedsig)) {
+    // gate = sigmoid(embn[:24] . w) (smearGate Linear 24 -> 1); at t == 0 the
+    // seed gate of a forward that continues a cached prefix (smearSeed)
     float p = 0.f;
     if (threadIdx.x < SMEAR_CH) p = src[threadIdx.x] * inv * wsg[threadIdx.x];
     p = warp_sum(threadIdx.x < 64 ? p : 0.f);
-    if (threadIdx.x == 0) smsig[(n / T) * (T - 1) + t - 1] = sigmoidf_(p);
+    if (threadIdx.x == 0) {
+      if (t >= 1) smsig[(n / T) * (T - 1) + t - 1] = sigmoidf_(p);
+      else seedsig[n / T] = sigmoidf_(p);
+    }
   }
 }
 
 // x[t] = embn[t] + lambda * smsig[t-1] * embn[t-1] (helpers.go:35-48; reads the
-// pre-smear embedding of the previous row).
+// pre-smear embedding of the previous row); with seed_prev, row 0 of each
+// sequence adds lambda * seedsig * seed_prev (smearSeed, helpers.go:53-67:
+// the previous token's stored embedding of a cached prefix).
 __global__ void smear_apply_kernel(const float* __restrict__ embn, const float* __restrict__ smsig,
                                    const float* __restrict__ lam, float* __restrict__ x, int C,
-                                   int T, int64_t total) {
+                                   int T, int64_t total, const float* __restrict__ seedsig,
+                                   const float* __restrict__ seed_prev) {
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   int64_t n = i / C;
@@ -65,20 +73,25 @@ __global__ void smear_apply_kernel(const float* __restrict__ embn, const float* 
   if (t >= 1) {
     float g = smsig[(n / T) * (T - 1) + t - 1] * lam[0];
     v += g * embn[i - C];
+  } else if (seed_prev) {
+    const int64_t b = n / T;
+    float g = seedsig[b] * lam[0];
+    v += g * seed_prev[b * C + (i - n * C)];
   }
   x[i] = v;
 }
 
 void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, const float* lam,
                         int B, int T, int C, float* raw, float* embn, float* smsig, float* x,
-                        hipStream_t st) {
+                        hipStream_t st, const float* seed_prev, float* seedsig) {
+  GN_CHECK(!seed_prev || seedsig, "embed_smear: a seed needs its gate buffer");
   int64_t N = (int64_t)B * T;
   hipLaunchKernelGGL(embed_norm_kernel, dim3((unsigned)N), dim3(256), 0, st, ids, wte, C, T, wsg,
-                     raw, embn, T > 1 ? smsig : nullptr);
+                     raw, embn, T > 1 ? smsig : nullptr, seed_prev ? seedsig : nullptr);
   GN_HIP(hipGetLastError());
   int64_t tot = N * C;
   hipLaunchKernelGGL(smear_apply_kernel, dim3((unsigned)ceil_div(tot, 256)), dim3(256), 0, st,
-                     embn, smsig, lam, x, C, T, tot);
+                     embn, smsig, lam, x, C, T, tot, seedsig, seed_prev);
   GN_HIP(hipGetLastError());
 }
 

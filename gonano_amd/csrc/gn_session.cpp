@@ -145,6 +145,24 @@ struct gn_session {
   std::vector<int> attn_ev_launches;
   std::vector<hipEvent_t> event_pool;
   size_t event_next = 0;
+  // device-resident prefix cache (inference/cache.go CacheManager): entries
+  // in LRU order, oldest first; each holds one prompt's prefill state
+  struct PrefixEntry {
+    std::vector<int32_t> tokens;
+    float* mem = nullptr;  // ktm | vtm | kdc | vdc | prev (gn::pc_layout)
+    int64_t bytes = 0;
+    double stored_at = 0.0;
+  };
+  std::vector<std::unique_ptr<PrefixEntry>> pc_entries;
+  bool pc_on = false;
+  int pc_max_entries = 0;   // 0: unbounded (CacheOptions.MaxEntries)
+  int64_t pc_max_bytes = 0; // 0: unbounded (CacheOptions.MaxBytes)
+  double pc_ttl = 0.0;      // seconds; 0: no expiry (CacheOptions.TTL)
+  int pc_max_prefix = 0;    // longer entries never hit; 0: any (NewPrefixCache)
+  int64_t pc_bytes = 0;
+  bool pc_defer = false;    // removed entries wait in pc_retired for the stream
+  std::vector<std::unique_ptr<PrefixEntry>> pc_retired;
+  std::vector<int32_t> pc_hits;  // prompt tokens taken from the cache, per group of the last call
   // decode steps replayed from one captured HIP graph per rollout
   bool decode_graph = true;
   bool capturing = false;
@@ -594,6 +612,15 @@ struct SeqBuffers {
   std::vector<float*> pre_kc, pre_vc;
   int gblocks = 0;
   int pf_maxseq = 0;  // prefill raw caches' length (0: T)
+  // continuation of a cached prefix (prefix cache hit, B == 1): pre_len
+  // positions already computed, their token-major keys/values per layer
+  // pre_k/pre_v [L][pre_len][Hkv*128] and the previous token's embedding
+  // seed_prev [C] for the smear; qoff == pre_len
+  int pre_len = 0;
+  const float *pre_k = nullptr, *pre_v = nullptr, *seed_prev = nullptr;
+  // when set, every layer's token-major keys/values of the whole sequence
+  // (prefix included) are copied here: [L][B*(pre_len+T)][Hkv*128]
+  float *tm_k_out = nullptr, *tm_v_out = nullptr;
   // prefill: the decode caches to fill (indexer keys [L][G*S][maxBlocks]
   // [Hkv][HI] of the complete blocks, replicated over S rows per prompt)
   float* dec_ikc = nullptr;
@@ -859,7 +886,8 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     sb.smsig = A<float>(s, "smsig", std::max<int64_t>((int64_t)B * (T - 1), 1));
     sb.x0 = A<float>(s, "x0", N * C);
     launch_embed_smear(sb.ids, s->wte, s->smg, s->sml, B, T, C, sb.raw, sb.embn, sb.smsig, sb.x0,
-                       st);
+                       st, sb.seed_prev,
+                       sb.seed_prev ? A<float>(s, "seed_sig", std::max(B, 1)) : nullptr);
     xcur = sb.x0;
   }
   const int l_end = sb.l1 < 0 ? L : sb.l1;
@@ -872,9 +900,23 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   float* qkv = s->mla ? nullptr : A<float>(s, "qkv", N * s->QKVW);
   const int bk = L / 2;
   sb.backout = nullptr;
+  GN_CHECK(sb.pre_len == 0 || (B == 1 && !save && !s->hca && sb.qoff == sb.pre_len && sb.pre_k &&
+                                sb.pre_v),
+           "prefix continuation: one sequence, prefill only, dense or latent attention");
   for (int l = sb.l0; l < l_end; l++) {
     Layer& ly = s->layers[l];
     sb.xin[l] = xcur;
+    // a continued prefix: this layer's keys/values of the whole sequence,
+    // the cached rows first, the new ones written after them
+    float* pre_k = nullptr;
+    float* pre_v = nullptr;
+    if (sb.pre_len > 0) {
+      const int64_t pk = (int64_t)sb.pre_len * s->KVW;
+      pre_k = A<float>(s, "pc_kall", (int64_t)(sb.pre_len + T) * s->KVW);
+      pre_v = A<float>(s, "pc_vall", (int64_t)(sb.pre_len + T) * s->KVW);
+      GN_HIP(hipMemcpyAsync(pre_k, sb.pre_k + l * pk, sizeof(float) * pk, hipMemcpyDeviceToDevice, st));
+      GN_HIP(hipMemcpyAsync(pre_v, sb.pre_v + l * pk, sizeof(float) * pk, hipMemcpyDeviceToDevice, st));
+    }
     if (s->split > 0 && l == s->split) {  // encoderHidden (transformer.go:310-312)
       sb.enc = A<float>(s, "ced_enc", N * C);
       GN_HIP(hipMemcpyAsync(sb.enc, xcur, sizeof(float) * N * C, hipMemcpyDeviceToDevice, st));
@@ -899,18 +941,21 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
       sgemm(s, dk);
       MlaAssembleArgs ma{};
       ma.xa = xa; ma.xw = s->XW; ma.qc = qc; ma.kvu = kvu; ma.cosT = s->cosT; ma.sinT = s->sinT;
-      ma.Hq = Hq; ma.Hkv = Hkv; ma.lat = s->lat; ma.rd = s->rd; ma.T = T; ma.pos0 = 0;
+      ma.Hq = Hq; ma.Hkv = Hkv; ma.lat = s->lat; ma.rd = s->rd; ma.T = T; ma.pos0 = sb.qoff;
       ma.q = layer_buf(s, "qn", l, save, N * Hq * HD);
-      ma.k = layer_buf(s, "kn", l, save, N * s->KVW);
-      ma.v = layer_buf(s, "v", l, save, N * s->KVW);
+      ma.k = pre_k ? pre_k + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "kn", l, save, N * s->KVW);
+      ma.v = pre_v ? pre_v + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "v", l, save, N * s->KVW);
       if (mode == SEQ_PREFILL) {  // latent + rotary-key cache of the prompt
-        ma.lat_cache = kcache_pf + (int64_t)l * B * T * s->lat;
-        ma.rk_cache = vcache_pf + (int64_t)l * B * T * Hkv * s->rd;
-        ma.maxSeq = T;
+        const int pm = sb.pf_maxseq > 0 ? sb.pf_maxseq : T;
+        ma.lat_cache = kcache_pf + (int64_t)l * B * pm * s->lat;
+        ma.rk_cache = vcache_pf + (int64_t)l * B * pm * Hkv * s->rd;
+        ma.maxSeq = pm;
       }
       launch_mla_assemble(ma, N, st);
       sb.xa[l] = xa;
-      sb.qn[l] = ma.q; sb.kn[l] = ma.k; sb.v[l] = ma.v;
+      sb.qn[l] = ma.q;
+      sb.kn[l] = pre_k ? pre_k : ma.k;
+      sb.v[l] = pre_v ? pre_v : ma.v;
     } else {
     sgemm(s, linear_fwd_desc(h, ly.wqkv, qkv, (int)N, C, s->QKVW));
     QkvPostArgs qa{};
@@ -919,8 +964,8 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     qa.cosT = s->cosT; qa.sinT = s->sinT;
     qa.C = C; qa.Hq = Hq; qa.Hkv = Hkv; qa.R = s->R; qa.T = T; qa.pos0 = sb.qoff;
     qa.qn = layer_buf(s, "qn", l, save, N * Hq * HD);
-    qa.kn = layer_buf(s, "kn", l, save, N * s->KVW);
-    qa.vout = layer_buf(s, "v", l, save, N * s->KVW);
+    qa.kn = pre_k ? pre_k + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "kn", l, save, N * s->KVW);
+    qa.vout = pre_v ? pre_v + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "v", l, save, N * s->KVW);
     qa.qrot = save ? layer_buf(s, "qrot", l, true, N * Hq * HD) : nullptr;
     qa.krot = save ? layer_buf(s, "krot", l, true, N * s->KVW) : nullptr;
     qa.vesig = (save && ly.has_ve) ? layer_buf(s, "vesig", l, true, N * Hkv) : nullptr;
@@ -932,8 +977,17 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
       qa.rows_per_seq = 1;
     }
     launch_qkv_post(qa, N, st);
-    sb.qn[l] = qa.qn; sb.kn[l] = qa.kn; sb.v[l] = qa.vout;
+    sb.qn[l] = qa.qn;
+    sb.kn[l] = pre_k ? pre_k : qa.kn;
+    sb.v[l] = pre_v ? pre_v : qa.vout;
     sb.qrot[l] = qa.qrot; sb.krot[l] = qa.krot; sb.vesig[l] = qa.vesig;
+    }
+    if (sb.tm_k_out) {  // the whole sequence's keys/values of this layer
+      const int64_t tm = (int64_t)B * (sb.pre_len + T) * s->KVW;
+      GN_HIP(hipMemcpyAsync(sb.tm_k_out + l * tm, sb.kn[l], sizeof(float) * tm,
+                            hipMemcpyDeviceToDevice, st));
+      GN_HIP(hipMemcpyAsync(sb.tm_v_out + l * tm, sb.v[l], sizeof(float) * tm,
+                            hipMemcpyDeviceToDevice, st));
     }
     if (s->hca) {
       hca_forward(s, sb, ly, l, mode);
@@ -943,6 +997,7 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
       fa.o = layer_buf(s, "o", l, save, N * Hq * HD);
       fa.lse = save ? layer_buf(s, "lse", l, true, N * Hq) : nullptr;
       fa.B = B; fa.T = T; fa.Hq = Hq; fa.Hkv = Hkv; fa.window = ly.window;
+      fa.Tk = sb.pre_len + T; fa.qoff = sb.pre_len;  // keys of the cached prefix first
       launch_flash_fwd(fa, st);
       sb.o[l] = fa.o; sb.lse[l] = fa.lse;
     }
@@ -1998,6 +2053,260 @@ static int prefill_ced(gn_session* s, SeqBuffers& sb, const int32_t* prompts, in
   return R;
 }
 
+// ---------------------------------------------------------------------------
+// Prefix cache (inference/cache.go CacheManager, inference/prefix.go
+// PrefixCache) on the device.  An entry holds one prompt's prefill state:
+// every layer's token-major keys/values [L][P][Hkv*128] (what a continued
+// prefill attends to), its decode-cache rows (dense: K and V [L][Hkv][P][128];
+// latent: the latent rows [L][P][lat] and rotated keys [L][P][Hkv*rd]) and
+// the last token's embedding (the next token's smear input, KVBuffer's
+// PrevEmbedding).
+// ---------------------------------------------------------------------------
+struct PcLayout {
+  int64_t ktm, vtm, kdc, vdc, prev, total;  // float offsets
+};
+static PcLayout pc_layout(const gn_session* s, int P) {
+  PcLayout o;
+  const int64_t tm = (int64_t)s->L * P * s->KVW;
+  const int64_t kdc = s->mla ? (int64_t)s->L * P * s->lat : tm;
+  const int64_t vdc = s->mla ? (int64_t)s->L * P * s->Hkv * s->rd : tm;
+  o.ktm = 0;
+  o.vtm = tm;
+  o.kdc = 2 * tm;
+  o.vdc = o.kdc + kdc;
+  o.prev = o.vdc + vdc;
+  o.total = o.prev + s->C;
+  return o;
+}
+static double pc_now() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+// Entries leave the list through pc_remove; their device memory is released
+// at once, or -- while a prefill still reads it (pc_defer) -- when that
+// prefill has finished (pc_flush).
+static void pc_remove(gn_session* s, size_t i) {
+  auto& e = s->pc_entries[i];
+  s->pc_bytes -= e->bytes;
+  if (s->pc_defer) s->pc_retired.push_back(std::move(e));
+  else (void)hipFree(e->mem);
+  s->pc_entries.erase(s->pc_entries.begin() + i);
+}
+static void pc_flush(gn_session* s) {
+  for (auto& e : s->pc_retired) (void)hipFree(e->mem);
+  s->pc_retired.clear();
+}
+// expireLocked (cache.go:236-252): entries stored longer ago than the TTL
+static void pc_expire(gn_session* s) {
+  if (s->pc_ttl <= 0) return;
+  const double now = pc_now();
+  for (size_t i = s->pc_entries.size(); i-- > 0;)
+    if (now - s->pc_entries[i]->stored_at > s->pc_ttl) pc_remove(s, i);
+}
+// Lookup (cache.go:79-119, prefix.go:38-60): the longest stored strict prefix
+// of the prompt (none longer than max_prefix when that is set), moved to the
+// most recently used end; nullptr on a miss.
+static gn_session::PrefixEntry* pc_lookup(gn_session* s, const int32_t* toks, int P) {
+  pc_expire(s);
+  int best = -1;
+  size_t best_len = 0;
+  for (size_t i = 0; i < s->pc_entries.size(); i++) {
+    const auto& e = s->pc_entries[i]->tokens;
+    if (e.empty() || e.size() >= (size_t)P || e.size() <= best_len) continue;
+    if (s->pc_max_prefix > 0 && e.size() > (size_t)s->pc_max_prefix) continue;
+    if (std::equal(e.begin(), e.end(), toks)) {
+      best = (int)i;
+      best_len = e.size();
+    }
+  }
+  if (best < 0) return nullptr;
+  auto e = std::move(s->pc_entries[best]);
+  s->pc_entries.erase(s->pc_entries.begin() + best);
+  s->pc_entries.push_back(std::move(e));
+  return s->pc_entries.back().get();
+}
+// evictLocked (cache.go:216-231): least recently used entries first, until
+// the entry count and then the byte total fit
+static void pc_evict(gn_session* s) {
+  while (s->pc_max_entries > 0 && (int)s->pc_entries.size() > s->pc_max_entries) pc_remove(s, 0);
+  while (s->pc_max_bytes > 0 && s->pc_bytes > s->pc_max_bytes && !s->pc_entries.empty())
+    pc_remove(s, 0);
+}
+// Store (cache.go:121-161): replaces an entry of the same prompt, appends the
+// new one at the most recently used end, then evicts.
+static void pc_insert(gn_session* s, std::unique_ptr<gn_session::PrefixEntry> e) {
+  for (size_t i = 0; i < s->pc_entries.size(); i++)
+    if (s->pc_entries[i]->tokens == e->tokens) {
+      pc_remove(s, i);
+      break;
+    }
+  s->pc_bytes += e->bytes;
+  s->pc_entries.push_back(std::move(e));
+  pc_evict(s);
+}
+static void pc_clear(gn_session* s) {
+  while (!s->pc_entries.empty()) pc_remove(s, s->pc_entries.size() - 1);
+}
+
+// Rows [0, count) of each of `layers` blocks: dst (block pitch dpitch floats)
+// <- src (block pitch spitch).
+static void copy_layer_rows(float* dst, int64_t dpitch, const float* src, int64_t spitch,
+                            int64_t count, int layers, hipStream_t st) {
+  if (count <= 0) return;
+  GN_HIP(hipMemcpy2DAsync(dst, sizeof(float) * dpitch, src, sizeof(float) * spitch,
+                          sizeof(float) * count, layers, hipMemcpyDeviceToDevice, st));
+}
+
+// The prefill of GenerateWith with a prefix cache (engine.go:120-173), for G
+// prompts as G successive calls would see the cache: prompt g looks up the
+// longest stored strict prefix, then stores its own state, evicting as the
+// limits require (the prompts of one call have one length, so none is a
+// strict prefix of another, but an earlier prompt's store can evict the
+// entry a later one would have hit).  That sequence is settled on the host
+// first, with the memory of entries it removes kept until the prefill has
+// run; then the prompts without a hit are prefilled together from position 0
+// and every hit continues from its entry over the rest of its prompt (B = 1:
+// the entry's keys attended first, its decode-cache rows copied in, the
+// smear seeded with its stored embedding -- KVBuffer.PrevEmbedding).  Fills
+// the decode prefill caches kpf/vpf (the plain prefill's layout) and each
+// prompt's last-row final norm and embedding lastfn/lastemb [G][C].
+static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, float* kpf,
+                           float* vpf, float* lastfn, float* lastemb) {
+  GN_CHECK(!s->hca && s->split == 0,
+           "prefix cache: compressed-attention and CED models are not cached");
+  const int L = s->L, C = s->C, Hkv = s->Hkv;
+  hipStream_t st = s->stream;
+  const int64_t KVW = s->KVW;
+  // floats per (layer, prompt) of the decode prefill caches
+  const int64_t kg = s->mla ? (int64_t)P * s->lat : (int64_t)Hkv * P * HD;
+  const int64_t vg = s->mla ? (int64_t)P * Hkv * s->rd : (int64_t)Hkv * P * HD;
+  const PcLayout lay = pc_layout(s, P);
+  struct Plan {
+    gn_session::PrefixEntry* src = nullptr;  // the hit (nullptr: a miss)
+    int m = 0;
+    gn_session::PrefixEntry* dst = nullptr;  // this prompt's new entry
+  };
+  std::vector<Plan> plan(G);
+  std::vector<gn_session::PrefixEntry*> made;
+  s->pc_defer = true;
+  try {
+    // 1) the cache sequence of G successive GenerateWith calls
+    for (int g = 0; g < G; g++) {
+      const int32_t* toks = prompts + (int64_t)g * P;
+      if (auto* e = pc_lookup(s, toks, P)) {
+        plan[g].src = e;
+        plan[g].m = (int)e->tokens.size();
+      }
+      auto ne = std::make_unique<gn_session::PrefixEntry>();
+      ne->tokens.assign(toks, toks + P);
+      ne->bytes = sizeof(float) * lay.total;
+      GN_HIP(hipMalloc(&ne->mem, ne->bytes));
+      ne->stored_at = pc_now();
+      plan[g].dst = ne.get();
+      made.push_back(ne.get());
+      pc_insert(s, std::move(ne));
+    }
+    s->pc_hits.assign(G, 0);
+    for (int g = 0; g < G; g++) s->pc_hits[g] = plan[g].m;
+    // 2) prompts with no cached prefix, together from position 0
+    std::vector<int> miss;
+    for (int g = 0; g < G; g++)
+      if (!plan[g].src) miss.push_back(g);
+    if (!miss.empty()) {
+      const int Gm = (int)miss.size();
+      std::vector<int32_t> ids((size_t)Gm * P);
+      for (int i = 0; i < Gm; i++)
+        memcpy(ids.data() + (size_t)i * P, prompts + (int64_t)miss[i] * P, sizeof(int32_t) * P);
+      SeqBuffers sb;
+      sb.B = Gm; sb.T = P; sb.N = (int64_t)Gm * P;
+      sb.ids = upload_ids(s, "pc_ids", ids.data(), sb.N, s->V);
+      sb.tm_k_out = A<float>(s, "pc_tmk", (size_t)L * sb.N * KVW);
+      sb.tm_v_out = A<float>(s, "pc_tmv", (size_t)L * sb.N * KVW);
+      float* kt = A<float>(s, "pc_kt", (size_t)L * Gm * kg);
+      float* vt = A<float>(s, "pc_vt", (size_t)L * Gm * vg);
+      seq_forward(s, sb, SEQ_PREFILL, kt, vt);
+      for (int i = 0; i < Gm; i++) {
+        const int g = miss[i];
+        copy_layer_rows(kpf + g * kg, G * kg, kt + i * kg, Gm * kg, kg, L, st);
+        copy_layer_rows(vpf + g * vg, G * vg, vt + i * vg, Gm * vg, vg, L, st);
+        const int64_t last = ((int64_t)i * P + P - 1) * C;
+        GN_HIP(hipMemcpyAsync(lastfn + (int64_t)g * C, sb.fn + last, sizeof(float) * C,
+                              hipMemcpyDeviceToDevice, st));
+        GN_HIP(hipMemcpyAsync(lastemb + (int64_t)g * C, sb.embn + last, sizeof(float) * C,
+                              hipMemcpyDeviceToDevice, st));
+        float* dm = plan[g].dst->mem;
+        copy_layer_rows(dm + lay.ktm, (int64_t)P * KVW, sb.tm_k_out + (int64_t)i * P * KVW,
+                        sb.N * KVW, (int64_t)P * KVW, L, st);
+        copy_layer_rows(dm + lay.vtm, (int64_t)P * KVW, sb.tm_v_out + (int64_t)i * P * KVW,
+                        sb.N * KVW, (int64_t)P * KVW, L, st);
+      }
+    }
+    // the state stored with prompt g: its decode-cache rows and last embedding
+    auto fill_entry = [&](int g) {
+      float* dm = plan[g].dst->mem;
+      copy_layer_rows(dm + lay.kdc, kg, kpf + g * kg, G * kg, kg, L, st);
+      copy_layer_rows(dm + lay.vdc, vg, vpf + g * vg, G * vg, vg, L, st);
+      GN_HIP(hipMemcpyAsync(dm + lay.prev, lastemb + (int64_t)g * C, sizeof(float) * C,
+                            hipMemcpyDeviceToDevice, st));
+    };
+    for (int g : miss) fill_entry(g);
+    // 3) every hit continues from its entry
+    for (int g = 0; g < G; g++) {
+      if (!plan[g].src) continue;
+      const int m = plan[g].m, T = P - m;
+      const PcLayout el = pc_layout(s, m);
+      const float* em = plan[g].src->mem;
+      float* kt = A<float>(s, "pc_kt1", (size_t)L * kg);
+      float* vt = A<float>(s, "pc_vt1", (size_t)L * vg);
+      if (s->mla) {  // latent rows and rotated keys of positions [0, m)
+        copy_layer_rows(kt, kg, em + el.kdc, (int64_t)m * s->lat, (int64_t)m * s->lat, L, st);
+        copy_layer_rows(vt, vg, em + el.vdc, (int64_t)m * Hkv * s->rd, (int64_t)m * Hkv * s->rd,
+                        L, st);
+      } else {  // K and V rows of positions [0, m) of every (layer, KV head)
+        copy_layer_rows(kt, (int64_t)P * HD, em + el.kdc, (int64_t)m * HD, (int64_t)m * HD,
+                        L * Hkv, st);
+        copy_layer_rows(vt, (int64_t)P * HD, em + el.vdc, (int64_t)m * HD, (int64_t)m * HD,
+                        L * Hkv, st);
+      }
+      SeqBuffers sb;
+      sb.B = 1; sb.T = T; sb.N = T;
+      sb.ids = upload_ids(s, "pc_ids1", prompts + (int64_t)g * P + m, T, s->V);
+      sb.qoff = m;
+      sb.pf_maxseq = P;
+      sb.pre_len = m;
+      sb.pre_k = em + el.ktm;
+      sb.pre_v = em + el.vtm;
+      sb.seed_prev = em + el.prev;
+      sb.tm_k_out = plan[g].dst->mem + lay.ktm;  // the whole prompt's keys/values
+      sb.tm_v_out = plan[g].dst->mem + lay.vtm;
+      seq_forward(s, sb, SEQ_PREFILL, kt, vt);
+      copy_layer_rows(kpf + g * kg, G * kg, kt, kg, kg, L, st);
+      copy_layer_rows(vpf + g * vg, G * vg, vt, vg, vg, L, st);
+      const int64_t last = (int64_t)(T - 1) * C;
+      GN_HIP(hipMemcpyAsync(lastfn + (int64_t)g * C, sb.fn + last, sizeof(float) * C,
+                            hipMemcpyDeviceToDevice, st));
+      GN_HIP(hipMemcpyAsync(lastemb + (int64_t)g * C, sb.embn + last, sizeof(float) * C,
+                            hipMemcpyDeviceToDevice, st));
+      fill_entry(g);
+    }
+    GN_HIP(hipStreamSynchronize(st));
+  } catch (...) {
+    // entries of this call may be incomplete: drop them (their memory is
+    // released after the stream has drained)
+    for (auto* e : made)
+      for (size_t i = 0; i < s->pc_entries.size(); i++)
+        if (s->pc_entries[i].get() == e) {
+          pc_remove(s, i);
+          break;
+        }
+    (void)hipStreamSynchronize(st);
+    s->pc_defer = false;
+    pc_flush(s);
+    throw;
+  }
+  s->pc_defer = false;
+  pc_flush(s);
+}
+
 static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S, int N,
                      float temperature, int top_k, const uint64_t* seeds, int32_t* rows_out,
                      int32_t* lens_out, const gn_generate_options& opt, int32_t* masks_out) {
@@ -2020,7 +2329,10 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
     lens_out[r] = P;
     if (masks_out) memset(masks_out + (int64_t)r * W, 0, sizeof(int32_t) * W);
   }
-  if (N == 0) return;
+  s->pc_hits.assign(G, 0);
+  // with a prefix cache the prompts are prefilled (and stored) even when no
+  // token is asked for, as GenerateWith does
+  if (N == 0 && !s->pc_on) return;
   // 1) batch prefill of every prompt (engine.go:141-173)
   SeqBuffers sb;
   sb.B = G; sb.T = P; sb.N = (int64_t)G * P;
@@ -2063,11 +2375,21 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
     sb.pf_ring = A<float>(s, "pf_ring", (size_t)L * G * s->ratio * HD);
   }
   int Tlast = P;
-  if (s->split > 0) Tlast = prefill_ced(s, sb, prompts, G, P, kpf, vpf, pf_tailk, pf_tailv);
-  else seq_forward(s, sb, SEQ_PREFILL, kpf, vpf);
-  // last-position logits of each prompt, expanded to its S rows (engine.go:182-191)
+  const bool pcache = s->pc_on;
   float* lastfn = A<float>(s, "pf_lastfn", (size_t)rows * C);
-  launch_expand_last_rows(sb.fn, lastfn, G, Tlast, S, C, st);
+  float *gfn = nullptr, *gemb = nullptr;  // per group (prefix cache)
+  if (pcache) {
+    gfn = A<float>(s, "pc_gfn", (size_t)G * C);
+    gemb = A<float>(s, "pc_gemb", (size_t)G * C);
+    prefill_cached(s, prompts, G, P, kpf, vpf, gfn, gemb);
+    if (N == 0) return;
+    launch_expand_last_rows(gfn, lastfn, G, 1, S, C, st);
+  } else {
+    if (s->split > 0) Tlast = prefill_ced(s, sb, prompts, G, P, kpf, vpf, pf_tailk, pf_tailv);
+    else seq_forward(s, sb, SEQ_PREFILL, kpf, vpf);
+    // last-position logits of each prompt, expanded to its S rows (engine.go:182-191)
+    launch_expand_last_rows(sb.fn, lastfn, G, Tlast, S, C, st);
+  }
   float* logits = A<float>(s, "dec_logits", (size_t)rows * V);
   sgemm(s, linear_fwd_desc(lastfn, s->lm, logits, rows, C, V, EPI_SOFTCAP));
   // 2) PrefillFrom (kvcache.go:383-448): replicate KV and the smear state
@@ -2105,7 +2427,8 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
                         G, S, Hkv, P, P, maxSeq, st);
   }
   float* prev = A<float>(s, "dec_prev", (size_t)rows * C);
-  launch_expand_last_rows(sb.embn, prev, G, Tlast, S, C, st);
+  if (pcache) launch_expand_last_rows(gemb, prev, G, 1, S, C, st);
+  else launch_expand_last_rows(sb.embn, prev, G, Tlast, S, C, st);
 
   // 3) decode loop (engine.go:238-325).  Iteration `step` runs the forward
   //    that feeds the previous column (none at step 0: the prefill logits)
@@ -2285,6 +2608,9 @@ int gn_session_destroy(gn_session* s) {
     if (!s) return;
     (void)hipSetDevice(s->device);
     (void)hipStreamSynchronize(s->stream);
+    s->pc_defer = false;
+    pc_clear(s);
+    pc_flush(s);
     s->arena.reset();
     for (auto e : s->event_pool) (void)hipEventDestroy(e);
     if (s->pinned) (void)hipHostFree(s->pinned);
@@ -2341,6 +2667,7 @@ int gn_session_set_params(gn_session* s, const float* params, int64_t count) {
     GN_CHECK(s && params, "null argument");
     copy_params(s, const_cast<float*>(params), count, true, false);
     s->derived_dirty = true;
+    pc_clear(s);  // stored prefills belong to the old parameters
   });
 }
 int gn_session_get_params(const gn_session* s, float* params, int64_t count) {
@@ -2595,6 +2922,53 @@ int gn_session_synchronize(gn_session* s) {
   });
 }
 
+// ---- prefix cache (inference/cache.go, inference/prefix.go) -----------------
+int gn_session_set_prefix_cache(gn_session* s, const gn_prefix_cache_options* o) {
+  return guard([&] {
+    GN_CHECK(s, "null session");
+    GN_HIP(hipSetDevice(s->device));
+    if (!o) {
+      pc_clear(s);
+      s->pc_on = false;
+      return;
+    }
+    if (s->hca || s->split > 0)
+      throw Error(GN_ERR_UNSUPPORTED,
+                  "prefix cache: compressed-attention and CED models are not cached");
+    GN_CHECK(o->max_entries >= 0 && o->max_bytes >= 0 && o->max_prefix >= 0 &&
+                 o->ttl_seconds >= 0.0,
+             "prefix cache: negative limit");
+    s->pc_on = true;
+    s->pc_max_entries = o->max_entries;
+    s->pc_max_bytes = o->max_bytes;
+    s->pc_max_prefix = o->max_prefix;
+    s->pc_ttl = o->ttl_seconds;
+    pc_evict(s);
+  });
+}
+int gn_session_prefix_cache_invalidate(gn_session* s) {
+  return guard([&] {
+    GN_CHECK(s, "null session");
+    GN_HIP(hipSetDevice(s->device));
+    pc_clear(s);
+  });
+}
+int gn_session_prefix_cache_len(gn_session* s, int32_t* entries, int64_t* bytes) {
+  return guard([&] {
+    GN_CHECK(s && entries, "null argument");
+    pc_expire(s);
+    *entries = (int32_t)s->pc_entries.size();
+    if (bytes) *bytes = s->pc_bytes;
+  });
+}
+int gn_session_prefix_cache_hits(const gn_session* s, int32_t* hits, int32_t groups) {
+  return guard([&] {
+    GN_CHECK(s && hits, "null argument");
+    GN_CHECK(groups == (int32_t)s->pc_hits.size(), "prefix cache: groups differ from the last call");
+    std::copy(s->pc_hits.begin(), s->pc_hits.end(), hits);
+  });
+}
+
 // ---- optimizer ---------------------------------------------------------------
 struct gn_optimizer {
   gn_session* s = nullptr;
@@ -2653,6 +3027,7 @@ int gn_optimizer_step(gn_optimizer* o) {
     optimizer_step(o->ts, s->stream, s->arena.get());
     GN_HIP(hipStreamSynchronize(s->stream));
     s->derived_dirty = true;  // absorbed decode weights follow the parameters
+    pc_clear(s);              // and stored prefills are stale
   });
 }
 int gn_optimizer_state_size(const gn_optimizer* o, int64_t* count) {

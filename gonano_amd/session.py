@@ -12,7 +12,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import GnConfig, GnGenerateOptions, GnTiming, GnToolFn, call, lib
+from ._lib import GnConfig, GnGenerateOptions, GnPrefixCacheOptions, GnTiming, GnToolFn, call, lib
 from .config import Config
 
 
@@ -230,6 +230,38 @@ class Session:
         """Replay rollout decode steps from one captured HIP graph (default)
         or launch every kernel of every step."""
         call("gn_session_set_decode_graph", self._h, 1 if enabled else 0)
+
+    def set_prefix_cache(self, max_entries: int = 0, max_bytes: int = 0, ttl: float = 0.0,
+                         max_prefix: int = 0, enabled: bool = True):
+        """Engine.Cache = NewCacheManager(CacheOptions{MaxEntries, MaxBytes,
+        TTL}) on the device (inference/cache.go:17-77); max_entries=1 with
+        max_prefix is Engine.Prefix = NewPrefixCache(maxPrefix)
+        (inference/prefix.go:29-35).  enabled=False turns it off and drops
+        every entry.  Generate and RL-step calls then prefill only what
+        follows each prompt's longest cached strict prefix."""
+        if not enabled:
+            call("gn_session_set_prefix_cache", self._h, None)
+            return
+        o = GnPrefixCacheOptions(max_entries, max_prefix, max_bytes, ttl)
+        call("gn_session_set_prefix_cache", self._h, C.byref(o))
+
+    def prefix_cache_invalidate(self):
+        """CacheManager.Invalidate (inference/cache.go:162-174)."""
+        call("gn_session_prefix_cache_invalidate", self._h)
+
+    def prefix_cache_len(self) -> tuple[int, int]:
+        """CacheManager.Len (inference/cache.go:176-180) and the entries'
+        device bytes."""
+        n, b = C.c_int32(), C.c_int64()
+        call("gn_session_prefix_cache_len", self._h, C.byref(n), C.byref(b))
+        return n.value, b.value
+
+    def prefix_cache_hits(self, groups: int) -> np.ndarray:
+        """Per group of the last generate call, the prompt tokens its cache
+        lookup matched (0: a miss)."""
+        out = np.zeros(groups, np.int32)
+        call("gn_session_prefix_cache_hits", self._h, out, groups)
+        return out
 
     def timing(self) -> dict:
         t = GnTiming()

@@ -396,6 +396,42 @@ int gn_session_aux_loss(const gn_session *session, double *out);
  * backends are synchronous; used to bracket timed regions). */
 int gn_session_synchronize(gn_session *session);
 
+/* ---- prefix cache (inference/cache.go CacheManager, inference/prefix.go
+ * PrefixCache) -------------------------------------------------------------
+ * Engine.Cache / Engine.Prefix (inference/engine.go:44-51, 120-173) kept in
+ * device memory: gn_generate_batch(_with) and gn_rl_step(_with) look every
+ * prompt up and store its prefill state; a prompt whose longest stored strict
+ * prefix has m tokens prefills only its last prompt_len - m tokens against
+ * the stored keys/values.  A batch of groups sees the cache as that many
+ * successive GenerateWith calls would (an earlier group's entry can serve a
+ * later group).  An entry holds every layer's keys/values of its prompt, its
+ * decode-cache rows and its last token embedding (KVBuffer.PrevEmbedding);
+ * `bytes` counts that device memory.  Entries are dropped whenever the
+ * parameters change (gn_session_set_params, gn_optimizer_step): their state
+ * would no longer equal a full prefill.  Not for compressed-attention or CED
+ * models (GN_ERR_UNSUPPORTED; the reference skips CED too,
+ * inference/prefix.go:17-19).  The on-disk tier (CacheOptions.DiskDir) and
+ * its sliding-window stripping are not built. */
+typedef struct gn_prefix_cache_options {
+  int32_t max_entries; /* CacheOptions.MaxEntries; 0: unbounded */
+  int32_t max_prefix;  /* NewPrefixCache(maxPrefix): longer entries never hit; 0: any */
+  int64_t max_bytes;   /* CacheOptions.MaxBytes (device bytes); 0: unbounded */
+  double ttl_seconds;  /* CacheOptions.TTL from storage; 0: no expiry */
+} gn_prefix_cache_options;
+/* NewCacheManager (cache.go:64-77) on the session: turns the cache on with
+ * these limits (evicting to fit), or off with options NULL (dropping every
+ * entry).  max_entries 1 with max_prefix is NewPrefixCache(maxPrefix). */
+int gn_session_set_prefix_cache(gn_session *session, const gn_prefix_cache_options *options);
+/* CacheManager.Invalidate (cache.go:162-174). */
+int gn_session_prefix_cache_invalidate(gn_session *session);
+/* CacheManager.Len (cache.go:176-180) after expiry, and the entries' device
+ * bytes (bytes nullable). */
+int gn_session_prefix_cache_len(gn_session *session, int32_t *entries, int64_t *bytes);
+/* Per group of the last generate call, the prompt tokens taken from the
+ * cache (Lookup's matched length; 0 for a miss or with the cache off).
+ * groups must equal that call's. */
+int gn_session_prefix_cache_hits(const gn_session *session, int32_t *hits, int32_t groups);
+
 #ifdef __cplusplus
 }
 #endif
