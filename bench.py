@@ -10,7 +10,7 @@ synthetic (uniform prompt ids, InitWeights-distributed random weights) and
 resident in HBM before the timed region.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config d12|d2|d20|latent_d12|flash_d12]
-                    [--phase rl|train|rollout|optimizer] [--no-graph]
+                    [--phase rl|train|rollout|optimizer|prefix] [--no-graph]
 """
 from __future__ import annotations
 
@@ -111,13 +111,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="d12", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--phase", default="rl", choices=["rl", "train", "rollout", "optimizer"],
+    ap.add_argument("--phase", default="rl",
+                    choices=["rl", "train", "rollout", "optimizer", "prefix"],
                     help="rl: the full RL step (the benchmark); train: only the recompute + "
                          "PG fwd/bwd on a synthetic batch of the workload's shape (for "
                          "counter profiles of the train-phase kernels); rollout: only the "
                          "rollouts (for kernel-trace and counter profiles of the decode "
                          "kernels in place); optimizer: only MuonAdamW steps with "
-                         "cmd/chat_rl's parameter groups")
+                         "cmd/chat_rl's parameter groups; prefix: the prompts' prefill "
+                         "with and without the device prefix cache")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every decode kernel instead of replaying the captured decode "
                          "graph (for kernel-trace profiles: rocprofv3 --kernel-trace has "
@@ -160,6 +162,8 @@ def main() -> int:
         return rollout_phase(args, sess, prompts, S, N, temp)
     if args.phase == "optimizer":
         return optimizer_phase(args, cfg, sess, prompts)
+    if args.phase == "prefix":
+        return prefix_phase(args, cfg, sess, prompts, temp)
 
     def step(i: int):
         seeds = np.array([i * 1000 + g for g in range(groups)], np.uint64)
@@ -401,6 +405,50 @@ def optimizer_phase(args, cfg, sess, prompts) -> int:
     res = optimizer_timing(cfg, sess, steps=args.steps)
     sess.close()
     print(json.dumps({"config": args.config, "optimizer": res}), flush=True)
+    return 0
+
+
+def prefix_phase(args, cfg, sess, prompts, temp) -> int:
+    """The prompts' prefill (Engine.GenerateWith's step 1, one sampled token
+    per prompt) without and with the device prefix cache
+    (inference/cache.go): the workload's prompts share their first 3/4 with
+    a stored prompt (a system prompt prefilled once, then each prompt's own
+    last quarter), so with the cache every prompt continues from the stored
+    keys/values over its last quarter.  Both legs run the same prompts and
+    return the same kind of rows; each call's host wall time is taken."""
+    G_, P = prompts.shape
+    m = 3 * P // 4
+    prompts = prompts.copy()
+    prompts[:, :m] = prompts[0, :m]
+    seeds = np.arange(G_, dtype=np.uint64)
+
+    def timed(n):
+        out = []
+        for _ in range(n):
+            sess.synchronize()
+            t0 = time.perf_counter()
+            sess.generate_batch(prompts, 1, 1, temp, 50, seeds)
+            out.append(1e3 * (time.perf_counter() - t0))
+        return out
+
+    timed(args.warmup)
+    full = timed(args.steps)
+    sess.set_prefix_cache(max_entries=4 * G_)
+    sess.generate_batch(prompts[:1, :m], 1, 1, temp, 50, seeds[:1])  # the shared prefix, stored
+    timed(args.warmup)
+    cached = timed(args.steps)
+    hits = sess.prefix_cache_hits(G_)
+    entries, nbytes = sess.prefix_cache_len()
+    sess.close()
+    assert (hits == m).all(), hits
+    med = lambda v: float(np.median(v))  # noqa: E731
+    print(json.dumps({
+        "metric": "prompt prefill ms (one sampled token per prompt)", "config": args.config,
+        "prompts": G_, "prompt_len": P, "cached_prefix": m, "steps": args.steps,
+        "full_prefill_ms": round(med(full), 3), "cached_prefill_ms": round(med(cached), 3),
+        "speedup": round(med(full) / med(cached), 2),
+        "prefill_tokens_full": G_ * P, "prefill_tokens_cached": G_ * (P - m),
+        "cache_entries": entries, "cache_bytes": nbytes}), flush=True)
     return 0
 
 

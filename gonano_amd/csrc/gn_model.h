@@ -10,6 +10,16 @@ void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, 
                         int B, int T, int C, float* raw, float* embn, float* smsig, float* x,
                         hipStream_t st, const float* seed_prev = nullptr,
                         float* seedsig = nullptr);
+// A batch of strided copies in one launch: block `d` copies outer x inner
+// rows of `count` floats, row (o, i) at src + o*s_outer + i*s_inner to
+// dst + o*d_outer + i*d_inner.  The descriptors live in device memory.
+struct CopyBlock {
+  const float* src;
+  float* dst;
+  int64_t count, s_outer, s_inner, d_outer, d_inner;
+  int32_t outer, inner;
+};
+void launch_copy_blocks(const CopyBlock* descs, int n, hipStream_t st);
 void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg, const float* lam,
                          int rows, int C, float* prev, float* x, float* x0, hipStream_t st);
 // xin (resp. x) may be the target of a residual-add GEMM whose split-K sum

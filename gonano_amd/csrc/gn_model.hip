@@ -492,6 +492,38 @@ __global__ void expand_last_rows_kernel(const float* __restrict__ src, float* __
   int g = (int)(row / S);
   dst[i] = src[((int64_t)g * T + T - 1) * C + c];
 }
+// One grid row per descriptor; each row's floats are split into chunks of
+// COPY_CHUNK spread over the blocks of the grid row, 16-byte moves where the
+// addresses, pitches and count allow it.
+constexpr int COPY_CHUNK = 4096;
+__global__ __launch_bounds__(256) void copy_blocks_kernel(const CopyBlock* __restrict__ descs) {
+  const CopyBlock d = descs[blockIdx.y];
+  const int64_t chunks = (d.count + COPY_CHUNK - 1) / COPY_CHUNK;
+  const int64_t work = chunks * d.outer * d.inner;
+  const bool vec = ((reinterpret_cast<uintptr_t>(d.src) | reinterpret_cast<uintptr_t>(d.dst)) & 15) == 0 &&
+                   ((d.count | d.s_outer | d.s_inner | d.d_outer | d.d_inner) & 3) == 0;
+  for (int64_t w = blockIdx.x; w < work; w += gridDim.x) {
+    const int64_t row = w / chunks, c0 = (w % chunks) * COPY_CHUNK;
+    const int64_t o = row / d.inner, i = row % d.inner;
+    const float* src = d.src + o * d.s_outer + i * d.s_inner + c0;
+    float* dst = d.dst + o * d.d_outer + i * d.d_inner + c0;
+    const int n = (int)min<int64_t>(COPY_CHUNK, d.count - c0);
+    if (vec) {
+      for (int k = threadIdx.x; k < n / 4; k += 256)
+        reinterpret_cast<float4*>(dst)[k] = reinterpret_cast<const float4*>(src)[k];
+    } else {
+      for (int k = threadIdx.x; k < n; k += 256) dst[k] = src[k];
+    }
+  }
+}
+
+void launch_copy_blocks(const CopyBlock* descs, int n, hipStream_t st) {
+  if (n <= 0) return;
+  GN_CHECK(n <= 65535, "copy_blocks: too many descriptors");
+  hipLaunchKernelGGL(copy_blocks_kernel, dim3(256, (unsigned)n), dim3(256), 0, st, descs);
+  GN_HIP(hipGetLastError());
+}
+
 void launch_expand_last_rows(const float* src, float* dst, int G, int T, int S, int C,
                              hipStream_t st) {
   int64_t total = (int64_t)G * S * C;

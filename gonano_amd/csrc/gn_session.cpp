@@ -162,6 +162,9 @@ struct gn_session {
   int64_t pc_bytes = 0;
   bool pc_defer = false;    // removed entries wait in pc_retired for the stream
   std::vector<std::unique_ptr<PrefixEntry>> pc_retired;
+  // device memory of removed entries kept for the next call's entries
+  // (hipFree synchronizes the device): (bytes, pointer)
+  std::vector<std::pair<int64_t, float*>> pc_pool;
   std::vector<int32_t> pc_hits;  // prompt tokens taken from the cache, per group of the last call
   // decode steps replayed from one captured HIP graph per rollout
   bool decode_graph = true;
@@ -612,14 +615,17 @@ struct SeqBuffers {
   std::vector<float*> pre_kc, pre_vc;
   int gblocks = 0;
   int pf_maxseq = 0;  // prefill raw caches' length (0: T)
-  // continuation of a cached prefix (prefix cache hit, B == 1): pre_len
-  // positions already computed, their token-major keys/values per layer
-  // pre_k/pre_v [L][pre_len][Hkv*128] and the previous token's embedding
-  // seed_prev [C] for the smear; qoff == pre_len
+  // continuation of cached prefixes (prefix cache hits): pre_len positions
+  // of every sequence already computed.  kv_k/kv_v [L][B][pre_len+T][Hkv*128]
+  // hold their token-major keys/values in the first pre_len rows of each
+  // sequence; the forward writes the new rows after them and attends the
+  // whole.  seed_prev [B][C] is each sequence's previous-token embedding for
+  // the smear; qoff == pre_len
   int pre_len = 0;
-  const float *pre_k = nullptr, *pre_v = nullptr, *seed_prev = nullptr;
-  // when set, every layer's token-major keys/values of the whole sequence
-  // (prefix included) are copied here: [L][B*(pre_len+T)][Hkv*128]
+  float *kv_k = nullptr, *kv_v = nullptr;
+  const float* seed_prev = nullptr;
+  // when set (a forward from position 0), every layer's token-major
+  // keys/values are copied here: [L][B*T][Hkv*128]
   float *tm_k_out = nullptr, *tm_v_out = nullptr;
   // prefill: the decode caches to fill (indexer keys [L][G*S][maxBlocks]
   // [Hkv][HI] of the complete blocks, replicated over S rows per prompt)
@@ -900,23 +906,21 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   float* qkv = s->mla ? nullptr : A<float>(s, "qkv", N * s->QKVW);
   const int bk = L / 2;
   sb.backout = nullptr;
-  GN_CHECK(sb.pre_len == 0 || (B == 1 && !save && !s->hca && sb.qoff == sb.pre_len && sb.pre_k &&
-                                sb.pre_v),
-           "prefix continuation: one sequence, prefill only, dense or latent attention");
+  GN_CHECK(sb.pre_len == 0 || (!save && !s->hca && sb.qoff == sb.pre_len && sb.kv_k && sb.kv_v &&
+                                !sb.tm_k_out),
+           "prefix continuation: prefill only, dense or latent attention");
+  const int Tall = sb.pre_len + T;  // keys per sequence
+  // the new rows' keys/values into the rows after each sequence's prefix
+  auto append_rows = [&](float* all, const float* rows) {
+    GN_HIP(hipMemcpy2DAsync(all + (int64_t)sb.pre_len * s->KVW, sizeof(float) * Tall * s->KVW, rows,
+                            sizeof(float) * T * s->KVW, sizeof(float) * T * s->KVW, B,
+                            hipMemcpyDeviceToDevice, st));
+  };
   for (int l = sb.l0; l < l_end; l++) {
     Layer& ly = s->layers[l];
     sb.xin[l] = xcur;
-    // a continued prefix: this layer's keys/values of the whole sequence,
-    // the cached rows first, the new ones written after them
-    float* pre_k = nullptr;
-    float* pre_v = nullptr;
-    if (sb.pre_len > 0) {
-      const int64_t pk = (int64_t)sb.pre_len * s->KVW;
-      pre_k = A<float>(s, "pc_kall", (int64_t)(sb.pre_len + T) * s->KVW);
-      pre_v = A<float>(s, "pc_vall", (int64_t)(sb.pre_len + T) * s->KVW);
-      GN_HIP(hipMemcpyAsync(pre_k, sb.pre_k + l * pk, sizeof(float) * pk, hipMemcpyDeviceToDevice, st));
-      GN_HIP(hipMemcpyAsync(pre_v, sb.pre_v + l * pk, sizeof(float) * pk, hipMemcpyDeviceToDevice, st));
-    }
+    float* pre_k = sb.pre_len > 0 ? sb.kv_k + (int64_t)l * B * Tall * s->KVW : nullptr;
+    float* pre_v = sb.pre_len > 0 ? sb.kv_v + (int64_t)l * B * Tall * s->KVW : nullptr;
     if (s->split > 0 && l == s->split) {  // encoderHidden (transformer.go:310-312)
       sb.enc = A<float>(s, "ced_enc", N * C);
       GN_HIP(hipMemcpyAsync(sb.enc, xcur, sizeof(float) * N * C, hipMemcpyDeviceToDevice, st));
@@ -943,8 +947,8 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
       ma.xa = xa; ma.xw = s->XW; ma.qc = qc; ma.kvu = kvu; ma.cosT = s->cosT; ma.sinT = s->sinT;
       ma.Hq = Hq; ma.Hkv = Hkv; ma.lat = s->lat; ma.rd = s->rd; ma.T = T; ma.pos0 = sb.qoff;
       ma.q = layer_buf(s, "qn", l, save, N * Hq * HD);
-      ma.k = pre_k ? pre_k + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "kn", l, save, N * s->KVW);
-      ma.v = pre_v ? pre_v + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "v", l, save, N * s->KVW);
+      ma.k = layer_buf(s, "kn", l, save, N * s->KVW);
+      ma.v = layer_buf(s, "v", l, save, N * s->KVW);
       if (mode == SEQ_PREFILL) {  // latent + rotary-key cache of the prompt
         const int pm = sb.pf_maxseq > 0 ? sb.pf_maxseq : T;
         ma.lat_cache = kcache_pf + (int64_t)l * B * pm * s->lat;
@@ -954,8 +958,8 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
       launch_mla_assemble(ma, N, st);
       sb.xa[l] = xa;
       sb.qn[l] = ma.q;
-      sb.kn[l] = pre_k ? pre_k : ma.k;
-      sb.v[l] = pre_v ? pre_v : ma.v;
+      sb.kn[l] = ma.k;
+      sb.v[l] = ma.v;
     } else {
     sgemm(s, linear_fwd_desc(h, ly.wqkv, qkv, (int)N, C, s->QKVW));
     QkvPostArgs qa{};
@@ -964,8 +968,8 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     qa.cosT = s->cosT; qa.sinT = s->sinT;
     qa.C = C; qa.Hq = Hq; qa.Hkv = Hkv; qa.R = s->R; qa.T = T; qa.pos0 = sb.qoff;
     qa.qn = layer_buf(s, "qn", l, save, N * Hq * HD);
-    qa.kn = pre_k ? pre_k + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "kn", l, save, N * s->KVW);
-    qa.vout = pre_v ? pre_v + (int64_t)sb.pre_len * s->KVW : layer_buf(s, "v", l, save, N * s->KVW);
+    qa.kn = layer_buf(s, "kn", l, save, N * s->KVW);
+    qa.vout = layer_buf(s, "v", l, save, N * s->KVW);
     qa.qrot = save ? layer_buf(s, "qrot", l, true, N * Hq * HD) : nullptr;
     qa.krot = save ? layer_buf(s, "krot", l, true, N * s->KVW) : nullptr;
     qa.vesig = (save && ly.has_ve) ? layer_buf(s, "vesig", l, true, N * Hkv) : nullptr;
@@ -978,12 +982,18 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
     }
     launch_qkv_post(qa, N, st);
     sb.qn[l] = qa.qn;
-    sb.kn[l] = pre_k ? pre_k : qa.kn;
-    sb.v[l] = pre_v ? pre_v : qa.vout;
+    sb.kn[l] = qa.kn;
+    sb.v[l] = qa.vout;
     sb.qrot[l] = qa.qrot; sb.krot[l] = qa.krot; sb.vesig[l] = qa.vesig;
     }
-    if (sb.tm_k_out) {  // the whole sequence's keys/values of this layer
-      const int64_t tm = (int64_t)B * (sb.pre_len + T) * s->KVW;
+    if (pre_k) {  // attend the cached prefixes and the new rows
+      append_rows(pre_k, sb.kn[l]);
+      append_rows(pre_v, sb.v[l]);
+      sb.kn[l] = pre_k;
+      sb.v[l] = pre_v;
+    }
+    if (sb.tm_k_out) {  // this layer's keys/values of every sequence
+      const int64_t tm = (int64_t)B * T * s->KVW;
       GN_HIP(hipMemcpyAsync(sb.tm_k_out + l * tm, sb.kn[l], sizeof(float) * tm,
                             hipMemcpyDeviceToDevice, st));
       GN_HIP(hipMemcpyAsync(sb.tm_v_out + l * tm, sb.v[l], sizeof(float) * tm,
@@ -997,7 +1007,7 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
       fa.o = layer_buf(s, "o", l, save, N * Hq * HD);
       fa.lse = save ? layer_buf(s, "lse", l, true, N * Hq) : nullptr;
       fa.B = B; fa.T = T; fa.Hq = Hq; fa.Hkv = Hkv; fa.window = ly.window;
-      fa.Tk = sb.pre_len + T; fa.qoff = sb.pre_len;  // keys of the cached prefix first
+      fa.Tk = Tall; fa.qoff = sb.pre_len;  // keys of the cached prefix first
       launch_flash_fwd(fa, st);
       sb.o[l] = fa.o; sb.lse[l] = fa.lse;
     }
@@ -2091,9 +2101,27 @@ static void pc_remove(gn_session* s, size_t i) {
   else (void)hipFree(e->mem);
   s->pc_entries.erase(s->pc_entries.begin() + i);
 }
-static void pc_flush(gn_session* s) {
-  for (auto& e : s->pc_retired) (void)hipFree(e->mem);
+// Removed entries' memory goes to the pool, which keeps at most `keep`
+// buffers (the newest); the rest is released.
+static void pc_flush(gn_session* s, size_t keep = 0) {
+  for (auto& e : s->pc_retired) s->pc_pool.push_back({e->bytes, e->mem});
   s->pc_retired.clear();
+  while (s->pc_pool.size() > keep) {
+    (void)hipFree(s->pc_pool.front().second);
+    s->pc_pool.erase(s->pc_pool.begin());
+  }
+}
+// Memory for a new entry: a pooled buffer of the same size, else hipMalloc.
+static float* pc_alloc(gn_session* s, int64_t bytes) {
+  for (size_t i = s->pc_pool.size(); i-- > 0;)
+    if (s->pc_pool[i].first == bytes) {
+      float* p = s->pc_pool[i].second;
+      s->pc_pool.erase(s->pc_pool.begin() + i);
+      return p;
+    }
+  float* p = nullptr;
+  GN_HIP(hipMalloc(&p, bytes));
+  return p;
 }
 // expireLocked (cache.go:236-252): entries stored longer ago than the TTL
 static void pc_expire(gn_session* s) {
@@ -2143,18 +2171,35 @@ static void pc_insert(gn_session* s, std::unique_ptr<gn_session::PrefixEntry> e)
   s->pc_entries.push_back(std::move(e));
   pc_evict(s);
 }
+// Every entry, and the pooled memory, released.
 static void pc_clear(gn_session* s) {
   while (!s->pc_entries.empty()) pc_remove(s, s->pc_entries.size() - 1);
+  if (!s->pc_defer) pc_flush(s);
 }
 
-// Rows [0, count) of each of `layers` blocks: dst (block pitch dpitch floats)
-// <- src (block pitch spitch).
-static void copy_layer_rows(float* dst, int64_t dpitch, const float* src, int64_t spitch,
-                            int64_t count, int layers, hipStream_t st) {
-  if (count <= 0) return;
-  GN_HIP(hipMemcpy2DAsync(dst, sizeof(float) * dpitch, src, sizeof(float) * spitch,
-                          sizeof(float) * count, layers, hipMemcpyDeviceToDevice, st));
-}
+// Strided copies gathered on the host and run as one launch per batch.  The
+// host descriptor arrays stay alive until the owner has synchronized the
+// stream.
+struct CopyList {
+  std::vector<CopyBlock> v;
+  std::vector<std::vector<CopyBlock>> sent;
+  void add(const float* src, float* dst, int64_t count, int outer, int64_t s_outer,
+           int64_t d_outer, int inner = 1, int64_t s_inner = 0, int64_t d_inner = 0) {
+    if (count > 0 && outer > 0 && inner > 0)
+      v.push_back(CopyBlock{src, dst, count, s_outer, s_inner, d_outer, d_inner, outer, inner});
+  }
+  void run(gn_session* s, const char* name) {
+    if (v.empty()) return;
+    sent.push_back(std::move(v));
+    v.clear();
+    const auto& h = sent.back();
+    CopyBlock* d = A<CopyBlock>(s, name, h.size());
+    GN_HIP(hipMemcpyAsync(d, h.data(), sizeof(CopyBlock) * h.size(), hipMemcpyHostToDevice,
+                          s->stream));
+    for (size_t i = 0; i < h.size(); i += 65535)
+      launch_copy_blocks(d + i, (int)std::min<size_t>(65535, h.size() - i), s->stream);
+  }
+};
 
 // The prefill of GenerateWith with a prefix cache (engine.go:120-173), for G
 // prompts as G successive calls would see the cache: prompt g looks up the
@@ -2163,18 +2208,18 @@ static void copy_layer_rows(float* dst, int64_t dpitch, const float* src, int64_
 // strict prefix of another, but an earlier prompt's store can evict the
 // entry a later one would have hit).  That sequence is settled on the host
 // first, with the memory of entries it removes kept until the prefill has
-// run; then the prompts without a hit are prefilled together from position 0
-// and every hit continues from its entry over the rest of its prompt (B = 1:
-// the entry's keys attended first, its decode-cache rows copied in, the
-// smear seeded with its stored embedding -- KVBuffer.PrevEmbedding).  Fills
-// the decode prefill caches kpf/vpf (the plain prefill's layout) and each
-// prompt's last-row final norm and embedding lastfn/lastemb [G][C].
+// run.  Then the prompts without a hit are prefilled together from position
+// 0, and the hits, batched by matched length m, continue from their entries
+// over the last P - m tokens (the entries' keys attended first, their
+// decode-cache rows copied in, the smear seeded with their stored embedding
+// -- KVBuffer.PrevEmbedding).  Fills the decode prefill caches kpf/vpf (the
+// plain prefill's layout) and each prompt's last-row final norm and
+// embedding lastfn/lastemb [G][C].
 static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, float* kpf,
                            float* vpf, float* lastfn, float* lastemb) {
   GN_CHECK(!s->hca && s->split == 0,
            "prefix cache: compressed-attention and CED models are not cached");
   const int L = s->L, C = s->C, Hkv = s->Hkv;
-  hipStream_t st = s->stream;
   const int64_t KVW = s->KVW;
   // floats per (layer, prompt) of the decode prefill caches
   const int64_t kg = s->mla ? (int64_t)P * s->lat : (int64_t)Hkv * P * HD;
@@ -2187,6 +2232,8 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
   };
   std::vector<Plan> plan(G);
   std::vector<gn_session::PrefixEntry*> made;
+  CopyList cp;
+  std::vector<std::vector<int32_t>> ids_kept;  // uploaded token ids, until the stream is idle
   s->pc_defer = true;
   try {
     // 1) the cache sequence of G successive GenerateWith calls
@@ -2199,7 +2246,7 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
       auto ne = std::make_unique<gn_session::PrefixEntry>();
       ne->tokens.assign(toks, toks + P);
       ne->bytes = sizeof(float) * lay.total;
-      GN_HIP(hipMalloc(&ne->mem, ne->bytes));
+      ne->mem = pc_alloc(s, ne->bytes);
       ne->stored_at = pc_now();
       plan[g].dst = ne.get();
       made.push_back(ne.get());
@@ -2207,88 +2254,107 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
     }
     s->pc_hits.assign(G, 0);
     for (int g = 0; g < G; g++) s->pc_hits[g] = plan[g].m;
+    // one batch of prompts (prompt g at batch row i), positions [m, P): the
+    // forward's decode caches kt/vt [L][B] and its last rows into the
+    // call's per-prompt outputs, the whole prompts' keys/values into their
+    // entries
+    auto collect = [&](const std::vector<int>& gs, int m, SeqBuffers& sb, const float* kt,
+                       const float* vt, const float* kall, const float* vall) {
+      const int B = (int)gs.size(), T = P - m;
+      for (int i = 0; i < B; i++) {
+        const int g = gs[i];
+        cp.add(kt + i * kg, kpf + g * kg, kg, L, B * kg, G * kg);
+        cp.add(vt + i * vg, vpf + g * vg, vg, L, B * vg, G * vg);
+        const int64_t last = ((int64_t)i * T + T - 1) * C;
+        cp.add(sb.fn + last, lastfn + (int64_t)g * C, C, 1, 0, 0);
+        cp.add(sb.embn + last, lastemb + (int64_t)g * C, C, 1, 0, 0);
+        float* dm = plan[g].dst->mem;
+        cp.add(kall + (int64_t)i * P * KVW, dm + lay.ktm, (int64_t)P * KVW, L, (int64_t)B * P * KVW,
+               (int64_t)P * KVW);
+        cp.add(vall + (int64_t)i * P * KVW, dm + lay.vtm, (int64_t)P * KVW, L, (int64_t)B * P * KVW,
+               (int64_t)P * KVW);
+        // the state stored with the prompt: its decode-cache rows and last embedding
+        cp.add(kt + i * kg, dm + lay.kdc, kg, L, B * kg, kg);
+        cp.add(vt + i * vg, dm + lay.vdc, vg, L, B * vg, vg);
+        cp.add(sb.embn + last, dm + lay.prev, C, 1, 0, 0);
+      }
+      cp.run(s, "pc_desc_out");
+    };
     // 2) prompts with no cached prefix, together from position 0
     std::vector<int> miss;
-    for (int g = 0; g < G; g++)
-      if (!plan[g].src) miss.push_back(g);
+    std::vector<std::pair<int, int>> hits;  // (m, g)
+    for (int g = 0; g < G; g++) {
+      if (plan[g].src) hits.push_back({plan[g].m, g});
+      else miss.push_back(g);
+    }
     if (!miss.empty()) {
-      const int Gm = (int)miss.size();
-      std::vector<int32_t> ids((size_t)Gm * P);
-      for (int i = 0; i < Gm; i++)
+      const int B = (int)miss.size();
+      ids_kept.emplace_back((size_t)B * P);
+      std::vector<int32_t>& ids = ids_kept.back();
+      for (int i = 0; i < B; i++)
         memcpy(ids.data() + (size_t)i * P, prompts + (int64_t)miss[i] * P, sizeof(int32_t) * P);
       SeqBuffers sb;
-      sb.B = Gm; sb.T = P; sb.N = (int64_t)Gm * P;
+      sb.B = B; sb.T = P; sb.N = (int64_t)B * P;
       sb.ids = upload_ids(s, "pc_ids", ids.data(), sb.N, s->V);
-      sb.tm_k_out = A<float>(s, "pc_tmk", (size_t)L * sb.N * KVW);
-      sb.tm_v_out = A<float>(s, "pc_tmv", (size_t)L * sb.N * KVW);
-      float* kt = A<float>(s, "pc_kt", (size_t)L * Gm * kg);
-      float* vt = A<float>(s, "pc_vt", (size_t)L * Gm * vg);
+      sb.tm_k_out = A<float>(s, "pc_kall", (size_t)L * sb.N * KVW);
+      sb.tm_v_out = A<float>(s, "pc_vall", (size_t)L * sb.N * KVW);
+      float* kt = A<float>(s, "pc_kt", (size_t)L * B * kg);
+      float* vt = A<float>(s, "pc_vt", (size_t)L * B * vg);
       seq_forward(s, sb, SEQ_PREFILL, kt, vt);
-      for (int i = 0; i < Gm; i++) {
-        const int g = miss[i];
-        copy_layer_rows(kpf + g * kg, G * kg, kt + i * kg, Gm * kg, kg, L, st);
-        copy_layer_rows(vpf + g * vg, G * vg, vt + i * vg, Gm * vg, vg, L, st);
-        const int64_t last = ((int64_t)i * P + P - 1) * C;
-        GN_HIP(hipMemcpyAsync(lastfn + (int64_t)g * C, sb.fn + last, sizeof(float) * C,
-                              hipMemcpyDeviceToDevice, st));
-        GN_HIP(hipMemcpyAsync(lastemb + (int64_t)g * C, sb.embn + last, sizeof(float) * C,
-                              hipMemcpyDeviceToDevice, st));
-        float* dm = plan[g].dst->mem;
-        copy_layer_rows(dm + lay.ktm, (int64_t)P * KVW, sb.tm_k_out + (int64_t)i * P * KVW,
-                        sb.N * KVW, (int64_t)P * KVW, L, st);
-        copy_layer_rows(dm + lay.vtm, (int64_t)P * KVW, sb.tm_v_out + (int64_t)i * P * KVW,
-                        sb.N * KVW, (int64_t)P * KVW, L, st);
-      }
+      collect(miss, 0, sb, kt, vt, sb.tm_k_out, sb.tm_v_out);
     }
-    // the state stored with prompt g: its decode-cache rows and last embedding
-    auto fill_entry = [&](int g) {
-      float* dm = plan[g].dst->mem;
-      copy_layer_rows(dm + lay.kdc, kg, kpf + g * kg, G * kg, kg, L, st);
-      copy_layer_rows(dm + lay.vdc, vg, vpf + g * vg, G * vg, vg, L, st);
-      GN_HIP(hipMemcpyAsync(dm + lay.prev, lastemb + (int64_t)g * C, sizeof(float) * C,
-                            hipMemcpyDeviceToDevice, st));
-    };
-    for (int g : miss) fill_entry(g);
-    // 3) every hit continues from its entry
-    for (int g = 0; g < G; g++) {
-      if (!plan[g].src) continue;
-      const int m = plan[g].m, T = P - m;
+    // 3) hits, one batch per matched length (one prompt length per call, so
+    //    equal m means equal continuation length)
+    std::sort(hits.begin(), hits.end());
+    for (size_t h0 = 0; h0 < hits.size();) {
+      size_t h1 = h0;
+      while (h1 < hits.size() && hits[h1].first == hits[h0].first) h1++;
+      const int m = hits[h0].first, T = P - m, B = (int)(h1 - h0);
+      std::vector<int> gs;
+      for (size_t h = h0; h < h1; h++) gs.push_back(hits[h].second);
       const PcLayout el = pc_layout(s, m);
-      const float* em = plan[g].src->mem;
-      float* kt = A<float>(s, "pc_kt1", (size_t)L * kg);
-      float* vt = A<float>(s, "pc_vt1", (size_t)L * vg);
-      if (s->mla) {  // latent rows and rotated keys of positions [0, m)
-        copy_layer_rows(kt, kg, em + el.kdc, (int64_t)m * s->lat, (int64_t)m * s->lat, L, st);
-        copy_layer_rows(vt, vg, em + el.vdc, (int64_t)m * Hkv * s->rd, (int64_t)m * Hkv * s->rd,
-                        L, st);
-      } else {  // K and V rows of positions [0, m) of every (layer, KV head)
-        copy_layer_rows(kt, (int64_t)P * HD, em + el.kdc, (int64_t)m * HD, (int64_t)m * HD,
-                        L * Hkv, st);
-        copy_layer_rows(vt, (int64_t)P * HD, em + el.vdc, (int64_t)m * HD, (int64_t)m * HD,
-                        L * Hkv, st);
+      float* kall = A<float>(s, "pc_kall", (size_t)L * B * P * KVW);
+      float* vall = A<float>(s, "pc_vall", (size_t)L * B * P * KVW);
+      float* kt = A<float>(s, "pc_kt", (size_t)L * B * kg);
+      float* vt = A<float>(s, "pc_vt", (size_t)L * B * vg);
+      float* prev = A<float>(s, "pc_prev", (size_t)B * C);
+      ids_kept.emplace_back((size_t)B * T);
+      std::vector<int32_t>& ids = ids_kept.back();
+      for (int i = 0; i < B; i++) {
+        const float* em = plan[gs[i]].src->mem;
+        memcpy(ids.data() + (size_t)i * T, prompts + (int64_t)gs[i] * P + m, sizeof(int32_t) * T);
+        // the entry's keys/values: rows [0, m) of sequence i of every layer
+        cp.add(em + el.ktm, kall + (int64_t)i * P * KVW, (int64_t)m * KVW, L, (int64_t)m * KVW,
+               (int64_t)B * P * KVW);
+        cp.add(em + el.vtm, vall + (int64_t)i * P * KVW, (int64_t)m * KVW, L, (int64_t)m * KVW,
+               (int64_t)B * P * KVW);
+        if (s->mla) {  // latent rows and rotated keys of positions [0, m)
+          cp.add(em + el.kdc, kt + i * kg, (int64_t)m * s->lat, L, (int64_t)m * s->lat, B * kg);
+          cp.add(em + el.vdc, vt + i * vg, (int64_t)m * Hkv * s->rd, L, (int64_t)m * Hkv * s->rd,
+                 B * vg);
+        } else {  // K and V rows [0, m) of every (layer, KV head)
+          cp.add(em + el.kdc, kt + i * kg, (int64_t)m * HD, L, (int64_t)Hkv * m * HD, B * kg, Hkv,
+                 (int64_t)m * HD, (int64_t)P * HD);
+          cp.add(em + el.vdc, vt + i * vg, (int64_t)m * HD, L, (int64_t)Hkv * m * HD, B * vg, Hkv,
+                 (int64_t)m * HD, (int64_t)P * HD);
+        }
+        cp.add(em + el.prev, prev + (int64_t)i * C, C, 1, 0, 0);
       }
+      cp.run(s, "pc_desc_in");
       SeqBuffers sb;
-      sb.B = 1; sb.T = T; sb.N = T;
-      sb.ids = upload_ids(s, "pc_ids1", prompts + (int64_t)g * P + m, T, s->V);
+      sb.B = B; sb.T = T; sb.N = (int64_t)B * T;
+      sb.ids = upload_ids(s, "pc_ids", ids.data(), sb.N, s->V);
       sb.qoff = m;
       sb.pf_maxseq = P;
       sb.pre_len = m;
-      sb.pre_k = em + el.ktm;
-      sb.pre_v = em + el.vtm;
-      sb.seed_prev = em + el.prev;
-      sb.tm_k_out = plan[g].dst->mem + lay.ktm;  // the whole prompt's keys/values
-      sb.tm_v_out = plan[g].dst->mem + lay.vtm;
+      sb.kv_k = kall;
+      sb.kv_v = vall;
+      sb.seed_prev = prev;
       seq_forward(s, sb, SEQ_PREFILL, kt, vt);
-      copy_layer_rows(kpf + g * kg, G * kg, kt, kg, kg, L, st);
-      copy_layer_rows(vpf + g * vg, G * vg, vt, vg, vg, L, st);
-      const int64_t last = (int64_t)(T - 1) * C;
-      GN_HIP(hipMemcpyAsync(lastfn + (int64_t)g * C, sb.fn + last, sizeof(float) * C,
-                            hipMemcpyDeviceToDevice, st));
-      GN_HIP(hipMemcpyAsync(lastemb + (int64_t)g * C, sb.embn + last, sizeof(float) * C,
-                            hipMemcpyDeviceToDevice, st));
-      fill_entry(g);
+      collect(gs, m, sb, kt, vt, kall, vall);
+      h0 = h1;
     }
-    GN_HIP(hipStreamSynchronize(st));
+    GN_HIP(hipStreamSynchronize(s->stream));
   } catch (...) {
     // entries of this call may be incomplete: drop them (their memory is
     // released after the stream has drained)
@@ -2298,13 +2364,13 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
           pc_remove(s, i);
           break;
         }
-    (void)hipStreamSynchronize(st);
+    (void)hipStreamSynchronize(s->stream);
     s->pc_defer = false;
     pc_flush(s);
     throw;
   }
   s->pc_defer = false;
-  pc_flush(s);
+  pc_flush(s, (size_t)G);  // the next call of this size reuses them
 }
 
 static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S, int N,
@@ -2610,7 +2676,6 @@ int gn_session_destroy(gn_session* s) {
     (void)hipStreamSynchronize(s->stream);
     s->pc_defer = false;
     pc_clear(s);
-    pc_flush(s);
     s->arena.reset();
     for (auto e : s->event_pool) (void)hipEventDestroy(e);
     if (s->pinned) (void)hipHostFree(s->pinned);
