@@ -16,6 +16,9 @@
 //     value (each of the k groups holds a value >= L);
 //  3. the values >= L (a few hundred at most for real logits) are compacted
 //     into LDS and bitonic-sorted; the k-th of them is the threshold.
+// When the row fits in the block's registers (V <= 16 float4 per thread,
+// V = 65,536 at 1024 threads) it is read from memory once: the group maxima,
+// the candidates and their values all come from registers and LDS.
 // If the candidates overflow the LDS buffer (e.g. massively tied logits) the
 // row falls back to an exact 4-pass 8-bit radix select over the whole row.
 #include "gn_model.h"
@@ -120,13 +123,16 @@ __device__ void bitonic_desc(float* a, int n) {
 static constexpr int NT = 1024;  // 16 waves per row: loads of a pass in flight together
 static constexpr int MAXG = 4096;  // group maxima
 static constexpr int MAXC = 2048;  // candidates
+static constexpr int REGV = 16;    // float4 per thread of a row held in registers
 
 __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
   __shared__ float buf[MAXG];
   __shared__ int cand_i[MAXC];
+  __shared__ float cand_v[MAXC];
   __shared__ uint32_t hist[4][256];
   __shared__ uint32_t sel_prefix, sel_k;
   __shared__ int ncand;
+  __shared__ float thr_s;
   __shared__ float best_v[NT / 64];
   __shared__ int best_i[NT / 64];
   __shared__ uint64_t base_s[2];
@@ -142,15 +148,31 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
     for (int v = tid; v < V; v += NT) better(bv, bi, z[v], v);
   } else {
     const int g = row / a.samples_per_group, ig = row % a.samples_per_group;
+    const int k = a.top_k;
+    const bool masking = k > 0 && k < V;
+    const float T = a.temperature;
+    const bool vec = V % 4 == 0 && a.ldl % 4 == 0 && ((uintptr_t)a.logits & 15) == 0;
+    const v4f* z4 = reinterpret_cast<const v4f*>(z);
+    const int V4 = V / 4;
+    // the row in registers: float4 c = tid + u * NT of thread tid, requested
+    // before the stream jump below so the two overlap
+    const bool inreg = masking && vec && V4 <= REGV * NT;
+    v4f zr[REGV];
+    if (inreg) {
+#pragma unroll
+      for (int u = 0; u < REGV; u++) {
+        const int c = tid + u * NT;
+        zr[u] = c < V4 ? z4[c] : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
+    }
     if (tid == 0) {
       u128 s = {a.base_states[2 * g], a.base_states[2 * g + 1]};
       s = pcg_advance(s, (uint64_t)ig * (uint64_t)V);
       base_s[0] = s.hi;
       base_s[1] = s.lo;
+      ncand = 0;
+      thr_s = -INFINITY;
     }
-    const int k = a.top_k;
-    const bool masking = k > 0 && k < V;
-    const float T = a.temperature;
     __syncthreads();
     const u128 rowbase = {base_s[0], base_s[1]};
     if (!masking) {
@@ -163,46 +185,89 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
         better(bv, bi, gumbel_score(z[v], T, s), v);
       }
     } else {
-      // 1) group maxima.  The bound holds for any partition of the row, so
-      //    the groups are strided (entry v belongs to group v mod ngroups)
-      //    and the pass reads the row with coalesced loads.
+      // 1) a lower bound of the k-th largest value.  The maxima of any
+      //    partition of the row bound it: the k-th largest of them is one
+      //    (each of the k groups holds a value >= it).  The groups are
+      //    strided (entry v belongs to group v mod ngroups) so the pass
+      //    reads the row with coalesced loads.
       int ngroups = NT;  // a power of two >= 4k (at most MAXG)
       while (ngroups < MAXG && ngroups < 4 * k) ngroups <<= 1;
-      const bool vec = V % 4 == 0 && a.ldl % 4 == 0 && ((uintptr_t)a.logits & 15) == 0;
-      const v4f* z4 = reinterpret_cast<const v4f*>(z);
-      const int V4 = V / 4;
-      if (vec) {
-        // float4 c belongs to group c mod ngroups
-        for (int gi = tid; gi < ngroups; gi += NT) {
-          float m = -INFINITY;
-#pragma unroll 16
-          for (int c = gi; c < V4; c += ngroups) {
-            const v4f t = z4[c];
-            m = fmaxf(m, fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])));
-          }
-          buf[gi] = m;
+      const bool fast = inreg && ngroups == NT;  // k <= 256: one group per thread
+      float lower;
+      if (fast) {
+        // One group per thread (its 64 registers).  Each of the 16 waves
+        // ranks its 64 maxima (value, then lane) and offers its m-th
+        // largest, m = ceil(k / 16); the smallest offer L bounds the k-th
+        // largest value: the 16 m >= k maxima ranked at or above m in their
+        // waves are all >= L.  No barrier-synchronized sort.
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < REGV; u++)
+          mx = fmaxf(mx, fmaxf(fmaxf(zr[u][0], zr[u][1]), fmaxf(zr[u][2], zr[u][3])));
+        if (mx != mx) mx = -INFINITY;  // an all-NaN group offers nothing
+        const int mrank = (k + NT / 64 - 1) / (NT / 64);
+        int rank = 0;
+        for (int o = 0; o < 64; o++) {
+          const float ov = __shfl(mx, o, 64);
+          rank += (ov > mx || (ov == mx && o < lane)) ? 1 : 0;
         }
+        if (rank == mrank - 1) buf[wid] = mx;  // one lane per wave: ranks are a permutation
+        __syncthreads();
+        lower = buf[0];
+#pragma unroll
+        for (int w = 1; w < NT / 64; w++) lower = fminf(lower, buf[w]);
       } else {
-        for (int gi = tid; gi < ngroups; gi += NT) {
-          float m = -INFINITY;
-          for (int v = gi; v < V; v += ngroups) m = fmaxf(m, z[v]);
-          buf[gi] = m;
+        if (inreg) {
+          // float4 c is in group c mod ngroups = tid + (u mod gpt) * NT
+          const int gpt = ngroups / NT;
+          for (int j = 0; j < gpt; j++) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < REGV; u++)
+              if ((u & (gpt - 1)) == j)
+                m = fmaxf(m, fmaxf(fmaxf(zr[u][0], zr[u][1]), fmaxf(zr[u][2], zr[u][3])));
+            buf[tid + j * NT] = m;
+          }
+        } else if (vec) {
+          // float4 c belongs to group c mod ngroups
+          for (int gi = tid; gi < ngroups; gi += NT) {
+            float m = -INFINITY;
+#pragma unroll 16
+            for (int c = gi; c < V4; c += ngroups) {
+              const v4f t = z4[c];
+              m = fmaxf(m, fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])));
+            }
+            buf[gi] = m;
+          }
+        } else {
+          for (int gi = tid; gi < ngroups; gi += NT) {
+            float m = -INFINITY;
+            for (int v = gi; v < V; v += ngroups) m = fmaxf(m, z[v]);
+            buf[gi] = m;
+          }
         }
+        __syncthreads();
+        bitonic_desc(buf, ngroups);
+        lower = k <= ngroups ? buf[k - 1] : -INFINITY;
       }
-      if (tid == 0) ncand = 0;
-      __syncthreads();
-      bitonic_desc(buf, ngroups);
-      const float lower = k <= ngroups ? buf[k - 1] : -INFINITY;
       __syncthreads();
       // 2) compact candidates >= lower (the row is read 8 float4 per thread
       //    at a time so the loads overlap)
       auto keep = [&](int v, float zv) {
-        if (zv >= lower) {
+        if (v < V && zv >= lower) {  // (padding past the row is -inf, and lower may be too)
           const int slot = atomicAdd(&ncand, 1);
-          if (slot < MAXC) cand_i[slot] = v;
+          if (slot < MAXC) {
+            cand_i[slot] = v;
+            cand_v[slot] = zv;
+          }
         }
       };
-      if (vec) {
+      if (inreg) {
+#pragma unroll
+        for (int u = 0; u < REGV; u++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) keep(4 * (tid + u * NT) + j, zr[u][j]);
+      } else if (vec) {
         for (int c0 = tid; c0 < V4; c0 += 8 * NT) {
           v4f t[8];
 #pragma unroll
@@ -222,17 +287,35 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
       const int nc = ncand;
       float thr;
       if (nc <= MAXC) {
-        int cp2 = 1;
-        while (cp2 < nc) cp2 <<= 1;
-        for (int i = tid; i < cp2; i += NT) buf[i] = i < nc ? z[cand_i[i]] : -INFINITY;
-        __syncthreads();
-        bitonic_desc(buf, cp2);
-        thr = buf[k - 1];
-        __syncthreads();
+        if (fast) {
+          // the k-th largest candidate value: the one with fewer than k
+          // candidates above it and at least k at or above it (all such
+          // candidates hold that same value)
+          for (int i = tid; i < nc; i += NT) {
+            const float x = cand_v[i];
+            int gt = 0, ge = 0;
+            for (int j = 0; j < nc; j++) {
+              const float y = cand_v[j];
+              gt += y > x ? 1 : 0;
+              ge += y >= x ? 1 : 0;
+            }
+            if (gt < k && k <= ge) thr_s = x;
+          }
+          __syncthreads();
+          thr = thr_s;
+        } else {
+          int cp2 = 1;
+          while (cp2 < nc) cp2 <<= 1;
+          for (int i = tid; i < cp2; i += NT) buf[i] = i < nc ? cand_v[i] : -INFINITY;
+          __syncthreads();
+          bitonic_desc(buf, cp2);
+          thr = buf[k - 1];
+          __syncthreads();
+        }
         // 3) Gumbel-max over the survivors, in index order per thread
         for (int i = tid; i < nc; i += NT) {
           const int v = cand_i[i];
-          const float zv = z[v];
+          const float zv = cand_v[i];
           if (zv >= thr) {
             float sc = gumbel_score(zv, T, pcg_advance(rowbase, (uint64_t)v + 1));
             better(bv, bi, sc, v);

@@ -113,12 +113,20 @@ def test_policy_gradient_step_matches_oracle(small, orc):
 def test_sampler_bit_exact(orc):
     from gonano_amd.backend import sample_next_token
     rng = np.random.default_rng(3)
+    # the row held in registers (V <= 65,536, V % 4 == 0) with 1, 2 and 4
+    # group maxima per thread (k up to 1024), the two-pass path (V > 65,536,
+    # or V % 4 != 0), argmax, no mask, and small rows mostly -inf (fewer
+    # finite entries than k: every entry is a candidate)
     for V, rows, T, k in [(4096, 64, 1.0, 50), (65536, 8, 1.0, 50), (32768, 16, 0.8, 50),
-                          (1000, 9, 1.0, 0), (300, 5, 1.0, 300), (777, 7, 0.0, 50), (5000, 4, 1.3, 1)]:
+                          (1000, 9, 1.0, 0), (300, 5, 1.0, 300), (777, 7, 0.0, 50), (5000, 4, 1.3, 1),
+                          (8192, 6, 1.0, 300), (8192, 6, 1.0, 600), (65536, 3, 1.0, 1000),
+                          (70004, 3, 1.0, 50), (1001, 5, 1.0, 50), (128, 3, 1.0, 50)]:
         z = (rng.standard_normal((rows, V)) * 2).astype(np.float32)
         z[:, ::97] = z[:, :1]  # ties, including at the threshold
         z = np.round(z * 64) / 64  # many exact duplicates
         z = z.astype(np.float32)
+        if V == 128:
+            z[:, :120] = -np.inf
         for seed in (0, 12345):
             g = orc.GoRNG(seed)
             state = np.array(g.hi_lo, np.uint64)
