@@ -485,6 +485,9 @@ struct SamplerArgs {
   float temperature;
   int top_k;
   int32_t* out;                 // [rows]
+  // logits holds lm_head products y: the logits are softcap15(y), applied on
+  // load (transformer.go:538-541); 0: logits holds the logits themselves
+  int softcap = 0;
 };
 void launch_sampler(const SamplerArgs& a, hipStream_t st);
 // Advances the Go PCG state {hi, lo} by n draws (tensors.RNG after n Float32

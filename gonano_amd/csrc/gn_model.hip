@@ -535,8 +535,10 @@ void launch_expand_last_rows(const float* src, float* dst, int G, int T, int S, 
 
 // ---------------------------------------------------------------------------
 // PG loss rows (trainer/rl.go:22-56, tensors/loss.go:16-46,
-// tensors/backward.go:108-116).  z [rows, V] softcapped logits (row stride
-// ldz) is overwritten by dL/d(pre-softcap logits):
+// tensors/backward.go:108-116).  z [rows, V] holds the lm_head products y
+// (row stride ldz); the logits are z = softcap15(y) (transformer.go:538-541,
+// applied here on load rather than in the product's epilogue, so the
+// product is a plain GEMM), and z is overwritten by dL/dy:
 //   g = (softmax(z) - onehot(t)) * (adv/norm) * (1 - (z/15)^2),
 // zero for ignored rows.  nll (0 for ignored) and the per-row loss term
 // nll*adv/norm (float64) are written per row.  Chunk row r is batch row
@@ -554,7 +556,11 @@ __device__ __forceinline__ int64_t loss_row_index(const int32_t* rowmap, int64_t
   return rowmap ? (int64_t)rowmap[row0 + r] : row0 + r;
 }
 // Buffer resource over `bytes` bytes from p (gfx9 word 3): loads beyond the
-// range return 0 and stores beyond it are dropped.
+// range return 0.  (Only loads go through it.  A 16-byte buffer store whose
+// offset is in an SGPR was measured to have its data registers overwritten
+// by the VALU instruction the compiler schedules right after it -- the
+// compiler inserts no wait state for that form -- so results are stored
+// with global stores, whose wide-store hazard the compiler does cover.)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
@@ -572,21 +578,27 @@ __global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
   // one VGPR offset and the group's byte offset as a scalar
   const __amdgpu_buffer_rsrc_t rs = row_rsrc(zr, V * 4);
   const int V4 = V >> 2, tid = threadIdx.x, voff = tid * 16;
+  v4f* zr4 = reinterpret_cast<v4f*>(zr);  // 16-byte aligned rows (launcher)
   const int32_t tg = targets[n];
   if (tg < 0) {
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < Q; k++) __builtin_amdgcn_raw_buffer_store_b128(zero, rs, voff, k * 16384, 0);
+    for (int k = 0; k < Q; k++)
+      if (FULL || tid + k * 1024 < V4) zr4[tid + k * 1024] = zero;
     if (tid == 0) {
       nll[n] = 0.f;
       loss_rows[row0 + r] = 0.0;
     }
     return;
   }
-  const float zt = zr[tg];
+  const float zt = softcap15(zr[tg]);
   v4f v[Q];
 #pragma unroll
-  for (int k = 0; k < Q; k++) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * 16384, 0);
+  for (int k = 0; k < Q; k++) {
+    v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * 16384, 0);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[k][c] = softcap15(v[k][c]);
+  }
   if (!FULL) {
 #pragma unroll
     for (int k = 0; k < Q; k++)
@@ -630,7 +642,7 @@ __global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
       const float sc = zj * ic;
       g[c] = (p * scale) * (1.f - sc * sc);
     }
-    __builtin_amdgcn_raw_buffer_store_b128(g, rs, voff, k * 16384, 0);
+    if (FULL || j < V4) zr4[j] = g;
   }
 }
 __global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z, int64_t ldz,
@@ -655,13 +667,13 @@ __global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z
     return;
   }
   float m = -INFINITY;
-  for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, zr[j]);
+  for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, softcap15(zr[j]));
   m = block_max(m, sf);
   double s = 0;
-  for (int j = threadIdx.x; j < V; j += 256) s += (double)expf(zr[j] - m);
+  for (int j = threadIdx.x; j < V; j += 256) s += (double)expf(softcap15(zr[j]) - m);
   s = block_sum<double>(s, sd);
   const float a = adv[n / T];
-  const float nl = m + (float)log(s) - zr[tg];
+  const float nl = m + (float)log(s) - softcap15(zr[tg]);
   if (threadIdx.x == 0) {
     nll[n] = nl;
     loss_rows[row0 + r] = (double)nl * (double)a / (double)norm;
@@ -671,7 +683,7 @@ __global__ __launch_bounds__(256) void pg_loss_rows_kernel(float* __restrict__ z
   const float ic = 1.0f / 15.0f;
   __syncthreads();
   for (int j = threadIdx.x; j < V; j += 256) {
-    float zj = zr[j];
+    float zj = softcap15(zr[j]);
     float p = expf(zj - m) * inv;
     if (j == tg) p -= 1.f;
     float sc = zj * ic;
@@ -745,10 +757,11 @@ void launch_scatter_rows(const float* src, const int32_t* idx, float* dst, int64
 
 // ---------------------------------------------------------------------------
 // Distillation rows (tensors/loss.go:84-214, trainer/distill.go:13-46).
-// z [rows, V] the student's softcapped logits (row stride ldz) is
-// overwritten by dL/d(pre-softcap logits):
+// z [rows, V] holds the student's lm_head products y and zt the teacher's
+// (row stride ldz); the logits are softcap15 of them, applied on load.  z is
+// overwritten by dL/dy:
 //   g = (float)((softmax(z/tau) - softmax(zt/tau)) * scale/tau) * (1 - (z/15)^2)
-// with zt the teacher's softcapped logits; the forward-KL loss of the row,
+// with z, zt the softcapped logits; the forward-KL loss of the row,
 // rounded to float32, is written to loss_rows (float64).  Rows whose target
 // slot is negative are masked: zero gradient, zero loss.  The maxima, sums
 // and exponentials are float64, as the reference computes them.
@@ -772,8 +785,8 @@ __global__ __launch_bounds__(256) void distill_rows_kernel(float* __restrict__ z
   }
   double smax = -INFINITY, tmax = -INFINITY;
   for (int j = threadIdx.x; j < V; j += 256) {
-    smax = fmax(smax, (double)zr[j] / tau);
-    tmax = fmax(tmax, (double)tr[j] / tau);
+    smax = fmax(smax, (double)softcap15(zr[j]) / tau);
+    tmax = fmax(tmax, (double)softcap15(tr[j]) / tau);
   }
   // block maxima in float64 (max is exact in any order)
   {
@@ -794,7 +807,7 @@ __global__ __launch_bounds__(256) void distill_rows_kernel(float* __restrict__ z
   }
   double ss = 0.0, ts = 0.0, ws = 0.0;
   for (int j = threadIdx.x; j < V; j += 256) {
-    const double a = (double)zr[j] / tau, b = (double)tr[j] / tau;
+    const double a = (double)softcap15(zr[j]) / tau, b = (double)softcap15(tr[j]) / tau;
     const double tw = exp(b - tmax);
     ss += exp(a - smax);
     ts += tw;
@@ -808,9 +821,9 @@ __global__ __launch_bounds__(256) void distill_rows_kernel(float* __restrict__ z
   const float ic = 1.0f / 15.0f;
   __syncthreads();
   for (int j = threadIdx.x; j < V; j += 256) {
-    const float zj = zr[j];
+    const float zj = softcap15(zr[j]);
     const double ps = exp((double)zj / tau - smax) * is;
-    const double pt = exp((double)tr[j] / tau - tmax) * it;
+    const double pt = exp((double)softcap15(tr[j]) / tau - tmax) * it;
     const float g = (float)((ps - pt) * gs);
     const float sc = zj * ic;
     zr[j] = g * (1.f - sc * sc);

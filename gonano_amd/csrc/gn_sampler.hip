@@ -140,12 +140,20 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
   const int row = blockIdx.x;
   const float* z = a.logits + (int64_t)row * a.ldl;
   const int V = a.V;
+  const bool sc = a.softcap != 0;
+  auto zl = [&](int v) { return sc ? softcap15(z[v]) : z[v]; };  // logit v
+  auto zl4 = [&](v4f t) {
+    if (sc)
+#pragma unroll
+      for (int c = 0; c < 4; c++) t[c] = softcap15(t[c]);
+    return t;
+  };
   float bv = -INFINITY;
   int bi = -1;
 
   if (a.temperature <= 0.f) {
     // argMax: first index of the largest value (sampler.go:37-45)
-    for (int v = tid; v < V; v += NT) better(bv, bi, z[v], v);
+    for (int v = tid; v < V; v += NT) better(bv, bi, zl(v), v);
   } else {
     const int g = row / a.samples_per_group, ig = row % a.samples_per_group;
     const int k = a.top_k;
@@ -162,7 +170,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
 #pragma unroll
       for (int u = 0; u < REGV; u++) {
         const int c = tid + u * NT;
-        zr[u] = c < V4 ? z4[c] : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        zr[u] = c < V4 ? zl4(z4[c]) : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       }
     }
     if (tid == 0) {
@@ -182,7 +190,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
       u128 s = pcg_advance(rowbase, (uint64_t)v0);
       for (int v = v0; v < v1; v++) {
         s = pcg_step(s);
-        better(bv, bi, gumbel_score(z[v], T, s), v);
+        better(bv, bi, gumbel_score(zl(v), T, s), v);
       }
     } else {
       // 1) a lower bound of the k-th largest value.  The maxima of any
@@ -234,7 +242,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
             float m = -INFINITY;
 #pragma unroll 16
             for (int c = gi; c < V4; c += ngroups) {
-              const v4f t = z4[c];
+              const v4f t = zl4(z4[c]);
               m = fmaxf(m, fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3])));
             }
             buf[gi] = m;
@@ -242,7 +250,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
         } else {
           for (int gi = tid; gi < ngroups; gi += NT) {
             float m = -INFINITY;
-            for (int v = gi; v < V; v += ngroups) m = fmaxf(m, z[v]);
+            for (int v = gi; v < V; v += ngroups) m = fmaxf(m, zl(v));
             buf[gi] = m;
           }
         }
@@ -273,7 +281,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
 #pragma unroll
           for (int u = 0; u < 8; u++) {
             const int c = c0 + u * NT;
-            t[u] = c < V4 ? z4[c] : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            t[u] = c < V4 ? zl4(z4[c]) : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
           }
 #pragma unroll
           for (int u = 0; u < 8; u++)
@@ -281,7 +289,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
             for (int j = 0; j < 4; j++) keep(4 * (c0 + u * NT) + j, t[u][j]);
         }
       } else {
-        for (int v = tid; v < V; v += NT) keep(v, z[v]);
+        for (int v = tid; v < V; v += NT) keep(v, zl(v));
       }
       __syncthreads();
       const int nc = ncand;
@@ -329,7 +337,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
           for (int i = tid; i < 4 * 256; i += NT) (&hist[0][0])[i] = 0;
           __syncthreads();
           for (int v = tid; v < V; v += NT) {
-            uint32_t u = order_key(z[v]);
+            uint32_t u = order_key(zl(v));
             if ((u & pmask) == prefix) atomicAdd(&hist[wid & 3][(u >> shift) & 255u], 1u);
           }
           __syncthreads();
@@ -352,7 +360,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
         }
         thr = key_float(prefix);
         for (int v = tid; v < V; v += NT) {
-          const float zv = z[v];
+          const float zv = zl(v);
           if (zv >= thr) {
             float sc = gumbel_score(zv, T, pcg_advance(rowbase, (uint64_t)v + 1));
             better(bv, bi, sc, v);

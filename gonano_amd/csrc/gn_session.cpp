@@ -18,6 +18,7 @@
 #include <string>
 #include <vector>
 
+#include "gn_blaslt.h"
 #include "gn_model.h"
 #include "gn_optimizer.h"
 #include "gn_tools.h"
@@ -128,6 +129,11 @@ struct gn_session {
   int64_t total = 0;
   hipStream_t stream = nullptr;
   std::unique_ptr<gn::DeviceArena> arena;
+  // plain products through hipBLASLt (null: every product on gemm_kernel)
+  struct LtDel {
+    void operator()(gn::BlasLt* b) const { gn::blaslt_destroy(b); }
+  };
+  std::unique_ptr<gn::BlasLt, LtDel> lt;
   float* params = nullptr;  // packed device storage
   float* grads = nullptr;
   float *wte = nullptr, *lm = nullptr, *rl = nullptr, *x0l = nullptr, *smg = nullptr,
@@ -199,16 +205,21 @@ static void* pinned(gn_session* s, size_t bytes) {
 }
 
 // GEMM launch with optional event timing (not while a graph is captured).
+// A session product: hipBLASLt when it takes it (plain epilogue, large
+// enough), gemm_kernel otherwise.
 static void sgemm(gn_session* s, const GemmDesc& d) {
+  auto run = [&] {
+    if (!blaslt_gemm(s->lt.get(), d, s->stream)) gemm(d, s->stream, s->arena.get());
+  };
   if (s->timing && !s->capturing) {
     hipEvent_t a = next_event(s), b = next_event(s);
     GN_HIP(hipEventRecord(a, s->stream));
-    gemm(d, s->stream, s->arena.get());
+    run();
     GN_HIP(hipEventRecord(b, s->stream));
     s->gemm_events.push_back({a, b});
     s->gemm_ev_flops.push_back(2.0 * d.M * (double)d.N * d.K);
   } else {
-    gemm(d, s->stream, s->arena.get());
+    run();
   }
 }
 
@@ -1454,11 +1465,11 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
   float* Zt = dc ? A<float>(s, "teacher_logits", chunk * V) : nullptr;
   for (int64_t r0 = 0; r0 < Nv; r0 += chunk) {
     const int64_t rows = std::min(chunk, Nv - r0);
-    sgemm(s, linear_fwd_desc(fnv + r0 * C, s->lm, Z, (int)rows, C, V, EPI_SOFTCAP));
+    // lm_head products; the loss kernels apply the softcap on load
+    sgemm(s, linear_fwd_desc(fnv + r0 * C, s->lm, Z, (int)rows, C, V));
     if (dc) {
       const int Ct = dc->teacher->C;
-      sgemm(s, linear_fwd_desc(tfnv + r0 * Ct, dc->teacher->lm, Zt, (int)rows, Ct, V,
-                               EPI_SOFTCAP));
+      sgemm(s, linear_fwd_desc(tfnv + r0 * Ct, dc->teacher->lm, Zt, (int)rows, Ct, V));
       launch_distill_rows(Z, Zt, V, V, r0, rows, rowmap, dtg, dc->tau, dc->scale, loss_rows, st);
     } else {
       launch_pg_loss_rows(Z, V, V, r0, rows, rowmap, dtg, dadv, T, norm, nll, loss_rows, st);
@@ -1972,7 +1983,8 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     if (l == bk) GN_HIP(hipMemcpyAsync(back, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
   }
   launch_norm_rows(x, back, s->bkl, rows, C, nullptr, h, st, pend);
-  sgemm(s, linear_fwd_desc(h, s->lm, logits, rows, C, s->V, EPI_SOFTCAP));
+  // lm_head products; the sampler applies the softcap on load
+  sgemm(s, linear_fwd_desc(h, s->lm, logits, rows, C, s->V));
 }
 
 // PrefillCED (model/transformer.go:363-449) of G prompts: the encoder over
@@ -2457,7 +2469,8 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
     launch_expand_last_rows(sb.fn, lastfn, G, Tlast, S, C, st);
   }
   float* logits = A<float>(s, "dec_logits", (size_t)rows * V);
-  sgemm(s, linear_fwd_desc(lastfn, s->lm, logits, rows, C, V, EPI_SOFTCAP));
+  // lm_head products; the sampler applies the softcap on load
+  sgemm(s, linear_fwd_desc(lastfn, s->lm, logits, rows, C, V));
   // 2) PrefillFrom (kvcache.go:383-448): replicate KV and the smear state
   float* kc = A<float>(s, "kv_k", (size_t)L * rows * maxSeq * kw);
   float* vc = A<float>(s, "kv_v", (size_t)L * rows * maxSeq * vw);
@@ -2525,6 +2538,7 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   SamplerArgs sa{};
   sa.logits = logits; sa.ldl = V; sa.rows = rows; sa.V = V; sa.samples_per_group = S;
   sa.base_states = dbase; sa.temperature = temperature; sa.top_k = top_k; sa.out = dtok;
+  sa.softcap = 1;  // the decode logits buffer holds lm_head products
 
   struct Graph {
     hipGraph_t g = nullptr;
@@ -2660,6 +2674,9 @@ int gn_session_create(const gn_config* config, int device, gn_session** out) {
       GN_HIP(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
       s->arena = std::make_unique<DeviceArena>(s->stream);
       build_session(s, *config);
+      // GN_GEMM_BLASLT=0 keeps every product on gemm_kernel
+      const char* lt = std::getenv("GN_GEMM_BLASLT");
+      if (!lt || std::strcmp(lt, "0") != 0) s->lt.reset(blaslt_create());
     } catch (...) {  // a rejected config or a failed allocation frees what was made
       if (s->stream) (void)gn_session_destroy(s);
       else delete s;
@@ -2676,6 +2693,7 @@ int gn_session_destroy(gn_session* s) {
     (void)hipStreamSynchronize(s->stream);
     s->pc_defer = false;
     pc_clear(s);
+    s->lt.reset();
     s->arena.reset();
     for (auto e : s->event_pool) (void)hipEventDestroy(e);
     if (s->pinned) (void)hipHostFree(s->pinned);
