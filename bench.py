@@ -179,8 +179,7 @@ def main() -> int:
         log(f"bench: warmup {i}: {wall * 1e3:.1f} ms (rollout {t['rollout_ms']:.1f} ms, "
             f"train {t['train_ms']:.1f} ms), loss {out['loss']:.6f}")
     walls, roll_ms, train_ms, toks = [], [], [], 0
-    gemm_ms = gemm_fl = 0.0
-    gemm_n = 0
+    gemm = {"ms": 0.0, "flops": 0.0, "n": 0, "lt_ms": 0.0, "lt_flops": 0.0, "lt_n": 0}
     sess.synchronize()
     t_start = time.perf_counter()
     for i in range(args.steps):
@@ -189,7 +188,7 @@ def main() -> int:
         roll_ms.append(t["rollout_ms"])
         train_ms.append(t["train_ms"])
         toks += int(np.sum(out["lens"] - P))
-        gemm_ms += t["gemm_ms"]; gemm_fl += t["gemm_flops"]; gemm_n += t["gemm_launches"]
+        add_gemm(gemm, t)
         log(f"bench: step {i}: {wall * 1e3:.1f} ms (rollout {t['rollout_ms']:.1f} ms, "
             f"train {t['train_ms']:.1f} ms), loss {out['loss']:.6f}, max_len {out['max_len']}")
     sess.synchronize()
@@ -211,7 +210,6 @@ def main() -> int:
 
     rollout_s = sum(roll_ms) / 1e3
     value = toks / rollout_s
-    gemm_tflops = gemm_fl / (gemm_ms / 1e3) / 1e12 if gemm_ms else 0.0
     attn_gbs = attn_b / (attn_ms / 1e3) / 1e9 if attn_ms else 0.0
     res = {
         "metric": METRIC,
@@ -248,17 +246,7 @@ def main() -> int:
             "rl_step_ms": round(ms_step, 2),
             "train_ms": round(sum(train_ms) / len(train_ms), 2),
         },
-        "roofline": {
-            "kernel": "gemm_kernel (fp32 MFMA, recompute + PG backward)",
-            "bound": "mfma",
-            "achieved": round(gemm_tflops, 2),
-            "peak": FP32_MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(gemm_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": gemm_traffic(args.config),
-            "launches": gemm_n,
-            "avg_launch_ms": round(gemm_ms / max(gemm_n, 1), 4),
-        },
+        "roofline": gemm_roofline(gemm, args.config),
         "decode_attention": {
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "launches": attn_n,
@@ -278,11 +266,48 @@ def main() -> int:
     return 0
 
 
+def add_gemm(acc: dict, t: dict) -> None:
+    """Adds one step's train-phase GEMM timing (all products; those on
+    hipBLASLt) to acc."""
+    acc["ms"] += t["gemm_ms"]; acc["flops"] += t["gemm_flops"]; acc["n"] += t["gemm_launches"]
+    acc["lt_ms"] += t["gemm_lt_ms"]; acc["lt_flops"] += t["gemm_lt_flops"]
+    acc["lt_n"] += t["gemm_lt_launches"]
+
+
+def _part(ms: float, flops: float, n: int) -> dict:
+    tf = flops / (ms / 1e3) / 1e12 if ms else 0.0
+    return {"achieved": round(tf, 2), "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "launches": n,
+            "avg_launch_ms": round(ms / max(n, 1), 4), "share_of_gemm_time": None}
+
+
+def gemm_roofline(g: dict, config: str) -> dict:
+    """The dominant kernels of the step: the train phase's fp32 products
+    (recompute forward, PG backward, lm_head), timed live per launch with
+    HIP events on the session stream.  Plain products run on hipBLASLt,
+    those with fused epilogues (ReLU^2 and its gradient, deferred split-K
+    sums) on gemm_kernel; `parts` splits the two."""
+    tf = g["flops"] / (g["ms"] / 1e3) / 1e12 if g["ms"] else 0.0
+    lt = _part(g["lt_ms"], g["lt_flops"], g["lt_n"])
+    own = _part(g["ms"] - g["lt_ms"], g["flops"] - g["lt_flops"], g["n"] - g["lt_n"])
+    if g["ms"]:
+        lt["share_of_gemm_time"] = round(g["lt_ms"] / g["ms"], 4)
+        own["share_of_gemm_time"] = round(1 - g["lt_ms"] / g["ms"], 4)
+    return {
+        "kernel": "train-phase fp32 GEMMs (hipBLASLt plain products + gemm_kernel fused "
+                  "epilogues; recompute + PG backward + lm_head)",
+        "bound": "mfma", "achieved": round(tf, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+        "traffic": gemm_traffic(config), "launches": g["n"],
+        "avg_launch_ms": round(g["ms"] / max(g["n"], 1), 4),
+        "parts": {"hipblaslt": lt, "gemm_kernel": own},
+    }
+
+
 def gemm_traffic(config: str):
     """HBM bytes per train-phase GEMM launch, from the committed rocprofv3
     --pmc summary of `bench.py --phase train` (FETCH_SIZE + WRITE_SIZE,
     each scaled by the copy-kernel calibration), or None if absent."""
-    path = os.path.join(ROOT, "profiles", f"gemm_kernel_{config}_train_traffic.json")
+    path = os.path.join(ROOT, "profiles", f"train_gemms_{config}_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -341,25 +366,22 @@ def train_phase(args, sess, prompts, S, N, reward_rng, reward_p) -> int:
         sess.policy_gradient_step(inputs, targets, adv, norm)
     sess.synchronize()
     t0 = time.perf_counter()
-    gemm_ms = gemm_fl = 0.0
-    gemm_n = 0
+    gemm = {"ms": 0.0, "flops": 0.0, "n": 0, "lt_ms": 0.0, "lt_flops": 0.0, "lt_n": 0}
     train = []
     for _ in range(args.steps):
         sess.zero_grad()
         loss, _ = sess.policy_gradient_step(inputs, targets, adv, norm)
         t = sess.timing()
         train.append(t["train_ms"])
-        gemm_ms += t["gemm_ms"]; gemm_fl += t["gemm_flops"]; gemm_n += t["gemm_launches"]
+        add_gemm(gemm, t)
     sess.synchronize()
     ms = 1e3 * (time.perf_counter() - t0) / args.steps
     sess.close()
-    tf = gemm_fl / (gemm_ms / 1e3) / 1e12 if gemm_ms else 0.0
     print(json.dumps({
         "metric": "train phase (recompute + PG fwd/bwd) ms", "value": round(ms, 2),
         "unit": "ms", "higher_is_better": False, "steps": args.steps, "warmup": args.warmup,
         "train_ms": round(sum(train) / len(train), 2), "loss": loss,
-        "gemm": {"achieved": round(tf, 2), "unit": "TFLOP/s", "launches": gemm_n,
-                 "avg_launch_ms": round(gemm_ms / max(gemm_n, 1), 4)}}), flush=True)
+        "gemm": gemm_roofline(gemm, args.config)}), flush=True)
     return 0
 
 

@@ -148,6 +148,7 @@ struct gn_session {
   gn_timing t{};
   std::vector<std::pair<hipEvent_t, hipEvent_t>> gemm_events, attn_events;
   std::vector<double> gemm_ev_flops, attn_ev_bytes;
+  std::vector<char> gemm_ev_lt;  // the product ran on hipBLASLt
   std::vector<int> attn_ev_launches;
   std::vector<hipEvent_t> event_pool;
   size_t event_next = 0;
@@ -208,8 +209,10 @@ static void* pinned(gn_session* s, size_t bytes) {
 // A session product: hipBLASLt when it takes it (plain epilogue, large
 // enough), gemm_kernel otherwise.
 static void sgemm(gn_session* s, const GemmDesc& d) {
+  bool lt = false;
   auto run = [&] {
-    if (!blaslt_gemm(s->lt.get(), d, s->stream)) gemm(d, s->stream, s->arena.get());
+    lt = blaslt_gemm(s->lt.get(), d, s->stream);
+    if (!lt) gemm(d, s->stream, s->arena.get());
   };
   if (s->timing && !s->capturing) {
     hipEvent_t a = next_event(s), b = next_event(s);
@@ -218,19 +221,29 @@ static void sgemm(gn_session* s, const GemmDesc& d) {
     GN_HIP(hipEventRecord(b, s->stream));
     s->gemm_events.push_back({a, b});
     s->gemm_ev_flops.push_back(2.0 * d.M * (double)d.N * d.K);
+    s->gemm_ev_lt.push_back(lt ? 1 : 0);
   } else {
     run();
   }
 }
 
+// GEMM events into gemm_* (all products) and lt_* (those on hipBLASLt;
+// nullable), attention events into attn_*.
 static void collect_timing(gn_session* s, double* gemm_ms, double* gemm_flops, int64_t* gemm_n,
-                           double* attn_ms, double* attn_bytes, int64_t* attn_n) {
+                           double* attn_ms, double* attn_bytes, int64_t* attn_n,
+                           double* lt_ms = nullptr, double* lt_flops = nullptr,
+                           int64_t* lt_n = nullptr) {
   for (size_t i = 0; i < s->gemm_events.size(); i++) {
     float ms = 0;
     GN_HIP(hipEventElapsedTime(&ms, s->gemm_events[i].first, s->gemm_events[i].second));
     *gemm_ms += ms;
     *gemm_flops += s->gemm_ev_flops[i];
     (*gemm_n)++;
+    if (lt_ms && s->gemm_ev_lt[i]) {
+      *lt_ms += ms;
+      *lt_flops += s->gemm_ev_flops[i];
+      (*lt_n)++;
+    }
   }
   for (size_t i = 0; i < s->attn_events.size(); i++) {
     float ms = 0;
@@ -241,6 +254,7 @@ static void collect_timing(gn_session* s, double* gemm_ms, double* gemm_flops, i
   }
   s->gemm_events.clear();
   s->gemm_ev_flops.clear();
+  s->gemm_ev_lt.clear();
   s->attn_events.clear();
   s->attn_ev_bytes.clear();
   s->attn_ev_launches.clear();
@@ -1607,9 +1621,11 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
     GN_HIP(hipEventElapsedTime(&ms, ev0, ev1));
     s->t.train_ms = ms;
     s->t.gemm_ms = 0; s->t.gemm_flops = 0; s->t.gemm_launches = 0;
+    s->t.gemm_lt_ms = 0; s->t.gemm_lt_flops = 0; s->t.gemm_lt_launches = 0;
     double am = 0, ab = 0;
     int64_t an = 0;
-    collect_timing(s, &s->t.gemm_ms, &s->t.gemm_flops, &s->t.gemm_launches, &am, &ab, &an);
+    collect_timing(s, &s->t.gemm_ms, &s->t.gemm_flops, &s->t.gemm_launches, &am, &ab, &an,
+                   &s->t.gemm_lt_ms, &s->t.gemm_lt_flops, &s->t.gemm_lt_launches);
   }
 }
 
@@ -1637,8 +1653,8 @@ static int pg_micro_batch(gn_session* s, int B, int T) {
 static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets, int B, int T,
                     const float* adv, float norm, float* loss_out, float* nll_out) {
   const int mb = pg_micro_batch(s, B, T);
-  double loss = 0, aux = 0, tms = 0, gms = 0, gfl = 0;
-  int64_t gn = 0;
+  double loss = 0, aux = 0, tms = 0, gms = 0, gfl = 0, lms = 0, lfl = 0;
+  int64_t gn = 0, ln = 0;
   s->bal_batch = B;
   try {
     for (int b0 = 0; b0 < B; b0 += mb) {
@@ -1649,6 +1665,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
       loss += l;
       aux += s->aux_loss * nb;
       tms += s->t.train_ms; gms += s->t.gemm_ms; gfl += s->t.gemm_flops; gn += s->t.gemm_launches;
+      lms += s->t.gemm_lt_ms; lfl += s->t.gemm_lt_flops; ln += s->t.gemm_lt_launches;
     }
   } catch (...) {
     s->bal_batch = 0;
@@ -1659,6 +1676,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
   s->aux_loss = aux / B;
   if (s->timing) {
     s->t.train_ms = tms; s->t.gemm_ms = gms; s->t.gemm_flops = gfl; s->t.gemm_launches = gn;
+    s->t.gemm_lt_ms = lms; s->t.gemm_lt_flops = lfl; s->t.gemm_lt_launches = ln;
   }
 }
 
@@ -2794,7 +2812,7 @@ int gn_forward(gn_session* s, const int32_t* ids, int32_t B, int32_t T, float* l
                             hipMemcpyDeviceToHost, s->stream));
     }
     GN_HIP(hipStreamSynchronize(s->stream));
-    s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->event_next = 0;
+    s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->gemm_ev_lt.clear(); s->event_next = 0;
   });
 }
 
@@ -2974,7 +2992,7 @@ int gn_session_set_timing(gn_session* s, int enabled) {
   return guard([&] {
     GN_CHECK(s, "null session");
     s->timing = enabled != 0;
-    s->gemm_events.clear(); s->gemm_ev_flops.clear();
+    s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->gemm_ev_lt.clear();
     s->attn_events.clear(); s->attn_ev_bytes.clear(); s->attn_ev_launches.clear();
     s->event_next = 0;
   });

@@ -110,6 +110,33 @@ def test_policy_gradient_step_matches_oracle(small, orc):
     assert rel_err(s.grads(), 2 * grads) < 1e-6
 
 
+@pytest.mark.parametrize("V", [12340, 33000, 50260, 50257])
+def test_pg_step_partial_vocab_rows(orc, V):
+    """Vocabularies that are not a multiple of 4096: the register loss
+    kernel's partial-row variants (4, 8 and 16 float4 per thread, padding
+    masked) and the streaming kernel (V % 4 != 0); NLL, loss and every
+    gradient against the oracle.  (50,257 is GPT-2's vocabulary.)"""
+    from gonano_amd.session import Session
+    cfg = G.Config(sequence_len=256, vocab_size=V, n_layer=1, n_head=2, n_kv_head=1, n_embd=256,
+                   window_pattern="L", rotary_dims=64)
+    w = G.init_weights(cfg, seed=3, perturb=0.1)
+    rng = np.random.default_rng(V)
+    inputs = rng.integers(0, V, (2, 96)).astype(np.int32)
+    targets = rng.integers(0, V, (2, 96)).astype(np.int32)
+    targets[:, :20] = -1
+    targets[1, 50] = V - 1  # the last entry of the padded group
+    adv = np.array([0.7, -0.3], np.float32)
+    with Session(cfg) as s:
+        s.set_params(w)
+        s.zero_grad()
+        loss, nll = s.policy_gradient_step(inputs, targets, adv, 97.0)
+        grads = s.grads()
+    wl, wnll, wg = orc.OracleModel(shape_of(cfg), w).pg_step(inputs, targets, adv, 97.0)
+    assert abs(loss - wl) <= 1e-4 * max(abs(wl), 1e-3)
+    assert_close(nll, wnll, 1e-3, 1e-4, "nll")
+    _compare_grads(cfg, grads, wg)
+
+
 def test_sampler_bit_exact(orc):
     from gonano_amd.backend import sample_next_token
     rng = np.random.default_rng(3)
