@@ -636,6 +636,7 @@ void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
   pa.perm_row = a.perm_row; pa.perm_w = a.perm_w; pa.inv = a.inv; pa.xg = a.xg;
   hipLaunchKernelGGL(moe_place_kernel, dim3(nblk), dim3(MOE_PB), 0, st, pa);
   GN_HIP(hipGetLastError());
+  if (!a.xg) return;  // the expert products read the token rows through perm_row
   hipLaunchKernelGGL(moe_gather_kernel, dim3((unsigned)ceil_div(npairs, 4)), dim3(256), 0, st, a.x,
                      a.perm_row, npairs, a.C, a.xg);
   GN_HIP(hipGetLastError());
@@ -677,6 +678,158 @@ void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st) {
   if (rows <= 0) return;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// Expert products over decode-size groups.  At decode the pairs per expert
+// are few, so an expert's weights are read once per step and the products
+// are bound by that stream, not by the matrix cores.  Block (expert e,
+// outputs j0..j0+15) of 4 waves: wave w requests its weight fragments (rows
+// j0..j0+15 over the w-th quarter of K, kept in registers) before anything
+// that depends on the routing, then multiplies the expert's pairs in
+// 32-pair chunks, two 16-row MFMA tiles at a time, as the weights arrive.  The 4 quarter sums are added
+// in LDS in wave order (deterministic) and one wave applies the epilogue.
+// No split-K partial buffers, no reduction launch.
+// ---------------------------------------------------------------------------
+static constexpr int MOE_XW = 4;   // waves per block (K quarters)
+
+template <int KH, bool GU>
+__global__ __launch_bounds__(64 * MOE_XW) void moe_expert_small_kernel(MoeExpertArgs a) {
+  constexpr int NW = GU ? 2 : 1;          // weight matrices (gate, up | down)
+  constexpr int JB = KH < 2 ? KH : 2;     // k groups of weights requested before the rows
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nb = a.N / 16;
+  const int e = blockIdx.x / nb, j0 = (blockIdx.x - e * nb) * 16;
+  const int r = lane & 15, q = lane >> 4;
+  const int kq = w * KH * 16 + 4 * q;  // this lane's first k of the wave's quarter
+  // B fragments: lane (r, q) holds weight row j0 + r, k = kq + 16 g + c.
+  // Loads complete in issue order (vmcnt), so the order of requests sets
+  // what the products can start on: the first JB k groups of weights, then
+  // the routing-dependent rows of the first chunk, then the remaining
+  // weights, which the products consume as they arrive.
+  v4f f[NW][KH];
+  const float* bw[NW];
+#pragma unroll
+  for (int m = 0; m < NW; m++) bw[m] = (m ? a.w1 : a.w0) + ((int64_t)e * a.N + j0 + r) * a.K + kq;
+#pragma unroll
+  for (int g = 0; g < JB; g++)
+#pragma unroll
+    for (int m = 0; m < NW; m++) f[m][g] = *reinterpret_cast<const v4f*>(bw[m] + 16 * g);
+  const int beg = a.off[e], cnt = a.off[e + 1] - beg;
+  if (cnt < 0) {
+    // Never taken (offsets do not decrease).  A use of the first fragments
+    // on a path that skips the products keeps their loads above this
+    // routing-dependent branch (the compiler would otherwise sink them
+    // below it, behind the latency of the offset load).
+    float z = 0.f;
+#pragma unroll
+    for (int m = 0; m < NW; m++)
+#pragma unroll
+      for (int g = 0; g < JB; g++) z += f[m][g][0] + f[m][g][1] + f[m][g][2] + f[m][g][3];
+    a.out[0] = z;
+    return;
+  }
+  const int nchunk = (cnt + 31) / 32;
+  if (nchunk == 0) return;
+  // A fragments of chunk t: lane (r, q) holds pair rows t*32 + 16h + r
+  // (clamped to the expert's last pair; those outputs are not stored)
+  v4f av[2][KH];
+  auto load_rows = [&](int t) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int pr = beg + min(t * 32 + 16 * h + r, cnt - 1);
+      const int64_t arow = GU ? (int64_t)a.perm_row[pr] : (int64_t)pr;
+      const float* ap = a.x + arow * a.K + kq;
+#pragma unroll
+      for (int g = 0; g < KH; g++) av[h][g] = *reinterpret_cast<const v4f*>(ap + 16 * g);
+    }
+  };
+  __shared__ v4f red[MOE_XW][2][NW][64];
+  auto chunk = [&](int t) {
+    v4f acc[2][NW];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int m = 0; m < NW; m++) acc[h][m] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < KH; g++)
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int m = 0; m < NW; m++)
+#pragma unroll
+          for (int h = 0; h < 2; h++)
+            acc[h][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[h][g][c], f[m][g][c], acc[h][m], 0, 0, 0);
+    if (t > 0) __syncthreads();  // the previous chunk's sums have been read
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int m = 0; m < NW; m++) red[w][h][m][lane] = acc[h][m];
+    __syncthreads();
+    if (w == t % MOE_XW) {
+      // D of a 16x16 block: lane holds output j0 + (lane & 15), pair rows 4q + c
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        v4f sm[NW];
+#pragma unroll
+        for (int m = 0; m < NW; m++) {
+          sm[m] = red[0][h][m][lane];
+#pragma unroll
+          for (int u = 1; u < MOE_XW; u++) sm[m] += red[u][h][m][lane];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const int p = t * 32 + 16 * h + 4 * q + c;
+          if (p < cnt) {
+            float v = sm[0][c];
+            if constexpr (GU) swiglu_eval(sm[0][c], sm[1][c], a.clamp, &v, nullptr, nullptr, 0.f);
+            a.out[(int64_t)(beg + p) * a.N + j0 + (lane & 15)] = v;
+          }
+        }
+      }
+    }
+  };
+  load_rows(0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int g = JB; g < KH; g++)
+#pragma unroll
+    for (int m = 0; m < NW; m++) f[m][g] = *reinterpret_cast<const v4f*>(bw[m] + 16 * g);
+  __builtin_amdgcn_sched_barrier(0);
+  chunk(0);
+  for (int t = 1; t < nchunk; t++) {
+    load_rows(t);
+    // every row load in flight before the first product
+    __builtin_amdgcn_sched_barrier(0);
+    chunk(t);
+  }
+}
+
+bool moe_expert_small_supported(int N, int K) {
+  if (N <= 0 || N % 16 || K <= 0 || K % (16 * MOE_XW)) return false;
+  const int kh = K / (16 * MOE_XW);
+  return kh <= 6 || kh == 8 || kh == 10 || kh == 12 || kh == 16;
+}
+
+bool launch_moe_expert_small(const MoeExpertArgs& a, hipStream_t st) {
+  if (!moe_expert_small_supported(a.N, a.K) || a.E <= 0) return false;
+  const int kh = a.K / (16 * MOE_XW);
+  GN_CHECK((a.w1 != nullptr) == (a.perm_row != nullptr), "moe expert: gate/up needs both");
+  const dim3 grid((unsigned)(a.E * (a.N / 16))), block(64 * MOE_XW);
+#define GN_MOE_X(KH)                                                          \
+  case KH:                                                                    \
+    if (a.w1) hipLaunchKernelGGL((moe_expert_small_kernel<KH, true>), grid, block, 0, st, a); \
+    else hipLaunchKernelGGL((moe_expert_small_kernel<KH, false>), grid, block, 0, st, a);     \
+    break;
+  switch (kh) {
+    GN_MOE_X(1) GN_MOE_X(2) GN_MOE_X(3) GN_MOE_X(4) GN_MOE_X(5) GN_MOE_X(6) GN_MOE_X(8)
+    GN_MOE_X(10) GN_MOE_X(12) GN_MOE_X(16)
+    default:
+      return false;
+  }
+#undef GN_MOE_X
+  GN_HIP(hipGetLastError());
+  return true;
 }
 
 // ---------------------------------------------------------------------------

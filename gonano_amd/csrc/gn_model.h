@@ -306,6 +306,25 @@ struct MoeCombineArgs {
 };
 void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st);
 
+// Expert products over decode-size groups (a few to tens of pairs per
+// expert): gate and up with the clamped SwiGLU fused (x: token rows read
+// through perm_row; w0 = gate, w1 = up weights [E][N][K]; out = SwiGLU
+// [pairs][N]), or down (x: SwiGLU rows in pair order; w0 = down weights
+// [E][N][K]; w1 = null; out [pairs][N]).  Returns false (nothing launched)
+// for shapes it does not take (N % 16, K % 64, K / 64 outside 1..16).
+struct MoeExpertArgs {
+  const float* x;
+  const int* perm_row;  // gate/up only
+  const int* off;       // [E + 1] pair offsets of the experts (device)
+  const float* w0;
+  const float* w1;
+  float* out;
+  int E, N, K;
+  float clamp;
+};
+bool launch_moe_expert_small(const MoeExpertArgs& a, hipStream_t st);
+bool moe_expert_small_supported(int N, int K);
+
 void launch_moe_bwd_prep(const float* g, const float* yg, const int* perm_row, const float* perm_w,
                          float scale, int64_t npairs, int C, float* gy, double* dotp,
                          hipStream_t st);

@@ -694,9 +694,12 @@ static MoeBuffers moe_buffers(gn_session* s, const std::string& pre, int64_t row
 // The feed-forward of a MoE block (model/block.go:40-45, mlp.go:62-76,
 // moe.go:118-198): xout = mid + (shared(h2) + routed(h2)).  gu and act
 // receive the shared expert's [gate | up] pre-activations and its SwiGLU.
+// small: decode-size batches (a few to tens of pairs per expert) run the
+// expert products as weight-streaming kernels (gate/up with the SwiGLU fused,
+// no gathered rows, no pre-activations kept) when the shapes allow.
 static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, const float* h2,
                             int64_t rows, float* gu, float* act, const MoeBuffers& m,
-                            float* xout) {
+                            float* xout, bool small = false) {
   const int C = s->C, F = s->F, E = s->E, EH = s->EH;
   const int64_t NK = rows * s->K;
   hipStream_t st = s->stream;
@@ -711,22 +714,35 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
   ra.E = E; ra.K = s->K; ra.C = C;
   ra.probs = m.probs; ra.sel = m.sel; ra.w = m.w; ra.blockcnt = m.blockcnt; ra.off = m.off;
   ra.perm_row = m.perm_row; ra.perm_w = m.perm_w; ra.inv = m.inv; ra.xg = m.xg;
+  const bool stream_experts =
+      small && moe_expert_small_supported(EH, C) && moe_expert_small_supported(C, EH);
+  if (stream_experts) ra.xg = nullptr;
   launch_moe_route(ra, st);
-  // expert gate and up projections into [gate | up] rows, SwiGLU, down
-  for (int half = 0; half < 2; half++) {
-    GemmDesc d = linear_fwd_desc(m.xg, half ? ly.eu : ly.eg, m.gug + half * EH, (int)NK, C, EH);
-    d.ldc = 2 * EH;
-    d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
-    d.group_stride = (int64_t)EH * C;
-    d.a_pad_rows = MOE_PAD;
-    sgemm(s, d);
+  if (stream_experts) {
+    MoeExpertArgs gx{};
+    gx.x = h2; gx.perm_row = m.perm_row; gx.off = m.off; gx.w0 = ly.eg; gx.w1 = ly.eu;
+    gx.out = m.hg; gx.E = E; gx.N = EH; gx.K = C; gx.clamp = s->clamp;
+    GN_CHECK(launch_moe_expert_small(gx, st), "moe: expert gate/up shape");
+    MoeExpertArgs dx{};
+    dx.x = m.hg; dx.off = m.off; dx.w0 = ly.ed; dx.out = m.yg; dx.E = E; dx.N = C; dx.K = EH;
+    GN_CHECK(launch_moe_expert_small(dx, st), "moe: expert down shape");
+  } else {
+    // expert gate and up projections into [gate | up] rows, SwiGLU, down
+    for (int half = 0; half < 2; half++) {
+      GemmDesc d = linear_fwd_desc(m.xg, half ? ly.eu : ly.eg, m.gug + half * EH, (int)NK, C, EH);
+      d.ldc = 2 * EH;
+      d.group = GEMM_GROUP_ROWS; d.group_off = m.off; d.groups = E;
+      d.group_stride = (int64_t)EH * C;
+      d.a_pad_rows = MOE_PAD;
+      sgemm(s, d);
+    }
+    launch_swiglu_rows(m.gug, EH, NK, s->clamp, m.hg, st);
+    GemmDesc dd = linear_fwd_desc(m.hg, ly.ed, m.yg, (int)NK, EH, C);
+    dd.group = GEMM_GROUP_ROWS; dd.group_off = m.off; dd.groups = E;
+    dd.group_stride = (int64_t)C * EH;
+    dd.a_pad_rows = MOE_PAD;
+    sgemm(s, dd);
   }
-  launch_swiglu_rows(m.gug, EH, NK, s->clamp, m.hg, st);
-  GemmDesc dd = linear_fwd_desc(m.hg, ly.ed, m.yg, (int)NK, EH, C);
-  dd.group = GEMM_GROUP_ROWS; dd.group_off = m.off; dd.groups = E;
-  dd.group_stride = (int64_t)C * EH;
-  dd.a_pad_rows = MOE_PAD;
-  sgemm(s, dd);
   MoeCombineArgs ca{};
   ca.mid = mid; ca.shared = shared; ca.yg = m.yg; ca.perm_w = m.perm_w; ca.sel = m.sel;
   ca.inv = m.inv; ca.scale = s->mscale; ca.K = s->K; ca.C = C; ca.out = xout;
@@ -1986,7 +2002,7 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     if (s->moe) {
       float* gu = A<float>(s, "dec_gu", (size_t)rows * 2 * F);
       MoeBuffers mb = moe_buffers(s, "dec_moe_", rows);
-      moe_ffn_forward(s, ly, x, h, rows, gu, act, mb, x);
+      moe_ffn_forward(s, ly, x, h, rows, gu, act, mb, x, true);
       if (l == bk) GN_HIP(hipMemcpyAsync(back, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
       continue;
     }
