@@ -663,7 +663,8 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   if (splits > 1) {
     GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
     // deferred partials live until their consumer runs, past later GEMMs'
-    p.part = ws->get<float>(defer ? "gemm_splitk_defer" : "gemm_splitk",
+    p.part = ws->get<float>(defer ? "gemm_splitk_defer" + std::to_string(d.defer_slot)
+                                  : std::string("gemm_splitk"),
                             (size_t)splits * d.M * d.N);
   }
   // two-level summation for long K ranges per workgroup (see gemm_kernel)

@@ -89,6 +89,19 @@ struct PendingSum {
 // Consumers hold every partial of their elements in registers (all loads in
 // flight at once), so a GEMM defers its sum only up to this many splits.
 constexpr int PENDING_MAX_SPLITS = 8;
+// Element i of a deferred product: its partials summed in split order in
+// float64 and rounded once (gemm_reduce_kernel's result before its epilogue).
+__device__ __forceinline__ float pending_value(const PendingSum& ps, int64_t i) {
+  float v[PENDING_MAX_SPLITS];
+#pragma unroll
+  for (int z = 0; z < PENDING_MAX_SPLITS; z++)
+    if (z < ps.splits) v[z] = ps.part[z * ps.stride + i];  // every load before the sum
+  double s = 0.0;
+#pragma unroll
+  for (int z = 0; z < PENDING_MAX_SPLITS; z++)
+    if (z < ps.splits) s += (double)v[z];
+  return (float)s;
+}
 
 struct GemmDesc {
   int M = 0, N = 0, K = 0;
@@ -116,6 +129,9 @@ struct GemmDesc {
   // *defer instead of launching the reduction; the consumer applies the sum
   // (and the residual add) as gemm_reduce_kernel would.
   PendingSum* defer = nullptr;
+  // partial buffer of a deferred sum: products whose sums are pending at the
+  // same time use different slots
+  int defer_slot = 0;
 };
 
 void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);

@@ -133,6 +133,13 @@ __device__ __forceinline__ int decode_pos(const MlaDecodeArgs& a) {
 
 __global__ __launch_bounds__(256) void mla_decode_prep_kernel(MlaDecodeArgs a) {
   const int row = blockIdx.x;
+  if (a.xa_sum.splits > 0) {
+    // the input projection's deferred sum: the row of xa, for this kernel
+    // and the absorbed-query product after it
+    for (int i = threadIdx.x; i < a.xw; i += blockDim.x)
+      a.xa_w[(int64_t)row * a.xw + i] = pending_value(a.xa_sum, (int64_t)row * a.xw + i);
+    __syncthreads();
+  }
   const int pos = decode_pos(a), half = a.rd >> 1;
   const float* cosr = a.cosT + (int64_t)pos * half;
   const float* sinr = a.sinT + (int64_t)pos * half;
@@ -361,6 +368,16 @@ int mla_decode_max_splits(int window, int maxSeq) {
   return ns;
 }
 
+void launch_mla_decode_prep(const MlaDecodeArgs& a, hipStream_t st) {
+  GN_CHECK(a.rd == MLA_RD && a.Hkv * a.rd <= 256, "mla decode: rotary width must be 64");
+  GN_CHECK(a.pos_dev || a.pos < a.maxSeq, "mla decode: position outside the cache");
+  GN_CHECK(a.xa_sum.splits == 0 || (a.xa_w == a.xa && a.xa_sum.stride == (int64_t)a.rows * a.xw &&
+                                    a.xa_sum.splits <= PENDING_MAX_SPLITS),
+           "mla decode: pending input-projection sum shape");
+  hipLaunchKernelGGL(mla_decode_prep_kernel, dim3(a.rows), dim3(256), 0, st, a);
+  GN_HIP(hipGetLastError());
+}
+
 void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
   GN_CHECK(a.lat % 4 == 0 && a.lat <= MLA_MAXLAT, "mla decode: latent width must be a multiple "
                                                   "of 4 and at most 256");
@@ -375,8 +392,6 @@ void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
   a.nsplit_max = ns_max;
   GN_CHECK(a.part_splits >= ns_max, "mla decode: split buffer too small");
   GN_CHECK(a.pos_dev || a.pos < a.maxSeq, "mla decode: position outside the cache");
-  hipLaunchKernelGGL(mla_decode_prep_kernel, dim3(a.rows), dim3(256), 0, st, a);
-  GN_HIP(hipGetLastError());
   const dim3 grid(a.rows, ns_max);
   hipEvent_t stop = ns_max > 1 ? nullptr : a.t_stop;
 #define GN_MLA_ATTN(H)                                                                        \
@@ -431,14 +446,18 @@ __device__ __forceinline__ void swiglu_eval(float g, float u, float c, float* ou
   }
 }
 
+// With a deferred [gate | up] product pending, gu stands for its sum.
 __global__ void swiglu_rows_kernel(const float* __restrict__ gu, int F, int64_t rows, float clamp,
-                                   float* __restrict__ act) {
+                                   float* __restrict__ act, PendingSum pend) {
   const int64_t n = rows * F;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = i / F, j = i % F;
+    const int64_t ig = r * 2 * F + j, iu = ig + F;
+    const float g = pend.splits > 0 ? pending_value(pend, ig) : gu[ig];
+    const float u = pend.splits > 0 ? pending_value(pend, iu) : gu[iu];
     float o;
-    swiglu_eval(gu[r * 2 * F + j], gu[r * 2 * F + F + j], clamp, &o, nullptr, nullptr, 0.f);
+    swiglu_eval(g, u, clamp, &o, nullptr, nullptr, 0.f);
     act[i] = o;
   }
 }
@@ -461,10 +480,12 @@ static unsigned grid_for(int64_t n) {
 }
 
 void launch_swiglu_rows(const float* gu, int F, int64_t rows, float clamp, float* act,
-                        hipStream_t st) {
+                        hipStream_t st, const PendingSum& pend) {
   if (rows <= 0) return;
+  GN_CHECK(pend.splits == 0 || (pend.stride == rows * 2 * (int64_t)F && pend.splits <= PENDING_MAX_SPLITS),
+           "swiglu: pending sum shape");
   hipLaunchKernelGGL(swiglu_rows_kernel, dim3(grid_for(rows * F)), dim3(256), 0, st, gu, F, rows,
-                     clamp, act);
+                     clamp, act, pend);
   GN_HIP(hipGetLastError());
 }
 void launch_swiglu_rows_bwd(const float* gu, const float* dact, int F, int64_t rows, float clamp,
@@ -486,17 +507,12 @@ static constexpr int MOE_PB = 256;  // (token, slot) pairs per placement block
 // logits (float64 total, p = float32(exp) * float32(1/total)), top-k of
 // logits + bias (largest first, ties to the smaller index), weights = the
 // chosen experts' probabilities.
-__global__ __launch_bounds__(256) void moe_gate_kernel(const float* __restrict__ logits,
-                                                       const float* __restrict__ bias,
-                                                       int64_t rows, int E, int K,
-                                                       float* __restrict__ probs,
-                                                       int32_t* __restrict__ sel,
-                                                       float* __restrict__ w) {
+// Softmax and top-k of one token's logits, lane e holding logit e (-inf for
+// lanes >= E).
+__device__ __forceinline__ void gate_route(float lg, bool on, const float* __restrict__ bias,
+                                           int64_t r, int E, int K, float* __restrict__ probs,
+                                           int32_t* __restrict__ sel, float* __restrict__ w) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  const bool on = lane < E;
-  const float lg = on ? logits[r * E + lane] : -INFINITY;
   float mx = lg;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
@@ -527,6 +543,77 @@ __global__ __launch_bounds__(256) void moe_gate_kernel(const float* __restrict__
       work = -INFINITY;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void moe_gate_kernel(const float* __restrict__ logits,
+                                                       const float* __restrict__ bias,
+                                                       int64_t rows, int E, int K,
+                                                       float* __restrict__ probs,
+                                                       int32_t* __restrict__ sel,
+                                                       float* __restrict__ w, PendingSum lsum) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const bool on = lane < E;
+  const float lg = !on ? -INFINITY
+                       : lsum.splits > 0 ? pending_value(lsum, r * E + lane) : logits[r * E + lane];
+  gate_route(lg, on, bias, r, E, K, probs, sel, w);
+}
+
+// Decode-size batches: one block per token computes the router logits
+// x[r] . wr[e] itself (wave v takes experts v, v + 4, ...; the 64 lanes
+// split the C columns, every load in flight at once, summed by shuffles --
+// another rounding order of the router product's dot product), then wave 0
+// routes the token.
+static constexpr int MOE_GATE_C4 = 8;  // float4 columns per lane: C <= 2048
+
+__global__ __launch_bounds__(256) void moe_gate_logits_kernel(const float* __restrict__ xin,
+                                                              const float* __restrict__ wr, int C,
+                                                              const float* __restrict__ bias,
+                                                              int E, int K,
+                                                              float* __restrict__ probs,
+                                                              int32_t* __restrict__ sel,
+                                                              float* __restrict__ w) {
+  __shared__ float lgs[MOE_MAXE];
+  const int lane = threadIdx.x & 63, v = threadIdx.x >> 6;
+  const int64_t r = blockIdx.x;
+  const int n4 = C / 4;
+  const v4f* xv = reinterpret_cast<const v4f*>(xin + r * C);
+  v4f xa[MOE_GATE_C4];
+#pragma unroll
+  for (int i = 0; i < MOE_GATE_C4; i++)
+    if (lane + 64 * i < n4) xa[i] = xv[lane + 64 * i];
+  for (int e0 = v; e0 < E; e0 += 16) {
+    // experts e0, e0 + 4, e0 + 8, e0 + 12 of this wave, loads issued together
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    v4f wa[4][MOE_GATE_C4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int e = e0 + 4 * j;
+      const v4f* wv = reinterpret_cast<const v4f*>(wr + (int64_t)min(e, E - 1) * C);
+#pragma unroll
+      for (int i = 0; i < MOE_GATE_C4; i++)
+        if (lane + 64 * i < n4) wa[j][i] = wv[lane + 64 * i];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int i = 0; i < MOE_GATE_C4; i++)
+        if (lane + 64 * i < n4)
+          acc[j] += xa[i][0] * wa[j][i][0] + xa[i][1] * wa[j][i][1] + xa[i][2] * wa[j][i][2] +
+                    xa[i][3] * wa[j][i][3];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float t = acc[j];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o, 64);
+      if (lane == 0 && e0 + 4 * j < E) lgs[e0 + 4 * j] = t;
+    }
+  }
+  __syncthreads();
+  if (v != 0) return;
+  const bool on = lane < E;
+  gate_route(on ? lgs[lane] : -INFINITY, on, bias, r, E, K, probs, sel, w);
 }
 
 // Rank of each pair among the pairs of its block that chose the same expert,
@@ -621,8 +708,18 @@ void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
   GN_CHECK(a.C % 4 == 0, "moe: model width must be a multiple of 4");
   const int64_t npairs = a.rows * a.K;
   if (a.rows <= 0) return;
-  hipLaunchKernelGGL(moe_gate_kernel, dim3((unsigned)ceil_div(a.rows, 4)), dim3(256), 0, st,
-                     a.logits, a.bias, a.rows, a.E, a.K, a.probs, a.sel, a.w);
+  GN_CHECK(a.logits_sum.splits == 0 || (a.logits_sum.stride == a.rows * (int64_t)a.E &&
+                                         a.logits_sum.splits <= PENDING_MAX_SPLITS),
+           "moe: pending router sum shape");
+  if (a.wr) {
+    GN_CHECK(a.C % 4 == 0 && a.C <= 256 * MOE_GATE_C4,
+             "moe: router in the gate kernel needs a width multiple of 4, at most 2048");
+    hipLaunchKernelGGL(moe_gate_logits_kernel, dim3((unsigned)a.rows), dim3(256), 0, st, a.x,
+                       a.wr, a.C, a.bias, a.E, a.K, a.probs, a.sel, a.w);
+  } else {
+    hipLaunchKernelGGL(moe_gate_kernel, dim3((unsigned)ceil_div(a.rows, 4)), dim3(256), 0, st,
+                       a.logits, a.bias, a.rows, a.E, a.K, a.probs, a.sel, a.w, a.logits_sum);
+  }
   GN_HIP(hipGetLastError());
   const int nblk = (int)ceil_div(npairs, MOE_PB);
   hipLaunchKernelGGL(moe_count_kernel, dim3(nblk), dim3(MOE_PB), 0, st, a.sel, npairs, a.E,
@@ -670,12 +767,17 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeCombineArgs a) {
   for (int c = threadIdx.x; c < a.C; c += blockDim.x) {
     float moe = 0.f;
     for (int k = 0; k < a.K; k++) moe += wk[k] * a.yg[(int64_t)pos[k] * a.C + c];
-    a.out[r * a.C + c] = a.mid[r * a.C + c] + (a.shared[r * a.C + c] + moe);
+    const float sh = a.shared_sum.splits > 0 ? pending_value(a.shared_sum, r * a.C + c)
+                                             : a.shared[r * a.C + c];
+    a.out[r * a.C + c] = a.mid[r * a.C + c] + (sh + moe);
   }
 }
 
 void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st) {
   if (rows <= 0) return;
+  GN_CHECK(a.shared_sum.splits == 0 || (a.shared_sum.stride == rows * (int64_t)a.C &&
+                                         a.shared_sum.splits <= PENDING_MAX_SPLITS),
+           "moe: pending shared-expert sum shape");
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }

@@ -232,6 +232,10 @@ void launch_mla_post_bwd(const MlaPostBwdArgs& a, int64_t rows, hipStream_t st);
 struct MlaDecodeArgs {
   const float* xa;    // [rows, xw]
   int xw;
+  // a deferred input projection: the prep kernel writes its sum into xa_w
+  // (== xa) before anything reads xa
+  PendingSum xa_sum;
+  float* xa_w = nullptr;
   const float* qabs;  // [rows, Hq, lat] absorbed content queries
   float* qrope;       // [rows, Hq, rd] (written by the prep kernel)
   float* lat_cache;   // layer base [rows][maxSeq][lat]
@@ -252,13 +256,17 @@ struct MlaDecodeArgs {
 // Largest number of key splits a decode step with this window and cache
 // length can use (sizes MlaDecodeArgs::part).
 int mla_decode_max_splits(int window, int maxSeq);
+// Rotates the new token's query/key rotary parts and appends (latent,
+// rotary key) to the caches; runs before the absorbed-query product.
+void launch_mla_decode_prep(const MlaDecodeArgs& a, hipStream_t st);
+// Absorbed attention over the caches (+ the split combine).
 void launch_mla_decode(MlaDecodeArgs a, hipStream_t st);
 void launch_replicate_rows(const float* src, float* dst, int G, int S, int P, int W, int maxSrc,
                            int maxDst, hipStream_t st);
 
 // ---- latent preset: DeepSeekMoE (model/moe.go) ---------------------------
 void launch_swiglu_rows(const float* gu, int F, int64_t rows, float clamp, float* act,
-                        hipStream_t st);
+                        hipStream_t st, const PendingSum& pend = PendingSum{});
 void launch_swiglu_rows_bwd(const float* gu, const float* dact, int F, int64_t rows, float clamp,
                             float* dgu, hipStream_t st);
 
@@ -276,7 +284,9 @@ struct MoeRouteArgs {
   int* perm_row;    // [rows*K] gathered pair -> token
   float* perm_w;    // [rows*K] gathered pair -> router weight
   int* inv;         // [rows*K] (token, slot) -> gathered pair
-  float* xg;        // [rows*K, C]
+  float* xg;        // [rows*K, C]; null: no gathered copy (the decode expert kernels read x)
+  PendingSum logits_sum;  // a deferred router product (then `logits` is unused)
+  const float* wr = nullptr;  // [E, C] router weights: logits computed from x in the gate kernel
 };
 void launch_moe_route(const MoeRouteArgs& a, hipStream_t st);
 struct MoePlaceArgs {
@@ -303,6 +313,7 @@ struct MoeCombineArgs {
   float scale;
   int K, C;
   float* out;
+  PendingSum shared_sum;  // a deferred shared-expert product (then `shared` is unused)
 };
 void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st);
 

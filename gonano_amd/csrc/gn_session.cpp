@@ -703,21 +703,36 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
   const int C = s->C, F = s->F, E = s->E, EH = s->EH;
   const int64_t NK = rows * s->K;
   hipStream_t st = s->stream;
-  sgemm(s, linear_fwd_desc(h2, ly.wgu, gu, (int)rows, C, 2 * F));
-  launch_swiglu_rows(gu, F, rows, s->clamp, act, st);
-  float* shared = A<float>(s, "moe_shared", rows * C);
-  sgemm(s, linear_fwd_desc(act, ly.wproj, shared, (int)rows, F, C));
+  const bool stream_experts =
+      small && moe_expert_small_supported(EH, C) && moe_expert_small_supported(C, EH);
+  // Decode-size batches leave the split-K sums of the shared-expert
+  // products to their consumers (the SwiGLU and combine kernels) instead of
+  // reduction launches (gu is then not materialized), and compute the router
+  // logits in the gate kernel.  The shared expert's output sum stays pending
+  // across the routed experts, in its own partial buffer.
   float* logits = A<float>(s, "moe_logits", rows * E);
-  sgemm(s, linear_fwd_desc(h2, ly.wr, logits, (int)rows, C, E));
+  PendingSum gsum, ssum;
+  // decode-size batches: the gate kernel computes the router logits itself
+  if (!small) sgemm(s, linear_fwd_desc(h2, ly.wr, logits, (int)rows, C, E));
   MoeRouteArgs ra{};
   ra.logits = logits; ra.bias = ly.rbias; ra.x = h2; ra.rows = rows;
   ra.E = E; ra.K = s->K; ra.C = C;
   ra.probs = m.probs; ra.sel = m.sel; ra.w = m.w; ra.blockcnt = m.blockcnt; ra.off = m.off;
-  ra.perm_row = m.perm_row; ra.perm_w = m.perm_w; ra.inv = m.inv; ra.xg = m.xg;
-  const bool stream_experts =
-      small && moe_expert_small_supported(EH, C) && moe_expert_small_supported(C, EH);
-  if (stream_experts) ra.xg = nullptr;
+  ra.perm_row = m.perm_row; ra.perm_w = m.perm_w; ra.inv = m.inv;
+  ra.xg = stream_experts ? nullptr : m.xg;
+  if (small) ra.wr = ly.wr;
   launch_moe_route(ra, st);
+  GemmDesc dg = linear_fwd_desc(h2, ly.wgu, gu, (int)rows, C, 2 * F);
+  if (small) dg.defer = &gsum;
+  sgemm(s, dg);
+  launch_swiglu_rows(gu, F, rows, s->clamp, act, st, gsum);
+  float* shared = A<float>(s, "moe_shared", rows * C);
+  GemmDesc ds = linear_fwd_desc(act, ly.wproj, shared, (int)rows, F, C);
+  if (small) {
+    ds.defer = &ssum;
+    ds.defer_slot = 1;
+  }
+  sgemm(s, ds);
   if (stream_experts) {
     MoeExpertArgs gx{};
     gx.x = h2; gx.perm_row = m.perm_row; gx.off = m.off; gx.w0 = ly.eg; gx.w1 = ly.eu;
@@ -746,6 +761,7 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
   MoeCombineArgs ca{};
   ca.mid = mid; ca.shared = shared; ca.yg = m.yg; ca.perm_w = m.perm_w; ca.sel = m.sel;
   ca.inv = m.inv; ca.scale = s->mscale; ca.K = s->K; ca.C = C; ca.out = xout;
+  ca.shared_sum = ssum;
   launch_moe_combine(ca, rows, st);
 }
 
@@ -1787,18 +1803,22 @@ static void prepare_decode_weights(gn_session* s) {
 
 // One absorbed-MLA decode layer (mlaForwardInference, mla.go:185-279) on
 // h; the attention output projection is added into x.
+// The output projection's residual add is left pending on x (*pend) for the
+// MLP norm; the input projection's split-K sum is applied by the prep kernel.
 static void mla_decode_layer(gn_session* s, const Layer& ly, int l, int rows, int pos, int maxSeq,
-                             const float* h, float* latc, float* rkc, float* x, const int* dpos) {
+                             const float* h, float* latc, float* rkc, float* x, const int* dpos,
+                             PendingSum* pend) {
   const int C = s->C, Hq = s->Hq, lat = s->lat;
   hipStream_t st = s->stream;
   float* xa = A<float>(s, "dec_xa", (size_t)rows * s->XW);
-  sgemm(s, linear_fwd_desc(h, ly.wxa, xa, rows, C, s->XW));
+  PendingSum xsum;
+  GemmDesc gx = linear_fwd_desc(h, ly.wxa, xa, rows, C, s->XW);
+  gx.defer = &xsum;
+  sgemm(s, gx);
   float* qabs = A<float>(s, "dec_qabs", (size_t)rows * Hq * lat);
-  GemmDesc gq = linear_fwd_desc(xa, ly.wqabs, qabs, rows, lat, Hq * lat);
-  gq.lda = s->XW;
-  sgemm(s, gq);
   MlaDecodeArgs md{};
   md.xa = xa; md.xw = s->XW; md.qabs = qabs;
+  md.xa_sum = xsum; md.xa_w = xa;
   md.qrope = A<float>(s, "dec_qrope", (size_t)rows * Hq * s->rd);
   md.lat_cache = latc + (int64_t)l * rows * maxSeq * lat;
   md.rk_cache = rkc + (int64_t)l * rows * maxSeq * s->Hkv * s->rd;
@@ -1808,6 +1828,10 @@ static void mla_decode_layer(gn_session* s, const Layer& ly, int l, int rows, in
   md.part = A<float>(s, "dec_mlapart", (size_t)rows * md.part_splits * Hq * (lat + 2));
   md.rows = rows; md.Hq = Hq; md.Hkv = s->Hkv; md.lat = lat; md.rd = s->rd;
   md.maxSeq = maxSeq; md.window = ly.window; md.pos = pos; md.pos_dev = dpos;
+  launch_mla_decode_prep(md, st);
+  GemmDesc gq = linear_fwd_desc(xa, ly.wqabs, qabs, rows, lat, Hq * lat);
+  gq.lda = s->XW;
+  sgemm(s, gq);
   if (s->timing && !s->capturing) {
     const int keys = pos + 1 - std::max(0, pos - ly.window);
     timed_attention(s, (double)rows * keys * (lat + s->Hkv * s->rd) * 4.0, md,
@@ -1817,6 +1841,7 @@ static void mla_decode_layer(gn_session* s, const Layer& ly, int l, int rows, in
   }
   GemmDesc go = linear_fwd_desc(md.out, ly.wcomb, x, rows, Hq * lat, C, EPI_ADD_SRC);
   go.aux = x; go.ldaux = C;
+  go.defer = pend;
   sgemm(s, go);
 }
 
@@ -1953,7 +1978,7 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st, pend);
     pend = PendingSum{};
     if (s->mla) {
-      mla_decode_layer(s, ly, l, rows, pos, maxSeq, h, kc, vc, x, dpos);
+      mla_decode_layer(s, ly, l, rows, pos, maxSeq, h, kc, vc, x, dpos, &pend);
     } else {
     PendingSum qsum;
     GemmDesc gq = linear_fwd_desc(h, ly.wqkv, qkv, rows, C, s->QKVW);
