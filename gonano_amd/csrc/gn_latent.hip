@@ -703,6 +703,59 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const float* __restrict
   for (int c = lane; c < C / 4; c += 64) dst[c] = src[c];
 }
 
+// Decode-size batches (at most MOE_SMALL_PAIRS pairs): counts, offsets and
+// the placement in one block, chunk by chunk in pair order (a pair's
+// position is its expert's offset + the pairs of earlier chunks and of
+// earlier lanes of its chunk with the same expert -- the multi-block
+// placement's order).
+static constexpr int MOE_SMALL_PAIRS = 16 * MOE_PB;
+
+__global__ __launch_bounds__(MOE_PB) void moe_route_small_kernel(MoePlaceArgs a, int* __restrict__ off) {
+  __shared__ int wcnt[4][MOE_MAXE];
+  __shared__ int cnt[MOE_MAXE];
+  __shared__ int base[MOE_MAXE];
+  __shared__ int offs[MOE_MAXE + 1];
+  const int tid = threadIdx.x;
+  const int nch = (int)((a.npairs + MOE_PB - 1) / MOE_PB);
+  if (tid < a.E) base[tid] = 0;
+  __syncthreads();
+  for (int c = 0; c < nch; c++) {
+    const int64_t p = (int64_t)c * MOE_PB + tid;
+    const bool valid = p < a.npairs;
+    block_rank(valid ? a.sel[p] : -1, valid, a.E, cnt, wcnt);
+    if (tid < a.E) base[tid] += cnt[tid];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int run = 0;
+    for (int x = 0; x < a.E; x++) {
+      offs[x] = run;
+      off[x] = run;
+      run += base[x];
+    }
+    offs[a.E] = run;
+    off[a.E] = run;
+  }
+  __syncthreads();
+  if (tid < a.E) base[tid] = 0;
+  __syncthreads();
+  for (int c = 0; c < nch; c++) {
+    const int64_t p = (int64_t)c * MOE_PB + tid;
+    const bool valid = p < a.npairs;
+    const int e = valid ? a.sel[p] : -1;
+    const int rank = block_rank(e, valid, a.E, cnt, wcnt);
+    if (valid) {
+      const int pos = offs[e] + base[e] + rank;
+      a.perm_row[pos] = (int)(p / a.K);
+      a.perm_w[pos] = a.w[p];
+      a.inv[p] = pos;
+    }
+    __syncthreads();
+    if (tid < a.E) base[tid] += cnt[tid];
+    __syncthreads();
+  }
+}
+
 void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
   GN_CHECK(a.E <= MOE_MAXE && a.K <= MOE_MAXK && a.K <= a.E, "moe: at most 64 experts, top-8");
   GN_CHECK(a.C % 4 == 0, "moe: model width must be a multiple of 4");
@@ -721,6 +774,16 @@ void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
                        a.logits, a.bias, a.rows, a.E, a.K, a.probs, a.sel, a.w, a.logits_sum);
   }
   GN_HIP(hipGetLastError());
+  if (!a.xg && npairs <= MOE_SMALL_PAIRS) {
+    // decode-size batch without a gathered copy: one placement block
+    MoePlaceArgs pa{};
+    pa.sel = a.sel; pa.w = a.w;
+    pa.npairs = npairs; pa.K = a.K; pa.E = a.E; pa.C = a.C;
+    pa.perm_row = a.perm_row; pa.perm_w = a.perm_w; pa.inv = a.inv;
+    hipLaunchKernelGGL(moe_route_small_kernel, dim3(1), dim3(MOE_PB), 0, st, pa, a.off);
+    GN_HIP(hipGetLastError());
+    return;
+  }
   const int nblk = (int)ceil_div(npairs, MOE_PB);
   hipLaunchKernelGGL(moe_count_kernel, dim3(nblk), dim3(MOE_PB), 0, st, a.sel, npairs, a.E,
                      a.blockcnt);
