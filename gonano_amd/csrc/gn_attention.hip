@@ -24,8 +24,9 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
-// Decode: one block of NW waves per (row, kv-head, split of up to 256 keys),
-// in three phases; all r query heads of the GQA group share every K/V load.
+// Decode: one block of NW waves per (row, kv-head, split of up to 256 or 512
+// keys), in three phases; all r query heads of the GQA group share every K/V
+// load.
 //  1. Scores.  Lanes form 8 groups of 8; in each step group g of a wave
 //     takes one key, and load i of lane part p of the group reads dims
 //     [4(p + 8i), 4(p + 8i) + 4) of it: each of the 4 load instructions of a
@@ -34,8 +35,10 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 //     An 8-lane reduction gives the r scores, kept in LDS.  Each wave
 //     streams a contiguous 1/NW of the split with two steps of K rows in
 //     flight.
-//  2. Softmax over the split: block max and sum per head, p = exp(s - max)
-//     written back over the scores.
+//  2. Softmax over the split: each wave reduces the block max per head from
+//     LDS itself (DPP + readlane, no cross-wave exchange), the owner thread
+//     of a key writes p = exp(s - max) back over the score, per-wave sums of
+//     p are added at the end; two barriers.
 //  3. P.V: thread t reads float4 (t mod 32) of V rows j = t/32 + 2*NW*i,
 //     i.e. two whole rows per wave instruction, and accumulates p[h][j] *
 //     V[j] for every head; the 2*NW row groups are added in LDS.  The first
@@ -49,14 +52,29 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 // tie on short ones; deeper per-wave queues at 4 waves (every K and V byte
 // of a 129-key split requested before the first wait, 219 VGPRs) were 8 %
 // slower; spreading a step's K loads over whole 128-byte lines (instead of
-// 64 bytes per lane) gained 3 %.
+// 64 bytes per lane) gained 3 %.  Per-block phase timestamps (cold caches,
+// 129 keys) put ~2 us of the former four-barrier shuffle softmax on every
+// block's critical path after its last K row arrived; the present phase 2
+// removes most of it (18.2 -> 17.1 us).  The rest of the gap to a plain
+// streaming read of the same bytes on the same grid (13.4 us) is the VALU
+// work of fp32 attention (768 FMAs per key and block plus reductions, ~4
+// cycles per wave instruction) landing after the last rows arrive: variants
+// that request every K and V byte up front (16 or 32 lanes per key), that
+// keep per-half-wave softmax states merged once, or that stream K and V in
+// one online-softmax pass all measured 16.7-18.6 us.
 // One split covering the whole window writes the normalized output; several
 // splits write (unnormalized output, max, sum) for decode_combine_kernel.
 // ---------------------------------------------------------------------------
-// Keys per split: at most DEC_KPS, balanced (300 keys -> 2 x 150).  Smaller
-// splits were measured slower: the combine pass they need costs more than
-// the extra workgroups gain.
+// Keys per split: at most DEC_KPS, balanced (300 keys -> 2 x 150), or up to
+// DEC_KPS_WIDE when the (row, kv-head) blocks alone already give two blocks
+// per CU (rows * Hkv >= DEC_WIDE_BLOCKS, plain windows): a 257-512-key window
+// then runs as one block per (row, kv-head) with no combine pass (d12 full
+// layer, 384 keys: 37-40 us against 46.6 us as 2 splits + combine; 512 keys:
+// 49 vs 57 us).  Smaller splits were measured slower: the combine pass they
+// need costs more than the extra workgroups gain.
 static constexpr int DEC_KPS = 256;
+static constexpr int DEC_KPS_WIDE = 512;
+static constexpr int DEC_WIDE_BLOCKS = 512;
 static constexpr int DEC_MAXR = 8;   // max GQA ratio
 // NW waves per block; the V rows of phase 3 are dealt to 2*NW row groups.
 template <int R, int NW>
@@ -76,12 +94,12 @@ struct DecWaves {
 struct DecSplit {
   int kstart, kend, kps, nsplit;
 };
-__host__ __device__ inline DecSplit dec_split(int kstart, int kend) {
+__host__ __device__ inline DecSplit dec_split(int kstart, int kend, int kps_max = DEC_KPS) {
   DecSplit d;
   d.kstart = kstart;
   d.kend = kend;
   const int n = kend - kstart;
-  const int ns = (n + DEC_KPS - 1) / DEC_KPS;
+  const int ns = (n + kps_max - 1) / kps_max;
   d.kps = (n + ns - 1) / ns;
   d.nsplit = (n + d.kps - 1) / d.kps;  // every split non-empty
   return d;
@@ -106,8 +124,10 @@ __host__ __device__ inline DecPlan dec_plan_at(const DecodeAttnArgs& a, int pos,
     p.g = count > 0 ? dec_split(0, count) : dec_empty();
     p.l = a.window > 0 ? dec_split(max(0, pos - a.window), pos + 1) : dec_empty();
   } else {
+    const int kps = a.split_keys > 0 ? a.split_keys : DEC_KPS;
     p.g = dec_empty();
-    p.l = a.pos_dev ? dec_split(max(0, pos - a.window), pos + 1) : dec_split(a.kstart, a.kend);
+    p.l = a.pos_dev ? dec_split(max(0, pos - a.window), pos + 1, kps)
+                    : dec_split(a.kstart, a.kend, kps);
   }
   p.nsplit = p.g.nsplit + p.l.nsplit;
   return p;
@@ -118,25 +138,29 @@ __device__ __forceinline__ DecPlan dec_plan(const DecodeAttnArgs& a, int bk) {
 }
 
 __device__ __forceinline__ float red8_sum(float v) { return sum8_dpp(v); }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// Wave-uniform maximum / sum of the 64 lanes without LDS round trips: a
+// 16-lane DPP reduction, then the four row results by readlane (a shuffle
+// butterfly is six dependent ds_bpermute/swizzle steps).  Every lane of the
+// wave must be active.
+__device__ __forceinline__ float wave_max_bcast(float v) {
+  v = max16_dpp(v);
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_bcast(float v) {
+  v = sum16_dpp(v);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
 template <int R, int NW>
 __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   constexpr int NT = 64 * NW;
   constexpr int KD = DecDepth<R, NW>::KD, VP = DecDepth<R, NW>::VP, RS = DecDepth<R, NW>::RS;
-  __shared__ float sc[R][DEC_KPS];
+  __shared__ float sc[R][DEC_KPS_WIDE];
   __shared__ __attribute__((aligned(16))) float pv[RS][R][HD];
-  __shared__ float wred[NW][R];
-  __shared__ float stat[2][R];  // max, sum per head
+  __shared__ float wred[NW][R];  // per-wave sums of p
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int bh = blockIdx.x, s = blockIdx.y;
   const DecPlan pl = dec_plan(a, bh);
@@ -219,38 +243,43 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   }
   __syncthreads();
 
-  // ---- phase 2: softmax over the split (thread t owns key t)
+  // ---- phase 2: softmax over the split.  Every wave takes the block
+  // maximum itself from the scores in LDS, so no wave waits on another for
+  // it; the thread owning key j writes p = exp(s - max) back over the score;
+  // the per-wave sums of p are added at the end.  (The former version, a
+  // shuffle-butterfly max and sum per wave merged through LDS over four
+  // barriers, cost ~2 us per block on the critical path.)
+  float mx[R];
+#pragma unroll
+  for (int h = 0; h < R; h++) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < DEC_KPS_WIDE / 64; k++)
+      if (64 * k < nk) {  // wave-uniform
+        const int j = lane + 64 * k;
+        if (j < nk) m = fmaxf(m, sc[h][j]);
+      }
+    mx[h] = wave_max_bcast(m);
+  }
+  __syncthreads();  // every wave has read the scores before p overwrites them
   {
-    float v[R], mx[R];
+    float ps[R];
+#pragma unroll
+    for (int h = 0; h < R; h++) ps[h] = 0.f;
+    for (int j = tid; j < nk; j += NT)
+#pragma unroll
+      for (int h = 0; h < R; h++) {
+        const float p = expf(sc[h][j] - mx[h]);
+        sc[h][j] = p;
+        ps[h] += p;
+      }
 #pragma unroll
     for (int h = 0; h < R; h++) {
-      v[h] = tid < nk ? sc[h][tid] : -INFINITY;
-      const float m = wave_max(v[h]);
-      if (lane == 0) wred[wid][h] = m;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < R; h++) {
-      mx[h] = wred[0][h];
-#pragma unroll
-      for (int w = 1; w < NW; w++) mx[h] = fmaxf(mx[h], wred[w][h]);
-      const float p = tid < nk ? expf(v[h] - mx[h]) : 0.f;
-      if (tid < nk) sc[h][tid] = p;
-      v[h] = wave_sum(p);
-    }
-    __syncthreads();  // everyone has read wred (max) and written p
-    if (lane == 0)
-#pragma unroll
-      for (int h = 0; h < R; h++) wred[wid][h] = v[h];
-    __syncthreads();
-    if (tid < R) {
-      stat[0][tid] = mx[tid];
-      float l = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; w++) l += wred[w][tid];
-      stat[1][tid] = l;
+      const float t = wave_sum_bcast(ps[h]);
+      if (lane == 0) wred[wid][h] = t;
     }
   }
+  __syncthreads();
 
   // ---- phase 3: P.V
   float acc[R][4];
@@ -304,13 +333,16 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
     float o = 0.f;
 #pragma unroll
     for (int r = 0; r < RS; r++) o += pv[r][h][dd];
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) l += wred[w][h];
     if (whole) {
-      a.o[((int64_t)row * a.Hq + hk * R + h) * HD + dd] = o / stat[1][h];
+      a.o[((int64_t)row * a.Hq + hk * R + h) * HD + dd] = o / l;
     } else {
       out[h * (HD + 2) + dd] = o;
       if (dd == 0) {
-        out[h * (HD + 2) + HD] = stat[0][h];
-        out[h * (HD + 2) + HD + 1] = stat[1][h];
+        out[h * (HD + 2) + HD] = mx[h];
+        out[h * (HD + 2) + HD + 1] = l;
       }
     }
   }
@@ -358,8 +390,8 @@ __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
   a.o[(int64_t)rq * HD + threadIdx.x] = o / total;
 }
 
-static int decode_attention_max_splits(int window, int maxSeq) {
-  return dec_split(0, std::min(window + 1, maxSeq)).nsplit;
+static int decode_attention_max_splits(int window, int maxSeq, int kps = DEC_KPS) {
+  return dec_split(0, std::min(window + 1, maxSeq), kps).nsplit;
 }
 
 int decode_attention_split_cap(const DecodeAttnArgs& a) {
@@ -373,6 +405,8 @@ int decode_attention_split_cap(const DecodeAttnArgs& a) {
 
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= DEC_MAXR, "decode attention: GQA ratio must be <= 8");
+  // wide splits only when the (row, kv-head) blocks fill the CUs on their own
+  a.split_keys = a.ratio <= 1 && (int64_t)a.rows * a.Hkv >= DEC_WIDE_BLOCKS ? DEC_KPS_WIDE : DEC_KPS;
   bool combine;
   if (a.ratio > 1) {
     GN_CHECK(a.ck && a.cv && a.maxBlocks > 0 && a.window >= 0, "decode attention: bad compressed cache");
@@ -388,11 +422,11 @@ void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   } else if (a.pos_dev) {
     // position read on the device: size for the longest key range
     GN_CHECK(a.window >= 0, "decode attention: bad window");
-    a.nsplit_max = decode_attention_max_splits(a.window, a.maxSeq);
+    a.nsplit_max = decode_attention_max_splits(a.window, a.maxSeq, a.split_keys);
     combine = a.nsplit_max > 1;
   } else {
     GN_CHECK(a.kend > a.kstart, "decode attention: empty key range");
-    a.nsplit_max = dec_split(a.kstart, a.kend).nsplit;
+    a.nsplit_max = dec_split(a.kstart, a.kend, a.split_keys).nsplit;
     combine = a.nsplit_max > 1;
   }
   // every block that does not cover its whole key range writes its split's

@@ -90,6 +90,7 @@ struct DecodeAttnArgs {
   const int* nsel = nullptr;
   int kcap = 0;
   int nsplit_max;      // set by the launcher: grid.y and the split stride of part
+  int split_keys = 0;  // set by the launcher: most keys per split of a plain window
   int64_t part_floats = 0;  // capacity of part in floats; the launcher rejects a
                             // grid whose split layout would not fit
   // optional events recorded by the dispatch itself (hipExtLaunchKernelGGL):
