@@ -76,6 +76,7 @@ static constexpr int DEC_KPS = 256;
 static constexpr int DEC_KPS_WIDE = 512;
 static constexpr int DEC_WIDE_BLOCKS = 512;
 static constexpr int DEC_MAXR = 8;   // max GQA ratio
+static constexpr int DEC_POST_SPLITS = DECODE_POST_MAX_SPLITS;
 // NW waves per block; the V rows of phase 3 are dealt to 2*NW row groups.
 template <int R, int NW>
 struct DecDepth {
@@ -154,13 +155,139 @@ __device__ __forceinline__ float wave_sum_bcast(float v) {
   return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
+// Fused q/k/v post-processing of one block's heads (fuse_post): wave w takes
+// heads w, w + NW, ... of the R query heads, the key head (R) and the value
+// head (R + 1) of kv-head hk; a lane holds dims lane and lane + 64.  The
+// arithmetic is qkv_post_kernel's (split partials summed in float64 in split
+// order, the VE gate's butterfly sum, the rotation and the norm as written
+// there), so fused and separate launches give the same bits.
 template <int R, int NW>
+struct DecPost {
+  static constexpr int HPW = (R + 2 + NW - 1) / NW;  // heads per wave
+  static constexpr int FZ = DEC_POST_SPLITS;         // partials loaded per element
+  float v[HPW][2][FZ];                               // raw values / partials
+  float cv[2], sv[2];                                // RoPE entries of the lane's dims
+  float hv, wv, ve[2];                               // VE gate inputs, the token's VE row
+
+  __device__ __forceinline__ static int col(const QkvPostArgs& p, int hk, int hd) {
+    return hd < R ? (hk * R + hd) * HD : hd == R ? (p.Hq + hk) * HD : (p.Hq + p.Hkv + hk) * HD;
+  }
+  // Every load of the prologue, issued before the attention's own loads and
+  // without branches: the token id (the one dependent address) first, then
+  // FZ partials per element at clamped split indices (the sum uses the
+  // first `splits`), the RoPE entries and the VE inputs.
+  __device__ __forceinline__ void load(const QkvPostArgs& p, int row, int hk, int pos, int wid,
+                                       int lane) {
+    const int vid = p.ve ? p.ids[row] : 0;
+    const int64_t rbase = (int64_t)row * (p.Hq + 2 * p.Hkv) * HD;
+    const PendingSum& ps = p.qkv_sum;
+    const float* src = ps.splits > 0 ? ps.part : p.qkv;
+    const int zmax = ps.splits > 0 ? ps.splits - 1 : 0;
+#pragma unroll
+    for (int u = 0; u < HPW; u++) {
+      const int hd = min(wid + NW * u, R + 1);
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int64_t i = rbase + col(p, hk, hd) + lane + 64 * e;
+#pragma unroll
+        for (int z = 0; z < FZ; z++) v[u][e][z] = src[min(z, zmax) * ps.stride + i];
+      }
+    }
+    const int half = p.R / 2, off = HD - p.R;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const int d = lane + 64 * e;
+      const int j = max(d - off, 0), jj = j < half ? j : j - half;
+      cv[e] = sv[e] = 0.f;
+      if (half > 0) {  // uniform
+        cv[e] = p.cosT[(int64_t)pos * half + jj];
+        sv[e] = p.sinT[(int64_t)pos * half + jj];
+      }
+    }
+    hv = wv = 0.f;
+    ve[0] = ve[1] = 0.f;
+    if (p.ve) {
+      hv = p.h[(int64_t)row * p.C + min(lane, VE_CH - 1)];
+      wv = p.wve[hk * VE_CH + min(lane, VE_CH - 1)];
+      const float* ver = p.ve + ((int64_t)vid * p.Hkv + hk) * HD;
+      ve[0] = ver[lane];
+      ve[1] = ver[lane + 64];
+    }
+  }
+  // q heads (rotated, normed, 1.2 x) into out[0..R), the key into out[R], the
+  // value into out[R + 1]; the block holding the position also writes the
+  // key and value rows of the cache.
+  __device__ __forceinline__ void compute(const QkvPostArgs& p, float (*out)[HD], float* kc,
+                                          float* vc, int64_t crow, bool write_cache, int wid,
+                                          int lane) {
+    const int half = p.R / 2, off = HD - p.R;
+#pragma unroll
+    for (int u = 0; u < HPW; u++) {
+      const int hd = wid + NW * u;
+      if (hd >= R + 2) continue;  // wave-uniform
+      float x[2];
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        if (p.qkv_sum.splits > 0) {
+          double sum = 0.0;
+#pragma unroll
+          for (int z = 0; z < FZ; z++)
+            if (z < p.qkv_sum.splits) sum += (double)v[u][e][z];
+          x[e] = (float)sum;
+        } else {
+          x[e] = v[u][e][0];
+        }
+      }
+      if (hd == R + 1) {  // v += gate * ve[id] (attention.go:247-248, 392-405)
+        if (p.ve) {
+          const float g = warp_sum(lane < VE_CH ? hv * wv : 0.f);
+          const float gate = sigmoidf_(g) * VE_SCALE;
+#pragma unroll
+          for (int e = 0; e < 2; e++) x[e] += gate * ve[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          out[hd][lane + 64 * e] = x[e];
+          if (write_cache) vc[crow * HD + lane + 64 * e] = x[e];
+        }
+        continue;
+      }
+      // rotate the trailing R dims (partners through LDS, this wave's own row)
+      out[hd][lane] = x[0];
+      out[hd][lane + 64] = x[1];
+      float y[2];
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int d = lane + 64 * e;
+        float t = out[hd][d];
+        if (d >= off) {
+          const int j = d - off;
+          if (j < half) t = out[hd][d] * cv[e] + out[hd][d + half] * sv[e];
+          else t = -out[hd][d - half] * sv[e] + out[hd][d] * cv[e];
+        }
+        y[e] = t;
+      }
+      const float ss = warp_sum(y[0] * y[0] + y[1] * y[1]);
+      const float inv = 1.f / sqrtf(ss / (float)HD + NORM_EPS);
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const float o = y[e] * inv * QK_SCALE;
+        out[hd][lane + 64 * e] = o;
+        if (hd == R && write_cache) kc[crow * HD + lane + 64 * e] = o;
+      }
+    }
+  }
+};
+
+template <int R, int NW, bool FUSE>
 __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   constexpr int NT = 64 * NW;
   constexpr int KD = DecDepth<R, NW>::KD, VP = DecDepth<R, NW>::VP, RS = DecDepth<R, NW>::RS;
   __shared__ float sc[R][DEC_KPS_WIDE];
   __shared__ __attribute__((aligned(16))) float pv[RS][R][HD];
   __shared__ float wred[NW][R];  // per-wave sums of p
+  // fused post-processing: q heads, the new key, the new value
+  __shared__ __attribute__((aligned(16))) float post[FUSE ? R + 2 : 1][HD];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int bh = blockIdx.x, s = blockIdx.y;
   const DecPlan pl = dec_plan(a, bh);
@@ -177,6 +304,17 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   const int* gsel = (glob && a.sel) ? a.sel + (int64_t)bh * a.kcap + ks : nullptr;
   const int64_t gbase = cbase - ks;
   auto krow = [&](int j) -> int64_t { return gsel ? gbase + gsel[j] : cbase + j; };
+  // fused: the query position's key is key jn of this split (-1: another
+  // split's); the cache holds it only after this block writes it, so the
+  // scores and P.V take it from `post`
+  int jn = -1, qpos = 0;
+  DecPost<R, NW> dp;
+  if constexpr (FUSE) {
+    qpos = a.pos_dev ? *a.pos_dev : a.kend - 1;
+    jn = qpos - ks < nk ? qpos - ks : -1;
+    dp.load(a.post, row, hk, qpos, wid, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   const int d4 = tid & 31, jr = tid >> 5;
   const v4f* vrow = reinterpret_cast<const v4f*>(vbase) + d4;
@@ -185,18 +323,20 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   // ---- phase 1: scores
   {
     const int g = lane >> 3, part = lane & 7;
-    const float* qrow = a.q + ((int64_t)row * a.Hq + hk * R) * HD + 4 * part;
     float qv[R][16];
+    auto read_q = [&](const float* qrow) {
 #pragma unroll
-    for (int h = 0; h < R; h++)
+      for (int h = 0; h < R; h++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const v4f t = *reinterpret_cast<const v4f*>(qrow + h * HD + 32 * i);
-        qv[h][4 * i] = t[0];
-        qv[h][4 * i + 1] = t[1];
-        qv[h][4 * i + 2] = t[2];
-        qv[h][4 * i + 3] = t[3];
-      }
+        for (int i = 0; i < 4; i++) {
+          const v4f t = *reinterpret_cast<const v4f*>(qrow + h * HD + 32 * i);
+          qv[h][4 * i] = t[0];
+          qv[h][4 * i + 1] = t[1];
+          qv[h][4 * i + 2] = t[2];
+          qv[h][4 * i + 3] = t[3];
+        }
+    };
+    if constexpr (!FUSE) read_q(a.q + ((int64_t)row * a.Hq + hk * R) * HD + 4 * part);
     const int qw = (nk + NW - 1) / NW;
     const int j0 = wid * qw, j1 = min(nk, j0 + qw);
     const v4f* kb = reinterpret_cast<const v4f*>(kbase + 4 * part);
@@ -217,11 +357,23 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
       const int j = jr + RS * i;
       vpre[i] = vrow[krow(j < nk ? j : 0) * (HD / 4)];
     }
+    if constexpr (FUSE) {
+      __builtin_amdgcn_sched_barrier(0);
+      // the cache rows of the position are this block's to write (the
+      // attention of this layer reads them from `post` only)
+      dp.compute(a.post, post, const_cast<float*>(a.kc), const_cast<float*>(a.vc),
+                 ((int64_t)row * a.Hkv + hk) * a.maxSeq + qpos, jn >= 0, wid, lane);
+      __syncthreads();
+      read_q(&post[0][4 * part]);
+    }
     for (int jb = j0; jb < j1; jb += 8 * KD) {
 #pragma unroll
       for (int t = 0; t < KD; t++) {
         const int jc = jb + 8 * t;  // wave-uniform
         if (jc < j1) {
+          if (FUSE && jc + g == jn)
+#pragma unroll
+            for (int i = 0; i < 4; i++) kr[t][i] = *reinterpret_cast<const v4f*>(&post[R][4 * (part + 8 * i)]);
           float d[R];
 #pragma unroll
           for (int h = 0; h < R; h++) {
@@ -287,7 +439,9 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   for (int h = 0; h < R; h++)
 #pragma unroll
     for (int c = 0; c < 4; c++) acc[h][c] = 0.f;
-  auto accumulate = [&](int j, const v4f& vv) {
+  auto accumulate = [&](int j, const v4f& vin) {
+    v4f vv = vin;
+    if (FUSE && j == jn) vv = *reinterpret_cast<const v4f*>(&post[R + 1][4 * d4]);
 #pragma unroll
     for (int h = 0; h < R; h++) {
       const float p = sc[h][j];
@@ -350,19 +504,25 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
 
 // One kernel per GQA ratio R, so each instance is sized (registers, LDS) for
 // its own R rather than for the largest.
-template <int R, int NW>
+template <int R, int NW, bool FUSE>
 __global__ __launch_bounds__(64 * NW) void decode_attn_kernel(DecodeAttnArgs a) {
-  decode_attn_body<R, NW>(a);
+  decode_attn_body<R, NW, FUSE>(a);
+}
+template <int R, bool FUSE>
+static void launch_decode_attn_f(dim3 grid, hipStream_t st, const DecodeAttnArgs& a,
+                                 hipEvent_t stop) {
+  constexpr int NW = DecWaves<R>::NW;
+  if (a.t_start || stop)
+    hipExtLaunchKernelGGL((decode_attn_kernel<R, NW, FUSE>), grid, dim3(64 * NW), 0, st,
+                          a.t_start, stop, 0, a);
+  else
+    hipLaunchKernelGGL((decode_attn_kernel<R, NW, FUSE>), grid, dim3(64 * NW), 0, st, a);
 }
 template <int R>
 static void launch_decode_attn(dim3 grid, hipStream_t st, const DecodeAttnArgs& a,
                                hipEvent_t stop) {
-  constexpr int NW = DecWaves<R>::NW;
-  if (a.t_start || stop)
-    hipExtLaunchKernelGGL((decode_attn_kernel<R, NW>), grid, dim3(64 * NW), 0, st, a.t_start,
-                          stop, 0, a);
-  else
-    hipLaunchKernelGGL((decode_attn_kernel<R, NW>), grid, dim3(64 * NW), 0, st, a);
+  if (a.fuse_post) launch_decode_attn_f<R, true>(grid, st, a, stop);
+  else launch_decode_attn_f<R, false>(grid, st, a, stop);
 }
 
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
@@ -405,6 +565,17 @@ int decode_attention_split_cap(const DecodeAttnArgs& a) {
 
 void launch_decode_attention(DecodeAttnArgs a, hipStream_t st) {
   GN_CHECK(a.Hq % a.Hkv == 0 && a.Hq / a.Hkv <= DEC_MAXR, "decode attention: GQA ratio must be <= 8");
+  if (a.fuse_post) {
+    const QkvPostArgs& p = a.post;
+    GN_CHECK(a.ratio <= 1 && !a.sel && p.Hq == a.Hq && p.Hkv == a.Hkv && p.T == 1 &&
+                 p.R % 2 == 0 && p.R <= HD && p.cosT && p.sinT && (p.qkv || p.qkv_sum.splits > 0) &&
+                 (!p.ve || (p.h && p.ids && p.wve)),
+             "decode attention: bad fused q/k/v arguments");
+    GN_CHECK(p.qkv_sum.splits == 0 ||
+                 (p.qkv_sum.stride == (int64_t)a.rows * (p.Hq + 2 * p.Hkv) * HD &&
+                  p.qkv_sum.splits <= DEC_POST_SPLITS),
+             "decode attention: fused q/k/v pending sum shape");
+  }
   // wide splits only when the (row, kv-head) blocks fill the CUs on their own
   a.split_keys = a.ratio <= 1 && (int64_t)a.rows * a.Hkv >= DEC_WIDE_BLOCKS ? DEC_KPS_WIDE : DEC_KPS;
   bool combine;

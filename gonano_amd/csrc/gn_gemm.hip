@@ -108,10 +108,10 @@ typedef __attribute__((address_space(3))) void lds_void;
 // holds k = 16g + 4q + c in component c, and MFMA c of the group consumes
 // component c of both operands.  Every k is paired with itself in A and B,
 // so the products summed are the same as in natural order.
-template <int BD, int NT, bool KCONTIG>
+template <int BD, int NT, bool KCONTIG, int TK = GK>
 struct TileIO {
-  static constexpr int ROWSLOTS = KCONTIG ? GK / 4 : BD / 4;  // 16-byte slots per LDS row
-  static constexpr int SIZE = BD * GK;                         // floats
+  static constexpr int ROWSLOTS = KCONTIG ? TK / 4 : BD / 4;  // 16-byte slots per LDS row
+  static constexpr int SIZE = BD * TK;                         // floats
   static constexpr int NV = SIZE / 4 / NT;                     // slots per thread
   static constexpr int RSTEP = NT / ROWSLOTS;                  // LDS rows per instruction
   static_assert(NV >= 1 && NT % ROWSLOTS == 0 && RSTEP % 8 == 0, "tile shape");
@@ -223,21 +223,22 @@ __device__ __forceinline__ void tile_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// C tile of BM x BN per workgroup of WM x WN x WK waves, K in GK-deep tiles
+// C tile of BM x BN per workgroup of WM x WN x WK waves, K in TK-deep tiles (GK unless given)
 // through an S-stage LDS ring: tile kt + S - 1 is in flight while tile kt
 // is multiplied.  The WK wave groups take alternate 16-deep k groups of
 // every tile (more waves per SIMD for small grids) and are added in LDS at
 // the end.  With p.splits > 1 each workgroup sums one K range into p.part
 // and gemm_reduce_kernel applies the epilogue.
 template <int BM, int BN, int WM, int WN, int WK, int S, bool FOLD, bool AK, bool BK, bool VEC,
-          int GRP>
+          int GRP, int TK = GK>
 __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p0) {
   constexpr int NT = 64 * WM * WN * WK;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int MI = TM / 16, NI = TN / 16;
-  static_assert((GK / 16) % WK == 0, "k groups per wave group");
-  using LA = TileIO<BM, NT, AK>;
-  using LB = TileIO<BN, NT, BK>;
+  static_assert((TK / 16) % WK == 0, "k groups per wave group");
+  static_assert(TK == GK || (AK && BK), "deep K tiles: K-contiguous operands");
+  using LA = TileIO<BM, NT, AK, TK>;
+  using LB = TileIO<BN, NT, BK, TK>;
   constexpr int PT = LA::NV + LB::NV;  // LDS-DMA instructions per tile and thread
   static_assert(S >= 2 && PT * (S - 2) < 64, "pipeline depth");
   static_assert((WK - 1) * WM * WN * MI * NI * 256 <= S * LA::SIZE,
@@ -281,14 +282,14 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
     kbeg = split * p.k_per_split;
     kend = min(p.K, kbeg + p.k_per_split);
   }
-  const int nkt = kend > kbeg ? (kend - kbeg + GK - 1) / GK : 0;
+  const int nkt = kend > kbeg ? (kend - kbeg + TK - 1) / TK : 0;
   // Rows mode with a padded A (a_pad): a tile may read up to BM rows past
   // its group's end (the next group's rows or the padding); those rows only
   // feed output rows >= p.M, which the epilogue discards, so partial groups
   // still take the direct path.
   const bool interior = VEC && (m0 + BM <= p.M || (GRP == GEMM_GROUP_ROWS && p.a_pad)) &&
                         n0 + BN <= p.N;
-  const int nfull = interior ? (kend - kbeg) / GK : 0;
+  const int nfull = interior ? (kend - kbeg) / TK : 0;
 
   LA la;
   LB lb;
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
   // Fills LDS stage `buf` with K tile kt; readable after wait_tiles and
   // tile_barrier.
   auto load = [&](int kt, int buf) {
-    const int k0 = kbeg + kt * GK;
+    const int k0 = kbeg + kt * TK;
     if (kt < nfull) {
       la.load_direct(p.A, p.lda, m0, k0, As[buf], wid);
       lb.load_direct(p.B, p.ldb, n0, k0, Bs[buf], wid);
@@ -334,7 +335,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
     // one tile's MFMAs into t; `fresh`: the first MFMA starts from zero
     auto tile_mma = [&](v4f(&t)[MI][NI], auto fresh) {
 #pragma unroll
-      for (int gi = 0; gi < GK / 16 / WK; gi++) {
+      for (int gi = 0; gi < TK / 16 / WK; gi++) {
         const int g = gi * WK + wk;
         v4f fa[MI], fb[NI];
 #pragma unroll
@@ -463,7 +464,7 @@ static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int spli
 
 // Both operands K-contiguous only (x.W^T): tile shapes whose M/N-contiguous
 // LDS layout would not divide into the workgroup's slots.
-template <int BM, int BN, int WM, int WN, int WK, int S>
+template <int BM, int BN, int WM, int WN, int WK, int S, int TK = GK>
 static void launch_cfg_kk(const GemmParams& p, bool vec, int splits, hipStream_t st) {
   GemmParams q = p;
   q.tiles_m = (int)ceil_div(p.M, BM);
@@ -472,10 +473,10 @@ static void launch_cfg_kk(const GemmParams& p, bool vec, int splits, hipStream_t
   dim3 grid(q.tiles_m * q.tiles_n * splits);
   dim3 block(64 * WM * WN * WK);
   if (vec)
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, false, true, true, true, GEMM_GROUP_NONE>),
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, false, true, true, true, GEMM_GROUP_NONE, TK>),
                        grid, block, 0, st, q);
   else
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, false, true, true, false, GEMM_GROUP_NONE>),
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, false, true, true, false, GEMM_GROUP_NONE, TK>),
                        grid, block, 0, st, q);
   GN_HIP(hipGetLastError());
 }
@@ -627,7 +628,9 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   // projections, N = 768 or 3072 at M = 256): 32x96 tiles with a split
   // count that makes the workgroups fill whole rounds of the CUs (the MLP
   // input projection: exactly 256 tiles; the output projections: 64 tiles
-  // x 4 splits), where 64x64 tiles leave a quarter of the CUs idle.
+  // x 4 splits), where 64x64 tiles leave a quarter of the CUs idle.  Their
+  // K tiles are 64 deep (half the barriers of 32-deep ones; 128-deep and
+  // deeper rings measured no faster).
   bool narrow = false;
   if (!use_big && !long_k && d.force_splits == 0 && d.N % 96 == 0 && d.a_kcontig && d.b_kcontig) {
     const int64_t nt = ceil_div(d.M, 32) * (d.N / 96);
@@ -675,8 +678,8 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     launch_cfg<128, 128, 2, 2, 1, 2, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   else if (fold)
     launch_cfg<64, 64, 2, 2, 2, 4, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
-  else if (narrow)
-    launch_cfg_kk<32, 96, 1, 2, 2, 4>(p, vec, splits, st);
+  else if (narrow)  // 64-deep K tiles, two stages (fc 21.3 -> 19.4 us, proj 18.7 -> 17.7 us)
+    launch_cfg_kk<32, 96, 1, 2, 2, 2, 64>(p, vec, splits, st);
   else
     launch_cfg<64, 64, 2, 2, 2, 4, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   if (defer) {

@@ -5,6 +5,12 @@
 
 namespace gn {
 
+static constexpr float NORM_EPS = 1e-6f;  // model/attention.go:11
+static constexpr float QK_SCALE = 1.2f;   // model/attention.go:14
+static constexpr int VE_CH = 12;          // model/attention.go:18
+static constexpr float VE_SCALE = 3.f;    // model/attention.go:21
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+
 // ---- embedding / norms --------------------------------------------------
 void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, const float* lam,
                         int B, int T, int C, float* raw, float* embn, float* smsig, float* x,
@@ -97,7 +103,19 @@ struct DecodeAttnArgs {
   // t_start when the attention kernel starts, t_stop when the last kernel of
   // the call (the combine, when launched) ends -- the calls' own duration
   hipEvent_t t_start = nullptr, t_stop = nullptr;
+  // Fused q/k/v post-processing (plain windows, one token per row): with
+  // fuse_post set, q is not read from `q`.  Each block computes its R query
+  // heads and its kv head from post.qkv (or the pending split-K partials
+  // post.qkv_sum) exactly as qkv_post_kernel does -- VE gate on v, RoPE on
+  // the trailing post.R dims, 1.2 * RMSNorm per head -- the block whose
+  // split holds the query position writes the new key and value to kc/vc,
+  // and the new key/value enter the block's scores and P.V from its own
+  // copy.  Read: post.{qkv | qkv_sum}, h, ids, ve, wve, cosT, sinT, C, R.
+  bool fuse_post = false;
+  QkvPostArgs post{};
 };
+// Most split-K partials of the q/k/v product a fused launch sums.
+constexpr int DECODE_POST_MAX_SPLITS = 4;
 // Split capacity a part buffer needs for launches with these arguments
 // (window, maxSeq, ratio, maxBlocks).
 int decode_attention_split_cap(const DecodeAttnArgs& a);

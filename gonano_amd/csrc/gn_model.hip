@@ -8,13 +8,8 @@ namespace gn {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-static constexpr float NORM_EPS = 1e-6f;  // model/attention.go:11
-static constexpr float QK_SCALE = 1.2f;   // model/attention.go:14
-static constexpr int VE_CH = 12;          // model/attention.go:18
-static constexpr float VE_SCALE = 3.f;    // model/attention.go:21
 static constexpr int SMEAR_CH = 24;       // model/helpers.go:7
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
 
 // Sum of a per-thread value over a 256-thread block (float).
 __device__ __forceinline__ float bsum256(float v, float* sc) { return block_sum<float>(v, sc); }

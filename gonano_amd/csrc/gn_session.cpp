@@ -27,7 +27,6 @@ namespace gn {
 
 static constexpr int HD = 128;
 static constexpr int SMEAR_CH = 24;
-static constexpr int VE_CH = 12;
 
 // -------------------------------------------------------------------------
 // Go PCG stream bookkeeping on the host (tensors/random.go:16-18).
@@ -175,6 +174,8 @@ struct gn_session {
   std::vector<int32_t> pc_hits;  // prompt tokens taken from the cache, per group of the last call
   // decode steps replayed from one captured HIP graph per rollout
   bool decode_graph = true;
+  // q/k/v post-processing inside the decode attention kernel (plain windows)
+  bool fuse_qkv_post = true;
   bool capturing = false;
   void* pinned = nullptr;  // host staging for the per-step copies
   size_t pinned_bytes = 0;
@@ -1996,8 +1997,14 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     qa.maxSeq = maxSeq;
     qa.rows_per_seq = 1;
     qa.qkv_sum = qsum;
-    launch_qkv_post(qa, rows, st);
+    // plain windows: the attention kernel does the q/k/v post-processing of
+    // its own heads (one launch less per layer; GN_FUSE_QKV_POST=0 keeps
+    // the separate launch, same results)
+    const bool fuse = !s->hca && s->fuse_qkv_post && qsum.splits <= DECODE_POST_MAX_SPLITS;
+    if (!fuse) launch_qkv_post(qa, rows, st);
     DecodeAttnArgs da{};
+    da.fuse_post = fuse;
+    da.post = qa;
     da.q = q; da.kc = qa.kcache; da.vc = qa.vcache; da.part = part; da.o = o;
     da.part_floats = (int64_t)rows * Hkv * part_splits * (Hq / Hkv) * (HD + 2);
     da.rows = rows; da.Hq = Hq; da.Hkv = Hkv; da.maxSeq = maxSeq;
@@ -2736,6 +2743,8 @@ int gn_session_create(const gn_config* config, int device, gn_session** out) {
       // GN_GEMM_BLASLT=0 keeps every product on gemm_kernel
       const char* lt = std::getenv("GN_GEMM_BLASLT");
       if (!lt || std::strcmp(lt, "0") != 0) s->lt.reset(blaslt_create());
+      const char* fp = std::getenv("GN_FUSE_QKV_POST");
+      s->fuse_qkv_post = !fp || std::strcmp(fp, "0") != 0;
     } catch (...) {  // a rejected config or a failed allocation frees what was made
       if (s->stream) (void)gn_session_destroy(s);
       else delete s;

@@ -10,8 +10,9 @@ CED, 16 experts of 768) -- with the row counts of their rollouts (256, 512,
 256, 64) and prompts long enough to reach the multi-split decode attention
 and the hierarchical selection, at a depth and vocabulary the oracle handles
 in seconds; plus the full d12 model (12 layers, V = 65536).  The paths
-checked include decode attention at GQA ratios 3, 5 and 6 with two and
-three key splits and the combine, the 32 x 96 decode GEMM tiles with
+checked include decode attention at GQA ratios 3, 5 and 6 with one or two
+key splits and the combine, with the q/k/v post-processing fused into it
+(plain windows) or launched apart, the 32 x 96 decode GEMM tiles with
 deferred split-K sums (M = 256, N a multiple of 96), MLA decode at 6:3
 heads, the sparse decode at 6:1, and the policy-gradient loss over several
 logits chunks (GN_LOGITS_CHUNK) with the rows without a target left out of
@@ -171,9 +172,11 @@ def d12w():
 
 def test_d12_width_rollout_teacher_forced(orc, d12w):
     """256 rows (16 groups x 16), 260-token prompts: the full-context layer
-    attends 260..267 keys in two splits with the combine, the windowed layer
-    129 keys in one; the decode MLP and output projections take the 32 x 96
-    tiles at M = 256."""
+    attends 260..267 keys and the windowed layer 129, each in one split (256
+    rows x 2 KV heads fill the CUs without splitting the keys); the attention
+    kernel does the q/k/v post-processing itself (VE gate on the full layer,
+    RoPE, QK-norm, the new key/value written to the cache); the decode MLP
+    and output projections take the 32 x 96 tiles at M = 256."""
     cfg, w = d12w
     _rollout_check(orc, cfg, w, 16, 16, 260, 8, 1.0, groups=(0, 7, 15))
 
@@ -199,6 +202,27 @@ def test_d12_width_graph_equals_eager(d12w):
             got = s.generate_batch(prompts, 16, 10, 1.0, 50, seeds)
             assert all(np.array_equal(a, b) for a, b in zip(got, eager))
             s.forward(prompts[:2, :8])
+
+
+def test_d12_width_fused_qkv_post_equals_separate(d12w, monkeypatch):
+    """The q/k/v post-processing inside the decode attention kernel (the
+    default) and the separate qkv_post launch (GN_FUSE_QKV_POST=0) give the
+    same rollouts token for token: the same arithmetic in the same order,
+    the new key and value written to the cache and used from the block's own
+    copy on the step they are made."""
+    from gonano_amd.session import Session
+    cfg, w = d12w
+    prompts = np.random.default_rng(4).integers(0, cfg.vocab_size, (16, 260)).astype(np.int32)
+    seeds = np.arange(100, 116, dtype=np.uint64)
+    out = {}
+    for fuse in ("0", "1"):
+        monkeypatch.setenv("GN_FUSE_QKV_POST", fuse)
+        with Session(cfg) as s:
+            s.set_params(w)
+            out[fuse] = s.generate_batch(prompts, 16, 12, 1.0, 50, seeds)
+    monkeypatch.delenv("GN_FUSE_QKV_POST")
+    assert len(out["0"]) == len(out["1"]) == 256
+    assert all(np.array_equal(a, b) for a, b in zip(out["0"], out["1"]))
 
 
 # ---- the full d12 model (BASELINE configs[1]) -------------------------------
@@ -239,8 +263,9 @@ def d20w():
 
 
 def test_d20_width_rollout_teacher_forced(orc, d20w):
-    """512 rows (32 x 16), 520-token prompts, T = 0.8: GQA ratio 5 with three
-    key splits on both layers (the 512-token window admits 513 keys)."""
+    """512 rows (32 x 16), 520-token prompts, T = 0.8: GQA ratio 5 with two
+    key splits (at most 512 keys each) and the combine on both layers (the
+    512-token window admits 513 keys)."""
     cfg, w = d20w
     _rollout_check(orc, cfg, w, 32, 16, 520, 6, 0.8, groups=(0, 31))
 
