@@ -852,16 +852,22 @@ void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st) {
 // outputs j0..j0+15) of 4 waves: wave w requests its weight fragments (rows
 // j0..j0+15 over the w-th quarter of K, kept in registers) before anything
 // that depends on the routing, then multiplies the expert's pairs in
-// 32-pair chunks, two 16-row MFMA tiles at a time, as the weights arrive.  The 4 quarter sums are added
-// in LDS in wave order (deterministic) and one wave applies the epilogue.
-// No split-K partial buffers, no reduction launch.
+// chunks of 64 (four 16-row MFMA tiles, each tile's rows requested while the
+// previous one is multiplied), as the weights arrive.  The 4 quarter sums are
+// added in LDS in wave order (deterministic) and one wave applies the
+// epilogue.  No split-K partial buffers, no reduction launch.  (Chunks of 32
+// pairs left every expert with more than 32 -- half of them at d12 decode,
+// 256 rows x top-2 over 16 experts -- a second serial pass of loads,
+// products, reduction and epilogue: 28 -> 20 us for the d12 gate/up product.)
 // ---------------------------------------------------------------------------
 static constexpr int MOE_XW = 4;   // waves per block (K quarters)
+static constexpr int MOE_CT = 4;   // 16-row tiles per chunk
 
 template <int KH, bool GU>
 __global__ __launch_bounds__(64 * MOE_XW) void moe_expert_small_kernel(MoeExpertArgs a) {
   constexpr int NW = GU ? 2 : 1;          // weight matrices (gate, up | down)
   constexpr int JB = KH < 2 ? KH : 2;     // k groups of weights requested before the rows
+  constexpr int NB = (NW + 2) * KH <= 40 ? 2 : 1;  // row buffers (double-buffered tiles)
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int nb = a.N / 16;
   const int e = blockIdx.x / nb, j0 = (blockIdx.x - e * nb) * 16;
@@ -870,7 +876,7 @@ __global__ __launch_bounds__(64 * MOE_XW) void moe_expert_small_kernel(MoeExpert
   // B fragments: lane (r, q) holds weight row j0 + r, k = kq + 16 g + c.
   // Loads complete in issue order (vmcnt), so the order of requests sets
   // what the products can start on: the first JB k groups of weights, then
-  // the routing-dependent rows of the first chunk, then the remaining
+  // the routing-dependent rows of the first tile, then the remaining
   // weights, which the products consume as they arrive.
   v4f f[NW][KH];
   const float* bw[NW];
@@ -894,57 +900,67 @@ __global__ __launch_bounds__(64 * MOE_XW) void moe_expert_small_kernel(MoeExpert
     a.out[0] = z;
     return;
   }
-  const int nchunk = (cnt + 31) / 32;
+  const int nchunk = (cnt + 16 * MOE_CT - 1) / (16 * MOE_CT);
   if (nchunk == 0) return;
-  // A fragments of chunk t: lane (r, q) holds pair rows t*32 + 16h + r
-  // (clamped to the expert's last pair; those outputs are not stored)
-  v4f av[2][KH];
-  auto load_rows = [&](int t) {
+  // A fragments of tile u of chunk t: lane (r, q) holds pair row
+  // t*64 + 16u + r (clamped to the expert's last pair; those outputs are not
+  // stored)
+  v4f av[NB][KH];
+  auto load_rows = [&](int t, int u, v4f(&dst)[KH]) {
+    const int pr = beg + min(t * 16 * MOE_CT + 16 * u + r, cnt - 1);
+    const int64_t arow = GU ? (int64_t)a.perm_row[pr] : (int64_t)pr;
+    const float* ap = a.x + arow * a.K + kq;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int pr = beg + min(t * 32 + 16 * h + r, cnt - 1);
-      const int64_t arow = GU ? (int64_t)a.perm_row[pr] : (int64_t)pr;
-      const float* ap = a.x + arow * a.K + kq;
-#pragma unroll
-      for (int g = 0; g < KH; g++) av[h][g] = *reinterpret_cast<const v4f*>(ap + 16 * g);
-    }
+    for (int g = 0; g < KH; g++) dst[g] = *reinterpret_cast<const v4f*>(ap + 16 * g);
   };
-  __shared__ v4f red[MOE_XW][2][NW][64];
-  auto chunk = [&](int t) {
-    v4f acc[2][NW];
+  __shared__ v4f red[MOE_XW][MOE_CT][NW][64];
+  auto chunk = [&](int t, bool first) {
+    const int tiles = min(MOE_CT, (cnt - t * 16 * MOE_CT + 15) / 16);  // block-uniform
+    v4f acc[MOE_CT][NW];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int u = 0; u < MOE_CT; u++)
 #pragma unroll
-      for (int m = 0; m < NW; m++) acc[h][m] = (v4f){0.f, 0.f, 0.f, 0.f};
+      for (int m = 0; m < NW; m++) acc[u][m] = (v4f){0.f, 0.f, 0.f, 0.f};
+    if (!first) load_rows(t, 0, av[0]);
 #pragma unroll
-    for (int g = 0; g < KH; g++)
+    for (int u = 0; u < MOE_CT; u++) {
+      if (u >= tiles) break;
+      v4f(&cur)[KH] = av[NB == 2 ? (u & 1) : 0];
+      if (NB == 2 && u + 1 < tiles) {
+        load_rows(t, u + 1, av[(u + 1) & 1]);  // the next tile's rows behind this tile's products
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-      for (int c = 0; c < 4; c++)
+      for (int g = 0; g < KH; g++)
 #pragma unroll
-        for (int m = 0; m < NW; m++)
+        for (int c = 0; c < 4; c++)
 #pragma unroll
-          for (int h = 0; h < 2; h++)
-            acc[h][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[h][g][c], f[m][g][c], acc[h][m], 0, 0, 0);
+          for (int m = 0; m < NW; m++)
+            acc[u][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[g][c], f[m][g][c], acc[u][m], 0, 0, 0);
+      if (NB == 1 && u + 1 < tiles) load_rows(t, u + 1, av[0]);
+    }
     if (t > 0) __syncthreads();  // the previous chunk's sums have been read
 #pragma unroll
-    for (int h = 0; h < 2; h++)
+    for (int u = 0; u < MOE_CT; u++)
+      if (u < tiles)
 #pragma unroll
-      for (int m = 0; m < NW; m++) red[w][h][m][lane] = acc[h][m];
+        for (int m = 0; m < NW; m++) red[w][u][m][lane] = acc[u][m];
     __syncthreads();
     if (w == t % MOE_XW) {
       // D of a 16x16 block: lane holds output j0 + (lane & 15), pair rows 4q + c
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
+      for (int u = 0; u < MOE_CT; u++) {
+        if (u >= tiles) break;
         v4f sm[NW];
 #pragma unroll
         for (int m = 0; m < NW; m++) {
-          sm[m] = red[0][h][m][lane];
+          sm[m] = red[0][u][m][lane];
 #pragma unroll
-          for (int u = 1; u < MOE_XW; u++) sm[m] += red[u][h][m][lane];
+          for (int v = 1; v < MOE_XW; v++) sm[m] += red[v][u][m][lane];
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-          const int p = t * 32 + 16 * h + 4 * q + c;
+          const int p = t * 16 * MOE_CT + 16 * u + 4 * q + c;
           if (p < cnt) {
             float v = sm[0][c];
             if constexpr (GU) swiglu_eval(sm[0][c], sm[1][c], a.clamp, &v, nullptr, nullptr, 0.f);
@@ -954,20 +970,15 @@ __global__ __launch_bounds__(64 * MOE_XW) void moe_expert_small_kernel(MoeExpert
       }
     }
   };
-  load_rows(0);
+  load_rows(0, 0, av[0]);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int g = JB; g < KH; g++)
 #pragma unroll
     for (int m = 0; m < NW; m++) f[m][g] = *reinterpret_cast<const v4f*>(bw[m] + 16 * g);
   __builtin_amdgcn_sched_barrier(0);
-  chunk(0);
-  for (int t = 1; t < nchunk; t++) {
-    load_rows(t);
-    // every row load in flight before the first product
-    __builtin_amdgcn_sched_barrier(0);
-    chunk(t);
-  }
+  chunk(0, true);
+  for (int t = 1; t < nchunk; t++) chunk(t, false);
 }
 
 bool moe_expert_small_supported(int N, int K) {
