@@ -165,12 +165,12 @@ __global__ __launch_bounds__(256) void mla_decode_prep_kernel(MlaDecodeArgs a) {
 // value is [latent | 0], mla.go:249-259).  Three phases, as the dense decode
 // kernel:
 //  1. scores: each 16-lane quarter-wave takes one key at a time (keys qw,
-//     qw + 16, ... of the split), lane l holds latent float4s l + 16c and
+//     qw + 4 NWV, ... of the split), lane l holds latent float4s l + 16c and
 //     rotary-key float4 l of kv head c (rotary width 64: 16 float4 per kv
 //     head), the next key is fetched while the current one is reduced
 //     (16-lane DPP sums); scores go to LDS;
 //  2. softmax per head over the split (each wave reduces the maximum itself);
-//  3. P.V: wave w takes keys w, w + 4, ...; lane l accumulates latent float4
+//  3. P.V: wave w takes keys w, w + NWV, ...; lane l accumulates latent float4
 //     l for every head (the rows were just read, so they come from L2);
 //     waves are added in LDS.
 // A split covering the whole range writes the normalized latent output,
@@ -193,11 +193,12 @@ __host__ __device__ inline void mla_split(int kstart, int kend, int* kps, int* n
   *nsplit = (n + *kps - 1) / *kps;
 }
 
-template <int NH>
-__global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
+template <int NH, int NWV>
+__global__ __launch_bounds__(64 * NWV) void mla_decode_attn_kernel(MlaDecodeArgs a) {
+  constexpr int NT = 64 * NWV;
   __shared__ float sc[NH][MLA_KPS];
-  __shared__ __attribute__((aligned(16))) float wacc[4][NH][MLA_MAXLAT];
-  __shared__ float wred[4][NH];
+  __shared__ __attribute__((aligned(16))) float wacc[NWV][NH][MLA_MAXLAT];
+  __shared__ float wred[NWV][NH];
   __shared__ float stat[2][NH];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int qw = tid >> 4, l16 = tid & 15;
@@ -242,14 +243,14 @@ __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
       }
     };
     if (qw < nk) fetch(qw);
-    for (int j = qw; j < nk; j += 16) {
+    for (int j = qw; j < nk; j += 4 * NWV) {
       v4f Lc[4], Kc[4];
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         Lc[c] = L[c];
         Kc[c] = K[c];
       }
-      if (j + 16 < nk) fetch(j + 16);
+      if (j + 4 * NWV < nk) fetch(j + 4 * NWV);
 #pragma unroll
       for (int h = 0; h < NH; h++) {
         float t = 0.f;
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
     float ps[NH];
 #pragma unroll
     for (int h = 0; h < NH; h++) ps[h] = 0.f;
-    for (int j = tid; j < nk; j += 256)
+    for (int j = tid; j < nk; j += NT)
 #pragma unroll
       for (int h = 0; h < NH; h++) {
         const float p = expf(sc[h][j] - mx[h]);
@@ -307,7 +308,10 @@ __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
     __syncthreads();
     if (tid < NH) {
       stat[0][tid] = mx[tid];
-      stat[1][tid] = wred[0][tid] + wred[1][tid] + wred[2][tid] + wred[3][tid];
+      float l = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWV; w++) l += wred[w][tid];
+      stat[1][tid] = l;
     }
   }
 
@@ -317,17 +321,17 @@ __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
     v4f acc[NH];
 #pragma unroll
     for (int h = 0; h < NH; h++) acc[h] = (v4f){0.f, 0.f, 0.f, 0.f};
-    constexpr int PV = MLA_KPS / 4;  // keys per wave at most
+    constexpr int PV = (MLA_KPS + NWV - 1) / NWV;  // keys per wave at most
     v4f Lr[PV];
 #pragma unroll
     for (int i = 0; i < PV; i++) {
-      const int j = wid + 4 * i;
+      const int j = wid + NWV * i;
       Lr[i] = (has && j < nk) ? *reinterpret_cast<const v4f*>(lbase + (int64_t)j * a.lat + 4 * lane)
                               : (v4f){0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int i = 0; i < PV; i++) {
-      const int j = wid + 4 * i;
+      const int j = wid + NWV * i;
       if (j < nk)
 #pragma unroll
         for (int h = 0; h < NH; h++) acc[h] += sc[h][j] * Lr[i];
@@ -338,9 +342,11 @@ __global__ __launch_bounds__(256) void mla_decode_attn_kernel(MlaDecodeArgs a) {
   }
   __syncthreads();
   const bool whole = nsplit == 1;
-  for (int i = tid; i < NH * a.lat; i += 256) {
+  for (int i = tid; i < NH * a.lat; i += NT) {
     const int h = i / a.lat, d = i % a.lat;
-    const float o = wacc[0][h][d] + wacc[1][h][d] + wacc[2][h][d] + wacc[3][h][d];
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; w++) o += wacc[w][h][d];
     if (whole) {
       a.out[((int64_t)row * NH + h) * a.lat + d] = o / stat[1][h];
     } else {
@@ -408,13 +414,24 @@ void launch_mla_decode(MlaDecodeArgs a, hipStream_t st) {
   GN_CHECK(a.pos_dev || a.pos < a.maxSeq, "mla decode: position outside the cache");
   const dim3 grid(a.rows, ns_max);
   hipEvent_t stop = ns_max > 1 ? nullptr : a.t_stop;
+  // One split per row at every step (the sliding windows): 8-wave blocks,
+  // twice the loads in flight of the single block per row a CU then holds
+  // (d12 latent, 129 keys: 22.9 vs 25.5 us); several splits: 4-wave blocks,
+  // two per CU (384 keys: 63.4 vs 66.7 us with 8 waves).
 #define GN_MLA_ATTN(H)                                                                        \
   do {                                                                                        \
-    if (a.t_start || stop)                                                                    \
-      hipExtLaunchKernelGGL(mla_decode_attn_kernel<H>, grid, dim3(256), 0, st, a.t_start,    \
-                            stop, 0, a);                                                      \
-    else                                                                                      \
-      hipLaunchKernelGGL(mla_decode_attn_kernel<H>, grid, dim3(256), 0, st, a);               \
+    if (ns_max == 1) {                                                                        \
+      if (a.t_start || stop)                                                                  \
+        hipExtLaunchKernelGGL((mla_decode_attn_kernel<H, 8>), grid, dim3(512), 0, st,        \
+                              a.t_start, stop, 0, a);                                         \
+      else                                                                                    \
+        hipLaunchKernelGGL((mla_decode_attn_kernel<H, 8>), grid, dim3(512), 0, st, a);        \
+    } else if (a.t_start || stop) {                                                           \
+      hipExtLaunchKernelGGL((mla_decode_attn_kernel<H, 4>), grid, dim3(256), 0, st,          \
+                            a.t_start, stop, 0, a);                                           \
+    } else {                                                                                  \
+      hipLaunchKernelGGL((mla_decode_attn_kernel<H, 4>), grid, dim3(256), 0, st, a);          \
+    }                                                                                         \
   } while (0)
   switch (a.Hq) {
     case 1: GN_MLA_ATTN(1); break;
