@@ -67,13 +67,13 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------------------
 // Keys per split: at most DEC_KPS, balanced (300 keys -> 2 x 150), or up to
 // DEC_KPS_WIDE when the (row, kv-head) blocks alone already give two blocks
-// per CU (rows * Hkv >= DEC_WIDE_BLOCKS, plain windows): a 257-512-key window
+// per CU (rows * Hkv >= DEC_WIDE_BLOCKS, plain windows): a 257-528-key window
 // then runs as one block per (row, kv-head) with no combine pass (d12 full
 // layer, 384 keys: 37-40 us against 46.6 us as 2 splits + combine; 512 keys:
 // 49 vs 57 us).  Smaller splits were measured slower: the combine pass they
 // need costs more than the extra workgroups gain.
 static constexpr int DEC_KPS = 256;
-static constexpr int DEC_KPS_WIDE = 512;
+static constexpr int DEC_KPS_WIDE = 528;  // 512-token windows admit 513 keys
 static constexpr int DEC_WIDE_BLOCKS = 512;
 static constexpr int DEC_MAXR = 8;   // max GQA ratio
 static constexpr int DEC_POST_SPLITS = DECODE_POST_MAX_SPLITS;
@@ -406,7 +406,7 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   for (int h = 0; h < R; h++) {
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < DEC_KPS_WIDE / 64; k++)
+    for (int k = 0; k < (DEC_KPS_WIDE + 63) / 64; k++)
       if (64 * k < nk) {  // wave-uniform
         const int j = lane + 64 * k;
         if (j < nk) m = fmaxf(m, sc[h][j]);

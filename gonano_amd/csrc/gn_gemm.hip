@@ -631,7 +631,7 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   // x 4 splits), where 64x64 tiles leave a quarter of the CUs idle.  Their
   // K tiles are 64 deep (half the barriers of 32-deep ones; 128-deep and
   // deeper rings measured no faster).
-  bool narrow = false;
+  int narrow = 0;  // narrow tile width (0: none)
   if (!use_big && !long_k && d.force_splits == 0 && d.N % 96 == 0 && d.a_kcontig && d.b_kcontig) {
     const int64_t nt = ceil_div(d.M, 32) * (d.N / 96);
     double best = 0.0;
@@ -645,8 +645,30 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
       }
     }
     if (best >= 0.9) {
-      narrow = true;
+      narrow = 96;
       splits = bs;
+    }
+  }
+  // 32 x 80 and 32 x 112 tiles (N a multiple of 80 or 112, not of 96) when
+  // the 64 x 64 tiling leaves CUs idle (the d20 decode projections at M =
+  // 512: N = 1280 gives 160 tiles, N = 1792 224).  A product whose split
+  // sums can be deferred takes the split count nearest two workgroups per
+  // CU (wo 31.9 -> 22.5 us, qkv 34.2 -> 29.6 us cold); others stay unsplit
+  // (fc with its ReLU^2 epilogue: 79.5 -> 73.2 us).
+  const bool can_defer = d.defer && ((d.epi == EPI_STORE && d.alpha == 1.f) || d.epi == EPI_ADD_SRC);
+  if (!narrow && !use_big && !long_k && d.force_splits == 0 && d.a_kcontig && d.b_kcontig &&
+      tiles * splits < (9 * cus) / 10) {
+    for (int bn : {80, 112}) {
+      if (d.N % bn) continue;
+      const int64_t nt = ceil_div(d.M, 32) * (d.N / bn);
+      if (nt < cus / 2) continue;
+      int bs = 1;
+      if (can_defer)
+        for (int s = 2; s <= PENDING_MAX_SPLITS && d.K / s >= 512; s++)
+          if (std::llabs(nt * s - 2 * cus) < std::llabs(nt * bs - 2 * cus)) bs = s;
+      narrow = bn;
+      splits = bs;
+      break;
     }
   }
   // k_per_split is a whole number of LDS tiles so that every split but the
@@ -678,8 +700,12 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     launch_cfg<128, 128, 2, 2, 1, 2, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   else if (fold)
     launch_cfg<64, 64, 2, 2, 2, 4, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
-  else if (narrow)  // 64-deep K tiles, two stages (fc 21.3 -> 19.4 us, proj 18.7 -> 17.7 us)
+  else if (narrow == 96)  // 64-deep K tiles, two stages (fc 21.3 -> 19.4 us, proj 18.7 -> 17.7 us)
     launch_cfg_kk<32, 96, 1, 2, 2, 2, 64>(p, vec, splits, st);
+  else if (narrow == 80)
+    launch_cfg_kk<32, 80, 2, 1, 2, 2, 64>(p, vec, splits, st);
+  else if (narrow == 112)
+    launch_cfg_kk<32, 112, 2, 1, 2, 2, 64>(p, vec, splits, st);
   else
     launch_cfg<64, 64, 2, 2, 2, 4, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st);
   if (defer) {

@@ -181,6 +181,15 @@ def test_d12_width_rollout_teacher_forced(orc, d12w):
     _rollout_check(orc, cfg, w, 16, 16, 260, 8, 1.0, groups=(0, 7, 15))
 
 
+def test_d12_width_split_combine_rollout(orc, d12w):
+    """32 rows (2 groups x 16) with 300-token prompts: 64 (row, kv-head)
+    blocks leave the keys in splits of at most 256, so the full-context
+    layer's 301..306 keys take two splits and the combine kernel (the dense
+    multi-split path; the benchmark's 256 and 512 rows run one split)."""
+    cfg, w = d12w
+    _rollout_check(orc, cfg, w, 2, 16, 300, 6, 1.0, groups=(0, 1))
+
+
 def test_d12_width_pg_step_chunked(orc, d12w, monkeypatch):
     cfg, w = d12w
     _pg_check(orc, cfg, w, B=3, T=300, prompt_len=150, chunk=128, monkeypatch=monkeypatch)
@@ -263,9 +272,10 @@ def d20w():
 
 
 def test_d20_width_rollout_teacher_forced(orc, d20w):
-    """512 rows (32 x 16), 520-token prompts, T = 0.8: GQA ratio 5 with two
-    key splits (at most 512 keys each) and the combine on both layers (the
-    512-token window admits 513 keys)."""
+    """512 rows (32 x 16), 520-token prompts, T = 0.8: GQA ratio 5, every
+    window in one split of up to 528 keys (the 512-token window admits 513);
+    the decode projections at M = 512 take the 32 x 80 / 32 x 112 tiles with
+    deferred split sums or run whole on hipBLASLt."""
     cfg, w = d20w
     _rollout_check(orc, cfg, w, 32, 16, 520, 6, 0.8, groups=(0, 31))
 
