@@ -71,6 +71,62 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, int row, int 
   }
 }
 
+// Epilogue of a whole BM x BN tile inside C with the epilogue kind fixed at
+// compile time (E; E == EPI_RELU2_SAVE + 16: ReLU^2 without the saved
+// pre-activation): the same arithmetic as gemm_epilogue, without its
+// per-element bounds check and dispatch, which compile to a branch around
+// every single store.  D of a 16x16 block: lane holds column (lane & 15),
+// rows 4*(lane>>4)+r.
+template <int E, int MI, int NI>
+__device__ __forceinline__ void store_tile(const GemmParams& p, const v4f (&acc)[MI][NI], int r0,
+                                           int c0, int lane) {
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NI; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int row = r0 + i * 16 + 4 * (lane >> 4) + r;
+        const int col = c0 + j * 16 + (lane & 15);
+        const int64_t ci = (int64_t)row * p.ldc + col;
+        const float v = acc[i][j][r];
+        if constexpr (E == EPI_STORE) {
+          p.C[ci] = v * p.alpha;
+        } else if constexpr (E == EPI_ADD_SRC) {
+          p.C[ci] = v + p.aux[(int64_t)row * p.ldaux + col];
+        } else if constexpr (E == EPI_ACCUM) {
+          p.C[ci] += v;
+        } else if constexpr (E == EPI_SOFTCAP) {
+          p.C[ci] = softcap15(v);
+        } else if constexpr (E == EPI_RELU2_SAVE || E == EPI_RELU2_SAVE + 16) {
+          if constexpr (E == EPI_RELU2_SAVE) p.aux_out[(int64_t)row * p.ldaux + col] = v;
+          const float u = v < 0.f ? 0.f : v;
+          p.C[ci] = u * u;
+        } else {
+          static_assert(E == EPI_DRELU2, "epilogue kind");
+          const float u = p.aux[(int64_t)row * p.ldaux + col];
+          p.C[ci] = u > 0.f ? (v * 2.f) * u : 0.f;
+        }
+      }
+}
+
+// Whole-tile epilogue: one dispatch on the (uniform) epilogue kind.
+template <int MI, int NI>
+__device__ __forceinline__ void store_tile_any(const GemmParams& p, const v4f (&acc)[MI][NI],
+                                               int r0, int c0, int lane) {
+  switch (p.epi) {
+    case EPI_STORE: store_tile<EPI_STORE>(p, acc, r0, c0, lane); break;
+    case EPI_ADD_SRC: store_tile<EPI_ADD_SRC>(p, acc, r0, c0, lane); break;
+    case EPI_ACCUM: store_tile<EPI_ACCUM>(p, acc, r0, c0, lane); break;
+    case EPI_SOFTCAP: store_tile<EPI_SOFTCAP>(p, acc, r0, c0, lane); break;
+    case EPI_RELU2_SAVE:
+      if (p.aux_out) store_tile<EPI_RELU2_SAVE>(p, acc, r0, c0, lane);
+      else store_tile<EPI_RELU2_SAVE + 16>(p, acc, r0, c0, lane);
+      break;
+    case EPI_DRELU2: store_tile<EPI_DRELU2>(p, acc, r0, c0, lane); break;
+  }
+}
+
 template <bool VEC>
 __device__ __forceinline__ v4f load4(const float* __restrict__ ptr, int valid) {
   v4f r = {0.f, 0.f, 0.f, 0.f};
@@ -397,6 +453,10 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
   }
   // D of a 16x16 block: lane holds column (lane & 15), rows 4*(lane>>4)+r.
   if (GRP == GEMM_GROUP_K || p.splits == 1) {
+    if (m0 + BM <= p.M && n0 + BN <= p.N) {
+      store_tile_any(p, acc, m0 + wm * TM, n0 + wn * TN, lane);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
@@ -412,6 +472,19 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
   // Split-K: this workgroup's partial sums; gemm_reduce_kernel adds them.
   // (rows mode: p.M is this group's end row; the partial buffer spans all rows)
   float* mine = p.part + (int64_t)split * p0.M * p.N;
+  if (m0 + BM <= p.M && n0 + BN <= p.N) {
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int j = 0; j < NI; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int row = m0 + wm * TM + i * 16 + 4 * (lane >> 4) + r;
+          const int col = n0 + wn * TN + j * 16 + (lane & 15);
+          mine[(int64_t)row * p.N + col] = acc[i][j][r];
+        }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < MI; i++)
 #pragma unroll
