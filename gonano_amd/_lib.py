@@ -173,6 +173,7 @@ _SIGS = {
     "gn_use_calculator": (C.c_int, [C.c_char_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_int32)]),
     "gn_sample_next_token": (C.c_int, [f32p, i64, i64, u64p, C.c_float, i64, i32p]),
     "gn_sample_next_token_static": (C.c_int, [f32p, i64, i64, u64p, C.c_float, i64, i32p]),
+    "gn_softcap_order_check": (C.c_int, [u64p]),
     "gn_session_set_timing": (C.c_int, [vp, C.c_int]),
     "gn_session_get_timing": (C.c_int, [vp, C.POINTER(GnTiming)]),
     "gn_session_synchronize": (C.c_int, [vp]),

@@ -227,6 +227,15 @@ def sample_next_token(logits: np.ndarray, rng_state: np.ndarray, temperature: fl
     return out
 
 
+def softcap_order_violations() -> int:
+    """Neighbouring floats (all 2^32 bit patterns but NaNs, in increasing
+    order) whose device softcap decreases: 0 when it is non-decreasing, which
+    the decode sampler's selection on raw lm_head products relies on."""
+    out = np.zeros(1, np.uint64)
+    call("gn_softcap_order_check", out)
+    return int(out[0])
+
+
 def sample_next_token_static(logits: np.ndarray, rng_state: np.ndarray, temperature: float,
                              top_k: int) -> np.ndarray:
     """sample_next_token through the allocation-free entry point (the

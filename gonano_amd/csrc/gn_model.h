@@ -539,6 +539,10 @@ struct SamplerArgs {
   int softcap = 0;
 };
 void launch_sampler(const SamplerArgs& a, hipStream_t st);
+// Neighbouring floats (in increasing order) whose softcap15 decreases, over
+// all 2^32 bit patterns but NaNs: 0 when softcap15 is non-decreasing, which
+// the sampler's selection on raw lm_head products assumes.
+uint64_t count_softcap_order_violations();
 // Advances the Go PCG state {hi, lo} by n draws (tensors.RNG after n Float32
 // calls, tensors/random.go:66-78).
 void advance_rng_state(uint64_t* state, uint64_t n);

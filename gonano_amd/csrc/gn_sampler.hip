@@ -21,6 +21,16 @@
 // the candidates and their values all come from registers and LDS.
 // If the candidates overflow the LDS buffer (e.g. massively tied logits) the
 // row falls back to an exact 4-pass 8-bit radix select over the whole row.
+//
+// Softcapped rows (the decode path hands over lm_head products y; the logits
+// are softcap15(y)): softcap15 is non-decreasing over every float (checked
+// exhaustively on the device by count_softcap_order_violations), so the
+// k-th largest logit is softcap15 of the k-th largest product, and steps 1-2
+// run on the raw products; only the candidates are softcapped.  Entries
+// below the bound L are dropped, which is exact when softcap15 of the float
+// below L is under the threshold (no dropped entry can tie it); otherwise
+// (a flat, saturated softcap across L) the row takes the radix select.
+// This keeps the tanh off all but a few hundred entries of a row.
 #include "gn_model.h"
 
 namespace gn {
@@ -47,20 +57,36 @@ __device__ __forceinline__ u128 pcg_mul() { return {0x2360ED051FC65DA4ull, 0x438
 __device__ __forceinline__ u128 pcg_inc() { return {6364136223846793005ull, 1442695040888963407ull}; }
 __device__ __forceinline__ u128 pcg_step(u128 s) { return add128(mul128(s, pcg_mul()), pcg_inc()); }
 
-// state after n further LCG steps
-__device__ u128 pcg_advance(u128 s, uint64_t n) {
-  u128 cm = pcg_mul(), cp = pcg_inc();
-  u128 am = {0, 1}, ap = {0, 0};
-  while (n) {
-    if (n & 1) {
-      am = mul128(am, cm);
-      ap = add128(mul128(ap, cm), cp);
-    }
-    cp = mul128(add128(cm, u128{0, 1}), cp);
-    cm = mul128(cm, cm);
-    n >>= 1;
+// Jumps of 2^j LCG steps (j = 0..63) as affine maps s -> a s + c, built at
+// compile time: f^(2^(j+1)) = f^(2^j) o f^(2^j), i.e. a' = a^2, c' = a c + c.
+struct PcgJump {
+  uint64_t ahi, alo, chi, clo;
+};
+struct PcgJumps {
+  PcgJump j[64];
+};
+constexpr PcgJumps make_pcg_jumps() {
+  PcgJumps t{};
+  unsigned __int128 a = ((unsigned __int128)0x2360ED051FC65DA4ull << 64) | 0x4385DF649FCCF645ull;
+  unsigned __int128 c = ((unsigned __int128)6364136223846793005ull << 64) | 1442695040888963407ull;
+  for (int i = 0; i < 64; i++) {
+    t.j[i] = {(uint64_t)(a >> 64), (uint64_t)a, (uint64_t)(c >> 64), (uint64_t)c};
+    c = a * c + c;
+    a = a * a;
   }
-  return add128(mul128(am, s), ap);
+  return t;
+}
+__constant__ PcgJumps kPcgJumps = make_pcg_jumps();
+
+// State after n further LCG steps: the jumps of n's set bits (powers of one
+// map commute), one 128-bit multiply-add per set bit.
+__device__ u128 pcg_advance(u128 s, uint64_t n) {
+  for (int j = 0; n; j++, n >>= 1)
+    if (n & 1) {
+      const PcgJump& J = kPcgJumps.j[j];
+      s = add128(mul128(u128{J.ahi, J.alo}, s), u128{J.chi, J.clo});
+    }
+  return s;
 }
 
 // DXSM permutation of the (post-step) state -> Uint64 -> Float32.
@@ -165,12 +191,18 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
     // the row in registers: float4 c = tid + u * NT of thread tid, requested
     // before the stream jump below so the two overlap
     const bool inreg = masking && vec && V4 <= REGV * NT;
+    int ngroups = NT;  // a power of two >= 4k (at most MAXG)
+    while (ngroups < MAXG && ngroups < 4 * k) ngroups <<= 1;
+    const bool fast = inreg && ngroups == NT;  // k <= 256: one group per thread
+    // raw: the registers hold the products y and the selection runs on them
+    const bool raw = fast && sc;
     v4f zr[REGV];
     if (inreg) {
 #pragma unroll
       for (int u = 0; u < REGV; u++) {
         const int c = tid + u * NT;
-        zr[u] = c < V4 ? zl4(z4[c]) : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        zr[u] = c < V4 ? (raw ? z4[c] : zl4(z4[c]))
+                       : (v4f){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
       }
     }
     if (tid == 0) {
@@ -198,9 +230,6 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
       //    (each of the k groups holds a value >= it).  The groups are
       //    strided (entry v belongs to group v mod ngroups) so the pass
       //    reads the row with coalesced loads.
-      int ngroups = NT;  // a power of two >= 4k (at most MAXG)
-      while (ngroups < MAXG && ngroups < 4 * k) ngroups <<= 1;
-      const bool fast = inreg && ngroups == NT;  // k <= 256: one group per thread
       float lower;
       if (fast) {
         // One group per thread (its 64 registers).  Each of the 16 waves
@@ -266,7 +295,7 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
           const int slot = atomicAdd(&ncand, 1);
           if (slot < MAXC) {
             cand_i[slot] = v;
-            cand_v[slot] = zv;
+            cand_v[slot] = raw ? softcap15(zv) : zv;
           }
         }
       };
@@ -293,8 +322,9 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
       }
       __syncthreads();
       const int nc = ncand;
-      float thr;
-      if (nc <= MAXC) {
+      float thr = 0.f;
+      bool small = nc <= MAXC;
+      if (small) {
         if (fast) {
           // the k-th largest candidate value: the one with fewer than k
           // candidates above it and at least k at or above it (all such
@@ -320,6 +350,11 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
           thr = buf[k - 1];
           __syncthreads();
         }
+        // Raw selection: every entry below the bound must stay below the
+        // threshold (thr and lower are the same in every thread).
+        if (raw && !(softcap15(nextafterf(lower, -INFINITY)) < thr)) small = false;
+      }
+      if (small) {
         // 3) Gumbel-max over the survivors, in index order per thread
         for (int i = tid; i < nc; i += NT) {
           const int v = cand_i[i];
@@ -383,6 +418,49 @@ __global__ __launch_bounds__(NT) void sampler_kernel(SamplerArgs a) {
     for (int w = 1; w < NT / 64; w++) better(bv, bi, best_v[w], best_i[w]);
     a.out[row] = bi < 0 ? 0 : bi;
   }
+}
+
+// Order check of softcap15 over every float, which the raw selection above
+// relies on: the floats are walked in increasing order (key k holds
+// key_float(k)), each thread a contiguous run of keys overlapping the next
+// run by one, and every neighbour pair whose softcap decreases (or is NaN
+// for a non-NaN input) is counted.  NaN bit patterns are skipped.
+__global__ __launch_bounds__(256) void softcap_order_kernel(unsigned long long* bad) {
+  const uint64_t nthreads = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t total = 1ull << 32;
+  const uint64_t per = (total + nthreads - 1) / nthreads;
+  const uint64_t k0 = t * per, k1 = k0 + per + 1 < total ? k0 + per + 1 : total;
+  unsigned long long n = 0;
+  float prev = 0.f;
+  bool have = false;
+  for (uint64_t k = k0; k < k1; k++) {
+    const float x = key_float((uint32_t)k);
+    if (x != x) {
+      have = false;
+      continue;
+    }
+    const float y = softcap15(x);
+    if (y != y || (have && y < prev)) n++;
+    prev = y;
+    have = true;
+  }
+  if (n) atomicAdd(bad, n);
+}
+
+uint64_t count_softcap_order_violations() {
+  unsigned long long* bad = nullptr;
+  GN_HIP(hipMalloc(&bad, sizeof(unsigned long long)));
+  unsigned long long h = 0;
+  hipError_t e = hipMemset(bad, 0, sizeof(h));
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(softcap_order_kernel, dim3(1024), dim3(256), 0, 0, bad);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(&h, bad, sizeof(h), hipMemcpyDeviceToHost);
+  (void)hipFree(bad);
+  GN_HIP(e);
+  return h;
 }
 
 void launch_sampler(const SamplerArgs& a, hipStream_t st) {

@@ -3038,6 +3038,13 @@ int gn_sample_next_token(const float* logits, int64_t rows, int64_t vocab, uint6
   });
 }
 
+int gn_softcap_order_check(uint64_t* violations) {
+  return guard([&] {
+    GN_CHECK(violations, "null argument");
+    *violations = count_softcap_order_violations();
+  });
+}
+
 int gn_session_set_timing(gn_session* s, int enabled) {
   return guard([&] {
     GN_CHECK(s, "null session");

@@ -367,6 +367,15 @@ int gn_sample_next_token_static(const float *logits, int64_t rows, int64_t vocab
                                 uint64_t *rng_state, float temperature, int64_t top_k,
                                 int32_t *out);
 
+/* Self-check of the decode sampler's softcap handling.  No counterpart in the
+ * reference: the decode sampler selects the top-k candidates on the raw
+ * lm_head products and softcaps only the candidates, which equals softcapping
+ * every logit first when softcap (15 tanh(y/15), transformer.go:538-541) is
+ * non-decreasing over floats.  *violations = the number of neighbouring
+ * floats, over all 2^32 bit patterns but NaNs, whose softcap decreases (or
+ * is NaN) as computed on the device; 0 confirms the assumption. */
+int gn_softcap_order_check(uint64_t *violations);
+
 /* Device time (ms) the session spent in its most recent calls, by phase, and
  * the average duration of the named kernel class measured with HIP events on
  * the session stream.  Enabled by gn_session_set_timing(session, 1). */

@@ -189,6 +189,55 @@ def test_generate_teacher_forced(small, orc):
                 assert group[i][P + t] == want[i], (g, i, t)
 
 
+def test_softcap_non_decreasing_over_all_floats():
+    """The decode sampler picks its top-k candidates on the raw lm_head
+    products and softcaps only those, which equals softcapping every logit
+    first because the device softcap is non-decreasing over all floats:
+    checked exhaustively, every neighbouring pair of the 2^32 bit patterns
+    but NaNs."""
+    from gonano_amd.backend import softcap_order_violations
+    assert softcap_order_violations() == 0
+
+
+def test_generate_saturated_softcap_teacher_forced(orc):
+    """lm_head scaled by 1e9: nearly every logit softcaps to exactly +-15, so
+    the sampler's selection on raw products cannot prove its bound (softcap
+    is flat across it) and every row takes the exact radix select over the
+    softcapped row, with thousands of tied logits kept; the tokens still
+    match the oracle's.  (At this scale no product falls in the band where
+    float32 and float64 tanh round to different sides of 15.)"""
+    from gonano_amd.session import Session
+    cfg = small_cfg()
+    w = G.init_weights(cfg, seed=11, perturb=0.1).copy()
+    (name, r, c, off), = [e for e in cfg.param_table() if e[0] == "lm_head.weight"]
+    w[off:off + r * c] *= 1e9
+    G_, P, S, N = 2, 20, 4, 6
+    prompts = np.random.default_rng(5).integers(0, cfg.vocab_size, (G_, P)).astype(np.int32)
+    seeds = np.array([3, 99], np.uint64)
+    with Session(cfg) as s:
+        s.set_params(w)
+        rows = s.generate_batch(prompts, S, N, 1.0, 50, seeds)
+    m = orc.OracleModel(shape_of(cfg), w)
+    checked = 0
+    for g in range(G_):
+        rng = orc.GoRNG(int(seeds[g]))
+        group = rows[g * S:(g + 1) * S]
+        for t in range(N):
+            live = [i for i in range(S) if len(group[i]) > P + t]
+            if not live:
+                break
+            ctx = np.stack([np.concatenate([r[:P + t], np.zeros(max(0, P + t - len(r)), np.int32)])
+                            for r in group])[:, :P + t]
+            z = m.forward(ctx)[:, -1, :] if t > 0 else np.repeat(m.forward(prompts[g:g + 1])[:, -1, :], S, 0)
+            z = z.astype(np.float32)
+            assert (np.abs(z) == 15.0).mean() > 0.9
+            want = orc.sample_next_token(z, rng, 1.0, 50)
+            for i in live:
+                assert group[i][P + t] == want[i], (g, i, t)
+                checked += 1
+    assert checked >= G_ * S
+
+
 def test_decode_graph_replays_match_eager(small):
     """Rollouts replayed from the captured decode graph equal the eager ones
     token for token, across repeated calls (a fresh capture per call, with
