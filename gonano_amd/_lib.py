@@ -189,6 +189,9 @@ _SIGS = {
     "gn_optimizer_step": (C.c_int, [vp]),
     "gn_optimizer_state_size": (C.c_int, [vp, C.POINTER(C.c_int64)]),
     "gn_optimizer_get_state": (C.c_int, [vp, f32p, i64]),
+    "gn_optimizer_set_hyper": (C.c_int, [vp, vp, vp, vp, C.c_int32]),
+    "gn_session_update_router_bias": (C.c_int, [vp, C.c_float]),
+    "gn_session_moe_loads": (C.c_int, [vp, C.POINTER(C.c_double), i64]),
     "gn_optimizer_destroy": (C.c_int, [vp]),
 }
 

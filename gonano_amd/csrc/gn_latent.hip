@@ -787,6 +787,37 @@ __global__ __launch_bounds__(MOE_PB) void moe_route_small_kernel(MoePlaceArgs a,
   }
 }
 
+__global__ __launch_bounds__(MOE_MAXE) void moe_load_accum_kernel(const int* off, int E,
+                                                                   double* load) {
+  const int e = threadIdx.x;
+  if (e < E) load[e] += (double)(off[e + 1] - off[e]);
+}
+void launch_moe_load_accum(const int* off, int E, double* load, hipStream_t st) {
+  GN_CHECK(E >= 1 && E <= MOE_MAXE, "moe: at most 64 experts");
+  hipLaunchKernelGGL(moe_load_accum_kernel, dim3(1), dim3(MOE_MAXE), 0, st, off, E, load);
+  GN_HIP(hipGetLastError());
+}
+
+// The counts are whole numbers (exact in float64), so the total and the mean
+// do not depend on the order of the additions.
+__global__ __launch_bounds__(MOE_MAXE) void moe_bias_update_kernel(double* load, float* bias,
+                                                                   int E, float speed) {
+  const int e = threadIdx.x;
+  double total = 0.0;
+  for (int i = 0; i < E; i++) total += load[i];
+  __syncthreads();  // every thread has read the counts before they are cleared
+  if (total <= 0.0 || e >= E) return;
+  const double diff = total / (double)E - load[e];
+  const float sign = diff > 0.0 ? 1.f : diff < 0.0 ? -1.f : 0.f;
+  bias[e] += speed * sign;
+  load[e] = 0.0;
+}
+void launch_moe_bias_update(double* load, float* bias, int E, float speed, hipStream_t st) {
+  GN_CHECK(E >= 1 && E <= MOE_MAXE, "moe: at most 64 experts");
+  hipLaunchKernelGGL(moe_bias_update_kernel, dim3(1), dim3(MOE_MAXE), 0, st, load, bias, E, speed);
+  GN_HIP(hipGetLastError());
+}
+
 void launch_moe_route(const MoeRouteArgs& a, hipStream_t st) {
   GN_CHECK(a.E <= MOE_MAXE && a.K <= MOE_MAXK && a.K <= a.E, "moe: at most 64 experts, top-8");
   GN_CHECK(a.C % 4 == 0, "moe: model width must be a multiple of 4");

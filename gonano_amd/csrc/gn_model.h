@@ -308,6 +308,13 @@ struct MoeRouteArgs {
   const float* wr = nullptr;  // [E, C] router weights: logits computed from x in the gate kernel
 };
 void launch_moe_route(const MoeRouteArgs& a, hipStream_t st);
+// MoE.forwardTraining's load counts (moe.go:192-193): load[e] += the tokens
+// the routing placed with expert e (off[e + 1] - off[e]).
+void launch_moe_load_accum(const int* off, int E, double* load, hipStream_t st);
+// MoE.updateRouterBias (moe.go:330-341): bias[e] += speed * sign(mean - load[e])
+// over one layer's counts, which are then cleared; no change while no token
+// was counted.
+void launch_moe_bias_update(double* load, float* bias, int E, float speed, hipStream_t st);
 struct MoePlaceArgs {
   const int32_t* sel;
   const float* w;
@@ -489,6 +496,10 @@ struct CsaSelectArgs {
   int* pool_out;          // Full with pool > 1: candidates published, or null
   int* npool_out;
   int groups_cap, wave_floats;  // set by the launcher
+  // 0: one block of 8 waves per row when the rows are few (decode), one wave
+  // per row otherwise; 1: one wave per row; 2: one block per row where the
+  // shapes allow.  Same selection either way.
+  int mode;
 };
 void launch_csa_select(CsaSelectArgs a, hipStream_t st);
 

@@ -104,6 +104,11 @@ struct gn_session {
   float clamp = 0.f, mscale = 1.f, bw = 0.f;
   bool derived_dirty = true;
   float* derived = nullptr;
+  // MoE.loadCounts of every layer ([L][E], float64; moe.go:41-43): tokens
+  // routed to each expert by the training forwards since the last
+  // UpdateRouterBias
+  double* moe_load = nullptr;
+  int csa_select_mode = 0;  // CsaSelectArgs::mode
   // flash preset: compressed attention (ratio > 1) with a local window
   bool hca = false;
   int ratio = 1, swa = 0;
@@ -528,6 +533,10 @@ static void build_session(gn_session* s, const gn_config& cfg) {
   GN_HIP(hipMalloc(&s->grads, sizeof(float) * cur));
   GN_HIP(hipMemsetAsync(s->params, 0, sizeof(float) * cur, s->stream));
   GN_HIP(hipMemsetAsync(s->grads, 0, sizeof(float) * cur, s->stream));
+  if (s->moe) {
+    GN_HIP(hipMalloc(&s->moe_load, sizeof(double) * s->L * s->E));
+    GN_HIP(hipMemsetAsync(s->moe_load, 0, sizeof(double) * s->L * s->E, s->stream));
+  }
   auto P = [&](int64_t o) { return o >= 0 ? s->params + o : nullptr; };
   auto G = [&](int64_t o) { return o >= 0 ? s->grads + o : nullptr; };
   for (int l = 0; l < s->L; l++) {
@@ -700,7 +709,7 @@ static MoeBuffers moe_buffers(gn_session* s, const std::string& pre, int64_t row
 // no gathered rows, no pre-activations kept) when the shapes allow.
 static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, const float* h2,
                             int64_t rows, float* gu, float* act, const MoeBuffers& m,
-                            float* xout, bool small = false) {
+                            float* xout, bool small = false, double* load = nullptr) {
   const int C = s->C, F = s->F, E = s->E, EH = s->EH;
   const int64_t NK = rows * s->K;
   hipStream_t st = s->stream;
@@ -723,6 +732,7 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
   ra.xg = stream_experts ? nullptr : m.xg;
   if (small) ra.wr = ly.wr;
   launch_moe_route(ra, st);
+  if (load) launch_moe_load_accum(m.off, E, load, st);  // moe.go:192-193
   GemmDesc dg = linear_fwd_desc(h2, ly.wgu, gu, (int)rows, C, 2 * F);
   if (small) dg.defer = &gsum;
   sgemm(s, dg);
@@ -822,6 +832,7 @@ static void csa_select_layer(gn_session* s, SeqBuffers& sb, const Layer& ly, int
     ca.pool_in = within ? sb.pool[p] : nullptr;
     ca.npool_in = within ? sb.npool[p] : nullptr;
     ca.sel = sel; ca.nsel = nsel; ca.pool_out = pool; ca.npool_out = npool;
+    ca.mode = s->csa_select_mode;
     launch_csa_select(ca, st);
   }
   sb.iq[l] = iq; sb.ik[l] = ik;
@@ -1083,7 +1094,9 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
       float* gu = layer_buf(s, "gu", l, save, N * 2 * F);
       float* act = layer_buf(s, "act", l, save, N * F);
       MoeBuffers mb = moe_buffers(s, save ? "moe" + std::to_string(l) + "_" : "moe*_", N);
-      moe_ffn_forward(s, ly, mid, h2, N, gu, act, mb, xout);
+      // training forwards count the routed tokens (MoE.forwardTraining)
+      moe_ffn_forward(s, ly, mid, h2, N, gu, act, mb, xout, false,
+                      save ? s->moe_load + (int64_t)l * s->E : nullptr);
       sb.gu[l] = gu; sb.act[l] = act; sb.moe[l] = mb;
       if (l == bk) {
         sb.backout = A<float>(s, "backout", N * C);
@@ -1929,6 +1942,7 @@ static void hca_decode_layer(gn_session* s, const Layer& ly, int l, int rows, in
     }
     ca.sel = s->dsel + (int64_t)l * sstride * s->topk;
     ca.nsel = s->dnsel + (int64_t)l * sstride;
+    ca.mode = s->csa_select_mode;
     launch_csa_select(ca, st);
   }
   da.sel = s->dsel + (int64_t)q * sstride * s->topk;
@@ -2745,6 +2759,9 @@ int gn_session_create(const gn_config* config, int device, gn_session** out) {
       if (!lt || std::strcmp(lt, "0") != 0) s->lt.reset(blaslt_create());
       const char* fp = std::getenv("GN_FUSE_QKV_POST");
       s->fuse_qkv_post = !fp || std::strcmp(fp, "0") != 0;
+      // GN_CSA_SELECT=wave / block forces one selection kernel (tests)
+      if (const char* cs = std::getenv("GN_CSA_SELECT"))
+        s->csa_select_mode = !std::strcmp(cs, "wave") ? 1 : !std::strcmp(cs, "block") ? 2 : 0;
     } catch (...) {  // a rejected config or a failed allocation frees what was made
       if (s->stream) (void)gn_session_destroy(s);
       else delete s;
@@ -2770,6 +2787,7 @@ int gn_session_destroy(gn_session* s) {
     (void)hipFree(s->cosT);
     (void)hipFree(s->sinT);
     if (s->derived) (void)hipFree(s->derived);
+    if (s->moe_load) (void)hipFree(s->moe_load);
     (void)hipStreamDestroy(s->stream);
     delete s;
   });
@@ -2839,6 +2857,31 @@ int gn_session_zero_grads(gn_session* s) {
     GN_HIP(hipSetDevice(s->device));
     for (const ParamEntry& e : s->table)
       GN_HIP(hipMemsetAsync(e.grad, 0, sizeof(float) * e.rows * e.cols, s->stream));
+    GN_HIP(hipStreamSynchronize(s->stream));
+  });
+}
+
+int gn_session_update_router_bias(gn_session* s, float speed) {
+  return guard([&] {
+    GN_CHECK(s, "null session");
+    if (!s->moe) return;  // Transformer.UpdateRouterBias: no MoE, nothing to do
+    GN_HIP(hipSetDevice(s->device));
+    for (int l = 0; l < s->L; l++)
+      launch_moe_bias_update(s->moe_load + (int64_t)l * s->E, s->layers[l].rbias, s->E, speed,
+                             s->stream);
+    GN_HIP(hipStreamSynchronize(s->stream));
+    s->derived_dirty = true;
+    pc_clear(s);  // stored prefills were routed with the old bias
+  });
+}
+int gn_session_moe_loads(const gn_session* s, double* loads, int64_t count) {
+  return guard([&] {
+    GN_CHECK(s && loads, "null argument");
+    GN_CHECK(count == (s->moe ? (int64_t)s->L * s->E : 0), "moe loads: count must be layers x experts");
+    if (!s->moe) return;
+    GN_HIP(hipSetDevice(s->device));
+    GN_HIP(hipMemcpyAsync(loads, s->moe_load, sizeof(double) * count, hipMemcpyDeviceToHost,
+                          s->stream));
     GN_HIP(hipStreamSynchronize(s->stream));
   });
 }
@@ -3186,6 +3229,19 @@ int gn_optimizer_step(gn_optimizer* o) {
     GN_HIP(hipStreamSynchronize(s->stream));
     s->derived_dirty = true;  // absorbed decode weights follow the parameters
     pc_clear(s);              // and stored prefills are stale
+  });
+}
+int gn_optimizer_set_hyper(gn_optimizer* o, const float* lr, const float* momentum,
+                           const float* weight_decay, int32_t count) {
+  return guard([&] {
+    GN_CHECK(o, "null optimizer");
+    GN_CHECK(count == (int32_t)o->ts.size(), "optimizer: one value per table entry");
+    for (int32_t i = 0; i < count; i++) {
+      gn_opt_param& h = o->ts[i].h;
+      if (lr) h.lr = lr[i];
+      if (momentum) h.momentum = momentum[i];
+      if (weight_decay) h.weight_decay = weight_decay[i];
+    }
   });
 }
 int gn_optimizer_state_size(const gn_optimizer* o, int64_t* count) {

@@ -384,16 +384,196 @@ __global__ __launch_bounds__(256) void csa_select_kernel(CsaSelectArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Selection for few rows (decode): one block of CSB_NW waves per row.  The
+// rank counts of every top-k stage are split over the block's waves (each
+// wave counts, for every value, the values of its own share of the list that
+// outrank it; the shares are added in LDS), so a row's selection takes a
+// fraction of the serial passes of one wave.  Same strict order (rank_key)
+// as the wave kernel, so the same selection.
+// ---------------------------------------------------------------------------
+static constexpr int CSB_NW = 8, CSB_NT = 64 * CSB_NW, CSB_MAXN = 512;
+// rows up to which the block kernel is chosen (fewer rows than CUs: the
+// one-wave-per-row grid would leave most of the chip idle)
+static constexpr int64_t CSB_ROWS = 128;
+
+// n <= CSB_MAXN values in LDS (NaN never outranks): the best `count` into
+// out[] in rank order; rk[] holds n rank counts.  Called by the whole block;
+// returns min(count, #non-NaN) and ends with out[] visible to every thread.
+template <int M>
+__device__ int block_topk_rank(const float* vals, int n, int count, int* out, int* rk,
+                               int* nvalid) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  for (int i = tid; i < n; i += CSB_NT) rk[i] = 0;
+  __syncthreads();
+  uint64_t key[M];
+  int r[M];
+#pragma unroll
+  for (int m = 0; m < M; m++) {
+    const int i = lane + 64 * m;
+    key[m] = i < n ? rank_key(vals[i], i) : 0;
+    r[m] = 0;
+  }
+  const int per = (n + CSB_NW - 1) / CSB_NW, j0 = wid * per, j1 = min(n, j0 + per);
+#pragma unroll 4
+  for (int j = j0; j < j1; j++) {
+    const uint64_t kj = rank_key(vals[j], j);
+#pragma unroll
+    for (int m = 0; m < M; m++) r[m] += kj > key[m];
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++)
+    if (lane + 64 * m < n && r[m] > 0) atomicAdd(&rk[lane + 64 * m], r[m]);
+  if (wid == 0) {
+    int mine = 0;
+#pragma unroll
+    for (int m = 0; m < M; m++) mine += key[m] != 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mine += __shfl_xor(mine, o, 64);
+    if (lane == 0) *nvalid = mine;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += CSB_NT)
+    if (rank_key(vals[i], i) != 0 && rk[i] < count) out[rk[i]] = i;
+  const int valid = *nvalid;
+  __syncthreads();
+  return min(count, valid);
+}
+__device__ int block_topk(const float* vals, int n, int count, int* out, int* rk, int* nvalid) {
+  switch ((n + 63) / 64) {
+    case 0:
+    case 1: return block_topk_rank<1>(vals, n, count, out, rk, nvalid);
+    case 2: return block_topk_rank<2>(vals, n, count, out, rk, nvalid);
+    case 3: return block_topk_rank<3>(vals, n, count, out, rk, nvalid);
+    case 4: return block_topk_rank<4>(vals, n, count, out, rk, nvalid);
+    case 5: return block_topk_rank<5>(vals, n, count, out, rk, nvalid);
+    case 6: return block_topk_rank<6>(vals, n, count, out, rk, nvalid);
+    case 7: return block_topk_rank<7>(vals, n, count, out, rk, nvalid);
+    default: return block_topk_rank<8>(vals, n, count, out, rk, nvalid);
+  }
+}
+
+// Wave 0 lists the allowed entries of a candidate list in order into cand[]
+// (compaction by ballot); returns the count to every thread.
+template <typename F>
+__device__ int block_compact(int total, F entry, int allowed, int* cand, int* ncand) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 64) {
+    int nc = 0;
+    for (int i0 = 0; i0 < total; i0 += 64) {
+      const int i = i0 + lane;
+      const int e = i < total ? entry(i) : -1;
+      const bool ok = e >= 0 && e < allowed;
+      const uint64_t m = __ballot(ok);
+      if (ok) cand[nc + __popcll(m & ((1ull << lane) - 1))] = e;
+      nc += __popcll(m);
+    }
+    if (lane == 0) *ncand = nc;
+  }
+  __syncthreads();
+  return *ncand;
+}
+
+__global__ __launch_bounds__(CSB_NT) void csa_select_block_kernel(CsaSelectArgs a) {
+  extern __shared__ float sm[];
+  __shared__ int nvalid, ncand;
+  const CsaShape& sh = a.shape;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t row = blockIdx.x;  // chunk row (z, t)
+  const int z = (int)(row / sh.T), t = (int)(row % sh.T);
+  const int64_t grow = ((int64_t)(sh.b0 * sh.Hkv) + z) * sh.T + t;  // global row
+  float* vals = sm;                                         // groups or candidate scores
+  int* cand = reinterpret_cast<int*>(vals + a.groups_cap);  // ccap entries
+  int* rank = cand + a.ccap;                                // max(gpt, K) + 1
+  int* rk = rank + std::max(a.gpt, a.K) + 1;                // CSB_MAXN rank counts
+  const float* score = a.scores + ((int64_t)z * sh.T + t) * sh.ldo;
+  const int allowed = allowed_blocks(t, sh);
+  int* sel = a.sel + grow * a.K;
+  if (allowed <= 0 || a.K <= 0) {  // block-uniform
+    if (tid == 0) {
+      a.nsel[grow] = 0;
+      if (a.npool_out) a.npool_out[grow] = 0;
+    }
+    return;
+  }
+  int nc;
+  if (a.pool_in) {  // Reindex: the fine stage within the producer's pool
+    const int* pl = a.pool_in + grow * a.ccap;
+    nc = block_compact(a.npool_in[grow], [&](int i) { return pl[i]; }, allowed, cand, &ncand);
+  } else if (a.pool == 1 && a.gpt >= a.K) {
+    // flat: the top-K of the top-budget entries are the top-K entries
+    for (int j = tid; j < allowed; j += CSB_NT) vals[j] = score[j];
+    __syncthreads();
+    const int n = block_topk(vals, allowed, a.K, rank, rk, &nvalid);
+    for (int i = tid; i < n; i += CSB_NT) sel[i] = rank[i];
+    if (tid == 0) a.nsel[grow] = n;
+    return;
+  } else {
+    const int ag = (allowed + a.pool - 1) / a.pool;
+    if (a.pool <= 64 && (a.pool & (a.pool - 1)) == 0) {
+      // IndexerBlockMax, coalesced: a wave takes 256-entry stretches, lane j
+      // of a stretch reads entry j, a group is `pool` adjacent lanes
+      for (int j0 = 256 * wid; j0 < allowed; j0 += 256 * CSB_NW) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int j = j0 + 64 * u + lane;
+          v[u] = j < allowed ? score[j] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int j = j0 + 64 * u + lane;
+          for (int o = 1; o < a.pool; o <<= 1) v[u] = fmaxf(v[u], __shfl_xor(v[u], o, 64));
+          if ((lane & (a.pool - 1)) == 0 && j < allowed) vals[j / a.pool] = v[u];
+        }
+      }
+    } else {
+      for (int g = tid; g < ag; g += CSB_NT) {  // IndexerBlockMax over the allowed entries
+        const int st = g * a.pool, en = min(st + a.pool, allowed);
+        float mx = -INFINITY;
+        for (int e = st; e < en; e++) mx = fmaxf(mx, score[e]);
+        vals[g] = mx;
+      }
+    }
+    __syncthreads();
+    const int ng = block_topk(vals, ag, a.gpt, rank, rk, &nvalid);
+    const int pool = a.pool;
+    nc = block_compact(ng * pool, [&](int i) { return rank[i / pool] * pool + i % pool; },
+                       allowed, cand, &ncand);
+  }
+  if (a.pool_out) {
+    int* po = a.pool_out + grow * a.ccap;
+    for (int i = tid; i < nc; i += CSB_NT) po[i] = cand[i];
+    if (tid == 0) a.npool_out[grow] = nc;
+  }
+  for (int i = tid; i < nc; i += CSB_NT) vals[i] = score[cand[i]];
+  __syncthreads();
+  const int n = block_topk(vals, nc, a.K, rank, rk, &nvalid);
+  for (int i = tid; i < n; i += CSB_NT) sel[i] = cand[rank[i]];
+  if (tid == 0) a.nsel[grow] = n;
+}
+
 void launch_csa_select(CsaSelectArgs a, hipStream_t st) {
   const CsaShape& s = a.shape;
   GN_CHECK(a.pool >= 1 && a.gpt >= 1 && a.K >= 1, "csa select: bad pool / budget / top-k");
   GN_CHECK(a.gpt * a.pool <= a.ccap && a.K <= a.ccap, "csa select: candidate capacity too small");
+  GN_CHECK(a.mode >= 0 && a.mode <= 2, "csa select: bad mode");
   a.groups_cap = std::max<int>((s.blocks + a.pool - 1) / a.pool, a.ccap);
+  const int64_t nrows = (int64_t)a.chunk_seqs * s.Hkv * s.T;
+  // the block kernel ranks lists of at most CSB_MAXN values: the groups (or,
+  // flat, the entries) and the candidates
+  const bool block_fits = a.groups_cap <= CSB_MAXN && a.ccap <= CSB_MAXN;
+  if (block_fits && (a.mode == 2 || (a.mode == 0 && nrows <= CSB_ROWS))) {
+    const size_t lds = sizeof(float) * ((size_t)a.groups_cap + a.ccap + std::max(a.gpt, a.K) + 1 +
+                                        CSB_MAXN);
+    hipLaunchKernelGGL(csa_select_block_kernel, dim3((unsigned)nrows), dim3(CSB_NT), lds, st, a);
+    GN_HIP(hipGetLastError());
+    return;
+  }
   a.wave_floats = a.groups_cap + a.ccap + std::max(a.gpt, a.K) + 1;
   const size_t lds = sizeof(float) * 4 * (size_t)a.wave_floats;
   GN_CHECK(lds <= 160 * 1024, "csa select: too many compressed blocks for one row in LDS");
-  const int64_t rows = (int64_t)a.chunk_seqs * s.Hkv * s.T;
-  hipLaunchKernelGGL(csa_select_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), lds, st, a);
+  hipLaunchKernelGGL(csa_select_kernel, dim3((unsigned)ceil_div(nrows, 4)), dim3(256), lds, st, a);
   GN_HIP(hipGetLastError());
 }
 

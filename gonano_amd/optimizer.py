@@ -192,6 +192,19 @@ class Optimizer:
         """MuonAdamW.Step (optimizer/optimizer.go:118-137)."""
         call("gn_optimizer_step", self._h)
 
+    def set_hyper(self, lr=None, momentum=None, weight_decay=None):
+        """Per-entry LR / Momentum / WeightDecay (table order); None keeps a
+        field as it is."""
+        arrs = []
+        for v in (lr, momentum, weight_decay):
+            arrs.append(None if v is None else np.ascontiguousarray(
+                np.broadcast_to(np.asarray(v, np.float32), (len(self.table),))))
+        ptr = [None if a is None else a.ctypes.data_as(C.c_void_p) for a in arrs]
+        call("gn_optimizer_set_hyper", self._h, ptr[0], ptr[1], ptr[2], len(self.table))
+        for name, a in zip(("lr", "momentum", "weight_decay"), arrs):
+            if a is not None:
+                self.table[name] = a
+
     def state(self) -> np.ndarray:
         n = C.c_int64()
         call("gn_optimizer_state_size", self._h, C.byref(n))
@@ -209,3 +222,59 @@ class Optimizer:
 
     def __exit__(self, *exc):
         self.close()
+
+
+# ---- Trainer.StepOptimizer's schedules (trainer/scheduler.go:10-41) ----------
+def lr_multiplier(step: int, num_iterations: int, warmup_steps: int, warmdown_ratio: float,
+                  final_lr_frac: float) -> float:
+    """trainer/scheduler.go:10-20, in float32 as the reference computes it."""
+    f = np.float32
+    warmdown = int(f(num_iterations) * f(warmdown_ratio))
+    if step < warmup_steps:
+        return float(f(step + 1) / f(warmup_steps))
+    if step <= num_iterations - warmdown:
+        return 1.0
+    progress = f(num_iterations - step) / f(warmdown)
+    return float(progress * f(1.0) + (f(1) - progress) * f(final_lr_frac))
+
+
+def muon_momentum(step: int, num_iterations: int, warmdown_ratio: float) -> float:
+    """trainer/scheduler.go:24-36."""
+    f = np.float32
+    warmdown = int(f(num_iterations) * f(warmdown_ratio))
+    start = num_iterations - warmdown
+    if step < 400:
+        fr = f(step) / f(400)
+        return float((f(1) - fr) * f(0.85) + fr * f(0.97))
+    if step >= start:
+        progress = f(step - start) / f(warmdown)
+        return float(f(0.97) * (f(1) - progress) + f(0.90) * progress)
+    return 0.97
+
+
+def weight_decay_cosine(step: int, num_iterations: int, base: float) -> float:
+    """trainer/scheduler.go:39-41."""
+    f = np.float32
+    return float(f(base) * f(0.5) * f(1 + math.cos(math.pi * float(step) / float(num_iterations))))
+
+
+def step_optimizer(opt: "Optimizer", session, initial_lr: np.ndarray, step: int,
+                   num_iterations: int, warmup_steps: int, warmdown_ratio: float,
+                   final_lr_frac: float, weight_decay: float):
+    """Trainer.StepOptimizer (trainer/trainer.go:80-102): the LR multiplier on
+    every group, the Muon momentum and cosine weight decay on Muon groups,
+    the momentum and zero weight decay on Sinkhorn groups; then the step,
+    UpdateRouterBias and ZeroGrad.  initial_lr: the table's LRs at creation."""
+    f = np.float32
+    mult = f(lr_multiplier(step, num_iterations, warmup_steps, warmdown_ratio, final_lr_frac))
+    mom = f(muon_momentum(step, num_iterations, warmdown_ratio))
+    wd = f(weight_decay_cosine(step, num_iterations, weight_decay))
+    kind = opt.table["kind"]
+    lr = (np.asarray(initial_lr, np.float32) * mult).astype(np.float32)
+    momentum = np.where(kind == KIND_ADAMW, opt.table["momentum"], mom).astype(np.float32)
+    decay = np.where(kind == KIND_MUON, wd,
+                     np.where(kind == KIND_SINKHORN, f(0), opt.table["weight_decay"])).astype(np.float32)
+    opt.set_hyper(lr, momentum, decay)
+    opt.step()
+    session.update_router_bias()
+    session.zero_grad()

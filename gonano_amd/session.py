@@ -132,6 +132,20 @@ class Session:
     def zero_grad(self):
         call("gn_session_zero_grads", self._h)
 
+    def update_router_bias(self, speed: float | None = None):
+        """Transformer.UpdateRouterBias (model/transformer.go:121-131) with
+        speed = Config.MoERouterBiasUpdate() unless given."""
+        if speed is None:
+            speed = self.cfg.router_bias_update if self.cfg.router_bias_update > 0 else 0.001
+        call("gn_session_update_router_bias", self._h, float(speed))
+
+    def moe_loads(self) -> np.ndarray:
+        """MoE.loadCounts of every layer, [n_layer, n_experts] (float64)."""
+        E = self.cfg.n_experts
+        out = np.zeros((self.cfg.n_layer if E > 0 else 0, E), np.float64)
+        call("gn_session_moe_loads", self._h, out.ctypes.data_as(C.POINTER(C.c_double)), out.size)
+        return out
+
     # -- compute --------------------------------------------------------------
     def forward(self, ids: np.ndarray) -> np.ndarray:
         ids = np.ascontiguousarray(ids, np.int32)

@@ -221,6 +221,16 @@ int gn_session_get_params(const gn_session *session, float *params, int64_t coun
 int gn_session_get_grads(const gn_session *session, float *grads, int64_t count);
 /* Transformer.ZeroGrad (model/params.go:97-101). */
 int gn_session_zero_grads(gn_session *session);
+/* Transformer.UpdateRouterBias (model/transformer.go:121-131, moe.go:330-341)
+ * with speed = Config.MoERouterBiasUpdate(): every MoE layer's router bias
+ * moves by +-speed toward balance from the tokens its training forwards
+ * (gn_rl_step / gn_pg_step / gn_distill_step, MoE.forwardTraining,
+ * moe.go:192-193) routed to each expert since the last update, and the
+ * counts are cleared.  No MoE: nothing to do. */
+int gn_session_update_router_bias(gn_session *session, float speed);
+/* Those counts (MoE.loadCounts), [n_layer][n_experts] in float64; count
+ * must be n_layer * n_experts (0 without MoE). */
+int gn_session_moe_loads(const gn_session *session, double *loads, int64_t count);
 
 /* trainer.DistillStep (trainer/distill.go:13-46) for one micro-batch:
  * the frozen `teacher` session (same device and vocabulary, any
@@ -263,6 +273,12 @@ int gn_optimizer_create(gn_session *session, const gn_opt_param *table, int32_t 
  * consuming the accumulated gradients (which stay as they are; ZeroGrad is
  * gn_session_zero_grads). */
 int gn_optimizer_step(gn_optimizer *optimizer);
+/* Trainer.StepOptimizer's schedules (trainer/trainer.go:80-102) set each
+ * group's LR, Momentum and WeightDecay before every Step: one value per
+ * table entry (the entry's group's value), in table order; a NULL array
+ * leaves that field as it is.  The state is kept. */
+int gn_optimizer_set_hyper(gn_optimizer *optimizer, const float *lr, const float *momentum,
+                           const float *weight_decay, int32_t count);
 /* The optimizer state, entry by entry: AdamW expAvg[n] expAvgSq[n]; Muon
  * momentum[n] secondMom[max(rows, cols)]; Sinkhorn momentum[n]. */
 int gn_optimizer_state_size(const gn_optimizer *optimizer, int64_t *count);

@@ -23,6 +23,7 @@ import pytest
 from conftest import assert_close, rel_err
 from gonano_amd import config as G
 from test_gpu_session import _compare_grads
+from tf_check import teacher_forced_group
 
 pytestmark = pytest.mark.gpu
 
@@ -101,27 +102,30 @@ def test_csa_policy_gradient_step_matches_oracle(csa, orc):
             assert np.any(grads[off:off + r * c]), name
 
 
-def _oracle_rows(orc, cfg, w, prompts, S, N, seeds):
+def _teacher_forced(orc, cfg, w, prompts, rows, S, N, seeds):
+    """Every sampled token of every row against the oracle's draw from the
+    group stream given the same fed columns (tf_check.teacher_forced_group),
+    so a near-tie flip between the engines' logits cannot change later
+    columns of the comparison."""
     m = oracle(orc, cfg, w)
-    out = []
+    checked = 0
     for g in range(prompts.shape[0]):
-        out += m.generate_batch(prompts[g], S, N, 1.0, 50, int(seeds[g]))
-    return out
+        checked += teacher_forced_group(orc, m, prompts[g], rows[g * S:(g + 1) * S],
+                                        int(seeds[g]), N, 1.0, 50)
+    assert checked > 0
 
 
 def test_csa_rollouts_match_oracle(csa, orc):
     """Engine.GenerateBatchWith end to end (engine.go:112-369): the prefill
     (PrefillCED's bounded replay under CED), PrefillFrom, and every decode
-    step's compression, indexer keys, selection and attention; the sampled
-    rows equal the oracle's token for token."""
+    step's compression, indexer keys, selection and attention; every sampled
+    token equals the oracle's draw by teacher forcing."""
     _, cfg, w, s = csa
     G_, P, S, N = 2, 37, 3, 20
     prompts = np.random.default_rng(4).integers(0, cfg.vocab_size, (G_, P)).astype(np.int32)
     seeds = np.array([7, 1000], np.uint64)
     got = s.generate_batch(prompts, S, N, 1.0, 50, seeds)
-    want = _oracle_rows(orc, cfg, w, prompts, S, N, seeds)
-    for i, (a, b) in enumerate(zip(got, want)):
-        assert np.array_equal(a, b), (i, a[P:].tolist(), b[P:].tolist())
+    _teacher_forced(orc, cfg, w, prompts, got, S, N, seeds)
 
 
 def test_csa_decode_graph_matches_eager(csa):
@@ -154,9 +158,7 @@ def test_csa_long_rollout_matches_oracle(orc):
     with Session(cfg) as s:
         s.set_params(w)
         got = s.generate_batch(prompts, 2, 180, 1.0, 50, seeds)
-    want = _oracle_rows(orc, cfg, w, prompts, 2, 180, seeds)
-    for a, b in zip(got, want):
-        assert np.array_equal(a, b)
+    _teacher_forced(orc, cfg, w, prompts, got, 2, 180, seeds)
 
 
 def test_ced_bounded_replay_rollout_matches_oracle(orc):
@@ -171,6 +173,28 @@ def test_ced_bounded_replay_rollout_matches_oracle(orc):
     with Session(cfg) as s:
         s.set_params(w)
         got = s.generate_batch(prompts, 2, 40, 1.0, 50, seeds)
-    want = _oracle_rows(orc, cfg, w, prompts, 2, 40, seeds)
-    for a, b in zip(got, want):
+    _teacher_forced(orc, cfg, w, prompts, got, 2, 40, seeds)
+
+
+@pytest.mark.parametrize("case", ["flat", "hier_fru", "ced"])
+def test_csa_select_kernels_agree(case, monkeypatch):
+    """The two selection kernels (one wave per row; one block of 8 waves per
+    row, chosen for decode-size row counts) rank by the same strict order,
+    so forward logits (prefill-size selections) and rollouts (decode-size
+    selections) are bitwise the same with either forced."""
+    from gonano_amd.session import Session
+    cfg = csa_cfg(case)
+    w = G.init_weights(cfg, seed=41, perturb=0.05 if cfg.ced else 0.1)
+    rng = np.random.default_rng(17)
+    ids = rng.integers(0, cfg.vocab_size, (2, 150)).astype(np.int32)
+    prompts = rng.integers(0, cfg.vocab_size, (2, 90)).astype(np.int32)
+    seeds = np.array([5, 6], np.uint64)
+    out = {}
+    for mode in ("wave", "block"):
+        monkeypatch.setenv("GN_CSA_SELECT", mode)
+        with Session(cfg) as s:
+            s.set_params(w)
+            out[mode] = (s.forward(ids), s.generate_batch(prompts, 3, 40, 1.0, 50, seeds))
+    assert np.array_equal(out["wave"][0], out["block"][0])
+    for a, b in zip(out["wave"][1], out["block"][1]):
         assert np.array_equal(a, b)

@@ -112,3 +112,57 @@ def test_optimizer_rejects_bad_tables():
         bad["ns_steps"] = 6  # five Polar Express coefficient sets
         with pytest.raises(HipError):
             OPT.Optimizer(s, bad)
+
+
+def test_step_optimizer_schedules_and_router_bias(orc):
+    """Trainer.StepOptimizer (trainer/trainer.go:80-102) at a warmdown step:
+    the groups' LR / Momentum / WeightDecay set through gn_optimizer_set_hyper
+    (the step equals the oracle's with the scheduled table), then
+    UpdateRouterBias (moe.go:330-341) from the tokens the training forward
+    counted (MoE.forwardTraining, moe.go:192-193: B*T*K per layer and
+    forward) and ZeroGrad; a second update with no training forward in
+    between changes nothing (the counts were cleared)."""
+    from gonano_amd.session import Session
+    cfg = _cfg("latent")
+    assert cfg.n_experts > 0
+    table = OPT.chat_rl_table(cfg)
+    w = G.init_weights(cfg, seed=5, perturb=0.05)
+    step, iters, warmup, ratio, final, wd0 = 700, 1000, 0, 0.5, 0.1, 0.2
+    mult = OPT.lr_multiplier(step, iters, warmup, ratio, final)
+    mom = OPT.muon_momentum(step, iters, ratio)
+    wd = OPT.weight_decay_cosine(step, iters, wd0)
+    assert abs(mult - 0.64) < 1e-6 and abs(mom - 0.942) < 1e-6  # 200/500 into the warmdown
+    sched = table.copy()
+    sched["lr"] = (table["lr"] * np.float32(mult)).astype(np.float32)
+    muon, sink = table["kind"] == OPT.KIND_MUON, table["kind"] == OPT.KIND_SINKHORN
+    sched["momentum"][muon | sink] = np.float32(mom)
+    sched["weight_decay"][muon] = np.float32(wd)
+    sched["weight_decay"][sink] = 0
+    ref = orc.OracleOptimizer(sched)
+    slices = cfg.param_slices()
+    bias_names = [f"transformer.h.{l}.moe.router_bias" for l in range(cfg.n_layer)]
+    assert all(n in slices for n in bias_names)
+    with Session(cfg) as s:
+        s.set_params(w)
+        assert not s.moe_loads().any()
+        with OPT.Optimizer(s, table) as opt:
+            g = _pg_grads(s, cfg, 1)  # one training forward of B x T = 2 x 96 tokens
+            loads = s.moe_loads()
+            assert loads.shape == (cfg.n_layer, cfg.n_experts)
+            assert (loads >= 0).all() and (loads == np.round(loads)).all()
+            assert (loads.sum(1) == 2 * 96 * cfg.experts_per_token).all()
+            OPT.step_optimizer(opt, s, table["lr"], step, iters, warmup, ratio, final, wd0)
+            p = s.get_params()
+            want = w.copy()
+            ref.step(want, g)
+            _compare(table, w, p, want, opt.state(), ref.state, "scheduled step")
+            speed = np.float32(0.001)  # Config.MoERouterBiasUpdate() default
+            for l, name in enumerate(bias_names):
+                off, r, c = slices[name]
+                mean = loads[l].sum() / cfg.n_experts
+                expect = (w[off:off + r * c] + speed * np.sign(mean - loads[l]).astype(np.float32))
+                assert np.array_equal(p[off:off + r * c], expect.astype(np.float32)), name
+            assert not s.moe_loads().any()
+            assert not s.grads().any()
+            s.update_router_bias()
+            assert np.array_equal(s.get_params(), p)

@@ -238,3 +238,21 @@ def test_full_table_step_is_finite(orc):
     o.step(p, g)
     assert np.isfinite(p).all() and np.isfinite(o.state).all()
     assert (p != w).mean() > 0.99
+
+
+def test_schedules_known_answers():
+    """Trainer.StepOptimizer's schedules against trainer/trainer_test.go:47-78
+    (warmup, plateau and end of LRMultiplier; MuonMomentum at 0 and in the
+    plateau; WeightDecayCosine at both ends), plus the warmdown ramps at
+    points the closed forms fix."""
+    assert abs(OPT.lr_multiplier(0, 100, 10, 0.5, 0.05) - 0.1) < 1e-5
+    assert OPT.lr_multiplier(50, 100, 10, 0.5, 0.05) == 1.0
+    assert abs(OPT.lr_multiplier(100, 100, 10, 0.5, 0.05) - 0.05) < 1e-5
+    assert abs(OPT.lr_multiplier(75, 100, 10, 0.5, 0.05) - 0.525) < 1e-6  # half-way down
+    assert abs(OPT.muon_momentum(0, 1000, 0.5) - 0.85) < 1e-5
+    assert abs(OPT.muon_momentum(500, 1000, 0.5) - 0.97) < 1e-5
+    assert abs(OPT.muon_momentum(200, 1000, 0.5) - 0.91) < 1e-6   # half-way up
+    assert abs(OPT.muon_momentum(750, 1000, 0.5) - 0.935) < 1e-6  # half-way down
+    assert abs(OPT.weight_decay_cosine(0, 100, 0.3) - 0.3) < 1e-5
+    assert abs(OPT.weight_decay_cosine(100, 100, 0.3)) < 1e-5
+    assert abs(OPT.weight_decay_cosine(50, 100, 0.3) - 0.15) < 1e-6
