@@ -12,6 +12,11 @@
  *         + 0x5851F42D4C957F2D14057B7EF767814F   (mod 2^128)
  * whose output is the DXSM permutation of the *new* state, and
  * Rand.Float32() = float32(uint32(Uint64()>>32) << 8 >> 8) / 2^24.
+ *
+ * The PCG transition, jump-ahead and DXSM output are pinned against numpy's
+ * independent PCG64 / PCG64DXSM.  The Float32 mapping is parity unpinned:
+ * it follows the published math/rand/v2 source, and neither that source nor
+ * a Go toolchain is in this container to check it against.
  */
 #include <ctype.h>
 #include <math.h>
