@@ -922,11 +922,17 @@ void launch_moe_combine(const MoeCombineArgs& a, int64_t rows, hipStream_t st) {
 // 256 rows x top-2 over 16 experts -- a second serial pass of loads,
 // products, reduction and epilogue: 28 -> 20 us for the d12 gate/up product.)
 // ---------------------------------------------------------------------------
+// Calls averaging at most 16 pairs per expert (flash d12 decode: 64 rows x
+// top-2 over 16 experts) take chunks of two tiles: half the accumulator
+// registers, so the down instance at K = 768 runs three waves per SIMD
+// (flash d12: its 768 blocks in one round of the CUs instead of 1.5).  The
+// gate/up instance holds twice the weights: forced to three waves it
+// spills 22 registers to scratch and measured slower (rollout 1080 ->
+// 1111 ms), so it keeps two.
 static constexpr int MOE_XW = 4;   // waves per block (K quarters)
-static constexpr int MOE_CT = 4;   // 16-row tiles per chunk
 
-template <int KH, bool GU>
-__global__ __launch_bounds__(64 * MOE_XW) void moe_expert_small_kernel(MoeExpertArgs a) {
+template <int KH, bool GU, int MOE_CT>
+__global__ __launch_bounds__(64 * MOE_XW, (MOE_CT == 2 && !GU) ? 3 : 1) void moe_expert_small_kernel(MoeExpertArgs a) {
   constexpr int NW = GU ? 2 : 1;          // weight matrices (gate, up | down)
   constexpr int JB = KH < 2 ? KH : 2;     // k groups of weights requested before the rows
   constexpr int NB = (NW + 2) * KH <= 40 ? 2 : 1;  // row buffers (double-buffered tiles)
@@ -1054,10 +1060,13 @@ bool launch_moe_expert_small(const MoeExpertArgs& a, hipStream_t st) {
   const int kh = a.K / (16 * MOE_XW);
   GN_CHECK((a.w1 != nullptr) == (a.perm_row != nullptr), "moe expert: gate/up needs both");
   const dim3 grid((unsigned)(a.E * (a.N / 16))), block(64 * MOE_XW);
-#define GN_MOE_X(KH)                                                          \
-  case KH:                                                                    \
-    if (a.w1) hipLaunchKernelGGL((moe_expert_small_kernel<KH, true>), grid, block, 0, st, a); \
-    else hipLaunchKernelGGL((moe_expert_small_kernel<KH, false>), grid, block, 0, st, a);     \
+  const bool small = a.pairs > 0 && a.pairs <= 16 * (int64_t)a.E;
+#define GN_MOE_X(KH)                                                                          \
+  case KH:                                                                                    \
+    if (a.w1 && small) hipLaunchKernelGGL((moe_expert_small_kernel<KH, true, 2>), grid, block, 0, st, a); \
+    else if (a.w1) hipLaunchKernelGGL((moe_expert_small_kernel<KH, true, 4>), grid, block, 0, st, a);    \
+    else if (small) hipLaunchKernelGGL((moe_expert_small_kernel<KH, false, 2>), grid, block, 0, st, a);  \
+    else hipLaunchKernelGGL((moe_expert_small_kernel<KH, false, 4>), grid, block, 0, st, a);             \
     break;
   switch (kh) {
     GN_MOE_X(1) GN_MOE_X(2) GN_MOE_X(3) GN_MOE_X(4) GN_MOE_X(5) GN_MOE_X(6) GN_MOE_X(8)

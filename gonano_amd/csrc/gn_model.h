@@ -358,6 +358,7 @@ struct MoeExpertArgs {
   float* out;
   int E, N, K;
   float clamp;
+  int64_t pairs = 0;  // token-expert pairs of the call (chooses the chunk size)
 };
 bool launch_moe_expert_small(const MoeExpertArgs& a, hipStream_t st);
 bool moe_expert_small_supported(int N, int K);

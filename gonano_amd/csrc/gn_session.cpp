@@ -747,10 +747,11 @@ static void moe_ffn_forward(gn_session* s, const Layer& ly, const float* mid, co
   if (stream_experts) {
     MoeExpertArgs gx{};
     gx.x = h2; gx.perm_row = m.perm_row; gx.off = m.off; gx.w0 = ly.eg; gx.w1 = ly.eu;
-    gx.out = m.hg; gx.E = E; gx.N = EH; gx.K = C; gx.clamp = s->clamp;
+    gx.out = m.hg; gx.E = E; gx.N = EH; gx.K = C; gx.clamp = s->clamp; gx.pairs = NK;
     GN_CHECK(launch_moe_expert_small(gx, st), "moe: expert gate/up shape");
     MoeExpertArgs dx{};
     dx.x = m.hg; dx.off = m.off; dx.w0 = ly.ed; dx.out = m.yg; dx.E = E; dx.N = C; dx.K = EH;
+    dx.pairs = NK;
     GN_CHECK(launch_moe_expert_small(dx, st), "moe: expert down shape");
   } else {
     // expert gate and up projections into [gate | up] rows, SwiGLU, down
