@@ -694,8 +694,13 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     // Small grids (the M = 256 decode projections): about 200 workgroups
     // (25/32 of a workgroup per CU) measured fastest; more splits cost more
     // in the reduction than they gain in parallelism.
-    splits = (int)std::min<int64_t>((25 * cus / 32 + tiles / 2) / tiles, d.K / 256);
-    splits = std::max(1, std::min(splits, 64));
+    // Few-row products (M <= 128: the flash decode's 64 rows, 8 to 24 tiles)
+    // take K splits down to 64 deep, so their serial K loop shortens too
+    // (flash d12 rollout 1080 -> 1013 ms at 128 deep, 1004 ms at 64; at
+    // M = 256, 128-deep splits left the latent and d12 rollouts unchanged).
+    const int kmin = d.M <= 128 ? 64 : 256;
+    splits = (int)std::min<int64_t>((25 * cus / 32 + tiles / 2) / tiles, d.K / kmin);
+    splits = std::max(1, std::min(splits, d.defer ? PENDING_MAX_SPLITS : 64));
   }
   // Narrow tiles for small grids whose N is a multiple of 96 (the d12 decode
   // projections, N = 768 or 3072 at M = 256): 32x96 tiles with a split
