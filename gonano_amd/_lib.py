@@ -59,9 +59,9 @@ class GnTiming(C.Structure):
         ("gemm_ms", C.c_double),
         ("gemm_flops", C.c_double),
         ("gemm_launches", C.c_int64),
-        ("gemm_lt_ms", C.c_double),
-        ("gemm_lt_flops", C.c_double),
-        ("gemm_lt_launches", C.c_int64),
+        ("gemm_wide_ms", C.c_double),
+        ("gemm_wide_flops", C.c_double),
+        ("gemm_wide_launches", C.c_int64),
     ]
 
 

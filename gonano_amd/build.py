@@ -30,7 +30,6 @@ SOURCES = [
     "gn_sampler.hip",
     "gn_static.hip",
     "gn_optimizer.hip",
-    "gn_blaslt.cpp",
     "gn_session.cpp",
     "gn_tools.cpp",
 ]
@@ -66,9 +65,7 @@ def build(verbose: bool = True) -> str:
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    # hipBLASLt for the session's plain products (ROCm's own library)
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-           "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{r.stdout}\n{r.stderr}")

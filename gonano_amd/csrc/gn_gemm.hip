@@ -10,6 +10,7 @@
 // (global_load_lds_dwordx4, no VGPR staging), laid out so that MFMA fragments
 // are read with conflict-free LDS accesses; see TileIO.  One barrier per K
 // tile; the loads of the next S-1 tiles stay in flight behind the MFMAs.
+#include <cstdlib>
 #include <type_traits>
 
 #include "gn_kernels.h"
@@ -590,9 +591,446 @@ static void launch_grouped(const GemmParams& p, bool ak, bool bk, bool vec, hipS
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
-void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
+// ---------------------------------------------------------------------------
+// Wide-tile engine for the large products: the train phase's Linear
+// forward and backward products and the lm_head (training and rollout).
+//
+// One 256 x 256 output tile per workgroup of four waves (2 x 2), each wave
+// owning 128 x 128 outputs: 256 accumulators per lane, held in the AGPR half
+// of gfx950's 512-entry register file (one wave per SIMD).  K runs in
+// 32-deep tiles through a two-stage LDS ring (2 x 64 KB of the 160 KB).
+// The wave tile sets the operand traffic: a 16-deep k group is 16
+// ds_read_b128 per wave for 256 MFMAs.
+//
+// The MFMA's row operand (src A, whose rows a lane's four D registers walk)
+// is the N side of the product and the column operand the M side, so a
+// lane's four results of a block are four consecutive columns of one row of
+// C: the epilogue stores 16-byte vectors.
+//
+// Pipeline, K tile kt in stage kt & 1:
+//   issue the group-1 fragment reads of tile kt
+//   256 MFMAs on the group-0 fragments of tile kt
+//   wait (own LDS reads, tile kt+1's loads), barrier
+//   issue tile kt+2's loads into stage kt & 1 (every wave holds group 1)
+//   issue the group-0 fragment reads of tile kt+1
+//   256 MFMAs on the group-1 fragments of tile kt
+// LDS latency hides behind MFMAs, a tile's loads have two tiles of MFMAs
+// (16384 cycles) to land, and there is one barrier per tile.
+//
+// Long K ranges are split (at most KCHUNK deep per workgroup) and the
+// partials summed in float64 in split order by gemm_reduce_kernel, which
+// bounds float32 rounding growth as the two-level summation of gemm_kernel
+// does.
+// ---------------------------------------------------------------------------
+namespace wide {
+
+constexpr int TILE = 256;      // output tile edge (M and N)
+constexpr int TK = 32;         // K depth of one LDS stage
+constexpr int SZ = TILE * TK;  // floats per operand stage (32 KB)
+constexpr int KCHUNK = 8192;   // deepest K range of one workgroup
+
+// One operand of a workgroup of NW waves: its K tile moved into an LDS
+// stage and read back as MFMA fragments.
+//
+// K-contiguous (X[d*ld + k]): LDS [256 d][32 k], 8 16-byte slots per row,
+// slot column XOR-swizzled by (row & 7).  A fragment is one ds_read_b128 of
+// 16 rows x 4 consecutive k per lane: lane (i, q) = (lane & 15, lane >> 4)
+// reads row d + i, k = 16 g + 4 q .. + 3, and MFMA step c of the group
+// takes component c (every k meets itself in both operands).
+//
+// Contiguous in d (X[k*ld + d]): LDS [32 k][256 d].  A read takes four
+// consecutive d at one k: lane (i, q) reads k = 16 g + 4 q + c, d = base +
+// 4 i .. + 3, for MFMA step c; component c' feeds block 4 b' + c', whose row
+// i is d = 64 b' + 4 i + c'.  The 16 lanes of a q read 256 contiguous bytes.
+//
+// Global -> LDS: global_load_lds_dwordx4 drops lane l's 16 bytes at (wave
+// base) + 16 l, so instruction t of wave w fills slots (t NW + w) 64 .. + 63
+// and the lane -> address map places them.  The map is the same for every
+// instruction up to a uniform row step, so a lane keeps one 32-bit offset
+// and the instructions add scalar steps.  Tiles are never partial: a tile
+// that would run past the operand's extent D (>= 256) is shifted back to
+// end at D, and the epilogue skips the rows it shares with the tile before.
+template <bool KC, int NW>
+struct WOp {
+  static constexpr int NI = SZ / 4 / (64 * NW);  // LDS-DMA instructions per thread and stage
+  uint32_t loff;  // the lane's byte offset from the tile corner (d0, k0), instruction 0
+
+  __device__ __forceinline__ void init(int64_t ld, int tid) {
+    const int w = tid >> 6, l = tid & 63;
+    if constexpr (KC)  // row w*8 + l/8, slot (l & 7) ^ (row & 7) = (l & 7) ^ (l >> 3)
+      loff = (uint32_t)(((int64_t)(w * 8 + (l >> 3)) * ld + 4 * ((l & 7) ^ (l >> 3))) * 4);
+    else  // row w, columns 4 l .. 4 l + 3
+      loff = (uint32_t)(((int64_t)w * ld + 4 * l) * 4);
+  }
+  // bytes between the rows of instructions t and t + 1
+  static __device__ __forceinline__ int64_t tstep(int64_t ld) {
+    return (KC ? (int64_t)NW * 8 * ld : (int64_t)NW * ld) * 4;
+  }
+  static __device__ __forceinline__ const char* corner(const float* X, int64_t ld, int d0, int k0) {
+    return reinterpret_cast<const char*>(KC ? X + (int64_t)d0 * ld + k0 : X + (int64_t)k0 * ld + d0);
+  }
+  // Instruction t of the K tile whose corner is at base.
+  __device__ __forceinline__ void dma_one(const char* base, int64_t step, float* S, int w,
+                                          int t) const {
+    __builtin_amdgcn_global_load_lds((const void*)(base + t * step + loff),
+                                     (lds_void*)(S + 4 * ((t * NW + w) * 64)), 16, 0, 0);
+  }
+  // Whole K tile at k0 of the tile starting at row d0.
+  __device__ __forceinline__ void dma(const float* __restrict__ X, int64_t ld, int d0, int k0,
+                                      float* S, int w) const {
+    const char* base = corner(X, ld, d0, k0);
+    const int64_t step = tstep(ld);
+#pragma unroll
+    for (int t = 0; t < NI; t++) dma_one(base, step, S, w, t);
+  }
+  // LDS float offset of the lane's first fragment read of k group g for
+  // the rows starting at d (a multiple of 64); the others are immediates.
+  static __device__ __forceinline__ int frag_base(int d, int g, int lane) {
+    const int i = lane & 15, q = lane >> 4;
+    if constexpr (KC) return (d + i) * TK + 4 * ((4 * g + q) ^ (i & 7));
+    else return (16 * g + 4 * q) * TILE + d + 4 * i;
+  }
+  // The R/16 fragments of the R rows whose first read is at S + base.
+  template <int R>
+  static __device__ __forceinline__ void frags(const float* __restrict__ S, int base,
+                                               v4f (&F)[R / 16]) {
+    if constexpr (KC) {
+#pragma unroll
+      for (int b = 0; b < R / 16; b++)
+        F[b] = *reinterpret_cast<const v4f*>(&S[base + 16 * b * TK]);
+    } else {
+#pragma unroll
+      for (int bb = 0; bb < R / 64; bb++)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          F[4 * bb + c] = *reinterpret_cast<const v4f*>(&S[base + c * TILE + 64 * bb]);
+    }
+  }
+  // Fragment j of the R/16 that frags() reads.
+  template <int R>
+  static __device__ __forceinline__ v4f frag(const float* __restrict__ S, int base, int j) {
+    if constexpr (KC) return *reinterpret_cast<const v4f*>(&S[base + 16 * j * TK]);
+    else return *reinterpret_cast<const v4f*>(&S[base + (j & 3) * TILE + 64 * (j >> 2)]);
+  }
+  // Operand of block b at MFMA step c.
+  template <int N>
+  static __device__ __forceinline__ float elem(const v4f (&F)[N], int b, int c) {
+    if constexpr (KC) return F[b][c];
+    else return F[(b >> 2) * 4 + c][b & 3];
+  }
+  // Row (within the wave's rows) of block b's MFMA row/column index i.
+  static __device__ __forceinline__ int row(int b, int i) {
+    if constexpr (KC) return 16 * b + i;
+    else return 64 * (b >> 2) + 4 * i + (b & 3);
+  }
+};
+
+// One MFMA accumulating in place in an AGPR quad.  Written as inline asm so
+// that the accumulators are tied to their registers across the K loop (the
+// builtin's untied destination let register allocation rotate the 256
+// accumulators through copies inside the loop), and volatile so that the
+// memory operations placed between MFMAs keep their source order.  No
+// hazard needs wait states here: the fragments come from LDS (lgkmcnt waits
+// are inserted for the asm's operands), the accumulators are written by
+// nothing but these MFMAs, each accumulator is reused 64 MFMAs later, and
+// the epilogue reads them after a vmcnt wait and s_nops (see the kernel).
+__device__ __forceinline__ void mfma_acc(v4f& acc, float a, float b) {
+  asm volatile("v_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+// The MFMAs of one 16-deep k group: acc[J][I], J over the wave's M blocks,
+// I over its N blocks.  after(n) runs after MFMA n (0-based) and issues
+// the memory operations spread over the group.
+template <bool AK, bool BK, int NW, int MI, int NI, class After>
+__device__ __forceinline__ void group_mma(v4f (&acc)[MI][NI], const v4f (&fa)[MI],
+                                          const v4f (&fb)[NI], After&& after) {
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int J = 0; J < MI; J++)
+#pragma unroll
+      for (int I = 0; I < NI; I++) {
+        mfma_acc(acc[J][I], WOp<BK, NW>::elem(fb, I, c), WOp<AK, NW>::elem(fa, J, c));
+        after((c * MI + J) * NI + I);
+      }
+}
+
+// Four consecutive outputs (row m, columns n .. n + 3) through epilogue E;
+// E == -1 stores split-K partials.  Same arithmetic as gemm_epilogue.
+template <int E>
+__device__ __forceinline__ void store4(const GemmParams& p, float* part, int m, int n, v4f v) {
+  if constexpr (E == -1) {
+    *reinterpret_cast<v4f*>(&part[(int64_t)m * p.N + n]) = v;
+  } else {
+    float* c = &p.C[(int64_t)m * p.ldc + n];
+    if constexpr (E == EPI_STORE) {
+      *reinterpret_cast<v4f*>(c) = v * p.alpha;
+    } else if constexpr (E == EPI_ADD_SRC) {
+      *reinterpret_cast<v4f*>(c) =
+          v + *reinterpret_cast<const v4f*>(&p.aux[(int64_t)m * p.ldaux + n]);
+    } else if constexpr (E == EPI_ACCUM) {
+      *reinterpret_cast<v4f*>(c) = *reinterpret_cast<const v4f*>(c) + v;
+    } else if constexpr (E == EPI_SOFTCAP) {
+      v4f o;
+#pragma unroll
+      for (int r = 0; r < 4; r++) o[r] = softcap15(v[r]);
+      *reinterpret_cast<v4f*>(c) = o;
+    } else if constexpr (E == EPI_RELU2_SAVE || E == EPI_RELU2_SAVE + 16) {
+      if constexpr (E == EPI_RELU2_SAVE)
+        *reinterpret_cast<v4f*>(&p.aux_out[(int64_t)m * p.ldaux + n]) = v;
+      v4f o;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float u = v[r] < 0.f ? 0.f : v[r];
+        o[r] = u * u;
+      }
+      *reinterpret_cast<v4f*>(c) = o;
+    } else {
+      static_assert(E == EPI_DRELU2, "epilogue kind");
+      const v4f u = *reinterpret_cast<const v4f*>(&p.aux[(int64_t)m * p.ldaux + n]);
+      v4f o;
+#pragma unroll
+      for (int r = 0; r < 4; r++) o[r] = u[r] > 0.f ? (v[r] * 2.f) * u[r] : 0.f;
+      *reinterpret_cast<v4f*>(c) = o;
+    }
+  }
+}
+
+// The wave's outputs, whose first row and column are mw, nw; rows before m0
+// and columns before n0 (a shifted tile's overlap with the tile before) are
+// skipped.  N % 4 == 0, and nw, n0 are multiples of 4.
+template <int E, bool AK, bool BK, int NW, int MI, int NI>
+__device__ __forceinline__ void store_wave(const GemmParams& p, float* part,
+                                           const v4f (&acc)[MI][NI], int mw, int nw, int m0,
+                                           int n0, int lane) {
+  const int q = lane >> 4;
+  const bool full = mw >= m0 && nw >= n0;
+#pragma unroll
+  for (int J = 0; J < MI; J++) {
+    const int m = mw + WOp<AK, NW>::row(J, lane & 15);
+#pragma unroll
+    for (int u = 0; u < NI; u++) {
+      int n;
+      v4f v;
+      if constexpr (BK) {
+        n = nw + 16 * u + 4 * q;
+        v = acc[J][u];
+      } else {
+        const int bb = u >> 2, r = u & 3;
+        n = nw + 64 * bb + 16 * q + 4 * r;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = acc[J][4 * bb + c][r];
+      }
+      if (full || (m >= m0 && n >= n0)) store4<E>(p, part, m, n, v);
+    }
+  }
+}
+
+// 256 x 256 tile per workgroup of WM x WN waves (wave tile 256/WM rows of M
+// by 256/WN columns of N), epilogue E (-1: split-K partials).  Every K range
+// is a whole number of tile pairs (K and k_per_split multiples of 2 TK), so
+// the loop body is two tiles, one per stage, and every LDS address is an
+// immediate from a per-lane base.  The stages are separate arrays: the LDS
+// reads of one stage provably do not alias the loads in flight into the
+// other.
+template <bool AK, bool BK, int WM, int WN, int E>
+__global__ __launch_bounds__(64 * WM * WN, (WM * WN) / 4) void gemm_wide_kernel(GemmParams p) {
+  constexpr int NW = WM * WN, TM = TILE / WM, TN = TILE / WN, MI = TM / 16, NI = TN / 16;
+  using LA = WOp<AK, NW>;
+  using LB = WOp<BK, NW>;
+  constexpr int PT = LA::NI + LB::NI;  // LDS-DMA instructions per thread and K tile
+  __shared__ __attribute__((aligned(16))) float As0[SZ];
+  __shared__ __attribute__((aligned(16))) float Bs0[SZ];
+  __shared__ __attribute__((aligned(16))) float As1[SZ];
+  __shared__ __attribute__((aligned(16))) float Bs1[SZ];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w % WM, wn = w / WM;
+  int tm, tn, split;
+  tile_coords(p, tm, tn, split);
+  // the tile's first row and column, and where it is loaded from (a tile
+  // past the end is shifted back to end at M resp. N)
+  const int m0 = tm * TILE, n0 = tn * TILE;
+  const int ms = min(m0, p.M - TILE), ns = min(n0, p.N - TILE);
+  const int kbeg = split * p.k_per_split, kend = min(p.K, kbeg + p.k_per_split);
+  const int nkt = kend > kbeg ? (kend - kbeg) / TK : 0;  // even
+  LA la;
+  LB lb;
+  la.init(p.lda, tid);
+  lb.init(p.ldb, tid);
+  // the first two K tiles (the loop issues the others; those past the end
+  // re-read the last tile into a stage nobody reads again)
+  auto load = [&](int kt, float* sa, float* sb) {
+    const int k0 = kbeg + kt * TK;
+    la.dma(p.A, p.lda, ms, k0, sa, w);
+    lb.dma(p.B, p.ldb, ns, k0, sb, w);
+  };
+  const int ab0 = LA::frag_base(wm * TM, 0, lane), ab1 = LA::frag_base(wm * TM, 1, lane);
+  const int bb0 = LB::frag_base(wn * TN, 0, lane), bb1 = LB::frag_base(wn * TN, 1, lane);
+
+  v4f acc[MI][NI];
+#pragma unroll
+  for (int J = 0; J < MI; J++)
+#pragma unroll
+    for (int I = 0; I < NI; I++) acc[J][I] = (v4f){0.f, 0.f, 0.f, 0.f};
+  v4f fa0[MI], fb0[NI], fa1[MI], fb1[NI];
+  if (nkt > 0) {
+    load(0, As0, Bs0);
+    load(1, As1, Bs1);
+    wait_vm_lgkm0<PT>();
+    tile_barrier();
+    LA::template frags<TM>(As0, ab0, fa0);
+    LB::template frags<TN>(Bs0, bb0, fb0);
+  }
+  // One K tile kt in stage (CA, CB); (XA, XB) holds tile kt+1.  MFMA n of a
+  // group is followed by memory operation n - 1 (n >= 1) of that group's
+  // list: first half, the group-1 fragment reads of tile kt; second half,
+  // the loads of tile kt+2 into (CA, CB), then the group-0 fragment reads
+  // of tile kt+1.
+  auto tile = [&](int kt, float* CA, float* CB, float* XA, float* XB) {
+    group_mma<AK, BK, NW>(acc, fa0, fb0, [&](int n) {
+      const int o = n - 1;
+      if (o >= 0 && o < MI) fa1[o] = LA::template frag<TM>(CA, ab1, o);
+      else if (o >= MI && o < MI + NI) fb1[o - MI] = LB::template frag<TN>(CB, bb1, o - MI);
+    });
+    // own fragment reads done; tile kt+1 (the only loads in flight) landed
+    wait_vm_lgkm0<0>();
+    tile_barrier();
+    // stage (CA, CB) is free: every wave holds its group-1 fragments
+    const int k2 = kbeg + min(kt + 2, nkt - 1) * TK;
+    const char* ga = LA::corner(p.A, p.lda, ms, k2);
+    const char* gb = LB::corner(p.B, p.ldb, ns, k2);
+    const int64_t sa = LA::tstep(p.lda), sb = LB::tstep(p.ldb);
+    group_mma<AK, BK, NW>(acc, fa1, fb1, [&](int n) {
+      const int o = n - 1;
+      if (o >= 0 && o < LA::NI) la.dma_one(ga, sa, CA, w, o);
+      else if (o >= LA::NI && o < PT) lb.dma_one(gb, sb, CB, w, o - LA::NI);
+      else if (o >= PT && o < PT + MI) fa0[o - PT] = LA::template frag<TM>(XA, ab0, o - PT);
+      else if (o >= PT + MI && o < PT + MI + NI)
+        fb0[o - PT - MI] = LB::template frag<TN>(XB, bb0, o - PT - MI);
+    });
+  };
+  for (int kt = 0; kt < nkt; kt += 2) {
+    tile(kt, As0, Bs0, As1, Bs1);
+    tile(kt + 1, As1, Bs1, As0, Bs0);
+    // wait states between the last MFMAs and any accumulator copy the
+    // compiler places at the loop's head (gonano_amd/isa_check checks the
+    // gap)
+    asm volatile("s_nop 7\n\ts_nop 7");
+  }
+  // the loads issued past the last tile; then 24 wait states before the
+  // accumulators are read (at least what an MFMA's result needs)
+  wait_vm_lgkm0<0>();
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+
+  float* part = E == -1 ? p.part + (int64_t)split * p.M * p.N : nullptr;
+  store_wave<E, AK, BK, NW>(p, part, acc, ms + wm * TM, ns + wn * TN, m0, n0, lane);
+}
+
+}  // namespace wide
+
+// The wide kernel for operand layouts (AK, BK) and epilogue E, or null
+// when that combination has no instance (gemm_kernel takes it).  The
+// instances are those the session's products use: x.W^T (forward,
+// lm_head), g.W (input gradients), g^T.x (weight gradients), and the
+// split-K partials (E == -1) of each.
+typedef void (*WideKernel)(GemmParams);
+static WideKernel wide_kernel(bool ak, bool bk, int e) {
+  using namespace wide;
+  constexpr int WM = 2, WN = 2;
+  if (ak && bk) {
+    switch (e) {
+      case -1: return gemm_wide_kernel<true, true, WM, WN, -1>;
+      case EPI_STORE: return gemm_wide_kernel<true, true, WM, WN, EPI_STORE>;
+      case EPI_ADD_SRC: return gemm_wide_kernel<true, true, WM, WN, EPI_ADD_SRC>;
+      case EPI_RELU2_SAVE: return gemm_wide_kernel<true, true, WM, WN, EPI_RELU2_SAVE>;
+      case EPI_RELU2_SAVE + 16: return gemm_wide_kernel<true, true, WM, WN, EPI_RELU2_SAVE + 16>;
+    }
+  } else if (ak && !bk) {
+    switch (e) {
+      case -1: return gemm_wide_kernel<true, false, WM, WN, -1>;
+      case EPI_STORE: return gemm_wide_kernel<true, false, WM, WN, EPI_STORE>;
+      case EPI_ACCUM: return gemm_wide_kernel<true, false, WM, WN, EPI_ACCUM>;
+      case EPI_DRELU2: return gemm_wide_kernel<true, false, WM, WN, EPI_DRELU2>;
+    }
+  } else if (!ak && !bk) {
+    switch (e) {
+      case -1: return gemm_wide_kernel<false, false, WM, WN, -1>;
+      case EPI_STORE: return gemm_wide_kernel<false, false, WM, WN, EPI_STORE>;
+      case EPI_ACCUM: return gemm_wide_kernel<false, false, WM, WN, EPI_ACCUM>;
+    }
+  }
+  return nullptr;
+}
+
+// Runs d on the wide-tile engine when it suits the product: large enough to
+// fill the chip with 256 x 256 tiles (after K splits), little padding, K a
+// multiple of 64, and the 16-byte alignment its vector loads and stores
+// need.  Returns false otherwise (gemm_kernel takes it).
+static bool gemm_wide(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
+                      DeviceArena* ws) {
+  using namespace wide;
+  if (d.group != GEMM_GROUP_NONE || d.defer || d.force_splits > 0 || !vec) return false;
+  if ((double)d.M * d.N * d.K < (double)(1 << 28)) return false;
+  if (d.M < TILE || d.N < TILE) return false;
+  if (d.K % (2 * TK) || d.N % 4 || d.ldc % 4 || !aligned16(d.C)) return false;
+  if (!d.a_kcontig && d.M % 4) return false;
+  const bool uses_aux = d.epi == EPI_ADD_SRC || d.epi == EPI_DRELU2;
+  if (uses_aux && (!aligned16(d.aux) || d.ldaux % 4)) return false;
+  if (d.epi == EPI_RELU2_SAVE && d.aux_out && (!aligned16(d.aux_out) || d.ldaux % 4)) return false;
+  const int64_t tm = ceil_div(d.M, TILE), tn = ceil_div(d.N, TILE), tiles = tm * tn;
+  // padding: at most 1/8 of the MFMA work on rows or columns past the product
+  if ((double)(tm * TILE) * (double)(tn * TILE) > 1.125 * (double)d.M * (double)d.N) return false;
+  const int64_t cus = 256;
+  int splits = (int)ceil_div(d.K, KCHUNK);
+  {
+    // more splits (each at least 1024 deep) while that makes whole rounds
+    // of the CUs fuller
+    const int smin = splits, smax = std::max<int>(smin, (int)std::min<int64_t>(64, d.K / 1024));
+    double best = -1.0;
+    for (int s = smin; s <= smax; s++) {
+      const int64_t wg = tiles * s;
+      const double eff = (double)wg / (double)(ceil_div(wg, cus) * cus);
+      if (eff > best + 1e-9) {
+        best = eff;
+        splits = s;
+      }
+      if (eff >= 0.999) break;
+    }
+  }
+  const int kps = (int)ceil_div(ceil_div(d.K, splits), 2 * TK) * 2 * TK;
+  splits = (int)ceil_div(d.K, kps);
+  // at least 3/4 of a round of the CUs (GN_GEMM_WIDE_MIN: another minimum
+  // workgroup count; tests take every eligible product with 1)
+  int64_t min_wg = (3 * cus) / 4;
+  if (const char* e = std::getenv("GN_GEMM_WIDE_MIN")) min_wg = std::max(1, std::atoi(e));
+  if (tiles * splits < min_wg) return false;
+  int e = splits > 1 ? -1 : d.epi;
+  if (e == EPI_RELU2_SAVE && !d.aux_out) e = EPI_RELU2_SAVE + 16;
+  const WideKernel kern = wide_kernel(d.a_kcontig, d.b_kcontig, e);
+  if (!kern) return false;
+  p.tiles_m = (int)tm;
+  p.tiles_n = (int)tn;
+  p.splits = splits;
+  p.k_per_split = kps;
+  if (splits > 1) {
+    GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
+    p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * splits)), dim3(256), 0, st, p);
+  GN_HIP(hipGetLastError());
+  if (splits > 1) {
+    const int64_t total = (int64_t)d.M * d.N;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                       p);
+    GN_HIP(hipGetLastError());
+  }
+  return true;
+}
+
+GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   GN_CHECK(d.M >= 0 && d.N >= 0 && d.K >= 0, "gemm: negative extent");
-  if (d.M == 0 || d.N == 0) return;
+  if (d.M == 0 || d.N == 0) return GEMM_ENGINE_TILE;
   GemmParams p{};
   p.A = d.A; p.B = d.B; p.C = d.C; p.aux = d.aux; p.aux_out = d.aux_out;
   p.lda = d.lda; p.ldb = d.ldb; p.ldc = d.ldc; p.ldaux = d.ldaux;
@@ -614,7 +1052,7 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
       if (d.M / d.groups >= 1024) {
         launch_grouped<128, 128, 2, 2, 1, 2, false, GEMM_GROUP_ROWS>(p, d.a_kcontig, d.b_kcontig,
                                                                      vec, st);
-        return;
+        return GEMM_ENGINE_TILE;
       }
       // Small groups (decode: a few to tens of rows per expert) stream each
       // expert's weights once; split K so that enough workgroups keep loads
@@ -657,9 +1095,9 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
       launch_grouped<128, 128, 2, 2, 1, 2, true, GEMM_GROUP_K>(p, d.a_kcontig, d.b_kcontig, vec,
                                                                st);
     }
-    return;
+    return GEMM_ENGINE_TILE;
   }
-
+  if (gemm_wide(d, p, vec, st, ws)) return GEMM_ENGINE_WIDE;
 
   // Tile choice: the 128x128 tile when it yields enough workgroups to cover
   // the 256 CUs, otherwise 64x64; split K when even that underfills the chip
@@ -796,6 +1234,7 @@ void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
                        p);
     GN_HIP(hipGetLastError());
   }
+  return GEMM_ENGINE_TILE;
 }
 
 }  // namespace gn

@@ -134,7 +134,12 @@ struct GemmDesc {
   int defer_slot = 0;
 };
 
-void gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);
+// Which kernel ran a product: gemm_kernel (tiles up to 128 x 128, fused
+// epilogues, grouped and deferred products) or the wide-tile engine (256 x
+// 256 tiles for the large products; gn_gemm.hip).
+enum GemmEngine { GEMM_ENGINE_TILE = 0, GEMM_ENGINE_WIDE = 1 };
+
+GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);
 
 // y[rows, out] = x[rows, in] . W[out, in]^T   (model/layers/linear.go:32-40)
 inline GemmDesc linear_fwd_desc(const float* x, const float* W, float* y, int rows, int in,

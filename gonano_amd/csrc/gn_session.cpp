@@ -18,7 +18,6 @@
 #include <string>
 #include <vector>
 
-#include "gn_blaslt.h"
 #include "gn_model.h"
 #include "gn_optimizer.h"
 #include "gn_tools.h"
@@ -133,11 +132,6 @@ struct gn_session {
   int64_t total = 0;
   hipStream_t stream = nullptr;
   std::unique_ptr<gn::DeviceArena> arena;
-  // plain products through hipBLASLt (null: every product on gemm_kernel)
-  struct LtDel {
-    void operator()(gn::BlasLt* b) const { gn::blaslt_destroy(b); }
-  };
-  std::unique_ptr<gn::BlasLt, LtDel> lt;
   float* params = nullptr;  // packed device storage
   float* grads = nullptr;
   float *wte = nullptr, *lm = nullptr, *rl = nullptr, *x0l = nullptr, *smg = nullptr,
@@ -152,7 +146,7 @@ struct gn_session {
   gn_timing t{};
   std::vector<std::pair<hipEvent_t, hipEvent_t>> gemm_events, attn_events;
   std::vector<double> gemm_ev_flops, attn_ev_bytes;
-  std::vector<char> gemm_ev_lt;  // the product ran on hipBLASLt
+  std::vector<char> gemm_ev_wide;  // the product ran on the wide-tile engine
   std::vector<int> attn_ev_launches;
   std::vector<hipEvent_t> event_pool;
   size_t event_next = 0;
@@ -212,43 +206,36 @@ static void* pinned(gn_session* s, size_t bytes) {
 }
 
 // GEMM launch with optional event timing (not while a graph is captured).
-// A session product: hipBLASLt when it takes it (plain epilogue, large
-// enough), gemm_kernel otherwise.
 static void sgemm(gn_session* s, const GemmDesc& d) {
-  bool lt = false;
-  auto run = [&] {
-    lt = blaslt_gemm(s->lt.get(), d, s->stream);
-    if (!lt) gemm(d, s->stream, s->arena.get());
-  };
   if (s->timing && !s->capturing) {
     hipEvent_t a = next_event(s), b = next_event(s);
     GN_HIP(hipEventRecord(a, s->stream));
-    run();
+    const GemmEngine e = gemm(d, s->stream, s->arena.get());
     GN_HIP(hipEventRecord(b, s->stream));
     s->gemm_events.push_back({a, b});
     s->gemm_ev_flops.push_back(2.0 * d.M * (double)d.N * d.K);
-    s->gemm_ev_lt.push_back(lt ? 1 : 0);
+    s->gemm_ev_wide.push_back(e == GEMM_ENGINE_WIDE ? 1 : 0);
   } else {
-    run();
+    gemm(d, s->stream, s->arena.get());
   }
 }
 
-// GEMM events into gemm_* (all products) and lt_* (those on hipBLASLt;
-// nullable), attention events into attn_*.
+// GEMM events into gemm_* (all products) and wide_* (those on the
+// wide-tile engine; nullable), attention events into attn_*.
 static void collect_timing(gn_session* s, double* gemm_ms, double* gemm_flops, int64_t* gemm_n,
                            double* attn_ms, double* attn_bytes, int64_t* attn_n,
-                           double* lt_ms = nullptr, double* lt_flops = nullptr,
-                           int64_t* lt_n = nullptr) {
+                           double* wide_ms = nullptr, double* wide_flops = nullptr,
+                           int64_t* wide_n = nullptr) {
   for (size_t i = 0; i < s->gemm_events.size(); i++) {
     float ms = 0;
     GN_HIP(hipEventElapsedTime(&ms, s->gemm_events[i].first, s->gemm_events[i].second));
     *gemm_ms += ms;
     *gemm_flops += s->gemm_ev_flops[i];
     (*gemm_n)++;
-    if (lt_ms && s->gemm_ev_lt[i]) {
-      *lt_ms += ms;
-      *lt_flops += s->gemm_ev_flops[i];
-      (*lt_n)++;
+    if (wide_ms && s->gemm_ev_wide[i]) {
+      *wide_ms += ms;
+      *wide_flops += s->gemm_ev_flops[i];
+      (*wide_n)++;
     }
   }
   for (size_t i = 0; i < s->attn_events.size(); i++) {
@@ -260,7 +247,7 @@ static void collect_timing(gn_session* s, double* gemm_ms, double* gemm_flops, i
   }
   s->gemm_events.clear();
   s->gemm_ev_flops.clear();
-  s->gemm_ev_lt.clear();
+  s->gemm_ev_wide.clear();
   s->attn_events.clear();
   s->attn_ev_bytes.clear();
   s->attn_ev_launches.clear();
@@ -1668,11 +1655,11 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
     GN_HIP(hipEventElapsedTime(&ms, ev0, ev1));
     s->t.train_ms = ms;
     s->t.gemm_ms = 0; s->t.gemm_flops = 0; s->t.gemm_launches = 0;
-    s->t.gemm_lt_ms = 0; s->t.gemm_lt_flops = 0; s->t.gemm_lt_launches = 0;
+    s->t.gemm_wide_ms = 0; s->t.gemm_wide_flops = 0; s->t.gemm_wide_launches = 0;
     double am = 0, ab = 0;
     int64_t an = 0;
     collect_timing(s, &s->t.gemm_ms, &s->t.gemm_flops, &s->t.gemm_launches, &am, &ab, &an,
-                   &s->t.gemm_lt_ms, &s->t.gemm_lt_flops, &s->t.gemm_lt_launches);
+                   &s->t.gemm_wide_ms, &s->t.gemm_wide_flops, &s->t.gemm_wide_launches);
   }
 }
 
@@ -1700,8 +1687,8 @@ static int pg_micro_batch(gn_session* s, int B, int T) {
 static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets, int B, int T,
                     const float* adv, float norm, float* loss_out, float* nll_out) {
   const int mb = pg_micro_batch(s, B, T);
-  double loss = 0, aux = 0, tms = 0, gms = 0, gfl = 0, lms = 0, lfl = 0;
-  int64_t gn = 0, ln = 0;
+  double loss = 0, aux = 0, tms = 0, gms = 0, gfl = 0, wms = 0, wfl = 0;
+  int64_t gn = 0, wn = 0;
   s->bal_batch = B;
   try {
     for (int b0 = 0; b0 < B; b0 += mb) {
@@ -1712,7 +1699,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
       loss += l;
       aux += s->aux_loss * nb;
       tms += s->t.train_ms; gms += s->t.gemm_ms; gfl += s->t.gemm_flops; gn += s->t.gemm_launches;
-      lms += s->t.gemm_lt_ms; lfl += s->t.gemm_lt_flops; ln += s->t.gemm_lt_launches;
+      wms += s->t.gemm_wide_ms; wfl += s->t.gemm_wide_flops; wn += s->t.gemm_wide_launches;
     }
   } catch (...) {
     s->bal_batch = 0;
@@ -1723,7 +1710,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
   s->aux_loss = aux / B;
   if (s->timing) {
     s->t.train_ms = tms; s->t.gemm_ms = gms; s->t.gemm_flops = gfl; s->t.gemm_launches = gn;
-    s->t.gemm_lt_ms = lms; s->t.gemm_lt_flops = lfl; s->t.gemm_lt_launches = ln;
+    s->t.gemm_wide_ms = wms; s->t.gemm_wide_flops = wfl; s->t.gemm_wide_launches = wn;
   }
 }
 
@@ -2755,9 +2742,6 @@ int gn_session_create(const gn_config* config, int device, gn_session** out) {
       GN_HIP(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
       s->arena = std::make_unique<DeviceArena>(s->stream);
       build_session(s, *config);
-      // GN_GEMM_BLASLT=0 keeps every product on gemm_kernel
-      const char* lt = std::getenv("GN_GEMM_BLASLT");
-      if (!lt || std::strcmp(lt, "0") != 0) s->lt.reset(blaslt_create());
       const char* fp = std::getenv("GN_FUSE_QKV_POST");
       s->fuse_qkv_post = !fp || std::strcmp(fp, "0") != 0;
       // GN_CSA_SELECT=wave / block forces one selection kernel (tests)
@@ -2779,7 +2763,6 @@ int gn_session_destroy(gn_session* s) {
     (void)hipStreamSynchronize(s->stream);
     s->pc_defer = false;
     pc_clear(s);
-    s->lt.reset();
     s->arena.reset();
     for (auto e : s->event_pool) (void)hipEventDestroy(e);
     if (s->pinned) (void)hipHostFree(s->pinned);
@@ -2906,7 +2889,7 @@ int gn_forward(gn_session* s, const int32_t* ids, int32_t B, int32_t T, float* l
                             hipMemcpyDeviceToHost, s->stream));
     }
     GN_HIP(hipStreamSynchronize(s->stream));
-    s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->gemm_ev_lt.clear(); s->event_next = 0;
+    s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->gemm_ev_wide.clear(); s->event_next = 0;
   });
 }
 
@@ -3093,7 +3076,7 @@ int gn_session_set_timing(gn_session* s, int enabled) {
   return guard([&] {
     GN_CHECK(s, "null session");
     s->timing = enabled != 0;
-    s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->gemm_ev_lt.clear();
+    s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->gemm_ev_wide.clear();
     s->attn_events.clear(); s->attn_ev_bytes.clear(); s->attn_ev_launches.clear();
     s->event_next = 0;
   });

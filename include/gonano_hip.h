@@ -404,9 +404,9 @@ typedef struct gn_timing {
   double gemm_ms;           /* GEMM launches inside the train step */
   double gemm_flops;        /* algorithmic flops of those launches */
   int64_t gemm_launches;
-  double gemm_lt_ms;        /* the part of them run by hipBLASLt (plain products) */
-  double gemm_lt_flops;
-  int64_t gemm_lt_launches;
+  double gemm_wide_ms;      /* the part of them run by the wide-tile engine (256x256 tiles) */
+  double gemm_wide_flops;
+  int64_t gemm_wide_launches;
 } gn_timing;
 int gn_session_set_timing(gn_session *session, int enabled);
 int gn_session_get_timing(const gn_session *session, gn_timing *out);

@@ -238,3 +238,22 @@ def test_attention(be, orc, qlen, klen, dim, offset, window, seg):
                              dim, offset, window)
     for g, w, nm in zip(got, want, "qkv"):
         assert_close(g, w, 5e-3, 1e-4, "d" + nm)
+
+
+@pytest.mark.parametrize("m,n,k", [(2000, 6000, 512), (4096, 3072, 768), (256, 12288, 1024)])
+def test_matmul_wide_engine(be, m, n, k):
+    """Products large enough for the 256 x 256-tile engine (at least 192
+    workgroups): MatMulTransposed (x.W^T, both operands K-contiguous) and
+    MatMul (B contiguous in N), against numpy in float64.  2000 x 6000
+    leaves a partial last tile in both dimensions (loaded shifted back to
+    end at M and N, the overlap not stored twice)."""
+    rng = np.random.default_rng(m + n + k)
+    a = rng.standard_normal((m, k)).astype(f32)
+    b = rng.standard_normal((k, n)).astype(f32)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    got = np.zeros((m, n), f32)
+    be.MatMul(got, a, b, m, n, k)
+    assert_close(got, want, 1e-4, 1e-4, "MatMul")
+    got2 = np.zeros((m, n), f32)
+    be.MatMulTransposed(got2, a, np.ascontiguousarray(b.T), m, n, k)
+    assert_close(got2, want, 1e-4, 1e-4, "MatMulTransposed")

@@ -127,7 +127,7 @@ def _compare_grads(cfg, got, w32, w64, tol=1e-4, scalar_tol=5e-4):
     assert not bad, f"{bad}\n{worst}"
 
 
-def _pg_check(orc, cfg, w, B, T, prompt_len, chunk, monkeypatch, seed=7):
+def _pg_check(orc, cfg, w, B, T, prompt_len, chunk, monkeypatch, seed=7, timing=False):
     """PolicyGradientStep on random sequences whose first prompt_len targets
     are ignored (the chat_rl masking); the logits run in chunks of `chunk`
     rows, so several chunks and a partial last one are exercised.  Loss, NLL
@@ -143,10 +143,12 @@ def _pg_check(orc, cfg, w, B, T, prompt_len, chunk, monkeypatch, seed=7):
     monkeypatch.setenv("GN_LOGITS_CHUNK", str(chunk))
     with Session(cfg) as s:
         s.set_params(w)
+        s.set_timing(timing)
         s.zero_grad()
         loss, nll = s.policy_gradient_step(inputs, targets, adv, float(T + 1))
         grads = s.grads()
         aux = s.aux_loss()
+        t = s.timing() if timing else None
     monkeypatch.delenv("GN_LOGITS_CHUNK")
     m32 = _model(orc, cfg, w)
     l32, n32, g32 = m32.pg_step(inputs, targets, adv, float(T + 1))
@@ -159,6 +161,7 @@ def _pg_check(orc, cfg, w, B, T, prompt_len, chunk, monkeypatch, seed=7):
     if cfg.moe:
         assert abs(aux - m32.aux_loss()) <= 1e-6 * max(abs(m32.aux_loss()), 1e-9)
     _compare_grads(cfg, grads, g32, g64)
+    return t
 
 
 # ---- dense d12 width (BASELINE configs[1] at 2 layers, V 4096) -------------
@@ -193,6 +196,27 @@ def test_d12_width_split_combine_rollout(orc, d12w):
 def test_d12_width_pg_step_chunked(orc, d12w, monkeypatch):
     cfg, w = d12w
     _pg_check(orc, cfg, w, B=3, T=300, prompt_len=150, chunk=128, monkeypatch=monkeypatch)
+
+
+def test_d12_width_pg_step_wide_engine(orc, d12w, monkeypatch):
+    """The policy-gradient step with every product the 256 x 256-tile engine
+    can take routed there at any grid size (GN_GEMM_WIDE_MIN=1; the
+    benchmark's 130,816-token products take it by size): 4 x 512 tokens
+    make every M, N >= 256 and every K a multiple of 64, so the instances
+    run are the forward products (plain qkv, residual-add wo, ReLU^2 fc
+    with the saved pre-activation, the proj product as split-K partials
+    with the residual add in the reduction), the input gradients (plain,
+    ReLU^2 backward, split-K partials), the weight gradients (split-K
+    partials over the tokens), and the lm_head forward, input gradient
+    (split over the vocabulary) and weight gradient (accumulated) over two
+    256-row logits chunks."""
+    cfg, w = d12w
+    monkeypatch.setenv("GN_GEMM_WIDE_MIN", "1")
+    t = _pg_check(orc, cfg, w, B=4, T=512, prompt_len=384, chunk=256, monkeypatch=monkeypatch,
+                  timing=True)
+    monkeypatch.delenv("GN_GEMM_WIDE_MIN")
+    # every product of the step ran on the wide engine
+    assert t["gemm_wide_launches"] == t["gemm_launches"], t
 
 
 def test_d12_width_graph_equals_eager(d12w):
@@ -275,7 +299,7 @@ def test_d20_width_rollout_teacher_forced(orc, d20w):
     """512 rows (32 x 16), 520-token prompts, T = 0.8: GQA ratio 5, every
     window in one split of up to 528 keys (the 512-token window admits 513);
     the decode projections at M = 512 take the 32 x 80 / 32 x 112 tiles with
-    deferred split sums or run whole on hipBLASLt."""
+    deferred split sums or run whole on gemm_kernel."""
     cfg, w = d20w
     _rollout_check(orc, cfg, w, 32, 16, 520, 6, 0.8, groups=(0, 31))
 

@@ -1,4 +1,5 @@
-"""The device code carries no wide-store data hazard (gonano_amd/isa_check):
+"""The device code carries no wide-store data hazard and no accumulator access
+too close to an inline-asm MFMA (gonano_amd/isa_check).  Wide stores:
 no store of more than 8 bytes is followed directly by a VALU write to its
 data registers.  The scanner itself is checked on hand-written assembly:
 the buffer-store case measured on MI355X, the global-store form, a write
@@ -49,3 +50,22 @@ def test_library_device_code_has_no_wide_store_hazard():
     except RuntimeError:
         pytest.skip("hipcc not available")
     assert isa_check.check() == []
+
+
+def test_mfma_gap_scanner():
+    """Accumulator reads after an inline-asm MFMA (which the compiler's
+    hazard recognizer does not see): too close on a straight path and
+    across a loop's back edge are found; 16 wait states pass; builtin MFMAs
+    (the compiler's own business) are not checked."""
+    asm_mfma = ";;#ASMSTART\nv_mfma_f32_16x16x4_f32 a[252:255], v1, v2, a[252:255]\n;;#ASMEND"
+    straight = _kernel(asm_mfma + "\ns_add_i32 s1, s2, s3\nv_accvgpr_read_b32 v133, a255")
+    assert len(isa_check.scan_mfma_gaps(straight)) == 1
+    loop = _kernel(".LBB1_2:\ns_min_u32 s8, s30, s42\nv_accvgpr_read_b32 v133, a255\n" + asm_mfma +
+                   "\ns_nop 3\ns_cbranch_scc0 .LBB1_2")
+    assert len(isa_check.scan_mfma_gaps(loop)) == 1
+    assert isa_check.scan_mfma_gaps(loop.replace("s_nop 3", "s_nop 7\n\ts_nop 7")) == []
+    other_reg = _kernel(asm_mfma + "\nv_accvgpr_read_b32 v133, a3")
+    assert isa_check.scan_mfma_gaps(other_reg) == []
+    builtin = _kernel("v_mfma_f32_16x16x4_f32 a[252:255], v1, v2, a[252:255]\n"
+                      "v_accvgpr_read_b32 v133, a255")
+    assert isa_check.scan_mfma_gaps(builtin) == []
