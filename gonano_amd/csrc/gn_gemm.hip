@@ -798,30 +798,72 @@ __device__ __forceinline__ void store4(const GemmParams& p, float* part, int m, 
 
 // The wave's outputs, whose first row and column are mw, nw; rows before m0
 // and columns before n0 (a shifted tile's overlap with the tile before) are
-// skipped.  N % 4 == 0, and nw, n0 are multiples of 4.
+// skipped.  N % 4 == 0, and nw, n0 are multiples of 4.  Epilogues that read
+// (the residual add, the ReLU^2 backward, the accumulate) load one block
+// row ahead: row J+1's 16-byte reads are in flight while row J is combined
+// and stored, instead of a full memory round trip per store.
 template <int E, bool AK, bool BK, int NW, int MI, int NI>
 __device__ __forceinline__ void store_wave(const GemmParams& p, float* part,
                                            const v4f (&acc)[MI][NI], int mw, int nw, int m0,
                                            int n0, int lane) {
   const int q = lane >> 4;
   const bool full = mw >= m0 && nw >= n0;
+  auto row = [&](int J) { return mw + WOp<AK, NW>::row(J, lane & 15); };
+  auto col = [&](int u) {
+    return BK ? nw + 16 * u + 4 * q : nw + 64 * (u >> 2) + 16 * q + 4 * (u & 3);
+  };
+  auto val = [&](int J, int u) {
+    v4f v;
+    if constexpr (BK) {
+      v = acc[J][u];
+    } else {
 #pragma unroll
-  for (int J = 0; J < MI; J++) {
-    const int m = mw + WOp<AK, NW>::row(J, lane & 15);
+      for (int c = 0; c < 4; c++) v[c] = acc[J][4 * (u >> 2) + c][u & 3];
+    }
+    return v;
+  };
+  constexpr bool READS = E == EPI_ADD_SRC || E == EPI_DRELU2 || E == EPI_ACCUM;
+  if constexpr (READS) {
+    const float* src = E == EPI_ACCUM ? p.C : p.aux;
+    const int64_t ld = E == EPI_ACCUM ? p.ldc : p.ldaux;
+    v4f cur[NI], nxt[NI];
 #pragma unroll
-    for (int u = 0; u < NI; u++) {
-      int n;
-      v4f v;
-      if constexpr (BK) {
-        n = nw + 16 * u + 4 * q;
-        v = acc[J][u];
-      } else {
-        const int bb = u >> 2, r = u & 3;
-        n = nw + 64 * bb + 16 * q + 4 * r;
+    for (int u = 0; u < NI; u++)
+      cur[u] = *reinterpret_cast<const v4f*>(&src[(int64_t)row(0) * ld + col(u)]);
 #pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = acc[J][4 * bb + c][r];
+    for (int J = 0; J < MI; J++) {
+      const int m = row(J);
+      if (J + 1 < MI) {
+#pragma unroll
+        for (int u = 0; u < NI; u++)
+          nxt[u] = *reinterpret_cast<const v4f*>(&src[(int64_t)row(J + 1) * ld + col(u)]);
       }
-      if (full || (m >= m0 && n >= n0)) store4<E>(p, part, m, n, v);
+#pragma unroll
+      for (int u = 0; u < NI; u++) {
+        const int n = col(u);
+        const v4f v = val(J, u), x = cur[u];
+        v4f o;
+        if constexpr (E == EPI_DRELU2) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) o[r] = x[r] > 0.f ? (v[r] * 2.f) * x[r] : 0.f;
+        } else {
+          o = x + v;  // ADD_SRC: acc + aux; ACCUM: C + acc (same sum)
+        }
+        if (full || (m >= m0 && n >= n0))
+          *reinterpret_cast<v4f*>(&p.C[(int64_t)m * p.ldc + n]) = o;
+      }
+#pragma unroll
+      for (int u = 0; u < NI; u++) cur[u] = nxt[u];
+    }
+  } else {
+#pragma unroll
+    for (int J = 0; J < MI; J++) {
+      const int m = row(J);
+#pragma unroll
+      for (int u = 0; u < NI; u++) {
+        const int n = col(u);
+        if (full || (m >= m0 && n >= n0)) store4<E>(p, part, m, n, val(J, u));
+      }
     }
   }
 }
