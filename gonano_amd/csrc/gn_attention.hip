@@ -654,24 +654,91 @@ __device__ __forceinline__ void key_range(int q0, int qlast, int Tk, int ratio, 
 }
 
 // ---------------------------------------------------------------------------
-// Flash forward on the matrix cores.  Block: 4 waves x 16 queries of one
-// (sequence, query head); keys in tiles of 64 through LDS (K row-major, V
-// transposed).  Each wave computes S^T = K.Q^T and O^T += V^T.P^T with
-// v_mfma_f32_16x16x4f32, so in both products a lane's column is one query
-// (lane & 15): the running max, the sum and the O rescale stay in the lane,
-// and the P values of a lane are directly the B operand of the second
-// product.  k order inside a 16-key block: MFMA c of the PV product takes
-// key 4*(lane >> 4) + c, which is where the S^T accumulator left it.
+// Flash attention on the matrix cores (training forward, prefill, backward).
+//
+// Operand tiles of FS rows x 128 dims (keys, or queries for dK/dV) go from
+// global memory straight into a two-stage LDS ring (global_load_lds_dwordx4,
+// no VGPR staging; the next tile is in flight while the current one is
+// multiplied, one barrier per tile).  A tile row is 32 16-byte slots, the
+// slot column XOR-swizzled by (row & 15), so both ways the kernels read it
+// are conflict-free ds_read_b128:
+//  * row fragments: 16 rows at one slot column (lane (l16, g) reads row
+//    R0 + l16, dims 4(4s + g) .. + 3) -- the A operand of S^T = K.Q^T,
+//    dP^T = V.dO^T, S = Q.K^T, dP = dO.V^T;
+//  * column fragments: one row, 16 consecutive slots (lane (l16, g) reads
+//    row R, dims 4(16gi + l16) .. + 3) -- the A operand of O^T += V^T.P^T,
+//    dQ^T += K^T.dS^T, dV^T += dO^T.P, dK^T += Q^T.dS.  Component cc of the
+//    read feeds output block (gi, cc), whose row i is dim 64 gi + 4 i + cc,
+//    so a lane's accumulator (gi, cc) register r holds dim 64 gi + 16 g +
+//    4 r + cc: for fixed (gi, r) the four blocks give four consecutive dims,
+//    stored as one 16-byte vector.
+// Rows past the operand's end are clamped to its last row (finite values
+// whose products the mask zeroes).  k order inside a 16-row block: MFMA c
+// takes row 4 (lane >> 4) + c, where the S^T / S accumulators leave it.
 // ---------------------------------------------------------------------------
-static constexpr int FQ = 64;   // queries per block
-static constexpr int FK = 64;   // keys per LDS tile
-static constexpr int FLK = HD + 4;   // K tile row stride (floats)
-static constexpr int FLV = FK + 4;   // V^T tile row stride
+static constexpr int FQ = 64;  // queries per forward / dQ block
+static constexpr int FK = 64;  // keys per dK/dV block
+static constexpr int FS = 32;  // rows per LDS stage
 
+__device__ __forceinline__ void fl_barrier() {
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+__device__ __forceinline__ void fl_wait_all() {
+  __builtin_amdgcn_s_waitcnt((0) | (7 << 4) | (0 << 8));  // vmcnt(0) expcnt(7) lgkmcnt(0)
+}
+
+typedef __attribute__((address_space(3))) void fl_lds_void;
+
+// FS rows into stage S by 256 threads: instruction t of wave w fills slots
+// (4t + w) 64 .. + 63, i.e. rows 2(4t + w) + (lane >> 5), physical slot
+// lane & 31 holding logical slot (lane & 31) ^ (row & 15).  rowptr(r) is
+// the first float of tile row r (already clamped).
+template <class RowPtr>
+__device__ __forceinline__ void fl_stage_load(float* S, RowPtr rowptr, int w, int lane) {
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int row = 2 * (4 * t + w) + (lane >> 5);
+    const int slot = (lane & 31) ^ (row & 15);
+    __builtin_amdgcn_global_load_lds((const void*)(rowptr(row) + 4 * slot),
+                                     (fl_lds_void*)(S + 4 * ((4 * t + w) * 64)), 16, 0, 0);
+  }
+}
+// Row fragment: row r0 + l16 (r0 % 16 == 0), logical slot 4s + g.
+__device__ __forceinline__ v4f fl_row(const float* S, int r0, int s, int l16, int g) {
+  return *reinterpret_cast<const v4f*>(&S[(r0 + l16) * HD + 4 * ((4 * s + g) ^ l16)]);
+}
+// Column fragment: row r, logical slot 16 gi + l16.
+__device__ __forceinline__ v4f fl_col(const float* S, int r, int gi, int l16) {
+  return *reinterpret_cast<const v4f*>(&S[r * HD + 4 * ((16 * gi + l16) ^ (r & 15))]);
+}
+// Store a column-fragment accumulator [2][4] of one lane's row at p (the
+// row's first dim): dims 64 gi + 16 g + 4 r + cc; add: p[] += acc.
+__device__ __forceinline__ void fl_store_cols(float* p, const v4f (&acc)[2][4], int g, bool add,
+                                              float scale) {
+#pragma unroll
+  for (int gi = 0; gi < 2; gi++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      v4f v = {acc[gi][0][r], acc[gi][1][r], acc[gi][2][r], acc[gi][3][r]};
+      float* q = p + 64 * gi + 16 * g + 4 * r;
+      v = v * scale;
+      if (add) v = *reinterpret_cast<const v4f*>(q) + v;
+      *reinterpret_cast<v4f*>(q) = v;
+    }
+}
+
+// Forward.  Block: 4 waves x 16 queries of one (sequence, query head); each
+// wave computes S^T = K.Q^T and O^T += V^T.P^T, a lane's column being its
+// query (lane & 15): the running max, the sum and the O rescale stay in the
+// lane, and its P values are the B operand of the second product directly.
 __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
-  __shared__ __attribute__((aligned(16))) float Ks[FK * FLK];
-  __shared__ __attribute__((aligned(16))) float Vt[HD * FLV];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ __attribute__((aligned(16))) float Ks0[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Vs0[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Ks1[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Vs1[FS * HD];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
   const int q0 = blockIdx.x * FQ;
   const int bh = blockIdx.y, b = bh / a.Hq, qh = bh % a.Hq;
@@ -686,49 +753,38 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
 #pragma unroll
     for (int s = 0; s < 8; s++) qf[s] = *reinterpret_cast<const v4f*>(qp + 16 * s);
   }
-  v4f acc[8];  // O^T[16i + 4g + r][t]
+  v4f acc[2][4];  // O^T, column-fragment layout
 #pragma unroll
-  for (int i = 0; i < 8; i++) acc[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int gi = 0; gi < 2; gi++)
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) acc[gi][cc] = (v4f){0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
 
   const int qlast = min(a.T, q0 + FQ) - 1;
   int kmin, kmax;
   key_range(q0, qlast, a.Tk, a.ratio, a.window, a.qoff, &kmin, &kmax);
-  for (int kt = (kmin / FK) * FK; kt < kmax; kt += FK) {
-    __syncthreads();  // previous tile fully consumed
-    // K tile rows (coalesced float4), V tile transposed into Vt[d][key]
+  const int kt0 = (kmin / FS) * FS;
+  const int ntile = kmax > kt0 ? (kmax - kt0 + FS - 1) / FS : 0;
+  const float* kbase = a.k + ((int64_t)b * a.Tk * a.Hkv + hk) * HD;
+  const float* vbase = a.v + ((int64_t)b * a.Tk * a.Hkv + hk) * HD;
+  const int64_t kvstride = (int64_t)a.Hkv * HD;
+  auto load = [&](int i, float* KS, float* VS) {
+    const int kt = kt0 + i * FS;
+    fl_stage_load(KS, [&](int r) { return kbase + min(kt + r, a.Tk - 1) * kvstride; }, w, lane);
+    fl_stage_load(VS, [&](int r) { return vbase + min(kt + r, a.Tk - 1) * kvstride; }, w, lane);
+  };
+  auto tile = [&](int i, const float* KS, const float* VS, float* XK, float* XV) {
+    fl_wait_all();  // tile i (the only loads in flight) landed
+    fl_barrier();   // ... for every wave; the other stage is no longer read
+    if (i + 1 < ntile) load(i + 1, XK, XV);
+    const int kt = kt0 + i * FS;
+    v4f st[FS / 16];  // S^T[kt + 16kb + 4g + r][t]
 #pragma unroll
-    for (int i = 0; i < FK * HD / 4 / 256; i++) {
-      const int idx = tid + 256 * i;
-      const int kr = idx >> 5, c4 = idx & 31;
-      const int kj = kt + kr;
-      v4f kv = {0.f, 0.f, 0.f, 0.f};
-      if (kj < a.Tk) kv = *reinterpret_cast<const v4f*>(
-          a.k + (((int64_t)b * a.Tk + kj) * a.Hkv + hk) * HD + 4 * c4);
-      *reinterpret_cast<v4f*>(&Ks[kr * FLK + 4 * c4]) = kv;
-    }
-#pragma unroll
-    for (int i = 0; i < FK * HD / 4 / 256; i++) {
-      const int idx = tid + 256 * i;
-      const int kr = idx & 63, c4 = idx >> 6;  // lanes walk keys: conflict-free stores
-      const int kj = kt + kr;
-      v4f vv = {0.f, 0.f, 0.f, 0.f};
-      if (kj < a.Tk) vv = *reinterpret_cast<const v4f*>(
-          a.v + (((int64_t)b * a.Tk + kj) * a.Hkv + hk) * HD + 4 * c4);
-#pragma unroll
-      for (int j = 0; j < 4; j++) Vt[(4 * c4 + j) * FLV + kr] = vv[j];
-    }
-    __syncthreads();
-
-    // S^T for the tile: st[kb] = S^T[kt + 16kb + 4g + r][t]
-    v4f st[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++) {
+    for (int kb = 0; kb < FS / 16; kb++) {
       st[kb] = (v4f){0.f, 0.f, 0.f, 0.f};
-      const float* kp = &Ks[(16 * kb + l16) * FLK + 4 * g];
 #pragma unroll
       for (int s = 0; s < 8; s++) {
-        const v4f kf = *reinterpret_cast<const v4f*>(kp + 16 * s);
+        const v4f kf = fl_row(KS, 16 * kb, s, l16, g);
 #pragma unroll
         for (int c = 0; c < 4; c++)
           st[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[c], qf[s][c], st[kb], 0, 0, 0);
@@ -737,7 +793,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
     // mask, online softmax (the lane's column is query t)
     float tmax = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++)
+    for (int kb = 0; kb < FS / 16; kb++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int kj = kt + 16 * kb + 4 * g + r;
@@ -751,7 +807,7 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
       const float sc = expf(m - mn);  // 0 while m is -inf
       float ps = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++)
+      for (int kb = 0; kb < FS / 16; kb++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float p = expf(st[kb][r] - mn);  // masked: exp(-inf) = 0
@@ -763,28 +819,36 @@ __global__ __launch_bounds__(256, 2) void flash_fwd_mfma_kernel(FlashArgs a) {
       l = l * sc + ps;
       m = mn;
 #pragma unroll
-      for (int i = 0; i < 8; i++) acc[i] *= sc;
+      for (int gi = 0; gi < 2; gi++)
+#pragma unroll
+        for (int cc = 0; cc < 4; cc++) acc[gi][cc] *= sc;
     } else {
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++) st[kb] = (v4f){0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < FS / 16; kb++) st[kb] = (v4f){0.f, 0.f, 0.f, 0.f};
     }
     // O^T += V^T P^T
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++)
+    for (int kb = 0; kb < FS / 16; kb++)
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const v4f vf = *reinterpret_cast<const v4f*>(&Vt[(16 * i + l16) * FLV + 16 * kb + 4 * g]);
+      for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-          acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[c], st[kb][c], acc[i], 0, 0, 0);
-      }
+        for (int gi = 0; gi < 2; gi++) {
+          const v4f vf = fl_col(VS, 16 * kb + 4 * g + c, gi, l16);
+#pragma unroll
+          for (int cc = 0; cc < 4; cc++)
+            acc[gi][cc] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[cc], st[kb][c], acc[gi][cc],
+                                                               0, 0, 0);
+        }
+  };
+  if (ntile > 0) load(0, Ks0, Vs0);
+  for (int i = 0; i < ntile; i += 2) {
+    tile(i, Ks0, Vs0, Ks1, Vs1);
+    if (i + 1 < ntile) tile(i + 1, Ks1, Vs1, Ks0, Vs0);
   }
   if (active) {
     // l == 0: no visible key (compressed attention before the first block)
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    float* op = a.o + (((int64_t)b * a.T + t) * a.Hq + qh) * HD + 4 * g;
-#pragma unroll
-    for (int i = 0; i < 8; i++) *reinterpret_cast<v4f*>(op + 16 * i) = acc[i] * inv;
+    fl_store_cols(a.o + (((int64_t)b * a.T + t) * a.Hq + qh) * HD, acc, g, false, inv);
     if (a.lse && g == 0)
       a.lse[((int64_t)b * a.T + t) * a.Hq + qh] = l > 0.f ? m + logf(l) : -INFINITY;
   }
@@ -827,9 +891,12 @@ __global__ __launch_bounds__(256) void flash_delta_kernel(const float* __restric
 // of a 16 block), so no accumulator is transposed through LDS.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs a) {
-  __shared__ __attribute__((aligned(16))) float Ks[FK * FLK];
-  __shared__ __attribute__((aligned(16))) float Vs[FK * FLK];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ __attribute__((aligned(16))) float Ks0[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Vs0[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Ks1[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Vs1[FS * HD];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
   const int q0 = blockIdx.x * FQ;
   const int bh = blockIdx.y, b = bh / a.Hq, qh = bh % a.Hq;
@@ -844,39 +911,37 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
     gf[s] = *reinterpret_cast<const v4f*>(a.dout + qrow * HD + 16 * s + 4 * g);
   }
   const float lse = a.lse[qrow], dl = a.delta[qrow];
-  v4f dq[8];  // dQ^T[16i + 4g + r][t]
+  v4f dq[2][4];  // dQ^T, column-fragment layout
 #pragma unroll
-  for (int i = 0; i < 8; i++) dq[i] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int gi = 0; gi < 2; gi++)
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) dq[gi][cc] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   const int qlast = min(a.T, q0 + FQ) - 1;
   int kmin, kmax;
   key_range(q0, qlast, a.Tk, a.ratio, a.window, a.qoff, &kmin, &kmax);
-  for (int kt = (kmin / FK) * FK; kt < kmax; kt += FK) {
-    __syncthreads();
+  const int kt0 = (kmin / FS) * FS;
+  const int ntile = kmax > kt0 ? (kmax - kt0 + FS - 1) / FS : 0;
+  const float* kbase = a.k + ((int64_t)b * a.Tk * a.Hkv + hk) * HD;
+  const float* vbase = a.v + ((int64_t)b * a.Tk * a.Hkv + hk) * HD;
+  const int64_t kvstride = (int64_t)a.Hkv * HD;
+  auto load = [&](int i, float* KS, float* VS) {
+    const int kt = kt0 + i * FS;
+    fl_stage_load(KS, [&](int r) { return kbase + min(kt + r, a.Tk - 1) * kvstride; }, w, lane);
+    fl_stage_load(VS, [&](int r) { return vbase + min(kt + r, a.Tk - 1) * kvstride; }, w, lane);
+  };
+  auto tile = [&](int i, const float* KS, const float* VS, float* XK, float* XV) {
+    fl_wait_all();
+    fl_barrier();
+    if (i + 1 < ntile) load(i + 1, XK, XV);
+    const int kt = kt0 + i * FS;
 #pragma unroll
-    for (int i = 0; i < FK * HD / 4 / 256; i++) {
-      const int idx = tid + 256 * i;
-      const int kr = idx >> 5, c4 = idx & 31;
-      const int kj = kt + kr;
-      v4f kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
-      if (kj < a.Tk) {
-        const int64_t off = (((int64_t)b * a.Tk + kj) * a.Hkv + hk) * HD + 4 * c4;
-        kv = *reinterpret_cast<const v4f*>(a.k + off);
-        vv = *reinterpret_cast<const v4f*>(a.v + off);
-      }
-      *reinterpret_cast<v4f*>(&Ks[kr * FLK + 4 * c4]) = kv;
-      *reinterpret_cast<v4f*>(&Vs[kr * FLK + 4 * c4]) = vv;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kb = 0; kb < FK / 16; kb++) {
+    for (int kb = 0; kb < FS / 16; kb++) {
       v4f st = {0.f, 0.f, 0.f, 0.f}, dpt = {0.f, 0.f, 0.f, 0.f};
-      const float* kp = &Ks[(16 * kb + l16) * FLK + 4 * g];
-      const float* vp = &Vs[(16 * kb + l16) * FLK + 4 * g];
 #pragma unroll
       for (int s = 0; s < 8; s++) {
-        const v4f kf = *reinterpret_cast<const v4f*>(kp + 16 * s);
-        const v4f vf = *reinterpret_cast<const v4f*>(vp + 16 * s);
+        const v4f kf = fl_row(KS, 16 * kb, s, l16, g);
+        const v4f vf = fl_row(VS, 16 * kb, s, l16, g);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           st = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[c], qf[s][c], st, 0, 0, 0);
@@ -887,36 +952,43 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dq_mfma_kernel(FlashBwdArgs 
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int kj = kt + 16 * kb + 4 * g + r;
-        const float p = (active && key_ok(kj, t, a.Tk, a.ratio, a.window, a.qoff)) ? expf(st[r] - lse) : 0.f;
+        const float p =
+            (active && key_ok(kj, t, a.Tk, a.ratio, a.window, a.qoff)) ? expf(st[r] - lse) : 0.f;
         ds[r] = p * (dpt[r] - dl);
       }
-      // dQ^T += K^T dS^T: A = K[16kb + 4g + c][16i + l16]
+      // dQ^T += K^T dS^T: A = K^T, column fragments of key rows 16kb + 4g + c
 #pragma unroll
-      for (int i = 0; i < 8; i++)
+      for (int c = 0; c < 4; c++)
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-          dq[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-              Ks[(16 * kb + 4 * g + c) * FLK + 16 * i + l16], ds[c], dq[i], 0, 0, 0);
+        for (int gi = 0; gi < 2; gi++) {
+          const v4f kc = fl_col(KS, 16 * kb + 4 * g + c, gi, l16);
+#pragma unroll
+          for (int cc = 0; cc < 4; cc++)
+            dq[gi][cc] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[cc], ds[c], dq[gi][cc], 0, 0, 0);
+        }
     }
+  };
+  if (ntile > 0) load(0, Ks0, Vs0);
+  for (int i = 0; i < ntile; i += 2) {
+    tile(i, Ks0, Vs0, Ks1, Vs1);
+    if (i + 1 < ntile) tile(i + 1, Ks1, Vs1, Ks0, Vs0);
   }
-  if (active) {
-    float* op = a.dq + qrow * HD + 4 * g;
-    if (a.dq_accum) {
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-        *reinterpret_cast<v4f*>(op + 16 * i) = *reinterpret_cast<const v4f*>(op + 16 * i) + dq[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) *reinterpret_cast<v4f*>(op + 16 * i) = dq[i];
-    }
-  }
+  if (active) fl_store_cols(a.dq + qrow * HD, dq, g, a.dq_accum, 1.f);
 }
 
+// dK/dV.  Block: 4 waves x 16 keys of one (sequence, KV head), over every
+// query head of the GQA group and the query tiles that see the keys; S and
+// dP come out with the lane's column = its key, so P and dS feed dV^T +=
+// dO^T.P and dK^T += Q^T.dS as B operands straight from the lane.
 __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArgs a) {
-  __shared__ __attribute__((aligned(16))) float Qs[FQ * FLK];
-  __shared__ __attribute__((aligned(16))) float Gs[FQ * FLK];
-  __shared__ float Ls[FQ], Ds[FQ];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ __attribute__((aligned(16))) float Qs0[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Gs0[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Qs1[FS * HD];
+  __shared__ __attribute__((aligned(16))) float Gs1[FS * HD];
+  // per stage: the tile's log-sum-exp [0, FS) and delta [FS, 2 FS)
+  __shared__ __attribute__((aligned(16))) float LD[2][2 * FS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
   const int k0 = blockIdx.x * FK;
   const int bk = blockIdx.y, b = bk / a.Hkv, hk = bk % a.Hkv;
@@ -930,12 +1002,14 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
     kf[s] = *reinterpret_cast<const v4f*>(a.k + krow * HD + 16 * s + 4 * g);
     vf[s] = *reinterpret_cast<const v4f*>(a.v + krow * HD + 16 * s + 4 * g);
   }
-  v4f dk[8], dv[8];  // dK^T, dV^T [16i + 4g + r][j]
+  v4f dk[2][4], dv[2][4];  // dK^T, dV^T, column-fragment layout
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    dk[i] = (v4f){0.f, 0.f, 0.f, 0.f};
-    dv[i] = (v4f){0.f, 0.f, 0.f, 0.f};
-  }
+  for (int gi = 0; gi < 2; gi++)
+#pragma unroll
+    for (int cc = 0; cc < 4; cc++) {
+      dk[gi][cc] = (v4f){0.f, 0.f, 0.f, 0.f};
+      dv[gi][cc] = (v4f){0.f, 0.f, 0.f, 0.f};
+    }
   const int klast = min(a.Tk, k0 + FK) - 1;
   // queries that can see a key of the block: [qbeg, qend)
   int qbeg, qend;
@@ -946,75 +1020,73 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_mfma_kernel(FlashBwdArg
     qbeg = k0;
     qend = a.window >= 0 ? min(a.T, klast + a.window + 1) : a.T;
   }
-  for (int h = 0; h < r; h++) {
-    const int qh = hk * r + h;
-    for (int qt = (qbeg / FQ) * FQ; qt < qend; qt += FQ) {
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < FQ * HD / 4 / 256; i++) {
-        const int idx = tid + 256 * i;
-        const int qr = idx >> 5, c4 = idx & 31;
-        const int tq = qt + qr;
-        v4f qv = {0.f, 0.f, 0.f, 0.f}, gv = {0.f, 0.f, 0.f, 0.f};
-        if (tq < a.T) {
-          const int64_t off = (((int64_t)b * a.T + tq) * a.Hq + qh) * HD + 4 * c4;
-          qv = *reinterpret_cast<const v4f*>(a.q + off);
-          gv = *reinterpret_cast<const v4f*>(a.dout + off);
-        }
-        *reinterpret_cast<v4f*>(&Qs[qr * FLK + 4 * c4]) = qv;
-        *reinterpret_cast<v4f*>(&Gs[qr * FLK + 4 * c4]) = gv;
-      }
-      if (tid < FQ) {
-        const int tq = qt + tid;
-        const int64_t row = ((int64_t)b * a.T + min(tq, a.T - 1)) * a.Hq + qh;
-        Ls[tid] = a.lse[row];
-        Ds[tid] = a.delta[row];
-      }
-      __syncthreads();
-#pragma unroll
-      for (int qb = 0; qb < FQ / 16; qb++) {
-        v4f sv = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
-        const float* qp = &Qs[(16 * qb + l16) * FLK + 4 * g];
-        const float* gp = &Gs[(16 * qb + l16) * FLK + 4 * g];
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-          const v4f qv = *reinterpret_cast<const v4f*>(qp + 16 * s);
-          const v4f gv = *reinterpret_cast<const v4f*>(gp + 16 * s);
-#pragma unroll
-          for (int c = 0; c < 4; c++) {
-            sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[c], kf[s][c], sv, 0, 0, 0);
-            dp = __builtin_amdgcn_mfma_f32_16x16x4f32(gv[c], vf[s][c], dp, 0, 0, 0);
-          }
-        }
-        // S[q][j], dP[q][j] for q = qt + 16qb + 4g + rr
-        v4f p, ds;
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-          const int ql = 16 * qb + 4 * g + rr, tq = qt + ql;
-          const bool ok = active && tq < a.T && key_ok(j, tq, a.Tk, a.ratio, a.window, a.qoff);
-          p[rr] = ok ? expf(sv[rr] - Ls[ql]) : 0.f;
-          ds[rr] = p[rr] * (dp[rr] - Ds[ql]);
-        }
-        // dV^T += dO^T P, dK^T += Q^T dS: A = X[16qb + 4g + c][16i + l16]
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-#pragma unroll
-          for (int c = 0; c < 4; c++) {
-            const int row = (16 * qb + 4 * g + c) * FLK + 16 * i + l16;
-            dv[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(Gs[row], p[c], dv[i], 0, 0, 0);
-            dk[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[row], ds[c], dk[i], 0, 0, 0);
-          }
-      }
+  const int qt0 = (qbeg / FS) * FS;
+  const int nq = qend > qt0 ? (qend - qt0 + FS - 1) / FS : 0;
+  const int ntile = nq * r;  // (head, query tile) pairs, head-major
+  const int64_t qstride = (int64_t)a.Hq * HD;
+  auto load = [&](int i, float* QS, float* GS, int st) {
+    const int qh = hk * r + i / nq, qt = qt0 + (i % nq) * FS;
+    const float* qb = a.q + ((int64_t)b * a.T * a.Hq + qh) * HD;
+    const float* gb = a.dout + ((int64_t)b * a.T * a.Hq + qh) * HD;
+    fl_stage_load(QS, [&](int rr) { return qb + min(qt + rr, a.T - 1) * qstride; }, w, lane);
+    fl_stage_load(GS, [&](int rr) { return gb + min(qt + rr, a.T - 1) * qstride; }, w, lane);
+    if (w == 0) {  // one dword per lane: lse of rows [0, FS), then delta
+      const int64_t row = ((int64_t)b * a.T + min(qt + (lane & (FS - 1)), a.T - 1)) * a.Hq + qh;
+      __builtin_amdgcn_global_load_lds((const void*)((lane < FS ? a.lse : a.delta) + row),
+                                       (fl_lds_void*)&LD[st][0], 4, 0, 0);
     }
+  };
+  auto tile = [&](int i, const float* QS, const float* GS, int st, float* XQ, float* XG) {
+    fl_wait_all();
+    fl_barrier();
+    if (i + 1 < ntile) load(i + 1, XQ, XG, st ^ 1);
+    const int qt = qt0 + (i % nq) * FS;
+#pragma unroll
+    for (int qb = 0; qb < FS / 16; qb++) {
+      v4f sv = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        const v4f qv = fl_row(QS, 16 * qb, s, l16, g);
+        const v4f gv = fl_row(GS, 16 * qb, s, l16, g);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          sv = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[c], kf[s][c], sv, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_16x16x4f32(gv[c], vf[s][c], dp, 0, 0, 0);
+        }
+      }
+      // S[q][j], dP[q][j] for q = qt + 16qb + 4g + rr
+      v4f p, ds;
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        const int ql = 16 * qb + 4 * g + rr, tq = qt + ql;
+        const bool ok = active && tq < a.T && key_ok(j, tq, a.Tk, a.ratio, a.window, a.qoff);
+        p[rr] = ok ? expf(sv[rr] - LD[st][ql]) : 0.f;
+        ds[rr] = p[rr] * (dp[rr] - LD[st][FS + ql]);
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS: column fragments of query rows 16qb + 4g + c
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int gi = 0; gi < 2; gi++) {
+          const int row = 16 * qb + 4 * g + c;
+          const v4f gc = fl_col(GS, row, gi, l16);
+          const v4f qc = fl_col(QS, row, gi, l16);
+#pragma unroll
+          for (int cc = 0; cc < 4; cc++) {
+            dv[gi][cc] = __builtin_amdgcn_mfma_f32_16x16x4f32(gc[cc], p[c], dv[gi][cc], 0, 0, 0);
+            dk[gi][cc] = __builtin_amdgcn_mfma_f32_16x16x4f32(qc[cc], ds[c], dk[gi][cc], 0, 0, 0);
+          }
+        }
+    }
+  };
+  if (ntile > 0) load(0, Qs0, Gs0, 0);
+  for (int i = 0; i < ntile; i += 2) {
+    tile(i, Qs0, Gs0, 0, Qs1, Gs1);
+    if (i + 1 < ntile) tile(i + 1, Qs1, Gs1, 1, Qs0, Gs0);
   }
   if (active) {
-    float* kp = a.dk + krow * HD + 4 * g;
-    float* vp = a.dv + krow * HD + 4 * g;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      *reinterpret_cast<v4f*>(kp + 16 * i) = dk[i];
-      *reinterpret_cast<v4f*>(vp + 16 * i) = dv[i];
-    }
+    fl_store_cols(a.dk + krow * HD, dk, g, false, 1.f);
+    fl_store_cols(a.dv + krow * HD, dv, g, false, 1.f);
   }
 }
 
