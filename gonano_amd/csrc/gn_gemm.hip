@@ -1070,6 +1070,308 @@ static bool gemm_wide(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// Slim-tile engine for the decode projections: x.W^T (both operands
+// K-contiguous) with M the decode batch (a few hundred rows), where the
+// whole product is a few microseconds of MFMA work spread over 256 CUs.
+//
+// One 32 x BN output tile (BN = 96, 128 or 160) per workgroup of four waves
+// (2 x 2), each wave owning 16 rows x BN/2 columns: BN/32 accumulator
+// blocks, in AGPRs, by the same in-place inline-asm MFMAs as the wide
+// engine.  A workgroup's K range is short (a few dozen 32-deep tiles), so
+// what bounds it is the latency of the first loads and of every tile's
+// loads behind the MFMAs: the tiles go through an S-stage LDS ring (S - 1
+// tiles in flight, one 16-24 KB stage each, up to 144 KB), enough to cover
+// ~2 us of load latency with MFMA work at one workgroup per CU.
+//
+// Pipeline, K tile kt in stage kt % S (its group-0 fragments in registers):
+//   the group-0 MFMAs, with the group-1 fragment reads of tile kt between
+//   wait (own LDS reads; tile kt+1's loads), barrier
+//   the group-1 MFMAs, with the loads of tile kt+S into stage kt % S and
+//   the group-0 fragment reads of tile kt+1 between
+// Every stage is its own LDS array (the loop is unrolled S times), so the
+// compiler can tell that the reads of one stage do not alias the loads in
+// flight into the others and inserts no wait for them.
+//
+// Split K ranges either go to a consumer that sums them (deferred sums,
+// PendingSum) or to gemm_reduce_kernel, both in float64 in split order.
+// ---------------------------------------------------------------------------
+namespace slim {
+
+constexpr int BM = 32;  // tile rows
+constexpr int TK = 32;  // K depth of one LDS stage
+constexpr int NW = 4;   // waves per workgroup (2 x 2)
+constexpr int MAXS = 8;  // deepest ring
+
+// One K-contiguous operand of R rows (R a multiple of 32) in an LDS stage:
+// [R][TK] floats, 8 16-byte slots per row, the slot column XOR-swizzled by
+// (row & 7) so that the fragment reads (16 rows x 4 k per 16 lanes) hit
+// distinct banks.  DMA instruction t of wave w fills slots (t NW + w) 64 ..
+// + 63, i.e. rows 8 (t NW + w) .. + 7, lane l taking row + (l >> 3) and
+// logical slot (l & 7) ^ (l >> 3); one 32-bit lane offset from the tile
+// corner serves every instruction (a uniform row step apart).
+template <int R>
+struct SOp {
+  static_assert(R % 32 == 0, "operand rows");
+  static constexpr int NI = R / 32;  // DMA instructions per thread and stage
+  static __device__ __forceinline__ uint32_t lane_off(int64_t ld, int tid) {
+    const int w = tid >> 6, l = tid & 63;
+    return (uint32_t)(((int64_t)(w * 8 + (l >> 3)) * ld + 4 * ((l & 7) ^ (l >> 3))) * 4);
+  }
+  static __device__ __forceinline__ void dma_one(const char* corner, uint32_t off, int64_t step,
+                                                 float* S, int w, int t) {
+    __builtin_amdgcn_global_load_lds((const void*)(corner + t * step + off),
+                                     (lds_void*)(S + 4 * ((t * NW + w) * 64)), 16, 0, 0);
+  }
+  // LDS float offset of lane's fragment read of k group g, rows d .. d + 15
+  // (d a multiple of 16)
+  static __device__ __forceinline__ int frag_off(int d, int g, int lane) {
+    const int i = lane & 15, q = lane >> 4;
+    return (d + i) * TK + 4 * ((4 * g + q) ^ (i & 7));
+  }
+};
+
+// Zeros standing in for the K tiles past the end of a workgroup's range (up
+// to 160 rows of one TK-deep tile, row stride TK); never written.
+__device__ __attribute__((aligned(16))) float zero_tile[160 * TK];
+
+// Calls f(integral_constant<I>) for I = 0 .. N-1.
+template <int I, int N, class F>
+__device__ __forceinline__ void unroll(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    unroll<I + 1, N>(f);
+  }
+}
+
+// The K loop runs a whole number of rounds of S tiles with no branch inside
+// (a branch between the loads and the reads of the ring would make the
+// compiler wait for every load in flight before the reads); the tiles past
+// the workgroup's range are loaded from zero_tile and add nothing.
+template <int BN, int S, int E>
+__global__ __launch_bounds__(64 * NW, 1) void gemm_slim_kernel(GemmParams p) {
+  constexpr int NB = BN / 32;  // accumulator blocks per wave (16 x 16 NB wave tile)
+  constexpr int SZ = (BM + BN) * TK;
+  using LA = SOp<BM>;
+  using LB = SOp<BN>;
+  constexpr int PT = LA::NI + LB::NI;  // DMA instructions per thread and stage
+  static_assert(S >= 2 && S <= MAXS && PT * (S - 1) < 64, "ring depth");
+  static_assert(BN <= 160, "zero tile rows");
+  static_assert(4 * NB - 1 >= PT + 1 + NB, "memory operations fit between the group's MFMAs");
+  __shared__ __attribute__((aligned(16))) float S0[SZ], S1[SZ], S2[SZ], S3[SZ], S4[SZ], S5[SZ],
+      S6[SZ], S7[SZ];
+  auto stage = [&](auto I) -> float* {
+    constexpr int i = decltype(I)::value % S;
+    if constexpr (i == 0) return S0;
+    else if constexpr (i == 1) return S1;
+    else if constexpr (i == 2) return S2;
+    else if constexpr (i == 3) return S3;
+    else if constexpr (i == 4) return S4;
+    else if constexpr (i == 5) return S5;
+    else if constexpr (i == 6) return S6;
+    else return S7;
+  };
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w & 1, wn = w >> 1;
+  int tm, tn, split;
+  tile_coords(p, tm, tn, split);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = split * p.k_per_split, kend = min(p.K, kbeg + p.k_per_split);
+  const int nkt = (kend - kbeg) / TK;  // >= 1 (host)
+  const uint32_t offa = LA::lane_off(p.lda, tid), offb = LB::lane_off(p.ldb, tid);
+  const uint32_t offz = LA::lane_off(TK, tid);  // the same map over zero_tile
+  const int64_t sa = (int64_t)NW * 8 * p.lda * 4, sb = (int64_t)NW * 8 * p.ldb * 4;
+  constexpr int64_t sz = (int64_t)NW * 8 * TK * 4;
+  const char* zero = reinterpret_cast<const char*>(zero_tile);
+  // DMA instruction o (< PT) of K tile kt into stage X: selects, not
+  // branches, between the operands and the zeros
+  auto dma = [&](int kt, float* X, int o) {
+    const bool real = kt < nkt;
+    if (o < LA::NI) {
+      const char* c = reinterpret_cast<const char*>(p.A + (int64_t)m0 * p.lda + kbeg + kt * TK);
+      LA::dma_one(real ? c : zero, real ? offa : offz, real ? sa : sz, X, w, o);
+    } else {
+      const char* c = reinterpret_cast<const char*>(p.B + (int64_t)n0 * p.ldb + kbeg + kt * TK);
+      LB::dma_one(real ? c : zero, real ? offb : offz, real ? sb : sz, X + BM * TK, w,
+                  o - LA::NI);
+    }
+  };
+  const int fa_0 = LA::frag_off(16 * wm, 0, lane), fa_1 = LA::frag_off(16 * wm, 1, lane);
+  const int fb_0 = BM * TK + LB::frag_off(16 * NB * wn, 0, lane);
+  const int fb_1 = BM * TK + LB::frag_off(16 * NB * wn, 1, lane);
+
+  v4f acc[1][NB];
+#pragma unroll
+  for (int I = 0; I < NB; I++) acc[0][I] = (v4f){0.f, 0.f, 0.f, 0.f};
+  v4f fa0[1], fb0[NB], fa1[1], fb1[NB];
+  // the first S tiles
+  unroll<0, S>([&](auto I) {
+#pragma unroll
+    for (int o = 0; o < PT; o++) dma(decltype(I)::value, stage(I), o);
+  });
+  wait_vm_lgkm0<PT * (S - 1)>();
+  tile_barrier();
+  {
+    const float* X = stage(std::integral_constant<int, 0>{});
+    fa0[0] = *reinterpret_cast<const v4f*>(&X[fa_0]);
+#pragma unroll
+    for (int u = 0; u < NB; u++) fb0[u] = *reinterpret_cast<const v4f*>(&X[fb_0 + 16 * u * TK]);
+  }
+  for (int kt0 = 0; kt0 < nkt; kt0 += S) {
+    unroll<0, S>([&](auto I) {
+      const int kt = kt0 + decltype(I)::value;
+      float* C = stage(I);
+      const float* X = stage(std::integral_constant<int, decltype(I)::value + 1>{});
+      wide::group_mma<true, true, NW>(acc, fa0, fb0, [&](int n) {
+        const int o = n - 1;
+        if (o == 0) fa1[0] = *reinterpret_cast<const v4f*>(&C[fa_1]);
+        else if (o >= 1 && o <= NB)
+          fb1[o - 1] = *reinterpret_cast<const v4f*>(&C[fb_1 + 16 * (o - 1) * TK]);
+      });
+      // own fragment reads done; tile kt+1 landed (tiles kt+2 .. kt+S-1 may
+      // still be in flight)
+      wait_vm_lgkm0<PT * (S - 2)>();
+      tile_barrier();
+      // stage C is free: every wave holds tile kt's group-1 fragments
+      wide::group_mma<true, true, NW>(acc, fa1, fb1, [&](int n) {
+        const int o = n - 1;
+        if (o >= 0 && o < PT) dma(kt + S, C, o);
+        else if (o == PT) fa0[0] = *reinterpret_cast<const v4f*>(&X[fa_0]);
+        else if (o > PT && o <= PT + NB)
+          fb0[o - PT - 1] = *reinterpret_cast<const v4f*>(&X[fb_0 + 16 * (o - PT - 1) * TK]);
+      });
+    });
+    // wait states between the last MFMAs and any accumulator copy the
+    // compiler places at the loop's head
+    asm volatile("s_nop 7\n\ts_nop 7");
+  }
+  // the loads issued past the last round (a workgroup must not end with LDS
+  // writes in flight); then wait states before the accumulators are read
+  wait_vm_lgkm0<0>();
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+  float* part = E == -1 ? p.part + (int64_t)split * p.M * p.N : nullptr;
+  const int mw = m0 + 16 * wm, nw = n0 + 16 * NB * wn;
+  wide::store_wave<E, true, true, NW>(p, part, acc, mw, nw, mw, nw, lane);
+}
+
+}  // namespace slim
+
+typedef void (*SlimKernel)(GemmParams);
+template <int BN, int S>
+static SlimKernel slim_kernel_s(int e) {
+  using namespace slim;
+  switch (e) {
+    case -1: return gemm_slim_kernel<BN, S, -1>;
+    case EPI_STORE: return gemm_slim_kernel<BN, S, EPI_STORE>;
+    case EPI_ADD_SRC: return gemm_slim_kernel<BN, S, EPI_ADD_SRC>;
+    case EPI_RELU2_SAVE: return gemm_slim_kernel<BN, S, EPI_RELU2_SAVE>;
+    case EPI_RELU2_SAVE + 16: return gemm_slim_kernel<BN, S, EPI_RELU2_SAVE + 16>;
+  }
+  return nullptr;
+}
+// Ring depth per tile width: the deepest that fits 160 KB of LDS (16, 20
+// and 24 KB stages).
+static int slim_depth(int bn) { return bn == 96 ? 8 : bn == 128 ? 7 : 6; }
+static SlimKernel slim_kernel(int bn, int e) {
+  switch (bn) {
+    case 96: return slim_kernel_s<96, 8>(e);
+    case 128: return slim_kernel_s<128, 7>(e);
+    case 160: return slim_kernel_s<160, 6>(e);
+  }
+  return nullptr;
+}
+
+// Runs d on the slim-tile engine when it suits: x.W^T with M a multiple of
+// 32 and at most 1024, N a multiple of one of the tile widths, K a multiple
+// of 32, a grid of at most ~1.5 rounds of the CUs even unsplit.  The tile
+// width and K split come from a cost model: rounds of workgroups times
+// (MFMA cycles of one workgroup's K range + the latency of its first
+// loads), plus a reduction launch when the split sums cannot be deferred.
+static bool gemm_slim(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
+                      DeviceArena* ws) {
+  if (d.group != GEMM_GROUP_NONE || d.force_splits > 0 || !vec) return false;
+  if (!d.a_kcontig || !d.b_kcontig || d.M % slim::BM || d.M > 1024 || d.K % slim::TK) return false;
+  if (d.ldc % 4 || !aligned16(d.C)) return false;
+  if (d.epi == EPI_ADD_SRC && (!aligned16(d.aux) || d.ldaux % 4)) return false;
+  if (d.epi == EPI_RELU2_SAVE && d.aux_out && (!aligned16(d.aux_out) || d.ldaux % 4)) return false;
+  if (d.epi != EPI_STORE && d.epi != EPI_ADD_SRC && d.epi != EPI_RELU2_SAVE) return false;
+  // GN_GEMM_SLIM: 0 turns the engine off, 1 takes every eligible product
+  // (tests), unset: the products the cost model and the latency floor give it
+  const char* env = std::getenv("GN_GEMM_SLIM");
+  const int mode = env ? std::atoi(env) : -1;
+  if (mode == 0) return false;
+  const bool can_defer = d.defer && ((d.epi == EPI_STORE && d.alpha == 1.f) || d.epi == EPI_ADD_SRC);
+  const int64_t cus = 256;
+  const double lat = 4800.0;     // first-load latency, cycles (~2 us)
+  const double reduce = 9600.0;  // a reduction launch
+  double best = 0.0;
+  int bn = 0, splits = 1;
+  for (int w : {96, 128, 160}) {
+    if (d.N % w) continue;
+    const int64_t tiles = (int64_t)(d.M / slim::BM) * (d.N / w);
+    if (tiles > (3 * cus) / 2) continue;
+    const int smax = std::min<int>(can_defer ? PENDING_MAX_SPLITS : 16, d.K / 128);
+    for (int s = 1; s <= std::max(1, smax); s++) {
+      const int kps = (int)ceil_div(ceil_div(d.K, s), slim::TK) * slim::TK;
+      if ((int)ceil_div(d.K, kps) != s) continue;
+      const int64_t wg = tiles * s;
+      const int ring = slim_depth(w);  // the K loop runs whole rounds of `ring` tiles
+      const double kt = (double)ceil_div(kps / slim::TK, ring) * ring * slim::TK;
+      const double t = (double)ceil_div(wg, cus) * (kt * w / 4.0 + lat) +
+                       (s > 1 && !can_defer ? reduce : 0.0);
+      if (bn == 0 || t < best - 1e-9) {
+        best = t;
+        bn = w;
+        splits = s;
+      }
+    }
+  }
+  if (bn == 0) return false;
+  const int kps = (int)ceil_div(ceil_div(d.K, splits), slim::TK) * slim::TK;
+  // Short K ranges per workgroup are dominated by the first loads' latency,
+  // which gemm_kernel's smaller tiles (two workgroups per CU) hide as well:
+  // measured at M = 256, the slim engine wins from 16 K tiles per workgroup
+  // (MLP products: 768-deep ranges, 15.5 -> 14.1 us and 15.1 -> 13.0 us)
+  // but not at 6 (qkv 8.8 vs 8.9 us, attention output 5.8 vs 7.2 us).
+  if (mode != 1 && kps < 16 * slim::TK) return false;
+  int e = splits > 1 ? -1 : d.epi;
+  if (e == EPI_RELU2_SAVE && !d.aux_out) e = EPI_RELU2_SAVE + 16;
+  const SlimKernel kern = slim_kernel(bn, e);
+  if (!kern) return false;
+  p.tiles_m = d.M / slim::BM;
+  p.tiles_n = d.N / bn;
+  p.splits = splits;
+  p.k_per_split = kps;
+  const bool defer = can_defer && splits > 1;
+  if (d.defer) {
+    GN_CHECK(d.ldc == d.N && ((d.epi == EPI_STORE && d.alpha == 1.f) ||
+                              (d.epi == EPI_ADD_SRC && d.aux == d.C && d.ldaux == d.N)),
+             "gemm: a deferred split-K sum needs a plain or in-place residual product");
+    *d.defer = PendingSum{};
+  }
+  if (splits > 1) {
+    GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
+    p.part = ws->get<float>(defer ? "gemm_splitk_defer" + std::to_string(d.defer_slot)
+                                  : std::string("gemm_splitk"),
+                            (size_t)splits * d.M * d.N);
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(p.tiles_m * p.tiles_n * splits)), dim3(64 * slim::NW),
+                     0, st, p);
+  GN_HIP(hipGetLastError());
+  if (defer) {
+    d.defer->part = p.part;
+    d.defer->splits = splits;
+    d.defer->stride = (int64_t)d.M * d.N;
+  } else if (splits > 1) {
+    const int64_t total = (int64_t)d.M * d.N;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                       p);
+    GN_HIP(hipGetLastError());
+  }
+  return true;
+}
+
 GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   GN_CHECK(d.M >= 0 && d.N >= 0 && d.K >= 0, "gemm: negative extent");
   if (d.M == 0 || d.N == 0) return GEMM_ENGINE_TILE;
@@ -1140,6 +1442,7 @@ GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
     return GEMM_ENGINE_TILE;
   }
   if (gemm_wide(d, p, vec, st, ws)) return GEMM_ENGINE_WIDE;
+  if (gemm_slim(d, p, vec, st, ws)) return GEMM_ENGINE_SLIM;
 
   // Tile choice: the 128x128 tile when it yields enough workgroups to cover
   // the 256 CUs, otherwise 64x64; split K when even that underfills the chip

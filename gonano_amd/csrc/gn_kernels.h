@@ -135,9 +135,10 @@ struct GemmDesc {
 };
 
 // Which kernel ran a product: gemm_kernel (tiles up to 128 x 128, fused
-// epilogues, grouped and deferred products) or the wide-tile engine (256 x
-// 256 tiles for the large products; gn_gemm.hip).
-enum GemmEngine { GEMM_ENGINE_TILE = 0, GEMM_ENGINE_WIDE = 1 };
+// epilogues, grouped and deferred products), the wide-tile engine (256 x
+// 256 tiles for the large products) or the slim-tile engine (32-row tiles
+// for the decode projections); all in gn_gemm.hip.
+enum GemmEngine { GEMM_ENGINE_TILE = 0, GEMM_ENGINE_WIDE = 1, GEMM_ENGINE_SLIM = 2 };
 
 GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws);
 

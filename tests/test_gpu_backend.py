@@ -257,3 +257,27 @@ def test_matmul_wide_engine(be, m, n, k):
     got2 = np.zeros((m, n), f32)
     be.MatMulTransposed(got2, a, np.ascontiguousarray(b.T), m, n, k)
     assert_close(got2, want, 1e-4, 1e-4, "MatMulTransposed")
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 3072, 768), (256, 768, 3072), (256, 1280, 768),
+                                   (256, 768, 768), (32, 96, 32), (64, 480, 544),
+                                   (512, 1280, 1280), (96, 640, 2048)])
+@pytest.mark.parametrize("mode", ["1", None])
+def test_matmul_slim_engine(be, monkeypatch, m, n, k, mode):
+    """Decode-sized x.W^T products (M a multiple of 32 up to 1024, N a
+    multiple of 96, 128 or 160): the slim-tile engine (GN_GEMM_SLIM=1: every
+    eligible product; unset: the default choice between it and
+    gemm_kernel), including K ranges that are not a whole number of ring
+    rounds (32 x 96 x 32: one real K tile of eight, the rest zeros) and split
+    K summed by the reduction kernel, against numpy in float64."""
+    if mode is None:
+        monkeypatch.delenv("GN_GEMM_SLIM", raising=False)
+    else:
+        monkeypatch.setenv("GN_GEMM_SLIM", mode)
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.standard_normal((m, k)).astype(f32)
+    w = rng.standard_normal((n, k)).astype(f32)
+    want = a.astype(np.float64) @ w.astype(np.float64).T
+    got = np.zeros((m, n), f32)
+    be.MatMulTransposed(got, a, w, m, n, k)
+    assert_close(got, want, 1e-4, 1e-4, "MatMulTransposed")
