@@ -240,7 +240,7 @@ def sample_next_token_static(logits: np.ndarray, rng_state: np.ndarray, temperat
                              top_k: int) -> np.ndarray:
     """sample_next_token through the allocation-free entry point (the
     library's fixed device staging array: rows <= 65536, rows * vocab <=
-    16 Mi floats; concurrent calls on one device must be serialized)."""
+    16 Mi floats; the library serializes calls on one device)."""
     logits = _f(np.ascontiguousarray(logits, np.float32))
     rows, vocab = logits.shape
     out = np.zeros(rows, np.int32)

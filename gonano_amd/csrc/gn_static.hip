@@ -12,7 +12,9 @@
 //   [256, 256 + kIdBytes)    the sampled ids, rows int32
 //   [256 + kIdBytes, end)    the logits, rows * vocab float32
 // Every call on a device reuses that device's copy and leaves the last
-// call's contents in it; two calls that overlap on one device race on it.
+// call's contents in it; calls on one device take that device's lock for
+// their whole duration (copies, sampler, stream synchronization), so they
+// never overlap on the array.
 #include <mutex>
 #include <vector>
 
@@ -33,6 +35,9 @@ static __device__ __align__(256) unsigned char scratch[kStaticBytes];
 // receive the address hipGetSymbolAddress returns for the current device.
 static std::mutex g_scratch_mu;
 static std::vector<void*> g_scratch_ptr;
+// One lock per device, held through a whole call.
+static constexpr int kMaxDevices = 64;
+static std::mutex g_call_mu[kMaxDevices];
 
 static unsigned char* scratch_on(int device) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -64,6 +69,8 @@ int gn_sample_next_token_static(const float* logits, int64_t rows, int64_t vocab
     if (rows == 0) return;
     int dev = 0;
     GN_HIP(hipGetDevice(&dev));
+    GN_CHECK(dev >= 0 && dev < kMaxDevices, "sample_next_token_static: device index above 63");
+    std::lock_guard<std::mutex> call_lock(g_call_mu[dev]);
     unsigned char* base = scratch_on(dev);
     uint64_t* dstate = reinterpret_cast<uint64_t*>(base);
     int32_t* dout = reinterpret_cast<int32_t*>(base + kStateBytes);

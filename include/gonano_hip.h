@@ -371,14 +371,17 @@ int gn_use_calculator(const char *expression, char *out, size_t cap, int32_t *ok
 int gn_sample_next_token(const float *logits, int64_t rows, int64_t vocab, uint64_t *rng_state,
                          float temperature, int64_t top_k, int32_t *out);
 /* gn_sample_next_token without any device allocation.  No counterpart in
- * the reference: for callers that cannot allocate device memory (code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * The logits, the RNG state and the sampled ids are staged through one fixed
- * 65 MiB array in the library's device memory (per GPU, held until the
- * process ends) on the calling thread's per-thread stream, so rows <= 65536
- * and rows * vocab <= 16,777,216 (GN_ERR_INVALID otherwise).  Results equal
- * gn_sample_next_token's.  Calls that overlap on one device race on the
- * array and must be serialized by the caller. */
+ * the reference: for callers that cannot allocate device memory (tight
+ * serving loops, harnesses that forbid hipMalloc).  The logits, the RNG
+ * state and the sampled ids are staged through one fixed 65 MiB array in the
+ * library's device memory (per GPU, held until the process ends) on the
+ * calling thread's per-thread stream, so rows <= 65536 and rows * vocab <=
+ * 16,777,216 (GN_ERR_INVALID otherwise).  Results equal
+ * gn_sample_next_token's.  Calls on one device are serialized by a lock the
+ * library holds from the first copy to the final stream synchronization
+ * (calls on different devices run concurrently).  The call copies from
+ * pageable host memory and synchronizes, so it cannot be captured into a
+ * HIP graph. */
 int gn_sample_next_token_static(const float *logits, int64_t rows, int64_t vocab,
                                 uint64_t *rng_state, float temperature, int64_t top_k,
                                 int32_t *out);

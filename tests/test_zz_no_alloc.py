@@ -1,8 +1,10 @@
 """The allocation-free sampler entry point (gn_sample_next_token_static)
 against gn_sample_next_token through the C-ABI: bit-exact sampled ids and
 the same advanced RNG state on two calls in a row, the second smaller than
-the first (the static staging array keeps the first call's contents), plus
-the size limits it rejects without touching the GPU."""
+the first (the static staging array keeps the first call's contents),
+calls from eight threads at once (the library serializes them on the
+device's lock), plus the size limits it rejects without touching the
+GPU."""
 import numpy as np
 import pytest
 
@@ -29,6 +31,37 @@ def test_static_sampler_matches_allocating_entry_point():
         got = sample_next_token_static(z, b, temp, k)
         assert np.array_equal(got, want), (rows, vocab, np.nonzero(got != want))
         assert np.array_equal(a, b)
+
+
+def test_static_sampler_concurrent_threads():
+    """Eight threads sample different logits through the one staging array
+    at the same time; each gets exactly the ids and state the allocating
+    entry point gives for its own inputs."""
+    import threading
+    from gonano_amd.backend import sample_next_token, sample_next_token_static
+    rng = np.random.default_rng(33)
+    cases = [(_case(rng, 64 + 16 * i, 4096 * (1 + i % 4)), 1000 + i) for i in range(8)]
+    want, got, states = {}, {}, {}
+    for i, (z, seed) in enumerate(cases):
+        a = np.array([seed, seed * 3 + 1], np.uint64)
+        want[i] = (sample_next_token(z, a, 1.0, 50), a.copy())
+
+    def work(i):
+        z, seed = cases[i]
+        for _ in range(5):
+            b = np.array([seed, seed * 3 + 1], np.uint64)
+            got.setdefault(i, []).append((sample_next_token_static(z, b, 1.0, 50), b.copy()))
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for i in range(8):
+        assert len(got[i]) == 5
+        for ids, st in got[i]:
+            assert np.array_equal(ids, want[i][0]), i
+            assert np.array_equal(st, want[i][1]), i
 
 
 def test_static_sampler_rejects_sizes_beyond_its_buffer():
