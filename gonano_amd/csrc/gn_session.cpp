@@ -649,6 +649,13 @@ struct SeqBuffers {
   // when set (a forward from position 0), every layer's token-major
   // keys/values are copied here: [L][B*T][Hkv*128]
   float *tm_k_out = nullptr, *tm_v_out = nullptr;
+  // compressed models with a prefix cache: the compressor's logits (h . Wl^T)
+  // of every Full layer -- a forward from position 0 copies them to
+  // tm_clog_out [L][B*T][128]; a continuation finds the prefix's rows in
+  // pre_clog [L][B][pre_len+T][128], writes the new rows after them and
+  // compresses the whole sequences
+  float* tm_clog_out = nullptr;
+  float* pre_clog = nullptr;
   // prefill: the decode caches to fill (indexer keys [L][G*S][maxBlocks]
   // [Hkv][HI] of the complete blocks, replicated over S rows per prompt)
   float* dec_ikc = nullptr;
@@ -842,7 +849,8 @@ static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, S
   const int64_t N = sb.N;
   const bool save = mode == SEQ_TRAIN;
   hipStream_t st = s->stream;
-  const int blocks = sb.replay ? sb.gblocks : (int)ceil_div(T, ratio);
+  const int Tall = sb.pre_len + T;  // positions per sequence (a continuation: its prefix too)
+  const int blocks = sb.replay ? sb.gblocks : (int)ceil_div(Tall, ratio);
   const bool ced = s->split > 0 && l >= s->split;
   if (ly.mode == 'F' && sb.replay) {  // the global blocks were filled from the encoder
     sb.hkc[l] = sb.pre_kc[l];
@@ -865,14 +873,24 @@ static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, S
     }
     float* clog = A<float>(s, "hca_clog", N * HD);
     sgemm(s, linear_fwd_desc(hin, ly.wcl, clog, (int)N, C, HD));
+    if (sb.tm_clog_out)
+      GN_HIP(hipMemcpyAsync(sb.tm_clog_out + (int64_t)l * N * HD, clog, sizeof(float) * N * HD,
+                            hipMemcpyDeviceToDevice, st));
+    if (sb.pre_len > 0) {  // the new rows after each sequence's prefix; compress the whole
+      float* all = sb.pre_clog + (int64_t)l * B * Tall * HD;
+      GN_HIP(hipMemcpy2DAsync(all + (int64_t)sb.pre_len * HD, sizeof(float) * Tall * HD, clog,
+                              sizeof(float) * T * HD, sizeof(float) * T * HD, B,
+                              hipMemcpyDeviceToDevice, st));
+      clog = all;
+    }
     HcaCompressArgs ca{};
     ca.clog = clog; ca.bias = ly.cbias; ca.k = kin; ca.v = vin;
-    ca.B = B; ca.T = T; ca.Hkv = Hkv; ca.ratio = ratio;
+    ca.B = B; ca.T = Tall; ca.Hkv = Hkv; ca.ratio = ratio;
     ca.probs = layer_buf(s, "hca_probs", l, save, (size_t)B * blocks * ratio * HD);
     ca.kc = layer_buf(s, "hca_kc", l, true, (size_t)B * blocks * s->KVW);
     ca.vc = layer_buf(s, "hca_vc", l, true, (size_t)B * blocks * s->KVW);
     if (mode == SEQ_PREFILL) {
-      const int64_t full = T / ratio;
+      const int64_t full = Tall / ratio;
       if (full > 0) {
         ca.ck_pf = sb.pf_ck + (int64_t)l * B * Hkv * full * HD;
         ca.cv_pf = sb.pf_cv + (int64_t)l * B * Hkv * full * HD;
@@ -893,7 +911,7 @@ static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, S
     } else {
       csa_select_layer(s, sb, ly, l, save, kc, blocks);
       if (mode == SEQ_PREFILL && sb.dec_ikc && !sb.replay) {  // the decode indexer-key cache
-        const int full = T / ratio;
+        const int full = Tall / ratio;
         launch_replicate_rows(sb.iq[l] ? sb.ik[l] : nullptr,
                               sb.dec_ikc + (int64_t)l * B * sb.dec_S * sb.dec_maxBlocks * Hkv * s->HI,
                               B, sb.dec_S, full, Hkv * s->HI, blocks, sb.dec_maxBlocks, st);
@@ -923,6 +941,7 @@ static void hca_forward(gn_session* s, SeqBuffers& sb, const Layer& ly, int l, S
     fl.o = A<float>(s, "hca_ol", N * Hq * HD);
     fl.lse = A<float>(s, "hca_ll", N * Hq);
     fl.B = B; fl.T = T; fl.Hq = Hq; fl.Hkv = Hkv; fl.window = s->swa;
+    fl.Tk = Tall; fl.qoff = sb.pre_len;  // a continuation: the prefix's rows first
     launch_flash_fwd(fl, st);
     launch_merge_branches(og, lg, fl.o, fl.lse, o, lse, N * Hq, st);
   }
@@ -963,9 +982,9 @@ static void seq_forward(gn_session* s, SeqBuffers& sb, SeqMode mode, float* kcac
   float* qkv = s->mla ? nullptr : A<float>(s, "qkv", N * s->QKVW);
   const int bk = L / 2;
   sb.backout = nullptr;
-  GN_CHECK(sb.pre_len == 0 || (!save && !s->hca && sb.qoff == sb.pre_len && sb.kv_k && sb.kv_v &&
-                                !sb.tm_k_out),
-           "prefix continuation: prefill only, dense or latent attention");
+  GN_CHECK(sb.pre_len == 0 || (!save && s->split == 0 && (!s->hca || sb.pre_clog) &&
+                                sb.qoff == sb.pre_len && sb.kv_k && sb.kv_v && !sb.tm_k_out),
+           "prefix continuation: prefill only, no encoder-decoder split");
   const int Tall = sb.pre_len + T;  // keys per sequence
   // the new rows' keys/values into the rows after each sequence's prefix
   auto append_rows = [&](float* all, const float* rows) {
@@ -2147,13 +2166,27 @@ static int prefill_ced(gn_session* s, SeqBuffers& sb, const int32_t* prompts, in
 // Prefix cache (inference/cache.go CacheManager, inference/prefix.go
 // PrefixCache) on the device.  An entry holds one prompt's prefill state:
 // every layer's token-major keys/values [L][P][Hkv*128] (what a continued
-// prefill attends to), its decode-cache rows (dense: K and V [L][Hkv][P][128];
-// latent: the latent rows [L][P][lat] and rotated keys [L][P][Hkv*rd]) and
-// the last token's embedding (the next token's smear input, KVBuffer's
-// PrevEmbedding).
+// prefill attends to), its decode-cache rows (dense and compressed: K and V
+// [L][Hkv][P][128]; latent: the latent rows [L][P][lat] and rotated keys
+// [L][P][Hkv*rd]), the last token's embedding (the next token's smear input,
+// KVBuffer's PrevEmbedding) and, for compressed attention, the Full layers'
+// compressor logits of every position.  A compressed model's continuation
+// compresses the whole sequence again from the stored logits and keys/values
+// together with the new rows' (the compressor pass is small next to the
+// projections), which gives the blocks, the logit ring of an incomplete last
+// block and the indexer keys exactly as a prefill from position 0 does.  The reference stores the whole KVBuffer
+// (its sliding-window rows too, or with CacheOptions.StripSWA without them,
+// rebuilt by a bounded replay on a hit: inference/cache.go:134-140,
+// 286-311); here the raw rows of every position are kept, so no replay is
+// needed.  Encoder-decoder (CED) models are not cached, as in the reference
+// (inference/engine.go:128-140).
+//
+// Byte accounting (MaxBytes): an entry counts the device bytes it holds, the
+// layout above -- not the reference's KVBuffer.BytesAllocated, whose
+// prefill buffer is sized to the whole SequenceLen.
 // ---------------------------------------------------------------------------
 struct PcLayout {
-  int64_t ktm, vtm, kdc, vdc, prev, total;  // float offsets
+  int64_t ktm, vtm, kdc, vdc, prev, clog, total;  // float offsets
 };
 static PcLayout pc_layout(const gn_session* s, int P) {
   PcLayout o;
@@ -2165,7 +2198,11 @@ static PcLayout pc_layout(const gn_session* s, int P) {
   o.kdc = 2 * tm;
   o.vdc = o.kdc + kdc;
   o.prev = o.vdc + vdc;
-  o.total = o.prev + s->C;
+  o.clog = o.prev + s->C;
+  // compressed attention: the compressor's logits of every position
+  // [L][P][128] (the Full layers' rows; the compressed blocks, the logit
+  // ring and the indexer keys are recomputed from them and the keys/values)
+  o.total = o.clog + (s->hca ? (int64_t)s->L * P * HD : 0);
   return o;
 }
 static double pc_now() {
@@ -2292,28 +2329,42 @@ struct CopyList {
 // 0, and the hits, batched by matched length m, continue from their entries
 // over the last P - m tokens (the entries' keys attended first, their
 // decode-cache rows copied in, the smear seeded with their stored embedding
-// -- KVBuffer.PrevEmbedding).  Fills the decode prefill caches kpf/vpf (the
-// plain prefill's layout) and each prompt's last-row final norm and
-// embedding lastfn/lastemb [G][C].
+// -- KVBuffer.PrevEmbedding; compressed attention: the stored compressor
+// logits in front of the new rows').  Fills the decode prefill caches
+// kpf/vpf (the plain prefill's layout), each prompt's last-row final norm
+// and embedding lastfn/lastemb [G][C] and, for compressed attention, out's
+// compressed caches pf_ck/pf_cv/pf_ring (layout [L][G]...) and indexer-key
+// decode cache dec_ikc (out.dec_S rows per prompt), as seq_forward fills
+// them for a plain prefill.
 static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, float* kpf,
-                           float* vpf, float* lastfn, float* lastemb) {
-  GN_CHECK(!s->hca && s->split == 0,
-           "prefix cache: compressed-attention and CED models are not cached");
+                           float* vpf, float* lastfn, float* lastemb, const SeqBuffers& out) {
+  GN_CHECK(s->split == 0, "prefix cache: encoder-decoder (CED) models are not cached");
   const int L = s->L, C = s->C, Hkv = s->Hkv;
   const int64_t KVW = s->KVW;
   // floats per (layer, prompt) of the decode prefill caches
   const int64_t kg = s->mla ? (int64_t)P * s->lat : (int64_t)Hkv * P * HD;
   const int64_t vg = s->mla ? (int64_t)P * Hkv * s->rd : (int64_t)Hkv * P * HD;
   const PcLayout lay = pc_layout(s, P);
+  // compressed attention: per (layer, prompt) floats of the complete blocks'
+  // cache, of the logit ring, and per (layer, row) of the indexer-key cache
+  const bool hca = s->hca;
+  const int full = hca ? P / s->ratio : 0;
+  const int64_t cg = (int64_t)Hkv * full * HD;
+  const int64_t rg = hca ? (int64_t)s->ratio * HD : 0;
+  const int64_t ikw = hca && out.dec_ikc ? (int64_t)out.dec_maxBlocks * Hkv * s->HI : 0;
+  if (hca) GN_CHECK(out.pf_ck && out.pf_cv && out.pf_ring, "prefix cache: compressed outputs");
   struct Plan {
     gn_session::PrefixEntry* src = nullptr;  // the hit (nullptr: a miss)
     int m = 0;
     gn_session::PrefixEntry* dst = nullptr;  // this prompt's new entry
   };
   std::vector<Plan> plan(G);
-  std::vector<gn_session::PrefixEntry*> made;
   CopyList cp;
   std::vector<std::vector<int32_t>> ids_kept;  // uploaded token ids, until the stream is idle
+  // the list as the call found it (least recently used first), restored if
+  // the call fails
+  std::vector<gn_session::PrefixEntry*> before;
+  for (const auto& e : s->pc_entries) before.push_back(e.get());
   s->pc_defer = true;
   try {
     // 1) the cache sequence of G successive GenerateWith calls
@@ -2329,17 +2380,35 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
       ne->mem = pc_alloc(s, ne->bytes);
       ne->stored_at = pc_now();
       plan[g].dst = ne.get();
-      made.push_back(ne.get());
       pc_insert(s, std::move(ne));
     }
     s->pc_hits.assign(G, 0);
     for (int g = 0; g < G; g++) s->pc_hits[g] = plan[g].m;
+    // compressed attention: a batch's compressed prefill caches, in the
+    // batch's own layout (set up by hca_targets, moved by collect)
+    float *bck = nullptr, *bcv = nullptr, *bring = nullptr, *bik = nullptr;
+    auto hca_targets = [&](SeqBuffers& sb) {
+      if (!hca) return;
+      const int B = sb.B;
+      bck = A<float>(s, "pc_bck", (size_t)L * B * std::max<int64_t>(cg, 1));
+      bcv = A<float>(s, "pc_bcv", (size_t)L * B * std::max<int64_t>(cg, 1));
+      bring = A<float>(s, "pc_bring", (size_t)L * B * rg);
+      sb.pf_ck = bck;
+      sb.pf_cv = bcv;
+      sb.pf_ring = bring;
+      if (ikw > 0) {
+        bik = A<float>(s, "pc_bik", (size_t)L * B * ikw);
+        sb.dec_ikc = bik;
+        sb.dec_S = 1;
+        sb.dec_maxBlocks = out.dec_maxBlocks;
+      }
+    };
     // one batch of prompts (prompt g at batch row i), positions [m, P): the
     // forward's decode caches kt/vt [L][B] and its last rows into the
-    // call's per-prompt outputs, the whole prompts' keys/values into their
-    // entries
+    // call's per-prompt outputs, the whole prompts' keys/values (compressed:
+    // and compressor logits clog [L][B][P][128]) into their entries
     auto collect = [&](const std::vector<int>& gs, int m, SeqBuffers& sb, const float* kt,
-                       const float* vt, const float* kall, const float* vall) {
+                       const float* vt, const float* kall, const float* vall, const float* clog) {
       const int B = (int)gs.size(), T = P - m;
       for (int i = 0; i < B; i++) {
         const int g = gs[i];
@@ -2357,6 +2426,20 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
         cp.add(kt + i * kg, dm + lay.kdc, kg, L, B * kg, kg);
         cp.add(vt + i * vg, dm + lay.vdc, vg, L, B * vg, vg);
         cp.add(sb.embn + last, dm + lay.prev, C, 1, 0, 0);
+        if (hca) {
+          cp.add(bck + i * cg, out.pf_ck + g * cg, cg, L, B * cg, G * cg);
+          cp.add(bcv + i * cg, out.pf_cv + g * cg, cg, L, B * cg, G * cg);
+          cp.add(bring + i * rg, out.pf_ring + g * rg, rg, L, B * rg, G * rg);
+          // the complete blocks' indexer keys into every row of the prompt
+          if (ikw > 0)
+            cp.add(bik + i * ikw, out.dec_ikc + (int64_t)g * out.dec_S * ikw,
+                   (int64_t)full * Hkv * s->HI, L, B * ikw, (int64_t)G * out.dec_S * ikw,
+                   out.dec_S, 0, ikw);
+          for (int l = 0; l < L; l++)  // the Full layers' compressor logits
+            if (s->layers[l].mode == 'F')
+              cp.add(clog + ((int64_t)l * B + i) * P * HD, dm + lay.clog + (int64_t)l * P * HD,
+                     (int64_t)P * HD, 1, 0, 0);
+        }
       }
       cp.run(s, "pc_desc_out");
     };
@@ -2378,10 +2461,12 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
       sb.ids = upload_ids(s, "pc_ids", ids.data(), sb.N, s->V);
       sb.tm_k_out = A<float>(s, "pc_kall", (size_t)L * sb.N * KVW);
       sb.tm_v_out = A<float>(s, "pc_vall", (size_t)L * sb.N * KVW);
+      if (hca) sb.tm_clog_out = A<float>(s, "pc_clog", (size_t)L * sb.N * HD);
+      hca_targets(sb);
       float* kt = A<float>(s, "pc_kt", (size_t)L * B * kg);
       float* vt = A<float>(s, "pc_vt", (size_t)L * B * vg);
       seq_forward(s, sb, SEQ_PREFILL, kt, vt);
-      collect(miss, 0, sb, kt, vt, sb.tm_k_out, sb.tm_v_out);
+      collect(miss, 0, sb, kt, vt, sb.tm_k_out, sb.tm_v_out, sb.tm_clog_out);
     }
     // 3) hits, one batch per matched length (one prompt length per call, so
     //    equal m means equal continuation length)
@@ -2398,6 +2483,7 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
       float* kt = A<float>(s, "pc_kt", (size_t)L * B * kg);
       float* vt = A<float>(s, "pc_vt", (size_t)L * B * vg);
       float* prev = A<float>(s, "pc_prev", (size_t)B * C);
+      float* clog = hca ? A<float>(s, "pc_clog", (size_t)L * B * P * HD) : nullptr;
       ids_kept.emplace_back((size_t)B * T);
       std::vector<int32_t>& ids = ids_kept.back();
       for (int i = 0; i < B; i++) {
@@ -2419,6 +2505,11 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
                  (int64_t)m * HD, (int64_t)P * HD);
         }
         cp.add(em + el.prev, prev + (int64_t)i * C, C, 1, 0, 0);
+        if (hca)  // the Full layers' compressor logits of positions [0, m)
+          for (int l = 0; l < L; l++)
+            if (s->layers[l].mode == 'F')
+              cp.add(em + el.clog + (int64_t)l * m * HD, clog + ((int64_t)l * B + i) * P * HD,
+                     (int64_t)m * HD, 1, 0, 0);
       }
       cp.run(s, "pc_desc_in");
       SeqBuffers sb;
@@ -2429,21 +2520,35 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
       sb.pre_len = m;
       sb.kv_k = kall;
       sb.kv_v = vall;
+      sb.pre_clog = clog;
       sb.seed_prev = prev;
+      hca_targets(sb);
       seq_forward(s, sb, SEQ_PREFILL, kt, vt);
-      collect(gs, m, sb, kt, vt, kall, vall);
+      collect(gs, m, sb, kt, vt, kall, vall, clog);
       h0 = h1;
     }
     GN_HIP(hipStreamSynchronize(s->stream));
   } catch (...) {
-    // entries of this call may be incomplete: drop them (their memory is
-    // released after the stream has drained)
-    for (auto* e : made)
-      for (size_t i = 0; i < s->pc_entries.size(); i++)
-        if (s->pc_entries[i].get() == e) {
-          pc_remove(s, i);
+    // The cache as the call found it: its entries in their order (those the
+    // call evicted or expired come back from pc_retired, untouched: retired
+    // memory is not reused before the flush); the call's own entries, which
+    // may be incomplete, are dropped and released after the stream has
+    // drained.
+    std::vector<std::unique_ptr<gn_session::PrefixEntry>> all;
+    for (auto& e : s->pc_entries) all.push_back(std::move(e));
+    for (auto& e : s->pc_retired) all.push_back(std::move(e));
+    s->pc_entries.clear();
+    s->pc_retired.clear();
+    s->pc_bytes = 0;
+    for (auto* want : before)
+      for (auto& e : all)
+        if (e.get() == want) {
+          s->pc_bytes += e->bytes;
+          s->pc_entries.push_back(std::move(e));
           break;
         }
+    for (auto& e : all)
+      if (e) s->pc_retired.push_back(std::move(e));
     (void)hipStreamSynchronize(s->stream);
     s->pc_defer = false;
     pc_flush(s);
@@ -2527,7 +2632,7 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   if (pcache) {
     gfn = A<float>(s, "pc_gfn", (size_t)G * C);
     gemb = A<float>(s, "pc_gemb", (size_t)G * C);
-    prefill_cached(s, prompts, G, P, kpf, vpf, gfn, gemb);
+    prefill_cached(s, prompts, G, P, kpf, vpf, gfn, gemb, sb);
     if (N == 0) return;
     launch_expand_last_rows(gfn, lastfn, G, 1, S, C, st);
   } else {
@@ -3117,9 +3222,9 @@ int gn_session_set_prefix_cache(gn_session* s, const gn_prefix_cache_options* o)
       s->pc_on = false;
       return;
     }
-    if (s->hca || s->split > 0)
+    if (s->split > 0)  // as the reference (inference/engine.go:128-140, 175-182)
       throw Error(GN_ERR_UNSUPPORTED,
-                  "prefix cache: compressed-attention and CED models are not cached");
+                  "prefix cache: encoder-decoder (CED) models are not cached");
     GN_CHECK(o->max_entries >= 0 && o->max_bytes >= 0 && o->max_prefix >= 0 &&
                  o->ttl_seconds >= 0.0,
              "prefix cache: negative limit");

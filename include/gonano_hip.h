@@ -436,13 +436,17 @@ int gn_session_synchronize(gn_session *session);
  * the stored keys/values.  A batch of groups sees the cache as that many
  * successive GenerateWith calls would (an earlier group's entry can serve a
  * later group).  An entry holds every layer's keys/values of its prompt, its
- * decode-cache rows and its last token embedding (KVBuffer.PrevEmbedding);
- * `bytes` counts that device memory.  Entries are dropped whenever the
- * parameters change (gn_session_set_params, gn_optimizer_step): their state
- * would no longer equal a full prefill.  Not for compressed-attention or CED
- * models (GN_ERR_UNSUPPORTED; the reference skips CED too,
- * inference/prefix.go:17-19).  The on-disk tier (CacheOptions.DiskDir) and
- * its sliding-window stripping are not built. */
+ * decode-cache rows, its last token embedding (KVBuffer.PrevEmbedding) and,
+ * for compressed attention, the Full layers' compressor logits of every
+ * position (a continuation recompresses the whole sequence from them, so the
+ * raw sliding-window rows are kept and CacheOptions.StripSWA's bounded replay
+ * is never needed); `bytes` counts that device memory (not the reference's
+ * KVBuffer.BytesAllocated).  Entries are dropped whenever the parameters
+ * change (gn_session_set_params, gn_optimizer_step): their state would no
+ * longer equal a full prefill.  Not for CED models (GN_ERR_UNSUPPORTED; the
+ * reference's engine skips them, inference/engine.go:128-140,
+ * inference/prefix.go:17-19).  A call that fails leaves the cache as it
+ * found it.  The on-disk tier (CacheOptions.DiskDir) is not built. */
 typedef struct gn_prefix_cache_options {
   int32_t max_entries; /* CacheOptions.MaxEntries; 0: unbounded */
   int32_t max_prefix;  /* NewPrefixCache(maxPrefix): longer entries never hit; 0: any */

@@ -8,7 +8,10 @@ and PrefixCache (inference/prefix.go).
   checked against the oracle's full prefill by teacher forcing, for
   continuations over a sliding-window boundary, of one token (the smear
   seeded alone) and of a longer stored extension (the longest prefix wins),
-  on a dense and a latent-attention MoE model.
+  on a dense model, a latent-attention MoE model and two compressed-attention
+  models (stored prefixes ending inside a compressed block; one with
+  hierarchical sparse selection, one with MoE), whose continuations compress
+  the whole sequences from the stored compressor logits.
 * The bookkeeping -- strict and longest prefix, LRU order, MaxEntries,
   MaxBytes, TTL from storage, maxPrefix, Invalidate, a batch seen as
   successive calls -- follows the reference's cache.go/prefix.go, checked by
@@ -39,7 +42,32 @@ def _latent():
                                  expert_hidden=256)
 
 
-@pytest.mark.parametrize("make,perturb", [(_dense, 0.1), (_latent, 0.05)], ids=["dense", "latent"])
+def _compressed_sparse():
+    # compressed attention (ratio 4, SWA 64) with hierarchical top-3 selection
+    # and a Full / Reindex / Reuse layer group; no encoder-decoder split
+    cfg = G.Config(sequence_len=512, vocab_size=2048, n_layer=3, n_head=2, n_kv_head=1,
+                   n_embd=256, window_pattern="SSSL", rotary_dims=64, compression_ratio=4,
+                   swa_window=64, sparse_topk=3, indexer_pool=2, indexer_candidates=8,
+                   indexer_dim=16, reuse_pattern="FRU")
+    cfg.validate()
+    return cfg
+
+
+def _compressed():
+    # compressed attention over every earlier block (no selection), a Full and
+    # a Reuse layer, with the DeepSeekMoE feed-forward
+    cfg = G.Config(sequence_len=512, vocab_size=2048, n_layer=2, n_head=2, n_kv_head=1,
+                   n_embd=256, window_pattern="SSSL", rotary_dims=64, compression_ratio=4,
+                   swa_window=64, reuse_pattern="FU")
+    cfg = G.enable_moe(cfg, n_experts=4, experts_per_token=2, expert_hidden=64,
+                       shared_hidden=96, balance_weight=1e-2)
+    cfg.validate()
+    return cfg
+
+
+@pytest.mark.parametrize("make,perturb", [(_dense, 0.1), (_latent, 0.05), (_compressed_sparse, 0.1),
+                                          (_compressed, 0.1)],
+                         ids=["dense", "latent", "compressed_sparse", "compressed"])
 def test_cached_continuation_matches_full_prefill(orc, make, perturb):
     from gonano_amd.session import Session
     cfg = make()
@@ -236,7 +264,8 @@ def test_batch_is_seen_as_successive_calls_and_random_sequence():
 
 def test_rl_step_uses_the_cache_and_unsupported_models():
     """gn_rl_step prefills through the cache too (its rollout is
-    GenerateBatchWith); compressed-attention and CED models refuse it."""
+    GenerateBatchWith); CED models refuse it (the reference's engine skips
+    them), the same compressed model without CED takes it."""
     from gonano_amd import _lib
     from gonano_amd.session import Session
     cfg = _small()
@@ -252,7 +281,12 @@ def test_rl_step_uses_the_cache_and_unsupported_models():
     fl = G.config_for_depth_ratio(4, 2048, 64, 128, 512, "SSSL", 1)
     fl.n_layer = 2
     G.apply_flash_preset(fl, sparse_topk=4, swa_window=128, n_experts=4)
+    assert fl.ced
     with Session(fl) as s:
         with pytest.raises(_lib.HipError) as e:
             s.set_prefix_cache()
         assert e.value.code == 4
+    fl.ced = False  # the same compressed model without the encoder-decoder split
+    with Session(fl) as s:
+        s.set_prefix_cache()
+        assert s.prefix_cache_len() == (0, 0)
