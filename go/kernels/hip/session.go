@@ -156,6 +156,11 @@ func (s *Session) SetPrefixCache(opts inference.CacheOptions, maxPrefix int) {
 		max_bytes:   C.int64_t(opts.MaxBytes),
 		ttl_seconds: C.double(opts.TTL.Seconds()),
 	}
+	if opts.DiskDir != "" {
+		dir := C.CString(opts.DiskDir)
+		defer C.free(unsafe.Pointer(dir))
+		o.disk_dir = dir
+	}
 	call(func() C.int { return C.gn_session_set_prefix_cache(s.h, &o) })
 }
 func (s *Session) DisablePrefixCache()  { call(func() C.int { return C.gn_session_set_prefix_cache(s.h, nil) }) }

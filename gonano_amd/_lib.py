@@ -93,6 +93,7 @@ class GnPrefixCacheOptions(C.Structure):
         ("max_prefix", C.c_int32),
         ("max_bytes", C.c_int64),
         ("ttl_seconds", C.c_double),
+        ("disk_dir", C.c_char_p),
     ]
 
 

@@ -13,7 +13,9 @@
 #include <chrono>
 #include <cmath>
 #include <cstdlib>
+#include <cstdio>
 #include <cstring>
+#include <filesystem>
 #include <memory>
 #include <string>
 #include <vector>
@@ -154,9 +156,12 @@ struct gn_session {
   // in LRU order, oldest first; each holds one prompt's prefill state
   struct PrefixEntry {
     std::vector<int32_t> tokens;
-    float* mem = nullptr;  // ktm | vtm | kdc | vdc | prev (gn::pc_layout)
+    // the state (gn::pc_layout) on the device; a disk-backed entry's is null
+    // except while a call that hit it uses it
+    float* mem = nullptr;
     int64_t bytes = 0;
     double stored_at = 0.0;
+    std::string path;  // the on-disk copy (CacheOptions.DiskDir), else empty
   };
   std::vector<std::unique_ptr<PrefixEntry>> pc_entries;
   bool pc_on = false;
@@ -171,6 +176,7 @@ struct gn_session {
   // (hipFree synchronizes the device): (bytes, pointer)
   std::vector<std::pair<int64_t, float*>> pc_pool;
   std::vector<int32_t> pc_hits;  // prompt tokens taken from the cache, per group of the last call
+  std::string pc_dir;            // on-disk tier directory (CacheOptions.DiskDir), empty: none
   // decode steps replayed from one captured HIP graph per rollout
   bool decode_graph = true;
   // q/k/v post-processing inside the decode attention kernel (plain windows)
@@ -2211,17 +2217,26 @@ static double pc_now() {
 // Entries leave the list through pc_remove; their device memory is released
 // at once, or -- while a prefill still reads it (pc_defer) -- when that
 // prefill has finished (pc_flush).
+// A disk-backed entry's file goes with it (removeEntryLocked, cache.go:
+// 201-214), also deferred while a prefill runs (a failed call restores it).
 static void pc_remove(gn_session* s, size_t i) {
   auto& e = s->pc_entries[i];
   s->pc_bytes -= e->bytes;
-  if (s->pc_defer) s->pc_retired.push_back(std::move(e));
-  else (void)hipFree(e->mem);
+  if (s->pc_defer) {
+    s->pc_retired.push_back(std::move(e));
+  } else {
+    if (!e->path.empty()) std::remove(e->path.c_str());
+    if (e->mem) (void)hipFree(e->mem);
+  }
   s->pc_entries.erase(s->pc_entries.begin() + i);
 }
 // Removed entries' memory goes to the pool, which keeps at most `keep`
-// buffers (the newest); the rest is released.
+// buffers (the newest); the rest is released.  Their files are deleted.
 static void pc_flush(gn_session* s, size_t keep = 0) {
-  for (auto& e : s->pc_retired) s->pc_pool.push_back({e->bytes, e->mem});
+  for (auto& e : s->pc_retired) {
+    if (!e->path.empty()) std::remove(e->path.c_str());
+    if (e->mem) s->pc_pool.push_back({e->bytes, e->mem});
+  }
   s->pc_retired.clear();
   while (s->pc_pool.size() > keep) {
     (void)hipFree(s->pc_pool.front().second);
@@ -2239,6 +2254,72 @@ static float* pc_alloc(gn_session* s, int64_t bytes) {
   float* p = nullptr;
   GN_HIP(hipMalloc(&p, bytes));
   return p;
+}
+// On-disk tier (CacheOptions.DiskDir; saveKVFile / loadKVFile, cache.go:
+// 145-150, 254-284): one file per entry, named by a hash of its tokens, with
+// the tokens in the header so that a file written for another sequence (a
+// hash collision, a stale file) is refused on load.  Format: "GNPC", version
+// 1, token count, state bytes (little-endian int64 each after the magic),
+// the tokens (int32), the state (float32, gn::pc_layout).
+static constexpr char PC_MAGIC[4] = {'G', 'N', 'P', 'C'};
+static std::string pc_file(const gn_session* s, const std::vector<int32_t>& toks) {
+  uint64_t h = 1469598103934665603ull;  // FNV-1a over the token bytes
+  for (int32_t t : toks)
+    for (int b = 0; b < 4; b++) {
+      h ^= (uint64_t)(((uint32_t)t >> (8 * b)) & 0xff);
+      h *= 1099511628211ull;
+    }
+  char name[64];
+  snprintf(name, sizeof name, "%016llx-%zu.kv", (unsigned long long)h, toks.size());
+  return (std::filesystem::path(s->pc_dir) / name).string();
+}
+// Writes e's device state to its file; true on success.
+static bool pc_save(gn_session* s, gn_session::PrefixEntry& e) {
+  const std::string path = pc_file(s, e.tokens);
+  std::vector<char> host((size_t)e.bytes);
+  if (hipMemcpy(host.data(), e.mem, (size_t)e.bytes, hipMemcpyDeviceToHost) != hipSuccess)
+    return false;
+  FILE* f = std::fopen(path.c_str(), "wb");
+  if (!f) return false;
+  const int64_t head[3] = {1, (int64_t)e.tokens.size(), e.bytes};
+  bool ok = std::fwrite(PC_MAGIC, 1, 4, f) == 4 && std::fwrite(head, 8, 3, f) == 3 &&
+            std::fwrite(e.tokens.data(), 4, e.tokens.size(), f) == e.tokens.size() &&
+            std::fwrite(host.data(), 1, host.size(), f) == host.size();
+  ok = std::fclose(f) == 0 && ok;
+  if (!ok) {
+    std::remove(path.c_str());
+    return false;
+  }
+  e.path = path;
+  return true;
+}
+// Reads e's file into fresh device memory; false (and nothing allocated)
+// when the file is missing, short, or written for another sequence.
+static bool pc_load(gn_session* s, gn_session::PrefixEntry& e) {
+  FILE* f = std::fopen(e.path.c_str(), "rb");
+  if (!f) return false;
+  char magic[4];
+  int64_t head[3];
+  std::vector<int32_t> toks;
+  std::vector<char> host;
+  bool ok = std::fread(magic, 1, 4, f) == 4 && std::memcmp(magic, PC_MAGIC, 4) == 0 &&
+            std::fread(head, 8, 3, f) == 3 && head[0] == 1 &&
+            head[1] == (int64_t)e.tokens.size() && head[2] == e.bytes;
+  if (ok) {
+    toks.resize(e.tokens.size());
+    host.resize((size_t)e.bytes);
+    ok = std::fread(toks.data(), 4, toks.size(), f) == toks.size() && toks == e.tokens &&
+         std::fread(host.data(), 1, host.size(), f) == host.size();
+  }
+  std::fclose(f);
+  if (!ok) return false;
+  float* mem = pc_alloc(s, e.bytes);
+  if (hipMemcpy(mem, host.data(), (size_t)e.bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    s->pc_pool.push_back({e.bytes, mem});
+    return false;
+  }
+  e.mem = mem;
+  return true;
 }
 // expireLocked (cache.go:236-252): entries stored longer ago than the TTL
 static void pc_expire(gn_session* s) {
@@ -2267,7 +2348,14 @@ static gn_session::PrefixEntry* pc_lookup(gn_session* s, const int32_t* toks, in
   auto e = std::move(s->pc_entries[best]);
   s->pc_entries.erase(s->pc_entries.begin() + best);
   s->pc_entries.push_back(std::move(e));
-  return s->pc_entries.back().get();
+  gn_session::PrefixEntry* hit = s->pc_entries.back().get();
+  // a disk-backed entry is read back for this call; one that cannot be read
+  // is dropped and the lookup misses (cache.go:112-117)
+  if (!hit->mem && !pc_load(s, *hit)) {
+    pc_remove(s, s->pc_entries.size() - 1);
+    return nullptr;
+  }
+  return hit;
 }
 // evictLocked (cache.go:216-231): least recently used entries first, until
 // the entry count and then the byte total fit
@@ -2550,11 +2638,28 @@ static void prefill_cached(gn_session* s, const int32_t* prompts, int G, int P, 
     for (auto& e : all)
       if (e) s->pc_retired.push_back(std::move(e));
     (void)hipStreamSynchronize(s->stream);
+    for (auto& e : s->pc_entries)  // read-back state of disk-backed entries
+      if (!e->path.empty() && e->mem) {
+        s->pc_pool.push_back({e->bytes, e->mem});
+        e->mem = nullptr;
+      }
     s->pc_defer = false;
     pc_flush(s);
     throw;
   }
   s->pc_defer = false;
+  pc_flush(s, (size_t)G);  // removed entries' files deleted (before a same-prompt entry's is written)
+  // disk tier: the new entries are written out (an entry whose file cannot be
+  // written stays in device memory, as Store keeps it in memory), and every
+  // disk-backed entry's device state is released
+  if (!s->pc_dir.empty())
+    for (auto& e : s->pc_entries)
+      if (e->path.empty() && e->mem) pc_save(s, *e);
+  for (auto& e : s->pc_entries)
+    if (!e->path.empty() && e->mem) {
+      s->pc_pool.push_back({e->bytes, e->mem});
+      e->mem = nullptr;
+    }
   pc_flush(s, (size_t)G);  // the next call of this size reuses them
 }
 
@@ -3233,6 +3338,14 @@ int gn_session_set_prefix_cache(gn_session* s, const gn_prefix_cache_options* o)
     s->pc_max_bytes = o->max_bytes;
     s->pc_max_prefix = o->max_prefix;
     s->pc_ttl = o->ttl_seconds;
+    // NewCacheManager (cache.go:64-77): the directory is created if missing;
+    // if that fails the cache keeps to device memory
+    s->pc_dir.clear();
+    if (o->disk_dir && o->disk_dir[0]) {
+      std::error_code ec;
+      std::filesystem::create_directories(o->disk_dir, ec);
+      if (!ec && std::filesystem::is_directory(o->disk_dir, ec)) s->pc_dir = o->disk_dir;
+    }
     pc_evict(s);
   });
 }

@@ -9,6 +9,7 @@ cmd/chat_rl's step loop (cmd/chat_rl/main.go:101-183).
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import numpy as np
 
@@ -246,17 +247,20 @@ class Session:
         call("gn_session_set_decode_graph", self._h, 1 if enabled else 0)
 
     def set_prefix_cache(self, max_entries: int = 0, max_bytes: int = 0, ttl: float = 0.0,
-                         max_prefix: int = 0, enabled: bool = True):
+                         max_prefix: int = 0, enabled: bool = True, disk_dir: str = ""):
         """Engine.Cache = NewCacheManager(CacheOptions{MaxEntries, MaxBytes,
-        TTL}) on the device (inference/cache.go:17-77); max_entries=1 with
-        max_prefix is Engine.Prefix = NewPrefixCache(maxPrefix)
-        (inference/prefix.go:29-35).  enabled=False turns it off and drops
-        every entry.  Generate and RL-step calls then prefill only what
-        follows each prompt's longest cached strict prefix."""
+        TTL, DiskDir}) on the device (inference/cache.go:17-77); max_entries=1
+        with max_prefix is Engine.Prefix = NewPrefixCache(maxPrefix)
+        (inference/prefix.go:29-35).  disk_dir: the on-disk tier (entries
+        written there, read back for the call that hits them).  enabled=False
+        turns it off and drops every entry.  Generate and RL-step calls then
+        prefill only what follows each prompt's longest cached strict
+        prefix."""
         if not enabled:
             call("gn_session_set_prefix_cache", self._h, None)
             return
-        o = GnPrefixCacheOptions(max_entries, max_prefix, max_bytes, ttl)
+        o = GnPrefixCacheOptions(max_entries, max_prefix, max_bytes, ttl,
+                                 os.fsencode(disk_dir) if disk_dir else None)
         call("gn_session_set_prefix_cache", self._h, C.byref(o))
 
     def prefix_cache_invalidate(self):

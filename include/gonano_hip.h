@@ -446,12 +446,19 @@ int gn_session_synchronize(gn_session *session);
  * longer equal a full prefill.  Not for CED models (GN_ERR_UNSUPPORTED; the
  * reference's engine skips them, inference/engine.go:128-140,
  * inference/prefix.go:17-19).  A call that fails leaves the cache as it
- * found it.  The on-disk tier (CacheOptions.DiskDir) is not built. */
+ * found it.  The on-disk tier is `disk_dir` below. */
 typedef struct gn_prefix_cache_options {
   int32_t max_entries; /* CacheOptions.MaxEntries; 0: unbounded */
   int32_t max_prefix;  /* NewPrefixCache(maxPrefix): longer entries never hit; 0: any */
-  int64_t max_bytes;   /* CacheOptions.MaxBytes (device bytes); 0: unbounded */
+  int64_t max_bytes;   /* CacheOptions.MaxBytes (entry bytes, either tier); 0: unbounded */
   double ttl_seconds;  /* CacheOptions.TTL from storage; 0: no expiry */
+  /* CacheOptions.DiskDir: entries are written to this directory (created if
+   * missing; if that fails, or for an entry whose file cannot be written,
+   * device memory is used) and read back for the call that hits them; a file
+   * that cannot be read drops its entry and misses.  Files are deleted with
+   * their entries (eviction, expiry, invalidation, new parameters, the
+   * session's end).  NULL or "": device memory only. */
+  const char *disk_dir;
 } gn_prefix_cache_options;
 /* NewCacheManager (cache.go:64-77) on the session: turns the cache on with
  * these limits (evicting to fit), or off with options NULL (dropping every

@@ -290,3 +290,53 @@ def test_rl_step_uses_the_cache_and_unsupported_models():
     with Session(fl) as s:
         s.set_prefix_cache()
         assert s.prefix_cache_len() == (0, 0)
+
+
+def test_disk_tier(tmp_path):
+    """CacheOptions.DiskDir (cache.go:25-28, 145-150, 254-284): entries are
+    written to the directory and read back for the call that hits them, with
+    the same results as the device-memory tier (bit for bit: the state makes
+    the round trip unchanged); eviction, a replaced prompt and invalidation
+    delete the files; a file that cannot be read (here: truncated) drops its
+    entry and the lookup misses.  On a compressed-attention model, whose
+    entries carry the compressor logits."""
+    from gonano_amd.session import Session
+    cfg = _compressed_sparse()
+    w = G.init_weights(cfg, seed=23, perturb=0.1)
+    V = cfg.vocab_size
+    rng = np.random.default_rng(5)
+    base = rng.integers(0, V, (2, 70)).astype(np.int32)
+    ext = np.concatenate([base, rng.integers(0, V, (2, 30))], axis=1).astype(np.int32)
+    calls = [base, ext, np.concatenate([ext, rng.integers(0, V, (2, 5))], axis=1).astype(np.int32)]
+    results = {}
+    for tier in ("memory", "disk"):
+        d = tmp_path / "kv"
+        with Session(cfg) as s:
+            s.set_params(w)
+            s.set_prefix_cache(max_entries=8, disk_dir=str(d) if tier == "disk" else "")
+            out = []
+            for i, prompts in enumerate(calls):
+                rows = s.generate_batch(prompts, 2, 4, 1.0, 50,
+                                        (10 * i + np.arange(2)).astype(np.uint64))
+                out.append((rows, s.prefix_cache_hits(2).tolist(), s.prefix_cache_len()))
+                if tier == "disk":
+                    assert len(list(d.iterdir())) == s.prefix_cache_len()[0] == 2 * (i + 1)
+            results[tier] = out
+            if tier == "disk":
+                # a truncated file: its entry is dropped and the prompt misses
+                f = sorted(d.iterdir(), key=lambda p: p.stat().st_mtime)[-1]
+                f.write_bytes(f.read_bytes()[:100])
+                n0 = s.prefix_cache_len()[0]
+                probe = np.concatenate([calls[2], rng.integers(0, V, (2, 1))], axis=1)
+                s.generate_batch(probe.astype(np.int32), 1, 1, 1.0, 50, np.arange(2, dtype=np.uint64))
+                assert sorted(s.prefix_cache_hits(2).tolist()) == [0, 105]
+                assert s.prefix_cache_len()[0] == n0 - 1 + 2
+                # eviction deletes files
+                s.set_prefix_cache(max_entries=3, disk_dir=str(d))
+                assert s.prefix_cache_len()[0] == 3 and len(list(d.iterdir())) == 3
+                s.prefix_cache_invalidate()
+                assert s.prefix_cache_len() == (0, 0) and not list(d.iterdir())
+    for (ra, ha, la), (rb, hb, lb) in zip(results["memory"], results["disk"]):
+        assert ha == hb and la == lb
+        assert np.array_equal(ra, rb)
+    assert [h for _, h, _ in results["disk"]] == [[0, 0], [70, 70], [100, 100]]
