@@ -1006,29 +1006,36 @@ static WideKernel wide_kernel(bool ak, bool bk, int e) {
 }
 
 // Runs d on the wide-tile engine when it suits the product: large enough to
-// fill the chip with 256 x 256 tiles (after K splits), little padding, K a
-// multiple of 64, and the 16-byte alignment its vector loads and stores
-// need.  Returns false otherwise (gemm_kernel takes it).
+// fill the chip with 256 x 256 tiles (after K splits), little padding, K at
+// least 64, and the 16-byte alignment its vector loads and stores need.
+// Returns false otherwise (gemm_kernel takes it).
 static bool gemm_wide(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
                       DeviceArena* ws) {
   using namespace wide;
   if (d.group != GEMM_GROUP_NONE || d.defer || d.force_splits > 0 || !vec) return false;
   if ((double)d.M * d.N * d.K < (double)(1 << 28)) return false;
   if (d.M < TILE || d.N < TILE) return false;
-  if (d.K % (2 * TK) || d.N % 4 || d.ldc % 4 || !aligned16(d.C)) return false;
+  if (d.N % 4 || d.ldc % 4 || !aligned16(d.C)) return false;
   if (!d.a_kcontig && d.M % 4) return false;
   const bool uses_aux = d.epi == EPI_ADD_SRC || d.epi == EPI_DRELU2;
   if (uses_aux && (!aligned16(d.aux) || d.ldaux % 4)) return false;
   if (d.epi == EPI_RELU2_SAVE && d.aux_out && (!aligned16(d.aux_out) || d.ldaux % 4)) return false;
+  // The engine runs K in whole 64-deep tile pairs: a K that is not a
+  // multiple of 64 (the weight gradients' token counts, 16 x 8703 or
+  // B x 1535) leaves its last K % 64 values to one more split, a
+  // gemm_kernel launch over the whole output writing that split's partial;
+  // gemm_reduce_kernel adds it after the engine's splits.
+  const int rem = d.K % (2 * TK), Kw = d.K - rem;
+  if (Kw < 2 * TK) return false;
   const int64_t tm = ceil_div(d.M, TILE), tn = ceil_div(d.N, TILE), tiles = tm * tn;
   // padding: at most 1/8 of the MFMA work on rows or columns past the product
   if ((double)(tm * TILE) * (double)(tn * TILE) > 1.125 * (double)d.M * (double)d.N) return false;
   const int64_t cus = 256;
-  int splits = (int)ceil_div(d.K, KCHUNK);
+  int splits = (int)ceil_div(Kw, KCHUNK);
   {
     // more splits (each at least 1024 deep) while that makes whole rounds
     // of the CUs fuller
-    const int smin = splits, smax = std::max<int>(smin, (int)std::min<int64_t>(64, d.K / 1024));
+    const int smin = splits, smax = std::max<int>(smin, (int)std::min<int64_t>(64, Kw / 1024));
     double best = -1.0;
     for (int s = smin; s <= smax; s++) {
       const int64_t wg = tiles * s;
@@ -1040,14 +1047,15 @@ static bool gemm_wide(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
       if (eff >= 0.999) break;
     }
   }
-  const int kps = (int)ceil_div(ceil_div(d.K, splits), 2 * TK) * 2 * TK;
-  splits = (int)ceil_div(d.K, kps);
+  const int kps = (int)ceil_div(ceil_div(Kw, splits), 2 * TK) * 2 * TK;
+  splits = (int)ceil_div(Kw, kps);
   // at least 3/4 of a round of the CUs (GN_GEMM_WIDE_MIN: another minimum
   // workgroup count; tests take every eligible product with 1)
   int64_t min_wg = (3 * cus) / 4;
   if (const char* e = std::getenv("GN_GEMM_WIDE_MIN")) min_wg = std::max(1, std::atoi(e));
   if (tiles * splits < min_wg) return false;
-  int e = splits > 1 ? -1 : d.epi;
+  const int parts = splits + (rem > 0 ? 1 : 0);  // partial sums, the remainder's last
+  int e = parts > 1 ? -1 : d.epi;
   if (e == EPI_RELU2_SAVE && !d.aux_out) e = EPI_RELU2_SAVE + 16;
   const WideKernel kern = wide_kernel(d.a_kcontig, d.b_kcontig, e);
   if (!kern) return false;
@@ -1055,13 +1063,30 @@ static bool gemm_wide(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
   p.tiles_n = (int)tn;
   p.splits = splits;
   p.k_per_split = kps;
-  if (splits > 1) {
+  p.K = Kw;
+  if (parts > 1) {
     GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
-    p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N);
+    p.part = ws->get<float>("gemm_splitk", (size_t)parts * d.M * d.N);
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * splits)), dim3(256), 0, st, p);
   GN_HIP(hipGetLastError());
-  if (splits > 1) {
+  if (rem > 0) {  // K values [Kw, K): a plain product into the last partial
+    GemmParams q = p;
+    q.A = d.a_kcontig ? d.A + Kw : d.A + (int64_t)Kw * d.lda;
+    q.B = d.b_kcontig ? d.B + Kw : d.B + (int64_t)Kw * d.ldb;
+    q.K = rem;
+    q.k_per_split = rem;
+    q.C = p.part + (int64_t)splits * d.M * d.N;
+    q.ldc = d.N;
+    q.epi = EPI_STORE;
+    q.alpha = 1.f;
+    q.aux = nullptr;
+    q.aux_out = nullptr;
+    q.part = nullptr;
+    launch_cfg<128, 128, 2, 2, 1, 2, false>(q, d.a_kcontig, d.b_kcontig, vec, 1, st);
+  }
+  if (parts > 1) {
+    p.splits = parts;
     const int64_t total = (int64_t)d.M * d.N;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
                        p);

@@ -245,6 +245,20 @@ def test_d12_width_pg_step_wide_engine(orc, d12w, monkeypatch):
     assert t["gemm_wide_launches"] == t["gemm_launches"], t
 
 
+def test_d12_width_pg_step_wide_engine_ragged_k(orc, d12w, monkeypatch):
+    """As above with 4 x 500 tokens: the weight gradients' K (2000 tokens) is
+    not a multiple of 64, so the engine runs K in [0, 1984) as its splits
+    and the last 16 tokens as one more split on gemm_kernel, summed with the
+    others by the reduction (the flash and d20 workloads' token counts,
+    16 x 8703 and B x 1535, take this path)."""
+    cfg, w = d12w
+    monkeypatch.setenv("GN_GEMM_WIDE_MIN", "1")
+    t = _pg_check(orc, cfg, w, B=4, T=500, prompt_len=372, chunk=256, monkeypatch=monkeypatch,
+                  timing=True)
+    monkeypatch.delenv("GN_GEMM_WIDE_MIN")
+    assert t["gemm_wide_launches"] == t["gemm_launches"], t
+
+
 def test_d12_width_graph_equals_eager(d12w):
     """The captured decode graph at the d12 width replays the eager steps
     token for token (two replays, eager work between them)."""
