@@ -26,8 +26,11 @@ struct CopyBlock {
   int32_t outer, inner;
 };
 void launch_copy_blocks(const CopyBlock* descs, int n, hipStream_t st);
-void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg, const float* lam,
-                         int rows, int C, float* prev, float* x, float* x0, hipStream_t st);
+// ovr (nullable): per row, a token fed instead of tok's (>= 0) or -1; the
+// fed token is written back to tok.
+void launch_embed_decode(int32_t* tok, const float* wte, const float* wsg, const float* lam,
+                         int rows, int C, float* prev, float* x, float* x0, hipStream_t st,
+                         const int32_t* ovr = nullptr);
 // xin (resp. x) may be the target of a residual-add GEMM whose split-K sum
 // was deferred (pend): the kernels then read xin + sum, and norm_rows
 // writes that value back to x.

@@ -92,7 +92,11 @@ void launch_embed_smear(const int32_t* ids, const float* wte, const float* wsg, 
 
 // Decode step embedding (transformer.go:276-300 with T == 1): embn =
 // norm(wte[tok]); x = embn + lambda*sigmoid(embn[:24].w)*prev; prev = embn.
-__global__ __launch_bounds__(256) void embed_decode_kernel(const int32_t* __restrict__ tok,
+// tok [rows] is the column fed; with ovr (nullable) a row whose ovr entry
+// is >= 0 is fed that token instead, and it is written back to tok (the
+// step's later kernels read the fed token).
+__global__ __launch_bounds__(256) void embed_decode_kernel(int32_t* tok,
+                                                           const int32_t* __restrict__ ovr,
                                                            const float* __restrict__ wte, int C,
                                                            const float* __restrict__ wsg,
                                                            const float* __restrict__ lam,
@@ -102,7 +106,9 @@ __global__ __launch_bounds__(256) void embed_decode_kernel(const int32_t* __rest
   __shared__ float sc[4];
   __shared__ float gate_s;
   const int64_t r = blockIdx.x;
-  const float* src = wte + (int64_t)tok[r] * C;
+  int32_t t = tok[r];
+  if (ovr && ovr[r] >= 0) t = ovr[r];
+  const float* src = wte + (int64_t)t * C;
   float ss = 0.f;
   for (int c = threadIdx.x; c < C; c += 256) ss += src[c] * src[c];
   ss = bsum256(ss, sc);
@@ -112,7 +118,8 @@ __global__ __launch_bounds__(256) void embed_decode_kernel(const int32_t* __rest
     p = warp_sum(p);
     if (threadIdx.x == 0) gate_s = sigmoidf_(p) * lam[0];
   }
-  __syncthreads();
+  __syncthreads();  // every thread has read tok[r]
+  if (ovr && threadIdx.x == 0) tok[r] = t;
   const float g = gate_s;
   for (int c = threadIdx.x; c < C; c += 256) {
     float e = src[c] * inv;
@@ -122,10 +129,11 @@ __global__ __launch_bounds__(256) void embed_decode_kernel(const int32_t* __rest
     x0[r * C + c] = v;
   }
 }
-void launch_embed_decode(const int32_t* tok, const float* wte, const float* wsg, const float* lam,
-                         int rows, int C, float* prev, float* x, float* x0, hipStream_t st) {
-  hipLaunchKernelGGL(embed_decode_kernel, dim3(rows), dim3(256), 0, st, tok, wte, C, wsg, lam,
-                     prev, x, x0);
+void launch_embed_decode(int32_t* tok, const float* wte, const float* wsg, const float* lam,
+                         int rows, int C, float* prev, float* x, float* x0, hipStream_t st,
+                         const int32_t* ovr) {
+  hipLaunchKernelGGL(embed_decode_kernel, dim3(rows), dim3(256), 0, st, tok, ovr, wte, C, wsg,
+                     lam, prev, x, x0);
   GN_HIP(hipGetLastError());
 }
 

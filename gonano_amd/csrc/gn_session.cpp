@@ -1964,7 +1964,8 @@ static void hca_decode_layer(gn_session* s, const Layer& ly, int l, int rows, in
 }
 
 static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* dtok, float* kc,
-                        float* vc, float* logits, const int* dpos = nullptr) {
+                        float* vc, float* logits, const int* dpos = nullptr,
+                        const int32_t* ovr = nullptr) {
   const int C = s->C, Hq = s->Hq, Hkv = s->Hkv, F = s->F, L = s->L;
   hipStream_t st = s->stream;
   float* x = A<float>(s, "dec_x", (size_t)rows * C);
@@ -1992,7 +1993,7 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   float* part = s->mla ? nullptr
                        : A<float>(s, "dec_part", (size_t)rows * Hkv * part_splits *
                                                      (Hq / Hkv) * (HD + 2));
-  launch_embed_decode(dtok, s->wte, s->smg, s->sml, rows, C, prev, x, x0, st);
+  launch_embed_decode(dtok, s->wte, s->smg, s->sml, rows, C, prev, x, x0, st, ovr);
   const int bk = L / 2;
   // The decode projections split K (M = rows is small); their partial sums
   // are added by the next row kernel instead of a reduction launch: qkv by
@@ -2787,12 +2788,24 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   if (pcache) launch_expand_last_rows(gemb, prev, G, 1, S, C, st);
   else launch_expand_last_rows(sb.embn, prev, G, Tlast, S, C, st);
 
-  // 3) decode loop (engine.go:238-325).  Iteration `step` runs the forward
-  //    that feeds the previous column (none at step 0: the prefill logits)
-  //    and samples column `step`.  After two eager iterations (which size
-  //    every buffer) forward + sampler are captured once as a HIP graph and
-  //    replayed; the step position, the column and the group streams'
-  //    base states reach the device through small copies before each launch.
+  // 3) decode loop (engine.go:238-325).  Step `step` runs the forward that
+  //    feeds column step - 1 (none at step 0: the prefill logits) and
+  //    samples column `step`.  After two eager steps (which size every
+  //    buffer) forward + sampler are captured once as a HIP graph and
+  //    replayed.  The sampler writes its ids into the buffer the next
+  //    forward reads, so the steps are pipelined: step `step` is launched
+  //    before the host runs the row state machine on column step - 1, and
+  //    the device is never idle waiting for the host.  That is exact because
+  //    whether a row's next column is forced depends only on the state
+  //    after the column before it: the forced tokens of column step - 1
+  //    (known once column step - 2 is processed) reach the forward as an
+  //    override (a token >= 0 replaces the sampled id; the embedding kernel
+  //    writes it back), and a step launched past the end (every row done
+  //    after its previous column) is discarded.  Per step the base states of
+  //    the group streams, the override and the position reach the device in
+  //    one copy from a pinned block (two blocks, alternating, so a copy
+  //    still queued is never overwritten), the sampled ids come back in one
+  //    copy (two buffers, alternating).
   std::vector<RowState> states(rows);
   // a prompt that ends inside a reasoning trace starts every row of its group
   // there, so the budget counts from the first generated token (engine.go:226-236)
@@ -2802,15 +2815,20 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
       states[r].in_thinking = prompts[(int64_t)(r / S) * P + P - 1] == opt.think_start;
   std::vector<u128h> stream(G);
   for (int g = 0; g < G; g++) stream[g] = new_rng_state(seeds[g]);
-  uint64_t* dbase = A<uint64_t>(s, "rng_base", 2 * G);
+  // device inputs of a step: base states [2G] u64 | override [rows] i32 | position
+  const size_t in_bytes = sizeof(uint64_t) * 2 * G + sizeof(int32_t) * (rows + 1);
+  char* din = A<char>(s, "dec_in", in_bytes);
+  uint64_t* dbase = reinterpret_cast<uint64_t*>(din);
+  int32_t* dovr = reinterpret_cast<int32_t*>(dbase + 2 * G);
+  int* dpos = dovr + rows;
   int32_t* dtok = A<int32_t>(s, "dec_tok", rows);
-  int* dpos = A<int>(s, "dec_pos", 1);
-  // pinned staging: base states | column | sampled | position
-  char* hp = static_cast<char*>(pinned(s, sizeof(uint64_t) * 2 * G + sizeof(int32_t) * (2 * rows + 1)));
-  uint64_t* base = reinterpret_cast<uint64_t*>(hp);
-  int32_t* column = reinterpret_cast<int32_t*>(base + 2 * G);
-  int32_t* sampled = column + rows;
-  int32_t* hpos = sampled + rows;
+  // pinned staging: two input blocks, then two sampled-id buffers
+  const size_t in_pad = (in_bytes + 255) / 256 * 256;
+  char* hp = static_cast<char*>(pinned(s, 2 * in_pad + 2 * sizeof(int32_t) * rows));
+  int32_t* hsampled[2] = {reinterpret_cast<int32_t*>(hp + 2 * in_pad),
+                          reinterpret_cast<int32_t*>(hp + 2 * in_pad) + rows};
+  hipEvent_t evs[2] = {next_event(s), next_event(s)};
+  std::vector<int32_t> column(rows);
   std::vector<char> done(rows, 0);
   int ndone = 0;
   SamplerArgs sa{};
@@ -2831,26 +2849,35 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
   // for their eager steps.)
   const bool use_graph = s->decode_graph && N >= 4;
 
-  for (int step = 0; step < N; step++) {
+  // Launches step `step`: its inputs (the override of the column it feeds
+  // comes from the rows' forced tokens), forward + sampler, the ids back.
+  auto launch = [&](int step) {
+    char* hin = hp + (step & 1) * in_pad;
+    uint64_t* base = reinterpret_cast<uint64_t*>(hin);
+    int32_t* ovr = reinterpret_cast<int32_t*>(base + 2 * G);
     for (int g = 0; g < G; g++) {
       base[2 * g] = (uint64_t)(stream[g] >> 64);
       base[2 * g + 1] = (uint64_t)stream[g];
       stream[g] = pcg_advance_host(stream[g], (u128h)S * (u128h)V);
     }
-    const int pos = P + step - 1;  // position of the previous column
-    if (step > 0) {
-      *hpos = pos;
-      GN_HIP(hipMemcpyAsync(dtok, column, sizeof(int32_t) * rows, hipMemcpyHostToDevice, st));
+    for (int r = 0; r < rows; r++) {
+      const RowState& rs = states[r];
+      ovr[r] = -1;
+      if (rs.forced_pos < rs.forced.size()) {
+        ovr[r] = rs.forced[rs.forced_pos];
+        GN_CHECK(ovr[r] >= 0 && ovr[r] < s->PV, "forced token outside the embedding table");
+      }
     }
-    GN_HIP(hipMemcpyAsync(dbase, base, sizeof(uint64_t) * 2 * G, hipMemcpyHostToDevice, st));
-    const bool replay = use_graph && step >= 2;
-    if (replay) {
-      GN_HIP(hipMemcpyAsync(dpos, hpos, sizeof(int), hipMemcpyHostToDevice, st));
+    const int pos = P + step - 1;  // position of the column fed
+    ovr[rows] = pos;
+    GN_HIP(hipMemcpyAsync(din, hin, in_bytes, hipMemcpyHostToDevice, st));
+    if (use_graph && step >= 2) {
       if (!graph.e) {
+        GN_HIP(hipStreamSynchronize(st));  // the capture starts on an idle stream
         GN_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         s->capturing = true;
         try {
-          decode_step(s, rows, pos, maxSeq, dtok, kc, vc, logits, dpos);
+          decode_step(s, rows, pos, maxSeq, dtok, kc, vc, logits, dpos, dovr);
           launch_sampler(sa, st);
         } catch (...) {
           s->capturing = false;
@@ -2865,12 +2892,18 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
       }
       GN_HIP(hipGraphLaunch(graph.e, st));
     } else {
-      if (step > 0) decode_step(s, rows, pos, maxSeq, dtok, kc, vc, logits);
+      if (step > 0) decode_step(s, rows, pos, maxSeq, dtok, kc, vc, logits, nullptr, dovr);
       launch_sampler(sa, st);
     }
-    GN_HIP(hipMemcpyAsync(sampled, dtok, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
-    GN_HIP(hipStreamSynchronize(st));
-    // the row state machine (engine.go:258-314)
+    GN_HIP(hipMemcpyAsync(hsampled[step & 1], dtok, sizeof(int32_t) * rows,
+                          hipMemcpyDeviceToHost, st));
+    GN_HIP(hipEventRecord(evs[step & 1], st));
+  };
+  // The row state machine on column `step` (engine.go:258-314); true when
+  // generation ends with it.
+  auto process = [&](int step) -> bool {
+    GN_HIP(hipEventSynchronize(evs[step & 1]));
+    const int32_t* sampled = hsampled[step & 1];
     for (int r = 0; r < rows; r++) {
       RowState& rs = states[r];
       int tok;
@@ -2913,11 +2946,20 @@ static void generate(gn_session* s, const int32_t* prompts, int G, int P, int S,
         }
       }
     }
-    if (ndone == rows) break;
-    if (step + 1 == N) break;  // the reference's final forward feeds no sample
-    for (int r = 0; r < rows; r++)
-      GN_CHECK(column[r] >= 0 && column[r] < s->PV, "forced token outside the embedding table");
+    // the reference's final forward feeds no sample
+    return ndone == rows || step + 1 == N;
+  };
+  if (N > 0) {
+    launch(0);
+    bool end = false;
+    for (int step = 1; step < N && !end; step++) {
+      launch(step);
+      end = process(step - 1);
+    }
+    if (!end) process(N - 1);
   }
+  // nothing may still write the pinned staging (a step launched past the end)
+  GN_HIP(hipStreamSynchronize(st));
   if (s->timing) {
     GN_HIP(hipEventRecord(ev1, st));
     GN_HIP(hipStreamSynchronize(st));
