@@ -205,7 +205,7 @@ struct QkvPostBwdArgs {
   int Hq, Hkv, R, T;
   float* dqkv;
   float* dpre;
-  float* gve;
+  float* gve_rows;  // [rows][Hkv*128] the value-embedding gradient of each token's row
 };
 void launch_qkv_post_bwd(const QkvPostBwdArgs& a, int64_t rows, hipStream_t st);
 void launch_ve_gate_bwd(const float* dpre, const float* h, const float* W, int C, int Hkv,
@@ -213,8 +213,19 @@ void launch_ve_gate_bwd(const float* dpre, const float* h, const float* W, int C
 void launch_smear_bwd(const float* ga, const float* embn, const float* smsig, const float* lam,
                       const float* wsg, int B, int T, int C, float* ge, float* ggate,
                       double* lam_rows, double* part, float* dwsg, float* dlam, hipStream_t st);
-void launch_embed_scatter(const float* g, const int32_t* ids, int C, int64_t N, float* gw,
-                          hipStream_t st);
+// A batch's tokens grouped by id (host-built, on the device): perm lists
+// token indices, ascending within each id; id u (of n_ids, ascending) owns
+// perm[off[u] .. off[u+1]) and is uid[u].
+struct TokenGroups {
+  const int32_t* perm = nullptr;
+  const int32_t* off = nullptr;
+  const int32_t* uid = nullptr;
+  int n_ids = 0;
+};
+// gw[id] += the rows g[n] of the tokens with that id, added in token order
+// (embedding and value-embedding backward).
+void launch_rows_scatter(const float* g, const TokenGroups& ids, int C, float* gw,
+                         hipStream_t st);
 
 // ---- latent preset: MLA (model/mla.go) ------------------------------------
 // xa rows are [q_lat (lat) | kv_lat (lat) | q_rope (Hq*rd) | k_rope (Hkv*rd)]

@@ -1100,7 +1100,7 @@ __global__ __launch_bounds__(256) void qkv_post_bwd_kernel(QkvPostBwdArgs a) {
   for (int i = tid; i < a.Hkv * D; i += 256) out[(a.Hq + a.Hkv) * D + i] = a.dv[n * a.Hkv * D + i];
   if (a.vesig) {
     const float* ver = a.ve + (int64_t)a.ids[n] * a.Hkv * D;
-    float* gver = a.gve + (int64_t)a.ids[n] * a.Hkv * D;
+    float* gver = a.gve_rows + n * a.Hkv * D;  // this token's row, scattered by id afterwards
     for (int hk = wid; hk < a.Hkv; hk += 4) {
       const float s = a.vesig[n * a.Hkv + hk];
       const float scale = s * VE_SCALE;
@@ -1109,7 +1109,7 @@ __global__ __launch_bounds__(256) void qkv_post_bwd_kernel(QkvPostBwdArgs a) {
       for (int e = 0; e < 2; e++) {
         int d = lane + 64 * e;
         float gv = a.dv[(n * a.Hkv + hk) * D + d];
-        atomicAdd(&gver[hk * D + d], gv * scale);
+        gver[hk * D + d] = gv * scale;
         dot += (double)gv * (double)ver[hk * D + d];
       }
       dot = warp_sum_d(dot);
@@ -1258,20 +1258,28 @@ void launch_smear_bwd(const float* ga, const float* embn, const float* smsig, co
   GN_HIP(hipGetLastError());
 }
 
-// Embedding backward: scatter-add rows of g into the table at ids
-// (linear.go:90-104).
-__global__ void embed_scatter_kernel(const float* __restrict__ g, const int32_t* __restrict__ ids,
-                                     int C, int64_t N, float* __restrict__ gw) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= N * C) return;
-  int64_t n = i / C;
-  int c = (int)(i % C);
-  atomicAdd(&gw[(int64_t)ids[n] * C + c], g[i]);
+// Embedding backward: scatter-add rows of g into the table at the tokens'
+// ids (linear.go:90-104: for n in order, gw[ids[n]] += g[n]).  The tokens
+// come grouped by id (ids.perm: token indices, ascending within an id,
+// ids.off: each id's range, ids.uid: the ids), so one thread owns each
+// (id, column) and adds the id's rows in token order: the reference's
+// float32 additions in its order, and the same bits on every run (float
+// atomics would add in arrival order).
+__global__ __launch_bounds__(256) void rows_scatter_kernel(const float* __restrict__ g, TokenGroups ids,
+                                                           int C, float* __restrict__ gw) {
+  const int u = blockIdx.x;
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  if (c >= C) return;
+  float* dst = gw + (int64_t)ids.uid[u] * C + c;
+  float acc = *dst;
+  for (int j = ids.off[u]; j < ids.off[u + 1]; j++) acc += g[(int64_t)ids.perm[j] * C + c];
+  *dst = acc;
 }
-void launch_embed_scatter(const float* g, const int32_t* ids, int C, int64_t N, float* gw,
-                          hipStream_t st) {
-  hipLaunchKernelGGL(embed_scatter_kernel, dim3((unsigned)ceil_div(N * C, 256)), dim3(256), 0, st,
-                     g, ids, C, N, gw);
+void launch_rows_scatter(const float* g, const TokenGroups& ids, int C, float* gw,
+                         hipStream_t st) {
+  if (ids.n_ids == 0) return;
+  hipLaunchKernelGGL(rows_scatter_kernel, dim3((unsigned)ids.n_ids, (unsigned)ceil_div(C, 256)),
+                     dim3(256), 0, st, g, ids, C, gw);
   GN_HIP(hipGetLastError());
 }
 

@@ -652,6 +652,8 @@ struct SeqBuffers {
   int pre_len = 0;
   float *kv_k = nullptr, *kv_v = nullptr;
   const float* seed_prev = nullptr;
+  // training: the tokens grouped by id, for the embedding gradients
+  TokenGroups groups;
   // when set (a forward from position 0), every layer's token-major
   // keys/values are copied here: [L][B*T][Hkv*128]
   float *tm_k_out = nullptr, *tm_v_out = nullptr;
@@ -1489,6 +1491,33 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
   SeqBuffers sb;
   sb.B = B; sb.T = T; sb.N = N;
   sb.ids = upload_ids(s, "ids", inputs, N, V);
+  // the tokens grouped by id (counting sort, token order kept within an id)
+  // for the deterministic embedding-gradient scatters
+  std::vector<int32_t> grp;  // perm [N] | off [U+1] | uid [U]
+  {
+    std::vector<int32_t> cnt((size_t)s->PV + 1, 0);
+    for (int64_t i = 0; i < N; i++) cnt[(size_t)inputs[i] + 1]++;
+    int U = 0;
+    for (int v = 0; v < s->PV; v++) U += cnt[(size_t)v + 1] > 0;
+    for (int v = 0; v < s->PV; v++) cnt[(size_t)v + 1] += cnt[v];
+    grp.resize((size_t)N + 2 * (size_t)U + 1);
+    int32_t *perm = grp.data(), *off = perm + N, *uid = off + U + 1;
+    std::vector<int32_t> fill(cnt.begin(), cnt.end() - 1);
+    for (int64_t i = 0; i < N; i++) perm[fill[inputs[i]]++] = (int32_t)i;
+    int u = 0;
+    for (int v = 0; v < s->PV; v++)
+      if (cnt[(size_t)v + 1] > cnt[v]) {
+        off[u] = cnt[v];
+        uid[u++] = v;
+      }
+    off[U] = (int32_t)N;
+    int32_t* d = A<int32_t>(s, "id_groups", grp.size());
+    GN_HIP(hipMemcpyAsync(d, grp.data(), sizeof(int32_t) * grp.size(), hipMemcpyHostToDevice, st));
+    sb.groups.perm = d;
+    sb.groups.off = d + N;
+    sb.groups.uid = d + N + U + 1;
+    sb.groups.n_ids = U;
+  }
   int32_t* dtg = A<int32_t>(s, "targets", N);
   GN_HIP(hipMemcpyAsync(dtg, targets, sizeof(int32_t) * N, hipMemcpyHostToDevice, st));
   float* dadv = A<float>(s, "adv", B);
@@ -1641,8 +1670,10 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
     qb.vesig = ly.has_ve ? sb.vesig[l] : nullptr;
     qb.ve = ly.ve; qb.ids = sb.ids; qb.cosT = s->cosT; qb.sinT = s->sinT;
     qb.Hq = Hq; qb.Hkv = Hkv; qb.R = s->R; qb.T = T;
-    qb.dqkv = dqkv; qb.dpre = dpre; qb.gve = ly.gve;
+    qb.dqkv = dqkv; qb.dpre = dpre;
+    qb.gve_rows = ly.has_ve ? A<float>(s, "gve_rows", (size_t)N * Hkv * HD) : nullptr;
     launch_qkv_post_bwd(qb, N, st);
+    if (ly.has_ve) launch_rows_scatter(qb.gve_rows, sb.groups, Hkv * HD, ly.gve, st);
     sgemm(s, linear_dx_desc(dqkv, ly.wqkv, dh, (int)N, C, s->QKVW));
     sgemm(s, linear_dw_desc(dqkv, sb.h[l], ly.gqkv, (int)N, C, s->QKVW));
     if (ly.has_ve) launch_ve_gate_bwd(dpre, sb.h[l], ly.wve, C, Hkv, N, ly.gwve, dh, part, st);
@@ -1664,7 +1695,7 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
   launch_smear_bwd(g, sb.embn, sb.smsig, s->sml, s->smg, B, T, C, ge, ggate, lam_rows, part,
                    s->gsmg, s->gsml, st);
   launch_rmsnorm_bwd(sb.raw, ge, nullptr, N, C, gb, st);
-  launch_embed_scatter(gb, sb.ids, C, N, s->gwte, st);
+  launch_rows_scatter(gb, sb.groups, C, s->gwte, st);
 
   double loss = 0, aux = 0;
   GN_HIP(hipMemcpyAsync(&loss, dloss, sizeof(double), hipMemcpyDeviceToHost, st));
