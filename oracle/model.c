@@ -572,8 +572,8 @@ static void rope_row(MODEL *m, REAL *dst, const REAL *src, int heads, int pos, i
 
 /* One (batch, head) attention with the reference mask; scores and
  * probabilities materialized (kernels/scalar/attention.go:16-49). */
-static void attn_fwd(const REAL *q, const REAL *k, const REAL *v, REAL *out, REAL *lse, int qlen,
-                     int klen, int D, int offset, int window) {
+static void attn_fwd_full(const REAL *q, const REAL *k, const REAL *v, REAL *out, REAL *lse,
+                          int qlen, int klen, int D, int offset, int window) {
   REAL *sc = (REAL *)malloc(sizeof(REAL) * klen);
   for (int qi = 0; qi < qlen; qi++) {
     int qpos = offset + qi;
@@ -602,6 +602,52 @@ static void attn_fwd(const REAL *q, const REAL *k, const REAL *v, REAL *out, REA
   }
   free(sc);
 }
+static void attn_key_range(int qpos, int klen, int window, int *lo, int *hi) {
+  *hi = qpos < klen - 1 ? qpos : klen - 1;
+  *lo = (window >= 0 && qpos - window > 0) ? qpos - window : 0;
+}
+/* The same over each query's valid keys [lo, hi] only: a masked score is
+ * -1e30, below every valid one (the maximum is unchanged), and its
+ * exponential and probability are exactly 0, so the sums skip exact zeros.
+ * Same results, O(T x window) work. */
+static void attn_fwd(const REAL *q, const REAL *k, const REAL *v, REAL *out, REAL *lse, int qlen,
+                     int klen, int D, int offset, int window) {
+  for (int qi = 0; qi < qlen; qi++) {
+    int lo, hi;
+    attn_key_range(offset + qi, klen, window, &lo, &hi);
+    if (lo > hi) { /* a row with no valid key: the reference's arithmetic */
+      attn_fwd_full(q, k, v, out, lse, qlen, klen, D, offset, window);
+      return;
+    }
+  }
+  REAL *sc = (REAL *)malloc(sizeof(REAL) * klen);
+  for (int qi = 0; qi < qlen; qi++) {
+    int lo, hi;
+    attn_key_range(offset + qi, klen, window, &lo, &hi);
+    REAL mx = 0;
+    for (int kj = lo; kj <= hi; kj++) {
+      double a = 0;
+      for (int d = 0; d < D; d++) a += (double)q[qi * D + d] * (double)k[(int64_t)kj * D + d];
+      REAL s = R(a);
+      sc[kj] = s;
+      if (kj == lo || s > mx) mx = s;
+    }
+    double tot = 0;
+    for (int kj = lo; kj <= hi; kj++) {
+      double e = exp((double)(sc[kj] - mx));
+      sc[kj] = R(e);
+      tot += e;
+    }
+    if (lse) lse[qi] = mx + R(log(tot));
+    REAL inv = R(1.0 / tot);
+    for (int d = 0; d < D; d++) {
+      double a = 0;
+      for (int kj = lo; kj <= hi; kj++) a += (double)sc[kj] * (double)v[(int64_t)kj * D + d];
+      out[qi * D + d] = R(a) * inv;
+    }
+  }
+  free(sc);
+}
 /* kernels/scalar/attention.go:145-205, gradients accumulated. */
 static void attn_bwd_corr(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
                           const REAL *lse, const REAL *corr, REAL *dq, REAL *dk, REAL *dv,
@@ -611,9 +657,10 @@ static void attn_bwd(const REAL *q, const REAL *k, const REAL *v, const REAL *do
                      int offset, int window) {
   attn_bwd_corr(q, k, v, dout, lse, NULL, dq, dk, dv, qlen, klen, D, offset, window);
 }
-/* corr, when given, replaces the row sum of dP*P (the merged-branch row
- * correction dO.O, model/train.go:211-226). */
-static void attn_bwd_corr(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
+/* kernels/scalar/attention.go:145-205 over every (query, key) pair, the
+ * masked ones included; corr, when given, replaces the row sum of dP*P (the
+ * merged-branch row correction dO.O, model/train.go:211-226). */
+static void attn_bwd_full(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
                           const REAL *lse, const REAL *corr, REAL *dq, REAL *dk, REAL *dv,
                           int qlen, int klen, int D, int offset, int window) {
   REAL *P = (REAL *)malloc(sizeof(REAL) * (int64_t)qlen * klen);
@@ -663,6 +710,66 @@ static void attn_bwd_corr(const REAL *q, const REAL *k, const REAL *v, const REA
   free(dS);
 }
 
+/* corr, when given, replaces the row sum of dP*P (the merged-branch row
+ * correction dO.O, model/train.go:211-226).
+ * The reference computes every (query, key) pair and masks the invalid ones
+ * to -1e30, whose probability is exactly 0, so every sum below gets exact
+ * zeros from them; those terms are skipped here (each query's valid keys
+ * are the range [lo, hi]), and the sums over queries (dv, dk) accumulate in
+ * float64 per element with the queries in ascending order, as the
+ * reference's loops add them.  Same results, O(T x window) work. */
+static void attn_bwd_corr(const REAL *q, const REAL *k, const REAL *v, const REAL *dout,
+                          const REAL *lse, const REAL *corr, REAL *dq, REAL *dk, REAL *dv,
+                          int qlen, int klen, int D, int offset, int window) {
+  for (int qi = 0; qi < qlen; qi++) {
+    int lo, hi;
+    attn_key_range(offset + qi, klen, window, &lo, &hi);
+    if (lo > hi) { /* no valid key: the reference's arithmetic on the masked row */
+      attn_bwd_full(q, k, v, dout, lse, corr, dq, dk, dv, qlen, klen, D, offset, window);
+      return;
+    }
+  }
+  double *adv = (double *)calloc((size_t)klen * D, sizeof(double));
+  double *adk = (double *)calloc((size_t)klen * D, sizeof(double));
+  double *P = (double *)malloc(sizeof(double) * klen);
+  double *dp = (double *)malloc(sizeof(double) * klen);
+  for (int qi = 0; qi < qlen; qi++) {
+    int lo, hi;
+    attn_key_range(offset + qi, klen, window, &lo, &hi);
+    for (int kj = lo; kj <= hi; kj++) {
+      double a = 0;
+      for (int d = 0; d < D; d++) a += (double)q[qi * D + d] * (double)k[(int64_t)kj * D + d];
+      REAL s = R(a);
+      P[kj] = (double)(s <= R(MASKED) ? R(0) : R(exp((double)(s - lse[qi]))));
+    }
+    for (int kj = lo; kj <= hi; kj++)
+      for (int d = 0; d < D; d++) adv[(int64_t)kj * D + d] += P[kj] * (double)dout[qi * D + d];
+    double rd = 0;
+    for (int kj = lo; kj <= hi; kj++) {
+      double a = 0;
+      for (int d = 0; d < D; d++) a += (double)dout[qi * D + d] * (double)v[(int64_t)kj * D + d];
+      dp[kj] = (double)R(a);
+      rd += dp[kj] * P[kj];
+    }
+    if (corr) rd = (double)corr[qi];
+    for (int kj = lo; kj <= hi; kj++) dp[kj] = (double)R(P[kj] * (dp[kj] - rd));
+    for (int d = 0; d < D; d++) {
+      double a = 0;
+      for (int kj = lo; kj <= hi; kj++) a += dp[kj] * (double)k[(int64_t)kj * D + d];
+      dq[qi * D + d] += R(a);
+    }
+    for (int kj = lo; kj <= hi; kj++)
+      for (int d = 0; d < D; d++) adk[(int64_t)kj * D + d] += dp[kj] * (double)q[qi * D + d];
+  }
+  for (int64_t i = 0; i < (int64_t)klen * D; i++) {
+    dv[i] += R(adv[i]);
+    dk[i] += R(adk[i]);
+  }
+  free(adv);
+  free(adk);
+  free(P);
+  free(dp);
+}
 /* tensors/math.go:38-45: z = 15*tanh(y*(1/15)) with the float32 reciprocal. */
 static REAL softcap(REAL y) {
   REAL inv = R(1) / R(SOFTCAP);
