@@ -62,6 +62,16 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 // that request every K and V byte up front (16 or 32 lanes per key), that
 // keep per-half-wave softmax states merged once, or that stream K and V in
 // one online-softmax pass all measured 16.7-18.6 us.
+// With the q/k/v post-processing fused in, the position's own key and value
+// (the last key of the last split) are not read from the cache: the block
+// computes them into LDS, scores that key in one extra step of the last
+// wave and adds that value row last, then writes both cache rows at its
+// end.  The cached keys split evenly over the waves (a 129-key window: 16
+// per wave, every K row requested before the first wait; before, 17 per
+// wave left one load behind the first step): d12 in place, 18.7 -> 18.2 us
+// per 129-key call, 41.5 -> 41.1 us on the full-context layers.  Copying V
+// rows 64..127 into LDS with global_load_lds at the start (so no V load is
+// left for phase 3) measured slower, 19.2 us.
 // One split covering the whole window writes the normalized output; several
 // splits write (unnormalized output, max, sum) for decode_combine_kernel.
 // ---------------------------------------------------------------------------
@@ -215,10 +225,8 @@ struct DecPost {
     }
   }
   // q heads (rotated, normed, 1.2 x) into out[0..R), the key into out[R], the
-  // value into out[R + 1]; the block holding the position also writes the
-  // key and value rows of the cache.
-  __device__ __forceinline__ void compute(const QkvPostArgs& p, float (*out)[HD], float* kc,
-                                          float* vc, int64_t crow, bool write_cache, int wid,
+  // value into out[R + 1].
+  __device__ __forceinline__ void compute(const QkvPostArgs& p, float (*out)[HD], int wid,
                                           int lane) {
     const int half = p.R / 2, off = HD - p.R;
 #pragma unroll
@@ -246,10 +254,7 @@ struct DecPost {
           for (int e = 0; e < 2; e++) x[e] += gate * ve[e];
         }
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-          out[hd][lane + 64 * e] = x[e];
-          if (write_cache) vc[crow * HD + lane + 64 * e] = x[e];
-        }
+        for (int e = 0; e < 2; e++) out[hd][lane + 64 * e] = x[e];
         continue;
       }
       // rotate the trailing R dims (partners through LDS, this wave's own row)
@@ -271,9 +276,7 @@ struct DecPost {
       const float inv = 1.f / sqrtf(ss / (float)HD + NORM_EPS);
 #pragma unroll
       for (int e = 0; e < 2; e++) {
-        const float o = y[e] * inv * QK_SCALE;
-        out[hd][lane + 64 * e] = o;
-        if (hd == R && write_cache) kc[crow * HD + lane + 64 * e] = o;
+        out[hd][lane + 64 * e] = y[e] * inv * QK_SCALE;
       }
     }
   }
@@ -315,6 +318,9 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
     dp.load(a.post, row, hk, qpos, wid, lane);
     __builtin_amdgcn_sched_barrier(0);
   }
+  // keys [0, nc) come from the cache; the position's own key, the last of
+  // its split, is taken from `post` (not loaded)
+  const int nc = jn >= 0 ? nk - 1 : nk;
 
   const int d4 = tid & 31, jr = tid >> 5;
   const v4f* vrow = reinterpret_cast<const v4f*>(vbase) + d4;
@@ -337,8 +343,8 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
         }
     };
     if constexpr (!FUSE) read_q(a.q + ((int64_t)row * a.Hq + hk * R) * HD + 4 * part);
-    const int qw = (nk + NW - 1) / NW;
-    const int j0 = wid * qw, j1 = min(nk, j0 + qw);
+    const int qw = (nc + NW - 1) / NW;
+    const int j0 = wid * qw, j1 = min(nc, j0 + qw);
     const v4f* kb = reinterpret_cast<const v4f*>(kbase + 4 * part);
     auto load = [&](int j, v4f* kd) {
       const int jj = j < j1 ? j : j0;  // clamp (value unused when j >= j1)
@@ -355,42 +361,55 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
 #pragma unroll
     for (int i = 0; i < VP; i++) {
       const int j = jr + RS * i;
-      vpre[i] = vrow[krow(j < nk ? j : 0) * (HD / 4)];
+      vpre[i] = vrow[krow(j < nc ? j : 0) * (HD / 4)];
     }
     if constexpr (FUSE) {
       __builtin_amdgcn_sched_barrier(0);
-      // the cache rows of the position are this block's to write (the
-      // attention of this layer reads them from `post` only)
-      dp.compute(a.post, post, const_cast<float*>(a.kc), const_cast<float*>(a.vc),
-                 ((int64_t)row * a.Hkv + hk) * a.maxSeq + qpos, jn >= 0, wid, lane);
+      // the new key and value stay in `post` until the end, where they are
+      // written to the cache rows of the position
+      dp.compute(a.post, post, wid, lane);
       __syncthreads();
       read_q(&post[0][4 * part]);
     }
+    // the R scores of the key whose row k holds (8-lane group sums), and
+    // their store for key j = jc + g when j < jend
+    auto dots = [&](const v4f* k, float* d) {
+#pragma unroll
+      for (int h = 0; h < R; h++) {
+        float x = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          x += k[i][0] * qv[h][4 * i] + k[i][1] * qv[h][4 * i + 1] + k[i][2] * qv[h][4 * i + 2] +
+               k[i][3] * qv[h][4 * i + 3];
+        d[h] = red8_sum(x);
+      }
+    };
+    auto store = [&](const float* d, int jc, int jend) {
+      const int j = jc + g;
+      if (part == 0 && j < jend)
+#pragma unroll
+        for (int h = 0; h < R; h++) sc[h][j] = d[h];
+    };
     for (int jb = j0; jb < j1; jb += 8 * KD) {
 #pragma unroll
       for (int t = 0; t < KD; t++) {
         const int jc = jb + 8 * t;  // wave-uniform
         if (jc < j1) {
-          if (FUSE && jc + g == jn)
-#pragma unroll
-            for (int i = 0; i < 4; i++) kr[t][i] = *reinterpret_cast<const v4f*>(&post[R][4 * (part + 8 * i)]);
           float d[R];
-#pragma unroll
-          for (int h = 0; h < R; h++) {
-            float x = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-              x += kr[t][i][0] * qv[h][4 * i] + kr[t][i][1] * qv[h][4 * i + 1] +
-                   kr[t][i][2] * qv[h][4 * i + 2] + kr[t][i][3] * qv[h][4 * i + 3];
-            d[h] = red8_sum(x);
-          }
+          dots(kr[t], d);
           if (jc + 8 * KD < j1) load(jc + 8 * KD + g, kr[t]);
-          const int j = jc + g;
-          if (part == 0 && j < j1)
-#pragma unroll
-            for (int h = 0; h < R; h++) sc[h][j] = d[h];
+          store(d, jc, j1);
         }
       }
+    }
+    // the position's own key: group 0 of the last wave (the same arithmetic
+    // as a cached key's)
+    if (FUSE && jn >= 0 && wid == NW - 1) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) kr[0][i] = *reinterpret_cast<const v4f*>(&post[R][4 * (part + 8 * i)]);
+      float d[R];
+      dots(kr[0], d);
+      store(d, jn, g == 0 ? jn + 1 : jn);
     }
   }
   __syncthreads();
@@ -439,9 +458,8 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   for (int h = 0; h < R; h++)
 #pragma unroll
     for (int c = 0; c < 4; c++) acc[h][c] = 0.f;
-  auto accumulate = [&](int j, const v4f& vin) {
-    v4f vv = vin;
-    if (FUSE && j == jn) vv = *reinterpret_cast<const v4f*>(&post[R + 1][4 * d4]);
+  // every thread adds its rows jr, jr + RS, ... in increasing order
+  auto accumulate = [&](int j, const v4f& vv) {
 #pragma unroll
     for (int h = 0; h < R; h++) {
       const float p = sc[h][j];
@@ -451,31 +469,34 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
   };
 #pragma unroll
   for (int i = 0; i < VP; i++)
-    if (jr + RS * i < nk) accumulate(jr + RS * i, vpre[i]);
-  if (RS * VP < nk) {  // block-uniform: the rest of a long split, two sets of 4 rows in flight
+    if (jr + RS * i < nc) accumulate(jr + RS * i, vpre[i]);
+  if (RS * VP < nc) {  // block-uniform: the rest of a long split, two sets of 4 rows in flight
     auto load4 = [&](int j, v4f* vv) {
 #pragma unroll
       for (int u = 0; u < 4; u++) {
         const int jj = j + RS * u;
-        vv[u] = vrow[krow(jj < nk ? jj : 0) * (HD / 4)];
+        vv[u] = vrow[krow(jj < nc ? jj : 0) * (HD / 4)];
       }
     };
     auto acc4 = [&](int j, const v4f* vv) {
 #pragma unroll
       for (int u = 0; u < 4; u++)
-        if (j + RS * u < nk) accumulate(j + RS * u, vv[u]);
+        if (j + RS * u < nc) accumulate(j + RS * u, vv[u]);
     };
     v4f va[4], vb[4];
     int jb = jr + RS * VP;
     load4(jb, va);
-    for (; jb < nk; jb += 8 * RS) {
-      if (jb + 4 * RS < nk) load4(jb + 4 * RS, vb);
+    for (; jb < nc; jb += 8 * RS) {
+      if (jb + 4 * RS < nc) load4(jb + 4 * RS, vb);
       acc4(jb, va);
-      if (jb + 4 * RS >= nk) break;
-      if (jb + 8 * RS < nk) load4(jb + 8 * RS, va);
+      if (jb + 4 * RS >= nc) break;
+      if (jb + 8 * RS < nc) load4(jb + 8 * RS, va);
       acc4(jb + 4 * RS, vb);
     }
   }
+  // the position's own value row, the last row of its thread
+  if (FUSE && jn >= 0 && jr == jn % RS)
+    accumulate(jn, *reinterpret_cast<const v4f*>(&post[R + 1][4 * d4]));
 #pragma unroll
   for (int h = 0; h < R; h++)
     *reinterpret_cast<v4f*>(&pv[jr][h][4 * d4]) = (v4f){acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
@@ -498,6 +519,15 @@ __device__ __forceinline__ void decode_attn_body(const DecodeAttnArgs& a) {
         out[h * (HD + 2) + HD] = mx[h];
         out[h * (HD + 2) + HD + 1] = l;
       }
+    }
+  }
+  // the cache rows of the position are this block's to write (this layer's
+  // attention took them from `post`)
+  if (FUSE && jn >= 0) {
+    const int64_t crow = ((int64_t)row * a.Hkv + hk) * a.maxSeq + qpos;
+    for (int i = tid; i < 2 * HD; i += NT) {
+      float* c = const_cast<float*>(i < HD ? a.kc : a.vc);
+      c[crow * HD + i % HD] = post[R + i / HD][i % HD];
     }
   }
 }
