@@ -552,8 +552,9 @@ void launch_expand_last_rows(const float* src, float* dst, int G, int T, int S, 
 // When the row fits in registers (V a multiple of 4, at most 1024 * 4 * Q
 // floats) one 1024-thread block holds it as Q float4 per thread: the logits
 // are read once and the gradient written once (the maximum, the float64
-// sum of exponentials and the gradient come from the registers).  Otherwise
-// the row is streamed three times (maximum, sum, gradient).
+// sum of exponentials and the gradient come from the registers); rows of
+// 32,768 entries or more take softcap15_fast / exp_softcapped below.
+// Otherwise the row is streamed three times (maximum, sum, gradient).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int64_t loss_row_index(const int32_t* rowmap, int64_t row0, int64_t r) {
   return rowmap ? (int64_t)rowmap[row0 + r] : row0 + r;
@@ -567,6 +568,40 @@ __device__ __forceinline__ int64_t loss_row_index(const int32_t* rowmap, int64_t
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
+// The register kernel's transcendentals, branch-free and cheaper than
+// tanhf / expf (which test ranges and, in tanhf's case, take two paths by
+// |x|: lanes of a wave that disagree run both).  The kernel is bound by
+// its arithmetic: with a 65,536 row in a whole CU's registers, the memory
+// idles while the block computes.
+//  * softcap15_fast: 15 tanh(y / 15) with tanh as an odd polynomial of
+//    degree 11 (relative minimax fit on [0, 0.55], 1.2 ulp in float32)
+//    below |x| = 0.55 and 1 - 2 / (e^(2|x|) + 1) above (hardware exp2 and
+//    reciprocal; no cancellation above 0.55): measured on the device
+//    within 4 ulp of 15 tanh(y / 15) over |y| <= 45, 2 ulp over |y| <= 8.
+//  * exp_softcapped(x) = e^x for x = z - max z of a softcapped row, so
+//    x in [-30, 0]: the hardware exp2 of x log2(e) with the product taken
+//    in two parts (x times the float nearest log2(e), plus x times the
+//    remainder), so the argument is off by its own rounding only and the
+//    error has no sign bias.  Measured on the device: 1.4 ulp over
+//    [-1, 0] (the terms that carry the sum), 23 ulp at worst near -29
+//    (terms below 1e-12 of the largest), mean relative error -3e-9 (expf:
+//    0.84 ulp, -2e-9).  With the constant alone the error was biased
+//    upward (+2e-7 mean relative over [-30, 0]).
+__device__ __forceinline__ float softcap15_fast(float y) {
+  const float x = y * (1.0f / 15.0f);
+  const float t = fabsf(x), u = t * t;
+  float p = fmaf(-0.006235599052160978f, u, 0.021039707586169243f);
+  p = fmaf(p, u, -0.05384271591901779f);
+  p = fmaf(p, u, 0.13332460820674896f);
+  p = fmaf(p, u, -0.3333331048488617f);
+  p = fmaf(p, u, 1.0f);
+  const float e = __builtin_amdgcn_exp2f(t * 2.8853900817779268f);  // e^(2t)
+  const float big = fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+  return copysignf(t < 0.55f ? t * p : big, x) * 15.0f;
+}
+__device__ __forceinline__ float exp_softcapped(float x) {
+  return __builtin_amdgcn_exp2f(fmaf(x, 1.4426950408889634f, x * 1.925963033500011e-08f));
+}
 template <int Q, bool FULL>
 __global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
     float* __restrict__ z, int64_t ldz, int V, int64_t row0, const int32_t* __restrict__ rowmap,
@@ -574,6 +609,12 @@ __global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
     float* __restrict__ nll, double* __restrict__ loss_rows) {
   __shared__ float sf[16];
   __shared__ double sd[16];
+  // rows of 32,768 entries or more take the branch-free softcap and
+  // exponential (the arithmetic bounds the kernel there); shorter rows keep
+  // tanhf / expf
+  constexpr bool FAST = Q >= 8;
+  auto sc = [](float y) { return FAST ? softcap15_fast(y) : softcap15(y); };
+  auto ex = [](float x) { return FAST ? exp_softcapped(x) : expf(x); };
   const int64_t r = blockIdx.x;
   const int64_t n = loss_row_index(rowmap, row0, r);
   float* zr = z + r * ldz;
@@ -594,13 +635,13 @@ __global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
     }
     return;
   }
-  const float zt = softcap15(zr[tg]);
+  const float zt = sc(zr[tg]);
   v4f v[Q];
 #pragma unroll
   for (int k = 0; k < Q; k++) {
     v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * 16384, 0);
 #pragma unroll
-    for (int c = 0; c < 4; c++) v[k][c] = softcap15(v[k][c]);
+    for (int c = 0; c < 4; c++) v[k][c] = sc(v[k][c]);
   }
   if (!FULL) {
 #pragma unroll
@@ -615,8 +656,8 @@ __global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
 #pragma unroll
   for (int k = 0; k < Q; k++) {
     if (FULL || tid + k * 1024 < V4)
-      s += ((double)expf(v[k][0] - m) + (double)expf(v[k][1] - m)) +
-           ((double)expf(v[k][2] - m) + (double)expf(v[k][3] - m));
+      s += ((double)ex(v[k][0] - m) + (double)ex(v[k][1] - m)) +
+           ((double)ex(v[k][2] - m) + (double)ex(v[k][3] - m));
   }
   s = block_sum<double>(s, sd);
   const float a = adv[n / T];
@@ -640,7 +681,7 @@ __global__ __launch_bounds__(1024) void pg_loss_rows_reg_kernel(
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       const float zj = v[k][c];
-      float p = expf(zj - mg) * inv;
+      float p = ex(zj - mg) * inv;
       if (4 * j + c == tg) p -= 1.f;
       const float sc = zj * ic;
       g[c] = (p * scale) * (1.f - sc * sc);
