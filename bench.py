@@ -127,6 +127,9 @@ def main() -> int:
     ap.add_argument("--no-optimizer", action="store_true",
                     help="skip the (untimed by the metric) optimizer-step timing, e.g. in "
                          "kernel-trace profiles of the RL step")
+    ap.add_argument("--rw-rate", action="store_true",
+                    help="run only the rates of a 1 GiB device copy and of an in-place "
+                         "rewrite of a [4096, 65536] tensor (the logits' read + write pattern)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a device copy of 1 GiB (5 times), the known-size "
                          "reference for HBM byte counters")
@@ -139,6 +142,8 @@ def main() -> int:
 
     if args.copy_calibration:
         return copy_calibration()
+    if args.rw_rate:
+        return rw_rate()
 
     from gonano_amd import config as G
     from gonano_amd.session import Session
@@ -179,7 +184,8 @@ def main() -> int:
         log(f"bench: warmup {i}: {wall * 1e3:.1f} ms (rollout {t['rollout_ms']:.1f} ms, "
             f"train {t['train_ms']:.1f} ms), loss {out['loss']:.6f}")
     walls, roll_ms, train_ms, toks = [], [], [], 0
-    gemm = {"ms": 0.0, "flops": 0.0, "n": 0, "wide_ms": 0.0, "wide_flops": 0.0, "wide_n": 0}
+    gemm = {"ms": 0.0, "flops": 0.0, "n": 0, "wide_ms": 0.0, "wide_flops": 0.0, "wide_n": 0,
+            "loss_ms": 0.0, "loss_bytes": 0.0, "loss_n": 0}
     sess.synchronize()
     t_start = time.perf_counter()
     for i in range(args.steps):
@@ -247,6 +253,7 @@ def main() -> int:
             "train_ms": round(sum(train_ms) / len(train_ms), 2),
         },
         "roofline": gemm_roofline(gemm, args.config),
+        "pg_loss": pg_loss_roofline(gemm),
         "decode_attention": {
             "bound": "hbm", "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "launches": attn_n,
@@ -268,10 +275,12 @@ def main() -> int:
 
 def add_gemm(acc: dict, t: dict) -> None:
     """Adds one step's train-phase GEMM timing (all products; those on the
-    wide-tile engine) to acc."""
+    wide-tile engine) and policy-gradient loss timing to acc."""
     acc["ms"] += t["gemm_ms"]; acc["flops"] += t["gemm_flops"]; acc["n"] += t["gemm_launches"]
     acc["wide_ms"] += t["gemm_wide_ms"]; acc["wide_flops"] += t["gemm_wide_flops"]
     acc["wide_n"] += t["gemm_wide_launches"]
+    acc["loss_ms"] += t["loss_ms"]; acc["loss_bytes"] += t["loss_bytes"]
+    acc["loss_n"] += t["loss_launches"]
 
 
 def _part(ms: float, flops: float, n: int) -> dict:
@@ -301,6 +310,19 @@ def gemm_roofline(g: dict, config: str) -> dict:
         "avg_launch_ms": round(g["ms"] / max(g["n"], 1), 4),
         "parts": {"gemm_wide_kernel": wide, "gemm_kernel": own},
     }
+
+
+def pg_loss_roofline(g: dict) -> dict:
+    """The policy-gradient loss rows (pg_loss_rows_reg_kernel: softcap, log-
+    softmax, NLL and the logits gradient written over the logits), timed
+    per launch with HIP events; algorithmic bytes = the logits chunk read
+    once and its gradient written once.  (`bench.py --rw-rate` times a
+    plain in-place rewrite of a [4096, 65536] tensor, the same read + write
+    pattern with no arithmetic.)"""
+    gbs = g["loss_bytes"] / (g["loss_ms"] / 1e3) / 1e9 if g["loss_ms"] else 0.0
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": g["loss_n"],
+            "avg_launch_ms": round(g["loss_ms"] / max(g["loss_n"], 1), 4)}
 
 
 def gemm_traffic(config: str):
@@ -366,7 +388,8 @@ def train_phase(args, sess, prompts, S, N, reward_rng, reward_p) -> int:
         sess.policy_gradient_step(inputs, targets, adv, norm)
     sess.synchronize()
     t0 = time.perf_counter()
-    gemm = {"ms": 0.0, "flops": 0.0, "n": 0, "wide_ms": 0.0, "wide_flops": 0.0, "wide_n": 0}
+    gemm = {"ms": 0.0, "flops": 0.0, "n": 0, "wide_ms": 0.0, "wide_flops": 0.0, "wide_n": 0,
+            "loss_ms": 0.0, "loss_bytes": 0.0, "loss_n": 0}
     train = []
     for _ in range(args.steps):
         sess.zero_grad()
@@ -485,6 +508,36 @@ def copy_calibration() -> int:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": 4 * n, "copies": 5}), flush=True)
+    return 0
+
+
+def rw_rate() -> int:
+    """Rates of a 1 GiB device copy and of an in-place rewrite of a
+    [4096, 65536] float32 tensor (torch's elementwise multiply: each float
+    read once and written once, the pattern of a kernel that rewrites the
+    logits it reads), timed with events after two untimed passes."""
+    import torch
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+
+    def rate(fn) -> float:
+        for _ in range(2):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(5):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return round(2 * 4 * n / (a.elapsed_time(b) / 5 / 1e3) / 1e9, 1)
+
+    copy_gbs = rate(lambda: dst.copy_(src))
+    x = src.view(4096, 65536)
+    inplace_gbs = rate(lambda: x.mul_(1.0))
+    print(json.dumps({"copy_gbs": copy_gbs, "copy_frac": round(copy_gbs / HBM_PEAK_GBS, 4),
+                      "inplace_rw_gbs": inplace_gbs,
+                      "inplace_rw_frac": round(inplace_gbs / HBM_PEAK_GBS, 4)}), flush=True)
     return 0
 
 

@@ -62,6 +62,9 @@ class GnTiming(C.Structure):
         ("gemm_wide_ms", C.c_double),
         ("gemm_wide_flops", C.c_double),
         ("gemm_wide_launches", C.c_int64),
+        ("loss_ms", C.c_double),
+        ("loss_bytes", C.c_double),
+        ("loss_launches", C.c_int64),
     ]
 
 

@@ -146,8 +146,8 @@ struct gn_session {
   // timing
   bool timing = false;
   gn_timing t{};
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> gemm_events, attn_events;
-  std::vector<double> gemm_ev_flops, attn_ev_bytes;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> gemm_events, attn_events, loss_events;
+  std::vector<double> gemm_ev_flops, attn_ev_bytes, loss_ev_bytes;
   std::vector<char> gemm_ev_wide;  // the product ran on the wide-tile engine
   std::vector<int> attn_ev_launches;
   std::vector<hipEvent_t> event_pool;
@@ -1483,6 +1483,8 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
   for (int64_t i = 0; i < N; i++)
     GN_CHECK(targets[i] == -1 || (targets[i] >= 0 && targets[i] < V), "target id out of range");
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  s->loss_events.clear();
+  s->loss_ev_bytes.clear();
   if (s->timing) {
     ev0 = next_event(s);
     ev1 = next_event(s);
@@ -1574,7 +1576,16 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
       sgemm(s, linear_fwd_desc(tfnv + r0 * Ct, dc->teacher->lm, Zt, (int)rows, Ct, V));
       launch_distill_rows(Z, Zt, V, V, r0, rows, rowmap, dtg, dc->tau, dc->scale, loss_rows, st);
     } else {
+      if (s->timing && !s->capturing) {
+      hipEvent_t a = next_event(s), b = next_event(s);
+      GN_HIP(hipEventRecord(a, st));
       launch_pg_loss_rows(Z, V, V, r0, rows, rowmap, dtg, dadv, T, norm, nll, loss_rows, st);
+      GN_HIP(hipEventRecord(b, st));
+      s->loss_events.push_back({a, b});
+      s->loss_ev_bytes.push_back(2.0 * 4.0 * (double)rows * V);
+    } else {
+      launch_pg_loss_rows(Z, V, V, r0, rows, rowmap, dtg, dadv, T, norm, nll, loss_rows, st);
+    }
     }
     sgemm(s, linear_dx_desc(Z, s->lm, dfnv + r0 * C, (int)rows, C, V));
     sgemm(s, linear_dw_desc(Z, fnv + r0 * C, s->glm, (int)rows, C, V));
@@ -1716,7 +1727,17 @@ static void pg_step_chunk(gn_session* s, const int32_t* inputs, const int32_t* t
     int64_t an = 0;
     collect_timing(s, &s->t.gemm_ms, &s->t.gemm_flops, &s->t.gemm_launches, &am, &ab, &an,
                    &s->t.gemm_wide_ms, &s->t.gemm_wide_flops, &s->t.gemm_wide_launches);
+    s->t.loss_ms = 0; s->t.loss_bytes = 0; s->t.loss_launches = 0;
+    for (size_t i = 0; i < s->loss_events.size(); i++) {
+      float lms = 0;
+      GN_HIP(hipEventElapsedTime(&lms, s->loss_events[i].first, s->loss_events[i].second));
+      s->t.loss_ms += lms;
+      s->t.loss_bytes += s->loss_ev_bytes[i];
+      s->t.loss_launches++;
+    }
   }
+  s->loss_events.clear();
+  s->loss_ev_bytes.clear();
 }
 
 // Sequences per micro-batch of the policy-gradient step: the saved
@@ -1743,8 +1764,8 @@ static int pg_micro_batch(gn_session* s, int B, int T) {
 static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets, int B, int T,
                     const float* adv, float norm, float* loss_out, float* nll_out) {
   const int mb = pg_micro_batch(s, B, T);
-  double loss = 0, aux = 0, tms = 0, gms = 0, gfl = 0, wms = 0, wfl = 0;
-  int64_t gn = 0, wn = 0;
+  double loss = 0, aux = 0, tms = 0, gms = 0, gfl = 0, wms = 0, wfl = 0, lms = 0, lby = 0;
+  int64_t gn = 0, wn = 0, ln = 0;
   s->bal_batch = B;
   try {
     for (int b0 = 0; b0 < B; b0 += mb) {
@@ -1756,6 +1777,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
       aux += s->aux_loss * nb;
       tms += s->t.train_ms; gms += s->t.gemm_ms; gfl += s->t.gemm_flops; gn += s->t.gemm_launches;
       wms += s->t.gemm_wide_ms; wfl += s->t.gemm_wide_flops; wn += s->t.gemm_wide_launches;
+      lms += s->t.loss_ms; lby += s->t.loss_bytes; ln += s->t.loss_launches;
     }
   } catch (...) {
     s->bal_batch = 0;
@@ -1767,6 +1789,7 @@ static void pg_step(gn_session* s, const int32_t* inputs, const int32_t* targets
   if (s->timing) {
     s->t.train_ms = tms; s->t.gemm_ms = gms; s->t.gemm_flops = gfl; s->t.gemm_launches = gn;
     s->t.gemm_wide_ms = wms; s->t.gemm_wide_flops = wfl; s->t.gemm_wide_launches = wn;
+    s->t.loss_ms = lms; s->t.loss_bytes = lby; s->t.loss_launches = ln;
   }
 }
 
@@ -3361,6 +3384,7 @@ int gn_session_set_timing(gn_session* s, int enabled) {
     s->timing = enabled != 0;
     s->gemm_events.clear(); s->gemm_ev_flops.clear(); s->gemm_ev_wide.clear();
     s->attn_events.clear(); s->attn_ev_bytes.clear(); s->attn_ev_launches.clear();
+    s->loss_events.clear(); s->loss_ev_bytes.clear();
     s->event_next = 0;
   });
 }

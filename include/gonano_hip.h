@@ -410,6 +410,9 @@ typedef struct gn_timing {
   double gemm_wide_ms;      /* the part of them run by the wide-tile engine (256x256 tiles) */
   double gemm_wide_flops;
   int64_t gemm_wide_launches;
+  double loss_ms;           /* policy-gradient loss launches inside the train step */
+  double loss_bytes;        /* algorithmic bytes of those launches: logits read + gradient written */
+  int64_t loss_launches;
 } gn_timing;
 int gn_session_set_timing(gn_session *session, int enabled);
 int gn_session_get_timing(const gn_session *session, gn_timing *out);
