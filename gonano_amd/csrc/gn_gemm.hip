@@ -39,6 +39,9 @@ struct GemmParams {
   int groups;
   int64_t gstride;
   int a_pad;  // rows mode: A is readable for at least 128 rows past its last row
+  // batched products (grid y): product y reads A + y*bsa, B + y*bsb and
+  // writes C + y*bsc, its split partials [splits][M][N] at part + y*splits*M*N
+  int64_t bsa, bsb, bsc;
 };
 
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, int row, int col, float v) {
@@ -309,6 +312,13 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
   int tm, tn, split;
   tile_coords(p0, tm, tn, split);
   GemmParams p = p0;
+  if constexpr (GRP == GEMM_GROUP_NONE) {
+    const int64_t y = blockIdx.y;  // batched products
+    p.A += y * p.bsa;
+    p.B += y * p.bsb;
+    p.C += y * p.bsc;
+    if (p.part) p.part += y * (int64_t)p.splits * p.M * p.N;
+  }
   int m0 = tm * BM, kbeg, kend;
   const int n0 = tn * BN;
   if constexpr (GRP == GEMM_GROUP_ROWS) {
@@ -504,6 +514,8 @@ __global__ void gemm_reduce_kernel(GemmParams p) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)p.M * p.N;
   if (idx >= total) return;
+  p.C += (int64_t)blockIdx.y * p.bsc;  // batched products
+  p.part += (int64_t)blockIdx.y * p.splits * total;
   double s = 0.0;
   for (int z = 0; z < p.splits; z++) s += (double)p.part[(int64_t)z * total + idx];
   gemm_epilogue(p, (int)(idx / p.N), (int)(idx % p.N), (float)s);
@@ -511,12 +523,12 @@ __global__ void gemm_reduce_kernel(GemmParams p) {
 
 template <int BM, int BN, int WM, int WN, int WK, int S, bool FOLD>
 static void launch_cfg(const GemmParams& p, bool ak, bool bk, bool vec, int splits,
-                       hipStream_t st) {
+                       hipStream_t st, int batch = 1) {
   GemmParams q = p;
   q.tiles_m = (int)ceil_div(p.M, BM);
   q.tiles_n = (int)ceil_div(p.N, BN);
   q.splits = splits;
-  dim3 grid(q.tiles_m * q.tiles_n * splits);
+  dim3 grid(q.tiles_m * q.tiles_n * splits, batch);
   dim3 block(64 * WM * WN * WK);
 #define GN_GEMM_LAUNCH(AK, BK, V)                                                             \
   hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, WK, S, FOLD, AK, BK, V, GEMM_GROUP_NONE>), \
@@ -1463,6 +1475,51 @@ GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
       // K mode: a group's whole row range per workgroup, two-level summation
       launch_grouped<128, 128, 2, 2, 1, 2, true, GEMM_GROUP_K>(p, d.a_kcontig, d.b_kcontig, vec,
                                                                st);
+    }
+    return GEMM_ENGINE_TILE;
+  }
+  if (d.batch > 1) {
+    // batched products of one shape (the compressed attention's per-sequence
+    // products): one launch, the batch on grid y; 128 x 128 tiles unless a
+    // side is at most 64 (then 64 x 64: no half-empty tiles); K split only
+    // while the batch leaves the CUs short of two workgroups each
+    GN_CHECK(d.group == GEMM_GROUP_NONE && !d.defer && (d.epi == EPI_STORE || d.epi == EPI_ACCUM),
+             "gemm: batched products store or accumulate");
+    p.bsa = d.batch_sa;
+    p.bsb = d.batch_sb;
+    p.bsc = d.batch_sc;
+    const int64_t cus = 256;
+    const bool big = d.M > 64 && d.N > 64;
+    const int bm = big ? 128 : 64, bn = big ? 128 : 64;
+    const int64_t tiles = ceil_div(d.M, bm) * ceil_div(d.N, bn) * d.batch;
+    int splits = 1;
+    if (tiles < 2 * cus && d.K >= 2048)
+      splits = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(2 * cus, tiles), d.K / 1024));
+    splits = std::min(splits, 64);
+    if (const char* e = std::getenv("GN_GEMM_BATCH_SPLITS"))  // tests: force the split path
+      splits = std::max(1, std::min(std::atoi(e), 64));
+    const int kps = d.K > 0 ? (int)ceil_div(ceil_div(d.K, splits), GK) * GK : 0;
+    splits = d.K > 0 ? (int)ceil_div(d.K, kps) : 1;
+    p.k_per_split = kps;
+    p.splits = splits;
+    if (splits > 1) {
+      GN_CHECK(ws != nullptr, "gemm: split-K needs a workspace");
+      p.part = ws->get<float>("gemm_splitk", (size_t)splits * d.M * d.N * d.batch);
+    }
+    const bool fold = kps >= 4096;
+    if (big && fold)
+      launch_cfg<128, 128, 2, 2, 1, 2, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st, d.batch);
+    else if (big)
+      launch_cfg<128, 128, 2, 2, 1, 2, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st, d.batch);
+    else if (fold)
+      launch_cfg<64, 64, 2, 2, 2, 4, true>(p, d.a_kcontig, d.b_kcontig, vec, splits, st, d.batch);
+    else
+      launch_cfg<64, 64, 2, 2, 2, 4, false>(p, d.a_kcontig, d.b_kcontig, vec, splits, st, d.batch);
+    if (splits > 1) {
+      const int64_t total = (int64_t)d.M * d.N;
+      hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256), (unsigned)d.batch),
+                         dim3(256), 0, st, p);
+      GN_HIP(hipGetLastError());
     }
     return GEMM_ENGINE_TILE;
   }

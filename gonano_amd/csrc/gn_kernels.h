@@ -132,6 +132,10 @@ struct GemmDesc {
   // partial buffer of a deferred sum: products whose sums are pending at the
   // same time use different slots
   int defer_slot = 0;
+  // batch products of one shape (gemm_kernel only; EPI_STORE or EPI_ACCUM):
+  // product i takes A + i*batch_sa, B + i*batch_sb, C + i*batch_sc
+  int batch = 1;
+  int64_t batch_sa = 0, batch_sb = 0, batch_sc = 0;
 };
 
 // Which kernel ran a product: gemm_kernel (tiles up to 128 x 128, fused

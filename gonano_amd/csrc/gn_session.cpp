@@ -219,7 +219,7 @@ static void sgemm(gn_session* s, const GemmDesc& d) {
     const GemmEngine e = gemm(d, s->stream, s->arena.get());
     GN_HIP(hipEventRecord(b, s->stream));
     s->gemm_events.push_back({a, b});
-    s->gemm_ev_flops.push_back(2.0 * d.M * (double)d.N * d.K);
+    s->gemm_ev_flops.push_back(2.0 * d.M * (double)d.N * d.K * d.batch);
     s->gemm_ev_wide.push_back(e == GEMM_ENGINE_WIDE ? 1 : 0);
   } else {
     gemm(d, s->stream, s->arena.get());
@@ -1345,25 +1345,31 @@ static float* csa_distill_backward(gn_session* s, SeqBuffers& sb, const Layer& l
     launch_indexer_scores(ma, nb, st);
     const int64_t nbk = indexer_mask_blocks(sh, nb);
     for (int h = 0; h < H; h++) launch_sum_partials(gwb + (int64_t)h * nbk, nbk, ly.gih + h, st);
-    for (int bl = 0; bl < nb; bl++)
-      for (int hh = 0; hh < Hkv; hh++)
-        for (int h = 0; h < H; h++) {
-          const int b = b0 + bl, z = bl * Hkv + hh;
-          const float* mh = masks + (int64_t)h * per + (int64_t)z * T * sh.ldo;
-          GemmDesc dq;  // gq[b, t, h] += mask . ik
-          dq.M = T; dq.N = dim; dq.K = blocks;
-          dq.A = mh; dq.lda = sh.ldo;
-          dq.B = sb.ik[l] + ((int64_t)b * blocks * Hkv + hh) * HI + h * dim;
-          dq.ldb = (int64_t)Hkv * HI; dq.b_kcontig = false;
-          dq.C = gq + (int64_t)b * T * HI + h * dim; dq.ldc = HI; dq.epi = EPI_ACCUM;
-          sgemm(s, dq);
-          GemmDesc dk;  // gk[b, s, hh, h] = mask^T . iq
-          dk.M = blocks; dk.N = dim; dk.K = T;
-          dk.A = mh; dk.lda = sh.ldo; dk.a_kcontig = false;
-          dk.B = sb.iq[l] + (int64_t)b * T * HI + h * dim; dk.ldb = HI; dk.b_kcontig = false;
-          dk.C = gk + ((int64_t)b * blocks * Hkv + hh) * HI + h * dim; dk.ldc = (int64_t)Hkv * HI;
-          sgemm(s, dk);
-        }
+    // per sequence (batched over the chunk's nb sequences), KV head and
+    // indexer head
+    for (int hh = 0; hh < Hkv; hh++)
+      for (int h = 0; h < H; h++) {
+        const int b = b0;
+        const float* mh = masks + (int64_t)h * per + (int64_t)hh * T * sh.ldo;
+        const int64_t mstride = (int64_t)Hkv * T * sh.ldo;  // sequence to sequence
+        GemmDesc dq;  // gq[b, t, h] += mask . ik
+        dq.M = T; dq.N = dim; dq.K = blocks;
+        dq.A = mh; dq.lda = sh.ldo;
+        dq.B = sb.ik[l] + ((int64_t)b * blocks * Hkv + hh) * HI + h * dim;
+        dq.ldb = (int64_t)Hkv * HI; dq.b_kcontig = false;
+        dq.C = gq + (int64_t)b * T * HI + h * dim; dq.ldc = HI; dq.epi = EPI_ACCUM;
+        dq.batch = nb;
+        dq.batch_sa = mstride; dq.batch_sb = (int64_t)blocks * Hkv * HI; dq.batch_sc = (int64_t)T * HI;
+        sgemm(s, dq);
+        GemmDesc dk;  // gk[b, s, hh, h] = mask^T . iq
+        dk.M = blocks; dk.N = dim; dk.K = T;
+        dk.A = mh; dk.lda = sh.ldo; dk.a_kcontig = false;
+        dk.B = sb.iq[l] + (int64_t)b * T * HI + h * dim; dk.ldb = HI; dk.b_kcontig = false;
+        dk.C = gk + ((int64_t)b * blocks * Hkv + hh) * HI + h * dim; dk.ldc = (int64_t)Hkv * HI;
+        dk.batch = nb;
+        dk.batch_sa = mstride; dk.batch_sb = (int64_t)T * HI; dk.batch_sc = (int64_t)blocks * Hkv * HI;
+        sgemm(s, dk);
+      }
   }
   sgemm(s, linear_dw_desc(gq, sb.h[l], ly.giq, (int)N, s->C, HI));
   sgemm(s, linear_dw_desc(gk, kc, ly.gik, B * blocks * Hkv, HD, HI));

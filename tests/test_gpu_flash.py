@@ -73,7 +73,13 @@ def test_flash_forward_matches_oracle(flash, orc, T):
     assert_close(got, want, 1e-3, 1e-4, "logits")
 
 
-def test_flash_policy_gradient_step_matches_oracle(flash, orc):
+@pytest.mark.parametrize("batch_splits", [None, "2"])
+def test_flash_policy_gradient_step_matches_oracle(flash, orc, monkeypatch, batch_splits):
+    """batch_splits "2": the indexer gradient's per-sequence products, one
+    batched launch per head, split K in two (GN_GEMM_BATCH_SPLITS) and sum
+    the partials of every sequence in one reduction launch."""
+    if batch_splits:
+        monkeypatch.setenv("GN_GEMM_BATCH_SPLITS", batch_splits)
     cfg, w, s = flash
     rng = np.random.default_rng(2)
     B, T = 3, 162
