@@ -1322,17 +1322,20 @@ static float* csa_distill_backward(gn_session* s, SeqBuffers& sb, const Layer& l
     IndexerScoreArgs ia{};
     ia.shape = sh; ia.iq = sb.iq[l]; ia.ik = sb.ik[l]; ia.w = ly.wih; ia.out = scores;
     launch_indexer_scores(ia, nb, st);
-    for (int bl = 0; bl < nb; bl++)
-      for (int hh = 0; hh < Hkv; hh++) {  // mean main-attention logits
-        const int b = b0 + bl, z = bl * Hkv + hh;
-        GemmDesc d;
-        d.M = T; d.N = blocks; d.K = HD;
-        d.A = qsum + ((int64_t)b * T * Hkv + hh) * HD; d.lda = (int64_t)Hkv * HD;
-        d.B = kc + ((int64_t)b * blocks * Hkv + hh) * HD; d.ldb = (int64_t)Hkv * HD;
-        d.C = tlog + (int64_t)z * T * sh.ldo; d.ldc = sh.ldo;
-        d.alpha = 1.f / (float)rr;
-        sgemm(s, d);
-      }
+    for (int hh = 0; hh < Hkv; hh++) {  // mean main-attention logits, batched over sequences
+      const int b = b0;
+      GemmDesc d;
+      d.M = T; d.N = blocks; d.K = HD;
+      d.A = qsum + ((int64_t)b * T * Hkv + hh) * HD; d.lda = (int64_t)Hkv * HD;
+      d.B = kc + ((int64_t)b * blocks * Hkv + hh) * HD; d.ldb = (int64_t)Hkv * HD;
+      d.C = tlog + (int64_t)hh * T * sh.ldo; d.ldc = sh.ldo;
+      d.alpha = 1.f / (float)rr;
+      d.batch = nb;
+      d.batch_sa = (int64_t)T * Hkv * HD;
+      d.batch_sb = (int64_t)blocks * Hkv * HD;
+      d.batch_sc = (int64_t)Hkv * T * sh.ldo;
+      sgemm(s, d);
+    }
     CsaDistillArgs da{};
     da.shape = sh; da.scores = scores; da.tlog = tlog;
     da.pool_in = within ? sb.pool[p] : nullptr;
