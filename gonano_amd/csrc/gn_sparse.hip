@@ -11,9 +11,9 @@
 // scores.
 //
 // Kernels:
-//  * indexer_scores: one 16x16 (t, s) tile per block from LDS copies of the
-//    query and key projections; tiles past every row's causal limit are
-//    skipped (their entries are never read).
+//  * indexer_scores: one 32x32 (t, s) tile per block (2x2 entries per
+//    thread) from LDS copies of the query and key projections; tiles past
+//    every row's causal limit are skipped (their entries are never read).
 //  * csa_select: one wave per row.  Group maxima live in LDS; the chosen
 //    groups and the final top-K come from repeated wave-wide argmax
 //    reductions over (value desc, index asc).
@@ -46,53 +46,99 @@ static constexpr int IHMAX = 8;  // indexer heads
 // gradient masks mask_out[h][z][t][s] = gs * w_h * [q_h . k_h > 0] (zero past
 // allowed(t)), and this block's partial of each head weight's gradient
 // sum gs * dot * [dot > 0] into gw_blocks[h * nblocks + block].
+// A block covers a (SR*16) x (SR*16) tile of (t, s); thread (tx, ty) takes
+// the SR x SR entries t0 + ty + 16 i, s0 + tx + 16 j, so each LDS value it
+// reads feeds SR dot products (one entry per thread read two values per
+// multiply-add).  Every entry's dot products run over e in order, as before.
+static constexpr int SR = 2;
+static constexpr int STT = ST * SR;
 __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerScoreArgs a) {
-  __shared__ float qs[ST][HIMAX + 1];
-  __shared__ float ks[ST][HIMAX + 1];
+  __shared__ float qs[STT][HIMAX + 1];
+  __shared__ float ks[STT][HIMAX + 1];
   __shared__ float red[4];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const CsaShape& sh = a.shape;
   const int HI = sh.H * sh.dim;
-  const int s0 = blockIdx.x * ST, t0 = blockIdx.y * ST, z = blockIdx.z;
+  const int s0 = blockIdx.x * STT, t0 = blockIdx.y * STT, z = blockIdx.z;
   const int b = sh.b0 + z / sh.Hkv, hh = z % sh.Hkv;
-  const int tl = min(sh.T, t0 + ST) - 1;
+  const int tl = min(sh.T, t0 + STT) - 1;
   const bool live = s0 < allowed_blocks(tl, sh);
   const bool bwd = a.mask_out != nullptr;
   const int64_t blk = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
   const int64_t nblk = (int64_t)gridDim.x * gridDim.y * gridDim.z;
-  const int t = t0 + ty, s = s0 + tx;
-  const bool in = t < sh.T && s < sh.ldo;
+  auto entry = [&](int i, int j, int& t, int& s) {
+    t = t0 + ty + ST * i;
+    s = s0 + tx + ST * j;
+    return t < sh.T && s < sh.ldo;
+  };
   if (!live) {  // past every row's causal limit: scores unread, masks zero
     if (bwd) {
-      if (in)
-        for (int h = 0; h < sh.H; h++)
-          a.mask_out[(int64_t)h * a.mask_stride + ((int64_t)z * sh.T + t) * sh.ldo + s] = 0.f;
+      for (int i = 0; i < SR; i++)
+        for (int j = 0; j < SR; j++) {
+          int t, s;
+          if (entry(i, j, t, s))
+            for (int h = 0; h < sh.H; h++)
+              a.mask_out[(int64_t)h * a.mask_stride + ((int64_t)z * sh.T + t) * sh.ldo + s] = 0.f;
+        }
       if (tid < sh.H) a.gw_blocks[(int64_t)tid * nblk + blk] = 0.f;
     }
     return;
   }
-  for (int i = tid; i < ST * HI; i += 256) {
+  for (int i = tid; i < STT * HI; i += 256) {
     const int r = i / HI, c = i % HI;
     const int tt = t0 + r, ss = s0 + r;
     qs[r][c] = tt < sh.T ? a.iq[((int64_t)b * sh.T + tt) * HI + c] : 0.f;
     ks[r][c] = ss < sh.blocks ? a.ik[(((int64_t)b * sh.blocks + ss) * sh.Hkv + hh) * HI + c] : 0.f;
   }
   __syncthreads();
-  const bool ok = in && s < allowed_blocks(t, sh);
-  const float g = (bwd && ok) ? a.gs[((int64_t)z * sh.T + t) * sh.ldo + s] : 0.f;
-  float total = 0.f;
+  bool ok[SR][SR], in[SR][SR];
+  float g[SR][SR], total[SR][SR];
+#pragma unroll
+  for (int i = 0; i < SR; i++)
+#pragma unroll
+    for (int j = 0; j < SR; j++) {
+      int t, s;
+      in[i][j] = entry(i, j, t, s);
+      ok[i][j] = in[i][j] && s < allowed_blocks(t, sh);
+      g[i][j] = (bwd && ok[i][j]) ? a.gs[((int64_t)z * sh.T + t) * sh.ldo + s] : 0.f;
+      total[i][j] = 0.f;
+    }
   float wpart[IHMAX];
   for (int h = 0; h < sh.H; h++) {
-    float dot = 0.f;
-    for (int e = 0; e < sh.dim; e++) dot += qs[ty][h * sh.dim + e] * ks[tx][h * sh.dim + e];
-    const bool pos = ok && dot > 0.f;
-    if (bwd) {
-      if (in) a.mask_out[(int64_t)h * a.mask_stride + ((int64_t)z * sh.T + t) * sh.ldo + s] =
-          pos ? g * a.w[h] : 0.f;
-      wpart[h] = pos ? g * dot : 0.f;
-    } else if (pos) {
-      total += a.w[h] * dot;
+    float dot[SR][SR];
+#pragma unroll
+    for (int i = 0; i < SR; i++)
+#pragma unroll
+      for (int j = 0; j < SR; j++) dot[i][j] = 0.f;
+    for (int e = 0; e < sh.dim; e++) {
+      float qv[SR], kv[SR];
+#pragma unroll
+      for (int i = 0; i < SR; i++) qv[i] = qs[ty + ST * i][h * sh.dim + e];
+#pragma unroll
+      for (int j = 0; j < SR; j++) kv[j] = ks[tx + ST * j][h * sh.dim + e];
+#pragma unroll
+      for (int i = 0; i < SR; i++)
+#pragma unroll
+        for (int j = 0; j < SR; j++) dot[i][j] += qv[i] * kv[j];
     }
+    float wp = 0.f;
+#pragma unroll
+    for (int i = 0; i < SR; i++)
+#pragma unroll
+      for (int j = 0; j < SR; j++) {
+        const bool pos = ok[i][j] && dot[i][j] > 0.f;
+        if (bwd) {
+          if (in[i][j]) {
+            const int t = t0 + ty + ST * i, s = s0 + tx + ST * j;
+            a.mask_out[(int64_t)h * a.mask_stride + ((int64_t)z * sh.T + t) * sh.ldo + s] =
+                pos ? g[i][j] * a.w[h] : 0.f;
+          }
+          wp += pos ? g[i][j] * dot[i][j] : 0.f;
+        } else if (pos) {
+          total[i][j] += a.w[h] * dot[i][j];
+        }
+      }
+    if (bwd) wpart[h] = wp;
   }
   if (bwd) {
     for (int h = 0; h < sh.H; h++) {
@@ -101,7 +147,14 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerScoreArgs a)
     }
     return;
   }
-  if (ok) a.out[((int64_t)z * sh.T + t) * sh.ldo + s] = total;
+#pragma unroll
+  for (int i = 0; i < SR; i++)
+#pragma unroll
+    for (int j = 0; j < SR; j++)
+      if (ok[i][j]) {
+        const int t = t0 + ty + ST * i, s = s0 + tx + ST * j;
+        a.out[((int64_t)z * sh.T + t) * sh.ldo + s] = total[i][j];
+      }
 }
 
 // Decode scores (one query per row, T == 1): the row's keys are streamed
@@ -169,13 +222,13 @@ void launch_indexer_scores(const IndexerScoreArgs& a, int chunk_seqs, hipStream_
     GN_HIP(hipGetLastError());
     return;
   }
-  dim3 grid((unsigned)ceil_div(s.ldo, ST), (unsigned)ceil_div(s.T, ST), (unsigned)(chunk_seqs * s.Hkv));
+  dim3 grid((unsigned)ceil_div(s.ldo, STT), (unsigned)ceil_div(s.T, STT), (unsigned)(chunk_seqs * s.Hkv));
   hipLaunchKernelGGL(indexer_scores_kernel, grid, dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }
 
 int64_t indexer_mask_blocks(const CsaShape& s, int chunk_seqs) {
-  return ceil_div(s.ldo, ST) * ceil_div(s.T, ST) * (int64_t)chunk_seqs * s.Hkv;
+  return ceil_div(s.ldo, STT) * ceil_div(s.T, STT) * (int64_t)chunk_seqs * s.Hkv;
 }
 
 // ---------------------------------------------------------------------------
