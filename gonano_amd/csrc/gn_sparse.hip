@@ -11,7 +11,7 @@
 // scores.
 //
 // Kernels:
-//  * indexer_scores: one 32x32 (t, s) tile per block (2x2 entries per
+//  * indexer_scores: one 64x64 (t, s) tile per block (4x4 entries per
 //    thread) from LDS copies of the query and key projections; tiles past
 //    every row's causal limit are skipped (their entries are never read).
 //  * csa_select: one wave per row.  Group maxima live in LDS; the chosen
@@ -50,15 +50,19 @@ static constexpr int IHMAX = 8;  // indexer heads
 // the SR x SR entries t0 + ty + 16 i, s0 + tx + 16 j, so each LDS value it
 // reads feeds SR dot products (one entry per thread read two values per
 // multiply-add).  Every entry's dot products run over e in order, as before.
-static constexpr int SR = 2;
+static constexpr int SR = 4;
 static constexpr int STT = ST * SR;
+// dynamic LDS: the query and key rows of the tile, STT x (H dim + 1) floats each
 __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerScoreArgs a) {
-  __shared__ float qs[STT][HIMAX + 1];
-  __shared__ float ks[STT][HIMAX + 1];
+  extern __shared__ float lds_qk[];
   __shared__ float red[4];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const CsaShape& sh = a.shape;
-  const int HI = sh.H * sh.dim;
+  const int HI = sh.H * sh.dim, HP = HI + 1;
+  float* qsb = lds_qk;
+  float* ksb = lds_qk + STT * HP;
+  auto qs_at = [&](int r, int c) -> float& { return qsb[r * HP + c]; };
+  auto ks_at = [&](int r, int c) -> float& { return ksb[r * HP + c]; };
   const int s0 = blockIdx.x * STT, t0 = blockIdx.y * STT, z = blockIdx.z;
   const int b = sh.b0 + z / sh.Hkv, hh = z % sh.Hkv;
   const int tl = min(sh.T, t0 + STT) - 1;
@@ -87,8 +91,8 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerScoreArgs a)
   for (int i = tid; i < STT * HI; i += 256) {
     const int r = i / HI, c = i % HI;
     const int tt = t0 + r, ss = s0 + r;
-    qs[r][c] = tt < sh.T ? a.iq[((int64_t)b * sh.T + tt) * HI + c] : 0.f;
-    ks[r][c] = ss < sh.blocks ? a.ik[(((int64_t)b * sh.blocks + ss) * sh.Hkv + hh) * HI + c] : 0.f;
+    qs_at(r, c) = tt < sh.T ? a.iq[((int64_t)b * sh.T + tt) * HI + c] : 0.f;
+    ks_at(r, c) = ss < sh.blocks ? a.ik[(((int64_t)b * sh.blocks + ss) * sh.Hkv + hh) * HI + c] : 0.f;
   }
   __syncthreads();
   bool ok[SR][SR], in[SR][SR];
@@ -113,9 +117,9 @@ __global__ __launch_bounds__(256) void indexer_scores_kernel(IndexerScoreArgs a)
     for (int e = 0; e < sh.dim; e++) {
       float qv[SR], kv[SR];
 #pragma unroll
-      for (int i = 0; i < SR; i++) qv[i] = qs[ty + ST * i][h * sh.dim + e];
+      for (int i = 0; i < SR; i++) qv[i] = qs_at(ty + ST * i, h * sh.dim + e);
 #pragma unroll
-      for (int j = 0; j < SR; j++) kv[j] = ks[tx + ST * j][h * sh.dim + e];
+      for (int j = 0; j < SR; j++) kv[j] = ks_at(tx + ST * j, h * sh.dim + e);
 #pragma unroll
       for (int i = 0; i < SR; i++)
 #pragma unroll
@@ -223,7 +227,13 @@ void launch_indexer_scores(const IndexerScoreArgs& a, int chunk_seqs, hipStream_
     return;
   }
   dim3 grid((unsigned)ceil_div(s.ldo, STT), (unsigned)ceil_div(s.T, STT), (unsigned)(chunk_seqs * s.Hkv));
-  hipLaunchKernelGGL(indexer_scores_kernel, grid, dim3(256), 0, st, a);
+  const size_t lds = sizeof(float) * 2 * STT * (s.H * s.dim + 1);  // <= 132 KB
+  static const bool lds_ok = hipFuncSetAttribute((const void*)indexer_scores_kernel,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)(sizeof(float) * 2 * STT * (HIMAX + 1))) ==
+                             hipSuccess;
+  GN_CHECK(lds_ok, "indexer: the score kernel's LDS size was refused");
+  hipLaunchKernelGGL(indexer_scores_kernel, grid, dim3(256), lds, st, a);
   GN_HIP(hipGetLastError());
 }
 
