@@ -1534,7 +1534,9 @@ GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
   const int64_t cus = 256;
   const int64_t big = ceil_div(d.M, 128) * ceil_div(d.N, 128);
   const bool long_k = d.K >= 4096;
-  const bool use_big = big >= cus || long_k;
+  // at most 64 rows (the flash decode's 64 rows: its lm_head, N = 65,536):
+  // 64 x 64 tiles, not half-empty 128-row ones
+  const bool use_big = (big >= cus && d.M > 64) || long_k;
   const int bm = use_big ? 128 : 64, bn = use_big ? 128 : 64;
   const int64_t tiles = ceil_div(d.M, bm) * ceil_div(d.N, bn);
   int splits = 1;
