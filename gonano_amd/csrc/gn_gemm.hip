@@ -641,6 +641,10 @@ constexpr int TK = 32;         // K depth of one LDS stage
 constexpr int SZ = TILE * TK;  // floats per operand stage (32 KB)
 constexpr int KCHUNK = 8192;   // deepest K range of one workgroup
 
+// Zeros read in place of the K rows past a grouped K range (one row of a
+// tile, 16 bytes per lane); never written.
+__device__ __attribute__((aligned(16))) float zero_row[TILE];
+
 // One operand of a workgroup of NW waves: its K tile moved into an LDS
 // stage and read back as MFMA fragments.
 //
@@ -686,6 +690,17 @@ struct WOp {
                                           int t) const {
     __builtin_amdgcn_global_load_lds((const void*)(base + t * step + loff),
                                      (lds_void*)(S + 4 * ((t * NW + w) * 64)), 16, 0, 0);
+  }
+  // As dma_one for a d-contiguous operand whose instruction t is K row
+  // (tile's first row) + t NW + w: the row is read when ok, else the 16
+  // bytes come from zl (the lane's slot of a zero row), so a K range may end
+  // anywhere inside the tile.
+  __device__ __forceinline__ void dma_one_k(const char* base, int64_t step, float* S, int w, int t,
+                                            bool ok, const char* zl) const {
+    static_assert(!KC, "K-row masking: d-contiguous operands");
+    const char* a = ok ? base + t * step + loff : zl;
+    __builtin_amdgcn_global_load_lds((const void*)a, (lds_void*)(S + 4 * ((t * NW + w) * 64)), 16,
+                                     0, 0);
   }
   // Whole K tile at k0 of the tile starting at row d0.
   __device__ __forceinline__ void dma(const float* __restrict__ X, int64_t ld, int d0, int k0,
@@ -887,8 +902,16 @@ __device__ __forceinline__ void store_wave(const GemmParams& p, float* part,
 // immediate from a per-lane base.  The stages are separate arrays: the LDS
 // reads of one stage provably do not alias the loads in flight into the
 // other.
-template <bool AK, bool BK, int WM, int WN, int E>
+//
+// GKM (expert-grouped K, GEMM_GROUP_K, both operands d-contiguous): split z
+// is (group g, part c) of the p.splits / p.groups parts of group g's rows
+// goff[g] .. goff[g+1], cut evenly; the range starts at its first row (no
+// alignment needed: every DMA instruction is one K row) and the rows of its
+// last tile pair past the range read zeros.  Partials land at split z, so
+// gemm_reduce_kernel sums group g's parts over grid y.
+template <bool AK, bool BK, int WM, int WN, int E, bool GKM = false>
 __global__ __launch_bounds__(64 * WM * WN, (WM * WN) / 4) void gemm_wide_kernel(GemmParams p) {
+  static_assert(!GKM || (!AK && !BK && E == -1), "grouped K: d-contiguous operands, partials");
   constexpr int NW = WM * WN, TM = TILE / WM, TN = TILE / WN, MI = TM / 16, NI = TN / 16;
   using LA = WOp<AK, NW>;
   using LB = WOp<BK, NW>;
@@ -906,8 +929,17 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN) / 4) void gemm_wide_kernel(
   // past the end is shifted back to end at M resp. N)
   const int m0 = tm * TILE, n0 = tn * TILE;
   const int ms = min(m0, p.M - TILE), ns = min(n0, p.N - TILE);
-  const int kbeg = split * p.k_per_split, kend = min(p.K, kbeg + p.k_per_split);
-  const int nkt = kend > kbeg ? (kend - kbeg) / TK : 0;  // even
+  int kbeg = split * p.k_per_split, kend = min(p.K, kbeg + p.k_per_split);
+  if constexpr (GKM) {
+    const int parts = p.splits / p.groups, g = split / parts, c = split - g * parts;
+    const int b = p.goff[g], cnt = p.goff[g + 1] - b, per = (cnt + parts - 1) / parts;
+    kbeg = b + min(c * per, cnt);
+    kend = b + min(c * per + per, cnt);
+  }
+  // even (GKM: rounded up to a tile pair, the rows past kend masked)
+  const int nkt = kend <= kbeg ? 0 : GKM ? 2 * ((kend - kbeg + 2 * TK - 1) / (2 * TK))
+                                         : (kend - kbeg) / TK;
+  const char* zl = reinterpret_cast<const char*>(zero_row) + 16 * lane;
   LA la;
   LB lb;
   la.init(p.lda, tid);
@@ -916,8 +948,18 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN) / 4) void gemm_wide_kernel(
   // re-read the last tile into a stage nobody reads again)
   auto load = [&](int kt, float* sa, float* sb) {
     const int k0 = kbeg + kt * TK;
-    la.dma(p.A, p.lda, ms, k0, sa, w);
-    lb.dma(p.B, p.ldb, ns, k0, sb, w);
+    if constexpr (GKM) {
+      const char* ga = LA::corner(p.A, p.lda, ms, k0);
+      const char* gb = LB::corner(p.B, p.ldb, ns, k0);
+      const int64_t sa_ = LA::tstep(p.lda), sb_ = LB::tstep(p.ldb);
+#pragma unroll
+      for (int t = 0; t < LA::NI; t++) la.dma_one_k(ga, sa_, sa, w, t, k0 + t * NW + w < kend, zl);
+#pragma unroll
+      for (int t = 0; t < LB::NI; t++) lb.dma_one_k(gb, sb_, sb, w, t, k0 + t * NW + w < kend, zl);
+    } else {
+      la.dma(p.A, p.lda, ms, k0, sa, w);
+      lb.dma(p.B, p.ldb, ns, k0, sb, w);
+    }
   };
   const int ab0 = LA::frag_base(wm * TM, 0, lane), ab1 = LA::frag_base(wm * TM, 1, lane);
   const int bb0 = LB::frag_base(wn * TN, 0, lane), bb1 = LB::frag_base(wn * TN, 1, lane);
@@ -957,9 +999,15 @@ __global__ __launch_bounds__(64 * WM * WN, (WM * WN) / 4) void gemm_wide_kernel(
     const int64_t sa = LA::tstep(p.lda), sb = LB::tstep(p.ldb);
     group_mma<AK, BK, NW>(acc, fa1, fb1, [&](int n) {
       const int o = n - 1;
-      if (o >= 0 && o < LA::NI) la.dma_one(ga, sa, CA, w, o);
-      else if (o >= LA::NI && o < PT) lb.dma_one(gb, sb, CB, w, o - LA::NI);
-      else if (o >= PT && o < PT + MI) fa0[o - PT] = LA::template frag<TM>(XA, ab0, o - PT);
+      if (o >= 0 && o < PT) {
+        if constexpr (GKM) {
+          if (o < LA::NI) la.dma_one_k(ga, sa, CA, w, o, k2 + o * NW + w < kend, zl);
+          else lb.dma_one_k(gb, sb, CB, w, o - LA::NI, k2 + (o - LA::NI) * NW + w < kend, zl);
+        } else {
+          if (o < LA::NI) la.dma_one(ga, sa, CA, w, o);
+          else lb.dma_one(gb, sb, CB, w, o - LA::NI);
+        }
+      } else if (o >= PT && o < PT + MI) fa0[o - PT] = LA::template frag<TM>(XA, ab0, o - PT);
       else if (o >= PT + MI && o < PT + MI + NI)
         fb0[o - PT - MI] = LB::template frag<TN>(XB, bb0, o - PT - MI);
     });
@@ -1015,6 +1063,67 @@ static WideKernel wide_kernel(bool ak, bool bk, int e) {
     }
   }
   return nullptr;
+}
+
+// Expert-grouped K (GEMM_GROUP_K: the MoE experts' weight gradients, each a
+// reduction over its expert's rows) on the wide-tile engine: each group's
+// rows are cut into `parts` even ranges, one workgroup per (tile, group,
+// part) writing a partial; gemm_reduce_kernel sums each group's parts
+// (float64, part order) into its output over grid y and applies the
+// epilogue.  parts gives whole rounds of the CUs with ranges of about 1024
+// rows or more on average.  The group sizes live on the device, so a range
+// may be empty (its partial is zero) or shorter than a tile pair (masked).
+static bool gemm_wide_grouped_k(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
+                                DeviceArena* ws) {
+  using namespace wide;
+  if (d.group != GEMM_GROUP_K || d.defer || d.force_splits > 0 || !vec) return false;
+  if (d.a_kcontig || d.b_kcontig || (d.epi != EPI_STORE && d.epi != EPI_ACCUM)) return false;
+  if (d.M < TILE || d.N < TILE || d.M % 4 || d.N % 4) return false;
+  // GN_GEMM_WIDE_GROUPED_K=0 keeps these products on gemm_kernel (A/B runs)
+  if (const char* e = std::getenv("GN_GEMM_WIDE_GROUPED_K"); e && std::atoi(e) == 0) return false;
+  const int64_t tm = ceil_div(d.M, TILE), tn = ceil_div(d.N, TILE), tiles = tm * tn;
+  // padding: at most 1/8 of the MFMA work on rows or columns past the product
+  if ((double)(tm * TILE) * (double)(tn * TILE) > 1.125 * (double)d.M * (double)d.N) return false;
+  const int64_t cus = 256, per_group = tiles * d.groups;
+  int64_t min_wg = (3 * cus) / 4;
+  if (const char* e = std::getenv("GN_GEMM_WIDE_MIN")) {
+    min_wg = std::max(1, std::atoi(e));
+  } else if ((double)d.M * d.N * d.K < (double)(1 << 28)) {
+    return false;
+  }
+  const int64_t avg = d.K / d.groups;
+  const int pmax = (int)std::max<int64_t>(1, std::min<int64_t>(64, avg / 1024));
+  int parts = 1;
+  double best = -1.0;
+  for (int s = 1; s <= pmax; s++) {
+    const int64_t wg = per_group * s;
+    const double eff = (double)wg / (double)(ceil_div(wg, cus) * cus);
+    if (eff > best + 1e-9) {
+      best = eff;
+      parts = s;
+    }
+    if (eff >= 0.999) break;
+  }
+  // GN_GEMM_WIDE_PARTS: another part count (tests: several parts of small
+  // groups, so that ranges end inside a tile pair or are empty)
+  if (const char* e = std::getenv("GN_GEMM_WIDE_PARTS")) parts = std::min(64, std::max(1, std::atoi(e)));
+  if (per_group * parts < min_wg) return false;
+  GN_CHECK(ws != nullptr, "gemm: grouped split-K needs a workspace");
+  p.part = ws->get<float>("gemm_splitk", (size_t)parts * d.groups * d.M * d.N);
+  p.tiles_m = (int)tm;
+  p.tiles_n = (int)tn;
+  p.splits = parts * d.groups;
+  p.k_per_split = d.K;
+  hipLaunchKernelGGL((gemm_wide_kernel<false, false, 2, 2, -1, true>),
+                     dim3((unsigned)(per_group * parts)), dim3(256), 0, st, p);
+  GN_HIP(hipGetLastError());
+  p.splits = parts;
+  p.bsc = d.group_stride;
+  const int64_t total = (int64_t)d.M * d.N;
+  hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)ceil_div(total, 256), (unsigned)d.groups),
+                     dim3(256), 0, st, p);
+  GN_HIP(hipGetLastError());
+  return true;
 }
 
 // Runs d on the wide-tile engine when it suits the product: large enough to
@@ -1472,6 +1581,7 @@ GemmEngine gemm(const GemmDesc& d, hipStream_t st, DeviceArena* ws) {
         GN_HIP(hipGetLastError());
       }
     } else {
+      if (gemm_wide_grouped_k(d, p, vec, st, ws)) return GEMM_ENGINE_WIDE;
       // K mode: a group's whole row range per workgroup, two-level summation
       launch_grouped<128, 128, 2, 2, 1, 2, true, GEMM_GROUP_K>(p, d.a_kcontig, d.b_kcontig, vec,
                                                                st);

@@ -398,6 +398,52 @@ def test_latent_width_pg_step_chunked(orc, latw, monkeypatch):
     _pg_check(orc, cfg, w, B=2, T=300, prompt_len=150, chunk=100, monkeypatch=monkeypatch)
 
 
+def _wide_launches(cfg, w, B, T, prompt_len, env, monkeypatch, seed=7):
+    """gemm_wide_launches of one policy-gradient step under env (no oracle)."""
+    from gonano_amd.session import Session
+    rng = np.random.default_rng(seed)
+    inputs = rng.integers(0, cfg.vocab_size, (B, T)).astype(np.int32)
+    targets = rng.integers(0, cfg.vocab_size, (B, T)).astype(np.int32)
+    targets[:, :prompt_len] = -1
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    with Session(cfg) as s:
+        s.set_params(w)
+        s.set_timing(True)
+        s.zero_grad()
+        s.policy_gradient_step(inputs, targets, np.full(B, 0.3, np.float32), float(T + 1))
+        t = s.timing()
+    for k in env:
+        monkeypatch.delenv(k)
+    return t["gemm_wide_launches"], t["gemm_launches"]
+
+
+@pytest.mark.parametrize("parts", ["1", "3"])
+def test_latent_width_pg_step_wide_grouped_k(orc, latw, monkeypatch, parts):
+    """The routed experts' weight gradients (GEMM_GROUP_K: one reduction
+    over each expert's rows) on the 256 x 256-tile engine, each expert's
+    rows cut into `parts` ranges (GN_GEMM_WIDE_PARTS; the benchmark's
+    16,000-row experts take 8 by the round-filling rule) whose partials
+    gemm_reduce_kernel sums into the gradient.  600 tokens give ~75 rows per
+    expert: every range ends inside a tile pair (rows past it read as
+    zeros), and at 3 parts some experts' last range is empty.  Against the
+    oracle as the other policy-gradient checks; the launch count against
+    GN_GEMM_WIDE_GROUPED_K=0 shows the three weight gradients of each layer
+    (down, gate, up) moved."""
+    cfg, w = latw
+    monkeypatch.setenv("GN_GEMM_WIDE_MIN", "1")
+    monkeypatch.setenv("GN_GEMM_WIDE_PARTS", parts)
+    _pg_check(orc, cfg, w, B=2, T=300, prompt_len=150, chunk=100, monkeypatch=monkeypatch)
+    monkeypatch.delenv("GN_GEMM_WIDE_PARTS")
+    monkeypatch.delenv("GN_GEMM_WIDE_MIN")
+    env = {"GN_GEMM_WIDE_MIN": "1", "GN_GEMM_WIDE_PARTS": parts, "GN_LOGITS_CHUNK": "100"}
+    on, n_on = _wide_launches(cfg, w, 2, 300, 150, env, monkeypatch)
+    off, n_off = _wide_launches(cfg, w, 2, 300, 150, {**env, "GN_GEMM_WIDE_GROUPED_K": "0"},
+                                monkeypatch)
+    report(f"wide launches {on} (grouped K off: {off}) of {n_on}")
+    assert n_on == n_off and on - off == 3 * cfg.n_layer, (on, off, n_on)
+
+
 # ---- flash d12 width (BASELINE configs[4] at 6 layers, V 4096) --------------
 @pytest.fixture(scope="module")
 def flashw():
@@ -420,3 +466,14 @@ def test_flash_width_rollout_teacher_forced(orc, flashw):
 def test_flash_width_pg_step_chunked(orc, flashw, monkeypatch):
     cfg, w = flashw
     _pg_check(orc, cfg, w, B=1, T=560, prompt_len=300, chunk=96, monkeypatch=monkeypatch)
+
+
+def test_flash_width_pg_step_wide_grouped_k(orc, flashw, monkeypatch):
+    """As the latent case at the flash width (experts of 768: 3 x 3 tiles
+    per expert), 2 parts per expert's rows."""
+    cfg, w = flashw
+    monkeypatch.setenv("GN_GEMM_WIDE_MIN", "1")
+    monkeypatch.setenv("GN_GEMM_WIDE_PARTS", "2")
+    _pg_check(orc, cfg, w, B=1, T=560, prompt_len=300, chunk=96, monkeypatch=monkeypatch)
+    monkeypatch.delenv("GN_GEMM_WIDE_PARTS")
+    monkeypatch.delenv("GN_GEMM_WIDE_MIN")
