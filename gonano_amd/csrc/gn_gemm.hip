@@ -114,6 +114,88 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const v4f (&acc)
       }
 }
 
+// A 64 x 64 wave tile (MI = NI = 4) through the wave's 16 KB LDS region S,
+// so that each store instruction writes four whole 256-byte row pieces
+// instead of 4 rows x 64 bytes one float per lane; same arithmetic as
+// store_tile.  D of a 16x16 block (lane: column lane & 15, rows
+// 4 (lane >> 4) + r) goes to S row-major with the column XOR 16 ((row >> 2)
+// & 3), which spreads the four row groups of one ds_write over all banks;
+// the reads take 16 bytes of one row per lane, the epilogue applied on the
+// way out, the reading epilogues' operand fetched in that pattern before
+// the staging writes.  Needs 16-byte aligned rows (ldc, ldaux % 4 == 0).
+template <int E, int MI, int NI>
+__device__ __forceinline__ void store_tile_staged(const GemmParams& p, const v4f (&acc)[MI][NI],
+                                                  int r0, int c0, int lane, float* S) {
+  static_assert(MI == 4 && NI == 4, "64 x 64 wave tiles");
+  const int q = lane >> 4, cl = lane & 15;
+  constexpr bool READS = E == EPI_ADD_SRC || E == EPI_ACCUM || E == EPI_DRELU2;
+  v4f xs[READS ? 16 : 1];
+  if constexpr (READS) {
+    const float* src = E == EPI_ACCUM ? p.C : p.aux;
+    const int64_t ld = E == EPI_ACCUM ? p.ldc : p.ldaux;
+#pragma unroll
+    for (int t = 0; t < 16; t++)
+      xs[t] = *reinterpret_cast<const v4f*>(&src[(int64_t)(r0 + 4 * t + q) * ld + c0 + 4 * cl]);
+  }
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < NI; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int row = 16 * i + 4 * q + r;
+        S[row * 64 + ((16 * j + cl) ^ (((row >> 2) & 3) << 4))] = acc[i][j][r];
+      }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int t = 0; t < 16; t++) {
+    const int row = 4 * t + q;
+    const v4f v = *reinterpret_cast<const v4f*>(&S[row * 64 + ((4 * cl) ^ ((t & 3) << 4))]);
+    const int64_t ci = (int64_t)(r0 + row) * p.ldc + c0 + 4 * cl;
+    v4f o;
+    if constexpr (E == EPI_STORE) {
+      o = v * p.alpha;
+    } else if constexpr (E == EPI_ADD_SRC || E == EPI_ACCUM) {
+      o = E == EPI_ADD_SRC ? v + xs[t] : xs[t] + v;
+    } else if constexpr (E == EPI_SOFTCAP) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) o[c] = softcap15(v[c]);
+    } else if constexpr (E == EPI_RELU2_SAVE || E == EPI_RELU2_SAVE + 16) {
+      if constexpr (E == EPI_RELU2_SAVE)
+        *reinterpret_cast<v4f*>(&p.aux_out[(int64_t)(r0 + row) * p.ldaux + c0 + 4 * cl]) = v;
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float u = v[c] < 0.f ? 0.f : v[c];
+        o[c] = u * u;
+      }
+    } else {
+      static_assert(E == EPI_DRELU2, "epilogue kind");
+#pragma unroll
+      for (int c = 0; c < 4; c++) o[c] = xs[t][c] > 0.f ? (v[c] * 2.f) * xs[t][c] : 0.f;
+    }
+    *reinterpret_cast<v4f*>(&p.C[ci]) = o;
+  }
+}
+
+template <int MI, int NI>
+__device__ __forceinline__ void store_tile_staged_any(const GemmParams& p,
+                                                      const v4f (&acc)[MI][NI], int r0, int c0,
+                                                      int lane, float* S) {
+  switch (p.epi) {
+    case EPI_STORE: store_tile_staged<EPI_STORE>(p, acc, r0, c0, lane, S); break;
+    case EPI_ADD_SRC: store_tile_staged<EPI_ADD_SRC>(p, acc, r0, c0, lane, S); break;
+    case EPI_ACCUM: store_tile_staged<EPI_ACCUM>(p, acc, r0, c0, lane, S); break;
+    case EPI_SOFTCAP: store_tile_staged<EPI_SOFTCAP>(p, acc, r0, c0, lane, S); break;
+    case EPI_RELU2_SAVE:
+      if (p.aux_out) store_tile_staged<EPI_RELU2_SAVE>(p, acc, r0, c0, lane, S);
+      else store_tile_staged<EPI_RELU2_SAVE + 16>(p, acc, r0, c0, lane, S);
+      break;
+    case EPI_DRELU2: store_tile_staged<EPI_DRELU2>(p, acc, r0, c0, lane, S); break;
+  }
+}
+
 // Whole-tile epilogue: one dispatch on the (uniform) epilogue kind.
 template <int MI, int NI>
 __device__ __forceinline__ void store_tile_any(const GemmParams& p, const v4f (&acc)[MI][NI],
@@ -465,6 +547,23 @@ __global__ __launch_bounds__(64 * WM * WN * WK, 2) void gemm_kernel(GemmParams p
   // D of a 16x16 block: lane holds column (lane & 15), rows 4*(lane>>4)+r.
   if (GRP == GEMM_GROUP_K || p.splits == 1) {
     if (m0 + BM <= p.M && n0 + BN <= p.N) {
+      if constexpr (MI == 4 && NI == 4 && WM * WN == 4 && WK == 1 && S == 2 &&
+                    LA::SIZE == 4096 && LB::SIZE == 4096) {
+        // 128 x 128 tiles: each wave stages its 64 x 64 outputs in one of
+        // the four (idle) 16 KB stage buffers
+        const bool rows16 = p.ldc % 4 == 0 && ((uintptr_t)p.C & 15) == 0 &&
+                            (p.epi == EPI_STORE || p.epi == EPI_SOFTCAP ||
+                             p.epi == EPI_ACCUM ||
+                             (p.epi == EPI_RELU2_SAVE && !p.aux_out) ||
+                             (p.ldaux % 4 == 0 &&
+                              ((uintptr_t)(p.epi == EPI_RELU2_SAVE ? p.aux_out : p.aux) & 15) == 0));
+        if (rows16) {
+          tile_barrier();  // every wave's fragment reads of the stages are done
+          float* Sw = wmn < 2 ? &As[wmn][0] : &Bs[wmn - 2][0];
+          store_tile_staged_any(p, acc, m0 + wm * TM, n0 + wn * TN, lane, Sw);
+          return;
+        }
+      }
       store_tile_any(p, acc, m0 + wm * TM, n0 + wn * TN, lane);
       return;
     }
