@@ -33,10 +33,11 @@ void launch_embed_decode(int32_t* tok, const float* wte, const float* wsg, const
                          const int32_t* ovr = nullptr);
 // xin (resp. x) may be the target of a residual-add GEMM whose split-K sum
 // was deferred (pend): the kernels then read xin + sum, and norm_rows
-// writes that value back to x.
+// writes that value back to x.  resid_norm writes it (xin + sum, before the
+// residual mix) to xs when xs is given.
 void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
                        int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st,
-                       const PendingSum& pend = PendingSum{});
+                       const PendingSum& pend = PendingSum{}, float* xs = nullptr);
 void launch_norm_rows(float* x, const float* back, const float* lam, int64_t rows, int C,
                       float* pre, float* y, hipStream_t st, const PendingSum& pend = PendingSum{});
 

@@ -172,7 +172,7 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
                                                          const float* __restrict__ lr,
                                                          const float* __restrict__ l0, int layer,
                                                          int C, float* xb, float* __restrict__ h,
-                                                         PendingSum pend) {
+                                                         PendingSum pend, float* __restrict__ xs) {
   __shared__ float sc[4];
   const int64_t r = blockIdx.x;
   const float a = lr[layer], b = l0[layer];
@@ -198,6 +198,7 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
   for (int k = 0; k < NE; k++) {
     if (!ok[k]) continue;
     const float x = pend.splits > 0 ? pl.sum(pend, k) + xi[k] : xi[k];
+    if (xs) xs[idx[k]] = x;
     const float v = __fmaf_rn(a, x, b * xz[k]);  // one rounding order on every build
     vals[k] = v;
     ss += v * v;
@@ -223,11 +224,11 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, const
   } while (0)
 void launch_resid_norm(const float* xin, const float* x0, const float* lr, const float* l0,
                        int layer, int64_t rows, int C, float* xb, float* h, hipStream_t st,
-                       const PendingSum& pend) {
+                       const PendingSum& pend, float* xs) {
   GN_CHECK(pend.splits == 0 || (pend.stride == rows * (int64_t)C && pend.splits <= PENDING_MAX_SPLITS),
            "resid_norm: pending sum shape");
   GN_ROW_NE_DISPATCH(C, hipLaunchKernelGGL(resid_norm_kernel<NE>, dim3((unsigned)rows), dim3(256),
-                                           0, st, xin, x0, lr, l0, layer, C, xb, h, pend));
+                                           0, st, xin, x0, lr, l0, layer, C, xb, h, pend, xs));
   GN_HIP(hipGetLastError());
 }
 

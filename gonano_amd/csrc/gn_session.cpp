@@ -2063,12 +2063,15 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   // qkv_post, the attention output projection by the MLP norm, the MLP
   // output projection by the next layer's residual mix (or the final norm).
   PendingSum pend;  // a residual-add product pending on x
+  bool back_pending = false;  // the backout copy is the next residual mix's summed x
   for (int l = 0; l < L; l++) {
     Layer& ly = s->layers[l];
     if (dec_enc && l == s->split)  // encoderHidden (transformer.go:310-312)
       GN_HIP(hipMemcpyAsync(dec_enc, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
-    launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st, pend);
+    launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st, pend,
+                      back_pending ? back : nullptr);
     pend = PendingSum{};
+    back_pending = false;
     if (s->mla) {
       mla_decode_layer(s, ly, l, rows, pos, maxSeq, h, kc, vc, x, dpos, &pend);
     } else {
@@ -2133,11 +2136,17 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     sgemm(s, gf);
     GemmDesc gp = linear_fwd_desc(act, ly.wproj, x, rows, F, C, EPI_ADD_SRC);
     gp.aux = x; gp.ldaux = C;
-    // x is copied right after this layer (backout) or the next one's start
-    // (CED encoder state): those layers sum their own product
-    if (l != bk && !(dec_enc && l + 1 == s->split)) gp.defer = &pend;
+    // x is copied at the next one's start (CED encoder state): that layer
+    // sums its own product.  The backout copy of x after layer bk is written
+    // by the next layer's residual mix, which sums the deferred product
+    // (the same float64 sum + x as the reduction), unless bk is the last layer.
+    const bool own = (dec_enc && l + 1 == s->split) || (l == bk && l + 1 == L);
+    if (!own) gp.defer = &pend;
     sgemm(s, gp);
-    if (l == bk) GN_HIP(hipMemcpyAsync(back, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
+    if (l == bk) {
+      if (own) GN_HIP(hipMemcpyAsync(back, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
+      else back_pending = true;
+    }
   }
   launch_norm_rows(x, back, s->bkl, rows, C, nullptr, h, st, pend);
   // lm_head products; the sampler applies the softcap on load
