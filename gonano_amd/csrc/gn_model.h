@@ -31,6 +31,13 @@ void launch_copy_blocks(const CopyBlock* descs, int n, hipStream_t st);
 void launch_embed_decode(int32_t* tok, const float* wte, const float* wsg, const float* lam,
                          int rows, int C, float* prev, float* x, float* x0, hipStream_t st,
                          const int32_t* ovr = nullptr);
+// launch_embed_decode followed by layer 0's residual mix and norm
+// (launch_resid_norm with no pending sum) in one launch: x0 = the embedding,
+// x = the mixed row, h = its norm.
+void launch_embed_decode_mix(int32_t* tok, const float* wte, const float* wsg, const float* lam,
+                             const float* lr, const float* l0, int rows, int C, float* prev,
+                             float* x, float* x0, float* h, hipStream_t st,
+                             const int32_t* ovr = nullptr);
 // xin (resp. x) may be the target of a residual-add GEMM whose split-K sum
 // was deferred (pend): the kernels then read xin + sum, and norm_rows
 // writes that value back to x.  resid_norm writes it (xin + sum, before the

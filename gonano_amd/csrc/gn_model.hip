@@ -137,6 +137,67 @@ void launch_embed_decode(int32_t* tok, const float* wte, const float* wsg, const
   GN_HIP(hipGetLastError());
 }
 
+// embed_decode_kernel followed by layer 0's combineResidual + RMSNorm
+// (resid_norm_kernel with no pending sum) in the same block: x0 = the
+// smeared embedding v, x = lr[0] v + l0[0] v, h = norm(x).  Element k of a
+// thread is column threadIdx.x + 256 k in both steps, as in the two kernels,
+// so the sums and the results are the same bits.
+template <int NE>
+__global__ __launch_bounds__(256) void embed_decode_mix_kernel(
+    int32_t* tok, const int32_t* __restrict__ ovr, const float* __restrict__ wte, int C,
+    const float* __restrict__ wsg, const float* __restrict__ lam, const float* __restrict__ lr,
+    const float* __restrict__ l0, float* __restrict__ prev, float* __restrict__ x,
+    float* __restrict__ x0, float* __restrict__ h) {
+  __shared__ float sc[4];
+  __shared__ float gate_s;
+  const int64_t r = blockIdx.x;
+  int32_t t = tok[r];
+  if (ovr && ovr[r] >= 0) t = ovr[r];
+  const float* src = wte + (int64_t)t * C;
+  float e[NE];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NE; k++) {
+    const int c = threadIdx.x + 256 * k;
+    e[k] = c < C ? src[c] : 0.f;
+    if (c < C) ss += e[k] * e[k];
+  }
+  ss = bsum256(ss, sc);
+  const float inv = 1.f / sqrtf(ss / (float)C + NORM_EPS);
+  if (threadIdx.x < 64) {
+    float p = threadIdx.x < SMEAR_CH ? src[threadIdx.x] * inv * wsg[threadIdx.x] : 0.f;
+    p = warp_sum(p);
+    if (threadIdx.x == 0) gate_s = sigmoidf_(p) * lam[0];
+  }
+  __syncthreads();  // every thread has read tok[r]; sc is free again
+  if (ovr && threadIdx.x == 0) tok[r] = t;
+  const float g = gate_s, a = lr[0], b = l0[0];
+  float vals[NE];
+  float ss2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NE; k++) {
+    const int c = threadIdx.x + 256 * k;
+    if (c >= C) continue;
+    const int64_t i = r * C + c;
+    const float en = e[k] * inv;
+    const float v = en + g * prev[i];
+    prev[i] = en;
+    x0[i] = v;
+    const float m = __fmaf_rn(a, v, b * v);  // resid_norm_kernel's mix of x = x0 = v
+    vals[k] = m;
+    ss2 += m * m;
+  }
+  ss2 = bsum256(ss2, sc);
+  const float inv2 = 1.f / sqrtf(ss2 / (float)C + NORM_EPS);
+#pragma unroll
+  for (int k = 0; k < NE; k++) {
+    const int c = threadIdx.x + 256 * k;
+    if (c >= C) continue;
+    x[r * C + c] = vals[k];
+    h[r * C + c] = vals[k] * inv2;
+  }
+}
+
 // Deferred split-K products: element i is the float64 sum of its partials
 // in split order, rounded once (gemm_reduce_kernel's result).  The row
 // kernels are latency-bound (one block per row, a few elements per
@@ -229,6 +290,15 @@ void launch_resid_norm(const float* xin, const float* x0, const float* lr, const
            "resid_norm: pending sum shape");
   GN_ROW_NE_DISPATCH(C, hipLaunchKernelGGL(resid_norm_kernel<NE>, dim3((unsigned)rows), dim3(256),
                                            0, st, xin, x0, lr, l0, layer, C, xb, h, pend, xs));
+  GN_HIP(hipGetLastError());
+}
+
+void launch_embed_decode_mix(int32_t* tok, const float* wte, const float* wsg, const float* lam,
+                             const float* lr, const float* l0, int rows, int C, float* prev,
+                             float* x, float* x0, float* h, hipStream_t st, const int32_t* ovr) {
+  GN_ROW_NE_DISPATCH(C, hipLaunchKernelGGL(embed_decode_mix_kernel<NE>, dim3((unsigned)rows),
+                                           dim3(256), 0, st, tok, ovr, wte, C, wsg, lam, lr, l0,
+                                           prev, x, x0, h));
   GN_HIP(hipGetLastError());
 }
 

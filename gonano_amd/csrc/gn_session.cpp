@@ -2056,7 +2056,9 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
   float* part = s->mla ? nullptr
                        : A<float>(s, "dec_part", (size_t)rows * Hkv * part_splits *
                                                      (Hq / Hkv) * (HD + 2));
-  launch_embed_decode(dtok, s->wte, s->smg, s->sml, rows, C, prev, x, x0, st, ovr);
+  // the embedding, smear and layer 0's residual mix + norm in one launch
+  launch_embed_decode_mix(dtok, s->wte, s->smg, s->sml, s->rl, s->x0l, rows, C, prev, x, x0, h,
+                          st, ovr);
   const int bk = L / 2;
   // The decode projections split K (M = rows is small); their partial sums
   // are added by the next row kernel instead of a reduction launch: qkv by
@@ -2068,8 +2070,9 @@ static void decode_step(gn_session* s, int rows, int pos, int maxSeq, int32_t* d
     Layer& ly = s->layers[l];
     if (dec_enc && l == s->split)  // encoderHidden (transformer.go:310-312)
       GN_HIP(hipMemcpyAsync(dec_enc, x, sizeof(float) * rows * C, hipMemcpyDeviceToDevice, st));
-    launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st, pend,
-                      back_pending ? back : nullptr);
+    if (l > 0)
+      launch_resid_norm(x, x0, s->rl, s->x0l, l, rows, C, x, h, st, pend,
+                        back_pending ? back : nullptr);
     pend = PendingSum{};
     back_pending = false;
     if (s->mla) {
