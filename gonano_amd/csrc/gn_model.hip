@@ -1090,7 +1090,31 @@ __global__ __launch_bounds__(256) void dot_partials_kernel(const float* __restri
                                                            double* __restrict__ part) {
   __shared__ double sd[4];
   double s0 = 0, s1 = 0;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+  const bool vec = ((((uintptr_t)a | (uintptr_t)b0 | (uintptr_t)b1) & 15) == 0);
+  const int64_t n4 = vec ? n / 4 : 0;
+  if (n4 > 0) {
+    // float4 loads, one float64 chain per component (summed in component
+    // order at the end): four independent dependency chains per thread
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4* a4 = reinterpret_cast<const f4*>(a);
+    const f4* p4 = reinterpret_cast<const f4*>(b0);
+    const f4* q4 = reinterpret_cast<const f4*>(b1);
+    double c0[4] = {0, 0, 0, 0}, c1[4] = {0, 0, 0, 0};
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+      const f4 x = a4[i], y = p4[i];
+      f4 z;
+      if (b1) z = q4[i];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        c0[c] += (double)x[c] * (double)(sign * y[c]);
+        if (b1) c1[c] += (double)x[c] * (double)z[c];
+      }
+    }
+    s0 = ((c0[0] + c0[1]) + c0[2]) + c0[3];
+    s1 = ((c1[0] + c1[1]) + c1[2]) + c1[3];
+  }
+  for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256) {
     s0 += (double)a[i] * (double)(sign * b0[i]);
     if (b1) s1 += (double)a[i] * (double)b1[i];
   }
