@@ -1125,21 +1125,24 @@ __global__ __launch_bounds__(256) void dot_partials_kernel(const float* __restri
     if (b1) part[gridDim.x + blockIdx.x] = s1;
   }
 }
-// Reduces npart partials (ordered) and adds float32(sum) into dst[0].
-__global__ void partials_to_grad_kernel(const double* __restrict__ part, int npart,
-                                        float* __restrict__ dst) {
-  if (threadIdx.x != 0) return;
+// Reduces npart partials and adds float32(sum) into dst[0]: one block of
+// 256 threads, thread t summing partials t, t + 256, ... in order, then the
+// block sum (a fixed order).
+__global__ __launch_bounds__(256) void partials_to_grad_kernel(const double* __restrict__ part,
+                                                               int npart, float* __restrict__ dst) {
+  __shared__ double sd[4];
   double s = 0;
-  for (int i = 0; i < npart; i++) s += part[i];
-  dst[0] += (float)s;
+  for (int i = threadIdx.x; i < npart; i += 256) s += part[i];
+  s = block_sum<double>(s, sd);
+  if (threadIdx.x == 0) dst[0] += (float)s;
 }
 void launch_dot_into_grad(const float* a, const float* b0, const float* b1, float sign, int64_t n,
                           float* dst0, float* dst1, double* part, hipStream_t st) {
   const int nb = 1024;
   hipLaunchKernelGGL(dot_partials_kernel, dim3(nb), dim3(256), 0, st, a, b0, b1, sign, n, part);
   GN_HIP(hipGetLastError());
-  hipLaunchKernelGGL(partials_to_grad_kernel, dim3(1), dim3(64), 0, st, part, nb, dst0);
-  if (b1) hipLaunchKernelGGL(partials_to_grad_kernel, dim3(1), dim3(64), 0, st, part + nb, nb, dst1);
+  hipLaunchKernelGGL(partials_to_grad_kernel, dim3(1), dim3(256), 0, st, part, nb, dst0);
+  if (b1) hipLaunchKernelGGL(partials_to_grad_kernel, dim3(1), dim3(256), 0, st, part + nb, nb, dst1);
   GN_HIP(hipGetLastError());
 }
 
