@@ -373,6 +373,10 @@ void launch_norm_rows(float* x, const float* back, const float* lam, int64_t row
 // every load that does not depend on another -- the q/k/v row (or its
 // split-K partials), the VE gate inputs, the token's VE row and the RoPE
 // table entries of this lane's dims -- is issued before the first wait.
+// PEND: the q/k/v rows arrive as deferred split-K partials (decode); the
+// other instance (prefill, training) holds no partials, a third of the
+// registers, so twice the blocks per CU keep loads in flight.
+template <bool PEND>
 __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   constexpr int D = 128;
   __shared__ __attribute__((aligned(16))) float row[16 * D];  // up to 16 heads of q/k/v
@@ -384,14 +388,14 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
   const int t = (int)(n % a.T);
   const int pos = (a.pos_dev ? *a.pos_dev : a.pos0) + t;
   // q/k/v row: float4 e of this thread is element (tid + 256e) of the row
-  const bool pend = a.qkv_sum.splits > 0;
+  constexpr bool pend = PEND;
   v4f rv[2];
-  v4f pv[2][PENDING_MAX_SPLITS];
+  v4f pv[2][PEND ? PENDING_MAX_SPLITS : 1];
 #pragma unroll
   for (int e = 0; e < 2; e++) {
     const int i = tid + 256 * e;
     if (i >= n4) continue;
-    if (pend) {
+    if constexpr (pend) {
       const v4f* P = reinterpret_cast<const v4f*>(a.qkv_sum.part) + n * n4 + i;
       const int64_t zs = a.qkv_sum.stride / 4;
 #pragma unroll
@@ -434,7 +438,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvPostArgs a) {
     const int i = tid + 256 * e;
     if (i >= n4) continue;
     v4f v = rv[e];
-    if (pend) {
+    if constexpr (pend) {
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         double sum = 0.0;
@@ -525,7 +529,10 @@ void launch_qkv_post(const QkvPostArgs& a, int64_t rows, hipStream_t st) {
                (a.qkv_sum.stride == rows * (int64_t)(a.Hq + 2 * a.Hkv) * 128 &&
                 a.qkv_sum.splits <= PENDING_MAX_SPLITS),
            "qkv_post: pending sum shape");
-  hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
+  if (a.qkv_sum.splits > 0)
+    hipLaunchKernelGGL(qkv_post_kernel<true>, dim3((unsigned)rows), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(qkv_post_kernel<false>, dim3((unsigned)rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }
 
