@@ -1201,18 +1201,34 @@ __global__ __launch_bounds__(256) void qkv_post_bwd_kernel(QkvPostBwdArgs a) {
   const float* cw = a.cosT + (int64_t)t * half;
   const float* sw = a.sinT + (int64_t)t * half;
   float* out = a.dqkv + n * (int64_t)H * D;
-  for (int hd = wid; hd < a.Hq + a.Hkv; hd += 4) {
+  // every q/k head of this wave (at most 4: <= 16 heads over 4 waves) is
+  // requested before the first reduction
+  constexpr int MH = 4;
+  float xa[MH][2], ga[MH][2];
+#pragma unroll
+  for (int k = 0; k < MH; k++) {
+    const int hd = wid + 4 * k;
+    if (hd >= a.Hq + a.Hkv) break;
     const bool isq = hd < a.Hq;
     const int hh = isq ? hd : hd - a.Hq;
     const float* gsrc = isq ? a.dqn + (n * a.Hq + hh) * D : a.dkn + (n * a.Hkv + hh) * D;
     const float* xsrc = isq ? a.qrot + (n * a.Hq + hh) * D : a.krot + (n * a.Hkv + hh) * D;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      xa[k][e] = xsrc[lane + 64 * e];
+      ga[k][e] = gsrc[lane + 64 * e];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < MH; k++) {
+    const int hd = wid + 4 * k;
+    if (hd >= a.Hq + a.Hkv) break;
     float x[2], g[2];
     double ss = 0, dot = 0;
 #pragma unroll
     for (int e = 0; e < 2; e++) {
-      int d = lane + 64 * e;
-      x[e] = xsrc[d];
-      g[e] = gsrc[d] * QK_SCALE;
+      x[e] = xa[k][e];
+      g[e] = ga[k][e] * QK_SCALE;
       ss += (double)x[e] * x[e];
       dot += (double)g[e] * x[e];
     }
@@ -1267,6 +1283,7 @@ __global__ __launch_bounds__(256) void qkv_post_bwd_kernel(QkvPostBwdArgs a) {
   }
 }
 void launch_qkv_post_bwd(const QkvPostBwdArgs& a, int64_t rows, hipStream_t st) {
+  GN_CHECK(a.Hq + a.Hkv <= 16, "qkv_post backward: at most 16 q/k heads");
   hipLaunchKernelGGL(qkv_post_bwd_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
   GN_HIP(hipGetLastError());
 }
