@@ -1,4 +1,4 @@
-"""RL-step benchmark on one MI355X (BASELINE.json metric: rollout tokens/sec
+"""RL-step benchmark on one MI355X (the benchmark's metric: rollout tokens/sec
 and RL-step ms at the d12 dense config, plus the achieved fraction of the
 fp32-MFMA and HBM peaks).
 
@@ -33,12 +33,12 @@ WORKLOADS = {
     # name: (config factory, groups, prompt len, samples, new tokens, temperature, reward p)
     "d12": ("dense_d12", 16, 256, 16, 256, 1.0, 0.3),
     "d2": ("dense_d2", 4, 32, 8, 24, 1.0, 0.3),
-    # 32 prompts of 512 tokens x 16 samples, 1024 new tokens, T=0.8,
+    # the benchmark's d20 workload: 32 prompts of 512 tokens x 16 samples, 1024 new tokens, T=0.8,
     # rewards uniform on {0, 1} (Bernoulli(0.5))
     "d20": ("dense_d20", 32, 512, 16, 1024, 0.8, 0.5),
-    # BASELINE configs[3] (the group split is unspecified there: 16 x 16 as d12)
+    # the benchmark's latent d12 workload (the group split is unspecified there: 16 x 16 as d12)
     "latent_d12": ("latent_d12", 16, 256, 16, 256, 1.0, 0.3),
-    # 64 rollouts (4 groups x 16) of 8192-token prompts + 512 new tokens
+    # the benchmark's flash d12 workload: 64 rollouts (4 groups x 16) of 8192-token prompts + 512 new tokens
     "flash_d12": ("flash_d12", 4, 8192, 16, 512, 1.0, 0.3),
 }
 
@@ -136,7 +136,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the RL step on a single MI355X "
-              "(see DESIGN.md for how the step shards across GPUs); use --gpus 1.",
+              "(sharding the rollout rows and the train micro-batches over one process per "
+              "GPU is a design, not a build target here); use --gpus 1.",
               file=sys.stderr)
         return 2
 

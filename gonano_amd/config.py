@@ -272,17 +272,17 @@ def config_for_depth_ratio(depth: int, vocab_size: int, aspect_ratio: int, head_
 
 
 def dense_d2() -> Config:
-    """ConfigForPreset(dense, 2, 32768, 64, 128, 512, "SSSL")."""
+    """The benchmark's d2 workload: ConfigForPreset(dense, 2, 32768, 64, 128, 512, "SSSL")."""
     return config_for_depth_ratio(2, 32768, 64, 128, 512, "SSSL", 1)
 
 
 def dense_d12() -> Config:
-    """depth 12, 6 query heads, 2 KV heads, vocab 65536, seq 512."""
+    """The benchmark's d12 workload: depth 12, 6 query heads, 2 KV heads, vocab 65536, seq 512."""
     return config_for_depth_ratio(12, 65536, 64, 128, 512, "SSSL", 3)
 
 
 def dense_d20() -> Config:
-    """depth 20, 10 query heads, 2 KV heads, seq 2048."""
+    """The benchmark's d20 workload: depth 20, 10 query heads, 2 KV heads, seq 2048."""
     return config_for_depth_ratio(20, 65536, 64, 128, 2048, "SSSL", 5)
 
 
@@ -361,7 +361,7 @@ def apply_flash_preset(cfg: Config, sparse_topk: int = 0, swa_window: int = 0,
 
 
 def flash_d12() -> Config:
-    """flash preset depth 12 (d_model 768, 6 query heads,
+    """The benchmark's flash d12 workload: flash preset depth 12 (d_model 768, 6 query heads,
     one KV head), compression 4, top-16 sparse selection (pool 8, 128
     candidates, indexer 64 x 1 head), SWA window 512, FRU reuse, CED split at
     layer 6, DeepSeekMoE 1 shared + 16 routed experts of hidden 768, top-2;
@@ -372,10 +372,10 @@ def flash_d12() -> Config:
 
 
 def latent_d12() -> Config:
-    """latent preset depth 12 (d_model 768, 6 query heads,
+    """The benchmark's latent d12 workload: latent preset depth 12 (d_model 768, 6 query heads,
     3 KV heads by the preset's grouped-query default), absorbed MLA with
     latent 256 (one MLALatent serves both the query and the KV latent, so
-    BASELINE's separate q latent of 384 cannot be expressed), rope 64,
+    the benchmark's separate q latent of 384 cannot be expressed), rope 64,
     DeepSeekMoE 1 shared + 16 routed experts of hidden 512, top-2."""
     cfg = config_for_depth_ratio(12, 65536, 64, 128, 512, "SSSL", 1)
     return apply_latent_preset(cfg, mla_latent=256, n_experts=16, experts_per_token=2,

@@ -1,7 +1,7 @@
 // gn_model.hip - fused row kernels of the dense transformer's forward and
 // backward (model/transformer.go, model/attention.go, model/train.go,
 // model/train_transformer.go).  Rows are tokens; one block per row unless
-// noted.  Head dimension is 128 (every BASELINE config).
+// noted.  Head dimension is 128 (every benchmark config).
 #include "gn_model.h"
 
 namespace gn {

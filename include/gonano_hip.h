@@ -14,8 +14,8 @@
  *
  *  2. gn_session_* / gn_generate_batch / gn_policy_gradient_step /
  *     gn_rl_step: a device-resident session that runs the fused hot path the
- *     interface cannot carry (SURVEY of the reference: the sampler, the PG
- *     loss loops, softcap backward, smear and embedding scatter are Go loops
+ *     interface cannot carry (in the reference the sampler, the PG loss
+ *     loops, softcap backward, smear and embedding scatter are Go loops
  *     outside kernels.Backend).  They replace Engine.GenerateBatchWith
  *     (inference/engine.go:336-369), trainer.PolicyGradientStep
  *     (trainer/rl.go:14-60) and the body of cmd/chat_rl's step loop

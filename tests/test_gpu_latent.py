@@ -4,7 +4,7 @@ routed experts), PolicyGradientStep's NLL, loss, balance loss and every
 parameter gradient, rollouts by teacher forcing (absorbed MLA decode against
 the latent cache, device-side routing inside the captured decode graph),
 graph replays against eager launches, and one RL step at the shape family
-of BASELINE configs[3].
+of the benchmark's latent d12 workload.
 
 Floating-point bars as the dense tests: 1e-4 normwise relative per tensor
 (the north-star tolerance) plus kerneltest.Close(1e-3, 1e-4) element-wise;

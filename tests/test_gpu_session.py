@@ -265,7 +265,7 @@ def test_decode_graph_replays_match_eager(small):
 
 
 def test_rl_step_d2_matches_oracle(orc):
-    """dense depth 2, 4 prompts x 8 samples, 24 new
+    """The benchmark's d2 workload: dense depth 2, 4 prompts x 8 samples, 24 new
     tokens, T=1.0, top-k 50, Bernoulli(0.3) rewards; the PG step on the
     GPU's rollouts is compared with the oracle's on the same tokens."""
     from gonano_amd.session import Session

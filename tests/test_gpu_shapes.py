@@ -1,7 +1,7 @@
 """Parity at the benchmark's shapes.
 
 The other GPU tests use narrow models (C = 256, two query heads) that the
-oracle finishes quickly; the kernel paths the BASELINE workloads select
+oracle finishes quickly; the kernel paths the benchmark workloads select
 depend on width, head counts, row counts and context lengths, so these
 tests run those exact widths -- d12 (C 768, 6:2 heads, F 3072), d20 (C 1280,
 10:2 heads), latent d12 (MLA latent 256 over 6:3 heads, 16 experts of 512)
@@ -190,7 +190,7 @@ def _pg_check(orc, cfg, w, B, T, prompt_len, chunk, monkeypatch, seed=7, timing=
     return t
 
 
-# ---- dense d12 width (BASELINE configs[1] at 2 layers, V 4096) -------------
+# ---- dense d12 width (the benchmark's d12 workload at 2 layers, V 4096) -----
 @pytest.fixture(scope="module")
 def d12w():
     cfg = d12_width()
@@ -328,7 +328,7 @@ def test_d12_vocab_pg_step_wide_engine(orc, d12v, monkeypatch):
     assert t["gemm_wide_launches"] == t["gemm_launches"], t
 
 
-# ---- the full d12 model -------------------------------
+# ---- the full d12 model (the benchmark's d12 workload) ----------------------
 @pytest.fixture(scope="module")
 def d12full():
     cfg = G.dense_d12()
@@ -356,7 +356,7 @@ def test_d12_rollout_teacher_forced(orc, d12full):
     _rollout_check(orc, cfg, w, 16, 16, 256, 4, 1.0, groups=(5,))
 
 
-# ---- dense d20 width (BASELINE configs[2] at 2 layers, V 4096) --------------
+# ---- dense d20 width (the benchmark's d20 workload at 2 layers, V 4096) -----
 @pytest.fixture(scope="module")
 def d20w():
     cfg = d20_width()
@@ -379,7 +379,7 @@ def test_d20_width_pg_step_chunked(orc, d20w, monkeypatch):
     _pg_check(orc, cfg, w, B=1, T=540, prompt_len=520, chunk=8, monkeypatch=monkeypatch)
 
 
-# ---- latent d12 width (BASELINE configs[3] at 2 layers, V 4096) -------------
+# ---- latent d12 width (the benchmark's latent d12 workload at 2 layers, V 4096) ---
 @pytest.fixture(scope="module")
 def latw():
     cfg = latent_width()
@@ -444,7 +444,7 @@ def test_latent_width_pg_step_wide_grouped_k(orc, latw, monkeypatch, parts):
     assert n_on == n_off and on - off == 3 * cfg.n_layer, (on, off, n_on)
 
 
-# ---- flash d12 width (BASELINE configs[4] at 6 layers, V 4096) --------------
+# ---- flash d12 width (the benchmark's flash d12 workload at 6 layers, V 4096) ---
 @pytest.fixture(scope="module")
 def flashw():
     cfg = flash_width()
