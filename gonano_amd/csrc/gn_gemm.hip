@@ -1332,6 +1332,8 @@ static bool gemm_wide(const GemmDesc& d, GemmParams p, bool vec, hipStream_t st,
                       DeviceArena* ws) {
   using namespace wide;
   if (d.group != GEMM_GROUP_NONE || d.defer || d.force_splits > 0 || !vec) return false;
+  // GN_GEMM_WIDE=0 leaves every plain product to gemm_kernel (tests)
+  if (const char* e = std::getenv("GN_GEMM_WIDE"); e && std::atoi(e) == 0) return false;
   if ((double)d.M * d.N * d.K < (double)(1 << 28)) return false;
   if (d.M < TILE || d.N < TILE) return false;
   if (d.N % 4 || d.ldc % 4 || !aligned16(d.C)) return false;

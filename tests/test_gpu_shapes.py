@@ -245,6 +245,20 @@ def test_d12_width_pg_step_wide_engine(orc, d12w, monkeypatch):
     assert t["gemm_wide_launches"] == t["gemm_launches"], t
 
 
+def test_d12_width_pg_step_tile_engine(orc, d12w, monkeypatch):
+    """The same 4 x 512-token step with the wide engine switched off
+    (GN_GEMM_WIDE=0): the large products run on gemm_kernel, whose 128 x 128
+    tiles take the epilogues through LDS (store, residual add, ReLU^2 with
+    the saved pre-activation, ReLU^2 backward) and whose long-K products
+    split K into float64-summed partials."""
+    cfg, w = d12w
+    monkeypatch.setenv("GN_GEMM_WIDE", "0")
+    t = _pg_check(orc, cfg, w, B=4, T=512, prompt_len=384, chunk=256, monkeypatch=monkeypatch,
+                  timing=True)
+    monkeypatch.delenv("GN_GEMM_WIDE")
+    assert t["gemm_wide_launches"] == 0, t
+
+
 def test_d12_width_pg_step_wide_engine_ragged_k(orc, d12w, monkeypatch):
     """As above with 4 x 500 tokens: the weight gradients' K (2000 tokens) is
     not a multiple of 64, so the engine runs K in [0, 1984) as its splits
